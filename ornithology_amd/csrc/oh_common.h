@@ -1,0 +1,166 @@
+// oh_common.h - device helpers shared by the HIP kernels (gfx950 / CDNA4).
+//
+// Everything here is exact: the scalar float functions reproduce the
+// reference CPU path bit for bit (the reference's libm is glibc; its expf and
+// log1pf are restated below from their published algorithms and were checked
+// against glibc on every float input). All kernels are compiled with
+// -ffp-contract=off, so a*b+c is two roundings unless fma() is written.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define OH_DEV __device__ __forceinline__
+
+// ---- bit casts / f16 -------------------------------------------------------
+OH_DEV uint32_t f2u(float f) { return __float_as_uint(f); }
+OH_DEV float u2f(uint32_t u) { return __uint_as_float(u); }
+
+// exact binary16 -> binary32 (hardware conversion is exact for every input)
+OH_DEV float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+
+// ---- glibc-compatible expf --------------------------------------------------
+// Algorithm of glibc 2.35 sysdeps/ieee754/flt-32/e_expf.c (ARM
+// optimized-routines, MIT): x*N/ln2 = k + r with |r| <= 1/2, N = 32;
+// 2^(k/N) from a 32-entry table of 2^(i/32) (correctly rounded doubles, exponent
+// bias folded in), degree-3 polynomial for 2^(r/N), one rounding to float. The
+// reduction r = x*N/ln2 - k and the polynomial are fused multiply-adds, which is
+// how the x86-64 FMA build of glibc evaluates them; that form matched glibc's
+// expf on every float input.
+__constant__ uint64_t k_exp2_tab[32] = {
+    0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull,
+    0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull,
+    0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull,
+    0x3feebfdad5362a27ull, 0x3feeb42b569d4f82ull, 0x3feeab07dd485429ull, 0x3feea47eb03a5585ull,
+    0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull, 0x3feea11473eb0187ull, 0x3feea589994cce13ull,
+    0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull,
+    0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
+    0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull,
+};
+
+OH_DEV float ref_expf(float x) {
+    const uint32_t ax = f2u(x) & 0x7fffffffu;
+    if (ax >= 0x42b00000u) {                       // |x| >= 88
+        if (f2u(x) == 0xff800000u) return 0.0f;    // -inf
+        if (ax >= 0x7f800000u) return x + x;       // nan, +inf
+        if (x > 0x1.62e42ep6f) return u2f(0x7f800000u);   // overflow
+        if (x < -0x1.9fe368p6f) return 0.0f;              // underflow
+    }
+    const double inv_ln2_n = 0x1.71547652b82fep+0 * 32.0;
+    const double shift = 0x1.8p+52;
+    const double c0 = 0x1.c6af84b912394p-5 / 32.0 / 32.0 / 32.0;
+    const double c1 = 0x1.ebfce50fac4f3p-3 / 32.0 / 32.0;
+    const double c2 = 0x1.62e42ff0c52d6p-1 / 32.0;
+    const double xd = (double)x;
+    const double z = inv_ln2_n * xd;
+    double kd = z + shift;
+    const uint64_t ki = (uint64_t)__double_as_longlong(kd);
+    kd -= shift;
+    const double r = fma(inv_ln2_n, xd, -kd);
+    uint64_t t = k_exp2_tab[ki % 32];
+    t += ki << 47;
+    const double s = __longlong_as_double((long long)t);
+    const double p = fma(c0, r, c1);
+    const double r2 = r * r;
+    double y = fma(c2, r, 1.0);
+    y = fma(p, r2, y);
+    y = y * s;
+    return (float)y;
+}
+
+// ---- glibc-compatible log1pf ------------------------------------------------
+// fdlibm s_log1pf.c (Sun Microsystems, freely redistributable), the
+// implementation glibc 2.35 uses: reduce 1+x = 2^k (1+f), log1p(f) via
+// s = f/(2+f) and a degree-7 polynomial in s^2, with a correction term c for
+// the rounding of 1+x. Matched glibc on all 2^32 inputs.
+OH_DEV float ref_log1pf(float x) {
+    const float ln2_hi = 6.9313812256e-01f, ln2_lo = 9.0580006145e-06f;
+    const float Lp1 = 6.6666668653e-01f, Lp2 = 4.0000000596e-01f, Lp3 = 2.8571429849e-01f,
+                Lp4 = 2.2222198546e-01f, Lp5 = 1.8183572590e-01f, Lp6 = 1.5313838422e-01f,
+                Lp7 = 1.4798198640e-01f;
+    float hfsq, f = 0.0f, c = 0.0f, s, z, R, u;
+    int32_t k, hx, hu = 0, ax;
+    hx = (int32_t)f2u(x);
+    ax = hx & 0x7fffffff;
+    k = 1;
+    if (hx < 0x3ed413d7) {                         // x < 0.41422
+        if (ax >= 0x3f800000) {                    // x <= -1
+            if (x == -1.0f) return u2f(0xff800000u);
+            return u2f(0x7fc00000u);
+        }
+        if (ax < 0x31000000) {                     // |x| < 2^-29
+            if (ax < 0x24800000) return x;         // |x| < 2^-54
+            return x - x * x * 0.5f;
+        }
+        if (hx > 0 || hx <= (int32_t)0xbe95f61f) { k = 0; f = x; hu = 1; }
+    } else if (hx >= 0x7f800000) {
+        return x + x;
+    }
+    if (k != 0) {
+        if (hx < 0x5a000000) {
+            u = 1.0f + x;
+            hu = (int32_t)f2u(u);
+            k = (hu >> 23) - 127;
+            c = (k > 0) ? 1.0f - (u - x) : x - (u - 1.0f);
+            c /= u;
+        } else {
+            u = x;
+            hu = (int32_t)f2u(u);
+            k = (hu >> 23) - 127;
+            c = 0.0f;
+        }
+        hu &= 0x007fffff;
+        if (hu < 0x3504f7) {
+            u = u2f((uint32_t)hu | 0x3f800000u);
+        } else {
+            k += 1;
+            u = u2f((uint32_t)hu | 0x3f000000u);
+            hu = (0x00800000 - hu) >> 2;
+        }
+        f = u - 1.0f;
+    }
+    hfsq = 0.5f * f * f;
+    if (hu == 0) {                                  // |f| < 2^-20
+        if (f == 0.0f) {
+            if (k == 0) return 0.0f;
+            c += (float)k * ln2_lo;
+            return (float)k * ln2_hi + c;
+        }
+        R = hfsq * (1.0f - 0.66666666666666666f * f);
+        if (k == 0) return f - R;
+        return (float)k * ln2_hi - ((R - ((float)k * ln2_lo + c)) - f);
+    }
+    s = f / (2.0f + f);
+    z = s * s;
+    R = z * (Lp1 + z * (Lp2 + z * (Lp3 + z * (Lp4 + z * (Lp5 + z * (Lp6 + z * Lp7))))));
+    if (k == 0) return f - (hfsq - s * (hfsq + R));
+    return (float)k * ln2_hi - ((hfsq - (s * (hfsq + R) + ((float)k * ln2_lo + c))) - f);
+}
+
+// reference activation helpers (src/ornith_tensor.c:117-123)
+OH_DEV float ref_sigmoid(float x) { return 1.0f / (1.0f + ref_expf(-x)); }
+OH_DEV float ref_silu(float x) { return x * ref_sigmoid(x); }
+OH_DEV float ref_softplus(float x) { return x > 20.0f ? x : ref_log1pf(ref_expf(x)); }
+
+// ---- wave helpers (wave64) --------------------------------------------------
+OH_DEV int lane_id() { return (int)(threadIdx.x & 63); }
+
+template <typename T>
+OH_DEV T shfl(T v, int src) { return __shfl(v, src, 64); }
+template <typename T>
+OH_DEV T shfl_xor(T v, int m) { return __shfl_xor(v, m, 64); }
+
+OH_DEV double wave_sum_d(double v) {
+    for (int m = 32; m >= 1; m >>= 1) v += shfl_xor(v, m);
+    return v;
+}
+OH_DEV int wave_sum_i(int v) {
+    for (int m = 32; m >= 1; m >>= 1) v += shfl_xor(v, m);
+    return v;
+}
+OH_DEV float wave_max_f(float v) {
+    for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, shfl_xor(v, m));
+    return v;
+}
+
+// signed 8-bit dot of four packed bytes, accumulated into c (exact integers)
+OH_DEV int dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }

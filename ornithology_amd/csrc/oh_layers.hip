@@ -1,0 +1,431 @@
+// oh_layers.hip - per-token layer kernels of the decode step (ornith_attn and
+// ornith_moe on CDNA4): token embedding, the fused gated delta-net step, GQA
+// decode over the Q8 KV cache, the MoE router and combine, and the greedy
+// argmax. Included into oh_kernels.hip (single device translation unit).
+//
+// All float arithmetic follows the reference order (see oh_common.h); the
+// places where a reduction order differs from the reference are marked
+// "tree-ordered" and only ever concern double-precision sums of squares or of
+// softmax terms, which are rounded to float once afterwards.
+
+namespace {
+
+// decode element i of row r of a plane-layout tensor (src/ornith_quant.c)
+OH_DEV float dec_elem(const uint8_t *A, const uint8_t *B, const uint8_t *C, int type,
+                      int in, int64_t r, int i) {
+    if (type == OH_F32) return ((const float *)A)[r * in + i];
+    if (type == OH_F16) return h2f(((const uint16_t *)A)[r * in + i]);
+    if (type == OH_BF16) return u2f((uint32_t)((const uint16_t *)A)[r * in + i] << 16);
+    const int nb = in / 256, b = i / 256, k = i % 256;
+    const int64_t bi = r * nb + b;
+    if (type == OH_Q4_K) {
+        const uint4 hdr = *(const uint4 *)(B + bi * 16);
+        const int j = k / 32, l = k % 32;
+        const uint8_t q = A[bi * 128 + 32 * (j / 2) + l];
+        int sc, mn;
+        q4k_sm(hdr, j, sc, mn);
+        const float d1 = h2f((uint16_t)(hdr.x & 0xffffu)) * sc;
+        const float m1 = h2f((uint16_t)(hdr.x >> 16)) * mn;
+        return d1 * (float)((j & 1) ? (q >> 4) : (q & 15)) - m1;
+    }
+    if (type == OH_Q6_K) {
+        const uint8_t *a = A + bi * 192;
+        const int hh = k / 128, kk = k % 128, qd = kk / 32, l = kk % 32;
+        const uint8_t ql = a[64 * hh + l + 32 * (qd & 1)];
+        const uint8_t qh = a[128 + 32 * hh + l];
+        const int lo = (qd < 2) ? (ql & 15) : (ql >> 4);
+        const int q = (lo | (((qh >> (2 * qd)) & 3) << 4)) - 32;
+        const int8_t sc = (int8_t)B[bi * 16 + 8 * hh + l / 16 + 2 * qd];
+        return h2f(*(const uint16_t *)(C + bi * 2)) * (float)sc * (float)q;
+    }
+    if (type == OH_Q8_0)
+        return (float)(int8_t)A[bi * 256 + k] * h2f(*(const uint16_t *)(B + bi * 16 + 2 * (k / 32)));
+    if (type == OH_IQ2_XXS) {
+        const float dd = h2f(*(const uint16_t *)(C + bi * 2));
+        const uint32_t *q = (const uint32_t *)(A + bi * 64);
+        const int g32 = k / 32, kk = (k % 32) / 8, j = k % 8;
+        const uint32_t w0 = q[2 * g32], w1 = q[2 * g32 + 1];
+        const float db = dd * (0.5f + (float)(w1 >> 28)) * 0.25f;
+        const uint64_t gv = k_iq2_grid[(w0 >> (8 * kk)) & 0xffu];
+        const uint32_t s7 = (w1 >> (7 * kk)) & 127u;
+        const uint32_t sg = s7 | ((__popc(s7) & 1u) << 7);
+        return db * (float)((gv >> (8 * j)) & 0xffu) * ((sg >> j) & 1u ? -1.0f : 1.0f);
+    }
+    return 0.0f;
+}
+
+// block-wide (256 threads) double sum, tree-ordered; every thread gets it
+OH_DEV double block_sum_d(double v, double *red) {
+    v = wave_sum_d(v);
+    const int w = (int)(threadIdx.x >> 6);
+    __syncthreads();
+    if (lane_id() == 0) red[w] = v;
+    __syncthreads();
+    return (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+} // namespace
+
+// ---- embedding (src/ornith_rforward.c:199-208) --------------------------------
+extern "C" __global__ void __launch_bounds__(256)
+oh_k_embed(const uint8_t *A, const uint8_t *B, const uint8_t *C, int type, int in,
+           const int32_t *toks, const int32_t *io_pos, float *x) {
+    const int32_t tok = toks[*io_pos];
+    const int i = (int)(blockIdx.x * 256 + threadIdx.x);
+    if (i < in) x[i] = dec_elem(A, B, C, type, in, tok, i);
+}
+
+// ---- gated delta-net decode step (src/ornith_rforward.c:457-503,300-319,
+//      src/ornith_attn.c:198-213,370-388) -----------------------------------------
+// One block of 256 threads covers 256/DK consecutive value heads, one state
+// row per thread. The conv window is double-buffered by position parity: the
+// step reads window[p] and the channel's single owner writes window[1-p], so
+// blocks sharing a key head never race. The state S of value head hv is kept
+// transposed in HBM (element (r, c) at S[hv][c][r]) so the row-per-lane walk
+// over c is a coalesced 256-byte load per wave.
+template <int DK>
+__global__ void __launch_bounds__(256)
+oh_k_delta_step(const float *cat, const float *gate, const float *ab,
+                const float *conv_w, float *conv_state, const float *ssm_a,
+                const float *dt_bias, const float *ssm_norm, float *S,
+                float *out, int8_t *oqs, float *oqd, int16_t *oqb,
+                const int32_t *io_pos, int nk, int nv, int K, int cc,
+                float eps, float out_scale) {
+    constexpr int HPB = 256 / DK;
+    __shared__ float qn[HPB][DK], kn[HPB][DK], vec[256];
+    __shared__ double red[HPB][DK / 64 > 0 ? DK / 64 : 1];
+    const int t = (int)threadIdx.x, hl = t / DK, r = t % DK;
+    const int hv = (int)blockIdx.x * HPB + hl, kh = hv % nk;
+    const int qd = nk * DK;
+    const int pos = *io_pos, p = pos & 1;
+    const float *win = conv_state + (size_t)p * (K - 1) * cc;
+    float *nwin = conv_state + (size_t)(1 - p) * (K - 1) * cc;
+
+    // causal depthwise conv (no bias) + SiLU for this row's q, k, v channels
+    float cv[3];
+    const int ch3[3] = { kh * DK + r, qd + kh * DK + r, 2 * qd + hv * DK + r };
+#pragma unroll
+    for (int a = 0; a < 3; a++) {
+        const int ch = ch3[a];
+        const float *w = conv_w + (size_t)ch * K;
+        float acc = 0.0f;
+        for (int j = 0; j < K - 1; j++) acc += w[j] * win[(size_t)j * cc + ch];
+        acc += w[K - 1] * cat[ch];
+        cv[a] = ref_silu(acc);
+        const bool owner = a == 2 || hv < nk;
+        if (owner) {
+            for (int j = 0; j + 1 < K - 1; j++) nwin[(size_t)j * cc + ch] = win[(size_t)(j + 1) * cc + ch];
+            if (K >= 2) nwin[(size_t)(K - 2) * cc + ch] = cat[ch];
+        }
+    }
+    // per-head L2 normalisation of q and k (src/ornith_tensor.c:155-160);
+    // tree-ordered double sums
+    {
+        double sq = wave_sum_d((double)cv[0] * cv[0]);
+        double sk = wave_sum_d((double)cv[1] * cv[1]);
+        const int w = r >> 6;
+        if (lane_id() == 0) red[hl][w] = sq;
+        __syncthreads();
+        double tq = red[hl][0];
+        for (int k = 1; k < DK / 64; k++) tq += red[hl][k];
+        __syncthreads();
+        if (lane_id() == 0) red[hl][w] = sk;
+        __syncthreads();
+        double tk = red[hl][0];
+        for (int k = 1; k < DK / 64; k++) tk += red[hl][k];
+        const float iq = (float)(1.0 / sqrt(tq + (double)1e-6f));
+        const float ik = (float)(1.0 / sqrt(tk + (double)1e-6f));
+        qn[hl][r] = cv[0] * iq;
+        kn[hl][r] = cv[1] * ik;
+        __syncthreads();
+    }
+    const float alpha = ref_expf(ssm_a[hv] * ref_softplus(ab[hv] + dt_bias[hv]));
+    const float beta = ref_sigmoid(ab[nv + hv]);
+
+    float *Sh = S + (size_t)hv * DK * DK;
+    float s[DK];
+#pragma unroll
+    for (int c = 0; c < DK; c++) s[c] = Sh[c * DK + r] * alpha;
+    float sk = 0.0f;
+#pragma unroll
+    for (int c = 0; c < DK; c++) sk += s[c] * kn[hl][c];
+    const float u = beta * (cv[2] - sk);
+#pragma unroll
+    for (int c = 0; c < DK; c++) s[c] += u * kn[hl][c];
+    float o = 0.0f;
+#pragma unroll
+    for (int c = 0; c < DK; c++) o += s[c] * qn[hl][c];
+#pragma unroll
+    for (int c = 0; c < DK; c++) Sh[c * DK + r] = s[c];
+
+    // 1/sqrt(dk), per-head RMSNorm(ssm_norm), * SiLU(gate)
+    o *= out_scale;
+    {
+        const double so = wave_sum_d((double)o * o);
+        __syncthreads();
+        if (lane_id() == 0) red[hl][r >> 6] = so;
+        __syncthreads();
+        double tot = red[hl][0];
+        for (int k = 1; k < DK / 64; k++) tot += red[hl][k];
+        const float inv = (float)(1.0 / sqrt(tot / (double)DK + (double)eps));
+        o = o * inv * ssm_norm[r];
+    }
+    o = o * ref_silu(gate[hv * DK + r]);
+    out[hv * DK + r] = o;
+    vec[t] = o;
+    __syncthreads();
+    if (t < 64) q8k_block_from_lds(vec, 0, oqs + (size_t)blockIdx.x * 256, oqd + blockIdx.x, oqb + (size_t)blockIdx.x * 16);
+}
+
+// ---- GQA decode (src/ornith_rforward.c:419-455, src/ornith_attn.c:65-149) -------
+// prep: per-head RMSNorm + partial NeoX RoPE (cos/sin from a host-built table
+// of the reference's powf/cosf/sinf values), Q8 append of k and v at `pos`.
+// Blocks [0, nh) are query heads, [nh, nh+nkv) key/value heads.
+// K codes are stored as [kvh][hd/4][cap] 32-bit words (4 codes each, so a
+// lane per position reads coalesced words); V codes [cap][kvh][hd] as in the
+// reference.
+extern "C" __global__ void __launch_bounds__(256)
+oh_k_attn_prep(const float *qproj, const float *kin, const float *vin,
+               const float *q_norm, const float *k_norm, const float2 *rope,
+               float *qr, float *gate, uint32_t *Kt, float *Ks, int8_t *Vq, float *Vs,
+               const int32_t *io_pos, int nh, int nkv, int hd, int rot, int cap, float eps) {
+    __shared__ float v[256];
+    __shared__ double red[4];
+    __shared__ float amax_s[4];
+    const int hb = (int)blockIdx.x, t = (int)threadIdx.x;
+    const int pos = *io_pos;
+    const bool isq = hb < nh;
+    const int h = isq ? hb : hb - nh;
+    const float *src = isq ? qproj + (size_t)h * 2 * hd : kin + (size_t)h * hd;
+    const float x = t < hd ? src[t] : 0.0f;
+    double ss = block_sum_d((double)x * x, red);
+    const float inv = (float)(1.0 / sqrt(ss / (double)hd + (double)eps));
+    const float *nw = isq ? q_norm : k_norm;
+    if (t < hd) v[t] = x * inv * nw[t];
+    __syncthreads();
+    int r = rot <= 0 || rot > hd ? hd : rot;
+    const int half = r / 2;
+    float y = t < hd ? v[t] : 0.0f;
+    if (t < half) {
+        const float2 cs = rope[(size_t)pos * (hd / 2) + t];
+        y = v[t] * cs.x - v[t + half] * cs.y;
+    } else if (t >= half && t < 2 * half) {
+        const float2 cs = rope[(size_t)pos * (hd / 2) + (t - half)];
+        y = v[t - half] * cs.y + v[t] * cs.x;
+    }
+    if (isq) {
+        if (t < hd) {
+            qr[(size_t)h * hd + t] = y;
+            gate[(size_t)h * hd + t] = qproj[(size_t)h * 2 * hd + hd + t];
+        }
+        return;
+    }
+    // Q8 encode of k (post norm/rope) and raw v (src/ornith_attn.c:65-77)
+    for (int which = 0; which < 2; which++) {
+        const float val = which == 0 ? y : (t < hd ? vin[(size_t)h * hd + t] : 0.0f);
+        float a = wave_max_f(fabsf(val));
+        __syncthreads();
+        if (lane_id() == 0) amax_s[t >> 6] = a;
+        __syncthreads();
+        const float amax = fmaxf(fmaxf(amax_s[0], amax_s[1]), fmaxf(amax_s[2], amax_s[3]));
+        int code = 0;
+        float scale = 0.0f;
+        if (amax != 0.0f) {
+            scale = amax / 127.0f;
+            const float iv = 127.0f / amax;
+            int q = (int)__builtin_rintf(val * iv);
+            code = q > 127 ? 127 : (q < -127 ? -127 : q);
+        }
+        const size_t off = (size_t)pos * nkv + h;
+        if (which == 0) {
+            // pack 4 consecutive codes into one word of Kt[h][t/4][pos]
+            const int c0 = shfl(code, (lane_id() & ~3) + 0), c1 = shfl(code, (lane_id() & ~3) + 1);
+            const int c2 = shfl(code, (lane_id() & ~3) + 2), c3 = shfl(code, (lane_id() & ~3) + 3);
+            if (t < hd && (t & 3) == 0)
+                Kt[((size_t)h * (hd / 4) + t / 4) * cap + pos] =
+                    (uint32_t)(c0 & 0xff) | ((uint32_t)(c1 & 0xff) << 8) |
+                    ((uint32_t)(c2 & 0xff) << 16) | ((uint32_t)(c3 & 0xff) << 24);
+            if (t == 0) Ks[off] = scale;
+        } else {
+            if (t < hd) Vq[off * hd + t] = (int8_t)code;
+            if (t == 0) Vs[off] = scale;
+        }
+    }
+}
+
+// scores[h][t] = (sum_i q_i*code_i) * Ks_t * scale, sequential over i
+// (src/ornith_attn.c:80-85,119-122). Grid (nh, cap/256); positions > pos exit.
+extern "C" __global__ void __launch_bounds__(256)
+oh_k_attn_scores(const float *qr, const uint32_t *Kt, const float *Ks, float *scores,
+                 const int32_t *io_pos, int nh, int nkv, int hd, int cap, float scale) {
+    __shared__ float q[256];
+    const int h = (int)blockIdx.x, t = (int)(blockIdx.y * 256 + threadIdx.x);
+    const int T = *io_pos + 1;
+    if ((int)blockIdx.y * 256 >= T) return;
+    const int kvh = h / (nh / nkv);
+    if ((int)threadIdx.x < hd) q[threadIdx.x] = qr[(size_t)h * hd + threadIdx.x];
+    __syncthreads();
+    if (t >= T) return;
+    const uint32_t *kw = Kt + (size_t)kvh * (hd / 4) * cap + t;
+    float acc = 0.0f;
+    for (int w = 0; w < hd / 4; w++) {
+        const uint32_t word = kw[(size_t)w * cap];
+        acc += q[4 * w + 0] * (float)(int8_t)(word & 0xff);
+        acc += q[4 * w + 1] * (float)(int8_t)((word >> 8) & 0xff);
+        acc += q[4 * w + 2] * (float)(int8_t)((word >> 16) & 0xff);
+        acc += q[4 * w + 3] * (float)(int8_t)(word >> 24);
+    }
+    const float ks = Ks[(size_t)t * nkv + kvh];
+    const float sc = ks == 0.0f ? 0.0f : acc * ks;
+    scores[(size_t)h * cap + t] = sc * scale;
+}
+
+// softmax over T (src/ornith_tensor.c:108-115; tree-ordered double sum) and the
+// output o_i = sum_t (p_t*Vs_t)*code_t,i, sequential over t, skipping zero
+// weights (src/ornith_attn.c:132-140); then o *= sigmoid(gate) and Q8_K of the
+// 256 outputs of this block. One block covers 256/hd heads.
+extern "C" __global__ void __launch_bounds__(256)
+oh_k_attn_out(float *scores, const int8_t *Vq, const float *Vs, const float *gate,
+              float *out, int8_t *oqs, float *oqd, int16_t *oqb,
+              const int32_t *io_pos, int nh, int nkv, int hd, int cap) {
+    __shared__ float vec[256];
+    __shared__ float pbuf[4][256];
+    __shared__ double red[4];
+    __shared__ float mred[4];
+    const int hpb = 256 / hd, t = (int)threadIdx.x;
+    const int T = *io_pos + 1;
+    for (int hl = 0; hl < hpb; hl++) {
+        const int h = (int)blockIdx.x * hpb + hl;
+        float *sc = scores + (size_t)h * cap;
+        float mx = -INFINITY;
+        for (int i = t; i < T; i += 256) mx = fmaxf(mx, sc[i]);
+        mx = wave_max_f(mx);
+        __syncthreads();
+        if (lane_id() == 0) mred[t >> 6] = mx;
+        __syncthreads();
+        mx = fmaxf(fmaxf(mred[0], mred[1]), fmaxf(mred[2], mred[3]));
+        double sum = 0.0;
+        for (int i = t; i < T; i += 256) { const float e = ref_expf(sc[i] - mx); sc[i] = e; sum += e; }
+        sum = block_sum_d(sum, red);
+        const float inv = (float)(1.0 / sum);
+        for (int i = t; i < T; i += 256) sc[i] = sc[i] * inv;
+        __syncthreads();
+    }
+    // output: thread -> (head hl, element i)
+    const int hl = t / hd, i = t % hd, h = (int)blockIdx.x * hpb + hl;
+    const int kvh = h / (nh / nkv);
+    const float *p = scores + (size_t)h * cap;
+    float o = 0.0f;
+    for (int t0 = 0; t0 < T; t0 += 256) {
+        const int n = T - t0 < 256 ? T - t0 : 256;
+        __syncthreads();
+        for (int k = t; k < hpb * 256; k += 256) {
+            const int hh = k / 256, tt = k % 256;
+            const int hg = (int)blockIdx.x * hpb + hh, kv2 = hg / (nh / nkv);
+            if (tt < n) pbuf[hh][tt] = scores[(size_t)hg * cap + t0 + tt] * Vs[(size_t)(t0 + tt) * nkv + kv2];
+        }
+        __syncthreads();
+        for (int k = 0; k < n; k++) {
+            const float sv = pbuf[hl][k];
+            if (sv == 0.0f) continue;
+            o += sv * (float)Vq[((size_t)(t0 + k) * nkv + kvh) * hd + i];
+        }
+    }
+    o *= ref_sigmoid(gate[(size_t)h * hd + i]);
+    out[(size_t)h * hd + i] = o;
+    vec[t] = o;
+    __syncthreads();
+    if (t < 64) q8k_block_from_lds(vec, 0, oqs + (size_t)blockIdx.x * 256, oqd + blockIdx.x, oqb + (size_t)blockIdx.x * 16);
+}
+
+// ---- MoE router (src/ornith_moe.c:8-30) ------------------------------------------
+// One wave: top-k by repeated scans (strict '>', ties -> lower index), softmax
+// over the selected logits with a sequential float sum; also sigmoid of the
+// shared-expert gate logit.
+extern "C" __global__ void __launch_bounds__(64)
+oh_k_moe_route(const float *logits, int ne, int k, const float *shgate_logit,
+               int32_t *idx, float *w, float *shgate) {
+    __shared__ unsigned char taken[1024];
+    const int lane = (int)threadIdx.x;
+    for (int e = lane; e < ne; e += 64) taken[e] = 0;
+    __syncthreads();
+    for (int s = 0; s < k; s++) {
+        float bv = -INFINITY; int bi = 0x7fffffff;
+        for (int e = lane; e < ne; e += 64)
+            if (!taken[e] && logits[e] > bv) { bv = logits[e]; bi = e; }
+        for (int m = 32; m >= 1; m >>= 1) {
+            const float ov = shfl_xor(bv, m); const int oi = shfl_xor(bi, m);
+            if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+        }
+        if (lane == 0) { idx[s] = bi; taken[bi] = 1; }
+        __syncthreads();
+    }
+    if (lane == 0) {
+        float mx = logits[idx[0]];
+        for (int s = 1; s < k; s++) if (logits[idx[s]] > mx) mx = logits[idx[s]];
+        float ws[64];
+        float sum = 0.0f;
+        for (int s = 0; s < k; s++) { ws[s] = ref_expf(logits[idx[s]] - mx); sum += ws[s]; }
+        for (int s = 0; s < k; s++) w[s] = ws[s] / sum;
+        if (shgate_logit) *shgate = ref_sigmoid(*shgate_logit);
+    }
+}
+
+// x += sum_s w_s * o_s (sequential in s, from 0) + shared * gate
+// (src/ornith_rforward.c:375-409)
+extern "C" __global__ void __launch_bounds__(256)
+oh_k_moe_combine(float *x, const float *o, const float *w, int k, int H,
+                 const float *so, const float *shgate) {
+    const int i = (int)(blockIdx.x * 256 + threadIdx.x);
+    if (i >= H) return;
+    float acc = 0.0f;
+    for (int s = 0; s < k; s++) acc += w[s] * o[(size_t)s * H + i];
+    if (so) {
+        const float v = shgate ? so[i] * *shgate : so[i];
+        acc += v;
+    }
+    x[i] = x[i] + acc;
+}
+
+// ---- greedy argmax over the logits (src/ornith_rforward.c:18-22) ----------------
+// stage 1: per-block best (largest value, lowest index on ties)
+extern "C" __global__ void __launch_bounds__(256)
+oh_k_argmax1(const float *v, int n, float *bv_out, int *bi_out) {
+    __shared__ float sv[4]; __shared__ int si[4];
+    float bv = -INFINITY; int bi = 0x7fffffff;
+    for (int i = (int)(blockIdx.x * 256 + threadIdx.x); i < n; i += (int)(gridDim.x * 256))
+        if (v[i] > bv || (v[i] == bv && i < bi)) { bv = v[i]; bi = i; }
+    for (int m = 32; m >= 1; m >>= 1) {
+        const float ov = shfl_xor(bv, m); const int oi = shfl_xor(bi, m);
+        if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+    }
+    if (lane_id() == 0) { sv[threadIdx.x >> 6] = bv; si[threadIdx.x >> 6] = bi; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        bv = sv[0]; bi = si[0];
+        for (int k = 1; k < 4; k++) if (sv[k] > bv || (sv[k] == bv && si[k] < bi)) { bv = sv[k]; bi = si[k]; }
+        bv_out[blockIdx.x] = bv; bi_out[blockIdx.x] = bi;
+    }
+}
+
+// stage 2: combine the per-block bests; write the next token at toks[pos]
+// (pos was already advanced by the step) and count the emitted tokens.
+extern "C" __global__ void __launch_bounds__(64)
+oh_k_argmax2(const float *bv_in, const int *bi_in, int nblk, int32_t *toks,
+             const int32_t *io_pos, int32_t *io_best) {
+    float bv = -INFINITY; int bi = 0x7fffffff;
+    for (int i = (int)threadIdx.x; i < nblk; i += 64)
+        if (bv_in[i] > bv || (bv_in[i] == bv && bi_in[i] < bi)) { bv = bv_in[i]; bi = bi_in[i]; }
+    for (int m = 32; m >= 1; m >>= 1) {
+        const float ov = shfl_xor(bv, m); const int oi = shfl_xor(bi, m);
+        if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+    }
+    if (threadIdx.x == 0) {
+        if (bi == 0x7fffffff) bi = 0;
+        toks[*io_pos] = bi;
+        *io_best = bi;
+    }
+}
+
+// advance the stream position after a token's layers (rforward_token s->pos++)
+extern "C" __global__ void oh_k_advance(int32_t *io_pos) { *io_pos = *io_pos + 1; }
