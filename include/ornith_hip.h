@@ -1,0 +1,168 @@
+/* ornith_hip.h - C ABI of the MI355X (gfx950) decode engine for
+ * ornithology-format qwen35moe GGUF models.
+ *
+ * Plain C types only (no HIP or torch types). Host pointers passed in are
+ * borrowed for the duration of the call. Every entry point returns an
+ * ornith_status value (src/ornith.h:34-41) and, on failure, leaves a message
+ * for ornith_hip_last_error() (the reference's global, non-thread-safe error
+ * buffer convention, src/ornith_util.c:7,25-30). Nothing aborts.
+ *
+ * Threading: one context per device, one HIP stream per context; calls on one
+ * context are not re-entrant (the reference serialises generation behind one
+ * mutex, src/ornith_server.c:791).
+ *
+ * Citations name the reference interface each entry point replaces
+ * (paths relative to the njbrake/ornithology tree).
+ */
+#ifndef ORNITH_HIP_H
+#define ORNITH_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ornith_status numbering (src/ornith.h:34-41) */
+#define ORNITH_HIP_OK              0
+#define ORNITH_HIP_ERR_IO          1
+#define ORNITH_HIP_ERR_FORMAT      2
+#define ORNITH_HIP_ERR_UNSUPPORTED 3
+#define ORNITH_HIP_ERR_OOM         4
+#define ORNITH_HIP_ERR_NOTFOUND    5
+#define ORNITH_HIP_ERR_DEVICE      6   /* HIP runtime error (no reference twin) */
+
+typedef struct ornith_hip_ctx ornith_hip_ctx;
+typedef struct ornith_hip_tensor ornith_hip_tensor;
+typedef struct ornith_hip_model ornith_hip_model;
+typedef struct ornith_hip_session ornith_hip_session;
+
+/* Q8_K activation super-block, byte-identical to oq8k_block
+ * (src/ornith_qdot.h:30-34): 292 bytes. */
+typedef struct {
+    float   d;
+    int8_t  qs[256];
+    int16_t bsums[16];
+} ornith_hip_q8k;
+
+/* The ornith_arch fields the decode path uses (src/ornith_model.h:22-64),
+ * inferred from tensor shapes exactly as rmodel_load does
+ * (src/ornith_rforward.c:719-816). */
+typedef struct {
+    int32_t hidden, n_layers, vocab, full_interval;
+    int32_t nh, nkv, hd, rope_dim;
+    int32_t nk, nv, dk, dv, conv_k;
+    int32_t ne, top_k, moe_inter, shared_inter;
+    float   rope_theta, eps;
+    int32_t eos;
+} ornith_hip_arch;
+
+/* Random-init model description: the tensor set and value streams of the
+ * repository's GGUF generator (N(0, sigma) projections via the counter-based
+ * generator, F32 norms/ssm tensors in the reference fixture ranges). */
+typedef struct {
+    int32_t hidden, n_layers, vocab, full_interval;
+    int32_t nh, nkv, hd;
+    int32_t nk, nv, dhead, conv_k;
+    int32_t ne, top_k, moe_inter, shared_inter;
+    uint32_t t_default, t_attn_v, t_ffn_down, t_output, t_embd;
+    uint64_t seed;
+    float    sigma;
+} ornith_hip_gen_cfg;
+
+const char *ornith_hip_last_error(void);            /* ornith_last_error, src/ornith_util.c:25-30 */
+
+int  ornith_hip_init(int device, ornith_hip_ctx **out);
+void ornith_hip_free(ornith_hip_ctx *ctx);
+
+/* ---- ornith_qdot / codecs (kernel-level boundary) --------------------------- */
+
+/* Copy one GGUF tensor (its raw block bytes) to the device in the engine's
+ * plane layout. dims[0] = input width, the product of the remaining dims =
+ * rows (GGUF {in, out[, ne]}, src/ornith_rforward.c:88-89,338-347). */
+int  ornith_hip_upload(ornith_hip_ctx *ctx, const char *name, uint32_t ggml_type,
+                       const void *host_bytes, uint64_t nbytes, uint32_t n_dims,
+                       const uint64_t *dims, ornith_hip_tensor **out);
+void ornith_hip_tensor_free(ornith_hip_tensor *t);
+
+/* qdot_quantize_row_q8_K (src/ornith_qdot.h:36-38): k % 256 == 0. */
+int  ornith_hip_quantize_q8K(ornith_hip_ctx *ctx, const float *x, int64_t k,
+                             ornith_hip_q8k *yq);
+
+/* matmul_batch_q (src/ornith_rforward.c:138-196): Y[t*out+o] = W[o,:].X[t,:]
+ * for Tn columns; Q8_K integer path for Q4_K/Q6_K/Q8_0 (qdot_can), ordered
+ * f32 fallback otherwise. Host X [Tn*in], Y [Tn*out]. */
+int  ornith_hip_matvec(ornith_hip_ctx *ctx, const ornith_hip_tensor *W,
+                       const float *x, float *y, int Tn);
+
+/* oq_dequantize of rows [row0, row0+nrows) (src/ornith_quant.h:64-66). */
+int  ornith_hip_dequant(ornith_hip_ctx *ctx, const ornith_hip_tensor *W,
+                        int64_t row0, int64_t nrows, float *out);
+
+/* ---- ornith_moe -------------------------------------------------------------- */
+
+/* ornith_moe_route (src/ornith_moe.h:35-36): top-k indices (ties to the lower
+ * index) and softmax weights over the selected logits. */
+int  ornith_hip_moe_route(ornith_hip_ctx *ctx, const float *logits, int ne, int k,
+                          int32_t *idx, float *w);
+
+/* ---- model and sessions (src/ornith_rforward.h:24-130) ------------------------ */
+
+/* rmodel_load: mmap the GGUF, infer the arch from tensor shapes, upload every
+ * tensor once. The mapping is released before returning. */
+int  ornith_hip_model_load(ornith_hip_ctx *ctx, const char *gguf_path,
+                           ornith_hip_model **out);
+/* Build the random-init model of `cfg` directly in HBM (same tensors and
+ * values as writing its GGUF with the generator and loading it). */
+int  ornith_hip_model_synth(ornith_hip_ctx *ctx, const ornith_hip_gen_cfg *cfg,
+                            ornith_hip_model **out);
+void ornith_hip_model_free(ornith_hip_model *m);
+int  ornith_hip_model_arch(const ornith_hip_model *m, ornith_hip_arch *out);   /* rmodel_arch */
+/* weight bytes resident on the device, and the GGUF bytes of one tensor */
+uint64_t ornith_hip_model_bytes(const ornith_hip_model *m);
+int  ornith_hip_model_tensor_info(const ornith_hip_model *m, const char *name,
+                                  uint32_t *type, uint64_t *nbytes, uint64_t *rows,
+                                  uint64_t *in);
+const ornith_hip_tensor *ornith_hip_model_tensor(const ornith_hip_model *m, const char *name);
+
+/* rmodel_session_new: capacity `cap` positions, Q8 KV cache (ORNITH_KV_Q8=1
+ * semantics, src/ornith_attn.h:39-68). */
+int  ornith_hip_session_new(ornith_hip_model *m, int cap, ornith_hip_session **out);
+void ornith_hip_session_free(ornith_hip_session *s);                             /* rmodel_session_free */
+/* rmodel_session_eval with ORNITH_PREFILL_SERIAL=1 semantics: the prompt runs
+ * through the token step (src/ornith_rforward.c:838-849,933-944). */
+int  ornith_hip_session_eval(ornith_hip_session *s, const int32_t *tokens, int n);
+/* rmodel_session_logits: copies the V next-token logits to `out`. */
+int  ornith_hip_session_logits(ornith_hip_session *s, float *out);
+int  ornith_hip_session_pos(const ornith_hip_session *s);                        /* rmodel_session_pos */
+/* rmodel_session_generate, greedy (sp == NULL): emits up to n_predict tokens
+ * into out_tokens, stopping without emitting at the model's eos id. */
+int  ornith_hip_session_generate(ornith_hip_session *s, int n_predict,
+                                 int32_t *out_tokens, int *n_out);
+/* rforward_token for one token (src/ornith_rforward.c:686-706). */
+int  ornith_hip_session_step(ornith_hip_session *s, int32_t token);
+
+/* Session state in the reference's host layouts (src/ornith_rforward.c:986-1171
+ * snapshot contents): delta state [nv][dv][dk]; conv window [(K-1)][Cc] oldest
+ * first; Q8 KV codes [len][nkv][hd] and scales [len][nkv]. */
+int  ornith_hip_session_get_delta(ornith_hip_session *s, int layer, float *S);
+int  ornith_hip_session_get_conv(ornith_hip_session *s, int layer, float *win);
+int  ornith_hip_session_get_kv(ornith_hip_session *s, int layer, int8_t *Kq,
+                               float *Ks, int8_t *Vq, float *Vs);
+
+/* ---- measurement (no reference twin) -------------------------------------------- */
+
+/* Time n_steps greedy decode steps already resident on the device (the step
+ * graph replayed back to back, the next token chosen on the device) with HIP
+ * events on the session stream; *ms = total elapsed. Advances the session. */
+int  ornith_hip_session_time_decode(ornith_hip_session *s, int n_steps, float *ms);
+/* Time `iters` launches of one matvec of W (activation already quantised on
+ * the device) with HIP events on the context stream; *ms = mean per launch. */
+int  ornith_hip_time_matvec(ornith_hip_ctx *ctx, const ornith_hip_tensor *W, int iters,
+                            float *ms);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

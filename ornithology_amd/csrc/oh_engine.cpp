@@ -1,0 +1,1227 @@
+// oh_engine.cpp - host side of the MI355X decode engine: GGUF mmap loading,
+// upload into the plane layout, arch inference, sessions and the per-token
+// kernel sequence (captured once into HIP graphs and replayed), behind the C
+// ABI of include/ornith_hip.h.
+//
+// Reference: src/ornith_rforward.c (rmodel_* / rsession_*), src/ornith_gguf_write.c
+// (GGUF v3 layout), src/ornith_model.h (arch).
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include <fcntl.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
+#include "../../include/ornith_hip.h"
+#include "oh_launch.h"
+#include "oh_types.h"
+
+// ---- errors (src/ornith_util.c:7,25-30 convention: one global buffer) ---------
+static char g_err[1024];
+static void seterr(const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+}
+extern "C" const char *ornith_hip_last_error(void) { return g_err; }
+
+#define HCHK(call)                                                                    \
+    do {                                                                              \
+        hipError_t e_ = (call);                                                       \
+        if (e_ != hipSuccess) {                                                       \
+            seterr("%s: %s (%s:%d)", #call, hipGetErrorString(e_), __FILE__, __LINE__); \
+            return e_ == hipErrorOutOfMemory ? ORNITH_HIP_ERR_OOM : ORNITH_HIP_ERR_DEVICE; \
+        }                                                                             \
+    } while (0)
+#define CHK(expr)                     \
+    do {                              \
+        int st_ = (expr);             \
+        if (st_ != ORNITH_HIP_OK) return st_; \
+    } while (0)
+
+// ---- context -----------------------------------------------------------------------
+struct ornith_hip_ctx {
+    int device = 0;
+    hipStream_t st = nullptr;
+    void *scratch = nullptr;
+    size_t scratch_bytes = 0;
+};
+
+static int ctx_scratch(ornith_hip_ctx *c, size_t bytes, void **out) {
+    if (bytes > c->scratch_bytes) {
+        if (c->scratch) HCHK(hipFree(c->scratch));
+        c->scratch = nullptr;
+        c->scratch_bytes = 0;
+        HCHK(hipMalloc(&c->scratch, bytes));
+        c->scratch_bytes = bytes;
+    }
+    *out = c->scratch;
+    return ORNITH_HIP_OK;
+}
+
+extern "C" int ornith_hip_init(int device, ornith_hip_ctx **out) {
+    *out = nullptr;
+    int n = 0;
+    HCHK(hipGetDeviceCount(&n));
+    if (device < 0 || device >= n) {
+        seterr("ornith_hip_init: device %d not present (%d visible)", device, n);
+        return ORNITH_HIP_ERR_NOTFOUND;
+    }
+    HCHK(hipSetDevice(device));
+    auto *c = new ornith_hip_ctx();
+    c->device = device;
+    hipError_t e = hipStreamCreateWithFlags(&c->st, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+        delete c;
+        seterr("hipStreamCreate: %s", hipGetErrorString(e));
+        return ORNITH_HIP_ERR_DEVICE;
+    }
+    *out = c;
+    return ORNITH_HIP_OK;
+}
+
+extern "C" void ornith_hip_free(ornith_hip_ctx *c) {
+    if (!c) return;
+    (void)hipSetDevice(c->device);
+    if (c->scratch) (void)hipFree(c->scratch);
+    if (c->st) (void)hipStreamDestroy(c->st);
+    delete c;
+}
+
+// ---- tensors in the plane layout (oh_types.h) ---------------------------------------
+struct ornith_hip_tensor {
+    ornith_hip_ctx *ctx = nullptr;
+    std::string name;
+    uint32_t type = 0, nd = 0;
+    uint64_t dims[4] = {0, 0, 0, 0};
+    int64_t in = 0, rows = 0;
+    uint64_t gguf_bytes = 0;
+    uint8_t *mem = nullptr;
+    uint8_t *A = nullptr, *B = nullptr, *C = nullptr;
+};
+
+static size_t elem_block(uint32_t t, size_t *bytes) {
+    switch (t) {
+    case OH_F32: *bytes = 4; return 1;
+    case OH_F16: case OH_BF16: *bytes = 2; return 1;
+    case OH_Q8_0: *bytes = 34; return 32;
+    case OH_Q4_K: *bytes = 144; return 256;
+    case OH_Q6_K: *bytes = 210; return 256;
+    case OH_IQ2_XXS: *bytes = 66; return 256;
+    default: *bytes = 0; return 0;
+    }
+}
+
+// GGUF byte size of n elements of type t; 0 if unsupported/misaligned
+// (oq_row_bytes, src/ornith_quant.c:140-146)
+static uint64_t gguf_nbytes(uint32_t t, uint64_t n) {
+    size_t bb;
+    const size_t be = elem_block(t, &bb);
+    if (!be || n % be) return 0;
+    return n / be * bb;
+}
+
+static size_t up256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+// plane sizes of a rows x in tensor
+static void plane_bytes(uint32_t t, int64_t rows, int64_t in, size_t *a, size_t *b, size_t *c) {
+    if (oh_is_quant(t)) {
+        const size_t nblk = (size_t)rows * (size_t)(in / 256);
+        *a = nblk * oh_plane_a(t);
+        *b = nblk * oh_plane_b(t);
+        *c = nblk * oh_plane_c(t);
+    } else {
+        size_t eb;
+        elem_block(t, &eb);
+        *a = (size_t)rows * in * eb;
+        *b = *c = 0;
+    }
+}
+
+// GGUF blocks -> planes (same bytes, regrouped)
+static void repack(uint32_t t, const uint8_t *src, size_t nblk, uint8_t *A, uint8_t *B, uint8_t *C) {
+    switch (t) {
+    case OH_Q4_K:
+        for (size_t i = 0; i < nblk; i++) {
+            memcpy(B + 16 * i, src + 144 * i, 16);
+            memcpy(A + 128 * i, src + 144 * i + 16, 128);
+        }
+        break;
+    case OH_Q6_K:
+        for (size_t i = 0; i < nblk; i++) {
+            memcpy(A + 192 * i, src + 210 * i, 192);
+            memcpy(B + 16 * i, src + 210 * i + 192, 16);
+            memcpy(C + 2 * i, src + 210 * i + 208, 2);
+        }
+        break;
+    case OH_Q8_0:   // nblk counts 256-element super-blocks = 8 GGUF blocks
+        for (size_t i = 0; i < nblk; i++)
+            for (int k = 0; k < 8; k++) {
+                memcpy(A + 256 * i + 32 * k, src + 272 * i + 34 * k + 2, 32);
+                memcpy(B + 16 * i + 2 * k, src + 272 * i + 34 * k, 2);
+            }
+        break;
+    case OH_IQ2_XXS:
+        for (size_t i = 0; i < nblk; i++) {
+            memcpy(A + 64 * i, src + 66 * i + 2, 64);
+            memcpy(C + 2 * i, src + 66 * i, 2);
+        }
+        break;
+    }
+}
+
+static int tensor_alloc(ornith_hip_ctx *ctx, const char *name, uint32_t type, uint32_t nd,
+                        const uint64_t *dims, ornith_hip_tensor **out) {
+    *out = nullptr;
+    if (nd < 1 || nd > 4) { seterr("tensor '%s': %u dims", name, nd); return ORNITH_HIP_ERR_FORMAT; }
+    uint64_t n = 1;
+    for (uint32_t d = 0; d < nd; d++) n *= dims[d];
+    const uint64_t gb = gguf_nbytes(type, n);
+    if (!gb && n) { seterr("tensor '%s': type %u cannot be sized", name, type); return ORNITH_HIP_ERR_UNSUPPORTED; }
+    const int64_t in = (int64_t)dims[0];
+    if (oh_is_quant(type) && in % 256) {
+        seterr("tensor '%s': type %u rows of %lld elements are not 256-block aligned",
+               name, type, (long long)in);
+        return ORNITH_HIP_ERR_UNSUPPORTED;
+    }
+    auto *t = new ornith_hip_tensor();
+    t->ctx = ctx;
+    t->name = name;
+    t->type = type;
+    t->nd = nd;
+    for (uint32_t d = 0; d < nd; d++) t->dims[d] = dims[d];
+    t->in = in;
+    t->rows = in ? (int64_t)(n / (uint64_t)in) : 0;
+    t->gguf_bytes = gb;
+    size_t a, b, c;
+    plane_bytes(type, t->rows, in, &a, &b, &c);
+    const size_t total = up256(a) + up256(b) + up256(c);
+    hipError_t e = hipMalloc(&t->mem, total ? total : 256);
+    if (e != hipSuccess) {
+        delete t;
+        seterr("tensor '%s': hipMalloc(%zu): %s", name, total, hipGetErrorString(e));
+        return ORNITH_HIP_ERR_OOM;
+    }
+    t->A = t->mem;
+    t->B = t->mem + up256(a);
+    t->C = t->B + up256(b);
+    *out = t;
+    return ORNITH_HIP_OK;
+}
+
+extern "C" void ornith_hip_tensor_free(ornith_hip_tensor *t) {
+    if (!t) return;
+    if (t->mem) (void)hipFree(t->mem);
+    delete t;
+}
+
+extern "C" int ornith_hip_upload(ornith_hip_ctx *ctx, const char *name, uint32_t type,
+                                 const void *host, uint64_t nbytes, uint32_t nd,
+                                 const uint64_t *dims, ornith_hip_tensor **out) {
+    *out = nullptr;
+    ornith_hip_tensor *t;
+    CHK(tensor_alloc(ctx, name, type, nd, dims, &t));
+    if (nbytes != t->gguf_bytes) {
+        seterr("tensor '%s': %llu bytes given, %llu expected", name,
+               (unsigned long long)nbytes, (unsigned long long)t->gguf_bytes);
+        ornith_hip_tensor_free(t);
+        return ORNITH_HIP_ERR_FORMAT;
+    }
+    size_t a, b, c;
+    plane_bytes(type, t->rows, t->in, &a, &b, &c);
+    hipError_t e;
+    if (oh_is_quant(type)) {
+        std::vector<uint8_t> h(up256(a) + up256(b) + up256(c));
+        const size_t nblk = (size_t)t->rows * (size_t)(t->in / 256);
+        repack(type, (const uint8_t *)host, nblk, h.data(), h.data() + up256(a), h.data() + up256(a) + up256(b));
+        e = hipMemcpy(t->mem, h.data(), h.size(), hipMemcpyHostToDevice);
+    } else {
+        e = hipMemcpy(t->A, host, a, hipMemcpyHostToDevice);
+    }
+    if (e != hipSuccess) {
+        seterr("tensor '%s': upload: %s", name, hipGetErrorString(e));
+        ornith_hip_tensor_free(t);
+        return ORNITH_HIP_ERR_DEVICE;
+    }
+    *out = t;
+    return ORNITH_HIP_OK;
+}
+
+// ---- matvec launch builder ------------------------------------------------------------
+struct Act {
+    const int8_t *qs = nullptr;
+    const float *d = nullptr;
+    const int16_t *bs = nullptr;
+    const float *xf = nullptr;
+};
+
+struct MvBuild {
+    oh_mvlaunch L;
+    int lds = 0;
+    MvBuild() { memset(&L, 0, sizeof L); }
+};
+
+// rows: rows of one expert for gathered segments, else all rows of W
+static int mv_add(MvBuild &b, const ornith_hip_tensor *W, const Act &act, float *y, int mode,
+                  const int32_t *eidx = nullptr, int eslot = 0) {
+    if (b.L.n >= OH_MAX_SEGS) { seterr("too many matvec segments"); return ORNITH_HIP_ERR_UNSUPPORTED; }
+    oh_mvseg &s = b.L.s[b.L.n];
+    memset(&s, 0, sizeof s);
+    s.A = W->A; s.B = W->B; s.C = W->C;
+    s.xqs = act.qs; s.xd = act.d; s.xbs = act.bs; s.xf = act.xf;
+    s.y = y;
+    s.eidx = eidx;
+    s.eslot = eslot;
+    s.type = (int)W->type;
+    s.in = (int)W->in;
+    s.rows = eidx ? (int)W->dims[1] : (int)W->rows;
+    s.mode = mode;
+    int blocks;
+    if (oh_qdot_can(W->type, W->in) && act.qs) {
+        s.nb = (int)(W->in / 256);
+        s.units = s.nb <= 8 ? (s.rows + 8 / s.nb - 1) / (8 / s.nb) : s.rows;
+        blocks = (s.units + 7) / 8;      // 4 waves x 2 units per block
+    } else {
+        if (!act.xf) { seterr("matvec '%s': no f32 activation for the fallback path", W->name.c_str()); return ORNITH_HIP_ERR_UNSUPPORTED; }
+        if (W->in > 16384) { seterr("matvec '%s': fallback input %lld too wide", W->name.c_str(), (long long)W->in); return ORNITH_HIP_ERR_UNSUPPORTED; }
+        s.nb = (int)(W->in / 256);
+        s.units = s.rows;
+        blocks = (s.rows + 255) / 256;
+        if ((int)W->in > b.lds) b.lds = (int)W->in;
+    }
+    s.block0 = b.L.total_blocks;
+    b.L.total_blocks += blocks;
+    b.L.n++;
+    return ORNITH_HIP_OK;
+}
+
+static int mv_go(MvBuild &b, hipStream_t st) {
+    HCHK(oh_launch_matvec(&b.L, b.lds, st));
+    return ORNITH_HIP_OK;
+}
+
+// ---- kernel-level entry points ---------------------------------------------------------
+extern "C" int ornith_hip_quantize_q8K(ornith_hip_ctx *ctx, const float *x, int64_t k,
+                                       ornith_hip_q8k *yq) {
+    if (k % 256) { seterr("quantize_q8K: k=%lld not a multiple of 256", (long long)k); return ORNITH_HIP_ERR_FORMAT; }
+    HCHK(hipSetDevice(ctx->device));
+    const int64_t nb = k / 256;
+    void *sp;
+    CHK(ctx_scratch(ctx, (size_t)k * 4 + (size_t)k + (size_t)nb * 4 + (size_t)nb * 32 + 1024, &sp));
+    float *dx = (float *)sp;
+    int8_t *qs = (int8_t *)(dx + k);
+    float *dd = (float *)up256((size_t)(qs + k));
+    int16_t *bs = (int16_t *)up256((size_t)(dd + nb));
+    HCHK(hipMemcpyAsync(dx, x, (size_t)k * 4, hipMemcpyHostToDevice, ctx->st));
+    for (int64_t off = 0; off < k; off += 8192) {
+        const int n = (int)(k - off < 8192 ? k - off : 8192);
+        HCHK(oh_launch_rmsnorm_q8k(dx + off, nullptr, 0.0f, n, nullptr, qs + off, dd + off / 256,
+                                   bs + off / 16, ctx->st));
+    }
+    std::vector<int8_t> hq((size_t)k);
+    std::vector<float> hd((size_t)nb);
+    std::vector<int16_t> hb((size_t)nb * 16);
+    HCHK(hipMemcpyAsync(hq.data(), qs, (size_t)k, hipMemcpyDeviceToHost, ctx->st));
+    HCHK(hipMemcpyAsync(hd.data(), dd, (size_t)nb * 4, hipMemcpyDeviceToHost, ctx->st));
+    HCHK(hipMemcpyAsync(hb.data(), bs, (size_t)nb * 32, hipMemcpyDeviceToHost, ctx->st));
+    HCHK(hipStreamSynchronize(ctx->st));
+    for (int64_t b = 0; b < nb; b++) {
+        yq[b].d = hd[b];
+        memcpy(yq[b].qs, hq.data() + b * 256, 256);
+        memcpy(yq[b].bsums, hb.data() + b * 16, 32);
+    }
+    return ORNITH_HIP_OK;
+}
+
+extern "C" int ornith_hip_matvec(ornith_hip_ctx *ctx, const ornith_hip_tensor *W,
+                                 const float *x, float *y, int Tn) {
+    HCHK(hipSetDevice(ctx->device));
+    const int64_t in = W->in, out = W->rows, nb = in / 256;
+    const bool q = oh_qdot_can(W->type, in);
+    void *sp;
+    CHK(ctx_scratch(ctx, (size_t)in * 5 + (size_t)nb * 40 + (size_t)out * 4 + 4096, &sp));
+    float *dx = (float *)sp;
+    float *dy = (float *)up256((size_t)(dx + in));
+    int8_t *qs = (int8_t *)up256((size_t)(dy + out));
+    float *dd = (float *)up256((size_t)(qs + in));
+    int16_t *bs = (int16_t *)up256((size_t)(dd + nb + 1));
+    for (int t = 0; t < Tn; t++) {
+        HCHK(hipMemcpyAsync(dx, x + (size_t)t * in, (size_t)in * 4, hipMemcpyHostToDevice, ctx->st));
+        Act act;
+        act.xf = dx;
+        if (q) {
+            for (int64_t off = 0; off < in; off += 8192) {
+                const int n = (int)(in - off < 8192 ? in - off : 8192);
+                HCHK(oh_launch_rmsnorm_q8k(dx + off, nullptr, 0.0f, n, nullptr, qs + off,
+                                           dd + off / 256, bs + off / 16, ctx->st));
+            }
+            act.qs = qs; act.d = dd; act.bs = bs;
+        }
+        MvBuild b;
+        CHK(mv_add(b, W, act, dy, 0));
+        CHK(mv_go(b, ctx->st));
+        HCHK(hipMemcpyAsync(y + (size_t)t * out, dy, (size_t)out * 4, hipMemcpyDeviceToHost, ctx->st));
+    }
+    HCHK(hipStreamSynchronize(ctx->st));
+    return ORNITH_HIP_OK;
+}
+
+extern "C" int ornith_hip_dequant(ornith_hip_ctx *ctx, const ornith_hip_tensor *W,
+                                  int64_t row0, int64_t nrows, float *out) {
+    if (row0 < 0 || nrows < 0 || row0 + nrows > W->rows) {
+        seterr("dequant: rows [%lld, %lld) outside [0, %lld)", (long long)row0,
+               (long long)(row0 + nrows), (long long)W->rows);
+        return ORNITH_HIP_ERR_FORMAT;
+    }
+    HCHK(hipSetDevice(ctx->device));
+    const size_t n = (size_t)nrows * W->in;
+    void *sp;
+    CHK(ctx_scratch(ctx, n * 4 + 256, &sp));
+    HCHK(oh_launch_dequant(W->A, W->B, W->C, (int)W->type, (int)W->in, row0, nrows, (float *)sp, ctx->st));
+    HCHK(hipMemcpyAsync(out, sp, n * 4, hipMemcpyDeviceToHost, ctx->st));
+    HCHK(hipStreamSynchronize(ctx->st));
+    return ORNITH_HIP_OK;
+}
+
+extern "C" int ornith_hip_moe_route(ornith_hip_ctx *ctx, const float *logits, int ne, int k,
+                                    int32_t *idx, float *w) {
+    if (ne < 1 || ne > 1024 || k < 1 || k > 64 || k > ne) {
+        seterr("moe_route: ne=%d k=%d unsupported", ne, k);
+        return ORNITH_HIP_ERR_UNSUPPORTED;
+    }
+    HCHK(hipSetDevice(ctx->device));
+    void *sp;
+    CHK(ctx_scratch(ctx, (size_t)ne * 4 + 1024, &sp));
+    float *dl = (float *)sp;
+    int32_t *di = (int32_t *)up256((size_t)(dl + ne));
+    float *dw = (float *)(di + 64);
+    HCHK(hipMemcpyAsync(dl, logits, (size_t)ne * 4, hipMemcpyHostToDevice, ctx->st));
+    HCHK(oh_launch_moe_route(dl, ne, k, nullptr, di, dw, nullptr, ctx->st));
+    HCHK(hipMemcpyAsync(idx, di, (size_t)k * 4, hipMemcpyDeviceToHost, ctx->st));
+    HCHK(hipMemcpyAsync(w, dw, (size_t)k * 4, hipMemcpyDeviceToHost, ctx->st));
+    HCHK(hipStreamSynchronize(ctx->st));
+    return ORNITH_HIP_OK;
+}
+
+extern "C" int ornith_hip_time_matvec(ornith_hip_ctx *ctx, const ornith_hip_tensor *W, int iters,
+                                      float *ms) {
+    HCHK(hipSetDevice(ctx->device));
+    const int64_t in = W->in, out = W->rows, nb = in / 256;
+    void *sp;
+    CHK(ctx_scratch(ctx, (size_t)in * 5 + (size_t)nb * 40 + (size_t)out * 4 + 4096, &sp));
+    float *dx = (float *)sp;
+    float *dy = (float *)up256((size_t)(dx + in));
+    int8_t *qs = (int8_t *)up256((size_t)(dy + out));
+    float *dd = (float *)up256((size_t)(qs + in));
+    int16_t *bs = (int16_t *)up256((size_t)(dd + nb + 1));
+    std::vector<float> hx((size_t)in);
+    for (int64_t i = 0; i < in; i++) hx[i] = (float)((i * 7919) % 255 - 127) / 64.0f;
+    HCHK(hipMemcpyAsync(dx, hx.data(), (size_t)in * 4, hipMemcpyHostToDevice, ctx->st));
+    Act act;
+    act.xf = dx;
+    if (oh_qdot_can(W->type, in)) {
+        for (int64_t off = 0; off < in; off += 8192) {
+            const int n = (int)(in - off < 8192 ? in - off : 8192);
+            HCHK(oh_launch_rmsnorm_q8k(dx + off, nullptr, 0.0f, n, nullptr, qs + off, dd + off / 256,
+                                       bs + off / 16, ctx->st));
+        }
+        act.qs = qs; act.d = dd; act.bs = bs;
+    }
+    MvBuild b;
+    CHK(mv_add(b, W, act, dy, 0));
+    CHK(mv_go(b, ctx->st));   // warm
+    hipEvent_t e0, e1;
+    HCHK(hipEventCreate(&e0));
+    HCHK(hipEventCreate(&e1));
+    HCHK(hipEventRecord(e0, ctx->st));
+    for (int i = 0; i < iters; i++) CHK(mv_go(b, ctx->st));
+    HCHK(hipEventRecord(e1, ctx->st));
+    HCHK(hipEventSynchronize(e1));
+    float el = 0.0f;
+    HCHK(hipEventElapsedTime(&el, e0, e1));
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    *ms = iters > 0 ? el / (float)iters : 0.0f;
+    return ORNITH_HIP_OK;
+}
+
+// ---- GGUF v3 mmap reader (format: src/ornith_gguf_write.c:1-11) --------------------------
+namespace {
+
+struct GgufKV { uint32_t vt; const uint8_t *val; size_t len; };
+struct GgufT { std::string name; uint32_t nd, type; uint64_t dims[4]; uint64_t off; const uint8_t *data; uint64_t nbytes; };
+
+struct Gguf {
+    uint8_t *map = nullptr;
+    size_t size = 0;
+    std::unordered_map<std::string, GgufKV> kv;
+    std::vector<GgufT> ts;
+    ~Gguf() { if (map) munmap(map, size); }
+};
+
+struct Rd {
+    const uint8_t *p, *end;
+    bool take(void *dst, size_t n) {
+        if ((size_t)(end - p) < n) return false;
+        if (dst) memcpy(dst, p, n);
+        p += n;
+        return true;
+    }
+};
+
+size_t gguf_scalar(uint32_t vt) {
+    switch (vt) {
+    case 0: case 1: case 7: return 1;
+    case 2: case 3: return 2;
+    case 4: case 5: case 6: return 4;
+    case 10: case 11: case 12: return 8;
+    default: return 0;
+    }
+}
+
+bool gguf_skip(Rd &r, uint32_t vt, int depth) {
+    if (vt == 8) { uint64_t n; return r.take(&n, 8) && r.take(nullptr, n); }
+    if (vt == 9) {
+        uint32_t et; uint64_t n;
+        if (depth > 3 || !r.take(&et, 4) || !r.take(&n, 8)) return false;
+        for (uint64_t i = 0; i < n; i++) if (!gguf_skip(r, et, depth + 1)) return false;
+        return true;
+    }
+    const size_t s = gguf_scalar(vt);
+    return s && r.take(nullptr, s);
+}
+
+int gguf_open(const char *path, Gguf &g) {
+    const int fd = open(path, O_RDONLY);
+    if (fd < 0) { seterr("cannot open %s", path); return ORNITH_HIP_ERR_IO; }
+    struct stat st;
+    if (fstat(fd, &st) != 0) { close(fd); seterr("fstat %s failed", path); return ORNITH_HIP_ERR_IO; }
+    g.size = (size_t)st.st_size;
+    void *m = g.size ? mmap(nullptr, g.size, PROT_READ, MAP_PRIVATE, fd, 0) : MAP_FAILED;
+    close(fd);
+    if (m == MAP_FAILED) { g.size = 0; seterr("mmap %s failed", path); return ORNITH_HIP_ERR_IO; }
+    g.map = (uint8_t *)m;
+    Rd r{g.map, g.map + g.size};
+    char magic[4];
+    uint32_t ver;
+    uint64_t nt, nkv;
+    if (!r.take(magic, 4) || memcmp(magic, "GGUF", 4) != 0) { seterr("not a GGUF file (bad magic)"); return ORNITH_HIP_ERR_FORMAT; }
+    if (!r.take(&ver, 4) || !r.take(&nt, 8) || !r.take(&nkv, 8)) { seterr("truncated GGUF header"); return ORNITH_HIP_ERR_FORMAT; }
+    if (ver < 2 || ver > 3) { seterr("unsupported GGUF version %u", ver); return ORNITH_HIP_ERR_UNSUPPORTED; }
+    if (nt > (1u << 24) || nkv > (1u << 24)) { seterr("implausible GGUF counts"); return ORNITH_HIP_ERR_FORMAT; }
+    uint32_t align = 32;
+    for (uint64_t i = 0; i < nkv; i++) {
+        uint64_t kl;
+        if (!r.take(&kl, 8) || (size_t)(r.end - r.p) < kl) { seterr("bad GGUF key #%llu", (unsigned long long)i); return ORNITH_HIP_ERR_FORMAT; }
+        std::string key((const char *)r.p, kl);
+        r.p += kl;
+        GgufKV v;
+        if (!r.take(&v.vt, 4)) { seterr("bad GGUF value type for '%s'", key.c_str()); return ORNITH_HIP_ERR_FORMAT; }
+        v.val = r.p;
+        if (!gguf_skip(r, v.vt, 0)) { seterr("bad GGUF value for '%s'", key.c_str()); return ORNITH_HIP_ERR_FORMAT; }
+        v.len = (size_t)(r.p - v.val);
+        if (key == "general.alignment" && v.vt == 4 && v.len >= 4) { uint32_t a; memcpy(&a, v.val, 4); if (a) align = a; }
+        g.kv[key] = v;
+    }
+    g.ts.resize(nt);
+    for (uint64_t i = 0; i < nt; i++) {
+        GgufT &t = g.ts[i];
+        uint64_t nl;
+        if (!r.take(&nl, 8) || (size_t)(r.end - r.p) < nl) { seterr("bad GGUF tensor record #%llu", (unsigned long long)i); return ORNITH_HIP_ERR_FORMAT; }
+        t.name.assign((const char *)r.p, nl);
+        r.p += nl;
+        if (!r.take(&t.nd, 4) || t.nd > 4 || t.nd < 1) { seterr("tensor '%s': bad dims", t.name.c_str()); return ORNITH_HIP_ERR_FORMAT; }
+        uint64_t n = 1;
+        for (uint32_t d = 0; d < t.nd; d++) {
+            if (!r.take(&t.dims[d], 8)) { seterr("tensor '%s': bad dims", t.name.c_str()); return ORNITH_HIP_ERR_FORMAT; }
+            n *= t.dims[d];
+        }
+        if (!r.take(&t.type, 4) || !r.take(&t.off, 8)) { seterr("tensor '%s': bad type/offset", t.name.c_str()); return ORNITH_HIP_ERR_FORMAT; }
+        t.nbytes = gguf_nbytes(t.type, n);
+        if (!t.nbytes && n) { seterr("tensor '%s': cannot size type %u for load", t.name.c_str(), t.type); return ORNITH_HIP_ERR_UNSUPPORTED; }
+    }
+    const size_t data0 = ((size_t)(r.p - g.map) + align - 1) / align * align;
+    if (data0 > g.size) { seterr("data section starts past EOF"); return ORNITH_HIP_ERR_FORMAT; }
+    for (auto &t : g.ts) {
+        if (t.off > g.size - data0 || t.nbytes > g.size - data0 - t.off) {
+            seterr("tensor '%s' data extends past EOF", t.name.c_str());
+            return ORNITH_HIP_ERR_FORMAT;
+        }
+        t.data = g.map + data0 + t.off;
+    }
+    return ORNITH_HIP_OK;
+}
+
+} // namespace
+
+// ---- model --------------------------------------------------------------------------------
+struct OhLayer {
+    bool full = false;
+    ornith_hip_tensor *attn_norm = nullptr, *post_norm = nullptr;
+    ornith_hip_tensor *q = nullptr, *k = nullptr, *v = nullptr, *q_norm = nullptr, *k_norm = nullptr, *o = nullptr;
+    ornith_hip_tensor *qkv = nullptr, *conv = nullptr, *ssm_a = nullptr, *dt_bias = nullptr, *ssm_norm = nullptr;
+    ornith_hip_tensor *alpha = nullptr, *beta = nullptr, *gate = nullptr, *ssm_out = nullptr;
+    ornith_hip_tensor *router = nullptr, *gate_exps = nullptr, *up_exps = nullptr, *down_exps = nullptr;
+    ornith_hip_tensor *gate_sh = nullptr, *up_sh = nullptr, *down_sh = nullptr, *gate_inp_sh = nullptr;
+    ornith_hip_tensor *ffn_gate = nullptr, *ffn_up = nullptr, *ffn_down = nullptr;
+};
+
+struct ornith_hip_model {
+    ornith_hip_ctx *ctx = nullptr;
+    ornith_hip_arch a;
+    std::vector<ornith_hip_tensor *> ts;
+    std::unordered_map<std::string, ornith_hip_tensor *> by;
+    std::vector<OhLayer> L;
+    ornith_hip_tensor *embd = nullptr, *out_norm = nullptr, *lm_head = nullptr;
+    uint64_t bytes = 0;
+};
+
+extern "C" void ornith_hip_model_free(ornith_hip_model *m) {
+    if (!m) return;
+    for (auto *t : m->ts) ornith_hip_tensor_free(t);
+    delete m;
+}
+
+static ornith_hip_tensor *mt(const ornith_hip_model *m, const std::string &n) {
+    auto it = m->by.find(n);
+    return it == m->by.end() ? nullptr : it->second;
+}
+static ornith_hip_tensor *mb(const ornith_hip_model *m, int l, const char *sfx) {
+    return mt(m, "blk." + std::to_string(l) + "." + sfx);
+}
+
+// metadata view shared by the GGUF and synthetic paths
+struct Meta {
+    std::string arch = "qwen35";
+    std::unordered_map<std::string, uint32_t> u32;
+    std::unordered_map<std::string, float> f32;
+    bool has_tokens = false;
+    int32_t eos = -1;
+};
+
+static bool is_full(const ornith_hip_arch &a, int l) {
+    return a.full_interval > 0 && l % a.full_interval == a.full_interval - 1;
+}
+
+// shape inference of rmodel_load (src/ornith_rforward.c:728-803) + the engine's
+// own limits, checked loudly
+static int infer_arch(ornith_hip_model *m, const Meta &md) {
+    ornith_hip_arch &a = m->a;
+    memset(&a, 0, sizeof a);
+    auto U = [&](const char *sfx, uint32_t def) {
+        auto it = md.u32.find(md.arch + "." + sfx);
+        return it == md.u32.end() ? def : it->second;
+    };
+    auto Fl = [&](const char *sfx, float def) {
+        auto it = md.f32.find(md.arch + "." + sfx);
+        return it == md.f32.end() ? def : it->second;
+    };
+    m->embd = mt(m, "token_embd.weight");
+    a.hidden = m->embd ? (int)m->embd->dims[0] : (int)U("embedding_length", 4096);
+    a.vocab = m->embd ? (int)m->embd->dims[1] : 248320;
+    int n = 0;
+    while (mb(m, n, "attn_norm.weight")) n++;
+    a.n_layers = n ? n : (int)U("block_count", 32);
+    int ff = -1;
+    for (int i = 0; i < a.n_layers; i++) if (mb(m, i, "attn_q.weight")) { ff = i; break; }
+    a.full_interval = ff >= 0 ? ff + 1 : (int)U("full_attention_interval", 4);
+    a.rope_theta = Fl("rope.freq_base", 1e7f);
+    a.eps = Fl("attention.layer_norm_rms_epsilon", 1e-6f);
+    a.rope_dim = (int)U("rope.dimension_count", 64);
+    {
+        const int fl = a.full_interval - 1;
+        auto *qn = mb(m, fl, "attn_q_norm.weight"), *q = mb(m, fl, "attn_q.weight"), *k = mb(m, fl, "attn_k.weight");
+        a.hd = qn ? (int)qn->dims[0] : 256;
+        const int qout = q ? (int)q->dims[1] : a.hd * 16;
+        a.nh = (qout / 2) / a.hd;
+        a.nkv = k ? (int)k->dims[1] / a.hd : 4;
+    }
+    {
+        int l0 = 0;
+        while (l0 < a.n_layers && is_full(a, l0)) l0++;
+        auto *sa = mb(m, l0, "ssm_a"), *sn = mb(m, l0, "ssm_norm.weight"), *qkv = mb(m, l0, "attn_qkv.weight"),
+             *cv = mb(m, l0, "ssm_conv1d.weight");
+        a.nv = sa ? (int)sa->dims[0] : 32;
+        a.dv = sn ? (int)sn->dims[0] : 128;
+        a.dk = a.dv;
+        a.conv_k = cv ? (int)cv->dims[0] : 4;
+        const int cc = qkv ? (int)qkv->dims[1] : 8192;
+        const int qd = (cc - a.nv * a.dv) / 2;
+        a.nk = a.dk ? qd / a.dk : 16;
+    }
+    auto *ge0 = mb(m, 0, "ffn_gate_exps.weight");
+    if (ge0) {
+        a.ne = (int)ge0->dims[2];
+        a.moe_inter = (int)ge0->dims[1];
+        a.top_k = (int)U("expert_used_count", 8);
+        auto *sh = mb(m, 0, "ffn_gate_shexp.weight");
+        a.shared_inter = sh ? (int)sh->dims[1] : 0;
+    } else {
+        auto *fg = mb(m, 0, "ffn_gate.weight");
+        a.shared_inter = fg ? (int)fg->dims[1] : (int)U("feed_forward_length", 12288);
+    }
+    if (!md.has_tokens) { seterr("no tokenizer.ggml.tokens"); return ORNITH_HIP_ERR_FORMAT; }
+    a.eos = md.eos;
+    m->out_norm = mt(m, "output_norm.weight");
+    m->lm_head = mt(m, "output.weight");
+    m->L.assign((size_t)a.n_layers, OhLayer());
+    for (int l = 0; l < a.n_layers; l++) {
+        OhLayer &y = m->L[l];
+        y.full = is_full(a, l);
+        y.attn_norm = mb(m, l, "attn_norm.weight"); y.post_norm = mb(m, l, "post_attention_norm.weight");
+        y.q = mb(m, l, "attn_q.weight"); y.k = mb(m, l, "attn_k.weight"); y.v = mb(m, l, "attn_v.weight");
+        y.o = mb(m, l, "attn_output.weight");
+        y.q_norm = mb(m, l, "attn_q_norm.weight"); y.k_norm = mb(m, l, "attn_k_norm.weight");
+        y.qkv = mb(m, l, "attn_qkv.weight"); y.conv = mb(m, l, "ssm_conv1d.weight");
+        y.ssm_a = mb(m, l, "ssm_a"); y.dt_bias = mb(m, l, "ssm_dt.bias"); y.ssm_norm = mb(m, l, "ssm_norm.weight");
+        y.alpha = mb(m, l, "ssm_alpha.weight"); y.beta = mb(m, l, "ssm_beta.weight");
+        y.gate = mb(m, l, "attn_gate.weight"); y.ssm_out = mb(m, l, "ssm_out.weight");
+        y.router = mb(m, l, "ffn_gate_inp.weight");
+        y.gate_exps = mb(m, l, "ffn_gate_exps.weight"); y.up_exps = mb(m, l, "ffn_up_exps.weight");
+        y.down_exps = mb(m, l, "ffn_down_exps.weight");
+        y.gate_sh = mb(m, l, "ffn_gate_shexp.weight"); y.up_sh = mb(m, l, "ffn_up_shexp.weight");
+        y.down_sh = mb(m, l, "ffn_down_shexp.weight"); y.gate_inp_sh = mb(m, l, "ffn_gate_inp_shexp.weight");
+        y.ffn_gate = mb(m, l, "ffn_gate.weight"); y.ffn_up = mb(m, l, "ffn_up.weight"); y.ffn_down = mb(m, l, "ffn_down.weight");
+    }
+    // ---- what this engine supports (checked, never assumed) ----
+    auto bad = [&](const char *why) { seterr("unsupported model: %s", why); return ORNITH_HIP_ERR_UNSUPPORTED; };
+    auto need_f32 = [&](const ornith_hip_tensor *t) { return t && t->type == OH_F32; };
+    if (!m->embd || !m->out_norm || !m->lm_head) return bad("token_embd/output_norm/output missing");
+    if (a.hidden % 256 || a.hidden > 8192) return bad("hidden must be a multiple of 256, <= 8192");
+    if (!need_f32(m->out_norm)) return bad("output_norm must be F32 (read as raw floats)");
+    for (int l = 0; l < a.n_layers; l++) {
+        const OhLayer &y = m->L[l];
+        if (!need_f32(y.attn_norm) || !need_f32(y.post_norm)) return bad("layer norms must be F32");
+        if (y.full) {
+            if (!y.q || !y.k || !y.v || !y.o || !need_f32(y.q_norm) || !need_f32(y.k_norm)) return bad("full-attention tensors missing or not F32 norms");
+            if (a.hd > 256 || 256 % a.hd || a.hd % 4) return bad("head_dim must divide 256");
+            if (a.nkv < 1 || a.nh % a.nkv) return bad("n_heads must be a multiple of n_kv_heads");
+            if ((a.nh * a.hd) % 256 || a.nh * a.hd > 8192) return bad("n_heads*head_dim must be a multiple of 256, <= 8192");
+        } else {
+            if (!y.qkv || !y.alpha || !y.beta || !y.gate || !y.ssm_out) return bad("linear-attention projections missing");
+            if (!need_f32(y.conv) || !need_f32(y.ssm_a) || !need_f32(y.dt_bias) || !need_f32(y.ssm_norm))
+                return bad("ssm_conv1d/ssm_a/ssm_dt.bias/ssm_norm must be F32");
+            if (a.dk != 64 && a.dk != 128) return bad("linear head dim must be 64 or 128");
+            if (a.nv % (256 / a.dk) || a.nk < 1) return bad("linear value heads must fill 256-element blocks");
+            if (a.conv_k < 2) return bad("conv kernel must be >= 2");
+            if (a.nv * a.dv > 8192) return bad("linear value width must be <= 8192");
+        }
+        if (a.ne > 0) {
+            if (!y.router || !y.gate_exps || !y.up_exps || !y.down_exps) return bad("MoE tensors missing");
+            if (a.ne > 1024 || a.top_k < 1 || a.top_k > 16 || a.top_k > a.ne) return bad("experts <= 1024 and 1 <= top_k <= 16");
+            if (a.moe_inter % 256 || a.moe_inter > 8192) return bad("expert FFN width must be a multiple of 256, <= 8192");
+            if (y.gate_sh && (a.shared_inter % 256 || a.shared_inter > 8192)) return bad("shared FFN width must be a multiple of 256");
+        } else {
+            if (!y.ffn_gate || !y.ffn_up || !y.ffn_down) return bad("dense FFN tensors missing");
+            if (a.shared_inter % 256 || a.shared_inter > 8192) return bad("FFN width must be a multiple of 256");
+        }
+    }
+    return ORNITH_HIP_OK;
+}
+
+extern "C" int ornith_hip_model_load(ornith_hip_ctx *ctx, const char *path, ornith_hip_model **out) {
+    *out = nullptr;
+    HCHK(hipSetDevice(ctx->device));
+    Gguf g;
+    CHK(gguf_open(path, g));
+    Meta md;
+    auto it = g.kv.find("general.architecture");
+    if (it != g.kv.end() && it->second.vt == 8 && it->second.len >= 8) {
+        uint64_t n;
+        memcpy(&n, it->second.val, 8);
+        if (n <= it->second.len - 8 && n < 64) md.arch.assign((const char *)it->second.val + 8, n);
+    }
+    for (auto &kv : g.kv) {
+        if ((kv.second.vt == 4 || kv.second.vt == 5) && kv.second.len >= 4) { uint32_t v; memcpy(&v, kv.second.val, 4); md.u32[kv.first] = v; }
+        if (kv.second.vt == 6 && kv.second.len >= 4) { float v; memcpy(&v, kv.second.val, 4); md.f32[kv.first] = v; }
+    }
+    md.has_tokens = g.kv.count("tokenizer.ggml.tokens") > 0;
+    auto ie = g.kv.find("tokenizer.ggml.eos_token_id");
+    if (ie != g.kv.end() && ie->second.len >= 4) memcpy(&md.eos, ie->second.val, 4);
+    auto *m = new ornith_hip_model();
+    m->ctx = ctx;
+    for (auto &t : g.ts) {
+        ornith_hip_tensor *dt;
+        int st = ornith_hip_upload(ctx, t.name.c_str(), t.type, t.data, t.nbytes, t.nd, t.dims, &dt);
+        if (st) { ornith_hip_model_free(m); return st; }
+        m->ts.push_back(dt);
+        m->by[t.name] = dt;
+        m->bytes += dt->gguf_bytes;
+    }
+    int st = infer_arch(m, md);
+    if (st) { ornith_hip_model_free(m); return st; }
+    *out = m;
+    return ORNITH_HIP_OK;
+}
+
+extern "C" int ornith_hip_model_arch(const ornith_hip_model *m, ornith_hip_arch *out) {
+    *out = m->a;
+    return ORNITH_HIP_OK;
+}
+extern "C" uint64_t ornith_hip_model_bytes(const ornith_hip_model *m) { return m->bytes; }
+extern "C" const ornith_hip_tensor *ornith_hip_model_tensor(const ornith_hip_model *m, const char *name) {
+    return mt(m, name);
+}
+extern "C" int ornith_hip_model_tensor_info(const ornith_hip_model *m, const char *name, uint32_t *type,
+                                            uint64_t *nbytes, uint64_t *rows, uint64_t *in) {
+    auto *t = mt(m, name);
+    if (!t) { seterr("no tensor '%s'", name); return ORNITH_HIP_ERR_NOTFOUND; }
+    if (type) *type = t->type;
+    if (nbytes) *nbytes = t->gguf_bytes;
+    if (rows) *rows = (uint64_t)t->rows;
+    if (in) *in = (uint64_t)t->in;
+    return ORNITH_HIP_OK;
+}
+
+// ---- sessions -----------------------------------------------------------------------------
+struct Q8Buf { int8_t *qs = nullptr; float *d = nullptr; int16_t *bs = nullptr; };
+
+struct LayerState {
+    float *S = nullptr, *conv = nullptr;                 // linear
+    uint32_t *Kt = nullptr; float *Ks = nullptr;         // full (Q8 KV)
+    int8_t *Vq = nullptr; float *Vs = nullptr;
+};
+
+struct ornith_hip_session {
+    ornith_hip_model *m = nullptr;
+    int cap = 0, pos = 0;
+    bool have_logits = false;
+    std::vector<void *> allocs;
+    int32_t *io = nullptr;        // [0] pos, [1] best
+    int32_t *toks = nullptr;      // [cap + 1]
+    float *x = nullptr, *xn = nullptr;
+    Q8Buf xq;
+    float *cat = nullptr, *gate = nullptr, *ab = nullptr;
+    float *o = nullptr;
+    Q8Buf oq;
+    float *qproj = nullptr, *kb = nullptr, *vb = nullptr, *qr = nullptr, *agate = nullptr, *scores = nullptr;
+    float2 *rope = nullptr;
+    float *rl = nullptr, *shl = nullptr, *shg = nullptr, *ew = nullptr;
+    int32_t *eidx = nullptr;
+    float *g = nullptr, *u = nullptr, *h = nullptr, *od = nullptr;
+    Q8Buf hq;
+    float *logits = nullptr, *amv = nullptr;
+    int *ami = nullptr;
+    std::vector<LayerState> ls;
+    hipGraphExec_t gbody = nullptr, ghead = nullptr;
+    bool graphs_tried = false;
+};
+
+extern "C" void ornith_hip_session_free(ornith_hip_session *s) {
+    if (!s) return;
+    (void)hipSetDevice(s->m->ctx->device);
+    if (s->gbody) (void)hipGraphExecDestroy(s->gbody);
+    if (s->ghead) (void)hipGraphExecDestroy(s->ghead);
+    for (void *p : s->allocs) (void)hipFree(p);
+    delete s;
+}
+
+template <typename T>
+static int salloc(ornith_hip_session *s, T **p, size_t n) {
+    void *v = nullptr;
+    HCHK(hipMalloc(&v, n * sizeof(T) + 256));
+    HCHK(hipMemset(v, 0, n * sizeof(T) + 256));
+    s->allocs.push_back(v);
+    *p = (T *)v;
+    return ORNITH_HIP_OK;
+}
+static int q8alloc(ornith_hip_session *s, Q8Buf &q, size_t n) {
+    CHK(salloc(s, &q.qs, n));
+    CHK(salloc(s, &q.d, n / 256 + 1));
+    CHK(salloc(s, &q.bs, n / 16 + 16));
+    return ORNITH_HIP_OK;
+}
+static Act act_of(const Q8Buf &q, const float *xf) {
+    Act a; a.qs = q.qs; a.d = q.d; a.bs = q.bs; a.xf = xf; return a;
+}
+static Act act_off(const Q8Buf &q, const float *xf, size_t elems) {
+    Act a; a.qs = q.qs + elems; a.d = q.d + elems / 256; a.bs = q.bs + elems / 16; a.xf = xf + elems; return a;
+}
+
+extern "C" int ornith_hip_session_new(ornith_hip_model *m, int cap, ornith_hip_session **out) {
+    *out = nullptr;
+    if (cap < 1) cap = 1;
+    HCHK(hipSetDevice(m->ctx->device));
+    const ornith_hip_arch &a = m->a;
+    auto *s = new ornith_hip_session();
+    s->m = m;
+    s->cap = cap;
+    const int H = a.hidden, qd = a.nk * a.dk, vd = a.nv * a.dv, cc = 2 * qd + vd;
+    const int aq = a.nh * a.hd, kvd = a.nkv * a.hd;
+    const int K = a.top_k, I = a.moe_inter > a.shared_inter ? a.moe_inter : a.shared_inter;
+    const int ow = vd > aq ? vd : aq;
+    int st = ORNITH_HIP_OK;
+#define A_(x) do { if ((st = (x)) != ORNITH_HIP_OK) { ornith_hip_session_free(s); return st; } } while (0)
+    A_(salloc(s, &s->io, 64));
+    A_(salloc(s, &s->toks, (size_t)cap + 1));
+    A_(salloc(s, &s->x, H)); A_(salloc(s, &s->xn, H)); A_(q8alloc(s, s->xq, H));
+    A_(salloc(s, &s->cat, cc > 0 ? cc : 1)); A_(salloc(s, &s->gate, vd > 0 ? vd : 1));
+    A_(salloc(s, &s->ab, 2 * (a.nv > 0 ? a.nv : 1)));
+    A_(salloc(s, &s->o, ow)); A_(q8alloc(s, s->oq, ow));
+    A_(salloc(s, &s->qproj, 2 * (size_t)aq)); A_(salloc(s, &s->kb, kvd)); A_(salloc(s, &s->vb, kvd));
+    A_(salloc(s, &s->qr, aq)); A_(salloc(s, &s->agate, aq));
+    A_(salloc(s, &s->scores, (size_t)a.nh * cap));
+    A_(salloc(s, &s->rl, a.ne > 0 ? a.ne : 1)); A_(salloc(s, &s->shl, 1)); A_(salloc(s, &s->shg, 1));
+    A_(salloc(s, &s->ew, 64)); A_(salloc(s, &s->eidx, 64));
+    const size_t nvec = (size_t)(K + 1);
+    A_(salloc(s, &s->g, nvec * I)); A_(salloc(s, &s->u, nvec * I)); A_(salloc(s, &s->h, nvec * I));
+    A_(q8alloc(s, s->hq, nvec * I));
+    A_(salloc(s, &s->od, nvec * H));
+    A_(salloc(s, &s->logits, a.vocab));
+    A_(salloc(s, &s->amv, OH_ARGMAX_BLOCKS)); A_(salloc(s, &s->ami, OH_ARGMAX_BLOCKS));
+    s->ls.resize((size_t)a.n_layers);
+    bool any_full = false;
+    for (int l = 0; l < a.n_layers; l++) {
+        LayerState &y = s->ls[l];
+        if (m->L[l].full) {
+            any_full = true;
+            A_(salloc(s, &y.Kt, (size_t)a.nkv * (a.hd / 4) * cap));
+            A_(salloc(s, &y.Ks, (size_t)cap * a.nkv));
+            A_(salloc(s, &y.Vq, (size_t)cap * a.nkv * a.hd));
+            A_(salloc(s, &y.Vs, (size_t)cap * a.nkv));
+        } else {
+            A_(salloc(s, &y.S, (size_t)a.nv * a.dk * a.dv));
+            A_(salloc(s, &y.conv, 2 * (size_t)(a.conv_k - 1) * cc));
+        }
+    }
+    if (any_full) {
+        // RoPE cos/sin per (pos, pair) with the reference's libm calls
+        // (ot_rope_partial, src/ornith_tensor.c:167-178)
+        int rot = a.rope_dim;
+        if (rot <= 0 || rot > a.hd) rot = a.hd;
+        const int half = a.hd / 2;
+        std::vector<float2> tab((size_t)cap * half);
+        std::vector<float> freq((size_t)rot / 2);
+        for (int i = 0; i < rot / 2; i++) freq[i] = powf(a.rope_theta, -2.0f * (float)i / (float)rot);
+        for (int p = 0; p < cap; p++)
+            for (int i = 0; i < half; i++) {
+                float2 cs = {1.0f, 0.0f};
+                if (i < rot / 2) {
+                    const float ang = (float)p * freq[i];
+                    cs.x = cosf(ang);
+                    cs.y = sinf(ang);
+                }
+                tab[(size_t)p * half + i] = cs;
+            }
+        A_(salloc(s, &s->rope, tab.size()));
+        hipError_t e = hipMemcpy(s->rope, tab.data(), tab.size() * sizeof(float2), hipMemcpyHostToDevice);
+        if (e != hipSuccess) { ornith_hip_session_free(s); seterr("rope upload: %s", hipGetErrorString(e)); return ORNITH_HIP_ERR_DEVICE; }
+    }
+#undef A_
+    *out = s;
+    return ORNITH_HIP_OK;
+}
+
+// ---- the token step ------------------------------------------------------------------------
+static int enqueue_body(ornith_hip_session *s, hipStream_t st) {
+    const ornith_hip_model *m = s->m;
+    const ornith_hip_arch &a = m->a;
+    const int H = a.hidden, qd = a.nk * a.dk, vd = a.nv * a.dv, cc = 2 * qd + vd;
+    const int32_t *pos = s->io;
+    HCHK(oh_launch_embed(m->embd->A, m->embd->B, m->embd->C, (int)m->embd->type, H, s->toks, pos, s->x, st));
+    for (int l = 0; l < a.n_layers; l++) {
+        const OhLayer &y = m->L[l];
+        LayerState &z = s->ls[l];
+        HCHK(oh_launch_rmsnorm_q8k(s->x, (const float *)y.attn_norm->A, a.eps, H, s->xn, s->xq.qs, s->xq.d, s->xq.bs, st));
+        const Act ax = act_of(s->xq, s->xn);
+        if (y.full) {
+            const int aqd = a.nh * a.hd;
+            MvBuild b;
+            CHK(mv_add(b, y.q, ax, s->qproj, 0));
+            CHK(mv_add(b, y.k, ax, s->kb, 0));
+            CHK(mv_add(b, y.v, ax, s->vb, 0));
+            CHK(mv_go(b, st));
+            HCHK(oh_launch_attn_prep(s->qproj, s->kb, s->vb, (const float *)y.q_norm->A, (const float *)y.k_norm->A,
+                                     s->rope, s->qr, s->agate, z.Kt, z.Ks, z.Vq, z.Vs, pos, a.nh, a.nkv, a.hd,
+                                     a.rope_dim, s->cap, a.eps, st));
+            const float scale = 1.0f / sqrtf((float)a.hd);
+            HCHK(oh_launch_attn_scores(s->qr, z.Kt, z.Ks, s->scores, pos, a.nh, a.nkv, a.hd, s->cap, scale, st));
+            HCHK(oh_launch_attn_out(s->scores, z.Vq, z.Vs, s->agate, s->o, s->oq.qs, s->oq.d, s->oq.bs, pos,
+                                    a.nh, a.nkv, a.hd, s->cap, st));
+            MvBuild b2;
+            CHK(mv_add(b2, y.o, act_of(s->oq, s->o), s->x, 1));
+            CHK(mv_go(b2, st));
+            (void)aqd;
+        } else {
+            MvBuild b;
+            CHK(mv_add(b, y.qkv, ax, s->cat, 0));
+            CHK(mv_add(b, y.gate, ax, s->gate, 0));
+            CHK(mv_add(b, y.alpha, ax, s->ab, 0));
+            CHK(mv_add(b, y.beta, ax, s->ab + a.nv, 0));
+            CHK(mv_go(b, st));
+            const float out_scale = 1.0f / sqrtf((float)a.dk);
+            HCHK(oh_launch_delta_step(a.dk, s->cat, s->gate, s->ab, (const float *)y.conv->A, z.conv,
+                                      (const float *)y.ssm_a->A, (const float *)y.dt_bias->A,
+                                      (const float *)y.ssm_norm->A, z.S, s->o, s->oq.qs, s->oq.d, s->oq.bs, pos,
+                                      a.nk, a.nv, a.conv_k, cc, a.eps, out_scale, st));
+            MvBuild b2;
+            CHK(mv_add(b2, y.ssm_out, act_of(s->oq, s->o), s->x, 1));
+            CHK(mv_go(b2, st));
+        }
+        // FFN: post_attention_norm, then MoE (or dense SwiGLU)
+        HCHK(oh_launch_rmsnorm_q8k(s->x, (const float *)y.post_norm->A, a.eps, H, s->xn, s->xq.qs, s->xq.d, s->xq.bs, st));
+        if (a.ne > 0) {
+            const int K = a.top_k, I = a.moe_inter, sI = a.shared_inter;
+            const int IW = I > sI ? I : sI;   // row stride of the g/u/h buffers
+            MvBuild b;
+            CHK(mv_add(b, y.router, ax, s->rl, 0));
+            if (y.gate_inp_sh) CHK(mv_add(b, y.gate_inp_sh, ax, s->shl, 0));
+            CHK(mv_go(b, st));
+            HCHK(oh_launch_moe_route(s->rl, a.ne, K, y.gate_inp_sh ? s->shl : nullptr, s->eidx, s->ew, s->shg, st));
+            MvBuild b2;
+            for (int k = 0; k < K; k++) {
+                CHK(mv_add(b2, y.gate_exps, ax, s->g + (size_t)k * IW, 0, s->eidx, k));
+                CHK(mv_add(b2, y.up_exps, ax, s->u + (size_t)k * IW, 0, s->eidx, k));
+            }
+            if (y.gate_sh) {
+                CHK(mv_add(b2, y.gate_sh, ax, s->g + (size_t)K * IW, 0));
+                CHK(mv_add(b2, y.up_sh, ax, s->u + (size_t)K * IW, 0));
+            }
+            CHK(mv_go(b2, st));
+            if (I == IW && (!y.gate_sh || sI == IW)) {
+                HCHK(oh_launch_swiglu_q8k(s->g, s->u, IW, K + (y.gate_sh ? 1 : 0), s->h, s->hq.qs, s->hq.d, s->hq.bs, st));
+            } else {
+                // widths differ: quantise each vector at its own width, same IW stride
+                for (int k = 0; k <= K; k++) {
+                    if (k == K && !y.gate_sh) break;
+                    const int n = k < K ? I : sI;
+                    const size_t off = (size_t)k * IW;
+                    HCHK(oh_launch_swiglu_q8k(s->g + off, s->u + off, n, 1, s->h + off, s->hq.qs + off,
+                                              s->hq.d + off / 256, s->hq.bs + off / 16, st));
+                }
+            }
+            MvBuild b3;
+            for (int k = 0; k < K; k++)
+                CHK(mv_add(b3, y.down_exps, act_off(s->hq, s->h, (size_t)k * IW), s->od + (size_t)k * H, 0, s->eidx, k));
+            if (y.gate_sh) CHK(mv_add(b3, y.down_sh, act_off(s->hq, s->h, (size_t)K * IW), s->od + (size_t)K * H, 0));
+            CHK(mv_go(b3, st));
+            HCHK(oh_launch_moe_combine(s->x, s->od, s->ew, K, H, y.gate_sh ? s->od + (size_t)K * H : nullptr,
+                                       y.gate_inp_sh ? s->shg : nullptr, st));
+        } else {
+            const int I = a.shared_inter;
+            MvBuild b;
+            CHK(mv_add(b, y.ffn_gate, ax, s->g, 0));
+            CHK(mv_add(b, y.ffn_up, ax, s->u, 0));
+            CHK(mv_go(b, st));
+            HCHK(oh_launch_swiglu_q8k(s->g, s->u, I, 1, s->h, s->hq.qs, s->hq.d, s->hq.bs, st));
+            MvBuild b2;
+            CHK(mv_add(b2, y.ffn_down, act_of(s->hq, s->h), s->x, 1));
+            CHK(mv_go(b2, st));
+        }
+    }
+    HCHK(oh_launch_advance(s->io, st));
+    return ORNITH_HIP_OK;
+}
+
+static int enqueue_head(ornith_hip_session *s, hipStream_t st) {
+    const ornith_hip_model *m = s->m;
+    const ornith_hip_arch &a = m->a;
+    HCHK(oh_launch_rmsnorm_q8k(s->x, (const float *)m->out_norm->A, a.eps, a.hidden, s->xn, s->xq.qs, s->xq.d, s->xq.bs, st));
+    MvBuild b;
+    CHK(mv_add(b, m->lm_head, act_of(s->xq, s->xn), s->logits, 0));
+    CHK(mv_go(b, st));
+    HCHK(oh_launch_argmax(s->logits, a.vocab, s->amv, s->ami, OH_ARGMAX_BLOCKS, s->toks, s->io, s->io + 1, st));
+    return ORNITH_HIP_OK;
+}
+
+static int capture(ornith_hip_session *s, int (*fn)(ornith_hip_session *, hipStream_t), hipGraphExec_t *out) {
+    hipStream_t st = s->m->ctx->st;
+    hipGraph_t g = nullptr;
+    HCHK(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+    int r = fn(s, st);
+    hipError_t e = hipStreamEndCapture(st, &g);
+    if (r != ORNITH_HIP_OK) { if (g) (void)hipGraphDestroy(g); return r; }
+    if (e != hipSuccess) { seterr("graph capture: %s", hipGetErrorString(e)); return ORNITH_HIP_ERR_DEVICE; }
+    e = hipGraphInstantiate(out, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (e != hipSuccess) { seterr("graph instantiate: %s", hipGetErrorString(e)); return ORNITH_HIP_ERR_DEVICE; }
+    return ORNITH_HIP_OK;
+}
+
+static bool graphs_enabled() {
+    const char *e = getenv("ORNITH_HIP_NO_GRAPH");
+    return !(e && e[0] == '1');
+}
+
+static int run_body(ornith_hip_session *s) {
+    hipStream_t st = s->m->ctx->st;
+    if (graphs_enabled()) {
+        if (!s->gbody) CHK(capture(s, enqueue_body, &s->gbody));
+        HCHK(hipGraphLaunch(s->gbody, st));
+        return ORNITH_HIP_OK;
+    }
+    return enqueue_body(s, st);
+}
+static int run_head(ornith_hip_session *s) {
+    hipStream_t st = s->m->ctx->st;
+    if (graphs_enabled()) {
+        if (!s->ghead) CHK(capture(s, enqueue_head, &s->ghead));
+        HCHK(hipGraphLaunch(s->ghead, st));
+        return ORNITH_HIP_OK;
+    }
+    return enqueue_head(s, st);
+}
+
+static int sync_pos(ornith_hip_session *s) {
+    HCHK(hipMemcpyAsync(s->io, &s->pos, sizeof(int32_t), hipMemcpyHostToDevice, s->m->ctx->st));
+    return ORNITH_HIP_OK;
+}
+
+extern "C" int ornith_hip_session_eval(ornith_hip_session *s, const int32_t *tokens, int n) {
+    if (n <= 0) return ORNITH_HIP_OK;
+    if (s->pos + n > s->cap) {
+        seterr("session capacity %d exceeded (pos %d + %d tokens)", s->cap, s->pos, n);
+        return ORNITH_HIP_ERR_UNSUPPORTED;
+    }
+    for (int i = 0; i < n; i++)
+        if (tokens[i] < 0 || tokens[i] >= s->m->a.vocab) {
+            seterr("token %d at %d outside the vocabulary (%d)", tokens[i], i, s->m->a.vocab);
+            return ORNITH_HIP_ERR_FORMAT;
+        }
+    HCHK(hipSetDevice(s->m->ctx->device));
+    hipStream_t st = s->m->ctx->st;
+    CHK(sync_pos(s));
+    HCHK(hipMemcpyAsync(s->toks + s->pos, tokens, (size_t)n * 4, hipMemcpyHostToDevice, st));
+    for (int i = 0; i < n; i++) CHK(run_body(s));
+    CHK(run_head(s));
+    HCHK(hipStreamSynchronize(st));
+    s->pos += n;
+    s->have_logits = true;
+    return ORNITH_HIP_OK;
+}
+
+extern "C" int ornith_hip_session_step(ornith_hip_session *s, int32_t token) {
+    return ornith_hip_session_eval(s, &token, 1);
+}
+
+extern "C" int ornith_hip_session_logits(ornith_hip_session *s, float *out) {
+    if (!s->have_logits) { seterr("session has no logits; eval a prompt first"); return ORNITH_HIP_ERR_FORMAT; }
+    HCHK(hipSetDevice(s->m->ctx->device));
+    HCHK(hipMemcpyAsync(out, s->logits, (size_t)s->m->a.vocab * 4, hipMemcpyDeviceToHost, s->m->ctx->st));
+    HCHK(hipStreamSynchronize(s->m->ctx->st));
+    return ORNITH_HIP_OK;
+}
+
+extern "C" int ornith_hip_session_pos(const ornith_hip_session *s) { return s->pos; }
+
+extern "C" int ornith_hip_session_generate(ornith_hip_session *s, int n_predict, int32_t *out_tokens,
+                                           int *n_out) {
+    if (n_out) *n_out = 0;
+    if (!s->have_logits) { seterr("session has no logits; eval a prompt first"); return ORNITH_HIP_ERR_FORMAT; }
+    HCHK(hipSetDevice(s->m->ctx->device));
+    hipStream_t st = s->m->ctx->st;
+    int n = n_predict < 0 ? 0 : n_predict;
+    if (n > s->cap - s->pos) n = s->cap - s->pos;
+    CHK(sync_pos(s));
+    const int32_t eos = s->m->a.eos;
+    int emitted = 0;
+    if (eos < 0) {
+        // no stop token: the whole loop stays on the device
+        for (int i = 0; i < n; i++) { CHK(run_body(s)); CHK(run_head(s)); }
+        HCHK(hipMemcpyAsync(out_tokens, s->toks + s->pos, (size_t)n * 4, hipMemcpyDeviceToHost, st));
+        HCHK(hipStreamSynchronize(st));
+        emitted = n;
+    } else {
+        for (int i = 0; i < n; i++) {
+            int32_t next;
+            HCHK(hipMemcpyAsync(&next, s->toks + s->pos + i, 4, hipMemcpyDeviceToHost, st));
+            HCHK(hipStreamSynchronize(st));
+            if (next == eos) break;
+            out_tokens[emitted++] = next;
+            CHK(run_body(s));
+            CHK(run_head(s));
+        }
+        HCHK(hipStreamSynchronize(st));
+    }
+    s->pos += emitted;
+    if (n_out) *n_out = emitted;
+    return ORNITH_HIP_OK;
+}
+
+extern "C" int ornith_hip_session_time_decode(ornith_hip_session *s, int n_steps, float *ms) {
+    if (!s->have_logits) { seterr("session has no logits; eval a prompt first"); return ORNITH_HIP_ERR_FORMAT; }
+    if (n_steps < 0 || s->pos + n_steps > s->cap) { seterr("time_decode: %d steps exceed capacity", n_steps); return ORNITH_HIP_ERR_UNSUPPORTED; }
+    HCHK(hipSetDevice(s->m->ctx->device));
+    hipStream_t st = s->m->ctx->st;
+    CHK(sync_pos(s));
+    if (graphs_enabled()) {
+        if (!s->gbody) CHK(capture(s, enqueue_body, &s->gbody));
+        if (!s->ghead) CHK(capture(s, enqueue_head, &s->ghead));
+    }
+    hipEvent_t e0, e1;
+    HCHK(hipEventCreate(&e0));
+    HCHK(hipEventCreate(&e1));
+    HCHK(hipEventRecord(e0, st));
+    for (int i = 0; i < n_steps; i++) { CHK(run_body(s)); CHK(run_head(s)); }
+    HCHK(hipEventRecord(e1, st));
+    HCHK(hipEventSynchronize(e1));
+    float el = 0.0f;
+    HCHK(hipEventElapsedTime(&el, e0, e1));
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    s->pos += n_steps;
+    *ms = el;
+    return ORNITH_HIP_OK;
+}
+
+// ---- state download in the reference layouts -------------------------------------------------
+extern "C" int ornith_hip_session_get_delta(ornith_hip_session *s, int l, float *S) {
+    const ornith_hip_arch &a = s->m->a;
+    if (l < 0 || l >= a.n_layers || s->m->L[l].full) { seterr("layer %d has no delta state", l); return ORNITH_HIP_ERR_NOTFOUND; }
+    HCHK(hipSetDevice(s->m->ctx->device));
+    const size_t per = (size_t)a.dk * a.dv;
+    std::vector<float> t((size_t)a.nv * per);
+    HCHK(hipMemcpy(t.data(), s->ls[l].S, t.size() * 4, hipMemcpyDeviceToHost));
+    for (int h = 0; h < a.nv; h++)        // device [h][c][r] -> reference [h][r][c]
+        for (int r = 0; r < a.dv; r++)
+            for (int c = 0; c < a.dk; c++) S[h * per + (size_t)r * a.dk + c] = t[h * per + (size_t)c * a.dv + r];
+    return ORNITH_HIP_OK;
+}
+
+extern "C" int ornith_hip_session_get_conv(ornith_hip_session *s, int l, float *win) {
+    const ornith_hip_arch &a = s->m->a;
+    if (l < 0 || l >= a.n_layers || s->m->L[l].full) { seterr("layer %d has no conv state", l); return ORNITH_HIP_ERR_NOTFOUND; }
+    HCHK(hipSetDevice(s->m->ctx->device));
+    const size_t cc = (size_t)(2 * a.nk * a.dk + a.nv * a.dv), wsz = (size_t)(a.conv_k - 1) * cc;
+    // the window written by the last step lives in parity (pos & 1)
+    HCHK(hipMemcpy(win, s->ls[l].conv + (size_t)(s->pos & 1) * wsz, wsz * 4, hipMemcpyDeviceToHost));
+    return ORNITH_HIP_OK;
+}
+
+extern "C" int ornith_hip_session_get_kv(ornith_hip_session *s, int l, int8_t *Kq, float *Ks,
+                                         int8_t *Vq, float *Vs) {
+    const ornith_hip_arch &a = s->m->a;
+    if (l < 0 || l >= a.n_layers || !s->m->L[l].full) { seterr("layer %d has no KV cache", l); return ORNITH_HIP_ERR_NOTFOUND; }
+    HCHK(hipSetDevice(s->m->ctx->device));
+    const int len = s->pos, cap = s->cap, hd = a.hd, nkv = a.nkv;
+    std::vector<uint32_t> kt((size_t)nkv * (hd / 4) * cap);
+    HCHK(hipMemcpy(kt.data(), s->ls[l].Kt, kt.size() * 4, hipMemcpyDeviceToHost));
+    for (int t = 0; t < len; t++)
+        for (int h = 0; h < nkv; h++)
+            for (int i = 0; i < hd; i++) {
+                const uint32_t w = kt[((size_t)h * (hd / 4) + i / 4) * cap + t];
+                Kq[((size_t)t * nkv + h) * hd + i] = (int8_t)((w >> (8 * (i & 3))) & 0xff);
+            }
+    HCHK(hipMemcpy(Ks, s->ls[l].Ks, (size_t)len * nkv * 4, hipMemcpyDeviceToHost));
+    HCHK(hipMemcpy(Vq, s->ls[l].Vq, (size_t)len * nkv * hd, hipMemcpyDeviceToHost));
+    HCHK(hipMemcpy(Vs, s->ls[l].Vs, (size_t)len * nkv * 4, hipMemcpyDeviceToHost));
+    return ORNITH_HIP_OK;
+}
+
+extern "C" int ornith_hip_model_synth(ornith_hip_ctx *ctx, const ornith_hip_gen_cfg *cfg,
+                                      ornith_hip_model **out) {
+    (void)ctx; (void)cfg;
+    *out = nullptr;
+    seterr("model_synth: not built yet");
+    return ORNITH_HIP_ERR_UNSUPPORTED;
+}

@@ -1,0 +1,117 @@
+// oh_kernels.hip - the single device translation unit of the engine: the
+// kernels of oh_mv.hip and oh_layers.hip plus their host launchers.
+#include "oh_mv.hip"
+#include "oh_layers.hip"
+#include "oh_launch.h"
+
+extern "C" {
+
+hipError_t oh_launch_matvec(const oh_mvlaunch *L, int lds_floats, hipStream_t st) {
+    if (L->total_blocks <= 0) return hipSuccess;
+    hipLaunchKernelGGL(oh_k_matvec, dim3(L->total_blocks), dim3(256),
+                       (size_t)lds_floats * sizeof(float), st, *L);
+    return hipGetLastError();
+}
+
+hipError_t oh_launch_rmsnorm_q8k(const float *x, const float *norm_w, float eps, int n,
+                                 float *xn_out, int8_t *qs, float *d, int16_t *bs, hipStream_t st) {
+    hipLaunchKernelGGL(oh_k_rmsnorm_q8k, dim3(1), dim3(256), 0, st, x, norm_w, eps, n, xn_out, qs, d, bs);
+    return hipGetLastError();
+}
+
+hipError_t oh_launch_swiglu_q8k(const float *g, const float *u, int n, int count, float *h_out,
+                                int8_t *qs, float *d, int16_t *bs, hipStream_t st) {
+    hipLaunchKernelGGL(oh_k_swiglu_q8k, dim3(count), dim3(256), 0, st, g, u, n, h_out, qs, d, bs);
+    return hipGetLastError();
+}
+
+hipError_t oh_launch_dequant(const uint8_t *A, const uint8_t *B, const uint8_t *C, int type, int in,
+                             int64_t row0, int64_t nrows, float *out, hipStream_t st) {
+    const int64_t n = nrows * in;
+    int64_t blocks = (n + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    if (blocks < 1) blocks = 1;
+    hipLaunchKernelGGL(oh_k_dequant, dim3((unsigned)blocks), dim3(256), 0, st, A, B, C, type, in, row0, nrows, out);
+    return hipGetLastError();
+}
+
+hipError_t oh_launch_embed(const uint8_t *A, const uint8_t *B, const uint8_t *C, int type, int in,
+                           const int32_t *toks, const int32_t *io_pos, float *x, hipStream_t st) {
+    hipLaunchKernelGGL(oh_k_embed, dim3((in + 255) / 256), dim3(256), 0, st, A, B, C, type, in, toks, io_pos, x);
+    return hipGetLastError();
+}
+
+hipError_t oh_launch_delta_step(int dk, const float *cat, const float *gate, const float *ab,
+                                const float *conv_w, float *conv_state, const float *ssm_a,
+                                const float *dt_bias, const float *ssm_norm, float *S, float *out,
+                                int8_t *oqs, float *oqd, int16_t *oqb, const int32_t *io_pos,
+                                int nk, int nv, int K, int cc, float eps, float out_scale,
+                                hipStream_t st) {
+    if (dk == 128) {
+        hipLaunchKernelGGL(oh_k_delta_step<128>, dim3(nv / 2), dim3(256), 0, st, cat, gate, ab, conv_w,
+                           conv_state, ssm_a, dt_bias, ssm_norm, S, out, oqs, oqd, oqb, io_pos, nk, nv, K,
+                           cc, eps, out_scale);
+    } else if (dk == 64) {
+        hipLaunchKernelGGL(oh_k_delta_step<64>, dim3(nv / 4), dim3(256), 0, st, cat, gate, ab, conv_w,
+                           conv_state, ssm_a, dt_bias, ssm_norm, S, out, oqs, oqd, oqb, io_pos, nk, nv, K,
+                           cc, eps, out_scale);
+    } else {
+        return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t oh_launch_attn_prep(const float *qproj, const float *kin, const float *vin,
+                               const float *q_norm, const float *k_norm, const float2 *rope,
+                               float *qr, float *gate, uint32_t *Kt, float *Ks, int8_t *Vq,
+                               float *Vs, const int32_t *io_pos, int nh, int nkv, int hd,
+                               int rot, int cap, float eps, hipStream_t st) {
+    hipLaunchKernelGGL(oh_k_attn_prep, dim3(nh + nkv), dim3(256), 0, st, qproj, kin, vin, q_norm, k_norm,
+                       rope, qr, gate, Kt, Ks, Vq, Vs, io_pos, nh, nkv, hd, rot, cap, eps);
+    return hipGetLastError();
+}
+
+hipError_t oh_launch_attn_scores(const float *qr, const uint32_t *Kt, const float *Ks,
+                                 float *scores, const int32_t *io_pos, int nh, int nkv, int hd,
+                                 int cap, float scale, hipStream_t st) {
+    hipLaunchKernelGGL(oh_k_attn_scores, dim3(nh, (cap + 255) / 256), dim3(256), 0, st, qr, Kt, Ks,
+                       scores, io_pos, nh, nkv, hd, cap, scale);
+    return hipGetLastError();
+}
+
+hipError_t oh_launch_attn_out(float *scores, const int8_t *Vq, const float *Vs, const float *gate,
+                              float *out, int8_t *oqs, float *oqd, int16_t *oqb,
+                              const int32_t *io_pos, int nh, int nkv, int hd, int cap,
+                              hipStream_t st) {
+    const int hpb = 256 / hd;
+    hipLaunchKernelGGL(oh_k_attn_out, dim3(nh / hpb), dim3(256), 0, st, scores, Vq, Vs, gate, out, oqs,
+                       oqd, oqb, io_pos, nh, nkv, hd, cap);
+    return hipGetLastError();
+}
+
+hipError_t oh_launch_moe_route(const float *logits, int ne, int k, const float *shgate_logit,
+                               int32_t *idx, float *w, float *shgate, hipStream_t st) {
+    hipLaunchKernelGGL(oh_k_moe_route, dim3(1), dim3(64), 0, st, logits, ne, k, shgate_logit, idx, w, shgate);
+    return hipGetLastError();
+}
+
+hipError_t oh_launch_moe_combine(float *x, const float *o, const float *w, int k, int H,
+                                 const float *so, const float *shgate, hipStream_t st) {
+    hipLaunchKernelGGL(oh_k_moe_combine, dim3((H + 255) / 256), dim3(256), 0, st, x, o, w, k, H, so, shgate);
+    return hipGetLastError();
+}
+
+hipError_t oh_launch_argmax(const float *v, int n, float *tmp_v, int *tmp_i, int nblk,
+                            int32_t *toks, const int32_t *io_pos, int32_t *io_best,
+                            hipStream_t st) {
+    hipLaunchKernelGGL(oh_k_argmax1, dim3(nblk), dim3(256), 0, st, v, n, tmp_v, tmp_i);
+    hipLaunchKernelGGL(oh_k_argmax2, dim3(1), dim3(64), 0, st, tmp_v, tmp_i, nblk, toks, io_pos, io_best);
+    return hipGetLastError();
+}
+
+hipError_t oh_launch_advance(int32_t *io_pos, hipStream_t st) {
+    hipLaunchKernelGGL(oh_k_advance, dim3(1), dim3(1), 0, st, io_pos);
+    return hipGetLastError();
+}
+
+} // extern "C"

@@ -1,0 +1,132 @@
+"""GPU: the whole decode step on the C1 config (tiny all-Q8_0 qwen35moe).
+
+Oracle: the reference's token path (rforward_token; prompt with
+ORNITH_PREFILL_SERIAL=1, Q8 KV). Bar: bit-exact prompt logits, per-step
+logits and 64 greedy tokens against the reference's golden fixture, and
+bit-exact session state (delta state, conv window, Q8 KV) against the
+oracle. The reference's default chunked prefill differs from its own token
+path by ~1.7% relative L2 on this model (an int8 activation code flips), so
+against that mode only the report is asserted loosely.
+"""
+import ctypes as C
+import hashlib
+
+import numpy as np
+import pytest
+
+import clibs
+from clibs import f32p, i32p
+
+pytestmark = pytest.mark.gpu
+GOLD = np.load(clibs.ROOT / "tests" / "golden" / "c1.npz")
+
+
+def u32(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+@pytest.fixture(scope="module")
+def c1(tmp_path_factory, hip_ctx):
+    p = tmp_path_factory.mktemp("c1") / "c1.gguf"
+    clibs.write_c1_gguf(p)
+    assert hashlib.sha256(p.read_bytes()).hexdigest() == str(GOLD["gguf_sha256"])
+    m = hip_ctx.load(str(p))
+    yield p, m
+    m.free()
+
+
+def test_c1_arch(c1):
+    _, m = c1
+    a = m.arch
+    assert (a["hidden"], a["n_layers"], a["vocab"], a["nh"], a["nkv"], a["hd"], a["nk"], a["nv"],
+            a["dk"], a["ne"], a["top_k"], a["moe_inter"], a["shared_inter"], a["eos"]) == \
+        (512, 4, 4096, 8, 2, 64, 4, 8, 64, 16, 4, 256, 256, -1)
+
+
+def test_c1_prompt_and_greedy_bitexact(c1):
+    _, m = c1
+    s = m.session(104)
+    s.eval(GOLD["prompt"])
+    assert np.array_equal(u32(s.logits()), u32(GOLD["serial_prompt_logits"]))
+    toks = s.generate(64)
+    assert np.array_equal(toks, GOLD["serial_tokens"])
+    assert np.array_equal(u32(s.logits()), u32(GOLD["serial_trace_logits"][-1]))
+    assert s.pos == 32 + 64
+    s.free()
+
+
+def test_c1_stepwise_logits_bitexact(c1):
+    _, m = c1
+    s = m.session(104)
+    s.eval(GOLD["prompt"])
+    steps = list(GOLD["serial_trace_steps"])
+    tok = int(np.argmax(s.logits()))
+    for k in range(64):
+        s.step(tok)
+        lg = s.logits()
+        if k in steps:
+            assert np.array_equal(u32(lg), u32(GOLD["serial_trace_logits"][steps.index(k)])), k
+        tok = int(np.argmax(lg))
+    s.free()
+
+
+def test_c1_state_bitexact_vs_oracle(c1, orc):
+    path, m = c1
+    om = C.c_void_p()
+    assert orc.orc_model_load(str(path).encode(), C.byref(om)) == 0
+    orc.orc_model_set_threads(om, 8)
+    os_ = orc.orc_session_new(om, 40, 1)
+    p = np.ascontiguousarray(GOLD["prompt"][:20])
+    assert orc.orc_session_eval(os_, i32p(p), 20, 1) == 0
+    s = m.session(40)
+    s.eval(p)
+    a = m.arch
+    cc = 2 * a["nk"] * a["dk"] + a["nv"] * a["dv"]
+    for layer in range(a["n_layers"]):
+        if layer % a["full_interval"] == a["full_interval"] - 1:
+            kq, ks, vq, vs = s.kv(layer)
+            kv = orc.orc_session_kv(os_, layer).contents
+            n = 20 * a["nkv"] * a["hd"]
+            assert np.array_equal(kq, np.ctypeslib.as_array(kv.Kq, (n,)))
+            assert np.array_equal(vq, np.ctypeslib.as_array(kv.Vq, (n,)))
+            assert np.array_equal(u32(ks), u32(np.ctypeslib.as_array(kv.Ks, (20 * a["nkv"],))))
+            assert np.array_equal(u32(vs), u32(np.ctypeslib.as_array(kv.Vs, (20 * a["nkv"],))))
+        else:
+            S = np.ctypeslib.as_array(orc.orc_session_delta(os_, layer), (a["nv"] * a["dv"] * a["dk"],))
+            assert np.array_equal(u32(s.delta_state(layer)), u32(S)), layer
+            W = np.ctypeslib.as_array(orc.orc_session_conv(os_, layer), ((a["conv_k"] - 1) * cc,))
+            assert np.array_equal(u32(s.conv_state(layer)), u32(W)), layer
+    s.free()
+    orc.orc_session_free(os_)
+    orc.orc_model_free(om)
+
+
+def test_c1_against_chunked_reference_mode(c1):
+    """Reported, not bit-exact: the reference's chunked prefill itself departs
+    from its token path on this model."""
+    _, m = c1
+    s = m.session(104)
+    s.eval(GOLD["prompt"])
+    lg = s.logits()
+    ref = GOLD["chunked_prompt_logits"]
+    rel = float(np.linalg.norm(lg - ref) / np.linalg.norm(ref))
+    ser = GOLD["serial_prompt_logits"]
+    ref_gap = float(np.linalg.norm(ser - ref) / np.linalg.norm(ref))
+    print(f"C1 prompt logits vs chunked reference: rel L2 {rel:.3e} (reference serial vs chunked: {ref_gap:.3e})")
+    assert abs(rel - ref_gap) < 1e-6 and int(np.argmax(lg)) == int(np.argmax(ref))
+    s.free()
+
+
+def test_session_errors(c1):
+    import ornithology_amd as oa
+    _, m = c1
+    s = m.session(8)
+    with pytest.raises(oa.HipError):
+        s.eval(np.arange(9, dtype=np.int32))            # capacity
+    with pytest.raises(oa.HipError):
+        s.eval(np.int32([5000]))                         # outside the vocabulary
+    with pytest.raises(oa.HipError):
+        s.logits()                                       # nothing evaluated yet
+    s.eval(np.int32([1, 2, 3]))
+    assert s.pos == 3
+    s.free()
