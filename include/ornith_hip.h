@@ -75,6 +75,7 @@ const char *ornith_hip_last_error(void);            /* ornith_last_error, src/or
 
 int  ornith_hip_init(int device, ornith_hip_ctx **out);
 void ornith_hip_free(ornith_hip_ctx *ctx);
+int  ornith_hip_sync(ornith_hip_ctx *ctx);            /* wait for all work on the device */
 
 /* ---- ornith_qdot / codecs (kernel-level boundary) --------------------------- */
 
@@ -85,6 +86,9 @@ int  ornith_hip_upload(ornith_hip_ctx *ctx, const char *name, uint32_t ggml_type
                        const void *host_bytes, uint64_t nbytes, uint32_t n_dims,
                        const uint64_t *dims, ornith_hip_tensor **out);
 void ornith_hip_tensor_free(ornith_hip_tensor *t);
+/* Inverse of upload: the tensor's bytes in GGUF block order (nbytes must be
+ * the GGUF size), e.g. to compare a synthesised tensor with a GGUF file. */
+int  ornith_hip_tensor_download(const ornith_hip_tensor *t, void *gguf_bytes, uint64_t nbytes);
 
 /* qdot_quantize_row_q8_K (src/ornith_qdot.h:36-38): k % 256 == 0. */
 int  ornith_hip_quantize_q8K(ornith_hip_ctx *ctx, const float *x, int64_t k,
@@ -157,6 +161,13 @@ int  ornith_hip_session_get_kv(ornith_hip_session *s, int layer, int8_t *Kq,
  * graph replayed back to back, the next token chosen on the device) with HIP
  * events on the session stream; *ms = total elapsed. Advances the session. */
 int  ornith_hip_session_time_decode(ornith_hip_session *s, int n_steps, float *ms);
+/* Run one greedy decode step eagerly with HIP events around every kernel
+ * launch: kinds[i] (0 matvec, 1 rmsnorm+Q8_K, 2 SwiGLU+Q8_K, 3 embed, 4 delta
+ * step, 5 attn prep, 6 attn scores, 7 attn out, 8 router, 9 MoE combine,
+ * 10 argmax, 11 advance), algorithmic HBM bytes[i] and ms[i]. Advances the
+ * session by one position. */
+int  ornith_hip_session_profile_step(ornith_hip_session *s, int max_launches, int32_t *kinds,
+                                     double *bytes, float *ms, int *n_launches);
 /* Time `iters` launches of one matvec of W (activation already quantised on
  * the device) with HIP events on the context stream; *ms = mean per launch. */
 int  ornith_hip_time_matvec(ornith_hip_ctx *ctx, const ornith_hip_tensor *W, int iters,

@@ -62,9 +62,11 @@ _SIGS = {
     "ornith_hip_last_error": (C.c_char_p, []),
     "ornith_hip_init": (C.c_int, [C.c_int, C.POINTER(_vp)]),
     "ornith_hip_free": (None, [_vp]),
+    "ornith_hip_sync": (C.c_int, [_vp]),
     "ornith_hip_upload": (C.c_int, [_vp, C.c_char_p, C.c_uint32, _vp, C.c_uint64, C.c_uint32,
                                     C.POINTER(C.c_uint64), C.POINTER(_vp)]),
     "ornith_hip_tensor_free": (None, [_vp]),
+    "ornith_hip_tensor_download": (C.c_int, [_vp, _vp, C.c_uint64]),
     "ornith_hip_quantize_q8K": (C.c_int, [_vp, _fp, C.c_int64, _vp]),
     "ornith_hip_matvec": (C.c_int, [_vp, _vp, _fp, _fp, C.c_int]),
     "ornith_hip_dequant": (C.c_int, [_vp, _vp, C.c_int64, C.c_int64, _fp]),
@@ -90,6 +92,7 @@ _SIGS = {
     "ornith_hip_session_get_kv": (C.c_int, [_vp, C.c_int, _vp, _fp, _vp, _fp]),
     "ornith_hip_session_time_decode": (C.c_int, [_vp, C.c_int, _fp]),
     "ornith_hip_time_matvec": (C.c_int, [_vp, _vp, C.c_int, _fp]),
+    "ornith_hip_session_profile_step": (C.c_int, [_vp, C.c_int, _ip, C.POINTER(C.c_double), _fp, _ip]),
 }
 
 _lib = None
@@ -134,6 +137,9 @@ class Context:
         h = _vp()
         _check(L.ornith_hip_init(device, C.byref(h)), "ornith_hip_init")
         self.h = h
+
+    def sync(self) -> None:
+        _check(lib().ornith_hip_sync(self.h), "ornith_hip_sync")
 
     def close(self):
         if self.h:
@@ -206,6 +212,13 @@ class Tensor:
         nrows = self.rows - row0 if nrows is None else nrows
         out = np.zeros(nrows * self.cols, np.float32)
         _check(lib().ornith_hip_dequant(self.ctx.h, self.h, row0, nrows, _f32(out)), "ornith_hip_dequant")
+        return out
+
+    def download(self, nbytes: int) -> np.ndarray:
+        """The tensor's bytes in GGUF block order."""
+        out = np.zeros(nbytes, np.uint8)
+        _check(lib().ornith_hip_tensor_download(self.h, C.c_void_p(out.ctypes.data), nbytes),
+               "ornith_hip_tensor_download")
         return out
 
     def time_matvec(self, iters: int) -> float:
@@ -294,6 +307,22 @@ class Session:
         ms = C.c_float(0)
         _check(lib().ornith_hip_session_time_decode(self.h, n_steps, C.byref(ms)), "ornith_hip_session_time_decode")
         return ms.value
+
+    KERNEL_KINDS = ("matvec", "rmsnorm_q8k", "swiglu_q8k", "embed", "delta_step", "attn_prep",
+                    "attn_scores", "attn_out", "moe_route", "moe_combine", "argmax", "advance")
+
+    def profile_step(self, max_launches: int = 4096):
+        """One eager decode step with per-launch HIP-event timing: list of
+        (kind, algorithmic bytes, ms)."""
+        kinds = np.zeros(max_launches, np.int32)
+        byts = np.zeros(max_launches, np.float64)
+        ms = np.zeros(max_launches, np.float32)
+        n = C.c_int32(0)
+        _check(lib().ornith_hip_session_profile_step(self.h, max_launches, _i32(kinds),
+                                                     byts.ctypes.data_as(C.POINTER(C.c_double)), _f32(ms),
+                                                     C.byref(n)), "ornith_hip_session_profile_step")
+        k = n.value
+        return [(self.KERNEL_KINDS[kinds[i]], float(byts[i]), float(ms[i])) for i in range(k)]
 
     def delta_state(self, layer: int) -> np.ndarray:
         a = self.model.arch

@@ -90,6 +90,12 @@ extern "C" int ornith_hip_init(int device, ornith_hip_ctx **out) {
     return ORNITH_HIP_OK;
 }
 
+extern "C" int ornith_hip_sync(ornith_hip_ctx *c) {
+    HCHK(hipSetDevice(c->device));
+    HCHK(hipDeviceSynchronize());
+    return ORNITH_HIP_OK;
+}
+
 extern "C" void ornith_hip_free(ornith_hip_ctx *c) {
     if (!c) return;
     (void)hipSetDevice(c->device);
@@ -268,6 +274,7 @@ struct Act {
 struct MvBuild {
     oh_mvlaunch L;
     int lds = 0;
+    double bytes = 0.0;    // algorithmic HBM bytes: weights read + activation + output
     MvBuild() { memset(&L, 0, sizeof L); }
 };
 
@@ -302,6 +309,10 @@ static int mv_add(MvBuild &b, const ornith_hip_tensor *W, const Act &act, float 
     s.block0 = b.L.total_blocks;
     b.L.total_blocks += blocks;
     b.L.n++;
+    b.bytes += (double)s.rows * (double)gguf_nbytes(W->type, (uint64_t)W->in) +
+               (act.qs && oh_qdot_can(W->type, W->in) ? (double)W->in * (1.0 + 4.0 / 256 + 32.0 / 256)
+                                                     : (double)W->in * 4.0) +
+               (double)s.rows * 4.0 * (mode == 1 ? 2.0 : 1.0);
     return ORNITH_HIP_OK;
 }
 
@@ -794,7 +805,7 @@ struct LayerState {
 
 struct ornith_hip_session {
     ornith_hip_model *m = nullptr;
-    int cap = 0, pos = 0;
+    int cap = 0, pos = 0, kvcap = 0;
     bool have_logits = false;
     std::vector<void *> allocs;
     int32_t *io = nullptr;        // [0] pos, [1] best
@@ -815,7 +826,46 @@ struct ornith_hip_session {
     std::vector<LayerState> ls;
     hipGraphExec_t gbody = nullptr, ghead = nullptr;
     bool graphs_tried = false;
+    // per-launch timing of an eager step (profile_step): events around each launch
+    bool rec = false;
+    std::vector<hipEvent_t> rec_ev;
+    std::vector<int> rec_kind;
+    std::vector<double> rec_bytes;
 };
+
+enum { K_MATVEC = 0, K_NORM_Q8K, K_SWIGLU_Q8K, K_EMBED, K_DELTA, K_ATTN_PREP, K_ATTN_SCORES,
+       K_ATTN_OUT, K_ROUTE, K_COMBINE, K_ARGMAX, K_ADVANCE };
+
+static int rec_begin(ornith_hip_session *s, hipStream_t st) {
+    if (!s->rec) return ORNITH_HIP_OK;
+    hipEvent_t e;
+    HCHK(hipEventCreate(&e));
+    HCHK(hipEventRecord(e, st));
+    s->rec_ev.push_back(e);
+    return ORNITH_HIP_OK;
+}
+static int rec_end(ornith_hip_session *s, hipStream_t st, int kind, double bytes) {
+    if (!s->rec) return ORNITH_HIP_OK;
+    hipEvent_t e;
+    HCHK(hipEventCreate(&e));
+    HCHK(hipEventRecord(e, st));
+    s->rec_ev.push_back(e);
+    s->rec_kind.push_back(kind);
+    s->rec_bytes.push_back(bytes);
+    return ORNITH_HIP_OK;
+}
+#define LAUNCH(kind, bytes, call)           \
+    do {                                    \
+        CHK(rec_begin(s, st));              \
+        HCHK(call);                         \
+        CHK(rec_end(s, st, kind, bytes));   \
+    } while (0)
+#define MVGO(b)                                        \
+    do {                                               \
+        CHK(rec_begin(s, st));                         \
+        CHK(mv_go(b, st));                             \
+        CHK(rec_end(s, st, K_MATVEC, (b).bytes));      \
+    } while (0)
 
 extern "C" void ornith_hip_session_free(ornith_hip_session *s) {
     if (!s) return;
@@ -856,6 +906,7 @@ extern "C" int ornith_hip_session_new(ornith_hip_model *m, int cap, ornith_hip_s
     auto *s = new ornith_hip_session();
     s->m = m;
     s->cap = cap;
+    s->kvcap = (cap + 15) / 16 * 16;   // KV storage stride (V is tiled by 16 positions)
     const int H = a.hidden, qd = a.nk * a.dk, vd = a.nv * a.dv, cc = 2 * qd + vd;
     const int aq = a.nh * a.hd, kvd = a.nkv * a.hd;
     const int K = a.top_k, I = a.moe_inter > a.shared_inter ? a.moe_inter : a.shared_inter;
@@ -870,7 +921,7 @@ extern "C" int ornith_hip_session_new(ornith_hip_model *m, int cap, ornith_hip_s
     A_(salloc(s, &s->o, ow)); A_(q8alloc(s, s->oq, ow));
     A_(salloc(s, &s->qproj, 2 * (size_t)aq)); A_(salloc(s, &s->kb, kvd)); A_(salloc(s, &s->vb, kvd));
     A_(salloc(s, &s->qr, aq)); A_(salloc(s, &s->agate, aq));
-    A_(salloc(s, &s->scores, (size_t)a.nh * cap));
+    A_(salloc(s, &s->scores, (size_t)a.nh * s->kvcap));
     A_(salloc(s, &s->rl, a.ne > 0 ? a.ne : 1)); A_(salloc(s, &s->shl, 1)); A_(salloc(s, &s->shg, 1));
     A_(salloc(s, &s->ew, 64)); A_(salloc(s, &s->eidx, 64));
     const size_t nvec = (size_t)(K + 1);
@@ -885,10 +936,10 @@ extern "C" int ornith_hip_session_new(ornith_hip_model *m, int cap, ornith_hip_s
         LayerState &y = s->ls[l];
         if (m->L[l].full) {
             any_full = true;
-            A_(salloc(s, &y.Kt, (size_t)a.nkv * (a.hd / 4) * cap));
-            A_(salloc(s, &y.Ks, (size_t)cap * a.nkv));
-            A_(salloc(s, &y.Vq, (size_t)cap * a.nkv * a.hd));
-            A_(salloc(s, &y.Vs, (size_t)cap * a.nkv));
+            A_(salloc(s, &y.Kt, (size_t)a.nkv * (a.hd / 4) * s->kvcap));
+            A_(salloc(s, &y.Ks, (size_t)s->kvcap * a.nkv));
+            A_(salloc(s, &y.Vq, (size_t)s->kvcap * a.nkv * a.hd));
+            A_(salloc(s, &y.Vs, (size_t)s->kvcap * a.nkv));
         } else {
             A_(salloc(s, &y.S, (size_t)a.nv * a.dk * a.dv));
             A_(salloc(s, &y.conv, 2 * (size_t)(a.conv_k - 1) * cc));
@@ -923,61 +974,74 @@ extern "C" int ornith_hip_session_new(ornith_hip_model *m, int cap, ornith_hip_s
 }
 
 // ---- the token step ------------------------------------------------------------------------
+// Algorithmic bytes of the small kernels (recorded by profile_step only).
+static double norm_bytes(int n, bool w) { return (double)n * (4.0 + (w ? 4.0 : 0.0) + 4.0 + 1.0 + 4.0 / 256 + 2.0 / 16); }
+
 static int enqueue_body(ornith_hip_session *s, hipStream_t st) {
     const ornith_hip_model *m = s->m;
     const ornith_hip_arch &a = m->a;
     const int H = a.hidden, qd = a.nk * a.dk, vd = a.nv * a.dv, cc = 2 * qd + vd;
     const int32_t *pos = s->io;
-    HCHK(oh_launch_embed(m->embd->A, m->embd->B, m->embd->C, (int)m->embd->type, H, s->toks, pos, s->x, st));
+    const double T = (double)(s->pos + 1);
+    LAUNCH(K_EMBED, (double)gguf_nbytes(m->embd->type, (uint64_t)H) + 4.0 * H,
+           oh_launch_embed(m->embd->A, m->embd->B, m->embd->C, (int)m->embd->type, H, s->toks, pos, s->x, st));
     for (int l = 0; l < a.n_layers; l++) {
         const OhLayer &y = m->L[l];
         LayerState &z = s->ls[l];
-        HCHK(oh_launch_rmsnorm_q8k(s->x, (const float *)y.attn_norm->A, a.eps, H, s->xn, s->xq.qs, s->xq.d, s->xq.bs, st));
+        LAUNCH(K_NORM_Q8K, norm_bytes(H, true),
+               oh_launch_rmsnorm_q8k(s->x, (const float *)y.attn_norm->A, a.eps, H, s->xn, s->xq.qs, s->xq.d, s->xq.bs, st));
         const Act ax = act_of(s->xq, s->xn);
         if (y.full) {
-            const int aqd = a.nh * a.hd;
+            const int aqd = a.nh * a.hd, kvd = a.nkv * a.hd;
             MvBuild b;
             CHK(mv_add(b, y.q, ax, s->qproj, 0));
             CHK(mv_add(b, y.k, ax, s->kb, 0));
             CHK(mv_add(b, y.v, ax, s->vb, 0));
-            CHK(mv_go(b, st));
-            HCHK(oh_launch_attn_prep(s->qproj, s->kb, s->vb, (const float *)y.q_norm->A, (const float *)y.k_norm->A,
-                                     s->rope, s->qr, s->agate, z.Kt, z.Ks, z.Vq, z.Vs, pos, a.nh, a.nkv, a.hd,
-                                     a.rope_dim, s->cap, a.eps, st));
+            MVGO(b);
+            LAUNCH(K_ATTN_PREP, 4.0 * (2.0 * aqd + 2.0 * kvd + 2.0 * a.hd) + 8.0 * aqd + 2.0 * (kvd + 4.0 * a.nkv),
+                   oh_launch_attn_prep(s->qproj, s->kb, s->vb, (const float *)y.q_norm->A, (const float *)y.k_norm->A,
+                                       s->rope, s->qr, s->agate, z.Kt, z.Ks, z.Vq, z.Vs, pos, a.nh, a.nkv, a.hd,
+                                       a.rope_dim, s->kvcap, a.eps, st));
             const float scale = 1.0f / sqrtf((float)a.hd);
-            HCHK(oh_launch_attn_scores(s->qr, z.Kt, z.Ks, s->scores, pos, a.nh, a.nkv, a.hd, s->cap, scale, st));
-            HCHK(oh_launch_attn_out(s->scores, z.Vq, z.Vs, s->agate, s->o, s->oq.qs, s->oq.d, s->oq.bs, pos,
-                                    a.nh, a.nkv, a.hd, s->cap, st));
+            LAUNCH(K_ATTN_SCORES, T * a.nkv * (a.hd + 4.0) + 4.0 * T * a.nh + 4.0 * aqd,
+                   oh_launch_attn_scores(s->qr, z.Kt, z.Ks, s->scores, pos, a.nh, a.nkv, a.hd, s->kvcap, scale, st));
+            LAUNCH(K_ATTN_OUT, T * a.nkv * (a.hd + 4.0) + 8.0 * T * a.nh + 9.0 * aqd,
+                   oh_launch_attn_out(s->scores, z.Vq, z.Vs, s->agate, s->o, s->oq.qs, s->oq.d, s->oq.bs, pos,
+                                      a.nh, a.nkv, a.hd, s->kvcap, st));
             MvBuild b2;
             CHK(mv_add(b2, y.o, act_of(s->oq, s->o), s->x, 1));
-            CHK(mv_go(b2, st));
-            (void)aqd;
+            MVGO(b2);
         } else {
             MvBuild b;
             CHK(mv_add(b, y.qkv, ax, s->cat, 0));
             CHK(mv_add(b, y.gate, ax, s->gate, 0));
             CHK(mv_add(b, y.alpha, ax, s->ab, 0));
             CHK(mv_add(b, y.beta, ax, s->ab + a.nv, 0));
-            CHK(mv_go(b, st));
+            MVGO(b);
             const float out_scale = 1.0f / sqrtf((float)a.dk);
-            HCHK(oh_launch_delta_step(a.dk, s->cat, s->gate, s->ab, (const float *)y.conv->A, z.conv,
-                                      (const float *)y.ssm_a->A, (const float *)y.dt_bias->A,
-                                      (const float *)y.ssm_norm->A, z.S, s->o, s->oq.qs, s->oq.d, s->oq.bs, pos,
-                                      a.nk, a.nv, a.conv_k, cc, a.eps, out_scale, st));
+            const double sb = 8.0 * a.nv * a.dk * a.dv + 8.0 * (a.conv_k - 1) * cc + 4.0 * cc * (a.conv_k + 1) +
+                              4.0 * vd * 3 + 1.1 * vd;
+            LAUNCH(K_DELTA, sb,
+                   oh_launch_delta_step(a.dk, s->cat, s->gate, s->ab, (const float *)y.conv->A, z.conv,
+                                        (const float *)y.ssm_a->A, (const float *)y.dt_bias->A,
+                                        (const float *)y.ssm_norm->A, z.S, s->o, s->oq.qs, s->oq.d, s->oq.bs, pos,
+                                        a.nk, a.nv, a.conv_k, cc, a.eps, out_scale, st));
             MvBuild b2;
             CHK(mv_add(b2, y.ssm_out, act_of(s->oq, s->o), s->x, 1));
-            CHK(mv_go(b2, st));
+            MVGO(b2);
         }
         // FFN: post_attention_norm, then MoE (or dense SwiGLU)
-        HCHK(oh_launch_rmsnorm_q8k(s->x, (const float *)y.post_norm->A, a.eps, H, s->xn, s->xq.qs, s->xq.d, s->xq.bs, st));
+        LAUNCH(K_NORM_Q8K, norm_bytes(H, true),
+               oh_launch_rmsnorm_q8k(s->x, (const float *)y.post_norm->A, a.eps, H, s->xn, s->xq.qs, s->xq.d, s->xq.bs, st));
         if (a.ne > 0) {
             const int K = a.top_k, I = a.moe_inter, sI = a.shared_inter;
             const int IW = I > sI ? I : sI;   // row stride of the g/u/h buffers
             MvBuild b;
             CHK(mv_add(b, y.router, ax, s->rl, 0));
             if (y.gate_inp_sh) CHK(mv_add(b, y.gate_inp_sh, ax, s->shl, 0));
-            CHK(mv_go(b, st));
-            HCHK(oh_launch_moe_route(s->rl, a.ne, K, y.gate_inp_sh ? s->shl : nullptr, s->eidx, s->ew, s->shg, st));
+            MVGO(b);
+            LAUNCH(K_ROUTE, 4.0 * a.ne + 8.0 * K,
+                   oh_launch_moe_route(s->rl, a.ne, K, y.gate_inp_sh ? s->shl : nullptr, s->eidx, s->ew, s->shg, st));
             MvBuild b2;
             for (int k = 0; k < K; k++) {
                 CHK(mv_add(b2, y.gate_exps, ax, s->g + (size_t)k * IW, 0, s->eidx, k));
@@ -987,50 +1051,56 @@ static int enqueue_body(ornith_hip_session *s, hipStream_t st) {
                 CHK(mv_add(b2, y.gate_sh, ax, s->g + (size_t)K * IW, 0));
                 CHK(mv_add(b2, y.up_sh, ax, s->u + (size_t)K * IW, 0));
             }
-            CHK(mv_go(b2, st));
+            MVGO(b2);
+            const int nvec = K + (y.gate_sh ? 1 : 0);
             if (I == IW && (!y.gate_sh || sI == IW)) {
-                HCHK(oh_launch_swiglu_q8k(s->g, s->u, IW, K + (y.gate_sh ? 1 : 0), s->h, s->hq.qs, s->hq.d, s->hq.bs, st));
+                LAUNCH(K_SWIGLU_Q8K, nvec * norm_bytes(IW, true),
+                       oh_launch_swiglu_q8k(s->g, s->u, IW, nvec, s->h, s->hq.qs, s->hq.d, s->hq.bs, st));
             } else {
                 // widths differ: quantise each vector at its own width, same IW stride
-                for (int k = 0; k <= K; k++) {
-                    if (k == K && !y.gate_sh) break;
+                for (int k = 0; k < nvec; k++) {
                     const int n = k < K ? I : sI;
                     const size_t off = (size_t)k * IW;
-                    HCHK(oh_launch_swiglu_q8k(s->g + off, s->u + off, n, 1, s->h + off, s->hq.qs + off,
-                                              s->hq.d + off / 256, s->hq.bs + off / 16, st));
+                    LAUNCH(K_SWIGLU_Q8K, norm_bytes(n, true),
+                           oh_launch_swiglu_q8k(s->g + off, s->u + off, n, 1, s->h + off, s->hq.qs + off,
+                                                s->hq.d + off / 256, s->hq.bs + off / 16, st));
                 }
             }
             MvBuild b3;
             for (int k = 0; k < K; k++)
                 CHK(mv_add(b3, y.down_exps, act_off(s->hq, s->h, (size_t)k * IW), s->od + (size_t)k * H, 0, s->eidx, k));
             if (y.gate_sh) CHK(mv_add(b3, y.down_sh, act_off(s->hq, s->h, (size_t)K * IW), s->od + (size_t)K * H, 0));
-            CHK(mv_go(b3, st));
-            HCHK(oh_launch_moe_combine(s->x, s->od, s->ew, K, H, y.gate_sh ? s->od + (size_t)K * H : nullptr,
-                                       y.gate_inp_sh ? s->shg : nullptr, st));
+            MVGO(b3);
+            LAUNCH(K_COMBINE, 4.0 * H * (nvec + 2),
+                   oh_launch_moe_combine(s->x, s->od, s->ew, K, H, y.gate_sh ? s->od + (size_t)K * H : nullptr,
+                                         y.gate_inp_sh ? s->shg : nullptr, st));
         } else {
             const int I = a.shared_inter;
             MvBuild b;
             CHK(mv_add(b, y.ffn_gate, ax, s->g, 0));
             CHK(mv_add(b, y.ffn_up, ax, s->u, 0));
-            CHK(mv_go(b, st));
-            HCHK(oh_launch_swiglu_q8k(s->g, s->u, I, 1, s->h, s->hq.qs, s->hq.d, s->hq.bs, st));
+            MVGO(b);
+            LAUNCH(K_SWIGLU_Q8K, norm_bytes(I, true),
+                   oh_launch_swiglu_q8k(s->g, s->u, I, 1, s->h, s->hq.qs, s->hq.d, s->hq.bs, st));
             MvBuild b2;
             CHK(mv_add(b2, y.ffn_down, act_of(s->hq, s->h), s->x, 1));
-            CHK(mv_go(b2, st));
+            MVGO(b2);
         }
     }
-    HCHK(oh_launch_advance(s->io, st));
+    LAUNCH(K_ADVANCE, 8.0, oh_launch_advance(s->io, st));
     return ORNITH_HIP_OK;
 }
 
 static int enqueue_head(ornith_hip_session *s, hipStream_t st) {
     const ornith_hip_model *m = s->m;
     const ornith_hip_arch &a = m->a;
-    HCHK(oh_launch_rmsnorm_q8k(s->x, (const float *)m->out_norm->A, a.eps, a.hidden, s->xn, s->xq.qs, s->xq.d, s->xq.bs, st));
+    LAUNCH(K_NORM_Q8K, norm_bytes(a.hidden, true),
+           oh_launch_rmsnorm_q8k(s->x, (const float *)m->out_norm->A, a.eps, a.hidden, s->xn, s->xq.qs, s->xq.d, s->xq.bs, st));
     MvBuild b;
     CHK(mv_add(b, m->lm_head, act_of(s->xq, s->xn), s->logits, 0));
-    CHK(mv_go(b, st));
-    HCHK(oh_launch_argmax(s->logits, a.vocab, s->amv, s->ami, OH_ARGMAX_BLOCKS, s->toks, s->io, s->io + 1, st));
+    MVGO(b);
+    LAUNCH(K_ARGMAX, 4.0 * a.vocab,
+           oh_launch_argmax(s->logits, a.vocab, s->amv, s->ami, OH_ARGMAX_BLOCKS, s->toks, s->io, s->io + 1, st));
     return ORNITH_HIP_OK;
 }
 
@@ -1203,25 +1273,205 @@ extern "C" int ornith_hip_session_get_kv(ornith_hip_session *s, int l, int8_t *K
     const ornith_hip_arch &a = s->m->a;
     if (l < 0 || l >= a.n_layers || !s->m->L[l].full) { seterr("layer %d has no KV cache", l); return ORNITH_HIP_ERR_NOTFOUND; }
     HCHK(hipSetDevice(s->m->ctx->device));
-    const int len = s->pos, cap = s->cap, hd = a.hd, nkv = a.nkv;
+    const int len = s->pos, cap = s->kvcap, hd = a.hd, nkv = a.nkv;
     std::vector<uint32_t> kt((size_t)nkv * (hd / 4) * cap);
     HCHK(hipMemcpy(kt.data(), s->ls[l].Kt, kt.size() * 4, hipMemcpyDeviceToHost));
+    std::vector<int8_t> vt((size_t)nkv * cap * hd);
+    HCHK(hipMemcpy(vt.data(), s->ls[l].Vq, vt.size(), hipMemcpyDeviceToHost));
     for (int t = 0; t < len; t++)
         for (int h = 0; h < nkv; h++)
             for (int i = 0; i < hd; i++) {
                 const uint32_t w = kt[((size_t)h * (hd / 4) + i / 4) * cap + t];
                 Kq[((size_t)t * nkv + h) * hd + i] = (int8_t)((w >> (8 * (i & 3))) & 0xff);
+                Vq[((size_t)t * nkv + h) * hd + i] = vt[(((size_t)h * (cap / 16) + t / 16) * hd + i) * 16 + (t & 15)];
             }
     HCHK(hipMemcpy(Ks, s->ls[l].Ks, (size_t)len * nkv * 4, hipMemcpyDeviceToHost));
-    HCHK(hipMemcpy(Vq, s->ls[l].Vq, (size_t)len * nkv * hd, hipMemcpyDeviceToHost));
     HCHK(hipMemcpy(Vs, s->ls[l].Vs, (size_t)len * nkv * 4, hipMemcpyDeviceToHost));
     return ORNITH_HIP_OK;
 }
 
-extern "C" int ornith_hip_model_synth(ornith_hip_ctx *ctx, const ornith_hip_gen_cfg *cfg,
+// ---- GGUF-order download of a tensor (planes -> GGUF blocks) -------------------------------------
+extern "C" int ornith_hip_tensor_download(const ornith_hip_tensor *t, void *out, uint64_t nbytes) {
+    if (nbytes != t->gguf_bytes) {
+        seterr("tensor '%s': %llu bytes requested, %llu held", t->name.c_str(), (unsigned long long)nbytes,
+               (unsigned long long)t->gguf_bytes);
+        return ORNITH_HIP_ERR_FORMAT;
+    }
+    HCHK(hipSetDevice(t->ctx->device));
+    size_t a, b, c;
+    plane_bytes(t->type, t->rows, t->in, &a, &b, &c);
+    if (!oh_is_quant(t->type)) {
+        HCHK(hipMemcpy(out, t->A, a, hipMemcpyDeviceToHost));
+        return ORNITH_HIP_OK;
+    }
+    std::vector<uint8_t> h(up256(a) + up256(b) + up256(c));
+    HCHK(hipMemcpy(h.data(), t->mem, h.size(), hipMemcpyDeviceToHost));
+    const uint8_t *A = h.data(), *B = A + up256(a), *C = B + up256(b);
+    uint8_t *o = (uint8_t *)out;
+    const size_t nblk = (size_t)t->rows * (size_t)(t->in / 256);
+    for (size_t i = 0; i < nblk; i++) {
+        switch (t->type) {
+        case OH_Q4_K: memcpy(o + 144 * i, B + 16 * i, 16); memcpy(o + 144 * i + 16, A + 128 * i, 128); break;
+        case OH_Q6_K:
+            memcpy(o + 210 * i, A + 192 * i, 192); memcpy(o + 210 * i + 192, B + 16 * i, 16);
+            memcpy(o + 210 * i + 208, C + 2 * i, 2);
+            break;
+        case OH_Q8_0:
+            for (int k = 0; k < 8; k++) {
+                memcpy(o + 272 * i + 34 * k, B + 16 * i + 2 * k, 2);
+                memcpy(o + 272 * i + 34 * k + 2, A + 256 * i + 32 * k, 32);
+            }
+            break;
+        case OH_IQ2_XXS: memcpy(o + 66 * i, C + 2 * i, 2); memcpy(o + 66 * i + 2, A + 64 * i, 64); break;
+        }
+    }
+    return ORNITH_HIP_OK;
+}
+
+// ---- on-device random init ----------------------------------------------------------------------
+// Stream key of a tensor: FNV-1a of its name xor seed*golden-gamma; element i
+// of the stream depends only on (key, i) (counter-based splitmix64).
+static uint64_t stream_key(uint64_t seed, const std::string &name) {
+    uint64_t h = 0xcbf29ce484222325ull;
+    for (unsigned char ch : name) { h ^= ch; h *= 0x100000001b3ull; }
+    return h ^ (seed * 0x9E3779B97F4A7C15ull);
+}
+
+extern "C" int ornith_hip_model_synth(ornith_hip_ctx *ctx, const ornith_hip_gen_cfg *c,
                                       ornith_hip_model **out) {
-    (void)ctx; (void)cfg;
     *out = nullptr;
-    seterr("model_synth: not built yet");
-    return ORNITH_HIP_ERR_UNSUPPORTED;
+    HCHK(hipSetDevice(ctx->device));
+    auto enc_ok = [](uint32_t t) { return t == OH_Q8_0 || t == OH_Q4_K || t == OH_Q6_K || t == OH_F32; };
+    if (!enc_ok(c->t_default) || !enc_ok(c->t_attn_v) || !enc_ok(c->t_ffn_down) || !enc_ok(c->t_output) ||
+        !enc_ok(c->t_embd)) {
+        seterr("model_synth: on-device encoders cover F32/Q8_0/Q4_K/Q6_K");
+        return ORNITH_HIP_ERR_UNSUPPORTED;
+    }
+    if (c->hidden <= 0 || c->n_layers <= 0 || c->vocab <= 0 || c->dhead <= 0 || c->conv_k < 2) {
+        seterr("model_synth: bad config");
+        return ORNITH_HIP_ERR_FORMAT;
+    }
+    const int H = c->hidden, V = c->vocab, qd = c->nk * c->dhead, vd = c->nv * c->dhead, cc = 2 * qd + vd;
+    // largest tensor (elements) sizes the f32 staging buffer
+    uint64_t mx = (uint64_t)H * V;
+    auto upd = [&](uint64_t n) { if (n > mx) mx = n; };
+    upd((uint64_t)H * cc); upd((uint64_t)H * 2 * c->nh * c->hd); upd((uint64_t)H * c->moe_inter * c->ne);
+    upd((uint64_t)c->nh * c->hd * H); upd((uint64_t)vd * H);
+    float *tmp = nullptr;
+    HCHK(hipMalloc(&tmp, mx * 4 + 256));
+    auto *m = new ornith_hip_model();
+    m->ctx = ctx;
+    hipStream_t st = ctx->st;
+    int status = ORNITH_HIP_OK;
+    auto add_q = [&](const std::string &name, uint32_t type, int nd, uint64_t d0, uint64_t d1, uint64_t d2) {
+        if (status) return;
+        const uint64_t dims[3] = {d0, d1, d2};
+        ornith_hip_tensor *t;
+        if ((status = tensor_alloc(ctx, name.c_str(), type, (uint32_t)nd, dims, &t))) return;
+        m->ts.push_back(t); m->by[name] = t; m->bytes += t->gguf_bytes;
+        const int64_t n = t->rows * t->in;
+        float *dst = type == OH_F32 ? (float *)t->A : tmp;
+        hipError_t e = oh_launch_fill_gauss(stream_key(c->seed, name), c->sigma, dst, n, st);
+        if (e == hipSuccess && type != OH_F32) e = oh_launch_encode(tmp, (int)type, n / 256, t->A, t->B, t->C, st);
+        if (e == hipSuccess) e = hipStreamSynchronize(st);   // tmp is reused by the next tensor
+        if (e != hipSuccess) { seterr("synth '%s': %s", name.c_str(), hipGetErrorString(e)); status = ORNITH_HIP_ERR_DEVICE; }
+    };
+    auto add_u = [&](const std::string &name, int nd, uint64_t d0, uint64_t d1, float lo, float hi) {
+        if (status) return;
+        const uint64_t dims[2] = {d0, d1};
+        ornith_hip_tensor *t;
+        if ((status = tensor_alloc(ctx, name.c_str(), OH_F32, (uint32_t)nd, dims, &t))) return;
+        m->ts.push_back(t); m->by[name] = t; m->bytes += t->gguf_bytes;
+        hipError_t e = oh_launch_fill_uniform(stream_key(c->seed, name), lo, hi, (float *)t->A, t->rows * t->in, st);
+        if (e != hipSuccess) { seterr("synth '%s': %s", name.c_str(), hipGetErrorString(e)); status = ORNITH_HIP_ERR_DEVICE; }
+    };
+    // same tensor set and order as the GGUF generator
+    add_q("token_embd.weight", c->t_embd, 2, H, V, 0);
+    add_u("output_norm.weight", 1, H, 0, 0.9f, 1.1f);
+    add_q("output.weight", c->t_output, 2, H, V, 0);
+    for (int l = 0; l < c->n_layers; l++) {
+        const bool full = c->full_interval > 0 && l % c->full_interval == c->full_interval - 1;
+        const std::string b = "blk." + std::to_string(l) + ".";
+        add_u(b + "attn_norm.weight", 1, H, 0, 0.9f, 1.1f);
+        add_u(b + "post_attention_norm.weight", 1, H, 0, 0.9f, 1.1f);
+        if (full) {
+            add_q(b + "attn_q.weight", c->t_default, 2, H, 2 * c->nh * c->hd, 0);
+            add_q(b + "attn_k.weight", c->t_default, 2, H, c->nkv * c->hd, 0);
+            add_q(b + "attn_v.weight", c->t_attn_v, 2, H, c->nkv * c->hd, 0);
+            add_u(b + "attn_q_norm.weight", 1, c->hd, 0, 0.9f, 1.1f);
+            add_u(b + "attn_k_norm.weight", 1, c->hd, 0, 0.9f, 1.1f);
+            add_q(b + "attn_output.weight", c->t_default, 2, c->nh * c->hd, H, 0);
+        } else {
+            add_q(b + "attn_qkv.weight", c->t_default, 2, H, cc, 0);
+            add_u(b + "ssm_conv1d.weight", 2, c->conv_k, cc, -0.2f, 0.2f);
+            add_u(b + "ssm_a", 1, c->nv, 0, -0.8f, -0.2f);
+            add_u(b + "ssm_dt.bias", 1, c->nv, 0, -0.05f, 0.05f);
+            add_u(b + "ssm_norm.weight", 1, c->dhead, 0, 0.9f, 1.1f);
+            add_q(b + "ssm_alpha.weight", c->t_default, 2, H, c->nv, 0);
+            add_q(b + "ssm_beta.weight", c->t_default, 2, H, c->nv, 0);
+            add_q(b + "attn_gate.weight", c->t_default, 2, H, vd, 0);
+            add_q(b + "ssm_out.weight", c->t_default, 2, vd, H, 0);
+        }
+        add_q(b + "ffn_gate_inp.weight", c->t_default, 2, H, c->ne, 0);
+        add_q(b + "ffn_gate_exps.weight", c->t_default, 3, H, c->moe_inter, c->ne);
+        add_q(b + "ffn_up_exps.weight", c->t_default, 3, H, c->moe_inter, c->ne);
+        add_q(b + "ffn_down_exps.weight", c->t_ffn_down, 3, c->moe_inter, H, c->ne);
+        if (c->shared_inter > 0) {
+            add_q(b + "ffn_gate_shexp.weight", c->t_default, 2, H, c->shared_inter, 0);
+            add_q(b + "ffn_up_shexp.weight", c->t_default, 2, H, c->shared_inter, 0);
+            add_q(b + "ffn_down_shexp.weight", c->t_ffn_down, 2, c->shared_inter, H, 0);
+            add_q(b + "ffn_gate_inp_shexp.weight", c->t_default, 1, H, 1, 0);
+        }
+    }
+    (void)hipStreamSynchronize(st);
+    (void)hipFree(tmp);
+    if (status) { ornith_hip_model_free(m); return status; }
+    Meta md;
+    md.arch = "qwen35moe";
+    md.u32["qwen35moe.block_count"] = (uint32_t)c->n_layers;
+    md.u32["qwen35moe.expert_used_count"] = (uint32_t)c->top_k;
+    md.u32["qwen35moe.rope.dimension_count"] = 64;
+    md.f32["qwen35moe.rope.freq_base"] = 1e7f;
+    md.f32["qwen35moe.attention.layer_norm_rms_epsilon"] = 1e-6f;
+    md.has_tokens = true;
+    md.eos = -1;
+    const int st2 = infer_arch(m, md);
+    if (st2) { ornith_hip_model_free(m); return st2; }
+    *out = m;
+    return ORNITH_HIP_OK;
+}
+
+// ---- one eager step with per-launch timing (HIP events around every launch) ------------------------
+extern "C" int ornith_hip_session_profile_step(ornith_hip_session *s, int max_launches, int32_t *kinds,
+                                               double *bytes, float *ms, int *n_launches) {
+    *n_launches = 0;
+    if (!s->have_logits) { seterr("session has no logits; eval a prompt first"); return ORNITH_HIP_ERR_FORMAT; }
+    if (s->pos + 1 > s->cap) { seterr("profile_step: session full"); return ORNITH_HIP_ERR_UNSUPPORTED; }
+    HCHK(hipSetDevice(s->m->ctx->device));
+    hipStream_t st = s->m->ctx->st;
+    CHK(sync_pos(s));
+    HCHK(hipStreamSynchronize(st));
+    s->rec = true;
+    s->rec_ev.clear(); s->rec_kind.clear(); s->rec_bytes.clear();
+    int r = enqueue_body(s, st);
+    if (r == ORNITH_HIP_OK) r = enqueue_head(s, st);
+    s->rec = false;
+    hipError_t e = hipStreamSynchronize(st);
+    const size_t n = s->rec_kind.size();
+    if (r == ORNITH_HIP_OK && e == hipSuccess) {
+        for (size_t i = 0; i < n && (int)i < max_launches; i++) {
+            float el = 0.0f;
+            (void)hipEventElapsedTime(&el, s->rec_ev[2 * i], s->rec_ev[2 * i + 1]);
+            kinds[i] = s->rec_kind[i];
+            bytes[i] = s->rec_bytes[i];
+            ms[i] = el;
+        }
+        *n_launches = (int)(n < (size_t)max_launches ? n : (size_t)max_launches);
+        s->pos += 1;
+    }
+    for (hipEvent_t ev : s->rec_ev) (void)hipEventDestroy(ev);
+    s->rec_ev.clear();
+    if (r) return r;
+    HCHK(e);
+    return ORNITH_HIP_OK;
 }

@@ -2,6 +2,7 @@
 // kernels of oh_mv.hip and oh_layers.hip plus their host launchers.
 #include "oh_mv.hip"
 #include "oh_layers.hip"
+#include "oh_synth.hip"
 #include "oh_launch.h"
 
 extern "C" {
@@ -106,6 +107,27 @@ hipError_t oh_launch_argmax(const float *v, int n, float *tmp_v, int *tmp_i, int
                             hipStream_t st) {
     hipLaunchKernelGGL(oh_k_argmax1, dim3(nblk), dim3(256), 0, st, v, n, tmp_v, tmp_i);
     hipLaunchKernelGGL(oh_k_argmax2, dim3(1), dim3(64), 0, st, tmp_v, tmp_i, nblk, toks, io_pos, io_best);
+    return hipGetLastError();
+}
+
+hipError_t oh_launch_fill_gauss(uint64_t key, float sigma, float *dst, int64_t n, hipStream_t st) {
+    int64_t blocks = (n + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    hipLaunchKernelGGL(oh_k_fill_gauss, dim3((unsigned)(blocks > 0 ? blocks : 1)), dim3(256), 0, st, key, sigma, dst, n);
+    return hipGetLastError();
+}
+
+hipError_t oh_launch_fill_uniform(uint64_t key, float lo, float hi, float *dst, int64_t n, hipStream_t st) {
+    int64_t blocks = (n + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    hipLaunchKernelGGL(oh_k_fill_uniform, dim3((unsigned)(blocks > 0 ? blocks : 1)), dim3(256), 0, st, key, lo, hi, dst, n);
+    return hipGetLastError();
+}
+
+hipError_t oh_launch_encode(const float *x, int type, int64_t nblk, uint8_t *A, uint8_t *B, uint8_t *C,
+                            hipStream_t st) {
+    if (nblk <= 0) return hipSuccess;
+    hipLaunchKernelGGL(oh_k_encode, dim3((unsigned)((nblk + 255) / 256)), dim3(256), 0, st, x, type, nblk, A, B, C);
     return hipGetLastError();
 }
 

@@ -41,6 +41,10 @@ hipError_t oh_launch_argmax(const float *v, int n, float *tmp_v, int *tmp_i, int
                             int32_t *toks, const int32_t *io_pos, int32_t *io_best,
                             hipStream_t st);
 hipError_t oh_launch_advance(int32_t *io_pos, hipStream_t st);
+hipError_t oh_launch_fill_gauss(uint64_t key, float sigma, float *dst, int64_t n, hipStream_t st);
+hipError_t oh_launch_fill_uniform(uint64_t key, float lo, float hi, float *dst, int64_t n, hipStream_t st);
+hipError_t oh_launch_encode(const float *x, int type, int64_t nblk, uint8_t *A, uint8_t *B, uint8_t *C,
+                            hipStream_t st);
 }
 
 // blocks used by the argmax's first stage (the caller sizes tmp_v/tmp_i)

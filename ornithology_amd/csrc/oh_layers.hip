@@ -182,8 +182,9 @@ oh_k_delta_step(const float *cat, const float *gate, const float *ab,
 // of the reference's powf/cosf/sinf values), Q8 append of k and v at `pos`.
 // Blocks [0, nh) are query heads, [nh, nh+nkv) key/value heads.
 // K codes are stored as [kvh][hd/4][cap] 32-bit words (4 codes each, so a
-// lane per position reads coalesced words); V codes [cap][kvh][hd] as in the
-// reference.
+// lane per position reads coalesced words); V codes as [kvh][cap/16][hd][16]
+// tiles (a lane per element reads 16 consecutive positions in one 16-byte
+// load). cap is a multiple of 16.
 extern "C" __global__ void __launch_bounds__(256)
 oh_k_attn_prep(const float *qproj, const float *kin, const float *vin,
                const float *q_norm, const float *k_norm, const float2 *rope,
@@ -247,7 +248,8 @@ oh_k_attn_prep(const float *qproj, const float *kin, const float *vin,
                     ((uint32_t)(c2 & 0xff) << 16) | ((uint32_t)(c3 & 0xff) << 24);
             if (t == 0) Ks[off] = scale;
         } else {
-            if (t < hd) Vq[off * hd + t] = (int8_t)code;
+            // tiles of 16 positions: Vq[h][pos/16][i][pos%16]
+            if (t < hd) Vq[(((size_t)h * (cap / 16) + pos / 16) * hd + t) * 16 + (pos & 15)] = (int8_t)code;
             if (t == 0) Vs[off] = scale;
         }
     }
@@ -314,8 +316,8 @@ oh_k_attn_out(float *scores, const int8_t *Vq, const float *Vs, const float *gat
     // output: thread -> (head hl, element i)
     const int hl = t / hd, i = t % hd, h = (int)blockIdx.x * hpb + hl;
     const int kvh = h / (nh / nkv);
-    const float *p = scores + (size_t)h * cap;
     float o = 0.0f;
+    const uint4 *vt = (const uint4 *)Vq + (size_t)kvh * (cap / 16) * hd + i;
     for (int t0 = 0; t0 < T; t0 += 256) {
         const int n = T - t0 < 256 ? T - t0 : 256;
         __syncthreads();
@@ -325,10 +327,15 @@ oh_k_attn_out(float *scores, const int8_t *Vq, const float *Vs, const float *gat
             if (tt < n) pbuf[hh][tt] = scores[(size_t)hg * cap + t0 + tt] * Vs[(size_t)(t0 + tt) * nkv + kv2];
         }
         __syncthreads();
-        for (int k = 0; k < n; k++) {
-            const float sv = pbuf[hl][k];
-            if (sv == 0.0f) continue;
-            o += sv * (float)Vq[((size_t)(t0 + k) * nkv + kvh) * hd + i];
+        for (int k0 = 0; k0 < n; k0 += 16) {
+            const uint4 cw = vt[(size_t)((t0 + k0) / 16) * hd];
+#pragma unroll
+            for (int j = 0; j < 16; j++) {
+                const int8_t c = (int8_t)(wsel(cw, j >> 2) >> (8 * (j & 3)));
+                const float sv = k0 + j < n ? pbuf[hl][k0 + j] : 0.0f;
+                const float nx = o + sv * (float)c;
+                o = sv != 0.0f ? nx : o;       // zero weights are skipped
+            }
         }
     }
     o *= ref_sigmoid(gate[(size_t)h * hd + i]);
@@ -345,30 +352,40 @@ oh_k_attn_out(float *scores, const int8_t *Vq, const float *Vs, const float *gat
 extern "C" __global__ void __launch_bounds__(64)
 oh_k_moe_route(const float *logits, int ne, int k, const float *shgate_logit,
                int32_t *idx, float *w, float *shgate) {
-    __shared__ unsigned char taken[1024];
+    // logits live in registers: lane owns experts lane + 64*j (j < 16, ne <= 1024)
     const int lane = (int)threadIdx.x;
-    for (int e = lane; e < ne; e += 64) taken[e] = 0;
-    __syncthreads();
+    float v[16];
+#pragma unroll
+    for (int j = 0; j < 16; j++) v[j] = lane + 64 * j < ne ? logits[lane + 64 * j] : -INFINITY;
+    uint32_t taken = 0;
+    float mine = 0.0f;                     // lane s keeps the s-th selected logit
+    int sel = 0;
     for (int s = 0; s < k; s++) {
         float bv = -INFINITY; int bi = 0x7fffffff;
-        for (int e = lane; e < ne; e += 64)
-            if (!taken[e] && logits[e] > bv) { bv = logits[e]; bi = e; }
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            const int e = lane + 64 * j;
+            if (e < ne && !(taken >> j & 1u) && v[j] > bv) { bv = v[j]; bi = e; }
+        }
         for (int m = 32; m >= 1; m >>= 1) {
             const float ov = shfl_xor(bv, m); const int oi = shfl_xor(bi, m);
             if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
         }
-        if (lane == 0) { idx[s] = bi; taken[bi] = 1; }
-        __syncthreads();
+        if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
+        if (lane == s) { mine = bv; sel = bi; }
     }
-    if (lane == 0) {
-        float mx = logits[idx[0]];
-        for (int s = 1; s < k; s++) if (logits[idx[s]] > mx) mx = logits[idx[s]];
-        float ws[64];
-        float sum = 0.0f;
-        for (int s = 0; s < k; s++) { ws[s] = ref_expf(logits[idx[s]] - mx); sum += ws[s]; }
-        for (int s = 0; s < k; s++) w[s] = ws[s] / sum;
-        if (shgate_logit) *shgate = ref_sigmoid(*shgate_logit);
-    }
+    // NaN/-inf logits can leave no candidate: never hand an out-of-range
+    // expert index to the gathered matvec
+    if (sel < 0 || sel >= ne) sel = 0;
+    if (lane < k) idx[lane] = sel;
+    // softmax over the selected logits in selection order (src/ornith_moe.c:23-29)
+    float mx = shfl(mine, 0);
+    for (int s = 1; s < k; s++) { const float x = shfl(mine, s); if (x > mx) mx = x; }
+    const float e = ref_expf(mine - mx);
+    float sum = 0.0f;
+    for (int s = 0; s < k; s++) sum += shfl(e, s);
+    if (lane < k) w[lane] = e / sum;
+    if (lane == 0 && shgate_logit) *shgate = ref_sigmoid(*shgate_logit);
 }
 
 // x += sum_s w_s * o_s (sequential in s, from 0) + shared * gate

@@ -70,6 +70,12 @@ class Arch(C.Structure):
         ("rope_theta", C.c_float), ("eps", C.c_float), ("eos", C.c_int)]
 
 
+class OrcTensor(C.Structure):
+    _fields_ = [("name", C.c_char * 256), ("n_dims", C.c_uint32), ("dims", C.c_uint64 * 4),
+                ("type", C.c_uint32), ("n_elements", C.c_uint64), ("data", C.c_void_p),
+                ("nbytes", C.c_uint64)]
+
+
 class OrcKV(C.Structure):
     _fields_ = [("K", fp), ("V", fp), ("Kq", C.POINTER(C.c_int8)), ("Vq", C.POINTER(C.c_int8)),
                 ("Ks", fp), ("Vs", fp), ("quantized", C.c_int), ("capacity", C.c_int),
@@ -146,6 +152,18 @@ def oracle():
         "orc_session_conv": (fp, [vp, C.c_int]),
         "orc_session_kv": (C.POINTER(OrcKV), [vp, C.c_int]),
         "orc_last_error": (C.c_char_p, []),
+        "orc_gguf_load": (C.c_int, [C.c_char_p, C.POINTER(vp)]),
+        "orc_gguf_free": (None, [vp]),
+        "orc_gguf_n_tensors": (C.c_uint64, [vp]),
+        "orc_gguf_tensor": (C.POINTER(OrcTensor), [vp, C.c_uint64]),
+        "orc_writer_new": (vp, []),
+        "orc_writer_free": (None, [vp]),
+        "orc_w_string": (C.c_int, [vp, C.c_char_p, C.c_char_p]),
+        "orc_w_u32": (C.c_int, [vp, C.c_char_p, C.c_uint32]),
+        "orc_w_f32": (C.c_int, [vp, C.c_char_p, C.c_float]),
+        "orc_w_arr_str": (C.c_int, [vp, C.c_char_p, C.POINTER(C.c_char_p), C.c_size_t]),
+        "orc_w_tensor": (C.c_int, [vp, C.c_char_p, C.c_uint32, C.POINTER(C.c_uint64), C.c_uint32, vp, C.c_uint64]),
+        "orc_writer_write": (C.c_int, [vp, C.c_char_p]),
     }
     for name, (res, args) in sig.items():
         f = getattr(L, name)
@@ -281,3 +299,19 @@ def write_c1_gguf(path: str, cfg: dict | None = None) -> None:
     st = L.orc_gen_write_gguf(C.byref(c), str(path).encode())
     if st:
         raise RuntimeError(L.orc_last_error().decode())
+
+
+def gguf_tensors(path) -> dict:
+    """name -> (type, dims, bytes) of every tensor of a GGUF, via the oracle loader."""
+    L = oracle()
+    g = C.c_void_p()
+    st = L.orc_gguf_load(str(path).encode(), C.byref(g))
+    if st:
+        raise RuntimeError(L.orc_last_error().decode())
+    out = {}
+    for i in range(L.orc_gguf_n_tensors(g)):
+        t = L.orc_gguf_tensor(g, i).contents
+        raw = C.string_at(t.data, t.nbytes) if t.nbytes else b""
+        out[t.name.decode()] = (t.type, tuple(t.dims[:t.n_dims]), np.frombuffer(raw, np.uint8).copy())
+    L.orc_gguf_free(g)
+    return out
