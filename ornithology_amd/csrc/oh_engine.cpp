@@ -816,6 +816,9 @@ struct ornith_hip_session {
     float *o = nullptr;
     Q8Buf oq;
     float *qproj = nullptr, *kb = nullptr, *vb = nullptr, *qr = nullptr, *agate = nullptr, *scores = nullptr;
+    float *apart = nullptr;       // split attention: partial outputs [groups][chunks][256]
+    int *acnt = nullptr;          // split attention: per-group completion counters (self-resetting)
+    int exact_max = 1024;         // contexts up to this walk the attention sum in one block
     float2 *rope = nullptr;
     float *rl = nullptr, *shl = nullptr, *shg = nullptr, *ew = nullptr;
     int32_t *eidx = nullptr;
@@ -922,6 +925,12 @@ extern "C" int ornith_hip_session_new(ornith_hip_model *m, int cap, ornith_hip_s
     A_(salloc(s, &s->qproj, 2 * (size_t)aq)); A_(salloc(s, &s->kb, kvd)); A_(salloc(s, &s->vb, kvd));
     A_(salloc(s, &s->qr, aq)); A_(salloc(s, &s->agate, aq));
     A_(salloc(s, &s->scores, (size_t)a.nh * s->kvcap));
+    A_(salloc(s, &s->apart, (size_t)a.nh * a.hd / 256 * ((s->kvcap + 255) / 256) * 256 + 256));
+    A_(salloc(s, &s->acnt, (size_t)a.nh + 64));
+    {
+        const char *e = getenv("ORNITH_HIP_EXACT_ATTN_MAX");
+        if (e && *e) s->exact_max = atoi(e);
+    }
     A_(salloc(s, &s->rl, a.ne > 0 ? a.ne : 1)); A_(salloc(s, &s->shl, 1)); A_(salloc(s, &s->shg, 1));
     A_(salloc(s, &s->ew, 64)); A_(salloc(s, &s->eidx, 64));
     const size_t nvec = (size_t)(K + 1);
@@ -1006,8 +1015,8 @@ static int enqueue_body(ornith_hip_session *s, hipStream_t st) {
             LAUNCH(K_ATTN_SCORES, T * a.nkv * (a.hd + 4.0) + 4.0 * T * a.nh + 4.0 * aqd,
                    oh_launch_attn_scores(s->qr, z.Kt, z.Ks, s->scores, pos, a.nh, a.nkv, a.hd, s->kvcap, scale, st));
             LAUNCH(K_ATTN_OUT, T * a.nkv * (a.hd + 4.0) + 8.0 * T * a.nh + 9.0 * aqd,
-                   oh_launch_attn_out(s->scores, z.Vq, z.Vs, s->agate, s->o, s->oq.qs, s->oq.d, s->oq.bs, pos,
-                                      a.nh, a.nkv, a.hd, s->kvcap, st));
+                   oh_launch_attn_out(s->scores, z.Vq, z.Vs, s->agate, s->o, s->oq.qs, s->oq.d, s->oq.bs,
+                                      s->apart, s->acnt, pos, a.nh, a.nkv, a.hd, s->kvcap, s->exact_max, st));
             MvBuild b2;
             CHK(mv_add(b2, y.o, act_of(s->oq, s->o), s->x, 1));
             MVGO(b2);

@@ -80,13 +80,13 @@ hipError_t oh_launch_attn_scores(const float *qr, const uint32_t *Kt, const floa
     return hipGetLastError();
 }
 
-hipError_t oh_launch_attn_out(float *scores, const int8_t *Vq, const float *Vs, const float *gate,
-                              float *out, int8_t *oqs, float *oqd, int16_t *oqb,
-                              const int32_t *io_pos, int nh, int nkv, int hd, int cap,
+hipError_t oh_launch_attn_out(const float *scores, const int8_t *Vq, const float *Vs, const float *gate,
+                              float *out, int8_t *oqs, float *oqd, int16_t *oqb, float *part, int *cnt,
+                              const int32_t *io_pos, int nh, int nkv, int hd, int cap, int exact_max,
                               hipStream_t st) {
     const int hpb = 256 / hd;
-    hipLaunchKernelGGL(oh_k_attn_out, dim3(nh / hpb), dim3(256), 0, st, scores, Vq, Vs, gate, out, oqs,
-                       oqd, oqb, io_pos, nh, nkv, hd, cap);
+    hipLaunchKernelGGL(oh_k_attn_out, dim3(nh / hpb, (cap + 255) / 256), dim3(256), 0, st, scores, Vq, Vs, gate,
+                       out, oqs, oqd, oqb, part, cnt, io_pos, nh, nkv, hd, cap, exact_max);
     return hipGetLastError();
 }
 

@@ -29,9 +29,9 @@ hipError_t oh_launch_attn_prep(const float *qproj, const float *kin, const float
 hipError_t oh_launch_attn_scores(const float *qr, const uint32_t *Kt, const float *Ks,
                                  float *scores, const int32_t *io_pos, int nh, int nkv, int hd,
                                  int cap, float scale, hipStream_t st);
-hipError_t oh_launch_attn_out(float *scores, const int8_t *Vq, const float *Vs, const float *gate,
-                              float *out, int8_t *oqs, float *oqd, int16_t *oqb,
-                              const int32_t *io_pos, int nh, int nkv, int hd, int cap,
+hipError_t oh_launch_attn_out(const float *scores, const int8_t *Vq, const float *Vs, const float *gate,
+                              float *out, int8_t *oqs, float *oqd, int16_t *oqb, float *part, int *cnt,
+                              const int32_t *io_pos, int nh, int nkv, int hd, int cap, int exact_max,
                               hipStream_t st);
 hipError_t oh_launch_moe_route(const float *logits, int ne, int k, const float *shgate_logit,
                                int32_t *idx, float *w, float *shgate, hipStream_t st);

@@ -270,12 +270,19 @@ oh_k_attn_scores(const float *qr, const uint32_t *Kt, const float *Ks, float *sc
     if (t >= T) return;
     const uint32_t *kw = Kt + (size_t)kvh * (hd / 4) * cap + t;
     float acc = 0.0f;
-    for (int w = 0; w < hd / 4; w++) {
-        const uint32_t word = kw[(size_t)w * cap];
-        acc += q[4 * w + 0] * (float)(int8_t)(word & 0xff);
-        acc += q[4 * w + 1] * (float)(int8_t)((word >> 8) & 0xff);
-        acc += q[4 * w + 2] * (float)(int8_t)((word >> 16) & 0xff);
-        acc += q[4 * w + 3] * (float)(int8_t)(word >> 24);
+    for (int w0 = 0; w0 < hd / 4; w0 += 16) {
+        uint32_t wd[16];
+#pragma unroll
+        for (int u = 0; u < 16; u++) wd[u] = w0 + u < hd / 4 ? kw[(size_t)(w0 + u) * cap] : 0u;
+#pragma unroll
+        for (int u = 0; u < 16; u++) {
+            if (w0 + u >= hd / 4) break;
+            const int w = w0 + u;
+            acc += q[4 * w + 0] * (float)(int8_t)(wd[u] & 0xff);
+            acc += q[4 * w + 1] * (float)(int8_t)((wd[u] >> 8) & 0xff);
+            acc += q[4 * w + 2] * (float)(int8_t)((wd[u] >> 16) & 0xff);
+            acc += q[4 * w + 3] * (float)(int8_t)(wd[u] >> 24);
+        }
     }
     const float ks = Ks[(size_t)t * nkv + kvh];
     const float sc = ks == 0.0f ? 0.0f : acc * ks;
@@ -285,20 +292,29 @@ oh_k_attn_scores(const float *qr, const uint32_t *Kt, const float *Ks, float *sc
 // softmax over T (src/ornith_tensor.c:108-115; tree-ordered double sum) and the
 // output o_i = sum_t (p_t*Vs_t)*code_t,i, sequential over t, skipping zero
 // weights (src/ornith_attn.c:132-140); then o *= sigmoid(gate) and Q8_K of the
-// 256 outputs of this block. One block covers 256/hd heads.
+// 256 outputs of a block (256/hd heads).
+// Grid (nh*hd/256, cap/256). For T <= exact_max, block (g, 0) walks all T in
+// order, as the reference does. Longer contexts split the walk into 256-position
+// chunks (block (g, k) takes chunk k, each walked in order) whose partial sums
+// the last block to finish adds in chunk order; the softmax statistics are the
+// same in every block. Blocks signal completion with a fenced atomic counter
+// that the last block resets; nothing waits.
 extern "C" __global__ void __launch_bounds__(256)
-oh_k_attn_out(float *scores, const int8_t *Vq, const float *Vs, const float *gate,
-              float *out, int8_t *oqs, float *oqd, int16_t *oqb,
-              const int32_t *io_pos, int nh, int nkv, int hd, int cap) {
+oh_k_attn_out(const float *scores, const int8_t *Vq, const float *Vs, const float *gate,
+              float *out, int8_t *oqs, float *oqd, int16_t *oqb, float *part, int *cnt,
+              const int32_t *io_pos, int nh, int nkv, int hd, int cap, int exact_max) {
     __shared__ float vec[256];
     __shared__ float pbuf[4][256];
+    __shared__ float inv_s[4], mx_s[4];
     __shared__ double red[4];
     __shared__ float mred[4];
-    const int hpb = 256 / hd, t = (int)threadIdx.x;
-    const int T = *io_pos + 1;
+    __shared__ int last;
+    const int hpb = 256 / hd, t = (int)threadIdx.x, g = (int)blockIdx.x, kc = (int)blockIdx.y;
+    const int T = *io_pos + 1, nch = (T + 255) / 256, maxch = gridDim.y;
+    const bool exact = T <= exact_max;
+    if (exact ? kc != 0 : kc >= nch) return;
     for (int hl = 0; hl < hpb; hl++) {
-        const int h = (int)blockIdx.x * hpb + hl;
-        float *sc = scores + (size_t)h * cap;
+        const float *sc = scores + (size_t)(g * hpb + hl) * cap;
         float mx = -INFINITY;
         for (int i = t; i < T; i += 256) mx = fmaxf(mx, sc[i]);
         mx = wave_max_f(mx);
@@ -307,42 +323,66 @@ oh_k_attn_out(float *scores, const int8_t *Vq, const float *Vs, const float *gat
         __syncthreads();
         mx = fmaxf(fmaxf(mred[0], mred[1]), fmaxf(mred[2], mred[3]));
         double sum = 0.0;
-        for (int i = t; i < T; i += 256) { const float e = ref_expf(sc[i] - mx); sc[i] = e; sum += e; }
+        for (int i = t; i < T; i += 256) sum += ref_expf(sc[i] - mx);
         sum = block_sum_d(sum, red);
-        const float inv = (float)(1.0 / sum);
-        for (int i = t; i < T; i += 256) sc[i] = sc[i] * inv;
-        __syncthreads();
+        if (t == 0) { mx_s[hl] = mx; inv_s[hl] = (float)(1.0 / sum); }
     }
-    // output: thread -> (head hl, element i)
-    const int hl = t / hd, i = t % hd, h = (int)blockIdx.x * hpb + hl;
+    const int hl = t / hd, i = t % hd, h = g * hpb + hl;
     const int kvh = h / (nh / nkv);
-    float o = 0.0f;
     const uint4 *vt = (const uint4 *)Vq + (size_t)kvh * (cap / 16) * hd + i;
-    for (int t0 = 0; t0 < T; t0 += 256) {
-        const int n = T - t0 < 256 ? T - t0 : 256;
+    const int c0 = exact ? 0 : kc, c1 = exact ? nch : kc + 1;
+    float o = 0.0f;
+    for (int ck = c0; ck < c1; ck++) {
+        const int t0 = ck * 256, n = T - t0 < 256 ? T - t0 : 256;
         __syncthreads();
         for (int k = t; k < hpb * 256; k += 256) {
             const int hh = k / 256, tt = k % 256;
-            const int hg = (int)blockIdx.x * hpb + hh, kv2 = hg / (nh / nkv);
-            if (tt < n) pbuf[hh][tt] = scores[(size_t)hg * cap + t0 + tt] * Vs[(size_t)(t0 + tt) * nkv + kv2];
-        }
-        __syncthreads();
-        for (int k0 = 0; k0 < n; k0 += 16) {
-            const uint4 cw = vt[(size_t)((t0 + k0) / 16) * hd];
-#pragma unroll
-            for (int j = 0; j < 16; j++) {
-                const int8_t c = (int8_t)(wsel(cw, j >> 2) >> (8 * (j & 3)));
-                const float sv = k0 + j < n ? pbuf[hl][k0 + j] : 0.0f;
-                const float nx = o + sv * (float)c;
-                o = sv != 0.0f ? nx : o;       // zero weights are skipped
+            const int hg = g * hpb + hh, kv2 = hg / (nh / nkv);
+            if (tt < n) {
+                const float p = ref_expf(scores[(size_t)hg * cap + t0 + tt] - mx_s[hh]) * inv_s[hh];
+                pbuf[hh][tt] = p * Vs[(size_t)(t0 + tt) * nkv + kv2];
             }
         }
+        __syncthreads();
+        // tiles of 16 positions, 8 tiles in flight, adds in position order
+        for (int k0 = 0; k0 < n; k0 += 128) {
+            uint4 cw[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const int tile = k0 + 16 * u < n ? k0 + 16 * u : ((n - 1) & ~15);
+                cw[u] = vt[(size_t)((t0 + tile) / 16) * hd];
+            }
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+#pragma unroll
+                for (int j = 0; j < 16; j++) {
+                    const int k = k0 + 16 * u + j;
+                    const int8_t c = (int8_t)(wsel(cw[u], j >> 2) >> (8 * (j & 3)));
+                    const float sv = k < n ? pbuf[hl][k] : 0.0f;
+                    const float nx = o + sv * (float)c;
+                    o = sv != 0.0f ? nx : o;       // zero weights are skipped
+                }
+            }
+        }
+    }
+    if (!exact) {
+        float *pp = part + ((size_t)g * maxch) * 256;
+        pp[(size_t)kc * 256 + t] = o;
+        __threadfence();
+        __syncthreads();
+        if (t == 0) last = atomicAdd(&cnt[g], 1) == nch - 1;
+        __syncthreads();
+        if (!last) return;
+        __threadfence();
+        o = 0.0f;
+        for (int k = 0; k < nch; k++) o += pp[(size_t)k * 256 + t];
+        if (t == 0) cnt[g] = 0;
     }
     o *= ref_sigmoid(gate[(size_t)h * hd + i]);
     out[(size_t)h * hd + i] = o;
     vec[t] = o;
     __syncthreads();
-    if (t < 64) q8k_block_from_lds(vec, 0, oqs + (size_t)blockIdx.x * 256, oqd + blockIdx.x, oqb + (size_t)blockIdx.x * 16);
+    if (t < 64) q8k_block_from_lds(vec, 0, oqs + (size_t)g * 256, oqd + g, oqb + (size_t)g * 16);
 }
 
 // ---- MoE router (src/ornith_moe.c:8-30) ------------------------------------------
