@@ -177,6 +177,11 @@ def cpu_baseline(model: oa.Model, cfg: dict, seconds: float) -> dict:
                        f"= {t_tok * 1e3:.1f} ms; Q8 KV; {ncores} threads")
 
 
+# profile kind -> kernel symbol (as rocprofv3 names it)
+KERNEL_SYMBOL = {"matvec": "oh_k_matvec", "moe_down": "oh_k_mv_down", "delta_step": "oh_k_delta_step",
+                 "attn_out": "oh_k_attn_out", "attn_scores": "oh_k_attn_scores"}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -248,7 +253,7 @@ def main() -> int:
                    "parallelism": "single GPU"},
         "hbm_gbs_step": round(step_gbs, 1), "roofline_frac_step": round(step_gbs / HBM_PEAK_GBS, 4),
         "bytes_per_token": {k: round(v) for k, v in bpt.items()},
-        "roofline": {"bound": "hbm", "kernel": f"oh_k_{dom}" if dom == "matvec" else dom,
+        "roofline": {"bound": "hbm", "kernel": KERNEL_SYMBOL.get(dom, dom),
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
                      "bytes_per_launch": round(d["bytes"] / d["launches"]),

@@ -309,7 +309,8 @@ class Session:
         return ms.value
 
     KERNEL_KINDS = ("matvec", "rmsnorm_q8k", "swiglu_q8k", "embed", "delta_step", "attn_prep",
-                    "attn_scores", "attn_out", "moe_route", "moe_combine", "argmax", "advance")
+                    "attn_scores", "attn_out", "moe_route", "moe_combine", "argmax", "advance",
+                    "moe_down")
 
     def profile_step(self, max_launches: int = 4096):
         """One eager decode step with per-launch HIP-event timing: list of

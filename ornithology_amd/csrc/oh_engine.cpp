@@ -143,7 +143,7 @@ static size_t up256(size_t x) { return (x + 255) & ~(size_t)255; }
 static void plane_bytes(uint32_t t, int64_t rows, int64_t in, size_t *a, size_t *b, size_t *c) {
     if (oh_is_quant(t)) {
         const size_t nblk = (size_t)rows * (size_t)(in / 256);
-        *a = nblk * oh_plane_a(t);
+        *a = oh_plane_a_bytes(t, nblk);
         *b = nblk * oh_plane_b(t);
         *c = nblk * oh_plane_c(t);
     } else {
@@ -160,12 +160,12 @@ static void repack(uint32_t t, const uint8_t *src, size_t nblk, uint8_t *A, uint
     case OH_Q4_K:
         for (size_t i = 0; i < nblk; i++) {
             memcpy(B + 16 * i, src + 144 * i, 16);
-            memcpy(A + 128 * i, src + 144 * i + 16, 128);
+            for (int k = 0; k < 128; k += 16) memcpy(A + oh_a_off(t, i, k), src + 144 * i + 16 + k, 16);
         }
         break;
     case OH_Q6_K:
         for (size_t i = 0; i < nblk; i++) {
-            memcpy(A + 192 * i, src + 210 * i, 192);
+            for (int k = 0; k < 192; k += 16) memcpy(A + oh_a_off(t, i, k), src + 210 * i + k, 16);
             memcpy(B + 16 * i, src + 210 * i + 192, 16);
             memcpy(C + 2 * i, src + 210 * i + 208, 2);
         }
@@ -173,7 +173,8 @@ static void repack(uint32_t t, const uint8_t *src, size_t nblk, uint8_t *A, uint
     case OH_Q8_0:   // nblk counts 256-element super-blocks = 8 GGUF blocks
         for (size_t i = 0; i < nblk; i++)
             for (int k = 0; k < 8; k++) {
-                memcpy(A + 256 * i + 32 * k, src + 272 * i + 34 * k + 2, 32);
+                memcpy(A + oh_a_off(t, i, 32 * k), src + 272 * i + 34 * k + 2, 16);
+                memcpy(A + oh_a_off(t, i, 32 * k + 16), src + 272 * i + 34 * k + 18, 16);
                 memcpy(B + 16 * i + 2 * k, src + 272 * i + 34 * k, 2);
             }
         break;
@@ -264,60 +265,119 @@ extern "C" int ornith_hip_upload(ornith_hip_ctx *ctx, const char *name, uint32_t
 }
 
 // ---- matvec launch builder ------------------------------------------------------------
+// Activation of a matvec segment: Q8_K planes (+ f32 for fallback rows), or
+// formed inside the launch from f32 inputs (RMSNorm or SwiGLU prologue).
 struct Act {
     const int8_t *qs = nullptr;
     const float *d = nullptr;
     const int16_t *bs = nullptr;
     const float *xf = nullptr;
+    int pro = OH_PRO_Q8K;
+    const float *xf2 = nullptr, *nw = nullptr;
+    float eps = 0.0f;
+    int8_t *oqs = nullptr;     // prologue result stored for later launches
+    float *oqd = nullptr;
+    int16_t *oqb = nullptr;
+    float *oxf = nullptr;
 };
 
 struct MvBuild {
     oh_mvlaunch L;
     int lds = 0;
+    int tk = -1;           // kernel variant (see oh_launch_matvec)
     double bytes = 0.0;    // algorithmic HBM bytes: weights read + activation + output
     MvBuild() { memset(&L, 0, sizeof L); }
 };
 
-// rows: rows of one expert for gathered segments, else all rows of W
+static bool seg_q8(const oh_mvseg &s) {
+    return oh_qdot_can((uint32_t)s.type, s.in) && (s.xqs || s.pro != OH_PRO_Q8K);
+}
+
+// rows: rows of one expert for stacked segments, else all rows of W. nsub
+// slots: slot k writes y + k*ystride and reads its activation at k*astride.
 static int mv_add(MvBuild &b, const ornith_hip_tensor *W, const Act &act, float *y, int mode,
-                  const int32_t *eidx = nullptr, int eslot = 0) {
+                  const int32_t *eidx = nullptr, int nsub = 1, int ystride = 0, int astride = 0) {
     if (b.L.n >= OH_MAX_SEGS) { seterr("too many matvec segments"); return ORNITH_HIP_ERR_UNSUPPORTED; }
     oh_mvseg &s = b.L.s[b.L.n];
     memset(&s, 0, sizeof s);
     s.A = W->A; s.B = W->B; s.C = W->C;
     s.xqs = act.qs; s.xd = act.d; s.xbs = act.bs; s.xf = act.xf;
+    s.pro = act.pro; s.xf2 = act.xf2; s.nw = act.nw; s.eps = act.eps;
+    s.oqs = act.oqs; s.oqd = act.oqd; s.oqb = act.oqb; s.oxf = act.oxf;
     s.y = y;
     s.eidx = eidx;
-    s.eslot = eslot;
+    s.nsub = nsub;
+    s.ystride = ystride;
+    s.astride = astride;
     s.type = (int)W->type;
     s.in = (int)W->in;
     s.rows = eidx ? (int)W->dims[1] : (int)W->rows;
     s.mode = mode;
-    int blocks;
-    if (oh_qdot_can(W->type, W->in) && act.qs) {
-        s.nb = (int)(W->in / 256);
-        s.units = s.nb <= 8 ? (s.rows + 8 / s.nb - 1) / (8 / s.nb) : s.rows;
-        blocks = (s.units + 7) / 8;      // 4 waves x 2 units per block
+    s.nb = (int)(W->in / 256);
+    if (act.pro != OH_PRO_Q8K && (W->in % 256 || W->in > 8192)) {
+        seterr("matvec '%s': fused prologue needs in %% 256 == 0 and in <= 8192", W->name.c_str());
+        return ORNITH_HIP_ERR_UNSUPPORTED;
+    }
+    const bool q8 = seg_q8(s);
+    if (q8) {
+        if (s.nb > 64) { seterr("matvec '%s': %d super-blocks per row (max 64)", W->name.c_str(), s.nb); return ORNITH_HIP_ERR_UNSUPPORTED; }
+        const int rps = 64 / s.nb;                  // rows per wave step (one super-block per lane)
+        s.units = (s.rows + rps - 1) / rps;
     } else {
         if (!act.xf) { seterr("matvec '%s': no f32 activation for the fallback path", W->name.c_str()); return ORNITH_HIP_ERR_UNSUPPORTED; }
-        if (W->in > 16384) { seterr("matvec '%s': fallback input %lld too wide", W->name.c_str(), (long long)W->in); return ORNITH_HIP_ERR_UNSUPPORTED; }
-        s.nb = (int)(W->in / 256);
+        if (W->in > 12288) { seterr("matvec '%s': fallback input %lld too wide", W->name.c_str(), (long long)W->in); return ORNITH_HIP_ERR_UNSUPPORTED; }
         s.units = s.rows;
-        blocks = (s.rows + 255) / 256;
-        if ((int)W->in > b.lds) b.lds = (int)W->in;
     }
-    s.block0 = b.L.total_blocks;
-    b.L.total_blocks += blocks;
     b.L.n++;
-    b.bytes += (double)s.rows * (double)gguf_nbytes(W->type, (uint64_t)W->in) +
-               (act.qs && oh_qdot_can(W->type, W->in) ? (double)W->in * (1.0 + 4.0 / 256 + 32.0 / 256)
-                                                     : (double)W->in * 4.0) +
-               (double)s.rows * 4.0 * (mode == 1 ? 2.0 : 1.0);
+    const double act_bytes = act.pro == OH_PRO_NORM ? 8.0 * W->in
+                           : act.pro == OH_PRO_SWIGLU ? 8.0 * W->in
+                           : q8 ? (double)W->in * (1.0 + 4.0 / 256 + 32.0 / 256) : (double)W->in * 4.0;
+    b.bytes += (double)nsub * ((double)s.rows * (double)gguf_nbytes(W->type, (uint64_t)W->in) + act_bytes +
+                               (double)s.rows * 4.0 * (mode == 1 ? 2.0 : 1.0));
     return ORNITH_HIP_OK;
 }
 
+// Lay the segments out over blocks: every wave gets a run of whole wave
+// steps sized so the launch spreads over ~4096 waves (16 per CU).
+static void mv_plan(MvBuild &b) {
+    int64_t steps = 0;
+    int tk = -2;
+    for (int i = 0; i < b.L.n; i++) {
+        const oh_mvseg &s = b.L.s[i];
+        if (seg_q8(s)) {
+            steps += (int64_t)s.units * s.nsub;
+            tk = tk == -2 || tk == s.type ? s.type : -1;
+        } else {
+            tk = -1;
+        }
+    }
+    b.tk = tk < 0 ? -1 : tk;
+    const int64_t spw = (steps + 4095) / 4096;
+    int blocks = 0;
+    b.lds = 0;
+    for (int i = 0; i < b.L.n; i++) {
+        oh_mvseg &s = b.L.s[i];
+        const bool q8 = seg_q8(s);
+        if (q8) {
+            s.upw = (int)(spw > 0 ? spw : 1);
+            s.bps = (s.units + OH_MV_WAVES * s.upw - 1) / (OH_MV_WAVES * s.upw);
+        } else {
+            s.upw = 1;
+            s.bps = (s.rows + 255) / 256;
+        }
+        s.block0 = blocks;
+        blocks += s.bps * s.nsub;
+        const int nb = s.in / 256;
+        const int voff = (nb * 272 + nb * 36 + 15) & ~15;
+        const int need = voff + ((!q8 || s.pro != OH_PRO_Q8K) ? s.in * 4 : 0);
+        if (need > b.lds) b.lds = need;
+    }
+    b.L.total_blocks = blocks;
+}
+
 static int mv_go(MvBuild &b, hipStream_t st) {
-    HCHK(oh_launch_matvec(&b.L, b.lds, st));
+    mv_plan(b);
+    HCHK(oh_launch_matvec(&b.L, b.tk, b.lds, st));
     return ORNITH_HIP_OK;
 }
 
@@ -816,6 +876,7 @@ struct ornith_hip_session {
     float *o = nullptr;
     Q8Buf oq;
     float *qproj = nullptr, *kb = nullptr, *vb = nullptr, *qr = nullptr, *agate = nullptr, *scores = nullptr;
+    int *rcnt = nullptr;          // router launch completion counter (self-resetting)
     float *apart = nullptr;       // split attention: partial outputs [groups][chunks][256]
     int *acnt = nullptr;          // split attention: per-group completion counters (self-resetting)
     int exact_max = 1024;         // contexts up to this walk the attention sum in one block
@@ -837,7 +898,7 @@ struct ornith_hip_session {
 };
 
 enum { K_MATVEC = 0, K_NORM_Q8K, K_SWIGLU_Q8K, K_EMBED, K_DELTA, K_ATTN_PREP, K_ATTN_SCORES,
-       K_ATTN_OUT, K_ROUTE, K_COMBINE, K_ARGMAX, K_ADVANCE };
+       K_ATTN_OUT, K_ROUTE, K_COMBINE, K_ARGMAX, K_ADVANCE, K_MV_DOWN };
 
 static int rec_begin(ornith_hip_session *s, hipStream_t st) {
     if (!s->rec) return ORNITH_HIP_OK;
@@ -897,8 +958,11 @@ static int q8alloc(ornith_hip_session *s, Q8Buf &q, size_t n) {
 static Act act_of(const Q8Buf &q, const float *xf) {
     Act a; a.qs = q.qs; a.d = q.d; a.bs = q.bs; a.xf = xf; return a;
 }
-static Act act_off(const Q8Buf &q, const float *xf, size_t elems) {
-    Act a; a.qs = q.qs + elems; a.d = q.d + elems / 256; a.bs = q.bs + elems / 16; a.xf = xf + elems; return a;
+static Act act_norm(const float *x, const float *w, float eps) {
+    Act a; a.pro = OH_PRO_NORM; a.xf = x; a.nw = w; a.eps = eps; return a;
+}
+static Act act_swiglu(const float *g, const float *u) {
+    Act a; a.pro = OH_PRO_SWIGLU; a.xf = g; a.xf2 = u; return a;
 }
 
 extern "C" int ornith_hip_session_new(ornith_hip_model *m, int cap, ornith_hip_session **out) {
@@ -927,6 +991,7 @@ extern "C" int ornith_hip_session_new(ornith_hip_model *m, int cap, ornith_hip_s
     A_(salloc(s, &s->scores, (size_t)a.nh * s->kvcap));
     A_(salloc(s, &s->apart, (size_t)a.nh * a.hd / 256 * ((s->kvcap + 255) / 256) * 256 + 256));
     A_(salloc(s, &s->acnt, (size_t)a.nh + 64));
+    A_(salloc(s, &s->rcnt, 64));
     {
         const char *e = getenv("ORNITH_HIP_EXACT_ATTN_MAX");
         if (e && *e) s->exact_max = atoi(e);
@@ -997,15 +1062,13 @@ static int enqueue_body(ornith_hip_session *s, hipStream_t st) {
     for (int l = 0; l < a.n_layers; l++) {
         const OhLayer &y = m->L[l];
         LayerState &z = s->ls[l];
-        LAUNCH(K_NORM_Q8K, norm_bytes(H, true),
-               oh_launch_rmsnorm_q8k(s->x, (const float *)y.attn_norm->A, a.eps, H, s->xn, s->xq.qs, s->xq.d, s->xq.bs, st));
-        const Act ax = act_of(s->xq, s->xn);
+        const Act an = act_norm(s->x, (const float *)y.attn_norm->A, a.eps);
         if (y.full) {
             const int aqd = a.nh * a.hd, kvd = a.nkv * a.hd;
             MvBuild b;
-            CHK(mv_add(b, y.q, ax, s->qproj, 0));
-            CHK(mv_add(b, y.k, ax, s->kb, 0));
-            CHK(mv_add(b, y.v, ax, s->vb, 0));
+            CHK(mv_add(b, y.q, an, s->qproj, 0));
+            CHK(mv_add(b, y.k, an, s->kb, 0));
+            CHK(mv_add(b, y.v, an, s->vb, 0));
             MVGO(b);
             LAUNCH(K_ATTN_PREP, 4.0 * (2.0 * aqd + 2.0 * kvd + 2.0 * a.hd) + 8.0 * aqd + 2.0 * (kvd + 4.0 * a.nkv),
                    oh_launch_attn_prep(s->qproj, s->kb, s->vb, (const float *)y.q_norm->A, (const float *)y.k_norm->A,
@@ -1022,10 +1085,10 @@ static int enqueue_body(ornith_hip_session *s, hipStream_t st) {
             MVGO(b2);
         } else {
             MvBuild b;
-            CHK(mv_add(b, y.qkv, ax, s->cat, 0));
-            CHK(mv_add(b, y.gate, ax, s->gate, 0));
-            CHK(mv_add(b, y.alpha, ax, s->ab, 0));
-            CHK(mv_add(b, y.beta, ax, s->ab + a.nv, 0));
+            CHK(mv_add(b, y.qkv, an, s->cat, 0));
+            CHK(mv_add(b, y.gate, an, s->gate, 0));
+            CHK(mv_add(b, y.alpha, an, s->ab, 0));
+            CHK(mv_add(b, y.beta, an, s->ab + a.nv, 0));
             MVGO(b);
             const float out_scale = 1.0f / sqrtf((float)a.dk);
             const double sb = 8.0 * a.nv * a.dk * a.dv + 8.0 * (a.conv_k - 1) * cc + 4.0 * cc * (a.conv_k + 1) +
@@ -1039,60 +1102,74 @@ static int enqueue_body(ornith_hip_session *s, hipStream_t st) {
             CHK(mv_add(b2, y.ssm_out, act_of(s->oq, s->o), s->x, 1));
             MVGO(b2);
         }
-        // FFN: post_attention_norm, then MoE (or dense SwiGLU)
-        LAUNCH(K_NORM_Q8K, norm_bytes(H, true),
-               oh_launch_rmsnorm_q8k(s->x, (const float *)y.post_norm->A, a.eps, H, s->xn, s->xq.qs, s->xq.d, s->xq.bs, st));
+        // FFN: post_attention_norm (formed inside the first FFN launch), then
+        // MoE (or dense SwiGLU)
+        const Act pn = act_norm(s->x, (const float *)y.post_norm->A, a.eps);
         if (a.ne > 0) {
             const int K = a.top_k, I = a.moe_inter, sI = a.shared_inter;
-            const int IW = I > sI ? I : sI;   // row stride of the g/u/h buffers
+            const int IW = I > sI ? I : sI;   // row stride of the g/u buffers
+            // router (+ shared-expert gate) with the top-k routing in the
+            // launch's last block; its first block keeps the normalised
+            // activation for the expert launch
+            Act pst = pn;
+            pst.oqs = s->xq.qs; pst.oqd = s->xq.d; pst.oqb = s->xq.bs; pst.oxf = s->xn;
             MvBuild b;
-            CHK(mv_add(b, y.router, ax, s->rl, 0));
-            if (y.gate_inp_sh) CHK(mv_add(b, y.gate_inp_sh, ax, s->shl, 0));
+            CHK(mv_add(b, y.router, pst, s->rl, 0));
+            if (y.gate_inp_sh) CHK(mv_add(b, y.gate_inp_sh, pn, s->shl, 0));
+            b.L.ep = OH_EP_ROUTE;
+            b.L.cnt = s->rcnt;
+            b.L.rlog = s->rl;
+            b.L.shl = y.gate_inp_sh ? s->shl : nullptr;
+            b.L.ne = a.ne;
+            b.L.topk = K;
+            b.L.ridx = s->eidx;
+            b.L.rw = s->ew;
+            b.L.shg = s->shg;
+            b.bytes += 8.0 * K;
             MVGO(b);
-            LAUNCH(K_ROUTE, 4.0 * a.ne + 8.0 * K,
-                   oh_launch_moe_route(s->rl, a.ne, K, y.gate_inp_sh ? s->shl : nullptr, s->eidx, s->ew, s->shg, st));
+            const Act ax = act_of(s->xq, s->xn);
             MvBuild b2;
-            for (int k = 0; k < K; k++) {
-                CHK(mv_add(b2, y.gate_exps, ax, s->g + (size_t)k * IW, 0, s->eidx, k));
-                CHK(mv_add(b2, y.up_exps, ax, s->u + (size_t)k * IW, 0, s->eidx, k));
-            }
+            CHK(mv_add(b2, y.gate_exps, ax, s->g, 0, s->eidx, K, IW, 0));
+            CHK(mv_add(b2, y.up_exps, ax, s->u, 0, s->eidx, K, IW, 0));
             if (y.gate_sh) {
                 CHK(mv_add(b2, y.gate_sh, ax, s->g + (size_t)K * IW, 0));
                 CHK(mv_add(b2, y.up_sh, ax, s->u + (size_t)K * IW, 0));
             }
             MVGO(b2);
-            const int nvec = K + (y.gate_sh ? 1 : 0);
-            if (I == IW && (!y.gate_sh || sI == IW)) {
-                LAUNCH(K_SWIGLU_Q8K, nvec * norm_bytes(IW, true),
-                       oh_launch_swiglu_q8k(s->g, s->u, IW, nvec, s->h, s->hq.qs, s->hq.d, s->hq.bs, st));
+            const uint32_t dt = y.down_exps->type;
+            const int nbd = I / 256, ns = K + (y.gate_sh ? 1 : 0);
+            const int rps = nbd >= 1 ? 64 / nbd : 1;
+            const int sq = (nbd * 272 + nbd * 36 + 15) & ~15, dlds = ns * sq + ns * I * 4 + ns * rps * 4;
+            const bool fuse = oh_qdot_can(dt, I) && nbd >= 1 && nbd <= 64 && ns <= 16 && dlds <= 65536 &&
+                              (!y.gate_sh || (y.down_sh->type == dt && sI == I));
+            if (fuse) {
+                oh_mvdown D;
+                memset(&D, 0, sizeof D);
+                D.A = y.down_exps->A; D.B = y.down_exps->B; D.C = y.down_exps->C;
+                if (y.gate_sh) { D.sA = y.down_sh->A; D.sB = y.down_sh->B; D.sC = y.down_sh->C; }
+                D.eidx = s->eidx; D.w = s->ew; D.shg = y.gate_inp_sh ? s->shg : nullptr;
+                D.g = s->g; D.u = s->u; D.x = s->x;
+                D.type = (int)dt; D.nb = nbd; D.in = I; D.rows = H; D.k = K; D.stride = IW;
+                const double db = (double)ns * ((double)H * gguf_nbytes(dt, (uint64_t)I) + 8.0 * I) + 8.0 * H + 4.0 * K;
+                LAUNCH(K_MV_DOWN, db, oh_launch_mv_down(&D, (H + rps - 1) / rps, 64 * ns, dlds, st));
             } else {
-                // widths differ: quantise each vector at its own width, same IW stride
-                for (int k = 0; k < nvec; k++) {
-                    const int n = k < K ? I : sI;
-                    const size_t off = (size_t)k * IW;
-                    LAUNCH(K_SWIGLU_Q8K, norm_bytes(n, true),
-                           oh_launch_swiglu_q8k(s->g + off, s->u + off, n, 1, s->h + off, s->hq.qs + off,
-                                                s->hq.d + off / 256, s->hq.bs + off / 16, st));
-                }
+                MvBuild b3;
+                CHK(mv_add(b3, y.down_exps, act_swiglu(s->g, s->u), s->od, 0, s->eidx, K, H, IW));
+                if (y.gate_sh)
+                    CHK(mv_add(b3, y.down_sh, act_swiglu(s->g + (size_t)K * IW, s->u + (size_t)K * IW),
+                               s->od + (size_t)K * H, 0));
+                MVGO(b3);
+                LAUNCH(K_COMBINE, 4.0 * H * (ns + 2),
+                       oh_launch_moe_combine(s->x, s->od, s->ew, K, H, y.gate_sh ? s->od + (size_t)K * H : nullptr,
+                                             y.gate_inp_sh ? s->shg : nullptr, st));
             }
-            MvBuild b3;
-            for (int k = 0; k < K; k++)
-                CHK(mv_add(b3, y.down_exps, act_off(s->hq, s->h, (size_t)k * IW), s->od + (size_t)k * H, 0, s->eidx, k));
-            if (y.gate_sh) CHK(mv_add(b3, y.down_sh, act_off(s->hq, s->h, (size_t)K * IW), s->od + (size_t)K * H, 0));
-            MVGO(b3);
-            LAUNCH(K_COMBINE, 4.0 * H * (nvec + 2),
-                   oh_launch_moe_combine(s->x, s->od, s->ew, K, H, y.gate_sh ? s->od + (size_t)K * H : nullptr,
-                                         y.gate_inp_sh ? s->shg : nullptr, st));
         } else {
-            const int I = a.shared_inter;
             MvBuild b;
-            CHK(mv_add(b, y.ffn_gate, ax, s->g, 0));
-            CHK(mv_add(b, y.ffn_up, ax, s->u, 0));
+            CHK(mv_add(b, y.ffn_gate, pn, s->g, 0));
+            CHK(mv_add(b, y.ffn_up, pn, s->u, 0));
             MVGO(b);
-            LAUNCH(K_SWIGLU_Q8K, norm_bytes(I, true),
-                   oh_launch_swiglu_q8k(s->g, s->u, I, 1, s->h, s->hq.qs, s->hq.d, s->hq.bs, st));
             MvBuild b2;
-            CHK(mv_add(b2, y.ffn_down, act_of(s->hq, s->h), s->x, 1));
+            CHK(mv_add(b2, y.ffn_down, act_swiglu(s->g, s->u), s->x, 1));
             MVGO(b2);
         }
     }
@@ -1103,10 +1180,8 @@ static int enqueue_body(ornith_hip_session *s, hipStream_t st) {
 static int enqueue_head(ornith_hip_session *s, hipStream_t st) {
     const ornith_hip_model *m = s->m;
     const ornith_hip_arch &a = m->a;
-    LAUNCH(K_NORM_Q8K, norm_bytes(a.hidden, true),
-           oh_launch_rmsnorm_q8k(s->x, (const float *)m->out_norm->A, a.eps, a.hidden, s->xn, s->xq.qs, s->xq.d, s->xq.bs, st));
     MvBuild b;
-    CHK(mv_add(b, m->lm_head, act_of(s->xq, s->xn), s->logits, 0));
+    CHK(mv_add(b, m->lm_head, act_norm(s->x, (const float *)m->out_norm->A, a.eps), s->logits, 0));
     MVGO(b);
     LAUNCH(K_ARGMAX, 4.0 * a.vocab,
            oh_launch_argmax(s->logits, a.vocab, s->amv, s->ami, OH_ARGMAX_BLOCKS, s->toks, s->io, s->io + 1, st));
@@ -1320,15 +1395,20 @@ extern "C" int ornith_hip_tensor_download(const ornith_hip_tensor *t, void *out,
     const size_t nblk = (size_t)t->rows * (size_t)(t->in / 256);
     for (size_t i = 0; i < nblk; i++) {
         switch (t->type) {
-        case OH_Q4_K: memcpy(o + 144 * i, B + 16 * i, 16); memcpy(o + 144 * i + 16, A + 128 * i, 128); break;
+        case OH_Q4_K:
+            memcpy(o + 144 * i, B + 16 * i, 16);
+            for (int k = 0; k < 128; k += 16) memcpy(o + 144 * i + 16 + k, A + oh_a_off(t->type, i, k), 16);
+            break;
         case OH_Q6_K:
-            memcpy(o + 210 * i, A + 192 * i, 192); memcpy(o + 210 * i + 192, B + 16 * i, 16);
+            for (int k = 0; k < 192; k += 16) memcpy(o + 210 * i + k, A + oh_a_off(t->type, i, k), 16);
+            memcpy(o + 210 * i + 192, B + 16 * i, 16);
             memcpy(o + 210 * i + 208, C + 2 * i, 2);
             break;
         case OH_Q8_0:
             for (int k = 0; k < 8; k++) {
                 memcpy(o + 272 * i + 34 * k, B + 16 * i + 2 * k, 2);
-                memcpy(o + 272 * i + 34 * k + 2, A + 256 * i + 32 * k, 32);
+                memcpy(o + 272 * i + 34 * k + 2, A + oh_a_off(t->type, i, 32 * k), 16);
+                memcpy(o + 272 * i + 34 * k + 18, A + oh_a_off(t->type, i, 32 * k + 16), 16);
             }
             break;
         case OH_IQ2_XXS: memcpy(o + 66 * i, C + 2 * i, 2); memcpy(o + 66 * i + 2, A + 64 * i, 64); break;

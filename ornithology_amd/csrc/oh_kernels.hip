@@ -7,10 +7,17 @@
 
 extern "C" {
 
-hipError_t oh_launch_matvec(const oh_mvlaunch *L, int lds_floats, hipStream_t st) {
+hipError_t oh_launch_matvec(const oh_mvlaunch *L, int tk, int lds_bytes, hipStream_t st) {
     if (L->total_blocks <= 0) return hipSuccess;
-    hipLaunchKernelGGL(oh_k_matvec, dim3(L->total_blocks), dim3(256),
-                       (size_t)lds_floats * sizeof(float), st, *L);
+    void (*k)(oh_mvlaunch) = tk == OH_Q4_K ? oh_k_mv_q4k : tk == OH_Q6_K ? oh_k_mv_q6k
+                           : tk == OH_Q8_0 ? oh_k_mv_q80 : oh_k_mv_mixed;
+    hipLaunchKernelGGL(k, dim3(L->total_blocks), dim3(256), (size_t)lds_bytes, st, *L);
+    return hipGetLastError();
+}
+
+hipError_t oh_launch_mv_down(const oh_mvdown *D, int blocks, int threads, int lds_bytes, hipStream_t st) {
+    if (blocks <= 0) return hipSuccess;
+    hipLaunchKernelGGL(oh_k_mv_down, dim3(blocks), dim3(threads), (size_t)lds_bytes, st, *D);
     return hipGetLastError();
 }
 

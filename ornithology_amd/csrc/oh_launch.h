@@ -6,7 +6,10 @@
 #include "oh_types.h"
 
 extern "C" {
-hipError_t oh_launch_matvec(const oh_mvlaunch *L, int lds_floats, hipStream_t st);
+// tk: the integer-path type every segment has (OH_Q4_K/OH_Q6_K/OH_Q8_0), or -1
+// for a launch that mixes types or has fallback segments
+hipError_t oh_launch_matvec(const oh_mvlaunch *L, int tk, int lds_bytes, hipStream_t st);
+hipError_t oh_launch_mv_down(const oh_mvdown *D, int blocks, int threads, int lds_bytes, hipStream_t st);
 hipError_t oh_launch_rmsnorm_q8k(const float *x, const float *norm_w, float eps, int n,
                                  float *xn_out, int8_t *qs, float *d, int16_t *bs, hipStream_t st);
 hipError_t oh_launch_swiglu_q8k(const float *g, const float *u, int n, int count, float *h_out,

@@ -21,7 +21,7 @@ OH_DEV float dec_elem(const uint8_t *A, const uint8_t *B, const uint8_t *C, int 
     if (type == OH_Q4_K) {
         const uint4 hdr = *(const uint4 *)(B + bi * 16);
         const int j = k / 32, l = k % 32;
-        const uint8_t q = A[bi * 128 + 32 * (j / 2) + l];
+        const uint8_t q = A[oh_a_off(OH_Q4_K, bi, 32 * (j / 2) + l)];
         int sc, mn;
         q4k_sm(hdr, j, sc, mn);
         const float d1 = h2f((uint16_t)(hdr.x & 0xffffu)) * sc;
@@ -29,17 +29,16 @@ OH_DEV float dec_elem(const uint8_t *A, const uint8_t *B, const uint8_t *C, int 
         return d1 * (float)((j & 1) ? (q >> 4) : (q & 15)) - m1;
     }
     if (type == OH_Q6_K) {
-        const uint8_t *a = A + bi * 192;
         const int hh = k / 128, kk = k % 128, qd = kk / 32, l = kk % 32;
-        const uint8_t ql = a[64 * hh + l + 32 * (qd & 1)];
-        const uint8_t qh = a[128 + 32 * hh + l];
+        const uint8_t ql = A[oh_a_off(OH_Q6_K, bi, 64 * hh + l + 32 * (qd & 1))];
+        const uint8_t qh = A[oh_a_off(OH_Q6_K, bi, 128 + 32 * hh + l)];
         const int lo = (qd < 2) ? (ql & 15) : (ql >> 4);
         const int q = (lo | (((qh >> (2 * qd)) & 3) << 4)) - 32;
         const int8_t sc = (int8_t)B[bi * 16 + 8 * hh + l / 16 + 2 * qd];
         return h2f(*(const uint16_t *)(C + bi * 2)) * (float)sc * (float)q;
     }
     if (type == OH_Q8_0)
-        return (float)(int8_t)A[bi * 256 + k] * h2f(*(const uint16_t *)(B + bi * 16 + 2 * (k / 32)));
+        return (float)(int8_t)A[oh_a_off(OH_Q8_0, bi, k)] * h2f(*(const uint16_t *)(B + bi * 16 + 2 * (k / 32)));
     if (type == OH_IQ2_XXS) {
         const float dd = h2f(*(const uint16_t *)(C + bi * 2));
         const uint32_t *q = (const uint32_t *)(A + bi * 64);
@@ -392,40 +391,7 @@ oh_k_attn_out(const float *scores, const int8_t *Vq, const float *Vs, const floa
 extern "C" __global__ void __launch_bounds__(64)
 oh_k_moe_route(const float *logits, int ne, int k, const float *shgate_logit,
                int32_t *idx, float *w, float *shgate) {
-    // logits live in registers: lane owns experts lane + 64*j (j < 16, ne <= 1024)
-    const int lane = (int)threadIdx.x;
-    float v[16];
-#pragma unroll
-    for (int j = 0; j < 16; j++) v[j] = lane + 64 * j < ne ? logits[lane + 64 * j] : -INFINITY;
-    uint32_t taken = 0;
-    float mine = 0.0f;                     // lane s keeps the s-th selected logit
-    int sel = 0;
-    for (int s = 0; s < k; s++) {
-        float bv = -INFINITY; int bi = 0x7fffffff;
-#pragma unroll
-        for (int j = 0; j < 16; j++) {
-            const int e = lane + 64 * j;
-            if (e < ne && !(taken >> j & 1u) && v[j] > bv) { bv = v[j]; bi = e; }
-        }
-        for (int m = 32; m >= 1; m >>= 1) {
-            const float ov = shfl_xor(bv, m); const int oi = shfl_xor(bi, m);
-            if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
-        }
-        if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
-        if (lane == s) { mine = bv; sel = bi; }
-    }
-    // NaN/-inf logits can leave no candidate: never hand an out-of-range
-    // expert index to the gathered matvec
-    if (sel < 0 || sel >= ne) sel = 0;
-    if (lane < k) idx[lane] = sel;
-    // softmax over the selected logits in selection order (src/ornith_moe.c:23-29)
-    float mx = shfl(mine, 0);
-    for (int s = 1; s < k; s++) { const float x = shfl(mine, s); if (x > mx) mx = x; }
-    const float e = ref_expf(mine - mx);
-    float sum = 0.0f;
-    for (int s = 0; s < k; s++) sum += shfl(e, s);
-    if (lane < k) w[lane] = e / sum;
-    if (lane == 0 && shgate_logit) *shgate = ref_sigmoid(*shgate_logit);
+    route_wave(logits, ne, k, shgate_logit, idx, w, shgate);
 }
 
 // x += sum_s w_s * o_s (sequential in s, from 0) + shared * gate

@@ -12,9 +12,14 @@
 //
 // Work mapping of the Q8_K path: a wave64 is 8 groups x 8 lanes; a group owns
 // one 256-element super-block and each lane 32 of its weights, loaded with
-// 8/16-byte vector loads from the plane layout (contiguous across the
-// group). A wave unit is one row (nb >= 8 super-blocks per row, in passes of
-// 8) or 8/nb rows (nb < 8).
+// 8/16-byte vector loads from the plane layout (contiguous across the group).
+// A unit is one row (nb > 8 super-blocks per row, taken in passes of 8) or
+// 8/nb rows (nb <= 8); a step is one unit-pass. Each wave owns a contiguous
+// run of units and streams its steps in batches of OH_MV_R with the next
+// batch's weight loads in flight while the current batch is reduced. The
+// activation (Q8_K codes, bsums, scales) sits in LDS; the block forms it in a
+// prologue (copy, RMSNorm + Q8_K, or SwiGLU + Q8_K) while the first batch of
+// weights is being fetched.
 #include "oh_common.h"
 #include "oh_types.h"
 #include "../../include/ornith_iq2xxs_grid.h"
@@ -23,14 +28,19 @@ __constant__ uint64_t k_iq2_grid[256] = { ORNITH_IQ2XXS_GRID_VALUES };
 
 namespace {
 
-constexpr int kWavesPerBlock = 4;
-constexpr int kUnitsPerWave = 2;
-
 OH_DEV uint32_t wsel(const uint4 &v, int k) {   // 32-bit word k of a uint4
     return k == 0 ? v.x : (k == 1 ? v.y : (k == 2 ? v.z : v.w));
 }
 OH_DEV uint32_t bsel(const uint4 &v, int k) {   // byte k of a uint4
     return (wsel(v, k >> 2) >> (8 * (k & 3))) & 0xffu;
+}
+
+// Block barrier that orders LDS only: it does not wait for the block's
+// outstanding global loads (prefetched weights).
+OH_DEV void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
 // 6-bit (scale, min) of sub-block j from the 12 packed bytes that start at
@@ -50,129 +60,201 @@ OH_DEV int group_isum(int v) {     // exact sum over the 8 lanes of a group
     return v;
 }
 
-// Float term of super-block sb for the group's row; identical in all 8 lanes.
-// bi = row*nb + sb indexes the planes. c = lane within the group.
-OH_DEV float term_q4k(const oh_mvseg &s, int64_t bi, int sb, int c) {
-    const uint4 hdr = *(const uint4 *)(s.B + bi * 16);
-    const uint4 q = *(const uint4 *)(s.A + bi * 128 + 16 * c);
-    const int p = c >> 1, h = c & 1;
-    const int8_t *aq = s.xqs + (int64_t)sb * 256;
-    const int4 alo = *(const int4 *)(aq + 64 * p + 16 * h);
-    const int4 ahi = *(const int4 *)(aq + 64 * p + 32 + 16 * h);
-    int dlo = 0, dhi = 0;
-    dlo = dot4((int)(q.x & 0x0f0f0f0fu), alo.x, dlo);
-    dlo = dot4((int)(q.y & 0x0f0f0f0fu), alo.y, dlo);
-    dlo = dot4((int)(q.z & 0x0f0f0f0fu), alo.z, dlo);
-    dlo = dot4((int)(q.w & 0x0f0f0f0fu), alo.w, dlo);
-    dhi = dot4((int)((q.x >> 4) & 0x0f0f0f0fu), ahi.x, dhi);
-    dhi = dot4((int)((q.y >> 4) & 0x0f0f0f0fu), ahi.y, dhi);
-    dhi = dot4((int)((q.z >> 4) & 0x0f0f0f0fu), ahi.z, dhi);
-    dhi = dot4((int)((q.w >> 4) & 0x0f0f0f0fu), ahi.w, dhi);
-    int sc0, mn0, sc1, mn1, scc, mnc;
-    q4k_sm(hdr, 2 * p, sc0, mn0);
-    q4k_sm(hdr, 2 * p + 1, sc1, mn1);
-    q4k_sm(hdr, c, scc, mnc);
-    const int16_t *bs = s.xbs + (int64_t)sb * 16;
-    int isum = group_isum(sc0 * dlo + sc1 * dhi);
-    int mins = group_isum(mnc * ((int)bs[2 * c] + (int)bs[2 * c + 1]));
-    const float yd = s.xd[sb];
-    const float d = yd * h2f((uint16_t)(hdr.x & 0xffffu));
-    const float dm = -yd * h2f((uint16_t)(hdr.x >> 16));
+// ---- Q8_K quantisation of one 256-element block held in LDS ------------------
+// One wave; exactly qdot_quantize_row_q8_K (src/ornith_qdot.c:32-62): the first
+// element of largest magnitude sets iscale = -127/x, codes = rint(iscale*x)
+// clamped, bsums per 16, d = 1/iscale.
+OH_DEV void q8k_block_from_lds(const float *v, int qb, int8_t *qs, float *d, int16_t *bs,
+                               int qstride = 256) {
+    const int lane = lane_id();
+    const float *xb = v + qb * 256;
+    float best = -1.0f; int bi = 0;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const int e = lane + 64 * k;
+        const float a = fabsf(xb[e]);
+        if (a > best) { best = a; bi = e; }
+    }
+    for (int m = 32; m >= 1; m >>= 1) {
+        const float ob = shfl_xor(best, m);
+        const int oi = shfl_xor(bi, m);
+        if (ob > best || (ob == best && oi < bi)) { best = ob; bi = oi; }
+    }
+    int8_t *q = qs + (int64_t)qb * qstride;
+    int16_t *b = bs + (int64_t)qb * 16;
+    if (best == 0.0f || !(best > 0.0f)) {
+#pragma unroll
+        for (int k = 0; k < 4; k++) q[lane + 64 * k] = 0;
+        if (lane < 16) b[lane] = 0;
+        if (lane == 0) d[qb] = 0.0f;
+        return;
+    }
+    const float iscale = -127.0f / xb[bi];
+    int sums[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const int e = lane + 64 * k;
+        float r = __builtin_rintf(iscale * xb[e]);
+        int v = (int)r;
+        v = v > 127 ? 127 : (v < -128 ? -128 : v);
+        q[e] = (int8_t)v;
+        sums[k] = v;
+    }
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        int sv = sums[k];
+        sv += shfl_xor(sv, 1); sv += shfl_xor(sv, 2); sv += shfl_xor(sv, 4); sv += shfl_xor(sv, 8);
+        if ((lane & 15) == 0) b[4 * k + (lane >> 4)] = (int16_t)sv;
+    }
+    if (lane == 0) d[qb] = 1.0f / iscale;
+}
+
+// In-place RMSNorm of v[0..n) in LDS (src/ornith_tensor.c:100-106): sum of
+// squares in double (tree-ordered), inv = (float)(1/sqrt(ss/n+eps)),
+// v_i = v_i * inv * w_i. All 256 threads; v must be visible block-wide.
+OH_DEV void rmsnorm_lds(float *v, const float *w, float eps, int n, double *red) {
+    const int tid = (int)threadIdx.x, wave = tid >> 6;
+    double ss = 0.0;
+    for (int i = tid; i < n; i += 256) ss += (double)v[i] * v[i];
+    ss = wave_sum_d(ss);
+    if (lane_id() == 0) red[wave] = ss;
+    lds_barrier();
+    const double tot = (red[0] + red[1]) + (red[2] + red[3]);
+    const float inv = (float)(1.0 / sqrt(tot / (double)n + (double)eps));
+    for (int i = tid; i < n; i += 256) v[i] = v[i] * inv * w[i];
+    lds_barrier();
+}
+
+// ---- one super-block per lane ----------------------------------------------------
+// A lane owns one 256-element super-block of a weight row: it loads the
+// block's A-plane pieces (coalesced across the wave by the tile interleave)
+// and its B/C bytes, and reduces them against the activation super-block in
+// LDS. Integer sums are exact in any order; the float term keeps the
+// reference's operations (src/ornith_qdot.c:64-216).
+struct WP { const uint8_t *A, *B, *C; };
+template <int T> struct SB;
+template <> struct SB<OH_Q4_K> { uint4 q[8]; uint4 h; };              // qs, d/dmin/scales
+template <> struct SB<OH_Q6_K> { uint4 q[12]; uint4 sc; uint32_t d; }; // ql+qh, scales, d
+template <> struct SB<OH_Q8_0> { uint4 q[16]; uint4 d; };             // 8 x qs[32], 8 x d
+
+// piece k of super-block bi is at [k * 64] of the returned pointer
+OH_DEV const uint4 *a_tile(const uint8_t *A, int pb, int64_t bi) {
+    return (const uint4 *)(A + (bi >> 6) * (int64_t)(64 * pb)) + (bi & 63);
+}
+OH_DEV void sb_load(SB<OH_Q4_K> &r, const WP &w, int64_t bi) {
+    const uint4 *a = a_tile(w.A, 128, bi);
+#pragma unroll
+    for (int k = 0; k < 8; k++) r.q[k] = a[k * 64];
+    r.h = *(const uint4 *)(w.B + bi * 16);
+}
+OH_DEV void sb_load(SB<OH_Q6_K> &r, const WP &w, int64_t bi) {
+    const uint4 *a = a_tile(w.A, 192, bi);
+#pragma unroll
+    for (int k = 0; k < 12; k++) r.q[k] = a[k * 64];
+    r.sc = *(const uint4 *)(w.B + bi * 16);
+    r.d = *(const uint16_t *)(w.C + bi * 2);
+}
+OH_DEV void sb_load(SB<OH_Q8_0> &r, const WP &w, int64_t bi) {
+    const uint4 *a = a_tile(w.A, 256, bi);
+#pragma unroll
+    for (int k = 0; k < 16; k++) r.q[k] = a[k * 64];
+    r.d = *(const uint4 *)(w.B + bi * 16);
+}
+
+OH_DEV uint32_t pword(const uint4 *q, int w) { return wsel(q[w >> 2], w & 3); }
+OH_DEV int aword(const int4 *a, int w) {
+    const int4 v = a[w >> 2];
+    return (w & 3) == 0 ? v.x : ((w & 3) == 1 ? v.y : ((w & 3) == 2 ? v.z : v.w));
+}
+
+// Q4_K: isum = sum_j sc_j * dot_j, mins = sum_j mn_j * (bsum_2j + bsum_2j+1);
+// term = yd*d * isum + (-yd*dmin) * mins
+OH_DEV float sb_term(const SB<OH_Q4_K> &r, const int8_t *aq, const int16_t *bs, float yd) {
+    const uint32_t y = r.h.y, z = r.h.z, w = r.h.w;
+    // 6-bit scales / mins of sub-blocks 0-3 and 4-7, one per byte
+    const uint32_t scl = y & 0x3f3f3f3fu, sch = (w & 0x0f0f0f0fu) | ((y >> 2) & 0x30303030u);
+    const uint32_t mnl = z & 0x3f3f3f3fu, mnh = ((w >> 4) & 0x0f0f0f0fu) | ((z >> 2) & 0x30303030u);
+    const int4 *a4 = (const int4 *)aq;
+    const uint32_t M = 0x0f0f0f0fu;
+    int isum = 0;
+#pragma unroll
+    for (int p = 0; p < 4; p++) {
+        int dl = 0, dh = 0;
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const uint32_t qv = pword(r.q, 8 * p + k);
+            dl = dot4((int)(qv & M), aword(a4, 16 * p + k), dl);
+            dh = dot4((int)((qv >> 4) & M), aword(a4, 16 * p + 8 + k), dh);
+        }
+        const uint32_t sw = p < 2 ? scl : sch;
+        const int s0 = (int)((sw >> (8 * ((2 * p) & 3))) & 0xffu);
+        const int s1 = (int)((sw >> (8 * ((2 * p + 1) & 3))) & 0xffu);
+        isum += s0 * dl + s1 * dh;
+    }
+    int mins = 0;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const int mn = (int)(((j < 4 ? mnl : mnh) >> (8 * (j & 3))) & 0xffu);
+        mins += mn * ((int)bs[2 * j] + (int)bs[2 * j + 1]);
+    }
+    const float d = yd * h2f((uint16_t)(r.h.x & 0xffffu));
+    const float dm = -yd * h2f((uint16_t)(r.h.x >> 16));
     return d * (float)isum + dm * (float)mins;
 }
 
-OH_DEV float term_q6k(const oh_mvseg &s, int64_t bi, int sb, int c) {
-    const int hh = c >> 2, m = c & 3;
-    const uint8_t *a = s.A + bi * 192;
-    const uint2 qa = *(const uint2 *)(a + 64 * hh + 8 * m);
-    const uint2 qb = *(const uint2 *)(a + 64 * hh + 32 + 8 * m);
-    const uint2 qh = *(const uint2 *)(a + 128 + 32 * hh + 8 * m);
-    const uint4 scv = *(const uint4 *)(s.B + bi * 16);
-    const int is = 8 * hh + (m >> 1);
-    const int sc1 = (int)(int8_t)bsel(scv, is), sc2 = (int)(int8_t)bsel(scv, is + 2);
-    const int sc3 = (int)(int8_t)bsel(scv, is + 4), sc4 = (int)(int8_t)bsel(scv, is + 6);
-    const int8_t *aq = s.xqs + (int64_t)sb * 256 + 128 * hh + 8 * m;
-    const int2 a1 = *(const int2 *)(aq), a2 = *(const int2 *)(aq + 32);
-    const int2 a3 = *(const int2 *)(aq + 64), a4 = *(const int2 *)(aq + 96);
-    int d1 = 0, d2 = 0, d3 = 0, d4 = 0, s1 = 0, s2 = 0, s3 = 0, s4 = 0;
+// Q6_K: sum over 16-element groups g of sc_g * (sum q*a - 32 * bsum_g);
+// term = (yd * d) * isum
+OH_DEV float sb_term(const SB<OH_Q6_K> &r, const int8_t *aq, const int16_t *bs, float yd) {
+    const int4 *a4 = (const int4 *)aq;
+    int isum = 0;
 #pragma unroll
-    for (int w = 0; w < 2; w++) {
-        const uint32_t la = w ? qa.y : qa.x, lb = w ? qb.y : qb.x, hb = w ? qh.y : qh.x;
-        const int q1 = (int)((la & 0x0f0f0f0fu) | ((hb & 0x03030303u) << 4));
-        const int q2 = (int)((lb & 0x0f0f0f0fu) | (((hb >> 2) & 0x03030303u) << 4));
-        const int q3 = (int)(((la >> 4) & 0x0f0f0f0fu) | (((hb >> 4) & 0x03030303u) << 4));
-        const int q4 = (int)(((lb >> 4) & 0x0f0f0f0fu) | (((hb >> 6) & 0x03030303u) << 4));
-        const int x1 = w ? a1.y : a1.x, x2 = w ? a2.y : a2.x, x3 = w ? a3.y : a3.x, x4 = w ? a4.y : a4.x;
-        d1 = dot4(q1, x1, d1); s1 = dot4(0x01010101, x1, s1);
-        d2 = dot4(q2, x2, d2); s2 = dot4(0x01010101, x2, s2);
-        d3 = dot4(q3, x3, d3); s3 = dot4(0x01010101, x3, s3);
-        d4 = dot4(q4, x4, d4); s4 = dot4(0x01010101, x4, s4);
+    for (int hh = 0; hh < 2; hh++) {
+        int D[8] = {0, 0, 0, 0, 0, 0, 0, 0};       // group 8hh + t
+#pragma unroll
+        for (int w = 0; w < 8; w++) {
+            const uint32_t la = pword(r.q, 16 * hh + w);        // ql[64hh + 4w ..]
+            const uint32_t lb = pword(r.q, 16 * hh + 8 + w);    // ql[64hh + 32 + 4w ..]
+            const uint32_t hb = pword(r.q, 32 + 8 * hh + w);    // qh[32hh + 4w ..]
+            const int q1 = (int)((la & 0x0f0f0f0fu) | ((hb & 0x03030303u) << 4));
+            const int q2 = (int)((lb & 0x0f0f0f0fu) | (((hb >> 2) & 0x03030303u) << 4));
+            const int q3 = (int)(((la >> 4) & 0x0f0f0f0fu) | (((hb >> 4) & 0x03030303u) << 4));
+            const int q4 = (int)(((lb >> 4) & 0x0f0f0f0fu) | (((hb >> 6) & 0x03030303u) << 4));
+            const int e = 32 * hh + w;                           // activation word of element 128hh + 4w
+            const int is = w >> 2;
+            D[0 + is] = dot4(q1, aword(a4, e), D[0 + is]);
+            D[2 + is] = dot4(q2, aword(a4, e + 8), D[2 + is]);
+            D[4 + is] = dot4(q3, aword(a4, e + 16), D[4 + is]);
+            D[6 + is] = dot4(q4, aword(a4, e + 24), D[6 + is]);
+        }
+#pragma unroll
+        for (int t = 0; t < 8; t++) {
+            const int g = 8 * hh + t;
+            const int sc = (int)(int8_t)bsel(r.sc, g);
+            isum += sc * (D[t] - 32 * (int)bs[g]);
+        }
     }
-    // sum_l q8 * (q - 32) * sc  ==  sc * (sum q8*q - 32 * sum q8), exactly
-    const int part = sc1 * (d1 - 32 * s1) + sc2 * (d2 - 32 * s2) +
-                     sc3 * (d3 - 32 * s3) + sc4 * (d4 - 32 * s4);
-    const int isum = group_isum(part);
-    const float d = s.xd[sb] * h2f(*(const uint16_t *)(s.C + bi * 2));
+    const float d = yd * h2f((uint16_t)r.d);
     return d * (float)isum;
 }
 
-OH_DEV float term_q8_0(const oh_mvseg &s, int64_t bi, int sb, int c) {
-    const int8_t *w = (const int8_t *)(s.A + bi * 256 + 32 * c);
-    const int4 w0 = *(const int4 *)w, w1 = *(const int4 *)(w + 16);
-    const int8_t *aq = s.xqs + (int64_t)sb * 256 + 32 * c;
-    const int4 a0 = *(const int4 *)aq, a1 = *(const int4 *)(aq + 16);
-    int is = 0;
-    is = dot4(w0.x, a0.x, is); is = dot4(w0.y, a0.y, is);
-    is = dot4(w0.z, a0.z, is); is = dot4(w0.w, a0.w, is);
-    is = dot4(w1.x, a1.x, is); is = dot4(w1.y, a1.y, is);
-    is = dot4(w1.z, a1.z, is); is = dot4(w1.w, a1.w, is);
-    const float prod = h2f(*(const uint16_t *)(s.B + bi * 16 + 2 * c)) * (float)is;
-    // blk_sum += wd * isum over the 8 Q8_0 blocks in order
-    const int base = lane_id() & ~7;
+// Q8_0: part = sum_b d_b * isum_b (in order); term = yd * part
+OH_DEV float sb_term(const SB<OH_Q8_0> &r, const int8_t *aq, const int16_t *, float yd) {
+    const int4 *a4 = (const int4 *)aq;
     float part = 0.0f;
 #pragma unroll
-    for (int k = 0; k < 8; k++) part += shfl(prod, base + k);
-    return s.xd[sb] * part;
-}
-
-template <int T>
-OH_DEV float term(const oh_mvseg &s, int64_t bi, int sb, int c) {
-    if (T == OH_Q4_K) return term_q4k(s, bi, sb, c);
-    if (T == OH_Q6_K) return term_q6k(s, bi, sb, c);
-    return term_q8_0(s, bi, sb, c);
-}
-
-OH_DEV void emit(const oh_mvseg &s, int row, float v) {
-    if (s.mode == 1) s.y[row] = s.y[row] + v;
-    else s.y[row] = v;
-}
-
-// One wave unit of a Q8_K-path segment.
-template <int T>
-OH_DEV void wave_unit(const oh_mvseg &s, int unit, int64_t row_base) {
-    const int lane = lane_id(), g = lane >> 3, c = lane & 7, nb = s.nb;
-    if (nb <= 8) {
-        const int rp = 8 / nb;
-        const int k = g / nb, sb = g - k * nb;
-        const int row = unit * rp + k;
-        const bool live = k < rp && row < s.rows;
-        float t = 0.0f;
-        if (live) t = term<T>(s, (row_base + row) * nb + sb, sb, c);
-        float acc = 0.0f;
-        for (int i = 0; i < nb; i++) acc += shfl(t, (k * nb + i) * 8);
-        if (live && sb == 0 && c == 0) emit(s, row, acc);
-    } else {
-        const int row = unit;
-        float acc = 0.0f;
-        for (int p0 = 0; p0 < nb; p0 += 8) {
-            const int sb = p0 + g;
-            float t = 0.0f;
-            if (sb < nb) t = term<T>(s, (row_base + row) * nb + sb, sb, c);
-            const int cnt = nb - p0 < 8 ? nb - p0 : 8;
-            for (int i = 0; i < cnt; i++) acc += shfl(t, i * 8);
-        }
-        if (lane == 0) emit(s, row, acc);
+    for (int b = 0; b < 8; b++) {
+        int is = 0;
+#pragma unroll
+        for (int k = 0; k < 8; k++) is = dot4((int)pword(r.q, 8 * b + k), aword(a4, 8 * b + k), is);
+        const uint16_t dh = (uint16_t)(wsel(r.d, b >> 1) >> (16 * (b & 1)));
+        part += h2f(dh) * (float)is;
     }
+    return yd * part;
+}
+
+OH_DEV void emit(float *y, int mode, int row, float v) {
+    if (mode == 1) y[row] = y[row] + v;
+    else y[row] = v;
 }
 
 // Fallback row: dequantise on the fly and accumulate w_i * x_i strictly in
@@ -214,36 +296,258 @@ OH_DEV float row_seq(const oh_mvseg &s, int64_t r, const float *x) {
     return acc;
 }
 
-} // namespace
+// ---- MoE routing of one wave (src/ornith_moe.c:8-30) ----------------------------
+// Top-k by repeated argmax (largest logit, lowest index on ties), then softmax
+// over the selected logits in selection order; the optional shared-expert gate
+// is sigmoid of its logit. ne <= 1024, k <= 64.
+OH_DEV void route_wave(const float *logits, int ne, int k, const float *shgate_logit,
+                       int32_t *idx, float *w, float *shgate) {
+    const int lane = lane_id();
+    float v[16];
+#pragma unroll
+    for (int j = 0; j < 16; j++) v[j] = lane + 64 * j < ne ? logits[lane + 64 * j] : -INFINITY;
+    uint32_t taken = 0;
+    float mine = 0.0f;                     // lane s keeps the s-th selected logit
+    int sel = 0;
+    for (int s = 0; s < k; s++) {
+        float bv = -INFINITY; int bi = 0x7fffffff;
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            const int e = lane + 64 * j;
+            if (e < ne && !(taken >> j & 1u) && v[j] > bv) { bv = v[j]; bi = e; }
+        }
+        for (int m = 32; m >= 1; m >>= 1) {
+            const float ov = shfl_xor(bv, m); const int oi = shfl_xor(bi, m);
+            if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+        }
+        if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
+        if (lane == s) { mine = bv; sel = bi; }
+    }
+    // NaN/-inf logits can leave no candidate: never hand an out-of-range
+    // expert index to the gathered matvec
+    if (sel < 0 || sel >= ne) sel = 0;
+    if (lane < k) idx[lane] = sel;
+    float mx = shfl(mine, 0);
+    for (int s = 1; s < k; s++) { const float x = shfl(mine, s); if (x > mx) mx = x; }
+    const float e = ref_expf(mine - mx);
+    float sum = 0.0f;
+    for (int s = 0; s < k; s++) sum += shfl(e, s);
+    if (lane < k) w[lane] = e / sum;
+    if (lane == 0 && shgate_logit) *shgate = ref_sigmoid(*shgate_logit);
+}
 
-// Multi-segment matvec. Q8_K-path segments: block = 4 waves x 2 units.
-// Fallback segments: block = 256 rows, one lane per row, x staged in LDS.
-extern "C" __global__ void __launch_bounds__(256)
-oh_k_matvec(oh_mvlaunch L) {
-    extern __shared__ float xs[];   // fallback segments only: in floats
+// ---- LDS layout of a matvec block ---------------------------------------------
+// [qs: nb x 272 B (256 codes + 16 B bank spread)][bsums: nb*16 int16][d: nb f32]
+// [pad to 16][v: in f32 (prologue input / fallback activation)]
+constexpr int kAS = 272;
+OH_HD inline int mv_lds_bs_off(int nb) { return nb * kAS; }
+OH_HD inline int mv_lds_d_off(int nb) { return nb * kAS + nb * 32; }
+OH_HD inline int mv_lds_v_off(int nb) { return (nb * kAS + nb * 36 + 15) & ~15; }
+
+// Block prologue: form the slot's activation in LDS. q8: Q8_K planes are
+// needed (integer path); otherwise only the f32 vector v.
+OH_DEV void mv_prologue(const oh_mvseg &s, int slot, int blk, uint8_t *smem, double *red, bool q8) {
+    const int in = s.in, nb = in / 256, tid = (int)threadIdx.x, wave = tid >> 6;
+    int8_t *aqs = (int8_t *)smem;
+    int16_t *abs = (int16_t *)(smem + mv_lds_bs_off(nb));
+    float *ad = (float *)(smem + mv_lds_d_off(nb));
+    float *v = (float *)(smem + mv_lds_v_off(nb));
+    const size_t ao = (size_t)slot * s.astride;
+    if (s.pro == OH_PRO_Q8K) {
+        if (q8) {
+            const int4 *gq = (const int4 *)(s.xqs + ao);
+            for (int i = tid; i < in / 16; i += 256) ((int4 *)aqs)[(i >> 4) * (kAS / 16) + (i & 15)] = gq[i];
+            for (int i = tid; i < nb * 16; i += 256) abs[i] = s.xbs[ao / 16 + i];
+            for (int i = tid; i < nb; i += 256) ad[i] = s.xd[ao / 256 + i];
+        } else {
+            for (int i = tid; i < in; i += 256) v[i] = s.xf[ao + i];
+        }
+        lds_barrier();
+        return;
+    }
+    if (s.pro == OH_PRO_SWIGLU) {
+        for (int i = tid; i < in; i += 256) v[i] = ref_silu(s.xf[ao + i]) * s.xf2[ao + i];
+        lds_barrier();
+    } else {
+        for (int i = tid; i < in; i += 256) v[i] = s.xf[ao + i];
+        lds_barrier();
+        rmsnorm_lds(v, s.nw, s.eps, in, red);
+    }
+    const bool store = blk == 0 && s.oqs != nullptr;
+    if (blk == 0 && s.oxf)
+        for (int i = tid; i < in; i += 256) s.oxf[ao + i] = v[i];
+    if (q8 || store) {
+        for (int qb = wave; qb < nb; qb += 4) {
+            q8k_block_from_lds(v, qb, aqs, ad, abs, kAS);
+            if (store) q8k_block_from_lds(v, qb, s.oqs + ao, s.oqd + ao / 256, s.oqb + ao / 16);
+        }
+    }
+    lds_barrier();
+}
+
+// Integer-path segment slot: every lane reduces one super-block; a wave step
+// covers 64/nb rows. Steps are double-buffered: the next step's loads are in
+// flight while the current one is reduced. All loads are unconditional
+// (dead lanes and steps past the end re-read an in-bounds block), so the
+// compiler never has to drain the queue at a branch.
+template <int T>
+OH_DEV void mv_seg(const oh_mvseg &s, int slot, int blk, uint8_t *smem, double *red) {
+    const int lane = lane_id(), wave = (int)(threadIdx.x >> 6);
+    const int nb = s.nb, rps = 64 / nb;
+    const int rl = lane / nb, sb = lane - rl * nb;
+    const int u0 = (blk * OH_MV_WAVES + wave) * s.upw;
+    const int u1 = u0 + s.upw < s.units ? u0 + s.upw : s.units;
+    const int S = u1 > u0 ? u1 - u0 : 0;
+    const int64_t row_base = s.eidx ? (int64_t)s.eidx[slot] * s.rows : 0;
+    float *y = s.y + (size_t)slot * s.ystride;
+    const WP wp = {s.A, s.B, s.C};
+    const int8_t *aq = (const int8_t *)smem + sb * kAS;
+    const int16_t *abs = (const int16_t *)(smem + mv_lds_bs_off(nb)) + sb * 16;
+    const float *adp = (const float *)(smem + mv_lds_d_off(nb)) + sb;
+    SB<T> ra, rb;
+    auto load = [&](SB<T> &r, int st) {
+        const int unit = u0 + (st < S ? st : S - 1);
+        const int row = unit * rps + (rl < rps ? rl : rps - 1);
+        const int rowc = row < s.rows ? row : s.rows - 1;
+        sb_load(r, wp, (row_base + rowc) * nb + sb);
+    };
+    auto comp = [&](const SB<T> &r, int st) {
+        const int row = (u0 + st) * rps + rl;
+        const bool live = st < S && rl < rps && row < s.rows;
+        const float tw = sb_term(r, aq, abs, *adp);
+        const float t = live ? tw : 0.0f;
+        // the row's super-block terms in order, from 0 (lanes rl*nb .. +nb-1)
+        float acc = 0.0f;
+        for (int i = 0; i < nb; i++) acc += shfl(t, rl * nb + i);
+        if (live && sb == 0) emit(y, s.mode, row, acc);
+    };
+    if (S > 0) load(ra, 0);
+    mv_prologue(s, slot, blk, smem, red, true);
+    for (int st = 0; st < S; st += 2) {
+        load(rb, st + 1);
+        comp(ra, st);
+        load(ra, st + 2);
+        comp(rb, st + 1);
+    }
+}
+
+// Launch body. TK >= 0: every segment is an integer-path segment of type TK;
+// TK < 0: any mix, including fallback segments (one lane per row, the f32
+// activation in LDS). With OH_EP_ROUTE the last block to finish (fenced
+// completion counter, reset by that block) routes the MoE.
+template <int TK>
+OH_DEV void mv_body(const oh_mvlaunch &L) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ double red[4];
+    __shared__ int last;
     int si = 0;
     while (si + 1 < L.n && (int)blockIdx.x >= L.s[si + 1].block0) si++;
     const oh_mvseg &s = L.s[si];
-    const int blk = (int)blockIdx.x - s.block0;
-    int64_t row_base = 0;
-    if (s.eidx) row_base = (int64_t)s.eidx[s.eslot] * s.rows;
-    if (oh_qdot_can((uint32_t)s.type, s.in) && s.xqs) {
-        const int wave = (int)(threadIdx.x >> 6);
-        for (int u = 0; u < kUnitsPerWave; u++) {
-            const int unit = (blk * kWavesPerBlock + wave) * kUnitsPerWave + u;
-            if (unit >= s.units) break;
-            switch (s.type) {
-            case OH_Q4_K: wave_unit<OH_Q4_K>(s, unit, row_base); break;
-            case OH_Q6_K: wave_unit<OH_Q6_K>(s, unit, row_base); break;
-            default: wave_unit<OH_Q8_0>(s, unit, row_base); break;
-            }
+    const int bseg = (int)blockIdx.x - s.block0;
+    const int slot = bseg / s.bps, blk = bseg - slot * s.bps;
+    if (TK >= 0) {
+        mv_seg<TK < 0 ? OH_Q4_K : TK>(s, slot, blk, smem, red);
+    } else if (oh_qdot_can((uint32_t)s.type, s.in) && (s.xqs || s.pro != OH_PRO_Q8K)) {
+        switch (s.type) {
+        case OH_Q4_K: mv_seg<OH_Q4_K>(s, slot, blk, smem, red); break;
+        case OH_Q6_K: mv_seg<OH_Q6_K>(s, slot, blk, smem, red); break;
+        default: mv_seg<OH_Q8_0>(s, slot, blk, smem, red); break;
         }
-        return;
+    } else {
+        mv_prologue(s, slot, blk, smem, red, false);
+        const float *v = (const float *)(smem + mv_lds_v_off(s.in / 256));
+        const int row = blk * 256 + (int)threadIdx.x;
+        const int64_t row_base = s.eidx ? (int64_t)s.eidx[slot] * s.rows : 0;
+        if (row < s.rows) emit(s.y + (size_t)slot * s.ystride, s.mode, row, row_seq(s, row_base + row, v));
     }
-    for (int i = (int)threadIdx.x; i < s.in; i += 256) xs[i] = s.xf[i];
-    __syncthreads();
-    const int row = blk * 256 + (int)threadIdx.x;
-    if (row < s.rows) emit(s, row, row_seq(s, row_base + row, xs));
+    if (L.ep == OH_EP_ROUTE) {
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            __threadfence();
+            last = atomicAdd(L.cnt, 1) == L.total_blocks - 1;
+        }
+        __syncthreads();
+        if (last) {
+            __threadfence();
+            if (threadIdx.x < 64) route_wave(L.rlog, L.ne, L.topk, L.shl, L.ridx, L.rw, L.shg);
+            if (threadIdx.x == 0) *L.cnt = 0;
+        }
+    }
+}
+
+// Fused MoE down projection and combine (src/ornith_rforward.c:375-409). A
+// block owns 64/nb output rows; wave j reduces slot j (the k routed experts in
+// routing order, then the shared expert) over those rows with one super-block
+// per lane. Slot j's activation is Q8_K(silu(g_j) * u_j), formed in LDS by the
+// block. Wave 0 then gives row r: x_r += (sum_j w_j * dot_j) + shg * dot_shared
+// in the reference's order.
+template <int T>
+OH_DEV void down_body(const oh_mvdown &D) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int lane = lane_id(), wave = (int)(threadIdx.x >> 6), nw = (int)(blockDim.x >> 6);
+    const int tid = (int)threadIdx.x;
+    const int nb = D.nb, in = D.in, ns = D.k + (D.sA ? 1 : 0), rps = 64 / nb;
+    const int rl = lane / nb, sb = lane - rl * nb;
+    const int sq = (nb * kAS + nb * 36 + 15) & ~15;     // one slot's Q8_K planes
+    float *v = (float *)(smem + ns * sq);                // ns x in f32
+    float *dots = v + ns * in;                           // ns x rps f32
+    const int row0 = (int)blockIdx.x * rps;
+    const int row = row0 + rl;
+    const bool live = rl < rps && row < D.rows && wave < ns;
+    const int j = wave < ns ? wave : ns - 1;
+    const bool sh = j >= D.k;
+    const WP wp = sh ? WP{D.sA, D.sB, D.sC} : WP{D.A, D.B, D.C};
+    const int64_t rb = sh ? 0 : (int64_t)D.eidx[j] * D.rows;
+    const int rowc = row < D.rows ? (rl < rps ? row : row0) : D.rows - 1;
+    SB<T> r;
+    sb_load(r, wp, (rb + rowc) * nb + sb);
+    for (int i = tid; i < ns * in; i += (int)blockDim.x) {
+        const int jj = i / in, e = i - jj * in;
+        v[i] = ref_silu(D.g[(size_t)jj * D.stride + e]) * D.u[(size_t)jj * D.stride + e];
+    }
+    lds_barrier();
+    for (int q = wave; q < ns * nb; q += nw) {
+        const int jj = q / nb, qb = q - jj * nb;
+        uint8_t *b = smem + (size_t)jj * sq;
+        q8k_block_from_lds(v + (size_t)jj * in, qb, (int8_t *)b, (float *)(b + mv_lds_d_off(nb)),
+                           (int16_t *)(b + mv_lds_bs_off(nb)), kAS);
+    }
+    lds_barrier();
+    if (wave < ns) {
+        const uint8_t *b = smem + (size_t)j * sq;
+        const float tw = sb_term(r, (const int8_t *)b + sb * kAS, (const int16_t *)(b + mv_lds_bs_off(nb)) + sb * 16,
+                                 ((const float *)(b + mv_lds_d_off(nb)))[sb]);
+        const float t = live ? tw : 0.0f;
+        float acc = 0.0f;
+        for (int i = 0; i < nb; i++) acc += shfl(t, rl * nb + i);
+        if (rl < rps && sb == 0) dots[j * rps + rl] = acc;
+    }
+    lds_barrier();
+    if (wave == 0 && lane < rps && row0 + lane < D.rows) {
+        float acc = 0.0f;
+        for (int jj = 0; jj < D.k; jj++) acc += D.w[jj] * dots[jj * rps + lane];
+        if (D.sA) {
+            const float so = dots[D.k * rps + lane];
+            const float vv = D.shg ? so * *D.shg : so;
+            acc += vv;
+        }
+        D.x[row0 + lane] = D.x[row0 + lane] + acc;
+    }
+}
+
+} // namespace
+
+extern "C" __global__ void __launch_bounds__(256) oh_k_mv_q4k(oh_mvlaunch L) { mv_body<OH_Q4_K>(L); }
+extern "C" __global__ void __launch_bounds__(256) oh_k_mv_q6k(oh_mvlaunch L) { mv_body<OH_Q6_K>(L); }
+extern "C" __global__ void __launch_bounds__(256) oh_k_mv_q80(oh_mvlaunch L) { mv_body<OH_Q8_0>(L); }
+extern "C" __global__ void __launch_bounds__(256) oh_k_mv_mixed(oh_mvlaunch L) { mv_body<-1>(L); }
+
+extern "C" __global__ void __launch_bounds__(1024) oh_k_mv_down(oh_mvdown D) {
+    switch (D.type) {
+    case OH_Q4_K: down_body<OH_Q4_K>(D); break;
+    case OH_Q6_K: down_body<OH_Q6_K>(D); break;
+    default: down_body<OH_Q8_0>(D); break;
+    }
 }
 
 // ---- Q8_K quantisation (optionally fused with RMSNorm) ----------------------
@@ -252,51 +556,6 @@ oh_k_matvec(oh_mvlaunch L) {
 // sum of squares in double (tree-ordered), inv = (float)(1/sqrt(ss/n+eps)),
 // xn_i = x_i * inv * w_i. Then each 256-block is quantised exactly as
 // qdot_quantize_row_q8_K (src/ornith_qdot.c:32-62).
-OH_DEV void q8k_block_from_lds(const float *v, int qb, int8_t *qs, float *d, int16_t *bs) {
-    const int lane = lane_id();
-    const float *xb = v + qb * 256;
-    // first element of largest magnitude (ties -> lowest index)
-    float best = -1.0f; int bi = 0;
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-        const int e = lane + 64 * k;
-        const float a = fabsf(xb[e]);
-        if (a > best) { best = a; bi = e; }
-    }
-    for (int m = 32; m >= 1; m >>= 1) {
-        const float ob = shfl_xor(best, m);
-        const int oi = shfl_xor(bi, m);
-        if (ob > best || (ob == best && oi < bi)) { best = ob; bi = oi; }
-    }
-    int8_t *q = qs + (int64_t)qb * 256;
-    int16_t *b = bs + (int64_t)qb * 16;
-    if (best == 0.0f || !(best > 0.0f)) {
-#pragma unroll
-        for (int k = 0; k < 4; k++) q[lane + 64 * k] = 0;
-        if (lane < 16) b[lane] = 0;
-        if (lane == 0) d[qb] = 0.0f;
-        return;
-    }
-    const float iscale = -127.0f / xb[bi];
-    int sums[4];
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-        const int e = lane + 64 * k;
-        float r = __builtin_rintf(iscale * xb[e]);
-        int v = (int)r;
-        v = v > 127 ? 127 : (v < -128 ? -128 : v);
-        q[e] = (int8_t)v;
-        sums[k] = v;
-    }
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-        int sv = sums[k];
-        sv += shfl_xor(sv, 1); sv += shfl_xor(sv, 2); sv += shfl_xor(sv, 4); sv += shfl_xor(sv, 8);
-        if ((lane & 15) == 0) b[4 * k + (lane >> 4)] = (int16_t)sv;
-    }
-    if (lane == 0) d[qb] = 1.0f / iscale;
-}
-
 extern "C" __global__ void __launch_bounds__(256)
 oh_k_rmsnorm_q8k(const float *x, const float *norm_w, float eps, int n,
                  float *xn_out, int8_t *qs, float *d, int16_t *bs) {
@@ -356,17 +615,16 @@ oh_k_dequant(const uint8_t *A, const uint8_t *B, const uint8_t *C, int type, int
             if (type == OH_Q4_K) {
                 const uint4 hdr = *(const uint4 *)(B + bi * 16);
                 const int j = k / 32, l = k % 32;
-                const uint8_t q = A[bi * 128 + 32 * (j / 2) + l];
+                const uint8_t q = A[oh_a_off(OH_Q4_K, bi, 32 * (j / 2) + l)];
                 int sc, mn;
                 q4k_sm(hdr, j, sc, mn);
                 const float dd = h2f((uint16_t)(hdr.x & 0xffffu)), dmin = h2f((uint16_t)(hdr.x >> 16));
                 const float d1 = dd * sc, m1 = dmin * mn;
                 y = d1 * (float)((j & 1) ? (q >> 4) : (q & 15)) - m1;
             } else if (type == OH_Q6_K) {
-                const uint8_t *a = A + bi * 192;
                 const int hh = k / 128, kk = k % 128, qd = kk / 32, l = kk % 32;
-                const uint8_t ql = a[64 * hh + l + 32 * (qd & 1)];
-                const uint8_t qh = a[128 + 32 * hh + l];
+                const uint8_t ql = A[oh_a_off(OH_Q6_K, bi, 64 * hh + l + 32 * (qd & 1))];
+                const uint8_t qh = A[oh_a_off(OH_Q6_K, bi, 128 + 32 * hh + l)];
                 const int lo = (qd < 2) ? (ql & 15) : (ql >> 4);
                 const int q = (lo | (((qh >> (2 * qd)) & 3) << 4)) - 32;
                 const int8_t sc = (int8_t)B[bi * 16 + 8 * hh + l / 16 + 2 * qd];
@@ -374,7 +632,7 @@ oh_k_dequant(const uint8_t *A, const uint8_t *B, const uint8_t *C, int type, int
                 y = dd * (float)sc * (float)q;
             } else if (type == OH_Q8_0) {
                 const int sbk = k / 32;
-                const int8_t q = (int8_t)A[bi * 256 + k];
+                const int8_t q = (int8_t)A[oh_a_off(OH_Q8_0, bi, k)];
                 y = (float)q * h2f(*(const uint16_t *)(B + bi * 16 + 2 * sbk));
             } else if (type == OH_IQ2_XXS) {
                 const float dd = h2f(*(const uint16_t *)(C + bi * 2));

@@ -88,10 +88,9 @@ oh_k_encode(const float *x, int type, int64_t nblk, uint8_t *A, uint8_t *B, uint
             const float d = amax / 127.0f;
             const float id = d != 0.0f ? 1.0f / d : 0.0f;
             *(uint16_t *)(B + b * 16 + 2 * sb) = f2h_rne(d);
-            int8_t *q = (int8_t *)(A + b * 256 + 32 * sb);
             for (int j = 0; j < 32; j++) {
                 long r = round_away(w[j] * id);
-                q[j] = (int8_t)(r > 127 ? 127 : (r < -127 ? -127 : r));
+                A[oh_a_off(OH_Q8_0, b, 32 * sb + j)] = (uint8_t)(int8_t)(r > 127 ? 127 : (r < -127 ? -127 : r));
             }
         }
     } else if (type == OH_Q4_K) {
@@ -126,7 +125,6 @@ oh_k_encode(const float *x, int type, int64_t nblk, uint8_t *A, uint8_t *B, uint
             ps[j] |= (uint8_t)(((mn[j] >> 4) & 3) << 6);
         }
         for (int i = 0; i < 16; i++) B[b * 16 + i] = hdr[i];
-        uint8_t *qs = A + b * 128;
         for (int j = 0; j < 8; j += 2) {
             const float rs0 = d * sc[j], rm0 = dmin * mn[j], irs0 = rs0 != 0.0f ? 1.0f / rs0 : 0.0f;
             const float rs1 = d * sc[j + 1], rm1 = dmin * mn[j + 1], irs1 = rs1 != 0.0f ? 1.0f / rs1 : 0.0f;
@@ -135,7 +133,7 @@ oh_k_encode(const float *x, int type, int64_t nblk, uint8_t *A, uint8_t *B, uint
                 long q1 = round_away((v[32 * (j + 1) + l] + rm1) * irs1);
                 q0 = q0 < 0 ? 0 : (q0 > 15 ? 15 : q0);
                 q1 = q1 < 0 ? 0 : (q1 > 15 ? 15 : q1);
-                qs[16 * j + l] = (uint8_t)(q0 | (q1 << 4));
+                A[oh_a_off(OH_Q4_K, b, 16 * j + l)] = (uint8_t)(q0 | (q1 << 4));
             }
         }
     } else if (type == OH_Q6_K) {
@@ -162,14 +160,13 @@ oh_k_encode(const float *x, int type, int64_t nblk, uint8_t *A, uint8_t *B, uint
                 Q[16 * g + l] = (uint8_t)(q < 0 ? 0 : (q > 63 ? 63 : q));
             }
         }
-        uint8_t *a = A + b * 192;
         for (int h = 0; h < 2; h++) {
             const uint8_t *q = Q + 128 * h;
             for (int l = 0; l < 32; l++) {
-                a[64 * h + l] = (uint8_t)((q[l] & 15) | ((q[l + 64] & 15) << 4));
-                a[64 * h + 32 + l] = (uint8_t)((q[l + 32] & 15) | ((q[l + 96] & 15) << 4));
-                a[128 + 32 * h + l] = (uint8_t)((q[l] >> 4) | ((q[l + 32] >> 4) << 2) |
-                                                ((q[l + 64] >> 4) << 4) | ((q[l + 96] >> 4) << 6));
+                A[oh_a_off(OH_Q6_K, b, 64 * h + l)] = (uint8_t)((q[l] & 15) | ((q[l + 64] & 15) << 4));
+                A[oh_a_off(OH_Q6_K, b, 64 * h + 32 + l)] = (uint8_t)((q[l + 32] & 15) | ((q[l + 96] & 15) << 4));
+                A[oh_a_off(OH_Q6_K, b, 128 + 32 * h + l)] =
+                    (uint8_t)((q[l] >> 4) | ((q[l + 32] >> 4) << 2) | ((q[l + 64] >> 4) << 4) | ((q[l + 96] >> 4) << 6));
             }
         }
     }

@@ -4,14 +4,16 @@
 // tensor of R rows and nb blocks per row (block = 256 elements, or 32 for
 // Q8_0 handled as 8 sub-blocks of a 256-element super-block), block b = r*nb+i
 // is split into up to three planes so that every wave load is 16-byte aligned
-// and contiguous across lanes:
+// and contiguous across lanes (A planes of the integer-path types are
+// additionally tile-interleaved, see oh_a_off):
 //   Q4_K    A: qs[128]            B: d,dmin,scales[12] (16 B)
 //   Q6_K    A: ql[128] qh[64]     B: scales[16]          C: d (f16)
 //   Q8_0    A: 8 x qs[32]         B: 8 x d (f16)
 //   IQ2_XXS A: qs[64]                                     C: d (f16)
 //   F32/F16/BF16: A holds the raw row-major values.
-// The byte count equals the GGUF byte count; decoding a plane-layout block
-// gives the same floats as decoding the GGUF block.
+// The byte count equals the GGUF byte count (plus the A-plane tile padding);
+// decoding a plane-layout block gives the same floats as decoding the GGUF
+// block.
 //
 // Q8_K activations use planes as well: qs[nb*256] int8, d[nb] f32,
 // bsums[nb*16] int16 (the 292-byte oq8k_block fields, split).
@@ -43,29 +45,90 @@ OH_HD static inline int oh_plane_c(uint32_t t) {
 OH_HD static inline int oh_is_quant(uint32_t t) {
     return t == OH_Q4_K || t == OH_Q6_K || t == OH_Q8_0 || t == OH_IQ2_XXS;
 }
+// The A plane of Q4_K / Q6_K / Q8_0 is tile-interleaved: super-blocks form
+// tiles of 64 (bi / 64) and inside a tile the 16-byte piece k of super-block
+// j = bi % 64 sits at (k*64 + j)*16. Sixty-four lanes that each load piece k
+// of one of 64 consecutive super-blocks then read 1 KB contiguously. The
+// plane is padded to whole tiles.
+OH_HD static inline int oh_a_tiled(uint32_t t) {
+    return t == OH_Q4_K || t == OH_Q6_K || t == OH_Q8_0;
+}
+OH_HD static inline uint64_t oh_a_off(uint32_t t, uint64_t bi, int byte) {
+    const int pb = oh_plane_a(t);
+    if (!oh_a_tiled(t)) return bi * (uint64_t)pb + (uint64_t)byte;
+    return (bi >> 6) * (uint64_t)(64 * pb) +
+           (uint64_t)((((byte >> 4) * 64) + (int)(bi & 63)) * 16 + (byte & 15));
+}
+// A-plane bytes of nblk super-blocks (tiles rounded up)
+OH_HD static inline uint64_t oh_plane_a_bytes(uint32_t t, uint64_t nblk) {
+    const uint64_t n = oh_a_tiled(t) ? (nblk + 63) / 64 * 64 : nblk;
+    return n * (uint64_t)oh_plane_a(t);
+}
+
 // integer Q8_K path exists (reference qdot_can, src/ornith_qdot.c:218-228)
 OH_HD static inline int oh_qdot_can(uint32_t t, int64_t in) {
     return in % 256 == 0 && (t == OH_Q4_K || t == OH_Q6_K || t == OH_Q8_0);
 }
 
-// One matvec segment of a multi-segment launch.
+// One matvec segment of a multi-segment launch. A segment is one weight
+// tensor applied in `nsub` slots: slot k uses rows [eidx[k]*rows, +rows) of a
+// stacked expert tensor (or the whole tensor when eidx is null), writes
+// y + k*ystride and reads its activation at slot offset k*astride.
+enum { OH_PRO_Q8K = 0, OH_PRO_NORM = 1, OH_PRO_SWIGLU = 2 };
 typedef struct {
     const uint8_t *A, *B, *C;      // weight planes (expert 0 for a stacked tensor)
-    const int8_t *xqs;             // Q8_K activation planes
+    // activation: OH_PRO_Q8K reads Q8_K planes (and xf for the f32 fallback);
+    // OH_PRO_NORM RMS-normalises xf with nw/eps; OH_PRO_SWIGLU forms
+    // silu(xf)*xf2; both then quantise to Q8_K inside the block.
+    const int8_t *xqs;
     const float *xd;
     const int16_t *xbs;
-    const float *xf;               // f32 activation (f32/IQ2_XXS fallback rows)
-    float *y;                      // output, row o -> y[o]
-    const int32_t *eidx;           // gathered expert: rows += eidx[eslot]*rows
+    const float *xf, *xf2, *nw;
+    // OH_PRO_NORM / OH_PRO_SWIGLU: the segment's first block also stores the
+    // activation it formed (Q8_K planes and f32) for later launches
+    int8_t *oqs;
+    float *oqd;
+    int16_t *oqb;
+    float *oxf;
+    float *y;                      // output, row o of slot k -> y[k*ystride + o]
+    const int32_t *eidx;           // stacked experts: slot k uses expert eidx[k]
+    float eps;
+    int pro;
     int type, nb, in, rows, mode;  // mode 0: y = dot, 1: y += dot
-    int eslot;
-    int units;                     // wave work units in this segment
+    int nsub, ystride, astride;
+    int units;                     // wave work units per slot
+    int upw;                       // units per wave
+    int bps;                       // blocks per slot
     int block0;                    // first block of the segment in the launch
 } oh_mvseg;
 
-#define OH_MAX_SEGS 24
+#define OH_MAX_SEGS 8
+#define OH_MV_WAVES 4              // waves per matvec block
+#define OH_MV_R 4                  // steps per prefetch batch of a wave
+// Launch epilogue: OH_EP_ROUTE makes the last block to finish run the MoE
+// router top-k over y of segment 0 (logits) and the shared-expert gate logit
+// of segment 1 (when present).
+enum { OH_EP_NONE = 0, OH_EP_ROUTE = 1 };
 typedef struct {
     oh_mvseg s[OH_MAX_SEGS];
     int n;
     int total_blocks;
+    int ep;
+    int *cnt;                      // completion counter (zero between launches)
+    const float *rlog, *shl;       // router logits, shared-expert gate logit (or null)
+    int ne, topk;
+    int32_t *ridx;
+    float *rw, *shg;
 } oh_mvlaunch;
+
+// Fused MoE down projection + combine (one block per row range, every slot).
+typedef struct {
+    const uint8_t *A, *B, *C;      // stacked down experts
+    const uint8_t *sA, *sB, *sC;   // shared-expert down (sA null: none)
+    const int32_t *eidx;
+    const float *w;                // routing weights [k]
+    const float *shg;              // sigmoid shared gate (null: ungated)
+    const float *g, *u;            // gate/up outputs, slot k at +k*stride
+    float *x;                      // residual, += combine
+    int type, nb, in, rows, k, stride;
+} oh_mvdown;
