@@ -178,8 +178,10 @@ def cpu_baseline(model: oa.Model, cfg: dict, seconds: float) -> dict:
 
 
 # profile kind -> kernel symbol (as rocprofv3 names it)
-KERNEL_SYMBOL = {"matvec": "oh_k_matvec", "moe_down": "oh_k_mv_down", "delta_step": "oh_k_delta_step",
-                 "attn_out": "oh_k_attn_out", "attn_scores": "oh_k_attn_scores"}
+KERNEL_SYMBOL = {"matvec": "oh_k_mv_q4k", "matvec_q6k": "oh_k_mv_q6k", "matvec_q80": "oh_k_mv_q80",
+                 "matvec_mixed": "oh_k_mv_mixed", "moe_down": "oh_k_mv_down", "delta_step": "oh_k_delta_step",
+                 "attn_out": "oh_k_attn_out", "attn_scores": "oh_k_attn_scores", "attn_flash": "oh_k_attn_flash",
+                 "attn_combine": "oh_k_attn_combine"}
 
 
 def main() -> int:

@@ -162,10 +162,12 @@ int  ornith_hip_session_get_kv(ornith_hip_session *s, int layer, int8_t *Kq,
  * events on the session stream; *ms = total elapsed. Advances the session. */
 int  ornith_hip_session_time_decode(ornith_hip_session *s, int n_steps, float *ms);
 /* Run one greedy decode step eagerly with HIP events around every kernel
- * launch: kinds[i] (0 matvec, 1 rmsnorm+Q8_K, 2 SwiGLU+Q8_K, 3 embed, 4 delta
- * step, 5 attn prep, 6 attn scores, 7 attn out, 8 router, 9 MoE combine,
- * 10 argmax, 11 advance, 12 fused MoE down + combine), algorithmic HBM
- * bytes[i] and ms[i]. Advances the session by one position. */
+ * launch: kinds[i] (0 matvec with Q4_K weights, 1 rmsnorm+Q8_K, 2 SwiGLU+Q8_K,
+ * 3 embed, 4 delta step, 5 attn prep, 6 attn scores, 7 attn out, 8 router,
+ * 9 MoE combine, 10 argmax, 11 advance, 12 fused MoE down + combine, 13 flash
+ * attention chunks, 14 flash merge, 15 matvec Q6_K, 16 matvec Q8_0, 17 matvec
+ * of mixed types), algorithmic HBM bytes[i] and ms[i]. Advances the session by
+ * one position. */
 int  ornith_hip_session_profile_step(ornith_hip_session *s, int max_launches, int32_t *kinds,
                                      double *bytes, float *ms, int *n_launches);
 /* Time `iters` launches of one matvec of W (activation already quantised on

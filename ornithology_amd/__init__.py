@@ -310,7 +310,7 @@ class Session:
 
     KERNEL_KINDS = ("matvec", "rmsnorm_q8k", "swiglu_q8k", "embed", "delta_step", "attn_prep",
                     "attn_scores", "attn_out", "moe_route", "moe_combine", "argmax", "advance",
-                    "moe_down")
+                    "moe_down", "attn_flash", "attn_combine", "matvec_q6k", "matvec_q80", "matvec_mixed")
 
     def profile_step(self, max_launches: int = 4096):
         """One eager decode step with per-launch HIP-event timing: list of

@@ -162,5 +162,29 @@ OH_DEV float wave_max_f(float v) {
     return v;
 }
 
+// DPP all-reduce within each 16-lane row (xor 1, xor 2, half-mirror, mirror:
+// after each step every lane holds the combined value of a group twice as
+// large). Only for order-independent operations (integer sums, max, min).
+template <int CTRL>
+OH_DEV int dpp_i(int v) { return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, false); }
+template <int CTRL>
+OH_DEV float dpp_f(float v) { return __int_as_float(dpp_i<CTRL>(__float_as_int(v))); }
+OH_DEV int row16_sum_i(int v) {
+    v += dpp_i<0xB1>(v); v += dpp_i<0x4E>(v); v += dpp_i<0x141>(v); v += dpp_i<0x140>(v);
+    return v;
+}
+OH_DEV float wave_max_fast(float v) {
+    v = fmaxf(v, dpp_f<0xB1>(v)); v = fmaxf(v, dpp_f<0x4E>(v));
+    v = fmaxf(v, dpp_f<0x141>(v)); v = fmaxf(v, dpp_f<0x140>(v));
+    v = fmaxf(v, shfl_xor(v, 16)); v = fmaxf(v, shfl_xor(v, 32));
+    return v;
+}
+OH_DEV int wave_min_fast(int v) {
+    v = min(v, dpp_i<0xB1>(v)); v = min(v, dpp_i<0x4E>(v));
+    v = min(v, dpp_i<0x141>(v)); v = min(v, dpp_i<0x140>(v));
+    v = min(v, shfl_xor(v, 16)); v = min(v, shfl_xor(v, 32));
+    return v;
+}
+
 // signed 8-bit dot of four packed bytes, accumulated into c (exact integers)
 OH_DEV int dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }

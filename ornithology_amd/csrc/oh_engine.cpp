@@ -272,8 +272,9 @@ struct Act {
     const float *d = nullptr;
     const int16_t *bs = nullptr;
     const float *xf = nullptr;
-    int pro = OH_PRO_Q8K;
+    int pro = OH_PRO_Q8K, gdim = 0;
     const float *xf2 = nullptr, *nw = nullptr;
+    const double *xruns = nullptr;
     float eps = 0.0f;
     int8_t *oqs = nullptr;     // prologue result stored for later launches
     float *oqd = nullptr;
@@ -302,7 +303,7 @@ static int mv_add(MvBuild &b, const ornith_hip_tensor *W, const Act &act, float 
     memset(&s, 0, sizeof s);
     s.A = W->A; s.B = W->B; s.C = W->C;
     s.xqs = act.qs; s.xd = act.d; s.xbs = act.bs; s.xf = act.xf;
-    s.pro = act.pro; s.xf2 = act.xf2; s.nw = act.nw; s.eps = act.eps;
+    s.pro = act.pro; s.xf2 = act.xf2; s.nw = act.nw; s.eps = act.eps; s.gdim = act.gdim; s.xruns = act.xruns;
     s.oqs = act.oqs; s.oqd = act.oqd; s.oqb = act.oqb; s.oxf = act.oxf;
     s.y = y;
     s.eidx = eidx;
@@ -314,6 +315,10 @@ static int mv_add(MvBuild &b, const ornith_hip_tensor *W, const Act &act, float 
     s.rows = eidx ? (int)W->dims[1] : (int)W->rows;
     s.mode = mode;
     s.nb = (int)(W->in / 256);
+    if (act.pro == OH_PRO_GNORM && (W->in > 4096 || act.gdim % 64 || W->in % act.gdim || !oh_qdot_can(W->type, W->in))) {
+        seterr("matvec '%s': gated-norm prologue needs an integer-path type, in <= 4096 and 64 | head | in", W->name.c_str());
+        return ORNITH_HIP_ERR_UNSUPPORTED;
+    }
     if (act.pro != OH_PRO_Q8K && (W->in % 256 || W->in > 8192)) {
         seterr("matvec '%s': fused prologue needs in %% 256 == 0 and in <= 8192", W->name.c_str());
         return ORNITH_HIP_ERR_UNSUPPORTED;
@@ -369,9 +374,10 @@ static void mv_plan(MvBuild &b) {
         blocks += s.bps * s.nsub;
         const int nb = s.in / 256;
         const int voff = (nb * 272 + nb * 36 + 15) & ~15;
-        const int need = voff + ((!q8 || s.pro != OH_PRO_Q8K) ? s.in * 4 : 0);
+        const int need = voff + ((!q8 || s.pro != OH_PRO_Q8K) ? s.in * 4 : 0) + (s.pro == OH_PRO_GNORM ? 256 : 0);
         if (need > b.lds) b.lds = need;
     }
+    if (b.L.route && ((b.L.ne + 3) & ~3) * 4 > b.lds) b.lds = ((b.L.ne + 3) & ~3) * 4;
     b.L.total_blocks = blocks;
 }
 
@@ -775,7 +781,8 @@ static int infer_arch(ornith_hip_model *m, const Meta &md) {
         if (!need_f32(y.attn_norm) || !need_f32(y.post_norm)) return bad("layer norms must be F32");
         if (y.full) {
             if (!y.q || !y.k || !y.v || !y.o || !need_f32(y.q_norm) || !need_f32(y.k_norm)) return bad("full-attention tensors missing or not F32 norms");
-            if (a.hd > 256 || 256 % a.hd || a.hd % 4) return bad("head_dim must divide 256");
+            if (a.hd != 64 && a.hd != 128 && a.hd != 256) return bad("head_dim must be 64, 128 or 256");
+            if (a.nh % a.nkv || a.nh / a.nkv > 16) return bad("query heads per KV head must divide and be <= 16");
             if (a.nkv < 1 || a.nh % a.nkv) return bad("n_heads must be a multiple of n_kv_heads");
             if ((a.nh * a.hd) % 256 || a.nh * a.hd > 8192) return bad("n_heads*head_dim must be a multiple of 256, <= 8192");
         } else {
@@ -784,8 +791,8 @@ static int infer_arch(ornith_hip_model *m, const Meta &md) {
                 return bad("ssm_conv1d/ssm_a/ssm_dt.bias/ssm_norm must be F32");
             if (a.dk != 64 && a.dk != 128) return bad("linear head dim must be 64 or 128");
             if (a.nv % (256 / a.dk) || a.nk < 1) return bad("linear value heads must fill 256-element blocks");
-            if (a.conv_k < 2) return bad("conv kernel must be >= 2");
-            if (a.nv * a.dv > 8192) return bad("linear value width must be <= 8192");
+            if (a.conv_k < 2 || a.conv_k > 8) return bad("conv kernel must be in [2, 8]");
+            if (a.nv * a.dv > 4096) return bad("linear value width must be <= 4096");
         }
         if (a.ne > 0) {
             if (!y.router || !y.gate_exps || !y.up_exps || !y.down_exps) return bad("MoE tensors missing");
@@ -876,9 +883,10 @@ struct ornith_hip_session {
     float *o = nullptr;
     Q8Buf oq;
     float *qproj = nullptr, *kb = nullptr, *vb = nullptr, *qr = nullptr, *agate = nullptr, *scores = nullptr;
-    int *rcnt = nullptr;          // router launch completion counter (self-resetting)
-    float *apart = nullptr;       // split attention: partial outputs [groups][chunks][256]
-    int *acnt = nullptr;          // split attention: per-group completion counters (self-resetting)
+    float *fpo = nullptr;         // flash attention: chunk outputs [nkv][chunks][nh/nkv][hd]
+    float *fpml = nullptr;        // flash attention: chunk (max, sum) [nkv][chunks][nh/nkv][2]
+    float *osz = nullptr;         // delta step: silu(gate) per output row
+    double *oruns = nullptr;      // delta step: sum of o^2 per 64-row run
     int exact_max = 1024;         // contexts up to this walk the attention sum in one block
     float2 *rope = nullptr;
     float *rl = nullptr, *shl = nullptr, *shg = nullptr, *ew = nullptr;
@@ -898,7 +906,8 @@ struct ornith_hip_session {
 };
 
 enum { K_MATVEC = 0, K_NORM_Q8K, K_SWIGLU_Q8K, K_EMBED, K_DELTA, K_ATTN_PREP, K_ATTN_SCORES,
-       K_ATTN_OUT, K_ROUTE, K_COMBINE, K_ARGMAX, K_ADVANCE, K_MV_DOWN };
+       K_ATTN_OUT, K_ROUTE, K_COMBINE, K_ARGMAX, K_ADVANCE, K_MV_DOWN, K_ATTN_FLASH, K_ATTN_COMBINE,
+       K_MATVEC_Q6K, K_MATVEC_Q80, K_MATVEC_MIXED };
 
 static int rec_begin(ornith_hip_session *s, hipStream_t st) {
     if (!s->rec) return ORNITH_HIP_OK;
@@ -924,11 +933,15 @@ static int rec_end(ornith_hip_session *s, hipStream_t st, int kind, double bytes
         HCHK(call);                         \
         CHK(rec_end(s, st, kind, bytes));   \
     } while (0)
-#define MVGO(b)                                        \
-    do {                                               \
-        CHK(rec_begin(s, st));                         \
-        CHK(mv_go(b, st));                             \
-        CHK(rec_end(s, st, K_MATVEC, (b).bytes));      \
+// matvec launches are recorded by kernel variant (see oh_launch_matvec)
+static int mv_kind(int tk) {
+    return tk == OH_Q4_K ? K_MATVEC : tk == OH_Q6_K ? K_MATVEC_Q6K : tk == OH_Q8_0 ? K_MATVEC_Q80 : K_MATVEC_MIXED;
+}
+#define MVGO(b)                                              \
+    do {                                                     \
+        CHK(rec_begin(s, st));                               \
+        CHK(mv_go(b, st));                                   \
+        CHK(rec_end(s, st, mv_kind((b).tk), (b).bytes));     \
     } while (0)
 
 extern "C" void ornith_hip_session_free(ornith_hip_session *s) {
@@ -961,6 +974,9 @@ static Act act_of(const Q8Buf &q, const float *xf) {
 static Act act_norm(const float *x, const float *w, float eps) {
     Act a; a.pro = OH_PRO_NORM; a.xf = x; a.nw = w; a.eps = eps; return a;
 }
+static Act act_gnorm(const float *o, const float *sz, const double *runs, const float *w, float eps, int gdim) {
+    Act a; a.pro = OH_PRO_GNORM; a.xf = o; a.xf2 = sz; a.xruns = runs; a.nw = w; a.eps = eps; a.gdim = gdim; return a;
+}
 static Act act_swiglu(const float *g, const float *u) {
     Act a; a.pro = OH_PRO_SWIGLU; a.xf = g; a.xf2 = u; return a;
 }
@@ -989,9 +1005,13 @@ extern "C" int ornith_hip_session_new(ornith_hip_model *m, int cap, ornith_hip_s
     A_(salloc(s, &s->qproj, 2 * (size_t)aq)); A_(salloc(s, &s->kb, kvd)); A_(salloc(s, &s->vb, kvd));
     A_(salloc(s, &s->qr, aq)); A_(salloc(s, &s->agate, aq));
     A_(salloc(s, &s->scores, (size_t)a.nh * s->kvcap));
-    A_(salloc(s, &s->apart, (size_t)a.nh * a.hd / 256 * ((s->kvcap + 255) / 256) * 256 + 256));
-    A_(salloc(s, &s->acnt, (size_t)a.nh + 64));
-    A_(salloc(s, &s->rcnt, 64));
+    {
+        const size_t nch = (size_t)(s->kvcap + oh_flash_chunk() - 1) / oh_flash_chunk();
+        A_(salloc(s, &s->fpo, (size_t)a.nh * nch * a.hd + 64));
+        A_(salloc(s, &s->fpml, (size_t)a.nh * nch * 2 + 64));
+    }
+    A_(salloc(s, &s->osz, (size_t)a.nv * a.dv + 64));
+    A_(salloc(s, &s->oruns, (size_t)a.nv * a.dv / 64 + 64));
     {
         const char *e = getenv("ORNITH_HIP_EXACT_ATTN_MAX");
         if (e && *e) s->exact_max = atoi(e);
@@ -1075,13 +1095,27 @@ static int enqueue_body(ornith_hip_session *s, hipStream_t st) {
                                        s->rope, s->qr, s->agate, z.Kt, z.Ks, z.Vq, z.Vs, pos, a.nh, a.nkv, a.hd,
                                        a.rope_dim, s->kvcap, a.eps, st));
             const float scale = 1.0f / sqrtf((float)a.hd);
-            LAUNCH(K_ATTN_SCORES, T * a.nkv * (a.hd + 4.0) + 4.0 * T * a.nh + 4.0 * aqd,
-                   oh_launch_attn_scores(s->qr, z.Kt, z.Ks, s->scores, pos, a.nh, a.nkv, a.hd, s->kvcap, scale, st));
-            LAUNCH(K_ATTN_OUT, T * a.nkv * (a.hd + 4.0) + 8.0 * T * a.nh + 9.0 * aqd,
-                   oh_launch_attn_out(s->scores, z.Vq, z.Vs, s->agate, s->o, s->oq.qs, s->oq.d, s->oq.bs,
-                                      s->apart, s->acnt, pos, a.nh, a.nkv, a.hd, s->kvcap, s->exact_max, st));
+            // contexts up to exact_max: scores + the reference-order walk;
+            // longer ones: flash chunks + merge (each pair exits for the other)
+            const bool ex = s->pos + 1 <= s->exact_max;
+            LAUNCH(K_ATTN_SCORES, ex ? T * a.nkv * (a.hd + 4.0) + 4.0 * T * a.nh + 4.0 * aqd : 0.0,
+                   oh_launch_attn_scores(s->qr, z.Kt, z.Ks, s->scores, pos, a.nh, a.nkv, a.hd, s->kvcap, scale,
+                                         s->exact_max, st));
+            LAUNCH(K_ATTN_OUT, ex ? T * a.nkv * (a.hd + 4.0) + 8.0 * T * a.nh + 8.0 * aqd : 0.0,
+                   oh_launch_attn_out(s->scores, z.Vq, z.Vs, s->agate, s->o, pos, a.nh, a.nkv, a.hd, s->kvcap,
+                                      s->exact_max, st));
+            const double nchd = ceil(T / (double)oh_flash_chunk());
+            LAUNCH(K_ATTN_FLASH, ex ? 0.0 : T * a.nkv * (2.0 * a.hd + 8.0) + 4.0 * aqd + 8.0 * nchd * aqd,
+                   oh_launch_attn_flash(s->qr, z.Kt, z.Ks, z.Vq, z.Vs, s->fpo, s->fpml, pos, a.nh, a.nkv, a.hd,
+                                        s->kvcap, scale, s->exact_max, st));
+            LAUNCH(K_ATTN_COMBINE, ex ? 0.0 : 4.0 * nchd * (aqd + 2.0 * a.nh) + 12.0 * aqd,
+                   oh_launch_attn_combine(s->fpo, s->fpml, s->agate, s->o, pos, a.nh, a.nkv, a.hd, s->kvcap,
+                                          s->exact_max, st));
             MvBuild b2;
-            CHK(mv_add(b2, y.o, act_of(s->oq, s->o), s->x, 1));
+            Act af;
+            af.pro = OH_PRO_F32;
+            af.xf = s->o;
+            CHK(mv_add(b2, y.o, af, s->x, 1));
             MVGO(b2);
         } else {
             MvBuild b;
@@ -1092,14 +1126,15 @@ static int enqueue_body(ornith_hip_session *s, hipStream_t st) {
             MVGO(b);
             const float out_scale = 1.0f / sqrtf((float)a.dk);
             const double sb = 8.0 * a.nv * a.dk * a.dv + 8.0 * (a.conv_k - 1) * cc + 4.0 * cc * (a.conv_k + 1) +
-                              4.0 * vd * 3 + 1.1 * vd;
+                              12.0 * vd + 16.0 * a.nv;
             LAUNCH(K_DELTA, sb,
-                   oh_launch_delta_step(a.dk, s->cat, s->gate, s->ab, (const float *)y.conv->A, z.conv,
-                                        (const float *)y.ssm_a->A, (const float *)y.dt_bias->A,
-                                        (const float *)y.ssm_norm->A, z.S, s->o, s->oq.qs, s->oq.d, s->oq.bs, pos,
-                                        a.nk, a.nv, a.conv_k, cc, a.eps, out_scale, st));
+                   oh_launch_delta_step(a.dk, s->cat, s->ab, s->gate, (const float *)y.conv->A, z.conv,
+                                        (const float *)y.ssm_a->A, (const float *)y.dt_bias->A, z.S, s->o, s->osz,
+                                        s->oruns, pos, a.nk, a.nv, a.conv_k, cc, out_scale, st));
+            // per-head gated RMSNorm of the delta output inside the projection
             MvBuild b2;
-            CHK(mv_add(b2, y.ssm_out, act_of(s->oq, s->o), s->x, 1));
+            CHK(mv_add(b2, y.ssm_out, act_gnorm(s->o, s->osz, s->oruns, (const float *)y.ssm_norm->A, a.eps, a.dv),
+                       s->x, 1));
             MVGO(b2);
         }
         // FFN: post_attention_norm (formed inside the first FFN launch), then
@@ -1108,25 +1143,16 @@ static int enqueue_body(ornith_hip_session *s, hipStream_t st) {
         if (a.ne > 0) {
             const int K = a.top_k, I = a.moe_inter, sI = a.shared_inter;
             const int IW = I > sI ? I : sI;   // row stride of the g/u buffers
-            // router (+ shared-expert gate) with the top-k routing in the
-            // launch's last block; its first block keeps the normalised
-            // activation for the expert launch
+            // router (+ shared-expert gate); its first block keeps the
+            // normalised activation for the expert launch
             Act pst = pn;
             pst.oqs = s->xq.qs; pst.oqd = s->xq.d; pst.oqb = s->xq.bs; pst.oxf = s->xn;
             MvBuild b;
             CHK(mv_add(b, y.router, pst, s->rl, 0));
             if (y.gate_inp_sh) CHK(mv_add(b, y.gate_inp_sh, pn, s->shl, 0));
-            b.L.ep = OH_EP_ROUTE;
-            b.L.cnt = s->rcnt;
-            b.L.rlog = s->rl;
-            b.L.shl = y.gate_inp_sh ? s->shl : nullptr;
-            b.L.ne = a.ne;
-            b.L.topk = K;
-            b.L.ridx = s->eidx;
-            b.L.rw = s->ew;
-            b.L.shg = s->shg;
-            b.bytes += 8.0 * K;
             MVGO(b);
+            // experts gate/up: every block routes first (top-k + softmax), the
+            // stacked segments then read the routed experts
             const Act ax = act_of(s->xq, s->xn);
             MvBuild b2;
             CHK(mv_add(b2, y.gate_exps, ax, s->g, 0, s->eidx, K, IW, 0));
@@ -1135,12 +1161,21 @@ static int enqueue_body(ornith_hip_session *s, hipStream_t st) {
                 CHK(mv_add(b2, y.gate_sh, ax, s->g + (size_t)K * IW, 0));
                 CHK(mv_add(b2, y.up_sh, ax, s->u + (size_t)K * IW, 0));
             }
+            b2.L.route = 1;
+            b2.L.rlog = s->rl;
+            b2.L.shl = y.gate_inp_sh ? s->shl : nullptr;
+            b2.L.ne = a.ne;
+            b2.L.topk = K;
+            b2.L.ridx = s->eidx;
+            b2.L.rw = s->ew;
+            b2.L.shg = s->shg;
+            b2.bytes += 4.0 * a.ne + 8.0 * K;
             MVGO(b2);
             const uint32_t dt = y.down_exps->type;
             const int nbd = I / 256, ns = K + (y.gate_sh ? 1 : 0);
             const int rps = nbd >= 1 ? 64 / nbd : 1;
             const int sq = (nbd * 272 + nbd * 36 + 15) & ~15, dlds = ns * sq + ns * I * 4 + ns * rps * 4;
-            const bool fuse = oh_qdot_can(dt, I) && nbd >= 1 && nbd <= 64 && ns <= 16 && dlds <= 65536 &&
+            const bool fuse = oh_qdot_can(dt, I) && nbd >= 1 && nbd <= 64 && ns <= 10 && dlds <= 65536 &&
                               (!y.gate_sh || (y.down_sh->type == dt && sI == I));
             if (fuse) {
                 oh_mvdown D;
@@ -1334,11 +1369,7 @@ extern "C" int ornith_hip_session_get_delta(ornith_hip_session *s, int l, float 
     if (l < 0 || l >= a.n_layers || s->m->L[l].full) { seterr("layer %d has no delta state", l); return ORNITH_HIP_ERR_NOTFOUND; }
     HCHK(hipSetDevice(s->m->ctx->device));
     const size_t per = (size_t)a.dk * a.dv;
-    std::vector<float> t((size_t)a.nv * per);
-    HCHK(hipMemcpy(t.data(), s->ls[l].S, t.size() * 4, hipMemcpyDeviceToHost));
-    for (int h = 0; h < a.nv; h++)        // device [h][c][r] -> reference [h][r][c]
-        for (int r = 0; r < a.dv; r++)
-            for (int c = 0; c < a.dk; c++) S[h * per + (size_t)r * a.dk + c] = t[h * per + (size_t)c * a.dv + r];
+    HCHK(hipMemcpy(S, s->ls[l].S, (size_t)a.nv * per * 4, hipMemcpyDeviceToHost));   // [h][r][c] on both sides
     return ORNITH_HIP_OK;
 }
 
@@ -1436,7 +1467,7 @@ extern "C" int ornith_hip_model_synth(ornith_hip_ctx *ctx, const ornith_hip_gen_
         seterr("model_synth: on-device encoders cover F32/Q8_0/Q4_K/Q6_K");
         return ORNITH_HIP_ERR_UNSUPPORTED;
     }
-    if (c->hidden <= 0 || c->n_layers <= 0 || c->vocab <= 0 || c->dhead <= 0 || c->conv_k < 2) {
+    if (c->hidden <= 0 || c->n_layers <= 0 || c->vocab <= 0 || c->dhead <= 0 || c->conv_k < 2 || c->conv_k > 8) {
         seterr("model_synth: bad config");
         return ORNITH_HIP_ERR_FORMAT;
     }

@@ -49,20 +49,17 @@ hipError_t oh_launch_embed(const uint8_t *A, const uint8_t *B, const uint8_t *C,
     return hipGetLastError();
 }
 
-hipError_t oh_launch_delta_step(int dk, const float *cat, const float *gate, const float *ab,
+hipError_t oh_launch_delta_step(int dk, const float *cat, const float *ab, const float *gate,
                                 const float *conv_w, float *conv_state, const float *ssm_a,
-                                const float *dt_bias, const float *ssm_norm, float *S, float *out,
-                                int8_t *oqs, float *oqd, int16_t *oqb, const int32_t *io_pos,
-                                int nk, int nv, int K, int cc, float eps, float out_scale,
+                                const float *dt_bias, float *S, float *out, float *out_gate, double *out_runs,
+                                const int32_t *io_pos, int nk, int nv, int K, int cc, float out_scale,
                                 hipStream_t st) {
     if (dk == 128) {
-        hipLaunchKernelGGL(oh_k_delta_step<128>, dim3(nv / 2), dim3(256), 0, st, cat, gate, ab, conv_w,
-                           conv_state, ssm_a, dt_bias, ssm_norm, S, out, oqs, oqd, oqb, io_pos, nk, nv, K,
-                           cc, eps, out_scale);
+        hipLaunchKernelGGL(oh_k_delta_step<128>, dim3(nv * 2), dim3(64), 0, st, cat, ab, gate, conv_w, conv_state,
+                           ssm_a, dt_bias, S, out, out_gate, out_runs, io_pos, nk, nv, K, cc, out_scale);
     } else if (dk == 64) {
-        hipLaunchKernelGGL(oh_k_delta_step<64>, dim3(nv / 4), dim3(256), 0, st, cat, gate, ab, conv_w,
-                           conv_state, ssm_a, dt_bias, ssm_norm, S, out, oqs, oqd, oqb, io_pos, nk, nv, K,
-                           cc, eps, out_scale);
+        hipLaunchKernelGGL(oh_k_delta_step<64>, dim3(nv), dim3(64), 0, st, cat, ab, gate, conv_w, conv_state,
+                           ssm_a, dt_bias, S, out, out_gate, out_runs, io_pos, nk, nv, K, cc, out_scale);
     } else {
         return hipErrorInvalidValue;
     }
@@ -81,19 +78,41 @@ hipError_t oh_launch_attn_prep(const float *qproj, const float *kin, const float
 
 hipError_t oh_launch_attn_scores(const float *qr, const uint32_t *Kt, const float *Ks,
                                  float *scores, const int32_t *io_pos, int nh, int nkv, int hd,
-                                 int cap, float scale, hipStream_t st) {
+                                 int cap, float scale, int exact_max, hipStream_t st) {
     hipLaunchKernelGGL(oh_k_attn_scores, dim3(nh, (cap + 255) / 256), dim3(256), 0, st, qr, Kt, Ks,
-                       scores, io_pos, nh, nkv, hd, cap, scale);
+                       scores, io_pos, nh, nkv, hd, cap, scale, exact_max);
     return hipGetLastError();
 }
 
 hipError_t oh_launch_attn_out(const float *scores, const int8_t *Vq, const float *Vs, const float *gate,
-                              float *out, int8_t *oqs, float *oqd, int16_t *oqb, float *part, int *cnt,
-                              const int32_t *io_pos, int nh, int nkv, int hd, int cap, int exact_max,
-                              hipStream_t st) {
-    const int hpb = 256 / hd;
-    hipLaunchKernelGGL(oh_k_attn_out, dim3(nh / hpb, (cap + 255) / 256), dim3(256), 0, st, scores, Vq, Vs, gate,
-                       out, oqs, oqd, oqb, part, cnt, io_pos, nh, nkv, hd, cap, exact_max);
+                              float *out, const int32_t *io_pos, int nh, int nkv, int hd, int cap,
+                              int exact_max, hipStream_t st) {
+    hipLaunchKernelGGL(oh_k_attn_out, dim3(nh / (256 / hd)), dim3(256), 0, st, scores, Vq, Vs, gate, out,
+                       io_pos, nh, nkv, hd, cap, exact_max);
+    return hipGetLastError();
+}
+
+int oh_flash_lds_bytes(int nh, int nkv, int hd) {
+    const int G = nh / nkv;
+    return G * hd * 4 + kFlashCh * (hd / 4 + 1) * 4 + 16 + (kFlashCh / 16) * hd * 16 + G * kFlashCh * 4 +
+           2 * kFlashCh * 4;
+}
+int oh_flash_chunk(void) { return kFlashCh; }
+
+hipError_t oh_launch_attn_flash(const float *qr, const uint32_t *Kt, const float *Ks, const int8_t *Vq,
+                                const float *Vs, float *part_o, float *part_ml, const int32_t *io_pos,
+                                int nh, int nkv, int hd, int cap, float scale, int exact_max, hipStream_t st) {
+    hipLaunchKernelGGL(oh_k_attn_flash, dim3(nkv, (cap + kFlashCh - 1) / kFlashCh), dim3(256),
+                       (size_t)oh_flash_lds_bytes(nh, nkv, hd), st, qr, Kt, Ks, Vq, Vs, part_o, part_ml, io_pos,
+                       nh, nkv, hd, cap, scale, exact_max);
+    return hipGetLastError();
+}
+
+hipError_t oh_launch_attn_combine(const float *part_o, const float *part_ml, const float *gate, float *out,
+                                  const int32_t *io_pos, int nh, int nkv, int hd, int cap, int exact_max,
+                                  hipStream_t st) {
+    hipLaunchKernelGGL(oh_k_attn_combine, dim3(nh, hd / 64), dim3(256), 0, st, part_o, part_ml, gate, out,
+                       io_pos, nh, nkv, hd, cap, exact_max);
     return hipGetLastError();
 }
 

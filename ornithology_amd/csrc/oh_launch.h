@@ -18,11 +18,10 @@ hipError_t oh_launch_dequant(const uint8_t *A, const uint8_t *B, const uint8_t *
                              int64_t row0, int64_t nrows, float *out, hipStream_t st);
 hipError_t oh_launch_embed(const uint8_t *A, const uint8_t *B, const uint8_t *C, int type, int in,
                            const int32_t *toks, const int32_t *io_pos, float *x, hipStream_t st);
-hipError_t oh_launch_delta_step(int dk, const float *cat, const float *gate, const float *ab,
+hipError_t oh_launch_delta_step(int dk, const float *cat, const float *ab, const float *gate,
                                 const float *conv_w, float *conv_state, const float *ssm_a,
-                                const float *dt_bias, const float *ssm_norm, float *S, float *out,
-                                int8_t *oqs, float *oqd, int16_t *oqb, const int32_t *io_pos,
-                                int nk, int nv, int K, int cc, float eps, float out_scale,
+                                const float *dt_bias, float *S, float *out, float *out_gate, double *out_runs,
+                                const int32_t *io_pos, int nk, int nv, int K, int cc, float out_scale,
                                 hipStream_t st);
 hipError_t oh_launch_attn_prep(const float *qproj, const float *kin, const float *vin,
                                const float *q_norm, const float *k_norm, const float2 *rope,
@@ -31,11 +30,19 @@ hipError_t oh_launch_attn_prep(const float *qproj, const float *kin, const float
                                int rot, int cap, float eps, hipStream_t st);
 hipError_t oh_launch_attn_scores(const float *qr, const uint32_t *Kt, const float *Ks,
                                  float *scores, const int32_t *io_pos, int nh, int nkv, int hd,
-                                 int cap, float scale, hipStream_t st);
+                                 int cap, float scale, int exact_max, hipStream_t st);
 hipError_t oh_launch_attn_out(const float *scores, const int8_t *Vq, const float *Vs, const float *gate,
-                              float *out, int8_t *oqs, float *oqd, int16_t *oqb, float *part, int *cnt,
-                              const int32_t *io_pos, int nh, int nkv, int hd, int cap, int exact_max,
-                              hipStream_t st);
+                              float *out, const int32_t *io_pos, int nh, int nkv, int hd, int cap,
+                              int exact_max, hipStream_t st);
+// flash decoding past exact_max positions: chunk partials, then their merge
+int oh_flash_lds_bytes(int nh, int nkv, int hd);
+int oh_flash_chunk(void);
+hipError_t oh_launch_attn_flash(const float *qr, const uint32_t *Kt, const float *Ks, const int8_t *Vq,
+                                const float *Vs, float *part_o, float *part_ml, const int32_t *io_pos,
+                                int nh, int nkv, int hd, int cap, float scale, int exact_max, hipStream_t st);
+hipError_t oh_launch_attn_combine(const float *part_o, const float *part_ml, const float *gate, float *out,
+                                  const int32_t *io_pos, int nh, int nkv, int hd, int cap, int exact_max,
+                                  hipStream_t st);
 hipError_t oh_launch_moe_route(const float *logits, int ne, int k, const float *shgate_logit,
                                int32_t *idx, float *w, float *shgate, hipStream_t st);
 hipError_t oh_launch_moe_combine(float *x, const float *o, const float *w, int k, int H,

@@ -76,104 +76,141 @@ oh_k_embed(const uint8_t *A, const uint8_t *B, const uint8_t *C, int type, int i
 
 // ---- gated delta-net decode step (src/ornith_rforward.c:457-503,300-319,
 //      src/ornith_attn.c:198-213,370-388) -----------------------------------------
-// One block of 256 threads covers 256/DK consecutive value heads, one state
-// row per thread. The conv window is double-buffered by position parity: the
-// step reads window[p] and the channel's single owner writes window[1-p], so
-// blocks sharing a key head never race. The state S of value head hv is kept
-// transposed in HBM (element (r, c) at S[hv][c][r]) so the row-per-lane walk
-// over c is a coalesced 256-byte load per wave.
+// One wave per 64 state rows of one value head (grid nv * DK/64). The state S
+// of value head hv is row-major in HBM (element (r, c) at S[hv][r][c], the
+// reference's layout). The wave reads its 64 x DK slab with contiguous 16-byte
+// loads, all issued right after the step's small inputs (vector loads
+// complete in order), transposes it through LDS so each lane walks its own row
+// in the reference's order, and writes it back the same way. The output is
+// o * 1/sqrt(dk) per row, silu(gate) per row and the sum of o^2 over the
+// wave's rows; the per-head gated RMSNorm is applied by the consumer (the
+// ssm_out projection prologue). The conv window is
+// double-buffered by position parity: the step reads window[p] and the
+// channel's single owner writes window[1-p], so waves sharing a key head never
+// race.
 template <int DK>
-__global__ void __launch_bounds__(256)
-oh_k_delta_step(const float *cat, const float *gate, const float *ab,
-                const float *conv_w, float *conv_state, const float *ssm_a,
-                const float *dt_bias, const float *ssm_norm, float *S,
-                float *out, int8_t *oqs, float *oqd, int16_t *oqb,
-                const int32_t *io_pos, int nk, int nv, int K, int cc,
-                float eps, float out_scale) {
-    constexpr int HPB = 256 / DK;
-    __shared__ float qn[HPB][DK], kn[HPB][DK], vec[256];
-    __shared__ double red[HPB][DK / 64 > 0 ? DK / 64 : 1];
-    const int t = (int)threadIdx.x, hl = t / DK, r = t % DK;
-    const int hv = (int)blockIdx.x * HPB + hl, kh = hv % nk;
-    const int qd = nk * DK;
+__global__ void __launch_bounds__(64)
+oh_k_delta_step(const float *cat, const float *ab, const float *gate, const float *conv_w,
+                float *conv_state, const float *ssm_a, const float *dt_bias, float *S, float *out,
+                float *out_gate, double *out_runs, const int32_t *io_pos, int nk, int nv, int K, int cc,
+                float out_scale) {
+    constexpr int KMAX = 8, NQ = DK / 64, TS = DK + 1;   // TS: padded LDS row (no bank conflicts)
+    __shared__ float qn[DK], kn[DK];
+    __shared__ float tile[64 * TS];
+    const int lane = (int)threadIdx.x;
+    const int hv = (int)blockIdx.x / NQ, slab = (int)blockIdx.x % NQ;
+    const int r = slab * 64 + lane, kh = hv % nk, qd = nk * DK;
     const int pos = *io_pos, p = pos & 1;
     const float *win = conv_state + (size_t)p * (K - 1) * cc;
     float *nwin = conv_state + (size_t)(1 - p) * (K - 1) * cc;
 
-    // causal depthwise conv (no bias) + SiLU for this row's q, k, v channels
-    float cv[3];
-    const int ch3[3] = { kh * DK + r, qd + kh * DK + r, 2 * qd + hv * DK + r };
+    // small inputs first: for channel a: q channels kh*DK + lane + 64i (i < NQ),
+    // k channels likewise, then this row's v channel
+    constexpr int NCH = 2 * NQ + 1;
+    int ch[NCH];
 #pragma unroll
-    for (int a = 0; a < 3; a++) {
-        const int ch = ch3[a];
-        const float *w = conv_w + (size_t)ch * K;
-        float acc = 0.0f;
-        for (int j = 0; j < K - 1; j++) acc += w[j] * win[(size_t)j * cc + ch];
-        acc += w[K - 1] * cat[ch];
+    for (int i = 0; i < NQ; i++) {
+        ch[i] = kh * DK + lane + 64 * i;
+        ch[NQ + i] = qd + kh * DK + lane + 64 * i;
+    }
+    ch[2 * NQ] = 2 * qd + hv * DK + r;
+    float cw[NCH][KMAX], wv[NCH][KMAX], cx[NCH];
+#pragma unroll
+    for (int a = 0; a < NCH; a++) {
+#pragma unroll
+        for (int j = 0; j < KMAX; j++) {
+            cw[a][j] = j < K ? conv_w[(size_t)ch[a] * K + j] : 0.0f;
+            wv[a][j] = j < K - 1 ? win[(size_t)j * cc + ch[a]] : 0.0f;
+        }
+        cx[a] = cat[ch[a]];
+    }
+    const float sa = ssm_a[hv], av = ab[hv], bv = ab[nv + hv], dtb = dt_bias[hv];
+    const float gz = gate[(size_t)hv * DK + r];
+    // then the state slab: rows [slab*64, +64) of head hv, contiguous
+    const float4 *Sr = (const float4 *)(S + ((size_t)hv * DK + slab * 64) * DK);
+    float4 st[DK / 4];
+#pragma unroll
+    for (int i = 0; i < DK / 4; i++) st[i] = Sr[lane + 64 * i];
+    __builtin_amdgcn_sched_barrier(0);
+
+    // causal depthwise conv (no bias) + SiLU
+    float cv[NCH];
+#pragma unroll
+    for (int a = 0; a < NCH; a++) {
+        float acc = 0.0f, wl = 0.0f;
+#pragma unroll
+        for (int j = 0; j < KMAX; j++) {
+            if (j < K - 1) acc += cw[a][j] * wv[a][j];
+            if (j == K - 1) wl = cw[a][j];
+        }
+        acc += wl * cx[a];
         cv[a] = ref_silu(acc);
-        const bool owner = a == 2 || hv < nk;
+        const bool owner = a == 2 * NQ || (hv < nk && slab == 0);
         if (owner) {
-            for (int j = 0; j + 1 < K - 1; j++) nwin[(size_t)j * cc + ch] = win[(size_t)(j + 1) * cc + ch];
-            if (K >= 2) nwin[(size_t)(K - 2) * cc + ch] = cat[ch];
+#pragma unroll
+            for (int j = 0; j + 1 < KMAX; j++)
+                if (j + 1 < K - 1) nwin[(size_t)j * cc + ch[a]] = wv[a][j + 1];
+            nwin[(size_t)(K - 2) * cc + ch[a]] = cx[a];
         }
     }
-    // per-head L2 normalisation of q and k (src/ornith_tensor.c:155-160);
-    // tree-ordered double sums
-    {
-        double sq = wave_sum_d((double)cv[0] * cv[0]);
-        double sk = wave_sum_d((double)cv[1] * cv[1]);
-        const int w = r >> 6;
-        if (lane_id() == 0) red[hl][w] = sq;
-        __syncthreads();
-        double tq = red[hl][0];
-        for (int k = 1; k < DK / 64; k++) tq += red[hl][k];
-        __syncthreads();
-        if (lane_id() == 0) red[hl][w] = sk;
-        __syncthreads();
-        double tk = red[hl][0];
-        for (int k = 1; k < DK / 64; k++) tk += red[hl][k];
-        const float iq = (float)(1.0 / sqrt(tq + (double)1e-6f));
-        const float ik = (float)(1.0 / sqrt(tk + (double)1e-6f));
-        qn[hl][r] = cv[0] * iq;
-        kn[hl][r] = cv[1] * ik;
-        __syncthreads();
+    // per-head L2 normalisation of q and k (src/ornith_tensor.c:155-160):
+    // double sums of each 64-channel run (butterfly), then the runs in order
+    double tq = 0.0, tk = 0.0;
+#pragma unroll
+    for (int i = 0; i < NQ; i++) {
+        const double sq = wave_sum_d((double)cv[i] * cv[i]);
+        const double sk = wave_sum_d((double)cv[NQ + i] * cv[NQ + i]);
+        tq = i == 0 ? sq : tq + sq;
+        tk = i == 0 ? sk : tk + sk;
     }
-    const float alpha = ref_expf(ssm_a[hv] * ref_softplus(ab[hv] + dt_bias[hv]));
-    const float beta = ref_sigmoid(ab[nv + hv]);
+    const float iq = (float)(1.0 / sqrt(tq + (double)1e-6f));
+    const float ik = (float)(1.0 / sqrt(tk + (double)1e-6f));
+#pragma unroll
+    for (int i = 0; i < NQ; i++) {
+        qn[lane + 64 * i] = cv[i] * iq;
+        kn[lane + 64 * i] = cv[NQ + i] * ik;
+    }
+    const float alpha = ref_expf(sa * ref_softplus(av + dtb));
+    const float beta = ref_sigmoid(bv);
+    // slab -> LDS, row-padded
+#pragma unroll
+    for (int i = 0; i < DK / 4; i++) {
+        const int f = lane + 64 * i, row = (4 * f) / DK, col = (4 * f) % DK;
+        float *t = tile + row * TS + col;
+        t[0] = st[i].x; t[1] = st[i].y; t[2] = st[i].z; t[3] = st[i].w;
+    }
+    __syncthreads();
 
-    float *Sh = S + (size_t)hv * DK * DK;
+    float *tr = tile + lane * TS;
     float s[DK];
 #pragma unroll
-    for (int c = 0; c < DK; c++) s[c] = Sh[c * DK + r] * alpha;
+    for (int c = 0; c < DK; c++) s[c] = tr[c] * alpha;
     float sk = 0.0f;
 #pragma unroll
-    for (int c = 0; c < DK; c++) sk += s[c] * kn[hl][c];
-    const float u = beta * (cv[2] - sk);
+    for (int c = 0; c < DK; c++) sk += s[c] * kn[c];
+    const float u = beta * (cv[2 * NQ] - sk);
 #pragma unroll
-    for (int c = 0; c < DK; c++) s[c] += u * kn[hl][c];
+    for (int c = 0; c < DK; c++) s[c] += u * kn[c];
     float o = 0.0f;
 #pragma unroll
-    for (int c = 0; c < DK; c++) o += s[c] * qn[hl][c];
+    for (int c = 0; c < DK; c++) o += s[c] * qn[c];
 #pragma unroll
-    for (int c = 0; c < DK; c++) Sh[c * DK + r] = s[c];
-
-    // 1/sqrt(dk), per-head RMSNorm(ssm_norm), * SiLU(gate)
-    o *= out_scale;
-    {
-        const double so = wave_sum_d((double)o * o);
-        __syncthreads();
-        if (lane_id() == 0) red[hl][r >> 6] = so;
-        __syncthreads();
-        double tot = red[hl][0];
-        for (int k = 1; k < DK / 64; k++) tot += red[hl][k];
-        const float inv = (float)(1.0 / sqrt(tot / (double)DK + (double)eps));
-        o = o * inv * ssm_norm[r];
-    }
-    o = o * ref_silu(gate[hv * DK + r]);
-    out[hv * DK + r] = o;
-    vec[t] = o;
+    for (int c = 0; c < DK; c++) tr[c] = s[c];
     __syncthreads();
-    if (t < 64) q8k_block_from_lds(vec, 0, oqs + (size_t)blockIdx.x * 256, oqd + blockIdx.x, oqb + (size_t)blockIdx.x * 16);
+    float4 *Sw = (float4 *)(S + ((size_t)hv * DK + slab * 64) * DK);
+#pragma unroll
+    for (int i = 0; i < DK / 4; i++) {
+        const int f = lane + 64 * i, row = (4 * f) / DK, col = (4 * f) % DK;
+        const float *t = tile + row * TS + col;
+        Sw[f] = make_float4(t[0], t[1], t[2], t[3]);
+    }
+    // the gated RMSNorm's inputs for the consumer: o, silu(gate) and the
+    // butterfly double sum of o^2 over this wave's 64 rows
+    o *= out_scale;
+    const double so = wave_sum_d((double)o * o);
+    out[(size_t)hv * DK + r] = o;
+    out_gate[(size_t)hv * DK + r] = ref_silu(gz);
+    if (lane == 0) out_runs[blockIdx.x] = so;
 }
 
 // ---- GQA decode (src/ornith_rforward.c:419-455, src/ornith_attn.c:65-149) -------
@@ -255,14 +292,16 @@ oh_k_attn_prep(const float *qproj, const float *kin, const float *vin,
 }
 
 // scores[h][t] = (sum_i q_i*code_i) * Ks_t * scale, sequential over i
-// (src/ornith_attn.c:80-85,119-122). Grid (nh, cap/256); positions > pos exit.
+// (src/ornith_attn.c:80-85,119-122). Grid (nh, cap/256); positions > pos exit,
+// and the whole grid exits when the context is longer than exact_max (the
+// flash kernels below take it).
 extern "C" __global__ void __launch_bounds__(256)
 oh_k_attn_scores(const float *qr, const uint32_t *Kt, const float *Ks, float *scores,
-                 const int32_t *io_pos, int nh, int nkv, int hd, int cap, float scale) {
+                 const int32_t *io_pos, int nh, int nkv, int hd, int cap, float scale, int exact_max) {
     __shared__ float q[256];
     const int h = (int)blockIdx.x, t = (int)(blockIdx.y * 256 + threadIdx.x);
     const int T = *io_pos + 1;
-    if ((int)blockIdx.y * 256 >= T) return;
+    if ((int)blockIdx.y * 256 >= T || T > exact_max) return;
     const int kvh = h / (nh / nkv);
     if ((int)threadIdx.x < hd) q[threadIdx.x] = qr[(size_t)h * hd + threadIdx.x];
     __syncthreads();
@@ -290,28 +329,19 @@ oh_k_attn_scores(const float *qr, const uint32_t *Kt, const float *Ks, float *sc
 
 // softmax over T (src/ornith_tensor.c:108-115; tree-ordered double sum) and the
 // output o_i = sum_t (p_t*Vs_t)*code_t,i, sequential over t, skipping zero
-// weights (src/ornith_attn.c:132-140); then o *= sigmoid(gate) and Q8_K of the
-// 256 outputs of a block (256/hd heads).
-// Grid (nh*hd/256, cap/256). For T <= exact_max, block (g, 0) walks all T in
-// order, as the reference does. Longer contexts split the walk into 256-position
-// chunks (block (g, k) takes chunk k, each walked in order) whose partial sums
-// the last block to finish adds in chunk order; the softmax statistics are the
-// same in every block. Blocks signal completion with a fenced atomic counter
-// that the last block resets; nothing waits.
+// weights (src/ornith_attn.c:132-140); then o *= sigmoid(gate). A block covers
+// 256/hd heads and walks all T positions in the reference's order. Contexts
+// longer than exact_max exit (the flash kernels below take them).
 extern "C" __global__ void __launch_bounds__(256)
 oh_k_attn_out(const float *scores, const int8_t *Vq, const float *Vs, const float *gate,
-              float *out, int8_t *oqs, float *oqd, int16_t *oqb, float *part, int *cnt,
-              const int32_t *io_pos, int nh, int nkv, int hd, int cap, int exact_max) {
-    __shared__ float vec[256];
+              float *out, const int32_t *io_pos, int nh, int nkv, int hd, int cap, int exact_max) {
     __shared__ float pbuf[4][256];
     __shared__ float inv_s[4], mx_s[4];
     __shared__ double red[4];
     __shared__ float mred[4];
-    __shared__ int last;
-    const int hpb = 256 / hd, t = (int)threadIdx.x, g = (int)blockIdx.x, kc = (int)blockIdx.y;
-    const int T = *io_pos + 1, nch = (T + 255) / 256, maxch = gridDim.y;
-    const bool exact = T <= exact_max;
-    if (exact ? kc != 0 : kc >= nch) return;
+    const int hpb = 256 / hd, t = (int)threadIdx.x, g = (int)blockIdx.x;
+    const int T = *io_pos + 1;
+    if (T > exact_max) return;
     for (int hl = 0; hl < hpb; hl++) {
         const float *sc = scores + (size_t)(g * hpb + hl) * cap;
         float mx = -INFINITY;
@@ -329,10 +359,9 @@ oh_k_attn_out(const float *scores, const int8_t *Vq, const float *Vs, const floa
     const int hl = t / hd, i = t % hd, h = g * hpb + hl;
     const int kvh = h / (nh / nkv);
     const uint4 *vt = (const uint4 *)Vq + (size_t)kvh * (cap / 16) * hd + i;
-    const int c0 = exact ? 0 : kc, c1 = exact ? nch : kc + 1;
     float o = 0.0f;
-    for (int ck = c0; ck < c1; ck++) {
-        const int t0 = ck * 256, n = T - t0 < 256 ? T - t0 : 256;
+    for (int t0 = 0; t0 < T; t0 += 256) {
+        const int n = T - t0 < 256 ? T - t0 : 256;
         __syncthreads();
         for (int k = t; k < hpb * 256; k += 256) {
             const int hh = k / 256, tt = k % 256;
@@ -364,24 +393,142 @@ oh_k_attn_out(const float *scores, const int8_t *Vq, const float *Vs, const floa
             }
         }
     }
-    if (!exact) {
-        float *pp = part + ((size_t)g * maxch) * 256;
-        pp[(size_t)kc * 256 + t] = o;
-        __threadfence();
-        __syncthreads();
-        if (t == 0) last = atomicAdd(&cnt[g], 1) == nch - 1;
-        __syncthreads();
-        if (!last) return;
-        __threadfence();
-        o = 0.0f;
-        for (int k = 0; k < nch; k++) o += pp[(size_t)k * 256 + t];
-        if (t == 0) cnt[g] = 0;
+    out[(size_t)h * hd + i] = o * ref_sigmoid(gate[(size_t)h * hd + i]);
+}
+
+// ---- flash decoding for long contexts ----------------------------------------------
+// Past exact_max positions the attention of one KV head is split into chunks
+// of 64 positions (block (kvh, chunk)): all nh/nkv query heads of the group
+// score the chunk against its Q8 keys once, take the chunk's softmax
+// statistics (max m, sum l of exp(s - m)) and the chunk's unnormalised output
+// sum_t exp(s_t - m) * Vs_t * code_t. attn_combine merges the chunks with the
+// usual rescaling. This re-associates the reference's sums (tolerance, not bit
+// parity), and reads each KV byte once per group instead of once per head.
+constexpr int kFlashCh = 64;
+
+extern "C" __global__ void __launch_bounds__(256)
+oh_k_attn_flash(const float *qr, const uint32_t *Kt, const float *Ks, const int8_t *Vq, const float *Vs,
+                float *part_o, float *part_ml, const int32_t *io_pos, int nh, int nkv, int hd, int cap,
+                float scale, int exact_max) {
+    extern __shared__ __align__(16) uint8_t fsm[];
+    const int T = *io_pos + 1;
+    const int g = (int)blockIdx.x, c = (int)blockIdx.y, t0 = c * kFlashCh;
+    if (T <= exact_max || t0 >= T) return;
+    const int G = nh / nkv, tid = (int)threadIdx.x, hw = hd / 4, kst = hw + 1;
+    const int nchmax = (cap + kFlashCh - 1) / kFlashCh;
+    float *q = (float *)fsm;                                  // [G][hd]
+    uint32_t *kc = (uint32_t *)(q + G * hd);                  // [64][hw + 1]
+    uint4 *vt = (uint4 *)(((uintptr_t)(kc + kFlashCh * kst) + 15) & ~(uintptr_t)15);   // [4][hd]
+    float *pp = (float *)(vt + (kFlashCh / 16) * hd);         // [G][64]
+    float *ks = pp + G * kFlashCh, *vs = ks + kFlashCh;       // [64] each
+    // loads: query heads of the group, the chunk's key words, value tiles, scales
+    for (int k = tid; k < G * hd; k += 256) q[k] = qr[(size_t)g * G * hd + k];
+    for (int k = tid; k < hw * kFlashCh; k += 256) {
+        const int w = k / kFlashCh, j = k % kFlashCh;
+        const int t = t0 + j < T ? t0 + j : T - 1;
+        kc[j * kst + w] = Kt[((size_t)g * hw + w) * cap + t];
     }
-    o *= ref_sigmoid(gate[(size_t)h * hd + i]);
-    out[(size_t)h * hd + i] = o;
-    vec[t] = o;
+    for (int k = tid; k < (kFlashCh / 16) * hd; k += 256) {
+        const int tt = k / hd, i = k % hd;
+        const int tile = (t0 / 16 + tt) * 16 < T ? t0 / 16 + tt : (T - 1) / 16;
+        vt[k] = ((const uint4 *)Vq)[((size_t)g * (cap / 16) + tile) * hd + i];
+    }
+    if (tid < kFlashCh) {
+        const int t = t0 + tid < T ? t0 + tid : T - 1;
+        ks[tid] = Ks[(size_t)t * nkv + g];
+        vs[tid] = Vs[(size_t)t * nkv + g];
+    }
     __syncthreads();
-    if (t < 64) q8k_block_from_lds(vec, 0, oqs + (size_t)g * 256, oqd + g, oqb + (size_t)g * 16);
+    // scores of (head h, position j)
+    for (int pr = tid; pr < G * kFlashCh; pr += 256) {
+        const int h = pr / kFlashCh, j = pr % kFlashCh;
+        const float4 *qh = (const float4 *)(q + h * hd);
+        const uint32_t *kj = kc + j * kst;
+        float acc = 0.0f;
+        for (int w = 0; w < hw; w++) {
+            const float4 qv = qh[w];
+            const uint32_t wd = kj[w];
+            acc = fmaf(qv.x, (float)(int8_t)(wd & 0xff), acc);
+            acc = fmaf(qv.y, (float)(int8_t)((wd >> 8) & 0xff), acc);
+            acc = fmaf(qv.z, (float)(int8_t)((wd >> 16) & 0xff), acc);
+            acc = fmaf(qv.w, (float)(int8_t)(wd >> 24), acc);
+        }
+        const float sc = ks[j] == 0.0f ? 0.0f : acc * ks[j] * scale;
+        pp[pr] = t0 + j < T ? sc : -INFINITY;
+    }
+    __syncthreads();
+    // per-head chunk statistics: a wave per head, a lane per position
+    const int wave = tid >> 6, lane = tid & 63;
+    for (int h = wave; h < G; h += 4) {
+        const float sv = pp[h * kFlashCh + lane];
+        const float m = wave_max_fast(sv);
+        const float e = sv == -INFINITY ? 0.0f : __expf(sv - m);
+        float l = e;
+        for (int mm = 32; mm >= 1; mm >>= 1) l += shfl_xor(l, mm);
+        pp[h * kFlashCh + lane] = e * vs[lane];
+        if (lane == 0) {
+            float *ml = part_ml + (((size_t)g * nchmax + c) * G + h) * 2;
+            ml[0] = m;
+            ml[1] = l;
+        }
+    }
+    __syncthreads();
+    // unnormalised outputs: thread -> dimension i, every head of the group
+    for (int k = tid; k < G * hd; k += 256) {
+        const int h = k / hd, i = k % hd;
+        const float *ph = pp + h * kFlashCh;
+        float o = 0.0f;
+#pragma unroll
+        for (int tt = 0; tt < kFlashCh / 16; tt++) {
+            const uint4 cw = vt[tt * hd + i];
+#pragma unroll
+            for (int j = 0; j < 16; j++) {
+                const int8_t cv = (int8_t)(wsel(cw, j >> 2) >> (8 * (j & 3)));
+                o = fmaf(ph[tt * 16 + j], (float)cv, o);
+            }
+        }
+        part_o[(((size_t)g * nchmax + c) * G + h) * hd + i] = o;
+    }
+}
+
+// Merge of the flash chunks of query head h (grid (nh, hd/64), 4 waves; wave w
+// takes chunks w, w+4, ...; a lane per dimension): running max rescaling,
+// then out = (sum_c o_c e^(m_c-M)) / (sum_c l_c e^(m_c-M)) * sigmoid(gate).
+extern "C" __global__ void __launch_bounds__(256)
+oh_k_attn_combine(const float *part_o, const float *part_ml, const float *gate, float *out,
+                  const int32_t *io_pos, int nh, int nkv, int hd, int cap, int exact_max) {
+    __shared__ float sm[4][3][64];
+    const int T = *io_pos + 1;
+    if (T <= exact_max) return;
+    const int h = (int)blockIdx.x, G = nh / nkv, g = h / G, hl = h % G;
+    const int wave = (int)(threadIdx.x >> 6), lane = (int)(threadIdx.x & 63);
+    const int i = (int)blockIdx.y * 64 + lane;
+    const int nch = (T + kFlashCh - 1) / kFlashCh, nchmax = (cap + kFlashCh - 1) / kFlashCh;
+    float M = -INFINITY, L = 0.0f, O = 0.0f;
+    for (int c = wave; c < nch; c += 4) {
+        const size_t base = ((size_t)g * nchmax + c) * G + hl;
+        const float m = part_ml[base * 2], l = part_ml[base * 2 + 1];
+        const float o = part_o[base * hd + i];
+        const float mn = fmaxf(M, m);
+        const float a = M == -INFINITY ? 0.0f : __expf(M - mn), b = __expf(m - mn);
+        O = O * a + o * b;
+        L = L * a + l * b;
+        M = mn;
+    }
+    sm[wave][0][lane] = M; sm[wave][1][lane] = L; sm[wave][2][lane] = O;
+    __syncthreads();
+    if (wave == 0) {
+        float Mt = -INFINITY;
+        for (int w = 0; w < 4; w++) Mt = fmaxf(Mt, sm[w][0][lane]);
+        float Lt = 0.0f, Ot = 0.0f;
+        for (int w = 0; w < 4; w++) {
+            const float mw = sm[w][0][lane];
+            const float f = mw == -INFINITY ? 0.0f : __expf(mw - Mt);
+            Lt += sm[w][1][lane] * f;
+            Ot += sm[w][2][lane] * f;
+        }
+        out[(size_t)h * hd + i] = Ot / Lt * ref_sigmoid(gate[(size_t)h * hd + i]);
+    }
 }
 
 // ---- MoE router (src/ornith_moe.c:8-30) ------------------------------------------

@@ -68,18 +68,15 @@ OH_DEV void q8k_block_from_lds(const float *v, int qb, int8_t *qs, float *d, int
                                int qstride = 256) {
     const int lane = lane_id();
     const float *xb = v + qb * 256;
-    float best = -1.0f; int bi = 0;
+    float a[4];
 #pragma unroll
-    for (int k = 0; k < 4; k++) {
-        const int e = lane + 64 * k;
-        const float a = fabsf(xb[e]);
-        if (a > best) { best = a; bi = e; }
-    }
-    for (int m = 32; m >= 1; m >>= 1) {
-        const float ob = shfl_xor(best, m);
-        const int oi = shfl_xor(bi, m);
-        if (ob > best || (ob == best && oi < bi)) { best = ob; bi = oi; }
-    }
+    for (int k = 0; k < 4; k++) a[k] = fabsf(xb[lane + 64 * k]);
+    // largest magnitude (NaN never wins), then its first index
+    const float best = wave_max_fast(fmaxf(fmaxf(a[0], a[1]), fmaxf(a[2], a[3])));
+    int bi = 256;
+#pragma unroll
+    for (int k = 3; k >= 0; k--) if (a[k] == best) bi = lane + 64 * k;
+    bi = wave_min_fast(bi);
     int8_t *q = qs + (int64_t)qb * qstride;
     int16_t *b = bs + (int64_t)qb * 16;
     if (best == 0.0f || !(best > 0.0f)) {
@@ -90,20 +87,14 @@ OH_DEV void q8k_block_from_lds(const float *v, int qb, int8_t *qs, float *d, int
         return;
     }
     const float iscale = -127.0f / xb[bi];
-    int sums[4];
 #pragma unroll
     for (int k = 0; k < 4; k++) {
         const int e = lane + 64 * k;
         float r = __builtin_rintf(iscale * xb[e]);
-        int v = (int)r;
-        v = v > 127 ? 127 : (v < -128 ? -128 : v);
-        q[e] = (int8_t)v;
-        sums[k] = v;
-    }
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-        int sv = sums[k];
-        sv += shfl_xor(sv, 1); sv += shfl_xor(sv, 2); sv += shfl_xor(sv, 4); sv += shfl_xor(sv, 8);
+        int c = (int)r;
+        c = c > 127 ? 127 : (c < -128 ? -128 : c);
+        q[e] = (int8_t)c;
+        const int sv = row16_sum_i(c);                 // codes 64k + 16g .. +15
         if ((lane & 15) == 0) b[4 * k + (lane >> 4)] = (int16_t)sv;
     }
     if (lane == 0) d[qb] = 1.0f / iscale;
@@ -371,7 +362,7 @@ OH_DEV void mv_prologue(const oh_mvseg &s, int slot, int blk, uint8_t *smem, dou
     } else {
         for (int i = tid; i < in; i += 256) v[i] = s.xf[ao + i];
         lds_barrier();
-        rmsnorm_lds(v, s.nw, s.eps, in, red);
+        if (s.pro == OH_PRO_NORM) rmsnorm_lds(v, s.nw, s.eps, in, red);
     }
     const bool store = blk == 0 && s.oqs != nullptr;
     if (blk == 0 && s.oxf)
@@ -385,20 +376,122 @@ OH_DEV void mv_prologue(const oh_mvseg &s, int slot, int blk, uint8_t *smem, dou
     lds_barrier();
 }
 
+// Prologue inputs held in registers (in <= 4096): they are loaded before the
+// first weight step, and the prologue consumes them while that step is still
+// in flight (vector loads complete in order, so inputs loaded after the
+// weights would wait for them).
+struct PIn { float4 a[4], b[4], c[4]; int4 q, bsv; float d; };
+
+OH_DEV void pro_load(PIn &p, const oh_mvseg &s, int slot) {
+    const int tid = (int)threadIdx.x, in = s.in, nb = in / 256;
+    const size_t ao = (size_t)slot * s.astride;
+    if (s.pro == OH_PRO_Q8K) {
+        const int n16 = in / 16;
+        p.q = ((const int4 *)(s.xqs + ao))[tid < n16 ? tid : n16 - 1];
+        p.bsv = ((const int4 *)(s.xbs + ao / 16))[tid < 2 * nb ? tid : 2 * nb - 1];
+        p.d = s.xd[ao / 256 + (tid < nb ? tid : nb - 1)];
+    } else {
+        const float4 *x = (const float4 *)(s.xf + ao);
+        const float4 *w = (const float4 *)(s.pro == OH_PRO_NORM ? s.nw : s.pro == OH_PRO_F32 ? s.xf + ao : s.xf2 + ao);
+        const int n4 = in / 4;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int i = tid + 256 * k < n4 ? tid + 256 * k : n4 - 1;
+            p.a[k] = x[i];
+            p.b[k] = w[i];
+            if (s.pro == OH_PRO_GNORM) p.c[k] = ((const float4 *)s.nw)[i % (s.gdim / 4)];
+        }
+    }
+}
+
+OH_DEV float4 f4_silu_mul(const float4 g, const float4 u) {
+    return make_float4(ref_silu(g.x) * u.x, ref_silu(g.y) * u.y, ref_silu(g.z) * u.z, ref_silu(g.w) * u.w);
+}
+
+OH_DEV void pro_compute(const PIn &p, const oh_mvseg &s, int slot, int blk, uint8_t *smem, double *red) {
+    const int in = s.in, nb = in / 256, tid = (int)threadIdx.x, wave = tid >> 6;
+    int8_t *aqs = (int8_t *)smem;
+    int16_t *abs = (int16_t *)(smem + mv_lds_bs_off(nb));
+    float *ad = (float *)(smem + mv_lds_d_off(nb));
+    float *v = (float *)(smem + mv_lds_v_off(nb));
+    float4 *v4 = (float4 *)v;
+    const size_t ao = (size_t)slot * s.astride;
+    if (s.pro == OH_PRO_Q8K) {
+        if (tid < in / 16) ((int4 *)aqs)[(tid >> 4) * (kAS / 16) + (tid & 15)] = p.q;
+        if (tid < 2 * nb) ((int4 *)abs)[tid] = p.bsv;
+        if (tid < nb) ad[tid] = p.d;
+        lds_barrier();
+        return;
+    }
+    const int n4 = in / 4;
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+        if (tid + 256 * k < n4) v4[tid + 256 * k] = s.pro == OH_PRO_SWIGLU ? f4_silu_mul(p.a[k], p.b[k]) : p.a[k];
+    lds_barrier();
+    if (s.pro == OH_PRO_GNORM) {
+        // per head of gdim elements (src/ornith_rforward.c:300-319): the runs'
+        // double sums of squares added in order, inv = 1/sqrt(ss/gdim + eps),
+        // v = v * inv * w * silu(z)
+        float *hinv = v + in;                       // [in/gdim]
+        const int gd = s.gdim, rpg = gd / 64;
+        if (tid < in / gd) {
+            double tot = s.xruns[tid * rpg];
+            for (int k = 1; k < rpg; k++) tot += s.xruns[tid * rpg + k];
+            hinv[tid] = (float)(1.0 / sqrt(tot / (double)gd + (double)s.eps));
+        }
+        lds_barrier();
+#pragma unroll
+        for (int k = 0; k < 4; k++)
+            if (tid + 256 * k < n4) {
+                const float inv = hinv[4 * (tid + 256 * k) / gd];
+                const float4 x = p.a[k], z = p.b[k], w = p.c[k];
+                v4[tid + 256 * k] = make_float4(x.x * inv * w.x * z.x, x.y * inv * w.y * z.y,
+                                                x.z * inv * w.z * z.z, x.w * inv * w.w * z.w);
+            }
+        lds_barrier();
+    }
+    if (s.pro == OH_PRO_NORM) {
+        // same summation order as the stand-alone RMSNorm kernel
+        double ss = 0.0;
+        for (int i = tid; i < in; i += 256) ss += (double)v[i] * v[i];
+        ss = wave_sum_d(ss);
+        if (lane_id() == 0) red[wave] = ss;
+        lds_barrier();
+        const double tot = (red[0] + red[1]) + (red[2] + red[3]);
+        const float inv = (float)(1.0 / sqrt(tot / (double)in + (double)s.eps));
+#pragma unroll
+        for (int k = 0; k < 4; k++)
+            if (tid + 256 * k < n4) {
+                const float4 x = p.a[k], w = p.b[k];
+                v4[tid + 256 * k] = make_float4(x.x * inv * w.x, x.y * inv * w.y, x.z * inv * w.z, x.w * inv * w.w);
+            }
+        lds_barrier();
+    }
+    const bool store = blk == 0 && s.oqs != nullptr;
+    if (blk == 0 && s.oxf)
+        for (int i = tid; i < in; i += 256) s.oxf[ao + i] = v[i];
+    for (int qb = wave; qb < nb; qb += 4) {
+        q8k_block_from_lds(v, qb, aqs, ad, abs, kAS);
+        if (store) q8k_block_from_lds(v, qb, s.oqs + ao, s.oqd + ao / 256, s.oqb + ao / 16);
+    }
+    lds_barrier();
+}
+
 // Integer-path segment slot: every lane reduces one super-block; a wave step
 // covers 64/nb rows. Steps are double-buffered: the next step's loads are in
 // flight while the current one is reduced. All loads are unconditional
 // (dead lanes and steps past the end re-read an in-bounds block), so the
-// compiler never has to drain the queue at a branch.
+// compiler never has to drain the queue at a branch. expert: the slot's
+// expert for stacked tensors.
 template <int T>
-OH_DEV void mv_seg(const oh_mvseg &s, int slot, int blk, uint8_t *smem, double *red) {
+OH_DEV void mv_seg(const oh_mvseg &s, int slot, int blk, int expert, uint8_t *smem, double *red) {
     const int lane = lane_id(), wave = (int)(threadIdx.x >> 6);
     const int nb = s.nb, rps = 64 / nb;
     const int rl = lane / nb, sb = lane - rl * nb;
     const int u0 = (blk * OH_MV_WAVES + wave) * s.upw;
     const int u1 = u0 + s.upw < s.units ? u0 + s.upw : s.units;
     const int S = u1 > u0 ? u1 - u0 : 0;
-    const int64_t row_base = s.eidx ? (int64_t)s.eidx[slot] * s.rows : 0;
+    const int64_t row_base = (int64_t)expert * s.rows;
     float *y = s.y + (size_t)slot * s.ystride;
     const WP wp = {s.A, s.B, s.C};
     const int8_t *aq = (const int8_t *)smem + sb * kAS;
@@ -406,7 +499,8 @@ OH_DEV void mv_seg(const oh_mvseg &s, int slot, int blk, uint8_t *smem, double *
     const float *adp = (const float *)(smem + mv_lds_d_off(nb)) + sb;
     SB<T> ra, rb;
     auto load = [&](SB<T> &r, int st) {
-        const int unit = u0 + (st < S ? st : S - 1);
+        int unit = u0 + (st < S ? st : S - 1);
+        unit = unit < 0 ? 0 : (unit >= s.units ? s.units - 1 : unit);
         const int row = unit * rps + (rl < rps ? rl : rps - 1);
         const int rowc = row < s.rows ? row : s.rows - 1;
         sb_load(r, wp, (row_base + rowc) * nb + sb);
@@ -421,8 +515,16 @@ OH_DEV void mv_seg(const oh_mvseg &s, int slot, int blk, uint8_t *smem, double *
         for (int i = 0; i < nb; i++) acc += shfl(t, rl * nb + i);
         if (live && sb == 0) emit(y, s.mode, row, acc);
     };
-    if (S > 0) load(ra, 0);
-    mv_prologue(s, slot, blk, smem, red, true);
+    if (s.in <= 4096) {
+        PIn pin;
+        pro_load(pin, s, slot);
+        load(ra, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        pro_compute(pin, s, slot, blk, smem, red);
+    } else {
+        load(ra, 0);
+        mv_prologue(s, slot, blk, smem, red, true);
+    }
     for (int st = 0; st < S; st += 2) {
         load(rb, st + 1);
         comp(ra, st);
@@ -431,47 +533,88 @@ OH_DEV void mv_seg(const oh_mvseg &s, int slot, int blk, uint8_t *smem, double *
     }
 }
 
+// MoE routing of a block (src/ornith_moe.c:8-30): expert e's rank is the
+// number of experts that precede it in the reference's selection order
+// (larger logit, or equal logit and lower index); the k experts of rank < k in
+// rank order are the reference's picks. Softmax over the selected logits in
+// that order by one thread. Logits that are NaN or -inf fall back to the
+// sequential selection of one wave. Results in LDS (sel, w, *shg); block 0
+// also stores them for later launches.
+OH_DEV void route_block(const oh_mvlaunch &L, float *lg, int *sel, float *rw, float *shg, int *bad, int *cnt) {
+    const int tid = (int)threadIdx.x, ne = L.ne, k = L.topk;
+    const int ne4 = (ne + 3) & ~3;
+    if (tid == 0) *bad = 0;
+    if (tid < 64) cnt[tid] = 0;
+    for (int e = tid; e < ne4; e += 256) lg[e] = e < ne ? L.rlog[e] : -INFINITY;
+    __syncthreads();
+    // rank by strictly larger logits; equal logits inside the top k (or a
+    // NaN / -inf anywhere) send the block to the sequential selection
+    const float4 *l4 = (const float4 *)lg;
+    for (int e = tid; e < ne; e += 256) {
+        const float v = lg[e];
+        if (!(v > -INFINITY)) *bad = 1;
+        int gt = 0;
+#pragma unroll 8
+        for (int j = 0; j < ne4 / 4; j++) {
+            const float4 u = l4[j];
+            gt += (int)(u.x > v) + (int)(u.y > v) + (int)(u.z > v) + (int)(u.w > v);
+        }
+        if (gt < k) {
+            if (atomicAdd(&cnt[gt], 1) != 0) *bad = 1;
+            sel[gt] = e;
+        }
+    }
+    __syncthreads();
+    if (*bad) {
+        if (tid < 64) route_wave(lg, ne, k, L.shl, sel, rw, shg);
+    } else if (tid == 0) {
+        float mx = lg[sel[0]];
+        for (int j = 1; j < k; j++) { const float x = lg[sel[j]]; if (x > mx) mx = x; }
+        float sum = 0.0f;
+        for (int j = 0; j < k; j++) { rw[j] = ref_expf(lg[sel[j]] - mx); sum += rw[j]; }
+        for (int j = 0; j < k; j++) rw[j] = rw[j] / sum;
+        if (L.shl) *shg = ref_sigmoid(*L.shl);
+    }
+    __syncthreads();
+    if (blockIdx.x == 0) {
+        if (tid < k) { L.ridx[tid] = sel[tid]; L.rw[tid] = rw[tid]; }
+        if (tid == 0 && L.shl) *L.shg = *shg;
+    }
+}
+
 // Launch body. TK >= 0: every segment is an integer-path segment of type TK;
 // TK < 0: any mix, including fallback segments (one lane per row, the f32
-// activation in LDS). With OH_EP_ROUTE the last block to finish (fenced
-// completion counter, reset by that block) routes the MoE.
+// activation in LDS). With L.route every block first routes the MoE and
+// stacked segments take their experts from that routing.
 template <int TK>
 OH_DEV void mv_body(const oh_mvlaunch &L) {
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ double red[4];
-    __shared__ int last;
+    __shared__ int rsel[64], rbad, rcnt[64];
+    __shared__ float rwt[64], rshg;
     int si = 0;
     while (si + 1 < L.n && (int)blockIdx.x >= L.s[si + 1].block0) si++;
     const oh_mvseg &s = L.s[si];
     const int bseg = (int)blockIdx.x - s.block0;
     const int slot = bseg / s.bps, blk = bseg - slot * s.bps;
+    if (L.route) {
+        route_block(L, (float *)smem, rsel, rwt, &rshg, &rbad, rcnt);
+    }
+    const int expert = !s.eidx ? 0 : (L.route ? rsel[slot] : s.eidx[slot]);
     if (TK >= 0) {
-        mv_seg<TK < 0 ? OH_Q4_K : TK>(s, slot, blk, smem, red);
+        mv_seg<TK < 0 ? OH_Q4_K : TK>(s, slot, blk, expert, smem, red);
     } else if (oh_qdot_can((uint32_t)s.type, s.in) && (s.xqs || s.pro != OH_PRO_Q8K)) {
         switch (s.type) {
-        case OH_Q4_K: mv_seg<OH_Q4_K>(s, slot, blk, smem, red); break;
-        case OH_Q6_K: mv_seg<OH_Q6_K>(s, slot, blk, smem, red); break;
-        default: mv_seg<OH_Q8_0>(s, slot, blk, smem, red); break;
+        case OH_Q4_K: mv_seg<OH_Q4_K>(s, slot, blk, expert, smem, red); break;
+        case OH_Q6_K: mv_seg<OH_Q6_K>(s, slot, blk, expert, smem, red); break;
+        default: mv_seg<OH_Q8_0>(s, slot, blk, expert, smem, red); break;
         }
     } else {
         mv_prologue(s, slot, blk, smem, red, false);
         const float *v = (const float *)(smem + mv_lds_v_off(s.in / 256));
         const int row = blk * 256 + (int)threadIdx.x;
-        const int64_t row_base = s.eidx ? (int64_t)s.eidx[slot] * s.rows : 0;
+        const int64_t row_base = (int64_t)expert * s.rows;
         if (row < s.rows) emit(s.y + (size_t)slot * s.ystride, s.mode, row, row_seq(s, row_base + row, v));
-    }
-    if (L.ep == OH_EP_ROUTE) {
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            __threadfence();
-            last = atomicAdd(L.cnt, 1) == L.total_blocks - 1;
-        }
-        __syncthreads();
-        if (last) {
-            __threadfence();
-            if (threadIdx.x < 64) route_wave(L.rlog, L.ne, L.topk, L.shl, L.ridx, L.rw, L.shg);
-            if (threadIdx.x == 0) *L.cnt = 0;
-        }
     }
 }
 
@@ -499,11 +642,31 @@ OH_DEV void down_body(const oh_mvdown &D) {
     const WP wp = sh ? WP{D.sA, D.sB, D.sC} : WP{D.A, D.B, D.C};
     const int64_t rb = sh ? 0 : (int64_t)D.eidx[j] * D.rows;
     const int rowc = row < D.rows ? (rl < rps ? row : row0) : D.rows - 1;
+    // SwiGLU inputs first (in <= 1024: at most 4 float4 of g and of u per
+    // thread), then the weights: vector loads complete in order
+    const int nf = ns * in / 4, bd = (int)blockDim.x;
+    float4 ga[4], ua[4];
+    if (in <= 1024) {
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int f = tid + bd * k < nf ? tid + bd * k : nf - 1;
+            const int jj = 4 * f / in, e = 4 * f - jj * in;
+            ga[k] = *(const float4 *)(D.g + (size_t)jj * D.stride + e);
+            ua[k] = *(const float4 *)(D.u + (size_t)jj * D.stride + e);
+        }
+    }
     SB<T> r;
     sb_load(r, wp, (rb + rowc) * nb + sb);
-    for (int i = tid; i < ns * in; i += (int)blockDim.x) {
-        const int jj = i / in, e = i - jj * in;
-        v[i] = ref_silu(D.g[(size_t)jj * D.stride + e]) * D.u[(size_t)jj * D.stride + e];
+    __builtin_amdgcn_sched_barrier(0);
+    if (in <= 1024) {
+#pragma unroll
+        for (int k = 0; k < 4; k++)
+            if (tid + bd * k < nf) ((float4 *)v)[tid + bd * k] = f4_silu_mul(ga[k], ua[k]);
+    } else {
+        for (int i = tid; i < ns * in; i += bd) {
+            const int jj = i / in, e = i - jj * in;
+            v[i] = ref_silu(D.g[(size_t)jj * D.stride + e]) * D.u[(size_t)jj * D.stride + e];
+        }
     }
     lds_barrier();
     for (int q = wave; q < ns * nb; q += nw) {
@@ -542,7 +705,7 @@ extern "C" __global__ void __launch_bounds__(256) oh_k_mv_q6k(oh_mvlaunch L) { m
 extern "C" __global__ void __launch_bounds__(256) oh_k_mv_q80(oh_mvlaunch L) { mv_body<OH_Q8_0>(L); }
 extern "C" __global__ void __launch_bounds__(256) oh_k_mv_mixed(oh_mvlaunch L) { mv_body<-1>(L); }
 
-extern "C" __global__ void __launch_bounds__(1024) oh_k_mv_down(oh_mvdown D) {
+extern "C" __global__ void __launch_bounds__(640) oh_k_mv_down(oh_mvdown D) {
     switch (D.type) {
     case OH_Q4_K: down_body<OH_Q4_K>(D); break;
     case OH_Q6_K: down_body<OH_Q6_K>(D); break;

@@ -74,16 +74,20 @@ OH_HD static inline int oh_qdot_can(uint32_t t, int64_t in) {
 // tensor applied in `nsub` slots: slot k uses rows [eidx[k]*rows, +rows) of a
 // stacked expert tensor (or the whole tensor when eidx is null), writes
 // y + k*ystride and reads its activation at slot offset k*astride.
-enum { OH_PRO_Q8K = 0, OH_PRO_NORM = 1, OH_PRO_SWIGLU = 2 };
+enum { OH_PRO_Q8K = 0, OH_PRO_NORM = 1, OH_PRO_SWIGLU = 2, OH_PRO_GNORM = 3, OH_PRO_F32 = 4 };
 typedef struct {
     const uint8_t *A, *B, *C;      // weight planes (expert 0 for a stacked tensor)
     // activation: OH_PRO_Q8K reads Q8_K planes (and xf for the f32 fallback);
     // OH_PRO_NORM RMS-normalises xf with nw/eps; OH_PRO_SWIGLU forms
-    // silu(xf)*xf2; both then quantise to Q8_K inside the block.
+    // silu(xf)*xf2; OH_PRO_GNORM RMS-normalises each gdim-element head of xf
+    // (sum of squares from xruns: one double per 64-element run) with nw/eps
+    // and multiplies by xf2 (= silu(gate)); OH_PRO_F32 takes xf as is; all
+    // four then quantise to Q8_K inside the block.
     const int8_t *xqs;
     const float *xd;
     const int16_t *xbs;
     const float *xf, *xf2, *nw;
+    const double *xruns;
     // OH_PRO_NORM / OH_PRO_SWIGLU: the segment's first block also stores the
     // activation it formed (Q8_K planes and f32) for later launches
     int8_t *oqs;
@@ -93,7 +97,7 @@ typedef struct {
     float *y;                      // output, row o of slot k -> y[k*ystride + o]
     const int32_t *eidx;           // stacked experts: slot k uses expert eidx[k]
     float eps;
-    int pro;
+    int pro, gdim;
     int type, nb, in, rows, mode;  // mode 0: y = dot, 1: y += dot
     int nsub, ystride, astride;
     int units;                     // wave work units per slot
@@ -105,17 +109,16 @@ typedef struct {
 #define OH_MAX_SEGS 8
 #define OH_MV_WAVES 4              // waves per matvec block
 #define OH_MV_R 4                  // steps per prefetch batch of a wave
-// Launch epilogue: OH_EP_ROUTE makes the last block to finish run the MoE
-// router top-k over y of segment 0 (logits) and the shared-expert gate logit
-// of segment 1 (when present).
-enum { OH_EP_NONE = 0, OH_EP_ROUTE = 1 };
+// A launch with `route` set first routes the MoE in every block: top-k over
+// the ne router logits rlog (plus the shared-expert gate logit shl, when
+// non-null); stacked segments then use the routed experts, and block 0 stores
+// the routing (ridx, rw, shg) for later launches.
 typedef struct {
     oh_mvseg s[OH_MAX_SEGS];
     int n;
     int total_blocks;
-    int ep;
-    int *cnt;                      // completion counter (zero between launches)
-    const float *rlog, *shl;       // router logits, shared-expert gate logit (or null)
+    int route;
+    const float *rlog, *shl;
     int ne, topk;
     int32_t *ridx;
     float *rw, *shg;

@@ -47,7 +47,7 @@ def test_profile_step_reports_every_launch(hip_ctx):
     kinds = [k for k, _, _ in rec]
     # per layer: input projections, output projection, router (+ routing),
     # experts gate/up, fused down + combine; then lm_head
-    assert kinds.count("matvec") == 4 * 4 + 1 and kinds.count("moe_down") == 4
+    assert sum(k.startswith("matvec") for k in kinds) == 4 * 4 + 1 and kinds.count("moe_down") == 4
     assert kinds.count("delta_step") == 3 and kinds.count("argmax") == 1
     assert "rmsnorm_q8k" not in kinds and "moe_route" not in kinds and "moe_combine" not in kinds
     assert all(ms > 0 for _, _, ms in rec) and s.pos == 5
