@@ -173,17 +173,24 @@ OH_DEV int row16_sum_i(int v) {
     v += dpp_i<0xB1>(v); v += dpp_i<0x4E>(v); v += dpp_i<0x141>(v); v += dpp_i<0x140>(v);
     return v;
 }
+// wave-wide max / min: DPP within each 16-lane row, then the four rows'
+// results read out as scalars (uniform in every lane)
 OH_DEV float wave_max_fast(float v) {
     v = fmaxf(v, dpp_f<0xB1>(v)); v = fmaxf(v, dpp_f<0x4E>(v));
     v = fmaxf(v, dpp_f<0x141>(v)); v = fmaxf(v, dpp_f<0x140>(v));
-    v = fmaxf(v, shfl_xor(v, 16)); v = fmaxf(v, shfl_xor(v, 32));
-    return v;
+    const int iv = __float_as_int(v);
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(iv, 0));
+    const float r1 = __int_as_float(__builtin_amdgcn_readlane(iv, 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(iv, 32));
+    const float r3 = __int_as_float(__builtin_amdgcn_readlane(iv, 48));
+    return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
 }
 OH_DEV int wave_min_fast(int v) {
     v = min(v, dpp_i<0xB1>(v)); v = min(v, dpp_i<0x4E>(v));
     v = min(v, dpp_i<0x141>(v)); v = min(v, dpp_i<0x140>(v));
-    v = min(v, shfl_xor(v, 16)); v = min(v, shfl_xor(v, 32));
-    return v;
+    const int r0 = __builtin_amdgcn_readlane(v, 0), r1 = __builtin_amdgcn_readlane(v, 16);
+    const int r2 = __builtin_amdgcn_readlane(v, 32), r3 = __builtin_amdgcn_readlane(v, 48);
+    return min(min(r0, r1), min(r2, r3));
 }
 
 // signed 8-bit dot of four packed bytes, accumulated into c (exact integers)

@@ -342,6 +342,26 @@ static int mv_add(MvBuild &b, const ornith_hip_tensor *W, const Act &act, float 
     return ORNITH_HIP_OK;
 }
 
+// gate/up pair: one segment reducing W and W2 (same type and shape) against
+// the same activation, emitting silu(W.x) * (W2.x)
+static bool pairable(const ornith_hip_tensor *W, const ornith_hip_tensor *W2) {
+    return W && W2 && W->type == W2->type && W->in == W2->in && W->rows == W2->rows &&
+           oh_qdot_can(W->type, W->in) && W->nd == W2->nd;
+}
+static int mv_add_pair(MvBuild &b, const ornith_hip_tensor *W, const ornith_hip_tensor *W2, const Act &act,
+                       float *y, const int32_t *eidx = nullptr, int nsub = 1, int ystride = 0) {
+    if (!pairable(W, W2) || (!act.qs && act.pro == OH_PRO_Q8K)) {
+        seterr("matvec pair '%s': unsupported", W->name.c_str());
+        return ORNITH_HIP_ERR_UNSUPPORTED;
+    }
+    CHK(mv_add(b, W, act, y, 0, eidx, nsub, ystride, 0));
+    oh_mvseg &s = b.L.s[b.L.n - 1];
+    s.A2 = W2->A; s.B2 = W2->B; s.C2 = W2->C;
+    s.pair = 1;
+    b.bytes += (double)nsub * (double)s.rows * (double)gguf_nbytes(W2->type, (uint64_t)W2->in);
+    return ORNITH_HIP_OK;
+}
+
 // Lay the segments out over blocks: every wave gets a run of whole wave
 // steps sized so the launch spreads over ~4096 waves (16 per CU).
 static void mv_plan(MvBuild &b) {
@@ -350,7 +370,7 @@ static void mv_plan(MvBuild &b) {
     for (int i = 0; i < b.L.n; i++) {
         const oh_mvseg &s = b.L.s[i];
         if (seg_q8(s)) {
-            steps += (int64_t)s.units * s.nsub;
+            steps += (int64_t)s.units * s.nsub * (s.pair ? 2 : 1);
             tk = tk == -2 || tk == s.type ? s.type : -1;
         } else {
             tk = -1;
@@ -364,7 +384,7 @@ static void mv_plan(MvBuild &b) {
         oh_mvseg &s = b.L.s[i];
         const bool q8 = seg_q8(s);
         if (q8) {
-            s.upw = (int)(spw > 0 ? spw : 1);
+            s.upw = (int)(spw / (s.pair ? 2 : 1) > 0 ? spw / (s.pair ? 2 : 1) : 1);
             s.bps = (s.units + OH_MV_WAVES * s.upw - 1) / (OH_MV_WAVES * s.upw);
         } else {
             s.upw = 1;
@@ -782,7 +802,8 @@ static int infer_arch(ornith_hip_model *m, const Meta &md) {
         if (y.full) {
             if (!y.q || !y.k || !y.v || !y.o || !need_f32(y.q_norm) || !need_f32(y.k_norm)) return bad("full-attention tensors missing or not F32 norms");
             if (a.hd != 64 && a.hd != 128 && a.hd != 256) return bad("head_dim must be 64, 128 or 256");
-            if (a.nh % a.nkv || a.nh / a.nkv > 16) return bad("query heads per KV head must divide and be <= 16");
+            if (a.nh % a.nkv || a.nh / a.nkv > 16 || (a.nh / a.nkv & (a.nh / a.nkv - 1)))
+                return bad("query heads per KV head must be a power of two <= 16");
             if (a.nkv < 1 || a.nh % a.nkv) return bad("n_heads must be a multiple of n_kv_heads");
             if ((a.nh * a.hd) % 256 || a.nh * a.hd > 8192) return bad("n_heads*head_dim must be a multiple of 256, <= 8192");
         } else {
@@ -1154,12 +1175,21 @@ static int enqueue_body(ornith_hip_session *s, hipStream_t st) {
             // experts gate/up: every block routes first (top-k + softmax), the
             // stacked segments then read the routed experts
             const Act ax = act_of(s->xq, s->xn);
+            // experts gate/up: every block routes first (top-k + softmax), the
+            // stacked segments then read the routed experts; gate and up rows
+            // are reduced together and emit h = silu(gate) * up
+            const bool paired = pairable(y.gate_exps, y.up_exps) && (!y.gate_sh || pairable(y.gate_sh, y.up_sh));
             MvBuild b2;
-            CHK(mv_add(b2, y.gate_exps, ax, s->g, 0, s->eidx, K, IW, 0));
-            CHK(mv_add(b2, y.up_exps, ax, s->u, 0, s->eidx, K, IW, 0));
-            if (y.gate_sh) {
-                CHK(mv_add(b2, y.gate_sh, ax, s->g + (size_t)K * IW, 0));
-                CHK(mv_add(b2, y.up_sh, ax, s->u + (size_t)K * IW, 0));
+            if (paired) {
+                CHK(mv_add_pair(b2, y.gate_exps, y.up_exps, ax, s->h, s->eidx, K, IW));
+                if (y.gate_sh) CHK(mv_add_pair(b2, y.gate_sh, y.up_sh, ax, s->h + (size_t)K * IW));
+            } else {
+                CHK(mv_add(b2, y.gate_exps, ax, s->g, 0, s->eidx, K, IW, 0));
+                CHK(mv_add(b2, y.up_exps, ax, s->u, 0, s->eidx, K, IW, 0));
+                if (y.gate_sh) {
+                    CHK(mv_add(b2, y.gate_sh, ax, s->g + (size_t)K * IW, 0));
+                    CHK(mv_add(b2, y.up_sh, ax, s->u + (size_t)K * IW, 0));
+                }
             }
             b2.L.route = 1;
             b2.L.rlog = s->rl;
@@ -1175,7 +1205,7 @@ static int enqueue_body(ornith_hip_session *s, hipStream_t st) {
             const int nbd = I / 256, ns = K + (y.gate_sh ? 1 : 0);
             const int rps = nbd >= 1 ? 64 / nbd : 1;
             const int sq = (nbd * 272 + nbd * 36 + 15) & ~15, dlds = ns * sq + ns * I * 4 + ns * rps * 4;
-            const bool fuse = oh_qdot_can(dt, I) && nbd >= 1 && nbd <= 64 && ns <= 10 && dlds <= 65536 &&
+            const bool fuse = paired && oh_qdot_can(dt, I) && nbd >= 1 && nbd <= 64 && ns <= 10 && dlds <= 65536 &&
                               (!y.gate_sh || (y.down_sh->type == dt && sI == I));
             if (fuse) {
                 oh_mvdown D;
@@ -1183,16 +1213,23 @@ static int enqueue_body(ornith_hip_session *s, hipStream_t st) {
                 D.A = y.down_exps->A; D.B = y.down_exps->B; D.C = y.down_exps->C;
                 if (y.gate_sh) { D.sA = y.down_sh->A; D.sB = y.down_sh->B; D.sC = y.down_sh->C; }
                 D.eidx = s->eidx; D.w = s->ew; D.shg = y.gate_inp_sh ? s->shg : nullptr;
-                D.g = s->g; D.u = s->u; D.x = s->x;
+                D.h = s->h; D.x = s->x;
                 D.type = (int)dt; D.nb = nbd; D.in = I; D.rows = H; D.k = K; D.stride = IW;
-                const double db = (double)ns * ((double)H * gguf_nbytes(dt, (uint64_t)I) + 8.0 * I) + 8.0 * H + 4.0 * K;
+                const double db = (double)ns * ((double)H * gguf_nbytes(dt, (uint64_t)I) + 4.0 * I) + 8.0 * H + 4.0 * K;
                 LAUNCH(K_MV_DOWN, db, oh_launch_mv_down(&D, (H + rps - 1) / rps, 64 * ns, dlds, st));
             } else {
                 MvBuild b3;
-                CHK(mv_add(b3, y.down_exps, act_swiglu(s->g, s->u), s->od, 0, s->eidx, K, H, IW));
-                if (y.gate_sh)
-                    CHK(mv_add(b3, y.down_sh, act_swiglu(s->g + (size_t)K * IW, s->u + (size_t)K * IW),
-                               s->od + (size_t)K * H, 0));
+                Act ah;
+                ah.pro = OH_PRO_F32;
+                ah.xf = s->h;
+                const Act a0 = paired ? ah : act_swiglu(s->g, s->u);
+                CHK(mv_add(b3, y.down_exps, a0, s->od, 0, s->eidx, K, H, IW));
+                if (y.gate_sh) {
+                    Act a1 = a0;
+                    a1.xf = a0.xf + (size_t)K * IW;
+                    if (!paired) a1.xf2 = a0.xf2 + (size_t)K * IW;
+                    CHK(mv_add(b3, y.down_sh, a1, s->od + (size_t)K * H, 0));
+                }
                 MVGO(b3);
                 LAUNCH(K_COMBINE, 4.0 * H * (ns + 2),
                        oh_launch_moe_combine(s->x, s->od, s->ew, K, H, y.gate_sh ? s->od + (size_t)K * H : nullptr,
@@ -1200,11 +1237,19 @@ static int enqueue_body(ornith_hip_session *s, hipStream_t st) {
             }
         } else {
             MvBuild b;
-            CHK(mv_add(b, y.ffn_gate, pn, s->g, 0));
-            CHK(mv_add(b, y.ffn_up, pn, s->u, 0));
+            const bool paired = pairable(y.ffn_gate, y.ffn_up);
+            if (paired) {
+                CHK(mv_add_pair(b, y.ffn_gate, y.ffn_up, pn, s->h));
+            } else {
+                CHK(mv_add(b, y.ffn_gate, pn, s->g, 0));
+                CHK(mv_add(b, y.ffn_up, pn, s->u, 0));
+            }
             MVGO(b);
             MvBuild b2;
-            CHK(mv_add(b2, y.ffn_down, act_swiglu(s->g, s->u), s->x, 1));
+            Act ah;
+            ah.pro = OH_PRO_F32;
+            ah.xf = s->h;
+            CHK(mv_add(b2, y.ffn_down, paired ? ah : act_swiglu(s->g, s->u), s->x, 1));
             MVGO(b2);
         }
     }

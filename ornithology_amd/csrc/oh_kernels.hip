@@ -92,9 +92,12 @@ hipError_t oh_launch_attn_out(const float *scores, const int8_t *Vq, const float
     return hipGetLastError();
 }
 
+// query heads per flash block: two (one when the group has a single head)
+static int flash_hb(int nh, int nkv) { return nh / nkv >= 2 ? 2 : 1; }
+
 int oh_flash_lds_bytes(int nh, int nkv, int hd) {
-    const int G = nh / nkv;
-    return G * hd * 4 + kFlashCh * (hd / 4 + 1) * 4 + 16 + (kFlashCh / 16) * hd * 16 + G * kFlashCh * 4 +
+    const int HB = flash_hb(nh, nkv);
+    return HB * (hd + 16) * 4 + kFlashCh * (hd / 4 + 1) * 4 + 16 + (kFlashCh / 16) * hd * 16 + HB * kFlashCh * 4 +
            2 * kFlashCh * 4;
 }
 int oh_flash_chunk(void) { return kFlashCh; }
@@ -102,7 +105,10 @@ int oh_flash_chunk(void) { return kFlashCh; }
 hipError_t oh_launch_attn_flash(const float *qr, const uint32_t *Kt, const float *Ks, const int8_t *Vq,
                                 const float *Vs, float *part_o, float *part_ml, const int32_t *io_pos,
                                 int nh, int nkv, int hd, int cap, float scale, int exact_max, hipStream_t st) {
-    hipLaunchKernelGGL(oh_k_attn_flash, dim3(nkv, (cap + kFlashCh - 1) / kFlashCh), dim3(256),
+    const int HB = flash_hb(nh, nkv), G = nh / nkv;
+    void (*k)(const float *, const uint32_t *, const float *, const int8_t *, const float *, float *, float *,
+              const int32_t *, int, int, int, int, float, int) = HB == 2 ? oh_k_attn_flash<2> : oh_k_attn_flash<1>;
+    hipLaunchKernelGGL(k, dim3(nkv * (G / HB), (cap + kFlashCh - 1) / kFlashCh), dim3(256),
                        (size_t)oh_flash_lds_bytes(nh, nkv, hd), st, qr, Kt, Ks, Vq, Vs, part_o, part_ml, io_pos,
                        nh, nkv, hd, cap, scale, exact_max);
     return hipGetLastError();

@@ -94,9 +94,12 @@ oh_k_delta_step(const float *cat, const float *ab, const float *gate, const floa
                 float *conv_state, const float *ssm_a, const float *dt_bias, float *S, float *out,
                 float *out_gate, double *out_runs, const int32_t *io_pos, int nk, int nv, int K, int cc,
                 float out_scale) {
-    constexpr int KMAX = 8, NQ = DK / 64, TS = DK + 1;   // TS: padded LDS row (no bank conflicts)
+    // TS: LDS row stride padded by 4 floats; with 16-byte accesses every
+    // 16-lane pass of a row-per-lane walk and of a coalesced row copy covers
+    // all 64 banks once
+    constexpr int KMAX = 8, NQ = DK / 64, TS = DK + 4;
     __shared__ float qn[DK], kn[DK];
-    __shared__ float tile[64 * TS];
+    __shared__ __align__(16) float tile[64 * TS];
     const int lane = (int)threadIdx.x;
     const int hv = (int)blockIdx.x / NQ, slab = (int)blockIdx.x % NQ;
     const int r = slab * 64 + lane, kh = hv % nk, qd = nk * DK;
@@ -176,15 +179,20 @@ oh_k_delta_step(const float *cat, const float *ab, const float *gate, const floa
 #pragma unroll
     for (int i = 0; i < DK / 4; i++) {
         const int f = lane + 64 * i, row = (4 * f) / DK, col = (4 * f) % DK;
-        float *t = tile + row * TS + col;
-        t[0] = st[i].x; t[1] = st[i].y; t[2] = st[i].z; t[3] = st[i].w;
+        *(float4 *)(tile + row * TS + col) = make_float4(st[i].x, st[i].y, st[i].z, st[i].w);
     }
     __syncthreads();
 
     float *tr = tile + lane * TS;
     float s[DK];
 #pragma unroll
-    for (int c = 0; c < DK; c++) s[c] = tr[c] * alpha;
+    for (int c = 0; c < DK / 4; c++) {
+        const float4 v = *(const float4 *)(tr + 4 * c);
+        s[4 * c + 0] = v.x * alpha;
+        s[4 * c + 1] = v.y * alpha;
+        s[4 * c + 2] = v.z * alpha;
+        s[4 * c + 3] = v.w * alpha;
+    }
     float sk = 0.0f;
 #pragma unroll
     for (int c = 0; c < DK; c++) sk += s[c] * kn[c];
@@ -195,14 +203,13 @@ oh_k_delta_step(const float *cat, const float *ab, const float *gate, const floa
 #pragma unroll
     for (int c = 0; c < DK; c++) o += s[c] * qn[c];
 #pragma unroll
-    for (int c = 0; c < DK; c++) tr[c] = s[c];
+    for (int c = 0; c < DK / 4; c++) *(float4 *)(tr + 4 * c) = make_float4(s[4 * c], s[4 * c + 1], s[4 * c + 2], s[4 * c + 3]);
     __syncthreads();
     float4 *Sw = (float4 *)(S + ((size_t)hv * DK + slab * 64) * DK);
 #pragma unroll
     for (int i = 0; i < DK / 4; i++) {
         const int f = lane + 64 * i, row = (4 * f) / DK, col = (4 * f) % DK;
-        const float *t = tile + row * TS + col;
-        Sw[f] = make_float4(t[0], t[1], t[2], t[3]);
+        Sw[f] = *(const float4 *)(tile + row * TS + col);
     }
     // the gated RMSNorm's inputs for the consumer: o, silu(gate) and the
     // butterfly double sum of o^2 over this wave's 64 rows
@@ -406,23 +413,32 @@ oh_k_attn_out(const float *scores, const int8_t *Vq, const float *Vs, const floa
 // parity), and reads each KV byte once per group instead of once per head.
 constexpr int kFlashCh = 64;
 
-extern "C" __global__ void __launch_bounds__(256)
+// HB query heads of one KV head per block (compile time: the loops over heads
+// unroll); grid (nkv * (G/HB), chunks) with G = nh/nkv.
+template <int HB>
+__global__ void __launch_bounds__(256)
 oh_k_attn_flash(const float *qr, const uint32_t *Kt, const float *Ks, const int8_t *Vq, const float *Vs,
                 float *part_o, float *part_ml, const int32_t *io_pos, int nh, int nkv, int hd, int cap,
                 float scale, int exact_max) {
     extern __shared__ __align__(16) uint8_t fsm[];
     const int T = *io_pos + 1;
-    const int g = (int)blockIdx.x, c = (int)blockIdx.y, t0 = c * kFlashCh;
+    const int G = nh / nkv, ngb = G / HB;
+    const int g = (int)blockIdx.x / ngb, hb0 = ((int)blockIdx.x % ngb) * HB;
+    const int c = (int)blockIdx.y, t0 = c * kFlashCh;
     if (T <= exact_max || t0 >= T) return;
-    const int G = nh / nkv, tid = (int)threadIdx.x, hw = hd / 4, kst = hw + 1;
+    const int tid = (int)threadIdx.x, hw = hd / 4, kst = hw + 1;
     const int nchmax = (cap + kFlashCh - 1) / kFlashCh;
-    float *q = (float *)fsm;                                  // [G][hd]
-    uint32_t *kc = (uint32_t *)(q + G * hd);                  // [64][hw + 1]
+    const int qst = hd + 16;                                  // head stride: quarters padded by a float4
+    float *q = (float *)fsm;                                  // [HB][4][hd/4 + 4]
+    uint32_t *kc = (uint32_t *)(q + HB * qst);                // [64][hw + 1]
     uint4 *vt = (uint4 *)(((uintptr_t)(kc + kFlashCh * kst) + 15) & ~(uintptr_t)15);   // [4][hd]
-    float *pp = (float *)(vt + (kFlashCh / 16) * hd);         // [G][64]
-    float *ks = pp + G * kFlashCh, *vs = ks + kFlashCh;       // [64] each
-    // loads: query heads of the group, the chunk's key words, value tiles, scales
-    for (int k = tid; k < G * hd; k += 256) q[k] = qr[(size_t)g * G * hd + k];
+    float *pp = (float *)(vt + (kFlashCh / 16) * hd);         // [HB][64]
+    float *ks = pp + HB * kFlashCh, *vs = ks + kFlashCh;      // [64] each
+    // loads: the block's query heads, the chunk's key words, value tiles, scales
+    for (int k = tid; k < HB * hd; k += 256) {
+        const int h = k / hd, e = k % hd, qq = e / (hd / 4);
+        q[h * qst + qq * (hd / 4 + 4) + e % (hd / 4)] = qr[((size_t)g * G + hb0) * hd + k];
+    }
     for (int k = tid; k < hw * kFlashCh; k += 256) {
         const int w = k / kFlashCh, j = k % kFlashCh;
         const int t = t0 + j < T ? t0 + j : T - 1;
@@ -439,55 +455,94 @@ oh_k_attn_flash(const float *qr, const uint32_t *Kt, const float *Ks, const int8
         vs[tid] = Vs[(size_t)t * nkv + g];
     }
     __syncthreads();
-    // scores of (head h, position j)
-    for (int pr = tid; pr < G * kFlashCh; pr += 256) {
-        const int h = pr / kFlashCh, j = pr % kFlashCh;
-        const float4 *qh = (const float4 *)(q + h * hd);
-        const uint32_t *kj = kc + j * kst;
-        float acc = 0.0f;
-        for (int w = 0; w < hw; w++) {
-            const float4 qv = qh[w];
+    // scores: thread -> (position j, quarter of the head dimension), the HB
+    // heads against its key codes; the quarters are summed with DPP
+    {
+        const int q4 = tid & 3, j = tid >> 2, wq = hw / 4;
+        const uint32_t *kj = kc + j * kst + q4 * wq;
+        const float4 *q4p = (const float4 *)(q + q4 * (hd / 4 + 4));
+        float acc[HB];
+#pragma unroll
+        for (int h = 0; h < HB; h++) acc[h] = 0.0f;
+#pragma unroll 4
+        for (int w = 0; w < wq; w++) {
             const uint32_t wd = kj[w];
-            acc = fmaf(qv.x, (float)(int8_t)(wd & 0xff), acc);
-            acc = fmaf(qv.y, (float)(int8_t)((wd >> 8) & 0xff), acc);
-            acc = fmaf(qv.z, (float)(int8_t)((wd >> 16) & 0xff), acc);
-            acc = fmaf(qv.w, (float)(int8_t)(wd >> 24), acc);
+            const float c0 = (float)(int8_t)(wd & 0xff), c1 = (float)(int8_t)((wd >> 8) & 0xff);
+            const float c2 = (float)(int8_t)((wd >> 16) & 0xff), c3 = (float)(int8_t)(wd >> 24);
+#pragma unroll
+            for (int h = 0; h < HB; h++) {
+                const float4 qv = q4p[h * (qst / 4) + w];
+                acc[h] = fmaf(qv.x, c0, acc[h]);
+                acc[h] = fmaf(qv.y, c1, acc[h]);
+                acc[h] = fmaf(qv.z, c2, acc[h]);
+                acc[h] = fmaf(qv.w, c3, acc[h]);
+            }
         }
-        const float sc = ks[j] == 0.0f ? 0.0f : acc * ks[j] * scale;
-        pp[pr] = t0 + j < T ? sc : -INFINITY;
+        const float kss = ks[j];
+        const bool valid = t0 + j < T;
+#pragma unroll
+        for (int h = 0; h < HB; h++) {
+            float v = acc[h];
+            v += dpp_f<0xB1>(v);
+            v += dpp_f<0x4E>(v);
+            if (q4 == 0) {
+                const float sc = kss == 0.0f ? 0.0f : v * kss * scale;
+                pp[h * kFlashCh + j] = valid ? sc : -INFINITY;
+            }
+        }
     }
     __syncthreads();
     // per-head chunk statistics: a wave per head, a lane per position
     const int wave = tid >> 6, lane = tid & 63;
-    for (int h = wave; h < G; h += 4) {
-        const float sv = pp[h * kFlashCh + lane];
-        const float m = wave_max_fast(sv);
-        const float e = sv == -INFINITY ? 0.0f : __expf(sv - m);
-        float l = e;
-        for (int mm = 32; mm >= 1; mm >>= 1) l += shfl_xor(l, mm);
-        pp[h * kFlashCh + lane] = e * vs[lane];
-        if (lane == 0) {
-            float *ml = part_ml + (((size_t)g * nchmax + c) * G + h) * 2;
-            ml[0] = m;
-            ml[1] = l;
+#pragma unroll
+    for (int h0 = 0; h0 < HB; h0 += 4) {
+        const int h = h0 + wave;
+        if (h < HB) {
+            const float sv = pp[h * kFlashCh + lane];
+            const float m = wave_max_fast(sv);
+            const float e = sv == -INFINITY ? 0.0f : __expf(sv - m);
+            float l = e;
+            for (int mm = 32; mm >= 1; mm >>= 1) l += shfl_xor(l, mm);
+            pp[h * kFlashCh + lane] = e * vs[lane];
+            if (lane == 0) {
+                float *ml = part_ml + (((size_t)g * nchmax + c) * G + hb0 + h) * 2;
+                ml[0] = m;
+                ml[1] = l;
+            }
         }
     }
     __syncthreads();
-    // unnormalised outputs: thread -> dimension i, every head of the group
-    for (int k = tid; k < G * hd; k += 256) {
-        const int h = k / hd, i = k % hd;
-        const float *ph = pp + h * kFlashCh;
-        float o = 0.0f;
+    // unnormalised outputs: thread -> (dimension i, head h1 + hs*k)
+    {
+        const int i = tid % hd, hs = 256 / hd, h1 = tid / hd;
+        float o[HB];
+#pragma unroll
+        for (int k = 0; k < HB; k++) o[k] = 0.0f;
+        const float4 *pp4 = (const float4 *)pp;
 #pragma unroll
         for (int tt = 0; tt < kFlashCh / 16; tt++) {
             const uint4 cw = vt[tt * hd + i];
 #pragma unroll
-            for (int j = 0; j < 16; j++) {
-                const int8_t cv = (int8_t)(wsel(cw, j >> 2) >> (8 * (j & 3)));
-                o = fmaf(ph[tt * 16 + j], (float)cv, o);
+            for (int j4 = 0; j4 < 4; j4++) {
+                const uint32_t wd = wsel(cw, j4);
+                const float c0 = (float)(int8_t)(wd & 0xff), c1 = (float)(int8_t)((wd >> 8) & 0xff);
+                const float c2 = (float)(int8_t)((wd >> 16) & 0xff), c3 = (float)(int8_t)(wd >> 24);
+#pragma unroll
+                for (int k = 0; k < HB; k++) {
+                    const int h = h1 + hs * k < HB ? h1 + hs * k : HB - 1;
+                    const float4 pv = pp4[(h * kFlashCh + tt * 16 + 4 * j4) / 4];
+                    o[k] = fmaf(pv.x, c0, o[k]);
+                    o[k] = fmaf(pv.y, c1, o[k]);
+                    o[k] = fmaf(pv.z, c2, o[k]);
+                    o[k] = fmaf(pv.w, c3, o[k]);
+                }
             }
         }
-        part_o[(((size_t)g * nchmax + c) * G + h) * hd + i] = o;
+#pragma unroll
+        for (int k = 0; k < HB; k++) {
+            const int h = h1 + hs * k;
+            if (h < HB) part_o[(((size_t)g * nchmax + c) * G + hb0 + h) * hd + i] = o[k];
+        }
     }
 }
 

@@ -100,6 +100,67 @@ OH_DEV void q8k_block_from_lds(const float *v, int qb, int8_t *qs, float *d, int
     if (lane == 0) d[qb] = 1.0f / iscale;
 }
 
+// Q8_K of the blocks qb0, qb0 + qstep, ... (< nb, at most N of them) of v by
+// one wave, the N blocks' reductions interleaved. Same result per block as
+// q8k_block_from_lds.
+template <int N>
+OH_DEV void q8k_blocks(const float *v, int qb0, int qstep, int nb, int8_t *qs, float *d, int16_t *bs,
+                       int qstride = 256) {
+    const int lane = lane_id();
+    float a[N][4], best[N];
+    int bi[N];
+#pragma unroll
+    for (int n = 0; n < N; n++) {
+        const int qb = qb0 + n * qstep < nb ? qb0 + n * qstep : nb - 1;
+#pragma unroll
+        for (int k = 0; k < 4; k++) a[n][k] = fabsf(v[qb * 256 + lane + 64 * k]);
+        best[n] = fmaxf(fmaxf(a[n][0], a[n][1]), fmaxf(a[n][2], a[n][3]));
+    }
+#pragma unroll
+    for (int n = 0; n < N; n++) best[n] = wave_max_fast(best[n]);
+#pragma unroll
+    for (int n = 0; n < N; n++) {
+        bi[n] = 256;
+#pragma unroll
+        for (int k = 3; k >= 0; k--) if (a[n][k] == best[n]) bi[n] = lane + 64 * k;
+    }
+#pragma unroll
+    for (int n = 0; n < N; n++) bi[n] = wave_min_fast(bi[n]);
+#pragma unroll
+    for (int n = 0; n < N; n++) {
+        const int qb = qb0 + n * qstep;
+        if (qb >= nb) break;
+        const float *xb = v + qb * 256;
+        int8_t *q = qs + (int64_t)qb * qstride;
+        int16_t *b = bs + (int64_t)qb * 16;
+        if (best[n] == 0.0f || !(best[n] > 0.0f)) {
+#pragma unroll
+            for (int k = 0; k < 4; k++) q[lane + 64 * k] = 0;
+            if (lane < 16) b[lane] = 0;
+            if (lane == 0) d[qb] = 0.0f;
+            continue;
+        }
+        const float iscale = -127.0f / xb[bi[n]];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int e = lane + 64 * k;
+            float r = __builtin_rintf(iscale * xb[e]);
+            int c = (int)r;
+            c = c > 127 ? 127 : (c < -128 ? -128 : c);
+            q[e] = (int8_t)c;
+            const int sv = row16_sum_i(c);
+            if ((lane & 15) == 0) b[4 * k + (lane >> 4)] = (int16_t)sv;
+        }
+        if (lane == 0) d[qb] = 1.0f / iscale;
+    }
+}
+
+// Q8_K of all nb blocks of v by the 4 waves of a block
+OH_DEV void q8k_all(const float *v, int nb, int8_t *qs, float *d, int16_t *bs, int qstride) {
+    const int wave = (int)(threadIdx.x >> 6);
+    for (int q0 = wave; q0 < nb; q0 += 16) q8k_blocks<4>(v, q0, 4, nb, qs, d, bs, qstride);
+}
+
 // In-place RMSNorm of v[0..n) in LDS (src/ornith_tensor.c:100-106): sum of
 // squares in double (tree-ordered), inv = (float)(1/sqrt(ss/n+eps)),
 // v_i = v_i * inv * w_i. All 256 threads; v must be visible block-wide.
@@ -380,7 +441,7 @@ OH_DEV void mv_prologue(const oh_mvseg &s, int slot, int blk, uint8_t *smem, dou
 // first weight step, and the prologue consumes them while that step is still
 // in flight (vector loads complete in order, so inputs loaded after the
 // weights would wait for them).
-struct PIn { float4 a[4], b[4], c[4]; int4 q, bsv; float d; };
+struct PIn { float4 a[4], b[4], c[4]; int4 q, bsv; float d; double r0, r1; };
 
 OH_DEV void pro_load(PIn &p, const oh_mvseg &s, int slot) {
     const int tid = (int)threadIdx.x, in = s.in, nb = in / 256;
@@ -401,11 +462,56 @@ OH_DEV void pro_load(PIn &p, const oh_mvseg &s, int slot) {
             p.b[k] = w[i];
             if (s.pro == OH_PRO_GNORM) p.c[k] = ((const float4 *)s.nw)[i % (s.gdim / 4)];
         }
+        if (s.pro == OH_PRO_GNORM) {
+            // this thread's head (tid < in/gdim): its first two run sums
+            const int rpg = s.gdim / 64, nh = in / s.gdim, h = tid < nh ? tid : nh - 1;
+            p.r0 = s.xruns[h * rpg];
+            p.r1 = s.xruns[h * rpg + (rpg > 1 ? 1 : 0)];
+        }
     }
 }
 
 OH_DEV float4 f4_silu_mul(const float4 g, const float4 u) {
     return make_float4(ref_silu(g.x) * u.x, ref_silu(g.y) * u.y, ref_silu(g.z) * u.z, ref_silu(g.w) * u.w);
+}
+
+// Q8_K of one 256-element block held in registers by a wave, four
+// consecutive elements x per lane (lane l: elements 4l..4l+3). Same result as
+// q8k_block_from_lds; codes are written as one packed word per lane.
+OH_DEV void q8k_regs(const float4 x, int qb, int8_t *qs, float *d, int16_t *bs, int qstride) {
+    const int lane = lane_id();
+    const float a0 = fabsf(x.x), a1 = fabsf(x.y), a2 = fabsf(x.z), a3 = fabsf(x.w);
+    const float best = wave_max_fast(fmaxf(fmaxf(a0, a1), fmaxf(a2, a3)));
+    int bi = 256;
+    if (a3 == best) bi = 4 * lane + 3;
+    if (a2 == best) bi = 4 * lane + 2;
+    if (a1 == best) bi = 4 * lane + 1;
+    if (a0 == best) bi = 4 * lane;
+    bi = wave_min_fast(bi);
+    int *qw = (int *)(qs + (int64_t)qb * qstride) + lane;
+    int16_t *b = bs + (int64_t)qb * 16;
+    if (best == 0.0f || !(best > 0.0f)) {
+        *qw = 0;
+        if (lane < 16) b[lane] = 0;
+        if (lane == 0) d[qb] = 0.0f;
+        return;
+    }
+    const int sel = bi & 3;
+    const float mine = sel == 0 ? x.x : (sel == 1 ? x.y : (sel == 2 ? x.z : x.w));
+    const float iscale = -127.0f / shfl(mine, bi >> 2);
+    int c[4];
+    const float xs[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int v = (int)__builtin_rintf(iscale * xs[j]);
+        c[j] = v > 127 ? 127 : (v < -128 ? -128 : v);
+    }
+    *qw = (c[0] & 0xff) | ((c[1] & 0xff) << 8) | ((c[2] & 0xff) << 16) | ((c[3] & 0xff) << 24);
+    int sv = c[0] + c[1] + c[2] + c[3];
+    sv += dpp_i<0xB1>(sv);
+    sv += dpp_i<0x4E>(sv);                         // codes 16*(lane/4) .. +15
+    if ((lane & 3) == 0) b[lane >> 2] = (int16_t)sv;
+    if (lane == 0) d[qb] = 1.0f / iscale;
 }
 
 OH_DEV void pro_compute(const PIn &p, const oh_mvseg &s, int slot, int blk, uint8_t *smem, double *red) {
@@ -423,35 +529,40 @@ OH_DEV void pro_compute(const PIn &p, const oh_mvseg &s, int slot, int blk, uint
         lds_barrier();
         return;
     }
+    // the activation in registers: thread tid owns float4 tid + 256k, i.e.
+    // elements 4*lane.. of super-block wave + 4k
     const int n4 = in / 4;
+    float4 fv[4];
 #pragma unroll
-    for (int k = 0; k < 4; k++)
-        if (tid + 256 * k < n4) v4[tid + 256 * k] = s.pro == OH_PRO_SWIGLU ? f4_silu_mul(p.a[k], p.b[k]) : p.a[k];
-    lds_barrier();
+    for (int k = 0; k < 4; k++) fv[k] = s.pro == OH_PRO_SWIGLU ? f4_silu_mul(p.a[k], p.b[k]) : p.a[k];
     if (s.pro == OH_PRO_GNORM) {
         // per head of gdim elements (src/ornith_rforward.c:300-319): the runs'
         // double sums of squares added in order, inv = 1/sqrt(ss/gdim + eps),
         // v = v * inv * w * silu(z)
-        float *hinv = v + in;                       // [in/gdim]
+        float *hinv = v;                            // [in/gdim]
         const int gd = s.gdim, rpg = gd / 64;
         if (tid < in / gd) {
-            double tot = s.xruns[tid * rpg];
-            for (int k = 1; k < rpg; k++) tot += s.xruns[tid * rpg + k];
+            double tot = p.r0;
+            if (rpg > 1) tot += p.r1;
+            for (int k = 2; k < rpg; k++) tot += s.xruns[tid * rpg + k];
             hinv[tid] = (float)(1.0 / sqrt(tot / (double)gd + (double)s.eps));
         }
         lds_barrier();
 #pragma unroll
-        for (int k = 0; k < 4; k++)
-            if (tid + 256 * k < n4) {
-                const float inv = hinv[4 * (tid + 256 * k) / gd];
-                const float4 x = p.a[k], z = p.b[k], w = p.c[k];
-                v4[tid + 256 * k] = make_float4(x.x * inv * w.x * z.x, x.y * inv * w.y * z.y,
-                                                x.z * inv * w.z * z.z, x.w * inv * w.w * z.w);
-            }
-        lds_barrier();
+        for (int k = 0; k < 4; k++) {
+            const int f = tid + 256 * k < n4 ? tid + 256 * k : n4 - 1;
+            const float inv = hinv[4 * f / gd];
+            const float4 x = p.a[k], z = p.b[k], w = p.c[k];
+            fv[k] = make_float4(x.x * inv * w.x * z.x, x.y * inv * w.y * z.y, x.z * inv * w.z * z.z,
+                                x.w * inv * w.w * z.w);
+        }
     }
     if (s.pro == OH_PRO_NORM) {
         // same summation order as the stand-alone RMSNorm kernel
+#pragma unroll
+        for (int k = 0; k < 4; k++)
+            if (tid + 256 * k < n4) v4[tid + 256 * k] = fv[k];
+        lds_barrier();
         double ss = 0.0;
         for (int i = tid; i < in; i += 256) ss += (double)v[i] * v[i];
         ss = wave_sum_d(ss);
@@ -460,19 +571,20 @@ OH_DEV void pro_compute(const PIn &p, const oh_mvseg &s, int slot, int blk, uint
         const double tot = (red[0] + red[1]) + (red[2] + red[3]);
         const float inv = (float)(1.0 / sqrt(tot / (double)in + (double)s.eps));
 #pragma unroll
-        for (int k = 0; k < 4; k++)
-            if (tid + 256 * k < n4) {
-                const float4 x = p.a[k], w = p.b[k];
-                v4[tid + 256 * k] = make_float4(x.x * inv * w.x, x.y * inv * w.y, x.z * inv * w.z, x.w * inv * w.w);
-            }
-        lds_barrier();
+        for (int k = 0; k < 4; k++) {
+            const float4 x = p.a[k], w = p.b[k];
+            fv[k] = make_float4(x.x * inv * w.x, x.y * inv * w.y, x.z * inv * w.z, x.w * inv * w.w);
+        }
     }
     const bool store = blk == 0 && s.oqs != nullptr;
-    if (blk == 0 && s.oxf)
-        for (int i = tid; i < in; i += 256) s.oxf[ao + i] = v[i];
-    for (int qb = wave; qb < nb; qb += 4) {
-        q8k_block_from_lds(v, qb, aqs, ad, abs, kAS);
-        if (store) q8k_block_from_lds(v, qb, s.oqs + ao, s.oqd + ao / 256, s.oqb + ao / 16);
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const int qb = wave + 4 * k;
+        if (qb < nb) {
+            if (blk == 0 && s.oxf) ((float4 *)(s.oxf + ao))[tid + 256 * k] = fv[k];
+            q8k_regs(fv[k], qb, aqs, ad, abs, kAS);
+            if (store) q8k_regs(fv[k], qb, s.oqs + ao, s.oqd + ao / 256, s.oqb + ao / 16, 256);
+        }
     }
     lds_barrier();
 }
@@ -490,30 +602,39 @@ OH_DEV void mv_seg(const oh_mvseg &s, int slot, int blk, int expert, uint8_t *sm
     const int rl = lane / nb, sb = lane - rl * nb;
     const int u0 = (blk * OH_MV_WAVES + wave) * s.upw;
     const int u1 = u0 + s.upw < s.units ? u0 + s.upw : s.units;
-    const int S = u1 > u0 ? u1 - u0 : 0;
+    // paired segments: step 2u reduces W, step 2u+1 the pair W2, same rows
+    const int sps = s.pair ? 2 : 1;
+    const int S = u1 > u0 ? (u1 - u0) * sps : 0;
     const int64_t row_base = (int64_t)expert * s.rows;
     float *y = s.y + (size_t)slot * s.ystride;
-    const WP wp = {s.A, s.B, s.C};
+    const WP wp = {s.A, s.B, s.C}, wp2 = {s.A2, s.B2, s.C2};
     const int8_t *aq = (const int8_t *)smem + sb * kAS;
     const int16_t *abs = (const int16_t *)(smem + mv_lds_bs_off(nb)) + sb * 16;
     const float *adp = (const float *)(smem + mv_lds_d_off(nb)) + sb;
     SB<T> ra, rb;
     auto load = [&](SB<T> &r, int st) {
-        int unit = u0 + (st < S ? st : S - 1);
+        const int sc = st < S ? st : S - 1;
+        int unit = u0 + sc / sps;
         unit = unit < 0 ? 0 : (unit >= s.units ? s.units - 1 : unit);
         const int row = unit * rps + (rl < rps ? rl : rps - 1);
         const int rowc = row < s.rows ? row : s.rows - 1;
-        sb_load(r, wp, (row_base + rowc) * nb + sb);
+        sb_load(r, (sc & (sps - 1)) ? wp2 : wp, (row_base + rowc) * nb + sb);
     };
+    float gsum = 0.0f;
     auto comp = [&](const SB<T> &r, int st) {
-        const int row = (u0 + st) * rps + rl;
+        const int row = (u0 + st / sps) * rps + rl;
         const bool live = st < S && rl < rps && row < s.rows;
         const float tw = sb_term(r, aq, abs, *adp);
         const float t = live ? tw : 0.0f;
         // the row's super-block terms in order, from 0 (lanes rl*nb .. +nb-1)
         float acc = 0.0f;
         for (int i = 0; i < nb; i++) acc += shfl(t, rl * nb + i);
-        if (live && sb == 0) emit(y, s.mode, row, acc);
+        if (s.pair) {
+            if ((st & 1) == 0) gsum = acc;
+            else if (live && sb == 0) emit(y, 0, row, ref_silu(gsum) * acc);
+        } else if (live && sb == 0) {
+            emit(y, s.mode, row, acc);
+        }
     };
     if (s.in <= 4096) {
         PIn pin;
@@ -621,8 +742,8 @@ OH_DEV void mv_body(const oh_mvlaunch &L) {
 // Fused MoE down projection and combine (src/ornith_rforward.c:375-409). A
 // block owns 64/nb output rows; wave j reduces slot j (the k routed experts in
 // routing order, then the shared expert) over those rows with one super-block
-// per lane. Slot j's activation is Q8_K(silu(g_j) * u_j), formed in LDS by the
-// block. Wave 0 then gives row r: x_r += (sum_j w_j * dot_j) + shg * dot_shared
+// per lane. Slot j's activation is Q8_K(h_j) (h_j = silu(gate) * up, emitted
+// by the paired expert launch), formed in LDS by the block. Wave 0 then gives row r: x_r += (sum_j w_j * dot_j) + shg * dot_shared
 // in the reference's order.
 template <int T>
 OH_DEV void down_body(const oh_mvdown &D) {
@@ -642,17 +763,16 @@ OH_DEV void down_body(const oh_mvdown &D) {
     const WP wp = sh ? WP{D.sA, D.sB, D.sC} : WP{D.A, D.B, D.C};
     const int64_t rb = sh ? 0 : (int64_t)D.eidx[j] * D.rows;
     const int rowc = row < D.rows ? (rl < rps ? row : row0) : D.rows - 1;
-    // SwiGLU inputs first (in <= 1024: at most 4 float4 of g and of u per
-    // thread), then the weights: vector loads complete in order
+    // activations first (in <= 1024: at most 4 float4 per thread), then the
+    // weights: vector loads complete in order
     const int nf = ns * in / 4, bd = (int)blockDim.x;
-    float4 ga[4], ua[4];
+    float4 ha[4];
     if (in <= 1024) {
 #pragma unroll
         for (int k = 0; k < 4; k++) {
             const int f = tid + bd * k < nf ? tid + bd * k : nf - 1;
             const int jj = 4 * f / in, e = 4 * f - jj * in;
-            ga[k] = *(const float4 *)(D.g + (size_t)jj * D.stride + e);
-            ua[k] = *(const float4 *)(D.u + (size_t)jj * D.stride + e);
+            ha[k] = *(const float4 *)(D.h + (size_t)jj * D.stride + e);
         }
     }
     SB<T> r;
@@ -661,19 +781,19 @@ OH_DEV void down_body(const oh_mvdown &D) {
     if (in <= 1024) {
 #pragma unroll
         for (int k = 0; k < 4; k++)
-            if (tid + bd * k < nf) ((float4 *)v)[tid + bd * k] = f4_silu_mul(ga[k], ua[k]);
+            if (tid + bd * k < nf) ((float4 *)v)[tid + bd * k] = make_float4(ha[k].x, ha[k].y, ha[k].z, ha[k].w);
     } else {
         for (int i = tid; i < ns * in; i += bd) {
             const int jj = i / in, e = i - jj * in;
-            v[i] = ref_silu(D.g[(size_t)jj * D.stride + e]) * D.u[(size_t)jj * D.stride + e];
+            v[i] = D.h[(size_t)jj * D.stride + e];
         }
     }
     lds_barrier();
-    for (int q = wave; q < ns * nb; q += nw) {
-        const int jj = q / nb, qb = q - jj * nb;
+    for (int jj = wave; jj < ns; jj += nw) {          // wave jj quantises slot jj
         uint8_t *b = smem + (size_t)jj * sq;
-        q8k_block_from_lds(v + (size_t)jj * in, qb, (int8_t *)b, (float *)(b + mv_lds_d_off(nb)),
-                           (int16_t *)(b + mv_lds_bs_off(nb)), kAS);
+        for (int q0 = 0; q0 < nb; q0 += 4)
+            q8k_blocks<4>(v + (size_t)jj * in, q0, 1, nb, (int8_t *)b, (float *)(b + mv_lds_d_off(nb)),
+                          (int16_t *)(b + mv_lds_bs_off(nb)), kAS);
     }
     lds_barrier();
     if (wave < ns) {

@@ -77,6 +77,11 @@ OH_HD static inline int oh_qdot_can(uint32_t t, int64_t in) {
 enum { OH_PRO_Q8K = 0, OH_PRO_NORM = 1, OH_PRO_SWIGLU = 2, OH_PRO_GNORM = 3, OH_PRO_F32 = 4 };
 typedef struct {
     const uint8_t *A, *B, *C;      // weight planes (expert 0 for a stacked tensor)
+    // pair != 0: a second tensor of the same type and shape (A2/B2/C2, e.g. the
+    // up projection next to the gate) is reduced against the same activation
+    // and the segment emits silu(W.x) * (W2.x) per row (mode 0)
+    const uint8_t *A2, *B2, *C2;
+    int pair;
     // activation: OH_PRO_Q8K reads Q8_K planes (and xf for the f32 fallback);
     // OH_PRO_NORM RMS-normalises xf with nw/eps; OH_PRO_SWIGLU forms
     // silu(xf)*xf2; OH_PRO_GNORM RMS-normalises each gdim-element head of xf
@@ -131,7 +136,7 @@ typedef struct {
     const int32_t *eidx;
     const float *w;                // routing weights [k]
     const float *shg;              // sigmoid shared gate (null: ungated)
-    const float *g, *u;            // gate/up outputs, slot k at +k*stride
+    const float *h;                // silu(gate)*up of slot k at +k*stride
     float *x;                      // residual, += combine
     int type, nb, in, rows, k, stride;
 } oh_mvdown;
