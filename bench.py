@@ -1,6 +1,6 @@
 #!/usr/bin/env python3
 """bench.py - decode tok/s at batch 1 and achieved HBM GB/s on the 35B-shaped
-Q4_K_M qwen35moe model, one MI355X.
+Q4_K_M qwen35moe model (the C3 configuration), one MI355X.
 
 Workload: hidden 2048, 40 layers (30 gated delta-net + 10 GQA), 256 experts
 top-8 with FFN 512 + shared expert 512, vocab 248320; every projection Q4_K
@@ -87,6 +87,93 @@ def bytes_per_token(model: oa.Model, cfg: dict, ctx_len: float) -> dict:
     cc = 2 * a["nk"] * a["dk"] + a["nv"] * a["dv"]
     state = n_lin * (2 * 4 * a["nv"] * a["dk"] * a["dv"] + 2 * 4 * (a["conv_k"] - 1) * cc)
     return dict(weights=w, kv=kv, state=state, total=w + kv + state)
+
+
+TRAFFIC_COPY_BYTES = 512 << 20
+TRAFFIC_REPS = 2
+TRAFFIC_PROMPT = 16
+
+
+def traffic_probe(kind: str) -> int:
+    """Under rocprofv3 --pmc: a device-to-device copy of TRAFFIC_COPY_BYTES
+    (the calibration kernel), then TRAFFIC_REPS back-to-back replays of one
+    decode step's `kind` launches on the C3 model after a 16-token prompt."""
+    import torch
+    a = torch.empty(TRAFFIC_COPY_BYTES // 4, dtype=torch.float32, device="cuda").fill_(1.0)
+    b = torch.empty_like(a)
+    b.copy_(a)
+    torch.cuda.synchronize()
+    del a, b
+    ctx = oa.Context(0)
+    model = ctx.synth(**C3)
+    sess = model.session(64)
+    sess.eval(np.arange(TRAFFIC_PROMPT, dtype=np.int32) * 7919 % C3["vocab"])
+    us, bpl, nps = sess.time_kind(kind, reps=TRAFFIC_REPS)
+    print(json.dumps({"kind": kind, "launches_per_step": nps, "reps": TRAFFIC_REPS, "us_per_launch": us,
+                      "bytes_per_launch": bpl, "copy_bytes": TRAFFIC_COPY_BYTES}), flush=True)
+    sess.free()
+    model.free()
+    ctx.close()
+    return 0
+
+
+def _counter_rows(path: str, counter: str):
+    import csv
+    rows = []
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            if r["Counter_Name"] == counter:
+                rows.append((int(r["Dispatch_Id"]), r["Kernel_Name"], float(r["Counter_Value"])))
+    rows.sort()
+    return rows
+
+
+def traffic_summarize(kind: str, fetch_csv: str, write_csv: str) -> int:
+    """FETCH_SIZE / WRITE_SIZE are KiB per dispatch. Each is scaled by what it
+    reads for the calibration copy (a copy of N bytes reads and writes N), and
+    the last TRAFFIC_REPS x launches_per_step dispatches of the kernel are
+    averaged (the replay of --traffic-probe)."""
+    sym = KERNEL_SYMBOL.get(kind, kind)
+    out = {}
+    for counter, path in (("FETCH_SIZE", fetch_csv), ("WRITE_SIZE", write_csv)):
+        rows = _counter_rows(path, counter)
+        copy = [v for _, n, v in rows if "copy" in n.lower() or "elementwise" in n.lower()]
+        kern = [v for _, n, v in rows if n.split("(")[0].strip() == sym]
+        if not copy or not kern:
+            print(f"traffic: no {counter} rows for the copy or {sym}", file=sys.stderr)
+            return 1
+        factor = max(copy) * 1024.0 / TRAFFIC_COPY_BYTES
+        out[counter] = dict(copy_kib=max(copy), factor=factor, dispatches=len(kern), kern_kib=kern)
+    n = min(out["FETCH_SIZE"]["dispatches"], out["WRITE_SIZE"]["dispatches"])
+    # the probe makes TRAFFIC_PROMPT prompt steps, one warm-up pass and
+    # TRAFFIC_REPS timed passes of the same launches; keep the timed ones
+    take = n * TRAFFIC_REPS // (TRAFFIC_PROMPT + 1 + TRAFFIC_REPS)
+    tf = ROOT / "profiles" / "traffic.json"
+    prev = json.loads(tf.read_text()) if tf.exists() else {}
+    fetch = out["FETCH_SIZE"]["kern_kib"][-take:]
+    write = out["WRITE_SIZE"]["kern_kib"][-take:]
+    fb = sum(fetch) / len(fetch) * 1024.0 / out["FETCH_SIZE"]["factor"]
+    wb = sum(write) / len(write) * 1024.0 / out["WRITE_SIZE"]["factor"]
+    prev[kind] = {"bytes_per_launch": round(fb + wb), "fetch_bytes_per_launch": round(fb),
+                  "write_bytes_per_launch": round(wb), "dispatches_averaged": len(fetch),
+                  "fetch_copy_factor": round(out["FETCH_SIZE"]["factor"], 4),
+                  "write_copy_factor": round(out["WRITE_SIZE"]["factor"], 4)}
+    tf.write_text(json.dumps(prev, indent=1) + "\n")
+    print(json.dumps(prev[kind]))
+    return 0
+
+
+def traffic_per_launch(kind: str):
+    """HBM bytes per launch of `kind` measured with rocprofv3 FETCH_SIZE +
+    WRITE_SIZE counter passes (calibrated on a device copy of known size),
+    from profiles/traffic.json when that measurement exists, else None."""
+    p = ROOT / "profiles" / "traffic.json"
+    if not p.exists():
+        return None
+    try:
+        return json.loads(p.read_text()).get(kind, {}).get("bytes_per_launch")
+    except (OSError, ValueError):
+        return None
 
 
 def profile_kernels(sess: oa.Session, reps: int) -> dict:
@@ -193,10 +280,19 @@ def main() -> int:
     ap.add_argument("--profile-reps", type=int, default=3)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--traffic-probe", metavar="KIND", default=None,
+                    help="run one device copy of known size and a replay of one step's KIND launches "
+                         "(for rocprofv3 FETCH_SIZE / WRITE_SIZE passes), then exit")
+    ap.add_argument("--traffic-summarize", nargs=3, metavar=("KIND", "FETCH_CSV", "WRITE_CSV"), default=None,
+                    help="turn the two counter CSVs of --traffic-probe runs into profiles/traffic.json")
     args = ap.parse_args()
+    if args.traffic_probe:
+        return traffic_probe(args.traffic_probe)
+    if args.traffic_summarize:
+        return traffic_summarize(*args.traffic_summarize)
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); "
-              "multi-GPU sharding is design-only (see DESIGN.md)", file=sys.stderr)
+              "multi-GPU sharding is a design, not a code path, in this build", file=sys.stderr)
         return 2
 
     ctx = oa.Context(0)
@@ -228,13 +324,18 @@ def main() -> int:
     bpt = bytes_per_token(model, C3, ctx_mid)
     step_gbs = bpt["total"] * tok_s / 1e9
 
+    # per-launch HIP events around every kernel of one eager step rank the
+    # kernels; the dominant one is then timed by a back-to-back replay of its
+    # launches (no per-launch event gaps), which is what the roofline uses
     prof = profile_kernels(sess, args.profile_reps)
     dom = max(prof, key=lambda k: prof[k]["ms"])
-    d = prof[dom]
-    achieved = (d["bytes"] / d["launches"]) / (d["ms"] / d["launches"] * 1e-3) / 1e9
     for k, v in sorted(prof.items(), key=lambda kv: -kv[1]["ms"]):
         log(f"  {k:12s} {v['launches']:6.0f} launches  {v['ms']:8.3f} ms/step  {v['bytes'] / 1e6:9.1f} MB/step  "
-            f"{v['bytes'] / max(v['ms'], 1e-9) / 1e6:8.1f} GB/s")
+            f"{v['bytes'] / max(v['ms'], 1e-9) / 1e6:8.1f} GB/s  (eager, per-launch events)")
+    us, bpl, nps = sess.time_kind(dom, reps=args.profile_reps + 2)
+    achieved = bpl / (us * 1e-6) / 1e9
+    log(f"roofline kernel {KERNEL_SYMBOL.get(dom, dom)}: {nps} launches/step replayed back to back: "
+        f"{us:.2f} us/launch, {bpl / 1e6:.2f} MB/launch -> {achieved:.1f} GB/s")
 
     cpu = None
     if not args.no_cpu:
@@ -257,9 +358,9 @@ def main() -> int:
         "bytes_per_token": {k: round(v) for k, v in bpt.items()},
         "roofline": {"bound": "hbm", "kernel": KERNEL_SYMBOL.get(dom, dom),
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "bytes_per_launch": round(d["bytes"] / d["launches"]),
-                     "avg_launch_us": round(d["ms"] / d["launches"] * 1e3, 3)},
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_per_launch(dom),
+                     "bytes_per_launch": round(bpl), "avg_launch_us": round(us, 3),
+                     "launches_per_step": nps},
         "cpu_baseline": cpu,
         "prefill_tok_s": round(args.ctx / t_prefill, 1),
     }

@@ -170,6 +170,14 @@ int  ornith_hip_session_time_decode(ornith_hip_session *s, int n_steps, float *m
  * one position. */
 int  ornith_hip_session_profile_step(ornith_hip_session *s, int max_launches, int32_t *kinds,
                                      double *bytes, float *ms, int *n_launches);
+/* Replay, back to back, the launches of one kind (numbering as above) that a
+ * decode step makes, `reps` times, between two HIP events on the session
+ * stream: *us_per_launch = mean time per launch, *bytes_per_launch = mean
+ * algorithmic HBM bytes, *launches_per_step = launches of that kind per step.
+ * The other kernels of the step do not run, so the session's state is
+ * meaningless afterwards: measurement only, free the session after. */
+int  ornith_hip_session_time_kind(ornith_hip_session *s, int kind, int reps, float *us_per_launch,
+                                  double *bytes_per_launch, int *launches_per_step);
 /* Time `iters` launches of one matvec of W (activation already quantised on
  * the device) with HIP events on the context stream; *ms = mean per launch. */
 int  ornith_hip_time_matvec(ornith_hip_ctx *ctx, const ornith_hip_tensor *W, int iters,

@@ -4,13 +4,11 @@
  * tests, __graft_entry__.smoke() and bench.py's cpu_baseline leg load it. Each
  * function restates the reference algorithm at the cited file:line of
  * njbrake/ornithology and keeps its floating-point operation order, so that a
- * gcc build with -std=c11 -ffp-contract=off reproduces the reference bits
- * (tests/test_oracle_vs_ref.py checks that against oracle/_ref and the golden
- * fixtures in tests/golden/).
- *
- * Parity status per function is listed in oracle/README-parity (and DESIGN.md);
- * every exported function here is pinned by at least one golden vector or
- * closed-form check.
+ * gcc build with -std=c11 -ffp-contract=off reproduces the reference bits.
+ * tests/test_oracle_quant.py, test_oracle_attn.py and test_oracle_model.py
+ * check that against oracle/_ref (the reference's own sources, compiled in
+ * place by oracle/Makefile) and against the fixtures in tests/golden/, and
+ * pin each function further by closed forms, brute force and known answers.
  */
 #ifndef ORNITH_ORACLE_H
 #define ORNITH_ORACLE_H

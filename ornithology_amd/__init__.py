@@ -93,6 +93,7 @@ _SIGS = {
     "ornith_hip_session_time_decode": (C.c_int, [_vp, C.c_int, _fp]),
     "ornith_hip_time_matvec": (C.c_int, [_vp, _vp, C.c_int, _fp]),
     "ornith_hip_session_profile_step": (C.c_int, [_vp, C.c_int, _ip, C.POINTER(C.c_double), _fp, _ip]),
+    "ornith_hip_session_time_kind": (C.c_int, [_vp, C.c_int, C.c_int, _fp, C.POINTER(C.c_double), _ip]),
 }
 
 _lib = None
@@ -311,6 +312,15 @@ class Session:
     KERNEL_KINDS = ("matvec", "rmsnorm_q8k", "swiglu_q8k", "embed", "delta_step", "attn_prep",
                     "attn_scores", "attn_out", "moe_route", "moe_combine", "argmax", "advance",
                     "moe_down", "attn_flash", "attn_combine", "matvec_q6k", "matvec_q80", "matvec_mixed")
+
+    def time_kind(self, kind: str, reps: int = 5):
+        """Back-to-back replay of one step's launches of `kind`: returns
+        (us per launch, algorithmic bytes per launch, launches per step).
+        Leaves the session state meaningless (measurement only)."""
+        us, by, n = C.c_float(), C.c_double(), C.c_int()
+        _check(lib().ornith_hip_session_time_kind(self.h, self.KERNEL_KINDS.index(kind), reps, C.byref(us),
+                                                  C.byref(by), C.byref(n)), "ornith_hip_session_time_kind")
+        return us.value, by.value, n.value
 
     def profile_step(self, max_launches: int = 4096):
         """One eager decode step with per-launch HIP-event timing: list of

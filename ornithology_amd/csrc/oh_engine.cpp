@@ -924,6 +924,10 @@ struct ornith_hip_session {
     std::vector<hipEvent_t> rec_ev;
     std::vector<int> rec_kind;
     std::vector<double> rec_bytes;
+    // kind replay (time_kind): launch only the kernels of one kind
+    int only = -1;
+    int only_n = 0;
+    double only_bytes = 0.0;
 };
 
 enum { K_MATVEC = 0, K_NORM_Q8K, K_SWIGLU_Q8K, K_EMBED, K_DELTA, K_ATTN_PREP, K_ATTN_SCORES,
@@ -948,21 +952,35 @@ static int rec_end(ornith_hip_session *s, hipStream_t st, int kind, double bytes
     s->rec_bytes.push_back(bytes);
     return ORNITH_HIP_OK;
 }
-#define LAUNCH(kind, bytes, call)           \
-    do {                                    \
-        CHK(rec_begin(s, st));              \
-        HCHK(call);                         \
-        CHK(rec_end(s, st, kind, bytes));   \
+// true when the launch of this kind runs (every launch unless a kind replay
+// is selecting one kind); counts the replayed launches and their bytes
+static bool keep(ornith_hip_session *s, int kind, double bytes) {
+    if (s->only < 0) return true;
+    if (kind != s->only) return false;
+    s->only_n++;
+    s->only_bytes += bytes;
+    return true;
+}
+#define LAUNCH(kind, bytes, call)                  \
+    do {                                           \
+        if (keep(s, (kind), (bytes))) {            \
+            CHK(rec_begin(s, st));                 \
+            HCHK(call);                            \
+            CHK(rec_end(s, st, kind, bytes));      \
+        }                                          \
     } while (0)
 // matvec launches are recorded by kernel variant (see oh_launch_matvec)
 static int mv_kind(int tk) {
     return tk == OH_Q4_K ? K_MATVEC : tk == OH_Q6_K ? K_MATVEC_Q6K : tk == OH_Q8_0 ? K_MATVEC_Q80 : K_MATVEC_MIXED;
 }
-#define MVGO(b)                                              \
-    do {                                                     \
-        CHK(rec_begin(s, st));                               \
-        CHK(mv_go(b, st));                                   \
-        CHK(rec_end(s, st, mv_kind((b).tk), (b).bytes));     \
+#define MVGO(b)                                                  \
+    do {                                                         \
+        mv_plan(b);                                              \
+        if (keep(s, mv_kind((b).tk), (b).bytes)) {               \
+            CHK(rec_begin(s, st));                               \
+            CHK(mv_go(b, st));                                   \
+            CHK(rec_end(s, st, mv_kind((b).tk), (b).bytes));     \
+        }                                                        \
     } while (0)
 
 extern "C" void ornith_hip_session_free(ornith_hip_session *s) {
@@ -1607,6 +1625,49 @@ extern "C" int ornith_hip_model_synth(ornith_hip_ctx *ctx, const ornith_hip_gen_
 }
 
 // ---- one eager step with per-launch timing (HIP events around every launch) ------------------------
+extern "C" int ornith_hip_session_time_kind(ornith_hip_session *s, int kind, int reps, float *us_per_launch,
+                                            double *bytes_per_launch, int *launches_per_step) {
+    *us_per_launch = 0.0f;
+    *bytes_per_launch = 0.0;
+    *launches_per_step = 0;
+    if (!s->have_logits) { seterr("session has no logits; eval a prompt first"); return ORNITH_HIP_ERR_FORMAT; }
+    if (kind < 0 || reps < 1) { seterr("time_kind: kind %d reps %d", kind, reps); return ORNITH_HIP_ERR_FORMAT; }
+    HCHK(hipSetDevice(s->m->ctx->device));
+    hipStream_t st = s->m->ctx->st;
+    CHK(sync_pos(s));
+    HCHK(hipStreamSynchronize(st));
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    HCHK(hipEventCreate(&e0));
+    HCHK(hipEventCreate(&e1));
+    s->only = kind;
+    s->only_n = 0;
+    s->only_bytes = 0.0;
+    int r = enqueue_body(s, st);                   // warm-up pass: counts launches and bytes
+    if (r == ORNITH_HIP_OK) r = enqueue_head(s, st);
+    const int n = s->only_n;
+    const double by = s->only_bytes;
+    hipError_t e = hipEventRecord(e0, st);
+    for (int i = 0; i < reps && r == ORNITH_HIP_OK && e == hipSuccess; i++) {
+        r = enqueue_body(s, st);
+        if (r == ORNITH_HIP_OK) r = enqueue_head(s, st);
+    }
+    if (e == hipSuccess) e = hipEventRecord(e1, st);
+    if (e == hipSuccess) e = hipEventSynchronize(e1);
+    s->only = -1;
+    float el = 0.0f;
+    if (r == ORNITH_HIP_OK && e == hipSuccess) e = hipEventElapsedTime(&el, e0, e1);
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    if (r) return r;
+    HCHK(e);
+    if (n > 0) {
+        *us_per_launch = el * 1000.0f / (float)(reps * n);
+        *bytes_per_launch = by / n;
+    }
+    *launches_per_step = n;
+    return ORNITH_HIP_OK;
+}
+
 extern "C" int ornith_hip_session_profile_step(ornith_hip_session *s, int max_launches, int32_t *kinds,
                                                double *bytes, float *ms, int *n_launches) {
     *n_launches = 0;

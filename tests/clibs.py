@@ -82,7 +82,7 @@ class OrcKV(C.Structure):
                 ("len", C.c_int), ("n_kv_heads", C.c_int), ("head_dim", C.c_int)]
 
 
-# Configs from BASELINE.json. C1 is the tiny all-Q8_0 model; C3 the 35B shape.
+# Benchmark configurations. C1 is the tiny all-Q8_0 model; C3 the 35B shape.
 C1 = dict(hidden=512, n_layers=4, vocab=4096, full_interval=4, nh=8, nkv=2, hd=64,
           nk=4, nv=8, dhead=64, conv_k=4, ne=16, top_k=4, moe_inter=256, shared_inter=256,
           t_default=Q8_0, t_attn_v=Q8_0, t_ffn_down=Q8_0, t_output=Q8_0, t_embd=Q8_0,
