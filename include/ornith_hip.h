@@ -157,9 +157,12 @@ int  ornith_hip_session_get_kv(ornith_hip_session *s, int layer, int8_t *Kq,
 
 /* ---- measurement (no reference twin) -------------------------------------------- */
 
-/* Time n_steps greedy decode steps already resident on the device (the step
- * graph replayed back to back, the next token chosen on the device) with HIP
- * events on the session stream; *ms = total elapsed. Advances the session. */
+/* Time n_steps greedy decode steps already resident on the device (back to
+ * back, the next token chosen on the device) with HIP events on the session
+ * stream; *ms = total elapsed. Advances the session. A decode step replays
+ * HIP graphs of one launch per operation; with ORNITH_HIP_STEP=1 in the
+ * environment it runs as two launches of the persistent step kernel (body,
+ * head) instead (the same for eval and generate). */
 int  ornith_hip_session_time_decode(ornith_hip_session *s, int n_steps, float *ms);
 /* Run one greedy decode step eagerly with HIP events around every kernel
  * launch: kinds[i] (0 matvec with Q4_K weights, 1 rmsnorm+Q8_K, 2 SwiGLU+Q8_K,
@@ -174,10 +177,19 @@ int  ornith_hip_session_profile_step(ornith_hip_session *s, int max_launches, in
  * decode step makes, `reps` times, between two HIP events on the session
  * stream: *us_per_launch = mean time per launch, *bytes_per_launch = mean
  * algorithmic HBM bytes, *launches_per_step = launches of that kind per step.
- * The other kernels of the step do not run, so the session's state is
- * meaningless afterwards: measurement only, free the session after. */
+ * Kinds 18 and 19 are the persistent step kernel's body and head launches
+ * (all operations of a step at the current position). The other kernels of
+ * the step do not run, so the session's state is meaningless afterwards:
+ * measurement only, free the session after. */
 int  ornith_hip_session_time_kind(ornith_hip_session *s, int kind, int reps, float *us_per_launch,
                                   double *bytes_per_launch, int *launches_per_step);
+/* One step-kernel body launch at the current position (the position does not
+ * advance; measurement only, like time_kind) with workgroup 0's real-time
+ * clock read after every grid barrier: per phase (operation) its kind
+ * (numbering as above, -1 for the second stage of a two-stage operation),
+ * algorithmic bytes and us from the previous barrier to its own. */
+int  ornith_hip_session_profile_phases(ornith_hip_session *s, int max_phases, int32_t *kinds,
+                                       double *bytes, float *us, int *n_phases);
 /* Time `iters` launches of one matvec of W (activation already quantised on
  * the device) with HIP events on the context stream; *ms = mean per launch. */
 int  ornith_hip_time_matvec(ornith_hip_ctx *ctx, const ornith_hip_tensor *W, int iters,

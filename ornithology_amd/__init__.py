@@ -94,6 +94,7 @@ _SIGS = {
     "ornith_hip_time_matvec": (C.c_int, [_vp, _vp, C.c_int, _fp]),
     "ornith_hip_session_profile_step": (C.c_int, [_vp, C.c_int, _ip, C.POINTER(C.c_double), _fp, _ip]),
     "ornith_hip_session_time_kind": (C.c_int, [_vp, C.c_int, C.c_int, _fp, C.POINTER(C.c_double), _ip]),
+    "ornith_hip_session_profile_phases": (C.c_int, [_vp, C.c_int, _ip, C.POINTER(C.c_double), _fp, _ip]),
 }
 
 _lib = None
@@ -311,7 +312,8 @@ class Session:
 
     KERNEL_KINDS = ("matvec", "rmsnorm_q8k", "swiglu_q8k", "embed", "delta_step", "attn_prep",
                     "attn_scores", "attn_out", "moe_route", "moe_combine", "argmax", "advance",
-                    "moe_down", "attn_flash", "attn_combine", "matvec_q6k", "matvec_q80", "matvec_mixed")
+                    "moe_down", "attn_flash", "attn_combine", "matvec_q6k", "matvec_q80", "matvec_mixed",
+                    "step_body", "step_head")
 
     def time_kind(self, kind: str, reps: int = 5):
         """Back-to-back replay of one step's launches of `kind`: returns
@@ -334,6 +336,20 @@ class Session:
                                                      C.byref(n)), "ornith_hip_session_profile_step")
         k = n.value
         return [(self.KERNEL_KINDS[kinds[i]], float(byts[i]), float(ms[i])) for i in range(k)]
+
+    def profile_phases(self, max_phases: int = 4096):
+        """One step-kernel body launch at the current position (the position
+        does not advance): list of (kind or None, algorithmic bytes, us) per
+        phase, timed by workgroup 0's clock between grid barriers."""
+        kinds = np.zeros(max_phases, np.int32)
+        byts = np.zeros(max_phases, np.float64)
+        us = np.zeros(max_phases, np.float32)
+        n = C.c_int32(0)
+        _check(lib().ornith_hip_session_profile_phases(self.h, max_phases, _i32(kinds),
+                                                       byts.ctypes.data_as(C.POINTER(C.c_double)), _f32(us),
+                                                       C.byref(n)), "ornith_hip_session_profile_phases")
+        return [(self.KERNEL_KINDS[kinds[i]] if kinds[i] >= 0 else None, float(byts[i]), float(us[i]))
+                for i in range(n.value)]
 
     def delta_state(self, layer: int) -> np.ndarray:
         a = self.model.arch

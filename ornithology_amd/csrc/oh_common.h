@@ -142,16 +142,58 @@ OH_DEV float ref_silu(float x) { return x * ref_sigmoid(x); }
 OH_DEV float ref_softplus(float x) { return x > 20.0f ? x : ref_log1pf(ref_expf(x)); }
 
 // ---- wave helpers (wave64) --------------------------------------------------
-OH_DEV int lane_id() { return (int)(threadIdx.x & 63); }
+// The thread index through an empty volatile asm: inside the persistent step
+// kernel every operation body computes its thread-dependent addresses afresh
+// instead of the compiler hoisting all of them out of the phase loop (where
+// they would stay live, and spill, across every phase).
+OH_DEV int tid_x() {
+    int t = (int)threadIdx.x;
+    asm volatile("" : "+v"(t));
+    return t;
+}
+OH_DEV int lane_id() { return tid_x() & 63; }
 
+// lane shuffles over the whole wave (ds_bpermute), with the lane index taken
+// from tid_x() so that no index computation is hoisted out of the step loop
+OH_DEV int bperm(int v, int src) { return __builtin_amdgcn_ds_bpermute(src << 2, v); }
+OH_DEV int shfl(int v, int src) { return bperm(v, src & 63); }
+OH_DEV float shfl(float v, int src) { return __int_as_float(bperm(__float_as_int(v), src & 63)); }
+OH_DEV double shfl(double v, int src) {
+    const long long b = __double_as_longlong(v);
+    const int lo = bperm((int)b, src & 63), hi = bperm((int)(b >> 32), src & 63);
+    return __longlong_as_double(((long long)hi << 32) | (unsigned)lo);
+}
 template <typename T>
-OH_DEV T shfl(T v, int src) { return __shfl(v, src, 64); }
-template <typename T>
-OH_DEV T shfl_xor(T v, int m) { return __shfl_xor(v, m, 64); }
+OH_DEV T shfl_xor(T v, int m) { return shfl(v, lane_id() ^ m); }
 
+// DPP all-reduce within each 16-lane row (xor 1, xor 2, half-mirror, mirror:
+// after each step every lane holds the combined value of a group twice as
+// large). Only for order-independent operations (integer sums, max, min).
+template <int CTRL>
+OH_DEV int dpp_i(int v) { return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, false); }
+template <int CTRL>
+OH_DEV float dpp_f(float v) { return __int_as_float(dpp_i<CTRL>(__float_as_int(v))); }
+template <int CTRL>
+OH_DEV double dpp_d(double v) {
+    const long long b = __double_as_longlong(v);
+    const int lo = dpp_i<CTRL>((int)b), hi = dpp_i<CTRL>((int)(b >> 32));
+    return __longlong_as_double(((long long)hi << 32) | (unsigned)lo);
+}
+OH_DEV double readlane_d(double v, int l) {
+    const long long b = __double_as_longlong(v);
+    const int lo = __builtin_amdgcn_readlane((int)b, l), hi = __builtin_amdgcn_readlane((int)(b >> 32), l);
+    return __longlong_as_double(((long long)hi << 32) | (unsigned)lo);
+}
+// Wave-wide double sum in a fixed tree (pairs, quads, eights and sixteens of
+// a row by DPP, then (row0 + row1) + (row2 + row3)); every lane gets it. Used
+// for sums of squares that the reference adds sequentially in double and
+// rounds to float afterwards.
 OH_DEV double wave_sum_d(double v) {
-    for (int m = 32; m >= 1; m >>= 1) v += shfl_xor(v, m);
-    return v;
+    v += dpp_d<0xB1>(v);
+    v += dpp_d<0x4E>(v);
+    v += dpp_d<0x141>(v);
+    v += dpp_d<0x140>(v);
+    return (readlane_d(v, 0) + readlane_d(v, 16)) + (readlane_d(v, 32) + readlane_d(v, 48));
 }
 OH_DEV int wave_sum_i(int v) {
     for (int m = 32; m >= 1; m >>= 1) v += shfl_xor(v, m);
@@ -162,13 +204,6 @@ OH_DEV float wave_max_f(float v) {
     return v;
 }
 
-// DPP all-reduce within each 16-lane row (xor 1, xor 2, half-mirror, mirror:
-// after each step every lane holds the combined value of a group twice as
-// large). Only for order-independent operations (integer sums, max, min).
-template <int CTRL>
-OH_DEV int dpp_i(int v) { return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, false); }
-template <int CTRL>
-OH_DEV float dpp_f(float v) { return __int_as_float(dpp_i<CTRL>(__float_as_int(v))); }
 OH_DEV int row16_sum_i(int v) {
     v += dpp_i<0xB1>(v); v += dpp_i<0x4E>(v); v += dpp_i<0x141>(v); v += dpp_i<0x140>(v);
     return v;
@@ -195,3 +230,88 @@ OH_DEV int wave_min_fast(int v) {
 
 // signed 8-bit dot of four packed bytes, accumulated into c (exact integers)
 OH_DEV int dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
+
+// ---- data shared between workgroups of one launch ----------------------------
+// The L2 caches of the XCDs are not coherent with each other, and a CU's L1 is
+// not coherent with other CUs. Values that one workgroup writes and another
+// reads later in the same launch (the persistent token-step kernel, whose
+// phases are separated by grid barriers) therefore use device-scope accesses:
+// relaxed device-scope atomic loads and stores, i.e. ordinary loads and stores
+// with the sc1 scope bit. A device-scope store is acknowledged once it is
+// visible at device scope, and a device-scope load does not return a
+// non-coherent cached copy. The grid barrier waits for the stores' completion
+// before it signals. Weights and other data that no launch writes use plain
+// accesses.
+#define OH_GLOBAL __attribute__((address_space(1)))
+template <typename T>
+OH_DEV T ldc(const T *p) {
+    return __hip_atomic_load((const OH_GLOBAL T *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <typename T>
+OH_DEV void stc(T *p, T v) { __hip_atomic_store((OH_GLOBAL T *)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+// Plain loads and stores of global memory through pointers taken from an
+// operation descriptor: the explicit address space makes them global_load /
+// global_store (a pointer read from memory would otherwise be accessed with
+// flat instructions, which also count against the LDS wait counter).
+template <typename T>
+OH_DEV T ldg(const T *p) { return *(const OH_GLOBAL T *)p; }
+template <typename T>
+OH_DEV void stg(T *p, const T &v) { *(OH_GLOBAL T *)p = v; }
+// HIP's vector types copy through a generic reference: load and store their
+// raw vector form instead
+typedef unsigned oh_u4 __attribute__((ext_vector_type(4)));
+typedef float oh_f4 __attribute__((ext_vector_type(4)));
+typedef float oh_f2 __attribute__((ext_vector_type(2)));
+template <>
+OH_DEV uint4 ldg(const uint4 *p) {
+    const oh_u4 v = *(const OH_GLOBAL oh_u4 *)p;
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+template <>
+OH_DEV float4 ldg(const float4 *p) {
+    const oh_f4 v = *(const OH_GLOBAL oh_f4 *)p;
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+template <>
+OH_DEV float2 ldg(const float2 *p) {
+    const oh_f2 v = *(const OH_GLOBAL oh_f2 *)p;
+    return make_float2(v.x, v.y);
+}
+template <>
+OH_DEV void stg(float4 *p, const float4 &v) {
+    oh_f4 r;
+    r.x = v.x; r.y = v.y; r.z = v.z; r.w = v.w;
+    *(OH_GLOBAL oh_f4 *)p = r;
+}
+OH_DEV float4 ldc4(const float4 *p) {
+    const double *q = (const double *)p;
+    const double a = ldc(q), b = ldc(q + 1);
+    const uint64_t ua = (uint64_t)__double_as_longlong(a), ub = (uint64_t)__double_as_longlong(b);
+    return make_float4(u2f((uint32_t)ua), u2f((uint32_t)(ua >> 32)), u2f((uint32_t)ub), u2f((uint32_t)(ub >> 32)));
+}
+OH_DEV int4 ldc4(const int4 *p) {
+    const float4 v = ldc4((const float4 *)p);
+    return make_int4((int)f2u(v.x), (int)f2u(v.y), (int)f2u(v.z), (int)f2u(v.w));
+}
+OH_DEV void stc4(float4 *p, const float4 v) {
+    double *q = (double *)p;
+    stc(q, __longlong_as_double((long long)(((uint64_t)f2u(v.y) << 32) | f2u(v.x))));
+    stc(q + 1, __longlong_as_double((long long)(((uint64_t)f2u(v.w) << 32) | f2u(v.z))));
+}
+
+// LDS ordering between the lanes of one wave (no workgroup barrier): waits for
+// the wave's LDS operations and keeps the compiler from moving LDS accesses
+// across it.
+OH_DEV void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// A no-op grid wait: the bodies of the token-step operations call wait()
+// before their first read of another phase's output; a standalone kernel has
+// nothing to wait for (the kernel boundary orders it).
+struct NoWait {
+    static constexpr bool kGrid = false;
+    OH_DEV bool wait() { return true; }
+};

@@ -363,8 +363,9 @@ static int mv_add_pair(MvBuild &b, const ornith_hip_tensor *W, const ornith_hip_
 }
 
 // Lay the segments out over blocks: every wave gets a run of whole wave
-// steps sized so the launch spreads over ~4096 waves (16 per CU).
-static void mv_plan(MvBuild &b) {
+// steps sized so the launch spreads over about `waves` waves (4096, i.e. 16
+// per CU, for a standalone launch; the resident waves of the step kernel).
+static void mv_plan(MvBuild &b, int waves = 4096) {
     int64_t steps = 0;
     int tk = -2;
     for (int i = 0; i < b.L.n; i++) {
@@ -377,7 +378,7 @@ static void mv_plan(MvBuild &b) {
         }
     }
     b.tk = tk < 0 ? -1 : tk;
-    const int64_t spw = (steps + 4095) / 4096;
+    const int64_t spw = (steps + waves - 1) / waves;
     int blocks = 0;
     b.lds = 0;
     for (int i = 0; i < b.L.n; i++) {
@@ -928,11 +929,19 @@ struct ornith_hip_session {
     int only = -1;
     int only_n = 0;
     double only_bytes = 0.0;
+    // persistent step kernel: the body and head programs in device memory,
+    // their barrier counters, the grid, and (profiling) phase timestamps
+    struct StepProg { oh_op *ops = nullptr; unsigned *ctrs = nullptr; int n = 0, lds = 0; double bytes = 0.0; };
+    StepProg sp_body, sp_head;
+    std::vector<int> sp_body_rk;
+    int step_grid = 0;
+    bool step_tried = false;
+    uint64_t *ts = nullptr;
 };
 
 enum { K_MATVEC = 0, K_NORM_Q8K, K_SWIGLU_Q8K, K_EMBED, K_DELTA, K_ATTN_PREP, K_ATTN_SCORES,
        K_ATTN_OUT, K_ROUTE, K_COMBINE, K_ARGMAX, K_ADVANCE, K_MV_DOWN, K_ATTN_FLASH, K_ATTN_COMBINE,
-       K_MATVEC_Q6K, K_MATVEC_Q80, K_MATVEC_MIXED };
+       K_MATVEC_Q6K, K_MATVEC_Q80, K_MATVEC_MIXED, K_STEP_BODY, K_STEP_HEAD };
 
 static int rec_begin(ornith_hip_session *s, hipStream_t st) {
     if (!s->rec) return ORNITH_HIP_OK;
@@ -973,15 +982,40 @@ static bool keep(ornith_hip_session *s, int kind, double bytes) {
 static int mv_kind(int tk) {
     return tk == OH_Q4_K ? K_MATVEC : tk == OH_Q6_K ? K_MATVEC_Q6K : tk == OH_Q8_0 ? K_MATVEC_Q80 : K_MATVEC_MIXED;
 }
-#define MVGO(b)                                                  \
-    do {                                                         \
-        mv_plan(b);                                              \
-        if (keep(s, mv_kind((b).tk), (b).bytes)) {               \
-            CHK(rec_begin(s, st));                               \
-            CHK(mv_go(b, st));                                   \
-            CHK(rec_end(s, st, mv_kind((b).tk), (b).bytes));     \
-        }                                                        \
-    } while (0)
+
+// ---- the token step as a program of operations ----------------------------------------------
+// The same list of operations runs either launch by launch (captured into HIP
+// graphs; profiling) or as the phases of the persistent step kernel.
+struct Prog {
+    std::vector<oh_op> ops;
+    std::vector<int> rk;          // record kind (profiling); -1: part of the previous record
+    std::vector<double> bytes;    // algorithmic HBM bytes
+    int lds = 0;                  // largest dynamic LDS of an operation
+    int waves = 4096;             // matvec planning target
+};
+static oh_op op_new(int kind, int nvb, int lds = 0) {
+    oh_op o;
+    memset(&o, 0, sizeof o);
+    o.kind = kind;
+    o.nvb = nvb;
+    o.tk = -1;
+    o.lds = lds;
+    return o;
+}
+static void prog_add(Prog &P, const oh_op &o, int rk, double bytes) {
+    if (o.nvb <= 0) return;
+    P.ops.push_back(o);
+    P.rk.push_back(rk);
+    P.bytes.push_back(bytes);
+    if (o.lds > P.lds) P.lds = o.lds;
+}
+static void prog_mv(Prog &P, MvBuild &b) {
+    mv_plan(b, P.waves);
+    oh_op o = op_new(OH_OP_MV, b.L.total_blocks, b.lds);
+    o.tk = b.tk;
+    o.u.mv = b.L;
+    prog_add(P, o, mv_kind(b.tk), b.bytes);
+}
 
 extern "C" void ornith_hip_session_free(ornith_hip_session *s) {
     if (!s) return;
@@ -1110,14 +1144,16 @@ extern "C" int ornith_hip_session_new(ornith_hip_model *m, int cap, ornith_hip_s
 // Algorithmic bytes of the small kernels (recorded by profile_step only).
 static double norm_bytes(int n, bool w) { return (double)n * (4.0 + (w ? 4.0 : 0.0) + 4.0 + 1.0 + 4.0 / 256 + 2.0 / 16); }
 
-static int enqueue_body(ornith_hip_session *s, hipStream_t st) {
+static int build_body(ornith_hip_session *s, Prog &P) {
     const ornith_hip_model *m = s->m;
     const ornith_hip_arch &a = m->a;
     const int H = a.hidden, qd = a.nk * a.dk, vd = a.nv * a.dv, cc = 2 * qd + vd;
-    const int32_t *pos = s->io;
     const double T = (double)(s->pos + 1);
-    LAUNCH(K_EMBED, (double)gguf_nbytes(m->embd->type, (uint64_t)H) + 4.0 * H,
-           oh_launch_embed(m->embd->A, m->embd->B, m->embd->C, (int)m->embd->type, H, s->toks, pos, s->x, st));
+    {
+        oh_op o = op_new(OH_OP_EMBED, (H + 255) / 256);
+        o.u.embed = {m->embd->A, m->embd->B, m->embd->C, s->toks, s->x, (int)m->embd->type, H};
+        prog_add(P, o, K_EMBED, (double)gguf_nbytes(m->embd->type, (uint64_t)H) + 4.0 * H);
+    }
     for (int l = 0; l < a.n_layers; l++) {
         const OhLayer &y = m->L[l];
         LayerState &z = s->ls[l];
@@ -1128,53 +1164,65 @@ static int enqueue_body(ornith_hip_session *s, hipStream_t st) {
             CHK(mv_add(b, y.q, an, s->qproj, 0));
             CHK(mv_add(b, y.k, an, s->kb, 0));
             CHK(mv_add(b, y.v, an, s->vb, 0));
-            MVGO(b);
-            LAUNCH(K_ATTN_PREP, 4.0 * (2.0 * aqd + 2.0 * kvd + 2.0 * a.hd) + 8.0 * aqd + 2.0 * (kvd + 4.0 * a.nkv),
-                   oh_launch_attn_prep(s->qproj, s->kb, s->vb, (const float *)y.q_norm->A, (const float *)y.k_norm->A,
-                                       s->rope, s->qr, s->agate, z.Kt, z.Ks, z.Vq, z.Vs, pos, a.nh, a.nkv, a.hd,
-                                       a.rope_dim, s->kvcap, a.eps, st));
+            prog_mv(P, b);
+            {
+                oh_op o = op_new(OH_OP_ATTN_PREP, a.nh + a.nkv);
+                o.u.prep = {s->qproj, s->kb, s->vb, (const float *)y.q_norm->A, (const float *)y.k_norm->A,
+                            (const float *)s->rope, s->qr, s->agate, z.Kt, z.Ks, z.Vq, z.Vs,
+                            a.nh, a.nkv, a.hd, a.rope_dim, s->kvcap, a.eps};
+                prog_add(P, o, K_ATTN_PREP, 4.0 * (2.0 * aqd + 2.0 * kvd + 2.0 * a.hd) + 8.0 * aqd +
+                                                2.0 * (kvd + 4.0 * a.nkv));
+            }
             const float scale = 1.0f / sqrtf((float)a.hd);
             // contexts up to exact_max: scores + the reference-order walk;
             // longer ones: flash chunks + merge (each pair exits for the other)
             const bool ex = s->pos + 1 <= s->exact_max;
-            LAUNCH(K_ATTN_SCORES, ex ? T * a.nkv * (a.hd + 4.0) + 4.0 * T * a.nh + 4.0 * aqd : 0.0,
-                   oh_launch_attn_scores(s->qr, z.Kt, z.Ks, s->scores, pos, a.nh, a.nkv, a.hd, s->kvcap, scale,
-                                         s->exact_max, st));
-            LAUNCH(K_ATTN_OUT, ex ? T * a.nkv * (a.hd + 4.0) + 8.0 * T * a.nh + 8.0 * aqd : 0.0,
-                   oh_launch_attn_out(s->scores, z.Vq, z.Vs, s->agate, s->o, pos, a.nh, a.nkv, a.hd, s->kvcap,
-                                      s->exact_max, st));
+            oh_op_attn at;
+            memset(&at, 0, sizeof at);
+            at.qr = s->qr; at.gate = s->agate; at.Kt = z.Kt; at.Ks = z.Ks; at.Vq = z.Vq; at.Vs = z.Vs;
+            at.scores = s->scores; at.part_o = s->fpo; at.part_ml = s->fpml; at.out = s->o;
+            at.nh = a.nh; at.nkv = a.nkv; at.hd = a.hd; at.cap = s->kvcap; at.exact_max = s->exact_max;
+            at.hb = oh_flash_hb(a.nh, a.nkv); at.scale = scale;
+            const int nch = (s->kvcap + oh_flash_chunk() - 1) / oh_flash_chunk();
             const double nchd = ceil(T / (double)oh_flash_chunk());
-            LAUNCH(K_ATTN_FLASH, ex ? 0.0 : T * a.nkv * (2.0 * a.hd + 8.0) + 4.0 * aqd + 8.0 * nchd * aqd,
-                   oh_launch_attn_flash(s->qr, z.Kt, z.Ks, z.Vq, z.Vs, s->fpo, s->fpml, pos, a.nh, a.nkv, a.hd,
-                                        s->kvcap, scale, s->exact_max, st));
-            LAUNCH(K_ATTN_COMBINE, ex ? 0.0 : 4.0 * nchd * (aqd + 2.0 * a.nh) + 12.0 * aqd,
-                   oh_launch_attn_combine(s->fpo, s->fpml, s->agate, s->o, pos, a.nh, a.nkv, a.hd, s->kvcap,
-                                          s->exact_max, st));
+            oh_op o1 = op_new(OH_OP_ATTN_SCORES, a.nh * ((s->kvcap + 255) / 256));
+            o1.u.attn = at;
+            prog_add(P, o1, K_ATTN_SCORES, ex ? T * a.nkv * (a.hd + 4.0) + 4.0 * T * a.nh + 4.0 * aqd : 0.0);
+            oh_op o2 = op_new(OH_OP_ATTN_OUT, a.nh / (256 / a.hd));
+            o2.u.attn = at;
+            prog_add(P, o2, K_ATTN_OUT, ex ? T * a.nkv * (a.hd + 4.0) + 8.0 * T * a.nh + 8.0 * aqd : 0.0);
+            oh_op o3 = op_new(OH_OP_ATTN_FLASH, a.nkv * (a.nh / a.nkv / at.hb) * nch, oh_flash_lds_bytes(a.nh, a.nkv, a.hd));
+            o3.u.attn = at;
+            prog_add(P, o3, K_ATTN_FLASH, ex ? 0.0 : T * a.nkv * (2.0 * a.hd + 8.0) + 4.0 * aqd + 8.0 * nchd * aqd);
+            oh_op o4 = op_new(OH_OP_ATTN_COMBINE, a.nh * (a.hd / 64));
+            o4.u.attn = at;
+            prog_add(P, o4, K_ATTN_COMBINE, ex ? 0.0 : 4.0 * nchd * (aqd + 2.0 * a.nh) + 12.0 * aqd);
             MvBuild b2;
             Act af;
             af.pro = OH_PRO_F32;
             af.xf = s->o;
             CHK(mv_add(b2, y.o, af, s->x, 1));
-            MVGO(b2);
+            prog_mv(P, b2);
         } else {
             MvBuild b;
             CHK(mv_add(b, y.qkv, an, s->cat, 0));
             CHK(mv_add(b, y.gate, an, s->gate, 0));
             CHK(mv_add(b, y.alpha, an, s->ab, 0));
             CHK(mv_add(b, y.beta, an, s->ab + a.nv, 0));
-            MVGO(b);
+            prog_mv(P, b);
             const float out_scale = 1.0f / sqrtf((float)a.dk);
             const double sb = 8.0 * a.nv * a.dk * a.dv + 8.0 * (a.conv_k - 1) * cc + 4.0 * cc * (a.conv_k + 1) +
                               12.0 * vd + 16.0 * a.nv;
-            LAUNCH(K_DELTA, sb,
-                   oh_launch_delta_step(a.dk, s->cat, s->ab, s->gate, (const float *)y.conv->A, z.conv,
-                                        (const float *)y.ssm_a->A, (const float *)y.dt_bias->A, z.S, s->o, s->osz,
-                                        s->oruns, pos, a.nk, a.nv, a.conv_k, cc, out_scale, st));
+            oh_op o = op_new(OH_OP_DELTA, a.nv * (a.dk / 64), oh_delta_lds_bytes(a.dk));
+            o.u.delta = {s->cat, s->ab, s->gate, (const float *)y.conv->A, (const float *)y.ssm_a->A,
+                         (const float *)y.dt_bias->A, z.conv, z.S, s->o, s->osz, s->oruns,
+                         a.dk, a.nk, a.nv, a.conv_k, cc, out_scale};
+            prog_add(P, o, K_DELTA, sb);
             // per-head gated RMSNorm of the delta output inside the projection
             MvBuild b2;
             CHK(mv_add(b2, y.ssm_out, act_gnorm(s->o, s->osz, s->oruns, (const float *)y.ssm_norm->A, a.eps, a.dv),
                        s->x, 1));
-            MVGO(b2);
+            prog_mv(P, b2);
         }
         // FFN: post_attention_norm (formed inside the first FFN launch), then
         // MoE (or dense SwiGLU)
@@ -1189,7 +1237,7 @@ static int enqueue_body(ornith_hip_session *s, hipStream_t st) {
             MvBuild b;
             CHK(mv_add(b, y.router, pst, s->rl, 0));
             if (y.gate_inp_sh) CHK(mv_add(b, y.gate_inp_sh, pn, s->shl, 0));
-            MVGO(b);
+            prog_mv(P, b);
             // experts gate/up: every block routes first (top-k + softmax), the
             // stacked segments then read the routed experts
             const Act ax = act_of(s->xq, s->xn);
@@ -1218,7 +1266,7 @@ static int enqueue_body(ornith_hip_session *s, hipStream_t st) {
             b2.L.rw = s->ew;
             b2.L.shg = s->shg;
             b2.bytes += 4.0 * a.ne + 8.0 * K;
-            MVGO(b2);
+            prog_mv(P, b2);
             const uint32_t dt = y.down_exps->type;
             const int nbd = I / 256, ns = K + (y.gate_sh ? 1 : 0);
             const int rps = nbd >= 1 ? 64 / nbd : 1;
@@ -1234,7 +1282,9 @@ static int enqueue_body(ornith_hip_session *s, hipStream_t st) {
                 D.h = s->h; D.x = s->x;
                 D.type = (int)dt; D.nb = nbd; D.in = I; D.rows = H; D.k = K; D.stride = IW;
                 const double db = (double)ns * ((double)H * gguf_nbytes(dt, (uint64_t)I) + 4.0 * I) + 8.0 * H + 4.0 * K;
-                LAUNCH(K_MV_DOWN, db, oh_launch_mv_down(&D, (H + rps - 1) / rps, 64 * ns, dlds, st));
+                oh_op o = op_new(OH_OP_MV_DOWN, (H + rps - 1) / rps, dlds);
+                o.u.down = D;
+                prog_add(P, o, K_MV_DOWN, db);
             } else {
                 MvBuild b3;
                 Act ah;
@@ -1248,10 +1298,11 @@ static int enqueue_body(ornith_hip_session *s, hipStream_t st) {
                     if (!paired) a1.xf2 = a0.xf2 + (size_t)K * IW;
                     CHK(mv_add(b3, y.down_sh, a1, s->od + (size_t)K * H, 0));
                 }
-                MVGO(b3);
-                LAUNCH(K_COMBINE, 4.0 * H * (ns + 2),
-                       oh_launch_moe_combine(s->x, s->od, s->ew, K, H, y.gate_sh ? s->od + (size_t)K * H : nullptr,
-                                             y.gate_inp_sh ? s->shg : nullptr, st));
+                prog_mv(P, b3);
+                oh_op o = op_new(OH_OP_MOE_COMBINE, (H + 255) / 256);
+                o.u.comb = {s->x, s->od, s->ew, y.gate_sh ? s->od + (size_t)K * H : nullptr,
+                            y.gate_inp_sh ? s->shg : nullptr, K, H};
+                prog_add(P, o, K_COMBINE, 4.0 * H * (ns + 2));
             }
         } else {
             MvBuild b;
@@ -1262,29 +1313,135 @@ static int enqueue_body(ornith_hip_session *s, hipStream_t st) {
                 CHK(mv_add(b, y.ffn_gate, pn, s->g, 0));
                 CHK(mv_add(b, y.ffn_up, pn, s->u, 0));
             }
-            MVGO(b);
+            prog_mv(P, b);
             MvBuild b2;
             Act ah;
             ah.pro = OH_PRO_F32;
             ah.xf = s->h;
             CHK(mv_add(b2, y.ffn_down, paired ? ah : act_swiglu(s->g, s->u), s->x, 1));
-            MVGO(b2);
+            prog_mv(P, b2);
         }
     }
+    return ORNITH_HIP_OK;
+}
+
+static int build_head(ornith_hip_session *s, Prog &P) {
+    const ornith_hip_model *m = s->m;
+    const ornith_hip_arch &a = m->a;
+    MvBuild b;
+    CHK(mv_add(b, m->lm_head, act_norm(s->x, (const float *)m->out_norm->A, a.eps), s->logits, 0));
+    prog_mv(P, b);
+    oh_op o = op_new(OH_OP_ARGMAX1, OH_ARGMAX_BLOCKS);
+    o.u.am = {s->logits, s->amv, s->ami, a.vocab, OH_ARGMAX_BLOCKS, s->toks, s->io + OH_IO_BEST};
+    prog_add(P, o, K_ARGMAX, 4.0 * a.vocab);
+    o.kind = OH_OP_ARGMAX2;
+    o.nvb = 1;
+    prog_add(P, o, -1, 0.0);
+    return ORNITH_HIP_OK;
+}
+
+// Launch a program operation by operation (records and kind selection as
+// LAUNCH does).
+static int run_prog(ornith_hip_session *s, const Prog &P, hipStream_t st) {
+    for (size_t i = 0; i < P.ops.size(); i++) {
+        if (P.rk[i] < 0) continue;
+        size_t j = i + 1;
+        while (j < P.ops.size() && P.rk[j] < 0) j++;
+        if (!keep(s, P.rk[i], P.bytes[i])) continue;
+        CHK(rec_begin(s, st));
+        for (size_t k = i; k < j; k++) HCHK(oh_launch_op(&P.ops[k], s->io, st));
+        CHK(rec_end(s, st, P.rk[i], P.bytes[i]));
+    }
+    return ORNITH_HIP_OK;
+}
+
+static int enqueue_body(ornith_hip_session *s, hipStream_t st) {
+    Prog P;
+    CHK(build_body(s, P));
+    CHK(run_prog(s, P, st));
     LAUNCH(K_ADVANCE, 8.0, oh_launch_advance(s->io, st));
     return ORNITH_HIP_OK;
 }
 
 static int enqueue_head(ornith_hip_session *s, hipStream_t st) {
-    const ornith_hip_model *m = s->m;
-    const ornith_hip_arch &a = m->a;
-    MvBuild b;
-    CHK(mv_add(b, m->lm_head, act_norm(s->x, (const float *)m->out_norm->A, a.eps), s->logits, 0));
-    MVGO(b);
-    LAUNCH(K_ARGMAX, 4.0 * a.vocab,
-           oh_launch_argmax(s->logits, a.vocab, s->amv, s->ami, OH_ARGMAX_BLOCKS, s->toks, s->io, s->io + 1, st));
+    Prog P;
+    CHK(build_head(s, P));
+    return run_prog(s, P, st);
+}
+
+// ---- the persistent step kernel -------------------------------------------------------------------
+// ORNITH_HIP_STEP=1 selects the persistent step kernel for decode steps;
+// otherwise each operation is its own launch (HIP graphs)
+static bool step_enabled() {
+    const char *e = getenv("ORNITH_HIP_STEP");
+    return e && e[0] == '1';
+}
+
+static int step_upload(ornith_hip_session *s, const Prog &P, ornith_hip_session::StepProg &sp) {
+    sp.n = (int)P.ops.size();
+    sp.lds = P.lds;
+    sp.bytes = 0.0;
+    for (double b : P.bytes) sp.bytes += b;
+    CHK(salloc(s, &sp.ops, P.ops.size()));
+    HCHK(hipMemcpy(sp.ops, P.ops.data(), P.ops.size() * sizeof(oh_op), hipMemcpyHostToDevice));
+    CHK(salloc(s, &sp.ctrs, P.ops.size() * OH_STEP_NCTR * OH_STEP_CSTRIDE));
     return ORNITH_HIP_OK;
 }
+
+// Build and upload the body and head programs once per session. The grid is
+// two resident 256-thread blocks per CU (one when the LDS does not allow
+// two), a multiple of OH_STEP_NCTR; matvecs are planned for its waves.
+// Returns ORNITH_HIP_OK with step_grid == 0 when the device cannot run it.
+static int step_prepare(ornith_hip_session *s) {
+    if (s->step_tried) return ORNITH_HIP_OK;
+    s->step_tried = true;
+    const int dev = s->m->ctx->device;
+    int coop = 0, cus = 0;
+    HCHK(hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev));
+    HCHK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+    if (!coop || cus <= 0) return ORNITH_HIP_OK;
+    for (int per = 2; per >= 1; per--) {
+        const int grid = per * cus / OH_STEP_NCTR * OH_STEP_NCTR;
+        if (grid < OH_STEP_NCTR) return ORNITH_HIP_OK;
+        Prog B, Hd;
+        B.waves = Hd.waves = grid * 4;
+        CHK(build_body(s, B));
+        CHK(build_head(s, Hd));
+        const int lds = B.lds > Hd.lds ? B.lds : Hd.lds;
+        int fit = 0;
+        HCHK(oh_step_blocks_per_cu(lds, &fit));
+        if (fit < per) continue;
+        CHK(step_upload(s, B, s->sp_body));
+        CHK(step_upload(s, Hd, s->sp_head));
+        s->sp_body_rk = B.rk;
+        s->sp_body.lds = s->sp_head.lds = lds;
+        s->step_grid = grid;
+        return ORNITH_HIP_OK;
+    }
+    return ORNITH_HIP_OK;
+}
+
+// advance: the body moves the position on (a replay for timing does not)
+static int step_launch(ornith_hip_session *s, bool body, uint64_t *ts, bool advance = true) {
+    const ornith_hip_session::StepProg &sp = body ? s->sp_body : s->sp_head;
+    HCHK(oh_launch_step(sp.ops, sp.n, s->io, sp.ctrs, body ? OH_IO_EPOCH_BODY : OH_IO_EPOCH_HEAD,
+                        body && advance ? 1 : 0, ts, s->step_grid, sp.lds, s->m->ctx->st));
+    return ORNITH_HIP_OK;
+}
+
+// a grid wait of the step kernel that gave up leaves io[OH_IO_ERR] set
+static int step_check(ornith_hip_session *s) {
+    if (!s->step_grid) return ORNITH_HIP_OK;
+    int32_t err = 0;
+    HCHK(hipMemcpy(&err, s->io + OH_IO_ERR, 4, hipMemcpyDeviceToHost));
+    if (err) {
+        seterr("step kernel: a grid barrier timed out; the session state is undefined");
+        return ORNITH_HIP_ERR_DEVICE;
+    }
+    return ORNITH_HIP_OK;
+}
+
+
 
 static int capture(ornith_hip_session *s, int (*fn)(ornith_hip_session *, hipStream_t), hipGraphExec_t *out) {
     hipStream_t st = s->m->ctx->st;
@@ -1307,6 +1464,10 @@ static bool graphs_enabled() {
 
 static int run_body(ornith_hip_session *s) {
     hipStream_t st = s->m->ctx->st;
+    if (step_enabled()) {
+        CHK(step_prepare(s));
+        if (s->step_grid) return step_launch(s, true, nullptr);
+    }
     if (graphs_enabled()) {
         if (!s->gbody) CHK(capture(s, enqueue_body, &s->gbody));
         HCHK(hipGraphLaunch(s->gbody, st));
@@ -1316,6 +1477,10 @@ static int run_body(ornith_hip_session *s) {
 }
 static int run_head(ornith_hip_session *s) {
     hipStream_t st = s->m->ctx->st;
+    if (step_enabled()) {
+        CHK(step_prepare(s));
+        if (s->step_grid) return step_launch(s, false, nullptr);
+    }
     if (graphs_enabled()) {
         if (!s->ghead) CHK(capture(s, enqueue_head, &s->ghead));
         HCHK(hipGraphLaunch(s->ghead, st));
@@ -1347,6 +1512,7 @@ extern "C" int ornith_hip_session_eval(ornith_hip_session *s, const int32_t *tok
     for (int i = 0; i < n; i++) CHK(run_body(s));
     CHK(run_head(s));
     HCHK(hipStreamSynchronize(st));
+    CHK(step_check(s));
     s->pos += n;
     s->have_logits = true;
     return ORNITH_HIP_OK;
@@ -1382,12 +1548,14 @@ extern "C" int ornith_hip_session_generate(ornith_hip_session *s, int n_predict,
         for (int i = 0; i < n; i++) { CHK(run_body(s)); CHK(run_head(s)); }
         HCHK(hipMemcpyAsync(out_tokens, s->toks + s->pos, (size_t)n * 4, hipMemcpyDeviceToHost, st));
         HCHK(hipStreamSynchronize(st));
+        CHK(step_check(s));
         emitted = n;
     } else {
         for (int i = 0; i < n; i++) {
             int32_t next;
             HCHK(hipMemcpyAsync(&next, s->toks + s->pos + i, 4, hipMemcpyDeviceToHost, st));
             HCHK(hipStreamSynchronize(st));
+            CHK(step_check(s));
             if (next == eos) break;
             out_tokens[emitted++] = next;
             CHK(run_body(s));
@@ -1406,7 +1574,8 @@ extern "C" int ornith_hip_session_time_decode(ornith_hip_session *s, int n_steps
     HCHK(hipSetDevice(s->m->ctx->device));
     hipStream_t st = s->m->ctx->st;
     CHK(sync_pos(s));
-    if (graphs_enabled()) {
+    if (step_enabled()) CHK(step_prepare(s));
+    if (!s->step_grid && graphs_enabled()) {
         if (!s->gbody) CHK(capture(s, enqueue_body, &s->gbody));
         if (!s->ghead) CHK(capture(s, enqueue_head, &s->ghead));
     }
@@ -1421,6 +1590,7 @@ extern "C" int ornith_hip_session_time_decode(ornith_hip_session *s, int n_steps
     HCHK(hipEventElapsedTime(&el, e0, e1));
     (void)hipEventDestroy(e0);
     (void)hipEventDestroy(e1);
+    CHK(step_check(s));
     s->pos += n_steps;
     *ms = el;
     return ORNITH_HIP_OK;
@@ -1636,6 +1806,34 @@ extern "C" int ornith_hip_session_time_kind(ornith_hip_session *s, int kind, int
     hipStream_t st = s->m->ctx->st;
     CHK(sync_pos(s));
     HCHK(hipStreamSynchronize(st));
+    if (kind == K_STEP_BODY || kind == K_STEP_HEAD) {
+        // back-to-back launches of one step-kernel program at the current
+        // position (the body does not advance); bytes at this position
+        const bool body = kind == K_STEP_BODY;
+        CHK(step_prepare(s));
+        if (!s->step_grid) { seterr("time_kind: the step kernel is not available"); return ORNITH_HIP_ERR_UNSUPPORTED; }
+        Prog P;
+        CHK(body ? build_body(s, P) : build_head(s, P));
+        double by = 0.0;
+        for (double b : P.bytes) by += b;
+        CHK(step_launch(s, body, nullptr, false));
+        hipEvent_t a0 = nullptr, a1 = nullptr;
+        HCHK(hipEventCreate(&a0));
+        HCHK(hipEventCreate(&a1));
+        HCHK(hipEventRecord(a0, st));
+        for (int i = 0; i < reps; i++) CHK(step_launch(s, body, nullptr, false));
+        HCHK(hipEventRecord(a1, st));
+        HCHK(hipEventSynchronize(a1));
+        float el = 0.0f;
+        HCHK(hipEventElapsedTime(&el, a0, a1));
+        (void)hipEventDestroy(a0);
+        (void)hipEventDestroy(a1);
+        CHK(step_check(s));
+        *us_per_launch = el * 1000.0f / (float)reps;
+        *bytes_per_launch = by;
+        *launches_per_step = 1;
+        return ORNITH_HIP_OK;
+    }
     hipEvent_t e0 = nullptr, e1 = nullptr;
     HCHK(hipEventCreate(&e0));
     HCHK(hipEventCreate(&e1));
@@ -1699,5 +1897,35 @@ extern "C" int ornith_hip_session_profile_step(ornith_hip_session *s, int max_la
     s->rec_ev.clear();
     if (r) return r;
     HCHK(e);
+    return ORNITH_HIP_OK;
+}
+
+// ---- phases of one step-kernel body launch (block 0's clock after each barrier) --------------------
+extern "C" int ornith_hip_session_profile_phases(ornith_hip_session *s, int max_phases, int32_t *kinds,
+                                                 double *bytes, float *us, int *n_phases) {
+    *n_phases = 0;
+    if (!s->have_logits) { seterr("session has no logits; eval a prompt first"); return ORNITH_HIP_ERR_FORMAT; }
+    HCHK(hipSetDevice(s->m->ctx->device));
+    hipStream_t st = s->m->ctx->st;
+    CHK(sync_pos(s));
+    CHK(step_prepare(s));
+    if (!s->step_grid) { seterr("profile_phases: the step kernel is not available"); return ORNITH_HIP_ERR_UNSUPPORTED; }
+    if (!s->ts) CHK(salloc(s, &s->ts, (size_t)s->sp_body.n + 8));
+    Prog P;
+    CHK(build_body(s, P));
+    CHK(step_launch(s, true, nullptr, false));        // warm
+    CHK(step_launch(s, true, s->ts, false));
+    HCHK(hipStreamSynchronize(st));
+    CHK(step_check(s));
+    const int n = s->sp_body.n;
+    std::vector<uint64_t> t((size_t)n + 1);
+    HCHK(hipMemcpy(t.data(), s->ts, t.size() * 8, hipMemcpyDeviceToHost));
+    const int m = n < max_phases ? n : max_phases;
+    for (int i = 0; i < m; i++) {
+        kinds[i] = i < (int)P.rk.size() ? P.rk[i] : -1;
+        bytes[i] = i < (int)P.bytes.size() ? P.bytes[i] : 0.0;
+        us[i] = (float)((double)(t[i + 1] - t[i]) / 100.0);   // 100 MHz real-time clock
+    }
+    *n_phases = m;
     return ORNITH_HIP_OK;
 }

@@ -3,6 +3,7 @@
 #include "oh_mv.hip"
 #include "oh_layers.hip"
 #include "oh_synth.hip"
+#include "oh_step.hip"
 #include "oh_launch.h"
 
 extern "C" {
@@ -12,12 +13,6 @@ hipError_t oh_launch_matvec(const oh_mvlaunch *L, int tk, int lds_bytes, hipStre
     void (*k)(oh_mvlaunch) = tk == OH_Q4_K ? oh_k_mv_q4k : tk == OH_Q6_K ? oh_k_mv_q6k
                            : tk == OH_Q8_0 ? oh_k_mv_q80 : oh_k_mv_mixed;
     hipLaunchKernelGGL(k, dim3(L->total_blocks), dim3(256), (size_t)lds_bytes, st, *L);
-    return hipGetLastError();
-}
-
-hipError_t oh_launch_mv_down(const oh_mvdown *D, int blocks, int threads, int lds_bytes, hipStream_t st) {
-    if (blocks <= 0) return hipSuccess;
-    hipLaunchKernelGGL(oh_k_mv_down, dim3(blocks), dim3(threads), (size_t)lds_bytes, st, *D);
     return hipGetLastError();
 }
 
@@ -43,102 +38,76 @@ hipError_t oh_launch_dequant(const uint8_t *A, const uint8_t *B, const uint8_t *
     return hipGetLastError();
 }
 
-hipError_t oh_launch_embed(const uint8_t *A, const uint8_t *B, const uint8_t *C, int type, int in,
-                           const int32_t *toks, const int32_t *io_pos, float *x, hipStream_t st) {
-    hipLaunchKernelGGL(oh_k_embed, dim3((in + 255) / 256), dim3(256), 0, st, A, B, C, type, in, toks, io_pos, x);
-    return hipGetLastError();
-}
 
-hipError_t oh_launch_delta_step(int dk, const float *cat, const float *ab, const float *gate,
-                                const float *conv_w, float *conv_state, const float *ssm_a,
-                                const float *dt_bias, float *S, float *out, float *out_gate, double *out_runs,
-                                const int32_t *io_pos, int nk, int nv, int K, int cc, float out_scale,
-                                hipStream_t st) {
-    if (dk == 128) {
-        hipLaunchKernelGGL(oh_k_delta_step<128>, dim3(nv * 2), dim3(64), 0, st, cat, ab, gate, conv_w, conv_state,
-                           ssm_a, dt_bias, S, out, out_gate, out_runs, io_pos, nk, nv, K, cc, out_scale);
-    } else if (dk == 64) {
-        hipLaunchKernelGGL(oh_k_delta_step<64>, dim3(nv), dim3(64), 0, st, cat, ab, gate, conv_w, conv_state,
-                           ssm_a, dt_bias, S, out, out_gate, out_runs, io_pos, nk, nv, K, cc, out_scale);
-    } else {
-        return hipErrorInvalidValue;
+hipError_t oh_launch_op(const oh_op *op, const int32_t *io, hipStream_t st) {
+    if (op->nvb <= 0) return hipSuccess;
+    const dim3 g(op->nvb), b256(256);
+    switch (op->kind) {
+    case OH_OP_MV:
+        return oh_launch_matvec(&op->u.mv, op->tk, op->lds, st);
+    case OH_OP_MV_DOWN: {
+        const int ns = op->u.down.k + (op->u.down.sA ? 1 : 0);
+        hipLaunchKernelGGL(oh_k_mv_down, g, dim3(64 * ns), (size_t)op->lds, st, op->u.down);
+        break;
+    }
+    case OH_OP_EMBED: hipLaunchKernelGGL(oh_k_embed, g, b256, 0, st, op->u.embed, io); break;
+    case OH_OP_DELTA:
+        if (op->u.delta.K > 8) return hipErrorInvalidValue;
+        if (op->u.delta.dk == 128) {
+            if (op->u.delta.K <= 4) hipLaunchKernelGGL((oh_k_delta_step<128, 4>), g, dim3(64), 0, st, op->u.delta, io);
+            else hipLaunchKernelGGL((oh_k_delta_step<128, 8>), g, dim3(64), 0, st, op->u.delta, io);
+        } else if (op->u.delta.dk == 64) {
+            if (op->u.delta.K <= 4) hipLaunchKernelGGL((oh_k_delta_step<64, 4>), g, dim3(64), 0, st, op->u.delta, io);
+            else hipLaunchKernelGGL((oh_k_delta_step<64, 8>), g, dim3(64), 0, st, op->u.delta, io);
+        } else {
+            return hipErrorInvalidValue;
+        }
+        break;
+    case OH_OP_ATTN_PREP: hipLaunchKernelGGL(oh_k_attn_prep, g, b256, 0, st, op->u.prep, io); break;
+    case OH_OP_ATTN_SCORES: hipLaunchKernelGGL(oh_k_attn_scores, g, b256, 0, st, op->u.attn, io); break;
+    case OH_OP_ATTN_OUT: hipLaunchKernelGGL(oh_k_attn_out, g, b256, 0, st, op->u.attn, io); break;
+    case OH_OP_ATTN_FLASH:
+        if (op->u.attn.hb == 2) hipLaunchKernelGGL(oh_k_attn_flash<2>, g, b256, (size_t)op->lds, st, op->u.attn, io);
+        else hipLaunchKernelGGL(oh_k_attn_flash<1>, g, b256, (size_t)op->lds, st, op->u.attn, io);
+        break;
+    case OH_OP_ATTN_COMBINE: hipLaunchKernelGGL(oh_k_attn_combine, g, b256, 0, st, op->u.attn, io); break;
+    case OH_OP_MOE_COMBINE: hipLaunchKernelGGL(oh_k_moe_combine, g, b256, 0, st, op->u.comb); break;
+    case OH_OP_ARGMAX1: hipLaunchKernelGGL(oh_k_argmax1, g, b256, 0, st, op->u.am); break;
+    case OH_OP_ARGMAX2: hipLaunchKernelGGL(oh_k_argmax2, dim3(1), dim3(64), 0, st, op->u.am, io); break;
+    default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
 }
 
-hipError_t oh_launch_attn_prep(const float *qproj, const float *kin, const float *vin,
-                               const float *q_norm, const float *k_norm, const float2 *rope,
-                               float *qr, float *gate, uint32_t *Kt, float *Ks, int8_t *Vq,
-                               float *Vs, const int32_t *io_pos, int nh, int nkv, int hd,
-                               int rot, int cap, float eps, hipStream_t st) {
-    hipLaunchKernelGGL(oh_k_attn_prep, dim3(nh + nkv), dim3(256), 0, st, qproj, kin, vin, q_norm, k_norm,
-                       rope, qr, gate, Kt, Ks, Vq, Vs, io_pos, nh, nkv, hd, rot, cap, eps);
-    return hipGetLastError();
-}
-
-hipError_t oh_launch_attn_scores(const float *qr, const uint32_t *Kt, const float *Ks,
-                                 float *scores, const int32_t *io_pos, int nh, int nkv, int hd,
-                                 int cap, float scale, int exact_max, hipStream_t st) {
-    hipLaunchKernelGGL(oh_k_attn_scores, dim3(nh, (cap + 255) / 256), dim3(256), 0, st, qr, Kt, Ks,
-                       scores, io_pos, nh, nkv, hd, cap, scale, exact_max);
-    return hipGetLastError();
-}
-
-hipError_t oh_launch_attn_out(const float *scores, const int8_t *Vq, const float *Vs, const float *gate,
-                              float *out, const int32_t *io_pos, int nh, int nkv, int hd, int cap,
-                              int exact_max, hipStream_t st) {
-    hipLaunchKernelGGL(oh_k_attn_out, dim3(nh / (256 / hd)), dim3(256), 0, st, scores, Vq, Vs, gate, out,
-                       io_pos, nh, nkv, hd, cap, exact_max);
-    return hipGetLastError();
-}
-
 // query heads per flash block: two (one when the group has a single head)
-static int flash_hb(int nh, int nkv) { return nh / nkv >= 2 ? 2 : 1; }
+int oh_flash_hb(int nh, int nkv) { return nh / nkv >= 2 ? 2 : 1; }
 
 int oh_flash_lds_bytes(int nh, int nkv, int hd) {
-    const int HB = flash_hb(nh, nkv);
+    const int HB = oh_flash_hb(nh, nkv);
     return HB * (hd + 16) * 4 + kFlashCh * (hd / 4 + 1) * 4 + 16 + (kFlashCh / 16) * hd * 16 + HB * kFlashCh * 4 +
            2 * kFlashCh * 4;
 }
 int oh_flash_chunk(void) { return kFlashCh; }
 
-hipError_t oh_launch_attn_flash(const float *qr, const uint32_t *Kt, const float *Ks, const int8_t *Vq,
-                                const float *Vs, float *part_o, float *part_ml, const int32_t *io_pos,
-                                int nh, int nkv, int hd, int cap, float scale, int exact_max, hipStream_t st) {
-    const int HB = flash_hb(nh, nkv), G = nh / nkv;
-    void (*k)(const float *, const uint32_t *, const float *, const int8_t *, const float *, float *, float *,
-              const int32_t *, int, int, int, int, float, int) = HB == 2 ? oh_k_attn_flash<2> : oh_k_attn_flash<1>;
-    hipLaunchKernelGGL(k, dim3(nkv * (G / HB), (cap + kFlashCh - 1) / kFlashCh), dim3(256),
-                       (size_t)oh_flash_lds_bytes(nh, nkv, hd), st, qr, Kt, Ks, Vq, Vs, part_o, part_ml, io_pos,
-                       nh, nkv, hd, cap, scale, exact_max);
-    return hipGetLastError();
+// delta step LDS of the working wave (step kernel: dynamic LDS)
+int oh_delta_lds_bytes(int dk) { return (2 * dk + 64 * (dk + 4)) * 4; }
+
+hipError_t oh_step_blocks_per_cu(int lds_bytes, int *blocks) {
+    hipError_t e = hipFuncSetAttribute((const void *)oh_k_step, hipFuncAttributeMaxDynamicSharedMemorySize, lds_bytes);
+    if (e != hipSuccess) return e;
+    return hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks, (const void *)oh_k_step, 256, (size_t)lds_bytes);
 }
 
-hipError_t oh_launch_attn_combine(const float *part_o, const float *part_ml, const float *gate, float *out,
-                                  const int32_t *io_pos, int nh, int nkv, int hd, int cap, int exact_max,
-                                  hipStream_t st) {
-    hipLaunchKernelGGL(oh_k_attn_combine, dim3(nh, hd / 64), dim3(256), 0, st, part_o, part_ml, gate, out,
-                       io_pos, nh, nkv, hd, cap, exact_max);
-    return hipGetLastError();
+hipError_t oh_launch_step(const oh_op *prog, int nops, int32_t *io, unsigned *ctrs, int epoch_slot, int advance,
+                          uint64_t *ts, int grid, int lds_bytes, hipStream_t st) {
+    void *args[] = {(void *)&prog, (void *)&nops, (void *)&io, (void *)&ctrs, (void *)&epoch_slot,
+                    (void *)&advance, (void *)&ts};
+    return hipLaunchCooperativeKernel((const void *)oh_k_step, dim3(grid), dim3(256), args, (size_t)lds_bytes, st);
 }
 
 hipError_t oh_launch_moe_route(const float *logits, int ne, int k, const float *shgate_logit,
                                int32_t *idx, float *w, float *shgate, hipStream_t st) {
     hipLaunchKernelGGL(oh_k_moe_route, dim3(1), dim3(64), 0, st, logits, ne, k, shgate_logit, idx, w, shgate);
-    return hipGetLastError();
-}
-
-hipError_t oh_launch_moe_combine(float *x, const float *o, const float *w, int k, int H,
-                                 const float *so, const float *shgate, hipStream_t st) {
-    hipLaunchKernelGGL(oh_k_moe_combine, dim3((H + 255) / 256), dim3(256), 0, st, x, o, w, k, H, so, shgate);
-    return hipGetLastError();
-}
-
-hipError_t oh_launch_argmax(const float *v, int n, float *tmp_v, int *tmp_i, int nblk,
-                            int32_t *toks, const int32_t *io_pos, int32_t *io_best,
-                            hipStream_t st) {
-    hipLaunchKernelGGL(oh_k_argmax1, dim3(nblk), dim3(256), 0, st, v, n, tmp_v, tmp_i);
-    hipLaunchKernelGGL(oh_k_argmax2, dim3(1), dim3(64), 0, st, tmp_v, tmp_i, nblk, toks, io_pos, io_best);
     return hipGetLastError();
 }
 

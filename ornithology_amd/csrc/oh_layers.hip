@@ -13,15 +13,15 @@ namespace {
 // decode element i of row r of a plane-layout tensor (src/ornith_quant.c)
 OH_DEV float dec_elem(const uint8_t *A, const uint8_t *B, const uint8_t *C, int type,
                       int in, int64_t r, int i) {
-    if (type == OH_F32) return ((const float *)A)[r * in + i];
-    if (type == OH_F16) return h2f(((const uint16_t *)A)[r * in + i]);
-    if (type == OH_BF16) return u2f((uint32_t)((const uint16_t *)A)[r * in + i] << 16);
+    if (type == OH_F32) return ldg((const float *)A + r * in + i);
+    if (type == OH_F16) return h2f(ldg((const uint16_t *)A + r * in + i));
+    if (type == OH_BF16) return u2f((uint32_t)ldg((const uint16_t *)A + r * in + i) << 16);
     const int nb = in / 256, b = i / 256, k = i % 256;
     const int64_t bi = r * nb + b;
     if (type == OH_Q4_K) {
-        const uint4 hdr = *(const uint4 *)(B + bi * 16);
+        const uint4 hdr = ldg((const uint4 *)(B + bi * 16));
         const int j = k / 32, l = k % 32;
-        const uint8_t q = A[oh_a_off(OH_Q4_K, bi, 32 * (j / 2) + l)];
+        const uint8_t q = ldg(A + oh_a_off(OH_Q4_K, bi, 32 * (j / 2) + l));
         int sc, mn;
         q4k_sm(hdr, j, sc, mn);
         const float d1 = h2f((uint16_t)(hdr.x & 0xffffu)) * sc;
@@ -30,20 +30,20 @@ OH_DEV float dec_elem(const uint8_t *A, const uint8_t *B, const uint8_t *C, int 
     }
     if (type == OH_Q6_K) {
         const int hh = k / 128, kk = k % 128, qd = kk / 32, l = kk % 32;
-        const uint8_t ql = A[oh_a_off(OH_Q6_K, bi, 64 * hh + l + 32 * (qd & 1))];
-        const uint8_t qh = A[oh_a_off(OH_Q6_K, bi, 128 + 32 * hh + l)];
+        const uint8_t ql = ldg(A + oh_a_off(OH_Q6_K, bi, 64 * hh + l + 32 * (qd & 1)));
+        const uint8_t qh = ldg(A + oh_a_off(OH_Q6_K, bi, 128 + 32 * hh + l));
         const int lo = (qd < 2) ? (ql & 15) : (ql >> 4);
         const int q = (lo | (((qh >> (2 * qd)) & 3) << 4)) - 32;
-        const int8_t sc = (int8_t)B[bi * 16 + 8 * hh + l / 16 + 2 * qd];
-        return h2f(*(const uint16_t *)(C + bi * 2)) * (float)sc * (float)q;
+        const int8_t sc = (int8_t)ldg(B + bi * 16 + 8 * hh + l / 16 + 2 * qd);
+        return h2f(ldg((const uint16_t *)(C + bi * 2))) * (float)sc * (float)q;
     }
     if (type == OH_Q8_0)
-        return (float)(int8_t)A[oh_a_off(OH_Q8_0, bi, k)] * h2f(*(const uint16_t *)(B + bi * 16 + 2 * (k / 32)));
+        return (float)(int8_t)ldg(A + oh_a_off(OH_Q8_0, bi, k)) * h2f(ldg((const uint16_t *)(B + bi * 16 + 2 * (k / 32))));
     if (type == OH_IQ2_XXS) {
-        const float dd = h2f(*(const uint16_t *)(C + bi * 2));
+        const float dd = h2f(ldg((const uint16_t *)(C + bi * 2)));
         const uint32_t *q = (const uint32_t *)(A + bi * 64);
         const int g32 = k / 32, kk = (k % 32) / 8, j = k % 8;
-        const uint32_t w0 = q[2 * g32], w1 = q[2 * g32 + 1];
+        const uint32_t w0 = ldg(q + 2 * g32), w1 = ldg(q + 2 * g32 + 1);
         const float db = dd * (0.5f + (float)(w1 >> 28)) * 0.25f;
         const uint64_t gv = k_iq2_grid[(w0 >> (8 * kk)) & 0xffu];
         const uint32_t s7 = (w1 >> (7 * kk)) & 127u;
@@ -56,7 +56,7 @@ OH_DEV float dec_elem(const uint8_t *A, const uint8_t *B, const uint8_t *C, int 
 // block-wide (256 threads) double sum, tree-ordered; every thread gets it
 OH_DEV double block_sum_d(double v, double *red) {
     v = wave_sum_d(v);
-    const int w = (int)(threadIdx.x >> 6);
+    const int w = (tid_x() >> 6);
     __syncthreads();
     if (lane_id() == 0) red[w] = v;
     __syncthreads();
@@ -66,49 +66,62 @@ OH_DEV double block_sum_d(double v, double *red) {
 } // namespace
 
 // ---- embedding (src/ornith_rforward.c:199-208) --------------------------------
-extern "C" __global__ void __launch_bounds__(256)
-oh_k_embed(const uint8_t *A, const uint8_t *B, const uint8_t *C, int type, int in,
-           const int32_t *toks, const int32_t *io_pos, float *x) {
-    const int32_t tok = toks[*io_pos];
-    const int i = (int)(blockIdx.x * 256 + threadIdx.x);
-    if (i < in) x[i] = dec_elem(A, B, C, type, in, tok, i);
+// The token id at toks[pos] was written by an earlier launch (or the host).
+template <class W>
+OH_DEV void embed_body(const oh_op_embed &a, int vb, int pos, W &w) {
+    if (!w.wait()) return;
+    const int32_t tok = ldg(a.toks + pos);
+    const int i = vb * 256 + tid_x();
+    if (i < a.in) stc(a.x + i, dec_elem(a.A, a.B, a.C, a.type, a.in, tok, i));
 }
 
 // ---- gated delta-net decode step (src/ornith_rforward.c:457-503,300-319,
 //      src/ornith_attn.c:198-213,370-388) -----------------------------------------
-// One wave per 64 state rows of one value head (grid nv * DK/64). The state S
-// of value head hv is row-major in HBM (element (r, c) at S[hv][r][c], the
-// reference's layout). The wave reads its 64 x DK slab with contiguous 16-byte
-// loads, all issued right after the step's small inputs (vector loads
-// complete in order), transposes it through LDS so each lane walks its own row
+// One wave per 64 state rows of one value head (virtual block vb of nv * DK/64;
+// in a 256-thread block only wave 0 works, the others take part in the grid
+// wait). The state S of value head hv is row-major in HBM (element (r, c) at
+// S[hv][r][c], the reference's layout). The wave reads its 64 x DK slab with
+// contiguous 16-byte loads, issued first (the state does not depend on the
+// previous phase), transposes it through LDS so each lane walks its own row
 // in the reference's order, and writes it back the same way. The output is
 // o * 1/sqrt(dk) per row, silu(gate) per row and the sum of o^2 over the
 // wave's rows; the per-head gated RMSNorm is applied by the consumer (the
-// ssm_out projection prologue). The conv window is
-// double-buffered by position parity: the step reads window[p] and the
-// channel's single owner writes window[1-p], so waves sharing a key head never
-// race.
-template <int DK>
-__global__ void __launch_bounds__(64)
-oh_k_delta_step(const float *cat, const float *ab, const float *gate, const float *conv_w,
-                float *conv_state, const float *ssm_a, const float *dt_bias, float *S, float *out,
-                float *out_gate, double *out_runs, const int32_t *io_pos, int nk, int nv, int K, int cc,
-                float out_scale) {
+// ssm_out projection prologue). The conv window is double-buffered by position
+// parity: the step reads window[p] and the channel's single owner writes
+// window[1-p], so waves sharing a key head never race. lds: 2*DK + 64*(DK+4)
+// floats for the working wave.
+template <int DK, int KMAX, class W>
+OH_DEV void delta_body(const oh_op_delta &a, int vb, int pos, float *lds, W &w) {
     // TS: LDS row stride padded by 4 floats; with 16-byte accesses every
     // 16-lane pass of a row-per-lane walk and of a coalesced row copy covers
-    // all 64 banks once
-    constexpr int KMAX = 8, NQ = DK / 64, TS = DK + 4;
-    __shared__ float qn[DK], kn[DK];
-    __shared__ __align__(16) float tile[64 * TS];
-    const int lane = (int)threadIdx.x;
-    const int hv = (int)blockIdx.x / NQ, slab = (int)blockIdx.x % NQ;
+    // all 64 banks once. KMAX >= conv_k bounds the conv taps held in registers.
+    constexpr int NQ = DK / 64, TS = DK + 4;
+    float *qn = lds, *kn = lds + DK, *tile = lds + 2 * DK;
+    const bool act = tid_x() < 64;
+    const int lane = lane_id();
+    const int nk = a.nk, nv = a.nv, K = a.K, cc = a.cc;
+    const int hv = vb / NQ, slab = vb % NQ;
     const int r = slab * 64 + lane, kh = hv % nk, qd = nk * DK;
-    const int pos = *io_pos, p = pos & 1;
-    const float *win = conv_state + (size_t)p * (K - 1) * cc;
-    float *nwin = conv_state + (size_t)(1 - p) * (K - 1) * cc;
+    const int p = pos & 1;
+    const float *win = a.conv_state + (size_t)p * (K - 1) * cc;
+    float *nwin = a.conv_state + (size_t)(1 - p) * (K - 1) * cc;
+    // the state slab: rows [slab*64, +64) of head hv, contiguous
+    float4 st[DK / 4];
+    if (act) {
+        const float4 *Sr = (const float4 *)(a.S + ((size_t)hv * DK + slab * 64) * DK);
+#pragma unroll
+        for (int i = 0; i < DK / 4; i++) st[i] = ldg(Sr + lane + 64 * i);
+    }
+    if (!w.wait() || !act) return;
+    // slab -> LDS, row-padded (frees the slab's registers for the step)
+#pragma unroll
+    for (int i = 0; i < DK / 4; i++) {
+        const int f = lane + 64 * i, row = (4 * f) / DK, col = (4 * f) % DK;
+        *(float4 *)(tile + row * TS + col) = make_float4(st[i].x, st[i].y, st[i].z, st[i].w);
+    }
 
-    // small inputs first: for channel a: q channels kh*DK + lane + 64i (i < NQ),
-    // k channels likewise, then this row's v channel
+    // channels of a: q channels kh*DK + lane + 64i (i < NQ), k channels
+    // likewise, then this row's v channel
     constexpr int NCH = 2 * NQ + 1;
     int ch[NCH];
 #pragma unroll
@@ -119,41 +132,35 @@ oh_k_delta_step(const float *cat, const float *ab, const float *gate, const floa
     ch[2 * NQ] = 2 * qd + hv * DK + r;
     float cw[NCH][KMAX], wv[NCH][KMAX], cx[NCH];
 #pragma unroll
-    for (int a = 0; a < NCH; a++) {
+    for (int c = 0; c < NCH; c++) {
 #pragma unroll
         for (int j = 0; j < KMAX; j++) {
-            cw[a][j] = j < K ? conv_w[(size_t)ch[a] * K + j] : 0.0f;
-            wv[a][j] = j < K - 1 ? win[(size_t)j * cc + ch[a]] : 0.0f;
+            cw[c][j] = j < K ? ldg(a.conv_w + (size_t)ch[c] * K + j) : 0.0f;
+            wv[c][j] = j < K - 1 ? ldg(win + (size_t)j * cc + ch[c]) : 0.0f;
         }
-        cx[a] = cat[ch[a]];
+        cx[c] = ldc(a.cat + ch[c]);
     }
-    const float sa = ssm_a[hv], av = ab[hv], bv = ab[nv + hv], dtb = dt_bias[hv];
-    const float gz = gate[(size_t)hv * DK + r];
-    // then the state slab: rows [slab*64, +64) of head hv, contiguous
-    const float4 *Sr = (const float4 *)(S + ((size_t)hv * DK + slab * 64) * DK);
-    float4 st[DK / 4];
-#pragma unroll
-    for (int i = 0; i < DK / 4; i++) st[i] = Sr[lane + 64 * i];
-    __builtin_amdgcn_sched_barrier(0);
+    const float sa = ldg(a.ssm_a + hv), av = ldc(a.ab + hv), bv = ldc(a.ab + nv + hv), dtb = ldg(a.dt_bias + hv);
+    const float gz = ldc(a.gate + (size_t)hv * DK + r);
 
     // causal depthwise conv (no bias) + SiLU
     float cv[NCH];
 #pragma unroll
-    for (int a = 0; a < NCH; a++) {
+    for (int c = 0; c < NCH; c++) {
         float acc = 0.0f, wl = 0.0f;
 #pragma unroll
         for (int j = 0; j < KMAX; j++) {
-            if (j < K - 1) acc += cw[a][j] * wv[a][j];
-            if (j == K - 1) wl = cw[a][j];
+            if (j < K - 1) acc += cw[c][j] * wv[c][j];
+            if (j == K - 1) wl = cw[c][j];
         }
-        acc += wl * cx[a];
-        cv[a] = ref_silu(acc);
-        const bool owner = a == 2 * NQ || (hv < nk && slab == 0);
+        acc += wl * cx[c];
+        cv[c] = ref_silu(acc);
+        const bool owner = c == 2 * NQ || (hv < nk && slab == 0);
         if (owner) {
 #pragma unroll
             for (int j = 0; j + 1 < KMAX; j++)
-                if (j + 1 < K - 1) nwin[(size_t)j * cc + ch[a]] = wv[a][j + 1];
-            nwin[(size_t)(K - 2) * cc + ch[a]] = cx[a];
+                if (j + 1 < K - 1) stg(nwin + (size_t)j * cc + ch[c], wv[c][j + 1]);
+            stg(nwin + (size_t)(K - 2) * cc + ch[c], cx[c]);
         }
     }
     // per-head L2 normalisation of q and k (src/ornith_tensor.c:155-160):
@@ -175,101 +182,103 @@ oh_k_delta_step(const float *cat, const float *ab, const float *gate, const floa
     }
     const float alpha = ref_expf(sa * ref_softplus(av + dtb));
     const float beta = ref_sigmoid(bv);
-    // slab -> LDS, row-padded
-#pragma unroll
-    for (int i = 0; i < DK / 4; i++) {
-        const int f = lane + 64 * i, row = (4 * f) / DK, col = (4 * f) % DK;
-        *(float4 *)(tile + row * TS + col) = make_float4(st[i].x, st[i].y, st[i].z, st[i].w);
-    }
-    __syncthreads();
+    wave_lds_sync();
 
+    // the lane's row walked twice from LDS (s = S * alpha is recomputed the
+    // same way): sk = sum_c s_c k_c; then s_c += u k_c, o = sum_c s_c q_c
     float *tr = tile + lane * TS;
-    float s[DK];
-#pragma unroll
+    float sk = 0.0f;
+#pragma unroll 8
     for (int c = 0; c < DK / 4; c++) {
         const float4 v = *(const float4 *)(tr + 4 * c);
-        s[4 * c + 0] = v.x * alpha;
-        s[4 * c + 1] = v.y * alpha;
-        s[4 * c + 2] = v.z * alpha;
-        s[4 * c + 3] = v.w * alpha;
+        const float4 kk = *(const float4 *)(kn + 4 * c);
+        sk += (v.x * alpha) * kk.x;
+        sk += (v.y * alpha) * kk.y;
+        sk += (v.z * alpha) * kk.z;
+        sk += (v.w * alpha) * kk.w;
     }
-    float sk = 0.0f;
-#pragma unroll
-    for (int c = 0; c < DK; c++) sk += s[c] * kn[c];
     const float u = beta * (cv[2 * NQ] - sk);
-#pragma unroll
-    for (int c = 0; c < DK; c++) s[c] += u * kn[c];
     float o = 0.0f;
-#pragma unroll
-    for (int c = 0; c < DK; c++) o += s[c] * qn[c];
-#pragma unroll
-    for (int c = 0; c < DK / 4; c++) *(float4 *)(tr + 4 * c) = make_float4(s[4 * c], s[4 * c + 1], s[4 * c + 2], s[4 * c + 3]);
-    __syncthreads();
-    float4 *Sw = (float4 *)(S + ((size_t)hv * DK + slab * 64) * DK);
+#pragma unroll 8
+    for (int c = 0; c < DK / 4; c++) {
+        const float4 v = *(const float4 *)(tr + 4 * c);
+        const float4 kk = *(const float4 *)(kn + 4 * c), qq = *(const float4 *)(qn + 4 * c);
+        float4 sv = make_float4(v.x * alpha, v.y * alpha, v.z * alpha, v.w * alpha);
+        sv.x += u * kk.x;
+        sv.y += u * kk.y;
+        sv.z += u * kk.z;
+        sv.w += u * kk.w;
+        o += sv.x * qq.x;
+        o += sv.y * qq.y;
+        o += sv.z * qq.z;
+        o += sv.w * qq.w;
+        *(float4 *)(tr + 4 * c) = sv;
+    }
+    wave_lds_sync();
+    float4 *Sw = (float4 *)(a.S + ((size_t)hv * DK + slab * 64) * DK);
 #pragma unroll
     for (int i = 0; i < DK / 4; i++) {
         const int f = lane + 64 * i, row = (4 * f) / DK, col = (4 * f) % DK;
-        Sw[f] = *(const float4 *)(tile + row * TS + col);
+        stg(Sw + f, *(const float4 *)(tile + row * TS + col));
     }
     // the gated RMSNorm's inputs for the consumer: o, silu(gate) and the
     // butterfly double sum of o^2 over this wave's 64 rows
-    o *= out_scale;
+    o *= a.out_scale;
     const double so = wave_sum_d((double)o * o);
-    out[(size_t)hv * DK + r] = o;
-    out_gate[(size_t)hv * DK + r] = ref_silu(gz);
-    if (lane == 0) out_runs[blockIdx.x] = so;
+    stc(a.out + (size_t)hv * DK + r, o);
+    stc(a.out_gate + (size_t)hv * DK + r, ref_silu(gz));
+    if (lane == 0) stc(a.out_runs + vb, so);
 }
 
 // ---- GQA decode (src/ornith_rforward.c:419-455, src/ornith_attn.c:65-149) -------
 // prep: per-head RMSNorm + partial NeoX RoPE (cos/sin from a host-built table
 // of the reference's powf/cosf/sinf values), Q8 append of k and v at `pos`.
-// Blocks [0, nh) are query heads, [nh, nh+nkv) key/value heads.
+// Virtual blocks [0, nh) are query heads, [nh, nh+nkv) key/value heads.
 // K codes are stored as [kvh][hd/4][cap] 32-bit words (4 codes each, so a
 // lane per position reads coalesced words); V codes as [kvh][cap/16][hd][16]
 // tiles (a lane per element reads 16 consecutive positions in one 16-byte
 // load). cap is a multiple of 16.
-extern "C" __global__ void __launch_bounds__(256)
-oh_k_attn_prep(const float *qproj, const float *kin, const float *vin,
-               const float *q_norm, const float *k_norm, const float2 *rope,
-               float *qr, float *gate, uint32_t *Kt, float *Ks, int8_t *Vq, float *Vs,
-               const int32_t *io_pos, int nh, int nkv, int hd, int rot, int cap, float eps) {
+template <class W>
+OH_DEV void prep_body(const oh_op_prep &a, int vb, int pos, W &w) {
     __shared__ float v[256];
     __shared__ double red[4];
     __shared__ float amax_s[4];
-    const int hb = (int)blockIdx.x, t = (int)threadIdx.x;
-    const int pos = *io_pos;
+    if (!w.wait()) return;
+    const int hb = vb, t = tid_x();
+    const int nh = a.nh, nkv = a.nkv, hd = a.hd, cap = a.cap;
     const bool isq = hb < nh;
     const int h = isq ? hb : hb - nh;
-    const float *src = isq ? qproj + (size_t)h * 2 * hd : kin + (size_t)h * hd;
-    const float x = t < hd ? src[t] : 0.0f;
+    const float *src = isq ? a.qproj + (size_t)h * 2 * hd : a.kin + (size_t)h * hd;
+    const float x = t < hd ? ldc(src + t) : 0.0f;
     double ss = block_sum_d((double)x * x, red);
-    const float inv = (float)(1.0 / sqrt(ss / (double)hd + (double)eps));
-    const float *nw = isq ? q_norm : k_norm;
-    if (t < hd) v[t] = x * inv * nw[t];
+    const float inv = (float)(1.0 / sqrt(ss / (double)hd + (double)a.eps));
+    const float *nw = isq ? a.q_norm : a.k_norm;
+    if (t < hd) v[t] = x * inv * ldg(nw + t);
     __syncthreads();
-    int r = rot <= 0 || rot > hd ? hd : rot;
+    const int r = a.rot <= 0 || a.rot > hd ? hd : a.rot;
     const int half = r / 2;
+    const float2 *rope = (const float2 *)a.rope;
     float y = t < hd ? v[t] : 0.0f;
     if (t < half) {
-        const float2 cs = rope[(size_t)pos * (hd / 2) + t];
+        const float2 cs = ldg(rope + (size_t)pos * (hd / 2) + t);
         y = v[t] * cs.x - v[t + half] * cs.y;
     } else if (t >= half && t < 2 * half) {
-        const float2 cs = rope[(size_t)pos * (hd / 2) + (t - half)];
+        const float2 cs = ldg(rope + (size_t)pos * (hd / 2) + (t - half));
         y = v[t - half] * cs.y + v[t] * cs.x;
     }
     if (isq) {
         if (t < hd) {
-            qr[(size_t)h * hd + t] = y;
-            gate[(size_t)h * hd + t] = qproj[(size_t)h * 2 * hd + hd + t];
+            stc(a.qr + (size_t)h * hd + t, y);
+            stc(a.gate + (size_t)h * hd + t, ldc(a.qproj + (size_t)h * 2 * hd + hd + t));
         }
         return;
     }
     // Q8 encode of k (post norm/rope) and raw v (src/ornith_attn.c:65-77)
     for (int which = 0; which < 2; which++) {
-        const float val = which == 0 ? y : (t < hd ? vin[(size_t)h * hd + t] : 0.0f);
-        float a = wave_max_f(fabsf(val));
+        const float val = which == 0 ? y : (t < hd ? ldc(a.vin + (size_t)h * hd + t) : 0.0f);
+        float am = wave_max_f(fabsf(val));
         __syncthreads();
-        if (lane_id() == 0) amax_s[t >> 6] = a;
+        if (lane_id() == 0) amax_s[t >> 6] = am;
         __syncthreads();
         const float amax = fmaxf(fmaxf(amax_s[0], amax_s[1]), fmaxf(amax_s[2], amax_s[3]));
         int code = 0;
@@ -286,86 +295,93 @@ oh_k_attn_prep(const float *qproj, const float *kin, const float *vin,
             const int c0 = shfl(code, (lane_id() & ~3) + 0), c1 = shfl(code, (lane_id() & ~3) + 1);
             const int c2 = shfl(code, (lane_id() & ~3) + 2), c3 = shfl(code, (lane_id() & ~3) + 3);
             if (t < hd && (t & 3) == 0)
-                Kt[((size_t)h * (hd / 4) + t / 4) * cap + pos] =
+                stc(a.Kt + ((size_t)h * (hd / 4) + t / 4) * cap + pos,
                     (uint32_t)(c0 & 0xff) | ((uint32_t)(c1 & 0xff) << 8) |
-                    ((uint32_t)(c2 & 0xff) << 16) | ((uint32_t)(c3 & 0xff) << 24);
-            if (t == 0) Ks[off] = scale;
+                    ((uint32_t)(c2 & 0xff) << 16) | ((uint32_t)(c3 & 0xff) << 24));
+            if (t == 0) stc(a.Ks + off, scale);
         } else {
             // tiles of 16 positions: Vq[h][pos/16][i][pos%16]
-            if (t < hd) Vq[(((size_t)h * (cap / 16) + pos / 16) * hd + t) * 16 + (pos & 15)] = (int8_t)code;
-            if (t == 0) Vs[off] = scale;
+            if (t < hd) stc(a.Vq + (((size_t)h * (cap / 16) + pos / 16) * hd + t) * 16 + (pos & 15), (int8_t)code);
+            if (t == 0) stc(a.Vs + off, scale);
         }
     }
 }
 
+// KV entries at earlier positions were written by earlier launches; the one
+// at `pos` by the prep phase of this launch with device-scope stores, before
+// any workgroup of this launch read its cache line. Plain loads therefore see
+// every entry.
+
 // scores[h][t] = (sum_i q_i*code_i) * Ks_t * scale, sequential over i
-// (src/ornith_attn.c:80-85,119-122). Grid (nh, cap/256); positions > pos exit,
-// and the whole grid exits when the context is longer than exact_max (the
-// flash kernels below take it).
-extern "C" __global__ void __launch_bounds__(256)
-oh_k_attn_scores(const float *qr, const uint32_t *Kt, const float *Ks, float *scores,
-                 const int32_t *io_pos, int nh, int nkv, int hd, int cap, float scale, int exact_max) {
+// (src/ornith_attn.c:80-85,119-122). Virtual block (h, 256-position tile):
+// vb = tile * nh + h; positions > pos exit, and everything exits when the
+// context is longer than exact_max (the flash path takes it).
+template <class W>
+OH_DEV void scores_body(const oh_op_attn &a, int vb, int pos, W &w) {
     __shared__ float q[256];
-    const int h = (int)blockIdx.x, t = (int)(blockIdx.y * 256 + threadIdx.x);
-    const int T = *io_pos + 1;
-    if ((int)blockIdx.y * 256 >= T || T > exact_max) return;
+    const int nh = a.nh, nkv = a.nkv, hd = a.hd, cap = a.cap;
+    const int h = vb % nh, ty = vb / nh, t = ty * 256 + tid_x();
+    const int T = pos + 1;
+    if (ty * 256 >= T || T > a.exact_max) return;
+    if (!w.wait()) return;
     const int kvh = h / (nh / nkv);
-    if ((int)threadIdx.x < hd) q[threadIdx.x] = qr[(size_t)h * hd + threadIdx.x];
+    if (tid_x() < hd) q[tid_x()] = ldc(a.qr + (size_t)h * hd + tid_x());
     __syncthreads();
     if (t >= T) return;
-    const uint32_t *kw = Kt + (size_t)kvh * (hd / 4) * cap + t;
+    const uint32_t *kw = a.Kt + (size_t)kvh * (hd / 4) * cap + t;
     float acc = 0.0f;
     for (int w0 = 0; w0 < hd / 4; w0 += 16) {
         uint32_t wd[16];
 #pragma unroll
-        for (int u = 0; u < 16; u++) wd[u] = w0 + u < hd / 4 ? kw[(size_t)(w0 + u) * cap] : 0u;
+        for (int u = 0; u < 16; u++) wd[u] = w0 + u < hd / 4 ? ldg(kw + (size_t)(w0 + u) * cap) : 0u;
 #pragma unroll
         for (int u = 0; u < 16; u++) {
             if (w0 + u >= hd / 4) break;
-            const int w = w0 + u;
-            acc += q[4 * w + 0] * (float)(int8_t)(wd[u] & 0xff);
-            acc += q[4 * w + 1] * (float)(int8_t)((wd[u] >> 8) & 0xff);
-            acc += q[4 * w + 2] * (float)(int8_t)((wd[u] >> 16) & 0xff);
-            acc += q[4 * w + 3] * (float)(int8_t)(wd[u] >> 24);
+            const int wi = w0 + u;
+            acc += q[4 * wi + 0] * (float)(int8_t)(wd[u] & 0xff);
+            acc += q[4 * wi + 1] * (float)(int8_t)((wd[u] >> 8) & 0xff);
+            acc += q[4 * wi + 2] * (float)(int8_t)((wd[u] >> 16) & 0xff);
+            acc += q[4 * wi + 3] * (float)(int8_t)(wd[u] >> 24);
         }
     }
-    const float ks = Ks[(size_t)t * nkv + kvh];
+    const float ks = ldg(a.Ks + (size_t)t * nkv + kvh);
     const float sc = ks == 0.0f ? 0.0f : acc * ks;
-    scores[(size_t)h * cap + t] = sc * scale;
+    stc(a.scores + (size_t)h * cap + t, sc * a.scale);
 }
 
 // softmax over T (src/ornith_tensor.c:108-115; tree-ordered double sum) and the
 // output o_i = sum_t (p_t*Vs_t)*code_t,i, sequential over t, skipping zero
-// weights (src/ornith_attn.c:132-140); then o *= sigmoid(gate). A block covers
-// 256/hd heads and walks all T positions in the reference's order. Contexts
-// longer than exact_max exit (the flash kernels below take them).
-extern "C" __global__ void __launch_bounds__(256)
-oh_k_attn_out(const float *scores, const int8_t *Vq, const float *Vs, const float *gate,
-              float *out, const int32_t *io_pos, int nh, int nkv, int hd, int cap, int exact_max) {
+// weights (src/ornith_attn.c:132-140); then o *= sigmoid(gate). A virtual
+// block covers 256/hd heads and walks all T positions in the reference's
+// order. Contexts longer than exact_max exit (the flash path takes them).
+template <class W>
+OH_DEV void out_body(const oh_op_attn &a, int vb, int pos, W &w) {
     __shared__ float pbuf[4][256];
     __shared__ float inv_s[4], mx_s[4];
     __shared__ double red[4];
     __shared__ float mred[4];
-    const int hpb = 256 / hd, t = (int)threadIdx.x, g = (int)blockIdx.x;
-    const int T = *io_pos + 1;
-    if (T > exact_max) return;
+    const int nh = a.nh, nkv = a.nkv, hd = a.hd, cap = a.cap;
+    const int hpb = 256 / hd, t = tid_x(), g = vb;
+    const int T = pos + 1;
+    if (T > a.exact_max) return;
+    if (!w.wait()) return;
     for (int hl = 0; hl < hpb; hl++) {
-        const float *sc = scores + (size_t)(g * hpb + hl) * cap;
+        const float *sc = a.scores + (size_t)(g * hpb + hl) * cap;
         float mx = -INFINITY;
-        for (int i = t; i < T; i += 256) mx = fmaxf(mx, sc[i]);
+        for (int i = t; i < T; i += 256) mx = fmaxf(mx, ldc(sc + i));
         mx = wave_max_f(mx);
         __syncthreads();
         if (lane_id() == 0) mred[t >> 6] = mx;
         __syncthreads();
         mx = fmaxf(fmaxf(mred[0], mred[1]), fmaxf(mred[2], mred[3]));
         double sum = 0.0;
-        for (int i = t; i < T; i += 256) sum += ref_expf(sc[i] - mx);
+        for (int i = t; i < T; i += 256) sum += ref_expf(ldc(sc + i) - mx);
         sum = block_sum_d(sum, red);
         if (t == 0) { mx_s[hl] = mx; inv_s[hl] = (float)(1.0 / sum); }
     }
     const int hl = t / hd, i = t % hd, h = g * hpb + hl;
     const int kvh = h / (nh / nkv);
-    const uint4 *vt = (const uint4 *)Vq + (size_t)kvh * (cap / 16) * hd + i;
+    const uint4 *vt = (const uint4 *)a.Vq + (size_t)kvh * (cap / 16) * hd + i;
     float o = 0.0f;
     for (int t0 = 0; t0 < T; t0 += 256) {
         const int n = T - t0 < 256 ? T - t0 : 256;
@@ -374,8 +390,8 @@ oh_k_attn_out(const float *scores, const int8_t *Vq, const float *Vs, const floa
             const int hh = k / 256, tt = k % 256;
             const int hg = g * hpb + hh, kv2 = hg / (nh / nkv);
             if (tt < n) {
-                const float p = ref_expf(scores[(size_t)hg * cap + t0 + tt] - mx_s[hh]) * inv_s[hh];
-                pbuf[hh][tt] = p * Vs[(size_t)(t0 + tt) * nkv + kv2];
+                const float p = ref_expf(ldc(a.scores + (size_t)hg * cap + t0 + tt) - mx_s[hh]) * inv_s[hh];
+                pbuf[hh][tt] = p * ldg(a.Vs + (size_t)(t0 + tt) * nkv + kv2);
             }
         }
         __syncthreads();
@@ -385,7 +401,7 @@ oh_k_attn_out(const float *scores, const int8_t *Vq, const float *Vs, const floa
 #pragma unroll
             for (int u = 0; u < 8; u++) {
                 const int tile = k0 + 16 * u < n ? k0 + 16 * u : ((n - 1) & ~15);
-                cw[u] = vt[(size_t)((t0 + tile) / 16) * hd];
+                cw[u] = ldg(vt + (size_t)((t0 + tile) / 16) * hd);
             }
 #pragma unroll
             for (int u = 0; u < 8; u++) {
@@ -400,59 +416,60 @@ oh_k_attn_out(const float *scores, const int8_t *Vq, const float *Vs, const floa
             }
         }
     }
-    out[(size_t)h * hd + i] = o * ref_sigmoid(gate[(size_t)h * hd + i]);
+    stc(a.out + (size_t)h * hd + i, o * ref_sigmoid(ldc(a.gate + (size_t)h * hd + i)));
 }
 
 // ---- flash decoding for long contexts ----------------------------------------------
 // Past exact_max positions the attention of one KV head is split into chunks
-// of 64 positions (block (kvh, chunk)): all nh/nkv query heads of the group
-// score the chunk against its Q8 keys once, take the chunk's softmax
-// statistics (max m, sum l of exp(s - m)) and the chunk's unnormalised output
+// of 64 positions: all nh/nkv query heads of the group score the chunk against
+// its Q8 keys once, take the chunk's softmax statistics (max m, sum l of
+// exp(s - m)) and the chunk's unnormalised output
 // sum_t exp(s_t - m) * Vs_t * code_t. attn_combine merges the chunks with the
 // usual rescaling. This re-associates the reference's sums (tolerance, not bit
 // parity), and reads each KV byte once per group instead of once per head.
 constexpr int kFlashCh = 64;
 
-// HB query heads of one KV head per block (compile time: the loops over heads
-// unroll); grid (nkv * (G/HB), chunks) with G = nh/nkv.
-template <int HB>
-__global__ void __launch_bounds__(256)
-oh_k_attn_flash(const float *qr, const uint32_t *Kt, const float *Ks, const int8_t *Vq, const float *Vs,
-                float *part_o, float *part_ml, const int32_t *io_pos, int nh, int nkv, int hd, int cap,
-                float scale, int exact_max) {
+// HB query heads of one KV head per virtual block (compile time: the loops
+// over heads unroll); vb = chunk * (nkv * G/HB) + group-block, G = nh/nkv.
+template <int HB, class W>
+OH_DEV void flash_body(const oh_op_attn &a, int vb, int pos, W &w) {
     extern __shared__ __align__(16) uint8_t fsm[];
-    const int T = *io_pos + 1;
-    const int G = nh / nkv, ngb = G / HB;
-    const int g = (int)blockIdx.x / ngb, hb0 = ((int)blockIdx.x % ngb) * HB;
-    const int c = (int)blockIdx.y, t0 = c * kFlashCh;
-    if (T <= exact_max || t0 >= T) return;
-    const int tid = (int)threadIdx.x, hw = hd / 4, kst = hw + 1;
+    const int nh = a.nh, nkv = a.nkv, hd = a.hd, cap = a.cap;
+    const int T = pos + 1;
+    const int G = nh / nkv, ngb = G / HB, gx = nkv * ngb;
+    const int bx = vb % gx, c = vb / gx;
+    const int g = bx / ngb, hb0 = (bx % ngb) * HB;
+    const int t0 = c * kFlashCh;
+    if (T <= a.exact_max || t0 >= T) return;
+    if (!w.wait()) return;
+    const int tid = tid_x(), hw = hd / 4, kst = hw + 1;
     const int nchmax = (cap + kFlashCh - 1) / kFlashCh;
     const int qst = hd + 16;                                  // head stride: quarters padded by a float4
     float *q = (float *)fsm;                                  // [HB][4][hd/4 + 4]
     uint32_t *kc = (uint32_t *)(q + HB * qst);                // [64][hw + 1]
-    uint4 *vt = (uint4 *)(((uintptr_t)(kc + kFlashCh * kst) + 15) & ~(uintptr_t)15);   // [4][hd]
+    const int vto = ((HB * qst + kFlashCh * kst) * 4 + 15) & ~15;
+    uint4 *vt = (uint4 *)(fsm + vto);                         // [4][hd]
     float *pp = (float *)(vt + (kFlashCh / 16) * hd);         // [HB][64]
     float *ks = pp + HB * kFlashCh, *vs = ks + kFlashCh;      // [64] each
     // loads: the block's query heads, the chunk's key words, value tiles, scales
     for (int k = tid; k < HB * hd; k += 256) {
         const int h = k / hd, e = k % hd, qq = e / (hd / 4);
-        q[h * qst + qq * (hd / 4 + 4) + e % (hd / 4)] = qr[((size_t)g * G + hb0) * hd + k];
+        q[h * qst + qq * (hd / 4 + 4) + e % (hd / 4)] = ldc(a.qr + ((size_t)g * G + hb0) * hd + k);
     }
     for (int k = tid; k < hw * kFlashCh; k += 256) {
-        const int w = k / kFlashCh, j = k % kFlashCh;
+        const int wi = k / kFlashCh, j = k % kFlashCh;
         const int t = t0 + j < T ? t0 + j : T - 1;
-        kc[j * kst + w] = Kt[((size_t)g * hw + w) * cap + t];
+        kc[j * kst + wi] = ldg(a.Kt + ((size_t)g * hw + wi) * cap + t);
     }
     for (int k = tid; k < (kFlashCh / 16) * hd; k += 256) {
         const int tt = k / hd, i = k % hd;
         const int tile = (t0 / 16 + tt) * 16 < T ? t0 / 16 + tt : (T - 1) / 16;
-        vt[k] = ((const uint4 *)Vq)[((size_t)g * (cap / 16) + tile) * hd + i];
+        vt[k] = ldg((const uint4 *)a.Vq + ((size_t)g * (cap / 16) + tile) * hd + i);
     }
     if (tid < kFlashCh) {
         const int t = t0 + tid < T ? t0 + tid : T - 1;
-        ks[tid] = Ks[(size_t)t * nkv + g];
-        vs[tid] = Vs[(size_t)t * nkv + g];
+        ks[tid] = ldg(a.Ks + (size_t)t * nkv + g);
+        vs[tid] = ldg(a.Vs + (size_t)t * nkv + g);
     }
     __syncthreads();
     // scores: thread -> (position j, quarter of the head dimension), the HB
@@ -465,13 +482,13 @@ oh_k_attn_flash(const float *qr, const uint32_t *Kt, const float *Ks, const int8
 #pragma unroll
         for (int h = 0; h < HB; h++) acc[h] = 0.0f;
 #pragma unroll 4
-        for (int w = 0; w < wq; w++) {
-            const uint32_t wd = kj[w];
+        for (int wi = 0; wi < wq; wi++) {
+            const uint32_t wd = kj[wi];
             const float c0 = (float)(int8_t)(wd & 0xff), c1 = (float)(int8_t)((wd >> 8) & 0xff);
             const float c2 = (float)(int8_t)((wd >> 16) & 0xff), c3 = (float)(int8_t)(wd >> 24);
 #pragma unroll
             for (int h = 0; h < HB; h++) {
-                const float4 qv = q4p[h * (qst / 4) + w];
+                const float4 qv = q4p[h * (qst / 4) + wi];
                 acc[h] = fmaf(qv.x, c0, acc[h]);
                 acc[h] = fmaf(qv.y, c1, acc[h]);
                 acc[h] = fmaf(qv.z, c2, acc[h]);
@@ -486,7 +503,7 @@ oh_k_attn_flash(const float *qr, const uint32_t *Kt, const float *Ks, const int8
             v += dpp_f<0xB1>(v);
             v += dpp_f<0x4E>(v);
             if (q4 == 0) {
-                const float sc = kss == 0.0f ? 0.0f : v * kss * scale;
+                const float sc = kss == 0.0f ? 0.0f : v * kss * a.scale;
                 pp[h * kFlashCh + j] = valid ? sc : -INFINITY;
             }
         }
@@ -505,9 +522,9 @@ oh_k_attn_flash(const float *qr, const uint32_t *Kt, const float *Ks, const int8
             for (int mm = 32; mm >= 1; mm >>= 1) l += shfl_xor(l, mm);
             pp[h * kFlashCh + lane] = e * vs[lane];
             if (lane == 0) {
-                float *ml = part_ml + (((size_t)g * nchmax + c) * G + hb0 + h) * 2;
-                ml[0] = m;
-                ml[1] = l;
+                float *ml = a.part_ml + (((size_t)g * nchmax + c) * G + hb0 + h) * 2;
+                stc(ml, m);
+                stc(ml + 1, l);
             }
         }
     }
@@ -541,49 +558,174 @@ oh_k_attn_flash(const float *qr, const uint32_t *Kt, const float *Ks, const int8
 #pragma unroll
         for (int k = 0; k < HB; k++) {
             const int h = h1 + hs * k;
-            if (h < HB) part_o[(((size_t)g * nchmax + c) * G + hb0 + h) * hd + i] = o[k];
+            if (h < HB) stc(a.part_o + (((size_t)g * nchmax + c) * G + hb0 + h) * hd + i, o[k]);
         }
     }
 }
 
-// Merge of the flash chunks of query head h (grid (nh, hd/64), 4 waves; wave w
-// takes chunks w, w+4, ...; a lane per dimension): running max rescaling,
-// then out = (sum_c o_c e^(m_c-M)) / (sum_c l_c e^(m_c-M)) * sigmoid(gate).
-extern "C" __global__ void __launch_bounds__(256)
-oh_k_attn_combine(const float *part_o, const float *part_ml, const float *gate, float *out,
-                  const int32_t *io_pos, int nh, int nkv, int hd, int cap, int exact_max) {
+// Merge of the flash chunks of query head h (virtual block vb = y * nh + h,
+// y < hd/64; 4 waves; wave w takes chunks w, w+4, ...; a lane per dimension):
+// running max rescaling, then
+// out = (sum_c o_c e^(m_c-M)) / (sum_c l_c e^(m_c-M)) * sigmoid(gate).
+template <class W>
+OH_DEV void combine_body(const oh_op_attn &a, int vb, int pos, W &w) {
     __shared__ float sm[4][3][64];
-    const int T = *io_pos + 1;
-    if (T <= exact_max) return;
-    const int h = (int)blockIdx.x, G = nh / nkv, g = h / G, hl = h % G;
-    const int wave = (int)(threadIdx.x >> 6), lane = (int)(threadIdx.x & 63);
-    const int i = (int)blockIdx.y * 64 + lane;
+    const int nh = a.nh, nkv = a.nkv, hd = a.hd, cap = a.cap;
+    const int T = pos + 1;
+    if (T <= a.exact_max) return;
+    if (!w.wait()) return;
+    const int h = vb % nh, G = nh / nkv, g = h / G, hl = h % G;
+    const int wave = (tid_x() >> 6), lane = (tid_x() & 63);
+    const int i = (vb / nh) * 64 + lane;
     const int nch = (T + kFlashCh - 1) / kFlashCh, nchmax = (cap + kFlashCh - 1) / kFlashCh;
     float M = -INFINITY, L = 0.0f, O = 0.0f;
     for (int c = wave; c < nch; c += 4) {
         const size_t base = ((size_t)g * nchmax + c) * G + hl;
-        const float m = part_ml[base * 2], l = part_ml[base * 2 + 1];
-        const float o = part_o[base * hd + i];
+        const float m = ldc(a.part_ml + base * 2), l = ldc(a.part_ml + base * 2 + 1);
+        const float o = ldc(a.part_o + base * hd + i);
         const float mn = fmaxf(M, m);
-        const float a = M == -INFINITY ? 0.0f : __expf(M - mn), b = __expf(m - mn);
-        O = O * a + o * b;
-        L = L * a + l * b;
+        const float e1 = M == -INFINITY ? 0.0f : __expf(M - mn), e2 = __expf(m - mn);
+        O = O * e1 + o * e2;
+        L = L * e1 + l * e2;
         M = mn;
     }
     sm[wave][0][lane] = M; sm[wave][1][lane] = L; sm[wave][2][lane] = O;
     __syncthreads();
     if (wave == 0) {
         float Mt = -INFINITY;
-        for (int w = 0; w < 4; w++) Mt = fmaxf(Mt, sm[w][0][lane]);
+        for (int k = 0; k < 4; k++) Mt = fmaxf(Mt, sm[k][0][lane]);
         float Lt = 0.0f, Ot = 0.0f;
-        for (int w = 0; w < 4; w++) {
-            const float mw = sm[w][0][lane];
+        for (int k = 0; k < 4; k++) {
+            const float mw = sm[k][0][lane];
             const float f = mw == -INFINITY ? 0.0f : __expf(mw - Mt);
-            Lt += sm[w][1][lane] * f;
-            Ot += sm[w][2][lane] * f;
+            Lt += sm[k][1][lane] * f;
+            Ot += sm[k][2][lane] * f;
         }
-        out[(size_t)h * hd + i] = Ot / Lt * ref_sigmoid(gate[(size_t)h * hd + i]);
+        stc(a.out + (size_t)h * hd + i, Ot / Lt * ref_sigmoid(ldc(a.gate + (size_t)h * hd + i)));
     }
+}
+
+// x += sum_s w_s * o_s (sequential in s, from 0) + shared * gate
+// (src/ornith_rforward.c:375-409)
+template <class W>
+OH_DEV void moe_combine_body(const oh_op_combine &a, int vb, W &w) {
+    if (!w.wait()) return;
+    const int i = vb * 256 + tid_x();
+    if (i >= a.H) return;
+    float acc = 0.0f;
+    for (int s = 0; s < a.k; s++) acc += ldc(a.w + s) * ldc(a.o + (size_t)s * a.H + i);
+    if (a.so) {
+        const float so = ldc(a.so + i);
+        const float v = a.shgate ? so * ldc(a.shgate) : so;
+        acc += v;
+    }
+    stc(a.x + i, ldc(a.x + i) + acc);
+}
+
+// ---- greedy argmax over the logits (src/ornith_rforward.c:18-22) ----------------
+// stage 1: per-block best (largest value, lowest index on ties) of the
+// elements vb, vb + nblk*256, ...
+template <class W>
+OH_DEV void argmax1_body(const oh_op_argmax &a, int vb, W &w) {
+    __shared__ float sv[4];
+    __shared__ int si[4];
+    if (!w.wait()) return;
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int i = vb * 256 + tid_x(); i < a.n; i += a.nblk * 256) {
+        const float x = ldc(a.v + i);
+        if (x > bv || (x == bv && i < bi)) { bv = x; bi = i; }
+    }
+    for (int m = 32; m >= 1; m >>= 1) {
+        const float ov = shfl_xor(bv, m); const int oi = shfl_xor(bi, m);
+        if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+    }
+    if (lane_id() == 0) { sv[tid_x() >> 6] = bv; si[tid_x() >> 6] = bi; }
+    __syncthreads();
+    if (tid_x() == 0) {
+        bv = sv[0]; bi = si[0];
+        for (int k = 1; k < 4; k++) if (sv[k] > bv || (sv[k] == bv && si[k] < bi)) { bv = sv[k]; bi = si[k]; }
+        stc(a.bv + vb, bv);
+        stc(a.bi + vb, bi);
+    }
+}
+
+// stage 2 (one wave): combine the per-block bests; write the next token at
+// toks[pos] (pos was already advanced by the body) and keep it in *best.
+template <class W>
+OH_DEV void argmax2_body(const oh_op_argmax &a, int pos, W &w) {
+    if (!w.wait()) return;
+    if (tid_x() >= 64) return;
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int i = tid_x(); i < a.nblk; i += 64) {
+        const float x = ldc(a.bv + i);
+        const int xi = ldc(a.bi + i);
+        if (x > bv || (x == bv && xi < bi)) { bv = x; bi = xi; }
+    }
+    for (int m = 32; m >= 1; m >>= 1) {
+        const float ov = shfl_xor(bv, m); const int oi = shfl_xor(bi, m);
+        if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+    }
+    if (tid_x() == 0) {
+        if (bi == 0x7fffffff) bi = 0;
+        stc(a.toks + pos, (int32_t)bi);
+        stc(a.best, (int32_t)bi);
+    }
+}
+
+// ---- standalone kernels (one launch per operation, captured into HIP graphs) -------
+extern "C" __global__ void __launch_bounds__(256) oh_k_embed(oh_op_embed a, const int32_t *io) {
+    NoWait w;
+    embed_body(a, (int)blockIdx.x, io[OH_IO_POS], w);
+}
+
+template <int DK, int KMAX>
+__global__ void __launch_bounds__(64) oh_k_delta_step(oh_op_delta a, const int32_t *io) {
+    __shared__ __align__(16) float lds[2 * DK + 64 * (DK + 4)];
+    NoWait w;
+    delta_body<DK, KMAX>(a, (int)blockIdx.x, io[OH_IO_POS], lds, w);
+}
+
+extern "C" __global__ void __launch_bounds__(256) oh_k_attn_prep(oh_op_prep a, const int32_t *io) {
+    NoWait w;
+    prep_body(a, (int)blockIdx.x, io[OH_IO_POS], w);
+}
+
+extern "C" __global__ void __launch_bounds__(256) oh_k_attn_scores(oh_op_attn a, const int32_t *io) {
+    NoWait w;
+    scores_body(a, (int)blockIdx.x, io[OH_IO_POS], w);
+}
+
+extern "C" __global__ void __launch_bounds__(256) oh_k_attn_out(oh_op_attn a, const int32_t *io) {
+    NoWait w;
+    out_body(a, (int)blockIdx.x, io[OH_IO_POS], w);
+}
+
+template <int HB>
+__global__ void __launch_bounds__(256) oh_k_attn_flash(oh_op_attn a, const int32_t *io) {
+    NoWait w;
+    flash_body<HB>(a, (int)blockIdx.x, io[OH_IO_POS], w);
+}
+
+extern "C" __global__ void __launch_bounds__(256) oh_k_attn_combine(oh_op_attn a, const int32_t *io) {
+    NoWait w;
+    combine_body(a, (int)blockIdx.x, io[OH_IO_POS], w);
+}
+
+extern "C" __global__ void __launch_bounds__(256) oh_k_moe_combine(oh_op_combine a) {
+    NoWait w;
+    moe_combine_body(a, (int)blockIdx.x, w);
+}
+
+extern "C" __global__ void __launch_bounds__(256) oh_k_argmax1(oh_op_argmax a) {
+    NoWait w;
+    argmax1_body(a, (int)blockIdx.x, w);
+}
+
+extern "C" __global__ void __launch_bounds__(64) oh_k_argmax2(oh_op_argmax a, const int32_t *io) {
+    NoWait w;
+    argmax2_body(a, io[OH_IO_POS], w);
 }
 
 // ---- MoE router (src/ornith_moe.c:8-30) ------------------------------------------
@@ -594,62 +736,6 @@ extern "C" __global__ void __launch_bounds__(64)
 oh_k_moe_route(const float *logits, int ne, int k, const float *shgate_logit,
                int32_t *idx, float *w, float *shgate) {
     route_wave(logits, ne, k, shgate_logit, idx, w, shgate);
-}
-
-// x += sum_s w_s * o_s (sequential in s, from 0) + shared * gate
-// (src/ornith_rforward.c:375-409)
-extern "C" __global__ void __launch_bounds__(256)
-oh_k_moe_combine(float *x, const float *o, const float *w, int k, int H,
-                 const float *so, const float *shgate) {
-    const int i = (int)(blockIdx.x * 256 + threadIdx.x);
-    if (i >= H) return;
-    float acc = 0.0f;
-    for (int s = 0; s < k; s++) acc += w[s] * o[(size_t)s * H + i];
-    if (so) {
-        const float v = shgate ? so[i] * *shgate : so[i];
-        acc += v;
-    }
-    x[i] = x[i] + acc;
-}
-
-// ---- greedy argmax over the logits (src/ornith_rforward.c:18-22) ----------------
-// stage 1: per-block best (largest value, lowest index on ties)
-extern "C" __global__ void __launch_bounds__(256)
-oh_k_argmax1(const float *v, int n, float *bv_out, int *bi_out) {
-    __shared__ float sv[4]; __shared__ int si[4];
-    float bv = -INFINITY; int bi = 0x7fffffff;
-    for (int i = (int)(blockIdx.x * 256 + threadIdx.x); i < n; i += (int)(gridDim.x * 256))
-        if (v[i] > bv || (v[i] == bv && i < bi)) { bv = v[i]; bi = i; }
-    for (int m = 32; m >= 1; m >>= 1) {
-        const float ov = shfl_xor(bv, m); const int oi = shfl_xor(bi, m);
-        if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
-    }
-    if (lane_id() == 0) { sv[threadIdx.x >> 6] = bv; si[threadIdx.x >> 6] = bi; }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        bv = sv[0]; bi = si[0];
-        for (int k = 1; k < 4; k++) if (sv[k] > bv || (sv[k] == bv && si[k] < bi)) { bv = sv[k]; bi = si[k]; }
-        bv_out[blockIdx.x] = bv; bi_out[blockIdx.x] = bi;
-    }
-}
-
-// stage 2: combine the per-block bests; write the next token at toks[pos]
-// (pos was already advanced by the step) and count the emitted tokens.
-extern "C" __global__ void __launch_bounds__(64)
-oh_k_argmax2(const float *bv_in, const int *bi_in, int nblk, int32_t *toks,
-             const int32_t *io_pos, int32_t *io_best) {
-    float bv = -INFINITY; int bi = 0x7fffffff;
-    for (int i = (int)threadIdx.x; i < nblk; i += 64)
-        if (bv_in[i] > bv || (bv_in[i] == bv && bi_in[i] < bi)) { bv = bv_in[i]; bi = bi_in[i]; }
-    for (int m = 32; m >= 1; m >>= 1) {
-        const float ov = shfl_xor(bv, m); const int oi = shfl_xor(bi, m);
-        if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
-    }
-    if (threadIdx.x == 0) {
-        if (bi == 0x7fffffff) bi = 0;
-        toks[*io_pos] = bi;
-        *io_best = bi;
-    }
 }
 
 // advance the stream position after a token's layers (rforward_token s->pos++)

@@ -63,7 +63,9 @@ OH_DEV int group_isum(int v) {     // exact sum over the 8 lanes of a group
 // ---- Q8_K quantisation of one 256-element block held in LDS ------------------
 // One wave; exactly qdot_quantize_row_q8_K (src/ornith_qdot.c:32-62): the first
 // element of largest magnitude sets iscale = -127/x, codes = rint(iscale*x)
-// clamped, bsums per 16, d = 1/iscale.
+// clamped, bsums per 16, d = 1/iscale. G: qs/d/bs are global memory read by
+// other workgroups (device-scope stores); otherwise LDS.
+template <bool G = false>
 OH_DEV void q8k_block_from_lds(const float *v, int qb, int8_t *qs, float *d, int16_t *bs,
                                int qstride = 256) {
     const int lane = lane_id();
@@ -79,11 +81,14 @@ OH_DEV void q8k_block_from_lds(const float *v, int qb, int8_t *qs, float *d, int
     bi = wave_min_fast(bi);
     int8_t *q = qs + (int64_t)qb * qstride;
     int16_t *b = bs + (int64_t)qb * 16;
+    auto put8 = [&](int8_t *p, int8_t x) { if (G) stc(p, x); else *p = x; };
+    auto put16 = [&](int16_t *p, int16_t x) { if (G) stc(p, x); else *p = x; };
+    auto putf = [&](float *p, float x) { if (G) stc(p, x); else *p = x; };
     if (best == 0.0f || !(best > 0.0f)) {
 #pragma unroll
-        for (int k = 0; k < 4; k++) q[lane + 64 * k] = 0;
-        if (lane < 16) b[lane] = 0;
-        if (lane == 0) d[qb] = 0.0f;
+        for (int k = 0; k < 4; k++) put8(q + lane + 64 * k, (int8_t)0);
+        if (lane < 16) put16(b + lane, (int16_t)0);
+        if (lane == 0) putf(d + qb, 0.0f);
         return;
     }
     const float iscale = -127.0f / xb[bi];
@@ -93,11 +98,11 @@ OH_DEV void q8k_block_from_lds(const float *v, int qb, int8_t *qs, float *d, int
         float r = __builtin_rintf(iscale * xb[e]);
         int c = (int)r;
         c = c > 127 ? 127 : (c < -128 ? -128 : c);
-        q[e] = (int8_t)c;
+        put8(q + e, (int8_t)c);
         const int sv = row16_sum_i(c);                 // codes 64k + 16g .. +15
-        if ((lane & 15) == 0) b[4 * k + (lane >> 4)] = (int16_t)sv;
+        if ((lane & 15) == 0) put16(b + 4 * k + (lane >> 4), (int16_t)sv);
     }
-    if (lane == 0) d[qb] = 1.0f / iscale;
+    if (lane == 0) putf(d + qb, 1.0f / iscale);
 }
 
 // Q8_K of the blocks qb0, qb0 + qstep, ... (< nb, at most N of them) of v by
@@ -157,7 +162,7 @@ OH_DEV void q8k_blocks(const float *v, int qb0, int qstep, int nb, int8_t *qs, f
 
 // Q8_K of all nb blocks of v by the 4 waves of a block
 OH_DEV void q8k_all(const float *v, int nb, int8_t *qs, float *d, int16_t *bs, int qstride) {
-    const int wave = (int)(threadIdx.x >> 6);
+    const int wave = (tid_x() >> 6);
     for (int q0 = wave; q0 < nb; q0 += 16) q8k_blocks<4>(v, q0, 4, nb, qs, d, bs, qstride);
 }
 
@@ -165,7 +170,7 @@ OH_DEV void q8k_all(const float *v, int nb, int8_t *qs, float *d, int16_t *bs, i
 // squares in double (tree-ordered), inv = (float)(1/sqrt(ss/n+eps)),
 // v_i = v_i * inv * w_i. All 256 threads; v must be visible block-wide.
 OH_DEV void rmsnorm_lds(float *v, const float *w, float eps, int n, double *red) {
-    const int tid = (int)threadIdx.x, wave = tid >> 6;
+    const int tid = tid_x(), wave = tid >> 6;
     double ss = 0.0;
     for (int i = tid; i < n; i += 256) ss += (double)v[i] * v[i];
     ss = wave_sum_d(ss);
@@ -173,7 +178,7 @@ OH_DEV void rmsnorm_lds(float *v, const float *w, float eps, int n, double *red)
     lds_barrier();
     const double tot = (red[0] + red[1]) + (red[2] + red[3]);
     const float inv = (float)(1.0 / sqrt(tot / (double)n + (double)eps));
-    for (int i = tid; i < n; i += 256) v[i] = v[i] * inv * w[i];
+    for (int i = tid; i < n; i += 256) v[i] = v[i] * inv * ldg(w + i);
     lds_barrier();
 }
 
@@ -196,21 +201,21 @@ OH_DEV const uint4 *a_tile(const uint8_t *A, int pb, int64_t bi) {
 OH_DEV void sb_load(SB<OH_Q4_K> &r, const WP &w, int64_t bi) {
     const uint4 *a = a_tile(w.A, 128, bi);
 #pragma unroll
-    for (int k = 0; k < 8; k++) r.q[k] = a[k * 64];
-    r.h = *(const uint4 *)(w.B + bi * 16);
+    for (int k = 0; k < 8; k++) r.q[k] = ldg(a + k * 64);
+    r.h = ldg((const uint4 *)(w.B + bi * 16));
 }
 OH_DEV void sb_load(SB<OH_Q6_K> &r, const WP &w, int64_t bi) {
     const uint4 *a = a_tile(w.A, 192, bi);
 #pragma unroll
-    for (int k = 0; k < 12; k++) r.q[k] = a[k * 64];
-    r.sc = *(const uint4 *)(w.B + bi * 16);
-    r.d = *(const uint16_t *)(w.C + bi * 2);
+    for (int k = 0; k < 12; k++) r.q[k] = ldg(a + k * 64);
+    r.sc = ldg((const uint4 *)(w.B + bi * 16));
+    r.d = ldg((const uint16_t *)(w.C + bi * 2));
 }
 OH_DEV void sb_load(SB<OH_Q8_0> &r, const WP &w, int64_t bi) {
     const uint4 *a = a_tile(w.A, 256, bi);
 #pragma unroll
-    for (int k = 0; k < 16; k++) r.q[k] = a[k * 64];
-    r.d = *(const uint4 *)(w.B + bi * 16);
+    for (int k = 0; k < 16; k++) r.q[k] = ldg(a + k * 64);
+    r.d = ldg((const uint4 *)(w.B + bi * 16));
 }
 
 OH_DEV uint32_t pword(const uint4 *q, int w) { return wsel(q[w >> 2], w & 3); }
@@ -304,9 +309,10 @@ OH_DEV float sb_term(const SB<OH_Q8_0> &r, const int8_t *aq, const int16_t *, fl
     return yd * part;
 }
 
+// outputs are read by later phases of the step kernel (device-scope accesses)
 OH_DEV void emit(float *y, int mode, int row, float v) {
-    if (mode == 1) y[row] = y[row] + v;
-    else y[row] = v;
+    if (mode == 1) stc(y + row, ldc(y + row) + v);
+    else stc(y + row, v);
 }
 
 // Fallback row: dequantise on the fly and accumulate w_i * x_i strictly in
@@ -316,21 +322,22 @@ OH_DEV float row_seq(const oh_mvseg &s, int64_t r, const float *x) {
     float acc = 0.0f;
     if (s.type == OH_F32) {
         const float *w = (const float *)s.A + r * in;
-        for (int i = 0; i < in; i++) acc += w[i] * x[i];
+        for (int i = 0; i < in; i++) acc += ldg(w + i) * x[i];
     } else if (s.type == OH_F16 || s.type == OH_BF16) {
         const uint16_t *w = (const uint16_t *)s.A + r * in;
         for (int i = 0; i < in; i++) {
-            const float wf = s.type == OH_F16 ? h2f(w[i]) : u2f((uint32_t)w[i] << 16);
+            const uint16_t wr = ldg(w + i);
+            const float wf = s.type == OH_F16 ? h2f(wr) : u2f((uint32_t)wr << 16);
             acc += wf * x[i];
         }
     } else if (s.type == OH_IQ2_XXS) {
         const int nb = in / 256;
         for (int b = 0; b < nb; b++) {
             const int64_t bi = r * nb + b;
-            const float d = h2f(*(const uint16_t *)(s.C + bi * 2));
+            const float d = h2f(ldg((const uint16_t *)(s.C + bi * 2)));
             const uint32_t *q = (const uint32_t *)(s.A + bi * 64);
             for (int g32 = 0; g32 < 8; g32++) {
-                const uint32_t w0 = q[2 * g32], w1 = q[2 * g32 + 1];
+                const uint32_t w0 = ldg(q + 2 * g32), w1 = ldg(q + 2 * g32 + 1);
                 const float db = d * (0.5f + (float)(w1 >> 28)) * 0.25f;
                 for (int k = 0; k < 4; k++) {
                     const uint64_t gv = k_iq2_grid[(w0 >> (8 * k)) & 0xffu];
@@ -399,7 +406,8 @@ OH_HD inline int mv_lds_v_off(int nb) { return (nb * kAS + nb * 36 + 15) & ~15; 
 // Block prologue: form the slot's activation in LDS. q8: Q8_K planes are
 // needed (integer path); otherwise only the f32 vector v.
 OH_DEV void mv_prologue(const oh_mvseg &s, int slot, int blk, uint8_t *smem, double *red, bool q8) {
-    const int in = s.in, nb = in / 256, tid = (int)threadIdx.x, wave = tid >> 6;
+    // activations come from earlier phases: device-scope loads
+    const int in = s.in, nb = in / 256, tid = tid_x(), wave = tid >> 6;
     int8_t *aqs = (int8_t *)smem;
     int16_t *abs = (int16_t *)(smem + mv_lds_bs_off(nb));
     float *ad = (float *)(smem + mv_lds_d_off(nb));
@@ -408,30 +416,30 @@ OH_DEV void mv_prologue(const oh_mvseg &s, int slot, int blk, uint8_t *smem, dou
     if (s.pro == OH_PRO_Q8K) {
         if (q8) {
             const int4 *gq = (const int4 *)(s.xqs + ao);
-            for (int i = tid; i < in / 16; i += 256) ((int4 *)aqs)[(i >> 4) * (kAS / 16) + (i & 15)] = gq[i];
-            for (int i = tid; i < nb * 16; i += 256) abs[i] = s.xbs[ao / 16 + i];
-            for (int i = tid; i < nb; i += 256) ad[i] = s.xd[ao / 256 + i];
+            for (int i = tid; i < in / 16; i += 256) ((int4 *)aqs)[(i >> 4) * (kAS / 16) + (i & 15)] = ldc4(gq + i);
+            for (int i = tid; i < nb * 16; i += 256) abs[i] = ldc(s.xbs + ao / 16 + i);
+            for (int i = tid; i < nb; i += 256) ad[i] = ldc(s.xd + ao / 256 + i);
         } else {
-            for (int i = tid; i < in; i += 256) v[i] = s.xf[ao + i];
+            for (int i = tid; i < in; i += 256) v[i] = ldc(s.xf + ao + i);
         }
         lds_barrier();
         return;
     }
     if (s.pro == OH_PRO_SWIGLU) {
-        for (int i = tid; i < in; i += 256) v[i] = ref_silu(s.xf[ao + i]) * s.xf2[ao + i];
+        for (int i = tid; i < in; i += 256) v[i] = ref_silu(ldc(s.xf + ao + i)) * ldc(s.xf2 + ao + i);
         lds_barrier();
     } else {
-        for (int i = tid; i < in; i += 256) v[i] = s.xf[ao + i];
+        for (int i = tid; i < in; i += 256) v[i] = ldc(s.xf + ao + i);
         lds_barrier();
         if (s.pro == OH_PRO_NORM) rmsnorm_lds(v, s.nw, s.eps, in, red);
     }
     const bool store = blk == 0 && s.oqs != nullptr;
     if (blk == 0 && s.oxf)
-        for (int i = tid; i < in; i += 256) s.oxf[ao + i] = v[i];
+        for (int i = tid; i < in; i += 256) stc(s.oxf + ao + i, v[i]);
     if (q8 || store) {
         for (int qb = wave; qb < nb; qb += 4) {
             q8k_block_from_lds(v, qb, aqs, ad, abs, kAS);
-            if (store) q8k_block_from_lds(v, qb, s.oqs + ao, s.oqd + ao / 256, s.oqb + ao / 16);
+            if (store) q8k_block_from_lds<true>(v, qb, s.oqs + ao, s.oqd + ao / 256, s.oqb + ao / 16);
         }
     }
     lds_barrier();
@@ -444,29 +452,32 @@ OH_DEV void mv_prologue(const oh_mvseg &s, int slot, int blk, uint8_t *smem, dou
 struct PIn { float4 a[4], b[4], c[4]; int4 q, bsv; float d; double r0, r1; };
 
 OH_DEV void pro_load(PIn &p, const oh_mvseg &s, int slot) {
-    const int tid = (int)threadIdx.x, in = s.in, nb = in / 256;
+    const int tid = tid_x(), in = s.in, nb = in / 256;
     const size_t ao = (size_t)slot * s.astride;
     if (s.pro == OH_PRO_Q8K) {
         const int n16 = in / 16;
-        p.q = ((const int4 *)(s.xqs + ao))[tid < n16 ? tid : n16 - 1];
-        p.bsv = ((const int4 *)(s.xbs + ao / 16))[tid < 2 * nb ? tid : 2 * nb - 1];
-        p.d = s.xd[ao / 256 + (tid < nb ? tid : nb - 1)];
+        p.q = ldc4((const int4 *)(s.xqs + ao) + (tid < n16 ? tid : n16 - 1));
+        p.bsv = ldc4((const int4 *)(s.xbs + ao / 16) + (tid < 2 * nb ? tid : 2 * nb - 1));
+        p.d = ldc(s.xd + ao / 256 + (tid < nb ? tid : nb - 1));
     } else {
+        // activations from earlier phases (device-scope loads); the RMSNorm
+        // weights are constant
         const float4 *x = (const float4 *)(s.xf + ao);
-        const float4 *w = (const float4 *)(s.pro == OH_PRO_NORM ? s.nw : s.pro == OH_PRO_F32 ? s.xf + ao : s.xf2 + ao);
+        const bool wc = s.pro == OH_PRO_NORM;
+        const float4 *w = (const float4 *)(wc ? s.nw : s.pro == OH_PRO_F32 ? s.xf + ao : s.xf2 + ao);
         const int n4 = in / 4;
 #pragma unroll
         for (int k = 0; k < 4; k++) {
             const int i = tid + 256 * k < n4 ? tid + 256 * k : n4 - 1;
-            p.a[k] = x[i];
-            p.b[k] = w[i];
-            if (s.pro == OH_PRO_GNORM) p.c[k] = ((const float4 *)s.nw)[i % (s.gdim / 4)];
+            p.a[k] = ldc4(x + i);
+            p.b[k] = wc ? ldg(w + i) : ldc4(w + i);
+            if (s.pro == OH_PRO_GNORM) p.c[k] = ldg((const float4 *)s.nw + i % (s.gdim / 4));
         }
         if (s.pro == OH_PRO_GNORM) {
             // this thread's head (tid < in/gdim): its first two run sums
             const int rpg = s.gdim / 64, nh = in / s.gdim, h = tid < nh ? tid : nh - 1;
-            p.r0 = s.xruns[h * rpg];
-            p.r1 = s.xruns[h * rpg + (rpg > 1 ? 1 : 0)];
+            p.r0 = ldc(s.xruns + h * rpg);
+            p.r1 = ldc(s.xruns + h * rpg + (rpg > 1 ? 1 : 0));
         }
     }
 }
@@ -477,7 +488,9 @@ OH_DEV float4 f4_silu_mul(const float4 g, const float4 u) {
 
 // Q8_K of one 256-element block held in registers by a wave, four
 // consecutive elements x per lane (lane l: elements 4l..4l+3). Same result as
-// q8k_block_from_lds; codes are written as one packed word per lane.
+// q8k_block_from_lds; codes are written as one packed word per lane. G: the
+// planes are global memory read by other workgroups (device-scope stores).
+template <bool G = false>
 OH_DEV void q8k_regs(const float4 x, int qb, int8_t *qs, float *d, int16_t *bs, int qstride) {
     const int lane = lane_id();
     const float a0 = fabsf(x.x), a1 = fabsf(x.y), a2 = fabsf(x.z), a3 = fabsf(x.w);
@@ -490,10 +503,13 @@ OH_DEV void q8k_regs(const float4 x, int qb, int8_t *qs, float *d, int16_t *bs, 
     bi = wave_min_fast(bi);
     int *qw = (int *)(qs + (int64_t)qb * qstride) + lane;
     int16_t *b = bs + (int64_t)qb * 16;
+    auto put32 = [&](int *p, int v) { if (G) stc(p, v); else *p = v; };
+    auto put16 = [&](int16_t *p, int16_t v) { if (G) stc(p, v); else *p = v; };
+    auto putf = [&](float *p, float v) { if (G) stc(p, v); else *p = v; };
     if (best == 0.0f || !(best > 0.0f)) {
-        *qw = 0;
-        if (lane < 16) b[lane] = 0;
-        if (lane == 0) d[qb] = 0.0f;
+        put32(qw, 0);
+        if (lane < 16) put16(b + lane, (int16_t)0);
+        if (lane == 0) putf(d + qb, 0.0f);
         return;
     }
     const int sel = bi & 3;
@@ -506,16 +522,16 @@ OH_DEV void q8k_regs(const float4 x, int qb, int8_t *qs, float *d, int16_t *bs, 
         const int v = (int)__builtin_rintf(iscale * xs[j]);
         c[j] = v > 127 ? 127 : (v < -128 ? -128 : v);
     }
-    *qw = (c[0] & 0xff) | ((c[1] & 0xff) << 8) | ((c[2] & 0xff) << 16) | ((c[3] & 0xff) << 24);
+    put32(qw, (c[0] & 0xff) | ((c[1] & 0xff) << 8) | ((c[2] & 0xff) << 16) | ((c[3] & 0xff) << 24));
     int sv = c[0] + c[1] + c[2] + c[3];
     sv += dpp_i<0xB1>(sv);
     sv += dpp_i<0x4E>(sv);                         // codes 16*(lane/4) .. +15
-    if ((lane & 3) == 0) b[lane >> 2] = (int16_t)sv;
-    if (lane == 0) d[qb] = 1.0f / iscale;
+    if ((lane & 3) == 0) put16(b + (lane >> 2), (int16_t)sv);
+    if (lane == 0) putf(d + qb, 1.0f / iscale);
 }
 
 OH_DEV void pro_compute(const PIn &p, const oh_mvseg &s, int slot, int blk, uint8_t *smem, double *red) {
-    const int in = s.in, nb = in / 256, tid = (int)threadIdx.x, wave = tid >> 6;
+    const int in = s.in, nb = in / 256, tid = tid_x(), wave = tid >> 6;
     int8_t *aqs = (int8_t *)smem;
     int16_t *abs = (int16_t *)(smem + mv_lds_bs_off(nb));
     float *ad = (float *)(smem + mv_lds_d_off(nb));
@@ -544,7 +560,7 @@ OH_DEV void pro_compute(const PIn &p, const oh_mvseg &s, int slot, int blk, uint
         if (tid < in / gd) {
             double tot = p.r0;
             if (rpg > 1) tot += p.r1;
-            for (int k = 2; k < rpg; k++) tot += s.xruns[tid * rpg + k];
+            for (int k = 2; k < rpg; k++) tot += ldc(s.xruns + tid * rpg + k);
             hinv[tid] = (float)(1.0 / sqrt(tot / (double)gd + (double)s.eps));
         }
         lds_barrier();
@@ -581,9 +597,9 @@ OH_DEV void pro_compute(const PIn &p, const oh_mvseg &s, int slot, int blk, uint
     for (int k = 0; k < 4; k++) {
         const int qb = wave + 4 * k;
         if (qb < nb) {
-            if (blk == 0 && s.oxf) ((float4 *)(s.oxf + ao))[tid + 256 * k] = fv[k];
+            if (blk == 0 && s.oxf) stc4((float4 *)(s.oxf + ao) + tid + 256 * k, fv[k]);
             q8k_regs(fv[k], qb, aqs, ad, abs, kAS);
-            if (store) q8k_regs(fv[k], qb, s.oqs + ao, s.oqd + ao / 256, s.oqb + ao / 16, 256);
+            if (store) q8k_regs<true>(fv[k], qb, s.oqs + ao, s.oqd + ao / 256, s.oqb + ao / 16, 256);
         }
     }
     lds_barrier();
@@ -594,10 +610,12 @@ OH_DEV void pro_compute(const PIn &p, const oh_mvseg &s, int slot, int blk, uint
 // flight while the current one is reduced. All loads are unconditional
 // (dead lanes and steps past the end re-read an in-bounds block), so the
 // compiler never has to drain the queue at a branch. expert: the slot's
-// expert for stacked tensors.
-template <int T>
-OH_DEV void mv_seg(const oh_mvseg &s, int slot, int blk, int expert, uint8_t *smem, double *red) {
-    const int lane = lane_id(), wave = (int)(threadIdx.x >> 6);
+// expert for stacked tensors. Inside the step kernel (W::kGrid) the first
+// step's weights are requested before the grid wait: they do not depend on
+// the previous phase.
+template <int T, class W>
+OH_DEV void mv_seg(const oh_mvseg &s, int slot, int blk, int expert, uint8_t *smem, double *red, W &w) {
+    const int lane = lane_id(), wave = __builtin_amdgcn_readfirstlane(tid_x() >> 6);
     const int nb = s.nb, rps = 64 / nb;
     const int rl = lane / nb, sb = lane - rl * nb;
     const int u0 = (blk * OH_MV_WAVES + wave) * s.upw;
@@ -638,19 +656,35 @@ OH_DEV void mv_seg(const oh_mvseg &s, int slot, int blk, int expert, uint8_t *sm
     };
     if (s.in <= 4096) {
         PIn pin;
-        pro_load(pin, s, slot);
-        load(ra, 0);
+        if (W::kGrid) {
+            load(ra, 0);
+            if (!w.wait()) return;
+            pro_load(pin, s, slot);
+        } else {
+            pro_load(pin, s, slot);
+            load(ra, 0);
+        }
         __builtin_amdgcn_sched_barrier(0);
         pro_compute(pin, s, slot, blk, smem, red);
     } else {
         load(ra, 0);
+        if (!w.wait()) return;
         mv_prologue(s, slot, blk, smem, red, true);
     }
-    for (int st = 0; st < S; st += 2) {
+    // ra holds step 0; a step's loads are only issued when it will be reduced
+    int st = 0;
+    for (; st + 2 < S; st += 2) {
         load(rb, st + 1);
         comp(ra, st);
         load(ra, st + 2);
         comp(rb, st + 1);
+    }
+    if (st + 1 < S) {
+        load(rb, st + 1);
+        comp(ra, st);
+        comp(rb, st + 1);
+    } else if (st < S) {
+        comp(ra, st);
     }
 }
 
@@ -659,14 +693,15 @@ OH_DEV void mv_seg(const oh_mvseg &s, int slot, int blk, int expert, uint8_t *sm
 // (larger logit, or equal logit and lower index); the k experts of rank < k in
 // rank order are the reference's picks. Softmax over the selected logits in
 // that order by one thread. Logits that are NaN or -inf fall back to the
-// sequential selection of one wave. Results in LDS (sel, w, *shg); block 0
-// also stores them for later launches.
-OH_DEV void route_block(const oh_mvlaunch &L, float *lg, int *sel, float *rw, float *shg, int *bad, int *cnt) {
-    const int tid = (int)threadIdx.x, ne = L.ne, k = L.topk;
+// sequential selection of one wave. Results in LDS (sel, w, *shg); virtual
+// block 0 also stores them for later phases.
+OH_DEV void route_block(const oh_mvlaunch &L, int vb, float *lg, int *sel, float *rw, float *shg, int *bad,
+                        int *cnt) {
+    const int tid = tid_x(), ne = L.ne, k = L.topk;
     const int ne4 = (ne + 3) & ~3;
     if (tid == 0) *bad = 0;
     if (tid < 64) cnt[tid] = 0;
-    for (int e = tid; e < ne4; e += 256) lg[e] = e < ne ? L.rlog[e] : -INFINITY;
+    for (int e = tid; e < ne4; e += 256) lg[e] = e < ne ? ldc(L.rlog + e) : -INFINITY;
     __syncthreads();
     // rank by strictly larger logits; equal logits inside the top k (or a
     // NaN / -inf anywhere) send the block to the sequential selection
@@ -687,105 +722,121 @@ OH_DEV void route_block(const oh_mvlaunch &L, float *lg, int *sel, float *rw, fl
     }
     __syncthreads();
     if (*bad) {
-        if (tid < 64) route_wave(lg, ne, k, L.shl, sel, rw, shg);
-    } else if (tid == 0) {
-        float mx = lg[sel[0]];
-        for (int j = 1; j < k; j++) { const float x = lg[sel[j]]; if (x > mx) mx = x; }
+        if (tid < 64) route_wave(lg, ne, k, nullptr, sel, rw, shg);
+        if (tid == 0 && L.shl) *shg = ref_sigmoid(ldc(L.shl));
+    } else if (tid < 64) {
+        // lane j: e_j = exp(l_j - max) in parallel; the sum in selection
+        // order, then w_j = e_j / sum
+        const float lj = tid < k ? lg[sel[tid]] : -INFINITY;
+        const float mx = wave_max_fast(lj);
+        const float e = tid < k ? ref_expf(lj - mx) : 0.0f;
         float sum = 0.0f;
-        for (int j = 0; j < k; j++) { rw[j] = ref_expf(lg[sel[j]] - mx); sum += rw[j]; }
-        for (int j = 0; j < k; j++) rw[j] = rw[j] / sum;
-        if (L.shl) *shg = ref_sigmoid(*L.shl);
+        for (int j = 0; j < k; j++) sum += shfl(e, j);
+        if (tid < k) rw[tid] = e / sum;
+        if (tid == 0 && L.shl) *shg = ref_sigmoid(ldc(L.shl));
     }
     __syncthreads();
-    if (blockIdx.x == 0) {
-        if (tid < k) { L.ridx[tid] = sel[tid]; L.rw[tid] = rw[tid]; }
-        if (tid == 0 && L.shl) *L.shg = *shg;
+    if (vb == 0) {
+        if (tid < k) { stc(L.ridx + tid, (int32_t)sel[tid]); stc(L.rw + tid, rw[tid]); }
+        if (tid == 0 && L.shl) stc(L.shg, *shg);
     }
 }
 
 // Launch body. TK >= 0: every segment is an integer-path segment of type TK;
 // TK < 0: any mix, including fallback segments (one lane per row, the f32
 // activation in LDS). With L.route every block first routes the MoE and
-// stacked segments take their experts from that routing.
-template <int TK>
-OH_DEV void mv_body(const oh_mvlaunch &L) {
+// stacked segments take their experts from that routing. vb: the virtual
+// block (blockIdx.x of a standalone launch).
+template <int TK, class W>
+OH_DEV void mv_body(const oh_mvlaunch &L, int vb, W &w) {
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ double red[4];
     __shared__ int rsel[64], rbad, rcnt[64];
     __shared__ float rwt[64], rshg;
     int si = 0;
-    while (si + 1 < L.n && (int)blockIdx.x >= L.s[si + 1].block0) si++;
+    while (si + 1 < L.n && vb >= L.s[si + 1].block0) si++;
     const oh_mvseg &s = L.s[si];
-    const int bseg = (int)blockIdx.x - s.block0;
+    const int bseg = vb - s.block0;
     const int slot = bseg / s.bps, blk = bseg - slot * s.bps;
     if (L.route) {
-        route_block(L, (float *)smem, rsel, rwt, &rshg, &rbad, rcnt);
+        if (!w.wait()) return;
+        route_block(L, vb, (float *)smem, rsel, rwt, &rshg, &rbad, rcnt);
+    } else if (s.eidx) {
+        if (!w.wait()) return;                    // the routing comes from an earlier phase
     }
-    const int expert = !s.eidx ? 0 : (L.route ? rsel[slot] : s.eidx[slot]);
+    const int expert = !s.eidx ? 0 : (L.route ? rsel[slot] : ldc(s.eidx + slot));
     if (TK >= 0) {
-        mv_seg<TK < 0 ? OH_Q4_K : TK>(s, slot, blk, expert, smem, red);
+        mv_seg<TK < 0 ? OH_Q4_K : TK>(s, slot, blk, expert, smem, red, w);
     } else if (oh_qdot_can((uint32_t)s.type, s.in) && (s.xqs || s.pro != OH_PRO_Q8K)) {
         switch (s.type) {
-        case OH_Q4_K: mv_seg<OH_Q4_K>(s, slot, blk, expert, smem, red); break;
-        case OH_Q6_K: mv_seg<OH_Q6_K>(s, slot, blk, expert, smem, red); break;
-        default: mv_seg<OH_Q8_0>(s, slot, blk, expert, smem, red); break;
+        case OH_Q4_K: mv_seg<OH_Q4_K>(s, slot, blk, expert, smem, red, w); break;
+        case OH_Q6_K: mv_seg<OH_Q6_K>(s, slot, blk, expert, smem, red, w); break;
+        default: mv_seg<OH_Q8_0>(s, slot, blk, expert, smem, red, w); break;
         }
     } else {
+        if (!w.wait()) return;
         mv_prologue(s, slot, blk, smem, red, false);
         const float *v = (const float *)(smem + mv_lds_v_off(s.in / 256));
-        const int row = blk * 256 + (int)threadIdx.x;
+        const int row = blk * 256 + tid_x();
         const int64_t row_base = (int64_t)expert * s.rows;
         if (row < s.rows) emit(s.y + (size_t)slot * s.ystride, s.mode, row, row_seq(s, row_base + row, v));
     }
 }
 
 // Fused MoE down projection and combine (src/ornith_rforward.c:375-409). A
-// block owns 64/nb output rows; wave j reduces slot j (the k routed experts in
-// routing order, then the shared expert) over those rows with one super-block
-// per lane. Slot j's activation is Q8_K(h_j) (h_j = silu(gate) * up, emitted
-// by the paired expert launch), formed in LDS by the block. Wave 0 then gives row r: x_r += (sum_j w_j * dot_j) + shg * dot_shared
-// in the reference's order.
-template <int T>
-OH_DEV void down_body(const oh_mvdown &D) {
+// block owns 64/nb output rows; its waves take the slots (the k routed experts
+// in routing order, then the shared expert) round-robin, MJ slots per wave at
+// most, reducing one super-block per lane over those rows. Slot j's activation
+// is Q8_K(h_j) (h_j = silu(gate) * up, emitted by the paired expert launch),
+// formed in LDS by the block. Wave 0 then gives row r:
+// x_r += (sum_j w_j * dot_j) + shg * dot_shared in the reference's order.
+template <int T, int MJ, class W>
+OH_DEV void down_body(const oh_mvdown &D, int vb, W &wt) {
     extern __shared__ __align__(16) uint8_t smem[];
-    const int lane = lane_id(), wave = (int)(threadIdx.x >> 6), nw = (int)(blockDim.x >> 6);
-    const int tid = (int)threadIdx.x;
+    constexpr int HA = MJ == 1 ? 4 : 5;                   // h float4 per thread
+    const int lane = lane_id(), wave = (tid_x() >> 6), nw = (int)(blockDim.x >> 6);
+    const int tid = tid_x();
     const int nb = D.nb, in = D.in, ns = D.k + (D.sA ? 1 : 0), rps = 64 / nb;
     const int rl = lane / nb, sb = lane - rl * nb;
     const int sq = (nb * kAS + nb * 36 + 15) & ~15;     // one slot's Q8_K planes
     float *v = (float *)(smem + ns * sq);                // ns x in f32
     float *dots = v + ns * in;                           // ns x rps f32
-    const int row0 = (int)blockIdx.x * rps;
+    const int row0 = vb * rps;
     const int row = row0 + rl;
-    const bool live = rl < rps && row < D.rows && wave < ns;
-    const int j = wave < ns ? wave : ns - 1;
-    const bool sh = j >= D.k;
-    const WP wp = sh ? WP{D.sA, D.sB, D.sC} : WP{D.A, D.B, D.C};
-    const int64_t rb = sh ? 0 : (int64_t)D.eidx[j] * D.rows;
     const int rowc = row < D.rows ? (rl < rps ? row : row0) : D.rows - 1;
-    // activations first (in <= 1024: at most 4 float4 per thread), then the
-    // weights: vector loads complete in order
+    // the routing, h and x come from earlier phases
+    if (!wt.wait()) return;
+    // activations first (at most HA float4 per thread), then the weights:
+    // vector loads complete in order
     const int nf = ns * in / 4, bd = (int)blockDim.x;
-    float4 ha[4];
-    if (in <= 1024) {
+    const bool hreg = nf <= HA * bd;
+    float4 ha[HA];
+    if (hreg) {
 #pragma unroll
-        for (int k = 0; k < 4; k++) {
+        for (int k = 0; k < HA; k++) {
             const int f = tid + bd * k < nf ? tid + bd * k : nf - 1;
             const int jj = 4 * f / in, e = 4 * f - jj * in;
-            ha[k] = *(const float4 *)(D.h + (size_t)jj * D.stride + e);
+            ha[k] = ldc4((const float4 *)(D.h + (size_t)jj * D.stride + e));
         }
     }
-    SB<T> r;
-    sb_load(r, wp, (rb + rowc) * nb + sb);
-    __builtin_amdgcn_sched_barrier(0);
-    if (in <= 1024) {
+    SB<T> r[MJ];
 #pragma unroll
-        for (int k = 0; k < 4; k++)
+    for (int m = 0; m < MJ; m++) {
+        const int j0 = wave + nw * m, j = j0 < ns ? j0 : ns - 1;
+        const bool sh = j >= D.k;
+        const WP wp = sh ? WP{D.sA, D.sB, D.sC} : WP{D.A, D.B, D.C};
+        const int64_t rb = sh ? 0 : (int64_t)ldc(D.eidx + j) * D.rows;
+        sb_load(r[m], wp, (rb + rowc) * nb + sb);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if (hreg) {
+#pragma unroll
+        for (int k = 0; k < HA; k++)
             if (tid + bd * k < nf) ((float4 *)v)[tid + bd * k] = make_float4(ha[k].x, ha[k].y, ha[k].z, ha[k].w);
     } else {
         for (int i = tid; i < ns * in; i += bd) {
             const int jj = i / in, e = i - jj * in;
-            v[i] = D.h[(size_t)jj * D.stride + e];
+            v[i] = ldc(D.h + (size_t)jj * D.stride + e);
         }
     }
     lds_barrier();
@@ -796,40 +847,60 @@ OH_DEV void down_body(const oh_mvdown &D) {
                           (int16_t *)(b + mv_lds_bs_off(nb)), kAS);
     }
     lds_barrier();
-    if (wave < ns) {
-        const uint8_t *b = smem + (size_t)j * sq;
-        const float tw = sb_term(r, (const int8_t *)b + sb * kAS, (const int16_t *)(b + mv_lds_bs_off(nb)) + sb * 16,
-                                 ((const float *)(b + mv_lds_d_off(nb)))[sb]);
-        const float t = live ? tw : 0.0f;
-        float acc = 0.0f;
-        for (int i = 0; i < nb; i++) acc += shfl(t, rl * nb + i);
-        if (rl < rps && sb == 0) dots[j * rps + rl] = acc;
+#pragma unroll
+    for (int m = 0; m < MJ; m++) {
+        const int j = wave + nw * m;
+        if (j < ns) {
+            const uint8_t *b = smem + (size_t)j * sq;
+            const float tw = sb_term(r[m], (const int8_t *)b + sb * kAS,
+                                     (const int16_t *)(b + mv_lds_bs_off(nb)) + sb * 16,
+                                     ((const float *)(b + mv_lds_d_off(nb)))[sb]);
+            const bool live = rl < rps && row < D.rows;
+            const float t = live ? tw : 0.0f;
+            float acc = 0.0f;
+            for (int i = 0; i < nb; i++) acc += shfl(t, rl * nb + i);
+            if (rl < rps && sb == 0) dots[j * rps + rl] = acc;
+        }
     }
     lds_barrier();
     if (wave == 0 && lane < rps && row0 + lane < D.rows) {
         float acc = 0.0f;
-        for (int jj = 0; jj < D.k; jj++) acc += D.w[jj] * dots[jj * rps + lane];
+        for (int jj = 0; jj < D.k; jj++) acc += ldc(D.w + jj) * dots[jj * rps + lane];
         if (D.sA) {
             const float so = dots[D.k * rps + lane];
-            const float vv = D.shg ? so * *D.shg : so;
+            const float vv = D.shg ? so * ldc(D.shg) : so;
             acc += vv;
         }
-        D.x[row0 + lane] = D.x[row0 + lane] + acc;
+        stc(D.x + row0 + lane, ldc(D.x + row0 + lane) + acc);
     }
 }
 
 } // namespace
 
-extern "C" __global__ void __launch_bounds__(256) oh_k_mv_q4k(oh_mvlaunch L) { mv_body<OH_Q4_K>(L); }
-extern "C" __global__ void __launch_bounds__(256) oh_k_mv_q6k(oh_mvlaunch L) { mv_body<OH_Q6_K>(L); }
-extern "C" __global__ void __launch_bounds__(256) oh_k_mv_q80(oh_mvlaunch L) { mv_body<OH_Q8_0>(L); }
-extern "C" __global__ void __launch_bounds__(256) oh_k_mv_mixed(oh_mvlaunch L) { mv_body<-1>(L); }
+extern "C" __global__ void __launch_bounds__(256) oh_k_mv_q4k(oh_mvlaunch L) {
+    NoWait w;
+    mv_body<OH_Q4_K>(L, (int)blockIdx.x, w);
+}
+extern "C" __global__ void __launch_bounds__(256) oh_k_mv_q6k(oh_mvlaunch L) {
+    NoWait w;
+    mv_body<OH_Q6_K>(L, (int)blockIdx.x, w);
+}
+extern "C" __global__ void __launch_bounds__(256) oh_k_mv_q80(oh_mvlaunch L) {
+    NoWait w;
+    mv_body<OH_Q8_0>(L, (int)blockIdx.x, w);
+}
+extern "C" __global__ void __launch_bounds__(256) oh_k_mv_mixed(oh_mvlaunch L) {
+    NoWait w;
+    mv_body<-1>(L, (int)blockIdx.x, w);
+}
 
+// one wave per slot (blockDim = 64 * slots)
 extern "C" __global__ void __launch_bounds__(640) oh_k_mv_down(oh_mvdown D) {
+    NoWait w;
     switch (D.type) {
-    case OH_Q4_K: down_body<OH_Q4_K>(D); break;
-    case OH_Q6_K: down_body<OH_Q6_K>(D); break;
-    default: down_body<OH_Q8_0>(D); break;
+    case OH_Q4_K: down_body<OH_Q4_K, 1>(D, (int)blockIdx.x, w); break;
+    case OH_Q6_K: down_body<OH_Q6_K, 1>(D, (int)blockIdx.x, w); break;
+    default: down_body<OH_Q8_0, 1>(D, (int)blockIdx.x, w); break;
     }
 }
 
@@ -844,7 +915,7 @@ oh_k_rmsnorm_q8k(const float *x, const float *norm_w, float eps, int n,
                  float *xn_out, int8_t *qs, float *d, int16_t *bs) {
     __shared__ float v[8192];
     __shared__ double red[4];
-    const int tid = (int)threadIdx.x, wave = tid >> 6;
+    const int tid = tid_x(), wave = tid >> 6;
     for (int i = tid; i < n; i += 256) v[i] = x[i];
     __syncthreads();
     if (norm_w) {
@@ -869,7 +940,7 @@ extern "C" __global__ void __launch_bounds__(256)
 oh_k_swiglu_q8k(const float *g, const float *u, int n, float *h_out,
                 int8_t *qs, float *d, int16_t *bs) {
     __shared__ float v[8192];
-    const int vec = (int)blockIdx.x, tid = (int)threadIdx.x, wave = tid >> 6;
+    const int vec = (int)blockIdx.x, tid = tid_x(), wave = tid >> 6;
     const float *gv = g + (int64_t)vec * n;
     const float *uv = u ? u + (int64_t)vec * n : nullptr;
     for (int i = tid; i < n; i += 256) v[i] = uv ? ref_silu(gv[i]) * uv[i] : gv[i];
@@ -885,7 +956,7 @@ extern "C" __global__ void __launch_bounds__(256)
 oh_k_dequant(const uint8_t *A, const uint8_t *B, const uint8_t *C, int type, int in,
              int64_t row0, int64_t nrows, float *out) {
     const int64_t n = nrows * in;
-    for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < n; e += (int64_t)gridDim.x * 256) {
+    for (int64_t e = (int64_t)blockIdx.x * 256 + tid_x(); e < n; e += (int64_t)gridDim.x * 256) {
         const int64_t r = row0 + e / in;
         const int i = (int)(e % in);
         float y = 0.0f;

@@ -140,3 +140,101 @@ typedef struct {
     float *x;                      // residual, += combine
     int type, nb, in, rows, k, stride;
 } oh_mvdown;
+
+// ---- operations of the token step -------------------------------------------
+// The decode step is a fixed list of operations. Each one runs either as its
+// own kernel launch (captured into a HIP graph) or as one phase of the
+// persistent step kernel, where grid barriers separate consecutive phases. An
+// operation is split into nvb virtual blocks of 256 threads (one wave for the
+// delta step); the current position is read from device memory at the start
+// of each kernel.
+enum {
+    OH_OP_MV = 0,          // u.mv, kernel variant tk
+    OH_OP_MV_DOWN,         // u.down
+    OH_OP_EMBED,           // u.embed
+    OH_OP_DELTA,           // u.delta
+    OH_OP_ATTN_PREP,       // u.prep
+    OH_OP_ATTN_SCORES,     // u.attn
+    OH_OP_ATTN_OUT,        // u.attn
+    OH_OP_ATTN_FLASH,      // u.attn
+    OH_OP_ATTN_COMBINE,    // u.attn
+    OH_OP_MOE_COMBINE,     // u.comb
+    OH_OP_ARGMAX1,         // u.am
+    OH_OP_ARGMAX2,         // u.am
+    OH_OP_COUNT
+};
+
+typedef struct {
+    const uint8_t *A, *B, *C;
+    const int32_t *toks;
+    float *x;
+    int type, in;
+} oh_op_embed;
+
+typedef struct {
+    const float *cat, *ab, *gate, *conv_w, *ssm_a, *dt_bias;
+    float *conv_state, *S, *out, *out_gate;
+    double *out_runs;
+    int dk, nk, nv, K, cc;
+    float out_scale;
+} oh_op_delta;
+
+typedef struct {
+    const float *qproj, *kin, *vin, *q_norm, *k_norm;
+    const float *rope;             // (cos, sin) per (position, pair)
+    float *qr, *gate;
+    uint32_t *Kt;
+    float *Ks;
+    int8_t *Vq;
+    float *Vs;
+    int nh, nkv, hd, rot, cap;
+    float eps;
+} oh_op_prep;
+
+// GQA scores / ordered output / flash chunks / flash merge
+typedef struct {
+    const float *qr, *gate;
+    const uint32_t *Kt;
+    const float *Ks;
+    const int8_t *Vq;
+    const float *Vs;
+    float *scores, *part_o, *part_ml, *out;
+    int nh, nkv, hd, cap, exact_max, hb;
+    float scale;
+} oh_op_attn;
+
+typedef struct {
+    float *x;
+    const float *o, *w, *so, *shgate;
+    int k, H;
+} oh_op_combine;
+
+typedef struct {
+    const float *v;
+    float *bv;
+    int *bi;
+    int n, nblk;
+    int32_t *toks, *best;
+} oh_op_argmax;
+
+typedef struct {
+    int kind, nvb;
+    int tk;                // OH_OP_MV: OH_Q4_K / OH_Q6_K / OH_Q8_0, or -1 (mixed)
+    int lds;               // dynamic LDS bytes of a standalone launch
+    union {
+        oh_mvlaunch mv;
+        oh_mvdown down;
+        oh_op_embed embed;
+        oh_op_delta delta;
+        oh_op_prep prep;
+        oh_op_attn attn;
+        oh_op_combine comb;
+        oh_op_argmax am;
+    } u;
+} oh_op;
+
+// Persistent step kernel: counters of one program phase (one per 64-byte
+// line, OH_STEP_NCTR of them) and the io words it uses.
+#define OH_STEP_NCTR 32
+#define OH_STEP_CSTRIDE 16
+enum { OH_IO_POS = 0, OH_IO_BEST = 1, OH_IO_EPOCH_BODY = 2, OH_IO_EPOCH_HEAD = 3, OH_IO_ERR = 4 };
