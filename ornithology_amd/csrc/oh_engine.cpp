@@ -399,6 +399,7 @@ static void mv_plan(MvBuild &b, int waves = 4096) {
         if (need > b.lds) b.lds = need;
     }
     if (b.L.route && ((b.L.ne + 3) & ~3) * 4 > b.lds) b.lds = ((b.L.ne + 3) & ~3) * 4;
+
     b.L.total_blocks = blocks;
 }
 
@@ -907,6 +908,8 @@ struct ornith_hip_session {
     float *qproj = nullptr, *kb = nullptr, *vb = nullptr, *qr = nullptr, *agate = nullptr, *scores = nullptr;
     float *fpo = nullptr;         // flash attention: chunk outputs [nkv][chunks][nh/nkv][hd]
     float *fpml = nullptr;        // flash attention: chunk (max, sum) [nkv][chunks][nh/nkv][2]
+    float *ddots = nullptr;       // step kernel's MoE down: slot dots [slots][hidden]
+    int *dcnt = nullptr;          // step kernel's MoE down: blocks done per row group
     float *osz = nullptr;         // delta step: silu(gate) per output row
     double *oruns = nullptr;      // delta step: sum of o^2 per 64-row run
     int exact_max = 1024;         // contexts up to this walk the attention sum in one block
@@ -941,7 +944,7 @@ struct ornith_hip_session {
 
 enum { K_MATVEC = 0, K_NORM_Q8K, K_SWIGLU_Q8K, K_EMBED, K_DELTA, K_ATTN_PREP, K_ATTN_SCORES,
        K_ATTN_OUT, K_ROUTE, K_COMBINE, K_ARGMAX, K_ADVANCE, K_MV_DOWN, K_ATTN_FLASH, K_ATTN_COMBINE,
-       K_MATVEC_Q6K, K_MATVEC_Q80, K_MATVEC_MIXED, K_STEP_BODY, K_STEP_HEAD };
+       K_MATVEC_Q6K, K_MATVEC_Q80, K_MATVEC_MIXED, K_STEP_BODY, K_STEP_HEAD, K_ATTN_MAIN };
 
 static int rec_begin(ornith_hip_session *s, hipStream_t st) {
     if (!s->rec) return ORNITH_HIP_OK;
@@ -992,6 +995,7 @@ struct Prog {
     std::vector<double> bytes;    // algorithmic HBM bytes
     int lds = 0;                  // largest dynamic LDS of an operation
     int waves = 4096;             // matvec planning target
+    bool step = false;            // built for the persistent step kernel
 };
 static oh_op op_new(int kind, int nvb, int lds = 0) {
     oh_op o;
@@ -1083,6 +1087,8 @@ extern "C" int ornith_hip_session_new(ornith_hip_model *m, int cap, ornith_hip_s
         A_(salloc(s, &s->fpo, (size_t)a.nh * nch * a.hd + 64));
         A_(salloc(s, &s->fpml, (size_t)a.nh * nch * 2 + 64));
     }
+    A_(salloc(s, &s->ddots, (size_t)(K + 1) * H + 64));
+    A_(salloc(s, &s->dcnt, (size_t)H + 64));
     A_(salloc(s, &s->osz, (size_t)a.nv * a.dv + 64));
     A_(salloc(s, &s->oruns, (size_t)a.nv * a.dv / 64 + 64));
     {
@@ -1176,7 +1182,7 @@ static int build_body(ornith_hip_session *s, Prog &P) {
             const float scale = 1.0f / sqrtf((float)a.hd);
             // contexts up to exact_max: scores + the reference-order walk;
             // longer ones: flash chunks + merge (each pair exits for the other)
-            const bool ex = s->pos + 1 <= s->exact_max;
+            const bool ex = s->pos + 1 <= (s->exact_max < 2048 ? s->exact_max : 2048);
             oh_op_attn at;
             memset(&at, 0, sizeof at);
             at.qr = s->qr; at.gate = s->agate; at.Kt = z.Kt; at.Ks = z.Ks; at.Vq = z.Vq; at.Vs = z.Vs;
@@ -1185,15 +1191,15 @@ static int build_body(ornith_hip_session *s, Prog &P) {
             at.hb = oh_flash_hb(a.nh, a.nkv); at.scale = scale;
             const int nch = (s->kvcap + oh_flash_chunk() - 1) / oh_flash_chunk();
             const double nchd = ceil(T / (double)oh_flash_chunk());
-            oh_op o1 = op_new(OH_OP_ATTN_SCORES, a.nh * ((s->kvcap + 255) / 256));
-            o1.u.attn = at;
-            prog_add(P, o1, K_ATTN_SCORES, ex ? T * a.nkv * (a.hd + 4.0) + 4.0 * T * a.nh + 4.0 * aqd : 0.0);
-            oh_op o2 = op_new(OH_OP_ATTN_OUT, a.nh / (256 / a.hd));
-            o2.u.attn = at;
-            prog_add(P, o2, K_ATTN_OUT, ex ? T * a.nkv * (a.hd + 4.0) + 8.0 * T * a.nh + 8.0 * aqd : 0.0);
-            oh_op o3 = op_new(OH_OP_ATTN_FLASH, a.nkv * (a.nh / a.nkv / at.hb) * nch, oh_flash_lds_bytes(a.nh, a.nkv, a.hd));
+            // exact walk (its scores in LDS) or flash chunks, then the merge
+            // of the chunks (which exits after an exact walk)
+            const int nv_ex = a.nh / (256 / a.hd), nv_fl = a.nkv * (a.nh / a.nkv / at.hb) * nch;
+            const int lds_ex = oh_exact_lds_bytes(a.hd, s->exact_max), lds_fl = oh_flash_lds_bytes(a.nh, a.nkv, a.hd);
+            oh_op o3 = op_new(OH_OP_ATTN_MAIN, nv_ex > nv_fl ? nv_ex : nv_fl, lds_ex > lds_fl ? lds_ex : lds_fl);
             o3.u.attn = at;
-            prog_add(P, o3, K_ATTN_FLASH, ex ? 0.0 : T * a.nkv * (2.0 * a.hd + 8.0) + 4.0 * aqd + 8.0 * nchd * aqd);
+            prog_add(P, o3, K_ATTN_MAIN,
+                     ex ? 2.0 * T * a.nkv * (a.hd + 4.0) + 4.0 * T * a.nh + 12.0 * aqd
+                        : T * a.nkv * (2.0 * a.hd + 8.0) + 4.0 * aqd + 8.0 * nchd * aqd);
             oh_op o4 = op_new(OH_OP_ATTN_COMBINE, a.nh * (a.hd / 64));
             o4.u.attn = at;
             prog_add(P, o4, K_ATTN_COMBINE, ex ? 0.0 : 4.0 * nchd * (aqd + 2.0 * a.nh) + 12.0 * aqd);
@@ -1272,6 +1278,7 @@ static int build_body(ornith_hip_session *s, Prog &P) {
             const int rps = nbd >= 1 ? 64 / nbd : 1;
             const int sq = (nbd * 272 + nbd * 36 + 15) & ~15, dlds = ns * sq + ns * I * 4 + ns * rps * 4;
             const bool fuse = paired && oh_qdot_can(dt, I) && nbd >= 1 && nbd <= 64 && ns <= 10 && dlds <= 65536 &&
+                              (!P.step || I <= 1024) &&
                               (!y.gate_sh || (y.down_sh->type == dt && sI == I));
             if (fuse) {
                 oh_mvdown D;
@@ -1283,6 +1290,13 @@ static int build_body(ornith_hip_session *s, Prog &P) {
                 D.type = (int)dt; D.nb = nbd; D.in = I; D.rows = H; D.k = K; D.stride = IW;
                 const double db = (double)ns * ((double)H * gguf_nbytes(dt, (uint64_t)I) + 4.0 * I) + 8.0 * H + 4.0 * K;
                 oh_op o = op_new(OH_OP_MV_DOWN, (H + rps - 1) / rps, dlds);
+                if (P.step) {
+                    // split form: (row group, 4-slot group) blocks, last one combines
+                    D.dots = s->ddots;
+                    D.cnt = s->dcnt;
+                    o.nvb = (H + rps - 1) / rps * ((ns + 3) / 4);
+                    o.lds = 4 * ((I * 4 + nbd * 272 + nbd * 36 + 15) & ~15);
+                }
                 o.u.down = D;
                 prog_add(P, o, K_MV_DOWN, db);
             } else {
@@ -1405,6 +1419,7 @@ static int step_prepare(ornith_hip_session *s) {
         if (grid < OH_STEP_NCTR) return ORNITH_HIP_OK;
         Prog B, Hd;
         B.waves = Hd.waves = grid * 4;
+        B.step = Hd.step = true;
         CHK(build_body(s, B));
         CHK(build_head(s, Hd));
         const int lds = B.lds > Hd.lds ? B.lds : Hd.lds;
@@ -1813,6 +1828,8 @@ extern "C" int ornith_hip_session_time_kind(ornith_hip_session *s, int kind, int
         CHK(step_prepare(s));
         if (!s->step_grid) { seterr("time_kind: the step kernel is not available"); return ORNITH_HIP_ERR_UNSUPPORTED; }
         Prog P;
+        P.step = true;
+        P.waves = s->step_grid * 4;
         CHK(body ? build_body(s, P) : build_head(s, P));
         double by = 0.0;
         for (double b : P.bytes) by += b;
@@ -1912,6 +1929,8 @@ extern "C" int ornith_hip_session_profile_phases(ornith_hip_session *s, int max_
     if (!s->step_grid) { seterr("profile_phases: the step kernel is not available"); return ORNITH_HIP_ERR_UNSUPPORTED; }
     if (!s->ts) CHK(salloc(s, &s->ts, (size_t)s->sp_body.n + 8));
     Prog P;
+    P.step = true;
+    P.waves = s->step_grid * 4;
     CHK(build_body(s, P));
     CHK(step_launch(s, true, nullptr, false));        // warm
     CHK(step_launch(s, true, s->ts, false));

@@ -64,12 +64,7 @@ hipError_t oh_launch_op(const oh_op *op, const int32_t *io, hipStream_t st) {
         }
         break;
     case OH_OP_ATTN_PREP: hipLaunchKernelGGL(oh_k_attn_prep, g, b256, 0, st, op->u.prep, io); break;
-    case OH_OP_ATTN_SCORES: hipLaunchKernelGGL(oh_k_attn_scores, g, b256, 0, st, op->u.attn, io); break;
-    case OH_OP_ATTN_OUT: hipLaunchKernelGGL(oh_k_attn_out, g, b256, 0, st, op->u.attn, io); break;
-    case OH_OP_ATTN_FLASH:
-        if (op->u.attn.hb == 2) hipLaunchKernelGGL(oh_k_attn_flash<2>, g, b256, (size_t)op->lds, st, op->u.attn, io);
-        else hipLaunchKernelGGL(oh_k_attn_flash<1>, g, b256, (size_t)op->lds, st, op->u.attn, io);
-        break;
+    case OH_OP_ATTN_MAIN: hipLaunchKernelGGL(oh_k_attn_main, g, b256, (size_t)op->lds, st, op->u.attn, io); break;
     case OH_OP_ATTN_COMBINE: hipLaunchKernelGGL(oh_k_attn_combine, g, b256, 0, st, op->u.attn, io); break;
     case OH_OP_MOE_COMBINE: hipLaunchKernelGGL(oh_k_moe_combine, g, b256, 0, st, op->u.comb); break;
     case OH_OP_ARGMAX1: hipLaunchKernelGGL(oh_k_argmax1, g, b256, 0, st, op->u.am); break;
@@ -79,8 +74,8 @@ hipError_t oh_launch_op(const oh_op *op, const int32_t *io, hipStream_t st) {
     return hipGetLastError();
 }
 
-// query heads per flash block: two (one when the group has a single head)
-int oh_flash_hb(int nh, int nkv) { return nh / nkv >= 2 ? 2 : 1; }
+// query heads per flash block: up to four of a KV head's group
+int oh_flash_hb(int nh, int nkv) { return nh / nkv >= 4 ? 4 : (nh / nkv >= 2 ? 2 : 1); }
 
 int oh_flash_lds_bytes(int nh, int nkv, int hd) {
     const int HB = oh_flash_hb(nh, nkv);
@@ -88,6 +83,12 @@ int oh_flash_lds_bytes(int nh, int nkv, int hd) {
            2 * kFlashCh * 4;
 }
 int oh_flash_chunk(void) { return kFlashCh; }
+
+// exact attention walk: the scores of a block's 256/hd heads in LDS
+int oh_exact_lds_bytes(int hd, int exact_max) {
+    const int lim = exact_max < kExactMax ? (exact_max > 0 ? exact_max : 0) : kExactMax;
+    return (256 / hd) * lim * 4;
+}
 
 // delta step LDS of the working wave (step kernel: dynamic LDS)
 int oh_delta_lds_bytes(int dk) { return (2 * dk + 64 * (dk + 4)) * 4; }

@@ -23,6 +23,7 @@ int oh_flash_hb(int nh, int nkv);
 int oh_flash_lds_bytes(int nh, int nkv, int hd);
 int oh_flash_chunk(void);
 int oh_delta_lds_bytes(int dk);
+int oh_exact_lds_bytes(int hd, int exact_max);
 // persistent step kernel: resident 256-thread blocks per CU at this dynamic
 // LDS size, and the cooperative launch of a program (prog in device memory)
 hipError_t oh_step_blocks_per_cu(int lds_bytes, int *blocks);

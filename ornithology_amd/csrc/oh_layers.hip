@@ -105,21 +105,6 @@ OH_DEV void delta_body(const oh_op_delta &a, int vb, int pos, float *lds, W &w) 
     const int p = pos & 1;
     const float *win = a.conv_state + (size_t)p * (K - 1) * cc;
     float *nwin = a.conv_state + (size_t)(1 - p) * (K - 1) * cc;
-    // the state slab: rows [slab*64, +64) of head hv, contiguous
-    float4 st[DK / 4];
-    if (act) {
-        const float4 *Sr = (const float4 *)(a.S + ((size_t)hv * DK + slab * 64) * DK);
-#pragma unroll
-        for (int i = 0; i < DK / 4; i++) st[i] = ldg(Sr + lane + 64 * i);
-    }
-    if (!w.wait() || !act) return;
-    // slab -> LDS, row-padded (frees the slab's registers for the step)
-#pragma unroll
-    for (int i = 0; i < DK / 4; i++) {
-        const int f = lane + 64 * i, row = (4 * f) / DK, col = (4 * f) % DK;
-        *(float4 *)(tile + row * TS + col) = make_float4(st[i].x, st[i].y, st[i].z, st[i].w);
-    }
-
     // channels of a: q channels kh*DK + lane + 64i (i < NQ), k channels
     // likewise, then this row's v channel
     constexpr int NCH = 2 * NQ + 1;
@@ -130,18 +115,43 @@ OH_DEV void delta_body(const oh_op_delta &a, int vb, int pos, float *lds, W &w) 
         ch[NQ + i] = qd + kh * DK + lane + 64 * i;
     }
     ch[2 * NQ] = 2 * qd + hv * DK + r;
-    float cw[NCH][KMAX], wv[NCH][KMAX], cx[NCH];
+    // everything that does not depend on the previous phase is requested
+    // before the grid wait: the state slab (rows [slab*64, +64) of head hv,
+    // contiguous), the conv weights and window, ssm_a and dt_bias
+    float4 st[DK / 4];
+    float cw[NCH][KMAX], wv[NCH][KMAX], sa = 0.0f, dtb = 0.0f;
+    if (act) {
+        const float4 *Sr = (const float4 *)(a.S + ((size_t)hv * DK + slab * 64) * DK);
 #pragma unroll
-    for (int c = 0; c < NCH; c++) {
+        for (int i = 0; i < DK / 4; i++) st[i] = ldg(Sr + lane + 64 * i);
 #pragma unroll
-        for (int j = 0; j < KMAX; j++) {
-            cw[c][j] = j < K ? ldg(a.conv_w + (size_t)ch[c] * K + j) : 0.0f;
-            wv[c][j] = j < K - 1 ? ldg(win + (size_t)j * cc + ch[c]) : 0.0f;
+        for (int c = 0; c < NCH; c++) {
+            if (KMAX == 4 && K == 4) {
+                const float4 c4 = ldg((const float4 *)(a.conv_w + (size_t)ch[c] * 4));
+                cw[c][0] = c4.x; cw[c][1] = c4.y; cw[c][2] = c4.z; cw[c][3] = c4.w;
+            } else {
+#pragma unroll
+                for (int j = 0; j < KMAX; j++) cw[c][j] = j < K ? ldg(a.conv_w + (size_t)ch[c] * K + j) : 0.0f;
+            }
+#pragma unroll
+            for (int j = 0; j < KMAX; j++) wv[c][j] = j < K - 1 ? ldg(win + (size_t)j * cc + ch[c]) : 0.0f;
         }
-        cx[c] = ldc(a.cat + ch[c]);
+        sa = ldg(a.ssm_a + hv);
+        dtb = ldg(a.dt_bias + hv);
     }
-    const float sa = ldg(a.ssm_a + hv), av = ldc(a.ab + hv), bv = ldc(a.ab + nv + hv), dtb = ldg(a.dt_bias + hv);
+    if (!w.wait() || !act) return;
+    // then this step's inputs from the input projection
+    float cx[NCH];
+#pragma unroll
+    for (int c = 0; c < NCH; c++) cx[c] = ldc(a.cat + ch[c]);
+    const float av = ldc(a.ab + hv), bv = ldc(a.ab + nv + hv);
     const float gz = ldc(a.gate + (size_t)hv * DK + r);
+    // slab -> LDS, row-padded (frees the slab's registers for the step)
+#pragma unroll
+    for (int i = 0; i < DK / 4; i++) {
+        const int f = lane + 64 * i, row = (4 * f) / DK, col = (4 * f) % DK;
+        *(float4 *)(tile + row * TS + col) = make_float4(st[i].x, st[i].y, st[i].z, st[i].w);
+    }
 
     // causal depthwise conv (no bias) + SiLU
     float cv[NCH];
@@ -184,35 +194,41 @@ OH_DEV void delta_body(const oh_op_delta &a, int vb, int pos, float *lds, W &w) 
     const float beta = ref_sigmoid(bv);
     wave_lds_sync();
 
-    // the lane's row walked twice from LDS (s = S * alpha is recomputed the
-    // same way): sk = sum_c s_c k_c; then s_c += u k_c, o = sum_c s_c q_c
+    // the lane's row in registers: s = S * alpha; sk = sum_c s_c k_c; then
+    // s_c += u k_c and o = sum_c s_c q_c, each sum in column order
     float *tr = tile + lane * TS;
-    float sk = 0.0f;
-#pragma unroll 8
+    float sr[DK];
+#pragma unroll
     for (int c = 0; c < DK / 4; c++) {
         const float4 v = *(const float4 *)(tr + 4 * c);
+        sr[4 * c + 0] = v.x * alpha;
+        sr[4 * c + 1] = v.y * alpha;
+        sr[4 * c + 2] = v.z * alpha;
+        sr[4 * c + 3] = v.w * alpha;
+    }
+    float sk = 0.0f;
+#pragma unroll
+    for (int c = 0; c < DK / 4; c++) {
         const float4 kk = *(const float4 *)(kn + 4 * c);
-        sk += (v.x * alpha) * kk.x;
-        sk += (v.y * alpha) * kk.y;
-        sk += (v.z * alpha) * kk.z;
-        sk += (v.w * alpha) * kk.w;
+        sk += sr[4 * c + 0] * kk.x;
+        sk += sr[4 * c + 1] * kk.y;
+        sk += sr[4 * c + 2] * kk.z;
+        sk += sr[4 * c + 3] * kk.w;
     }
     const float u = beta * (cv[2 * NQ] - sk);
     float o = 0.0f;
-#pragma unroll 8
+#pragma unroll
     for (int c = 0; c < DK / 4; c++) {
-        const float4 v = *(const float4 *)(tr + 4 * c);
         const float4 kk = *(const float4 *)(kn + 4 * c), qq = *(const float4 *)(qn + 4 * c);
-        float4 sv = make_float4(v.x * alpha, v.y * alpha, v.z * alpha, v.w * alpha);
-        sv.x += u * kk.x;
-        sv.y += u * kk.y;
-        sv.z += u * kk.z;
-        sv.w += u * kk.w;
-        o += sv.x * qq.x;
-        o += sv.y * qq.y;
-        o += sv.z * qq.z;
-        o += sv.w * qq.w;
-        *(float4 *)(tr + 4 * c) = sv;
+        sr[4 * c + 0] += u * kk.x;
+        sr[4 * c + 1] += u * kk.y;
+        sr[4 * c + 2] += u * kk.z;
+        sr[4 * c + 3] += u * kk.w;
+        o += sr[4 * c + 0] * qq.x;
+        o += sr[4 * c + 1] * qq.y;
+        o += sr[4 * c + 2] * qq.z;
+        o += sr[4 * c + 3] * qq.w;
+        *(float4 *)(tr + 4 * c) = make_float4(sr[4 * c], sr[4 * c + 1], sr[4 * c + 2], sr[4 * c + 3]);
     }
     wave_lds_sync();
     float4 *Sw = (float4 *)(a.S + ((size_t)hv * DK + slab * 64) * DK);
@@ -312,50 +328,19 @@ OH_DEV void prep_body(const oh_op_prep &a, int vb, int pos, W &w) {
 // any workgroup of this launch read its cache line. Plain loads therefore see
 // every entry.
 
-// scores[h][t] = (sum_i q_i*code_i) * Ks_t * scale, sequential over i
-// (src/ornith_attn.c:80-85,119-122). Virtual block (h, 256-position tile):
-// vb = tile * nh + h; positions > pos exit, and everything exits when the
-// context is longer than exact_max (the flash path takes it).
-template <class W>
-OH_DEV void scores_body(const oh_op_attn &a, int vb, int pos, W &w) {
-    __shared__ float q[256];
-    const int nh = a.nh, nkv = a.nkv, hd = a.hd, cap = a.cap;
-    const int h = vb % nh, ty = vb / nh, t = ty * 256 + tid_x();
-    const int T = pos + 1;
-    if (ty * 256 >= T || T > a.exact_max) return;
-    if (!w.wait()) return;
-    const int kvh = h / (nh / nkv);
-    if (tid_x() < hd) q[tid_x()] = ldc(a.qr + (size_t)h * hd + tid_x());
-    __syncthreads();
-    if (t >= T) return;
-    const uint32_t *kw = a.Kt + (size_t)kvh * (hd / 4) * cap + t;
-    float acc = 0.0f;
-    for (int w0 = 0; w0 < hd / 4; w0 += 16) {
-        uint32_t wd[16];
-#pragma unroll
-        for (int u = 0; u < 16; u++) wd[u] = w0 + u < hd / 4 ? ldg(kw + (size_t)(w0 + u) * cap) : 0u;
-#pragma unroll
-        for (int u = 0; u < 16; u++) {
-            if (w0 + u >= hd / 4) break;
-            const int wi = w0 + u;
-            acc += q[4 * wi + 0] * (float)(int8_t)(wd[u] & 0xff);
-            acc += q[4 * wi + 1] * (float)(int8_t)((wd[u] >> 8) & 0xff);
-            acc += q[4 * wi + 2] * (float)(int8_t)((wd[u] >> 16) & 0xff);
-            acc += q[4 * wi + 3] * (float)(int8_t)(wd[u] >> 24);
-        }
-    }
-    const float ks = ldg(a.Ks + (size_t)t * nkv + kvh);
-    const float sc = ks == 0.0f ? 0.0f : acc * ks;
-    stc(a.scores + (size_t)h * cap + t, sc * a.scale);
-}
+// Longest context of the exact walk (its scores stay in LDS).
+constexpr int kExactMax = 2048;
 
-// softmax over T (src/ornith_tensor.c:108-115; tree-ordered double sum) and the
-// output o_i = sum_t (p_t*Vs_t)*code_t,i, sequential over t, skipping zero
-// weights (src/ornith_attn.c:132-140); then o *= sigmoid(gate). A virtual
-// block covers 256/hd heads and walks all T positions in the reference's
-// order. Contexts longer than exact_max exit (the flash path takes them).
+// Exact GQA output of the block's 256/hd query heads (virtual block g):
+// scores s_t = (sum_i q_i*code_i) * Ks_t * scale, sequential over i
+// (src/ornith_attn.c:80-85,119-122), kept in LDS; softmax over T
+// (src/ornith_tensor.c:108-115; tree-ordered double sum) and the output
+// o_i = sum_t (p_t*Vs_t)*code_t,i, sequential over t, skipping zero weights
+// (src/ornith_attn.c:132-140); then o *= sigmoid(gate).
 template <class W>
-OH_DEV void out_body(const oh_op_attn &a, int vb, int pos, W &w) {
+OH_DEV void exact_body(const oh_op_attn &a, int vb, int pos, int lim, W &w) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ float q[256];
     __shared__ float pbuf[4][256];
     __shared__ float inv_s[4], mx_s[4];
     __shared__ double red[4];
@@ -363,19 +348,51 @@ OH_DEV void out_body(const oh_op_attn &a, int vb, int pos, W &w) {
     const int nh = a.nh, nkv = a.nkv, hd = a.hd, cap = a.cap;
     const int hpb = 256 / hd, t = tid_x(), g = vb;
     const int T = pos + 1;
-    if (T > a.exact_max) return;
+    if (T > lim || g * hpb >= nh) return;
     if (!w.wait()) return;
+    float *sc = (float *)smem;                               // [hpb][lim]
+    q[t] = ldc(a.qr + (size_t)g * 256 + t);                  // the block's heads are contiguous
+    __syncthreads();
     for (int hl = 0; hl < hpb; hl++) {
-        const float *sc = a.scores + (size_t)(g * hpb + hl) * cap;
+        const int kvh = (g * hpb + hl) / (nh / nkv);
+        const float *qh = q + hl * hd;
+        for (int t0 = 0; t0 < T; t0 += 256) {
+            const int tt = t0 + t;
+            if (tt < T) {
+                const uint32_t *kw = a.Kt + (size_t)kvh * (hd / 4) * cap + tt;
+                float acc = 0.0f;
+                for (int w0 = 0; w0 < hd / 4; w0 += 16) {
+                    uint32_t wd[16];
+#pragma unroll
+                    for (int u = 0; u < 16; u++) wd[u] = w0 + u < hd / 4 ? ldg(kw + (size_t)(w0 + u) * cap) : 0u;
+#pragma unroll
+                    for (int u = 0; u < 16; u++) {
+                        if (w0 + u >= hd / 4) break;
+                        const int wi = w0 + u;
+                        acc += qh[4 * wi + 0] * (float)(int8_t)(wd[u] & 0xff);
+                        acc += qh[4 * wi + 1] * (float)(int8_t)((wd[u] >> 8) & 0xff);
+                        acc += qh[4 * wi + 2] * (float)(int8_t)((wd[u] >> 16) & 0xff);
+                        acc += qh[4 * wi + 3] * (float)(int8_t)(wd[u] >> 24);
+                    }
+                }
+                const float ks = ldg(a.Ks + (size_t)tt * nkv + kvh);
+                const float v = ks == 0.0f ? 0.0f : acc * ks;
+                sc[hl * lim + tt] = v * a.scale;
+            }
+        }
+    }
+    __syncthreads();
+    for (int hl = 0; hl < hpb; hl++) {
+        const float *sh = sc + hl * lim;
         float mx = -INFINITY;
-        for (int i = t; i < T; i += 256) mx = fmaxf(mx, ldc(sc + i));
+        for (int i = t; i < T; i += 256) mx = fmaxf(mx, sh[i]);
         mx = wave_max_f(mx);
         __syncthreads();
         if (lane_id() == 0) mred[t >> 6] = mx;
         __syncthreads();
         mx = fmaxf(fmaxf(mred[0], mred[1]), fmaxf(mred[2], mred[3]));
         double sum = 0.0;
-        for (int i = t; i < T; i += 256) sum += ref_expf(ldc(sc + i) - mx);
+        for (int i = t; i < T; i += 256) sum += ref_expf(sh[i] - mx);
         sum = block_sum_d(sum, red);
         if (t == 0) { mx_s[hl] = mx; inv_s[hl] = (float)(1.0 / sum); }
     }
@@ -390,7 +407,7 @@ OH_DEV void out_body(const oh_op_attn &a, int vb, int pos, W &w) {
             const int hh = k / 256, tt = k % 256;
             const int hg = g * hpb + hh, kv2 = hg / (nh / nkv);
             if (tt < n) {
-                const float p = ref_expf(ldc(a.scores + (size_t)hg * cap + t0 + tt) - mx_s[hh]) * inv_s[hh];
+                const float p = ref_expf(sc[hh * lim + t0 + tt] - mx_s[hh]) * inv_s[hh];
                 pbuf[hh][tt] = p * ldg(a.Vs + (size_t)(t0 + tt) * nkv + kv2);
             }
         }
@@ -432,7 +449,7 @@ constexpr int kFlashCh = 64;
 // HB query heads of one KV head per virtual block (compile time: the loops
 // over heads unroll); vb = chunk * (nkv * G/HB) + group-block, G = nh/nkv.
 template <int HB, class W>
-OH_DEV void flash_body(const oh_op_attn &a, int vb, int pos, W &w) {
+OH_DEV void flash_body(const oh_op_attn &a, int vb, int pos, int lim, W &w) {
     extern __shared__ __align__(16) uint8_t fsm[];
     const int nh = a.nh, nkv = a.nkv, hd = a.hd, cap = a.cap;
     const int T = pos + 1;
@@ -440,7 +457,7 @@ OH_DEV void flash_body(const oh_op_attn &a, int vb, int pos, W &w) {
     const int bx = vb % gx, c = vb / gx;
     const int g = bx / ngb, hb0 = (bx % ngb) * HB;
     const int t0 = c * kFlashCh;
-    if (T <= a.exact_max || t0 >= T) return;
+    if (T <= lim || t0 >= T) return;
     if (!w.wait()) return;
     const int tid = tid_x(), hw = hd / 4, kst = hw + 1;
     const int nchmax = (cap + kFlashCh - 1) / kFlashCh;
@@ -536,7 +553,7 @@ OH_DEV void flash_body(const oh_op_attn &a, int vb, int pos, W &w) {
 #pragma unroll
         for (int k = 0; k < HB; k++) o[k] = 0.0f;
         const float4 *pp4 = (const float4 *)pp;
-#pragma unroll
+#pragma unroll 1
         for (int tt = 0; tt < kFlashCh / 16; tt++) {
             const uint4 cw = vt[tt * hd + i];
 #pragma unroll
@@ -563,6 +580,23 @@ OH_DEV void flash_body(const oh_op_attn &a, int vb, int pos, W &w) {
     }
 }
 
+// The attention of the current step: up to lim = min(exact_max, kExactMax)
+// positions the exact walk (virtual blocks [0, nh*hd/256)), beyond that the
+// flash chunks (virtual blocks as flash_body).
+template <class W>
+OH_DEV void attn_main_body(const oh_op_attn &a, int vb, int pos, W &w) {
+    const int lim = a.exact_max < kExactMax ? a.exact_max : kExactMax;
+    if (pos + 1 <= lim) {
+        exact_body(a, vb, pos, lim, w);
+    } else if (a.hb == 4) {
+        flash_body<4>(a, vb, pos, lim, w);
+    } else if (a.hb == 2) {
+        flash_body<2>(a, vb, pos, lim, w);
+    } else {
+        flash_body<1>(a, vb, pos, lim, w);
+    }
+}
+
 // Merge of the flash chunks of query head h (virtual block vb = y * nh + h,
 // y < hd/64; 4 waves; wave w takes chunks w, w+4, ...; a lane per dimension):
 // running max rescaling, then
@@ -572,22 +606,34 @@ OH_DEV void combine_body(const oh_op_attn &a, int vb, int pos, W &w) {
     __shared__ float sm[4][3][64];
     const int nh = a.nh, nkv = a.nkv, hd = a.hd, cap = a.cap;
     const int T = pos + 1;
-    if (T <= a.exact_max) return;
+    const int lim = a.exact_max < kExactMax ? a.exact_max : kExactMax;
+    if (T <= lim) return;
     if (!w.wait()) return;
     const int h = vb % nh, G = nh / nkv, g = h / G, hl = h % G;
     const int wave = (tid_x() >> 6), lane = (tid_x() & 63);
     const int i = (vb / nh) * 64 + lane;
     const int nch = (T + kFlashCh - 1) / kFlashCh, nchmax = (cap + kFlashCh - 1) / kFlashCh;
     float M = -INFINITY, L = 0.0f, O = 0.0f;
-    for (int c = wave; c < nch; c += 4) {
-        const size_t base = ((size_t)g * nchmax + c) * G + hl;
-        const float m = ldc(a.part_ml + base * 2), l = ldc(a.part_ml + base * 2 + 1);
-        const float o = ldc(a.part_o + base * hd + i);
-        const float mn = fmaxf(M, m);
-        const float e1 = M == -INFINITY ? 0.0f : __expf(M - mn), e2 = __expf(m - mn);
-        O = O * e1 + o * e2;
-        L = L * e1 + l * e2;
-        M = mn;
+    // chunks wave, wave+4, ... in order; their partials requested 8 at a time
+    for (int c0 = wave; c0 < nch; c0 += 32) {
+        float mb[8], lb[8], ob[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int c = c0 + 4 * u < nch ? c0 + 4 * u : c0;
+            const size_t base = ((size_t)g * nchmax + c) * G + hl;
+            mb[u] = ldc(a.part_ml + base * 2);
+            lb[u] = ldc(a.part_ml + base * 2 + 1);
+            ob[u] = ldc(a.part_o + base * hd + i);
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            if (c0 + 4 * u >= nch) break;
+            const float m = mb[u], mn = fmaxf(M, m);
+            const float e1 = M == -INFINITY ? 0.0f : __expf(M - mn), e2 = __expf(m - mn);
+            O = O * e1 + ob[u] * e2;
+            L = L * e1 + lb[u] * e2;
+            M = mn;
+        }
     }
     sm[wave][0][lane] = M; sm[wave][1][lane] = L; sm[wave][2][lane] = O;
     __syncthreads();
@@ -692,20 +738,9 @@ extern "C" __global__ void __launch_bounds__(256) oh_k_attn_prep(oh_op_prep a, c
     prep_body(a, (int)blockIdx.x, io[OH_IO_POS], w);
 }
 
-extern "C" __global__ void __launch_bounds__(256) oh_k_attn_scores(oh_op_attn a, const int32_t *io) {
+extern "C" __global__ void __launch_bounds__(256) oh_k_attn_main(oh_op_attn a, const int32_t *io) {
     NoWait w;
-    scores_body(a, (int)blockIdx.x, io[OH_IO_POS], w);
-}
-
-extern "C" __global__ void __launch_bounds__(256) oh_k_attn_out(oh_op_attn a, const int32_t *io) {
-    NoWait w;
-    out_body(a, (int)blockIdx.x, io[OH_IO_POS], w);
-}
-
-template <int HB>
-__global__ void __launch_bounds__(256) oh_k_attn_flash(oh_op_attn a, const int32_t *io) {
-    NoWait w;
-    flash_body<HB>(a, (int)blockIdx.x, io[OH_IO_POS], w);
+    attn_main_body(a, (int)blockIdx.x, io[OH_IO_POS], w);
 }
 
 extern "C" __global__ void __launch_bounds__(256) oh_k_attn_combine(oh_op_attn a, const int32_t *io) {

@@ -639,6 +639,9 @@ OH_DEV void mv_seg(const oh_mvseg &s, int slot, int blk, int expert, uint8_t *sm
         sb_load(r, (sc & (sps - 1)) ? wp2 : wp, (row_base + rowc) * nb + sb);
     };
     float gsum = 0.0f;
+    // y += dot (mode 1): the first step's output row is read together with
+    // the prologue inputs rather than after the reduction
+    float ypre = 0.0f;
     auto comp = [&](const SB<T> &r, int st) {
         const int row = (u0 + st / sps) * rps + rl;
         const bool live = st < S && rl < rps && row < s.rows;
@@ -651,8 +654,13 @@ OH_DEV void mv_seg(const oh_mvseg &s, int slot, int blk, int expert, uint8_t *sm
             if ((st & 1) == 0) gsum = acc;
             else if (live && sb == 0) emit(y, 0, row, ref_silu(gsum) * acc);
         } else if (live && sb == 0) {
-            emit(y, s.mode, row, acc);
+            if (s.mode == 1 && st == 0) stc(y + row, ypre + acc);
+            else emit(y, s.mode, row, acc);
         }
+    };
+    auto y_prefetch = [&]() {
+        const int row = u0 * rps + rl;
+        if (s.mode == 1 && !s.pair && S > 0 && rl < rps && row < s.rows && sb == 0) ypre = ldc(y + row);
     };
     if (s.in <= 4096) {
         PIn pin;
@@ -660,8 +668,10 @@ OH_DEV void mv_seg(const oh_mvseg &s, int slot, int blk, int expert, uint8_t *sm
             load(ra, 0);
             if (!w.wait()) return;
             pro_load(pin, s, slot);
+            y_prefetch();
         } else {
             pro_load(pin, s, slot);
+            y_prefetch();
             load(ra, 0);
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -669,6 +679,7 @@ OH_DEV void mv_seg(const oh_mvseg &s, int slot, int blk, int expert, uint8_t *sm
     } else {
         load(ra, 0);
         if (!w.wait()) return;
+        y_prefetch();
         mv_prologue(s, slot, blk, smem, red, true);
     }
     // ra holds step 0; a step's loads are only issued when it will be reduced
@@ -699,10 +710,12 @@ OH_DEV void route_block(const oh_mvlaunch &L, int vb, float *lg, int *sel, float
                         int *cnt) {
     const int tid = tid_x(), ne = L.ne, k = L.topk;
     const int ne4 = (ne + 3) & ~3;
+    const bool has_sh = L.shl != nullptr;
     if (tid == 0) *bad = 0;
     if (tid < 64) cnt[tid] = 0;
     for (int e = tid; e < ne4; e += 256) lg[e] = e < ne ? ldc(L.rlog + e) : -INFINITY;
     __syncthreads();
+    const float shl = has_sh ? ldc(L.shl) : 0.0f;
     // rank by strictly larger logits; equal logits inside the top k (or a
     // NaN / -inf anywhere) send the block to the sequential selection
     const float4 *l4 = (const float4 *)lg;
@@ -723,7 +736,7 @@ OH_DEV void route_block(const oh_mvlaunch &L, int vb, float *lg, int *sel, float
     __syncthreads();
     if (*bad) {
         if (tid < 64) route_wave(lg, ne, k, nullptr, sel, rw, shg);
-        if (tid == 0 && L.shl) *shg = ref_sigmoid(ldc(L.shl));
+        if (tid == 0 && has_sh) *shg = ref_sigmoid(shl);
     } else if (tid < 64) {
         // lane j: e_j = exp(l_j - max) in parallel; the sum in selection
         // order, then w_j = e_j / sum
@@ -733,12 +746,12 @@ OH_DEV void route_block(const oh_mvlaunch &L, int vb, float *lg, int *sel, float
         float sum = 0.0f;
         for (int j = 0; j < k; j++) sum += shfl(e, j);
         if (tid < k) rw[tid] = e / sum;
-        if (tid == 0 && L.shl) *shg = ref_sigmoid(ldc(L.shl));
+        if (tid == 0 && has_sh) *shg = ref_sigmoid(shl);
     }
     __syncthreads();
     if (vb == 0) {
         if (tid < k) { stc(L.ridx + tid, (int32_t)sel[tid]); stc(L.rw + tid, rw[tid]); }
-        if (tid == 0 && L.shl) stc(L.shg, *shg);
+        if (tid == 0 && has_sh) stc(L.shg, *shg);
     }
 }
 
@@ -873,6 +886,93 @@ OH_DEV void down_body(const oh_mvdown &D, int vb, W &wt) {
         }
         stc(D.x + row0 + lane, ldc(D.x + row0 + lane) + acc);
     }
+}
+
+// Split form of the fused down projection for the step kernel, where a block
+// has 4 waves: virtual block vb = (row group rg of 64/nb rows, slot group g);
+// wave w reduces slot j = 4g + w over the row group (its activation Q8_K(h_j)
+// formed in the wave's own LDS) and stores the dots with device-scope stores.
+// After its stores complete the block counts itself in cnt[rg]; the last of
+// the row group's blocks combines x_r += (sum_j w_j * dot_j) + shg * dot_shared
+// in the reference's order and resets the counter. Same arithmetic as
+// down_body.
+template <int T, class W>
+OH_DEV void down_split(const oh_mvdown &D, int vb, W &wt) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ int s_last;
+    constexpr int HA = 4;                                 // h float4 per lane (in <= 1024)
+    const int lane = lane_id(), wave = __builtin_amdgcn_readfirstlane(tid_x() >> 6);
+    const int nb = D.nb, in = D.in, ns = D.k + (D.sA ? 1 : 0), rps = 64 / nb, ng = (ns + 3) / 4;
+    const int rg = vb / ng, g = vb - rg * ng;
+    const int j0 = 4 * g + wave;
+    const bool act = j0 < ns;
+    const int j = act ? j0 : ns - 1;
+    const int rl = lane / nb, sb = lane - rl * nb;
+    const int row0 = rg * rps, row = row0 + rl;
+    const int rowc = row < D.rows ? (rl < rps ? row : row0) : D.rows - 1;
+    const int wb = (in * 4 + nb * kAS + nb * 36 + 15) & ~15;   // one wave's LDS
+    float *v = (float *)(smem + wave * wb);
+    uint8_t *q = (uint8_t *)(v + in);
+    if (!wt.wait()) return;
+    // routing first, then this slot's activation, then (once the expert is
+    // known) its weights: vector loads complete in order. (Requesting the
+    // weights before the wait from a routing kept in LDS was measured slower:
+    // the traffic lands in the gate/up phase still running.)
+    const bool sh = j >= D.k;
+    const int e = sh ? 0 : ldc(D.eidx + j);
+    const int nf = in / 4;
+    float4 ha[HA];
+#pragma unroll
+    for (int k = 0; k < HA; k++) {
+        const int f = lane + 64 * k < nf ? lane + 64 * k : nf - 1;
+        ha[k] = ldc4((const float4 *)(D.h + (size_t)j * D.stride) + f);
+    }
+    const WP wp = sh ? WP{D.sA, D.sB, D.sC} : WP{D.A, D.B, D.C};
+    SB<T> r;
+    sb_load(r, wp, ((int64_t)e * D.rows + rowc) * nb + sb);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int k = 0; k < HA; k++)
+        if (lane + 64 * k < nf) ((float4 *)v)[lane + 64 * k] = make_float4(ha[k].x, ha[k].y, ha[k].z, ha[k].w);
+    wave_lds_sync();
+    for (int q0 = 0; q0 < nb; q0 += 4)
+        q8k_blocks<4>(v, q0, 1, nb, (int8_t *)q, (float *)(q + mv_lds_d_off(nb)), (int16_t *)(q + mv_lds_bs_off(nb)), kAS);
+    wave_lds_sync();
+    const float tw = sb_term(r, (const int8_t *)q + sb * kAS, (const int16_t *)(q + mv_lds_bs_off(nb)) + sb * 16,
+                             ((const float *)(q + mv_lds_d_off(nb)))[sb]);
+    const bool live = act && rl < rps && row < D.rows;
+    const float t = live ? tw : 0.0f;
+    float acc = 0.0f;
+    for (int i = 0; i < nb; i++) acc += shfl(t, rl * nb + i);
+    if (live && sb == 0) stc(D.dots + (size_t)j * D.rows + row, acc);
+    // count the block in its row group once every wave's stores completed
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (tid_x() == 0)
+        s_last = __hip_atomic_fetch_add(D.cnt + rg, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == ng - 1;
+    __syncthreads();
+    if (!s_last) return;
+    if (wave == 0 && lane < rps && row0 + lane < D.rows) {
+        const int rr = row0 + lane;
+        float dv[16], wv[16];
+#pragma unroll
+        for (int jj = 0; jj < 16; jj++) {
+            const int jc = jj < ns ? jj : ns - 1;
+            dv[jj] = ldc(D.dots + (size_t)jc * D.rows + rr);
+            wv[jj] = jj < D.k ? ldc(D.w + jj) : 0.0f;
+        }
+        const float sg = D.shg ? ldc(D.shg) : 1.0f;
+        const float xr = ldc(D.x + rr);
+        float sum = 0.0f;
+        for (int jj = 0; jj < D.k; jj++) sum += wv[jj] * dv[jj];
+        if (D.sA) {
+            const float so = dv[D.k];
+            const float vv = D.shg ? so * sg : so;
+            sum += vv;
+        }
+        stc(D.x + rr, xr + sum);
+    }
+    if (tid_x() == 0) stc(D.cnt + rg, 0);
 }
 
 } // namespace

@@ -99,9 +99,9 @@ OH_DEV void run_vb(const oh_op &op, int vb, int pos, W &w) {
         else mv_body<-1>(op.u.mv, vb, w);
         break;
     case OH_OP_MV_DOWN:
-        if (op.u.down.type == OH_Q4_K) down_body<OH_Q4_K, 3>(op.u.down, vb, w);
-        else if (op.u.down.type == OH_Q6_K) down_body<OH_Q6_K, 3>(op.u.down, vb, w);
-        else down_body<OH_Q8_0, 3>(op.u.down, vb, w);
+        if (op.u.down.type == OH_Q4_K) down_split<OH_Q4_K>(op.u.down, vb, w);
+        else if (op.u.down.type == OH_Q6_K) down_split<OH_Q6_K>(op.u.down, vb, w);
+        else down_split<OH_Q8_0>(op.u.down, vb, w);
         break;
     case OH_OP_EMBED: embed_body(op.u.embed, vb, pos, w); break;
     case OH_OP_DELTA:
@@ -114,12 +114,7 @@ OH_DEV void run_vb(const oh_op &op, int vb, int pos, W &w) {
         }
         break;
     case OH_OP_ATTN_PREP: prep_body(op.u.prep, vb, pos, w); break;
-    case OH_OP_ATTN_SCORES: scores_body(op.u.attn, vb, pos, w); break;
-    case OH_OP_ATTN_OUT: out_body(op.u.attn, vb, pos, w); break;
-    case OH_OP_ATTN_FLASH:
-        if (op.u.attn.hb == 2) flash_body<2>(op.u.attn, vb, pos, w);
-        else flash_body<1>(op.u.attn, vb, pos, w);
-        break;
+    case OH_OP_ATTN_MAIN: attn_main_body(op.u.attn, vb, pos, w); break;
     case OH_OP_ATTN_COMBINE: combine_body(op.u.attn, vb, pos, w); break;
     case OH_OP_MOE_COMBINE: moe_combine_body(op.u.comb, vb, w); break;
     case OH_OP_ARGMAX1: argmax1_body(op.u.am, vb, w); break;

@@ -138,6 +138,11 @@ typedef struct {
     const float *shg;              // sigmoid shared gate (null: ungated)
     const float *h;                // silu(gate)*up of slot k at +k*stride
     float *x;                      // residual, += combine
+    // split form (step kernel): a virtual block is (row group, group of 4
+    // slots); slot dots go to dots[slot*rows + row], the last block of a row
+    // group (counted in cnt[row group]) combines
+    float *dots;
+    int *cnt;
     int type, nb, in, rows, k, stride;
 } oh_mvdown;
 
@@ -154,10 +159,8 @@ enum {
     OH_OP_EMBED,           // u.embed
     OH_OP_DELTA,           // u.delta
     OH_OP_ATTN_PREP,       // u.prep
-    OH_OP_ATTN_SCORES,     // u.attn
-    OH_OP_ATTN_OUT,        // u.attn
-    OH_OP_ATTN_FLASH,      // u.attn
-    OH_OP_ATTN_COMBINE,    // u.attn
+    OH_OP_ATTN_MAIN,       // u.attn: the exact walk, or flash chunks past its limit
+    OH_OP_ATTN_COMBINE,    // u.attn: merge of the flash chunks
     OH_OP_MOE_COMBINE,     // u.comb
     OH_OP_ARGMAX1,         // u.am
     OH_OP_ARGMAX2,         // u.am
