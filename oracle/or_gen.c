@@ -93,6 +93,13 @@ int orc_gen_write_gguf(const orc_gen_cfg *c, const char *path) {
             CK(add_q(w, &pl, c, N("attn_gate.weight"), c->t_default, 2, H, vd, 0));
             CK(add_q(w, &pl, c, N("ssm_out.weight"), c->t_default, 2, vd, H, 0));
         }
+        if (c->ne <= 0) {
+            /* dense SwiGLU FFN of width shared_inter */
+            CK(add_q(w, &pl, c, N("ffn_gate.weight"), c->t_default, 2, H, c->shared_inter, 0));
+            CK(add_q(w, &pl, c, N("ffn_up.weight"), c->t_default, 2, H, c->shared_inter, 0));
+            CK(add_q(w, &pl, c, N("ffn_down.weight"), c->t_ffn_down, 2, c->shared_inter, H, 0));
+            continue;
+        }
         CK(add_q(w, &pl, c, N("ffn_gate_inp.weight"), c->t_default, 2, H, c->ne, 0));
         CK(add_q(w, &pl, c, N("ffn_gate_exps.weight"), c->t_default, 3, H, c->moe_inter, c->ne));
         CK(add_q(w, &pl, c, N("ffn_up_exps.weight"), c->t_default, 3, H, c->moe_inter, c->ne));

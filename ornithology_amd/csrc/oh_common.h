@@ -268,6 +268,11 @@ OH_DEV uint4 ldg(const uint4 *p) {
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 template <>
+OH_DEV int4 ldg(const int4 *p) {
+    const oh_u4 v = *(const OH_GLOBAL oh_u4 *)p;
+    return make_int4((int)v.x, (int)v.y, (int)v.z, (int)v.w);
+}
+template <>
 OH_DEV float4 ldg(const float4 *p) {
     const oh_f4 v = *(const OH_GLOBAL oh_f4 *)p;
     return make_float4(v.x, v.y, v.z, v.w);

@@ -448,6 +448,28 @@ extern "C" int ornith_hip_matvec(ornith_hip_ctx *ctx, const ornith_hip_tensor *W
     const int64_t in = W->in, out = W->rows, nb = in / 256;
     const bool q = oh_qdot_can(W->type, in);
     void *sp;
+    if (q && Tn > 1 && in <= 8192) {
+        // Tn columns: each quantised to Q8_K, one batched launch
+        const size_t T = (size_t)Tn;
+        CHK(ctx_scratch(ctx, T * in * 5 + T * nb * 40 + T * out * 4 + 4096, &sp));
+        float *dx = (float *)sp;
+        float *dy = (float *)up256((size_t)(dx + T * in));
+        int8_t *qs = (int8_t *)up256((size_t)(dy + T * out));
+        float *dd = (float *)up256((size_t)(qs + T * in));
+        int16_t *bs = (int16_t *)up256((size_t)(dd + T * nb + 1));
+        HCHK(hipMemcpyAsync(dx, x, T * in * 4, hipMemcpyHostToDevice, ctx->st));
+        HCHK(oh_launch_norm_q8k_rows(dx, nullptr, 0.0f, (int)in, Tn, nullptr, qs, dd, bs, ctx->st));
+        oh_mvbatch B;
+        memset(&B, 0, sizeof B);
+        B.A = W->A; B.B = W->B; B.C = W->C;
+        B.xqs = qs; B.xd = dd; B.xbs = bs; B.y = dy;
+        B.type = (int)W->type; B.nb = (int)nb; B.in = (int)in; B.rows = (int)out;
+        B.ncol = Tn; B.adiv = 1; B.ystride = (int)out; B.tcol = oh_mvb_tcol((int)nb);
+        HCHK(oh_launch_mvb(&B, 1, ctx->st));
+        HCHK(hipMemcpyAsync(y, dy, T * out * 4, hipMemcpyDeviceToHost, ctx->st));
+        HCHK(hipStreamSynchronize(ctx->st));
+        return ORNITH_HIP_OK;
+    }
     CHK(ctx_scratch(ctx, (size_t)in * 5 + (size_t)nb * 40 + (size_t)out * 4 + 4096, &sp));
     float *dx = (float *)sp;
     float *dy = (float *)up256((size_t)(dx + in));
@@ -936,6 +958,19 @@ struct ornith_hip_session {
     // their barrier counters, the grid, and (profiling) phase timestamps
     struct StepProg { oh_op *ops = nullptr; unsigned *ctrs = nullptr; int n = 0, lds = 0; double bytes = 0.0; };
     StepProg sp_body, sp_head;
+    // layer-major prefill: buffers for chunks of up to pf_tc tokens
+    struct Pf {
+        int tc = 0;
+        int32_t pos_after = 0;
+        float *X = nullptr, *CAT = nullptr, *Z = nullptr, *A = nullptr, *Bg = nullptr, *CONV = nullptr;
+        float *QN = nullptr, *KN = nullptr, *AL = nullptr, *BE = nullptr, *O = nullptr, *OG = nullptr;
+        double *RUNS = nullptr;
+        float *QP = nullptr, *KB = nullptr, *VB = nullptr, *QR = nullptr, *AG = nullptr, *OA = nullptr;
+        float *FPO = nullptr, *FPML = nullptr, *RL = nullptr, *SHL = nullptr, *SHG = nullptr, *RW = nullptr;
+        int32_t *RIDX = nullptr, *CNT = nullptr, *LIST = nullptr;
+        float *Hh = nullptr, *HSH = nullptr, *OD = nullptr, *ODSH = nullptr, *STAGE = nullptr;
+        Q8Buf XQ, OQ, OAQ, HQ, HSQ;
+    } pf;
     std::vector<int> sp_body_rk;
     int step_grid = 0;
     bool step_tried = false;
@@ -1509,6 +1544,183 @@ static int sync_pos(ornith_hip_session *s) {
     return ORNITH_HIP_OK;
 }
 
+// ---- layer-major prefill (src/ornith_rforward.c:647-682 structure) ----------------------
+// Every layer over a chunk of tokens before the next: batched matvecs for the
+// projections (weights read once per chunk), the conv / delta state / KV cache
+// advanced in token order with the decode step's arithmetic. Bit-identical to
+// the same tokens fed through the token step.
+static const int kPfChunk = 256, kPfAttnSub = 16;
+
+static bool pf_mvb_ok(const ornith_hip_tensor *W) {
+    return W && oh_qdot_can(W->type, W->in) && W->in <= 8192 && W->in / 256 <= 64;
+}
+
+static bool pf_supported(const ornith_hip_model *m) {
+    const ornith_hip_arch &a = m->a;
+    if (a.hidden > 8192 || a.nv * a.dv > 8192 || a.nh * a.hd > 8192) return false;
+    for (int l = 0; l < a.n_layers; l++) {
+        const OhLayer &y = m->L[l];
+        if (y.full) {
+            if (!pf_mvb_ok(y.q) || !pf_mvb_ok(y.k) || !pf_mvb_ok(y.v) || !pf_mvb_ok(y.o)) return false;
+        } else {
+            if (!pf_mvb_ok(y.qkv) || !pf_mvb_ok(y.gate) || !pf_mvb_ok(y.alpha) || !pf_mvb_ok(y.beta) ||
+                !pf_mvb_ok(y.ssm_out))
+                return false;
+            if (a.dk != 64 && a.dk != 128) return false;
+        }
+        if (a.ne > 0) {
+            if (!pf_mvb_ok(y.router) || !pf_mvb_ok(y.gate_exps) || !pf_mvb_ok(y.up_exps) || !pf_mvb_ok(y.down_exps))
+                return false;
+            if (!pairable(y.gate_exps, y.up_exps) || a.moe_inter > 8192 || a.ne > 1024 || a.top_k > 64) return false;
+            if (y.gate_sh && (!pf_mvb_ok(y.gate_sh) || !pf_mvb_ok(y.up_sh) || !pf_mvb_ok(y.down_sh) ||
+                              !pairable(y.gate_sh, y.up_sh) || a.shared_inter > 8192))
+                return false;
+            if (y.gate_inp_sh && !pf_mvb_ok(y.gate_inp_sh)) return false;
+        } else if (!pf_mvb_ok(y.ffn_gate) || !pf_mvb_ok(y.ffn_up) || !pf_mvb_ok(y.ffn_down) ||
+                   !pairable(y.ffn_gate, y.ffn_up) || a.shared_inter > 8192) {
+            return false;
+        }
+    }
+    return true;
+}
+
+static int pf_alloc(ornith_hip_session *s, int tc) {
+    auto &p = s->pf;
+    if (p.tc >= tc) return ORNITH_HIP_OK;
+    const ornith_hip_arch &a = s->m->a;
+    const size_t T = (size_t)tc, H = a.hidden, qd = (size_t)a.nk * a.dk, vd = (size_t)a.nv * a.dv;
+    const size_t cc = 2 * qd + vd, aq = (size_t)a.nh * a.hd, kvd = (size_t)a.nkv * a.hd;
+    const size_t K = a.top_k > 0 ? a.top_k : 1, I = a.moe_inter > 0 ? a.moe_inter : 1;
+    const size_t sI = a.shared_inter > 0 ? a.shared_inter : 1, ne = a.ne > 0 ? a.ne : 1;
+    const size_t nch = (s->kvcap + oh_flash_chunk() - 1) / oh_flash_chunk();
+    CHK(salloc(s, &p.X, T * H));
+    CHK(q8alloc(s, p.XQ, T * H));
+    CHK(salloc(s, &p.CAT, T * cc + 1)); CHK(salloc(s, &p.CONV, T * cc + 1));
+    CHK(salloc(s, &p.Z, T * vd + 1)); CHK(salloc(s, &p.O, T * vd + 1)); CHK(salloc(s, &p.OG, T * vd + 1));
+    CHK(q8alloc(s, p.OQ, T * vd + 256));
+    CHK(salloc(s, &p.A, T * a.nv + 1)); CHK(salloc(s, &p.Bg, T * a.nv + 1));
+    CHK(salloc(s, &p.AL, T * a.nv + 1)); CHK(salloc(s, &p.BE, T * a.nv + 1));
+    CHK(salloc(s, &p.QN, T * qd + 1)); CHK(salloc(s, &p.KN, T * qd + 1));
+    CHK(salloc(s, &p.RUNS, T * (vd / 64) + 1));
+    CHK(salloc(s, &p.STAGE, (size_t)(a.conv_k > 1 ? a.conv_k - 1 : 1) * cc + 1));
+    CHK(salloc(s, &p.QP, T * 2 * aq + 1)); CHK(salloc(s, &p.KB, T * kvd + 1)); CHK(salloc(s, &p.VB, T * kvd + 1));
+    CHK(salloc(s, &p.QR, T * aq + 1)); CHK(salloc(s, &p.AG, T * aq + 1)); CHK(salloc(s, &p.OA, T * aq + 1));
+    CHK(q8alloc(s, p.OAQ, T * aq + 256));
+    CHK(salloc(s, &p.FPO, (size_t)kPfAttnSub * a.nh * nch * a.hd + 64));
+    CHK(salloc(s, &p.FPML, (size_t)kPfAttnSub * a.nh * nch * 2 + 64));
+    CHK(salloc(s, &p.RL, T * ne)); CHK(salloc(s, &p.SHL, T)); CHK(salloc(s, &p.SHG, T));
+    CHK(salloc(s, &p.RW, T * K)); CHK(salloc(s, &p.RIDX, T * K));
+    CHK(salloc(s, &p.CNT, ne)); CHK(salloc(s, &p.LIST, ne * T));
+    CHK(salloc(s, &p.Hh, T * K * I)); CHK(q8alloc(s, p.HQ, T * K * I + 256));
+    CHK(salloc(s, &p.HSH, T * sI)); CHK(q8alloc(s, p.HSQ, T * sI + 256));
+    CHK(salloc(s, &p.OD, T * K * H)); CHK(salloc(s, &p.ODSH, T * H));
+    p.tc = tc;
+    return ORNITH_HIP_OK;
+}
+
+// Y[col] (+)= W . X[col]: dense columns [0, T), or grouped by expert (list/cnt)
+static int pf_mvb(const ornith_hip_tensor *W, const ornith_hip_tensor *W2, const Q8Buf &x, float *y, int ystride,
+                  int T, int mode, hipStream_t st, const int32_t *cnt = nullptr, const int32_t *list = nullptr,
+                  int lstride = 0, int adiv = 1, int groups = 1) {
+    oh_mvbatch B;
+    memset(&B, 0, sizeof B);
+    B.A = W->A; B.B = W->B; B.C = W->C;
+    if (W2) { B.A2 = W2->A; B.B2 = W2->B; B.C2 = W2->C; B.pair = 1; }
+    B.xqs = x.qs; B.xd = x.d; B.xbs = x.bs; B.y = y;
+    B.type = (int)W->type; B.nb = (int)(W->in / 256); B.in = (int)W->in;
+    B.rows = list ? (int)W->dims[1] : (int)W->rows;
+    B.mode = mode; B.ncol = T; B.adiv = adiv; B.ystride = ystride; B.tcol = oh_mvb_tcol(B.nb);
+    B.cnt = cnt; B.list = list; B.lstride = lstride;
+    HCHK(oh_launch_mvb(&B, groups, st));
+    return ORNITH_HIP_OK;
+}
+
+static int pf_chunk(ornith_hip_session *s, int base, int T, hipStream_t st) {
+    const ornith_hip_model *m = s->m;
+    const ornith_hip_arch &a = m->a;
+    auto &p = s->pf;
+    const int H = a.hidden, qd = a.nk * a.dk, vd = a.nv * a.dv, cc = 2 * qd + vd, aq = a.nh * a.hd;
+    const int kvd = a.nkv * a.hd;
+    oh_op_embed emb = {m->embd->A, m->embd->B, m->embd->C, s->toks, p.X, (int)m->embd->type, H};
+    HCHK(oh_launch_embed_rows(&emb, base, T, st));
+    for (int l = 0; l < a.n_layers; l++) {
+        const OhLayer &y = m->L[l];
+        LayerState &z = s->ls[l];
+        HCHK(oh_launch_norm_q8k_rows(p.X, (const float *)y.attn_norm->A, a.eps, H, T, nullptr, p.XQ.qs, p.XQ.d,
+                                     p.XQ.bs, st));
+        if (y.full) {
+            CHK(pf_mvb(y.q, nullptr, p.XQ, p.QP, 2 * aq, T, 0, st));
+            CHK(pf_mvb(y.k, nullptr, p.XQ, p.KB, kvd, T, 0, st));
+            CHK(pf_mvb(y.v, nullptr, p.XQ, p.VB, kvd, T, 0, st));
+            oh_op_prep pr = {p.QP, p.KB, p.VB, (const float *)y.q_norm->A, (const float *)y.k_norm->A,
+                             (const float *)s->rope, p.QR, p.AG, z.Kt, z.Ks, z.Vq, z.Vs,
+                             a.nh, a.nkv, a.hd, a.rope_dim, s->kvcap, a.eps};
+            HCHK(oh_launch_prep_rows(&pr, base, T, st));
+            oh_op_attn at;
+            memset(&at, 0, sizeof at);
+            at.qr = p.QR; at.gate = p.AG; at.Kt = z.Kt; at.Ks = z.Ks; at.Vq = z.Vq; at.Vs = z.Vs;
+            at.part_o = p.FPO; at.part_ml = p.FPML; at.out = p.OA;
+            at.nh = a.nh; at.nkv = a.nkv; at.hd = a.hd; at.cap = s->kvcap; at.exact_max = s->exact_max;
+            at.hb = oh_flash_hb(a.nh, a.nkv); at.scale = 1.0f / sqrtf((float)a.hd);
+            const int nch = (s->kvcap + oh_flash_chunk() - 1) / oh_flash_chunk();
+            const int nv_ex = a.nh / (256 / a.hd), nv_fl = a.nkv * (a.nh / a.nkv / at.hb) * nch;
+            const int lds_ex = oh_exact_lds_bytes(a.hd, s->exact_max), lds_fl = oh_flash_lds_bytes(a.nh, a.nkv, a.hd);
+            const size_t po = (size_t)a.nh * nch * a.hd, pml = (size_t)a.nh * nch * 2;
+            for (int t0 = 0; t0 < T; t0 += kPfAttnSub)
+                HCHK(oh_launch_attn_rows(&at, nv_ex > nv_fl ? nv_ex : nv_fl, lds_ex > lds_fl ? lds_ex : lds_fl, base,
+                                         t0, T - t0 < kPfAttnSub ? T - t0 : kPfAttnSub, po, pml, st));
+            HCHK(oh_launch_norm_q8k_rows(p.OA, nullptr, 0.0f, aq, T, nullptr, p.OAQ.qs, p.OAQ.d, p.OAQ.bs, st));
+            CHK(pf_mvb(y.o, nullptr, p.OAQ, p.X, H, T, 1, st));
+        } else {
+            CHK(pf_mvb(y.qkv, nullptr, p.XQ, p.CAT, cc, T, 0, st));
+            CHK(pf_mvb(y.gate, nullptr, p.XQ, p.Z, vd, T, 0, st));
+            CHK(pf_mvb(y.alpha, nullptr, p.XQ, p.A, a.nv, T, 0, st));
+            CHK(pf_mvb(y.beta, nullptr, p.XQ, p.Bg, a.nv, T, 0, st));
+            HCHK(oh_launch_conv_rows(p.CAT, (const float *)y.conv->A, z.conv, p.CONV, p.STAGE, T, base, cc, a.conv_k, st));
+            HCHK(oh_launch_qk_gates_rows(a.dk, p.CONV, p.A, p.Bg, (const float *)y.ssm_a->A,
+                                         (const float *)y.dt_bias->A, p.QN, p.KN, p.AL, p.BE, T, a.nk, a.nv, cc, st));
+            HCHK(oh_launch_delta_scan(a.dk, p.QN, p.KN, p.CONV, p.AL, p.BE, p.Z, z.S, p.O, p.OG, p.RUNS, T, a.nk,
+                                      a.nv, cc, 1.0f / sqrtf((float)a.dk), st));
+            HCHK(oh_launch_gnorm_q8k_rows(p.O, p.OG, p.RUNS, (const float *)y.ssm_norm->A, a.eps, vd, a.dv, T,
+                                          p.OQ.qs, p.OQ.d, p.OQ.bs, st));
+            CHK(pf_mvb(y.ssm_out, nullptr, p.OQ, p.X, H, T, 1, st));
+        }
+        HCHK(oh_launch_norm_q8k_rows(p.X, (const float *)y.post_norm->A, a.eps, H, T, nullptr, p.XQ.qs, p.XQ.d,
+                                     p.XQ.bs, st));
+        if (a.ne > 0) {
+            const int K = a.top_k, I = a.moe_inter, sI = a.shared_inter;
+            CHK(pf_mvb(y.router, nullptr, p.XQ, p.RL, a.ne, T, 0, st));
+            if (y.gate_inp_sh) CHK(pf_mvb(y.gate_inp_sh, nullptr, p.XQ, p.SHL, 1, T, 0, st));
+            HCHK(oh_launch_route_rows(p.RL, a.ne, K, y.gate_inp_sh ? p.SHL : nullptr, p.RIDX, p.RW,
+                                      y.gate_inp_sh ? p.SHG : nullptr, T, st));
+            HCHK(oh_launch_group_pairs(p.RIDX, T * K, p.CNT, a.ne, p.LIST, T, st));
+            CHK(pf_mvb(y.gate_exps, y.up_exps, p.XQ, p.Hh, I, T, 0, st, p.CNT, p.LIST, T, K, a.ne));
+            HCHK(oh_launch_norm_q8k_rows(p.Hh, nullptr, 0.0f, I, T * K, nullptr, p.HQ.qs, p.HQ.d, p.HQ.bs, st));
+            CHK(pf_mvb(y.down_exps, nullptr, p.HQ, p.OD, H, T, 0, st, p.CNT, p.LIST, T, 1, a.ne));
+            if (y.gate_sh) {
+                CHK(pf_mvb(y.gate_sh, y.up_sh, p.XQ, p.HSH, sI, T, 0, st));
+                HCHK(oh_launch_norm_q8k_rows(p.HSH, nullptr, 0.0f, sI, T, nullptr, p.HSQ.qs, p.HSQ.d, p.HSQ.bs, st));
+                CHK(pf_mvb(y.down_sh, nullptr, p.HSQ, p.ODSH, H, T, 0, st));
+            }
+            HCHK(oh_launch_moe_combine_rows(p.X, p.OD, p.RW, K, H, y.gate_sh ? p.ODSH : nullptr,
+                                            y.gate_inp_sh ? p.SHG : nullptr, T, st));
+        } else {
+            const int I = a.shared_inter;
+            CHK(pf_mvb(y.ffn_gate, y.ffn_up, p.XQ, p.HSH, I, T, 0, st));
+            HCHK(oh_launch_norm_q8k_rows(p.HSH, nullptr, 0.0f, I, T, nullptr, p.HSQ.qs, p.HSQ.d, p.HSQ.bs, st));
+            CHK(pf_mvb(y.ffn_down, nullptr, p.HSQ, p.X, H, T, 1, st));
+        }
+    }
+    // the last token's hidden state feeds the head
+    HCHK(hipMemcpyAsync(s->x, p.X + (size_t)(T - 1) * H, (size_t)H * 4, hipMemcpyDeviceToDevice, st));
+    return ORNITH_HIP_OK;
+}
+
+static bool pf_enabled() {
+    const char *e = getenv("ORNITH_HIP_PREFILL");
+    return !(e && e[0] == '0');
+}
+
 extern "C" int ornith_hip_session_eval(ornith_hip_session *s, const int32_t *tokens, int n) {
     if (n <= 0) return ORNITH_HIP_OK;
     if (s->pos + n > s->cap) {
@@ -1524,7 +1736,16 @@ extern "C" int ornith_hip_session_eval(ornith_hip_session *s, const int32_t *tok
     hipStream_t st = s->m->ctx->st;
     CHK(sync_pos(s));
     HCHK(hipMemcpyAsync(s->toks + s->pos, tokens, (size_t)n * 4, hipMemcpyHostToDevice, st));
-    for (int i = 0; i < n; i++) CHK(run_body(s));
+    if (n > 1 && pf_enabled() && pf_supported(s->m)) {
+        // layer-major over chunks of tokens, then the head at the last one
+        CHK(pf_alloc(s, n < kPfChunk ? n : kPfChunk));
+        for (int c0 = 0; c0 < n; c0 += kPfChunk)
+            CHK(pf_chunk(s, s->pos + c0, n - c0 < kPfChunk ? n - c0 : kPfChunk, st));
+        s->pf.pos_after = s->pos + n;   // outlives the asynchronous copy
+        HCHK(hipMemcpyAsync(s->io + OH_IO_POS, &s->pf.pos_after, 4, hipMemcpyHostToDevice, st));
+    } else {
+        for (int i = 0; i < n; i++) CHK(run_body(s));
+    }
     CHK(run_head(s));
     HCHK(hipStreamSynchronize(st));
     CHK(step_check(s));
@@ -1724,7 +1945,7 @@ extern "C" int ornith_hip_model_synth(ornith_hip_ctx *ctx, const ornith_hip_gen_
     uint64_t mx = (uint64_t)H * V;
     auto upd = [&](uint64_t n) { if (n > mx) mx = n; };
     upd((uint64_t)H * cc); upd((uint64_t)H * 2 * c->nh * c->hd); upd((uint64_t)H * c->moe_inter * c->ne);
-    upd((uint64_t)c->nh * c->hd * H); upd((uint64_t)vd * H);
+    upd((uint64_t)c->nh * c->hd * H); upd((uint64_t)vd * H); upd((uint64_t)H * c->shared_inter);
     float *tmp = nullptr;
     HCHK(hipMalloc(&tmp, mx * 4 + 256));
     auto *m = new ornith_hip_model();
@@ -1779,6 +2000,13 @@ extern "C" int ornith_hip_model_synth(ornith_hip_ctx *ctx, const ornith_hip_gen_
             add_q(b + "ssm_beta.weight", c->t_default, 2, H, c->nv, 0);
             add_q(b + "attn_gate.weight", c->t_default, 2, H, vd, 0);
             add_q(b + "ssm_out.weight", c->t_default, 2, vd, H, 0);
+        }
+        if (c->ne <= 0) {
+            // dense SwiGLU FFN of width shared_inter
+            add_q(b + "ffn_gate.weight", c->t_default, 2, H, c->shared_inter, 0);
+            add_q(b + "ffn_up.weight", c->t_default, 2, H, c->shared_inter, 0);
+            add_q(b + "ffn_down.weight", c->t_ffn_down, 2, c->shared_inter, H, 0);
+            continue;
         }
         add_q(b + "ffn_gate_inp.weight", c->t_default, 2, H, c->ne, 0);
         add_q(b + "ffn_gate_exps.weight", c->t_default, 3, H, c->moe_inter, c->ne);

@@ -4,6 +4,7 @@
 #include "oh_layers.hip"
 #include "oh_synth.hip"
 #include "oh_step.hip"
+#include "oh_prefill.hip"
 #include "oh_launch.h"
 
 extern "C" {
@@ -13,6 +14,94 @@ hipError_t oh_launch_matvec(const oh_mvlaunch *L, int tk, int lds_bytes, hipStre
     void (*k)(oh_mvlaunch) = tk == OH_Q4_K ? oh_k_mv_q4k : tk == OH_Q6_K ? oh_k_mv_q6k
                            : tk == OH_Q8_0 ? oh_k_mv_q80 : oh_k_mv_mixed;
     hipLaunchKernelGGL(k, dim3(L->total_blocks), dim3(256), (size_t)lds_bytes, st, *L);
+    return hipGetLastError();
+}
+
+hipError_t oh_launch_mvb(const oh_mvbatch *B, int groups, hipStream_t st) {
+    const int rps = 64 / B->nb, blocks = (B->rows + 4 * rps - 1) / (4 * rps);
+    if (blocks <= 0 || groups <= 0) return hipSuccess;
+    void (*k)(oh_mvbatch) = B->type == OH_Q4_K ? oh_k_mvb_q4k : B->type == OH_Q6_K ? oh_k_mvb_q6k : oh_k_mvb_q80;
+    hipLaunchKernelGGL(k, dim3(blocks, groups), dim3(256), (size_t)B->tcol * mvb_col_bytes(B->nb), st, *B);
+    return hipGetLastError();
+}
+
+int oh_mvb_tcol(int nb) {
+    const int t = 32768 / mvb_col_bytes(nb);
+    return t < 1 ? 1 : (t > 64 ? 64 : t);
+}
+
+hipError_t oh_launch_norm_q8k_rows(const float *x, const float *norm_w, float eps, int n, int rows, float *xn_out,
+                                   int8_t *qs, float *d, int16_t *bs, hipStream_t st) {
+    if (rows <= 0) return hipSuccess;
+    hipLaunchKernelGGL(oh_k_norm_q8k_rows, dim3(rows), dim3(256), 0, st, x, norm_w, eps, n, xn_out, qs, d, bs);
+    return hipGetLastError();
+}
+
+// ---- prefill launchers ----
+hipError_t oh_launch_embed_rows(const oh_op_embed *a, int base, int T, hipStream_t st) {
+    hipLaunchKernelGGL(oh_k_embed_rows, dim3((a->in + 255) / 256, T), dim3(256), 0, st, *a, base);
+    return hipGetLastError();
+}
+hipError_t oh_launch_conv_rows(const float *cat, const float *conv_w, float *conv_state, float *out, float *stage,
+                               int T, int base, int cc, int K, hipStream_t st) {
+    const dim3 g((cc + 255) / 256, T), gw((cc + 255) / 256, K - 1);
+    hipLaunchKernelGGL(oh_k_conv_rows, g, dim3(256), 0, st, cat, conv_w, conv_state, out, T, base, cc, K);
+    if (((base + T) & 1) != (base & 1)) {
+        hipLaunchKernelGGL(oh_k_conv_window, gw, dim3(256), 0, st, cat, conv_state, T, base, cc, K);
+    } else {
+        hipLaunchKernelGGL(oh_k_conv_window_stage, gw, dim3(256), 0, st, cat, conv_state, stage, T, base, cc, K);
+        hipError_t e = hipMemcpyAsync(conv_state + (size_t)(base & 1) * (K - 1) * cc, stage,
+                                      (size_t)(K - 1) * cc * 4, hipMemcpyDeviceToDevice, st);
+        if (e != hipSuccess) return e;
+    }
+    return hipGetLastError();
+}
+hipError_t oh_launch_qk_gates_rows(int dk, const float *conv, const float *A, const float *Bg, const float *ssm_a,
+                                   const float *dt_bias, float *qn, float *kn, float *al, float *be, int T, int nk,
+                                   int nv, int cc, hipStream_t st) {
+    const dim3 g(nk + nv, T);
+    if (dk == 128) hipLaunchKernelGGL(oh_k_qk_gates_rows<128>, g, dim3(64), 0, st, conv, A, Bg, ssm_a, dt_bias, qn, kn, al, be, nk, nv, cc);
+    else if (dk == 64) hipLaunchKernelGGL(oh_k_qk_gates_rows<64>, g, dim3(64), 0, st, conv, A, Bg, ssm_a, dt_bias, qn, kn, al, be, nk, nv, cc);
+    else return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+hipError_t oh_launch_delta_scan(int dk, const float *qn, const float *kn, const float *conv, const float *al,
+                                const float *be, const float *z, float *S, float *out, float *out_gate,
+                                double *out_runs, int T, int nk, int nv, int cc, float out_scale, hipStream_t st) {
+    if (dk == 128) hipLaunchKernelGGL(oh_k_delta_scan<128>, dim3(nv * 2), dim3(64), 0, st, qn, kn, conv, al, be, z, S, out, out_gate, out_runs, T, nk, nv, cc, out_scale);
+    else if (dk == 64) hipLaunchKernelGGL(oh_k_delta_scan<64>, dim3(nv), dim3(64), 0, st, qn, kn, conv, al, be, z, S, out, out_gate, out_runs, T, nk, nv, cc, out_scale);
+    else return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+hipError_t oh_launch_gnorm_q8k_rows(const float *x, const float *sz, const double *runs, const float *w, float eps,
+                                    int n, int gdim, int T, int8_t *qs, float *d, int16_t *bs, hipStream_t st) {
+    hipLaunchKernelGGL(oh_k_gnorm_q8k_rows, dim3(T), dim3(256), 0, st, x, sz, runs, w, eps, n, gdim, qs, d, bs);
+    return hipGetLastError();
+}
+hipError_t oh_launch_prep_rows(const oh_op_prep *a, int base, int T, hipStream_t st) {
+    hipLaunchKernelGGL(oh_k_prep_rows, dim3(a->nh + a->nkv, T), dim3(256), 0, st, *a, base);
+    return hipGetLastError();
+}
+hipError_t oh_launch_attn_rows(const oh_op_attn *a, int nvb_main, int lds, int base, int t0, int n, size_t po_stride,
+                               size_t pml_stride, hipStream_t st) {
+    hipLaunchKernelGGL(oh_k_attn_main_rows, dim3(nvb_main, n), dim3(256), (size_t)lds, st, *a, base, t0, po_stride, pml_stride);
+    hipLaunchKernelGGL(oh_k_attn_combine_rows, dim3(a->nh * (a->hd / 64), n), dim3(256), 0, st, *a, base, t0, po_stride, pml_stride);
+    return hipGetLastError();
+}
+hipError_t oh_launch_route_rows(const float *logits, int ne, int k, const float *shl, int32_t *idx, float *w,
+                                float *shg, int T, hipStream_t st) {
+    hipLaunchKernelGGL(oh_k_route_rows, dim3(T), dim3(64), 0, st, logits, ne, k, shl, idx, w, shg);
+    return hipGetLastError();
+}
+hipError_t oh_launch_group_pairs(const int32_t *idx, int npairs, int32_t *cnt, int ne, int32_t *list, int lstride,
+                                 hipStream_t st) {
+    hipLaunchKernelGGL(oh_k_fill_i32, dim3((ne + 255) / 256), dim3(256), 0, st, cnt, ne, 0);
+    hipLaunchKernelGGL(oh_k_group_pairs, dim3((npairs + 255) / 256), dim3(256), 0, st, idx, npairs, cnt, list, lstride);
+    return hipGetLastError();
+}
+hipError_t oh_launch_moe_combine_rows(float *x, const float *o, const float *w, int k, int H, const float *so,
+                                      const float *shgate, int T, hipStream_t st) {
+    hipLaunchKernelGGL(oh_k_moe_combine_rows, dim3((H + 255) / 256, T), dim3(256), 0, st, x, o, w, k, H, so, shgate);
     return hipGetLastError();
 }
 

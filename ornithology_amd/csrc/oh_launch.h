@@ -9,6 +9,33 @@ extern "C" {
 // tk: the integer-path type every segment has (OH_Q4_K/OH_Q6_K/OH_Q8_0), or -1
 // for a launch that mixes types or has fallback segments
 hipError_t oh_launch_matvec(const oh_mvlaunch *L, int tk, int lds_bytes, hipStream_t st);
+// batched matvec (grid: row blocks x groups) and its LDS column tile
+hipError_t oh_launch_mvb(const oh_mvbatch *B, int groups, hipStream_t st);
+int oh_mvb_tcol(int nb);
+// RMSNorm (norm_w non-null) + Q8_K of `rows` vectors of n <= 8192 elements
+hipError_t oh_launch_norm_q8k_rows(const float *x, const float *norm_w, float eps, int n, int rows, float *xn_out,
+                                   int8_t *qs, float *d, int16_t *bs, hipStream_t st);
+// prefill (layer-major over T tokens)
+hipError_t oh_launch_embed_rows(const oh_op_embed *a, int base, int T, hipStream_t st);
+hipError_t oh_launch_conv_rows(const float *cat, const float *conv_w, float *conv_state, float *out, float *stage,
+                               int T, int base, int cc, int K, hipStream_t st);
+hipError_t oh_launch_qk_gates_rows(int dk, const float *conv, const float *A, const float *Bg, const float *ssm_a,
+                                   const float *dt_bias, float *qn, float *kn, float *al, float *be, int T, int nk,
+                                   int nv, int cc, hipStream_t st);
+hipError_t oh_launch_delta_scan(int dk, const float *qn, const float *kn, const float *conv, const float *al,
+                                const float *be, const float *z, float *S, float *out, float *out_gate,
+                                double *out_runs, int T, int nk, int nv, int cc, float out_scale, hipStream_t st);
+hipError_t oh_launch_gnorm_q8k_rows(const float *x, const float *sz, const double *runs, const float *w, float eps,
+                                    int n, int gdim, int T, int8_t *qs, float *d, int16_t *bs, hipStream_t st);
+hipError_t oh_launch_prep_rows(const oh_op_prep *a, int base, int T, hipStream_t st);
+hipError_t oh_launch_attn_rows(const oh_op_attn *a, int nvb_main, int lds, int base, int t0, int n, size_t po_stride,
+                               size_t pml_stride, hipStream_t st);
+hipError_t oh_launch_route_rows(const float *logits, int ne, int k, const float *shl, int32_t *idx, float *w,
+                                float *shg, int T, hipStream_t st);
+hipError_t oh_launch_group_pairs(const int32_t *idx, int npairs, int32_t *cnt, int ne, int32_t *list, int lstride,
+                                 hipStream_t st);
+hipError_t oh_launch_moe_combine_rows(float *x, const float *o, const float *w, int k, int H, const float *so,
+                                      const float *shgate, int T, hipStream_t st);
 hipError_t oh_launch_rmsnorm_q8k(const float *x, const float *norm_w, float eps, int n,
                                  float *xn_out, int8_t *qs, float *d, int16_t *bs, hipStream_t st);
 hipError_t oh_launch_swiglu_q8k(const float *g, const float *u, int n, int count, float *h_out,

@@ -975,6 +975,78 @@ OH_DEV void down_split(const oh_mvdown &D, int vb, W &wt) {
     if (tid_x() == 0) stc(D.cnt + rg, 0);
 }
 
+// ---- batched matvec (prefill) --------------------------------------------------
+// A block owns 4 wave steps of rows (64/nb rows each, one super-block per lane,
+// its weights loaded once); the activation columns are staged in LDS tcol at
+// a time (the matvec prologue's layout) and every wave reduces its
+// super-blocks against each staged column: per (row, column) the matvec's dot
+// (src/ornith_rforward.c:100-116 with Tn columns). Grid (row blocks, groups).
+OH_HD inline int mvb_col_bytes(int nb) { return (nb * kAS + nb * 36 + 15) & ~15; }
+
+template <int T>
+OH_DEV void mvb_body(const oh_mvbatch &B) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ int scol[64];
+    const int lane = lane_id(), wave = __builtin_amdgcn_readfirstlane(tid_x() >> 6), tid = tid_x();
+    const int nb = B.nb, in = B.in, rps = 64 / nb, rl = lane / nb, sb = lane - rl * nb;
+    const int g = (int)blockIdx.y;
+    const int ncol = B.list ? B.cnt[g] : B.ncol;
+    if (ncol <= 0) return;
+    const int r0 = ((int)blockIdx.x * 4 + wave) * rps, row = r0 + rl;
+    const bool rlive = rl < rps && row < B.rows;
+    const int rowc0 = rl < rps ? row : r0, rowc = rowc0 < B.rows ? rowc0 : B.rows - 1;
+    const int64_t rbase = B.list ? (int64_t)g * B.rows : 0;
+    const WP wp{B.A, B.B, B.C}, wp2{B.A2, B.B2, B.C2};
+    SB<T> r, r2;
+    sb_load(r, wp, (rbase + rowc) * nb + sb);
+    if (B.pair) sb_load(r2, wp2, (rbase + rowc) * nb + sb);
+    const int cs = mvb_col_bytes(nb), n16 = in / 16;
+    for (int c0 = 0; c0 < ncol; c0 += B.tcol) {
+        const int n = ncol - c0 < B.tcol ? ncol - c0 : B.tcol;
+        __syncthreads();                              // the previous tile is consumed
+        if (tid < n) scol[tid] = B.list ? ldg(B.list + (size_t)g * B.lstride + c0 + tid) : c0 + tid;
+        __syncthreads();
+        for (int i = tid; i < n * n16; i += 256) {
+            const int c = i / n16, q = i - c * n16;
+            const int a = scol[c] / B.adiv;
+            ((int4 *)(smem + c * cs))[(q >> 4) * (kAS / 16) + (q & 15)] = ldg((const int4 *)(B.xqs + (size_t)a * in) + q);
+        }
+        for (int i = tid; i < n * 2 * nb; i += 256) {
+            const int c = i / (2 * nb), q = i - c * 2 * nb;
+            const int a = scol[c] / B.adiv;
+            ((int4 *)(smem + c * cs + mv_lds_bs_off(nb)))[q] = ldg((const int4 *)(B.xbs + (size_t)a * nb * 16) + q);
+        }
+        for (int i = tid; i < n * nb; i += 256) {
+            const int c = i / nb, q = i - c * nb;
+            const int a = scol[c] / B.adiv;
+            ((float *)(smem + c * cs + mv_lds_d_off(nb)))[q] = ldg(B.xd + (size_t)a * nb + q);
+        }
+        __syncthreads();
+#pragma unroll 1
+        for (int c = 0; c < n; c++) {
+            const uint8_t *cb = smem + c * cs;
+            const int8_t *aq = (const int8_t *)cb + sb * kAS;
+            const int16_t *abs = (const int16_t *)(cb + mv_lds_bs_off(nb)) + sb * 16;
+            const float yd = ((const float *)(cb + mv_lds_d_off(nb)))[sb];
+            const float t1 = rlive ? sb_term(r, aq, abs, yd) : 0.0f;
+            float acc = 0.0f;
+            for (int i = 0; i < nb; i++) acc += shfl(t1, rl * nb + i);
+            float out = acc;
+            if (B.pair) {
+                const float t2 = rlive ? sb_term(r2, aq, abs, yd) : 0.0f;
+                float acc2 = 0.0f;
+                for (int i = 0; i < nb; i++) acc2 += shfl(t2, rl * nb + i);
+                out = ref_silu(acc) * acc2;
+            }
+            if (rlive && sb == 0) {
+                float *yp = B.y + (size_t)scol[c] * B.ystride + row;
+                if (B.mode == 1) stg(yp, ldg(yp) + out);
+                else stg(yp, out);
+            }
+        }
+    }
+}
+
 } // namespace
 
 extern "C" __global__ void __launch_bounds__(256) oh_k_mv_q4k(oh_mvlaunch L) {
@@ -1102,4 +1174,37 @@ oh_k_dequant(const uint8_t *A, const uint8_t *B, const uint8_t *C, int type, int
         }
         out[e] = y;
     }
+}
+
+extern "C" __global__ void __launch_bounds__(256) oh_k_mvb_q4k(oh_mvbatch B) { mvb_body<OH_Q4_K>(B); }
+extern "C" __global__ void __launch_bounds__(256) oh_k_mvb_q6k(oh_mvbatch B) { mvb_body<OH_Q6_K>(B); }
+extern "C" __global__ void __launch_bounds__(256) oh_k_mvb_q80(oh_mvbatch B) { mvb_body<OH_Q8_0>(B); }
+
+// Q8_K (optionally after RMSNorm) of `rows` vectors of n elements, one block
+// per vector; the same arithmetic as oh_k_rmsnorm_q8k (and the matvec's
+// RMSNorm prologue). xn_out (optional) receives the normalised f32 vectors.
+extern "C" __global__ void __launch_bounds__(256)
+oh_k_norm_q8k_rows(const float *x, const float *norm_w, float eps, int n, float *xn_out, int8_t *qs, float *d,
+                   int16_t *bs) {
+    __shared__ float v[8192];
+    __shared__ double red[4];
+    const size_t r = blockIdx.x;
+    const int tid = tid_x(), wave = tid >> 6, nqb = n / 256;
+    const float *xr = x + r * n;
+    for (int i = tid; i < n; i += 256) v[i] = ldg(xr + i);
+    __syncthreads();
+    if (norm_w) {
+        double ss = 0.0;
+        for (int i = tid; i < n; i += 256) ss += (double)v[i] * v[i];
+        ss = wave_sum_d(ss);
+        if (lane_id() == 0) red[wave] = ss;
+        __syncthreads();
+        const double tot = (red[0] + red[1]) + (red[2] + red[3]);
+        const float inv = (float)(1.0 / sqrt(tot / (double)n + (double)eps));
+        __syncthreads();
+        for (int i = tid; i < n; i += 256) v[i] = v[i] * inv * ldg(norm_w + i);
+        __syncthreads();
+    }
+    if (xn_out) for (int i = tid; i < n; i += 256) stg(xn_out + r * n + i, v[i]);
+    for (int qb = wave; qb < nqb; qb += 4) q8k_block_from_lds(v, qb, qs + r * n, d + r * nqb, bs + r * nqb * 16);
 }

@@ -1,0 +1,277 @@
+// oh_prefill.hip - layer-major prompt processing (src/ornith_rforward.c:513-682
+// structure): every layer runs over a chunk of T tokens before the next, the
+// projections as batched matvecs (oh_k_mvb_*), the recurrent parts (conv
+// window, delta state, KV cache) advanced in token order. Each per-token
+// computation repeats the decode step's arithmetic in the same order, and the
+// delta recurrence is stepped token by token, so a prompt processed here gives
+// bit-identical logits and state to the same prompt fed through the token
+// step (the reference's ORNITH_PREFILL_SERIAL=1 mode). Included into
+// oh_kernels.hip after the operation bodies.
+
+// ---- embedding of T tokens: grid (H/256, T), token t at toks[base + t] -----------
+extern "C" __global__ void __launch_bounds__(256) oh_k_embed_rows(oh_op_embed a, int base) {
+    NoWait w;
+    oh_op_embed b = a;
+    b.x = a.x + (size_t)blockIdx.y * a.in;
+    embed_body(b, (int)blockIdx.x, base + (int)blockIdx.y, w);
+}
+
+// ---- causal depthwise conv + SiLU over T tokens (src/ornith_attn.c:370-388) ------
+// Thread per (channel, token): the K-1 inputs before token t come from the
+// chunk or, for the first tokens, from the window state (row j = position
+// base-(K-1)+j), summed as the decode step sums them. The window the next step
+// reads (parity (base+T)&1) receives the last K-1 inputs.
+extern "C" __global__ void __launch_bounds__(256)
+oh_k_conv_rows(const float *cat, const float *conv_w, float *conv_state, float *out, int T, int base, int cc, int K) {
+    const int c = (int)(blockIdx.x * 256 + tid_x()), t = (int)blockIdx.y;
+    if (c >= cc) return;
+    const float *win = conv_state + (size_t)(base & 1) * (K - 1) * cc;
+    float acc = 0.0f;
+    for (int j = 0; j < K - 1; j++) {
+        const int tj = t - (K - 1) + j;
+        const float xv = tj >= 0 ? ldg(cat + (size_t)tj * cc + c) : ldg(win + (size_t)(t + j) * cc + c);
+        acc += ldg(conv_w + (size_t)c * K + j) * xv;
+    }
+    acc += ldg(conv_w + (size_t)c * K + K - 1) * ldg(cat + (size_t)t * cc + c);
+    stg(out + (size_t)t * cc + c, ref_silu(acc));
+}
+
+// the window after the chunk (a separate launch: the conv above reads the old one)
+extern "C" __global__ void __launch_bounds__(256)
+oh_k_conv_window(const float *cat, float *conv_state, int T, int base, int cc, int K) {
+    const int c = (int)(blockIdx.x * 256 + tid_x()), j = (int)blockIdx.y;   // j < K-1
+    if (c >= cc) return;
+    const float *win = conv_state + (size_t)(base & 1) * (K - 1) * cc;
+    float *nwin = conv_state + (size_t)((base + T) & 1) * (K - 1) * cc;
+    const int tj = T - (K - 1) + j;
+    const float v = tj >= 0 ? ldg(cat + (size_t)tj * cc + c) : ldg(win + (size_t)(T + j) * cc + c);
+    if (nwin != win) stg(nwin + (size_t)j * cc + c, v);
+}
+// same-parity case (T even): the new window overwrites the old one in place,
+// so it is staged first
+extern "C" __global__ void __launch_bounds__(256)
+oh_k_conv_window_stage(const float *cat, const float *conv_state, float *stage, int T, int base, int cc, int K) {
+    const int c = (int)(blockIdx.x * 256 + tid_x()), j = (int)blockIdx.y;
+    if (c >= cc) return;
+    const float *win = conv_state + (size_t)(base & 1) * (K - 1) * cc;
+    const int tj = T - (K - 1) + j;
+    stg(stage + (size_t)j * cc + c, tj >= 0 ? ldg(cat + (size_t)tj * cc + c) : ldg(win + (size_t)(T + j) * cc + c));
+}
+
+// ---- per (token, key head): L2 norms of q and k; per (token, value head): gates --
+// grid (nk + nv, T), one wave: blocks [0, nk) normalise q and k of key head kh
+// (double sums of each 64-channel run, the runs added in order, as the decode
+// step), blocks [nk, nk+nv) form alpha = exp(ssm_a * softplus(a + dt_bias)) and
+// beta = sigmoid(b) of value head hv.
+template <int DK>
+__global__ void __launch_bounds__(64)
+oh_k_qk_gates_rows(const float *conv, const float *A, const float *Bg, const float *ssm_a, const float *dt_bias,
+                   float *qn, float *kn, float *al, float *be, int nk, int nv, int cc) {
+    constexpr int NQ = DK / 64;
+    const int t = (int)blockIdx.y, h = (int)blockIdx.x, lane = lane_id();
+    if (h < nk) {
+        const int qd = nk * DK;
+        const float *cq = conv + (size_t)t * cc + h * DK, *ck = conv + (size_t)t * cc + qd + h * DK;
+        float vq[NQ], vk[NQ];
+        double tq = 0.0, tk = 0.0;
+#pragma unroll
+        for (int i = 0; i < NQ; i++) {
+            vq[i] = ldg(cq + lane + 64 * i);
+            vk[i] = ldg(ck + lane + 64 * i);
+        }
+#pragma unroll
+        for (int i = 0; i < NQ; i++) {
+            const double sq = wave_sum_d((double)vq[i] * vq[i]);
+            const double sk = wave_sum_d((double)vk[i] * vk[i]);
+            tq = i == 0 ? sq : tq + sq;
+            tk = i == 0 ? sk : tk + sk;
+        }
+        const float iq = (float)(1.0 / sqrt(tq + (double)1e-6f));
+        const float ik = (float)(1.0 / sqrt(tk + (double)1e-6f));
+#pragma unroll
+        for (int i = 0; i < NQ; i++) {
+            stg(qn + ((size_t)t * nk + h) * DK + lane + 64 * i, vq[i] * iq);
+            stg(kn + ((size_t)t * nk + h) * DK + lane + 64 * i, vk[i] * ik);
+        }
+    } else if (lane == 0) {
+        const int hv = h - nk;
+        const float av = ldg(A + (size_t)t * nv + hv), bv = ldg(Bg + (size_t)t * nv + hv);
+        stg(al + (size_t)t * nv + hv, ref_expf(ldg(ssm_a + hv) * ref_softplus(av + ldg(dt_bias + hv))));
+        stg(be + (size_t)t * nv + hv, ref_sigmoid(bv));
+    }
+}
+
+// ---- the delta recurrence over T tokens (src/ornith_attn.c:198-213) ---------------
+// One wave per 64 state rows of value head hv (grid nv * DK/64); each lane
+// keeps its row in registers for the whole chunk and steps it token by token
+// exactly as the decode step does: s = S*alpha, sk = sum s*k, u = beta(v-sk),
+// s += u*k, o = sum s*q (sums in column order). Per token it writes o*scale,
+// silu(gate) and the run sum of o^2 over its 64 rows (the gated norm's inputs).
+template <int DK>
+__global__ void __launch_bounds__(64)
+oh_k_delta_scan(const float *qn, const float *kn, const float *conv, const float *al, const float *be,
+                const float *z, float *S, float *out, float *out_gate, double *out_runs, int T, int nk, int nv,
+                int cc, float out_scale) {
+    constexpr int NQ = DK / 64;
+    __shared__ __align__(16) float kq[2][2 * DK];              // [buffer][k | q]
+    const int lane = lane_id(), vb = (int)blockIdx.x;
+    const int hv = vb / NQ, slab = vb % NQ, r = slab * 64 + lane, kh = hv % nk;
+    const int qd = nk * DK, vd = nv * DK;
+    float *Sr = S + ((size_t)hv * DK + r) * DK;
+    float s[DK];
+#pragma unroll
+    for (int c = 0; c < DK / 4; c++) {
+        const float4 v = ldg((const float4 *)Sr + c);
+        s[4 * c] = v.x; s[4 * c + 1] = v.y; s[4 * c + 2] = v.z; s[4 * c + 3] = v.w;
+    }
+    // token t's k and q (uniform over the wave) through LDS, the next token's
+    // already requested while t is stepped
+    float pk[NQ], pq[NQ], pv, pa, pb, pz;
+    auto fetch = [&](int t) {
+        const int tc = t < T ? t : T - 1;
+#pragma unroll
+        for (int i = 0; i < NQ; i++) {
+            pk[i] = ldg(kn + ((size_t)tc * nk + kh) * DK + lane + 64 * i);
+            pq[i] = ldg(qn + ((size_t)tc * nk + kh) * DK + lane + 64 * i);
+        }
+        pv = ldg(conv + (size_t)tc * cc + 2 * qd + hv * DK + r);
+        pa = ldg(al + (size_t)tc * nv + hv);
+        pb = ldg(be + (size_t)tc * nv + hv);
+        pz = ldg(z + (size_t)tc * vd + hv * DK + r);
+    };
+    fetch(0);
+    for (int t = 0; t < T; t++) {
+        const int bf = t & 1;
+#pragma unroll
+        for (int i = 0; i < NQ; i++) {
+            kq[bf][lane + 64 * i] = pk[i];
+            kq[bf][DK + lane + 64 * i] = pq[i];
+        }
+        const float v = pv, alpha = pa, beta = pb, gz = pz;
+        fetch(t + 1);
+        wave_lds_sync();
+        const float *kk = kq[bf], *qq = kq[bf] + DK;
+#pragma unroll
+        for (int c = 0; c < DK; c++) s[c] = s[c] * alpha;
+        float sk = 0.0f;
+#pragma unroll
+        for (int c = 0; c < DK; c++) sk += s[c] * kk[c];
+        const float u = beta * (v - sk);
+#pragma unroll
+        for (int c = 0; c < DK; c++) s[c] += u * kk[c];
+        float o = 0.0f;
+#pragma unroll
+        for (int c = 0; c < DK; c++) o += s[c] * qq[c];
+        o *= out_scale;
+        const double so = wave_sum_d((double)o * o);
+        stg(out + (size_t)t * vd + hv * DK + r, o);
+        stg(out_gate + (size_t)t * vd + hv * DK + r, ref_silu(gz));
+        if (lane == 0) stg(out_runs + (size_t)t * (vd / 64) + vb, so);
+    }
+#pragma unroll
+    for (int c = 0; c < DK / 4; c++) stg((float4 *)Sr + c, make_float4(s[4 * c], s[4 * c + 1], s[4 * c + 2], s[4 * c + 3]));
+}
+
+// ---- gated per-head RMSNorm + Q8_K of T vectors (src/ornith_rforward.c:300-319) ---
+// one block per token: per head of gdim elements the runs' sums of squares in
+// order, inv = 1/sqrt(ss/gdim + eps), v = x * inv * w * silu(z); then Q8_K.
+extern "C" __global__ void __launch_bounds__(256)
+oh_k_gnorm_q8k_rows(const float *x, const float *sz, const double *runs, const float *w, float eps, int n,
+                    int gdim, int8_t *qs, float *d, int16_t *bs) {
+    __shared__ float v[8192];
+    __shared__ float hinv[128];
+    const size_t t = blockIdx.x;
+    const int tid = tid_x(), wave = tid >> 6, nh = n / gdim, rpg = gdim / 64, nqb = n / 256;
+    if (tid < nh) {
+        const double *rr = runs + t * (n / 64) + (size_t)tid * rpg;
+        double tot = ldg(rr);
+        for (int k = 1; k < rpg; k++) tot += ldg(rr + k);
+        hinv[tid] = (float)(1.0 / sqrt(tot / (double)gdim + (double)eps));
+    }
+    __syncthreads();
+    for (int i = tid; i < n; i += 256)
+        v[i] = ldg(x + t * n + i) * hinv[i / gdim] * ldg(w + i % gdim) * ldg(sz + t * n + i);
+    __syncthreads();
+    for (int qb = wave; qb < nqb; qb += 4) q8k_block_from_lds(v, qb, qs + t * n, d + t * nqb, bs + t * nqb * 16);
+}
+
+// ---- GQA over T tokens: the decode operations with token t at position base+t ----
+extern "C" __global__ void __launch_bounds__(256) oh_k_prep_rows(oh_op_prep a, int base) {
+    NoWait w;
+    const int t = (int)blockIdx.y;
+    oh_op_prep b = a;
+    b.qproj = a.qproj + (size_t)t * 2 * a.nh * a.hd;
+    b.kin = a.kin + (size_t)t * a.nkv * a.hd;
+    b.vin = a.vin + (size_t)t * a.nkv * a.hd;
+    b.qr = a.qr + (size_t)t * a.nh * a.hd;
+    b.gate = a.gate + (size_t)t * a.nh * a.hd;
+    prep_body(b, (int)blockIdx.x, base + t, w);
+}
+
+// tokens t0 + blockIdx.y; flash partials per token at part + (blockIdx.y) * pstride
+extern "C" __global__ void __launch_bounds__(256)
+oh_k_attn_main_rows(oh_op_attn a, int base, int t0, size_t po_stride, size_t pml_stride) {
+    NoWait w;
+    const int t = t0 + (int)blockIdx.y, qd = a.nh * a.hd;
+    oh_op_attn b = a;
+    b.qr = a.qr + (size_t)t * qd;
+    b.gate = a.gate + (size_t)t * qd;
+    b.out = a.out + (size_t)t * qd;
+    b.part_o = a.part_o + (size_t)blockIdx.y * po_stride;
+    b.part_ml = a.part_ml + (size_t)blockIdx.y * pml_stride;
+    attn_main_body(b, (int)blockIdx.x, base + t, w);
+}
+
+extern "C" __global__ void __launch_bounds__(256)
+oh_k_attn_combine_rows(oh_op_attn a, int base, int t0, size_t po_stride, size_t pml_stride) {
+    NoWait w;
+    const int t = t0 + (int)blockIdx.y, qd = a.nh * a.hd;
+    oh_op_attn b = a;
+    b.gate = a.gate + (size_t)t * qd;
+    b.out = a.out + (size_t)t * qd;
+    b.part_o = a.part_o + (size_t)blockIdx.y * po_stride;
+    b.part_ml = a.part_ml + (size_t)blockIdx.y * pml_stride;
+    combine_body(b, (int)blockIdx.x, base + t, w);
+}
+
+// ---- MoE over T tokens ------------------------------------------------------------
+// routing of token t (one wave): the decode route (src/ornith_moe.c:8-30)
+extern "C" __global__ void __launch_bounds__(64)
+oh_k_route_rows(const float *logits, int ne, int k, const float *shgate_logit, int32_t *idx, float *w,
+                float *shgate) {
+    const size_t t = blockIdx.x;
+    route_wave(logits + t * ne, ne, k, shgate_logit ? shgate_logit + t : nullptr, idx + t * k, w + t * k,
+               shgate ? shgate + t : nullptr);
+}
+
+// expert lists: pair p = t*k + s goes to list[e*lstride + j] of expert e = idx[p]
+// (the order inside a list does not matter: every pair is computed on its own)
+extern "C" __global__ void __launch_bounds__(256)
+oh_k_group_pairs(const int32_t *idx, int npairs, int32_t *cnt, int32_t *list, int lstride) {
+    const int p = (int)(blockIdx.x * 256 + tid_x());
+    if (p >= npairs) return;
+    const int e = ldg(idx + p);
+    const int j = atomicAdd(cnt + e, 1);
+    stg(list + (size_t)e * lstride + j, (int32_t)p);
+}
+
+extern "C" __global__ void __launch_bounds__(256) oh_k_fill_i32(int32_t *p, int n, int32_t v) {
+    const int i = (int)(blockIdx.x * 256 + tid_x());
+    if (i < n) p[i] = v;
+}
+
+// x_t += sum_s w_ts * o_ts (s in routing order) + shared * gate_t; grid (H/256, T)
+extern "C" __global__ void __launch_bounds__(256)
+oh_k_moe_combine_rows(float *x, const float *o, const float *w, int k, int H, const float *so, const float *shgate) {
+    const int i = (int)(blockIdx.x * 256 + tid_x());
+    const size_t t = blockIdx.y;
+    if (i >= H) return;
+    float acc = 0.0f;
+    for (int s = 0; s < k; s++) acc += ldg(w + t * k + s) * ldg(o + (t * k + s) * H + i);
+    if (so) {
+        const float sv = ldg(so + t * H + i);
+        const float v = shgate ? sv * ldg(shgate + t) : sv;
+        acc += v;
+    }
+    stg(x + t * H + i, ldg(x + t * H + i) + acc);
+}

@@ -241,3 +241,22 @@ typedef struct {
 #define OH_STEP_NCTR 32
 #define OH_STEP_CSTRIDE 16
 enum { OH_IO_POS = 0, OH_IO_BEST = 1, OH_IO_EPOCH_BODY = 2, OH_IO_EPOCH_HEAD = 3, OH_IO_ERR = 4 };
+
+// Batched matvec (prefill): Y[col] = W . X[col] for many activation columns,
+// the same integer dot per (row, column) as the matvec. Columns are dense
+// [0, ncol) with activation index c and output index c, or grouped: group g
+// (blockIdx.y; stacked expert g) has cnt[g] columns list[g*lstride + j] = p,
+// activation index p / adiv, output index p. Activation index a: Q8_K planes
+// xqs + a*in, xd + a*nb, xbs + a*nb*16. Output row o of column index p at
+// y[p*ystride + o] (mode 1: +=). pair: W2 reduced too, emitting silu(W.x)*(W2.x).
+typedef struct {
+    const uint8_t *A, *B, *C, *A2, *B2, *C2;
+    const int8_t *xqs;
+    const float *xd;
+    const int16_t *xbs;
+    float *y;
+    const int32_t *cnt, *list;
+    int type, nb, in, rows, pair, mode;
+    int ncol, lstride, adiv, ystride;
+    int tcol;                      // columns staged in LDS at a time
+} oh_mvbatch;

@@ -1,0 +1,106 @@
+"""GPU: the layer-major prefill (every layer over a chunk of prompt tokens with
+batched projections, src/ornith_rforward.c:647-682) against the reference and
+against the token-by-token path (ORNITH_HIP_PREFILL=0).
+
+Bar: bit-exact prompt logits and 64 greedy tokens on C1 against the
+reference's serial golden fixture; bit-identical logits, tokens and session
+state (delta state, conv window, Q8 KV cache) between the two paths on
+Q4_K/Q6_K models with MoE and dense FFNs, on prompts that span several chunks,
+with odd and even chunk starts, on the exact and flash attention paths."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import clibs
+from clibs import i32p
+
+pytestmark = pytest.mark.gpu
+GOLD = np.load(clibs.ROOT / "tests" / "golden" / "c1.npz")
+
+MIX = dict(clibs.C1, hidden=768, n_layers=4, vocab=1000, nh=4, nkv=1, hd=128, nk=2, nv=4, dhead=128,
+           ne=8, top_k=2, moe_inter=512, shared_inter=512, t_default=clibs.Q4_K, t_attn_v=clibs.Q6_K,
+           t_ffn_down=clibs.Q6_K, t_output=clibs.Q6_K, t_embd=clibs.Q4_K, seed=5)
+DENSE = dict(MIX, ne=0, top_k=0, moe_inter=0, shared_inter=1024, seed=7)
+
+
+def u32(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+def test_prefill_c1_matches_reference(hip_ctx, monkeypatch):
+    monkeypatch.setenv("ORNITH_HIP_PREFILL", "1")
+    m = hip_ctx.synth(**clibs.C1)
+    s = m.session(104)
+    s.eval(GOLD["prompt"])
+    assert np.array_equal(u32(s.logits()), u32(GOLD["serial_prompt_logits"]))
+    assert np.array_equal(s.generate(64), GOLD["serial_tokens"])
+    s.free()
+    m.free()
+
+
+def test_prefill_dense_matches_oracle(hip_ctx, orc, tmp_path, monkeypatch):
+    """A dense-FFN model (ffn_gate/ffn_up/ffn_down, src/ornith_rforward.c:325-333)
+    against the oracle's token path: prompt logits bit-exact."""
+    monkeypatch.setenv("ORNITH_HIP_PREFILL", "1")
+    path = tmp_path / "dense.gguf"
+    clibs.write_c1_gguf(path, DENSE)
+    om = C.c_void_p()
+    assert orc.orc_model_load(str(path).encode(), C.byref(om)) == 0
+    orc.orc_model_set_threads(om, 8)
+    os_ = orc.orc_session_new(om, 40, 1)
+    p = np.random.default_rng(4).integers(0, DENSE["vocab"], 20).astype(np.int32)
+    assert orc.orc_session_eval(os_, i32p(p), 20, 1) == 0
+    want = np.ctypeslib.as_array(orc.orc_session_logits(os_), (DENSE["vocab"],)).copy()
+    m = hip_ctx.synth(**DENSE)
+    s = m.session(40)
+    s.eval(p)
+    assert np.array_equal(u32(s.logits()), u32(want))
+    s.free()
+    m.free()
+    orc.orc_session_free(os_)
+    orc.orc_model_free(om)
+
+
+def evals(m, chunks, cap, prefill, monkeypatch, exact_max):
+    monkeypatch.setenv("ORNITH_HIP_PREFILL", "1" if prefill else "0")
+    if exact_max is not None:
+        monkeypatch.setenv("ORNITH_HIP_EXACT_ATTN_MAX", str(exact_max))
+    s = m.session(cap)
+    logits = []
+    for c in chunks:
+        s.eval(c)
+        logits.append(s.logits().copy())
+    return s, logits
+
+
+def same_state(m, a, b):
+    arch = m.arch
+    assert a.pos == b.pos
+    for l in range(arch["n_layers"]):
+        if (l + 1) % arch["full_interval"]:
+            assert np.array_equal(u32(a.delta_state(l)), u32(b.delta_state(l))), l
+            assert np.array_equal(u32(a.conv_state(l)), u32(b.conv_state(l))), l
+        else:
+            for x, y in zip(a.kv(l), b.kv(l)):
+                assert np.array_equal(x.view(np.uint8), y.view(np.uint8)), l
+
+
+@pytest.mark.parametrize("cfg", ["moe", "dense"])
+@pytest.mark.parametrize("exact_max", [None, 0], ids=["exact", "flash"])
+def test_prefill_equals_token_path(hip_ctx, monkeypatch, cfg, exact_max):
+    m = hip_ctx.synth(**(MIX if cfg == "moe" else DENSE))
+    a = m.arch
+    rng = np.random.default_rng(3)
+    # 300 tokens span two chunks; then evals starting at odd and even positions
+    chunks = [rng.integers(0, a["vocab"], n).astype(np.int32) for n in (300, 7, 2, 33)]
+    sp, lp = evals(m, chunks, 400, True, monkeypatch, exact_max)
+    st, lt = evals(m, chunks, 400, False, monkeypatch, exact_max)
+    for x, y in zip(lp, lt):
+        assert np.array_equal(u32(x), u32(y))
+    same_state(m, sp, st)
+    assert np.array_equal(sp.generate(24), st.generate(24))
+    assert np.array_equal(u32(sp.logits()), u32(st.logits()))
+    sp.free()
+    st.free()
+    m.free()

@@ -72,6 +72,14 @@ def test_matvec_vs_oracle(hip_ctx, orc, t, shape):
         r = np.zeros(out, np.float32)
         orc.orc_matvec(t, bp(enc), n, out, f32p(np.ascontiguousarray(xc)), f32p(r), 0, 8)
         assert np.array_equal(u32(y3[c * out:(c + 1) * out]), u32(r))
+    if n <= 2048:
+        # more columns than one LDS tile of the batched kernel
+        cols = [x * np.float32(1.0 + 0.25 * k) for k in range(70)]
+        y70 = W.matvec(np.concatenate(cols))
+        for c in (0, 1, 31, 32, 63, 64, 69):
+            r = np.zeros(out, np.float32)
+            orc.orc_matvec(t, bp(enc), n, out, f32p(np.ascontiguousarray(cols[c])), f32p(r), 0, 8)
+            assert np.array_equal(u32(y70[c * out:(c + 1) * out]), u32(r)), (c, name, shape)
     W.free()
 
 

@@ -12,9 +12,10 @@ GOLD = np.load(clibs.ROOT / "tests" / "golden" / "c1.npz")
 MIX = dict(clibs.C1, hidden=768, n_layers=4, vocab=1000, nh=4, nkv=1, hd=128, nk=2, nv=4, dhead=128,
            ne=8, top_k=2, moe_inter=512, shared_inter=256, t_default=clibs.Q4_K, t_attn_v=clibs.Q6_K,
            t_ffn_down=clibs.Q6_K, t_output=clibs.Q6_K, t_embd=clibs.Q4_K, seed=3)
+DENSE = dict(MIX, ne=0, top_k=0, moe_inter=0, shared_inter=1024, seed=7)
 
 
-@pytest.mark.parametrize("cfg", [clibs.C1, MIX], ids=["C1-Q8_0", "Q4_K_M-mix"])
+@pytest.mark.parametrize("cfg", [clibs.C1, MIX, DENSE], ids=["C1-Q8_0", "Q4_K_M-mix", "dense"])
 def test_synth_equals_generator_bytes(hip_ctx, tmp_path, cfg):
     p = tmp_path / "gen.gguf"
     clibs.write_c1_gguf(p, cfg)
