@@ -134,8 +134,14 @@ const ornith_hip_tensor *ornith_hip_model_tensor(const ornith_hip_model *m, cons
  * semantics, src/ornith_attn.h:39-68). */
 int  ornith_hip_session_new(ornith_hip_model *m, int cap, ornith_hip_session **out);
 void ornith_hip_session_free(ornith_hip_session *s);                             /* rmodel_session_free */
-/* rmodel_session_eval with ORNITH_PREFILL_SERIAL=1 semantics: the prompt runs
- * through the token step (src/ornith_rforward.c:838-849,933-944). */
+/* rmodel_session_eval (src/ornith_rforward.c:838-849,933-944): the prompt runs
+ * layer by layer over chunks of up to 256 tokens (batched projections). As in
+ * the reference, gated delta-net layers use the chunked scan of 32-token
+ * chunks (src/ornith_attn.c:215-349) unless ORNITH_PREFILL_SERIAL=1 selects the
+ * token recurrence; either way the results are the reference's bits for that
+ * mode. Models past the batched path's limits (a projection wider than 8192,
+ * a type without the integer dot) and ORNITH_HIP_PREFILL=0 run the prompt
+ * through the token step, i.e. with ORNITH_PREFILL_SERIAL=1 results. */
 int  ornith_hip_session_eval(ornith_hip_session *s, const int32_t *tokens, int n);
 /* rmodel_session_logits: copies the V next-token logits to `out`. */
 int  ornith_hip_session_logits(ornith_hip_session *s, float *out);

@@ -968,7 +968,7 @@ struct ornith_hip_session {
         float *QP = nullptr, *KB = nullptr, *VB = nullptr, *QR = nullptr, *AG = nullptr, *OA = nullptr;
         float *FPO = nullptr, *FPML = nullptr, *RL = nullptr, *SHL = nullptr, *SHG = nullptr, *RW = nullptr;
         int32_t *RIDX = nullptr, *CNT = nullptr, *LIST = nullptr;
-        float *Hh = nullptr, *HSH = nullptr, *OD = nullptr, *ODSH = nullptr, *STAGE = nullptr;
+        float *Hh = nullptr, *HSH = nullptr, *OD = nullptr, *ODSH = nullptr, *STAGE = nullptr, *GR = nullptr;
         Q8Buf XQ, OQ, OAQ, HQ, HSQ;
     } pf;
     std::vector<int> sp_body_rk;
@@ -1550,6 +1550,9 @@ static int sync_pos(ornith_hip_session *s) {
 // advanced in token order with the decode step's arithmetic. Bit-identical to
 // the same tokens fed through the token step.
 static const int kPfChunk = 256, kPfAttnSub = 16;
+// the chunked delta scan counts its 32-token chunks from the start of the
+// evaluation: engine chunks must not split one
+static_assert(kPfChunk % 32 == 0, "engine chunks hold whole delta chunks");
 
 static bool pf_mvb_ok(const ornith_hip_tensor *W) {
     return W && oh_qdot_can(W->type, W->in) && W->in <= 8192 && W->in / 256 <= 64;
@@ -1602,6 +1605,7 @@ static int pf_alloc(ornith_hip_session *s, int tc) {
     CHK(salloc(s, &p.AL, T * a.nv + 1)); CHK(salloc(s, &p.BE, T * a.nv + 1));
     CHK(salloc(s, &p.QN, T * qd + 1)); CHK(salloc(s, &p.KN, T * qd + 1));
     CHK(salloc(s, &p.RUNS, T * (vd / 64) + 1));
+    CHK(salloc(s, &p.GR, (size_t)oh_delta_grams_floats(tc, a.nk > 0 ? a.nk : 1) + 1));
     CHK(salloc(s, &p.STAGE, (size_t)(a.conv_k > 1 ? a.conv_k - 1 : 1) * cc + 1));
     CHK(salloc(s, &p.QP, T * 2 * aq + 1)); CHK(salloc(s, &p.KB, T * kvd + 1)); CHK(salloc(s, &p.VB, T * kvd + 1));
     CHK(salloc(s, &p.QR, T * aq + 1)); CHK(salloc(s, &p.AG, T * aq + 1)); CHK(salloc(s, &p.OA, T * aq + 1));
@@ -1635,7 +1639,7 @@ static int pf_mvb(const ornith_hip_tensor *W, const ornith_hip_tensor *W2, const
     return ORNITH_HIP_OK;
 }
 
-static int pf_chunk(ornith_hip_session *s, int base, int T, hipStream_t st) {
+static int pf_chunk(ornith_hip_session *s, int base, int T, bool chunked, hipStream_t st) {
     const ornith_hip_model *m = s->m;
     const ornith_hip_arch &a = m->a;
     auto &p = s->pf;
@@ -1679,8 +1683,12 @@ static int pf_chunk(ornith_hip_session *s, int base, int T, hipStream_t st) {
             HCHK(oh_launch_conv_rows(p.CAT, (const float *)y.conv->A, z.conv, p.CONV, p.STAGE, T, base, cc, a.conv_k, st));
             HCHK(oh_launch_qk_gates_rows(a.dk, p.CONV, p.A, p.Bg, (const float *)y.ssm_a->A,
                                          (const float *)y.dt_bias->A, p.QN, p.KN, p.AL, p.BE, T, a.nk, a.nv, cc, st));
-            HCHK(oh_launch_delta_scan(a.dk, p.QN, p.KN, p.CONV, p.AL, p.BE, p.Z, z.S, p.O, p.OG, p.RUNS, T, a.nk,
-                                      a.nv, cc, 1.0f / sqrtf((float)a.dk), st));
+            if (chunked)
+                HCHK(oh_launch_delta_chunked(a.dk, p.QN, p.KN, p.CONV, p.AL, p.BE, p.Z, p.GR, z.S, p.O, p.OG, p.RUNS,
+                                             T, a.nk, a.nv, cc, 1.0f / sqrtf((float)a.dk), st));
+            else
+                HCHK(oh_launch_delta_scan(a.dk, p.QN, p.KN, p.CONV, p.AL, p.BE, p.Z, z.S, p.O, p.OG, p.RUNS, T, a.nk,
+                                          a.nv, cc, 1.0f / sqrtf((float)a.dk), st));
             HCHK(oh_launch_gnorm_q8k_rows(p.O, p.OG, p.RUNS, (const float *)y.ssm_norm->A, a.eps, vd, a.dv, T,
                                           p.OQ.qs, p.OQ.d, p.OQ.bs, st));
             CHK(pf_mvb(y.ssm_out, nullptr, p.OQ, p.X, H, T, 1, st));
@@ -1721,7 +1729,16 @@ static bool pf_enabled() {
     return !(e && e[0] == '0');
 }
 
-extern "C" int ornith_hip_session_eval(ornith_hip_session *s, const int32_t *tokens, int n) {
+// the reference's prompt mode switch (src/ornith_rforward.c:838-849): default
+// chunked delta scan, ORNITH_PREFILL_SERIAL=1 the token-by-token recurrence
+static bool prefill_serial() {
+    const char *e = getenv("ORNITH_PREFILL_SERIAL");
+    return e && e[0] == '1';
+}
+
+// tokens through the layer-major prompt path (rprefill) or, with token_path,
+// through the token step (rforward_token) one at a time
+static int session_eval(ornith_hip_session *s, const int32_t *tokens, int n, bool token_path) {
     if (n <= 0) return ORNITH_HIP_OK;
     if (s->pos + n > s->cap) {
         seterr("session capacity %d exceeded (pos %d + %d tokens)", s->cap, s->pos, n);
@@ -1736,11 +1753,12 @@ extern "C" int ornith_hip_session_eval(ornith_hip_session *s, const int32_t *tok
     hipStream_t st = s->m->ctx->st;
     CHK(sync_pos(s));
     HCHK(hipMemcpyAsync(s->toks + s->pos, tokens, (size_t)n * 4, hipMemcpyHostToDevice, st));
-    if (n > 1 && pf_enabled() && pf_supported(s->m)) {
+    const bool serial = prefill_serial();
+    if (!token_path && (n > 1 || !serial) && pf_enabled() && pf_supported(s->m)) {
         // layer-major over chunks of tokens, then the head at the last one
         CHK(pf_alloc(s, n < kPfChunk ? n : kPfChunk));
         for (int c0 = 0; c0 < n; c0 += kPfChunk)
-            CHK(pf_chunk(s, s->pos + c0, n - c0 < kPfChunk ? n - c0 : kPfChunk, st));
+            CHK(pf_chunk(s, s->pos + c0, n - c0 < kPfChunk ? n - c0 : kPfChunk, !serial, st));
         s->pf.pos_after = s->pos + n;   // outlives the asynchronous copy
         HCHK(hipMemcpyAsync(s->io + OH_IO_POS, &s->pf.pos_after, 4, hipMemcpyHostToDevice, st));
     } else {
@@ -1754,8 +1772,14 @@ extern "C" int ornith_hip_session_eval(ornith_hip_session *s, const int32_t *tok
     return ORNITH_HIP_OK;
 }
 
+extern "C" int ornith_hip_session_eval(ornith_hip_session *s, const int32_t *tokens, int n) {
+    return session_eval(s, tokens, n, false);
+}
+
+// rforward_token whatever the prompt mode (a one-token evaluation in the
+// chunked mode is a one-token delta chunk, which rounds differently)
 extern "C" int ornith_hip_session_step(ornith_hip_session *s, int32_t token) {
-    return ornith_hip_session_eval(s, &token, 1);
+    return session_eval(s, &token, 1, true);
 }
 
 extern "C" int ornith_hip_session_logits(ornith_hip_session *s, float *out) {

@@ -73,6 +73,23 @@ hipError_t oh_launch_delta_scan(int dk, const float *qn, const float *kn, const 
     else return hipErrorInvalidValue;
     return hipGetLastError();
 }
+int oh_delta_grams_floats(int T, int nk) { return (T + kDeltaChunk - 1) / kDeltaChunk * nk * 2 * kDeltaChunk * kDeltaChunk; }
+hipError_t oh_launch_delta_chunked(int dk, const float *qn, const float *kn, const float *conv, const float *al,
+                                   const float *be, const float *z, float *grams, float *S, float *out,
+                                   float *out_gate, double *out_runs, int T, int nk, int nv, int cc, float out_scale,
+                                   hipStream_t st) {
+    const dim3 gg(nk, (T + kDeltaChunk - 1) / kDeltaChunk);
+    if (dk == 128) {
+        hipLaunchKernelGGL(oh_k_delta_grams<128>, gg, dim3(256), 0, st, qn, kn, T, nk, grams);
+        hipLaunchKernelGGL(oh_k_delta_chunked<128>, dim3(nv * 2), dim3(64), 0, st, qn, kn, conv, al, be, z, grams, S, out, out_gate, out_runs, T, nk, nv, cc, out_scale);
+    } else if (dk == 64) {
+        hipLaunchKernelGGL(oh_k_delta_grams<64>, gg, dim3(256), 0, st, qn, kn, T, nk, grams);
+        hipLaunchKernelGGL(oh_k_delta_chunked<64>, dim3(nv), dim3(64), 0, st, qn, kn, conv, al, be, z, grams, S, out, out_gate, out_runs, T, nk, nv, cc, out_scale);
+    } else {
+        return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
 hipError_t oh_launch_gnorm_q8k_rows(const float *x, const float *sz, const double *runs, const float *w, float eps,
                                     int n, int gdim, int T, int8_t *qs, float *d, int16_t *bs, hipStream_t st) {
     hipLaunchKernelGGL(oh_k_gnorm_q8k_rows, dim3(T), dim3(256), 0, st, x, sz, runs, w, eps, n, gdim, qs, d, bs);

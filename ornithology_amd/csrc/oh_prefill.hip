@@ -172,6 +172,177 @@ oh_k_delta_scan(const float *qn, const float *kn, const float *conv, const float
     for (int c = 0; c < DK / 4; c++) stg((float4 *)Sr + c, make_float4(s[4 * c], s[4 * c + 1], s[4 * c + 2], s[4 * c + 3]));
 }
 
+// ---- chunked delta scan (the reference's default prompt mode) --------------------
+// ornith_delta_prefill / delta_chunk (src/ornith_attn.c:215-349): the prompt in
+// chunks of kDeltaChunk tokens counted from the start of the evaluation; per
+// chunk, with S_in the incoming state,
+//   p_i = prod_{l<=i} alpha_l, Sk_i = S_in k_i, Sq_i = S_in q_i,
+//   u_i = beta_i v_i - beta_i p_i Sk_i - sum_{j<i} beta_i (p_i/p_j)(k_j.k_i) u_j,
+//   o_i = p_i Sq_i + sum_{j<=i} (p_i/p_j)(k_j.q_i) u_j,
+//   S_out = p_{C-1} S_in + sum_j (p_{C-1}/p_j) u_j k_j^T,
+// where p_i/p_j is accumulated as the running product of alpha_{j+1..i}. Every
+// float is formed in the reference's order, so the result equals its bits
+// (it differs from the token-by-token recurrence in rounding).
+constexpr int kDeltaChunk = 32;
+
+// the chunk Gram matrices, once per (key head, chunk): kk[i][j] = k_j.k_i and
+// kq[i][j] = k_j.q_i (ot_dot order: sequential over the head dimension)
+template <int DK>
+__global__ void __launch_bounds__(256)
+oh_k_delta_grams(const float *qn, const float *kn, int T, int nk, float *grams) {
+    constexpr int CH = kDeltaChunk, LD = DK + 1;
+    __shared__ float ks[CH * LD], qs[CH * LD];
+    const int kh = (int)blockIdx.x, ch = (int)blockIdx.y, tid = tid_x();
+    const int c0 = ch * CH, C = T - c0 < CH ? T - c0 : CH;
+    for (int e = tid; e < CH * DK; e += 256) {
+        const int i = e / DK, c = e - i * DK;
+        const size_t src = ((size_t)(c0 + (i < C ? i : 0)) * nk + kh) * DK + c;
+        ks[i * LD + c] = i < C ? ldg(kn + src) : 0.0f;
+        qs[i * LD + c] = i < C ? ldg(qn + src) : 0.0f;
+    }
+    __syncthreads();
+    // pair p < 2*CH*CH: p / (CH*CH) selects kk or kq, then (i, j) = row, column
+    constexpr int NP = 2 * CH * CH / 256;
+    float acc[NP];
+    int ii[NP], jj[NP], wq[NP];
+#pragma unroll
+    for (int m = 0; m < NP; m++) {
+        const int p = tid + 256 * m;
+        wq[m] = p / (CH * CH);
+        ii[m] = (p % (CH * CH)) / CH;
+        jj[m] = p % CH;
+        acc[m] = 0.0f;
+    }
+    for (int c = 0; c < DK; c++) {
+#pragma unroll
+        for (int m = 0; m < NP; m++) {
+            const float a = ks[jj[m] * LD + c];
+            const float b = wq[m] ? qs[ii[m] * LD + c] : ks[ii[m] * LD + c];
+            acc[m] += a * b;
+        }
+    }
+    float *g = grams + ((size_t)ch * nk + kh) * 2 * CH * CH;
+#pragma unroll
+    for (int m = 0; m < NP; m++) stg(g + tid + 256 * m, acc[m]);
+}
+
+// one wave per 64 rows of one value head's state, the rows in registers; a
+// lane owns state row r and its u / Sk / Sq columns (in LDS, [i][lane])
+template <int DK>
+__global__ void __launch_bounds__(64)
+oh_k_delta_chunked(const float *qn, const float *kn, const float *conv, const float *al, const float *be,
+                   const float *z, const float *grams, float *S, float *out, float *out_gate, double *out_runs,
+                   int T, int nk, int nv, int cc, float out_scale) {
+    constexpr int CH = kDeltaChunk, NQ = DK / 64;
+    __shared__ __align__(16) float kc[CH][DK], qc[CH][DK];
+    __shared__ float M[CH][CH + 1], W[CH][CH + 1];       // k_j.k_i / k_j.q_i, then the coefficients
+    __shared__ float Sq[CH][64], U[CH][64];
+    __shared__ float alpha[CH], beta[CH], p[CH], wend[CH];
+    const int lane = lane_id(), vb = (int)blockIdx.x;
+    const int hv = vb / NQ, slab = vb % NQ, r = slab * 64 + lane, kh = hv % nk;
+    const int qd = nk * DK, vd = nv * DK;
+    float *Sr = S + ((size_t)hv * DK + r) * DK;
+    float s[DK];
+#pragma unroll
+    for (int c = 0; c < DK / 4; c++) {
+        const float4 v = ldg((const float4 *)Sr + c);
+        s[4 * c] = v.x; s[4 * c + 1] = v.y; s[4 * c + 2] = v.z; s[4 * c + 3] = v.w;
+    }
+    for (int c0 = 0, ch = 0; c0 < T; c0 += CH, ch++) {
+        const int C = T - c0 < CH ? T - c0 : CH;
+        wave_lds_sync();                                 // the previous chunk is consumed
+        for (int e = lane; e < C * DK / 4; e += 64) {
+            const int i = e / (DK / 4), c = e - i * (DK / 4);
+            const size_t src = ((size_t)(c0 + i) * nk + kh) * DK;
+            ((float4 *)kc[i])[c] = ldg((const float4 *)(kn + src) + c);
+            ((float4 *)qc[i])[c] = ldg((const float4 *)(qn + src) + c);
+        }
+        const float *g = grams + ((size_t)ch * nk + kh) * 2 * CH * CH;
+        for (int e = lane; e < CH * CH; e += 64) {
+            M[e / CH][e % CH] = ldg(g + e);
+            W[e / CH][e % CH] = ldg(g + CH * CH + e);
+        }
+        if (lane < C) {
+            alpha[lane] = ldg(al + (size_t)(c0 + lane) * nv + hv);
+            beta[lane] = ldg(be + (size_t)(c0 + lane) * nv + hv);
+        }
+        for (int i = 0; i < C; i++) U[i][lane] = ldg(conv + (size_t)(c0 + i) * cc + 2 * qd + hv * DK + r);
+        wave_lds_sync();
+        // decay products: lane i owns row i of the coefficient tables, which
+        // turn in place into M[i][j] = beta_i (p_i/p_j) k_j.k_i and
+        // W[i][j] = (p_i/p_j) k_j.q_i
+        if (lane < C) {
+            const int i = lane;
+            float pi = alpha[0];
+            for (int l = 1; l <= i; l++) pi = pi * alpha[l];
+            p[i] = pi;
+            const float bi = beta[i];
+            float ratio = 1.0f;
+            for (int j = i - 1; j >= 0; j--) {
+                ratio *= alpha[j + 1];
+                M[i][j] = bi * ratio * M[i][j];
+                W[i][j] = ratio * W[i][j];
+            }
+        }
+        if (lane == 0) {
+            float ratio = 1.0f;
+            for (int j = C - 1; j >= 0; j--) {
+                wend[j] = ratio;
+                ratio *= alpha[j];
+            }
+        }
+        wave_lds_sync();
+        // projections of the incoming state; U starts as
+        // t_i = beta_i v_i - beta_i p_i (S_in k_i)
+        for (int i = 0; i < C; i++) {
+            float ak = 0.0f, aq = 0.0f;
+            const float *ki = kc[i], *qi = qc[i];
+#pragma unroll
+            for (int c = 0; c < DK; c++) {
+                ak += s[c] * ki[c];
+                aq += s[c] * qi[c];
+            }
+            const float bi = beta[i], pi = p[i];
+            U[i][lane] = bi * U[i][lane] - bi * pi * ak;
+            Sq[i][lane] = aq;
+        }
+        // forward substitution (I + M) U = T, this lane's state row
+        for (int i = 0; i < C; i++) {
+            float u = U[i][lane];
+            for (int j = i - 1; j >= 0; j--) {
+                const float mij = M[i][j];
+                if (mij != 0.0f) u -= mij * U[j][lane];
+            }
+            U[i][lane] = u;
+        }
+        // outputs, scaled by 1/sqrt(dk), with the per-run sums of squares of
+        // the gated RMSNorm and silu of the gate
+        for (int i = 0; i < C; i++) {
+            float o = p[i] * Sq[i][lane];
+            o += W[i][i] * U[i][lane];
+            for (int j = i - 1; j >= 0; j--) o += W[i][j] * U[j][lane];
+            o *= out_scale;
+            const int t = c0 + i;
+            const double so = wave_sum_d((double)o * o);
+            stg(out + (size_t)t * vd + hv * DK + r, o);
+            stg(out_gate + (size_t)t * vd + hv * DK + r, ref_silu(ldg(z + (size_t)t * vd + hv * DK + r)));
+            if (lane == 0) stg(out_runs + (size_t)t * (vd / 64) + vb, so);
+        }
+        // S_out = p_{C-1} S_in + sum_j (p_{C-1}/p_j) u_j k_j^T, j descending
+        const float pc = p[C - 1];
+#pragma unroll
+        for (int c = 0; c < DK; c++) s[c] *= pc;
+        for (int j = C - 1; j >= 0; j--) {
+            const float ur = wend[j] * U[j][lane];
+            if (ur == 0.0f) continue;
+#pragma unroll
+            for (int c = 0; c < DK; c++) s[c] += ur * kc[j][c];
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < DK / 4; c++) stg((float4 *)Sr + c, make_float4(s[4 * c], s[4 * c + 1], s[4 * c + 2], s[4 * c + 3]));
+}
+
 // ---- gated per-head RMSNorm + Q8_K of T vectors (src/ornith_rforward.c:300-319) ---
 // one block per token: per head of gdim elements the runs' sums of squares in
 // order, inv = 1/sqrt(ss/gdim + eps), v = x * inv * w * silu(z); then Q8_K.

@@ -18,6 +18,14 @@ def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) GPU and libornith_hip.so")
 
 
+@pytest.fixture(autouse=True)
+def serial_prefill(monkeypatch):
+    """Prompts run in the reference's ORNITH_PREFILL_SERIAL=1 mode (the token
+    recurrence) unless a test sets ORNITH_PREFILL_SERIAL=0, the reference's
+    default chunked delta scan."""
+    monkeypatch.setenv("ORNITH_PREFILL_SERIAL", "1")
+
+
 @pytest.fixture(scope="session")
 def orc():
     import clibs

@@ -1,12 +1,16 @@
 """GPU: the layer-major prefill (every layer over a chunk of prompt tokens with
-batched projections, src/ornith_rforward.c:647-682) against the reference and
-against the token-by-token path (ORNITH_HIP_PREFILL=0).
+batched projections, src/ornith_rforward.c:647-682) in both of the
+reference's prompt modes: ORNITH_PREFILL_SERIAL=1 (token recurrence) against
+the reference and against the token-by-token path (ORNITH_HIP_PREFILL=0), and
+the default chunked delta scan (src/ornith_attn.c:215-349) against the
+reference's golden fixture and the oracle.
 
 Bar: bit-exact prompt logits and 64 greedy tokens on C1 against the
 reference's serial golden fixture; bit-identical logits, tokens and session
-state (delta state, conv window, Q8 KV cache) between the two paths on
-Q4_K/Q6_K models with MoE and dense FFNs, on prompts that span several chunks,
-with odd and even chunk starts, on the exact and flash attention paths."""
+state (delta state, conv window, Q8 KV cache) between the two paths, and
+against the oracle's chunked mode, on Q4_K/Q6_K models with MoE and dense FFNs,
+on prompts that span several chunks, with odd and even chunk starts and
+partial delta chunks, on the exact and flash attention paths."""
 import ctypes as C
 
 import numpy as np
@@ -72,6 +76,54 @@ def evals(m, chunks, cap, prefill, monkeypatch, exact_max):
         s.eval(c)
         logits.append(s.logits().copy())
     return s, logits
+
+
+def oracle_state(orc, os_, arch, layer, pos):
+    """The oracle session's state in the layouts of Session.delta_state/conv_state/kv."""
+    if (layer + 1) % arch["full_interval"]:
+        cc = 2 * arch["nk"] * arch["dk"] + arch["nv"] * arch["dv"]
+        S = np.ctypeslib.as_array(orc.orc_session_delta(os_, layer), (arch["nv"] * arch["dv"] * arch["dk"],))
+        W = np.ctypeslib.as_array(orc.orc_session_conv(os_, layer), ((arch["conv_k"] - 1) * cc,))
+        return S.copy(), W.copy()
+    kv = orc.orc_session_kv(os_, layer).contents
+    n = pos * arch["nkv"] * arch["hd"]
+    return (np.ctypeslib.as_array(kv.Kq, (n,)).copy(), np.ctypeslib.as_array(kv.Ks, (pos * arch["nkv"],)).copy(),
+            np.ctypeslib.as_array(kv.Vq, (n,)).copy(), np.ctypeslib.as_array(kv.Vs, (pos * arch["nkv"],)).copy())
+
+
+@pytest.mark.parametrize("cfg", ["moe", "dense"])
+def test_chunked_mode_matches_oracle(hip_ctx, orc, tmp_path, monkeypatch, cfg):
+    """The reference's default prompt mode over several evaluations: a
+    300-token prompt (two engine chunks, a partial last delta chunk), then
+    7, 1 (a one-token chunk) and 33 tokens; logits after each and the whole
+    session state bit-identical to the oracle's chunked mode."""
+    monkeypatch.setenv("ORNITH_PREFILL_SERIAL", "0")
+    c = MIX if cfg == "moe" else DENSE
+    path = tmp_path / "m.gguf"
+    clibs.write_c1_gguf(path, c)
+    om = C.c_void_p()
+    assert orc.orc_model_load(str(path).encode(), C.byref(om)) == 0
+    orc.orc_model_set_threads(om, 8)
+    os_ = orc.orc_session_new(om, 400, 1)
+    m = hip_ctx.synth(**c)
+    a = m.arch
+    s = m.session(400)
+    rng = np.random.default_rng(6)
+    for n in (300, 7, 1, 33):
+        p = rng.integers(0, a["vocab"], n).astype(np.int32)
+        assert orc.orc_session_eval(os_, i32p(p), n, 0) == 0
+        s.eval(p)
+        want = np.ctypeslib.as_array(orc.orc_session_logits(os_), (a["vocab"],))
+        assert np.array_equal(u32(s.logits()), u32(want)), n
+    for l in range(a["n_layers"]):
+        want = oracle_state(orc, os_, a, l, s.pos)
+        got = (s.delta_state(l), s.conv_state(l)) if (l + 1) % a["full_interval"] else s.kv(l)
+        for x, y in zip(got, want):
+            assert np.array_equal(np.ascontiguousarray(x).view(np.uint8), np.ascontiguousarray(y).view(np.uint8)), l
+    s.free()
+    m.free()
+    orc.orc_session_free(os_)
+    orc.orc_model_free(om)
 
 
 def same_state(m, a, b):
