@@ -6,8 +6,8 @@ Workload: hidden 2048, 40 layers (30 gated delta-net + 10 GQA), 256 experts
 top-8 with FFN 512 + shared expert 512, vocab 248320; every projection Q4_K
 except attn_v / ffn_down_exps / ffn_down_shexp in Q6_K; N(0,0.02) random-init
 weights synthesised in HBM with the repository generator's value streams; a
-4096-token random prompt through the token step fills the Q8 KV cache; then
-greedy decode. A "step" is one token through the whole stack (40 layers +
+4096-token random prompt through the layer-major prefill (the reference's
+default chunked delta scan) fills the Q8 KV cache; then greedy decode. A "step" is one token through the whole stack (40 layers +
 lm_head + argmax), everything resident in HBM, the next token chosen on the
 device.
 
@@ -91,13 +91,15 @@ def bytes_per_token(model: oa.Model, cfg: dict, ctx_len: float) -> dict:
 
 TRAFFIC_COPY_BYTES = 512 << 20
 TRAFFIC_REPS = 2
-TRAFFIC_PROMPT = 16
+TRAFFIC_PROMPT = 1
 
 
 def traffic_probe(kind: str) -> int:
     """Under rocprofv3 --pmc: a device-to-device copy of TRAFFIC_COPY_BYTES
-    (the calibration kernel), then TRAFFIC_REPS back-to-back replays of one
-    decode step's `kind` launches on the C3 model after a 16-token prompt."""
+    (the calibration kernel), then one token step and TRAFFIC_REPS
+    back-to-back replays of one decode step's `kind` launches on the C3 model
+    (so the kernel's dispatches are TRAFFIC_PROMPT + 1 + TRAFFIC_REPS equal
+    passes)."""
     import torch
     a = torch.empty(TRAFFIC_COPY_BYTES // 4, dtype=torch.float32, device="cuda").fill_(1.0)
     b = torch.empty_like(a)
@@ -107,7 +109,8 @@ def traffic_probe(kind: str) -> int:
     ctx = oa.Context(0)
     model = ctx.synth(**C3)
     sess = model.session(64)
-    sess.eval(np.arange(TRAFFIC_PROMPT, dtype=np.int32) * 7919 % C3["vocab"])
+    for i in range(TRAFFIC_PROMPT):
+        sess.step(i * 7919 % C3["vocab"])
     us, bpl, nps = sess.time_kind(kind, reps=TRAFFIC_REPS)
     print(json.dumps({"kind": kind, "launches_per_step": nps, "reps": TRAFFIC_REPS, "us_per_launch": us,
                       "bytes_per_launch": bpl, "copy_bytes": TRAFFIC_COPY_BYTES}), flush=True)
@@ -145,7 +148,7 @@ def traffic_summarize(kind: str, fetch_csv: str, write_csv: str) -> int:
         factor = max(copy) * 1024.0 / TRAFFIC_COPY_BYTES
         out[counter] = dict(copy_kib=max(copy), factor=factor, dispatches=len(kern), kern_kib=kern)
     n = min(out["FETCH_SIZE"]["dispatches"], out["WRITE_SIZE"]["dispatches"])
-    # the probe makes TRAFFIC_PROMPT prompt steps, one warm-up pass and
+    # the probe makes TRAFFIC_PROMPT token steps, one warm-up pass and
     # TRAFFIC_REPS timed passes of the same launches; keep the timed ones
     take = n * TRAFFIC_REPS // (TRAFFIC_PROMPT + 1 + TRAFFIC_REPS)
     tf = ROOT / "profiles" / "traffic.json"
@@ -267,8 +270,8 @@ def cpu_baseline(model: oa.Model, cfg: dict, seconds: float) -> dict:
 # profile kind -> kernel symbol (as rocprofv3 names it)
 KERNEL_SYMBOL = {"matvec": "oh_k_mv_q4k", "matvec_q6k": "oh_k_mv_q6k", "matvec_q80": "oh_k_mv_q80",
                  "matvec_mixed": "oh_k_mv_mixed", "moe_down": "oh_k_mv_down", "delta_step": "oh_k_delta_step",
-                 "attn_out": "oh_k_attn_out", "attn_scores": "oh_k_attn_scores", "attn_flash": "oh_k_attn_flash",
-                 "attn_combine": "oh_k_attn_combine"}
+                 "attn_main": "oh_k_attn_main", "attn_combine": "oh_k_attn_combine", "attn_prep": "oh_k_attn_prep",
+                 "step_body": "oh_k_step", "step_head": "oh_k_step"}
 
 
 def main() -> int:
@@ -308,7 +311,8 @@ def main() -> int:
     t0 = time.perf_counter()
     sess.eval(prompt)
     t_prefill = time.perf_counter() - t0
-    log(f"prompt of {args.ctx} tokens through the token step: {t_prefill:.1f} s ({args.ctx / t_prefill:.0f} tok/s)")
+    log(f"prompt of {args.ctx} tokens through the layer-major prefill: {t_prefill:.2f} s "
+        f"({args.ctx / t_prefill:.0f} tok/s)")
 
     if args.warmup:
         sess.time_decode(args.warmup)
