@@ -442,6 +442,12 @@ extern "C" int ornith_hip_quantize_q8K(ornith_hip_ctx *ctx, const float *x, int6
     return ORNITH_HIP_OK;
 }
 
+// batched Q4_K products on the matrix cores (ORNITH_HIP_MMQ=0: the vector-ALU kernels)
+static bool mmq_enabled() {
+    const char *e = getenv("ORNITH_HIP_MMQ");
+    return !(e && e[0] == '0');
+}
+
 extern "C" int ornith_hip_matvec(ornith_hip_ctx *ctx, const ornith_hip_tensor *W,
                                  const float *x, float *y, int Tn) {
     HCHK(hipSetDevice(ctx->device));
@@ -451,14 +457,26 @@ extern "C" int ornith_hip_matvec(ornith_hip_ctx *ctx, const ornith_hip_tensor *W
     if (q && Tn > 1 && in <= 8192) {
         // Tn columns: each quantised to Q8_K, one batched launch
         const size_t T = (size_t)Tn;
-        CHK(ctx_scratch(ctx, T * in * 5 + T * nb * 40 + T * out * 4 + 4096, &sp));
+        CHK(ctx_scratch(ctx, T * in * 5 + T * nb * 56 + T * out * 4 + 4096, &sp));
         float *dx = (float *)sp;
         float *dy = (float *)up256((size_t)(dx + T * in));
         int8_t *qs = (int8_t *)up256((size_t)(dy + T * out));
         float *dd = (float *)up256((size_t)(qs + T * in));
         int16_t *bs = (int16_t *)up256((size_t)(dd + T * nb + 1));
+        int8_t *bp = (int8_t *)up256((size_t)(bs + T * nb * 16));
         HCHK(hipMemcpyAsync(dx, x, T * in * 4, hipMemcpyHostToDevice, ctx->st));
-        HCHK(oh_launch_norm_q8k_rows(dx, nullptr, 0.0f, (int)in, Tn, nullptr, qs, dd, bs, ctx->st));
+        HCHK(oh_launch_norm_q8k_rows(dx, nullptr, 0.0f, (int)in, Tn, nullptr, qs, dd, bs, ctx->st, bp));
+        if (mmq_enabled() && oh_mmq_can(W->type, (int)out, (int)in)) {
+            oh_mmq M;
+            memset(&M, 0, sizeof M);
+            M.A = W->A; M.B = W->B;
+            M.xqs = qs; M.xd = dd; M.xbp = bp; M.y = dy;
+            M.nb = (int)nb; M.in = (int)in; M.rows = (int)out; M.ncol = Tn; M.adiv = 1; M.ystride = (int)out;
+            HCHK(oh_launch_mmq(&M, 0, 0, ctx->st));
+            HCHK(hipMemcpyAsync(y, dy, T * out * 4, hipMemcpyDeviceToHost, ctx->st));
+            HCHK(hipStreamSynchronize(ctx->st));
+            return ORNITH_HIP_OK;
+        }
         oh_mvbatch B;
         memset(&B, 0, sizeof B);
         B.A = W->A; B.B = W->B; B.C = W->C;
@@ -907,7 +925,9 @@ extern "C" int ornith_hip_model_tensor_info(const ornith_hip_model *m, const cha
 }
 
 // ---- sessions -----------------------------------------------------------------------------
-struct Q8Buf { int8_t *qs = nullptr; float *d = nullptr; int16_t *bs = nullptr; };
+// Q8_K planes; bp: per super-block the pair-sum bytes of the matrix-core
+// product's min term
+struct Q8Buf { int8_t *qs = nullptr; float *d = nullptr; int16_t *bs = nullptr; int8_t *bp = nullptr; };
 
 struct LayerState {
     float *S = nullptr, *conv = nullptr;                 // linear
@@ -969,6 +989,8 @@ struct ornith_hip_session {
         float *FPO = nullptr, *FPML = nullptr, *RL = nullptr, *SHL = nullptr, *SHG = nullptr, *RW = nullptr;
         int32_t *RIDX = nullptr, *CNT = nullptr, *LIST = nullptr;
         float *Hh = nullptr, *HSH = nullptr, *OD = nullptr, *ODSH = nullptr, *STAGE = nullptr, *GR = nullptr;
+        float *GU = nullptr, *GSH = nullptr;      // [gate | up] rows of the matrix-core pairs
+        int32_t *ITEMS = nullptr;
         Q8Buf XQ, OQ, OAQ, HQ, HSQ;
     } pf;
     std::vector<int> sp_body_rk;
@@ -1078,6 +1100,7 @@ static int q8alloc(ornith_hip_session *s, Q8Buf &q, size_t n) {
     CHK(salloc(s, &q.qs, n));
     CHK(salloc(s, &q.d, n / 256 + 1));
     CHK(salloc(s, &q.bs, n / 16 + 16));
+    CHK(salloc(s, &q.bp, n / 16 + 16));
     return ORNITH_HIP_OK;
 }
 static Act act_of(const Q8Buf &q, const float *xf) {
@@ -1618,6 +1641,8 @@ static int pf_alloc(ornith_hip_session *s, int tc) {
     CHK(salloc(s, &p.Hh, T * K * I)); CHK(q8alloc(s, p.HQ, T * K * I + 256));
     CHK(salloc(s, &p.HSH, T * sI)); CHK(q8alloc(s, p.HSQ, T * sI + 256));
     CHK(salloc(s, &p.OD, T * K * H)); CHK(salloc(s, &p.ODSH, T * H));
+    CHK(salloc(s, &p.GU, T * K * 2 * I)); CHK(salloc(s, &p.GSH, T * 2 * sI));
+    CHK(salloc(s, &p.ITEMS, (T * K + 63) / 64 + ne + 2));
     p.tc = tc;
     return ORNITH_HIP_OK;
 }
@@ -1639,6 +1664,51 @@ static int pf_mvb(const ornith_hip_tensor *W, const ornith_hip_tensor *W2, const
     return ORNITH_HIP_OK;
 }
 
+// Q4_K projections with whole 128-row tiles run on the matrix cores
+static bool pf_use_mmq(const ornith_hip_tensor *W, bool grouped) {
+    const int rows = grouped ? (int)W->dims[1] : (int)W->rows;
+    return mmq_enabled() && oh_mmq_can(W->type, rows, (int)W->in);
+}
+
+static int pf_mmq(const ornith_hip_tensor *W, const ornith_hip_tensor *W2, const Q8Buf &x, float *y, int ystride,
+                  int T, int mode, hipStream_t st, const int32_t *cnt = nullptr, const int32_t *list = nullptr,
+                  int lstride = 0, int adiv = 1, const int32_t *items = nullptr, int max_items = 0) {
+    oh_mmq M;
+    memset(&M, 0, sizeof M);
+    M.A = W->A; M.B = W->B;
+    if (W2) { M.A2 = W2->A; M.B2 = W2->B; }
+    M.xqs = x.qs; M.xd = x.d; M.xbp = x.bp; M.y = y;
+    M.cnt = cnt; M.list = list; M.items = items;
+    M.nb = (int)(W->in / 256); M.in = (int)W->in; M.rows = list ? (int)W->dims[1] : (int)W->rows;
+    M.mode = mode; M.ncol = T; M.lstride = lstride; M.adiv = adiv; M.ystride = ystride;
+    HCHK(oh_launch_mmq(&M, max_items, W2 != nullptr, st));
+    return ORNITH_HIP_OK;
+}
+
+// y (+)= W . x over T dense columns
+static int pf_mm(const ornith_hip_tensor *W, const Q8Buf &x, float *y, int ystride, int T, int mode,
+                 hipStream_t st) {
+    if (pf_use_mmq(W, false)) return pf_mmq(W, nullptr, x, y, ystride, T, mode, st);
+    return pf_mvb(W, nullptr, x, y, ystride, T, mode, st);
+}
+
+// h = silu(Wg . x) * (Wu . x) for `npairs` output rows (T dense columns, or the
+// grouped expert pairs), quantised to Q8_K in hq
+static int pf_swiglu(const ornith_hip_tensor *Wg, const ornith_hip_tensor *Wu, const Q8Buf &x, int I, int npairs,
+                     int T, Q8Buf &hq, float *gu, float *hbuf, hipStream_t st, const int32_t *cnt = nullptr,
+                     const int32_t *list = nullptr, int lstride = 0, int adiv = 1, int groups = 1,
+                     const int32_t *items = nullptr, int max_items = 0) {
+    const bool grouped = list != nullptr;
+    if (pf_use_mmq(Wg, grouped) && pf_use_mmq(Wu, grouped)) {
+        CHK(pf_mmq(Wg, Wu, x, gu, 2 * I, T, 0, st, cnt, list, lstride, adiv, items, max_items));
+        HCHK(oh_launch_norm_q8k_rows(gu, nullptr, 0.0f, I, npairs, nullptr, hq.qs, hq.d, hq.bs, st, hq.bp, 1));
+    } else {
+        CHK(pf_mvb(Wg, Wu, x, hbuf, I, T, 0, st, cnt, list, lstride, adiv, groups));
+        HCHK(oh_launch_norm_q8k_rows(hbuf, nullptr, 0.0f, I, npairs, nullptr, hq.qs, hq.d, hq.bs, st, hq.bp));
+    }
+    return ORNITH_HIP_OK;
+}
+
 static int pf_chunk(ornith_hip_session *s, int base, int T, bool chunked, hipStream_t st) {
     const ornith_hip_model *m = s->m;
     const ornith_hip_arch &a = m->a;
@@ -1651,11 +1721,11 @@ static int pf_chunk(ornith_hip_session *s, int base, int T, bool chunked, hipStr
         const OhLayer &y = m->L[l];
         LayerState &z = s->ls[l];
         HCHK(oh_launch_norm_q8k_rows(p.X, (const float *)y.attn_norm->A, a.eps, H, T, nullptr, p.XQ.qs, p.XQ.d,
-                                     p.XQ.bs, st));
+                                     p.XQ.bs, st, p.XQ.bp));
         if (y.full) {
-            CHK(pf_mvb(y.q, nullptr, p.XQ, p.QP, 2 * aq, T, 0, st));
-            CHK(pf_mvb(y.k, nullptr, p.XQ, p.KB, kvd, T, 0, st));
-            CHK(pf_mvb(y.v, nullptr, p.XQ, p.VB, kvd, T, 0, st));
+            CHK(pf_mm(y.q, p.XQ, p.QP, 2 * aq, T, 0, st));
+            CHK(pf_mm(y.k, p.XQ, p.KB, kvd, T, 0, st));
+            CHK(pf_mm(y.v, p.XQ, p.VB, kvd, T, 0, st));
             oh_op_prep pr = {p.QP, p.KB, p.VB, (const float *)y.q_norm->A, (const float *)y.k_norm->A,
                              (const float *)s->rope, p.QR, p.AG, z.Kt, z.Ks, z.Vq, z.Vs,
                              a.nh, a.nkv, a.hd, a.rope_dim, s->kvcap, a.eps};
@@ -1673,13 +1743,14 @@ static int pf_chunk(ornith_hip_session *s, int base, int T, bool chunked, hipStr
             for (int t0 = 0; t0 < T; t0 += kPfAttnSub)
                 HCHK(oh_launch_attn_rows(&at, nv_ex > nv_fl ? nv_ex : nv_fl, lds_ex > lds_fl ? lds_ex : lds_fl, base,
                                          t0, T - t0 < kPfAttnSub ? T - t0 : kPfAttnSub, po, pml, st));
-            HCHK(oh_launch_norm_q8k_rows(p.OA, nullptr, 0.0f, aq, T, nullptr, p.OAQ.qs, p.OAQ.d, p.OAQ.bs, st));
-            CHK(pf_mvb(y.o, nullptr, p.OAQ, p.X, H, T, 1, st));
+            HCHK(oh_launch_norm_q8k_rows(p.OA, nullptr, 0.0f, aq, T, nullptr, p.OAQ.qs, p.OAQ.d, p.OAQ.bs, st,
+                                         p.OAQ.bp));
+            CHK(pf_mm(y.o, p.OAQ, p.X, H, T, 1, st));
         } else {
-            CHK(pf_mvb(y.qkv, nullptr, p.XQ, p.CAT, cc, T, 0, st));
-            CHK(pf_mvb(y.gate, nullptr, p.XQ, p.Z, vd, T, 0, st));
-            CHK(pf_mvb(y.alpha, nullptr, p.XQ, p.A, a.nv, T, 0, st));
-            CHK(pf_mvb(y.beta, nullptr, p.XQ, p.Bg, a.nv, T, 0, st));
+            CHK(pf_mm(y.qkv, p.XQ, p.CAT, cc, T, 0, st));
+            CHK(pf_mm(y.gate, p.XQ, p.Z, vd, T, 0, st));
+            CHK(pf_mm(y.alpha, p.XQ, p.A, a.nv, T, 0, st));
+            CHK(pf_mm(y.beta, p.XQ, p.Bg, a.nv, T, 0, st));
             HCHK(oh_launch_conv_rows(p.CAT, (const float *)y.conv->A, z.conv, p.CONV, p.STAGE, T, base, cc, a.conv_k, st));
             HCHK(oh_launch_qk_gates_rows(a.dk, p.CONV, p.A, p.Bg, (const float *)y.ssm_a->A,
                                          (const float *)y.dt_bias->A, p.QN, p.KN, p.AL, p.BE, T, a.nk, a.nv, cc, st));
@@ -1690,33 +1761,36 @@ static int pf_chunk(ornith_hip_session *s, int base, int T, bool chunked, hipStr
                 HCHK(oh_launch_delta_scan(a.dk, p.QN, p.KN, p.CONV, p.AL, p.BE, p.Z, z.S, p.O, p.OG, p.RUNS, T, a.nk,
                                           a.nv, cc, 1.0f / sqrtf((float)a.dk), st));
             HCHK(oh_launch_gnorm_q8k_rows(p.O, p.OG, p.RUNS, (const float *)y.ssm_norm->A, a.eps, vd, a.dv, T,
-                                          p.OQ.qs, p.OQ.d, p.OQ.bs, st));
-            CHK(pf_mvb(y.ssm_out, nullptr, p.OQ, p.X, H, T, 1, st));
+                                          p.OQ.qs, p.OQ.d, p.OQ.bs, st, p.OQ.bp));
+            CHK(pf_mm(y.ssm_out, p.OQ, p.X, H, T, 1, st));
         }
         HCHK(oh_launch_norm_q8k_rows(p.X, (const float *)y.post_norm->A, a.eps, H, T, nullptr, p.XQ.qs, p.XQ.d,
-                                     p.XQ.bs, st));
+                                     p.XQ.bs, st, p.XQ.bp));
         if (a.ne > 0) {
             const int K = a.top_k, I = a.moe_inter, sI = a.shared_inter;
-            CHK(pf_mvb(y.router, nullptr, p.XQ, p.RL, a.ne, T, 0, st));
-            if (y.gate_inp_sh) CHK(pf_mvb(y.gate_inp_sh, nullptr, p.XQ, p.SHL, 1, T, 0, st));
+            CHK(pf_mm(y.router, p.XQ, p.RL, a.ne, T, 0, st));
+            if (y.gate_inp_sh) CHK(pf_mm(y.gate_inp_sh, p.XQ, p.SHL, 1, T, 0, st));
             HCHK(oh_launch_route_rows(p.RL, a.ne, K, y.gate_inp_sh ? p.SHL : nullptr, p.RIDX, p.RW,
                                       y.gate_inp_sh ? p.SHG : nullptr, T, st));
             HCHK(oh_launch_group_pairs(p.RIDX, T * K, p.CNT, a.ne, p.LIST, T, st));
-            CHK(pf_mvb(y.gate_exps, y.up_exps, p.XQ, p.Hh, I, T, 0, st, p.CNT, p.LIST, T, K, a.ne));
-            HCHK(oh_launch_norm_q8k_rows(p.Hh, nullptr, 0.0f, I, T * K, nullptr, p.HQ.qs, p.HQ.d, p.HQ.bs, st));
-            CHK(pf_mvb(y.down_exps, nullptr, p.HQ, p.OD, H, T, 0, st, p.CNT, p.LIST, T, 1, a.ne));
+            const int max_items = (T * K + 63) / 64 + a.ne;
+            HCHK(oh_launch_mmq_items(p.CNT, a.ne, p.ITEMS, st));
+            CHK(pf_swiglu(y.gate_exps, y.up_exps, p.XQ, I, T * K, T, p.HQ, p.GU, p.Hh, st, p.CNT, p.LIST, T, K, a.ne,
+                          p.ITEMS, max_items));
+            if (pf_use_mmq(y.down_exps, true))
+                CHK(pf_mmq(y.down_exps, nullptr, p.HQ, p.OD, H, T, 0, st, p.CNT, p.LIST, T, 1, p.ITEMS, max_items));
+            else
+                CHK(pf_mvb(y.down_exps, nullptr, p.HQ, p.OD, H, T, 0, st, p.CNT, p.LIST, T, 1, a.ne));
             if (y.gate_sh) {
-                CHK(pf_mvb(y.gate_sh, y.up_sh, p.XQ, p.HSH, sI, T, 0, st));
-                HCHK(oh_launch_norm_q8k_rows(p.HSH, nullptr, 0.0f, sI, T, nullptr, p.HSQ.qs, p.HSQ.d, p.HSQ.bs, st));
-                CHK(pf_mvb(y.down_sh, nullptr, p.HSQ, p.ODSH, H, T, 0, st));
+                CHK(pf_swiglu(y.gate_sh, y.up_sh, p.XQ, sI, T, T, p.HSQ, p.GSH, p.HSH, st));
+                CHK(pf_mm(y.down_sh, p.HSQ, p.ODSH, H, T, 0, st));
             }
             HCHK(oh_launch_moe_combine_rows(p.X, p.OD, p.RW, K, H, y.gate_sh ? p.ODSH : nullptr,
                                             y.gate_inp_sh ? p.SHG : nullptr, T, st));
         } else {
             const int I = a.shared_inter;
-            CHK(pf_mvb(y.ffn_gate, y.ffn_up, p.XQ, p.HSH, I, T, 0, st));
-            HCHK(oh_launch_norm_q8k_rows(p.HSH, nullptr, 0.0f, I, T, nullptr, p.HSQ.qs, p.HSQ.d, p.HSQ.bs, st));
-            CHK(pf_mvb(y.ffn_down, nullptr, p.HSQ, p.X, H, T, 1, st));
+            CHK(pf_swiglu(y.ffn_gate, y.ffn_up, p.XQ, I, T, T, p.HSQ, p.GSH, p.HSH, st));
+            CHK(pf_mm(y.ffn_down, p.HSQ, p.X, H, T, 1, st));
         }
     }
     // the last token's hidden state feeds the head

@@ -5,6 +5,7 @@
 #include "oh_synth.hip"
 #include "oh_step.hip"
 #include "oh_prefill.hip"
+#include "oh_mmq.hip"
 #include "oh_launch.h"
 
 extern "C" {
@@ -31,9 +32,10 @@ int oh_mvb_tcol(int nb) {
 }
 
 hipError_t oh_launch_norm_q8k_rows(const float *x, const float *norm_w, float eps, int n, int rows, float *xn_out,
-                                   int8_t *qs, float *d, int16_t *bs, hipStream_t st) {
+                                   int8_t *qs, float *d, int16_t *bs, hipStream_t st, int8_t *bp, int swiglu) {
     if (rows <= 0) return hipSuccess;
-    hipLaunchKernelGGL(oh_k_norm_q8k_rows, dim3(rows), dim3(256), 0, st, x, norm_w, eps, n, xn_out, qs, d, bs);
+    hipLaunchKernelGGL(oh_k_norm_q8k_rows, dim3(rows), dim3(256), 0, st, x, norm_w, eps, n, xn_out, qs, d, bs, bp,
+                       swiglu);
     return hipGetLastError();
 }
 
@@ -90,9 +92,31 @@ hipError_t oh_launch_delta_chunked(int dk, const float *qn, const float *kn, con
     }
     return hipGetLastError();
 }
+bool oh_mmq_can(uint32_t type, int rows, int in) {
+    return type == OH_Q4_K && rows > 0 && rows % kMqRows == 0 && in % 256 == 0 && in > 0;
+}
+hipError_t oh_launch_mmq(const oh_mmq *M, int max_items, int pair, hipStream_t st) {
+    const int ty = M->list ? max_items : (M->ncol + kMqCols - 1) / kMqCols;
+    if (ty <= 0) return hipSuccess;
+    static bool lds_set = false;   // two stages exceed the default dynamic LDS limit
+    if (!lds_set) {
+        const hipError_t e = hipFuncSetAttribute((const void *)oh_k_mmq_q4k,
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, 2 * kMqStage);
+        if (e != hipSuccess) return e;
+        lds_set = true;
+    }
+    hipLaunchKernelGGL(oh_k_mmq_q4k, dim3(M->rows / kMqRows, ty, pair ? 2 : 1), dim3(256), 2 * kMqStage, st, *M);
+    return hipGetLastError();
+}
+hipError_t oh_launch_mmq_items(const int32_t *cnt, int ne, int32_t *items, hipStream_t st) {
+    if (ne > 1024) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(oh_k_mmq_items, dim3(1), dim3(256), 0, st, cnt, ne, items);
+    return hipGetLastError();
+}
 hipError_t oh_launch_gnorm_q8k_rows(const float *x, const float *sz, const double *runs, const float *w, float eps,
-                                    int n, int gdim, int T, int8_t *qs, float *d, int16_t *bs, hipStream_t st) {
-    hipLaunchKernelGGL(oh_k_gnorm_q8k_rows, dim3(T), dim3(256), 0, st, x, sz, runs, w, eps, n, gdim, qs, d, bs);
+                                    int n, int gdim, int T, int8_t *qs, float *d, int16_t *bs, hipStream_t st,
+                                    int8_t *bp) {
+    hipLaunchKernelGGL(oh_k_gnorm_q8k_rows, dim3(T), dim3(256), 0, st, x, sz, runs, w, eps, n, gdim, qs, d, bs, bp);
     return hipGetLastError();
 }
 hipError_t oh_launch_prep_rows(const oh_op_prep *a, int base, int T, hipStream_t st) {

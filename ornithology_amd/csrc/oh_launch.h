@@ -13,8 +13,11 @@ hipError_t oh_launch_matvec(const oh_mvlaunch *L, int tk, int lds_bytes, hipStre
 hipError_t oh_launch_mvb(const oh_mvbatch *B, int groups, hipStream_t st);
 int oh_mvb_tcol(int nb);
 // RMSNorm (norm_w non-null) + Q8_K of `rows` vectors of n <= 8192 elements
+// bp: also the Q8_K pair-sum bytes (the matrix-core product's min term);
+// swiglu: x holds rows of [gate | up] (2n) and the vector is silu(gate) * up
 hipError_t oh_launch_norm_q8k_rows(const float *x, const float *norm_w, float eps, int n, int rows, float *xn_out,
-                                   int8_t *qs, float *d, int16_t *bs, hipStream_t st);
+                                   int8_t *qs, float *d, int16_t *bs, hipStream_t st, int8_t *bp = nullptr,
+                                   int swiglu = 0);
 // prefill (layer-major over T tokens)
 hipError_t oh_launch_embed_rows(const oh_op_embed *a, int base, int T, hipStream_t st);
 hipError_t oh_launch_conv_rows(const float *cat, const float *conv_w, float *conv_state, float *out, float *stage,
@@ -32,7 +35,14 @@ hipError_t oh_launch_delta_chunked(int dk, const float *qn, const float *kn, con
                                    float *out_gate, double *out_runs, int T, int nk, int nv, int cc, float out_scale,
                                    hipStream_t st);
 hipError_t oh_launch_gnorm_q8k_rows(const float *x, const float *sz, const double *runs, const float *w, float eps,
-                                    int n, int gdim, int T, int8_t *qs, float *d, int16_t *bs, hipStream_t st);
+                                    int n, int gdim, int T, int8_t *qs, float *d, int16_t *bs, hipStream_t st,
+                                    int8_t *bp = nullptr);
+// Q4_K x Q8_K products on the matrix cores: rows % 128 == 0; dense (ncol
+// columns) or grouped (items from oh_launch_mmq_items, at most max_items);
+// pair: a second weight set (A2/B2) for rows [rows, 2 rows)
+hipError_t oh_launch_mmq(const oh_mmq *M, int max_items, int pair, hipStream_t st);
+hipError_t oh_launch_mmq_items(const int32_t *cnt, int ne, int32_t *items, hipStream_t st);
+bool oh_mmq_can(uint32_t type, int rows, int in);
 hipError_t oh_launch_prep_rows(const oh_op_prep *a, int base, int T, hipStream_t st);
 hipError_t oh_launch_attn_rows(const oh_op_attn *a, int nvb_main, int lds, int base, int t0, int n, size_t po_stride,
                                size_t pml_stride, hipStream_t st);

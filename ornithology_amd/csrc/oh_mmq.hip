@@ -1,0 +1,227 @@
+// Exact batched Q4_K x Q8_K products on the matrix cores (prompt path).
+//
+// Y[p][row] = vec_dot_q4_K(W[row], X[p / adiv]) for every (row, column p), with
+// the reference's arithmetic (src/ornith_qdot.c:76-105): per super-block i the
+// integer sums isum = sum_j sc_j * sum_l q4 * q8 and summs = sum_j m_j *
+// (bsums_2j + bsums_2j+1), then sumf += d * (float)isum + dm * (float)summs in
+// super-block order, d = yd * f16(d), dm = -yd * f16(dmin).
+//
+// The integer sums run on v_mfma_i32_32x32x32_i8. Each 6-bit sub-block scale
+// splits as sc = 8 * hi + lo (hi, lo < 8), so q4 * lo and q4 * hi (at most
+// 105) stay int8 and a whole super-block accumulates exactly in int32:
+// isum = 8 * (q4*hi . q8) + (q4*lo . q8). The min term is a K = 8 product of
+// the 6-bit mins with the Q8_K pair sums, which split as 64 * bh + bl into
+// int8 bytes (the activation quantiser emits them). Integer sums are exact in
+// any order, so only the float combine needs the reference's order, and it is
+// done per (row, column, super-block) exactly as the scalar dot does it.
+//
+// Block: 256 threads, a tile of 128 rows x 64 columns; wave w owns rows
+// [32w, 32w + 32) and both 32-column halves. One super-block per stage; the
+// stage's operands go global -> LDS with global_load_lds (no registers), two
+// stages in flight. LDS layouts are piece-major so that the 32 lanes of an
+// MFMA operand read consecutive 16-byte chunks.
+
+typedef int mq_v4i __attribute__((ext_vector_type(4)));
+typedef int mq_v16i __attribute__((ext_vector_type(16)));
+typedef __attribute__((address_space(3))) void mq_lds_t;
+
+constexpr int kMqRows = 128, kMqCols = 64;
+constexpr int kMqA = 0;                         // codes [8 pieces][128 rows][16 B]
+constexpr int kMqB = kMqA + 8 * 128 * 16;       // activation codes [16 pieces][64 cols][16 B]
+constexpr int kMqH = kMqB + 16 * 64 * 16;       // weight headers [4 dwords][128 rows]
+constexpr int kMqP = kMqH + 4 * 128 * 4;        // pair-sum bytes [64 cols][16 B]
+constexpr int kMqD = kMqP + 64 * 16;            // activation d [64 cols]
+constexpr int kMqStage = kMqD + 64 * 4;         // 36096 B
+constexpr int kMqLoads = 16 + 16 + 8 + 1 + 1;   // wave-loads per stage
+
+namespace {
+
+OH_DEV void mq_load16(const void *g, uint8_t *lds) {
+    __builtin_amdgcn_global_load_lds(g, (mq_lds_t *)lds, 16, 0, 0);
+}
+OH_DEV void mq_load4(const void *g, uint8_t *lds) {
+    __builtin_amdgcn_global_load_lds(g, (mq_lds_t *)lds, 4, 0, 0);
+}
+
+// wave-load L of super-block i into stage S; lane-dependent global address,
+// wave-uniform LDS base (lane k writes 16 B, or 4 B, at base + k * size)
+OH_DEV void mq_stage_load(const oh_mmq &M, const uint8_t *A, const uint8_t *Bh, int64_t rbase, int R0, int i,
+                          uint8_t *S, int L, int lane, int acol) {
+    const int nb = M.nb;
+    if (L < 16) {                                   // codes: piece p, rows rh*64 + lane
+        const int p = L >> 1, rh = L & 1;
+        const int64_t bi = (rbase + R0 + rh * 64 + lane) * nb + i;
+        const uint4 *src = (const uint4 *)(A + (bi >> 6) * (int64_t)(64 * 128)) + (bi & 63) + p * 64;
+        mq_load16(src, S + kMqA + (p * 128 + rh * 64) * 16);
+    } else if (L < 32) {                            // activation codes: piece q, column lane
+        const int q = L - 16;
+        mq_load16(M.xqs + (size_t)acol * M.in + (size_t)i * 256 + q * 16, S + kMqB + q * 64 * 16);
+    } else if (L < 40) {                            // header dword f of rows rh*64 + lane
+        const int f = (L - 32) >> 1, rh = (L - 32) & 1;
+        const int64_t bi = (rbase + R0 + rh * 64 + lane) * nb + i;
+        mq_load4(Bh + bi * 16 + f * 4, S + kMqH + (f * 128 + rh * 64) * 4);
+    } else if (L == 40) {                           // pair-sum bytes of column lane
+        mq_load16(M.xbp + ((size_t)acol * nb + i) * 16, S + kMqP);
+    } else {                                        // activation d of column lane
+        mq_load4(M.xd + (size_t)acol * nb + i, S + kMqD);
+    }
+}
+
+} // namespace
+
+extern "C" __global__ void __launch_bounds__(256, 2) oh_k_mmq_q4k(oh_mmq M) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ int sact[kMqCols], sout[kMqCols];
+    const int tid = tid_x(), lane = lane_id();
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int zi = (int)blockIdx.z;
+    int g = 0, tile = (int)blockIdx.y, n;
+    if (M.list) {
+        if ((int)blockIdx.y >= ldg(M.items)) return;
+        const int it = ldg(M.items + 1 + blockIdx.y);
+        g = it >> 16;
+        tile = it & 0xffff;
+        n = ldg(M.cnt + g) - tile * kMqCols;
+    } else {
+        n = M.ncol - tile * kMqCols;
+    }
+    n = n < kMqCols ? n : kMqCols;
+    if (n <= 0) return;
+    const int R0 = (int)blockIdx.x * kMqRows;
+    const uint8_t *A = zi ? M.A2 : M.A, *Bh = zi ? M.B2 : M.B;
+    const int64_t rbase = M.list ? (int64_t)g * M.rows : 0;
+    if (tid < kMqCols) {
+        const int c = tid < n ? tid : n - 1;
+        const int p = M.list ? ldg(M.list + (size_t)g * M.lstride + tile * kMqCols + c) : tile * kMqCols + c;
+        sact[tid] = p / M.adiv;
+        sout[tid] = p;
+    }
+    __syncthreads();
+    const int acol = sact[lane];                    // this lane's column in activation loads
+    auto stage = [&](int i, int buf) {
+        uint8_t *S = smem + buf * kMqStage;
+        for (int L = wave; L < kMqLoads; L += 4) mq_stage_load(M, A, Bh, rbase, R0, i, S, L, lane, acol);
+    };
+
+    const int h = lane >> 5, lr = lane & 31, arow = 32 * wave + lr;
+    const uint32_t NM = 0x0f0f0f0fu;
+    float acc[2][16];
+#pragma unroll
+    for (int t = 0; t < 2; t++)
+#pragma unroll
+        for (int v = 0; v < 16; v++) acc[t][v] = 0.0f;
+
+    const int nb = M.nb;
+    stage(0, 0);
+    for (int i = 0; i < nb; i++) {
+        const int buf = i & 1;
+        if (i + 1 < nb) {
+            stage(i + 1, buf ^ 1);
+            // this wave's loads of stage i are the older ones; every wave
+            // issued at least 10 for stage i + 1
+            asm volatile("s_waitcnt vmcnt(10)" ::: "memory");
+        } else {
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        }
+        __syncthreads();
+        const uint8_t *S = smem + buf * kMqStage;
+        const uint32_t *H = (const uint32_t *)(S + kMqH);
+        // scales and mins of this lane's A row (sb_term's unpacking of scales[12])
+        const uint32_t hy = H[128 + arow], hz = H[256 + arow], hw = H[384 + arow];
+        const uint32_t scl = hy & 0x3f3f3f3fu, sch = (hw & 0x0f0f0f0fu) | ((hy >> 2) & 0x30303030u);
+        const uint32_t mnl = hz & 0x3f3f3f3fu, mnh = ((hw >> 4) & 0x0f0f0f0fu) | ((hz >> 2) & 0x30303030u);
+        mq_v16i ihi[2], ilo[2];
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) { ihi[t][v] = 0; ilo[t][v] = 0; }
+#pragma unroll
+        for (int m = 0; m < 4; m++) {
+            // piece 2m + h holds elements 16h.. of sub-blocks 2m (low nibbles)
+            // and 2m + 1 (high nibbles)
+            const uint4 wq = *(const uint4 *)(S + kMqA + ((2 * m + h) * 128 + arow) * 16);
+#pragma unroll
+            for (int e = 0; e < 2; e++) {
+                const int s = 2 * m + e;
+                const uint32_t sc = ((s < 4 ? scl : sch) >> (8 * (s & 3))) & 0xffu;
+                const uint32_t lo = sc & 7u, hi = sc >> 3;
+                const uint32_t n0 = (e ? wq.x >> 4 : wq.x) & NM, n1 = (e ? wq.y >> 4 : wq.y) & NM;
+                const uint32_t n2 = (e ? wq.z >> 4 : wq.z) & NM, n3 = (e ? wq.w >> 4 : wq.w) & NM;
+                // bytes of at most 15 * 7: no carry between the packed bytes
+                const mq_v4i alo = {(int)(n0 * lo), (int)(n1 * lo), (int)(n2 * lo), (int)(n3 * lo)};
+                const mq_v4i ahi = {(int)(n0 * hi), (int)(n1 * hi), (int)(n2 * hi), (int)(n3 * hi)};
+#pragma unroll
+                for (int t = 0; t < 2; t++) {
+                    const mq_v4i xb = *(const mq_v4i *)(S + kMqB + ((2 * s + h) * 64 + 32 * t + lr) * 16);
+                    ihi[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ahi, xb, ihi[t], 0, 0, 0);
+                    ilo[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(alo, xb, ilo[t], 0, 0, 0);
+                }
+            }
+        }
+        // mins: K = 8 (bytes 0..7 of the lanes of the first half), the rest zero
+        const mq_v4i am = h ? mq_v4i{0, 0, 0, 0} : mq_v4i{(int)mnl, (int)mnh, 0, 0};
+        mq_v16i shi[2], slo[2];
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            const uint4 bp = *(const uint4 *)(S + kMqP + (32 * t + lr) * 16);
+            const mq_v4i bl = h ? mq_v4i{0, 0, 0, 0} : mq_v4i{(int)bp.x, (int)bp.y, 0, 0};
+            const mq_v4i bh = h ? mq_v4i{0, 0, 0, 0} : mq_v4i{(int)bp.z, (int)bp.w, 0, 0};
+            mq_v16i zero;
+#pragma unroll
+            for (int v = 0; v < 16; v++) zero[v] = 0;
+            shi[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(am, bh, zero, 0, 0, 0);
+            slo[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(am, bl, zero, 0, 0, 0);
+        }
+        // float combine: output (row 8*(v/4) + 4h + v%4, column lr) of each
+        // 32x32 tile, per super-block in order
+        const float *XD = (const float *)(S + kMqD);
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            const float yd = XD[32 * t + lr], nyd = -yd;
+#pragma unroll
+            for (int vg = 0; vg < 4; vg++) {
+                const uint4 dd = *(const uint4 *)(H + 32 * wave + 8 * vg + 4 * h);
+                const uint32_t dw[4] = {dd.x, dd.y, dd.z, dd.w};
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    const int v = 4 * vg + k;
+                    const float d = yd * h2f((uint16_t)(dw[k] & 0xffffu));
+                    const float dm = nyd * h2f((uint16_t)(dw[k] >> 16));
+                    const int isum = (ihi[t][v] << 3) + ilo[t][v];
+                    const int summs = (shi[t][v] << 6) + slo[t][v];
+                    acc[t][v] += d * (float)isum + dm * (float)summs;
+                }
+            }
+        }
+        __syncthreads();                            // stage buf is refilled next iteration
+    }
+    const size_t zoff = (size_t)zi * M.rows;
+#pragma unroll
+    for (int t = 0; t < 2; t++) {
+        const int col = 32 * t + lr;
+        if (col >= n) continue;
+        float *yc = M.y + (size_t)sout[col] * M.ystride + zoff + R0 + 32 * wave + 4 * h;
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+            float *yp = yc + 8 * (v / 4) + (v % 4);
+            if (M.mode == 1) stg(yp, ldg(yp) + acc[t][v]);
+            else stg(yp, acc[t][v]);
+        }
+    }
+}
+
+// Work items of a grouped product: (group, 64-column tile) pairs, packed as
+// g << 16 | tile after the count in items[0]. One block of 256 threads.
+extern "C" __global__ void __launch_bounds__(256) oh_k_mmq_items(const int32_t *cnt, int ne, int32_t *items) {
+    __shared__ int pre[1025];
+    const int tid = tid_x();
+    for (int g = tid; g < ne; g += 256) pre[g + 1] = (ldg(cnt + g) + kMqCols - 1) / kMqCols;
+    if (tid == 0) pre[0] = 0;
+    __syncthreads();
+    if (tid == 0)
+        for (int g = 0; g < ne; g++) pre[g + 1] += pre[g];
+    __syncthreads();
+    for (int g = tid; g < ne; g += 256)
+        for (int k = pre[g]; k < pre[g + 1]; k++) stg(items + 1 + k, (g << 16) | (k - pre[g]));
+    if (tid == 0) stg(items, pre[ne]);
+}

@@ -67,7 +67,7 @@ OH_DEV int group_isum(int v) {     // exact sum over the 8 lanes of a group
 // other workgroups (device-scope stores); otherwise LDS.
 template <bool G = false>
 OH_DEV void q8k_block_from_lds(const float *v, int qb, int8_t *qs, float *d, int16_t *bs,
-                               int qstride = 256) {
+                               int qstride = 256, int8_t *bp = nullptr) {
     const int lane = lane_id();
     const float *xb = v + qb * 256;
     float a[4];
@@ -88,6 +88,7 @@ OH_DEV void q8k_block_from_lds(const float *v, int qb, int8_t *qs, float *d, int
 #pragma unroll
         for (int k = 0; k < 4; k++) put8(q + lane + 64 * k, (int8_t)0);
         if (lane < 16) put16(b + lane, (int16_t)0);
+        if (bp && lane < 16) bp[(int64_t)qb * 16 + lane] = 0;
         if (lane == 0) putf(d + qb, 0.0f);
         return;
     }
@@ -101,6 +102,15 @@ OH_DEV void q8k_block_from_lds(const float *v, int qb, int8_t *qs, float *d, int
         put8(q + e, (int8_t)c);
         const int sv = row16_sum_i(c);                 // codes 64k + 16g .. +15
         if ((lane & 15) == 0) put16(b + 4 * k + (lane >> 4), (int16_t)sv);
+        if (bp) {
+            // pair sums bsums_2j + bsums_2j+1 (j = 2k + lane/32) as 64 * bh + bl
+            const int ps = sv + shfl(sv, lane ^ 16);
+            if ((lane & 31) == 0) {
+                const int j = 2 * k + (lane >> 5);
+                bp[(int64_t)qb * 16 + j] = (int8_t)(ps & 63);
+                bp[(int64_t)qb * 16 + 8 + j] = (int8_t)(ps >> 6);
+            }
+        }
     }
     if (lane == 0) putf(d + qb, 1.0f / iscale);
 }
@@ -1185,13 +1195,19 @@ extern "C" __global__ void __launch_bounds__(256) oh_k_mvb_q80(oh_mvbatch B) { m
 // RMSNorm prologue). xn_out (optional) receives the normalised f32 vectors.
 extern "C" __global__ void __launch_bounds__(256)
 oh_k_norm_q8k_rows(const float *x, const float *norm_w, float eps, int n, float *xn_out, int8_t *qs, float *d,
-                   int16_t *bs) {
+                   int16_t *bs, int8_t *bp, int swiglu) {
     __shared__ float v[8192];
     __shared__ double red[4];
     const size_t r = blockIdx.x;
     const int tid = tid_x(), wave = tid >> 6, nqb = n / 256;
-    const float *xr = x + r * n;
-    for (int i = tid; i < n; i += 256) v[i] = ldg(xr + i);
+    if (swiglu) {
+        // rows of [gate | up] (2n): v = silu(gate) * up, the paired matvec's h
+        const float *xr = x + r * 2 * n;
+        for (int i = tid; i < n; i += 256) v[i] = ref_silu(ldg(xr + i)) * ldg(xr + n + i);
+    } else {
+        const float *xr = x + r * n;
+        for (int i = tid; i < n; i += 256) v[i] = ldg(xr + i);
+    }
     __syncthreads();
     if (norm_w) {
         double ss = 0.0;
@@ -1206,5 +1222,6 @@ oh_k_norm_q8k_rows(const float *x, const float *norm_w, float eps, int n, float 
         __syncthreads();
     }
     if (xn_out) for (int i = tid; i < n; i += 256) stg(xn_out + r * n + i, v[i]);
-    for (int qb = wave; qb < nqb; qb += 4) q8k_block_from_lds(v, qb, qs + r * n, d + r * nqb, bs + r * nqb * 16);
+    for (int qb = wave; qb < nqb; qb += 4)
+        q8k_block_from_lds(v, qb, qs + r * n, d + r * nqb, bs + r * nqb * 16, 256, bp ? bp + r * nqb * 16 : nullptr);
 }

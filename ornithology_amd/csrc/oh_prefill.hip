@@ -348,7 +348,7 @@ oh_k_delta_chunked(const float *qn, const float *kn, const float *conv, const fl
 // order, inv = 1/sqrt(ss/gdim + eps), v = x * inv * w * silu(z); then Q8_K.
 extern "C" __global__ void __launch_bounds__(256)
 oh_k_gnorm_q8k_rows(const float *x, const float *sz, const double *runs, const float *w, float eps, int n,
-                    int gdim, int8_t *qs, float *d, int16_t *bs) {
+                    int gdim, int8_t *qs, float *d, int16_t *bs, int8_t *bp) {
     __shared__ float v[8192];
     __shared__ float hinv[128];
     const size_t t = blockIdx.x;
@@ -363,7 +363,8 @@ oh_k_gnorm_q8k_rows(const float *x, const float *sz, const double *runs, const f
     for (int i = tid; i < n; i += 256)
         v[i] = ldg(x + t * n + i) * hinv[i / gdim] * ldg(w + i % gdim) * ldg(sz + t * n + i);
     __syncthreads();
-    for (int qb = wave; qb < nqb; qb += 4) q8k_block_from_lds(v, qb, qs + t * n, d + t * nqb, bs + t * nqb * 16);
+    for (int qb = wave; qb < nqb; qb += 4)
+        q8k_block_from_lds(v, qb, qs + t * n, d + t * nqb, bs + t * nqb * 16, 256, bp ? bp + t * nqb * 16 : nullptr);
 }
 
 // ---- GQA over T tokens: the decode operations with token t at position base+t ----

@@ -260,3 +260,18 @@ typedef struct {
     int ncol, lstride, adiv, ystride;
     int tcol;                      // columns staged in LDS at a time
 } oh_mvbatch;
+
+// Q4_K x Q8_K products of T columns on the matrix cores (prompt path): the
+// same (dense | grouped) column addressing as oh_mvbatch; with A2/B2 the
+// second weight set writes rows [rows, 2 rows) of each output row.
+typedef struct {
+    const uint8_t *A, *B, *A2, *B2;   // Q4_K planes (expert 0 of a stack)
+    const int8_t *xqs;                // Q8_K activation planes [a][in], [a][nb], [a][nb][16]
+    const float *xd;
+    const int8_t *xbp;                // per super-block: bytes bl_j, then bh_j, of the pair sums 64*bh + bl
+    float *y;                         // y[p * ystride + row]
+    const int32_t *cnt, *list;        // grouped columns (list != NULL)
+    const int32_t *items;             // grouped: count, then (group << 16 | 64-column tile)
+    int nb, in, rows, mode;           // mode 1: y += product
+    int ncol, lstride, adiv, ystride;
+} oh_mmq;

@@ -83,6 +83,31 @@ def test_matvec_vs_oracle(hip_ctx, orc, t, shape):
     W.free()
 
 
+@pytest.mark.parametrize("shape,ncol", [((2048, 1024), 70), ((512, 384), 1), ((4096, 256), 130), ((1024, 200), 65)])
+def test_batched_q4k_distinct_columns(hip_ctx, orc, monkeypatch, shape, ncol):
+    """Batched Q4_K products (matmul_batch_q Tn semantics) on independent
+    columns: the matrix-core path (rows a multiple of 128) and the vector-ALU
+    path (ORNITH_HIP_MMQ=0, and 200 rows) both equal the oracle's per-column
+    qdot bit for bit; partial 64-column tiles included."""
+    n, out = shape
+    w = clibs.gauss(11, f"bq.{n}.{out}", n * out, 0.02)
+    enc = clibs.quantize(orc, Q4_K, w)
+    W = hip_ctx.upload("w", Q4_K, enc, (n, out))
+    cols = [clibs.gauss(12 + c, f"bx.{n}.{c}", n, 1.0) for c in range(ncol)]
+    ref = []
+    for c in range(ncol):
+        r = np.zeros(out, np.float32)
+        orc.orc_matvec(Q4_K, bp(enc), n, out, f32p(np.ascontiguousarray(cols[c])), f32p(r), 0, 8)
+        ref.append(r)
+    for mmq in ("1", "0"):
+        monkeypatch.setenv("ORNITH_HIP_MMQ", mmq)
+        y = W.matvec(np.concatenate(cols))
+        for c in range(ncol):
+            got = y[c * out:(c + 1) * out]
+            assert np.array_equal(u32(got), u32(ref[c])), (mmq, c, np.nonzero(u32(got) != u32(ref[c]))[0][:8])
+    W.free()
+
+
 @pytest.mark.parametrize("t,shape", [(IQ2_XXS, (2048, 48)), (IQ2_XXS, (512, 33)), (F32, (512, 100)), (F32, (1000, 7))])
 def test_fallback_matvec_vs_oracle(hip_ctx, orc, t, shape):
     n, out = shape
