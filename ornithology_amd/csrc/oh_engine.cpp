@@ -983,7 +983,7 @@ struct ornith_hip_session {
         int tc = 0;
         int32_t pos_after = 0;
         float *X = nullptr, *CAT = nullptr, *Z = nullptr, *A = nullptr, *Bg = nullptr, *CONV = nullptr;
-        float *QN = nullptr, *KN = nullptr, *AL = nullptr, *BE = nullptr, *O = nullptr, *OG = nullptr;
+        float *QN = nullptr, *KN = nullptr, *AL = nullptr, *BE = nullptr, *O = nullptr;
         double *RUNS = nullptr;
         float *QP = nullptr, *KB = nullptr, *VB = nullptr, *QR = nullptr, *AG = nullptr, *OA = nullptr;
         float *FPO = nullptr, *FPML = nullptr, *RL = nullptr, *SHL = nullptr, *SHG = nullptr, *RW = nullptr;
@@ -1622,7 +1622,7 @@ static int pf_alloc(ornith_hip_session *s, int tc) {
     CHK(salloc(s, &p.X, T * H));
     CHK(q8alloc(s, p.XQ, T * H));
     CHK(salloc(s, &p.CAT, T * cc + 1)); CHK(salloc(s, &p.CONV, T * cc + 1));
-    CHK(salloc(s, &p.Z, T * vd + 1)); CHK(salloc(s, &p.O, T * vd + 1)); CHK(salloc(s, &p.OG, T * vd + 1));
+    CHK(salloc(s, &p.Z, T * vd + 1)); CHK(salloc(s, &p.O, T * vd + 1));
     CHK(q8alloc(s, p.OQ, T * vd + 256));
     CHK(salloc(s, &p.A, T * a.nv + 1)); CHK(salloc(s, &p.Bg, T * a.nv + 1));
     CHK(salloc(s, &p.AL, T * a.nv + 1)); CHK(salloc(s, &p.BE, T * a.nv + 1));
@@ -1755,12 +1755,12 @@ static int pf_chunk(ornith_hip_session *s, int base, int T, bool chunked, hipStr
             HCHK(oh_launch_qk_gates_rows(a.dk, p.CONV, p.A, p.Bg, (const float *)y.ssm_a->A,
                                          (const float *)y.dt_bias->A, p.QN, p.KN, p.AL, p.BE, T, a.nk, a.nv, cc, st));
             if (chunked)
-                HCHK(oh_launch_delta_chunked(a.dk, p.QN, p.KN, p.CONV, p.AL, p.BE, p.Z, p.GR, z.S, p.O, p.OG, p.RUNS,
-                                             T, a.nk, a.nv, cc, 1.0f / sqrtf((float)a.dk), st));
+                HCHK(oh_launch_delta_chunked(a.dk, p.QN, p.KN, p.CONV, p.AL, p.BE, p.GR, z.S, p.O, p.RUNS, T, a.nk,
+                                             a.nv, cc, 1.0f / sqrtf((float)a.dk), st));
             else
-                HCHK(oh_launch_delta_scan(a.dk, p.QN, p.KN, p.CONV, p.AL, p.BE, p.Z, z.S, p.O, p.OG, p.RUNS, T, a.nk,
-                                          a.nv, cc, 1.0f / sqrtf((float)a.dk), st));
-            HCHK(oh_launch_gnorm_q8k_rows(p.O, p.OG, p.RUNS, (const float *)y.ssm_norm->A, a.eps, vd, a.dv, T,
+                HCHK(oh_launch_delta_scan(a.dk, p.QN, p.KN, p.CONV, p.AL, p.BE, z.S, p.O, p.RUNS, T, a.nk, a.nv, cc,
+                                          1.0f / sqrtf((float)a.dk), st));
+            HCHK(oh_launch_gnorm_q8k_rows(p.O, p.Z, p.RUNS, (const float *)y.ssm_norm->A, a.eps, vd, a.dv, T,
                                           p.OQ.qs, p.OQ.d, p.OQ.bs, st, p.OQ.bp));
             CHK(pf_mm(y.ssm_out, p.OQ, p.X, H, T, 1, st));
         }

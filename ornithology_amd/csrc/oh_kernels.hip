@@ -22,7 +22,17 @@ hipError_t oh_launch_mvb(const oh_mvbatch *B, int groups, hipStream_t st) {
     const int rps = 64 / B->nb, blocks = (B->rows + 4 * rps - 1) / (4 * rps);
     if (blocks <= 0 || groups <= 0) return hipSuccess;
     void (*k)(oh_mvbatch) = B->type == OH_Q4_K ? oh_k_mvb_q4k : B->type == OH_Q6_K ? oh_k_mvb_q6k : oh_k_mvb_q80;
-    hipLaunchKernelGGL(k, dim3(blocks, groups), dim3(256), (size_t)B->tcol * mvb_col_bytes(B->nb), st, *B);
+    oh_mvbatch b = *B;
+    int gy = groups;
+    if (!B->list && blocks < 256 && B->ncol > B->tcol) {
+        // few rows: spread the columns over blocks too (about 512 blocks)
+        int chunks = (512 + blocks - 1) / blocks;
+        const int maxc = (B->ncol + B->tcol - 1) / B->tcol;
+        chunks = chunks < maxc ? chunks : maxc;
+        b.cpb = (B->ncol + chunks - 1) / chunks;
+        gy = (B->ncol + b.cpb - 1) / b.cpb;
+    }
+    hipLaunchKernelGGL(k, dim3(blocks, gy), dim3(256), (size_t)B->tcol * mvb_col_bytes(B->nb), st, b);
     return hipGetLastError();
 }
 
@@ -68,25 +78,24 @@ hipError_t oh_launch_qk_gates_rows(int dk, const float *conv, const float *A, co
     return hipGetLastError();
 }
 hipError_t oh_launch_delta_scan(int dk, const float *qn, const float *kn, const float *conv, const float *al,
-                                const float *be, const float *z, float *S, float *out, float *out_gate,
-                                double *out_runs, int T, int nk, int nv, int cc, float out_scale, hipStream_t st) {
-    if (dk == 128) hipLaunchKernelGGL(oh_k_delta_scan<128>, dim3(nv * 2), dim3(64), 0, st, qn, kn, conv, al, be, z, S, out, out_gate, out_runs, T, nk, nv, cc, out_scale);
-    else if (dk == 64) hipLaunchKernelGGL(oh_k_delta_scan<64>, dim3(nv), dim3(64), 0, st, qn, kn, conv, al, be, z, S, out, out_gate, out_runs, T, nk, nv, cc, out_scale);
+                                const float *be, float *S, float *out, double *out_runs, int T, int nk, int nv,
+                                int cc, float out_scale, hipStream_t st) {
+    if (dk == 128) hipLaunchKernelGGL(oh_k_delta_scan<128>, dim3(nv * 2), dim3(64), 0, st, qn, kn, conv, al, be, S, out, out_runs, T, nk, nv, cc, out_scale);
+    else if (dk == 64) hipLaunchKernelGGL(oh_k_delta_scan<64>, dim3(nv), dim3(64), 0, st, qn, kn, conv, al, be, S, out, out_runs, T, nk, nv, cc, out_scale);
     else return hipErrorInvalidValue;
     return hipGetLastError();
 }
 int oh_delta_grams_floats(int T, int nk) { return (T + kDeltaChunk - 1) / kDeltaChunk * nk * 2 * kDeltaChunk * kDeltaChunk; }
 hipError_t oh_launch_delta_chunked(int dk, const float *qn, const float *kn, const float *conv, const float *al,
-                                   const float *be, const float *z, float *grams, float *S, float *out,
-                                   float *out_gate, double *out_runs, int T, int nk, int nv, int cc, float out_scale,
-                                   hipStream_t st) {
+                                   const float *be, float *grams, float *S, float *out, double *out_runs, int T,
+                                   int nk, int nv, int cc, float out_scale, hipStream_t st) {
     const dim3 gg(nk, (T + kDeltaChunk - 1) / kDeltaChunk);
     if (dk == 128) {
         hipLaunchKernelGGL(oh_k_delta_grams<128>, gg, dim3(256), 0, st, qn, kn, T, nk, grams);
-        hipLaunchKernelGGL(oh_k_delta_chunked<128>, dim3(nv * 2), dim3(64), 0, st, qn, kn, conv, al, be, z, grams, S, out, out_gate, out_runs, T, nk, nv, cc, out_scale);
+        hipLaunchKernelGGL(oh_k_delta_chunked<128>, dim3(nv * 2), dim3(256), 0, st, qn, kn, conv, al, be, grams, S, out, out_runs, T, nk, nv, cc, out_scale);
     } else if (dk == 64) {
         hipLaunchKernelGGL(oh_k_delta_grams<64>, gg, dim3(256), 0, st, qn, kn, T, nk, grams);
-        hipLaunchKernelGGL(oh_k_delta_chunked<64>, dim3(nv), dim3(64), 0, st, qn, kn, conv, al, be, z, grams, S, out, out_gate, out_runs, T, nk, nv, cc, out_scale);
+        hipLaunchKernelGGL(oh_k_delta_chunked<64>, dim3(nv), dim3(256), 0, st, qn, kn, conv, al, be, grams, S, out, out_runs, T, nk, nv, cc, out_scale);
     } else {
         return hipErrorInvalidValue;
     }
@@ -113,10 +122,10 @@ hipError_t oh_launch_mmq_items(const int32_t *cnt, int ne, int32_t *items, hipSt
     hipLaunchKernelGGL(oh_k_mmq_items, dim3(1), dim3(256), 0, st, cnt, ne, items);
     return hipGetLastError();
 }
-hipError_t oh_launch_gnorm_q8k_rows(const float *x, const float *sz, const double *runs, const float *w, float eps,
+hipError_t oh_launch_gnorm_q8k_rows(const float *x, const float *z, const double *runs, const float *w, float eps,
                                     int n, int gdim, int T, int8_t *qs, float *d, int16_t *bs, hipStream_t st,
                                     int8_t *bp) {
-    hipLaunchKernelGGL(oh_k_gnorm_q8k_rows, dim3(T), dim3(256), 0, st, x, sz, runs, w, eps, n, gdim, qs, d, bs, bp);
+    hipLaunchKernelGGL(oh_k_gnorm_q8k_rows, dim3(T), dim3(256), 0, st, x, z, runs, w, eps, n, gdim, qs, d, bs, bp);
     return hipGetLastError();
 }
 hipError_t oh_launch_prep_rows(const oh_op_prep *a, int base, int T, hipStream_t st) {

@@ -999,9 +999,12 @@ OH_DEV void mvb_body(const oh_mvbatch &B) {
     __shared__ int scol[64];
     const int lane = lane_id(), wave = __builtin_amdgcn_readfirstlane(tid_x() >> 6), tid = tid_x();
     const int nb = B.nb, in = B.in, rps = 64 / nb, rl = lane / nb, sb = lane - rl * nb;
-    const int g = (int)blockIdx.y;
-    const int ncol = B.list ? B.cnt[g] : B.ncol;
-    if (ncol <= 0) return;
+    const int g = B.list ? (int)blockIdx.y : 0;
+    // dense: block y takes columns [y * cpb, (y + 1) * cpb)
+    const int cbeg = B.list || !B.cpb ? 0 : (int)blockIdx.y * B.cpb;
+    int ncol = B.list ? B.cnt[g] : B.ncol;
+    if (!B.list && B.cpb) ncol = ncol < cbeg + B.cpb ? ncol : cbeg + B.cpb;
+    if (ncol <= cbeg) return;
     const int r0 = ((int)blockIdx.x * 4 + wave) * rps, row = r0 + rl;
     const bool rlive = rl < rps && row < B.rows;
     const int rowc0 = rl < rps ? row : r0, rowc = rowc0 < B.rows ? rowc0 : B.rows - 1;
@@ -1011,7 +1014,7 @@ OH_DEV void mvb_body(const oh_mvbatch &B) {
     sb_load(r, wp, (rbase + rowc) * nb + sb);
     if (B.pair) sb_load(r2, wp2, (rbase + rowc) * nb + sb);
     const int cs = mvb_col_bytes(nb), n16 = in / 16;
-    for (int c0 = 0; c0 < ncol; c0 += B.tcol) {
+    for (int c0 = cbeg; c0 < ncol; c0 += B.tcol) {
         const int n = ncol - c0 < B.tcol ? ncol - c0 : B.tcol;
         __syncthreads();                              // the previous tile is consumed
         if (tid < n) scol[tid] = B.list ? ldg(B.list + (size_t)g * B.lstride + c0 + tid) : c0 + tid;

@@ -110,8 +110,7 @@ oh_k_qk_gates_rows(const float *conv, const float *A, const float *Bg, const flo
 template <int DK>
 __global__ void __launch_bounds__(64)
 oh_k_delta_scan(const float *qn, const float *kn, const float *conv, const float *al, const float *be,
-                const float *z, float *S, float *out, float *out_gate, double *out_runs, int T, int nk, int nv,
-                int cc, float out_scale) {
+                float *S, float *out, double *out_runs, int T, int nk, int nv, int cc, float out_scale) {
     constexpr int NQ = DK / 64;
     __shared__ __align__(16) float kq[2][2 * DK];              // [buffer][k | q]
     const int lane = lane_id(), vb = (int)blockIdx.x;
@@ -126,7 +125,7 @@ oh_k_delta_scan(const float *qn, const float *kn, const float *conv, const float
     }
     // token t's k and q (uniform over the wave) through LDS, the next token's
     // already requested while t is stepped
-    float pk[NQ], pq[NQ], pv, pa, pb, pz;
+    float pk[NQ], pq[NQ], pv, pa, pb;
     auto fetch = [&](int t) {
         const int tc = t < T ? t : T - 1;
 #pragma unroll
@@ -137,7 +136,6 @@ oh_k_delta_scan(const float *qn, const float *kn, const float *conv, const float
         pv = ldg(conv + (size_t)tc * cc + 2 * qd + hv * DK + r);
         pa = ldg(al + (size_t)tc * nv + hv);
         pb = ldg(be + (size_t)tc * nv + hv);
-        pz = ldg(z + (size_t)tc * vd + hv * DK + r);
     };
     fetch(0);
     for (int t = 0; t < T; t++) {
@@ -147,7 +145,7 @@ oh_k_delta_scan(const float *qn, const float *kn, const float *conv, const float
             kq[bf][lane + 64 * i] = pk[i];
             kq[bf][DK + lane + 64 * i] = pq[i];
         }
-        const float v = pv, alpha = pa, beta = pb, gz = pz;
+        const float v = pv, alpha = pa, beta = pb;
         fetch(t + 1);
         wave_lds_sync();
         const float *kk = kq[bf], *qq = kq[bf] + DK;
@@ -165,7 +163,6 @@ oh_k_delta_scan(const float *qn, const float *kn, const float *conv, const float
         o *= out_scale;
         const double so = wave_sum_d((double)o * o);
         stg(out + (size_t)t * vd + hv * DK + r, o);
-        stg(out_gate + (size_t)t * vd + hv * DK + r, ref_silu(gz));
         if (lane == 0) stg(out_runs + (size_t)t * (vd / 64) + vb, so);
     }
 #pragma unroll
@@ -226,53 +223,69 @@ oh_k_delta_grams(const float *qn, const float *kn, int T, int nk, float *grams) 
     for (int m = 0; m < NP; m++) stg(g + tid + 256 * m, acc[m]);
 }
 
-// one wave per 64 rows of one value head's state, the rows in registers; a
-// lane owns state row r and its u / Sk / Sq columns (in LDS, [i][lane])
+// Four waves per 64 rows of one value head's state; lane l of every wave owns
+// state row r = 64 * slab + l and keeps the whole row in registers (for the
+// projections). Per chunk: the waves split the chunk's tokens for the S_in
+// projections and the outputs (token i to wave i % 4), wave 0 runs the forward
+// substitution, and each wave updates a quarter of the columns of every row in
+// LDS (the update is independent per element), after which every wave reloads
+// the full rows. Every float is still formed in delta_chunk's order.
 template <int DK>
-__global__ void __launch_bounds__(64)
+__global__ void __launch_bounds__(256)
 oh_k_delta_chunked(const float *qn, const float *kn, const float *conv, const float *al, const float *be,
-                   const float *z, const float *grams, float *S, float *out, float *out_gate, double *out_runs,
-                   int T, int nk, int nv, int cc, float out_scale) {
-    constexpr int CH = kDeltaChunk, NQ = DK / 64;
+                   const float *grams, float *S, float *out, double *out_runs, int T, int nk, int nv, int cc,
+                   float out_scale) {
+    constexpr int CH = kDeltaChunk, NQ = DK / 64, NW = 4, CW = DK / NW, XS = DK + 4;
     __shared__ __align__(16) float kc[CH][DK], qc[CH][DK];
     __shared__ float M[CH][CH + 1], W[CH][CH + 1];       // k_j.k_i / k_j.q_i, then the coefficients
     __shared__ float Sq[CH][64], U[CH][64];
     __shared__ float alpha[CH], beta[CH], p[CH], wend[CH];
-    const int lane = lane_id(), vb = (int)blockIdx.x;
-    const int hv = vb / NQ, slab = vb % NQ, r = slab * 64 + lane, kh = hv % nk;
+    __shared__ __align__(16) float xs[64 * XS];         // the 64 state rows, row stride DK + 4
+    const int tid = tid_x(), lane = lane_id();
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int vb = (int)blockIdx.x, hv = vb / NQ, slab = vb % NQ, r = slab * 64 + lane, kh = hv % nk;
     const int qd = nk * DK, vd = nv * DK;
-    float *Sr = S + ((size_t)hv * DK + r) * DK;
-    float s[DK];
-#pragma unroll
-    for (int c = 0; c < DK / 4; c++) {
-        const float4 v = ldg((const float4 *)Sr + c);
-        s[4 * c] = v.x; s[4 * c + 1] = v.y; s[4 * c + 2] = v.z; s[4 * c + 3] = v.w;
+    float *Srow = S + ((size_t)hv * DK + slab * 64) * DK;
+    // the slab: global -> LDS (coalesced), then each lane's row into registers
+    for (int e = tid; e < 64 * DK / 4; e += 256) {
+        const int row = e / (DK / 4), c4 = e - row * (DK / 4);
+        *(float4 *)(xs + row * XS + 4 * c4) = ldg((const float4 *)Srow + e);
     }
+    __syncthreads();
+    float s[DK];
+    auto reload = [&]() {
+#pragma unroll
+        for (int c = 0; c < DK / 4; c++) {
+            const float4 v = *(const float4 *)(xs + lane * XS + 4 * c);
+            s[4 * c] = v.x; s[4 * c + 1] = v.y; s[4 * c + 2] = v.z; s[4 * c + 3] = v.w;
+        }
+    };
+    reload();
     for (int c0 = 0, ch = 0; c0 < T; c0 += CH, ch++) {
         const int C = T - c0 < CH ? T - c0 : CH;
-        wave_lds_sync();                                 // the previous chunk is consumed
-        for (int e = lane; e < C * DK / 4; e += 64) {
+        __syncthreads();                                 // the previous chunk is consumed
+        for (int e = tid; e < C * DK / 4; e += 256) {
             const int i = e / (DK / 4), c = e - i * (DK / 4);
             const size_t src = ((size_t)(c0 + i) * nk + kh) * DK;
             ((float4 *)kc[i])[c] = ldg((const float4 *)(kn + src) + c);
             ((float4 *)qc[i])[c] = ldg((const float4 *)(qn + src) + c);
         }
         const float *g = grams + ((size_t)ch * nk + kh) * 2 * CH * CH;
-        for (int e = lane; e < CH * CH; e += 64) {
+        for (int e = tid; e < CH * CH; e += 256) {
             M[e / CH][e % CH] = ldg(g + e);
             W[e / CH][e % CH] = ldg(g + CH * CH + e);
         }
-        if (lane < C) {
-            alpha[lane] = ldg(al + (size_t)(c0 + lane) * nv + hv);
-            beta[lane] = ldg(be + (size_t)(c0 + lane) * nv + hv);
+        if (tid < C) {
+            alpha[tid] = ldg(al + (size_t)(c0 + tid) * nv + hv);
+            beta[tid] = ldg(be + (size_t)(c0 + tid) * nv + hv);
         }
-        for (int i = 0; i < C; i++) U[i][lane] = ldg(conv + (size_t)(c0 + i) * cc + 2 * qd + hv * DK + r);
-        wave_lds_sync();
-        // decay products: lane i owns row i of the coefficient tables, which
+        for (int i = wave; i < C; i += NW) U[i][lane] = ldg(conv + (size_t)(c0 + i) * cc + 2 * qd + hv * DK + r);
+        __syncthreads();
+        // decay products: thread i owns row i of the coefficient tables, which
         // turn in place into M[i][j] = beta_i (p_i/p_j) k_j.k_i and
         // W[i][j] = (p_i/p_j) k_j.q_i
-        if (lane < C) {
-            const int i = lane;
+        if (tid < C) {
+            const int i = tid;
             float pi = alpha[0];
             for (int l = 1; l <= i; l++) pi = pi * alpha[l];
             p[i] = pi;
@@ -284,40 +297,50 @@ oh_k_delta_chunked(const float *qn, const float *kn, const float *conv, const fl
                 W[i][j] = ratio * W[i][j];
             }
         }
-        if (lane == 0) {
+        if (tid == 64) {
             float ratio = 1.0f;
             for (int j = C - 1; j >= 0; j--) {
                 wend[j] = ratio;
                 ratio *= alpha[j];
             }
         }
-        wave_lds_sync();
-        // projections of the incoming state; U starts as
-        // t_i = beta_i v_i - beta_i p_i (S_in k_i)
-        for (int i = 0; i < C; i++) {
-            float ak = 0.0f, aq = 0.0f;
-            const float *ki = kc[i], *qi = qc[i];
+        __syncthreads();
+        // projections of the incoming state (this wave's tokens, two at a
+        // time); U starts as t_i = beta_i v_i - beta_i p_i (S_in k_i)
+        for (int i0 = wave; i0 < C; i0 += 2 * NW) {
+            const int i1 = i0 + NW < C ? i0 + NW : i0;
+            float ak0 = 0.0f, aq0 = 0.0f, ak1 = 0.0f, aq1 = 0.0f;
+            const float *k0 = kc[i0], *q0 = qc[i0], *k1 = kc[i1], *q1 = qc[i1];
 #pragma unroll
             for (int c = 0; c < DK; c++) {
-                ak += s[c] * ki[c];
-                aq += s[c] * qi[c];
+                ak0 += s[c] * k0[c];
+                aq0 += s[c] * q0[c];
+                ak1 += s[c] * k1[c];
+                aq1 += s[c] * q1[c];
             }
-            const float bi = beta[i], pi = p[i];
-            U[i][lane] = bi * U[i][lane] - bi * pi * ak;
-            Sq[i][lane] = aq;
-        }
-        // forward substitution (I + M) U = T, this lane's state row
-        for (int i = 0; i < C; i++) {
-            float u = U[i][lane];
-            for (int j = i - 1; j >= 0; j--) {
-                const float mij = M[i][j];
-                if (mij != 0.0f) u -= mij * U[j][lane];
+            U[i0][lane] = beta[i0] * U[i0][lane] - beta[i0] * p[i0] * ak0;
+            Sq[i0][lane] = aq0;
+            if (i1 != i0) {
+                U[i1][lane] = beta[i1] * U[i1][lane] - beta[i1] * p[i1] * ak1;
+                Sq[i1][lane] = aq1;
             }
-            U[i][lane] = u;
         }
-        // outputs, scaled by 1/sqrt(dk), with the per-run sums of squares of
-        // the gated RMSNorm and silu of the gate
-        for (int i = 0; i < C; i++) {
+        __syncthreads();
+        // forward substitution (I + M) U = T, every lane its own row
+        if (wave == 0) {
+            for (int i = 0; i < C; i++) {
+                float u = U[i][lane];
+                for (int j = i - 1; j >= 0; j--) {
+                    const float mij = M[i][j];
+                    if (mij != 0.0f) u -= mij * U[j][lane];
+                }
+                U[i][lane] = u;
+            }
+        }
+        __syncthreads();
+        // outputs of this wave's tokens, scaled by 1/sqrt(dk), with the per-run
+        // sums of squares of the gated RMSNorm
+        for (int i = wave; i < C; i += NW) {
             float o = p[i] * Sq[i][lane];
             o += W[i][i] * U[i][lane];
             for (int j = i - 1; j >= 0; j--) o += W[i][j] * U[j][lane];
@@ -325,29 +348,40 @@ oh_k_delta_chunked(const float *qn, const float *kn, const float *conv, const fl
             const int t = c0 + i;
             const double so = wave_sum_d((double)o * o);
             stg(out + (size_t)t * vd + hv * DK + r, o);
-            stg(out_gate + (size_t)t * vd + hv * DK + r, ref_silu(ldg(z + (size_t)t * vd + hv * DK + r)));
             if (lane == 0) stg(out_runs + (size_t)t * (vd / 64) + vb, so);
         }
-        // S_out = p_{C-1} S_in + sum_j (p_{C-1}/p_j) u_j k_j^T, j descending
-        const float pc = p[C - 1];
+        // S_out = p_{C-1} S_in + sum_j (p_{C-1}/p_j) u_j k_j^T, j descending:
+        // this wave's CW columns of every row
+        {
+            const float pc = p[C - 1];
+            float u[CW];
+            float *xr = xs + lane * XS + wave * CW;
 #pragma unroll
-        for (int c = 0; c < DK; c++) s[c] *= pc;
-        for (int j = C - 1; j >= 0; j--) {
-            const float ur = wend[j] * U[j][lane];
-            if (ur == 0.0f) continue;
+            for (int c = 0; c < CW; c++) u[c] = xr[c] * pc;
+            for (int j = C - 1; j >= 0; j--) {
+                const float ur = wend[j] * U[j][lane];
+                if (ur == 0.0f) continue;
+                const float *kj = kc[j] + wave * CW;
 #pragma unroll
-            for (int c = 0; c < DK; c++) s[c] += ur * kc[j][c];
+                for (int c = 0; c < CW; c++) u[c] += ur * kj[c];
+            }
+#pragma unroll
+            for (int c = 0; c < CW; c++) xr[c] = u[c];
         }
+        __syncthreads();
+        reload();
     }
-#pragma unroll
-    for (int c = 0; c < DK / 4; c++) stg((float4 *)Sr + c, make_float4(s[4 * c], s[4 * c + 1], s[4 * c + 2], s[4 * c + 3]));
+    for (int e = tid; e < 64 * DK / 4; e += 256) {
+        const int row = e / (DK / 4), c4 = e - row * (DK / 4);
+        stg((float4 *)Srow + e, *(const float4 *)(xs + row * XS + 4 * c4));
+    }
 }
 
 // ---- gated per-head RMSNorm + Q8_K of T vectors (src/ornith_rforward.c:300-319) ---
 // one block per token: per head of gdim elements the runs' sums of squares in
 // order, inv = 1/sqrt(ss/gdim + eps), v = x * inv * w * silu(z); then Q8_K.
 extern "C" __global__ void __launch_bounds__(256)
-oh_k_gnorm_q8k_rows(const float *x, const float *sz, const double *runs, const float *w, float eps, int n,
+oh_k_gnorm_q8k_rows(const float *x, const float *z, const double *runs, const float *w, float eps, int n,
                     int gdim, int8_t *qs, float *d, int16_t *bs, int8_t *bp) {
     __shared__ float v[8192];
     __shared__ float hinv[128];
@@ -361,7 +395,7 @@ oh_k_gnorm_q8k_rows(const float *x, const float *sz, const double *runs, const f
     }
     __syncthreads();
     for (int i = tid; i < n; i += 256)
-        v[i] = ldg(x + t * n + i) * hinv[i / gdim] * ldg(w + i % gdim) * ldg(sz + t * n + i);
+        v[i] = ldg(x + t * n + i) * hinv[i / gdim] * ldg(w + i % gdim) * ref_silu(ldg(z + t * n + i));
     __syncthreads();
     for (int qb = wave; qb < nqb; qb += 4)
         q8k_block_from_lds(v, qb, qs + t * n, d + t * nqb, bs + t * nqb * 16, 256, bp ? bp + t * nqb * 16 : nullptr);

@@ -259,6 +259,7 @@ typedef struct {
     int type, nb, in, rows, pair, mode;
     int ncol, lstride, adiv, ystride;
     int tcol;                      // columns staged in LDS at a time
+    int cpb;                       // dense: columns per block along grid y (0: all)
 } oh_mvbatch;
 
 // Q4_K x Q8_K products of T columns on the matrix cores (prompt path): the
