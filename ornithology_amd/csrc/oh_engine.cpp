@@ -1572,10 +1572,17 @@ static int sync_pos(ornith_hip_session *s) {
 // projections (weights read once per chunk), the conv / delta state / KV cache
 // advanced in token order with the decode step's arithmetic. Bit-identical to
 // the same tokens fed through the token step.
-static const int kPfChunk = 256, kPfAttnSub = 16;
-// the chunked delta scan counts its 32-token chunks from the start of the
-// evaluation: engine chunks must not split one
-static_assert(kPfChunk % 32 == 0, "engine chunks hold whole delta chunks");
+static const int kPfChunk = 2048, kPfAttnSub = 32;
+
+// tokens per engine chunk (ORNITH_HIP_PREFILL_CHUNK, default 2048): a multiple
+// of 32, because the chunked delta scan counts its 32-token chunks from the
+// start of the evaluation and an engine chunk must not split one
+static int pf_chunk_tokens() {
+    const char *e = getenv("ORNITH_HIP_PREFILL_CHUNK");
+    int c = e && *e ? atoi(e) : kPfChunk;
+    c = c / 32 * 32;
+    return c < 32 ? 32 : (c > kPfChunk ? kPfChunk : c);
+}
 
 static bool pf_mvb_ok(const ornith_hip_tensor *W) {
     return W && oh_qdot_can(W->type, W->in) && W->in <= 8192 && W->in / 256 <= 64;
@@ -1830,9 +1837,10 @@ static int session_eval(ornith_hip_session *s, const int32_t *tokens, int n, boo
     const bool serial = prefill_serial();
     if (!token_path && (n > 1 || !serial) && pf_enabled() && pf_supported(s->m)) {
         // layer-major over chunks of tokens, then the head at the last one
-        CHK(pf_alloc(s, n < kPfChunk ? n : kPfChunk));
-        for (int c0 = 0; c0 < n; c0 += kPfChunk)
-            CHK(pf_chunk(s, s->pos + c0, n - c0 < kPfChunk ? n - c0 : kPfChunk, !serial, st));
+        const int ct = pf_chunk_tokens();
+        CHK(pf_alloc(s, n < ct ? n : ct));
+        for (int c0 = 0; c0 < n; c0 += ct)
+            CHK(pf_chunk(s, s->pos + c0, n - c0 < ct ? n - c0 : ct, !serial, st));
         s->pf.pos_after = s->pos + n;   // outlives the asynchronous copy
         HCHK(hipMemcpyAsync(s->io + OH_IO_POS, &s->pf.pos_after, 4, hipMemcpyHostToDevice, st));
     } else {

@@ -68,6 +68,7 @@ def test_prefill_dense_matches_oracle(hip_ctx, orc, tmp_path, monkeypatch):
 
 def evals(m, chunks, cap, prefill, monkeypatch, exact_max):
     monkeypatch.setenv("ORNITH_HIP_PREFILL", "1" if prefill else "0")
+    monkeypatch.setenv("ORNITH_HIP_PREFILL_CHUNK", "96")
     if exact_max is not None:
         monkeypatch.setenv("ORNITH_HIP_EXACT_ATTN_MAX", str(exact_max))
     s = m.session(cap)
@@ -94,10 +95,12 @@ def oracle_state(orc, os_, arch, layer, pos):
 @pytest.mark.parametrize("cfg", ["moe", "dense"])
 def test_chunked_mode_matches_oracle(hip_ctx, orc, tmp_path, monkeypatch, cfg):
     """The reference's default prompt mode over several evaluations: a
-    300-token prompt (two engine chunks, a partial last delta chunk), then
-    7, 1 (a one-token chunk) and 33 tokens; logits after each and the whole
-    session state bit-identical to the oracle's chunked mode."""
+    300-token prompt (engine chunks of 96 tokens: four, the last partial,
+    with a partial last delta chunk), then 7, 1 (a one-token chunk) and 33
+    tokens; logits after each and the whole session state bit-identical to
+    the oracle's chunked mode."""
     monkeypatch.setenv("ORNITH_PREFILL_SERIAL", "0")
+    monkeypatch.setenv("ORNITH_HIP_PREFILL_CHUNK", "96")
     c = MIX if cfg == "moe" else DENSE
     path = tmp_path / "m.gguf"
     clibs.write_c1_gguf(path, c)
@@ -144,7 +147,8 @@ def test_prefill_equals_token_path(hip_ctx, monkeypatch, cfg, exact_max):
     m = hip_ctx.synth(**(MIX if cfg == "moe" else DENSE))
     a = m.arch
     rng = np.random.default_rng(3)
-    # 300 tokens span two chunks; then evals starting at odd and even positions
+    # 300 tokens span four engine chunks of 96; then evals starting at odd and
+    # even positions
     chunks = [rng.integers(0, a["vocab"], n).astype(np.int32) for n in (300, 7, 2, 33)]
     sp, lp = evals(m, chunks, 400, True, monkeypatch, exact_max)
     st, lt = evals(m, chunks, 400, False, monkeypatch, exact_max)
