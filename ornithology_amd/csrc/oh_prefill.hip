@@ -238,7 +238,7 @@ oh_k_delta_chunked(const float *qn, const float *kn, const float *conv, const fl
     constexpr int CH = kDeltaChunk, NQ = DK / 64, NW = 4, CW = DK / NW, XS = DK + 4;
     __shared__ __align__(16) float kc[CH][DK], qc[CH][DK];
     __shared__ float M[CH][CH + 1], W[CH][CH + 1];       // k_j.k_i / k_j.q_i, then the coefficients
-    __shared__ float Sq[CH][64], U[CH][64];
+    __shared__ float U[CH][64];
     __shared__ float alpha[CH], beta[CH], p[CH], wend[CH];
     __shared__ __align__(16) float xs[64 * XS];         // the 64 state rows, row stride DK + 4
     const int tid = tid_x(), lane = lane_id();
@@ -306,67 +306,96 @@ oh_k_delta_chunked(const float *qn, const float *kn, const float *conv, const fl
         }
         __syncthreads();
         // projections of the incoming state (this wave's tokens, two at a
-        // time); U starts as t_i = beta_i v_i - beta_i p_i (S_in k_i)
-        for (int i0 = wave; i0 < C; i0 += 2 * NW) {
-            const int i1 = i0 + NW < C ? i0 + NW : i0;
-            float ak0 = 0.0f, aq0 = 0.0f, ak1 = 0.0f, aq1 = 0.0f;
-            const float *k0 = kc[i0], *q0 = qc[i0], *k1 = kc[i1], *q1 = qc[i1];
+        // time); U starts as t_i = beta_i v_i - beta_i p_i (S_in k_i); Sq of
+        // the wave's k-th token (i = wave + 4k) stays in sq[k]
+        float sq[CH / NW];
 #pragma unroll
-            for (int c = 0; c < DK; c++) {
-                ak0 += s[c] * k0[c];
-                aq0 += s[c] * q0[c];
-                ak1 += s[c] * k1[c];
-                aq1 += s[c] * q1[c];
-            }
-            U[i0][lane] = beta[i0] * U[i0][lane] - beta[i0] * p[i0] * ak0;
-            Sq[i0][lane] = aq0;
-            if (i1 != i0) {
-                U[i1][lane] = beta[i1] * U[i1][lane] - beta[i1] * p[i1] * ak1;
-                Sq[i1][lane] = aq1;
-            }
-        }
-        __syncthreads();
-        // forward substitution (I + M) U = T, every lane its own row
-        if (wave == 0) {
-            for (int i = 0; i < C; i++) {
-                float u = U[i][lane];
-                for (int j = i - 1; j >= 0; j--) {
-                    const float mij = M[i][j];
-                    if (mij != 0.0f) u -= mij * U[j][lane];
+        for (int k = 0; k < CH / NW; k += 2) {
+            const int i0 = wave + NW * k, i1 = i0 + NW;
+            if (i0 < C) {
+                const int i1c = i1 < C ? i1 : i0;
+                float ak0 = 0.0f, aq0 = 0.0f, ak1 = 0.0f, aq1 = 0.0f;
+                const float *k0 = kc[i0], *q0 = qc[i0], *k1 = kc[i1c], *q1 = qc[i1c];
+#pragma unroll
+                for (int c = 0; c < DK; c++) {
+                    ak0 += s[c] * k0[c];
+                    aq0 += s[c] * q0[c];
+                    ak1 += s[c] * k1[c];
+                    aq1 += s[c] * q1[c];
                 }
-                U[i][lane] = u;
+                U[i0][lane] = beta[i0] * U[i0][lane] - beta[i0] * p[i0] * ak0;
+                sq[k] = aq0;
+                if (i1 < C) {
+                    U[i1][lane] = beta[i1] * U[i1][lane] - beta[i1] * p[i1] * ak1;
+                    sq[k + 1] = aq1;
+                }
             }
         }
         __syncthreads();
+        // forward substitution (I + M) U = T by wave 0, every lane its own row,
+        // the 32 values in registers
+        float u[CH];
+        if (wave == 0) {
+#pragma unroll
+            for (int i = 0; i < CH; i++) u[i] = i < C ? U[i][lane] : 0.0f;
+#pragma unroll
+            for (int i = 1; i < CH; i++) {
+                if (i < C) {
+                    float ui = u[i];
+#pragma unroll
+                    for (int j = i - 1; j >= 0; j--) {
+                        const float mij = M[i][j];
+                        ui = mij != 0.0f ? ui - mij * u[j] : ui;
+                    }
+                    u[i] = ui;
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < CH; i++)
+                if (i < C) U[i][lane] = u[i];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < CH; i++) u[i] = i < C ? U[i][lane] : 0.0f;
         // outputs of this wave's tokens, scaled by 1/sqrt(dk), with the per-run
         // sums of squares of the gated RMSNorm
-        for (int i = wave; i < C; i += NW) {
-            float o = p[i] * Sq[i][lane];
-            o += W[i][i] * U[i][lane];
-            for (int j = i - 1; j >= 0; j--) o += W[i][j] * U[j][lane];
-            o *= out_scale;
-            const int t = c0 + i;
-            const double so = wave_sum_d((double)o * o);
-            stg(out + (size_t)t * vd + hv * DK + r, o);
-            if (lane == 0) stg(out_runs + (size_t)t * (vd / 64) + vb, so);
+#pragma unroll
+        for (int k = 0; k < CH / NW; k++) {
+            const int i = wave + NW * k;
+            if (i < C) {
+                float o = p[i] * sq[k];
+                o += W[i][i] * u[i];
+#pragma unroll
+                for (int j = CH - 1; j >= 0; j--)
+                    if (j < i) o += W[i][j] * u[j];
+                o *= out_scale;
+                const int t = c0 + i;
+                const double so = wave_sum_d((double)o * o);
+                stg(out + (size_t)t * vd + hv * DK + r, o);
+                if (lane == 0) stg(out_runs + (size_t)t * (vd / 64) + vb, so);
+            }
         }
         // S_out = p_{C-1} S_in + sum_j (p_{C-1}/p_j) u_j k_j^T, j descending:
         // this wave's CW columns of every row
         {
             const float pc = p[C - 1];
-            float u[CW];
+            float x[CW];
             float *xr = xs + lane * XS + wave * CW;
 #pragma unroll
-            for (int c = 0; c < CW; c++) u[c] = xr[c] * pc;
-            for (int j = C - 1; j >= 0; j--) {
-                const float ur = wend[j] * U[j][lane];
-                if (ur == 0.0f) continue;
-                const float *kj = kc[j] + wave * CW;
+            for (int c = 0; c < CW; c++) x[c] = xr[c] * pc;
 #pragma unroll
-                for (int c = 0; c < CW; c++) u[c] += ur * kj[c];
+            for (int j = CH - 1; j >= 0; j--) {
+                if (j < C) {
+                    const float ur = wend[j] * u[j];
+                    if (ur != 0.0f) {
+                        const float *kj = kc[j] + wave * CW;
+#pragma unroll
+                        for (int c = 0; c < CW; c++) x[c] += ur * kj[c];
+                    }
+                }
             }
 #pragma unroll
-            for (int c = 0; c < CW; c++) xr[c] = u[c];
+            for (int c = 0; c < CW; c++) xr[c] = x[c];
         }
         __syncthreads();
         reload();
