@@ -984,7 +984,6 @@ struct ornith_hip_session {
         int32_t pos_after = 0;
         float *X = nullptr, *CAT = nullptr, *Z = nullptr, *A = nullptr, *Bg = nullptr, *CONV = nullptr;
         float *QN = nullptr, *KN = nullptr, *AL = nullptr, *BE = nullptr, *O = nullptr;
-        double *RUNS = nullptr;
         float *QP = nullptr, *KB = nullptr, *VB = nullptr, *QR = nullptr, *AG = nullptr, *OA = nullptr;
         float *FPO = nullptr, *FPML = nullptr, *RL = nullptr, *SHL = nullptr, *SHG = nullptr, *RW = nullptr;
         int32_t *RIDX = nullptr, *CNT = nullptr, *LIST = nullptr;
@@ -1634,7 +1633,6 @@ static int pf_alloc(ornith_hip_session *s, int tc) {
     CHK(salloc(s, &p.A, T * a.nv + 1)); CHK(salloc(s, &p.Bg, T * a.nv + 1));
     CHK(salloc(s, &p.AL, T * a.nv + 1)); CHK(salloc(s, &p.BE, T * a.nv + 1));
     CHK(salloc(s, &p.QN, T * qd + 1)); CHK(salloc(s, &p.KN, T * qd + 1));
-    CHK(salloc(s, &p.RUNS, T * (vd / 64) + 1));
     CHK(salloc(s, &p.GR, (size_t)oh_delta_grams_floats(tc, a.nk > 0 ? a.nk : 1) + 1));
     CHK(salloc(s, &p.STAGE, (size_t)(a.conv_k > 1 ? a.conv_k - 1 : 1) * cc + 1));
     CHK(salloc(s, &p.QP, T * 2 * aq + 1)); CHK(salloc(s, &p.KB, T * kvd + 1)); CHK(salloc(s, &p.VB, T * kvd + 1));
@@ -1762,13 +1760,13 @@ static int pf_chunk(ornith_hip_session *s, int base, int T, bool chunked, hipStr
             HCHK(oh_launch_qk_gates_rows(a.dk, p.CONV, p.A, p.Bg, (const float *)y.ssm_a->A,
                                          (const float *)y.dt_bias->A, p.QN, p.KN, p.AL, p.BE, T, a.nk, a.nv, cc, st));
             if (chunked)
-                HCHK(oh_launch_delta_chunked(a.dk, p.QN, p.KN, p.CONV, p.AL, p.BE, p.GR, z.S, p.O, p.RUNS, T, a.nk,
-                                             a.nv, cc, 1.0f / sqrtf((float)a.dk), st));
+                HCHK(oh_launch_delta_chunked(a.dk, p.QN, p.KN, p.CONV, p.AL, p.BE, p.GR, z.S, p.O, T, a.nk, a.nv, cc,
+                                             1.0f / sqrtf((float)a.dk), st));
             else
-                HCHK(oh_launch_delta_scan(a.dk, p.QN, p.KN, p.CONV, p.AL, p.BE, z.S, p.O, p.RUNS, T, a.nk, a.nv, cc,
+                HCHK(oh_launch_delta_scan(a.dk, p.QN, p.KN, p.CONV, p.AL, p.BE, z.S, p.O, T, a.nk, a.nv, cc,
                                           1.0f / sqrtf((float)a.dk), st));
-            HCHK(oh_launch_gnorm_q8k_rows(p.O, p.Z, p.RUNS, (const float *)y.ssm_norm->A, a.eps, vd, a.dv, T,
-                                          p.OQ.qs, p.OQ.d, p.OQ.bs, st, p.OQ.bp));
+            HCHK(oh_launch_gnorm_q8k_rows(p.O, p.Z, (const float *)y.ssm_norm->A, a.eps, vd, a.dv, T, p.OQ.qs,
+                                          p.OQ.d, p.OQ.bs, st, p.OQ.bp));
             CHK(pf_mm(y.ssm_out, p.OQ, p.X, H, T, 1, st));
         }
         HCHK(oh_launch_norm_q8k_rows(p.X, (const float *)y.post_norm->A, a.eps, H, T, nullptr, p.XQ.qs, p.XQ.d,

@@ -78,24 +78,24 @@ hipError_t oh_launch_qk_gates_rows(int dk, const float *conv, const float *A, co
     return hipGetLastError();
 }
 hipError_t oh_launch_delta_scan(int dk, const float *qn, const float *kn, const float *conv, const float *al,
-                                const float *be, float *S, float *out, double *out_runs, int T, int nk, int nv,
-                                int cc, float out_scale, hipStream_t st) {
-    if (dk == 128) hipLaunchKernelGGL(oh_k_delta_scan<128>, dim3(nv * 2), dim3(64), 0, st, qn, kn, conv, al, be, S, out, out_runs, T, nk, nv, cc, out_scale);
-    else if (dk == 64) hipLaunchKernelGGL(oh_k_delta_scan<64>, dim3(nv), dim3(64), 0, st, qn, kn, conv, al, be, S, out, out_runs, T, nk, nv, cc, out_scale);
+                                const float *be, float *S, float *out, int T, int nk, int nv, int cc,
+                                float out_scale, hipStream_t st) {
+    if (dk == 128) hipLaunchKernelGGL(oh_k_delta_scan<128>, dim3(nv * 2), dim3(64), 0, st, qn, kn, conv, al, be, S, out, T, nk, nv, cc, out_scale);
+    else if (dk == 64) hipLaunchKernelGGL(oh_k_delta_scan<64>, dim3(nv), dim3(64), 0, st, qn, kn, conv, al, be, S, out, T, nk, nv, cc, out_scale);
     else return hipErrorInvalidValue;
     return hipGetLastError();
 }
 int oh_delta_grams_floats(int T, int nk) { return (T + kDeltaChunk - 1) / kDeltaChunk * nk * 2 * kDeltaChunk * kDeltaChunk; }
 hipError_t oh_launch_delta_chunked(int dk, const float *qn, const float *kn, const float *conv, const float *al,
-                                   const float *be, float *grams, float *S, float *out, double *out_runs, int T,
-                                   int nk, int nv, int cc, float out_scale, hipStream_t st) {
+                                   const float *be, float *grams, float *S, float *out, int T, int nk, int nv,
+                                   int cc, float out_scale, hipStream_t st) {
     const dim3 gg(nk, (T + kDeltaChunk - 1) / kDeltaChunk);
     if (dk == 128) {
         hipLaunchKernelGGL(oh_k_delta_grams<128>, gg, dim3(256), 0, st, qn, kn, T, nk, grams);
-        hipLaunchKernelGGL(oh_k_delta_chunked<128>, dim3(nv * 2), dim3(256), 0, st, qn, kn, conv, al, be, grams, S, out, out_runs, T, nk, nv, cc, out_scale);
+        hipLaunchKernelGGL(oh_k_delta_chunked<128>, dim3(nv * 8), dim3(256), 0, st, qn, kn, conv, al, be, grams, S, out, T, nk, nv, cc, out_scale);
     } else if (dk == 64) {
         hipLaunchKernelGGL(oh_k_delta_grams<64>, gg, dim3(256), 0, st, qn, kn, T, nk, grams);
-        hipLaunchKernelGGL(oh_k_delta_chunked<64>, dim3(nv), dim3(256), 0, st, qn, kn, conv, al, be, grams, S, out, out_runs, T, nk, nv, cc, out_scale);
+        hipLaunchKernelGGL(oh_k_delta_chunked<64>, dim3(nv * 4), dim3(256), 0, st, qn, kn, conv, al, be, grams, S, out, T, nk, nv, cc, out_scale);
     } else {
         return hipErrorInvalidValue;
     }
@@ -122,10 +122,9 @@ hipError_t oh_launch_mmq_items(const int32_t *cnt, int ne, int32_t *items, hipSt
     hipLaunchKernelGGL(oh_k_mmq_items, dim3(1), dim3(256), 0, st, cnt, ne, items);
     return hipGetLastError();
 }
-hipError_t oh_launch_gnorm_q8k_rows(const float *x, const float *z, const double *runs, const float *w, float eps,
-                                    int n, int gdim, int T, int8_t *qs, float *d, int16_t *bs, hipStream_t st,
-                                    int8_t *bp) {
-    hipLaunchKernelGGL(oh_k_gnorm_q8k_rows, dim3(T), dim3(256), 0, st, x, z, runs, w, eps, n, gdim, qs, d, bs, bp);
+hipError_t oh_launch_gnorm_q8k_rows(const float *x, const float *z, const float *w, float eps, int n, int gdim,
+                                    int T, int8_t *qs, float *d, int16_t *bs, hipStream_t st, int8_t *bp) {
+    hipLaunchKernelGGL(oh_k_gnorm_q8k_rows, dim3(T), dim3(256), 0, st, x, z, w, eps, n, gdim, qs, d, bs, bp);
     return hipGetLastError();
 }
 hipError_t oh_launch_prep_rows(const oh_op_prep *a, int base, int T, hipStream_t st) {

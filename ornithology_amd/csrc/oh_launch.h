@@ -26,17 +26,18 @@ hipError_t oh_launch_qk_gates_rows(int dk, const float *conv, const float *A, co
                                    const float *dt_bias, float *qn, float *kn, float *al, float *be, int T, int nk,
                                    int nv, int cc, hipStream_t st);
 hipError_t oh_launch_delta_scan(int dk, const float *qn, const float *kn, const float *conv, const float *al,
-                                const float *be, float *S, float *out, double *out_runs, int T, int nk, int nv,
-                                int cc, float out_scale, hipStream_t st);
+                                const float *be, float *S, float *out, int T, int nk, int nv, int cc,
+                                float out_scale, hipStream_t st);
 // the reference's chunked delta scan (grams per key head and chunk, then the scan)
 int oh_delta_grams_floats(int T, int nk);
 hipError_t oh_launch_delta_chunked(int dk, const float *qn, const float *kn, const float *conv, const float *al,
-                                   const float *be, float *grams, float *S, float *out, double *out_runs, int T,
-                                   int nk, int nv, int cc, float out_scale, hipStream_t st);
+                                   const float *be, float *grams, float *S, float *out, int T, int nk, int nv,
+                                   int cc, float out_scale, hipStream_t st);
 // z: the raw attention gate (silu applied here)
-hipError_t oh_launch_gnorm_q8k_rows(const float *x, const float *z, const double *runs, const float *w, float eps,
-                                    int n, int gdim, int T, int8_t *qs, float *d, int16_t *bs, hipStream_t st,
-                                    int8_t *bp = nullptr);
+// gated per-head RMSNorm (sums of squares per 64-element run, as the decode
+// step forms them) + Q8_K of T vectors
+hipError_t oh_launch_gnorm_q8k_rows(const float *x, const float *z, const float *w, float eps, int n, int gdim,
+                                    int T, int8_t *qs, float *d, int16_t *bs, hipStream_t st, int8_t *bp = nullptr);
 // Q4_K x Q8_K products on the matrix cores: rows % 128 == 0; dense (ncol
 // columns) or grouped (items from oh_launch_mmq_items, at most max_items);
 // pair: a second weight set (A2/B2) for rows [rows, 2 rows)

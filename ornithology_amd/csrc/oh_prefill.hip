@@ -110,7 +110,7 @@ oh_k_qk_gates_rows(const float *conv, const float *A, const float *Bg, const flo
 template <int DK>
 __global__ void __launch_bounds__(64)
 oh_k_delta_scan(const float *qn, const float *kn, const float *conv, const float *al, const float *be,
-                float *S, float *out, double *out_runs, int T, int nk, int nv, int cc, float out_scale) {
+                float *S, float *out, int T, int nk, int nv, int cc, float out_scale) {
     constexpr int NQ = DK / 64;
     __shared__ __align__(16) float kq[2][2 * DK];              // [buffer][k | q]
     const int lane = lane_id(), vb = (int)blockIdx.x;
@@ -161,9 +161,7 @@ oh_k_delta_scan(const float *qn, const float *kn, const float *conv, const float
 #pragma unroll
         for (int c = 0; c < DK; c++) o += s[c] * qq[c];
         o *= out_scale;
-        const double so = wave_sum_d((double)o * o);
         stg(out + (size_t)t * vd + hv * DK + r, o);
-        if (lane == 0) stg(out_runs + (size_t)t * (vd / 64) + vb, so);
     }
 #pragma unroll
     for (int c = 0; c < DK / 4; c++) stg((float4 *)Sr + c, make_float4(s[4 * c], s[4 * c + 1], s[4 * c + 2], s[4 * c + 3]));
@@ -223,31 +221,30 @@ oh_k_delta_grams(const float *qn, const float *kn, int T, int nk, float *grams) 
     for (int m = 0; m < NP; m++) stg(g + tid + 256 * m, acc[m]);
 }
 
-// Four waves per 64 rows of one value head's state; lane l of every wave owns
-// state row r = 64 * slab + l and keeps the whole row in registers (for the
-// projections). Per chunk: the waves split the chunk's tokens for the S_in
-// projections and the outputs (token i to wave i % 4), wave 0 runs the forward
-// substitution, and each wave updates a quarter of the columns of every row in
-// LDS (the update is independent per element), after which every wave reloads
-// the full rows. Every float is still formed in delta_chunk's order.
+// A block per 16 rows of one value head's state (256 blocks at C3). Thread
+// (r, g) = (tid % 16, tid / 16) keeps state row r in registers and takes
+// tokens g and g + 16 of each chunk for the S_in projections and the outputs;
+// the first 16 threads run the forward substitution of their rows; for the
+// state update thread (tid / 16, tid % 16) owns DK / 16 columns of one row in
+// LDS (the update is independent per element). Every float is formed in
+// delta_chunk's order.
 template <int DK>
 __global__ void __launch_bounds__(256)
 oh_k_delta_chunked(const float *qn, const float *kn, const float *conv, const float *al, const float *be,
-                   const float *grams, float *S, float *out, double *out_runs, int T, int nk, int nv, int cc,
-                   float out_scale) {
-    constexpr int CH = kDeltaChunk, NQ = DK / 64, NW = 4, CW = DK / NW, XS = DK + 4;
-    __shared__ __align__(16) float kc[CH][DK], qc[CH][DK];
+                   const float *grams, float *S, float *out, int T, int nk, int nv, int cc, float out_scale) {
+    constexpr int CH = kDeltaChunk, RB = 16, KS = DK + 4, XS = DK + 4, CPL = DK / 16;
+    __shared__ __align__(16) float kc[CH][KS], qc[CH][KS];
     __shared__ float M[CH][CH + 1], W[CH][CH + 1];       // k_j.k_i / k_j.q_i, then the coefficients
-    __shared__ float U[CH][64];
+    __shared__ float U[CH][RB + 1], Sq[CH][RB + 1];      // [token][row]
     __shared__ float alpha[CH], beta[CH], p[CH], wend[CH];
-    __shared__ __align__(16) float xs[64 * XS];         // the 64 state rows, row stride DK + 4
-    const int tid = tid_x(), lane = lane_id();
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int vb = (int)blockIdx.x, hv = vb / NQ, slab = vb % NQ, r = slab * 64 + lane, kh = hv % nk;
-    const int qd = nk * DK, vd = nv * DK;
-    float *Srow = S + ((size_t)hv * DK + slab * 64) * DK;
-    // the slab: global -> LDS (coalesced), then each lane's row into registers
-    for (int e = tid; e < 64 * DK / 4; e += 256) {
+    __shared__ __align__(16) float xs[RB * XS];
+    const int tid = tid_x();
+    const int vb = (int)blockIdx.x, hv = vb / (DK / RB), slab = vb % (DK / RB), kh = hv % nk;
+    const int qd = nk * DK, vd = nv * DK, r0 = hv * DK + slab * RB;
+    const int r = tid % RB, g = tid / RB;                // projections, outputs, reload
+    const int ur = tid / RB, ucg = tid % RB;             // update: row, column group
+    float *Srow = S + (size_t)r0 * DK;
+    for (int e = tid; e < RB * DK / 4; e += 256) {
         const int row = e / (DK / 4), c4 = e - row * (DK / 4);
         *(float4 *)(xs + row * XS + 4 * c4) = ldg((const float4 *)Srow + e);
     }
@@ -256,7 +253,7 @@ oh_k_delta_chunked(const float *qn, const float *kn, const float *conv, const fl
     auto reload = [&]() {
 #pragma unroll
         for (int c = 0; c < DK / 4; c++) {
-            const float4 v = *(const float4 *)(xs + lane * XS + 4 * c);
+            const float4 v = *(const float4 *)(xs + r * XS + 4 * c);
             s[4 * c] = v.x; s[4 * c + 1] = v.y; s[4 * c + 2] = v.z; s[4 * c + 3] = v.w;
         }
     };
@@ -267,19 +264,22 @@ oh_k_delta_chunked(const float *qn, const float *kn, const float *conv, const fl
         for (int e = tid; e < C * DK / 4; e += 256) {
             const int i = e / (DK / 4), c = e - i * (DK / 4);
             const size_t src = ((size_t)(c0 + i) * nk + kh) * DK;
-            ((float4 *)kc[i])[c] = ldg((const float4 *)(kn + src) + c);
-            ((float4 *)qc[i])[c] = ldg((const float4 *)(qn + src) + c);
+            *(float4 *)(&kc[i][4 * c]) = ldg((const float4 *)(kn + src) + c);
+            *(float4 *)(&qc[i][4 * c]) = ldg((const float4 *)(qn + src) + c);
         }
-        const float *g = grams + ((size_t)ch * nk + kh) * 2 * CH * CH;
+        const float *gm = grams + ((size_t)ch * nk + kh) * 2 * CH * CH;
         for (int e = tid; e < CH * CH; e += 256) {
-            M[e / CH][e % CH] = ldg(g + e);
-            W[e / CH][e % CH] = ldg(g + CH * CH + e);
+            M[e / CH][e % CH] = ldg(gm + e);
+            W[e / CH][e % CH] = ldg(gm + CH * CH + e);
         }
         if (tid < C) {
             alpha[tid] = ldg(al + (size_t)(c0 + tid) * nv + hv);
             beta[tid] = ldg(be + (size_t)(c0 + tid) * nv + hv);
         }
-        for (int i = wave; i < C; i += NW) U[i][lane] = ldg(conv + (size_t)(c0 + i) * cc + 2 * qd + hv * DK + r);
+        for (int e = tid; e < C * RB; e += 256) {
+            const int i = e / RB, rr = e - i * RB;
+            U[i][rr] = ldg(conv + (size_t)(c0 + i) * cc + 2 * qd + r0 + rr);
+        }
         __syncthreads();
         // decay products: thread i owns row i of the coefficient tables, which
         // turn in place into M[i][j] = beta_i (p_i/p_j) k_j.k_i and
@@ -305,39 +305,34 @@ oh_k_delta_chunked(const float *qn, const float *kn, const float *conv, const fl
             }
         }
         __syncthreads();
-        // projections of the incoming state (this wave's tokens, two at a
-        // time); U starts as t_i = beta_i v_i - beta_i p_i (S_in k_i); Sq of
-        // the wave's k-th token (i = wave + 4k) stays in sq[k]
-        float sq[CH / NW];
+        // projections of the incoming state, tokens g and g + 16; U starts as
+        // t_i = beta_i v_i - beta_i p_i (S_in k_i)
+        {
+            const int i0 = g, i1 = g + RB;
+            const int j0 = i0 < C ? i0 : 0, j1 = i1 < C ? i1 : 0;
+            float ak0 = 0.0f, aq0 = 0.0f, ak1 = 0.0f, aq1 = 0.0f;
 #pragma unroll
-        for (int k = 0; k < CH / NW; k += 2) {
-            const int i0 = wave + NW * k, i1 = i0 + NW;
+            for (int c = 0; c < DK; c++) {
+                ak0 += s[c] * kc[j0][c];
+                aq0 += s[c] * qc[j0][c];
+                ak1 += s[c] * kc[j1][c];
+                aq1 += s[c] * qc[j1][c];
+            }
             if (i0 < C) {
-                const int i1c = i1 < C ? i1 : i0;
-                float ak0 = 0.0f, aq0 = 0.0f, ak1 = 0.0f, aq1 = 0.0f;
-                const float *k0 = kc[i0], *q0 = qc[i0], *k1 = kc[i1c], *q1 = qc[i1c];
-#pragma unroll
-                for (int c = 0; c < DK; c++) {
-                    ak0 += s[c] * k0[c];
-                    aq0 += s[c] * q0[c];
-                    ak1 += s[c] * k1[c];
-                    aq1 += s[c] * q1[c];
-                }
-                U[i0][lane] = beta[i0] * U[i0][lane] - beta[i0] * p[i0] * ak0;
-                sq[k] = aq0;
-                if (i1 < C) {
-                    U[i1][lane] = beta[i1] * U[i1][lane] - beta[i1] * p[i1] * ak1;
-                    sq[k + 1] = aq1;
-                }
+                U[i0][r] = beta[i0] * U[i0][r] - beta[i0] * p[i0] * ak0;
+                Sq[i0][r] = aq0;
+            }
+            if (i1 < C) {
+                U[i1][r] = beta[i1] * U[i1][r] - beta[i1] * p[i1] * ak1;
+                Sq[i1][r] = aq1;
             }
         }
         __syncthreads();
-        // forward substitution (I + M) U = T by wave 0, every lane its own row,
-        // the 32 values in registers
-        float u[CH];
-        if (wave == 0) {
+        // forward substitution (I + M) U = T, a thread per row, in registers
+        if (tid < RB) {
+            float u[CH];
 #pragma unroll
-            for (int i = 0; i < CH; i++) u[i] = i < C ? U[i][lane] : 0.0f;
+            for (int i = 0; i < CH; i++) u[i] = i < C ? U[i][tid] : 0.0f;
 #pragma unroll
             for (int i = 1; i < CH; i++) {
                 if (i < C) {
@@ -352,55 +347,53 @@ oh_k_delta_chunked(const float *qn, const float *kn, const float *conv, const fl
             }
 #pragma unroll
             for (int i = 0; i < CH; i++)
-                if (i < C) U[i][lane] = u[i];
+                if (i < C) U[i][tid] = u[i];
         }
         __syncthreads();
+        // outputs of tokens g and g + 16, scaled by 1/sqrt(dk)
+        {
+            float u[CH];
 #pragma unroll
-        for (int i = 0; i < CH; i++) u[i] = i < C ? U[i][lane] : 0.0f;
-        // outputs of this wave's tokens, scaled by 1/sqrt(dk), with the per-run
-        // sums of squares of the gated RMSNorm
+            for (int j = 0; j < CH; j++) u[j] = j < C ? U[j][r] : 0.0f;
 #pragma unroll
-        for (int k = 0; k < CH / NW; k++) {
-            const int i = wave + NW * k;
-            if (i < C) {
-                float o = p[i] * sq[k];
-                o += W[i][i] * u[i];
+            for (int h = 0; h < 2; h++) {
+                const int i = g + RB * h;
+                if (i < C) {
+                    float o = p[i] * Sq[i][r];
+                    o += W[i][i] * u[i];
 #pragma unroll
-                for (int j = CH - 1; j >= 0; j--)
-                    if (j < i) o += W[i][j] * u[j];
-                o *= out_scale;
-                const int t = c0 + i;
-                const double so = wave_sum_d((double)o * o);
-                stg(out + (size_t)t * vd + hv * DK + r, o);
-                if (lane == 0) stg(out_runs + (size_t)t * (vd / 64) + vb, so);
+                    for (int j = CH - 1; j >= 0; j--)
+                        if (j < i) o += W[i][j] * u[j];
+                    o *= out_scale;
+                    stg(out + (size_t)(c0 + i) * vd + r0 + r, o);
+                }
             }
         }
         // S_out = p_{C-1} S_in + sum_j (p_{C-1}/p_j) u_j k_j^T, j descending:
-        // this wave's CW columns of every row
+        // CPL columns of row ur
         {
             const float pc = p[C - 1];
-            float x[CW];
-            float *xr = xs + lane * XS + wave * CW;
+            float x[CPL];
+            float *xr = xs + ur * XS + ucg * CPL;
 #pragma unroll
-            for (int c = 0; c < CW; c++) x[c] = xr[c] * pc;
+            for (int c = 0; c < CPL; c++) x[c] = xr[c] * pc;
 #pragma unroll
             for (int j = CH - 1; j >= 0; j--) {
                 if (j < C) {
-                    const float ur = wend[j] * u[j];
-                    if (ur != 0.0f) {
-                        const float *kj = kc[j] + wave * CW;
+                    const float uj = wend[j] * U[j][ur];
+                    if (uj != 0.0f) {
 #pragma unroll
-                        for (int c = 0; c < CW; c++) x[c] += ur * kj[c];
+                        for (int c = 0; c < CPL; c++) x[c] += uj * kc[j][ucg * CPL + c];
                     }
                 }
             }
 #pragma unroll
-            for (int c = 0; c < CW; c++) xr[c] = x[c];
+            for (int c = 0; c < CPL; c++) xr[c] = x[c];
         }
         __syncthreads();
         reload();
     }
-    for (int e = tid; e < 64 * DK / 4; e += 256) {
+    for (int e = tid; e < RB * DK / 4; e += 256) {
         const int row = e / (DK / 4), c4 = e - row * (DK / 4);
         stg((float4 *)Srow + e, *(const float4 *)(xs + row * XS + 4 * c4));
     }
@@ -410,16 +403,24 @@ oh_k_delta_chunked(const float *qn, const float *kn, const float *conv, const fl
 // one block per token: per head of gdim elements the runs' sums of squares in
 // order, inv = 1/sqrt(ss/gdim + eps), v = x * inv * w * silu(z); then Q8_K.
 extern "C" __global__ void __launch_bounds__(256)
-oh_k_gnorm_q8k_rows(const float *x, const float *z, const double *runs, const float *w, float eps, int n,
-                    int gdim, int8_t *qs, float *d, int16_t *bs, int8_t *bp) {
+oh_k_gnorm_q8k_rows(const float *x, const float *z, const float *w, float eps, int n, int gdim, int8_t *qs,
+                    float *d, int16_t *bs, int8_t *bp) {
     __shared__ float v[8192];
     __shared__ float hinv[128];
+    __shared__ double runs[128];
     const size_t t = blockIdx.x;
-    const int tid = tid_x(), wave = tid >> 6, nh = n / gdim, rpg = gdim / 64, nqb = n / 256;
+    const int tid = tid_x(), lane = lane_id(), wave = tid >> 6, nh = n / gdim, rpg = gdim / 64, nqb = n / 256;
+    // double sums of squares of each 64-element run (the decode step's
+    // butterfly over its 64 state rows), then per head the runs in order
+    for (int rn = wave; rn < n / 64; rn += 4) {
+        const float o = ldg(x + t * n + rn * 64 + lane);
+        const double so = wave_sum_d((double)o * o);
+        if (lane == 0) runs[rn] = so;
+    }
+    __syncthreads();
     if (tid < nh) {
-        const double *rr = runs + t * (n / 64) + (size_t)tid * rpg;
-        double tot = ldg(rr);
-        for (int k = 1; k < rpg; k++) tot += ldg(rr + k);
+        double tot = runs[tid * rpg];
+        for (int k = 1; k < rpg; k++) tot += runs[tid * rpg + k];
         hinv[tid] = (float)(1.0 / sqrt(tot / (double)gdim + (double)eps));
     }
     __syncthreads();
