@@ -1742,12 +1742,9 @@ static int pf_chunk(ornith_hip_session *s, int base, int T, bool chunked, hipStr
             at.nh = a.nh; at.nkv = a.nkv; at.hd = a.hd; at.cap = s->kvcap; at.exact_max = s->exact_max;
             at.hb = oh_flash_hb(a.nh, a.nkv); at.scale = 1.0f / sqrtf((float)a.hd);
             const int nch = (s->kvcap + oh_flash_chunk() - 1) / oh_flash_chunk();
-            const int nv_ex = a.nh / (256 / a.hd), nv_fl = a.nkv * (a.nh / a.nkv / at.hb) * nch;
-            const int lds_ex = oh_exact_lds_bytes(a.hd, s->exact_max), lds_fl = oh_flash_lds_bytes(a.nh, a.nkv, a.hd);
             const size_t po = (size_t)a.nh * nch * a.hd, pml = (size_t)a.nh * nch * 2;
             for (int t0 = 0; t0 < T; t0 += kPfAttnSub)
-                HCHK(oh_launch_attn_rows(&at, nv_ex > nv_fl ? nv_ex : nv_fl, lds_ex > lds_fl ? lds_ex : lds_fl, base,
-                                         t0, T - t0 < kPfAttnSub ? T - t0 : kPfAttnSub, po, pml, st));
+                HCHK(oh_launch_attn_rows(&at, base, t0, T - t0 < kPfAttnSub ? T - t0 : kPfAttnSub, po, pml, st));
             HCHK(oh_launch_norm_q8k_rows(p.OA, nullptr, 0.0f, aq, T, nullptr, p.OAQ.qs, p.OAQ.d, p.OAQ.bs, st,
                                          p.OAQ.bp));
             CHK(pf_mm(y.o, p.OAQ, p.X, H, T, 1, st));

@@ -131,9 +131,23 @@ hipError_t oh_launch_prep_rows(const oh_op_prep *a, int base, int T, hipStream_t
     hipLaunchKernelGGL(oh_k_prep_rows, dim3(a->nh + a->nkv, T), dim3(256), 0, st, *a, base);
     return hipGetLastError();
 }
-hipError_t oh_launch_attn_rows(const oh_op_attn *a, int nvb_main, int lds, int base, int t0, int n, size_t po_stride,
-                               size_t pml_stride, hipStream_t st) {
-    hipLaunchKernelGGL(oh_k_attn_main_rows, dim3(nvb_main, n), dim3(256), (size_t)lds, st, *a, base, t0, po_stride, pml_stride);
+hipError_t oh_launch_attn_rows(const oh_op_attn *a, int base, int t0, int n, size_t po_stride, size_t pml_stride,
+                               hipStream_t st) {
+    const int lim = a->exact_max < kExactMax ? a->exact_max : kExactMax;
+    if (base + t0 + 1 <= lim)       // some tokens walk exactly
+        hipLaunchKernelGGL(oh_k_attn_exact_rows, dim3(a->nh / (256 / a->hd), n), dim3(256),
+                           (size_t)oh_exact_lds_bytes(a->hd, a->exact_max), st, *a, base, t0);
+    if (base + t0 + n > lim) {      // some tokens take the flash chunks
+        const int nch = (base + t0 + n + kFlashCh - 1) / kFlashCh;
+        const int nvb = a->nkv * (a->nh / a->nkv / a->hb) * nch;
+        const size_t lds = (size_t)oh_flash_lds_bytes(a->nh, a->nkv, a->hd);
+        if (a->hb == 4)
+            hipLaunchKernelGGL(oh_k_attn_flash_rows<4>, dim3(nvb), dim3(256), lds, st, *a, base, t0, n, po_stride, pml_stride);
+        else if (a->hb == 2)
+            hipLaunchKernelGGL(oh_k_attn_flash_rows<2>, dim3(nvb), dim3(256), lds, st, *a, base, t0, n, po_stride, pml_stride);
+        else
+            hipLaunchKernelGGL(oh_k_attn_flash_rows<1>, dim3(nvb), dim3(256), lds, st, *a, base, t0, n, po_stride, pml_stride);
+    }
     hipLaunchKernelGGL(oh_k_attn_combine_rows, dim3(a->nh * (a->hd / 64), n), dim3(256), 0, st, *a, base, t0, po_stride, pml_stride);
     return hipGetLastError();
 }

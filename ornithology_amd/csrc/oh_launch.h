@@ -45,8 +45,8 @@ hipError_t oh_launch_mmq(const oh_mmq *M, int max_items, int pair, hipStream_t s
 hipError_t oh_launch_mmq_items(const int32_t *cnt, int ne, int32_t *items, hipStream_t st);
 bool oh_mmq_can(uint32_t type, int rows, int in);
 hipError_t oh_launch_prep_rows(const oh_op_prep *a, int base, int T, hipStream_t st);
-hipError_t oh_launch_attn_rows(const oh_op_attn *a, int nvb_main, int lds, int base, int t0, int n, size_t po_stride,
-                               size_t pml_stride, hipStream_t st);
+hipError_t oh_launch_attn_rows(const oh_op_attn *a, int base, int t0, int n, size_t po_stride, size_t pml_stride,
+                               hipStream_t st);
 hipError_t oh_launch_route_rows(const float *logits, int ne, int k, const float *shl, int32_t *idx, float *w,
                                 float *shg, int T, hipStream_t st);
 hipError_t oh_launch_group_pairs(const int32_t *idx, int npairs, int32_t *cnt, int ne, int32_t *list, int lstride,

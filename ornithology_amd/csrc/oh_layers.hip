@@ -446,55 +446,73 @@ OH_DEV void exact_body(const oh_op_attn &a, int vb, int pos, int lim, W &w) {
 // parity), and reads each KV byte once per group instead of once per head.
 constexpr int kFlashCh = 64;
 
-// HB query heads of one KV head per virtual block (compile time: the loops
-// over heads unroll); vb = chunk * (nkv * G/HB) + group-block, G = nh/nkv.
-template <int HB, class W>
-OH_DEV void flash_body(const oh_op_attn &a, int vb, int pos, int lim, W &w) {
-    extern __shared__ __align__(16) uint8_t fsm[];
-    const int nh = a.nh, nkv = a.nkv, hd = a.hd, cap = a.cap;
-    const int T = pos + 1;
-    const int G = nh / nkv, ngb = G / HB, gx = nkv * ngb;
-    const int bx = vb % gx, c = vb / gx;
-    const int g = bx / ngb, hb0 = (bx % ngb) * HB;
-    const int t0 = c * kFlashCh;
-    if (T <= lim || t0 >= T) return;
-    if (!w.wait()) return;
-    const int tid = tid_x(), hw = hd / 4, kst = hw + 1;
-    const int nchmax = (cap + kFlashCh - 1) / kFlashCh;
-    const int qst = hd + 16;                                  // head stride: quarters padded by a float4
-    float *q = (float *)fsm;                                  // [HB][4][hd/4 + 4]
-    uint32_t *kc = (uint32_t *)(q + HB * qst);                // [64][hw + 1]
-    const int vto = ((HB * qst + kFlashCh * kst) * 4 + 15) & ~15;
-    uint4 *vt = (uint4 *)(fsm + vto);                         // [4][hd]
-    float *pp = (float *)(vt + (kFlashCh / 16) * hd);         // [HB][64]
-    float *ks = pp + HB * kFlashCh, *vs = ks + kFlashCh;      // [64] each
-    // loads: the block's query heads, the chunk's key words, value tiles, scales
-    for (int k = tid; k < HB * hd; k += 256) {
-        const int h = k / hd, e = k % hd, qq = e / (hd / 4);
-        q[h * qst + qq * (hd / 4 + 4) + e % (hd / 4)] = ldc(a.qr + ((size_t)g * G + hb0) * hd + k);
+// LDS of a flash block: the HB query heads (quarters padded by a float4),
+// the chunk's key words, value tiles, probabilities and scales
+template <int HB> struct FlashLds {
+    float *q, *pp, *ks, *vs;
+    uint32_t *kc;
+    uint4 *vt;
+    int qst, kst;
+    OH_DEV FlashLds(uint8_t *fsm, int hd) {
+        qst = hd + 16;
+        kst = hd / 4 + 1;
+        q = (float *)fsm;                                     // [HB][4][hd/4 + 4]
+        kc = (uint32_t *)(q + HB * qst);                      // [64][hd/4 + 1]
+        const int vto = ((HB * qst + kFlashCh * kst) * 4 + 15) & ~15;
+        vt = (uint4 *)(fsm + vto);                            // [4][hd]
+        pp = (float *)(vt + (kFlashCh / 16) * hd);            // [HB][64]
+        ks = pp + HB * kFlashCh;                              // [64]
+        vs = ks + kFlashCh;                                   // [64]
     }
+};
+
+// the chunk of KV group g starting at t0 (positions past T - 1 read T - 1's)
+template <int HB>
+OH_DEV void flash_tile(const oh_op_attn &a, const FlashLds<HB> &L, int g, int t0, int T) {
+    const int tid = tid_x(), hd = a.hd, hw = hd / 4, cap = a.cap, nkv = a.nkv;
     for (int k = tid; k < hw * kFlashCh; k += 256) {
         const int wi = k / kFlashCh, j = k % kFlashCh;
         const int t = t0 + j < T ? t0 + j : T - 1;
-        kc[j * kst + wi] = ldg(a.Kt + ((size_t)g * hw + wi) * cap + t);
+        L.kc[j * L.kst + wi] = ldg(a.Kt + ((size_t)g * hw + wi) * cap + t);
     }
     for (int k = tid; k < (kFlashCh / 16) * hd; k += 256) {
         const int tt = k / hd, i = k % hd;
         const int tile = (t0 / 16 + tt) * 16 < T ? t0 / 16 + tt : (T - 1) / 16;
-        vt[k] = ldg((const uint4 *)a.Vq + ((size_t)g * (cap / 16) + tile) * hd + i);
+        L.vt[k] = ldg((const uint4 *)a.Vq + ((size_t)g * (cap / 16) + tile) * hd + i);
     }
     if (tid < kFlashCh) {
         const int t = t0 + tid < T ? t0 + tid : T - 1;
-        ks[tid] = ldg(a.Ks + (size_t)t * nkv + g);
-        vs[tid] = ldg(a.Vs + (size_t)t * nkv + g);
+        L.ks[tid] = ldg(a.Ks + (size_t)t * nkv + g);
+        L.vs[tid] = ldg(a.Vs + (size_t)t * nkv + g);
+    }
+}
+
+// One query position of context T against the chunk c in LDS (positions of
+// the tile at or past T score -inf, so they add exact zeros): the HB heads'
+// scores, the chunk statistics (m, l) into part_ml and the unnormalised output
+// into part_o. The queries are read from qsrc (COH: written by another block
+// of the same launch).
+template <int HB, bool COH>
+OH_DEV void flash_token(const oh_op_attn &a, const FlashLds<HB> &L, int g, int hb0, int c, int T, const float *qsrc,
+                        float *part_o, float *part_ml) {
+    const int nh = a.nh, nkv = a.nkv, hd = a.hd, cap = a.cap;
+    const int G = nh / nkv;
+    const int t0 = c * kFlashCh;
+    const int tid = tid_x(), hw = hd / 4;
+    const int nchmax = (cap + kFlashCh - 1) / kFlashCh;
+    const int qst = L.qst, kst = L.kst;
+    for (int k = tid; k < HB * hd; k += 256) {
+        const int h = k / hd, e = k % hd, qq = e / (hd / 4);
+        const float *src = qsrc + ((size_t)g * G + hb0) * hd + k;
+        L.q[h * qst + qq * (hd / 4 + 4) + e % (hd / 4)] = COH ? ldc(src) : ldg(src);
     }
     __syncthreads();
     // scores: thread -> (position j, quarter of the head dimension), the HB
     // heads against its key codes; the quarters are summed with DPP
     {
         const int q4 = tid & 3, j = tid >> 2, wq = hw / 4;
-        const uint32_t *kj = kc + j * kst + q4 * wq;
-        const float4 *q4p = (const float4 *)(q + q4 * (hd / 4 + 4));
+        const uint32_t *kj = L.kc + j * kst + q4 * wq;
+        const float4 *q4p = (const float4 *)(L.q + q4 * (hd / 4 + 4));
         float acc[HB];
 #pragma unroll
         for (int h = 0; h < HB; h++) acc[h] = 0.0f;
@@ -512,7 +530,7 @@ OH_DEV void flash_body(const oh_op_attn &a, int vb, int pos, int lim, W &w) {
                 acc[h] = fmaf(qv.w, c3, acc[h]);
             }
         }
-        const float kss = ks[j];
+        const float kss = L.ks[j];
         const bool valid = t0 + j < T;
 #pragma unroll
         for (int h = 0; h < HB; h++) {
@@ -521,7 +539,7 @@ OH_DEV void flash_body(const oh_op_attn &a, int vb, int pos, int lim, W &w) {
             v += dpp_f<0x4E>(v);
             if (q4 == 0) {
                 const float sc = kss == 0.0f ? 0.0f : v * kss * a.scale;
-                pp[h * kFlashCh + j] = valid ? sc : -INFINITY;
+                L.pp[h * kFlashCh + j] = valid ? sc : -INFINITY;
             }
         }
     }
@@ -532,14 +550,14 @@ OH_DEV void flash_body(const oh_op_attn &a, int vb, int pos, int lim, W &w) {
     for (int h0 = 0; h0 < HB; h0 += 4) {
         const int h = h0 + wave;
         if (h < HB) {
-            const float sv = pp[h * kFlashCh + lane];
+            const float sv = L.pp[h * kFlashCh + lane];
             const float m = wave_max_fast(sv);
             const float e = sv == -INFINITY ? 0.0f : __expf(sv - m);
             float l = e;
             for (int mm = 32; mm >= 1; mm >>= 1) l += shfl_xor(l, mm);
-            pp[h * kFlashCh + lane] = e * vs[lane];
+            L.pp[h * kFlashCh + lane] = e * L.vs[lane];
             if (lane == 0) {
-                float *ml = a.part_ml + (((size_t)g * nchmax + c) * G + hb0 + h) * 2;
+                float *ml = part_ml + (((size_t)g * nchmax + c) * G + hb0 + h) * 2;
                 stc(ml, m);
                 stc(ml + 1, l);
             }
@@ -552,10 +570,10 @@ OH_DEV void flash_body(const oh_op_attn &a, int vb, int pos, int lim, W &w) {
         float o[HB];
 #pragma unroll
         for (int k = 0; k < HB; k++) o[k] = 0.0f;
-        const float4 *pp4 = (const float4 *)pp;
+        const float4 *pp4 = (const float4 *)L.pp;
 #pragma unroll 1
         for (int tt = 0; tt < kFlashCh / 16; tt++) {
-            const uint4 cw = vt[tt * hd + i];
+            const uint4 cw = L.vt[tt * hd + i];
 #pragma unroll
             for (int j4 = 0; j4 < 4; j4++) {
                 const uint32_t wd = wsel(cw, j4);
@@ -575,9 +593,27 @@ OH_DEV void flash_body(const oh_op_attn &a, int vb, int pos, int lim, W &w) {
 #pragma unroll
         for (int k = 0; k < HB; k++) {
             const int h = h1 + hs * k;
-            if (h < HB) stc(a.part_o + (((size_t)g * nchmax + c) * G + hb0 + h) * hd + i, o[k]);
+            if (h < HB) stc(part_o + (((size_t)g * nchmax + c) * G + hb0 + h) * hd + i, o[k]);
         }
     }
+}
+
+// HB query heads of one KV head per virtual block (compile time: the loops
+// over heads unroll); vb = chunk * (nkv * G/HB) + group-block, G = nh/nkv.
+template <int HB, class W>
+OH_DEV void flash_body(const oh_op_attn &a, int vb, int pos, int lim, W &w) {
+    extern __shared__ __align__(16) uint8_t fsm[];
+    const int nh = a.nh, nkv = a.nkv;
+    const int T = pos + 1;
+    const int G = nh / nkv, ngb = G / HB, gx = nkv * ngb;
+    const int bx = vb % gx, c = vb / gx;
+    const int g = bx / ngb, hb0 = (bx % ngb) * HB;
+    const int t0 = c * kFlashCh;
+    if (T <= lim || t0 >= T) return;
+    if (!w.wait()) return;
+    const FlashLds<HB> L(fsm, a.hd);
+    flash_tile<HB>(a, L, g, t0, T);
+    flash_token<HB, true>(a, L, g, hb0, c, T, a.qr, a.part_o, a.part_ml);
 }
 
 // The attention of the current step: up to lim = min(exact_max, kExactMax)

@@ -445,17 +445,43 @@ extern "C" __global__ void __launch_bounds__(256) oh_k_prep_rows(oh_op_prep a, i
 }
 
 // tokens t0 + blockIdx.y; flash partials per token at part + (blockIdx.y) * pstride
-extern "C" __global__ void __launch_bounds__(256)
-oh_k_attn_main_rows(oh_op_attn a, int base, int t0, size_t po_stride, size_t pml_stride) {
+// exact walks of the sub-batch's tokens whose context is at most lim (the
+// others exit): token t0 + blockIdx.y at position base + t0 + blockIdx.y
+extern "C" __global__ void __launch_bounds__(256) oh_k_attn_exact_rows(oh_op_attn a, int base, int t0) {
     NoWait w;
     const int t = t0 + (int)blockIdx.y, qd = a.nh * a.hd;
+    const int lim = a.exact_max < kExactMax ? a.exact_max : kExactMax;
     oh_op_attn b = a;
     b.qr = a.qr + (size_t)t * qd;
     b.gate = a.gate + (size_t)t * qd;
     b.out = a.out + (size_t)t * qd;
-    b.part_o = a.part_o + (size_t)blockIdx.y * po_stride;
-    b.part_ml = a.part_ml + (size_t)blockIdx.y * pml_stride;
-    attn_main_body(b, (int)blockIdx.x, base + t, w);
+    exact_body(b, (int)blockIdx.x, base + t, lim, w);
+}
+
+// flash chunks of the n tokens t0.. of a sub-batch: each block stages its KV
+// chunk once (up to the last token's context) and runs flash_token for every
+// token whose context exceeds lim and reaches the chunk; the per-token
+// arithmetic is the decode step's, and the tile positions a token cannot see
+// score -inf (exact zeros), so each token's partials equal the decode step's
+template <int HB>
+__global__ void __launch_bounds__(256)
+oh_k_attn_flash_rows(oh_op_attn a, int base, int t0, int n, size_t po_stride, size_t pml_stride) {
+    extern __shared__ __align__(16) uint8_t fsm[];
+    const int lim = a.exact_max < kExactMax ? a.exact_max : kExactMax;
+    const int G = a.nh / a.nkv, ngb = G / HB, gx = a.nkv * ngb;
+    const int vb = (int)blockIdx.x, bx = vb % gx, c = vb / gx;
+    const int g = bx / ngb, hb0 = (bx % ngb) * HB, tc0 = c * kFlashCh;
+    const int Tmax = base + t0 + n, qd = a.nh * a.hd;
+    if (Tmax <= lim || tc0 >= Tmax) return;
+    const FlashLds<HB> L(fsm, a.hd);
+    flash_tile<HB>(a, L, g, tc0, Tmax);
+    for (int k = 0; k < n; k++) {
+        const int T = base + t0 + k + 1;
+        if (T <= lim || tc0 >= T) continue;
+        flash_token<HB, false>(a, L, g, hb0, c, T, a.qr + (size_t)(t0 + k) * qd, a.part_o + (size_t)k * po_stride,
+                               a.part_ml + (size_t)k * pml_stride);
+        __syncthreads();                                // q and the probabilities are reused
+    }
 }
 
 extern "C" __global__ void __launch_bounds__(256)
