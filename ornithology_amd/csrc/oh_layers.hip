@@ -487,12 +487,19 @@ OH_DEV void flash_tile(const oh_op_attn &a, const FlashLds<HB> &L, int g, int t0
     }
 }
 
+// element k < HB * hd of the block's query heads into the LDS layout
+template <int HB>
+OH_DEV void flash_q_put(const FlashLds<HB> &L, int hd, int k, float v) {
+    const int h = k / hd, e = k % hd, qq = e / (hd / 4);
+    L.q[h * L.qst + qq * (hd / 4 + 4) + e % (hd / 4)] = v;
+}
+
 // One query position of context T against the chunk c in LDS (positions of
 // the tile at or past T score -inf, so they add exact zeros): the HB heads'
 // scores, the chunk statistics (m, l) into part_ml and the unnormalised output
-// into part_o. The queries are read from qsrc (COH: written by another block
-// of the same launch).
-template <int HB, bool COH>
+// into part_o. LOADQ: the queries are read from qsrc (COH: written by another
+// block of the same launch); otherwise the caller has put them into LDS.
+template <int HB, bool COH, bool LOADQ = true>
 OH_DEV void flash_token(const oh_op_attn &a, const FlashLds<HB> &L, int g, int hb0, int c, int T, const float *qsrc,
                         float *part_o, float *part_ml) {
     const int nh = a.nh, nkv = a.nkv, hd = a.hd, cap = a.cap;
@@ -501,10 +508,11 @@ OH_DEV void flash_token(const oh_op_attn &a, const FlashLds<HB> &L, int g, int h
     const int tid = tid_x(), hw = hd / 4;
     const int nchmax = (cap + kFlashCh - 1) / kFlashCh;
     const int qst = L.qst, kst = L.kst;
-    for (int k = tid; k < HB * hd; k += 256) {
-        const int h = k / hd, e = k % hd, qq = e / (hd / 4);
-        const float *src = qsrc + ((size_t)g * G + hb0) * hd + k;
-        L.q[h * qst + qq * (hd / 4 + 4) + e % (hd / 4)] = COH ? ldc(src) : ldg(src);
+    if (LOADQ) {
+        for (int k = tid; k < HB * hd; k += 256) {
+            const float *src = qsrc + ((size_t)g * G + hb0) * hd + k;
+            flash_q_put<HB>(L, hd, k, COH ? ldc(src) : ldg(src));
+        }
     }
     __syncthreads();
     // scores: thread -> (position j, quarter of the head dimension), the HB

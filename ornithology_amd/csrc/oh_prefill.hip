@@ -475,11 +475,25 @@ oh_k_attn_flash_rows(oh_op_attn a, int base, int t0, int n, size_t po_stride, si
     if (Tmax <= lim || tc0 >= Tmax) return;
     const FlashLds<HB> L(fsm, a.hd);
     flash_tile<HB>(a, L, g, tc0, Tmax);
-    for (int k = 0; k < n; k++) {
-        const int T = base + t0 + k + 1;
-        if (T <= lim || tc0 >= T) continue;
-        flash_token<HB, false>(a, L, g, hb0, c, T, a.qr + (size_t)(t0 + k) * qd, a.part_o + (size_t)k * po_stride,
-                               a.part_ml + (size_t)k * pml_stride);
+    // the first token that uses this chunk; each token's queries are requested
+    // into registers while the previous token computes
+    int k = 0;
+    while (k < n && (base + t0 + k + 1 <= lim || tc0 >= base + t0 + k + 1)) k++;
+    const int tid = tid_x(), nq = HB * a.hd;
+    float qv[4];
+    auto qload = [&](int kk) {
+        const float *src = a.qr + (size_t)(t0 + kk) * qd + ((size_t)g * G + hb0) * a.hd;
+#pragma unroll
+        for (int m = 0; m < 4; m++) qv[m] = tid + 256 * m < nq ? ldg(src + tid + 256 * m) : 0.0f;
+    };
+    if (k < n) qload(k);
+    for (; k < n; k++) {
+#pragma unroll
+        for (int m = 0; m < 4; m++)
+            if (tid + 256 * m < nq) flash_q_put<HB>(L, a.hd, tid + 256 * m, qv[m]);
+        if (k + 1 < n) qload(k + 1);
+        flash_token<HB, false, false>(a, L, g, hb0, c, base + t0 + k + 1, nullptr, a.part_o + (size_t)k * po_stride,
+                                      a.part_ml + (size_t)k * pml_stride);
         __syncthreads();                                // q and the probabilities are reused
     }
 }
