@@ -87,6 +87,7 @@ _SIGS = {
     "ornith_hip_session_pos": (C.c_int, [_vp]),
     "ornith_hip_session_generate": (C.c_int, [_vp, C.c_int, _ip, _ip]),
     "ornith_hip_session_step": (C.c_int, [_vp, C.c_int32]),
+    "ornith_hip_batch_step": (C.c_int, [C.POINTER(_vp), C.c_int, _ip, _ip]),
     "ornith_hip_session_get_delta": (C.c_int, [_vp, C.c_int, _fp]),
     "ornith_hip_session_get_conv": (C.c_int, [_vp, C.c_int, _fp]),
     "ornith_hip_session_get_kv": (C.c_int, [_vp, C.c_int, _vp, _fp, _vp, _fp]),
@@ -269,6 +270,18 @@ class Model:
         h = _vp()
         _check(lib().ornith_hip_session_new(self.h, cap, C.byref(h)), "ornith_hip_session_new")
         return Session(self, h)
+
+    def batch_step(self, sessions, tokens) -> np.ndarray:
+        """One token step of each session at once (ornith_hip_batch_step);
+        returns each session's greedy next token."""
+        n = len(sessions)
+        hs = (_vp * n)(*[s.h for s in sessions])
+        t = np.ascontiguousarray(tokens, np.int32)
+        if t.size != n:
+            raise ValueError(f"batch_step: {n} sessions, {t.size} tokens")
+        out = np.zeros(n, np.int32)
+        _check(lib().ornith_hip_batch_step(hs, n, _i32(t), _i32(out)), "ornith_hip_batch_step")
+        return out
 
     def free(self):
         if self.h:

@@ -992,6 +992,19 @@ struct ornith_hip_session {
         int32_t *ITEMS = nullptr;
         Q8Buf XQ, OQ, OAQ, HQ, HSQ;
     } pf;
+    // batch decode led by this session: buffers for up to bw_n sessions
+    struct Bw {
+        int n = 0;
+        float *X = nullptr, *CAT = nullptr, *Z = nullptr, *AB = nullptr, *O = nullptr, *OG = nullptr;
+        double *RUNS = nullptr;
+        float *QP = nullptr, *KB = nullptr, *VB = nullptr, *QR = nullptr, *AG = nullptr, *OA = nullptr;
+        float *RL = nullptr, *SHL = nullptr, *SHG = nullptr, *RW = nullptr, *LOGITS = nullptr;
+        int32_t *RIDX = nullptr, *CNT = nullptr, *LIST = nullptr, *ITEMS = nullptr, *IDX = nullptr;
+        float *Hh = nullptr, *HSH = nullptr, *OD = nullptr, *ODSH = nullptr, *GU = nullptr, *GSH = nullptr;
+        uint8_t *OPS = nullptr;
+        size_t ops_bytes = 0;
+        Q8Buf XQ, OQ, OAQ, HQ, HSQ;
+    } bw;
     std::vector<int> sp_body_rk;
     int step_grid = 0;
     bool step_tried = false;
@@ -1846,6 +1859,207 @@ static int session_eval(ornith_hip_session *s, const int32_t *tokens, int n, boo
     CHK(step_check(s));
     s->pos += n;
     s->have_logits = true;
+    return ORNITH_HIP_OK;
+}
+
+// ---- decode of several sessions at once -------------------------------------------------
+// One token step (rforward_token, src/ornith_rforward.c:686-706) for each of n
+// sessions of one model: the projections batched over the sessions
+// (matmul_batch_q's Tn columns, src/ornith_rforward.c:91-196), the recurrent
+// state, KV cache and attention of each session by the decode step's own
+// kernels. Each column's arithmetic is its session's token step.
+static int bw_alloc(ornith_hip_session *s, int n, size_t ops_bytes) {
+    auto &p = s->bw;
+    if (p.n >= n && p.ops_bytes >= ops_bytes) return ORNITH_HIP_OK;
+    const ornith_hip_arch &a = s->m->a;
+    const size_t N = (size_t)(n > p.n ? n : p.n), H = a.hidden, qd = (size_t)a.nk * a.dk, vd = (size_t)a.nv * a.dv;
+    const size_t cc = 2 * qd + vd, aq = (size_t)a.nh * a.hd, kvd = (size_t)a.nkv * a.hd;
+    const size_t K = a.top_k > 0 ? a.top_k : 1, I = a.moe_inter > 0 ? a.moe_inter : 1;
+    const size_t sI = a.shared_inter > 0 ? a.shared_inter : 1, ne = a.ne > 0 ? a.ne : 1;
+    CHK(salloc(s, &p.X, N * H)); CHK(q8alloc(s, p.XQ, N * H));
+    CHK(salloc(s, &p.CAT, N * cc + 1)); CHK(salloc(s, &p.Z, N * vd + 1)); CHK(salloc(s, &p.AB, N * 2 * a.nv + 1));
+    CHK(salloc(s, &p.O, N * vd + 1)); CHK(salloc(s, &p.OG, N * vd + 1)); CHK(salloc(s, &p.RUNS, N * (vd / 64) + 1));
+    CHK(q8alloc(s, p.OQ, N * vd + 256));
+    CHK(salloc(s, &p.QP, N * 2 * aq + 1)); CHK(salloc(s, &p.KB, N * kvd + 1)); CHK(salloc(s, &p.VB, N * kvd + 1));
+    CHK(salloc(s, &p.QR, N * aq + 1)); CHK(salloc(s, &p.AG, N * aq + 1)); CHK(salloc(s, &p.OA, N * aq + 1));
+    CHK(q8alloc(s, p.OAQ, N * aq + 256));
+    CHK(salloc(s, &p.RL, N * ne)); CHK(salloc(s, &p.SHL, N)); CHK(salloc(s, &p.SHG, N));
+    CHK(salloc(s, &p.RW, N * K)); CHK(salloc(s, &p.RIDX, N * K));
+    CHK(salloc(s, &p.CNT, ne)); CHK(salloc(s, &p.LIST, ne * N));
+    CHK(salloc(s, &p.ITEMS, (N * K + 63) / 64 + ne + 2));
+    CHK(salloc(s, &p.Hh, N * K * I)); CHK(q8alloc(s, p.HQ, N * K * I + 256));
+    CHK(salloc(s, &p.HSH, N * sI)); CHK(q8alloc(s, p.HSQ, N * sI + 256));
+    CHK(salloc(s, &p.GU, N * K * 2 * I)); CHK(salloc(s, &p.GSH, N * 2 * sI));
+    CHK(salloc(s, &p.OD, N * K * H)); CHK(salloc(s, &p.ODSH, N * H));
+    CHK(salloc(s, &p.LOGITS, N * (size_t)a.vocab)); CHK(salloc(s, &p.IDX, 3 * N + 1));
+    const size_t ob = ops_bytes > p.ops_bytes ? ops_bytes : p.ops_bytes;
+    CHK(salloc(s, &p.OPS, ob));
+    p.ops_bytes = ob;
+    p.n = (int)N;
+    return ORNITH_HIP_OK;
+}
+
+extern "C" int ornith_hip_batch_step(ornith_hip_session **ss, int n, const int32_t *tokens, int32_t *next) {
+    if (n <= 0) return ORNITH_HIP_OK;
+    if (!ss || !tokens) { seterr("batch_step: null sessions or tokens"); return ORNITH_HIP_ERR_FORMAT; }
+    ornith_hip_session *s0 = ss[0];
+    const ornith_hip_model *m = s0->m;
+    const ornith_hip_arch &a = m->a;
+    for (int b = 0; b < n; b++) {
+        if (!ss[b] || ss[b]->m != m) { seterr("batch_step: session %d is not of the first session's model", b); return ORNITH_HIP_ERR_FORMAT; }
+        for (int c = 0; c < b; c++)
+            if (ss[c] == ss[b]) { seterr("batch_step: session %d appears twice", b); return ORNITH_HIP_ERR_FORMAT; }
+        if (ss[b]->pos + 1 > ss[b]->cap) {
+            seterr("session capacity %d exceeded (pos %d + 1 token) in batch slot %d", ss[b]->cap, ss[b]->pos, b);
+            return ORNITH_HIP_ERR_UNSUPPORTED;
+        }
+        if (tokens[b] < 0 || tokens[b] >= a.vocab) {
+            seterr("token %d in batch slot %d outside the vocabulary (%d)", tokens[b], b, a.vocab);
+            return ORNITH_HIP_ERR_FORMAT;
+        }
+    }
+    if (!pf_supported(m) || !oh_qdot_can(m->lm_head->type, m->lm_head->in) || m->lm_head->in > 8192) {
+        seterr("batch_step: the model is outside the batched projection path (widths <= 8192, integer dot types)");
+        return ORNITH_HIP_ERR_UNSUPPORTED;
+    }
+    HCHK(hipSetDevice(m->ctx->device));
+    hipStream_t st = m->ctx->st;
+    const int H = a.hidden, qd = a.nk * a.dk, vd = a.nv * a.dv, cc = 2 * qd + vd, aq = a.nh * a.hd;
+    const int kvd = a.nkv * a.hd;
+    // per-layer descriptors of every session: delta ops (linear layers) or
+    // prep + attention ops (full layers), n of each, then tokens and positions
+    size_t ob = 0;
+    std::vector<size_t> lofs((size_t)a.n_layers);
+    for (int l = 0; l < a.n_layers; l++) {
+        lofs[l] = ob;
+        ob += m->L[l].full ? (size_t)n * (sizeof(oh_op_prep) + sizeof(oh_op_attn)) : (size_t)n * sizeof(oh_op_delta);
+        ob = (ob + 15) & ~(size_t)15;
+    }
+    const size_t tok_ofs = ob;
+    ob += (size_t)n * 8 + 16;
+    CHK(bw_alloc(s0, n, ob));
+    auto &p = s0->bw;
+    std::vector<uint8_t> host(ob, 0);
+    int nvb_main = 1, lds_main = 0;
+    for (int l = 0; l < a.n_layers; l++) {
+        const OhLayer &y = m->L[l];
+        uint8_t *dst = host.data() + lofs[l];
+        for (int b = 0; b < n; b++) {
+            ornith_hip_session *sb = ss[b];
+            const LayerState &z = sb->ls[l];
+            if (y.full) {
+                oh_op_prep pr = {p.QP + (size_t)b * 2 * aq, p.KB + (size_t)b * kvd, p.VB + (size_t)b * kvd,
+                                 (const float *)y.q_norm->A, (const float *)y.k_norm->A, (const float *)sb->rope,
+                                 p.QR + (size_t)b * aq, p.AG + (size_t)b * aq, z.Kt, z.Ks, z.Vq, z.Vs,
+                                 a.nh, a.nkv, a.hd, a.rope_dim, sb->kvcap, a.eps};
+                memcpy(dst + (size_t)b * sizeof(oh_op_prep), &pr, sizeof pr);
+                oh_op_attn at;
+                memset(&at, 0, sizeof at);
+                at.qr = p.QR + (size_t)b * aq; at.gate = p.AG + (size_t)b * aq;
+                at.Kt = z.Kt; at.Ks = z.Ks; at.Vq = z.Vq; at.Vs = z.Vs;
+                at.scores = sb->scores; at.part_o = sb->fpo; at.part_ml = sb->fpml; at.out = p.OA + (size_t)b * aq;
+                at.nh = a.nh; at.nkv = a.nkv; at.hd = a.hd; at.cap = sb->kvcap; at.exact_max = sb->exact_max;
+                at.hb = oh_flash_hb(a.nh, a.nkv); at.scale = 1.0f / sqrtf((float)a.hd);
+                memcpy(dst + (size_t)n * sizeof(oh_op_prep) + (size_t)b * sizeof(oh_op_attn), &at, sizeof at);
+                const int nch = (sb->kvcap + oh_flash_chunk() - 1) / oh_flash_chunk();
+                const int nv_ex = a.nh / (256 / a.hd), nv_fl = a.nkv * (a.nh / a.nkv / at.hb) * nch;
+                const int lds_ex = oh_exact_lds_bytes(a.hd, sb->exact_max), lds_fl = oh_flash_lds_bytes(a.nh, a.nkv, a.hd);
+                nvb_main = std::max(nvb_main, std::max(nv_ex, nv_fl));
+                lds_main = std::max(lds_main, std::max(lds_ex, lds_fl));
+            } else {
+                oh_op_delta d = {p.CAT + (size_t)b * cc, p.AB + (size_t)b * 2 * a.nv, p.Z + (size_t)b * vd,
+                                 (const float *)y.conv->A, (const float *)y.ssm_a->A, (const float *)y.dt_bias->A,
+                                 z.conv, z.S, p.O + (size_t)b * vd, p.OG + (size_t)b * vd,
+                                 p.RUNS + (size_t)b * (vd / 64), a.dk, a.nk, a.nv, a.conv_k, cc,
+                                 1.0f / sqrtf((float)a.dk)};
+                memcpy(dst + (size_t)b * sizeof(oh_op_delta), &d, sizeof d);
+            }
+        }
+    }
+    int32_t *htp = (int32_t *)(host.data() + tok_ofs);
+    for (int b = 0; b < n; b++) { htp[b] = tokens[b]; htp[n + b] = ss[b]->pos; }
+    HCHK(hipMemcpyAsync(p.OPS, host.data(), ob, hipMemcpyHostToDevice, st));
+    const int32_t *dtok = (const int32_t *)(p.OPS + tok_ofs), *dpos = dtok + n;
+    for (int b = 0; b < n; b++)   // the token also goes into the session's history
+        HCHK(hipMemcpyAsync(ss[b]->toks + ss[b]->pos, tokens + b, 4, hipMemcpyHostToDevice, st));
+
+    oh_op_embed emb = {m->embd->A, m->embd->B, m->embd->C, dtok, p.X, (int)m->embd->type, H};
+    HCHK(oh_launch_embed_rows(&emb, 0, n, st));
+    for (int l = 0; l < a.n_layers; l++) {
+        const OhLayer &y = m->L[l];
+        const uint8_t *dops = p.OPS + lofs[l];
+        HCHK(oh_launch_norm_q8k_rows(p.X, (const float *)y.attn_norm->A, a.eps, H, n, nullptr, p.XQ.qs, p.XQ.d,
+                                     p.XQ.bs, st, p.XQ.bp));
+        if (y.full) {
+            CHK(pf_mm(y.q, p.XQ, p.QP, 2 * aq, n, 0, st));
+            CHK(pf_mm(y.k, p.XQ, p.KB, kvd, n, 0, st));
+            CHK(pf_mm(y.v, p.XQ, p.VB, kvd, n, 0, st));
+            const oh_op_prep *pops = (const oh_op_prep *)dops;
+            const oh_op_attn *aops = (const oh_op_attn *)(dops + (size_t)n * sizeof(oh_op_prep));
+            HCHK(oh_launch_prep_batch(pops, dpos, n, a.nh, a.nkv, st));
+            HCHK(oh_launch_attn_batch(aops, dpos, n, nvb_main, lds_main, a.nh, a.hd, st));
+            HCHK(oh_launch_norm_q8k_rows(p.OA, nullptr, 0.0f, aq, n, nullptr, p.OAQ.qs, p.OAQ.d, p.OAQ.bs, st,
+                                         p.OAQ.bp));
+            CHK(pf_mm(y.o, p.OAQ, p.X, H, n, 1, st));
+        } else {
+            CHK(pf_mm(y.qkv, p.XQ, p.CAT, cc, n, 0, st));
+            CHK(pf_mm(y.gate, p.XQ, p.Z, vd, n, 0, st));
+            CHK(pf_mm(y.alpha, p.XQ, p.AB, 2 * a.nv, n, 0, st));
+            CHK(pf_mm(y.beta, p.XQ, p.AB + a.nv, 2 * a.nv, n, 0, st));
+            HCHK(oh_launch_delta_batch((const oh_op_delta *)dops, dpos, n, a.dk, a.conv_k, a.nv, st));
+            HCHK(oh_launch_gnorm_q8k_rows(p.O, p.Z, (const float *)y.ssm_norm->A, a.eps, vd, a.dv, n, p.OQ.qs,
+                                          p.OQ.d, p.OQ.bs, st, p.OQ.bp));
+            CHK(pf_mm(y.ssm_out, p.OQ, p.X, H, n, 1, st));
+        }
+        HCHK(oh_launch_norm_q8k_rows(p.X, (const float *)y.post_norm->A, a.eps, H, n, nullptr, p.XQ.qs, p.XQ.d,
+                                     p.XQ.bs, st, p.XQ.bp));
+        if (a.ne > 0) {
+            const int K = a.top_k, I = a.moe_inter, sI = a.shared_inter;
+            CHK(pf_mm(y.router, p.XQ, p.RL, a.ne, n, 0, st));
+            if (y.gate_inp_sh) CHK(pf_mm(y.gate_inp_sh, p.XQ, p.SHL, 1, n, 0, st));
+            HCHK(oh_launch_route_rows(p.RL, a.ne, K, y.gate_inp_sh ? p.SHL : nullptr, p.RIDX, p.RW,
+                                      y.gate_inp_sh ? p.SHG : nullptr, n, st));
+            HCHK(oh_launch_group_pairs(p.RIDX, n * K, p.CNT, a.ne, p.LIST, n, st));
+            const int max_items = (n * K + 63) / 64 + a.ne;
+            HCHK(oh_launch_mmq_items(p.CNT, a.ne, p.ITEMS, st));
+            CHK(pf_swiglu(y.gate_exps, y.up_exps, p.XQ, I, n * K, n, p.HQ, p.GU, p.Hh, st, p.CNT, p.LIST, n, K, a.ne,
+                          p.ITEMS, max_items));
+            if (pf_use_mmq(y.down_exps, true))
+                CHK(pf_mmq(y.down_exps, nullptr, p.HQ, p.OD, H, n, 0, st, p.CNT, p.LIST, n, 1, p.ITEMS, max_items));
+            else
+                CHK(pf_mvb(y.down_exps, nullptr, p.HQ, p.OD, H, n, 0, st, p.CNT, p.LIST, n, 1, a.ne));
+            if (y.gate_sh) {
+                CHK(pf_swiglu(y.gate_sh, y.up_sh, p.XQ, sI, n, n, p.HSQ, p.GSH, p.HSH, st));
+                CHK(pf_mm(y.down_sh, p.HSQ, p.ODSH, H, n, 0, st));
+            }
+            HCHK(oh_launch_moe_combine_rows(p.X, p.OD, p.RW, K, H, y.gate_sh ? p.ODSH : nullptr,
+                                            y.gate_inp_sh ? p.SHG : nullptr, n, st));
+        } else {
+            CHK(pf_swiglu(y.ffn_gate, y.ffn_up, p.XQ, a.shared_inter, n, n, p.HSQ, p.GSH, p.HSH, st));
+            CHK(pf_mm(y.ffn_down, p.HSQ, p.X, H, n, 1, st));
+        }
+    }
+    // head: output norm, lm_head over the n columns, each session's logits and
+    // greedy token
+    HCHK(oh_launch_norm_q8k_rows(p.X, (const float *)m->out_norm->A, a.eps, H, n, nullptr, p.XQ.qs, p.XQ.d,
+                                 p.XQ.bs, st, p.XQ.bp));
+    CHK(pf_mm(m->lm_head, p.XQ, p.LOGITS, a.vocab, n, 0, st));
+    HCHK(oh_launch_argmax_rows(p.LOGITS, a.vocab, n, p.IDX, st));
+    for (int b = 0; b < n; b++) {
+        HCHK(hipMemcpyAsync(ss[b]->logits, p.LOGITS + (size_t)b * a.vocab, (size_t)a.vocab * 4,
+                            hipMemcpyDeviceToDevice, st));
+        // the greedy token at the next position, where the token step's head
+        // leaves it (session_generate continues from there)
+        HCHK(hipMemcpyAsync(ss[b]->toks + ss[b]->pos + 1, p.IDX + b, 4, hipMemcpyDeviceToDevice, st));
+    }
+    std::vector<int32_t> hn((size_t)n);
+    HCHK(hipMemcpyAsync(hn.data(), p.IDX, (size_t)n * 4, hipMemcpyDeviceToHost, st));
+    HCHK(hipStreamSynchronize(st));
+    for (int b = 0; b < n; b++) {
+        ss[b]->pos += 1;
+        ss[b]->have_logits = true;
+        if (next) next[b] = hn[b];
+    }
     return ORNITH_HIP_OK;
 }
 

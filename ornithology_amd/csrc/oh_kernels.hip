@@ -6,6 +6,7 @@
 #include "oh_step.hip"
 #include "oh_prefill.hip"
 #include "oh_mmq.hip"
+#include "oh_batch.hip"
 #include "oh_launch.h"
 
 extern "C" {
@@ -99,6 +100,36 @@ hipError_t oh_launch_delta_chunked(int dk, const float *qn, const float *kn, con
     } else {
         return hipErrorInvalidValue;
     }
+    return hipGetLastError();
+}
+hipError_t oh_launch_delta_batch(const oh_op_delta *ops, const int32_t *pos, int n, int dk, int K, int nv,
+                                 hipStream_t st) {
+    if (K > 8) return hipErrorInvalidValue;
+    if (dk == 128) {
+        const dim3 g(nv * 2, n);
+        if (K <= 4) hipLaunchKernelGGL((oh_k_delta_batch<128, 4>), g, dim3(64), 0, st, ops, pos);
+        else hipLaunchKernelGGL((oh_k_delta_batch<128, 8>), g, dim3(64), 0, st, ops, pos);
+    } else if (dk == 64) {
+        const dim3 g(nv, n);
+        if (K <= 4) hipLaunchKernelGGL((oh_k_delta_batch<64, 4>), g, dim3(64), 0, st, ops, pos);
+        else hipLaunchKernelGGL((oh_k_delta_batch<64, 8>), g, dim3(64), 0, st, ops, pos);
+    } else {
+        return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+hipError_t oh_launch_prep_batch(const oh_op_prep *ops, const int32_t *pos, int n, int nh, int nkv, hipStream_t st) {
+    hipLaunchKernelGGL(oh_k_prep_batch, dim3(nh + nkv, n), dim3(256), 0, st, ops, pos);
+    return hipGetLastError();
+}
+hipError_t oh_launch_attn_batch(const oh_op_attn *ops, const int32_t *pos, int n, int nvb_main, int lds, int nh,
+                                int hd, hipStream_t st) {
+    hipLaunchKernelGGL(oh_k_attn_main_batch, dim3(nvb_main, n), dim3(256), (size_t)lds, st, ops, pos);
+    hipLaunchKernelGGL(oh_k_attn_combine_batch, dim3(nh * (hd / 64), n), dim3(256), 0, st, ops, pos);
+    return hipGetLastError();
+}
+hipError_t oh_launch_argmax_rows(const float *v, int n, int rows, int32_t *out, hipStream_t st) {
+    hipLaunchKernelGGL(oh_k_argmax_rows, dim3(rows), dim3(256), 0, st, v, n, out);
     return hipGetLastError();
 }
 bool oh_mmq_can(uint32_t type, int rows, int in) {

@@ -44,6 +44,14 @@ hipError_t oh_launch_gnorm_q8k_rows(const float *x, const float *z, const float 
 hipError_t oh_launch_mmq(const oh_mmq *M, int max_items, int pair, hipStream_t st);
 hipError_t oh_launch_mmq_items(const int32_t *cnt, int ne, int32_t *items, hipStream_t st);
 bool oh_mmq_can(uint32_t type, int rows, int in);
+// decode of n sessions at once: the decode bodies, one grid row per session,
+// descriptors and positions in device arrays of n
+hipError_t oh_launch_delta_batch(const oh_op_delta *ops, const int32_t *pos, int n, int dk, int K, int nv,
+                                 hipStream_t st);
+hipError_t oh_launch_prep_batch(const oh_op_prep *ops, const int32_t *pos, int n, int nh, int nkv, hipStream_t st);
+hipError_t oh_launch_attn_batch(const oh_op_attn *ops, const int32_t *pos, int n, int nvb_main, int lds, int nh,
+                                int hd, hipStream_t st);
+hipError_t oh_launch_argmax_rows(const float *v, int n, int rows, int32_t *out, hipStream_t st);
 hipError_t oh_launch_prep_rows(const oh_op_prep *a, int base, int T, hipStream_t st);
 hipError_t oh_launch_attn_rows(const oh_op_attn *a, int base, int t0, int n, size_t po_stride, size_t pml_stride,
                                hipStream_t st);

@@ -1,0 +1,87 @@
+"""GPU: decode of several sessions at once (ornith_hip_batch_step) against
+each session's own token step (ornith_hip_session_step = rforward_token).
+
+Bar: every session's logits after every batch step bit-identical to the same
+session stepped alone, and the greedy tokens identical, on C1 (Q8_0) and on
+Q4_K/Q6_K MoE and dense models; sessions at different positions, on the exact
+and flash attention paths; a session that joins or leaves between steps."""
+import numpy as np
+import pytest
+
+import clibs
+
+pytestmark = pytest.mark.gpu
+
+MIX = dict(clibs.C1, hidden=768, n_layers=4, vocab=1000, nh=4, nkv=1, hd=128, nk=2, nv=4, dhead=128,
+           ne=8, top_k=2, moe_inter=512, shared_inter=512, t_default=clibs.Q4_K, t_attn_v=clibs.Q6_K,
+           t_ffn_down=clibs.Q6_K, t_output=clibs.Q6_K, t_embd=clibs.Q4_K, seed=5)
+DENSE = dict(MIX, ne=0, top_k=0, moe_inter=0, shared_inter=1024, seed=7)
+CFGS = {"c1": clibs.C1, "moe": MIX, "dense": DENSE}
+
+
+def u32(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+def prompts(vocab, n, seed):
+    rng = np.random.default_rng(seed)
+    return [rng.integers(0, vocab, 3 + 7 * b).astype(np.int32) for b in range(n)]
+
+
+@pytest.mark.parametrize("cfg", ["c1", "moe", "dense"])
+@pytest.mark.parametrize("n", [1, 3, 8])
+@pytest.mark.parametrize("exact_max", [None, 0], ids=["exact", "flash"])
+def test_batch_step_equals_single_steps(hip_ctx, monkeypatch, cfg, n, exact_max):
+    if exact_max is not None:
+        monkeypatch.setenv("ORNITH_HIP_EXACT_ATTN_MAX", str(exact_max))
+    m = hip_ctx.synth(**CFGS[cfg])
+    V = m.arch["vocab"]
+    ps = prompts(V, n, 11)
+    single = [m.session(128) for _ in range(n)]
+    batch = [m.session(128) for _ in range(n)]
+    for b in range(n):
+        single[b].eval(ps[b])
+        batch[b].eval(ps[b])
+    toks = np.array([int(np.argmax(s.logits())) for s in single], np.int32)
+    for step in range(6):
+        nxt = m.batch_step(batch, toks)
+        want = []
+        for b in range(n):
+            single[b].step(int(toks[b]))
+            lg = single[b].logits()
+            got = batch[b].logits()
+            assert np.array_equal(u32(got), u32(lg)), (cfg, n, step, b)
+            want.append(int(np.argmax(lg)))
+            assert batch[b].pos == single[b].pos
+        assert np.array_equal(nxt, np.array(want, np.int32)), (nxt, want)
+        toks = nxt
+    for s in single + batch:
+        s.free()
+    m.free()
+
+
+def test_batch_membership_changes(hip_ctx):
+    """Sessions join and leave the batch between steps; a session stepped in a
+    batch continues with its own token step and generate."""
+    m = hip_ctx.synth(**MIX)
+    V = m.arch["vocab"]
+    ps = prompts(V, 4, 12)
+    a = [m.session(96) for _ in range(4)]
+    r = [m.session(96) for _ in range(4)]
+    for b in range(4):
+        a[b].eval(ps[b])
+        r[b].eval(ps[b])
+    groups = [[0, 1, 2, 3], [1, 3], [2, 0, 3], [3]]
+    for g in groups:
+        toks = np.array([int(np.argmax(r[b].logits())) for b in g], np.int32)
+        m.batch_step([a[b] for b in g], toks)
+        for b, t in zip(g, toks):
+            r[b].step(int(t))
+            assert np.array_equal(u32(a[b].logits()), u32(r[b].logits())), (g, b)
+    for b in range(4):
+        assert np.array_equal(a[b].generate(5), r[b].generate(5))
+    with pytest.raises(Exception):
+        m.batch_step([a[0], a[0]], np.array([1, 2], np.int32))
+    for s in a + r:
+        s.free()
+    m.free()
