@@ -54,3 +54,15 @@ extern "C" __global__ void __launch_bounds__(256) oh_k_argmax_rows(const float *
         stg(out + blockIdx.x, bi == 0x7fffffff ? 0 : bi);
     }
 }
+
+// each session's token history: this step's token at its position and the
+// greedy next one after it (toks: the sessions' history arrays)
+extern "C" __global__ void __launch_bounds__(256)
+oh_k_batch_tokens(int32_t *const *toks, const int32_t *pos, const int32_t *tok, const int32_t *next, int n) {
+    const int b = (int)(blockIdx.x * 256 + tid_x());
+    if (b >= n) return;
+    int32_t *t = ldg(toks + b);
+    const int p = ldg(pos + b);
+    stg(t + p, ldg(tok + b));
+    stg(t + p + 1, ldg(next + b));
+}

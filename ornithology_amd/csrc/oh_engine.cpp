@@ -11,6 +11,8 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
+#include <algorithm>
+#include <atomic>
 #include <cstring>
 #include <string>
 #include <unordered_map>
@@ -937,6 +939,7 @@ struct LayerState {
 
 struct ornith_hip_session {
     ornith_hip_model *m = nullptr;
+    uint64_t sid = 0;             // unique per session of the process
     int cap = 0, pos = 0, kvcap = 0;
     bool have_logits = false;
     std::vector<void *> allocs;
@@ -1003,7 +1006,10 @@ struct ornith_hip_session {
         float *Hh = nullptr, *HSH = nullptr, *OD = nullptr, *ODSH = nullptr, *GU = nullptr, *GSH = nullptr;
         uint8_t *OPS = nullptr;
         size_t ops_bytes = 0;
+        int gen = 0;                   // bumped when the buffers are reallocated
         Q8Buf XQ, OQ, OAQ, HQ, HSQ;
+        hipGraphExec_t graph = nullptr;  // the captured step of the key's sessions
+        std::vector<uint64_t> key;
     } bw;
     std::vector<int> sp_body_rk;
     int step_grid = 0;
@@ -1095,6 +1101,7 @@ extern "C" void ornith_hip_session_free(ornith_hip_session *s) {
     (void)hipSetDevice(s->m->ctx->device);
     if (s->gbody) (void)hipGraphExecDestroy(s->gbody);
     if (s->ghead) (void)hipGraphExecDestroy(s->ghead);
+    if (s->bw.graph) (void)hipGraphExecDestroy(s->bw.graph);
     for (void *p : s->allocs) (void)hipFree(p);
     delete s;
 }
@@ -1134,6 +1141,8 @@ extern "C" int ornith_hip_session_new(ornith_hip_model *m, int cap, ornith_hip_s
     HCHK(hipSetDevice(m->ctx->device));
     const ornith_hip_arch &a = m->a;
     auto *s = new ornith_hip_session();
+    static std::atomic<uint64_t> next_sid{1};
+    s->sid = next_sid++;
     s->m = m;
     s->cap = cap;
     s->kvcap = (cap + 15) / 16 * 16;   // KV storage stride (V is tiled by 16 positions)
@@ -1682,10 +1691,13 @@ static int pf_mvb(const ornith_hip_tensor *W, const ornith_hip_tensor *W2, const
     return ORNITH_HIP_OK;
 }
 
-// Q4_K projections with whole 128-row tiles run on the matrix cores
-static bool pf_use_mmq(const ornith_hip_tensor *W, bool grouped) {
+// Q4_K projections with whole 128-row tiles over at least 64 tokens run on
+// the matrix cores; fewer columns (batch decode) stay on the vector-ALU kernel,
+// whose whole reduction is in flight at once
+static const int kMmqMinTokens = 64;
+static bool pf_use_mmq(const ornith_hip_tensor *W, bool grouped, int T) {
     const int rows = grouped ? (int)W->dims[1] : (int)W->rows;
-    return mmq_enabled() && oh_mmq_can(W->type, rows, (int)W->in);
+    return mmq_enabled() && T >= kMmqMinTokens && oh_mmq_can(W->type, rows, (int)W->in);
 }
 
 static int pf_mmq(const ornith_hip_tensor *W, const ornith_hip_tensor *W2, const Q8Buf &x, float *y, int ystride,
@@ -1706,7 +1718,7 @@ static int pf_mmq(const ornith_hip_tensor *W, const ornith_hip_tensor *W2, const
 // y (+)= W . x over T dense columns
 static int pf_mm(const ornith_hip_tensor *W, const Q8Buf &x, float *y, int ystride, int T, int mode,
                  hipStream_t st) {
-    if (pf_use_mmq(W, false)) return pf_mmq(W, nullptr, x, y, ystride, T, mode, st);
+    if (pf_use_mmq(W, false, T)) return pf_mmq(W, nullptr, x, y, ystride, T, mode, st);
     return pf_mvb(W, nullptr, x, y, ystride, T, mode, st);
 }
 
@@ -1717,7 +1729,7 @@ static int pf_swiglu(const ornith_hip_tensor *Wg, const ornith_hip_tensor *Wu, c
                      const int32_t *list = nullptr, int lstride = 0, int adiv = 1, int groups = 1,
                      const int32_t *items = nullptr, int max_items = 0) {
     const bool grouped = list != nullptr;
-    if (pf_use_mmq(Wg, grouped) && pf_use_mmq(Wu, grouped)) {
+    if (pf_use_mmq(Wg, grouped, T) && pf_use_mmq(Wu, grouped, T)) {
         CHK(pf_mmq(Wg, Wu, x, gu, 2 * I, T, 0, st, cnt, list, lstride, adiv, items, max_items));
         HCHK(oh_launch_norm_q8k_rows(gu, nullptr, 0.0f, I, npairs, nullptr, hq.qs, hq.d, hq.bs, st, hq.bp, 1));
     } else {
@@ -1792,7 +1804,7 @@ static int pf_chunk(ornith_hip_session *s, int base, int T, bool chunked, hipStr
             HCHK(oh_launch_mmq_items(p.CNT, a.ne, p.ITEMS, st));
             CHK(pf_swiglu(y.gate_exps, y.up_exps, p.XQ, I, T * K, T, p.HQ, p.GU, p.Hh, st, p.CNT, p.LIST, T, K, a.ne,
                           p.ITEMS, max_items));
-            if (pf_use_mmq(y.down_exps, true))
+            if (pf_use_mmq(y.down_exps, true, T))
                 CHK(pf_mmq(y.down_exps, nullptr, p.HQ, p.OD, H, T, 0, st, p.CNT, p.LIST, T, 1, p.ITEMS, max_items));
             else
                 CHK(pf_mvb(y.down_exps, nullptr, p.HQ, p.OD, H, T, 0, st, p.CNT, p.LIST, T, 1, a.ne));
@@ -1896,6 +1908,100 @@ static int bw_alloc(ornith_hip_session *s, int n, size_t ops_bytes) {
     CHK(salloc(s, &p.OPS, ob));
     p.ops_bytes = ob;
     p.n = (int)N;
+    p.gen++;
+    return ORNITH_HIP_OK;
+}
+
+// the device work of one batch step (its descriptors, tokens and positions
+// already in p.OPS): everything but the host copies, so that it can be
+// captured once and replayed for the same sessions
+struct BatchPlan {
+    ornith_hip_session **ss;
+    int n;
+    std::vector<size_t> lofs;
+    size_t tok_ofs;
+    int nvb_main, lds_main;
+};
+
+static int batch_enqueue(const BatchPlan &B, hipStream_t st) {
+    ornith_hip_session **ss = B.ss;
+    const int n = B.n;
+    ornith_hip_session *s0 = ss[0];
+    const ornith_hip_model *m = s0->m;
+    const ornith_hip_arch &a = m->a;
+    auto &p = s0->bw;
+    const int H = a.hidden, qd = a.nk * a.dk, vd = a.nv * a.dv, cc = 2 * qd + vd, aq = a.nh * a.hd;
+    const int kvd = a.nkv * a.hd;
+    const int32_t *dtok = (const int32_t *)(p.OPS + B.tok_ofs), *dpos = dtok + n;
+    int32_t *const *dtoks = (int32_t *const *)(p.OPS + B.tok_ofs + (((size_t)n * 8 + 15) & ~(size_t)15));
+    oh_op_embed emb = {m->embd->A, m->embd->B, m->embd->C, dtok, p.X, (int)m->embd->type, H};
+    HCHK(oh_launch_embed_rows(&emb, 0, n, st));
+    for (int l = 0; l < a.n_layers; l++) {
+        const OhLayer &y = m->L[l];
+        const uint8_t *dops = p.OPS + B.lofs[l];
+        HCHK(oh_launch_norm_q8k_rows(p.X, (const float *)y.attn_norm->A, a.eps, H, n, nullptr, p.XQ.qs, p.XQ.d,
+                                     p.XQ.bs, st, p.XQ.bp));
+        if (y.full) {
+            CHK(pf_mm(y.q, p.XQ, p.QP, 2 * aq, n, 0, st));
+            CHK(pf_mm(y.k, p.XQ, p.KB, kvd, n, 0, st));
+            CHK(pf_mm(y.v, p.XQ, p.VB, kvd, n, 0, st));
+            const oh_op_prep *pops = (const oh_op_prep *)dops;
+            const oh_op_attn *aops = (const oh_op_attn *)(dops + (size_t)n * sizeof(oh_op_prep));
+            HCHK(oh_launch_prep_batch(pops, dpos, n, a.nh, a.nkv, st));
+            HCHK(oh_launch_attn_batch(aops, dpos, n, B.nvb_main, B.lds_main, a.nh, a.hd, st));
+            HCHK(oh_launch_norm_q8k_rows(p.OA, nullptr, 0.0f, aq, n, nullptr, p.OAQ.qs, p.OAQ.d, p.OAQ.bs, st,
+                                         p.OAQ.bp));
+            CHK(pf_mm(y.o, p.OAQ, p.X, H, n, 1, st));
+        } else {
+            CHK(pf_mm(y.qkv, p.XQ, p.CAT, cc, n, 0, st));
+            CHK(pf_mm(y.gate, p.XQ, p.Z, vd, n, 0, st));
+            CHK(pf_mm(y.alpha, p.XQ, p.AB, 2 * a.nv, n, 0, st));
+            CHK(pf_mm(y.beta, p.XQ, p.AB + a.nv, 2 * a.nv, n, 0, st));
+            HCHK(oh_launch_delta_batch((const oh_op_delta *)dops, dpos, n, a.dk, a.conv_k, a.nv, st));
+            HCHK(oh_launch_gnorm_q8k_rows(p.O, p.Z, (const float *)y.ssm_norm->A, a.eps, vd, a.dv, n, p.OQ.qs,
+                                          p.OQ.d, p.OQ.bs, st, p.OQ.bp));
+            CHK(pf_mm(y.ssm_out, p.OQ, p.X, H, n, 1, st));
+        }
+        HCHK(oh_launch_norm_q8k_rows(p.X, (const float *)y.post_norm->A, a.eps, H, n, nullptr, p.XQ.qs, p.XQ.d,
+                                     p.XQ.bs, st, p.XQ.bp));
+        if (a.ne > 0) {
+            const int K = a.top_k, I = a.moe_inter, sI = a.shared_inter;
+            CHK(pf_mm(y.router, p.XQ, p.RL, a.ne, n, 0, st));
+            if (y.gate_inp_sh) CHK(pf_mm(y.gate_inp_sh, p.XQ, p.SHL, 1, n, 0, st));
+            HCHK(oh_launch_route_rows(p.RL, a.ne, K, y.gate_inp_sh ? p.SHL : nullptr, p.RIDX, p.RW,
+                                      y.gate_inp_sh ? p.SHG : nullptr, n, st));
+            HCHK(oh_launch_group_pairs(p.RIDX, n * K, p.CNT, a.ne, p.LIST, n, st));
+            const int max_items = (n * K + 63) / 64 + a.ne;
+            HCHK(oh_launch_mmq_items(p.CNT, a.ne, p.ITEMS, st));
+            CHK(pf_swiglu(y.gate_exps, y.up_exps, p.XQ, I, n * K, n, p.HQ, p.GU, p.Hh, st, p.CNT, p.LIST, n, K, a.ne,
+                          p.ITEMS, max_items));
+            if (pf_use_mmq(y.down_exps, true, n))
+                CHK(pf_mmq(y.down_exps, nullptr, p.HQ, p.OD, H, n, 0, st, p.CNT, p.LIST, n, 1, p.ITEMS, max_items));
+            else
+                CHK(pf_mvb(y.down_exps, nullptr, p.HQ, p.OD, H, n, 0, st, p.CNT, p.LIST, n, 1, a.ne));
+            if (y.gate_sh) {
+                CHK(pf_swiglu(y.gate_sh, y.up_sh, p.XQ, sI, n, n, p.HSQ, p.GSH, p.HSH, st));
+                CHK(pf_mm(y.down_sh, p.HSQ, p.ODSH, H, n, 0, st));
+            }
+            HCHK(oh_launch_moe_combine_rows(p.X, p.OD, p.RW, K, H, y.gate_sh ? p.ODSH : nullptr,
+                                            y.gate_inp_sh ? p.SHG : nullptr, n, st));
+        } else {
+            CHK(pf_swiglu(y.ffn_gate, y.ffn_up, p.XQ, a.shared_inter, n, n, p.HSQ, p.GSH, p.HSH, st));
+            CHK(pf_mm(y.ffn_down, p.HSQ, p.X, H, n, 1, st));
+        }
+    }
+    // head: output norm, lm_head over the n columns, each session's logits and
+    // greedy token; the token history of each session gets this step's token
+    // and, at the next position, the greedy one (where the token step's head
+    // leaves it for session_generate)
+    HCHK(oh_launch_norm_q8k_rows(p.X, (const float *)m->out_norm->A, a.eps, H, n, nullptr, p.XQ.qs, p.XQ.d,
+                                 p.XQ.bs, st, p.XQ.bp));
+    CHK(pf_mm(m->lm_head, p.XQ, p.LOGITS, a.vocab, n, 0, st));
+    HCHK(oh_launch_argmax_rows(p.LOGITS, a.vocab, n, p.IDX, st));
+    for (int b = 0; b < n; b++)
+        HCHK(hipMemcpyAsync(ss[b]->logits, p.LOGITS + (size_t)b * a.vocab, (size_t)a.vocab * 4,
+                            hipMemcpyDeviceToDevice, st));
+    HCHK(oh_launch_batch_tokens(dtoks, dpos, dtok, p.IDX, n, st));
     return ORNITH_HIP_OK;
 }
 
@@ -1924,26 +2030,31 @@ extern "C" int ornith_hip_batch_step(ornith_hip_session **ss, int n, const int32
     }
     HCHK(hipSetDevice(m->ctx->device));
     hipStream_t st = m->ctx->st;
-    const int H = a.hidden, qd = a.nk * a.dk, vd = a.nv * a.dv, cc = 2 * qd + vd, aq = a.nh * a.hd;
+    const int qd = a.nk * a.dk, vd = a.nv * a.dv, cc = 2 * qd + vd, aq = a.nh * a.hd;
     const int kvd = a.nkv * a.hd;
     // per-layer descriptors of every session: delta ops (linear layers) or
-    // prep + attention ops (full layers), n of each, then tokens and positions
+    // prep + attention ops (full layers), n of each; then tokens, positions
+    // and the sessions' token histories
+    BatchPlan B;
+    B.ss = ss;
+    B.n = n;
+    B.lofs.resize((size_t)a.n_layers);
     size_t ob = 0;
-    std::vector<size_t> lofs((size_t)a.n_layers);
     for (int l = 0; l < a.n_layers; l++) {
-        lofs[l] = ob;
+        B.lofs[l] = ob;
         ob += m->L[l].full ? (size_t)n * (sizeof(oh_op_prep) + sizeof(oh_op_attn)) : (size_t)n * sizeof(oh_op_delta);
         ob = (ob + 15) & ~(size_t)15;
     }
-    const size_t tok_ofs = ob;
-    ob += (size_t)n * 8 + 16;
+    B.tok_ofs = ob;
+    ob += (((size_t)n * 8 + 15) & ~(size_t)15) + (size_t)n * sizeof(int32_t *) + 16;
     CHK(bw_alloc(s0, n, ob));
     auto &p = s0->bw;
     std::vector<uint8_t> host(ob, 0);
-    int nvb_main = 1, lds_main = 0;
+    B.nvb_main = 1;
+    B.lds_main = 0;
     for (int l = 0; l < a.n_layers; l++) {
         const OhLayer &y = m->L[l];
-        uint8_t *dst = host.data() + lofs[l];
+        uint8_t *dst = host.data() + B.lofs[l];
         for (int b = 0; b < n; b++) {
             ornith_hip_session *sb = ss[b];
             const LayerState &z = sb->ls[l];
@@ -1964,8 +2075,8 @@ extern "C" int ornith_hip_batch_step(ornith_hip_session **ss, int n, const int32
                 const int nch = (sb->kvcap + oh_flash_chunk() - 1) / oh_flash_chunk();
                 const int nv_ex = a.nh / (256 / a.hd), nv_fl = a.nkv * (a.nh / a.nkv / at.hb) * nch;
                 const int lds_ex = oh_exact_lds_bytes(a.hd, sb->exact_max), lds_fl = oh_flash_lds_bytes(a.nh, a.nkv, a.hd);
-                nvb_main = std::max(nvb_main, std::max(nv_ex, nv_fl));
-                lds_main = std::max(lds_main, std::max(lds_ex, lds_fl));
+                B.nvb_main = std::max(B.nvb_main, std::max(nv_ex, nv_fl));
+                B.lds_main = std::max(B.lds_main, std::max(lds_ex, lds_fl));
             } else {
                 oh_op_delta d = {p.CAT + (size_t)b * cc, p.AB + (size_t)b * 2 * a.nv, p.Z + (size_t)b * vd,
                                  (const float *)y.conv->A, (const float *)y.ssm_a->A, (const float *)y.dt_bias->A,
@@ -1976,81 +2087,34 @@ extern "C" int ornith_hip_batch_step(ornith_hip_session **ss, int n, const int32
             }
         }
     }
-    int32_t *htp = (int32_t *)(host.data() + tok_ofs);
-    for (int b = 0; b < n; b++) { htp[b] = tokens[b]; htp[n + b] = ss[b]->pos; }
+    int32_t *htp = (int32_t *)(host.data() + B.tok_ofs);
+    int32_t **htk = (int32_t **)(host.data() + B.tok_ofs + (((size_t)n * 8 + 15) & ~(size_t)15));
+    for (int b = 0; b < n; b++) { htp[b] = tokens[b]; htp[n + b] = ss[b]->pos; htk[b] = ss[b]->toks; }
     HCHK(hipMemcpyAsync(p.OPS, host.data(), ob, hipMemcpyHostToDevice, st));
-    const int32_t *dtok = (const int32_t *)(p.OPS + tok_ofs), *dpos = dtok + n;
-    for (int b = 0; b < n; b++)   // the token also goes into the session's history
-        HCHK(hipMemcpyAsync(ss[b]->toks + ss[b]->pos, tokens + b, 4, hipMemcpyHostToDevice, st));
-
-    oh_op_embed emb = {m->embd->A, m->embd->B, m->embd->C, dtok, p.X, (int)m->embd->type, H};
-    HCHK(oh_launch_embed_rows(&emb, 0, n, st));
-    for (int l = 0; l < a.n_layers; l++) {
-        const OhLayer &y = m->L[l];
-        const uint8_t *dops = p.OPS + lofs[l];
-        HCHK(oh_launch_norm_q8k_rows(p.X, (const float *)y.attn_norm->A, a.eps, H, n, nullptr, p.XQ.qs, p.XQ.d,
-                                     p.XQ.bs, st, p.XQ.bp));
-        if (y.full) {
-            CHK(pf_mm(y.q, p.XQ, p.QP, 2 * aq, n, 0, st));
-            CHK(pf_mm(y.k, p.XQ, p.KB, kvd, n, 0, st));
-            CHK(pf_mm(y.v, p.XQ, p.VB, kvd, n, 0, st));
-            const oh_op_prep *pops = (const oh_op_prep *)dops;
-            const oh_op_attn *aops = (const oh_op_attn *)(dops + (size_t)n * sizeof(oh_op_prep));
-            HCHK(oh_launch_prep_batch(pops, dpos, n, a.nh, a.nkv, st));
-            HCHK(oh_launch_attn_batch(aops, dpos, n, nvb_main, lds_main, a.nh, a.hd, st));
-            HCHK(oh_launch_norm_q8k_rows(p.OA, nullptr, 0.0f, aq, n, nullptr, p.OAQ.qs, p.OAQ.d, p.OAQ.bs, st,
-                                         p.OAQ.bp));
-            CHK(pf_mm(y.o, p.OAQ, p.X, H, n, 1, st));
-        } else {
-            CHK(pf_mm(y.qkv, p.XQ, p.CAT, cc, n, 0, st));
-            CHK(pf_mm(y.gate, p.XQ, p.Z, vd, n, 0, st));
-            CHK(pf_mm(y.alpha, p.XQ, p.AB, 2 * a.nv, n, 0, st));
-            CHK(pf_mm(y.beta, p.XQ, p.AB + a.nv, 2 * a.nv, n, 0, st));
-            HCHK(oh_launch_delta_batch((const oh_op_delta *)dops, dpos, n, a.dk, a.conv_k, a.nv, st));
-            HCHK(oh_launch_gnorm_q8k_rows(p.O, p.Z, (const float *)y.ssm_norm->A, a.eps, vd, a.dv, n, p.OQ.qs,
-                                          p.OQ.d, p.OQ.bs, st, p.OQ.bp));
-            CHK(pf_mm(y.ssm_out, p.OQ, p.X, H, n, 1, st));
+    if (graphs_enabled()) {
+        // one captured step per set of sessions (ids, not addresses), buffer
+        // generation and product path
+        std::vector<uint64_t> key;
+        key.push_back((uint64_t)n);
+        key.push_back((uint64_t)p.gen);
+        key.push_back(mmq_enabled() ? 1u : 0u);
+        for (int b = 0; b < n; b++) key.push_back(ss[b]->sid);
+        if (!p.graph || p.key != key) {
+            if (p.graph) { (void)hipGraphExecDestroy(p.graph); p.graph = nullptr; }
+            hipGraph_t g = nullptr;
+            HCHK(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+            const int r = batch_enqueue(B, st);
+            hipError_t e = hipStreamEndCapture(st, &g);
+            if (r != ORNITH_HIP_OK) { if (g) (void)hipGraphDestroy(g); return r; }
+            if (e != hipSuccess) { seterr("batch graph capture: %s", hipGetErrorString(e)); return ORNITH_HIP_ERR_DEVICE; }
+            e = hipGraphInstantiate(&p.graph, g, nullptr, nullptr, 0);
+            (void)hipGraphDestroy(g);
+            if (e != hipSuccess) { p.graph = nullptr; seterr("batch graph instantiate: %s", hipGetErrorString(e)); return ORNITH_HIP_ERR_DEVICE; }
+            p.key = key;
         }
-        HCHK(oh_launch_norm_q8k_rows(p.X, (const float *)y.post_norm->A, a.eps, H, n, nullptr, p.XQ.qs, p.XQ.d,
-                                     p.XQ.bs, st, p.XQ.bp));
-        if (a.ne > 0) {
-            const int K = a.top_k, I = a.moe_inter, sI = a.shared_inter;
-            CHK(pf_mm(y.router, p.XQ, p.RL, a.ne, n, 0, st));
-            if (y.gate_inp_sh) CHK(pf_mm(y.gate_inp_sh, p.XQ, p.SHL, 1, n, 0, st));
-            HCHK(oh_launch_route_rows(p.RL, a.ne, K, y.gate_inp_sh ? p.SHL : nullptr, p.RIDX, p.RW,
-                                      y.gate_inp_sh ? p.SHG : nullptr, n, st));
-            HCHK(oh_launch_group_pairs(p.RIDX, n * K, p.CNT, a.ne, p.LIST, n, st));
-            const int max_items = (n * K + 63) / 64 + a.ne;
-            HCHK(oh_launch_mmq_items(p.CNT, a.ne, p.ITEMS, st));
-            CHK(pf_swiglu(y.gate_exps, y.up_exps, p.XQ, I, n * K, n, p.HQ, p.GU, p.Hh, st, p.CNT, p.LIST, n, K, a.ne,
-                          p.ITEMS, max_items));
-            if (pf_use_mmq(y.down_exps, true))
-                CHK(pf_mmq(y.down_exps, nullptr, p.HQ, p.OD, H, n, 0, st, p.CNT, p.LIST, n, 1, p.ITEMS, max_items));
-            else
-                CHK(pf_mvb(y.down_exps, nullptr, p.HQ, p.OD, H, n, 0, st, p.CNT, p.LIST, n, 1, a.ne));
-            if (y.gate_sh) {
-                CHK(pf_swiglu(y.gate_sh, y.up_sh, p.XQ, sI, n, n, p.HSQ, p.GSH, p.HSH, st));
-                CHK(pf_mm(y.down_sh, p.HSQ, p.ODSH, H, n, 0, st));
-            }
-            HCHK(oh_launch_moe_combine_rows(p.X, p.OD, p.RW, K, H, y.gate_sh ? p.ODSH : nullptr,
-                                            y.gate_inp_sh ? p.SHG : nullptr, n, st));
-        } else {
-            CHK(pf_swiglu(y.ffn_gate, y.ffn_up, p.XQ, a.shared_inter, n, n, p.HSQ, p.GSH, p.HSH, st));
-            CHK(pf_mm(y.ffn_down, p.HSQ, p.X, H, n, 1, st));
-        }
-    }
-    // head: output norm, lm_head over the n columns, each session's logits and
-    // greedy token
-    HCHK(oh_launch_norm_q8k_rows(p.X, (const float *)m->out_norm->A, a.eps, H, n, nullptr, p.XQ.qs, p.XQ.d,
-                                 p.XQ.bs, st, p.XQ.bp));
-    CHK(pf_mm(m->lm_head, p.XQ, p.LOGITS, a.vocab, n, 0, st));
-    HCHK(oh_launch_argmax_rows(p.LOGITS, a.vocab, n, p.IDX, st));
-    for (int b = 0; b < n; b++) {
-        HCHK(hipMemcpyAsync(ss[b]->logits, p.LOGITS + (size_t)b * a.vocab, (size_t)a.vocab * 4,
-                            hipMemcpyDeviceToDevice, st));
-        // the greedy token at the next position, where the token step's head
-        // leaves it (session_generate continues from there)
-        HCHK(hipMemcpyAsync(ss[b]->toks + ss[b]->pos + 1, p.IDX + b, 4, hipMemcpyDeviceToDevice, st));
+        HCHK(hipGraphLaunch(p.graph, st));
+    } else {
+        CHK(batch_enqueue(B, st));
     }
     std::vector<int32_t> hn((size_t)n);
     HCHK(hipMemcpyAsync(hn.data(), p.IDX, (size_t)n * 4, hipMemcpyDeviceToHost, st));

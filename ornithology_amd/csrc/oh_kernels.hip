@@ -128,6 +128,11 @@ hipError_t oh_launch_attn_batch(const oh_op_attn *ops, const int32_t *pos, int n
     hipLaunchKernelGGL(oh_k_attn_combine_batch, dim3(nh * (hd / 64), n), dim3(256), 0, st, ops, pos);
     return hipGetLastError();
 }
+hipError_t oh_launch_batch_tokens(int32_t *const *toks, const int32_t *pos, const int32_t *tok, const int32_t *next,
+                                  int n, hipStream_t st) {
+    hipLaunchKernelGGL(oh_k_batch_tokens, dim3((n + 255) / 256), dim3(256), 0, st, toks, pos, tok, next, n);
+    return hipGetLastError();
+}
 hipError_t oh_launch_argmax_rows(const float *v, int n, int rows, int32_t *out, hipStream_t st) {
     hipLaunchKernelGGL(oh_k_argmax_rows, dim3(rows), dim3(256), 0, st, v, n, out);
     return hipGetLastError();

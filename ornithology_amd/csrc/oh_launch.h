@@ -52,6 +52,8 @@ hipError_t oh_launch_prep_batch(const oh_op_prep *ops, const int32_t *pos, int n
 hipError_t oh_launch_attn_batch(const oh_op_attn *ops, const int32_t *pos, int n, int nvb_main, int lds, int nh,
                                 int hd, hipStream_t st);
 hipError_t oh_launch_argmax_rows(const float *v, int n, int rows, int32_t *out, hipStream_t st);
+hipError_t oh_launch_batch_tokens(int32_t *const *toks, const int32_t *pos, const int32_t *tok, const int32_t *next,
+                                  int n, hipStream_t st);
 hipError_t oh_launch_prep_rows(const oh_op_prep *a, int base, int T, hipStream_t st);
 hipError_t oh_launch_attn_rows(const oh_op_attn *a, int base, int t0, int n, size_t po_stride, size_t pml_stride,
                                hipStream_t st);
