@@ -13,7 +13,9 @@ device.
 
 Prints ONE JSON line (driver contract) with the roofline of the dominant
 kernel (per-launch HIP-event timing of one eager step) and the CPU baseline
-(the oracle port on a bounded sample on this host's cores).
+(the oracle port on a bounded sample on this host's cores). Also reported:
+the prompt rate (`prefill_tok_s`) and `batch_decode`, 8 sessions with their
+own 4096-token prompts stepped together (Model.batch_step).
 """
 from __future__ import annotations
 
@@ -267,6 +269,29 @@ def cpu_baseline(model: oa.Model, cfg: dict, seconds: float) -> dict:
                        f"= {t_tok * 1e3:.1f} ms; Q8 KV; {ncores} threads")
 
 
+def batch_decode(model: oa.Model, n: int, ctx_len: int, steps: int) -> dict:
+    """n sessions, each with its own ctx_len-token random prompt, stepped
+    together by Model.batch_step (one token per session per step, greedy);
+    wall clock around `steps` steps after 3 warm-up steps."""
+    sess = []
+    rng = np.random.default_rng(1)
+    for _ in range(n):
+        s = model.session(ctx_len + steps + 8)
+        s.eval(rng.integers(0, C3["vocab"], ctx_len, dtype=np.int64).astype(np.int32))
+        sess.append(s)
+    toks = np.array([int(np.argmax(s.logits())) for s in sess], np.int32)
+    for _ in range(3):
+        toks = model.batch_step(sess, toks)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        toks = model.batch_step(sess, toks)
+    el = time.perf_counter() - t0
+    for s in sess:
+        s.free()
+    return {"sessions": n, "context_tokens": ctx_len, "steps": steps, "ms_per_step": round(el / steps * 1e3, 3),
+            "tok_s": round(n * steps / el, 1)}
+
+
 # profile kind -> kernel symbol (as rocprofv3 names it)
 KERNEL_SYMBOL = {"matvec": "oh_k_mv_q4k", "matvec_q6k": "oh_k_mv_q6k", "matvec_q80": "oh_k_mv_q80",
                  "matvec_mixed": "oh_k_mv_mixed", "moe_down": "oh_k_mv_down", "delta_step": "oh_k_delta_step",
@@ -283,6 +308,8 @@ def main() -> int:
     ap.add_argument("--profile-reps", type=int, default=3)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--batch", type=int, default=8, help="sessions of the batch-decode figure (0: skip)")
+    ap.add_argument("--batch-steps", type=int, default=32)
     ap.add_argument("--traffic-probe", metavar="KIND", default=None,
                     help="run one device copy of known size and a replay of one step's KIND launches "
                          "(for rocprofv3 FETCH_SIZE / WRITE_SIZE passes), then exit")
@@ -341,6 +368,12 @@ def main() -> int:
     log(f"roofline kernel {KERNEL_SYMBOL.get(dom, dom)}: {nps} launches/step replayed back to back: "
         f"{us:.2f} us/launch, {bpl / 1e6:.2f} MB/launch -> {achieved:.1f} GB/s")
 
+    batch = None
+    if args.batch > 0:
+        batch = batch_decode(model, args.batch, args.ctx, args.batch_steps)
+        log(f"batch decode: {args.batch} sessions at {args.ctx} context: {batch['ms_per_step']:.2f} ms/step "
+            f"-> {batch['tok_s']:.1f} tok/s")
+
     cpu = None
     if not args.no_cpu:
         try:
@@ -367,6 +400,7 @@ def main() -> int:
                      "launches_per_step": nps},
         "cpu_baseline": cpu,
         "prefill_tok_s": round(args.ctx / t_prefill, 1),
+        "batch_decode": batch,
     }
     print(json.dumps(out), flush=True)
     sess.free()

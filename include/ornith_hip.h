@@ -164,6 +164,16 @@ int  ornith_hip_session_step(ornith_hip_session *s, int32_t token);
  * must not overlap (the first session holds the step's buffers). */
 int  ornith_hip_batch_step(ornith_hip_session **s, int n, const int32_t *tokens, int32_t *next);
 
+/* rmodel_session_save (src/ornith_rforward.c:1019-1075): the session as an
+ * ORNSESS v1 file (Q8 KV cache), byte-identical to the reference's file for
+ * the same state. */
+int  ornith_hip_session_save(ornith_hip_session *s, const char *path);
+/* rmodel_session_load (src/ornith_rforward.c:1077-1171): a new session from
+ * an ORNSESS v1 file, capacity pos + extra_cap; the same errors as the
+ * reference (bad magic or version, fingerprint mismatch, truncation, prefix
+ * hash), plus ORNITH_HIP_ERR_UNSUPPORTED for an f32 KV cache. */
+int  ornith_hip_session_load(ornith_hip_model *m, const char *path, int extra_cap, ornith_hip_session **out);
+
 /* Session state in the reference's host layouts (src/ornith_rforward.c:986-1171
  * snapshot contents): delta state [nv][dv][dk]; conv window [(K-1)][Cc] oldest
  * first; Q8 KV codes [len][nkv][hd] and scales [len][nkv]. */

@@ -88,6 +88,8 @@ _SIGS = {
     "ornith_hip_session_generate": (C.c_int, [_vp, C.c_int, _ip, _ip]),
     "ornith_hip_session_step": (C.c_int, [_vp, C.c_int32]),
     "ornith_hip_batch_step": (C.c_int, [C.POINTER(_vp), C.c_int, _ip, _ip]),
+    "ornith_hip_session_save": (C.c_int, [_vp, C.c_char_p]),
+    "ornith_hip_session_load": (C.c_int, [_vp, C.c_char_p, C.c_int, C.POINTER(_vp)]),
     "ornith_hip_session_get_delta": (C.c_int, [_vp, C.c_int, _fp]),
     "ornith_hip_session_get_conv": (C.c_int, [_vp, C.c_int, _fp]),
     "ornith_hip_session_get_kv": (C.c_int, [_vp, C.c_int, _vp, _fp, _vp, _fp]),
@@ -271,6 +273,13 @@ class Model:
         _check(lib().ornith_hip_session_new(self.h, cap, C.byref(h)), "ornith_hip_session_new")
         return Session(self, h)
 
+    def load_session(self, path, extra_cap: int = 0) -> "Session":
+        """rmodel_session_load: a session from an ORNSESS snapshot."""
+        h = _vp()
+        _check(lib().ornith_hip_session_load(self.h, str(path).encode(), int(extra_cap), C.byref(h)),
+               "ornith_hip_session_load")
+        return Session(self, h)
+
     def batch_step(self, sessions, tokens) -> np.ndarray:
         """One token step of each session at once (ornith_hip_batch_step);
         returns each session's greedy next token."""
@@ -298,6 +307,10 @@ class Session:
     def eval(self, tokens) -> None:
         t = np.ascontiguousarray(tokens, np.int32)
         _check(lib().ornith_hip_session_eval(self.h, _i32(t), t.size), "ornith_hip_session_eval")
+
+    def save(self, path) -> None:
+        """rmodel_session_save: the session as an ORNSESS snapshot."""
+        _check(lib().ornith_hip_session_save(self.h, str(path).encode()), "ornith_hip_session_save")
 
     def step(self, token: int) -> None:
         _check(lib().ornith_hip_session_step(self.h, int(token)), "ornith_hip_session_step")

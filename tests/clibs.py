@@ -239,6 +239,7 @@ def ref():
         "rmodel_session_logits": (fp, [vp]),
         "rmodel_session_pos": (C.c_int, [vp]),
         "rmodel_session_generate": (C.c_int, [vp, C.c_int, ip, C.c_int, vp, TOKEN_CB, vp, ip]),
+        "rmodel_session_save": (C.c_int, [vp, C.c_char_p]),
         "ornith_last_error": (C.c_char_p, []),
     }
     for name, (res, args) in sig.items():

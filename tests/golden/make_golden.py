@@ -7,6 +7,8 @@ seeds/ids and the reference's outputs.
   c1.npz      C1 (tiny all-Q8_0 qwen35moe) GGUF sha256, prompt, 64 greedy
               tokens and logits at several steps, for the default chunked
               prefill and for ORNITH_PREFILL_SERIAL=1, both with ORNITH_KV_Q8=1.
+  c1_session.json  SHA-256 and size of the reference's ORNSESS snapshot of a
+              C1 session after the prompt and 8 greedy tokens, per prompt mode.
   codecs.npz  reference encodings of N(0,0.02) rows for Q8_0/Q4_K/Q6_K/IQ2_XXS
               at in=2048 and in=512, their decoded floats, the Q8_K bytes of
               N(0,1) seed-1 activations and the reference qdot / fallback dot.
@@ -175,6 +177,46 @@ def make_c1(out: Path) -> None:
         print("c1:", h_ref, "tokens", res["chunked_tokens"][:16], "...")
 
 
+SESSION_GEN = 8
+
+
+def make_session(out: Path) -> None:
+    """rmodel_session_save after the C1 prompt and SESSION_GEN greedy tokens,
+    Q8 KV, for the chunked and the serial prompt mode: the file's hash."""
+    import json
+    R = clibs.ref()
+    res = {}
+    with tempfile.TemporaryDirectory() as td:
+        p_ref = Path(td) / "c1_ref.gguf"
+        write_with_reference(p_ref, C1)
+        prompt = clibs.ids(C1["seed"], "prompt", PROMPT_LEN, C1["vocab"])
+        for mode, serial in (("chunked", False), ("serial", True)):
+            os.environ["ORNITH_KV_Q8"] = "1"
+            if serial:
+                os.environ["ORNITH_PREFILL_SERIAL"] = "1"
+            else:
+                os.environ.pop("ORNITH_PREFILL_SERIAL", None)
+            m = C.c_void_p()
+            assert R.rmodel_load(str(p_ref).encode(), C.byref(m)) == 0, R.ornith_last_error()
+            s = R.rmodel_session_new(m, PROMPT_LEN + SESSION_GEN + 8)
+            assert R.rmodel_session_eval(s, i32p(prompt), len(prompt)) == 0
+            toks = []
+            cb = clibs.TOKEN_CB(lambda tok, piece, ud: toks.append(tok))
+            fin = C.c_int(0)
+            assert R.rmodel_session_generate(s, SESSION_GEN, None, 0, None, cb, None, C.byref(fin)) == 0
+            f = Path(td) / f"{mode}.ornsess"
+            assert R.rmodel_session_save(s, str(f).encode()) == 0
+            data = f.read_bytes()
+            res[mode] = {"pos": PROMPT_LEN + SESSION_GEN, "tokens": [int(t) for t in toks],
+                         "bytes": len(data), "sha256": hashlib.sha256(data).hexdigest()}
+            R.rmodel_session_free(s)
+            R.rmodel_free(m)
+            os.environ.pop("ORNITH_PREFILL_SERIAL", None)
+    (out / "c1_session.json").write_text(json.dumps({"prompt_len": PROMPT_LEN, "generated": SESSION_GEN,
+                                                      "modes": res}, indent=1) + "\n")
+    print("c1 session:", {k: v["sha256"][:16] for k, v in res.items()})
+
+
 def make_codecs(out: Path) -> None:
     R = clibs.ref()
     rows = 16
@@ -212,3 +254,4 @@ if __name__ == "__main__":
         sys.exit("oracle/_ref/libornith_ref.so not built: run `make -C oracle` where the reference tree exists")
     make_codecs(HERE)
     make_c1(HERE)
+    make_session(HERE)
