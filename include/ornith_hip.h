@@ -69,6 +69,7 @@ typedef struct {
     uint32_t t_default, t_attn_v, t_ffn_down, t_output, t_embd;
     uint64_t seed;
     float    sigma;
+    uint32_t t_exps;   /* routed experts gate/up/down; 0: t_default / t_ffn_down */
 } ornith_hip_gen_cfg;
 
 const char *ornith_hip_last_error(void);            /* ornith_last_error, src/ornith_util.c:25-30 */
@@ -101,6 +102,10 @@ int  ornith_hip_matvec(ornith_hip_ctx *ctx, const ornith_hip_tensor *W,
                        const float *x, float *y, int Tn);
 
 /* oq_dequantize of rows [row0, row0+nrows) (src/ornith_quant.h:64-66). */
+/* oq_quantize (src/ornith_quant.h:51-66) on the device: n floats (whole
+ * 256-blocks) -> GGUF blocks of Q8_0, Q4_K, Q6_K or IQ2_XXS, byte-identical
+ * to the reference's encoders (src/ornith_quant.c:155-175, 451-561, 703-789). */
+int  ornith_hip_quantize(ornith_hip_ctx *ctx, uint32_t ggml_type, const float *x, uint64_t n, void *out);
 int  ornith_hip_dequant(ornith_hip_ctx *ctx, const ornith_hip_tensor *W,
                         int64_t row0, int64_t nrows, float *out);
 

@@ -101,9 +101,9 @@ int orc_gen_write_gguf(const orc_gen_cfg *c, const char *path) {
             continue;
         }
         CK(add_q(w, &pl, c, N("ffn_gate_inp.weight"), c->t_default, 2, H, c->ne, 0));
-        CK(add_q(w, &pl, c, N("ffn_gate_exps.weight"), c->t_default, 3, H, c->moe_inter, c->ne));
-        CK(add_q(w, &pl, c, N("ffn_up_exps.weight"), c->t_default, 3, H, c->moe_inter, c->ne));
-        CK(add_q(w, &pl, c, N("ffn_down_exps.weight"), c->t_ffn_down, 3, c->moe_inter, H, c->ne));
+        CK(add_q(w, &pl, c, N("ffn_gate_exps.weight"), c->t_exps ? c->t_exps : c->t_default, 3, H, c->moe_inter, c->ne));
+        CK(add_q(w, &pl, c, N("ffn_up_exps.weight"), c->t_exps ? c->t_exps : c->t_default, 3, H, c->moe_inter, c->ne));
+        CK(add_q(w, &pl, c, N("ffn_down_exps.weight"), c->t_exps ? c->t_exps : c->t_ffn_down, 3, c->moe_inter, H, c->ne));
         if (c->shared_inter > 0) {
             CK(add_q(w, &pl, c, N("ffn_gate_shexp.weight"), c->t_default, 2, H, c->shared_inter, 0));
             CK(add_q(w, &pl, c, N("ffn_up_shexp.weight"), c->t_default, 2, H, c->shared_inter, 0));

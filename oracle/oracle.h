@@ -188,6 +188,8 @@ typedef struct {
     uint32_t t_embd;        /* token_embd                                 */
     uint64_t seed;
     float sigma;            /* N(0, sigma) for projection weights          */
+    uint32_t t_exps;        /* routed experts gate/up/down; 0: t_default /
+                               t_ffn_down as above                         */
 } orc_gen_cfg;
 
 int orc_gen_write_gguf(const orc_gen_cfg *cfg, const char *path);

@@ -55,7 +55,7 @@ class GenCfg(C.Structure):
         "nk", "nv", "dhead", "conv_k", "ne", "top_k", "moe_inter", "shared_inter")] + [
         ("t_default", C.c_uint32), ("t_attn_v", C.c_uint32), ("t_ffn_down", C.c_uint32),
         ("t_output", C.c_uint32), ("t_embd", C.c_uint32), ("seed", C.c_uint64),
-        ("sigma", C.c_float)]
+        ("sigma", C.c_float), ("t_exps", C.c_uint32)]
 
 
 _SIGS = {
@@ -88,6 +88,7 @@ _SIGS = {
     "ornith_hip_session_generate": (C.c_int, [_vp, C.c_int, _ip, _ip]),
     "ornith_hip_session_step": (C.c_int, [_vp, C.c_int32]),
     "ornith_hip_batch_step": (C.c_int, [C.POINTER(_vp), C.c_int, _ip, _ip]),
+    "ornith_hip_quantize": (C.c_int, [_vp, C.c_uint32, _fp, C.c_uint64, _vp]),
     "ornith_hip_session_save": (C.c_int, [_vp, C.c_char_p]),
     "ornith_hip_session_load": (C.c_int, [_vp, C.c_char_p, C.c_int, C.POINTER(_vp)]),
     "ornith_hip_session_get_delta": (C.c_int, [_vp, C.c_int, _fp]),
@@ -165,6 +166,15 @@ class Context:
         _check(lib().ornith_hip_upload(self.h, name.encode(), ggml_type, C.c_void_p(data.ctypes.data),
                                        data.nbytes, len(dims), d, C.byref(h)), "ornith_hip_upload")
         return Tensor(self, h, ggml_type, dims)
+
+    def quantize(self, ggml_type: int, x: np.ndarray) -> np.ndarray:
+        """oq_quantize on the device (Q8_0, Q4_K, Q6_K, IQ2_XXS): GGUF block bytes."""
+        x = np.ascontiguousarray(x, np.float32)
+        nbytes = {Q8_0: 34 * 8, Q4_K: 144, Q6_K: 210, IQ2_XXS: 66}[ggml_type] * (x.size // 256)
+        out = np.zeros(nbytes, np.uint8)
+        _check(lib().ornith_hip_quantize(self.h, ggml_type, _f32(x), x.size, out.ctypes.data_as(_vp)),
+               "ornith_hip_quantize")
+        return out
 
     def quantize_q8k(self, x: np.ndarray) -> np.ndarray:
         x = np.ascontiguousarray(x, np.float32)

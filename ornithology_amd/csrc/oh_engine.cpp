@@ -517,6 +517,31 @@ extern "C" int ornith_hip_matvec(ornith_hip_ctx *ctx, const ornith_hip_tensor *W
     return ORNITH_HIP_OK;
 }
 
+// oq_quantize on the device: n floats (whole super-blocks) -> GGUF blocks of
+// Q8_0 / Q4_K / Q6_K / IQ2_XXS, the encoders of the model synthesis
+extern "C" int ornith_hip_quantize(ornith_hip_ctx *ctx, uint32_t type, const float *x, uint64_t n, void *out) {
+    if (type != OH_Q8_0 && type != OH_Q4_K && type != OH_Q6_K && type != OH_IQ2_XXS) {
+        seterr("quantize: type %u has no device encoder (Q8_0, Q4_K, Q6_K, IQ2_XXS)", type);
+        return ORNITH_HIP_ERR_UNSUPPORTED;
+    }
+    if (n == 0 || n % 256) { seterr("quantize: %llu values is not a whole number of 256-blocks", (unsigned long long)n); return ORNITH_HIP_ERR_FORMAT; }
+    HCHK(hipSetDevice(ctx->device));
+    const uint64_t dims[2] = {256, n / 256};
+    ornith_hip_tensor *t = nullptr;
+    CHK(tensor_alloc(ctx, "quantize", type, 2, dims, &t));
+    float *dx = nullptr;
+    hipError_t e = hipMalloc(&dx, n * 4);
+    if (e == hipSuccess) e = hipMemcpyAsync(dx, x, n * 4, hipMemcpyHostToDevice, ctx->st);
+    if (e == hipSuccess) e = oh_launch_encode(dx, (int)type, (int64_t)(n / 256), t->A, t->B, t->C, ctx->st);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->st);
+    if (dx) (void)hipFree(dx);
+    int r = ORNITH_HIP_OK;
+    if (e != hipSuccess) { seterr("quantize: %s", hipGetErrorString(e)); r = ORNITH_HIP_ERR_DEVICE; }
+    if (r == ORNITH_HIP_OK) r = ornith_hip_tensor_download(t, out, t->gguf_bytes);
+    ornith_hip_tensor_free(t);
+    return r;
+}
+
 extern "C" int ornith_hip_dequant(ornith_hip_ctx *ctx, const ornith_hip_tensor *W,
                                   int64_t row0, int64_t nrows, float *out) {
     if (row0 < 0 || nrows < 0 || row0 + nrows > W->rows) {
@@ -2500,10 +2525,12 @@ extern "C" int ornith_hip_model_synth(ornith_hip_ctx *ctx, const ornith_hip_gen_
                                       ornith_hip_model **out) {
     *out = nullptr;
     HCHK(hipSetDevice(ctx->device));
-    auto enc_ok = [](uint32_t t) { return t == OH_Q8_0 || t == OH_Q4_K || t == OH_Q6_K || t == OH_F32; };
+    auto enc_ok = [](uint32_t t) {
+        return t == OH_Q8_0 || t == OH_Q4_K || t == OH_Q6_K || t == OH_IQ2_XXS || t == OH_F32;
+    };
     if (!enc_ok(c->t_default) || !enc_ok(c->t_attn_v) || !enc_ok(c->t_ffn_down) || !enc_ok(c->t_output) ||
-        !enc_ok(c->t_embd)) {
-        seterr("model_synth: on-device encoders cover F32/Q8_0/Q4_K/Q6_K");
+        !enc_ok(c->t_embd) || (c->t_exps && !enc_ok(c->t_exps))) {
+        seterr("model_synth: on-device encoders cover F32/Q8_0/Q4_K/Q6_K/IQ2_XXS");
         return ORNITH_HIP_ERR_UNSUPPORTED;
     }
     if (c->hidden <= 0 || c->n_layers <= 0 || c->vocab <= 0 || c->dhead <= 0 || c->conv_k < 2 || c->conv_k > 8) {
@@ -2579,9 +2606,9 @@ extern "C" int ornith_hip_model_synth(ornith_hip_ctx *ctx, const ornith_hip_gen_
             continue;
         }
         add_q(b + "ffn_gate_inp.weight", c->t_default, 2, H, c->ne, 0);
-        add_q(b + "ffn_gate_exps.weight", c->t_default, 3, H, c->moe_inter, c->ne);
-        add_q(b + "ffn_up_exps.weight", c->t_default, 3, H, c->moe_inter, c->ne);
-        add_q(b + "ffn_down_exps.weight", c->t_ffn_down, 3, c->moe_inter, H, c->ne);
+        add_q(b + "ffn_gate_exps.weight", c->t_exps ? c->t_exps : c->t_default, 3, H, c->moe_inter, c->ne);
+        add_q(b + "ffn_up_exps.weight", c->t_exps ? c->t_exps : c->t_default, 3, H, c->moe_inter, c->ne);
+        add_q(b + "ffn_down_exps.weight", c->t_exps ? c->t_exps : c->t_ffn_down, 3, c->moe_inter, H, c->ne);
         if (c->shared_inter > 0) {
             add_q(b + "ffn_gate_shexp.weight", c->t_default, 2, H, c->shared_inter, 0);
             add_q(b + "ffn_up_shexp.weight", c->t_default, 2, H, c->shared_inter, 0);

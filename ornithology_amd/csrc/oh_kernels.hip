@@ -317,6 +317,10 @@ hipError_t oh_launch_fill_uniform(uint64_t key, float lo, float hi, float *dst, 
 hipError_t oh_launch_encode(const float *x, int type, int64_t nblk, uint8_t *A, uint8_t *B, uint8_t *C,
                             hipStream_t st) {
     if (nblk <= 0) return hipSuccess;
+    if (type == OH_IQ2_XXS) {
+        hipLaunchKernelGGL(oh_k_encode_iq2xxs, dim3((unsigned)((nblk + 3) / 4)), dim3(256), 0, st, x, nblk, A, C);
+        return hipGetLastError();
+    }
     hipLaunchKernelGGL(oh_k_encode, dim3((unsigned)((nblk + 255) / 256)), dim3(256), 0, st, x, type, nblk, A, B, C);
     return hipGetLastError();
 }

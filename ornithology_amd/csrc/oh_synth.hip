@@ -171,3 +171,127 @@ oh_k_encode(const float *x, int type, int64_t nblk, uint8_t *A, uint8_t *B, uint
         }
     }
 }
+
+// IQ2_XXS (src/ornith_quant.c:703-789, quantize_iq2_xxs_core without
+// importance weights): one wave per 256-element super-block. Lanes 0..31 take
+// the 32 sub-groups of 8 (group lane / 4, sub-group lane % 4): magnitudes and
+// the sign bits, an odd count fixed by flipping the smallest magnitude. Per
+// group of 32 the scale search over trial magnitudes t = 4..64: for each
+// trial the four sub-groups' smallest error over the 256 grid points (lane l
+// holds points l + 64q), added in sub-group order, a strictly smaller total
+// replacing the best as in the reference's loop. Then d (binary16), the 4-bit
+// group scales and the grid picks (the lowest index among equal errors).
+extern "C" __global__ void __launch_bounds__(256)
+oh_k_encode_iq2xxs(const float *x, int64_t nblk, uint8_t *A, uint8_t *C) {
+    __shared__ float smag[4][32][8];
+    __shared__ uint32_t ssgn[4][32];
+    const int wave = tid_x() >> 6, lane = lane_id();
+    const int64_t b = (int64_t)blockIdx.x * 4 + wave;
+    if (b >= nblk) return;
+    const float *v = x + b * 256;
+    float (*mag)[8] = smag[wave];
+    if (lane < 32) {
+        const float *xk = v + 8 * lane;
+        uint32_t s = 0;
+        int nneg = 0;
+        float m[8];
+        for (int j = 0; j < 8; j++) {
+            const float val = xk[j];
+            if (val < 0.0f) { m[j] = -val; s |= 1u << j; nneg++; }
+            else m[j] = val;
+        }
+        if (nneg & 1) {
+            int imin = 0;
+            float vmin = m[0];
+            for (int j = 1; j < 8; j++)
+                if (m[j] < vmin) { vmin = m[j]; imin = j; }
+            s ^= 1u << imin;
+        }
+        for (int j = 0; j < 8; j++) mag[lane][j] = m[j];
+        ssgn[wave][lane] = s & 127u;
+    }
+    wave_lds_sync();
+    float gm[4][8];
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const uint64_t gw = k_iq2_grid[lane + 64 * q];
+#pragma unroll
+        for (int j = 0; j < 8; j++) gm[q][j] = (float)((gw >> (8 * j)) & 0xff);
+    }
+    // the smallest sum_j (mag_j - s * grid_j)^2 over the grid and its first index
+    auto best = [&](const float *mg, float s, int *gidx) -> float {
+        float tm[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) tm[j] = mg[j];
+        float be = 1e30f;
+        int bg = 0;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            float e = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const float df = tm[j] - s * gm[q][j];
+                e += df * df;
+            }
+            if (e < be) { be = e; bg = lane + 64 * q; }
+        }
+        for (int m = 32; m >= 1; m >>= 1) {
+            const float oe = shfl_xor(be, m);
+            const int og = shfl_xor(bg, m);
+            if (oe < be || (oe == be && og < bg)) { be = oe; bg = og; }
+        }
+        if (gidx) *gidx = bg;
+        return be;
+    };
+    float gsc[8];
+    for (int g32 = 0; g32 < 8; g32++) {
+        float gmax = 0.0f;
+        for (int k = 0; k < 4; k++)
+            for (int j = 0; j < 8; j++)
+                if (mag[4 * g32 + k][j] > gmax) gmax = mag[4 * g32 + k][j];
+        if (gmax < 1e-12f) { gsc[g32] = 0.0f; continue; }
+        const float base = gmax / 43.0f;
+        float best_s = base, best_e = 1e30f;
+        for (int t = 4; t <= 64; t++) {
+            const float s = base * 43.0f / (float)t;
+            float tot = 0.0f;
+            for (int k = 0; k < 4; k++) tot += best(mag[4 * g32 + k], s, nullptr);
+            if (tot < best_e) { best_e = tot; best_s = s; }
+        }
+        gsc[g32] = best_s;
+    }
+    float mx = 0.0f;
+    for (int g32 = 0; g32 < 8; g32++) if (gsc[g32] > mx) mx = gsc[g32];
+    uint32_t *qw = (uint32_t *)(A + b * 64);
+    if (mx <= 0.0f) {                          // all-zero block
+        if (lane < 16) stg(qw + lane, 0u);
+        if (lane == 0) stg((uint16_t *)C + b, f2h_rne(0.0f));
+        return;
+    }
+    const uint16_t dh = f2h_rne(mx / (0.25f * 15.5f));
+    const float qd = 0.25f * h2f(dh);
+    uint32_t words[16];
+    for (int g32 = 0; g32 < 8; g32++) {
+        long l = 0;
+        if (qd > 0.0f && gsc[g32] > 0.0f) l = round_away(gsc[g32] / qd - 0.5f);
+        l = l < 0 ? 0 : (l > 15 ? 15 : l);
+        const float db = qd * (0.5f + (float)l);
+        uint32_t a0 = 0, a1 = 0;
+        for (int k = 0; k < 4; k++) {
+            int g = 0;
+            if (db > 0.0f) best(mag[4 * g32 + k], db, &g);
+            a0 |= (uint32_t)(g & 0xff) << (8 * k);
+            a1 |= (ssgn[wave][4 * g32 + k] & 127u) << (7 * k);
+        }
+        a1 |= (uint32_t)l << 28;
+        words[2 * g32] = a0;
+        words[2 * g32 + 1] = a1;
+    }
+    if (lane < 16) {
+        uint32_t w = words[0];
+#pragma unroll
+        for (int k = 1; k < 16; k++) if (lane == k) w = words[k];
+        stg(qw + lane, w);
+    }
+    if (lane == 0) stg((uint16_t *)C + b, dh);
+}

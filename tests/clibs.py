@@ -60,7 +60,7 @@ class GenCfg(C.Structure):
         "nk", "nv", "dhead", "conv_k", "ne", "top_k", "moe_inter", "shared_inter")] + [
         ("t_default", C.c_uint32), ("t_attn_v", C.c_uint32), ("t_ffn_down", C.c_uint32),
         ("t_output", C.c_uint32), ("t_embd", C.c_uint32), ("seed", C.c_uint64),
-        ("sigma", C.c_float)]
+        ("sigma", C.c_float), ("t_exps", C.c_uint32)]
 
 
 class Arch(C.Structure):

@@ -159,3 +159,35 @@ def test_upload_rejects_bad_sizes(hip_ctx):
         hip_ctx.upload("bad", Q4_K, np.zeros(100, np.uint8), (256, 1))
     with pytest.raises(oa.HipError):
         hip_ctx.upload("bad2", Q8_0, np.zeros(34, np.uint8), (32, 1))   # 32-wide Q8_0 rows unsupported
+
+
+CODECS = np.load(clibs.ROOT / "tests" / "golden" / "codecs.npz")
+
+
+@pytest.mark.parametrize("t", [Q8_0, Q4_K, Q6_K, IQ2_XXS])
+@pytest.mark.parametrize("n", [2048, 512])
+def test_device_encoders_equal_reference(hip_ctx, t, n):
+    """oq_quantize on the device against the reference's own encodings of the
+    same N(0, 0.02) rows (golden codecs.npz), byte for byte."""
+    tn = clibs.TYPE_NAMES[t]
+    w = clibs.gauss(0, f"w.{tn}.{n}", 16 * n, 0.02)
+    got = hip_ctx.quantize(t, w)
+    want = CODECS[f"{tn}_{n}_enc"]
+    assert np.array_equal(got, want), np.nonzero(got != want)[0][:8]
+
+
+def test_iq2xxs_encoder_edge_blocks(hip_ctx, orc):
+    """IQ2_XXS edge cases against the oracle encoder (pinned to the reference
+    by the golden rows): an all-zero block, a block with one zero group, an odd
+    number of negatives with tied smallest magnitudes, and large values."""
+    rng = np.random.default_rng(3)
+    blocks = [np.zeros(256, np.float32)]
+    b = rng.normal(0, 0.02, 256).astype(np.float32)
+    b[32:64] = 0.0
+    blocks.append(b)
+    c = np.full(256, 0.01, np.float32)
+    c[::3] *= -1.0
+    blocks.append(c)
+    blocks.append(rng.normal(0, 30.0, 256).astype(np.float32))
+    x = np.concatenate(blocks)
+    assert np.array_equal(hip_ctx.quantize(IQ2_XXS, x), clibs.quantize(orc, IQ2_XXS, x))

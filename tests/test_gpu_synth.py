@@ -13,9 +13,13 @@ MIX = dict(clibs.C1, hidden=768, n_layers=4, vocab=1000, nh=4, nkv=1, hd=128, nk
            ne=8, top_k=2, moe_inter=512, shared_inter=256, t_default=clibs.Q4_K, t_attn_v=clibs.Q6_K,
            t_ffn_down=clibs.Q6_K, t_output=clibs.Q6_K, t_embd=clibs.Q4_K, seed=3)
 DENSE = dict(MIX, ne=0, top_k=0, moe_inter=0, shared_inter=1024, seed=7)
+# C4's type mix at a small shape: IQ2_XXS routed experts, Q4_K / Q6_K elsewhere
+IQX = dict(clibs.C1, hidden=256, n_layers=2, full_interval=2, vocab=512, nh=2, nkv=1, hd=128, nk=1, nv=2,
+           dhead=128, ne=2, top_k=1, moe_inter=256, shared_inter=256, t_default=clibs.Q4_K, t_attn_v=clibs.Q6_K,
+           t_ffn_down=clibs.Q6_K, t_output=clibs.Q6_K, t_embd=clibs.Q4_K, t_exps=clibs.IQ2_XXS, seed=9)
 
 
-@pytest.mark.parametrize("cfg", [clibs.C1, MIX, DENSE], ids=["C1-Q8_0", "Q4_K_M-mix", "dense"])
+@pytest.mark.parametrize("cfg", [clibs.C1, MIX, DENSE, IQX], ids=["C1-Q8_0", "Q4_K_M-mix", "dense", "IQ2_XXS-experts"])
 def test_synth_equals_generator_bytes(hip_ctx, tmp_path, cfg):
     p = tmp_path / "gen.gguf"
     clibs.write_c1_gguf(p, cfg)
@@ -54,3 +58,34 @@ def test_profile_step_reports_every_launch(hip_ctx):
     assert all(ms > 0 for _, _, ms in rec) and s.pos == 5
     s.free()
     m.free()
+
+
+def test_iq2xxs_experts_decode_matches_oracle(hip_ctx, orc, tmp_path):
+    """C4's path at a small shape: the IQ2_XXS routed experts through the
+    reference's f32 fallback (dequantised row . f32 activation,
+    src/ornith_rforward.c:119-133): prompt logits and 6 greedy steps
+    bit-identical to the oracle."""
+    import ctypes as C
+    from clibs import i32p
+    p = tmp_path / "iqx.gguf"
+    clibs.write_c1_gguf(p, IQX)
+    om = C.c_void_p()
+    assert orc.orc_model_load(str(p).encode(), C.byref(om)) == 0
+    orc.orc_model_set_threads(om, 8)
+    os_ = orc.orc_session_new(om, 40, 1)
+    prompt = np.random.default_rng(2).integers(0, IQX["vocab"], 12).astype(np.int32)
+    assert orc.orc_session_eval(os_, i32p(prompt), 12, 1) == 0
+    m = hip_ctx.synth(**IQX)
+    s = m.session(40)
+    s.eval(prompt)
+    V = IQX["vocab"]
+    for k in range(7):
+        want = np.ctypeslib.as_array(orc.orc_session_logits(os_), (V,)).copy()
+        assert np.array_equal(s.logits().view(np.uint32), want.view(np.uint32)), k
+        tok = int(np.argmax(want))
+        assert orc.orc_session_step(os_, tok) == 0
+        s.step(tok)
+    s.free()
+    m.free()
+    orc.orc_session_free(os_)
+    orc.orc_model_free(om)
