@@ -43,6 +43,16 @@ C3 = dict(hidden=2048, n_layers=40, vocab=248320, full_interval=4, nh=16, nkv=2,
           t_default=oa.Q4_K, t_attn_v=oa.Q6_K, t_ffn_down=oa.Q6_K, t_output=oa.Q4_K, t_embd=oa.Q4_K,
           seed=0, sigma=0.02)
 
+# 397B-shaped MoE sized to one GPU: routed experts IQ2_XXS, the rest Q4_K
+C4 = dict(hidden=4096, n_layers=60, vocab=248320, full_interval=4, nh=32, nkv=2, hd=256,
+          nk=16, nv=64, dhead=128, conv_k=4, ne=512, top_k=10, moe_inter=1024, shared_inter=1024,
+          t_default=oa.Q4_K, t_attn_v=oa.Q4_K, t_ffn_down=oa.Q4_K, t_output=oa.Q4_K, t_embd=oa.Q4_K,
+          t_exps=oa.IQ2_XXS, seed=0, sigma=0.02)
+# C2 matvec microbench: [in x out] shapes and weight types
+C2_SHAPES = [(2048, 248320), (2048, 4096), (512, 2048)]
+C2_TYPES = [oa.Q8_0, oa.Q4_K, oa.Q6_K, oa.IQ2_XXS]
+C2_COLD_BYTES = 1 << 30          # distinct weight copies per cold measurement (> 256 MB of caches)
+
 
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
@@ -196,41 +206,15 @@ def cpu_baseline(model: oa.Model, cfg: dict, seconds: float) -> dict:
     """Oracle port (the C restatement of the reference path, same per-matvec
     thread fan-out) on this host: a 4-layer slice (3 delta-net + 1 GQA) of the
     same weights with the full 248320-row lm_head, written to a GGUF and run
-    for greedy decode steps after a 4-token prompt; per-token time scaled to 40
-    layers as lm_head+embed + 10 x (4-layer body)."""
+    for greedy decode steps after a 4-token prompt; per-token time scaled to
+    the model's layers as lm_head+embed + n_layers/4 x (4-layer body)."""
     sys.path.insert(0, str(ROOT / "tests"))
     import clibs
     L = clibs.oracle()
     ncores = min(16, len(os.sched_getaffinity(0)))
-    sl = dict(cfg, n_layers=4)
-    names = [n for n in tensor_names(sl)]
     with tempfile.TemporaryDirectory() as td:
-        path = str(Path(td) / "c3_slice.gguf")
-        w = L.orc_writer_new()
-        L.orc_w_string(w, b"general.architecture", b"qwen35moe")
-        L.orc_w_u32(w, b"qwen35moe.expert_used_count", cfg["top_k"])
-        L.orc_w_u32(w, b"qwen35moe.rope.dimension_count", 64)
-        L.orc_w_f32(w, b"qwen35moe.rope.freq_base", 1e7)
-        L.orc_w_f32(w, b"qwen35moe.attention.layer_norm_rms_epsilon", 1e-6)
-        toks = (C.c_char_p * cfg["vocab"])(*[f"t{i}".encode() for i in range(cfg["vocab"])])
-        L.orc_w_arr_str(w, b"tokenizer.ggml.tokens", toks, cfg["vocab"])
-        keep = []
-        for n in names:
-            info = model.tensor_info(n)
-            if info is None:
-                continue
-            data = model.tensor(n).download(info["nbytes"])
-            keep.append(data)
-            dims = [info["cols"], info["rows"]]
-            if "_exps." in n:
-                dims = [info["cols"], info["rows"] // cfg["ne"], cfg["ne"]]
-            elif info["rows"] == 1 and n.endswith(("_norm.weight", "ssm_a", "ssm_dt.bias", "ffn_gate_inp_shexp.weight")):
-                dims = [info["cols"]]
-            d = (C.c_uint64 * len(dims))(*dims)
-            assert L.orc_w_tensor(w, n.encode(), len(dims), d, info["type"], C.c_void_p(data.ctypes.data), data.nbytes) == 0
-        assert L.orc_writer_write(w, path.encode()) == 0, L.orc_last_error()
-        L.orc_writer_free(w)
-        del keep
+        path = str(Path(td) / "slice.gguf")
+        clibs.write_model_gguf(model, cfg, path, n_layers=4)
         m = C.c_void_p()
         assert L.orc_model_load(path.encode(), C.byref(m)) == 0, L.orc_last_error()
         L.orc_model_set_threads(m, ncores)
@@ -265,7 +249,7 @@ def cpu_baseline(model: oa.Model, cfg: dict, seconds: float) -> dict:
     return dict(value=1.0 / t_tok, unit="tok/s", cores=ncores, kind="port",
                 sample=f"oracle port, 4-layer slice (3 DN + 1 GQA) of the same weights + full lm_head: "
                        f"{steps} greedy steps after a 4-token prompt ({t_step4 * 1e3:.1f} ms/step) and {nh} "
-                       f"lm_head matvecs ({t_head * 1e3:.1f} ms); token time = head + 10 x body "
+                       f"lm_head matvecs ({t_head * 1e3:.1f} ms); token time = head + {cfg['n_layers'] // 4} x body "
                        f"= {t_tok * 1e3:.1f} ms; Q8 KV; {ncores} threads")
 
 
@@ -277,7 +261,7 @@ def batch_decode(model: oa.Model, n: int, ctx_len: int, steps: int) -> dict:
     rng = np.random.default_rng(1)
     for _ in range(n):
         s = model.session(ctx_len + steps + 8)
-        s.eval(rng.integers(0, C3["vocab"], ctx_len, dtype=np.int64).astype(np.int32))
+        s.eval(rng.integers(0, model.arch["vocab"], ctx_len, dtype=np.int64).astype(np.int32))
         sess.append(s)
     toks = np.array([int(np.argmax(s.logits())) for s in sess], np.int32)
     for _ in range(3):
@@ -299,12 +283,106 @@ KERNEL_SYMBOL = {"matvec": "oh_k_mv_q4k", "matvec_q6k": "oh_k_mv_q6k", "matvec_q
                  "step_body": "oh_k_step", "step_head": "oh_k_step"}
 
 
+def c2_bench(args) -> int:
+    """C2: the quantized matvec over N(0, 0.02) weights encoded on the device
+    (seeded), per type and [in x out] shape. Cold: launches go round-robin over
+    distinct copies of the weights totalling >= 1 GiB (more than L2 + MALL),
+    replayed as one HIP graph; hot: the same tensor every launch. CPU: the
+    oracle port's qdot / f32-fallback matvec on this host's cores."""
+    sys.path.insert(0, str(ROOT / "tests"))
+    import clibs
+    L = clibs.oracle()
+    ncores = min(16, len(os.sched_getaffinity(0)))
+    ctx = oa.Context(0)
+    rows = []
+    for (n, out) in C2_SHAPES:
+        w = (np.random.default_rng(hash((n, out)) & 0xffff).standard_normal(n * out, dtype=np.float32)
+             * np.float32(0.02))
+        x = np.random.default_rng(1).standard_normal(n, dtype=np.float32)
+        for t in C2_TYPES:
+            name = clibs.TYPE_NAMES[t]
+            enc = ctx.quantize(t, w)
+            ncopy = max(2, min(512, -(-C2_COLD_BYTES // enc.nbytes)))
+            ts = [ctx.upload(f"c2.{name}.{k}", t, enc, (n, out)) for k in range(ncopy)]
+            iters = max(2 * ncopy, 64)
+            cold = ctx.time_matvec_set(ts, iters)
+            hot = ts[0].time_matvec(64)
+            for tt in ts:
+                tt.free()
+            # CPU: one matvec of the same weights and activation
+            y = np.zeros(out, np.float32)
+            reps, t0 = 0, time.perf_counter()
+            while reps < 1 or time.perf_counter() - t0 < args.cpu_seconds / 12:
+                L.orc_matvec(t, clibs.bp(enc), n, out, clibs.f32p(x), clibs.f32p(y), 0, ncores)
+                reps += 1
+            cpu_ms = (time.perf_counter() - t0) / reps * 1e3
+            r = {"type": name, "in": n, "out": out, "weight_bytes": int(enc.nbytes), "copies": ncopy,
+                 "cold_us": round(cold * 1e3, 3), "cold_gbs": round(enc.nbytes / (cold * 1e-3) / 1e9, 1),
+                 "hot_us": round(hot * 1e3, 3), "hot_gbs": round(enc.nbytes / (hot * 1e-3) / 1e9, 1),
+                 "cpu_ms": round(cpu_ms, 3), "cpu_threads": ncores}
+            log(f"C2 {name:8s} [{n} x {out}] {enc.nbytes / 1e6:8.2f} MB: cold {r['cold_us']:9.2f} us "
+                f"({r['cold_gbs']:7.1f} GB/s), hot {r['hot_us']:9.2f} us ({r['hot_gbs']:7.1f} GB/s), "
+                f"cpu {cpu_ms:9.3f} ms")
+            rows.append(r)
+        del w
+    big = [r for r in rows if r["out"] == C2_SHAPES[0][1]]
+    best = max(big, key=lambda r: r["cold_gbs"])
+    print(json.dumps({"metric": "C2 quantized matvec, cold HBM GB/s of the weight stream", "value": best["cold_gbs"],
+                      "unit": "GB/s", "n_gpus": 1, "higher_is_better": True, "data": "synthetic",
+                      "config": {"workload": "ornith_qdot matvec microbench (C2)", "best": best["type"]},
+                      "roofline": {"bound": "hbm", "achieved": best["cold_gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                   "frac": round(best["cold_gbs"] / HBM_PEAK_GBS, 4)},
+                      "rows": rows}), flush=True)
+    ctx.close()
+    return 0
+
+
+def c5_bench(args) -> int:
+    """C5: the C3 weights, a 32768-token random prompt through the chunked
+    layer-major prefill (2048-token chunks), then greedy decode at batch 1 and
+    at batch 8 (eight independent seeded prompts of the same length)."""
+    ctx = oa.Context(0)
+    model = ctx.synth(**C3)
+    ctx.sync()
+    T = args.ctx
+    steps = args.steps
+    sess = model.session(T + steps + 16)
+    prompt = np.random.default_rng(0).integers(0, C3["vocab"], T, dtype=np.int64).astype(np.int32)
+    t0 = time.perf_counter()
+    sess.eval(prompt)
+    t_pf = time.perf_counter() - t0
+    log(f"C5 prompt of {T} tokens: {t_pf:.2f} s ({T / t_pf:.0f} tok/s)")
+    ms = sess.time_decode(steps)
+    log(f"C5 batch 1: {steps} steps after {T} tokens: {ms / steps:.3f} ms/step -> {steps / (ms / 1e3):.1f} tok/s")
+    bpt = bytes_per_token(model, C3, T + steps / 2)
+    sess.free()
+    bt = None
+    if args.batch > 0:
+        bt = batch_decode(model, args.batch, T, args.batch_steps)
+        log(f"C5 batch {args.batch}: {bt['ms_per_step']:.2f} ms/step -> {bt['tok_s']:.1f} tok/s")
+    tok_s = steps / (ms / 1e3)
+    print(json.dumps({"metric": "C5 long-context decode tok/s after a chunked 32K prefill", "value": round(tok_s, 2),
+                      "unit": "tok/s", "n_gpus": 1, "steps": steps, "ms_per_step": round(ms / steps, 4),
+                      "higher_is_better": True, "data": "synthetic",
+                      "config": {"workload": "35B-shaped decode after a 32768-token chunked prefill (C5)",
+                                 "context_tokens": T, "prefill_chunk": 2048},
+                      "prefill_tok_s": round(T / t_pf, 1), "prefill_s": round(t_pf, 3),
+                      "hbm_gbs_step": round(bpt["total"] * tok_s / 1e9, 1),
+                      "bytes_per_token": {k: round(v) for k, v in bpt.items()}, "batch_decode": bt}), flush=True)
+    model.free()
+    ctx.close()
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--config", choices=("c3", "c2", "c4", "c5"), default="c3",
+                    help="c3: the headline decode bench (default); c2: matvec microbench; c4: 397B-shaped "
+                         "IQ2_XXS-expert decode; c5: 32K prefill + long-context decode at batch 1 and 8")
+    ap.add_argument("--steps", type=int, default=None, help="decode steps (c3 256, c4 128, c5 512)")
     ap.add_argument("--warmup", type=int, default=8)
-    ap.add_argument("--ctx", type=int, default=4096, help="prompt tokens before decode")
+    ap.add_argument("--ctx", type=int, default=None, help="prompt tokens before decode (c3 4096, c4 2048, c5 32768)")
     ap.add_argument("--profile-reps", type=int, default=3)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
@@ -324,17 +402,33 @@ def main() -> int:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); "
               "multi-GPU sharding is a design, not a code path, in this build", file=sys.stderr)
         return 2
+    dflt = {"c3": (4096, 256), "c4": (2048, 128), "c5": (32768, 512), "c2": (0, 0)}[args.config]
+    args.ctx = dflt[0] if args.ctx is None else args.ctx
+    args.steps = dflt[1] if args.steps is None else args.steps
+    if args.config == "c2":
+        return c2_bench(args)
+    if args.config == "c5":
+        return c5_bench(args)
+    cfg = C3 if args.config == "c3" else C4
+    if args.config == "c4":
+        args.batch = 0
+        workload = ("397B-shaped qwen35moe decode sized to one GPU, batch 1, routed experts IQ2_XXS, the rest Q4_K, "
+                    f"{args.ctx}-token Q8 KV context, greedy")
+        dtype = "f32 (IQ2_XXS experts: the reference's f32 fallback) + int8 dot (Q8_K x Q4_K)"
+    else:
+        workload = ("35B-shaped qwen35moe decode, batch 1, Q4_K_M mix (Q6_K attn_v/ffn_down), "
+                    f"{args.ctx}-token Q8 KV context, greedy")
+        dtype = "int8 dot (Q8_K x Q4_K/Q6_K) + f32"
 
     ctx = oa.Context(0)
     t0 = time.perf_counter()
-    model = ctx.synth(**C3)
+    model = ctx.synth(**cfg)
     ctx.sync()
     t_synth = time.perf_counter() - t0
-    log(f"synthesised 35B-shaped model in HBM: {model.nbytes / 1e9:.2f} GB in {t_synth:.1f} s")
-
+    log(f"synthesised {args.config} model in HBM: {model.nbytes / 1e9:.2f} GB in {t_synth:.1f} s")
     cap = args.ctx + args.warmup + args.steps + args.profile_reps + 8
     sess = model.session(cap)
-    prompt = np.random.default_rng(0).integers(0, C3["vocab"], args.ctx, dtype=np.int64).astype(np.int32)
+    prompt = np.random.default_rng(0).integers(0, cfg["vocab"], args.ctx, dtype=np.int64).astype(np.int32)
     t0 = time.perf_counter()
     sess.eval(prompt)
     t_prefill = time.perf_counter() - t0
@@ -352,7 +446,7 @@ def main() -> int:
     log(f"timed {args.steps} decode steps: {ms:.2f} ms (events), {wall * 1e3:.2f} ms (wall) -> {tok_s:.1f} tok/s")
 
     ctx_mid = args.ctx + args.warmup + args.steps / 2
-    bpt = bytes_per_token(model, C3, ctx_mid)
+    bpt = bytes_per_token(model, cfg, ctx_mid)
     step_gbs = bpt["total"] * tok_s / 1e9
 
     # per-launch HIP events around every kernel of one eager step rank the
@@ -377,7 +471,7 @@ def main() -> int:
     cpu = None
     if not args.no_cpu:
         try:
-            cpu = cpu_baseline(model, C3, args.cpu_seconds)
+            cpu = cpu_baseline(model, cfg, args.cpu_seconds)
             log(f"cpu baseline: {cpu['value']:.3f} tok/s on {cpu['cores']} threads")
         except Exception as e:  # reported, never hides the GPU number
             log(f"cpu baseline failed: {e!r}")
@@ -386,9 +480,8 @@ def main() -> int:
         "metric": METRIC, "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms / args.steps, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "int8 dot (Q8_K x Q4_K/Q6_K) + f32", "data": "synthetic",
-        "config": {"workload": "35B-shaped qwen35moe decode, batch 1, Q4_K_M mix (Q6_K attn_v/ffn_down), "
-                               "4096-token Q8 KV context, greedy",
+        "dtype": dtype, "data": "synthetic",
+        "config": {"workload": workload,
                    "context_tokens": args.ctx, "batch": 1, "weights_gb": round(model.nbytes / 1e9, 3),
                    "parallelism": "single GPU"},
         "hbm_gbs_step": round(step_gbs, 1), "roofline_frac_step": round(step_gbs / HBM_PEAK_GBS, 4),

@@ -226,6 +226,13 @@ int  ornith_hip_session_profile_phases(ornith_hip_session *s, int max_phases, in
  * the device) with HIP events on the context stream; *ms = mean per launch. */
 int  ornith_hip_time_matvec(ornith_hip_ctx *ctx, const ornith_hip_tensor *W, int iters,
                             float *ms);
+/* Cold-cache variant: n weight tensors of one type and shape (distinct
+ * copies, together larger than the device caches) take turns; `iters`
+ * launches in that round-robin order are captured as one HIP graph and
+ * replayed between HIP events; *ms = mean per launch. No reference twin
+ * (measurement only). */
+int  ornith_hip_time_matvec_set(ornith_hip_ctx *ctx, const ornith_hip_tensor *const *W, int n, int iters,
+                                float *ms);
 
 #ifdef __cplusplus
 }

@@ -96,6 +96,7 @@ _SIGS = {
     "ornith_hip_session_get_kv": (C.c_int, [_vp, C.c_int, _vp, _fp, _vp, _fp]),
     "ornith_hip_session_time_decode": (C.c_int, [_vp, C.c_int, _fp]),
     "ornith_hip_time_matvec": (C.c_int, [_vp, _vp, C.c_int, _fp]),
+    "ornith_hip_time_matvec_set": (C.c_int, [_vp, C.POINTER(_vp), C.c_int, C.c_int, _fp]),
     "ornith_hip_session_profile_step": (C.c_int, [_vp, C.c_int, _ip, C.POINTER(C.c_double), _fp, _ip]),
     "ornith_hip_session_time_kind": (C.c_int, [_vp, C.c_int, C.c_int, _fp, C.POINTER(C.c_double), _ip]),
     "ornith_hip_session_profile_phases": (C.c_int, [_vp, C.c_int, _ip, C.POINTER(C.c_double), _fp, _ip]),
@@ -175,6 +176,15 @@ class Context:
         _check(lib().ornith_hip_quantize(self.h, ggml_type, _f32(x), x.size, out.ctypes.data_as(_vp)),
                "ornith_hip_quantize")
         return out
+
+    def time_matvec_set(self, tensors, iters: int) -> float:
+        """Mean ms per matvec launch, round-robin over distinct tensors of one
+        type and shape (cold caches), replayed as one HIP graph."""
+        arr = (_vp * len(tensors))(*[t.h for t in tensors])
+        ms = C.c_float(0)
+        _check(lib().ornith_hip_time_matvec_set(self.h, arr, len(tensors), iters, C.byref(ms)),
+               "ornith_hip_time_matvec_set")
+        return ms.value
 
     def quantize_q8k(self, x: np.ndarray) -> np.ndarray:
         x = np.ascontiguousarray(x, np.float32)

@@ -282,6 +282,12 @@ OH_DEV float2 ldg(const float2 *p) {
     const oh_f2 v = *(const OH_GLOBAL oh_f2 *)p;
     return make_float2(v.x, v.y);
 }
+typedef unsigned oh_u2 __attribute__((ext_vector_type(2)));
+template <>
+OH_DEV uint2 ldg(const uint2 *p) {
+    const oh_u2 v = *(const OH_GLOBAL oh_u2 *)p;
+    return make_uint2(v.x, v.y);
+}
 template <>
 OH_DEV void stg(float4 *p, const float4 &v) {
     oh_f4 r;

@@ -317,8 +317,8 @@ static int mv_add(MvBuild &b, const ornith_hip_tensor *W, const Act &act, float 
     s.rows = eidx ? (int)W->dims[1] : (int)W->rows;
     s.mode = mode;
     s.nb = (int)(W->in / 256);
-    if (act.pro == OH_PRO_GNORM && (W->in > 4096 || act.gdim % 64 || W->in % act.gdim || !oh_qdot_can(W->type, W->in))) {
-        seterr("matvec '%s': gated-norm prologue needs an integer-path type, in <= 4096 and 64 | head | in", W->name.c_str());
+    if (act.pro == OH_PRO_GNORM && (W->in > 8192 || act.gdim % 64 || W->in % act.gdim || !oh_qdot_can(W->type, W->in))) {
+        seterr("matvec '%s': gated-norm prologue needs an integer-path type, in <= 8192 and 64 | head | in", W->name.c_str());
         return ORNITH_HIP_ERR_UNSUPPORTED;
     }
     if (act.pro != OH_PRO_Q8K && (W->in % 256 || W->in > 8192)) {
@@ -391,17 +391,17 @@ static void mv_plan(MvBuild &b, int waves = 4096) {
             s.bps = (s.units + OH_MV_WAVES * s.upw - 1) / (OH_MV_WAVES * s.upw);
         } else {
             s.upw = 1;
-            s.bps = (s.rows + 255) / 256;
+            s.bps = s.type == OH_IQ2_XXS ? (s.rows + OH_IQ2_ROWS - 1) / OH_IQ2_ROWS : (s.rows + 255) / 256;
         }
         s.block0 = blocks;
         blocks += s.bps * s.nsub;
         const int nb = s.in / 256;
         const int voff = (nb * 272 + nb * 36 + 15) & ~15;
-        const int need = voff + ((!q8 || s.pro != OH_PRO_Q8K) ? s.in * 4 : 0) + (s.pro == OH_PRO_GNORM ? 256 : 0);
+        int need = voff + ((!q8 || s.pro != OH_PRO_Q8K) ? s.in * 4 : 0) + (s.pro == OH_PRO_GNORM ? 512 : 0);
+        if (!q8 && s.type == OH_IQ2_XXS) need = ((voff + s.in * 4 + 15) & ~15) + 2048;   // + the grid
         if (need > b.lds) b.lds = need;
     }
     if (b.L.route && ((b.L.ne + 3) & ~3) * 4 > b.lds) b.lds = ((b.L.ne + 3) & ~3) * 4;
-
     b.L.total_blocks = blocks;
 }
 
@@ -618,6 +618,73 @@ extern "C" int ornith_hip_time_matvec(ornith_hip_ctx *ctx, const ornith_hip_tens
     (void)hipEventDestroy(e0);
     (void)hipEventDestroy(e1);
     *ms = iters > 0 ? el / (float)iters : 0.0f;
+    return ORNITH_HIP_OK;
+}
+
+extern "C" int ornith_hip_time_matvec_set(ornith_hip_ctx *ctx, const ornith_hip_tensor *const *W, int n,
+                                          int iters, float *ms) {
+    if (n < 1 || iters < 1) { seterr("time_matvec_set: need n >= 1 and iters >= 1"); return ORNITH_HIP_ERR_FORMAT; }
+    for (int i = 1; i < n; i++)
+        if (W[i]->type != W[0]->type || W[i]->in != W[0]->in || W[i]->rows != W[0]->rows) {
+            seterr("time_matvec_set: tensors differ in type or shape");
+            return ORNITH_HIP_ERR_FORMAT;
+        }
+    HCHK(hipSetDevice(ctx->device));
+    const int64_t in = W[0]->in, out = W[0]->rows, nb = in / 256;
+    void *sp;
+    CHK(ctx_scratch(ctx, (size_t)in * 5 + (size_t)nb * 40 + (size_t)out * 4 + 4096, &sp));
+    float *dx = (float *)sp;
+    float *dy = (float *)up256((size_t)(dx + in));
+    int8_t *qs = (int8_t *)up256((size_t)(dy + out));
+    float *dd = (float *)up256((size_t)(qs + in));
+    int16_t *bs = (int16_t *)up256((size_t)(dd + nb + 1));
+    std::vector<float> hx((size_t)in);
+    for (int64_t i = 0; i < in; i++) hx[i] = (float)((i * 7919) % 255 - 127) / 64.0f;
+    HCHK(hipMemcpyAsync(dx, hx.data(), (size_t)in * 4, hipMemcpyHostToDevice, ctx->st));
+    Act act;
+    act.xf = dx;
+    if (oh_qdot_can(W[0]->type, in)) {
+        for (int64_t off = 0; off < in; off += 8192) {
+            const int k = (int)(in - off < 8192 ? in - off : 8192);
+            HCHK(oh_launch_rmsnorm_q8k(dx + off, nullptr, 0.0f, k, nullptr, qs + off, dd + off / 256,
+                                       bs + off / 16, ctx->st));
+        }
+        act.qs = qs; act.d = dd; act.bs = bs;
+    }
+    std::vector<MvBuild> bl((size_t)n);
+    for (int i = 0; i < n; i++) {
+        CHK(mv_add(bl[i], W[i], act, dy, 0));
+        mv_plan(bl[i]);
+    }
+    HCHK(hipStreamSynchronize(ctx->st));
+    hipGraph_t g = nullptr;
+    hipGraphExec_t ge = nullptr;
+    HCHK(hipStreamBeginCapture(ctx->st, hipStreamCaptureModeThreadLocal));
+    hipError_t ce = hipSuccess;
+    for (int i = 0; i < iters && ce == hipSuccess; i++) ce = oh_launch_matvec(&bl[i % n].L, bl[i % n].tk, bl[i % n].lds, ctx->st);
+    const hipError_t ee = hipStreamEndCapture(ctx->st, &g);
+    if (ce != hipSuccess || ee != hipSuccess) {
+        if (g) (void)hipGraphDestroy(g);
+        HCHK(ce != hipSuccess ? ce : ee);
+    }
+    hipError_t ie = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    HCHK(ie);
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    float el = 0.0f;
+    hipError_t r = hipGraphLaunch(ge, ctx->st);                  // warm
+    if (r == hipSuccess) r = hipEventCreate(&e0);
+    if (r == hipSuccess) r = hipEventCreate(&e1);
+    if (r == hipSuccess) r = hipEventRecord(e0, ctx->st);
+    if (r == hipSuccess) r = hipGraphLaunch(ge, ctx->st);
+    if (r == hipSuccess) r = hipEventRecord(e1, ctx->st);
+    if (r == hipSuccess) r = hipEventSynchronize(e1);
+    if (r == hipSuccess) r = hipEventElapsedTime(&el, e0, e1);
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    (void)hipGraphExecDestroy(ge);
+    HCHK(r);
+    *ms = el / (float)iters;
     return ORNITH_HIP_OK;
 }
 
@@ -882,7 +949,7 @@ static int infer_arch(ornith_hip_model *m, const Meta &md) {
             if (a.dk != 64 && a.dk != 128) return bad("linear head dim must be 64 or 128");
             if (a.nv % (256 / a.dk) || a.nk < 1) return bad("linear value heads must fill 256-element blocks");
             if (a.conv_k < 2 || a.conv_k > 8) return bad("conv kernel must be in [2, 8]");
-            if (a.nv * a.dv > 4096) return bad("linear value width must be <= 4096");
+            if (a.nv * a.dv > 8192) return bad("linear value width must be <= 8192");
         }
         if (a.ne > 0) {
             if (!y.router || !y.gate_exps || !y.up_exps || !y.down_exps) return bad("MoE tensors missing");
@@ -1348,14 +1415,12 @@ static int build_body(ornith_hip_session *s, Prog &P) {
             CHK(mv_add(b, y.router, pst, s->rl, 0));
             if (y.gate_inp_sh) CHK(mv_add(b, y.gate_inp_sh, pn, s->shl, 0));
             prog_mv(P, b);
-            // experts gate/up: every block routes first (top-k + softmax), the
-            // stacked segments then read the routed experts
             const Act ax = act_of(s->xq, s->xn);
+            const bool paired = pairable(y.gate_exps, y.up_exps) && (!y.gate_sh || pairable(y.gate_sh, y.up_sh));
+            MvBuild b2;
             // experts gate/up: every block routes first (top-k + softmax), the
             // stacked segments then read the routed experts; gate and up rows
             // are reduced together and emit h = silu(gate) * up
-            const bool paired = pairable(y.gate_exps, y.up_exps) && (!y.gate_sh || pairable(y.gate_sh, y.up_sh));
-            MvBuild b2;
             if (paired) {
                 CHK(mv_add_pair(b2, y.gate_exps, y.up_exps, ax, s->h, s->eidx, K, IW));
                 if (y.gate_sh) CHK(mv_add_pair(b2, y.gate_sh, y.up_sh, ax, s->h + (size_t)K * IW));
@@ -1550,7 +1615,6 @@ static int step_launch(ornith_hip_session *s, bool body, uint64_t *ts, bool adva
 
 // a grid wait of the step kernel that gave up leaves io[OH_IO_ERR] set
 static int step_check(ornith_hip_session *s) {
-    if (!s->step_grid) return ORNITH_HIP_OK;
     int32_t err = 0;
     HCHK(hipMemcpy(&err, s->io + OH_IO_ERR, 4, hipMemcpyDeviceToHost));
     if (err) {

@@ -15,6 +15,16 @@ hipError_t oh_launch_matvec(const oh_mvlaunch *L, int tk, int lds_bytes, hipStre
     if (L->total_blocks <= 0) return hipSuccess;
     void (*k)(oh_mvlaunch) = tk == OH_Q4_K ? oh_k_mv_q4k : tk == OH_Q6_K ? oh_k_mv_q6k
                            : tk == OH_Q8_0 ? oh_k_mv_q80 : oh_k_mv_mixed;
+    if (lds_bytes > 65536) {
+        // wide fallback rows (IQ2_XXS products, f32 activations past 8K)
+        static bool raised[4];
+        const int ki = tk == OH_Q4_K ? 0 : tk == OH_Q6_K ? 1 : tk == OH_Q8_0 ? 2 : 3;
+        if (!raised[ki]) {
+            const hipError_t e = hipFuncSetAttribute((const void *)k, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+            if (e != hipSuccess) return e;
+            raised[ki] = true;
+        }
+    }
     hipLaunchKernelGGL(k, dim3(L->total_blocks), dim3(256), (size_t)lds_bytes, st, *L);
     return hipGetLastError();
 }

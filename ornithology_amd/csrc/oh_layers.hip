@@ -264,34 +264,40 @@ OH_DEV void prep_body(const oh_op_prep &a, int vb, int pos, W &w) {
     const int nh = a.nh, nkv = a.nkv, hd = a.hd, cap = a.cap;
     const bool isq = hb < nh;
     const int h = isq ? hb : hb - nh;
-    const float *src = isq ? a.qproj + (size_t)h * 2 * hd : a.kin + (size_t)h * hd;
-    const float x = t < hd ? ldc(src + t) : 0.0f;
-    double ss = block_sum_d((double)x * x, red);
-    const float inv = (float)(1.0 / sqrt(ss / (double)hd + (double)a.eps));
-    const float *nw = isq ? a.q_norm : a.k_norm;
-    if (t < hd) v[t] = x * inv * ldg(nw + t);
-    __syncthreads();
     const int r = a.rot <= 0 || a.rot > hd ? hd : a.rot;
     const int half = r / 2;
+    // every input is requested before the first reduction: the head's
+    // values, its norm weight, the RoPE (cos, sin) of this element's pair,
+    // and the gate (query heads) or the raw v (kv heads)
+    const float *src = isq ? a.qproj + (size_t)h * 2 * hd : a.kin + (size_t)h * hd;
+    const float *nw = isq ? a.q_norm : a.k_norm;
     const float2 *rope = (const float2 *)a.rope;
+    const float x = t < hd ? ldc(src + t) : 0.0f;
+    const float nwt = t < hd ? ldg(nw + t) : 0.0f;
+    const int pi = t < half ? t : t - half;
+    const float2 cs = t < 2 * half ? ldg(rope + (size_t)pos * (hd / 2) + pi) : make_float2(1.0f, 0.0f);
+    const float other = t < hd ? (isq ? ldc(a.qproj + (size_t)h * 2 * hd + hd + t) : ldc(a.vin + (size_t)h * hd + t))
+                               : 0.0f;
+    double ss = block_sum_d((double)x * x, red);
+    const float inv = (float)(1.0 / sqrt(ss / (double)hd + (double)a.eps));
+    if (t < hd) v[t] = x * inv * nwt;
+    __syncthreads();
     float y = t < hd ? v[t] : 0.0f;
     if (t < half) {
-        const float2 cs = ldg(rope + (size_t)pos * (hd / 2) + t);
         y = v[t] * cs.x - v[t + half] * cs.y;
     } else if (t >= half && t < 2 * half) {
-        const float2 cs = ldg(rope + (size_t)pos * (hd / 2) + (t - half));
         y = v[t - half] * cs.y + v[t] * cs.x;
     }
     if (isq) {
         if (t < hd) {
             stc(a.qr + (size_t)h * hd + t, y);
-            stc(a.gate + (size_t)h * hd + t, ldc(a.qproj + (size_t)h * 2 * hd + hd + t));
+            stc(a.gate + (size_t)h * hd + t, other);
         }
         return;
     }
     // Q8 encode of k (post norm/rope) and raw v (src/ornith_attn.c:65-77)
     for (int which = 0; which < 2; which++) {
-        const float val = which == 0 ? y : (t < hd ? ldc(a.vin + (size_t)h * hd + t) : 0.0f);
+        const float val = which == 0 ? y : other;
         float am = wave_max_f(fabsf(val));
         __syncthreads();
         if (lane_id() == 0) amax_s[t >> 6] = am;
@@ -466,24 +472,48 @@ template <int HB> struct FlashLds {
     }
 };
 
-// the chunk of KV group g starting at t0 (positions past T - 1 read T - 1's)
+// the chunk of KV group g starting at t0 (positions past T - 1 read T - 1's).
+// Every load of the tile (at most 16 key words and 4 value pieces per thread,
+// hd <= 256) is issued before the first LDS store, so the tile costs one
+// memory round trip rather than one per loop pass.
 template <int HB>
 OH_DEV void flash_tile(const oh_op_attn &a, const FlashLds<HB> &L, int g, int t0, int T) {
     const int tid = tid_x(), hd = a.hd, hw = hd / 4, cap = a.cap, nkv = a.nkv;
-    for (int k = tid; k < hw * kFlashCh; k += 256) {
+    constexpr int KW = 64 * kFlashCh / 256, VW = (kFlashCh / 16) * 256 / 256;
+    const int nkw = hw * kFlashCh, nvw = (kFlashCh / 16) * hd;
+    uint32_t kr[KW];
+    uint4 vr[VW];
+#pragma unroll
+    for (int u = 0; u < KW; u++) {
+        const int k = tid + 256 * u < nkw ? tid + 256 * u : nkw - 1;
         const int wi = k / kFlashCh, j = k % kFlashCh;
         const int t = t0 + j < T ? t0 + j : T - 1;
-        L.kc[j * L.kst + wi] = ldg(a.Kt + ((size_t)g * hw + wi) * cap + t);
+        kr[u] = ldg(a.Kt + ((size_t)g * hw + wi) * cap + t);
     }
-    for (int k = tid; k < (kFlashCh / 16) * hd; k += 256) {
+#pragma unroll
+    for (int u = 0; u < VW; u++) {
+        const int k = tid + 256 * u < nvw ? tid + 256 * u : nvw - 1;
         const int tt = k / hd, i = k % hd;
         const int tile = (t0 / 16 + tt) * 16 < T ? t0 / 16 + tt : (T - 1) / 16;
-        L.vt[k] = ldg((const uint4 *)a.Vq + ((size_t)g * (cap / 16) + tile) * hd + i);
+        vr[u] = ldg((const uint4 *)a.Vq + ((size_t)g * (cap / 16) + tile) * hd + i);
     }
+    float ksv = 0.0f, vsv = 0.0f;
     if (tid < kFlashCh) {
         const int t = t0 + tid < T ? t0 + tid : T - 1;
-        L.ks[tid] = ldg(a.Ks + (size_t)t * nkv + g);
-        L.vs[tid] = ldg(a.Vs + (size_t)t * nkv + g);
+        ksv = ldg(a.Ks + (size_t)t * nkv + g);
+        vsv = ldg(a.Vs + (size_t)t * nkv + g);
+    }
+#pragma unroll
+    for (int u = 0; u < KW; u++) {
+        const int k = tid + 256 * u;
+        if (k < nkw) L.kc[(k % kFlashCh) * L.kst + k / kFlashCh] = kr[u];
+    }
+#pragma unroll
+    for (int u = 0; u < VW; u++)
+        if (tid + 256 * u < nvw) L.vt[tid + 256 * u] = vr[u];
+    if (tid < kFlashCh) {
+        L.ks[tid] = ksv;
+        L.vs[tid] = vsv;
     }
 }
 
@@ -620,8 +650,18 @@ OH_DEV void flash_body(const oh_op_attn &a, int vb, int pos, int lim, W &w) {
     if (T <= lim || t0 >= T) return;
     if (!w.wait()) return;
     const FlashLds<HB> L(fsm, a.hd);
+    // the queries (written by the prep phase) and the tile are all requested
+    // before the first wait: HB * hd <= 1024 floats, at most 4 per thread
+    const int tid = tid_x(), nq = HB * a.hd;
+    const float *qs = a.qr + ((size_t)g * G + hb0) * a.hd;
+    float qv[4];
+#pragma unroll
+    for (int m = 0; m < 4; m++) qv[m] = ldc(qs + (tid + 256 * m < nq ? tid + 256 * m : nq - 1));
     flash_tile<HB>(a, L, g, t0, T);
-    flash_token<HB, true>(a, L, g, hb0, c, T, a.qr, a.part_o, a.part_ml);
+#pragma unroll
+    for (int m = 0; m < 4; m++)
+        if (tid + 256 * m < nq) flash_q_put<HB>(L, a.hd, tid + 256 * m, qv[m]);
+    flash_token<HB, true, false>(a, L, g, hb0, c, T, nullptr, a.part_o, a.part_ml);
 }
 
 // The attention of the current step: up to lim = min(exact_max, kExactMax)
@@ -658,11 +698,13 @@ OH_DEV void combine_body(const oh_op_attn &a, int vb, int pos, W &w) {
     const int i = (vb / nh) * 64 + lane;
     const int nch = (T + kFlashCh - 1) / kFlashCh, nchmax = (cap + kFlashCh - 1) / kFlashCh;
     float M = -INFINITY, L = 0.0f, O = 0.0f;
-    // chunks wave, wave+4, ... in order; their partials requested 8 at a time
-    for (int c0 = wave; c0 < nch; c0 += 32) {
-        float mb[8], lb[8], ob[8];
+    // chunks wave, wave+4, ... in order; their partials requested 32 at a
+    // time (one round trip up to 128 chunks = 8192 positions)
+    constexpr int CB = 32;
+    for (int c0 = wave; c0 < nch; c0 += 4 * CB) {
+        float mb[CB], lb[CB], ob[CB];
 #pragma unroll
-        for (int u = 0; u < 8; u++) {
+        for (int u = 0; u < CB; u++) {
             const int c = c0 + 4 * u < nch ? c0 + 4 * u : c0;
             const size_t base = ((size_t)g * nchmax + c) * G + hl;
             mb[u] = ldc(a.part_ml + base * 2);
@@ -670,7 +712,7 @@ OH_DEV void combine_body(const oh_op_attn &a, int vb, int pos, W &w) {
             ob[u] = ldc(a.part_o + base * hd + i);
         }
 #pragma unroll
-        for (int u = 0; u < 8; u++) {
+        for (int u = 0; u < CB; u++) {
             if (c0 + 4 * u >= nch) break;
             const float m = mb[u], mn = fmaxf(M, m);
             const float e1 = M == -INFINITY ? 0.0f : __expf(M - mn), e2 = __expf(m - mn);

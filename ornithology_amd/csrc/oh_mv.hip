@@ -176,22 +176,6 @@ OH_DEV void q8k_all(const float *v, int nb, int8_t *qs, float *d, int16_t *bs, i
     for (int q0 = wave; q0 < nb; q0 += 16) q8k_blocks<4>(v, q0, 4, nb, qs, d, bs, qstride);
 }
 
-// In-place RMSNorm of v[0..n) in LDS (src/ornith_tensor.c:100-106): sum of
-// squares in double (tree-ordered), inv = (float)(1/sqrt(ss/n+eps)),
-// v_i = v_i * inv * w_i. All 256 threads; v must be visible block-wide.
-OH_DEV void rmsnorm_lds(float *v, const float *w, float eps, int n, double *red) {
-    const int tid = tid_x(), wave = tid >> 6;
-    double ss = 0.0;
-    for (int i = tid; i < n; i += 256) ss += (double)v[i] * v[i];
-    ss = wave_sum_d(ss);
-    if (lane_id() == 0) red[wave] = ss;
-    lds_barrier();
-    const double tot = (red[0] + red[1]) + (red[2] + red[3]);
-    const float inv = (float)(1.0 / sqrt(tot / (double)n + (double)eps));
-    for (int i = tid; i < n; i += 256) v[i] = v[i] * inv * ldg(w + i);
-    lds_barrier();
-}
-
 // ---- one super-block per lane ----------------------------------------------------
 // A lane owns one 256-element super-block of a weight row: it loads the
 // block's A-plane pieces (coalesced across the wave by the tile interleave)
@@ -325,8 +309,9 @@ OH_DEV void emit(float *y, int mode, int row, float v) {
     else stc(y + row, v);
 }
 
-// Fallback row: dequantise on the fly and accumulate w_i * x_i strictly in
-// order (reference mv_run f32 path + ot_dot, src/ornith_rforward.c:119-133).
+// Fallback row of an F32 / F16 / BF16 tensor: convert on the fly and
+// accumulate w_i * x_i strictly in order (reference mv_run f32 path + ot_dot,
+// src/ornith_rforward.c:119-133).
 OH_DEV float row_seq(const oh_mvseg &s, int64_t r, const float *x) {
     const int in = s.in;
     float acc = 0.0f;
@@ -339,27 +324,6 @@ OH_DEV float row_seq(const oh_mvseg &s, int64_t r, const float *x) {
             const uint16_t wr = ldg(w + i);
             const float wf = s.type == OH_F16 ? h2f(wr) : u2f((uint32_t)wr << 16);
             acc += wf * x[i];
-        }
-    } else if (s.type == OH_IQ2_XXS) {
-        const int nb = in / 256;
-        for (int b = 0; b < nb; b++) {
-            const int64_t bi = r * nb + b;
-            const float d = h2f(ldg((const uint16_t *)(s.C + bi * 2)));
-            const uint32_t *q = (const uint32_t *)(s.A + bi * 64);
-            for (int g32 = 0; g32 < 8; g32++) {
-                const uint32_t w0 = ldg(q + 2 * g32), w1 = ldg(q + 2 * g32 + 1);
-                const float db = d * (0.5f + (float)(w1 >> 28)) * 0.25f;
-                for (int k = 0; k < 4; k++) {
-                    const uint64_t gv = k_iq2_grid[(w0 >> (8 * k)) & 0xffu];
-                    const uint32_t s7 = (w1 >> (7 * k)) & 127u;
-                    const uint32_t sg = s7 | ((__popc(s7) & 1u) << 7);
-                    const float *xx = x + b * 256 + g32 * 32 + k * 8;
-                    for (int j = 0; j < 8; j++) {
-                        const float wv = db * (float)((gv >> (8 * j)) & 0xffu) * ((sg >> j) & 1u ? -1.0f : 1.0f);
-                        acc += wv * xx[j];
-                    }
-                }
-            }
         }
     }
     return acc;
@@ -413,8 +377,73 @@ OH_HD inline int mv_lds_bs_off(int nb) { return nb * kAS; }
 OH_HD inline int mv_lds_d_off(int nb) { return nb * kAS + nb * 32; }
 OH_HD inline int mv_lds_v_off(int nb) { return (nb * kAS + nb * 36 + 15) & ~15; }
 
-// Block prologue: form the slot's activation in LDS. q8: Q8_K planes are
-// needed (integer path); otherwise only the f32 vector v.
+// IQ2_XXS rows (src/ornith_quant.c:660-680 decode, then ot_dot's strictly
+// sequential f32 accumulation, src/ornith_rforward.c:119-133): one lane per
+// row walks its row in element order, forming y_i * x_i and adding it at once.
+// y = (db * g) * (+-1), so y * x = +-((db * g) * x) exactly, and acc + (-t) is
+// acc - t. The f32 activation and the 256-entry grid sit in LDS (every lane
+// reads the same activation word); each row's next super-block (64 code bytes
+// and d) is in flight while the current one is reduced. LDS after v: the grid.
+OH_HD inline int mv_lds_iq2_off(int nb, int in) { return (mv_lds_v_off(nb) + in * 4 + 15) & ~15; }
+
+OH_DEV void iq2_rows(const oh_mvseg &s, int slot, int blk, int expert, uint8_t *smem) {
+    const int in = s.in, nb = in / 256, tid = tid_x();
+    const float *v = (const float *)(smem + mv_lds_v_off(nb));
+    uint64_t *grid = (uint64_t *)(smem + mv_lds_iq2_off(nb, in));
+    const int row = blk * OH_IQ2_ROWS + tid;
+    const int64_t bi0 = ((int64_t)expert * s.rows + (row < s.rows ? row : s.rows - 1)) * nb;
+    uint4 qa[4], qn[4];
+    uint16_t da, dn;
+    auto fetch = [&](uint4 *q, uint16_t &d, int b) {
+        const int bc = b < nb ? b : nb - 1;
+        const uint4 *src = (const uint4 *)(s.A + (bi0 + bc) * 64);
+#pragma unroll
+        for (int k = 0; k < 4; k++) q[k] = ldg(src + k);
+        d = ldg((const uint16_t *)(s.C + (bi0 + bc) * 2));
+    };
+    fetch(qa, da, 0);
+    grid[tid] = k_iq2_grid[tid];
+    lds_barrier();
+    float acc = 0.0f;
+    for (int b = 0; b < nb; b++) {
+        fetch(qn, dn, b + 1);
+        const float dd = h2f(da);
+        const float4 *xb = (const float4 *)(v + b * 256);
+#pragma unroll
+        for (int g32 = 0; g32 < 8; g32++) {
+            const uint32_t w0 = wsel(qa[g32 >> 1], 2 * (g32 & 1)), w1 = wsel(qa[g32 >> 1], 2 * (g32 & 1) + 1);
+            const float db = dd * (0.5f + (float)(w1 >> 28)) * 0.25f;
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const uint64_t gv = grid[(w0 >> (8 * k)) & 0xffu];
+                const uint32_t s7 = (w1 >> (7 * k)) & 127u;
+                const uint32_t sg = s7 | ((__popc(s7) & 1u) << 7);
+                const float4 x0 = xb[g32 * 8 + 2 * k], x1 = xb[g32 * 8 + 2 * k + 1];
+                const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    const float t = db * (float)((uint32_t)(gv >> (8 * j)) & 0xffu) * xs[j];
+                    acc += (sg >> j) & 1u ? -t : t;
+                }
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < 4; k++) qa[k] = qn[k];
+        da = dn;
+    }
+    if (row < s.rows) emit(s.y + (size_t)slot * s.ystride, s.mode, row, acc);
+}
+
+OH_DEV float4 f4_silu_mul(const float4 g, const float4 u) {
+    return make_float4(ref_silu(g.x) * u.x, ref_silu(g.y) * u.y, ref_silu(g.z) * u.z, ref_silu(g.w) * u.w);
+}
+
+// Block prologue for inputs wider than the register prologue (and the
+// fallback rows): form the slot's activation in LDS. q8: Q8_K planes are
+// needed (integer path); otherwise only the f32 vector v. The inputs are read
+// in passes of up to 4 float4 per thread (4096 floats); every load of a pass
+// is issued before its first LDS store, so a pass costs one memory round trip.
+// Same values and summation orders as pro_compute.
 OH_DEV void mv_prologue(const oh_mvseg &s, int slot, int blk, uint8_t *smem, double *red, bool q8) {
     // activations come from earlier phases: device-scope loads
     const int in = s.in, nb = in / 256, tid = tid_x(), wave = tid >> 6;
@@ -422,30 +451,130 @@ OH_DEV void mv_prologue(const oh_mvseg &s, int slot, int blk, uint8_t *smem, dou
     int16_t *abs = (int16_t *)(smem + mv_lds_bs_off(nb));
     float *ad = (float *)(smem + mv_lds_d_off(nb));
     float *v = (float *)(smem + mv_lds_v_off(nb));
+    float4 *v4 = (float4 *)v;
     const size_t ao = (size_t)slot * s.astride;
+    constexpr int PW = 4;                              // float4 per thread per pass
     if (s.pro == OH_PRO_Q8K) {
         if (q8) {
             const int4 *gq = (const int4 *)(s.xqs + ao);
-            for (int i = tid; i < in / 16; i += 256) ((int4 *)aqs)[(i >> 4) * (kAS / 16) + (i & 15)] = ldc4(gq + i);
+            const int n16 = in / 16;
+            for (int i0 = 0; i0 < n16; i0 += 256 * PW) {
+                int4 r[PW];
+#pragma unroll
+                for (int u = 0; u < PW; u++) r[u] = ldc4(gq + (i0 + tid + 256 * u < n16 ? i0 + tid + 256 * u : n16 - 1));
+#pragma unroll
+                for (int u = 0; u < PW; u++) {
+                    const int i = i0 + tid + 256 * u;
+                    if (i < n16) ((int4 *)aqs)[(i >> 4) * (kAS / 16) + (i & 15)] = r[u];
+                }
+            }
             for (int i = tid; i < nb * 16; i += 256) abs[i] = ldc(s.xbs + ao / 16 + i);
             for (int i = tid; i < nb; i += 256) ad[i] = ldc(s.xd + ao / 256 + i);
         } else {
-            for (int i = tid; i < in; i += 256) v[i] = ldc(s.xf + ao + i);
+            // any width (fallback rows): scalar passes of 16 per thread
+            for (int i0 = 0; i0 < in; i0 += 256 * 16) {
+                float r[16];
+#pragma unroll
+                for (int u = 0; u < 16; u++) r[u] = ldc(s.xf + ao + (i0 + tid + 256 * u < in ? i0 + tid + 256 * u : in - 1));
+#pragma unroll
+                for (int u = 0; u < 16; u++)
+                    if (i0 + tid + 256 * u < in) v[i0 + tid + 256 * u] = r[u];
+            }
         }
         lds_barrier();
         return;
     }
-    if (s.pro == OH_PRO_SWIGLU) {
-        for (int i = tid; i < in; i += 256) v[i] = ref_silu(ldc(s.xf + ao + i)) * ldc(s.xf2 + ao + i);
+    // in % 256 == 0 here (mv_add)
+    const int n4 = in / 4;
+    const float4 *x4 = (const float4 *)(s.xf + ao);
+    if (s.pro == OH_PRO_GNORM) {
+        // per head of gdim elements: inv_h = 1/sqrt(sum of the head's run
+        // sums, in order / gdim + eps); v = x * inv_h * w * silu(z)
+        float *hinv = v + in;                          // [in / gdim]
+        const int gd = s.gdim, rpg = gd / 64, nhd = in / gd;
+        for (int h = tid; h < nhd; h += 256) {
+            double tot = ldc(s.xruns + h * rpg);
+            for (int k = 1; k < rpg; k++) tot += ldc(s.xruns + h * rpg + k);
+            hinv[h] = (float)(1.0 / sqrt(tot / (double)gd + (double)s.eps));
+        }
+        lds_barrier();
+        const float4 *z4 = (const float4 *)(s.xf2 + ao), *w4 = (const float4 *)s.nw;
+        for (int i0 = 0; i0 < n4; i0 += 256 * PW) {
+            float4 xr[PW], zr[PW], wr[PW];
+#pragma unroll
+            for (int u = 0; u < PW; u++) {
+                const int f = i0 + tid + 256 * u < n4 ? i0 + tid + 256 * u : n4 - 1;
+                xr[u] = ldc4(x4 + f);
+                zr[u] = ldc4(z4 + f);
+                wr[u] = ldg(w4 + f % (gd / 4));
+            }
+#pragma unroll
+            for (int u = 0; u < PW; u++) {
+                const int f = i0 + tid + 256 * u;
+                if (f < n4) {
+                    const float inv = hinv[4 * f / gd];
+                    const float4 x = xr[u], z = zr[u], w = wr[u];
+                    v4[f] = make_float4(x.x * inv * w.x * z.x, x.y * inv * w.y * z.y, x.z * inv * w.z * z.z,
+                                        x.w * inv * w.w * z.w);
+                }
+            }
+        }
+        lds_barrier();
+    } else if (s.pro == OH_PRO_SWIGLU) {
+        const float4 *u4 = (const float4 *)(s.xf2 + ao);
+        for (int i0 = 0; i0 < n4; i0 += 256 * PW) {
+            float4 gr[PW], ur[PW];
+#pragma unroll
+            for (int u = 0; u < PW; u++) {
+                const int f = i0 + tid + 256 * u < n4 ? i0 + tid + 256 * u : n4 - 1;
+                gr[u] = ldc4(x4 + f);
+                ur[u] = ldc4(u4 + f);
+            }
+#pragma unroll
+            for (int u = 0; u < PW; u++)
+                if (i0 + tid + 256 * u < n4) v4[i0 + tid + 256 * u] = f4_silu_mul(gr[u], ur[u]);
+        }
         lds_barrier();
     } else {
-        for (int i = tid; i < in; i += 256) v[i] = ldc(s.xf + ao + i);
+        for (int i0 = 0; i0 < n4; i0 += 256 * PW) {
+            float4 xr[PW];
+#pragma unroll
+            for (int u = 0; u < PW; u++) xr[u] = ldc4(x4 + (i0 + tid + 256 * u < n4 ? i0 + tid + 256 * u : n4 - 1));
+#pragma unroll
+            for (int u = 0; u < PW; u++)
+                if (i0 + tid + 256 * u < n4) v4[i0 + tid + 256 * u] = xr[u];
+        }
         lds_barrier();
-        if (s.pro == OH_PRO_NORM) rmsnorm_lds(v, s.nw, s.eps, in, red);
+        if (s.pro == OH_PRO_NORM) {
+            // the weights are requested before the reduction; the sum of
+            // squares in the order of the stand-alone RMSNorm kernel
+            const float4 *w4 = (const float4 *)s.nw;
+            double ss = 0.0;
+            for (int i = tid; i < in; i += 256) ss += (double)v[i] * v[i];
+            ss = wave_sum_d(ss);
+            if (lane_id() == 0) red[wave] = ss;
+            lds_barrier();
+            const double tot = (red[0] + red[1]) + (red[2] + red[3]);
+            const float inv = (float)(1.0 / sqrt(tot / (double)in + (double)s.eps));
+            for (int i0 = 0; i0 < n4; i0 += 256 * PW) {
+                float4 wr[PW];
+#pragma unroll
+                for (int u = 0; u < PW; u++) wr[u] = ldg(w4 + (i0 + tid + 256 * u < n4 ? i0 + tid + 256 * u : n4 - 1));
+#pragma unroll
+                for (int u = 0; u < PW; u++) {
+                    const int f = i0 + tid + 256 * u;
+                    if (f < n4) {
+                        const float4 x = v4[f], w = wr[u];
+                        v4[f] = make_float4(x.x * inv * w.x, x.y * inv * w.y, x.z * inv * w.z, x.w * inv * w.w);
+                    }
+                }
+            }
+            lds_barrier();
+        }
     }
     const bool store = blk == 0 && s.oqs != nullptr;
     if (blk == 0 && s.oxf)
-        for (int i = tid; i < in; i += 256) stc(s.oxf + ao + i, v[i]);
+        for (int f = tid; f < n4; f += 256) stc4((float4 *)(s.oxf + ao) + f, v4[f]);
     if (q8 || store) {
         for (int qb = wave; qb < nb; qb += 4) {
             q8k_block_from_lds(v, qb, aqs, ad, abs, kAS);
@@ -490,10 +619,6 @@ OH_DEV void pro_load(PIn &p, const oh_mvseg &s, int slot) {
             p.r1 = ldc(s.xruns + h * rpg + (rpg > 1 ? 1 : 0));
         }
     }
-}
-
-OH_DEV float4 f4_silu_mul(const float4 g, const float4 u) {
-    return make_float4(ref_silu(g.x) * u.x, ref_silu(g.y) * u.y, ref_silu(g.z) * u.z, ref_silu(g.w) * u.w);
 }
 
 // Q8_K of one 256-element block held in registers by a wave, four
@@ -781,13 +906,13 @@ OH_DEV void mv_body(const oh_mvlaunch &L, int vb, W &w) {
     const oh_mvseg &s = L.s[si];
     const int bseg = vb - s.block0;
     const int slot = bseg / s.bps, blk = bseg - slot * s.bps;
-    if (L.route) {
+    if (L.route == 1) {
         if (!w.wait()) return;
         route_block(L, vb, (float *)smem, rsel, rwt, &rshg, &rbad, rcnt);
     } else if (s.eidx) {
         if (!w.wait()) return;                    // the routing comes from an earlier phase
     }
-    const int expert = !s.eidx ? 0 : (L.route ? rsel[slot] : ldc(s.eidx + slot));
+    const int expert = !s.eidx ? 0 : (L.route == 1 ? rsel[slot] : ldc(s.eidx + slot));
     if (TK >= 0) {
         mv_seg<TK < 0 ? OH_Q4_K : TK>(s, slot, blk, expert, smem, red, w);
     } else if (oh_qdot_can((uint32_t)s.type, s.in) && (s.xqs || s.pro != OH_PRO_Q8K)) {
@@ -799,6 +924,10 @@ OH_DEV void mv_body(const oh_mvlaunch &L, int vb, W &w) {
     } else {
         if (!w.wait()) return;
         mv_prologue(s, slot, blk, smem, red, false);
+        if (s.type == OH_IQ2_XXS) {
+            iq2_rows(s, slot, blk, expert, smem);
+            return;
+        }
         const float *v = (const float *)(smem + mv_lds_v_off(s.in / 256));
         const int row = blk * 256 + tid_x();
         const int64_t row_base = (int64_t)expert * s.rows;
@@ -829,8 +958,14 @@ OH_DEV void down_body(const oh_mvdown &D, int vb, W &wt) {
     const int rowc = row < D.rows ? (rl < rps ? row : row0) : D.rows - 1;
     // the routing, h and x come from earlier phases
     if (!wt.wait()) return;
-    // activations first (at most HA float4 per thread), then the weights:
-    // vector loads complete in order
+    // the residual rows, routing weights and shared gate of the combine are
+    // requested first (they are consumed last), then the activations (at most
+    // HA float4 per thread), then the weights: vector loads complete in order
+    __shared__ float cw[17];
+    const bool comb = wave == 0 && lane < rps && row0 + lane < D.rows;
+    const float xrow = comb ? ldc(D.x + row0 + lane) : 0.0f;
+    if (tid < D.k) cw[tid] = ldc(D.w + tid);
+    if (tid == 16) cw[16] = D.shg ? ldc(D.shg) : 1.0f;
     const int nf = ns * in / 4, bd = (int)blockDim.x;
     const bool hreg = nf <= HA * bd;
     float4 ha[HA];
@@ -886,15 +1021,15 @@ OH_DEV void down_body(const oh_mvdown &D, int vb, W &wt) {
         }
     }
     lds_barrier();
-    if (wave == 0 && lane < rps && row0 + lane < D.rows) {
+    if (comb) {
         float acc = 0.0f;
-        for (int jj = 0; jj < D.k; jj++) acc += ldc(D.w + jj) * dots[jj * rps + lane];
+        for (int jj = 0; jj < D.k; jj++) acc += cw[jj] * dots[jj * rps + lane];
         if (D.sA) {
             const float so = dots[D.k * rps + lane];
-            const float vv = D.shg ? so * ldc(D.shg) : so;
+            const float vv = D.shg ? so * cw[16] : so;
             acc += vv;
         }
-        stc(D.x + row0 + lane, ldc(D.x + row0 + lane) + acc);
+        stc(D.x + row0 + lane, xrow + acc);
     }
 }
 

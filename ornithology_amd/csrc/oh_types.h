@@ -112,6 +112,8 @@ typedef struct {
 } oh_mvseg;
 
 #define OH_MAX_SEGS 8
+// IQ2_XXS rows of the f32 fallback per 256-thread block (one lane per row)
+#define OH_IQ2_ROWS 256
 #define OH_MV_WAVES 4              // waves per matvec block
 #define OH_MV_R 4                  // steps per prefetch batch of a wave
 // A launch with `route` set first routes the MoE in every block: top-k over

@@ -316,3 +316,63 @@ def gguf_tensors(path) -> dict:
         out[t.name.decode()] = (t.type, tuple(t.dims[:t.n_dims]), np.frombuffer(raw, np.uint8).copy())
     L.orc_gguf_free(g)
     return out
+
+
+def model_tensor_names(cfg: dict) -> list:
+    """The qwen35moe tensor names of a generator configuration (the ones a
+    model may hold; absent ones are skipped by the callers)."""
+    names = ["token_embd.weight", "output_norm.weight", "output.weight"]
+    fi = cfg.get("full_interval", 4)
+    for l in range(cfg["n_layers"]):
+        b = f"blk.{l}."
+        names += [b + "attn_norm.weight", b + "post_attention_norm.weight"]
+        if l % fi == fi - 1:
+            names += [b + s for s in ("attn_q.weight", "attn_k.weight", "attn_v.weight", "attn_q_norm.weight",
+                                      "attn_k_norm.weight", "attn_output.weight")]
+        else:
+            names += [b + s for s in ("attn_qkv.weight", "ssm_conv1d.weight", "ssm_a", "ssm_dt.bias",
+                                      "ssm_norm.weight", "ssm_alpha.weight", "ssm_beta.weight",
+                                      "attn_gate.weight", "ssm_out.weight")]
+        names += [b + s for s in ("ffn_gate_inp.weight", "ffn_gate_exps.weight", "ffn_up_exps.weight",
+                                  "ffn_down_exps.weight", "ffn_gate_shexp.weight", "ffn_up_shexp.weight",
+                                  "ffn_down_shexp.weight", "ffn_gate_inp_shexp.weight", "ffn_gate.weight",
+                                  "ffn_up.weight", "ffn_down.weight")]
+    return names
+
+
+def write_model_gguf(model, cfg: dict, path, n_layers: int | None = None) -> None:
+    """Write the tensors of a device model (the first n_layers layers) to a
+    GGUF with the oracle writer, with the metadata the reference loader reads
+    (architecture, expert count, RoPE, eps, vocabulary strings)."""
+    L = oracle()
+    c = dict(cfg, n_layers=n_layers or cfg["n_layers"])
+    ne = cfg["ne"]
+    w = L.orc_writer_new()
+    L.orc_w_string(w, b"general.architecture", b"qwen35moe")
+    L.orc_w_u32(w, b"qwen35moe.block_count", c["n_layers"])
+    L.orc_w_u32(w, b"qwen35moe.expert_used_count", cfg["top_k"])
+    L.orc_w_u32(w, b"qwen35moe.rope.dimension_count", 64)
+    L.orc_w_f32(w, b"qwen35moe.rope.freq_base", 1e7)
+    L.orc_w_f32(w, b"qwen35moe.attention.layer_norm_rms_epsilon", 1e-6)
+    toks = (C.c_char_p * cfg["vocab"])(*[f"t{i}".encode() for i in range(cfg["vocab"])])
+    L.orc_w_arr_str(w, b"tokenizer.ggml.tokens", toks, cfg["vocab"])
+    keep = []
+    for n in model_tensor_names(c):
+        info = model.tensor_info(n)
+        if info is None:
+            continue
+        data = model.tensor(n).download(info["nbytes"])
+        keep.append(data)
+        dims = [info["cols"], info["rows"]]
+        if "_exps." in n:
+            dims = [info["cols"], info["rows"] // ne, ne]
+        elif info["rows"] == 1 and n.endswith(("_norm.weight", "ssm_a", "ssm_dt.bias", "ffn_gate_inp_shexp.weight")):
+            dims = [info["cols"]]
+        d = (C.c_uint64 * len(dims))(*dims)
+        st = L.orc_w_tensor(w, n.encode(), len(dims), d, info["type"], C.c_void_p(data.ctypes.data), data.nbytes)
+        if st:
+            raise RuntimeError(L.orc_last_error().decode())
+    st = L.orc_writer_write(w, str(path).encode())
+    L.orc_writer_free(w)
+    if st:
+        raise RuntimeError(L.orc_last_error().decode())

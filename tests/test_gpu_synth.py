@@ -18,6 +18,14 @@ IQX = dict(clibs.C1, hidden=256, n_layers=2, full_interval=2, vocab=512, nh=2, n
            dhead=128, ne=2, top_k=1, moe_inter=256, shared_inter=256, t_default=clibs.Q4_K, t_attn_v=clibs.Q6_K,
            t_ffn_down=clibs.Q6_K, t_output=clibs.Q6_K, t_embd=clibs.Q4_K, t_exps=clibs.IQ2_XXS, seed=9)
 
+# C4's head geometry at a small hidden size: 64 value heads of 128 (the gated
+# norm prologue of ssm_out over 8192 inputs), 32 query heads of 256
+# (attn_output over 8192 inputs), 12288 conv channels, IQ2_XXS experts over
+# several super-blocks per row
+C4X = dict(clibs.C1, hidden=1024, n_layers=4, full_interval=4, vocab=512, nh=32, nkv=2, hd=256, nk=16, nv=64,
+           dhead=128, ne=4, top_k=2, moe_inter=512, shared_inter=512, t_default=clibs.Q4_K, t_attn_v=clibs.Q4_K,
+           t_ffn_down=clibs.Q4_K, t_output=clibs.Q4_K, t_embd=clibs.Q4_K, t_exps=clibs.IQ2_XXS, seed=11)
+
 
 @pytest.mark.parametrize("cfg", [clibs.C1, MIX, DENSE, IQX], ids=["C1-Q8_0", "Q4_K_M-mix", "dense", "IQ2_XXS-experts"])
 def test_synth_equals_generator_bytes(hip_ctx, tmp_path, cfg):
@@ -60,25 +68,28 @@ def test_profile_step_reports_every_launch(hip_ctx):
     m.free()
 
 
-def test_iq2xxs_experts_decode_matches_oracle(hip_ctx, orc, tmp_path):
+@pytest.mark.parametrize("cfg", [IQX, C4X], ids=["IQ2_XXS-experts", "C4-heads"])
+def test_iq2xxs_experts_decode_matches_oracle(hip_ctx, orc, tmp_path, cfg):
     """C4's path at a small shape: the IQ2_XXS routed experts through the
     reference's f32 fallback (dequantised row . f32 activation,
     src/ornith_rforward.c:119-133): prompt logits and 6 greedy steps
-    bit-identical to the oracle."""
+    bit-identical to the oracle. The device synthesis (byte-identical to the
+    generator, test_synth_equals_generator_bytes) is written out for the
+    oracle, which would take minutes to encode the IQ2_XXS experts itself."""
     import ctypes as C
     from clibs import i32p
     p = tmp_path / "iqx.gguf"
-    clibs.write_c1_gguf(p, IQX)
+    m = hip_ctx.synth(**cfg)
+    clibs.write_model_gguf(m, cfg, p)
     om = C.c_void_p()
     assert orc.orc_model_load(str(p).encode(), C.byref(om)) == 0
     orc.orc_model_set_threads(om, 8)
     os_ = orc.orc_session_new(om, 40, 1)
-    prompt = np.random.default_rng(2).integers(0, IQX["vocab"], 12).astype(np.int32)
+    prompt = np.random.default_rng(2).integers(0, cfg["vocab"], 12).astype(np.int32)
     assert orc.orc_session_eval(os_, i32p(prompt), 12, 1) == 0
-    m = hip_ctx.synth(**IQX)
     s = m.session(40)
     s.eval(prompt)
-    V = IQX["vocab"]
+    V = cfg["vocab"]
     for k in range(7):
         want = np.ctypeslib.as_array(orc.orc_session_logits(os_), (V,)).copy()
         assert np.array_equal(s.logits().view(np.uint32), want.view(np.uint32)), k
