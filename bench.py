@@ -214,7 +214,9 @@ def cpu_baseline(model: oa.Model, cfg: dict, seconds: float) -> dict:
     ncores = min(16, len(os.sched_getaffinity(0)))
     with tempfile.TemporaryDirectory() as td:
         path = str(Path(td) / "slice.gguf")
+        log("cpu baseline: writing the 4-layer slice GGUF")
         clibs.write_model_gguf(model, cfg, path, n_layers=4)
+        log("cpu baseline: slice written, timing the oracle port")
         m = C.c_void_p()
         assert L.orc_model_load(path.encode(), C.byref(m)) == 0, L.orc_last_error()
         L.orc_model_set_threads(m, ncores)
@@ -287,7 +289,8 @@ def c2_bench(args) -> int:
     """C2: the quantized matvec over N(0, 0.02) weights encoded on the device
     (seeded), per type and [in x out] shape. Cold: launches go round-robin over
     distinct copies of the weights totalling >= 1 GiB (more than L2 + MALL),
-    replayed as one HIP graph; hot: the same tensor every launch. CPU: the
+    replayed as one HIP graph; hot: the same tensor every launch (also one
+    graph). CPU: the
     oracle port's qdot / f32-fallback matvec on this host's cores."""
     sys.path.insert(0, str(ROOT / "tests"))
     import clibs
@@ -306,7 +309,7 @@ def c2_bench(args) -> int:
             ts = [ctx.upload(f"c2.{name}.{k}", t, enc, (n, out)) for k in range(ncopy)]
             iters = max(2 * ncopy, 64)
             cold = ctx.time_matvec_set(ts, iters)
-            hot = ts[0].time_matvec(64)
+            hot = ctx.time_matvec_set(ts[:1], 64)
             for tt in ts:
                 tt.free()
             # CPU: one matvec of the same weights and activation
@@ -410,7 +413,9 @@ def main() -> int:
     if args.config == "c5":
         return c5_bench(args)
     cfg = C3 if args.config == "c3" else C4
+    metric = METRIC
     if args.config == "c4":
+        metric = "decode tok/s @batch1 + achieved HBM GB/s (% of roofline), 397B-shaped, IQ2_XXS routed experts"
         args.batch = 0
         workload = ("397B-shaped qwen35moe decode sized to one GPU, batch 1, routed experts IQ2_XXS, the rest Q4_K, "
                     f"{args.ctx}-token Q8 KV context, greedy")
@@ -477,7 +482,7 @@ def main() -> int:
             log(f"cpu baseline failed: {e!r}")
 
     out = {
-        "metric": METRIC, "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1,
+        "metric": metric, "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms / args.steps, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": dtype, "data": "synthetic",

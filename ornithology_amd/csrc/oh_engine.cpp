@@ -2635,6 +2635,10 @@ extern "C" int ornith_hip_model_synth(ornith_hip_ctx *ctx, const ornith_hip_gen_
         hipError_t e = oh_launch_fill_uniform(stream_key(c->seed, name), lo, hi, (float *)t->A, t->rows * t->in, st);
         if (e != hipSuccess) { seterr("synth '%s': %s", name.c_str(), hipGetErrorString(e)); status = ORNITH_HIP_ERR_DEVICE; }
     };
+    // ORNITH_HIP_VERBOSE=1: one line per synthesised layer on stderr (a large
+    // model with IQ2_XXS experts takes minutes)
+    const char *vb = getenv("ORNITH_HIP_VERBOSE");
+    const bool verbose = vb && vb[0] == '1';
     // same tensor set and order as the GGUF generator
     add_q("token_embd.weight", c->t_embd, 2, H, V, 0);
     add_u("output_norm.weight", 1, H, 0, 0.9f, 1.1f);
@@ -2678,6 +2682,10 @@ extern "C" int ornith_hip_model_synth(ornith_hip_ctx *ctx, const ornith_hip_gen_
             add_q(b + "ffn_up_shexp.weight", c->t_default, 2, H, c->shared_inter, 0);
             add_q(b + "ffn_down_shexp.weight", c->t_ffn_down, 2, c->shared_inter, H, 0);
             add_q(b + "ffn_gate_inp_shexp.weight", c->t_default, 1, H, 1, 0);
+        }
+        if (verbose && !status) {
+            fprintf(stderr, "model_synth: layer %d/%d done, %.2f GB\n", l + 1, c->n_layers, (double)m->bytes / 1e9);
+            fflush(stderr);
         }
     }
     (void)hipStreamSynchronize(st);

@@ -698,9 +698,8 @@ OH_DEV void combine_body(const oh_op_attn &a, int vb, int pos, W &w) {
     const int i = (vb / nh) * 64 + lane;
     const int nch = (T + kFlashCh - 1) / kFlashCh, nchmax = (cap + kFlashCh - 1) / kFlashCh;
     float M = -INFINITY, L = 0.0f, O = 0.0f;
-    // chunks wave, wave+4, ... in order; their partials requested 32 at a
-    // time (one round trip up to 128 chunks = 8192 positions)
-    constexpr int CB = 32;
+    // chunks wave, wave+4, ... in order; their partials requested 8 at a time
+    constexpr int CB = 8;
     for (int c0 = wave; c0 < nch; c0 += 4 * CB) {
         float mb[CB], lb[CB], ob[CB];
 #pragma unroll
