@@ -1687,6 +1687,13 @@ static const int kPfChunk = 2048, kPfAttnSub = 32;
 // tokens per engine chunk (ORNITH_HIP_PREFILL_CHUNK, default 2048): a multiple
 // of 32, because the chunked delta scan counts its 32-token chunks from the
 // start of the evaluation and an engine chunk must not split one
+// prompt attention past the exact walk on the matrix cores; on unless
+// ORNITH_HIP_ATTN_MFMA=0
+static bool attn_mfma_enabled() {
+    const char *e = getenv("ORNITH_HIP_ATTN_MFMA");
+    return !(e && e[0] == '0');
+}
+
 static int pf_chunk_tokens() {
     const char *e = getenv("ORNITH_HIP_PREFILL_CHUNK");
     int c = e && *e ? atoi(e) : kPfChunk;
@@ -1857,8 +1864,16 @@ static int pf_chunk(ornith_hip_session *s, int base, int T, bool chunked, hipStr
             at.hb = oh_flash_hb(a.nh, a.nkv); at.scale = 1.0f / sqrtf((float)a.hd);
             const int nch = (s->kvcap + oh_flash_chunk() - 1) / oh_flash_chunk();
             const size_t po = (size_t)a.nh * nch * a.hd, pml = (size_t)a.nh * nch * 2;
-            for (int t0 = 0; t0 < T; t0 += kPfAttnSub)
-                HCHK(oh_launch_attn_rows(&at, base, t0, T - t0 < kPfAttnSub ? T - t0 : kPfAttnSub, po, pml, st));
+            // tokens whose context fits the exact walk take it (sub-batches of
+            // kPfAttnSub); the rest go to the matrix-core kernel in one launch
+            // (ORNITH_HIP_ATTN_MFMA=0: the flash chunks of the decode step)
+            const int lim = s->exact_max < 2048 ? s->exact_max : 2048;
+            const int tsplit = attn_mfma_enabled() && oh_attn_mfma_supported(a.hd, a.nh, a.nkv)
+                             ? (lim - base < 0 ? 0 : (lim - base > T ? T : lim - base)) : T;
+            for (int t0 = 0; t0 < tsplit; t0 += kPfAttnSub)
+                HCHK(oh_launch_attn_rows(&at, base, t0, tsplit - t0 < kPfAttnSub ? tsplit - t0 : kPfAttnSub, po, pml,
+                                         st));
+            if (tsplit < T) HCHK(oh_launch_attn_mfma_rows(&at, base, tsplit, T - tsplit, st));
             HCHK(oh_launch_norm_q8k_rows(p.OA, nullptr, 0.0f, aq, T, nullptr, p.OAQ.qs, p.OAQ.d, p.OAQ.bs, st,
                                          p.OAQ.bp));
             CHK(pf_mm(y.o, p.OAQ, p.X, H, T, 1, st));

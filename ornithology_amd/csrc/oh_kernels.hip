@@ -7,6 +7,7 @@
 #include "oh_prefill.hip"
 #include "oh_mmq.hip"
 #include "oh_batch.hip"
+#include "oh_attn_mfma.hip"
 #include "oh_launch.h"
 
 extern "C" {

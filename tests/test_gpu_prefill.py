@@ -69,6 +69,9 @@ def test_prefill_dense_matches_oracle(hip_ctx, orc, tmp_path, monkeypatch):
 def evals(m, chunks, cap, prefill, monkeypatch, exact_max):
     monkeypatch.setenv("ORNITH_HIP_PREFILL", "1" if prefill else "0")
     monkeypatch.setenv("ORNITH_HIP_PREFILL_CHUNK", "96")
+    # the prompt's flash chunks are the decode step's (bit-identical); the
+    # matrix-core prompt attention is checked to tolerance below
+    monkeypatch.setenv("ORNITH_HIP_ATTN_MFMA", "0")
     if exact_max is not None:
         monkeypatch.setenv("ORNITH_HIP_EXACT_ATTN_MAX", str(exact_max))
     s = m.session(cap)
@@ -159,4 +162,43 @@ def test_prefill_equals_token_path(hip_ctx, monkeypatch, cfg, exact_max):
     assert np.array_equal(u32(sp.logits()), u32(st.logits()))
     sp.free()
     st.free()
+    m.free()
+
+
+@pytest.mark.parametrize("cfg,n,exact_max,chunk", [("moe", 300, 64, 96), ("c1", 1200, None, 2048)],
+                         ids=["moe-hd128-chunks", "c1-hd64-past-1024"])
+def test_mfma_prompt_attention_within_tolerance(hip_ctx, orc, tmp_path, monkeypatch, cfg, n, exact_max, chunk):
+    """Prompt attention past the exact walk on the matrix cores (fp16 operands
+    with the Q8 scales folded in, fp32 accumulation and online softmax):
+    against the reference order (the oracle's chunked mode) the prompt logits
+    stay within 1e-2 relative L2 and pick the same next token, for prompts that
+    cross the exact-walk limit, inside one engine chunk and over several. The
+    flash chunks (ORNITH_HIP_ATTN_MFMA=0) on the same prompt meet the same bar."""
+    monkeypatch.setenv("ORNITH_PREFILL_SERIAL", "0")
+    monkeypatch.setenv("ORNITH_HIP_PREFILL_CHUNK", str(chunk))
+    if exact_max is not None:
+        monkeypatch.setenv("ORNITH_HIP_EXACT_ATTN_MAX", str(exact_max))
+    c = MIX if cfg == "moe" else clibs.C1
+    path = tmp_path / "m.gguf"
+    clibs.write_c1_gguf(path, c)
+    om = C.c_void_p()
+    assert orc.orc_model_load(str(path).encode(), C.byref(om)) == 0
+    orc.orc_model_set_threads(om, 8)
+    os_ = orc.orc_session_new(om, n + 8, 1)
+    p = np.random.default_rng(8).integers(0, c["vocab"], n).astype(np.int32)
+    assert orc.orc_session_eval(os_, i32p(p), n, 0) == 0
+    want = np.ctypeslib.as_array(orc.orc_session_logits(os_), (c["vocab"],)).copy()
+    orc.orc_session_free(os_)
+    orc.orc_model_free(om)
+    m = hip_ctx.synth(**c)
+    for mfma in ("1", "0"):
+        monkeypatch.setenv("ORNITH_HIP_ATTN_MFMA", mfma)
+        s = m.session(n + 8)
+        s.eval(p)
+        got = s.logits()
+        rel = float(np.linalg.norm(got - want) / np.linalg.norm(want))
+        print(f"{cfg} n={n} mfma={mfma}: rel L2 {rel:.3e}")
+        assert np.isfinite(got).all() and rel < 1e-2, (mfma, rel)
+        assert int(np.argmax(got)) == int(np.argmax(want)), mfma
+        s.free()
     m.free()
