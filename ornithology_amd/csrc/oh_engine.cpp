@@ -471,7 +471,7 @@ extern "C" int ornith_hip_matvec(ornith_hip_ctx *ctx, const ornith_hip_tensor *W
         if (mmq_enabled() && oh_mmq_can(W->type, (int)out, (int)in)) {
             oh_mmq M;
             memset(&M, 0, sizeof M);
-            M.A = W->A; M.B = W->B;
+            M.A = W->A; M.B = W->B; M.C = W->C; M.type = (int)W->type;
             M.xqs = qs; M.xd = dd; M.xbp = bp; M.y = dy;
             M.nb = (int)nb; M.in = (int)in; M.rows = (int)out; M.ncol = Tn; M.adiv = 1; M.ystride = (int)out;
             HCHK(oh_launch_mmq(&M, 0, 0, ctx->st));
@@ -1801,8 +1801,8 @@ static int pf_mmq(const ornith_hip_tensor *W, const ornith_hip_tensor *W2, const
                   int lstride = 0, int adiv = 1, const int32_t *items = nullptr, int max_items = 0) {
     oh_mmq M;
     memset(&M, 0, sizeof M);
-    M.A = W->A; M.B = W->B;
-    if (W2) { M.A2 = W2->A; M.B2 = W2->B; }
+    M.A = W->A; M.B = W->B; M.C = W->C; M.type = (int)W->type;
+    if (W2) { M.A2 = W2->A; M.B2 = W2->B; M.C2 = W2->C; }
     M.xqs = x.qs; M.xd = x.d; M.xbp = x.bp; M.y = y;
     M.cnt = cnt; M.list = list; M.items = items;
     M.nb = (int)(W->in / 256); M.in = (int)W->in; M.rows = list ? (int)W->dims[1] : (int)W->rows;

@@ -149,11 +149,24 @@ hipError_t oh_launch_argmax_rows(const float *v, int n, int rows, int32_t *out, 
     return hipGetLastError();
 }
 bool oh_mmq_can(uint32_t type, int rows, int in) {
-    return type == OH_Q4_K && rows > 0 && rows % kMqRows == 0 && in % 256 == 0 && in > 0;
+    return (type == OH_Q4_K || (type == OH_Q6_K && in <= 8192)) && rows > 0 && rows % kMqRows == 0 &&
+           in % 256 == 0 && in > 0;
 }
 hipError_t oh_launch_mmq(const oh_mmq *M, int max_items, int pair, hipStream_t st) {
     const int ty = M->list ? max_items : (M->ncol + kMqCols - 1) / kMqCols;
     if (ty <= 0) return hipSuccess;
+    const dim3 grid(M->rows / kMqRows, ty, pair ? 2 : 1);
+    if (M->type == OH_Q6_K) {
+        static bool lds6 = false;      // stages + the rows' d exceed the default dynamic LDS limit
+        if (!lds6) {
+            const hipError_t e = hipFuncSetAttribute((const void *)oh_k_mmq_q6k,
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize, m6_lds_bytes(32));
+            if (e != hipSuccess) return e;
+            lds6 = true;
+        }
+        hipLaunchKernelGGL(oh_k_mmq_q6k, grid, dim3(256), (size_t)m6_lds_bytes(M->nb), st, *M);
+        return hipGetLastError();
+    }
     static bool lds_set = false;   // two stages exceed the default dynamic LDS limit
     if (!lds_set) {
         const hipError_t e = hipFuncSetAttribute((const void *)oh_k_mmq_q4k,
@@ -161,7 +174,7 @@ hipError_t oh_launch_mmq(const oh_mmq *M, int max_items, int pair, hipStream_t s
         if (e != hipSuccess) return e;
         lds_set = true;
     }
-    hipLaunchKernelGGL(oh_k_mmq_q4k, dim3(M->rows / kMqRows, ty, pair ? 2 : 1), dim3(256), 2 * kMqStage, st, *M);
+    hipLaunchKernelGGL(oh_k_mmq_q4k, grid, dim3(256), 2 * kMqStage, st, *M);
     return hipGetLastError();
 }
 hipError_t oh_launch_mmq_items(const int32_t *cnt, int ne, int32_t *items, hipStream_t st) {

@@ -210,6 +210,197 @@ extern "C" __global__ void __launch_bounds__(256, 2) oh_k_mmq_q4k(oh_mmq M) {
     }
 }
 
+// ---- Q6_K x Q8_K (src/ornith_qdot.c:109-138) --------------------------------
+// Per super-block the reference's integer sum is isum = sum_g sc_g *
+// sum_{i in g} (q6_i - 32) * q8_i over the 16-element groups g, and the float
+// combine sumf += (yd * f16(d)) * isum in super-block order. The integer sum
+// is formed exactly on v_mfma_i32_32x32x32_i8: each weight becomes
+// p = sc_g * (q6 - 32) (|p| <= 4096), split as p = 64 * hi + lo with
+// lo in [0, 63] and hi in [-64, 64], both int8; then isum =
+// 64 * (hi . q8) + (lo . q8), exact in int32. A lane's 16 K-values of one
+// MFMA are exactly one group (one scale). The transform runs on packed int16
+// (two weights per instruction).
+//
+// Block and stage pipeline as oh_k_mmq_q4k; the stage holds the 12 code
+// pieces (ql 0-7, qh 8-11) of 128 rows, the rows' 16 group scales, the 64
+// columns' activation codes and d; the rows' f16 d of every super-block sit in
+// LDS for the whole launch.
+constexpr int kM6A = 0;                          // codes [12 pieces][128 rows][16 B]
+constexpr int kM6B = kM6A + 12 * 128 * 16;       // activation codes [16 pieces][64 cols][16 B]
+constexpr int kM6S = kM6B + 16 * 64 * 16;        // group scales [128 rows][16 B]
+constexpr int kM6X = kM6S + 128 * 16;            // activation d [64 cols]
+constexpr int kM6Stage = kM6X + 64 * 4;          // 43264 B
+constexpr int kM6Loads = 24 + 16 + 2 + 1;        // wave-loads per stage
+OH_HD inline int m6_lds_bytes(int nb) { return 2 * kM6Stage + 128 * nb * 2; }
+
+typedef short m6_s2 __attribute__((ext_vector_type(2)));
+
+namespace {
+
+OH_DEV void m6_stage_load(const oh_mmq &M, const uint8_t *A, const uint8_t *Bs, int64_t rbase, int R0, int i,
+                          uint8_t *S, int L, int lane, int acol) {
+    const int nb = M.nb;
+    if (L < 24) {                                   // codes: piece p, rows rh*64 + lane
+        const int p = L >> 1, rh = L & 1;
+        const int64_t bi = (rbase + R0 + rh * 64 + lane) * nb + i;
+        const uint4 *src = (const uint4 *)(A + (bi >> 6) * (int64_t)(64 * 192)) + (bi & 63) + p * 64;
+        mq_load16(src, S + kM6A + (p * 128 + rh * 64) * 16);
+    } else if (L < 40) {                            // activation codes: piece q, column lane
+        const int q = L - 24;
+        mq_load16(M.xqs + (size_t)acol * M.in + (size_t)i * 256 + q * 16, S + kM6B + q * 64 * 16);
+    } else if (L < 42) {                            // group scales of rows rh*64 + lane
+        const int rh = L - 40;
+        const int64_t bi = (rbase + R0 + rh * 64 + lane) * nb + i;
+        mq_load16(Bs + bi * 16, S + kM6S + rh * 64 * 16);
+    } else {                                        // activation d of column lane
+        mq_load4(M.xd + (size_t)acol * nb + i, S + kM6X);
+    }
+}
+
+// sixteen weights of one group (bytes of q6 in [0, 63], four per word) times
+// the group scale, split into the lo / hi int8 operands
+OH_DEV void m6_split(const uint32_t q6[4], int sc, mq_v4i &lo, mq_v4i &hi) {
+    const m6_s2 scv = {(short)sc, (short)sc}, off = {(short)(-32 * sc), (short)(-32 * sc)};
+    const m6_s2 m63 = {63, 63};
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        // bytes 0,1 and 2,3 of the word as int16 pairs
+        const uint32_t u01 = __builtin_amdgcn_perm(0u, q6[k], 0x0c010c00u);
+        const uint32_t u23 = __builtin_amdgcn_perm(0u, q6[k], 0x0c030c02u);
+        const m6_s2 p01 = __builtin_bit_cast(m6_s2, u01) * scv + off;
+        const m6_s2 p23 = __builtin_bit_cast(m6_s2, u23) * scv + off;
+        const uint32_t l01 = __builtin_bit_cast(uint32_t, p01 & m63), l23 = __builtin_bit_cast(uint32_t, p23 & m63);
+        const uint32_t h01 = __builtin_bit_cast(uint32_t, p01 >> (m6_s2){6, 6});
+        const uint32_t h23 = __builtin_bit_cast(uint32_t, p23 >> (m6_s2){6, 6});
+        // low bytes of the four int16 values, in order
+        lo[k] = (int)__builtin_amdgcn_perm(l23, l01, 0x06040200u);
+        hi[k] = (int)__builtin_amdgcn_perm(h23, h01, 0x06040200u);
+    }
+}
+
+} // namespace
+
+extern "C" __global__ void __launch_bounds__(256, 1) oh_k_mmq_q6k(oh_mmq M) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ int sact[kMqCols], sout[kMqCols];
+    const int tid = tid_x(), lane = lane_id();
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int zi = (int)blockIdx.z;
+    int g = 0, tile = (int)blockIdx.y, n;
+    if (M.list) {
+        if ((int)blockIdx.y >= ldg(M.items)) return;
+        const int it = ldg(M.items + 1 + blockIdx.y);
+        g = it >> 16;
+        tile = it & 0xffff;
+        n = ldg(M.cnt + g) - tile * kMqCols;
+    } else {
+        n = M.ncol - tile * kMqCols;
+    }
+    n = n < kMqCols ? n : kMqCols;
+    if (n <= 0) return;
+    const int R0 = (int)blockIdx.x * kMqRows;
+    const uint8_t *A = zi ? M.A2 : M.A, *Bs = zi ? M.B2 : M.B, *Cd = zi ? M.C2 : M.C;
+    const int64_t rbase = M.list ? (int64_t)g * M.rows : 0;
+    const int nb = M.nb;
+    uint16_t *Dr = (uint16_t *)(smem + 2 * kM6Stage);      // [128 rows][nb] f16 d
+    for (int k = tid; k < 128 * nb; k += 256) {
+        const int r = k / nb, i = k - r * nb;
+        Dr[k] = ldg((const uint16_t *)(Cd + ((rbase + R0 + r) * nb + i) * 2));
+    }
+    if (tid < kMqCols) {
+        const int c = tid < n ? tid : n - 1;
+        const int p = M.list ? ldg(M.list + (size_t)g * M.lstride + tile * kMqCols + c) : tile * kMqCols + c;
+        sact[tid] = p / M.adiv;
+        sout[tid] = p;
+    }
+    __syncthreads();
+    const int acol = sact[lane];
+    auto stage = [&](int i, int buf) {
+        uint8_t *S = smem + buf * kM6Stage;
+        for (int L = wave; L < kM6Loads; L += 4) m6_stage_load(M, A, Bs, rbase, R0, i, S, L, lane, acol);
+    };
+
+    const int h = lane >> 5, lr = lane & 31, arow = 32 * wave + lr;
+    const uint32_t NM = 0x0f0f0f0fu;
+    float acc[2][16];
+#pragma unroll
+    for (int t = 0; t < 2; t++)
+#pragma unroll
+        for (int v = 0; v < 16; v++) acc[t][v] = 0.0f;
+
+    stage(0, 0);
+    for (int i = 0; i < nb; i++) {
+        const int buf = i & 1;
+        if (i + 1 < nb) {
+            stage(i + 1, buf ^ 1);
+            // this wave's loads of stage i are the older ones; every wave
+            // issued at least 10 for stage i + 1
+            asm volatile("s_waitcnt vmcnt(10)" ::: "memory");
+        } else {
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        }
+        __syncthreads();
+        const uint8_t *S = smem + buf * kM6Stage;
+        const int8_t *sc8 = (const int8_t *)(S + kM6S + arow * 16);
+        mq_v16i ihi[2], ilo[2];
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) { ihi[t][v] = 0; ilo[t][v] = 0; }
+#pragma unroll
+        for (int ks = 0; ks < 8; ks++) {
+            // this lane's group gq = 2 ks + h: elements 16 gq .. + 15 of the
+            // super-block (half hh, quarter qt, 16-element part pr)
+            const int gq = 2 * ks + h, hh = gq >> 3, qt = (gq & 7) >> 1, pr = gq & 1;
+            const uint4 wl = *(const uint4 *)(S + kM6A + ((4 * hh + 2 * (qt & 1) + pr) * 128 + arow) * 16);
+            const uint4 wh = *(const uint4 *)(S + kM6A + ((8 + 2 * hh + pr) * 128 + arow) * 16);
+            const uint32_t l4[4] = {wl.x, wl.y, wl.z, wl.w}, h4[4] = {wh.x, wh.y, wh.z, wh.w};
+            uint32_t q6[4];
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const uint32_t nib = (qt >> 1) ? (l4[k] >> 4) & NM : l4[k] & NM;
+                q6[k] = nib | (((h4[k] >> (2 * qt)) & 0x03030303u) << 4);
+            }
+            mq_v4i alo, ahi;
+            m6_split(q6, (int)sc8[gq], alo, ahi);
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+                const mq_v4i xb = *(const mq_v4i *)(S + kM6B + ((2 * ks + h) * 64 + 32 * t + lr) * 16);
+                ihi[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ahi, xb, ihi[t], 0, 0, 0);
+                ilo[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(alo, xb, ilo[t], 0, 0, 0);
+            }
+        }
+        // float combine: output (row 8*(v/4) + 4h + v%4, column lr) of each
+        // 32x32 tile, per super-block in order
+        const float *XD = (const float *)(S + kM6X);
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            const float yd = XD[32 * t + lr];
+#pragma unroll
+            for (int v = 0; v < 16; v++) {
+                const int row = 32 * wave + 8 * (v / 4) + 4 * h + (v % 4);
+                const float d = yd * h2f(Dr[row * nb + i]);
+                const int isum = 64 * ihi[t][v] + ilo[t][v];
+                acc[t][v] += d * (float)isum;
+            }
+        }
+        __syncthreads();                            // stage buf is refilled next iteration
+    }
+    const size_t zoff = (size_t)zi * M.rows;
+#pragma unroll
+    for (int t = 0; t < 2; t++) {
+        const int col = 32 * t + lr;
+        if (col >= n) continue;
+        float *yc = M.y + (size_t)sout[col] * M.ystride + zoff + R0 + 32 * wave + 4 * h;
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+            float *yp = yc + 8 * (v / 4) + (v % 4);
+            if (M.mode == 1) stg(yp, ldg(yp) + acc[t][v]);
+            else stg(yp, acc[t][v]);
+        }
+    }
+}
+
 // Work items of a grouped product: (group, 64-column tile) pairs, packed as
 // g << 16 | tile after the count in items[0]. One block of 256 threads.
 extern "C" __global__ void __launch_bounds__(256) oh_k_mmq_items(const int32_t *cnt, int ne, int32_t *items) {

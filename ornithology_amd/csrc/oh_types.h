@@ -264,11 +264,13 @@ typedef struct {
     int cpb;                       // dense: columns per block along grid y (0: all)
 } oh_mvbatch;
 
-// Q4_K x Q8_K products of T columns on the matrix cores (prompt path): the
+// Q4_K / Q6_K x Q8_K products of T columns on the matrix cores (prompt path): the
 // same (dense | grouped) column addressing as oh_mvbatch; with A2/B2 the
 // second weight set writes rows [rows, 2 rows) of each output row.
 typedef struct {
-    const uint8_t *A, *B, *A2, *B2;   // Q4_K planes (expert 0 of a stack)
+    const uint8_t *A, *B, *A2, *B2;   // Q4_K / Q6_K planes (expert 0 of a stack)
+    const uint8_t *C, *C2;            // Q6_K: d (f16) per super-block
+    int type;                         // OH_Q4_K or OH_Q6_K
     const int8_t *xqs;                // Q8_K activation planes [a][in], [a][nb], [a][nb][16]
     const float *xd;
     const int8_t *xbp;                // per super-block: bytes bl_j, then bh_j, of the pair sums 64*bh + bl

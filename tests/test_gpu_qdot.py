@@ -83,21 +83,24 @@ def test_matvec_vs_oracle(hip_ctx, orc, t, shape):
     W.free()
 
 
+@pytest.mark.parametrize("t", [Q4_K, Q6_K], ids=["Q4_K", "Q6_K"])
 @pytest.mark.parametrize("shape,ncol", [((2048, 1024), 70), ((512, 384), 1), ((4096, 256), 130), ((1024, 200), 65)])
-def test_batched_q4k_distinct_columns(hip_ctx, orc, monkeypatch, shape, ncol):
-    """Batched Q4_K products (matmul_batch_q Tn semantics) on independent
-    columns: the matrix-core path (rows a multiple of 128) and the vector-ALU
-    path (ORNITH_HIP_MMQ=0, and 200 rows) both equal the oracle's per-column
-    qdot bit for bit; partial 64-column tiles included."""
+def test_batched_q4k_distinct_columns(hip_ctx, orc, monkeypatch, shape, ncol, t):
+    """Batched Q4_K / Q6_K products (matmul_batch_q Tn semantics) on
+    independent columns: the matrix-core path (rows a multiple of 128) and the
+    vector-ALU path (ORNITH_HIP_MMQ=0, and 200 rows) both equal the oracle's
+    per-column qdot bit for bit; partial 64-column tiles included."""
     n, out = shape
     w = clibs.gauss(11, f"bq.{n}.{out}", n * out, 0.02)
-    enc = clibs.quantize(orc, Q4_K, w)
-    W = hip_ctx.upload("w", Q4_K, enc, (n, out))
+    if t == Q6_K:
+        w = w * np.float32(40.0)          # wide code and scale ranges (large |sc * (q6 - 32)|)
+    enc = clibs.quantize(orc, t, w)
+    W = hip_ctx.upload("w", t, enc, (n, out))
     cols = [clibs.gauss(12 + c, f"bx.{n}.{c}", n, 1.0) for c in range(ncol)]
     ref = []
     for c in range(ncol):
         r = np.zeros(out, np.float32)
-        orc.orc_matvec(Q4_K, bp(enc), n, out, f32p(np.ascontiguousarray(cols[c])), f32p(r), 0, 8)
+        orc.orc_matvec(t, bp(enc), n, out, f32p(np.ascontiguousarray(cols[c])), f32p(r), 0, 8)
         ref.append(r)
     for mmq in ("1", "0"):
         monkeypatch.setenv("ORNITH_HIP_MMQ", mmq)
