@@ -55,6 +55,38 @@ extern "C" __global__ void __launch_bounds__(256) oh_k_argmax_rows(const float *
     }
 }
 
+// the same greedy token per row in two stages (the token step's head): stage
+// 1 takes the best of one slice of a row (grid: OH_ARGMAX_BLOCKS x rows, the
+// token step's argmax1), stage 2 one wave per row over the slices' bests
+extern "C" __global__ void __launch_bounds__(256)
+oh_k_argmax_rows1(const float *v, int n, float *bv, int *bi) {
+    NoWait w;
+    oh_op_argmax a;
+    a.v = v + (size_t)blockIdx.y * n;
+    a.bv = bv + (size_t)blockIdx.y * OH_ARGMAX_BLOCKS;
+    a.bi = bi + (size_t)blockIdx.y * OH_ARGMAX_BLOCKS;
+    a.n = n;
+    a.nblk = OH_ARGMAX_BLOCKS;
+    argmax1_body(a, (int)blockIdx.x, w);
+}
+extern "C" __global__ void __launch_bounds__(64)
+oh_k_argmax_rows2(const float *bv, const int *bi, int32_t *out) {
+    const float *rv = bv + (size_t)blockIdx.x * OH_ARGMAX_BLOCKS;
+    const int *ri = bi + (size_t)blockIdx.x * OH_ARGMAX_BLOCKS;
+    float b = -INFINITY;
+    int k = 0x7fffffff;
+    for (int i = tid_x(); i < OH_ARGMAX_BLOCKS; i += 64) {
+        const float x = ldg(rv + i);
+        const int xi = ldg(ri + i);
+        if (x > b || (x == b && xi < k)) { b = x; k = xi; }
+    }
+    for (int m = 32; m >= 1; m >>= 1) {
+        const float ov = shfl_xor(b, m); const int oi = shfl_xor(k, m);
+        if (ov > b || (ov == b && oi < k)) { b = ov; k = oi; }
+    }
+    if (tid_x() == 0) stg(out + blockIdx.x, k == 0x7fffffff ? 0 : k);
+}
+
 // each session's token history: this step's token at its position and the
 // greedy next one after it (toks: the sessions' history arrays)
 extern "C" __global__ void __launch_bounds__(256)

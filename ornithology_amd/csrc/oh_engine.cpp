@@ -1096,6 +1096,8 @@ struct ornith_hip_session {
         float *RL = nullptr, *SHL = nullptr, *SHG = nullptr, *RW = nullptr, *LOGITS = nullptr;
         int32_t *RIDX = nullptr, *CNT = nullptr, *LIST = nullptr, *ITEMS = nullptr, *IDX = nullptr;
         float *Hh = nullptr, *HSH = nullptr, *OD = nullptr, *ODSH = nullptr, *GU = nullptr, *GSH = nullptr;
+        float *AMV = nullptr;          // argmax stage-1 bests [n][OH_ARGMAX_BLOCKS]
+        int32_t *AMI = nullptr;
         uint8_t *OPS = nullptr;
         size_t ops_bytes = 0;
         int gen = 0;                   // bumped when the buffers are reallocated
@@ -1694,6 +1696,13 @@ static bool attn_mfma_enabled() {
     return !(e && e[0] == '0');
 }
 
+// batch decode below the matrix-core column count through the fused slotted
+// launches; on unless ORNITH_HIP_BATCH_FUSED=0
+static bool batch_fused() {
+    const char *e = getenv("ORNITH_HIP_BATCH_FUSED");
+    return !(e && e[0] == '0');
+}
+
 static int pf_chunk_tokens() {
     const char *e = getenv("ORNITH_HIP_PREFILL_CHUNK");
     int c = e && *e ? atoi(e) : kPfChunk;
@@ -2008,6 +2017,7 @@ static int bw_alloc(ornith_hip_session *s, int n, size_t ops_bytes) {
     CHK(salloc(s, &p.GU, N * K * 2 * I)); CHK(salloc(s, &p.GSH, N * 2 * sI));
     CHK(salloc(s, &p.OD, N * K * H)); CHK(salloc(s, &p.ODSH, N * H));
     CHK(salloc(s, &p.LOGITS, N * (size_t)a.vocab)); CHK(salloc(s, &p.IDX, 3 * N + 1));
+    CHK(salloc(s, &p.AMV, N * OH_ARGMAX_BLOCKS)); CHK(salloc(s, &p.AMI, N * OH_ARGMAX_BLOCKS));
     const size_t ob = ops_bytes > p.ops_bytes ? ops_bytes : p.ops_bytes;
     CHK(salloc(s, &p.OPS, ob));
     p.ops_bytes = ob;
@@ -2040,38 +2050,92 @@ static int batch_enqueue(const BatchPlan &B, hipStream_t st) {
     int32_t *const *dtoks = (int32_t *const *)(p.OPS + B.tok_ofs + (((size_t)n * 8 + 15) & ~(size_t)15));
     oh_op_embed emb = {m->embd->A, m->embd->B, m->embd->C, dtok, p.X, (int)m->embd->type, H};
     HCHK(oh_launch_embed_rows(&emb, 0, n, st));
+    // below the matrix-core column count the dense projections run as the
+    // token step's fused multi-segment launches with one slot per session
+    // (the normalisation / gated norm / f32 activation formed in the launch's
+    // prologue, weights re-read per slot from the caches); the expert and
+    // head products keep the column-streaming batched kernels
+    const bool fused = n < kMmqMinTokens && batch_fused();
     for (int l = 0; l < a.n_layers; l++) {
         const OhLayer &y = m->L[l];
         const uint8_t *dops = p.OPS + B.lofs[l];
-        HCHK(oh_launch_norm_q8k_rows(p.X, (const float *)y.attn_norm->A, a.eps, H, n, nullptr, p.XQ.qs, p.XQ.d,
-                                     p.XQ.bs, st, p.XQ.bp));
+        const Act an = act_norm(p.X, (const float *)y.attn_norm->A, a.eps);
+        if (!fused)
+            HCHK(oh_launch_norm_q8k_rows(p.X, (const float *)y.attn_norm->A, a.eps, H, n, nullptr, p.XQ.qs, p.XQ.d,
+                                         p.XQ.bs, st, p.XQ.bp));
         if (y.full) {
-            CHK(pf_mm(y.q, p.XQ, p.QP, 2 * aq, n, 0, st));
-            CHK(pf_mm(y.k, p.XQ, p.KB, kvd, n, 0, st));
-            CHK(pf_mm(y.v, p.XQ, p.VB, kvd, n, 0, st));
+            if (fused) {
+                MvBuild b;
+                CHK(mv_add(b, y.q, an, p.QP, 0, nullptr, n, 2 * aq, H));
+                CHK(mv_add(b, y.k, an, p.KB, 0, nullptr, n, kvd, H));
+                CHK(mv_add(b, y.v, an, p.VB, 0, nullptr, n, kvd, H));
+                CHK(mv_go(b, st));
+            } else {
+                CHK(pf_mm(y.q, p.XQ, p.QP, 2 * aq, n, 0, st));
+                CHK(pf_mm(y.k, p.XQ, p.KB, kvd, n, 0, st));
+                CHK(pf_mm(y.v, p.XQ, p.VB, kvd, n, 0, st));
+            }
             const oh_op_prep *pops = (const oh_op_prep *)dops;
             const oh_op_attn *aops = (const oh_op_attn *)(dops + (size_t)n * sizeof(oh_op_prep));
             HCHK(oh_launch_prep_batch(pops, dpos, n, a.nh, a.nkv, st));
             HCHK(oh_launch_attn_batch(aops, dpos, n, B.nvb_main, B.lds_main, a.nh, a.hd, st));
-            HCHK(oh_launch_norm_q8k_rows(p.OA, nullptr, 0.0f, aq, n, nullptr, p.OAQ.qs, p.OAQ.d, p.OAQ.bs, st,
-                                         p.OAQ.bp));
-            CHK(pf_mm(y.o, p.OAQ, p.X, H, n, 1, st));
+            if (fused) {
+                MvBuild b;
+                Act af;
+                af.pro = OH_PRO_F32;
+                af.xf = p.OA;
+                CHK(mv_add(b, y.o, af, p.X, 1, nullptr, n, H, aq));
+                CHK(mv_go(b, st));
+            } else {
+                HCHK(oh_launch_norm_q8k_rows(p.OA, nullptr, 0.0f, aq, n, nullptr, p.OAQ.qs, p.OAQ.d, p.OAQ.bs, st,
+                                             p.OAQ.bp));
+                CHK(pf_mm(y.o, p.OAQ, p.X, H, n, 1, st));
+            }
         } else {
-            CHK(pf_mm(y.qkv, p.XQ, p.CAT, cc, n, 0, st));
-            CHK(pf_mm(y.gate, p.XQ, p.Z, vd, n, 0, st));
-            CHK(pf_mm(y.alpha, p.XQ, p.AB, 2 * a.nv, n, 0, st));
-            CHK(pf_mm(y.beta, p.XQ, p.AB + a.nv, 2 * a.nv, n, 0, st));
+            if (fused) {
+                MvBuild b;
+                CHK(mv_add(b, y.qkv, an, p.CAT, 0, nullptr, n, cc, H));
+                CHK(mv_add(b, y.gate, an, p.Z, 0, nullptr, n, vd, H));
+                CHK(mv_add(b, y.alpha, an, p.AB, 0, nullptr, n, 2 * a.nv, H));
+                CHK(mv_add(b, y.beta, an, p.AB + a.nv, 0, nullptr, n, 2 * a.nv, H));
+                CHK(mv_go(b, st));
+            } else {
+                CHK(pf_mm(y.qkv, p.XQ, p.CAT, cc, n, 0, st));
+                CHK(pf_mm(y.gate, p.XQ, p.Z, vd, n, 0, st));
+                CHK(pf_mm(y.alpha, p.XQ, p.AB, 2 * a.nv, n, 0, st));
+                CHK(pf_mm(y.beta, p.XQ, p.AB + a.nv, 2 * a.nv, n, 0, st));
+            }
             HCHK(oh_launch_delta_batch((const oh_op_delta *)dops, dpos, n, a.dk, a.conv_k, a.nv, st));
-            HCHK(oh_launch_gnorm_q8k_rows(p.O, p.Z, (const float *)y.ssm_norm->A, a.eps, vd, a.dv, n, p.OQ.qs,
-                                          p.OQ.d, p.OQ.bs, st, p.OQ.bp));
-            CHK(pf_mm(y.ssm_out, p.OQ, p.X, H, n, 1, st));
+            if (fused) {
+                MvBuild b;
+                CHK(mv_add(b, y.ssm_out, act_gnorm(p.O, p.OG, p.RUNS, (const float *)y.ssm_norm->A, a.eps, a.dv),
+                           p.X, 1, nullptr, n, H, vd));
+                CHK(mv_go(b, st));
+            } else {
+                HCHK(oh_launch_gnorm_q8k_rows(p.O, p.Z, (const float *)y.ssm_norm->A, a.eps, vd, a.dv, n, p.OQ.qs,
+                                              p.OQ.d, p.OQ.bs, st, p.OQ.bp));
+                CHK(pf_mm(y.ssm_out, p.OQ, p.X, H, n, 1, st));
+            }
         }
-        HCHK(oh_launch_norm_q8k_rows(p.X, (const float *)y.post_norm->A, a.eps, H, n, nullptr, p.XQ.qs, p.XQ.d,
-                                     p.XQ.bs, st, p.XQ.bp));
+        const Act pn = act_norm(p.X, (const float *)y.post_norm->A, a.eps);
+        if (!fused || a.ne <= 0)
+            HCHK(oh_launch_norm_q8k_rows(p.X, (const float *)y.post_norm->A, a.eps, H, n, nullptr, p.XQ.qs, p.XQ.d,
+                                         p.XQ.bs, st, p.XQ.bp));
         if (a.ne > 0) {
             const int K = a.top_k, I = a.moe_inter, sI = a.shared_inter;
-            CHK(pf_mm(y.router, p.XQ, p.RL, a.ne, n, 0, st));
-            if (y.gate_inp_sh) CHK(pf_mm(y.gate_inp_sh, p.XQ, p.SHL, 1, n, 0, st));
+            if (fused) {
+                // router + shared gate; each slot's first block stores its
+                // Q8_K activation (p.XQ) for the expert products
+                Act pst = pn;
+                pst.oqs = p.XQ.qs; pst.oqd = p.XQ.d; pst.oqb = p.XQ.bs;
+                MvBuild b;
+                CHK(mv_add(b, y.router, pst, p.RL, 0, nullptr, n, a.ne, H));
+                if (y.gate_inp_sh) CHK(mv_add(b, y.gate_inp_sh, pn, p.SHL, 0, nullptr, n, 1, H));
+                CHK(mv_go(b, st));
+            } else {
+                CHK(pf_mm(y.router, p.XQ, p.RL, a.ne, n, 0, st));
+                if (y.gate_inp_sh) CHK(pf_mm(y.gate_inp_sh, p.XQ, p.SHL, 1, n, 0, st));
+            }
             HCHK(oh_launch_route_rows(p.RL, a.ne, K, y.gate_inp_sh ? p.SHL : nullptr, p.RIDX, p.RW,
                                       y.gate_inp_sh ? p.SHG : nullptr, n, st));
             HCHK(oh_launch_group_pairs(p.RIDX, n * K, p.CNT, a.ne, p.LIST, n, st));
@@ -2101,7 +2165,7 @@ static int batch_enqueue(const BatchPlan &B, hipStream_t st) {
     HCHK(oh_launch_norm_q8k_rows(p.X, (const float *)m->out_norm->A, a.eps, H, n, nullptr, p.XQ.qs, p.XQ.d,
                                  p.XQ.bs, st, p.XQ.bp));
     CHK(pf_mm(m->lm_head, p.XQ, p.LOGITS, a.vocab, n, 0, st));
-    HCHK(oh_launch_argmax_rows(p.LOGITS, a.vocab, n, p.IDX, st));
+    HCHK(oh_launch_argmax_rows(p.LOGITS, a.vocab, n, p.IDX, st, p.AMV, p.AMI));
     for (int b = 0; b < n; b++)
         HCHK(hipMemcpyAsync(ss[b]->logits, p.LOGITS + (size_t)b * a.vocab, (size_t)a.vocab * 4,
                             hipMemcpyDeviceToDevice, st));

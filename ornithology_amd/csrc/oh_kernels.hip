@@ -144,8 +144,13 @@ hipError_t oh_launch_batch_tokens(int32_t *const *toks, const int32_t *pos, cons
     hipLaunchKernelGGL(oh_k_batch_tokens, dim3((n + 255) / 256), dim3(256), 0, st, toks, pos, tok, next, n);
     return hipGetLastError();
 }
-hipError_t oh_launch_argmax_rows(const float *v, int n, int rows, int32_t *out, hipStream_t st) {
-    hipLaunchKernelGGL(oh_k_argmax_rows, dim3(rows), dim3(256), 0, st, v, n, out);
+hipError_t oh_launch_argmax_rows(const float *v, int n, int rows, int32_t *out, hipStream_t st, float *bv, int *bi) {
+    if (!bv || !bi) {
+        hipLaunchKernelGGL(oh_k_argmax_rows, dim3(rows), dim3(256), 0, st, v, n, out);
+        return hipGetLastError();
+    }
+    hipLaunchKernelGGL(oh_k_argmax_rows1, dim3(OH_ARGMAX_BLOCKS, rows), dim3(256), 0, st, v, n, bv, bi);
+    hipLaunchKernelGGL(oh_k_argmax_rows2, dim3(rows), dim3(64), 0, st, bv, bi, out);
     return hipGetLastError();
 }
 bool oh_mmq_can(uint32_t type, int rows, int in) {

@@ -51,7 +51,9 @@ hipError_t oh_launch_delta_batch(const oh_op_delta *ops, const int32_t *pos, int
 hipError_t oh_launch_prep_batch(const oh_op_prep *ops, const int32_t *pos, int n, int nh, int nkv, hipStream_t st);
 hipError_t oh_launch_attn_batch(const oh_op_attn *ops, const int32_t *pos, int n, int nvb_main, int lds, int nh,
                                 int hd, hipStream_t st);
-hipError_t oh_launch_argmax_rows(const float *v, int n, int rows, int32_t *out, hipStream_t st);
+// greedy token per row; with scratch bv/bi (rows x OH_ARGMAX_BLOCKS) in two stages
+hipError_t oh_launch_argmax_rows(const float *v, int n, int rows, int32_t *out, hipStream_t st,
+                                 float *bv = nullptr, int *bi = nullptr);
 hipError_t oh_launch_batch_tokens(int32_t *const *toks, const int32_t *pos, const int32_t *tok, const int32_t *next,
                                   int n, hipStream_t st);
 hipError_t oh_launch_prep_rows(const oh_op_prep *a, int base, int T, hipStream_t st);
@@ -96,5 +98,4 @@ hipError_t oh_launch_encode(const float *x, int type, int64_t nblk, uint8_t *A, 
                             hipStream_t st);
 }
 
-// blocks used by the argmax's first stage (the caller sizes tmp_v/tmp_i)
-#define OH_ARGMAX_BLOCKS 256
+

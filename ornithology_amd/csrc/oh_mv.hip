@@ -493,8 +493,9 @@ OH_DEV void mv_prologue(const oh_mvseg &s, int slot, int blk, uint8_t *smem, dou
         float *hinv = v + in;                          // [in / gdim]
         const int gd = s.gdim, rpg = gd / 64, nhd = in / gd;
         for (int h = tid; h < nhd; h += 256) {
-            double tot = ldc(s.xruns + h * rpg);
-            for (int k = 1; k < rpg; k++) tot += ldc(s.xruns + h * rpg + k);
+            const double *xr = s.xruns + ao / 64;      // the slot's run sums
+            double tot = ldc(xr + h * rpg);
+            for (int k = 1; k < rpg; k++) tot += ldc(xr + h * rpg + k);
             hinv[h] = (float)(1.0 / sqrt(tot / (double)gd + (double)s.eps));
         }
         lds_barrier();
@@ -615,8 +616,9 @@ OH_DEV void pro_load(PIn &p, const oh_mvseg &s, int slot) {
         if (s.pro == OH_PRO_GNORM) {
             // this thread's head (tid < in/gdim): its first two run sums
             const int rpg = s.gdim / 64, nh = in / s.gdim, h = tid < nh ? tid : nh - 1;
-            p.r0 = ldc(s.xruns + h * rpg);
-            p.r1 = ldc(s.xruns + h * rpg + (rpg > 1 ? 1 : 0));
+            const double *xr = s.xruns + ao / 64;      // the slot's run sums
+            p.r0 = ldc(xr + h * rpg);
+            p.r1 = ldc(xr + h * rpg + (rpg > 1 ? 1 : 0));
         }
     }
 }
@@ -695,7 +697,7 @@ OH_DEV void pro_compute(const PIn &p, const oh_mvseg &s, int slot, int blk, uint
         if (tid < in / gd) {
             double tot = p.r0;
             if (rpg > 1) tot += p.r1;
-            for (int k = 2; k < rpg; k++) tot += ldc(s.xruns + tid * rpg + k);
+            for (int k = 2; k < rpg; k++) tot += ldc(s.xruns + ao / 64 + tid * rpg + k);
             hinv[tid] = (float)(1.0 / sqrt(tot / (double)gd + (double)s.eps));
         }
         lds_barrier();

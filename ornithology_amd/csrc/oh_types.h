@@ -86,7 +86,8 @@ typedef struct {
     // OH_PRO_NORM RMS-normalises xf with nw/eps; OH_PRO_SWIGLU forms
     // silu(xf)*xf2; OH_PRO_GNORM RMS-normalises each gdim-element head of xf
     // (sum of squares from xruns: one double per 64-element run) with nw/eps
-    // and multiplies by xf2 (= silu(gate)); OH_PRO_F32 takes xf as is; all
+    // and multiplies by xf2 (= silu(gate)); slot k's run sums start at
+    // xruns + k*astride/64; OH_PRO_F32 takes xf as is; all
     // four then quantise to Q8_K inside the block.
     const int8_t *xqs;
     const float *xd;
@@ -112,6 +113,8 @@ typedef struct {
 } oh_mvseg;
 
 #define OH_MAX_SEGS 8
+// blocks used by the argmax's first stage (the caller sizes its scratch)
+#define OH_ARGMAX_BLOCKS 256
 // IQ2_XXS rows of the f32 fallback per 256-thread block (one lane per row)
 #define OH_IQ2_ROWS 256
 #define OH_MV_WAVES 4              // waves per matvec block

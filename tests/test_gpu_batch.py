@@ -31,7 +31,11 @@ def prompts(vocab, n, seed):
 @pytest.mark.parametrize("cfg", ["c1", "moe", "dense"])
 @pytest.mark.parametrize("n", [1, 3, 8])
 @pytest.mark.parametrize("exact_max", [None, 0], ids=["exact", "flash"])
-def test_batch_step_equals_single_steps(hip_ctx, monkeypatch, cfg, n, exact_max):
+@pytest.mark.parametrize("fused", ["1", "0"], ids=["slotted-launches", "batched-kernels"])
+def test_batch_step_equals_single_steps(hip_ctx, monkeypatch, cfg, n, exact_max, fused):
+    """Both batch plans: the token step's fused launches with one slot per
+    session, and the column-streaming batched kernels."""
+    monkeypatch.setenv("ORNITH_HIP_BATCH_FUSED", fused)
     if exact_max is not None:
         monkeypatch.setenv("ORNITH_HIP_EXACT_ATTN_MAX", str(exact_max))
     m = hip_ctx.synth(**CFGS[cfg])
