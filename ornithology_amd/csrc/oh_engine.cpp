@@ -1457,7 +1457,7 @@ static int build_body(ornith_hip_session *s, Prog &P) {
                 D.A = y.down_exps->A; D.B = y.down_exps->B; D.C = y.down_exps->C;
                 if (y.gate_sh) { D.sA = y.down_sh->A; D.sB = y.down_sh->B; D.sC = y.down_sh->C; }
                 D.eidx = s->eidx; D.w = s->ew; D.shg = y.gate_inp_sh ? s->shg : nullptr;
-                D.h = s->h; D.x = s->x;
+                D.h = s->h; D.hsh = s->h + (size_t)K * IW; D.x = s->x;
                 D.type = (int)dt; D.nb = nbd; D.in = I; D.rows = H; D.k = K; D.stride = IW;
                 const double db = (double)ns * ((double)H * gguf_nbytes(dt, (uint64_t)I) + 4.0 * I) + 8.0 * H + 4.0 * K;
                 oh_op o = op_new(OH_OP_MV_DOWN, (H + rps - 1) / rps, dlds);
@@ -2135,6 +2135,47 @@ static int batch_enqueue(const BatchPlan &B, hipStream_t st) {
             } else {
                 CHK(pf_mm(y.router, p.XQ, p.RL, a.ne, n, 0, st));
                 if (y.gate_inp_sh) CHK(pf_mm(y.gate_inp_sh, p.XQ, p.SHL, 1, n, 0, st));
+            }
+            // the token step's two MoE launches for all n tokens: the experts
+            // gate/up with each (token, expert) slot routing its own token,
+            // then the fused down projection + combine with a grid row per
+            // token (same conditions as the token step's fused down)
+            const bool paired = pairable(y.gate_exps, y.up_exps) && (!y.gate_sh || pairable(y.gate_sh, y.up_sh));
+            const uint32_t dt = y.down_exps->type;
+            const int nbd = I / 256, ns = K + (y.gate_sh ? 1 : 0);
+            const int rps = nbd >= 1 ? 64 / nbd : 1;
+            const int dlds = ns * ((nbd * 272 + nbd * 36 + 15) & ~15) + ns * I * 4 + ns * rps * 4;
+            if (fused && paired && oh_qdot_can(dt, I) && nbd >= 1 && nbd <= 64 && ns <= 10 && dlds <= 65536 &&
+                y.gate_exps->type == y.router->type && (!y.gate_sh || (y.down_sh->type == dt && sI == I))) {
+                MvBuild b2;
+                const Act ax = act_of(p.XQ, nullptr);
+                CHK(mv_add_pair(b2, y.gate_exps, y.up_exps, ax, p.Hh, p.RIDX, n * K, I));
+                b2.L.s[b2.L.n - 1].astride = H;
+                b2.L.s[b2.L.n - 1].adiv = K;
+                if (y.gate_sh) {
+                    CHK(mv_add_pair(b2, y.gate_sh, y.up_sh, ax, p.HSH, nullptr, n, sI));
+                    b2.L.s[b2.L.n - 1].astride = H;
+                }
+                b2.L.route = 1;
+                b2.L.tslots = K;
+                b2.L.rlog = p.RL;
+                b2.L.shl = y.gate_inp_sh ? p.SHL : nullptr;
+                b2.L.ne = a.ne;
+                b2.L.topk = K;
+                b2.L.ridx = p.RIDX;
+                b2.L.rw = p.RW;
+                b2.L.shg = p.SHG;
+                CHK(mv_go(b2, st));
+                oh_mvdown D;
+                memset(&D, 0, sizeof D);
+                D.A = y.down_exps->A; D.B = y.down_exps->B; D.C = y.down_exps->C;
+                if (y.gate_sh) { D.sA = y.down_sh->A; D.sB = y.down_sh->B; D.sC = y.down_sh->C; }
+                D.eidx = p.RIDX; D.w = p.RW; D.shg = y.gate_inp_sh ? p.SHG : nullptr;
+                D.h = p.Hh; D.hsh = p.HSH; D.x = p.X;
+                D.hts = (size_t)K * I; D.hsts = (size_t)sI; D.xts = (size_t)H;
+                D.type = (int)dt; D.nb = nbd; D.in = I; D.rows = H; D.k = K; D.stride = I;
+                HCHK(oh_launch_mv_down_rows(&D, (H + rps - 1) / rps, n, dlds, st));
+                continue;
             }
             HCHK(oh_launch_route_rows(p.RL, a.ne, K, y.gate_inp_sh ? p.SHL : nullptr, p.RIDX, p.RW,
                                       y.gate_inp_sh ? p.SHG : nullptr, n, st));

@@ -256,6 +256,13 @@ hipError_t oh_launch_dequant(const uint8_t *A, const uint8_t *B, const uint8_t *
 }
 
 
+hipError_t oh_launch_mv_down_rows(const oh_mvdown *D, int nvb, int ntok, int lds, hipStream_t st) {
+    if (nvb <= 0 || ntok <= 0) return hipSuccess;
+    const int ns = D->k + (D->sA ? 1 : 0);
+    hipLaunchKernelGGL(oh_k_mv_down, dim3(nvb, ntok), dim3(64 * ns), (size_t)lds, st, *D);
+    return hipGetLastError();
+}
+
 hipError_t oh_launch_op(const oh_op *op, const int32_t *io, hipStream_t st) {
     if (op->nvb <= 0) return hipSuccess;
     const dim3 g(op->nvb), b256(256);

@@ -71,6 +71,8 @@ hipError_t oh_launch_swiglu_q8k(const float *g, const float *u, int n, int count
                                 int8_t *qs, float *d, int16_t *bs, hipStream_t st);
 hipError_t oh_launch_dequant(const uint8_t *A, const uint8_t *B, const uint8_t *C, int type, int in,
                              int64_t row0, int64_t nrows, float *out, hipStream_t st);
+// the fused MoE down + combine for ntok tokens (grid y = token)
+hipError_t oh_launch_mv_down_rows(const oh_mvdown *D, int nvb, int ntok, int lds, hipStream_t st);
 // one operation of the token step as its own launch (io: position word)
 hipError_t oh_launch_op(const oh_op *op, const int32_t *io, hipStream_t st);
 // flash decoding past exact_max positions: query heads per block, LDS bytes,

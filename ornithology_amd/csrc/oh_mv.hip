@@ -452,7 +452,7 @@ OH_DEV void mv_prologue(const oh_mvseg &s, int slot, int blk, uint8_t *smem, dou
     float *ad = (float *)(smem + mv_lds_d_off(nb));
     float *v = (float *)(smem + mv_lds_v_off(nb));
     float4 *v4 = (float4 *)v;
-    const size_t ao = (size_t)slot * s.astride;
+    const size_t ao = (size_t)(s.adiv > 1 ? slot / s.adiv : slot) * s.astride;
     constexpr int PW = 4;                              // float4 per thread per pass
     if (s.pro == OH_PRO_Q8K) {
         if (q8) {
@@ -593,7 +593,7 @@ struct PIn { float4 a[4], b[4], c[4]; int4 q, bsv; float d; double r0, r1; };
 
 OH_DEV void pro_load(PIn &p, const oh_mvseg &s, int slot) {
     const int tid = tid_x(), in = s.in, nb = in / 256;
-    const size_t ao = (size_t)slot * s.astride;
+    const size_t ao = (size_t)(s.adiv > 1 ? slot / s.adiv : slot) * s.astride;
     if (s.pro == OH_PRO_Q8K) {
         const int n16 = in / 16;
         p.q = ldc4((const int4 *)(s.xqs + ao) + (tid < n16 ? tid : n16 - 1));
@@ -674,7 +674,7 @@ OH_DEV void pro_compute(const PIn &p, const oh_mvseg &s, int slot, int blk, uint
     float *ad = (float *)(smem + mv_lds_d_off(nb));
     float *v = (float *)(smem + mv_lds_v_off(nb));
     float4 *v4 = (float4 *)v;
-    const size_t ao = (size_t)slot * s.astride;
+    const size_t ao = (size_t)(s.adiv > 1 ? slot / s.adiv : slot) * s.astride;
     if (s.pro == OH_PRO_Q8K) {
         if (tid < in / 16) ((int4 *)aqs)[(tid >> 4) * (kAS / 16) + (tid & 15)] = p.q;
         if (tid < 2 * nb) ((int4 *)abs)[tid] = p.bsv;
@@ -841,18 +841,19 @@ OH_DEV void mv_seg(const oh_mvseg &s, int slot, int blk, int expert, uint8_t *sm
 // (larger logit, or equal logit and lower index); the k experts of rank < k in
 // rank order are the reference's picks. Softmax over the selected logits in
 // that order by one thread. Logits that are NaN or -inf fall back to the
-// sequential selection of one wave. Results in LDS (sel, w, *shg); virtual
-// block 0 also stores them for later phases.
-OH_DEV void route_block(const oh_mvlaunch &L, int vb, float *lg, int *sel, float *rw, float *shg, int *bad,
-                        int *cnt) {
+// sequential selection of one wave. Results in LDS (sel, w, *shg); with
+// `store` the block also stores them (token tok's) for later phases.
+OH_DEV void route_block(const oh_mvlaunch &L, int tok, bool store, float *lg, int *sel, float *rw, float *shg,
+                        int *bad, int *cnt) {
     const int tid = tid_x(), ne = L.ne, k = L.topk;
     const int ne4 = (ne + 3) & ~3;
     const bool has_sh = L.shl != nullptr;
+    const float *rlog = L.rlog + (size_t)tok * ne;
     if (tid == 0) *bad = 0;
     if (tid < 64) cnt[tid] = 0;
-    for (int e = tid; e < ne4; e += 256) lg[e] = e < ne ? ldc(L.rlog + e) : -INFINITY;
+    for (int e = tid; e < ne4; e += 256) lg[e] = e < ne ? ldc(rlog + e) : -INFINITY;
     __syncthreads();
-    const float shl = has_sh ? ldc(L.shl) : 0.0f;
+    const float shl = has_sh ? ldc(L.shl + tok) : 0.0f;
     // rank by strictly larger logits; equal logits inside the top k (or a
     // NaN / -inf anywhere) send the block to the sequential selection
     const float4 *l4 = (const float4 *)lg;
@@ -886,9 +887,9 @@ OH_DEV void route_block(const oh_mvlaunch &L, int vb, float *lg, int *sel, float
         if (tid == 0 && has_sh) *shg = ref_sigmoid(shl);
     }
     __syncthreads();
-    if (vb == 0) {
-        if (tid < k) { stc(L.ridx + tid, (int32_t)sel[tid]); stc(L.rw + tid, rw[tid]); }
-        if (tid == 0 && has_sh) stc(L.shg, *shg);
+    if (store) {
+        if (tid < k) { stc(L.ridx + (size_t)tok * k + tid, (int32_t)sel[tid]); stc(L.rw + (size_t)tok * k + tid, rw[tid]); }
+        if (tid == 0 && has_sh) stc(L.shg + tok, *shg);
     }
 }
 
@@ -908,13 +909,20 @@ OH_DEV void mv_body(const oh_mvlaunch &L, int vb, W &w) {
     const oh_mvseg &s = L.s[si];
     const int bseg = vb - s.block0;
     const int slot = bseg / s.bps, blk = bseg - slot * s.bps;
-    if (L.route == 1) {
+    if (L.route && L.tslots > 0) {
+        // several tokens: a stacked-segment block routes its own token
+        if (s.eidx) {
+            if (!w.wait()) return;
+            route_block(L, slot / L.tslots, blk == 0 && slot % L.tslots == 0, (float *)smem, rsel, rwt, &rshg,
+                        &rbad, rcnt);
+        }
+    } else if (L.route) {
         if (!w.wait()) return;
-        route_block(L, vb, (float *)smem, rsel, rwt, &rshg, &rbad, rcnt);
+        route_block(L, 0, vb == 0, (float *)smem, rsel, rwt, &rshg, &rbad, rcnt);
     } else if (s.eidx) {
         if (!w.wait()) return;                    // the routing comes from an earlier phase
     }
-    const int expert = !s.eidx ? 0 : (L.route == 1 ? rsel[slot] : ldc(s.eidx + slot));
+    const int expert = !s.eidx ? 0 : (L.route ? rsel[L.tslots > 0 ? slot % L.tslots : slot] : ldc(s.eidx + slot));
     if (TK >= 0) {
         mv_seg<TK < 0 ? OH_Q4_K : TK>(s, slot, blk, expert, smem, red, w);
     } else if (oh_qdot_can((uint32_t)s.type, s.in) && (s.xqs || s.pro != OH_PRO_Q8K)) {
@@ -976,7 +984,7 @@ OH_DEV void down_body(const oh_mvdown &D, int vb, W &wt) {
         for (int k = 0; k < HA; k++) {
             const int f = tid + bd * k < nf ? tid + bd * k : nf - 1;
             const int jj = 4 * f / in, e = 4 * f - jj * in;
-            ha[k] = ldc4((const float4 *)(D.h + (size_t)jj * D.stride + e));
+            ha[k] = ldc4((const float4 *)((jj < D.k ? D.h + (size_t)jj * D.stride : D.hsh) + e));
         }
     }
     SB<T> r[MJ];
@@ -996,7 +1004,7 @@ OH_DEV void down_body(const oh_mvdown &D, int vb, W &wt) {
     } else {
         for (int i = tid; i < ns * in; i += bd) {
             const int jj = i / in, e = i - jj * in;
-            v[i] = ldc(D.h + (size_t)jj * D.stride + e);
+            v[i] = ldc((jj < D.k ? D.h + (size_t)jj * D.stride : D.hsh) + e);
         }
     }
     lds_barrier();
@@ -1072,7 +1080,7 @@ OH_DEV void down_split(const oh_mvdown &D, int vb, W &wt) {
 #pragma unroll
     for (int k = 0; k < HA; k++) {
         const int f = lane + 64 * k < nf ? lane + 64 * k : nf - 1;
-        ha[k] = ldc4((const float4 *)(D.h + (size_t)j * D.stride) + f);
+        ha[k] = ldc4((const float4 *)(j < D.k ? D.h + (size_t)j * D.stride : D.hsh) + f);
     }
     const WP wp = sh ? WP{D.sA, D.sB, D.sC} : WP{D.A, D.B, D.C};
     SB<T> r;
@@ -1217,8 +1225,17 @@ extern "C" __global__ void __launch_bounds__(256) oh_k_mv_mixed(oh_mvlaunch L) {
 }
 
 // one wave per slot (blockDim = 64 * slots)
-extern "C" __global__ void __launch_bounds__(640) oh_k_mv_down(oh_mvdown D) {
+extern "C" __global__ void __launch_bounds__(640) oh_k_mv_down(oh_mvdown D0) {
     NoWait w;
+    // token blockIdx.y of a batch (0: the only token)
+    oh_mvdown D = D0;
+    const int t = (int)blockIdx.y;
+    D.h += t * D0.hts;
+    D.hsh += t * D0.hsts;
+    D.x += t * D0.xts;
+    D.eidx += (size_t)t * D0.k;
+    D.w += (size_t)t * D0.k;
+    if (D0.shg) D.shg += t;
     switch (D.type) {
     case OH_Q4_K: down_body<OH_Q4_K, 1>(D, (int)blockIdx.x, w); break;
     case OH_Q6_K: down_body<OH_Q6_K, 1>(D, (int)blockIdx.x, w); break;

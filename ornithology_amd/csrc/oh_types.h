@@ -106,6 +106,7 @@ typedef struct {
     int pro, gdim;
     int type, nb, in, rows, mode;  // mode 0: y = dot, 1: y += dot
     int nsub, ystride, astride;
+    int adiv;                      // slot k reads the activation of slot k / adiv (0, 1: its own)
     int units;                     // wave work units per slot
     int upw;                       // units per wave
     int bps;                       // blocks per slot
@@ -122,7 +123,11 @@ typedef struct {
 // A launch with `route` set first routes the MoE in every block: top-k over
 // the ne router logits rlog (plus the shared-expert gate logit shl, when
 // non-null); stacked segments then use the routed experts, and block 0 stores
-// the routing (ridx, rw, shg) for later launches.
+// the routing (ridx, rw, shg) for later launches. tslots > 0 (several tokens):
+// stacked slot k belongs to token k / tslots and is its expert k % tslots;
+// only stacked-segment blocks route (their token's logits at rlog + t*ne,
+// shl + t), and the first block of a token's first slot stores its routing
+// at ridx + t*topk, rw + t*topk, shg + t.
 typedef struct {
     oh_mvseg s[OH_MAX_SEGS];
     int n;
@@ -132,6 +137,7 @@ typedef struct {
     int ne, topk;
     int32_t *ridx;
     float *rw, *shg;
+    int tslots;
 } oh_mvlaunch;
 
 // Fused MoE down projection + combine (one block per row range, every slot).
@@ -141,8 +147,12 @@ typedef struct {
     const int32_t *eidx;
     const float *w;                // routing weights [k]
     const float *shg;              // sigmoid shared gate (null: ungated)
-    const float *h;                // silu(gate)*up of slot k at +k*stride
+    const float *h;                // silu(gate)*up of routed slot k at +k*stride
+    const float *hsh;              // silu(gate)*up of the shared expert
     float *x;                      // residual, += combine
+    // several tokens (grid y = token t): h + t*hts, hsh + t*hsts, x + t*xts,
+    // eidx / w + t*k, shg + t
+    size_t hts, hsts, xts;
     // split form (step kernel): a virtual block is (row group, group of 4
     // slots); slot dots go to dots[slot*rows + row], the last block of a row
     // group (counted in cnt[row group]) combines
