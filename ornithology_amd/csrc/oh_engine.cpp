@@ -1050,6 +1050,7 @@ struct ornith_hip_session {
     float *osz = nullptr;         // delta step: silu(gate) per output row
     double *oruns = nullptr;      // delta step: sum of o^2 per 64-row run
     int exact_max = 1024;         // contexts up to this walk the attention sum in one block
+    int flash_mfma = 1;           // decode flash chunks on the matrix cores (ORNITH_HIP_FLASH_MFMA=0: VALU)
     float2 *rope = nullptr;
     float *rl = nullptr, *shl = nullptr, *shg = nullptr, *ew = nullptr;
     int32_t *eidx = nullptr;
@@ -1256,7 +1257,7 @@ extern "C" int ornith_hip_session_new(ornith_hip_model *m, int cap, ornith_hip_s
     A_(salloc(s, &s->qr, aq)); A_(salloc(s, &s->agate, aq));
     A_(salloc(s, &s->scores, (size_t)a.nh * s->kvcap));
     {
-        const size_t nch = (size_t)(s->kvcap + oh_flash_chunk() - 1) / oh_flash_chunk();
+        const size_t nch = (size_t)oh_flash_slots(s->kvcap);
         A_(salloc(s, &s->fpo, (size_t)a.nh * nch * a.hd + 64));
         A_(salloc(s, &s->fpml, (size_t)a.nh * nch * 2 + 64));
     }
@@ -1267,6 +1268,8 @@ extern "C" int ornith_hip_session_new(ornith_hip_model *m, int cap, ornith_hip_s
     {
         const char *e = getenv("ORNITH_HIP_EXACT_ATTN_MAX");
         if (e && *e) s->exact_max = atoi(e);
+        const char *f = getenv("ORNITH_HIP_FLASH_MFMA");
+        if (f && *f) s->flash_mfma = atoi(f) != 0;
     }
     A_(salloc(s, &s->rl, a.ne > 0 ? a.ne : 1)); A_(salloc(s, &s->shl, 1)); A_(salloc(s, &s->shg, 1));
     A_(salloc(s, &s->ew, 64)); A_(salloc(s, &s->eidx, 64));
@@ -1361,13 +1364,12 @@ static int build_body(ornith_hip_session *s, Prog &P) {
             at.qr = s->qr; at.gate = s->agate; at.Kt = z.Kt; at.Ks = z.Ks; at.Vq = z.Vq; at.Vs = z.Vs;
             at.scores = s->scores; at.part_o = s->fpo; at.part_ml = s->fpml; at.out = s->o;
             at.nh = a.nh; at.nkv = a.nkv; at.hd = a.hd; at.cap = s->kvcap; at.exact_max = s->exact_max;
-            at.hb = oh_flash_hb(a.nh, a.nkv); at.scale = scale;
-            const int nch = (s->kvcap + oh_flash_chunk() - 1) / oh_flash_chunk();
-            const double nchd = ceil(T / (double)oh_flash_chunk());
+            at.hb = oh_flash_form(a.nh, a.nkv, a.hd, s->flash_mfma); at.scale = scale;
+            const double nchd = oh_flash_parts((int)T, s->kvcap, at.hb);
             // exact walk (its scores in LDS) or flash chunks, then the merge
             // of the chunks (which exits after an exact walk)
-            const int nv_ex = a.nh / (256 / a.hd), nv_fl = a.nkv * (a.nh / a.nkv / at.hb) * nch;
-            const int lds_ex = oh_exact_lds_bytes(a.hd, s->exact_max), lds_fl = oh_flash_lds_bytes(a.nh, a.nkv, a.hd);
+            const int nv_ex = a.nh / (256 / a.hd), nv_fl = oh_flash_nvb(a.nh, a.nkv, s->kvcap, at.hb);
+            const int lds_ex = oh_exact_lds_bytes(a.hd, s->exact_max), lds_fl = oh_flash_form_lds(a.nh, a.nkv, a.hd, at.hb);
             oh_op o3 = op_new(OH_OP_ATTN_MAIN, nv_ex > nv_fl ? nv_ex : nv_fl, lds_ex > lds_fl ? lds_ex : lds_fl);
             o3.u.attn = at;
             prog_add(P, o3, K_ATTN_MAIN,
@@ -2279,11 +2281,10 @@ extern "C" int ornith_hip_batch_step(ornith_hip_session **ss, int n, const int32
                 at.Kt = z.Kt; at.Ks = z.Ks; at.Vq = z.Vq; at.Vs = z.Vs;
                 at.scores = sb->scores; at.part_o = sb->fpo; at.part_ml = sb->fpml; at.out = p.OA + (size_t)b * aq;
                 at.nh = a.nh; at.nkv = a.nkv; at.hd = a.hd; at.cap = sb->kvcap; at.exact_max = sb->exact_max;
-                at.hb = oh_flash_hb(a.nh, a.nkv); at.scale = 1.0f / sqrtf((float)a.hd);
+                at.hb = oh_flash_form(a.nh, a.nkv, a.hd, sb->flash_mfma); at.scale = 1.0f / sqrtf((float)a.hd);
                 memcpy(dst + (size_t)n * sizeof(oh_op_prep) + (size_t)b * sizeof(oh_op_attn), &at, sizeof at);
-                const int nch = (sb->kvcap + oh_flash_chunk() - 1) / oh_flash_chunk();
-                const int nv_ex = a.nh / (256 / a.hd), nv_fl = a.nkv * (a.nh / a.nkv / at.hb) * nch;
-                const int lds_ex = oh_exact_lds_bytes(a.hd, sb->exact_max), lds_fl = oh_flash_lds_bytes(a.nh, a.nkv, a.hd);
+                const int nv_ex = a.nh / (256 / a.hd), nv_fl = oh_flash_nvb(a.nh, a.nkv, sb->kvcap, at.hb);
+                const int lds_ex = oh_exact_lds_bytes(a.hd, sb->exact_max), lds_fl = oh_flash_form_lds(a.nh, a.nkv, a.hd, at.hb);
                 B.nvb_main = std::max(B.nvb_main, std::max(nv_ex, nv_fl));
                 B.lds_main = std::max(B.lds_main, std::max(lds_ex, lds_fl));
             } else {

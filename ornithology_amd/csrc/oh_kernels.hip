@@ -308,6 +308,24 @@ int oh_flash_lds_bytes(int nh, int nkv, int hd) {
 }
 int oh_flash_chunk(void) { return kFlashCh; }
 
+// flash form of a decode attention: 0 = the matrix-core chunks (every query
+// head of a KV head per block), else the query heads per VALU flash block
+int oh_flash_form(int nh, int nkv, int hd, int mfma) {
+    if (mfma && nkv > 0 && nh % nkv == 0 && nh / nkv <= 16 && (hd == 64 || hd == 128 || hd == 256)) return 0;
+    return oh_flash_hb(nh, nkv);
+}
+int oh_flash_nvb(int nh, int nkv, int cap, int hb) {
+    return hb == 0 ? nkv * fd_blocks(cap) : nkv * (nh / nkv / hb) * ((cap + kFlashCh - 1) / kFlashCh);
+}
+int oh_flash_form_lds(int nh, int nkv, int hd, int hb) { return hb == 0 ? kFdLds : oh_flash_lds_bytes(nh, nkv, hd); }
+int oh_flash_slots(int cap) { return fd_slots(cap); }
+// partials per KV head at context T
+int oh_flash_parts(int T, int cap, int hb) {
+    if (hb != 0) return (T + kFlashCh - 1) / kFlashCh;
+    const int tpb = fd_tpb(T, cap);
+    return ((T + kFdT - 1) / kFdT + tpb - 1) / tpb;
+}
+
 // exact attention walk: the scores of a block's 256/hd heads in LDS
 int oh_exact_lds_bytes(int hd, int exact_max) {
     const int lim = exact_max < kExactMax ? (exact_max > 0 ? exact_max : 0) : kExactMax;

@@ -78,6 +78,11 @@ hipError_t oh_launch_op(const oh_op *op, const int32_t *io, hipStream_t st);
 // flash decoding past exact_max positions: query heads per block, LDS bytes,
 // chunk length
 int oh_flash_hb(int nh, int nkv);
+int oh_flash_form(int nh, int nkv, int hd, int mfma);
+int oh_flash_nvb(int nh, int nkv, int cap, int hb);
+int oh_flash_form_lds(int nh, int nkv, int hd, int hb);
+int oh_flash_slots(int cap);
+int oh_flash_parts(int T, int cap, int hb);
 int oh_flash_lds_bytes(int nh, int nkv, int hd);
 int oh_flash_chunk(void);
 int oh_delta_lds_bytes(int dk);

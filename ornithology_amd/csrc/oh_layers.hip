@@ -664,6 +664,247 @@ OH_DEV void flash_body(const oh_op_attn &a, int vb, int pos, int lim, W &w) {
     flash_token<HB, true, false>(a, L, g, hb0, c, T, nullptr, a.part_o, a.part_ml);
 }
 
+// ---- flash decoding on the matrix cores --------------------------------------------
+// The same chunked form (re-associated softmax and V sums, tolerance bar) for
+// the decode token, with every query head of a KV head in one block: block b
+// of KV head g takes the 32-position tiles [b*tpb, (b+1)*tpb) of the context
+// and its four waves take every fourth tile. Per tile a wave forms S^T = K Q^T
+// (32 positions x the G <= 16 query heads of g as columns) with
+// v_mfma_f32_16x16x32_f16 on the raw int8 key codes (exact in fp16) against
+// the pre-scaled queries split into fp16 high and low parts (two products:
+// about 22 significant bits; each head's queries and each wave's P*Vs are
+// first brought to at most 1 by an exact power of two, undone in fp32), scales
+// by the keys' scales in fp32, keeps a running max and sum per head, and
+// accumulates O^T += V^T P^T on the raw value codes with P*Vs split the same
+// way. The four waves' (m, l, O) merge in
+// LDS into one partial per block; attn_combine merges the blocks.
+//
+// Lane layouts of v_mfma_f32_16x16x32_f16: A (16 x 32) lane l holds row l%16,
+// k = 8*(l/16) + j; B (32 x 16) column l%16, the same k; D (16 x 16) column
+// l%16, rows 4*(l/16) + v. Row r of the two S^T sub-tiles u = 0, 1 is position
+// 8*(r/4) + 4u + r%4 of the tile, so D value v of sub-tile u in lane (c, q)
+// is position 8q + 4u + v: exactly the B operand (k = 8q + j) of the tile's
+// 32-position V^T P^T product.
+typedef _Float16 fd_h8 __attribute__((ext_vector_type(8)));
+typedef float fd_f4 __attribute__((ext_vector_type(4)));
+constexpr int kFdT = 32;          // positions per wave tile
+constexpr int kFdMaxBlk = 128;    // blocks per KV head
+
+OH_HD inline int fd_blocks(int cap) {
+    const int b = (cap + kFdT - 1) / kFdT;
+    return b < kFdMaxBlk ? b : kFdMaxBlk;
+}
+// partial slots per KV head (both flash forms share the partial buffers)
+OH_HD inline int fd_slots(int cap) {
+    const int c = (cap + kFlashCh - 1) / kFlashCh, b = fd_blocks(cap);
+    return c > b ? c : b;
+}
+// tiles per block for context T (the blocks holding work: ceil(tiles / tpb))
+OH_HD inline int fd_tpb(int T, int cap) {
+    const int nt = (T + kFdT - 1) / kFdT, B = fd_blocks(cap);
+    return (nt + B - 1) / B;
+}
+constexpr int kFdLds = 4 * 64 * 2 * 4 + 4 * 4 * 64 * 16;   // merge: (m, l) and four dim tiles per wave
+
+template <int HD, class W>
+OH_DEV void flashm_body(const oh_op_attn &a, int vb, int pos, int lim, W &w) {
+    extern __shared__ __align__(16) uint8_t fsm[];
+    constexpr int NS = HD / 32, ND = HD / 16, HW = HD / 4;
+    const int nkv = a.nkv, G = a.nh / nkv, cap = a.cap, T = pos + 1;
+    const int g = vb % nkv, b = vb / nkv;
+    const int nt = (T + kFdT - 1) / kFdT, tpb = fd_tpb(T, cap), tb = b * tpb;
+    if (T <= lim || tb >= nt) return;
+    if (!w.wait()) return;
+    const int te = tb + tpb < nt ? tb + tpb : nt;
+    const int tid = tid_x(), lane = tid & 63, wave = tid >> 6;
+    const int col = lane & 15, qd = lane >> 4, r = lane & 15;
+    const bool cv = col < G;
+    // the queries (written by the prep operation) as B operands: K-step s
+    // holds dims 32 s + 8 qd .. + 7 of head col, times 1/sqrt(hd) and 2^-eq
+    // (eq: the exponent of the head's largest |q|, so the fp16 halves keep
+    // their precision whatever the magnitude)
+    fd_h8 qh[NS], ql[NS];
+    int eq = 0;
+    {
+        const float *qs = a.qr + (size_t)(g * G + (cv ? col : 0)) * HD + 8 * qd;
+        float xv[NS][8];
+        float amax = 0.0f;
+#pragma unroll
+        for (int s = 0; s < NS; s++) {
+            const float4 x0 = ldc4((const float4 *)(qs + 32 * s)), x1 = ldc4((const float4 *)(qs + 32 * s + 4));
+            const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                xv[s][j] = cv ? xs[j] * a.scale : 0.0f;
+                amax = fmaxf(amax, fabsf(xv[s][j]));
+            }
+        }
+        amax = fmaxf(amax, shfl_xor(amax, 16));
+        amax = fmaxf(amax, shfl_xor(amax, 32));
+        if (amax > 0.0f && amax <= 3.0e38f) frexpf(amax, &eq);
+#pragma unroll
+        for (int s = 0; s < NS; s++)
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const float v = ldexpf(xv[s][j], -eq);
+                const _Float16 h = (_Float16)v;
+                qh[s][j] = h;
+                ql[s][j] = (_Float16)(v - (float)h);
+            }
+    }
+    fd_f4 o[ND];
+#pragma unroll
+    for (int d = 0; d < ND; d++) o[d] = fd_f4{0.0f, 0.0f, 0.0f, 0.0f};
+    // O is kept in units of 2^-ev, ev the exponent of the largest value scale
+    // seen so far by this wave (P*Vs*2^-ev <= 1 keeps the fp16 halves exact)
+    float m = -INFINITY, l = 0.0f, vm = 0.0f;
+    int ev = 0;
+    const uint32_t *kb = a.Kt + (size_t)g * HW * cap;
+    const uint8_t *vq = (const uint8_t *)a.Vq + (size_t)g * (cap / 16) * HD * 16;
+    for (int t = tb + wave; t < te; t += 4) {
+        const int p0 = t * kFdT;
+        // every load of the tile first: key words, value codes, scales
+        uint32_t kw[2][NS][2];
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            int p = p0 + 8 * (r >> 2) + 4 * u + (r & 3);
+            p = p < T ? p : T - 1;
+#pragma unroll
+            for (int s = 0; s < NS; s++) {
+                kw[u][s][0] = ldg(kb + (size_t)(8 * s + 2 * qd) * cap + p);
+                kw[u][s][1] = ldg(kb + (size_t)(8 * s + 2 * qd + 1) * cap + p);
+            }
+        }
+        int vt = (p0 + 8 * qd) / 16;
+        vt = vt <= (T - 1) / 16 ? vt : (T - 1) / 16;
+        uint2 vw[ND];
+#pragma unroll
+        for (int d = 0; d < ND; d++)
+            vw[d] = ldg((const uint2 *)(vq + ((size_t)vt * HD + 16 * d + r) * 16 + 8 * (qd & 1)));
+        float ks[8], vs[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int p = p0 + 8 * qd + j, pc = p < T ? p : T - 1;
+            ks[j] = ldg(a.Ks + (size_t)pc * nkv + g);
+            vs[j] = ldg(a.Vs + (size_t)pc * nkv + g);
+        }
+        // scores of positions p0 + 8 qd + j for head col
+        float sj[8];
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            fd_f4 sc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int s = 0; s < NS; s++) {
+                fd_h8 ka;
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    ka[j] = (_Float16)(float)(int8_t)(kw[u][s][0] >> (8 * j));
+                    ka[4 + j] = (_Float16)(float)(int8_t)(kw[u][s][1] >> (8 * j));
+                }
+                sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qh[s], sc, 0, 0, 0);
+                sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, ql[s], sc, 0, 0, 0);
+            }
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const int j = 4 * u + v;
+                const float k = ks[j];
+                const float x = k == 0.0f ? 0.0f : sc[v] * ldexpf(k, eq);
+                sj[j] = p0 + 8 * qd + j < T ? x : -INFINITY;
+            }
+        }
+        // online softmax per head (the tile's first position is < T, so the
+        // new max is finite)
+        float mx = sj[0];
+#pragma unroll
+        for (int j = 1; j < 8; j++) mx = fmaxf(mx, sj[j]);
+        mx = fmaxf(mx, shfl_xor(mx, 16));
+        mx = fmaxf(mx, shfl_xor(mx, 32));
+        const float mn = fmaxf(m, mx);
+        const float corr = m == -INFINITY ? 0.0f : __expf(m - mn);
+        float vx = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+            if (p0 + 8 * qd + j < T) vx = fmaxf(vx, fabsf(vs[j]));
+        vx = fmaxf(vx, shfl_xor(vx, 16));
+        vx = fmaxf(vx, shfl_xor(vx, 32));
+        vm = fmaxf(vm, vx);
+        int en = ev;
+        if (vm > 0.0f && vm <= 3.0e38f) frexpf(vm, &en);
+        const float fac = corr * ldexpf(1.0f, ev - en);
+        ev = en;
+        float ls = 0.0f;
+        fd_h8 ph, pl;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const float e = sj[j] == -INFINITY ? 0.0f : __expf(sj[j] - mn);
+            ls += e;
+            const float pv = p0 + 8 * qd + j < T ? e * ldexpf(vs[j], -ev) : 0.0f;
+            const _Float16 h = (_Float16)pv;
+            ph[j] = h;
+            pl[j] = (_Float16)(pv - (float)h);
+        }
+        ls += shfl_xor(ls, 16);
+        ls += shfl_xor(ls, 32);
+        l = l * corr + ls;
+        m = mn;
+        if (__ballot(fac != 1.0f) != 0) {
+#pragma unroll
+            for (int d = 0; d < ND; d++) o[d] *= fac;
+        }
+#pragma unroll
+        for (int d = 0; d < ND; d++) {
+            fd_h8 va;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                va[j] = (_Float16)(float)(int8_t)(vw[d].x >> (8 * j));
+                va[4 + j] = (_Float16)(float)(int8_t)(vw[d].y >> (8 * j));
+            }
+            o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, ph, o[d], 0, 0, 0);
+            o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pl, o[d], 0, 0, 0);
+        }
+    }
+    {
+        const float u = ldexpf(1.0f, ev);
+#pragma unroll
+        for (int d = 0; d < ND; d++) o[d] *= u;
+    }
+    // merge the four waves: factors exp(m_w - M) per lane, then the dim tiles
+    // four at a time through LDS (thread (wave, lane) merges tile d0 + wave)
+    float *sml = (float *)fsm;                                  // [4][64][2]
+    fd_f4 *sob = (fd_f4 *)(fsm + 4 * 64 * 2 * 4);               // [4 waves][4 tiles][64]
+    sml[(wave * 64 + lane) * 2] = m;
+    sml[(wave * 64 + lane) * 2 + 1] = l;
+    __syncthreads();
+    float M = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < 4; k++) M = fmaxf(M, sml[(k * 64 + lane) * 2]);
+    float f[4], L = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const float mk = sml[(k * 64 + lane) * 2];
+        f[k] = mk == -INFINITY ? 0.0f : __expf(mk - M);
+        L += sml[(k * 64 + lane) * 2 + 1] * f[k];
+    }
+    const int S = fd_slots(cap);
+    const size_t pb = ((size_t)g * S + b) * G + col;
+    if (cv && wave == 0 && qd == 0) {
+        stc(a.part_ml + pb * 2, M);
+        stc(a.part_ml + pb * 2 + 1, L);
+    }
+#pragma unroll
+    for (int d0 = 0; d0 < ND; d0 += 4) {
+#pragma unroll
+        for (int k = 0; k < 4; k++) sob[(wave * 4 + k) * 64 + lane] = o[d0 + k];
+        __syncthreads();
+        fd_f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int k = 0; k < 4; k++) acc += sob[(k * 4 + wave) * 64 + lane] * f[k];
+        if (cv) stc4((float4 *)(a.part_o + pb * HD + 16 * (d0 + wave) + 4 * qd),
+                     make_float4(acc[0], acc[1], acc[2], acc[3]));
+        __syncthreads();
+    }
+}
+
 // The attention of the current step: up to lim = min(exact_max, kExactMax)
 // positions the exact walk (virtual blocks [0, nh*hd/256)), beyond that the
 // flash chunks (virtual blocks as flash_body).
@@ -672,6 +913,10 @@ OH_DEV void attn_main_body(const oh_op_attn &a, int vb, int pos, W &w) {
     const int lim = a.exact_max < kExactMax ? a.exact_max : kExactMax;
     if (pos + 1 <= lim) {
         exact_body(a, vb, pos, lim, w);
+    } else if (a.hb == 0) {
+        if (a.hd == 256) flashm_body<256>(a, vb, pos, lim, w);
+        else if (a.hd == 128) flashm_body<128>(a, vb, pos, lim, w);
+        else flashm_body<64>(a, vb, pos, lim, w);
     } else if (a.hb == 4) {
         flash_body<4>(a, vb, pos, lim, w);
     } else if (a.hb == 2) {
@@ -696,7 +941,9 @@ OH_DEV void combine_body(const oh_op_attn &a, int vb, int pos, W &w) {
     const int h = vb % nh, G = nh / nkv, g = h / G, hl = h % G;
     const int wave = (tid_x() >> 6), lane = (tid_x() & 63);
     const int i = (vb / nh) * 64 + lane;
-    const int nch = (T + kFlashCh - 1) / kFlashCh, nchmax = (cap + kFlashCh - 1) / kFlashCh;
+    const int nch = a.hb == 0 ? (((T + kFdT - 1) / kFdT) + fd_tpb(T, cap) - 1) / fd_tpb(T, cap)
+                              : (T + kFlashCh - 1) / kFlashCh;
+    const int nchmax = a.hb == 0 ? fd_slots(cap) : (cap + kFlashCh - 1) / kFlashCh;
     float M = -INFINITY, L = 0.0f, O = 0.0f;
     // chunks wave, wave+4, ... in order; their partials requested 8 at a time
     constexpr int CB = 8;

@@ -69,9 +69,11 @@ def test_prefill_dense_matches_oracle(hip_ctx, orc, tmp_path, monkeypatch):
 def evals(m, chunks, cap, prefill, monkeypatch, exact_max):
     monkeypatch.setenv("ORNITH_HIP_PREFILL", "1" if prefill else "0")
     monkeypatch.setenv("ORNITH_HIP_PREFILL_CHUNK", "96")
-    # the prompt's flash chunks are the decode step's (bit-identical); the
-    # matrix-core prompt attention is checked to tolerance below
+    # the prompt's flash chunks are the decode step's VALU flash chunks
+    # (bit-identical); the matrix-core prompt and decode attention are checked
+    # to tolerance (below and in test_gpu_flash_decode.py)
     monkeypatch.setenv("ORNITH_HIP_ATTN_MFMA", "0")
+    monkeypatch.setenv("ORNITH_HIP_FLASH_MFMA", "0")
     if exact_max is not None:
         monkeypatch.setenv("ORNITH_HIP_EXACT_ATTN_MAX", str(exact_max))
     s = m.session(cap)
