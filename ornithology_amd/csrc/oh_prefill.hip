@@ -234,9 +234,10 @@ oh_k_delta_chunked(const float *qn, const float *kn, const float *conv, const fl
                    const float *grams, float *S, float *out, int T, int nk, int nv, int cc, float out_scale) {
     constexpr int CH = kDeltaChunk, RB = 16, KS = DK + 4, XS = DK + 4, CPL = DK / 16;
     __shared__ __align__(16) float kc[CH][KS], qc[CH][KS];
-    __shared__ float M[CH][CH + 1], W[CH][CH + 1];       // k_j.k_i / k_j.q_i, then the coefficients
+    __shared__ __align__(16) float M[CH][CH + 4], W[CH][CH + 4];   // k_j.k_i / k_j.q_i, then the coefficients
     __shared__ float U[CH][RB + 1], Sq[CH][RB + 1];      // [token][row]
     __shared__ float alpha[CH], beta[CH], p[CH], wend[CH];
+    __shared__ int mz[CH];                               // row i of M holds a zero (j < i)
     __shared__ __align__(16) float xs[RB * XS];
     const int tid = tid_x();
     const int vb = (int)blockIdx.x, hv = vb / (DK / RB), slab = vb % (DK / RB), kh = hv % nk;
@@ -257,29 +258,65 @@ oh_k_delta_chunked(const float *qn, const float *kn, const float *conv, const fl
             s[4 * c] = v.x; s[4 * c + 1] = v.y; s[4 * c + 2] = v.z; s[4 * c + 3] = v.w;
         }
     };
-    reload();
+    // the next chunk's keys, queries, Gram matrices, values and gates are
+    // requested into registers while the current chunk is computed
+    constexpr int NKQ = CH * DK / 4 / 256, NG = CH * CH / 256, NU = CH * RB / 256;
+    float4 rk[NKQ], rq[NKQ];
+    float rm[NG], rw[NG], ru[NU], ral = 0.0f, rbe = 0.0f;
+    auto fetch = [&](int cs, int chn) {
+        const int Cn = T - cs < CH ? T - cs : CH;
+        if (Cn <= 0) return;
+#pragma unroll
+        for (int m = 0; m < NKQ; m++) {
+            const int e = tid + 256 * m, i = e / (DK / 4), c = e - i * (DK / 4);
+            const size_t src = ((size_t)(cs + (i < Cn ? i : 0)) * nk + kh) * DK;
+            rk[m] = ldg((const float4 *)(kn + src) + c);
+            rq[m] = ldg((const float4 *)(qn + src) + c);
+        }
+        const float *gm = grams + ((size_t)chn * nk + kh) * 2 * CH * CH;
+#pragma unroll
+        for (int m = 0; m < NG; m++) {
+            rm[m] = ldg(gm + tid + 256 * m);
+            rw[m] = ldg(gm + CH * CH + tid + 256 * m);
+        }
+        if (tid < Cn) {
+            ral = ldg(al + (size_t)(cs + tid) * nv + hv);
+            rbe = ldg(be + (size_t)(cs + tid) * nv + hv);
+        }
+#pragma unroll
+        for (int m = 0; m < NU; m++) {
+            const int e = tid + 256 * m, i = e / RB, rr = e - i * RB;
+            ru[m] = ldg(conv + (size_t)(cs + (i < Cn ? i : 0)) * cc + 2 * qd + r0 + rr);
+        }
+    };
+    fetch(0, 0);
     for (int c0 = 0, ch = 0; c0 < T; c0 += CH, ch++) {
         const int C = T - c0 < CH ? T - c0 : CH;
         __syncthreads();                                 // the previous chunk is consumed
-        for (int e = tid; e < C * DK / 4; e += 256) {
-            const int i = e / (DK / 4), c = e - i * (DK / 4);
-            const size_t src = ((size_t)(c0 + i) * nk + kh) * DK;
-            *(float4 *)(&kc[i][4 * c]) = ldg((const float4 *)(kn + src) + c);
-            *(float4 *)(&qc[i][4 * c]) = ldg((const float4 *)(qn + src) + c);
+#pragma unroll
+        for (int m = 0; m < NKQ; m++) {
+            const int e = tid + 256 * m, i = e / (DK / 4), c = e - i * (DK / 4);
+            if (i < C) {
+                *(float4 *)(&kc[i][4 * c]) = rk[m];
+                *(float4 *)(&qc[i][4 * c]) = rq[m];
+            }
         }
-        const float *gm = grams + ((size_t)ch * nk + kh) * 2 * CH * CH;
-        for (int e = tid; e < CH * CH; e += 256) {
-            M[e / CH][e % CH] = ldg(gm + e);
-            W[e / CH][e % CH] = ldg(gm + CH * CH + e);
+#pragma unroll
+        for (int m = 0; m < NG; m++) {
+            const int e = tid + 256 * m;
+            M[e / CH][e % CH] = rm[m];
+            W[e / CH][e % CH] = rw[m];
         }
         if (tid < C) {
-            alpha[tid] = ldg(al + (size_t)(c0 + tid) * nv + hv);
-            beta[tid] = ldg(be + (size_t)(c0 + tid) * nv + hv);
+            alpha[tid] = ral;
+            beta[tid] = rbe;
         }
-        for (int e = tid; e < C * RB; e += 256) {
-            const int i = e / RB, rr = e - i * RB;
-            U[i][rr] = ldg(conv + (size_t)(c0 + i) * cc + 2 * qd + r0 + rr);
+#pragma unroll
+        for (int m = 0; m < NU; m++) {
+            const int e = tid + 256 * m, i = e / RB, rr = e - i * RB;
+            if (i < C) U[i][rr] = ru[m];
         }
+        fetch(c0 + CH, ch + 1);
         __syncthreads();
         // decay products: thread i owns row i of the coefficient tables, which
         // turn in place into M[i][j] = beta_i (p_i/p_j) k_j.k_i and
@@ -291,11 +328,15 @@ oh_k_delta_chunked(const float *qn, const float *kn, const float *conv, const fl
             p[i] = pi;
             const float bi = beta[i];
             float ratio = 1.0f;
+            int z = 0;
             for (int j = i - 1; j >= 0; j--) {
                 ratio *= alpha[j + 1];
-                M[i][j] = bi * ratio * M[i][j];
+                const float mij = bi * ratio * M[i][j];
+                M[i][j] = mij;
+                z |= mij == 0.0f;
                 W[i][j] = ratio * W[i][j];
             }
+            mz[i] = z;
         }
         if (tid == 64) {
             float ratio = 1.0f;
@@ -306,7 +347,9 @@ oh_k_delta_chunked(const float *qn, const float *kn, const float *conv, const fl
         }
         __syncthreads();
         // projections of the incoming state, tokens g and g + 16; U starts as
-        // t_i = beta_i v_i - beta_i p_i (S_in k_i)
+        // t_i = beta_i v_i - beta_i p_i (S_in k_i); the state row comes from
+        // LDS here (it is live only in this phase)
+        reload();
         {
             const int i0 = g, i1 = g + RB;
             const int j0 = i0 < C ? i0 : 0, j1 = i1 < C ? i1 : 0;
@@ -328,7 +371,11 @@ oh_k_delta_chunked(const float *qn, const float *kn, const float *conv, const fl
             }
         }
         __syncthreads();
-        // forward substitution (I + M) U = T, a thread per row, in registers
+        // forward substitution (I + M) U = T, a thread per row, in registers:
+        // u_i = (((t_i - m_{i,i-1} u_{i-1}) - m_{i,i-2} u_{i-2}) ...), a term
+        // with m = 0 skipped (subtracting an exact +0 leaves u_i's bits as
+        // they are, so the zero test sits on the product, off the chain). Row
+        // i's coefficients are read into registers before its chain starts.
         if (tid < RB) {
             float u[CH];
 #pragma unroll
@@ -336,11 +383,23 @@ oh_k_delta_chunked(const float *qn, const float *kn, const float *conv, const fl
 #pragma unroll
             for (int i = 1; i < CH; i++) {
                 if (i < C) {
-                    float ui = u[i];
+                    float mr[CH];
 #pragma unroll
-                    for (int j = i - 1; j >= 0; j--) {
-                        const float mij = M[i][j];
-                        ui = mij != 0.0f ? ui - mij * u[j] : ui;
+                    for (int q = 0; q < CH / 4; q++)
+                        if (4 * q < i) {
+                            const float4 v = *(const float4 *)&M[i][4 * q];
+                            mr[4 * q] = v.x; mr[4 * q + 1] = v.y; mr[4 * q + 2] = v.z; mr[4 * q + 3] = v.w;
+                        }
+                    float ui = u[i];
+                    if (__builtin_amdgcn_readfirstlane(mz[i]) == 0) {
+#pragma unroll
+                        for (int j = i - 1; j >= 0; j--) ui = ui - mr[j] * u[j];
+                    } else {
+#pragma unroll
+                        for (int j = i - 1; j >= 0; j--) {
+                            const float pr = mr[j] != 0.0f ? mr[j] * u[j] : 0.0f;
+                            ui = ui - pr;
+                        }
                     }
                     u[i] = ui;
                 }
@@ -350,7 +409,8 @@ oh_k_delta_chunked(const float *qn, const float *kn, const float *conv, const fl
                 if (i < C) U[i][tid] = u[i];
         }
         __syncthreads();
-        // outputs of tokens g and g + 16, scaled by 1/sqrt(dk)
+        // outputs of tokens g and g + 16, scaled by 1/sqrt(dk): o_i =
+        // p_i Sq_i + w_ii u_i + sum_{j<i} w_ij u_j, j descending
         {
             float u[CH];
 #pragma unroll
@@ -359,11 +419,17 @@ oh_k_delta_chunked(const float *qn, const float *kn, const float *conv, const fl
             for (int h = 0; h < 2; h++) {
                 const int i = g + RB * h;
                 if (i < C) {
+                    float wr[CH];
+#pragma unroll
+                    for (int q = 0; q < CH / 4; q++) {
+                        const float4 v = *(const float4 *)&W[i][4 * q];
+                        wr[4 * q] = v.x; wr[4 * q + 1] = v.y; wr[4 * q + 2] = v.z; wr[4 * q + 3] = v.w;
+                    }
                     float o = p[i] * Sq[i][r];
-                    o += W[i][i] * u[i];
+                    o += W[i][i] * U[i][r];
 #pragma unroll
                     for (int j = CH - 1; j >= 0; j--)
-                        if (j < i) o += W[i][j] * u[j];
+                        if (j < i) o += wr[j] * u[j];
                     o *= out_scale;
                     stg(out + (size_t)(c0 + i) * vd + r0 + r, o);
                 }
@@ -373,26 +439,35 @@ oh_k_delta_chunked(const float *qn, const float *kn, const float *conv, const fl
         // CPL columns of row ur
         {
             const float pc = p[C - 1];
-            float x[CPL];
+            float x[CPL], uw[CH];
             float *xr = xs + ur * XS + ucg * CPL;
+#pragma unroll
+            for (int j = 0; j < CH; j++) uw[j] = j < C ? wend[j] * U[j][ur] : 0.0f;
 #pragma unroll
             for (int c = 0; c < CPL; c++) x[c] = xr[c] * pc;
 #pragma unroll
             for (int j = CH - 1; j >= 0; j--) {
                 if (j < C) {
-                    const float uj = wend[j] * U[j][ur];
+                    // the key segment is read whether or not the term is
+                    // skipped, so the reads can run ahead of the sums
+                    float kk[CPL];
+#pragma unroll
+                    for (int c4 = 0; c4 < CPL / 4; c4++) {
+                        const float4 v = *(const float4 *)&kc[j][ucg * CPL + 4 * c4];
+                        kk[4 * c4] = v.x; kk[4 * c4 + 1] = v.y; kk[4 * c4 + 2] = v.z; kk[4 * c4 + 3] = v.w;
+                    }
+                    const float uj = uw[j];
                     if (uj != 0.0f) {
 #pragma unroll
-                        for (int c = 0; c < CPL; c++) x[c] += uj * kc[j][ucg * CPL + c];
+                        for (int c = 0; c < CPL; c++) x[c] += uj * kk[c];
                     }
                 }
             }
 #pragma unroll
             for (int c = 0; c < CPL; c++) xr[c] = x[c];
         }
-        __syncthreads();
-        reload();
     }
+    __syncthreads();                                     // every row's update is in LDS
     for (int e = tid; e < RB * DK / 4; e += 256) {
         const int row = e / (DK / 4), c4 = e - row * (DK / 4);
         stg((float4 *)Srow + e, *(const float4 *)(xs + row * XS + 4 * c4));
