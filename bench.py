@@ -425,6 +425,9 @@ def main() -> int:
                     f"{args.ctx}-token Q8 KV context, greedy")
         dtype = "int8 dot (Q8_K x Q4_K/Q6_K) + f32"
 
+    if os.environ.get("ORNITH_HIP_NO_GRAPH") == "1" and args.batch > 0:
+        log("ORNITH_HIP_NO_GRAPH=1: the batch-decode figure needs HIP graphs, skipped")
+        args.batch = 0
     ctx = oa.Context(0)
     t0 = time.perf_counter()
     model = ctx.synth(**cfg)

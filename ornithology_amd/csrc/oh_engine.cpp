@@ -2239,6 +2239,12 @@ extern "C" int ornith_hip_batch_step(ornith_hip_session **ss, int n, const int32
         seterr("batch_step: the model is outside the batched projection path (widths <= 8192, integer dot types)");
         return ORNITH_HIP_ERR_UNSUPPORTED;
     }
+    if (!graphs_enabled()) {
+        // the batch step runs as one captured HIP graph; its eager form is
+        // switched off (a GPU fault in an eager batch run is not explained)
+        seterr("batch_step: needs HIP graphs (unset ORNITH_HIP_NO_GRAPH)");
+        return ORNITH_HIP_ERR_UNSUPPORTED;
+    }
     HCHK(hipSetDevice(m->ctx->device));
     hipStream_t st = m->ctx->st;
     const int qd = a.nk * a.dk, vd = a.nv * a.dv, cc = 2 * qd + vd, aq = a.nh * a.hd;
