@@ -432,9 +432,12 @@ OH_DEV void exact_body(const oh_op_attn &a, int vb, int pos, int lim, W &w) {
                 for (int j = 0; j < 16; j++) {
                     const int k = k0 + 16 * u + j;
                     const int8_t c = (int8_t)(wsel(cw[u], j >> 2) >> (8 * (j & 3)));
+                    // the reference skips zero weights; o starts at +0 and a
+                    // round-to-nearest sum is -0 only when both addends are,
+                    // so o is never -0 and adding 0 * c = +-0 leaves its bits
+                    // unchanged: the plain sum equals the skipping one
                     const float sv = k < n ? pbuf[hl][k] : 0.0f;
-                    const float nx = o + sv * (float)c;
-                    o = sv != 0.0f ? nx : o;       // zero weights are skipped
+                    o = o + sv * (float)c;
                 }
             }
         }
