@@ -702,10 +702,12 @@ OH_HD inline int fd_slots(int cap) {
     const int c = (cap + kFlashCh - 1) / kFlashCh, b = fd_blocks(cap);
     return c > b ? c : b;
 }
-// tiles per block for context T (the blocks holding work: ceil(tiles / tpb))
+// tiles per block for context T (the blocks holding work: ceil(tiles / tpb)):
+// at least one per wave, so the merge has fewer partials at short contexts
 OH_HD inline int fd_tpb(int T, int cap) {
     const int nt = (T + kFdT - 1) / kFdT, B = fd_blocks(cap);
-    return (nt + B - 1) / B;
+    const int t = (nt + B - 1) / B;
+    return t > 4 ? t : 4;
 }
 constexpr int kFdLds = 4 * 64 * 2 * 4 + 4 * 4 * 64 * 16;   // merge: (m, l) and four dim tiles per wave
 
