@@ -146,10 +146,13 @@ def same_state(m, a, b):
                 assert np.array_equal(x.view(np.uint8), y.view(np.uint8)), l
 
 
-@pytest.mark.parametrize("cfg", ["moe", "dense"])
+HD256 = dict(MIX, hd=256, seed=9)     # head_dim 256: the four-token exact prompt walk
+
+
+@pytest.mark.parametrize("cfg", ["moe", "dense", "hd256"])
 @pytest.mark.parametrize("exact_max", [None, 0], ids=["exact", "flash"])
 def test_prefill_equals_token_path(hip_ctx, monkeypatch, cfg, exact_max):
-    m = hip_ctx.synth(**(MIX if cfg == "moe" else DENSE))
+    m = hip_ctx.synth(**{"moe": MIX, "dense": DENSE, "hd256": HD256}[cfg])
     a = m.arch
     rng = np.random.default_rng(3)
     # 300 tokens span four engine chunks of 96; then evals starting at odd and
