@@ -101,6 +101,7 @@ int  ornith_hip_quantize_q8K(ornith_hip_ctx *ctx, const float *x, int64_t k,
 int  ornith_hip_matvec(ornith_hip_ctx *ctx, const ornith_hip_tensor *W,
                        const float *x, float *y, int Tn);
 
+
 /* oq_dequantize of rows [row0, row0+nrows) (src/ornith_quant.h:64-66). */
 /* oq_quantize (src/ornith_quant.h:51-66) on the device: n floats (whole
  * 256-blocks) -> GGUF blocks of Q8_0, Q4_K, Q6_K or IQ2_XXS, byte-identical
@@ -186,6 +187,16 @@ int  ornith_hip_session_get_delta(ornith_hip_session *s, int layer, float *S);
 int  ornith_hip_session_get_conv(ornith_hip_session *s, int layer, float *win);
 int  ornith_hip_session_get_kv(ornith_hip_session *s, int layer, int8_t *Kq,
                                float *Ks, int8_t *Vq, float *Vs);
+/* The attention of the last full-attention layer as the most recent
+ * evaluation left it (a parity hook, no reference twin; the inputs and output
+ * of ornith_gqa_step inside full_attn, src/ornith_rforward.c:419-455,
+ * src/ornith_attn.c:87-149): row < 0, the decode step's; row >= 0, that row of
+ * the most recent prompt chunk. q: query heads after q_norm + RoPE [nh*hd];
+ * gate [nh*hd]; o = attention * sigmoid(gate) [nh*hd], before attn_output's
+ * Q8_K; *pos: the row's position. Needs a model whose last layer is
+ * full attention. */
+int  ornith_hip_session_get_attn(ornith_hip_session *s, int row, float *q, float *gate, float *o,
+                                 int32_t *pos);
 
 /* ---- measurement (no reference twin) -------------------------------------------- */
 

@@ -166,7 +166,16 @@ void orc_gqa_step(orc_kv *c, const float *q, const float *k, const float *v,
         }
     }
     c->len++;
+    orc_gqa_attend(c, q, n_heads, out, scale);
+}
+
+/* the attention half of orc_gqa_step: every head over the c->len cached
+ * positions (src/ornith_attn.c:111-149) */
+void orc_gqa_attend(const orc_kv *c, const float *q, int n_heads, float *out, float scale) {
+    const int hd = c->head_dim, nkv = c->n_kv_heads;
+    if (scale <= 0.0f) scale = 1.0f / sqrtf((float)hd);
     const int T = c->len, group = n_heads / nkv;
+    if (T <= 0) return;
     float *p = malloc((size_t)T * sizeof(float));
     for (int h = 0; h < n_heads; h++) {
         const int kvh = h / group;

@@ -88,6 +88,9 @@ void  orc_kv_free(orc_kv *c);
 float orc_kv_quant_vec(const float *x, int n, int8_t *q);
 void  orc_gqa_step(orc_kv *c, const float *q, const float *k, const float *v,
                    int n_heads, float *out, float scale);
+/* attention over the c->len cached positions without appending (the second
+ * half of orc_gqa_step, src/ornith_attn.c:111-149) */
+void  orc_gqa_attend(const orc_kv *c, const float *q, int n_heads, float *out, float scale);
 void  orc_delta_step(float *S, int dk, int dv, const float *q, const float *k,
                      const float *v, float alpha, float beta, float *o);
 void  orc_delta_prefill(float *S, int dk, int dv, const float *Q,

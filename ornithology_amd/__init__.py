@@ -94,6 +94,7 @@ _SIGS = {
     "ornith_hip_session_get_delta": (C.c_int, [_vp, C.c_int, _fp]),
     "ornith_hip_session_get_conv": (C.c_int, [_vp, C.c_int, _fp]),
     "ornith_hip_session_get_kv": (C.c_int, [_vp, C.c_int, _vp, _fp, _vp, _fp]),
+    "ornith_hip_session_get_attn": (C.c_int, [_vp, C.c_int, _fp, _fp, _fp, _ip]),
     "ornith_hip_session_time_decode": (C.c_int, [_vp, C.c_int, _fp]),
     "ornith_hip_time_matvec": (C.c_int, [_vp, _vp, C.c_int, _fp]),
     "ornith_hip_time_matvec_set": (C.c_int, [_vp, C.POINTER(_vp), C.c_int, C.c_int, _fp]),
@@ -420,6 +421,19 @@ class Session:
         _check(lib().ornith_hip_session_get_kv(self.h, layer, C.c_void_p(kq.ctypes.data), _f32(ks),
                                                C.c_void_p(vq.ctypes.data), _f32(vs)), "ornith_hip_session_get_kv")
         return kq, ks, vq, vs
+
+    def attn(self, row: int = -1):
+        """(q, gate, o, pos) of the last full-attention layer: the decode
+        step's (row < 0) or row `row` of the most recent prompt chunk."""
+        a = self.model.arch
+        n = a["nh"] * a["hd"]
+        q = np.zeros(n, np.float32)
+        g = np.zeros(n, np.float32)
+        o = np.zeros(n, np.float32)
+        p = C.c_int32(0)
+        _check(lib().ornith_hip_session_get_attn(self.h, row, _f32(q), _f32(g), _f32(o), C.byref(p)),
+               "ornith_hip_session_get_attn")
+        return q, g, o, int(p.value)
 
     def free(self):
         if self.h:

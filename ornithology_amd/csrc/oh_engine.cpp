@@ -450,6 +450,13 @@ static bool mmq_enabled() {
     return !(e && e[0] == '0');
 }
 
+// device bytes of matvec_cols' buffer: input, output, Q8_K planes (256-aligned)
+static size_t matvec_col_bytes(int64_t in, int64_t out) {
+    return (size_t)in * 5 + (size_t)(in / 256) * 40 + (size_t)out * 4 + 4096;
+}
+static int matvec_cols(ornith_hip_ctx *ctx, const ornith_hip_tensor *W, const float *x, float *y, int Tn,
+                       void *sp);
+
 extern "C" int ornith_hip_matvec(ornith_hip_ctx *ctx, const ornith_hip_tensor *W,
                                  const float *x, float *y, int Tn) {
     HCHK(hipSetDevice(ctx->device));
@@ -490,7 +497,18 @@ extern "C" int ornith_hip_matvec(ornith_hip_ctx *ctx, const ornith_hip_tensor *W
         HCHK(hipStreamSynchronize(ctx->st));
         return ORNITH_HIP_OK;
     }
-    CHK(ctx_scratch(ctx, (size_t)in * 5 + (size_t)nb * 40 + (size_t)out * 4 + 4096, &sp));
+    CHK(ctx_scratch(ctx, matvec_col_bytes(in, out), &sp));
+    return matvec_cols(ctx, W, x, y, Tn, sp);
+}
+
+// The single-column path of ornith_hip_matvec over a caller-provided device
+// buffer `sp` of at least matvec_col_bytes(in, out) bytes: per column, the
+// input copied in, quantised to Q8_K (integer path), one matvec launch, the
+// output copied out. Allocates nothing.
+static int matvec_cols(ornith_hip_ctx *ctx, const ornith_hip_tensor *W, const float *x, float *y, int Tn,
+                       void *sp) {
+    const int64_t in = W->in, out = W->rows, nb = in / 256;
+    const bool q = oh_qdot_can(W->type, in);
     float *dx = (float *)sp;
     float *dy = (float *)up256((size_t)(dx + in));
     int8_t *qs = (int8_t *)up256((size_t)(dy + out));
@@ -1078,6 +1096,7 @@ struct ornith_hip_session {
     struct Pf {
         int tc = 0;
         int32_t pos_after = 0;
+        int last_base = 0, last_T = 0;   // the most recent chunk (its buffers hold the last layer's rows)
         float *X = nullptr, *CAT = nullptr, *Z = nullptr, *A = nullptr, *Bg = nullptr, *CONV = nullptr;
         float *QN = nullptr, *KN = nullptr, *AL = nullptr, *BE = nullptr, *O = nullptr;
         float *QP = nullptr, *KB = nullptr, *VB = nullptr, *QR = nullptr, *AG = nullptr, *OA = nullptr;
@@ -1974,8 +1993,11 @@ static int session_eval(ornith_hip_session *s, const int32_t *tokens, int n, boo
         // layer-major over chunks of tokens, then the head at the last one
         const int ct = pf_chunk_tokens();
         CHK(pf_alloc(s, n < ct ? n : ct));
-        for (int c0 = 0; c0 < n; c0 += ct)
+        for (int c0 = 0; c0 < n; c0 += ct) {
             CHK(pf_chunk(s, s->pos + c0, n - c0 < ct ? n - c0 : ct, !serial, st));
+            s->pf.last_base = s->pos + c0;
+            s->pf.last_T = n - c0 < ct ? n - c0 : ct;
+        }
         s->pf.pos_after = s->pos + n;   // outlives the asynchronous copy
         HCHK(hipMemcpyAsync(s->io + OH_IO_POS, &s->pf.pos_after, 4, hipMemcpyHostToDevice, st));
     } else {
@@ -2466,6 +2488,42 @@ extern "C" int ornith_hip_session_get_kv(ornith_hip_session *s, int l, int8_t *K
             }
     HCHK(hipMemcpy(Ks, s->ls[l].Ks, (size_t)len * nkv * 4, hipMemcpyDeviceToHost));
     HCHK(hipMemcpy(Vs, s->ls[l].Vs, (size_t)len * nkv * 4, hipMemcpyDeviceToHost));
+    return ORNITH_HIP_OK;
+}
+
+// The last full-attention layer's attention inputs and output as the most
+// recent evaluation left them: row < 0, the decode step's (the query heads
+// after q_norm and RoPE, the output gate, and o = attention * sigmoid(gate)
+// before attn_output's Q8_K, src/ornith_rforward.c:419-455); row >= 0, that
+// row of the most recent prompt chunk. Only meaningful when the model's last
+// layer is a full-attention layer (later linear layers reuse o). *pos: the
+// position the row attended from.
+extern "C" int ornith_hip_session_get_attn(ornith_hip_session *s, int row, float *q, float *gate, float *o,
+                                           int32_t *pos) {
+    const ornith_hip_arch &a = s->m->a;
+    const size_t aq = (size_t)a.nh * a.hd;
+    if (a.n_layers < 1 || !s->m->L[a.n_layers - 1].full) {
+        seterr("get_attn: the last layer is not a full-attention layer");
+        return ORNITH_HIP_ERR_UNSUPPORTED;
+    }
+    HCHK(hipSetDevice(s->m->ctx->device));
+    HCHK(hipStreamSynchronize(s->m->ctx->st));
+    const float *dq, *dg, *dout;
+    if (row < 0) {
+        if (s->pos < 1) { seterr("get_attn: no decode step yet"); return ORNITH_HIP_ERR_UNSUPPORTED; }
+        dq = s->qr; dg = s->agate; dout = s->o;
+        *pos = s->pos - 1;
+    } else {
+        if (row >= s->pf.last_T || !s->pf.QR) {
+            seterr("get_attn: row %d outside the last prompt chunk (%d rows)", row, s->pf.last_T);
+            return ORNITH_HIP_ERR_FORMAT;
+        }
+        dq = s->pf.QR + (size_t)row * aq; dg = s->pf.AG + (size_t)row * aq; dout = s->pf.OA + (size_t)row * aq;
+        *pos = s->pf.last_base + row;
+    }
+    HCHK(hipMemcpy(q, dq, aq * 4, hipMemcpyDeviceToHost));
+    HCHK(hipMemcpy(gate, dg, aq * 4, hipMemcpyDeviceToHost));
+    HCHK(hipMemcpy(o, dout, aq * 4, hipMemcpyDeviceToHost));
     return ORNITH_HIP_OK;
 }
 

@@ -127,6 +127,7 @@ def oracle():
         "orc_kv_free": (None, [C.POINTER(OrcKV)]),
         "orc_kv_quant_vec": (C.c_float, [fp, C.c_int, vp]),
         "orc_gqa_step": (None, [C.POINTER(OrcKV), fp, fp, fp, C.c_int, fp, C.c_float]),
+        "orc_gqa_attend": (None, [C.POINTER(OrcKV), fp, C.c_int, fp, C.c_float]),
         "orc_delta_step": (None, [fp, C.c_int, C.c_int, fp, fp, fp, C.c_float, C.c_float, fp]),
         "orc_delta_prefill": (None, [fp, C.c_int, C.c_int, fp, fp, fp, fp, fp, C.c_int, C.c_int, fp]),
         "orc_conv_step": (None, [fp, C.c_int, C.c_int, fp, fp, fp, fp]),
