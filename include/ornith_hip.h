@@ -101,6 +101,16 @@ int  ornith_hip_quantize_q8K(ornith_hip_ctx *ctx, const float *x, int64_t k,
 int  ornith_hip_matvec(ornith_hip_ctx *ctx, const ornith_hip_tensor *W,
                        const float *x, float *y, int Tn);
 
+/* No counterpart in the reference. ornith_hip_matvec for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc): the same results, computed one column at
+ * a time in a fixed 4 MiB device array per GPU (resolved by ornith_hip_init)
+ * instead of a buffer the library allocates. Limit: in*5 + (in/256)*40 +
+ * out*4 + 4096 <= 4 MiB (e.g. out <= 1,040,000 rows at in = 2048); larger
+ * tensors return ORNITH_HIP_ERR_UNSUPPORTED. Calls that overlap on one GPU
+ * share the array and race: serialise them. */
+int  ornith_hip_matvec_noalloc(ornith_hip_ctx *ctx, const ornith_hip_tensor *W,
+                               const float *x, float *y, int Tn);
 
 /* oq_dequantize of rows [row0, row0+nrows) (src/ornith_quant.h:64-66). */
 /* oq_quantize (src/ornith_quant.h:51-66) on the device: n floats (whole

@@ -69,6 +69,7 @@ _SIGS = {
     "ornith_hip_tensor_download": (C.c_int, [_vp, _vp, C.c_uint64]),
     "ornith_hip_quantize_q8K": (C.c_int, [_vp, _fp, C.c_int64, _vp]),
     "ornith_hip_matvec": (C.c_int, [_vp, _vp, _fp, _fp, C.c_int]),
+    "ornith_hip_matvec_noalloc": (C.c_int, [_vp, _vp, _fp, _fp, C.c_int]),
     "ornith_hip_dequant": (C.c_int, [_vp, _vp, C.c_int64, C.c_int64, _fp]),
     "ornith_hip_moe_route": (C.c_int, [_vp, _fp, C.c_int, C.c_int, _ip, _fp]),
     "ornith_hip_model_load": (C.c_int, [_vp, C.c_char_p, C.POINTER(_vp)]),
@@ -232,6 +233,16 @@ class Tensor:
         tn = x.size // self.cols
         y = np.zeros(tn * self.rows, np.float32)
         _check(lib().ornith_hip_matvec(self.ctx.h, self.h, _f32(x), _f32(y), tn), "ornith_hip_matvec")
+        return y
+
+    def matvec_noalloc(self, x: np.ndarray) -> np.ndarray:
+        """matvec through the entry point that allocates nothing (the fixed
+        per-device scratch array; results equal matvec's)."""
+        x = np.ascontiguousarray(x, np.float32)
+        tn = x.size // self.cols
+        y = np.zeros(tn * self.rows, np.float32)
+        _check(lib().ornith_hip_matvec_noalloc(self.ctx.h, self.h, _f32(x), _f32(y), tn),
+               "ornith_hip_matvec_noalloc")
         return y
 
     def dequant(self, row0: int = 0, nrows: int | None = None) -> np.ndarray:

@@ -13,6 +13,7 @@
 #include <cstdlib>
 #include <algorithm>
 #include <atomic>
+#include <mutex>
 #include <cstring>
 #include <string>
 #include <unordered_map>
@@ -71,6 +72,31 @@ static int ctx_scratch(ornith_hip_ctx *c, size_t bytes, void **out) {
     return ORNITH_HIP_OK;
 }
 
+// ---- the no-allocation matvec's scratch --------------------------------------------
+// ornith_hip_matvec_noalloc stages its input, output and Q8_K planes in this
+// fixed device array instead of allocating. Each device holds its own copy
+// until the process ends. In host code `scratch` only names the symbol:
+// kernels and copies get the device address that hipGetSymbolAddress returns
+// for the current device, resolved once per device by ornith_hip_init.
+#define OH_NOALLOC_SCRATCH_BYTES (4u << 20)
+static __device__ __align__(256) uint8_t scratch[OH_NOALLOC_SCRATCH_BYTES];
+#define OH_MAX_DEVICES 64
+static void *g_scratch_dev[OH_MAX_DEVICES];
+static std::mutex g_scratch_mu;
+
+static int noalloc_setup(int device) {
+    if (device < 0 || device >= OH_MAX_DEVICES) {
+        seterr("ornith_hip_init: device %d beyond the %d the library tracks", device, OH_MAX_DEVICES);
+        return ORNITH_HIP_ERR_UNSUPPORTED;
+    }
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (g_scratch_dev[device]) return ORNITH_HIP_OK;
+    void *p = nullptr;
+    HCHK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));   // the current device's copy
+    g_scratch_dev[device] = p;
+    return ORNITH_HIP_OK;
+}
+
 extern "C" int ornith_hip_init(int device, ornith_hip_ctx **out) {
     *out = nullptr;
     int n = 0;
@@ -87,6 +113,12 @@ extern "C" int ornith_hip_init(int device, ornith_hip_ctx **out) {
         delete c;
         seterr("hipStreamCreate: %s", hipGetErrorString(e));
         return ORNITH_HIP_ERR_DEVICE;
+    }
+    const int r = noalloc_setup(device);
+    if (r != ORNITH_HIP_OK) {
+        (void)hipStreamDestroy(c->st);
+        delete c;
+        return r;
     }
     *out = c;
     return ORNITH_HIP_OK;
@@ -533,6 +565,32 @@ static int matvec_cols(ornith_hip_ctx *ctx, const ornith_hip_tensor *W, const fl
     }
     HCHK(hipStreamSynchronize(ctx->st));
     return ORNITH_HIP_OK;
+}
+
+// ornith_hip_matvec without any allocation: the single-column path over the
+// device's fixed scratch array (results equal ornith_hip_matvec's; every
+// column is its own launch sequence). Calls that overlap on one device share
+// the array and race; the caller serialises them.
+extern "C" int ornith_hip_matvec_noalloc(ornith_hip_ctx *ctx, const ornith_hip_tensor *W,
+                                         const float *x, float *y, int Tn) {
+    if (!ctx || !W || (Tn > 0 && (!x || !y))) {
+        seterr("matvec_noalloc: null context, tensor or buffer");
+        return ORNITH_HIP_ERR_FORMAT;
+    }
+    if (Tn <= 0) return ORNITH_HIP_OK;
+    const size_t need = matvec_col_bytes(W->in, W->rows);
+    if (need > OH_NOALLOC_SCRATCH_BYTES) {
+        seterr("matvec_noalloc: '%s' (%lld x %lld) needs %zu scratch bytes, above the fixed %u",
+               W->name.c_str(), (long long)W->in, (long long)W->rows, need, OH_NOALLOC_SCRATCH_BYTES);
+        return ORNITH_HIP_ERR_UNSUPPORTED;
+    }
+    void *sp = ctx->device >= 0 && ctx->device < OH_MAX_DEVICES ? g_scratch_dev[ctx->device] : nullptr;
+    if (!sp) {
+        seterr("matvec_noalloc: device %d has no scratch address (context not from ornith_hip_init)", ctx->device);
+        return ORNITH_HIP_ERR_DEVICE;
+    }
+    HCHK(hipSetDevice(ctx->device));
+    return matvec_cols(ctx, W, x, y, Tn, sp);
 }
 
 // oq_quantize on the device: n floats (whole super-blocks) -> GGUF blocks of
