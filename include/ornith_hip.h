@@ -243,6 +243,19 @@ int  ornith_hip_session_time_kind(ornith_hip_session *s, int kind, int reps, flo
  * algorithmic bytes and us from the previous barrier to its own. */
 int  ornith_hip_session_profile_phases(ornith_hip_session *s, int max_phases, int32_t *kinds,
                                        double *bytes, float *us, int *n_phases);
+/* Measurement (no reference twin): one run of the decode step as a single
+ * persistent launch with clocks, not advancing the session: per operation
+ * its kind (0 embed, 1 matvec, 2 delta-net, 3 GQA prep, 4 attention,
+ * 5 attention merge, 6 MoE down, 7 greedy token) and the earliest / latest
+ * time a workgroup was done with it, in microseconds from the launch's start.
+ * ORNITH_HIP_ERR_UNSUPPORTED when the model has no such launch. */
+int  ornith_hip_session_profile_decode(ornith_hip_session *s, int max_ops, int32_t *kinds,
+                                       float *us_first, float *us_last, int *n_ops);
+/* Measurement: the sub-phase clocks of operation `op` of that launch, 8 per
+ * workgroup (start, weights requested, inputs arrived, activation arrived,
+ * prologue done, done; -1 where not recorded), microseconds from the start. */
+int  ornith_hip_session_profile_decode_op(ornith_hip_session *s, int op, float *us, int max_groups,
+                                          int *grid_out);
 /* Time `iters` launches of one matvec of W (activation already quantised on
  * the device) with HIP events on the context stream; *ms = mean per launch. */
 int  ornith_hip_time_matvec(ornith_hip_ctx *ctx, const ornith_hip_tensor *W, int iters,

@@ -102,6 +102,8 @@ _SIGS = {
     "ornith_hip_session_profile_step": (C.c_int, [_vp, C.c_int, _ip, C.POINTER(C.c_double), _fp, _ip]),
     "ornith_hip_session_time_kind": (C.c_int, [_vp, C.c_int, C.c_int, _fp, C.POINTER(C.c_double), _ip]),
     "ornith_hip_session_profile_phases": (C.c_int, [_vp, C.c_int, _ip, C.POINTER(C.c_double), _fp, _ip]),
+    "ornith_hip_session_profile_decode": (C.c_int, [_vp, C.c_int, _ip, _fp, _fp, _ip]),
+    "ornith_hip_session_profile_decode_op": (C.c_int, [_vp, C.c_int, _fp, C.c_int, _ip]),
 }
 
 _lib = None
@@ -394,6 +396,27 @@ class Session:
                                                      C.byref(n)), "ornith_hip_session_profile_step")
         k = n.value
         return [(self.KERNEL_KINDS[kinds[i]], float(byts[i]), float(ms[i])) for i in range(k)]
+
+    DECODE_OPS = ("embed", "matvec", "delta", "attn_prep", "attn", "attn_merge", "moe_down", "argmax")
+
+    def profile_decode(self, max_ops: int = 4096):
+        """[(kind, first_done_us, last_done_us)] per operation of one run of the
+        decode step as a single persistent launch (the position is not advanced)."""
+        kinds = np.zeros(max_ops, np.int32)
+        a = np.zeros(max_ops, np.float32)
+        b = np.zeros(max_ops, np.float32)
+        n = C.c_int(0)
+        _check(lib().ornith_hip_session_profile_decode(self.h, max_ops, _i32(kinds), _f32(a), _f32(b), C.byref(n)),
+               "ornith_hip_session_profile_decode")
+        return [(self.DECODE_OPS[kinds[i]], float(a[i]), float(b[i])) for i in range(n.value)]
+
+    def profile_decode_op(self, op: int, max_groups: int = 1024) -> np.ndarray:
+        """[groups, 8] sub-phase clocks (us) of operation `op` of the decode launch"""
+        us = np.zeros(max_groups * 8, np.float32)
+        g = C.c_int(0)
+        _check(lib().ornith_hip_session_profile_decode_op(self.h, op, _f32(us), max_groups, C.byref(g)),
+               "ornith_hip_session_profile_decode_op")
+        return us[:g.value * 8].reshape(g.value, 8)
 
     def profile_phases(self, max_phases: int = 4096):
         """One step-kernel body launch at the current position (the position

@@ -37,7 +37,9 @@ __constant__ uint64_t k_exp2_tab[32] = {
     0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull,
 };
 
-OH_DEV float ref_expf(float x) {
+// tab: the 32 table entries (k_exp2_tab, or a copy of it in LDS)
+template <typename TabT>
+OH_DEV float ref_expf_tab(float x, const TabT *tab) {
     const uint32_t ax = f2u(x) & 0x7fffffffu;
     if (ax >= 0x42b00000u) {                       // |x| >= 88
         if (f2u(x) == 0xff800000u) return 0.0f;    // -inf
@@ -56,7 +58,7 @@ OH_DEV float ref_expf(float x) {
     const uint64_t ki = (uint64_t)__double_as_longlong(kd);
     kd -= shift;
     const double r = fma(inv_ln2_n, xd, -kd);
-    uint64_t t = k_exp2_tab[ki % 32];
+    uint64_t t = tab[ki % 32];
     t += ki << 47;
     const double s = __longlong_as_double((long long)t);
     const double p = fma(c0, r, c1);
@@ -66,6 +68,7 @@ OH_DEV float ref_expf(float x) {
     y = y * s;
     return (float)y;
 }
+OH_DEV float ref_expf(float x) { return ref_expf_tab(x, k_exp2_tab); }
 
 // ---- glibc-compatible log1pf ------------------------------------------------
 // fdlibm s_log1pf.c (Sun Microsystems, freely redistributable), the

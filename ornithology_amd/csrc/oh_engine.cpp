@@ -1184,6 +1184,18 @@ struct ornith_hip_session {
         std::vector<uint64_t> key;
     } bw;
     std::vector<int> sp_body_rk;
+    // the decode step as one persistent launch (oh_k_decode): its program in
+    // device memory, grid (0: not available for this model), LDS and bytes
+    struct DecProg {
+        oh_dop *ops = nullptr;
+        int n = 0, lds = 0, grid = 0;
+        double bytes = 0.0;
+        std::vector<int> kinds;          // per operation: OH_D_* kind
+        std::vector<double> obytes;      // per operation: algorithmic bytes
+        uint64_t *ts = nullptr;          // profiling clocks
+    };
+    DecProg dec;
+    bool dec_tried = false;
     int step_grid = 0;
     bool step_tried = false;
     uint64_t *ts = nullptr;
@@ -1699,12 +1711,323 @@ static int step_check(ornith_hip_session *s) {
     int32_t err = 0;
     HCHK(hipMemcpy(&err, s->io + OH_IO_ERR, 4, hipMemcpyDeviceToHost));
     if (err) {
-        seterr("step kernel: a grid barrier timed out; the session state is undefined");
+        seterr("decode step: a wait between workgroups timed out; the session state is undefined");
         return ORNITH_HIP_ERR_DEVICE;
     }
     return ORNITH_HIP_OK;
 }
 
+
+// ---- the decode step as one persistent launch (oh_decode.hip) -------------------------------
+// Opt-in (ORNITH_HIP_DECODE=1): on C3 it measures 3.2 ms per token against
+// the per-launch HIP-graph step's 2.7 ms, so the graph step stays the default.
+// The program covers models whose every projection has the integer dot
+// (Q4_K / Q6_K / Q8_0, inputs <= 8192), MoE FFNs with paired gate/up and a
+// down projection of one type (shared expert included), delta-net head dims
+// 64 / 128 with conv kernels <= 8; other models keep the per-launch step.
+static bool dec_enabled() {
+    const char *e = getenv("ORNITH_HIP_DECODE");
+    return e && e[0] == '1';
+}
+
+struct DecB {
+    std::vector<oh_dop> ops;
+    std::vector<double> obytes;   // per operation (filled by dec_note)
+    uint64_t *base = nullptr;   // word arena (a dummy base while sizing)
+    size_t used = 0;            // words
+    int G = 0, lds = 0;
+    double bytes = 0.0;
+    uint64_t *alloc(size_t n) {
+        uint64_t *p = base + used;
+        used += (n + 31) & ~(size_t)31;
+        return p;
+    }
+};
+
+static bool dq(const ornith_hip_tensor *W) { return W && oh_qdot_can(W->type, W->in) && W->in <= 8192; }
+
+static oh_dmv dmv_new(const uint64_t *x, const float *nw, int pro, int in, float eps) {
+    oh_dmv M;
+    memset(&M, 0, sizeof M);
+    M.x = x; M.nw = nw; M.pro = pro; M.in = in; M.nb = in / 256; M.eps = eps;
+    return M;
+}
+// one segment: W (and W2, paired) applied in nsub slots (stacked: slot k is
+// the routed expert k); output slot k row r at y[k * ystride + r]
+static void dmv_seg(oh_dmv &M, const ornith_hip_tensor *W, const ornith_hip_tensor *W2, uint64_t *y, int nsub,
+                    int ystride, int stacked, int mode, float *yp = nullptr) {
+    oh_dseg &g = M.s[M.nseg++];
+    memset(&g, 0, sizeof g);
+    g.A = W->A; g.B = W->B; g.C = W->C;
+    if (W2) { g.A2 = W2->A; g.B2 = W2->B; g.C2 = W2->C; g.pair = 1; }
+    g.y = y; g.yp = yp; g.type = (int)W->type;
+    g.rows = stacked ? (int)W->dims[1] : (int)W->rows;
+    g.nsub = nsub; g.ystride = ystride; g.stacked = stacked; g.mode = mode;
+    const int rps = 64 / M.nb;
+    g.units = (g.rows + rps - 1) / rps;
+    g.step0 = M.nsteps;
+    M.nsteps += g.units * nsub;
+}
+// The decode launch's matvec (a front wave polling the inputs, three
+// stepping waves per workgroup) exists for these (type, super-blocks per
+// input) pairs; mode-1 output only in one segment; routing over <= 1024.
+static bool dmv_ok(const oh_dmv &M) {
+    const int t = M.s[0].type, nb = M.nb;
+    const bool shape = t == OH_Q4_K ? (nb == 2 || nb == 4 || nb == 8 || nb == 16)
+                     : t == OH_Q6_K ? (nb == 4 || nb == 8 || nb == 16) : (nb == 2 || nb == 4 || nb == 8);
+    for (int i = 0; i < M.nseg; i++)
+        if (M.s[i].type != t || (M.s[i].mode == 1 && M.nseg != 1)) return false;
+    return shape && M.ne <= 1024;
+}
+// deal the steps to `waves` of the grid's 4 G waves from wave0 on, counted
+// as the three stepping waves per workgroup; dynamic LDS of the operation
+static bool dmv_add(DecB &b, oh_dmv &M, int wave0, int waves, double bytes) {
+    if (!dmv_ok(M)) return false;
+    M.wspec = 1;
+    wave0 = (int)((long long)wave0 * 3 / 4);
+    waves = (int)((long long)waves * 3 / 4);
+    M.wave0 = wave0;
+    M.spw = (M.nsteps + waves - 1) / waves;
+    if (M.spw < 1) M.spw = 1;
+    // residual rows of a workgroup's steps: at most 1024 words
+    if (M.s[0].mode == 1 && 3 * M.spw * (64 / M.nb) > 1024) return false;
+    const int l = ((M.nb * 272 + M.nb * 36 + 15) & ~15) + (M.in + 1024 + ((M.ne + 3) & ~3)) * 4;
+    if (l > b.lds) b.lds = l;
+    oh_dop o;
+    memset(&o, 0, sizeof o);
+    o.kind = OH_D_MV;
+    o.nvb = b.G;
+    o.u.mv = M;
+    b.ops.push_back(o);
+    b.bytes += bytes;
+    return true;
+}
+static double wbytes(const ornith_hip_tensor *W, int rows) { return (double)rows * gguf_nbytes(W->type, (uint64_t)W->in); }
+
+// Build the program; false (with nothing built) when the model is outside it.
+static bool dec_build(ornith_hip_session *s, DecB &b) {
+    const ornith_hip_model *m = s->m;
+    const ornith_hip_arch &a = m->a;
+    const int H = a.hidden, qd = a.nk * a.dk, vd = a.nv * a.dv, cc = 2 * qd + vd, aq = a.nh * a.hd;
+    const int kvd = a.nkv * a.hd, G = b.G, W4 = 4 * G;
+    const double T = (double)(s->pos + 1);
+    if (H % 256 || H > 8192 || !dq(m->lm_head) || a.ne <= 0 || a.top_k > 64 || a.ne > 1024) return false;
+    if (m->embd->type != OH_F32 && m->embd->type != OH_F16 && m->embd->type != OH_BF16 && !oh_is_quant(m->embd->type))
+        return false;
+    uint64_t *x = b.alloc(H);
+    {
+        oh_dop o;
+        memset(&o, 0, sizeof o);
+        o.kind = OH_D_EMBED;
+        o.nvb = (H + 255) / 256;
+        o.u.emb = {m->embd->A, m->embd->B, m->embd->C, s->toks, x, (int)m->embd->type, H};
+        b.ops.push_back(o);
+        b.bytes += (double)gguf_nbytes(m->embd->type, (uint64_t)H);
+    }
+    for (int l = 0; l < a.n_layers; l++) {
+        const OhLayer &y = m->L[l];
+        LayerState &z = s->ls[l];
+        uint64_t *xmid = b.alloc(H);
+        if (y.full) {
+            if (!dq(y.q) || !dq(y.k) || !dq(y.v) || !dq(y.o) || y.k->type != y.q->type) return false;
+            if (a.hd > 256 || 256 % a.hd || a.nh + a.nkv > 4096) return false;
+            uint64_t *qkv = b.alloc(2 * (size_t)aq + 2 * (size_t)kvd);
+            oh_dmv M = dmv_new(x, (const float *)y.attn_norm->A, OH_PRO_NORM, H, a.eps);
+            dmv_seg(M, y.q, nullptr, qkv, 1, 0, 0, 0);
+            dmv_seg(M, y.k, nullptr, qkv + 2 * aq, 1, 0, 0, 0);
+            const double qb = wbytes(y.q, 2 * aq) + wbytes(y.k, kvd);
+            if (y.v->type == y.q->type) {
+                dmv_seg(M, y.v, nullptr, qkv + 2 * aq + kvd, 1, 0, 0, 0);
+                if (!dmv_add(b, M, 0, W4, qb + wbytes(y.v, kvd))) return false;
+            } else {
+                // v in its own operation on the last waves, q/k on the others
+                oh_dmv V = dmv_new(x, (const float *)y.attn_norm->A, OH_PRO_NORM, H, a.eps);
+                dmv_seg(V, y.v, nullptr, qkv + 2 * aq + kvd, 1, 0, 0, 0);
+                int vw = (int)((double)W4 * V.nsteps / (V.nsteps + M.nsteps));
+                vw = vw < 4 ? 4 : (vw > W4 - 4 ? W4 - 4 : vw);
+                vw = (vw + 3) & ~3;
+                if (!dmv_add(b, V, W4 - vw, vw, wbytes(y.v, kvd))) return false;
+                if (!dmv_add(b, M, 0, W4 - vw, qb)) return false;
+            }
+            // prep (q/k norm, RoPE, KV append) -> attention -> merge
+            uint64_t *pflags = b.alloc(a.nh + a.nkv);
+            const int lim = s->exact_max < 2048 ? s->exact_max : 2048;
+            oh_op_attn at;
+            memset(&at, 0, sizeof at);
+            at.qr = s->qr; at.gate = s->agate; at.Kt = z.Kt; at.Ks = z.Ks; at.Vq = z.Vq; at.Vs = z.Vs;
+            at.scores = s->scores; at.part_o = s->fpo; at.part_ml = s->fpml; at.out = s->o;
+            at.nh = a.nh; at.nkv = a.nkv; at.hd = a.hd; at.cap = s->kvcap; at.exact_max = s->exact_max;
+            at.hb = oh_flash_form(a.nh, a.nkv, a.hd, s->flash_mfma); at.scale = 1.0f / sqrtf((float)a.hd);
+            const int nv_ex = a.nh / (256 / a.hd), nv_fl = oh_flash_nvb(a.nh, a.nkv, s->kvcap, at.hb);
+            const int nva = nv_ex > nv_fl ? nv_ex : nv_fl, ncb = a.nh * (a.hd / 64);
+            uint64_t *aflags = b.alloc(nva + ncb), *cflags = aflags + nva;
+            oh_dop o;
+            memset(&o, 0, sizeof o);
+            o.kind = OH_D_PREP;
+            o.nvb = a.nh + a.nkv;
+            o.u.at.p = {nullptr, nullptr, nullptr, (const float *)y.q_norm->A, (const float *)y.k_norm->A,
+                        (const float *)s->rope, s->qr, s->agate, z.Kt, z.Ks, z.Vq, z.Vs,
+                        a.nh, a.nkv, a.hd, a.rope_dim, s->kvcap, a.eps};
+            o.u.at.qkv = qkv;
+            o.u.at.flags = pflags;
+            b.ops.push_back(o);
+            o.kind = OH_D_ATTN;
+            o.nvb = nva;
+            o.u.at.a = at;
+            o.u.at.wflags = pflags;
+            o.u.at.nwait_ex = o.u.at.nwait_fl = a.nh + a.nkv;
+            o.u.at.flags = aflags;
+            o.u.at.lim = lim;
+            b.ops.push_back(o);
+            const int lds_ex = oh_exact_lds_bytes(a.hd, s->exact_max), lds_fl = oh_flash_form_lds(a.nh, a.nkv, a.hd, at.hb);
+            if (lds_ex > b.lds) b.lds = lds_ex;
+            if (lds_fl > b.lds) b.lds = lds_fl;
+            const double nch = oh_flash_parts((int)T, s->kvcap, at.hb);
+            b.bytes += T * a.nkv * (2.0 * a.hd + 8.0);
+            o.kind = OH_D_COMBINE;
+            o.nvb = ncb;
+            o.u.at.wflags = aflags;
+            o.u.at.nwait_fl = nva;
+            o.u.at.flags = cflags;
+            b.ops.push_back(o);
+            (void)nch;
+            // attn_output, x += (plain input behind the attention's flags)
+            oh_dmv O = dmv_new(nullptr, nullptr, OH_PRO_F32, aq, a.eps);
+            O.xp = s->o;
+            O.xflags = aflags;
+            O.nflags_ex = nva;
+            O.nflags_fl = nva + ncb;
+            O.exact_lim = lim;
+            O.xres = x;
+            dmv_seg(O, y.o, nullptr, xmid, 1, 0, 0, 1);
+            if (O.s[0].units > 2 * 3 * G) return false;
+            if (!dmv_add(b, O, 0, W4, wbytes(y.o, H))) return false;
+        } else {
+            if (!dq(y.qkv) || !dq(y.gate) || !dq(y.alpha) || !dq(y.beta) || !dq(y.ssm_out)) return false;
+            if (y.gate->type != y.qkv->type || y.alpha->type != y.qkv->type || y.beta->type != y.qkv->type) return false;
+            if ((a.dk != 64 && a.dk != 128) || a.dv != a.dk || a.conv_k < 2 || a.conv_k > 8) return false;
+            if (y.conv->type != OH_F32 || y.ssm_norm->type != OH_F32) return false;
+            uint64_t *cat = b.alloc(cc), *zz = b.alloc(vd), *ab = b.alloc(2 * (size_t)a.nv), *o = b.alloc(vd);
+            oh_dmv M = dmv_new(x, (const float *)y.attn_norm->A, OH_PRO_NORM, H, a.eps);
+            dmv_seg(M, y.qkv, nullptr, cat, 1, 0, 0, 0);
+            dmv_seg(M, y.gate, nullptr, zz, 1, 0, 0, 0);
+            dmv_seg(M, y.alpha, nullptr, ab, 1, 0, 0, 0);
+            dmv_seg(M, y.beta, nullptr, ab + a.nv, 1, 0, 0, 0);
+            if (!dmv_add(b, M, 0, W4, wbytes(y.qkv, cc) + wbytes(y.gate, vd) + wbytes(y.alpha, a.nv) + wbytes(y.beta, a.nv))) return false;
+            oh_dop d;
+            memset(&d, 0, sizeof d);
+            d.kind = OH_D_DELTA;
+            d.nvb = a.nv;
+            d.u.dl = {cat, ab, zz, (const float *)y.conv->A, (const float *)y.ssm_a->A, (const float *)y.dt_bias->A,
+                      (const float *)y.ssm_norm->A, z.conv, z.S, o, a.dk, a.nk, a.nv, a.conv_k, cc,
+                      1.0f / sqrtf((float)a.dk), a.eps};
+            b.ops.push_back(d);
+            const int dl = (4 * a.dk + 4 + (a.dk / 64) * 64 * (a.dk + 4)) * 4 + 8 * 8;
+            if (dl > b.lds) b.lds = dl;
+            b.bytes += 8.0 * a.nv * a.dk * a.dv + 8.0 * (a.conv_k - 1) * cc;
+            oh_dmv O = dmv_new(o, nullptr, OH_PRO_F32, vd, a.eps);
+            O.xres = x;
+            dmv_seg(O, y.ssm_out, nullptr, xmid, 1, 0, 0, 1);
+            if (O.s[0].units > 2 * 3 * G) return false;
+            if (!dmv_add(b, O, 0, W4, wbytes(y.ssm_out, H))) return false;
+        }
+        // MoE FFN: router (+ shared gate), experts gate/up, down + combine
+        const int K = a.top_k, I = a.moe_inter;
+        if (!dq(y.router) || !dq(y.gate_exps) || !pairable(y.gate_exps, y.up_exps) || !y.down_exps ||
+            !oh_qdot_can(y.down_exps->type, I) || I % 256 || I / 256 > 64 || y.gate_exps->type != y.router->type)
+            return false;
+        const bool sh = y.gate_sh != nullptr;
+        if (sh && (!pairable(y.gate_sh, y.up_sh) || y.gate_sh->type != y.gate_exps->type || a.shared_inter != I ||
+                   !y.down_sh || y.down_sh->type != y.down_exps->type))
+            return false;
+        if (y.gate_inp_sh && (!dq(y.gate_inp_sh) || y.gate_inp_sh->type != y.router->type)) return false;
+        uint64_t *rl = b.alloc(a.ne + 1), *shl = y.gate_inp_sh ? rl + a.ne : nullptr;
+        oh_dmv R = dmv_new(xmid, (const float *)y.post_norm->A, OH_PRO_NORM, H, a.eps);
+        dmv_seg(R, y.router, nullptr, rl, 1, 0, 0, 0);
+        if (y.gate_inp_sh) dmv_seg(R, y.gate_inp_sh, nullptr, shl, 1, 0, 0, 0);
+        if (!dmv_add(b, R, 0, W4, wbytes(y.router, a.ne) + (y.gate_inp_sh ? wbytes(y.gate_inp_sh, 1) : 0.0))) return false;
+        const int ns = K + (sh ? 1 : 0);
+        uint64_t *h = b.alloc((size_t)ns * I), *xout = b.alloc(H);
+        oh_dmv E = dmv_new(xmid, (const float *)y.post_norm->A, OH_PRO_NORM, H, a.eps);
+        E.route = 1; E.rlog = rl; E.shl = shl; E.ne = a.ne; E.topk = K;
+        dmv_seg(E, y.gate_exps, y.up_exps, h, K, I, 1, 0);
+        if (sh) dmv_seg(E, y.gate_sh, y.up_sh, h + (size_t)K * I, 1, 0, 0, 0);
+        if (!dmv_add(b, E, 0, W4, (double)ns * 2.0 * (double)I * gguf_nbytes(y.gate_exps->type, (uint64_t)H))) return false;
+        oh_dop dn;
+        memset(&dn, 0, sizeof dn);
+        dn.kind = OH_D_DOWN;
+        const int rpb = (H + G - 1) / G, nbd = I / 256;
+        // a (row, slot)'s super-blocks sit in consecutive lanes of one wave;
+        // at most 4 units per stepping thread, 64 rows per workgroup
+        if (rpb * ns * nbd > 768 || 64 % nbd || rpb > 64) return false;
+        dn.nvb = (H + rpb - 1) / rpb;
+        dn.u.dn.A = y.down_exps->A; dn.u.dn.B = y.down_exps->B; dn.u.dn.C = y.down_exps->C;
+        if (sh) { dn.u.dn.sA = y.down_sh->A; dn.u.dn.sB = y.down_sh->B; dn.u.dn.sC = y.down_sh->C; }
+        dn.u.dn.h = h; dn.u.dn.rlog = rl; dn.u.dn.shl = shl; dn.u.dn.xres = xmid; dn.u.dn.y = xout;
+        dn.u.dn.type = (int)y.down_exps->type; dn.u.dn.nb = nbd; dn.u.dn.in = I; dn.u.dn.rows = H;
+        dn.u.dn.k = K; dn.u.dn.ne = a.ne; dn.u.dn.rpb = rpb;
+        b.ops.push_back(dn);
+        const int sq = (nbd * 272 + nbd * 36 + 15) & ~15;
+        const int ld = ns * sq + ns * I * 4 + 64 * ns * 4 + ((a.ne + 3) & ~3) * 4;
+        if (ld > b.lds) b.lds = ld;
+        b.bytes += (double)ns * (double)H * gguf_nbytes(y.down_exps->type, (uint64_t)I);
+        x = xout;
+    }
+    // head: output norm, lm_head (plain logits + per-workgroup argmax), greedy token
+    uint64_t *amax = b.alloc(2 * (size_t)G);
+    oh_dmv Hm = dmv_new(x, (const float *)m->out_norm->A, OH_PRO_NORM, H, a.eps);
+    dmv_seg(Hm, m->lm_head, nullptr, nullptr, 1, 0, 0, 0, s->logits);
+    Hm.amax = amax;
+    if (!dmv_add(b, Hm, 0, W4, wbytes(m->lm_head, a.vocab))) return false;
+    oh_dop am;
+    memset(&am, 0, sizeof am);
+    am.kind = OH_D_ARGMAX;
+    am.nvb = 1;
+    am.u.am = {amax, G, a.vocab, s->toks};
+    b.ops.push_back(am);
+    return true;
+}
+
+// Size, allocate and upload the program once per session (its contents do
+// not depend on the position). Leaves dec.grid = 0 when the model or the
+// device cannot run it.
+static int dec_prepare(ornith_hip_session *s) {
+    if (s->dec_tried) return ORNITH_HIP_OK;
+    s->dec_tried = true;
+    const int dev = s->m->ctx->device;
+    int coop = 0, cus = 0;
+    HCHK(hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev));
+    HCHK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+    if (!coop || cus <= 0) return ORNITH_HIP_OK;
+    DecB sz;
+    sz.G = cus;
+    uint64_t dummy[1];
+    sz.base = dummy;
+    if (!dec_build(s, sz)) return ORNITH_HIP_OK;
+    int fit = 0;
+    HCHK(oh_decode_blocks_per_cu(sz.lds, &fit));
+    if (fit < 1) return ORNITH_HIP_OK;
+    DecB b;
+    b.G = cus;
+    CHK(salloc(s, &b.base, sz.used + 64));          // zeroed: tag 0 is never a live tag
+    if (!dec_build(s, b)) return ORNITH_HIP_OK;
+    CHK(salloc(s, &s->dec.ops, b.ops.size()));
+    HCHK(hipMemcpy(s->dec.ops, b.ops.data(), b.ops.size() * sizeof(oh_dop), hipMemcpyHostToDevice));
+    const int32_t one = 1;
+    HCHK(hipMemcpy(s->io + OH_IO_TAG, &one, 4, hipMemcpyHostToDevice));
+    s->dec.n = (int)b.ops.size();
+    s->dec.kinds.clear();
+    for (const oh_dop &o : b.ops) s->dec.kinds.push_back(o.kind);
+    s->dec.lds = b.lds;
+    s->dec.bytes = b.bytes;
+    s->dec.grid = cus;
+    return ORNITH_HIP_OK;
+}
+
+static int dec_launch(ornith_hip_session *s, bool advance = true) {
+    HCHK(oh_launch_decode(s->dec.ops, s->dec.n, s->io, advance ? 1 : 0, s->dec.grid, s->dec.lds, s->m->ctx->st));
+    return ORNITH_HIP_OK;
+}
 
 
 static int capture(ornith_hip_session *s, int (*fn)(ornith_hip_session *, hipStream_t), hipGraphExec_t *out) {
@@ -1751,6 +2074,17 @@ static int run_head(ornith_hip_session *s) {
         return ORNITH_HIP_OK;
     }
     return enqueue_head(s, st);
+}
+
+// One decode step (body and head): the persistent launch where the model
+// has one, else the per-launch body and head.
+static int run_step(ornith_hip_session *s) {
+    if (dec_enabled() && !step_enabled()) {
+        CHK(dec_prepare(s));
+        if (s->dec.grid) return dec_launch(s);
+    }
+    CHK(run_body(s));
+    return run_head(s);
 }
 
 static int sync_pos(ornith_hip_session *s) {
@@ -2058,10 +2392,15 @@ static int session_eval(ornith_hip_session *s, const int32_t *tokens, int n, boo
         }
         s->pf.pos_after = s->pos + n;   // outlives the asynchronous copy
         HCHK(hipMemcpyAsync(s->io + OH_IO_POS, &s->pf.pos_after, 4, hipMemcpyHostToDevice, st));
+        CHK(run_head(s));
+    } else if (n == 1) {
+        // one token: body and head as one step (the greedy token lands at
+        // toks[pos + 1], past the evaluated token)
+        CHK(run_step(s));
     } else {
         for (int i = 0; i < n; i++) CHK(run_body(s));
+        CHK(run_head(s));
     }
-    CHK(run_head(s));
     HCHK(hipStreamSynchronize(st));
     CHK(step_check(s));
     s->pos += n;
@@ -2456,7 +2795,7 @@ extern "C" int ornith_hip_session_generate(ornith_hip_session *s, int n_predict,
     int emitted = 0;
     if (eos < 0) {
         // no stop token: the whole loop stays on the device
-        for (int i = 0; i < n; i++) { CHK(run_body(s)); CHK(run_head(s)); }
+        for (int i = 0; i < n; i++) CHK(run_step(s));
         HCHK(hipMemcpyAsync(out_tokens, s->toks + s->pos, (size_t)n * 4, hipMemcpyDeviceToHost, st));
         HCHK(hipStreamSynchronize(st));
         CHK(step_check(s));
@@ -2469,8 +2808,7 @@ extern "C" int ornith_hip_session_generate(ornith_hip_session *s, int n_predict,
             CHK(step_check(s));
             if (next == eos) break;
             out_tokens[emitted++] = next;
-            CHK(run_body(s));
-            CHK(run_head(s));
+            CHK(run_step(s));
         }
         HCHK(hipStreamSynchronize(st));
     }
@@ -2486,7 +2824,8 @@ extern "C" int ornith_hip_session_time_decode(ornith_hip_session *s, int n_steps
     hipStream_t st = s->m->ctx->st;
     CHK(sync_pos(s));
     if (step_enabled()) CHK(step_prepare(s));
-    if (!s->step_grid && graphs_enabled()) {
+    if (dec_enabled() && !step_enabled()) CHK(dec_prepare(s));
+    if (!s->step_grid && !s->dec.grid && graphs_enabled()) {
         if (!s->gbody) CHK(capture(s, enqueue_body, &s->gbody));
         if (!s->ghead) CHK(capture(s, enqueue_head, &s->ghead));
     }
@@ -2494,7 +2833,7 @@ extern "C" int ornith_hip_session_time_decode(ornith_hip_session *s, int n_steps
     HCHK(hipEventCreate(&e0));
     HCHK(hipEventCreate(&e1));
     HCHK(hipEventRecord(e0, st));
-    for (int i = 0; i < n_steps; i++) { CHK(run_body(s)); CHK(run_head(s)); }
+    for (int i = 0; i < n_steps; i++) CHK(run_step(s));
     HCHK(hipEventRecord(e1, st));
     HCHK(hipEventSynchronize(e1));
     float el = 0.0f;
@@ -3086,5 +3425,80 @@ extern "C" int ornith_hip_session_profile_phases(ornith_hip_session *s, int max_
         us[i] = (float)((double)(t[i + 1] - t[i]) / 100.0);   // 100 MHz real-time clock
     }
     *n_phases = m;
+    return ORNITH_HIP_OK;
+}
+
+// One decode launch with clocks (after a warm-up launch; neither advances the
+// position): per operation its kind and, over the workgroups, the earliest and
+// the latest time it was done (microseconds from the earliest start).
+extern "C" int ornith_hip_session_profile_decode(ornith_hip_session *s, int max_ops, int32_t *kinds,
+                                                 float *us_first, float *us_last, int *n_ops) {
+    *n_ops = 0;
+    if (!s->have_logits) { seterr("session has no logits; eval a prompt first"); return ORNITH_HIP_ERR_FORMAT; }
+    HCHK(hipSetDevice(s->m->ctx->device));
+    hipStream_t st = s->m->ctx->st;
+    CHK(sync_pos(s));
+    CHK(dec_prepare(s));
+    if (!s->dec.grid) { seterr("profile_decode: the decode launch is not available for this model"); return ORNITH_HIP_ERR_UNSUPPORTED; }
+    const int G = s->dec.grid, n = s->dec.n;
+    if (!s->dec.ts) CHK(salloc(s, &s->dec.ts, (size_t)(n + 1) * G));
+    HCHK(oh_launch_decode(s->dec.ops, n, s->io, 0, G, s->dec.lds, st));
+    HCHK(oh_launch_decode(s->dec.ops, n, s->io, 0, G, s->dec.lds, st, s->dec.ts));
+    HCHK(hipStreamSynchronize(st));
+    CHK(step_check(s));
+    std::vector<uint64_t> t((size_t)(n + 1) * G);
+    HCHK(hipMemcpy(t.data(), s->dec.ts, t.size() * 8, hipMemcpyDeviceToHost));
+    uint64_t t0 = t[0];
+    for (int b = 1; b < G; b++) t0 = t[b] < t0 ? t[b] : t0;
+    const int m = n < max_ops ? n : max_ops;
+    for (int i = 0; i < m; i++) {
+        uint64_t lo = ~0ull, hi = 0;
+        for (int b = 0; b < G; b++) {
+            const uint64_t v = t[(size_t)(i + 1) * G + b];
+            lo = v < lo ? v : lo;
+            hi = v > hi ? v : hi;
+        }
+        kinds[i] = s->dec.kinds[i];
+        us_first[i] = (float)((double)(lo - t0) / 100.0);
+        us_last[i] = (float)((double)(hi - t0) / 100.0);
+    }
+    *n_ops = m;
+    return ORNITH_HIP_OK;
+}
+
+// Sub-phase clocks of one operation of the decode launch (measurement): per
+// workgroup 8 stamps (0 start, 1 weights requested, 2 inputs arrived, 3 the
+// activation arrived, 4 prologue done, 5 done; unused ones 0) in microseconds
+// from the launch's earliest start, -1 where not recorded. grid_out: workgroups.
+extern "C" int ornith_hip_session_profile_decode_op(ornith_hip_session *s, int op, float *us, int max_groups,
+                                                    int *grid_out) {
+    *grid_out = 0;
+    if (!s->have_logits) { seterr("session has no logits; eval a prompt first"); return ORNITH_HIP_ERR_FORMAT; }
+    HCHK(hipSetDevice(s->m->ctx->device));
+    hipStream_t st = s->m->ctx->st;
+    CHK(sync_pos(s));
+    CHK(dec_prepare(s));
+    if (!s->dec.grid) { seterr("profile_decode_op: the decode launch is not available for this model"); return ORNITH_HIP_ERR_UNSUPPORTED; }
+    const int G = s->dec.grid, n = s->dec.n;
+    if (op < 0 || op >= n) { seterr("profile_decode_op: operation %d outside [0, %d)", op, n); return ORNITH_HIP_ERR_FORMAT; }
+    if (!s->dec.ts) CHK(salloc(s, &s->dec.ts, (size_t)(n + 1) * G));
+    uint64_t *ts2 = nullptr;
+    CHK(salloc(s, &ts2, (size_t)G * 8));
+    HCHK(oh_launch_decode(s->dec.ops, n, s->io, 0, G, s->dec.lds, st));
+    HCHK(oh_launch_decode(s->dec.ops, n, s->io, 0, G, s->dec.lds, st, s->dec.ts, op, ts2));
+    HCHK(hipStreamSynchronize(st));
+    CHK(step_check(s));
+    std::vector<uint64_t> t((size_t)G), t2((size_t)G * 8);
+    HCHK(hipMemcpy(t.data(), s->dec.ts, (size_t)G * 8, hipMemcpyDeviceToHost));
+    HCHK(hipMemcpy(t2.data(), ts2, t2.size() * 8, hipMemcpyDeviceToHost));
+    uint64_t t0 = t[0];
+    for (int b = 1; b < G; b++) t0 = t[b] < t0 ? t[b] : t0;
+    const int m = G < max_groups ? G : max_groups;
+    for (int b = 0; b < m; b++)
+        for (int k = 0; k < 8; k++) {
+            const uint64_t v = t2[(size_t)b * 8 + k];
+            us[b * 8 + k] = v == 0 ? -1.0f : (float)((double)(v - t0) / 100.0);
+        }
+    *grid_out = m;
     return ORNITH_HIP_OK;
 }

@@ -8,6 +8,7 @@
 #include "oh_mmq.hip"
 #include "oh_batch.hip"
 #include "oh_attn_mfma.hip"
+#include "oh_decode.hip"
 #include "oh_launch.h"
 
 extern "C" {
@@ -339,6 +340,19 @@ hipError_t oh_step_blocks_per_cu(int lds_bytes, int *blocks) {
     hipError_t e = hipFuncSetAttribute((const void *)oh_k_step, hipFuncAttributeMaxDynamicSharedMemorySize, lds_bytes);
     if (e != hipSuccess) return e;
     return hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks, (const void *)oh_k_step, 256, (size_t)lds_bytes);
+}
+
+hipError_t oh_decode_blocks_per_cu(int lds_bytes, int *blocks) {
+    hipError_t e = hipFuncSetAttribute((const void *)oh_k_decode, hipFuncAttributeMaxDynamicSharedMemorySize, lds_bytes);
+    if (e != hipSuccess) return e;
+    return hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks, (const void *)oh_k_decode, 256, (size_t)lds_bytes);
+}
+
+hipError_t oh_launch_decode(const oh_dop *prog, int nops, int32_t *io, int advance, int grid, int lds_bytes,
+                            hipStream_t st, uint64_t *ts, int prof_op, uint64_t *ts2) {
+    void *args[] = {(void *)&prog, (void *)&nops, (void *)&io, (void *)&advance, (void *)&ts, (void *)&prof_op,
+                    (void *)&ts2};
+    return hipLaunchCooperativeKernel((const void *)oh_k_decode, dim3(grid), dim3(256), args, (size_t)lds_bytes, st);
 }
 
 hipError_t oh_launch_step(const oh_op *prog, int nops, int32_t *io, unsigned *ctrs, int epoch_slot, int advance,

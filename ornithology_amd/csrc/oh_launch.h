@@ -96,6 +96,14 @@ int oh_attn_mfma_supported(int hd, int nh, int nkv);
 hipError_t oh_step_blocks_per_cu(int lds_bytes, int *blocks);
 hipError_t oh_launch_step(const oh_op *prog, int nops, int32_t *io, unsigned *ctrs, int epoch_slot, int advance,
                           uint64_t *ts, int grid, int lds_bytes, hipStream_t st);
+// the decode step as one persistent launch (oh_decode.hip): resident
+// 256-thread blocks per CU at this dynamic LDS size, and the cooperative
+// launch of a program (prog in device memory)
+hipError_t oh_decode_blocks_per_cu(int lds_bytes, int *blocks);
+// ts (optional): per-workgroup start and end-of-operation clocks, (nops + 1) * grid;
+// ts2 (optional): operation prof_op's sub-phase clocks, 8 per workgroup
+hipError_t oh_launch_decode(const oh_dop *prog, int nops, int32_t *io, int advance, int grid, int lds_bytes,
+                            hipStream_t st, uint64_t *ts = nullptr, int prof_op = -1, uint64_t *ts2 = nullptr);
 hipError_t oh_launch_moe_route(const float *logits, int ne, int k, const float *shgate_logit,
                                int32_t *idx, float *w, float *shgate, hipStream_t st);
 hipError_t oh_launch_advance(int32_t *io_pos, hipStream_t st);

@@ -293,3 +293,96 @@ typedef struct {
     int nb, in, rows, mode;           // mode 1: y += product
     int ncol, lstride, adiv, ystride;
 } oh_mmq;
+
+// ---- the decode step as one persistent launch (oh_decode.hip) ----------------
+// Values that one workgroup hands to others travel as tagged words: 64 bits,
+// the low 32 the value (a float's bits), the high 32 the step's tag (a
+// per-session launch counter, never 0). Every operation writes its own region
+// of the session's word arena, so a reader waits for exactly the words it
+// needs until their tag is the current one; no barrier and no counter. Bulk
+// outputs (attention partials, KV append) use plain device-scope stores
+// followed by one tagged flag word per writing workgroup.
+enum {
+    OH_D_EMBED = 0,    // u.emb: token row -> tagged x
+    OH_D_MV,           // u.mv: multi-segment matvec with prologue (+ routing, + argmax partials)
+    OH_D_DELTA,        // u.dl: gated delta-net step, one workgroup per value head
+    OH_D_PREP,         // u.at: q/k norm + RoPE + KV append (flags)
+    OH_D_ATTN,         // u.at: exact walk (o + flags) or flash chunks (partials + flags)
+    OH_D_COMBINE,      // u.at: merge of the flash chunks (o + flags)
+    OH_D_DOWN,         // u.dn: MoE down projection + combine (routing recomputed)
+    OH_D_ARGMAX,       // u.am: greedy token from the lm_head's per-workgroup partials
+    OH_D_COUNT
+};
+#define OH_D_MAXSEG 6
+typedef struct {
+    const uint8_t *A, *B, *C, *A2, *B2, *C2;
+    uint64_t *y;            // tagged output: slot k, row r at y[k * ystride + r]
+    float *yp;              // optional plain copy of the output (logits)
+    int type, pair, rows, nsub, ystride, stacked, mode;   // mode 1: y = xres[r] + dot
+    int units;              // wave steps per slot (ceil(rows / (64 / nb)))
+    int step0;              // the segment's first step in the operation
+} oh_dseg;
+typedef struct {
+    const uint64_t *x;      // tagged activation [in]
+    const float *xp;        // or a plain activation (flag-gated, pro F32)
+    const uint64_t *xflags; // flags gating xp: nflags words
+    int nflags_ex, nflags_fl;   // flags to wait for: exact-walk / flash contexts
+    const float *nw;        // RMSNorm weight (pro NORM)
+    const uint64_t *xres;   // tagged residual for mode-1 segments
+    const uint64_t *rlog, *shl;   // routing: tagged router logits [ne], shared-gate logit
+    uint64_t *amax;         // head: tagged (value, index) of each workgroup's best row [G][2]
+    int pro, in, nb, nseg, nsteps, spw, route, ne, topk, exact_lim;
+    int wave0;              // the operation's steps go to the grid's waves from wave0 on
+    int wspec;              // 1: wave 0 of a workgroup forms the inputs, waves 1-3 take the steps
+    float eps;
+    oh_dseg s[OH_D_MAXSEG];
+} oh_dmv;
+typedef struct {
+    const uint8_t *A, *B, *C;
+    const int32_t *toks;
+    uint64_t *x;
+    int type, in;
+} oh_demb;
+typedef struct {
+    const uint64_t *cat, *ab, *z;          // tagged: qkv projection [cc], alpha|beta [2 nv], gate [nv dv]
+    const float *conv_w, *ssm_a, *dt_bias, *norm_w;
+    float *conv_state, *S;
+    uint64_t *o;                           // tagged gated-normed output [nv dv]
+    int dk, nk, nv, K, cc;
+    float out_scale, eps;
+} oh_ddelta;
+typedef struct {
+    oh_op_prep p;                          // prep (qproj/kin/vin unused: the tagged inputs below)
+    oh_op_attn a;                          // attention / combine
+    const uint64_t *qkv;                   // tagged: q projection [nh 2hd] | k [nkv hd] | v [nkv hd]
+    uint64_t *flags;                       // this operation's flag per workgroup
+    const uint64_t *wflags;                // flags waited for
+    int nwait_ex, nwait_fl;                // ... at exact-walk / flash contexts
+    int lim;                               // exact-walk limit
+} oh_datt;
+typedef struct {
+    const uint8_t *A, *B, *C, *sA, *sB, *sC;
+    const uint64_t *h;                     // tagged silu(gate)*up: slot j at j * I, shared at k * I
+    const uint64_t *rlog, *shl;            // tagged router logits (routing recomputed)
+    const uint64_t *xres;                  // tagged residual [H]
+    uint64_t *y;                           // tagged output [H]
+    int type, nb, in, rows, k, ne, rpb;    // rpb: rows per workgroup
+} oh_ddown;
+typedef struct {
+    const uint64_t *amax;                  // [nparts][2]
+    int nparts, vocab;
+    int32_t *toks;                         // the greedy token goes to toks[pos + 1]
+} oh_dargmax;
+typedef struct {
+    int kind, nvb;
+    union {
+        oh_demb emb;
+        oh_dmv mv;
+        oh_ddelta dl;
+        oh_datt at;
+        oh_ddown dn;
+        oh_dargmax am;
+    } u;
+} oh_dop;
+// io words of the decode launch (after the step kernel's)
+enum { OH_IO_TAG = 8, OH_IO_DONE = 9 };
