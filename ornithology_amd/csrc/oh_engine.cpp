@@ -1111,6 +1111,7 @@ struct ornith_hip_session {
     int cap = 0, pos = 0, kvcap = 0;
     bool have_logits = false;
     std::vector<void *> allocs;
+    std::vector<size_t> asz;      // bytes requested for each of allocs
     int32_t *io = nullptr;        // [0] pos, [1] best
     int32_t *toks = nullptr;      // [cap + 1]
     float *x = nullptr, *xn = nullptr;
@@ -1296,6 +1297,7 @@ static int salloc(ornith_hip_session *s, T **p, size_t n) {
     HCHK(hipMalloc(&v, n * sizeof(T) + 256));
     HCHK(hipMemset(v, 0, n * sizeof(T) + 256));
     s->allocs.push_back(v);
+    s->asz.push_back(n * sizeof(T));
     *p = (T *)v;
     return ORNITH_HIP_OK;
 }
@@ -2447,6 +2449,108 @@ static int bw_alloc(ornith_hip_session *s, int n, size_t ops_bytes) {
     return ORNITH_HIP_OK;
 }
 
+// Host-side bounds check of a batch step's per-session descriptors (before
+// they are uploaded): every buffer a descriptor names, with the extent the
+// step's kernels reach through it at the session's position, lies inside one
+// allocation of the session that owns it (the batch buffers: the leading
+// session), and the attention grid and LDS cover every session's own.
+// Returns a description of the first violation, or an empty string.
+static bool owns(const ornith_hip_session *s, const void *p, size_t bytes) {
+    const uintptr_t a = (uintptr_t)p;
+    for (size_t i = 0; i < s->allocs.size(); i++) {
+        const uintptr_t b = (uintptr_t)s->allocs[i];
+        if (a >= b && a + bytes >= a && a + bytes <= b + s->asz[i]) return true;
+    }
+    return false;
+}
+
+static std::string batch_check(ornith_hip_session *const *ss, int n, const std::vector<size_t> &lofs,
+                               const uint8_t *host, int nvb_main, int lds_main) {
+    const ornith_hip_session *s0 = ss[0];
+    const ornith_hip_model *m = s0->m;
+    const ornith_hip_arch &a = m->a;
+    const size_t F = sizeof(float), qd = (size_t)a.nk * a.dk, vd = (size_t)a.nv * a.dv, cc = 2 * qd + vd;
+    const size_t aq = (size_t)a.nh * a.hd, kvd = (size_t)a.nkv * a.hd;
+    char msg[256];
+#define BC(own, ptr, bytes, what)                                                                           \
+    do {                                                                                                    \
+        if (!owns(own, ptr, bytes)) {                                                                       \
+            snprintf(msg, sizeof msg, "layer %d session %d: %s (%zu bytes) outside its allocations", l, b,  \
+                     what, (size_t)(bytes));                                                                \
+            return msg;                                                                                     \
+        }                                                                                                   \
+    } while (0)
+    for (int l = 0; l < a.n_layers; l++) {
+        const uint8_t *src = host + lofs[(size_t)l];
+        for (int b = 0; b < n; b++) {
+            const ornith_hip_session *sb = ss[b];
+            const int pos = sb->pos;
+            if (m->L[l].full) {
+                oh_op_prep pr;
+                oh_op_attn at;
+                memcpy(&pr, src + (size_t)b * sizeof(oh_op_prep), sizeof pr);
+                memcpy(&at, src + (size_t)n * sizeof(oh_op_prep) + (size_t)b * sizeof(oh_op_attn), sizeof at);
+                const size_t cap = (size_t)pr.cap, S = (size_t)oh_flash_slots(pr.cap);
+                if (pr.cap % 16 || pos >= pr.cap || at.cap != pr.cap) {
+                    snprintf(msg, sizeof msg, "layer %d session %d: position %d, KV capacity %d / %d", l, b, pos,
+                             pr.cap, at.cap);
+                    return msg;
+                }
+                BC(s0, pr.qproj, 2 * aq * F, "q projection");
+                BC(s0, pr.kin, kvd * F, "k projection");
+                BC(s0, pr.vin, kvd * F, "v projection");
+                BC(sb, pr.rope, ((size_t)pos + 1) * (a.hd / 2) * 2 * F, "RoPE table");
+                BC(s0, pr.qr, aq * F, "rotated queries");
+                BC(s0, pr.gate, aq * F, "output gate");
+                BC(sb, pr.Kt, kvd / 4 * cap * 4, "K codes");
+                BC(sb, pr.Ks, cap * a.nkv * F, "K scales");
+                BC(sb, pr.Vq, cap * kvd, "V codes");
+                BC(sb, pr.Vs, cap * a.nkv * F, "V scales");
+                if (at.qr != pr.qr || at.gate != pr.gate || at.Kt != pr.Kt || at.Ks != pr.Ks || at.Vq != pr.Vq ||
+                    at.Vs != pr.Vs) {
+                    snprintf(msg, sizeof msg, "layer %d session %d: attention and prep name different buffers", l, b);
+                    return msg;
+                }
+                BC(sb, at.scores, (size_t)a.nh * cap * F, "scores");
+                BC(sb, at.part_o, (size_t)a.nh * S * a.hd * F, "flash partial outputs");
+                BC(sb, at.part_ml, (size_t)a.nh * S * 2 * F, "flash partial max/sum");
+                BC(s0, at.out, aq * F, "attention output");
+                const int nv_ex = a.nh / (256 / a.hd), nv_fl = oh_flash_nvb(a.nh, a.nkv, at.cap, at.hb);
+                const int lds_ex = oh_exact_lds_bytes(a.hd, at.exact_max);
+                const int lds_fl = oh_flash_form_lds(a.nh, a.nkv, a.hd, at.hb);
+                if (nvb_main < nv_ex || nvb_main < nv_fl || lds_main < lds_ex || lds_main < lds_fl ||
+                    lds_main > 65536) {
+                    snprintf(msg, sizeof msg, "layer %d session %d: attention grid %d / LDS %d below %d, %d / %d, %d",
+                             l, b, nvb_main, lds_main, nv_ex, nv_fl, lds_ex, lds_fl);
+                    return msg;
+                }
+            } else {
+                oh_op_delta d;
+                memcpy(&d, src + (size_t)b * sizeof(oh_op_delta), sizeof d);
+                if (d.cc != (int)cc || d.nv != a.nv || d.dk != a.dk || d.K != a.conv_k) {
+                    snprintf(msg, sizeof msg, "layer %d session %d: delta shape", l, b);
+                    return msg;
+                }
+                BC(s0, d.cat, cc * F, "qkv mix");
+                BC(s0, d.ab, 2 * (size_t)a.nv * F, "alpha/beta");
+                BC(s0, d.gate, vd * F, "z gate");
+                BC(sb, d.conv_state, 2 * (size_t)(a.conv_k - 1) * cc * F, "conv window (two parities)");
+                BC(sb, d.S, vd * a.dk * F, "delta state");
+                BC(s0, d.out, vd * F, "delta output");
+                BC(s0, d.out_gate, vd * F, "delta output gate");
+                BC(s0, d.out_runs, vd / 64 * sizeof(double), "delta output runs");
+            }
+        }
+    }
+#undef BC
+    for (int b = 0; b < n; b++)
+        if (ss[b]->pos + 1 > ss[b]->cap || !owns(ss[b], ss[b]->toks, ((size_t)ss[b]->pos + 2) * 4)) {
+            snprintf(msg, sizeof msg, "session %d: token history at position %d of %d", b, ss[b]->pos, ss[b]->cap);
+            return msg;
+        }
+    return std::string();
+}
+
 // the device work of one batch step (its descriptors, tokens and positions
 // already in p.OPS): everything but the host copies, so that it can be
 // captured once and replayed for the same sessions
@@ -2654,6 +2758,20 @@ extern "C" int ornith_hip_batch_step(ornith_hip_session **ss, int n, const int32
             return ORNITH_HIP_ERR_FORMAT;
         }
     }
+    // one KV capacity, exact_max and flash form across the batch, and every
+    // context on the same attention path (all within exact_max or all past
+    // it): the only mixes the batch step is run with; others are refused
+    for (int b = 1; b < n; b++) {
+        const ornith_hip_session *x = ss[b], *y = ss[0];
+        const int lim = oh_exact_limit(y->exact_max);
+        if (x->kvcap != y->kvcap || x->exact_max != y->exact_max || x->flash_mfma != y->flash_mfma ||
+            (x->pos + 1 <= lim) != (y->pos + 1 <= lim)) {
+            seterr("batch_step: session %d differs from session 0 in KV capacity (%d / %d), attention settings or "
+                   "attention path (position %d / %d); a batch takes sessions of one capacity on one path",
+                   b, x->kvcap, y->kvcap, x->pos, y->pos);
+            return ORNITH_HIP_ERR_UNSUPPORTED;
+        }
+    }
     if (!pf_supported(m) || !oh_qdot_can(m->lm_head->type, m->lm_head->in) || m->lm_head->in > 8192) {
         seterr("batch_step: the model is outside the batched projection path (widths <= 8192, integer dot types)");
         return ORNITH_HIP_ERR_UNSUPPORTED;
@@ -2722,19 +2840,30 @@ extern "C" int ornith_hip_batch_step(ornith_hip_session **ss, int n, const int32
             }
         }
     }
+    // the full bounds check runs whenever a plan is captured (the descriptors
+    // of the same sessions do not change between replays; the positions are
+    // checked against the capacities above on every step)
+    auto check = [&]() -> int {
+        const std::string bad = batch_check(ss, n, B.lofs, host.data(), B.nvb_main, B.lds_main);
+        if (!bad.empty()) { seterr("batch_step plan: %s", bad.c_str()); return ORNITH_HIP_ERR_DEVICE; }
+        return ORNITH_HIP_OK;
+    };
     int32_t *htp = (int32_t *)(host.data() + B.tok_ofs);
     int32_t **htk = (int32_t **)(host.data() + B.tok_ofs + (((size_t)n * 8 + 15) & ~(size_t)15));
     for (int b = 0; b < n; b++) { htp[b] = tokens[b]; htp[n + b] = ss[b]->pos; htk[b] = ss[b]->toks; }
     HCHK(hipMemcpyAsync(p.OPS, host.data(), ob, hipMemcpyHostToDevice, st));
     if (graphs_enabled()) {
         // one captured step per set of sessions (ids, not addresses), buffer
-        // generation and product path
+        // generation, product path, batch plan and attention grid
         std::vector<uint64_t> key;
         key.push_back((uint64_t)n);
         key.push_back((uint64_t)p.gen);
         key.push_back(mmq_enabled() ? 1u : 0u);
+        key.push_back(batch_fused() ? 1u : 0u);
+        key.push_back((uint64_t)B.nvb_main << 32 | (uint32_t)B.lds_main);
         for (int b = 0; b < n; b++) key.push_back(ss[b]->sid);
         if (!p.graph || p.key != key) {
+            CHK(check());
             if (p.graph) { (void)hipGraphExecDestroy(p.graph); p.graph = nullptr; }
             hipGraph_t g = nullptr;
             HCHK(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
@@ -2749,6 +2878,7 @@ extern "C" int ornith_hip_batch_step(ornith_hip_session **ss, int n, const int32
         }
         HCHK(hipGraphLaunch(p.graph, st));
     } else {
+        CHK(check());
         CHK(batch_enqueue(B, st));
     }
     std::vector<int32_t> hn((size_t)n);

@@ -327,6 +327,9 @@ int oh_flash_parts(int T, int cap, int hb) {
     return ((T + kFdT - 1) / kFdT + tpb - 1) / tpb;
 }
 
+// contexts up to this many positions take the exact attention walk
+int oh_exact_limit(int exact_max) { return exact_max < kExactMax ? exact_max : kExactMax; }
+
 // exact attention walk: the scores of a block's 256/hd heads in LDS
 int oh_exact_lds_bytes(int hd, int exact_max) {
     const int lim = exact_max < kExactMax ? (exact_max > 0 ? exact_max : 0) : kExactMax;

@@ -127,6 +127,53 @@ def test_c1_chunked_mode_matches_reference(c1, monkeypatch):
     s.free()
 
 
+@pytest.mark.parametrize("serial", [1, 0], ids=["serial", "chunked"])
+def test_c1_short_prompts_vs_oracle(c1, orc, monkeypatch, serial):
+    """Prompts of 1 to 8 tokens (shorter than, equal to and just past the conv
+    kernel's K-1 = 3 window rows, and one delta chunk's tail): prompt logits,
+    delta state and conv window after the prompt, and the logits of one
+    decode step, bit-exact against the oracle (pinned to the reference's own
+    build on these prompts)."""
+    monkeypatch.setenv("ORNITH_PREFILL_SERIAL", str(serial))
+    path, m = c1
+    om = C.c_void_p()
+    assert orc.orc_model_load(str(path).encode(), C.byref(om)) == 0
+    orc.orc_model_set_threads(om, 8)
+    a = m.arch
+    V = a["vocab"]
+    cc = 2 * a["nk"] * a["dk"] + a["nv"] * a["dv"]
+    rng = np.random.default_rng(11)
+    bad = []
+    for n in (1, 2, 3, 4, 5, 7, 8):
+        p = rng.integers(0, V, n).astype(np.int32)
+        os_ = orc.orc_session_new(om, 32, 1)
+        assert orc.orc_session_eval(os_, i32p(p), n, serial) == 0
+        s = m.session(32)
+        s.eval(p)
+        ref = np.ctypeslib.as_array(orc.orc_session_logits(os_), (V,)).copy()
+        if not np.array_equal(u32(s.logits()), u32(ref)):
+            bad.append((n, "prompt logits"))
+        for layer in range(a["n_layers"]):
+            if layer % a["full_interval"] == a["full_interval"] - 1:
+                continue
+            S = np.ctypeslib.as_array(orc.orc_session_delta(os_, layer), (a["nv"] * a["dv"] * a["dk"],))
+            if not np.array_equal(u32(s.delta_state(layer)), u32(S)):
+                bad.append((n, "delta state", layer))
+            W = np.ctypeslib.as_array(orc.orc_session_conv(os_, layer), ((a["conv_k"] - 1) * cc,))
+            if not np.array_equal(u32(s.conv_state(layer)), u32(W)):
+                bad.append((n, "conv window", layer))
+        t = int(np.argmax(ref))
+        assert orc.orc_session_step(os_, t) == 0
+        s.step(t)
+        ref = np.ctypeslib.as_array(orc.orc_session_logits(os_), (V,)).copy()
+        if not np.array_equal(u32(s.logits()), u32(ref)):
+            bad.append((n, "step logits"))
+        s.free()
+        orc.orc_session_free(os_)
+    orc.orc_model_free(om)
+    assert not bad, bad
+
+
 def test_session_errors(c1):
     import ornithology_amd as oa
     _, m = c1
