@@ -168,16 +168,19 @@ int  ornith_hip_session_generate(ornith_hip_session *s, int n_predict,
                                  int32_t *out_tokens, int *n_out);
 /* rforward_token for one token (src/ornith_rforward.c:686-706). */
 int  ornith_hip_session_step(ornith_hip_session *s, int32_t token);
-/* One token step for each of n sessions of the same model at once (any
- * positions): token[i] goes through s[i] exactly as ornith_hip_session_step
+/* One token step for each of n sessions of the same model at once: token[i]
+ * goes through s[i] exactly as ornith_hip_session_step
  * would (rforward_token per session, src/ornith_rforward.c:686-706) and each
  * session's logits are left for ornith_hip_session_logits; next (n entries,
  * may be NULL) receives each session's greedy next token. The projections run
  * over the n sessions together (matmul_batch_q's Tn columns,
  * src/ornith_rforward.c:91-196), so the weights are read once per step. No
  * single reference call does this; it is the multi-sequence form of the token
- * step. Sessions must be distinct; calls sharing a session or a first session
- * must not overlap (the first session holds the step's buffers). */
+ * step. Sessions must be distinct, of one KV capacity and attention setting,
+ * with every context on the same attention path (all within the exact walk
+ * or all past it), and HIP graphs on; other batches return
+ * ORNITH_HIP_ERR_UNSUPPORTED. Calls sharing a session or a first session must
+ * not overlap (the first session holds the step's buffers). */
 int  ornith_hip_batch_step(ornith_hip_session **s, int n, const int32_t *tokens, int32_t *next);
 
 /* rmodel_session_save (src/ornith_rforward.c:1019-1075): the session as an

@@ -40,3 +40,21 @@ def test_init_without_gpu_reports_error():
     st = L.ornith_hip_init(0, C.byref(h))
     assert st != 0 and not h
     assert L.ornith_hip_last_error()
+
+
+def test_header_compiles_as_c11_caller(tmp_path):
+    """The C caller of the boundary (tests/c_caller/ornith_generate.c)
+    compiles as strict C11 against include/ornith_hip.h with every warning an
+    error, and links against the in-tree library."""
+    import shutil
+    import subprocess
+    if not shutil.which("gcc"):
+        pytest.skip("no gcc")
+    root = oa.HEADER.parent.parent
+    src = root / "tests" / "c_caller" / "ornith_generate.c"
+    out = tmp_path / "ornith_generate"
+    lib = root / "ornithology_amd"
+    r = subprocess.run(["gcc", "-std=c11", "-Wall", "-Wextra", "-Werror", "-pedantic", "-O2",
+                        f"-I{root / 'include'}", str(src), "-o", str(out), f"-L{lib}", "-lornith_hip",
+                        "-Wl,-rpath-link,/opt/rocm/lib"], capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
