@@ -202,57 +202,117 @@ def profile_kernels(sess: oa.Session, reps: int) -> dict:
     return {k: dict(launches=v[0] / reps, bytes=v[1] / reps, ms=v[2] / reps) for k, v in agg.items()}
 
 
-def cpu_baseline(model: oa.Model, cfg: dict, seconds: float) -> dict:
+def cpu_host() -> dict:
+    """This host's CPUs as the CPU baseline uses them: nproc, the CPUs this
+    process may run on, the CPU model, the NUMA nodes, and the per-GPU CPU
+    share the box grants (OMP_NUM_THREADS there)."""
+    allowed = sorted(os.sched_getaffinity(0))
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    nodes = {}
+    for d in sorted(Path("/sys/devices/system/node").glob("node[0-9]*")):
+        cpus = set()
+        try:
+            for part in (d / "cpulist").read_text().strip().split(","):
+                if part:
+                    a, _, b = part.partition("-")
+                    cpus.update(range(int(a), int(b or a) + 1))
+        except OSError:
+            continue
+        nodes[int(d.name[4:])] = cpus
+    share = os.environ.get("OMP_NUM_THREADS")
+    return {"nproc": os.cpu_count(), "allowed": allowed, "model": model, "nodes": nodes,
+            "share": int(share) if share and share.isdigit() else None}
+
+
+def cpu_pin(host: dict) -> tuple:
+    """Pin this process to the NUMA node holding most of its allowed CPUs (in
+    process, no re-exec); threads = min(that node's allowed CPUs, 64) as the
+    reference sizes its pool (src/ornith_rforward.c:811-812), capped by the
+    box's per-GPU CPU share. Returns (node, cpus, threads, previous mask)."""
+    prev = set(host["allowed"])
+    node, cpus = None, prev
+    if host["nodes"]:
+        node = max(host["nodes"], key=lambda k: len(host["nodes"][k] & prev))
+        cpus = host["nodes"][node] & prev or prev
+    os.sched_setaffinity(0, cpus)
+    threads = min(len(cpus), 64)
+    if host["share"]:
+        threads = min(threads, host["share"])
+    return node, sorted(cpus), threads, prev
+
+
+def cpu_baseline(model: oa.Model, cfg: dict, ctx_len: int, reps: int = 3, steps: int = 16) -> dict:
     """Oracle port (the C restatement of the reference path, same per-matvec
-    thread fan-out) on this host: a 4-layer slice (3 delta-net + 1 GQA) of the
-    same weights with the full 248320-row lm_head, written to a GGUF and run
-    for greedy decode steps after a 4-token prompt; per-token time scaled to
-    the model's layers as lm_head+embed + n_layers/4 x (4-layer body)."""
+    thread fan-out) on this host, pinned to one NUMA node: a 4-layer slice
+    (3 delta-net + 1 GQA) of the same weights with the full 248320-row
+    lm_head, written to a GGUF; the session moved to ctx_len positions with
+    a seeded Q8 KV cache (orc_session_seed_context: an oracle prefill of
+    4096 tokens takes minutes), then `reps` repetitions of `steps` greedy
+    decode steps and of the lm_head matvec alone, best and mean as `ornith
+    bench` reports them (src/ornith_bench.c:108-146). Token time =
+    lm_head + n_layers/4 x (slice step - lm_head)."""
     sys.path.insert(0, str(ROOT / "tests"))
     import clibs
     L = clibs.oracle()
-    ncores = min(16, len(os.sched_getaffinity(0)))
-    with tempfile.TemporaryDirectory() as td:
-        path = str(Path(td) / "slice.gguf")
-        log("cpu baseline: writing the 4-layer slice GGUF")
-        clibs.write_model_gguf(model, cfg, path, n_layers=4)
-        log("cpu baseline: slice written, timing the oracle port")
-        m = C.c_void_p()
-        assert L.orc_model_load(path.encode(), C.byref(m)) == 0, L.orc_last_error()
-        L.orc_model_set_threads(m, ncores)
-        s = L.orc_session_new(m, 4096, 1)
-        prompt = np.ascontiguousarray(np.arange(1, 5, dtype=np.int32))
-        L.orc_session_eval(s, clibs.i32p(prompt), 4, 1)
-        # lm_head alone (same threads) to split head and body
-        x = np.ones(cfg["hidden"], np.float32)
-        y = np.zeros(cfg["vocab"], np.float32)
-        head = model.tensor_info("output.weight")
-        hw = model.tensor("output.weight").download(head["nbytes"])
-        t0 = time.perf_counter()
-        nh = 0
-        while time.perf_counter() - t0 < seconds * 0.25 or nh < 2:
-            L.orc_matvec(head["type"], C.c_void_p(hw.ctypes.data), cfg["hidden"], cfg["vocab"], clibs.f32p(x),
-                         clibs.f32p(y), 0, ncores)
-            nh += 1
-        t_head = (time.perf_counter() - t0) / nh
-        t0 = time.perf_counter()
-        steps = 0
-        tok = 7
-        while time.perf_counter() - t0 < seconds * 0.75 or steps < 2:
-            L.orc_session_step(s, tok)
-            lg = np.ctypeslib.as_array(L.orc_session_logits(s), (cfg["vocab"],))
-            tok = int(np.argmax(lg))
-            steps += 1
-        t_step4 = (time.perf_counter() - t0) / steps
-        L.orc_session_free(s)
-        L.orc_model_free(m)
-    t_body4 = max(t_step4 - t_head, 0.0)
-    t_tok = t_head + (cfg["n_layers"] / 4) * t_body4
-    return dict(value=1.0 / t_tok, unit="tok/s", cores=ncores, kind="port",
-                sample=f"oracle port, 4-layer slice (3 DN + 1 GQA) of the same weights + full lm_head: "
-                       f"{steps} greedy steps after a 4-token prompt ({t_step4 * 1e3:.1f} ms/step) and {nh} "
-                       f"lm_head matvecs ({t_head * 1e3:.1f} ms); token time = head + {cfg['n_layers'] // 4} x body "
-                       f"= {t_tok * 1e3:.1f} ms; Q8 KV; {ncores} threads")
+    host = cpu_host()
+    node, cpus, threads, prev = cpu_pin(host)
+    try:
+        with tempfile.TemporaryDirectory() as td:
+            path = str(Path(td) / "slice.gguf")
+            log("cpu baseline: writing the 4-layer slice GGUF")
+            clibs.write_model_gguf(model, cfg, path, n_layers=4)
+            log(f"cpu baseline: slice written; oracle port on {threads} threads, NUMA node {node} "
+                f"({len(cpus)} CPUs), context {ctx_len}")
+            m = C.c_void_p()
+            assert L.orc_model_load(path.encode(), C.byref(m)) == 0, L.orc_last_error()
+            L.orc_model_set_threads(m, threads)
+            s = L.orc_session_new(m, ctx_len + reps * steps + 8, 1)
+            assert L.orc_session_seed_context(s, ctx_len, 1) == 0
+            x = np.ones(cfg["hidden"], np.float32)
+            y = np.zeros(cfg["vocab"], np.float32)
+            head = model.tensor_info("output.weight")
+            hw = model.tensor("output.weight").download(head["nbytes"])
+            t_head, t_step = [], []
+            tok = 7
+            for _ in range(reps):
+                t0 = time.perf_counter()
+                L.orc_matvec(head["type"], C.c_void_p(hw.ctypes.data), cfg["hidden"], cfg["vocab"],
+                             clibs.f32p(x), clibs.f32p(y), 0, threads)
+                t_head.append(time.perf_counter() - t0)
+                t0 = time.perf_counter()
+                for _ in range(steps):
+                    L.orc_session_step(s, tok)
+                    tok = int(np.argmax(np.ctypeslib.as_array(L.orc_session_logits(s), (cfg["vocab"],))))
+                t_step.append((time.perf_counter() - t0) / steps)
+            L.orc_session_free(s)
+            L.orc_model_free(m)
+    finally:
+        os.sched_setaffinity(0, prev)
+
+    def tok_time(h, st):
+        return h + (cfg["n_layers"] / 4) * max(st - h, 0.0)
+
+    best = tok_time(min(t_head), min(t_step))
+    mean = tok_time(sum(t_head) / reps, sum(t_step) / reps)
+    nodes = {str(k): len(v) for k, v in host["nodes"].items()}
+    return dict(value=round(1.0 / mean, 4), unit="tok/s", cores=threads, kind="port",
+                best=round(1.0 / best, 4), mean=round(1.0 / mean, 4), reps=reps,
+                host={"nproc": host["nproc"], "allowed_cpus": len(host["allowed"]), "cpu_model": host["model"],
+                      "numa_nodes": nodes, "pinned_node": node, "pinned_cpus": len(cpus),
+                      "gpu_cpu_share": host["share"]},
+                sample=f"oracle port, 4-layer slice (3 DN + 1 GQA) of the same weights + full lm_head at "
+                       f"{ctx_len} positions (seeded Q8 KV): {reps} reps x {steps} greedy steps "
+                       f"(best {min(t_step) * 1e3:.1f} / mean {sum(t_step) / reps * 1e3:.1f} ms per step) and "
+                       f"{reps} lm_head matvecs (best {min(t_head) * 1e3:.1f} ms); token time = head + "
+                       f"{cfg['n_layers'] // 4} x (step - head) = {mean * 1e3:.1f} ms mean, {best * 1e3:.1f} ms "
+                       f"best; {threads} threads pinned to NUMA node {node}")
 
 
 def batch_decode(model: oa.Model, n: int, ctx_len: int, steps: int) -> dict:
@@ -295,7 +355,9 @@ def c2_bench(args) -> int:
     sys.path.insert(0, str(ROOT / "tests"))
     import clibs
     L = clibs.oracle()
-    ncores = min(16, len(os.sched_getaffinity(0)))
+    host = cpu_host()
+    node, cpus, ncores, prev = cpu_pin(host)
+    log(f"C2 CPU leg: oracle port on {ncores} threads, NUMA node {node} ({len(cpus)} CPUs), {host['model']}")
     ctx = oa.Context(0)
     rows = []
     for (n, out) in C2_SHAPES:
@@ -328,6 +390,7 @@ def c2_bench(args) -> int:
                 f"cpu {cpu_ms:9.3f} ms")
             rows.append(r)
         del w
+    os.sched_setaffinity(0, prev)
     big = [r for r in rows if r["out"] == C2_SHAPES[0][1]]
     best = max(big, key=lambda r: r["cold_gbs"])
     print(json.dumps({"metric": "C2 quantized matvec, cold HBM GB/s of the weight stream", "value": best["cold_gbs"],
@@ -479,8 +542,9 @@ def main() -> int:
     cpu = None
     if not args.no_cpu:
         try:
-            cpu = cpu_baseline(model, cfg, args.cpu_seconds)
-            log(f"cpu baseline: {cpu['value']:.3f} tok/s on {cpu['cores']} threads")
+            cpu = cpu_baseline(model, cfg, args.ctx)
+            log(f"cpu baseline: {cpu['value']:.3f} tok/s mean, {cpu['best']:.3f} best, on {cpu['cores']} "
+                f"threads ({cpu['host']})")
         except Exception as e:  # reported, never hides the GPU number
             log(f"cpu baseline failed: {e!r}")
 

@@ -211,6 +211,34 @@ float *orc_session_delta(orc_session *s, int l) { return s->S[l]; }
 float *orc_session_conv(orc_session *s, int l) { return s->conv[l]; }
 orc_kv *orc_session_kv(orc_session *s, int l) { return is_full(&s->m->a, l) ? &s->kv[l] : NULL; }
 
+int orc_session_seed_context(orc_session *s, int n, uint64_t seed) {
+    const orc_arch *a = &s->m->a;
+    if (s->pos != 0 || n < 0 || n >= s->cap) return -1;
+    uint64_t x = seed * 0x9E3779B97F4A7C15ull + 1;
+    for (int l = 0; l < a->n_layers; l++) {
+        if (!is_full(a, l)) continue;
+        orc_kv *c = &s->kv[l];
+        if (!c->quantized) return -1;
+        const size_t nc = (size_t)n * c->n_kv_heads * c->head_dim, ns = (size_t)n * c->n_kv_heads;
+        for (size_t i = 0; i < nc; i++) {
+            x = x * 6364136223846793005ull + 1442695040888963407ull;
+            c->Kq[i] = (int8_t)((int)((x >> 33) % 255u) - 127);
+            x = x * 6364136223846793005ull + 1442695040888963407ull;
+            c->Vq[i] = (int8_t)((int)((x >> 33) % 255u) - 127);
+        }
+        for (size_t i = 0; i < ns; i++) {
+            x = x * 6364136223846793005ull + 1442695040888963407ull;
+            c->Ks[i] = (float)((x >> 40) + 1) * 0x1p-30f;
+            x = x * 6364136223846793005ull + 1442695040888963407ull;
+            c->Vs[i] = (float)((x >> 40) + 1) * 0x1p-30f;
+        }
+        c->len = n;
+    }
+    s->pos = n;
+    s->nhist = n;
+    return 0;
+}
+
 /* ---- layer math (src/ornith_rforward.c:282-503) ----------------------------- */
 static float decay_alpha(float a_in, float a_coef, float dt_bias) {
     return expf(a_coef * orc_softplus(a_in + dt_bias));

@@ -177,6 +177,13 @@ int  orc_session_step(orc_session *s, int32_t token);
 float  *orc_session_delta(orc_session *s, int L);
 float  *orc_session_conv(orc_session *s, int L);
 orc_kv *orc_session_kv(orc_session *s, int L);
+/* Timing aid for the CPU baseline, not part of the reference's algorithm:
+ * move an empty session to position n (< cap) with every full-attention
+ * layer's Q8 KV cache holding n seeded positions (codes in [-127, 127],
+ * scales in (0, 2^-6]), as if an n-token prompt had run, so that the next
+ * token steps cost what they cost at that context. Returns 0, or -1 when the
+ * session is not empty, n is out of range or the cache is not Q8. */
+int orc_session_seed_context(orc_session *s, int n, uint64_t seed);
 
 /* ---- random-init GGUF generator --------------------------------------- */
 typedef struct {

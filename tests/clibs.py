@@ -152,6 +152,7 @@ def oracle():
         "orc_session_delta": (fp, [vp, C.c_int]),
         "orc_session_conv": (fp, [vp, C.c_int]),
         "orc_session_kv": (C.POINTER(OrcKV), [vp, C.c_int]),
+        "orc_session_seed_context": (C.c_int, [vp, C.c_int, C.c_uint64]),
         "orc_last_error": (C.c_char_p, []),
         "orc_gguf_load": (C.c_int, [C.c_char_p, C.POINTER(vp)]),
         "orc_gguf_free": (None, [vp]),
