@@ -191,6 +191,16 @@ OH_DEV double readlane_d(double v, int l) {
 // a row by DPP, then (row0 + row1) + (row2 + row3)); every lane gets it. Used
 // for sums of squares that the reference adds sequentially in double and
 // rounds to float afterwards.
+// sum over each 16-lane row (every lane of the row holds it): the first four
+// levels of wave_sum_d, so a 64-lane wave_sum_d equals (g0 + g1) + (g2 + g3)
+// over the four rows' g
+OH_DEV double row16_sum_d(double v) {
+    v += dpp_d<0xB1>(v);
+    v += dpp_d<0x4E>(v);
+    v += dpp_d<0x141>(v);
+    v += dpp_d<0x140>(v);
+    return v;
+}
 OH_DEV double wave_sum_d(double v) {
     v += dpp_d<0xB1>(v);
     v += dpp_d<0x4E>(v);

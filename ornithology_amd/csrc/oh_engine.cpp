@@ -309,6 +309,7 @@ struct Act {
     int pro = OH_PRO_Q8K, gdim = 0;
     const float *xf2 = nullptr, *nw = nullptr;
     const double *xruns = nullptr;
+    int runs16 = 0;            // xruns: 16-row partials (OH_OP_DELTA16) instead of 64-row run sums
     float eps = 0.0f;
     int8_t *oqs = nullptr;     // prologue result stored for later launches
     float *oqd = nullptr;
@@ -337,7 +338,7 @@ static int mv_add(MvBuild &b, const ornith_hip_tensor *W, const Act &act, float 
     memset(&s, 0, sizeof s);
     s.A = W->A; s.B = W->B; s.C = W->C;
     s.xqs = act.qs; s.xd = act.d; s.xbs = act.bs; s.xf = act.xf;
-    s.pro = act.pro; s.xf2 = act.xf2; s.nw = act.nw; s.eps = act.eps; s.gdim = act.gdim; s.xruns = act.xruns;
+    s.pro = act.pro; s.xf2 = act.xf2; s.nw = act.nw; s.eps = act.eps; s.gdim = act.gdim; s.xruns = act.xruns; s.runs16 = act.runs16;
     s.oqs = act.oqs; s.oqd = act.oqd; s.oqb = act.oqb; s.oxf = act.oxf;
     s.y = y;
     s.eidx = eidx;
@@ -1125,7 +1126,7 @@ struct ornith_hip_session {
     float *ddots = nullptr;       // step kernel's MoE down: slot dots [slots][hidden]
     int *dcnt = nullptr;          // step kernel's MoE down: blocks done per row group
     float *osz = nullptr;         // delta step: silu(gate) per output row
-    double *oruns = nullptr;      // delta step: sum of o^2 per 64-row run
+    double *oruns = nullptr;      // delta step: sum of o^2 per 16-row run (per 64 rows: the step kernel)
     int exact_max = 1024;         // contexts up to this walk the attention sum in one block
     int flash_mfma = 1;           // decode flash chunks on the matrix cores (ORNITH_HIP_FLASH_MFMA=0: VALU)
     float2 *rope = nullptr;
@@ -1314,8 +1315,11 @@ static Act act_of(const Q8Buf &q, const float *xf) {
 static Act act_norm(const float *x, const float *w, float eps) {
     Act a; a.pro = OH_PRO_NORM; a.xf = x; a.nw = w; a.eps = eps; return a;
 }
-static Act act_gnorm(const float *o, const float *sz, const double *runs, const float *w, float eps, int gdim) {
-    Act a; a.pro = OH_PRO_GNORM; a.xf = o; a.xf2 = sz; a.xruns = runs; a.nw = w; a.eps = eps; a.gdim = gdim; return a;
+static Act act_gnorm(const float *o, const float *sz, const double *runs, const float *w, float eps, int gdim,
+                     int runs16 = 0) {
+    Act a; a.pro = OH_PRO_GNORM; a.xf = o; a.xf2 = sz; a.xruns = runs; a.nw = w; a.eps = eps; a.gdim = gdim;
+    a.runs16 = runs16;
+    return a;
 }
 static Act act_swiglu(const float *g, const float *u) {
     Act a; a.pro = OH_PRO_SWIGLU; a.xf = g; a.xf2 = u; return a;
@@ -1355,7 +1359,7 @@ extern "C" int ornith_hip_session_new(ornith_hip_model *m, int cap, ornith_hip_s
     A_(salloc(s, &s->ddots, (size_t)(K + 1) * H + 64));
     A_(salloc(s, &s->dcnt, (size_t)H + 64));
     A_(salloc(s, &s->osz, (size_t)a.nv * a.dv + 64));
-    A_(salloc(s, &s->oruns, (size_t)a.nv * a.dv / 64 + 64));
+    A_(salloc(s, &s->oruns, (size_t)a.nv * a.dv / 16 + 64));
     {
         const char *e = getenv("ORNITH_HIP_EXACT_ATTN_MAX");
         if (e && *e) s->exact_max = atoi(e);
@@ -1485,15 +1489,16 @@ static int build_body(ornith_hip_session *s, Prog &P) {
             const float out_scale = 1.0f / sqrtf((float)a.dk);
             const double sb = 8.0 * a.nv * a.dk * a.dv + 8.0 * (a.conv_k - 1) * cc + 4.0 * cc * (a.conv_k + 1) +
                               12.0 * vd + 16.0 * a.nv;
-            oh_op o = op_new(OH_OP_DELTA, a.nv * (a.dk / 64), oh_delta_lds_bytes(a.dk));
+            // 16 state rows per 256-thread block (nv * dk / 16 blocks)
+            oh_op o = op_new(OH_OP_DELTA16, a.nv * (a.dk / 16), oh_delta16_lds_bytes(a.dk));
             o.u.delta = {s->cat, s->ab, s->gate, (const float *)y.conv->A, (const float *)y.ssm_a->A,
                          (const float *)y.dt_bias->A, z.conv, z.S, s->o, s->osz, s->oruns,
                          a.dk, a.nk, a.nv, a.conv_k, cc, out_scale};
             prog_add(P, o, K_DELTA, sb);
             // per-head gated RMSNorm of the delta output inside the projection
             MvBuild b2;
-            CHK(mv_add(b2, y.ssm_out, act_gnorm(s->o, s->osz, s->oruns, (const float *)y.ssm_norm->A, a.eps, a.dv),
-                       s->x, 1));
+            CHK(mv_add(b2, y.ssm_out,
+                       act_gnorm(s->o, s->osz, s->oruns, (const float *)y.ssm_norm->A, a.eps, a.dv, 1), s->x, 1));
             prog_mv(P, b2);
         }
         // FFN: post_attention_norm (formed inside the first FFN launch), then

@@ -288,6 +288,18 @@ hipError_t oh_launch_op(const oh_op *op, const int32_t *io, hipStream_t st) {
             return hipErrorInvalidValue;
         }
         break;
+    case OH_OP_DELTA16:
+        if (op->u.delta.K > 8) return hipErrorInvalidValue;
+        if (op->u.delta.dk == 128) {
+            if (op->u.delta.K <= 4) hipLaunchKernelGGL((oh_k_delta16<128, 4>), g, b256, 0, st, op->u.delta, io);
+            else hipLaunchKernelGGL((oh_k_delta16<128, 8>), g, b256, 0, st, op->u.delta, io);
+        } else if (op->u.delta.dk == 64) {
+            if (op->u.delta.K <= 4) hipLaunchKernelGGL((oh_k_delta16<64, 4>), g, b256, 0, st, op->u.delta, io);
+            else hipLaunchKernelGGL((oh_k_delta16<64, 8>), g, b256, 0, st, op->u.delta, io);
+        } else {
+            return hipErrorInvalidValue;
+        }
+        break;
     case OH_OP_ATTN_PREP: hipLaunchKernelGGL(oh_k_attn_prep, g, b256, 0, st, op->u.prep, io); break;
     case OH_OP_ATTN_MAIN: hipLaunchKernelGGL(oh_k_attn_main, g, b256, (size_t)op->lds, st, op->u.attn, io); break;
     case OH_OP_ATTN_COMBINE: hipLaunchKernelGGL(oh_k_attn_combine, g, b256, 0, st, op->u.attn, io); break;
@@ -338,6 +350,7 @@ int oh_exact_lds_bytes(int hd, int exact_max) {
 
 // delta step LDS of the working wave (step kernel: dynamic LDS)
 int oh_delta_lds_bytes(int dk) { return (2 * dk + 64 * (dk + 4)) * 4; }
+int oh_delta16_lds_bytes(int dk) { return delta16_lds_floats(dk) * 4; }
 
 hipError_t oh_step_blocks_per_cu(int lds_bytes, int *blocks) {
     hipError_t e = hipFuncSetAttribute((const void *)oh_k_step, hipFuncAttributeMaxDynamicSharedMemorySize, lds_bytes);

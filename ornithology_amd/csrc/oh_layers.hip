@@ -246,6 +246,195 @@ OH_DEV void delta_body(const oh_op_delta &a, int vb, int pos, float *lds, W &w) 
     if (lane == 0) stc(a.out_runs + vb, so);
 }
 
+// ---- the same decode step, 16 state rows per 256-thread block --------------------
+// delta_body's arithmetic spread over four times as many blocks with four
+// waves each: virtual block vb of nv * DK/16 takes rows [slab*16, +16) of
+// value head hv (256 blocks at C3). Every thread loads two float4 of the
+// 16 x DK state slab (contiguous, coalesced) before anything else and keeps
+// them in registers. Waves 0 and 1 form the conv + SiLU + L2 norm of the key
+// head's q and k channels (a lane per channel, lane + 64 i, as delta_body's
+// wave), wave 2's lanes 0..15 the 16 rows' v channels and silu(gate), wave 3's
+// lane 0 alpha and beta. The delta rule per row (s_c = S_c * alpha,
+// sk = sum s_c k_c, u = beta (v - sk), s_c += u k_c, o = sum s_c q_c, the
+// sums in column order) then runs as: every thread forms the products of its
+// eight elements (s_c k_c, later s_c q_c after the update, which it also
+// stores as the new state) into an LDS tile, and lanes 0..15 of wave 0 add
+// their row's products in column order; the same floats as delta_body's row
+// walk, with the chains reduced to adds. The sum of o^2 is left as 16-row
+// partials (row16_sum_d), whose (g0 + g1) + (g2 + g3) is delta_body's 64-row
+// run sum.
+// The conv window is double-buffered by position parity as in delta_body;
+// its q/k channels are written by slab 0 of value head kh (hv < nk).
+// lds: delta16_lds_floats(DK) floats.
+OH_HD constexpr int delta16_lds_floats(int dk) { return 2 * dk + 2 * 16 + 4 + 16 * (dk + 4); }
+
+template <int DK, int KMAX, class W>
+OH_DEV void delta16_body(const oh_op_delta &a, int vb, int pos, float *lds, W &w) {
+    constexpr int NQ = DK / 64, TS = DK + 4, RB = 16, NF = RB * DK / 4 / 256;
+    static_assert(NF >= 1 && RB * DK / 4 % 256 == 0, "16 rows of DK columns: whole float4 per thread");
+    float *qn = lds, *kn = lds + DK, *vrow = lds + 2 * DK, *urow = vrow + RB, *coef = urow + RB;
+    float *tile = coef + 4;                               // [RB][TS], 16-byte aligned
+    const int tid = tid_x(), lane = tid & 63, wave = tid >> 6;
+    const int nk = a.nk, nv = a.nv, K = a.K, cc = a.cc, qd = nk * DK;
+    const int hv = vb / (DK / RB), slab = vb % (DK / RB), kh = hv % nk;
+    const int r0 = slab * RB;                             // first row (within the head)
+    const int p = pos & 1;
+    const float *win = a.conv_state + (size_t)p * (K - 1) * cc;
+    float *nwin = a.conv_state + (size_t)(1 - p) * (K - 1) * cc;
+    // the state slab first (it does not depend on the previous phase)
+    const float4 *Sr = (const float4 *)(a.S + ((size_t)hv * DK + r0) * DK);
+    float4 st[NF];
+#pragma unroll
+    for (int i = 0; i < NF; i++) st[i] = ldg(Sr + tid + 256 * i);
+    // this lane's conv channels: q (wave 0) or k (wave 1) channels of key
+    // head kh, lane + 64 i; the v channel of row lane (wave 2, lanes < 16)
+    const bool qk = wave < 2, vl = wave == 2 && lane < RB;
+    int ch[NQ];
+#pragma unroll
+    for (int i = 0; i < NQ; i++)
+        ch[i] = qk ? (wave == 0 ? 0 : qd) + kh * DK + lane + 64 * i : 2 * qd + hv * DK + r0 + (lane & (RB - 1));
+    float cw[NQ][KMAX] = {}, wv[NQ][KMAX] = {}, sa = 0.0f, dtb = 0.0f;
+    if (qk || vl) {
+#pragma unroll
+        for (int i = 0; i < NQ; i++) {
+            if (i > 0 && !qk) break;
+            if (KMAX == 4 && K == 4) {
+                const float4 c4 = ldg((const float4 *)(a.conv_w + (size_t)ch[i] * 4));
+                cw[i][0] = c4.x; cw[i][1] = c4.y; cw[i][2] = c4.z; cw[i][3] = c4.w;
+            } else {
+#pragma unroll
+                for (int j = 0; j < KMAX; j++) cw[i][j] = j < K ? ldg(a.conv_w + (size_t)ch[i] * K + j) : 0.0f;
+            }
+#pragma unroll
+            for (int j = 0; j < KMAX; j++) wv[i][j] = j < K - 1 ? ldg(win + (size_t)j * cc + ch[i]) : 0.0f;
+        }
+    }
+    if (wave == 3 && lane == 0) {
+        sa = ldg(a.ssm_a + hv);
+        dtb = ldg(a.dt_bias + hv);
+    }
+    if (!w.wait()) return;
+    // this step's inputs from the input projection
+    float cx[NQ];
+#pragma unroll
+    for (int i = 0; i < NQ; i++) cx[i] = (qk || (vl && i == 0)) ? ldc(a.cat + ch[i]) : 0.0f;
+    const float gz = vl ? ldc(a.gate + (size_t)hv * DK + r0 + lane) : 0.0f;
+    float av = 0.0f, bv = 0.0f;
+    if (wave == 3 && lane == 0) {
+        av = ldc(a.ab + hv);
+        bv = ldc(a.ab + nv + hv);
+    }
+    // causal depthwise conv (no bias) + SiLU, in delta_body's order
+    float cv[NQ];
+#pragma unroll
+    for (int i = 0; i < NQ; i++) {
+        float acc = 0.0f, wl = 0.0f;
+#pragma unroll
+        for (int j = 0; j < KMAX; j++) {
+            if (j < K - 1) acc += cw[i][j] * wv[i][j];
+            if (j == K - 1) wl = cw[i][j];
+        }
+        acc += wl * cx[i];
+        cv[i] = ref_silu(acc);
+    }
+    const bool owner = vl || (qk && hv < nk && slab == 0);
+    if (owner) {
+#pragma unroll
+        for (int i = 0; i < NQ; i++) {
+            if (i > 0 && !qk) break;
+#pragma unroll
+            for (int j = 0; j + 1 < KMAX; j++)
+                if (j + 1 < K - 1) stg(nwin + (size_t)j * cc + ch[i], wv[i][j + 1]);
+            stg(nwin + (size_t)(K - 2) * cc + ch[i], cx[i]);
+        }
+    }
+    if (qk) {
+        // per-head L2 normalisation (src/ornith_tensor.c:155-160): double
+        // sums of each 64-channel run, then the runs in order
+        double t = 0.0;
+#pragma unroll
+        for (int i = 0; i < NQ; i++) {
+            const double sq = wave_sum_d((double)cv[i] * cv[i]);
+            t = i == 0 ? sq : t + sq;
+        }
+        const float inv = (float)(1.0 / sqrt(t + (double)1e-6f));
+        float *dst = wave == 0 ? qn : kn;
+#pragma unroll
+        for (int i = 0; i < NQ; i++) dst[lane + 64 * i] = cv[i] * inv;
+    } else if (vl) {
+        vrow[lane] = cv[0];
+        stc(a.out_gate + (size_t)hv * DK + r0 + lane, ref_silu(gz));
+    } else if (wave == 3 && lane == 0) {
+        coef[0] = ref_expf(sa * ref_softplus(av + dtb));
+        coef[1] = ref_sigmoid(bv);
+    }
+    __syncthreads();
+    // the products each row walk adds are formed element-parallel (every
+    // thread its eight elements), so the two ordered sums are adds only:
+    // pk_c = (S_c * alpha) * k_c into the tile
+    const float alpha = coef[0];
+    float4 sa4[NF];
+#pragma unroll
+    for (int i = 0; i < NF; i++) {
+        const int f = tid + 256 * i, row = (4 * f) / DK, col = (4 * f) % DK;
+        const float4 x = st[i], kk = *(const float4 *)(kn + col);
+        sa4[i] = make_float4(x.x * alpha, x.y * alpha, x.z * alpha, x.w * alpha);
+        *(float4 *)(tile + row * TS + col) =
+            make_float4(sa4[i].x * kk.x, sa4[i].y * kk.y, sa4[i].z * kk.z, sa4[i].w * kk.w);
+    }
+    __syncthreads();
+    // sk = sum_c pk_c in column order; u = beta (v - sk)
+    if (wave == 0 && lane < RB) {
+        const float *tr = tile + lane * TS;
+        float sk = 0.0f;
+#pragma unroll
+        for (int c = 0; c < DK / 4; c++) {
+            const float4 t = *(const float4 *)(tr + 4 * c);
+            sk += t.x;
+            sk += t.y;
+            sk += t.z;
+            sk += t.w;
+        }
+        urow[lane] = coef[1] * (vrow[lane] - sk);
+    }
+    __syncthreads();
+    // s_c += u k_c (the new state, stored) and po_c = s_c q_c into the tile
+    float4 *Sw = (float4 *)(a.S + ((size_t)hv * DK + r0) * DK);
+#pragma unroll
+    for (int i = 0; i < NF; i++) {
+        const int f = tid + 256 * i, row = (4 * f) / DK, col = (4 * f) % DK;
+        const float u = urow[row];
+        const float4 kk = *(const float4 *)(kn + col), qq = *(const float4 *)(qn + col);
+        float s0 = sa4[i].x, s1 = sa4[i].y, s2 = sa4[i].z, s3 = sa4[i].w;
+        s0 += u * kk.x;
+        s1 += u * kk.y;
+        s2 += u * kk.z;
+        s3 += u * kk.w;
+        stg(Sw + f, make_float4(s0, s1, s2, s3));
+        *(float4 *)(tile + row * TS + col) = make_float4(s0 * qq.x, s1 * qq.y, s2 * qq.z, s3 * qq.w);
+    }
+    __syncthreads();
+    // o = sum_c po_c in column order
+    if (wave == 0) {
+        float o = 0.0f;
+        if (lane < RB) {
+            const float *tr = tile + lane * TS;
+#pragma unroll
+            for (int c = 0; c < DK / 4; c++) {
+                const float4 t = *(const float4 *)(tr + 4 * c);
+                o += t.x;
+                o += t.y;
+                o += t.z;
+                o += t.w;
+            }
+            o *= a.out_scale;
+            stc(a.out + (size_t)hv * DK + r0 + lane, o);
+        }
+        const double g = row16_sum_d(lane < RB ? (double)o * o : 0.0);
+        if (lane == 0) stc(a.out_runs + vb, g);
+    }
+}
+
 // ---- GQA decode (src/ornith_rforward.c:419-455, src/ornith_attn.c:65-149) -------
 // prep: per-head RMSNorm + partial NeoX RoPE (cos/sin from a host-built table
 // of the reference's powf/cosf/sinf values), Q8 append of k and v at `pos`.
@@ -1068,6 +1257,13 @@ __global__ void __launch_bounds__(64) oh_k_delta_step(oh_op_delta a, const int32
     __shared__ __align__(16) float lds[2 * DK + 64 * (DK + 4)];
     NoWait w;
     delta_body<DK, KMAX>(a, (int)blockIdx.x, io[OH_IO_POS], lds, w);
+}
+
+template <int DK, int KMAX>
+__global__ void __launch_bounds__(256) oh_k_delta16(oh_op_delta a, const int32_t *io) {
+    __shared__ __align__(16) float lds[delta16_lds_floats(DK)];
+    NoWait w;
+    delta16_body<DK, KMAX>(a, (int)blockIdx.x, io[OH_IO_POS], lds, w);
 }
 
 extern "C" __global__ void __launch_bounds__(256) oh_k_attn_prep(oh_op_prep a, const int32_t *io) {

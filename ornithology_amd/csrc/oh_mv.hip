@@ -493,9 +493,18 @@ OH_DEV void mv_prologue(const oh_mvseg &s, int slot, int blk, uint8_t *smem, dou
         float *hinv = v + in;                          // [in / gdim]
         const int gd = s.gdim, rpg = gd / 64, nhd = in / gd;
         for (int h = tid; h < nhd; h += 256) {
-            const double *xr = s.xruns + ao / 64;      // the slot's run sums
-            double tot = ldc(xr + h * rpg);
-            for (int k = 1; k < rpg; k++) tot += ldc(xr + h * rpg + k);
+            double tot;
+            if (s.runs16) {
+                // 16-row partials: each 64-row run is (g0 + g1) + (g2 + g3)
+                const double *g = s.xruns + ao / 16 + (size_t)h * (gd / 16);
+                tot = (ldc(g) + ldc(g + 1)) + (ldc(g + 2) + ldc(g + 3));
+                for (int k = 1; k < rpg; k++)
+                    tot += (ldc(g + 4 * k) + ldc(g + 4 * k + 1)) + (ldc(g + 4 * k + 2) + ldc(g + 4 * k + 3));
+            } else {
+                const double *xr = s.xruns + ao / 64;  // the slot's run sums
+                tot = ldc(xr + h * rpg);
+                for (int k = 1; k < rpg; k++) tot += ldc(xr + h * rpg + k);
+            }
             hinv[h] = (float)(1.0 / sqrt(tot / (double)gd + (double)s.eps));
         }
         lds_barrier();
@@ -614,11 +623,17 @@ OH_DEV void pro_load(PIn &p, const oh_mvseg &s, int slot) {
             if (s.pro == OH_PRO_GNORM) p.c[k] = ldg((const float4 *)s.nw + i % (s.gdim / 4));
         }
         if (s.pro == OH_PRO_GNORM) {
-            // this thread's head (tid < in/gdim): its first two run sums
-            const int rpg = s.gdim / 64, nh = in / s.gdim, h = tid < nh ? tid : nh - 1;
-            const double *xr = s.xruns + ao / 64;      // the slot's run sums
-            p.r0 = ldc(xr + h * rpg);
-            p.r1 = ldc(xr + h * rpg + (rpg > 1 ? 1 : 0));
+            if (s.runs16) {
+                // 16-row partials (in/16 <= 256): this thread's one
+                const int n16 = in / 16;
+                p.r0 = ldc(s.xruns + ao / 16 + (tid < n16 ? tid : n16 - 1));
+            } else {
+                // this thread's head (tid < in/gdim): its first two run sums
+                const int rpg = s.gdim / 64, nh = in / s.gdim, h = tid < nh ? tid : nh - 1;
+                const double *xr = s.xruns + ao / 64;  // the slot's run sums
+                p.r0 = ldc(xr + h * rpg);
+                p.r1 = ldc(xr + h * rpg + (rpg > 1 ? 1 : 0));
+            }
         }
     }
 }
@@ -694,7 +709,19 @@ OH_DEV void pro_compute(const PIn &p, const oh_mvseg &s, int slot, int blk, uint
         // v = v * inv * w * silu(z)
         float *hinv = v;                            // [in/gdim]
         const int gd = s.gdim, rpg = gd / 64;
-        if (tid < in / gd) {
+        if (s.runs16) {
+            // the 16-row partials through LDS (after hinv's at most 64
+            // floats); each 64-row run is (g0 + g1) + (g2 + g3)
+            double *gp = (double *)(v + 64);
+            if (tid < in / 16) gp[tid] = p.r0;
+            lds_barrier();
+            if (tid < in / gd) {
+                const double *g = gp + tid * (gd / 16);
+                double tot = (g[0] + g[1]) + (g[2] + g[3]);
+                for (int k = 1; k < rpg; k++) tot += (g[4 * k] + g[4 * k + 1]) + (g[4 * k + 2] + g[4 * k + 3]);
+                hinv[tid] = (float)(1.0 / sqrt(tot / (double)gd + (double)s.eps));
+            }
+        } else if (tid < in / gd) {
             double tot = p.r0;
             if (rpg > 1) tot += p.r1;
             for (int k = 2; k < rpg; k++) tot += ldc(s.xruns + ao / 64 + tid * rpg + k);

@@ -113,6 +113,15 @@ OH_DEV void run_vb(const oh_op &op, int vb, int pos, W &w) {
             else delta_body<64, 8>(op.u.delta, vb, pos, (float *)smem, w);
         }
         break;
+    case OH_OP_DELTA16:
+        if (op.u.delta.dk == 128) {
+            if (op.u.delta.K <= 4) delta16_body<128, 4>(op.u.delta, vb, pos, (float *)smem, w);
+            else delta16_body<128, 8>(op.u.delta, vb, pos, (float *)smem, w);
+        } else {
+            if (op.u.delta.K <= 4) delta16_body<64, 4>(op.u.delta, vb, pos, (float *)smem, w);
+            else delta16_body<64, 8>(op.u.delta, vb, pos, (float *)smem, w);
+        }
+        break;
     case OH_OP_ATTN_PREP: prep_body(op.u.prep, vb, pos, w); break;
     case OH_OP_ATTN_MAIN: attn_main_body(op.u.attn, vb, pos, w); break;
     case OH_OP_ATTN_COMBINE: combine_body(op.u.attn, vb, pos, w); break;

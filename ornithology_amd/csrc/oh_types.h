@@ -94,6 +94,9 @@ typedef struct {
     const int16_t *xbs;
     const float *xf, *xf2, *nw;
     const double *xruns;
+    // runs16: xruns holds one double per 16-element run instead (slot k's at
+    // xruns + k*astride/16) and a 64-element run sum is (g0 + g1) + (g2 + g3)
+    // of its four
     // OH_PRO_NORM / OH_PRO_SWIGLU: the segment's first block also stores the
     // activation it formed (Q8_K planes and f32) for later launches
     int8_t *oqs;
@@ -103,7 +106,7 @@ typedef struct {
     float *y;                      // output, row o of slot k -> y[k*ystride + o]
     const int32_t *eidx;           // stacked experts: slot k uses expert eidx[k]
     float eps;
-    int pro, gdim;
+    int pro, gdim, runs16;
     int type, nb, in, rows, mode;  // mode 0: y = dot, 1: y += dot
     int nsub, ystride, astride;
     int adiv;                      // slot k reads the activation of slot k / adiv (0, 1: its own)
@@ -172,7 +175,8 @@ enum {
     OH_OP_MV = 0,          // u.mv, kernel variant tk
     OH_OP_MV_DOWN,         // u.down
     OH_OP_EMBED,           // u.embed
-    OH_OP_DELTA,           // u.delta
+    OH_OP_DELTA,           // u.delta (64 rows per virtual block, one wave; 64-row run sums)
+    OH_OP_DELTA16,         // u.delta (16 rows per 256-thread virtual block; 16-row run partials)
     OH_OP_ATTN_PREP,       // u.prep
     OH_OP_ATTN_MAIN,       // u.attn: the exact walk, or flash chunks past its limit
     OH_OP_ATTN_COMBINE,    // u.attn: merge of the flash chunks
