@@ -208,6 +208,18 @@ OH_DEV double wave_sum_d(double v) {
     v += dpp_d<0x140>(v);
     return (readlane_d(v, 0) + readlane_d(v, 16)) + (readlane_d(v, 32) + readlane_d(v, 48));
 }
+// float sum over the wave: DPP within each 16-lane row, then the rows
+OH_DEV float wave_sum_f(float v) {
+    v += __int_as_float(dpp_i<0xB1>(__float_as_int(v)));
+    v += __int_as_float(dpp_i<0x4E>(__float_as_int(v)));
+    v += __int_as_float(dpp_i<0x141>(__float_as_int(v)));
+    v += __int_as_float(dpp_i<0x140>(__float_as_int(v)));
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return (r0 + r1) + (r2 + r3);
+}
 OH_DEV int wave_sum_i(int v) {
     for (int m = 32; m >= 1; m >>= 1) v += shfl_xor(v, m);
     return v;

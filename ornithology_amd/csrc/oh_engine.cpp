@@ -325,9 +325,25 @@ struct MvBuild {
     MvBuild() { memset(&L, 0, sizeof L); }
 };
 
+// IQ2_XXS products of the token step summed as a tree over lanes (f32
+// arithmetic, each weight decoded exactly; a tolerance path) instead of the
+// reference's element-order f32 fallback (src/ornith_rforward.c:119-133):
+// ORNITH_HIP_IQ2_TREE=1, read when a step program is built. Off by default.
+static bool iq2_tree_on() {
+    const char *e = getenv("ORNITH_HIP_IQ2_TREE");
+    return e && e[0] == '1';
+}
+// the tree path takes IQ2_XXS rows of 512..4096 inputs (whole codebook
+// entries per lane) against an f32 activation the segment already holds
+static bool iq2_tree_can(uint32_t type, int64_t in) {
+    return type == OH_IQ2_XXS && (in == 512 || in == 1024 || in == 2048 || in == 4096) && iq2_tree_on();
+}
+
 static bool seg_q8(const oh_mvseg &s) {
     return oh_qdot_can((uint32_t)s.type, s.in) && (s.xqs || s.pro != OH_PRO_Q8K);
 }
+// a segment laid out in wave steps (integer path, or IQ2_XXS tree rows: one row per step)
+static bool seg_steps(const oh_mvseg &s) { return seg_q8(s) || s.iq2tree; }
 
 // rows: rows of one expert for stacked segments, else all rows of W. nsub
 // slots: slot k writes y + k*ystride and reads its activation at k*astride.
@@ -359,10 +375,13 @@ static int mv_add(MvBuild &b, const ornith_hip_tensor *W, const Act &act, float 
         return ORNITH_HIP_ERR_UNSUPPORTED;
     }
     const bool q8 = seg_q8(s);
+    s.iq2tree = !q8 && iq2_tree_can(W->type, W->in) && act.xf && (act.pro == OH_PRO_Q8K || act.pro == OH_PRO_F32);
     if (q8) {
         if (s.nb > 64) { seterr("matvec '%s': %d super-blocks per row (max 64)", W->name.c_str(), s.nb); return ORNITH_HIP_ERR_UNSUPPORTED; }
         const int rps = 64 / s.nb;                  // rows per wave step (one super-block per lane)
         s.units = (s.rows + rps - 1) / rps;
+    } else if (s.iq2tree) {
+        s.units = s.rows;                           // one row per wave step
     } else {
         if (!act.xf) { seterr("matvec '%s': no f32 activation for the fallback path", W->name.c_str()); return ORNITH_HIP_ERR_UNSUPPORTED; }
         if (W->in > 12288) { seterr("matvec '%s': fallback input %lld too wide", W->name.c_str(), (long long)W->in); return ORNITH_HIP_ERR_UNSUPPORTED; }
@@ -381,7 +400,7 @@ static int mv_add(MvBuild &b, const ornith_hip_tensor *W, const Act &act, float 
 // the same activation, emitting silu(W.x) * (W2.x)
 static bool pairable(const ornith_hip_tensor *W, const ornith_hip_tensor *W2) {
     return W && W2 && W->type == W2->type && W->in == W2->in && W->rows == W2->rows &&
-           oh_qdot_can(W->type, W->in) && W->nd == W2->nd;
+           (oh_qdot_can(W->type, W->in) || iq2_tree_can(W->type, W->in)) && W->nd == W2->nd;
 }
 static int mv_add_pair(MvBuild &b, const ornith_hip_tensor *W, const ornith_hip_tensor *W2, const Act &act,
                        float *y, const int32_t *eidx = nullptr, int nsub = 1, int ystride = 0) {
@@ -391,6 +410,11 @@ static int mv_add_pair(MvBuild &b, const ornith_hip_tensor *W, const ornith_hip_
     }
     CHK(mv_add(b, W, act, y, 0, eidx, nsub, ystride, 0));
     oh_mvseg &s = b.L.s[b.L.n - 1];
+    if (!seg_steps(s)) {
+        b.L.n--;
+        seterr("matvec pair '%s': the pair needs the integer or the IQ2_XXS tree path", W->name.c_str());
+        return ORNITH_HIP_ERR_UNSUPPORTED;
+    }
     s.A2 = W2->A; s.B2 = W2->B; s.C2 = W2->C;
     s.pair = 1;
     b.bytes += (double)nsub * (double)s.rows * (double)gguf_nbytes(W2->type, (uint64_t)W2->in);
@@ -405,9 +429,9 @@ static void mv_plan(MvBuild &b, int waves = 4096) {
     int tk = -2;
     for (int i = 0; i < b.L.n; i++) {
         const oh_mvseg &s = b.L.s[i];
-        if (seg_q8(s)) {
+        if (seg_steps(s)) {
             steps += (int64_t)s.units * s.nsub * (s.pair ? 2 : 1);
-            tk = tk == -2 || tk == s.type ? s.type : -1;
+            tk = (tk == -2 || tk == s.type) && !s.iq2tree ? s.type : -1;
         } else {
             tk = -1;
         }
@@ -419,7 +443,7 @@ static void mv_plan(MvBuild &b, int waves = 4096) {
     for (int i = 0; i < b.L.n; i++) {
         oh_mvseg &s = b.L.s[i];
         const bool q8 = seg_q8(s);
-        if (q8) {
+        if (seg_steps(s)) {
             s.upw = (int)(spw / (s.pair ? 2 : 1) > 0 ? spw / (s.pair ? 2 : 1) : 1);
             s.bps = (s.units + OH_MV_WAVES * s.upw - 1) / (OH_MV_WAVES * s.upw);
         } else {
@@ -432,6 +456,7 @@ static void mv_plan(MvBuild &b, int waves = 4096) {
         const int voff = (nb * 272 + nb * 36 + 15) & ~15;
         int need = voff + ((!q8 || s.pro != OH_PRO_Q8K) ? s.in * 4 : 0) + (s.pro == OH_PRO_GNORM ? 512 : 0);
         if (!q8 && s.type == OH_IQ2_XXS) need = ((voff + s.in * 4 + 15) & ~15) + 2048;   // + the grid
+        if (s.iq2tree) need = 0;                    // x in registers, the tables in static LDS
         if (need > b.lds) b.lds = need;
     }
     if (b.L.route && ((b.L.ne + 3) & ~3) * 4 > b.lds) b.lds = ((b.L.ne + 3) & ~3) * 4;

@@ -303,6 +303,24 @@ OH_DEV float sb_term(const SB<OH_Q8_0> &r, const int8_t *aq, const int16_t *, fl
     return yd * part;
 }
 
+// LDS tables of the IQ2_XXS tolerance path: the codebook and, per 7-bit
+// sign field, its byte mask (0xff where the weight is negative; bit 7 the
+// field's parity, the decoder's sign rule, src/ornith_quant.c:660-680)
+__shared__ uint64_t s_iq2_grid[256];
+__shared__ uint64_t s_iq2_sign[128];
+OH_DEV void iq2_tables_load() {
+    const int t = tid_x();
+    for (int i = t; i < 256; i += (int)blockDim.x) s_iq2_grid[i] = k_iq2_grid[i];
+    for (int i = t; i < 128; i += (int)blockDim.x) {
+        const uint32_t sg = (uint32_t)i | ((uint32_t)(__popc(i) & 1) << 7);
+        uint64_t m = 0;
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+            if ((sg >> j) & 1u) m |= 0xffull << (8 * j);
+        s_iq2_sign[i] = m;
+    }
+}
+
 // outputs are read by later phases of the step kernel (device-scope accesses)
 OH_DEV void emit(float *y, int mode, int row, float v) {
     if (mode == 1) stc(y + row, ldc(y + row) + v);
@@ -920,6 +938,116 @@ OH_DEV void route_block(const oh_mvlaunch &L, int tok, bool store, float *lg, in
     }
 }
 
+// IQ2_XXS rows in tolerance mode (segment flag iq2tree): the reference's f32
+// arithmetic (f32 activation, every weight decoded exactly, src/ornith_quant.c
+// :660-680) with the dot summed as a tree instead of in element order (its f32
+// fallback, src/ornith_rforward.c:119-133). Lane l of a wave owns elements
+// [l E, (l + 1) E) of every row (E = in / 64, whole 8-weight codebook
+// entries) and keeps that slice of x in registers; a wave walks its rows one
+// per step (gate and up rows of a pair in turn), with the next rows' words in
+// flight. Per row the lane adds, for each sub-block part it owns,
+// db * sum_j (g_j s_j) x_j (db = d (0.5 + ls) 0.25, the decoder's scale) and
+// the 64 lane sums meet in a butterfly.
+template <int E, class W>
+OH_DEV void iq2_tree(const oh_mvseg &s, int slot, int blk, int expert, W &w) {
+    constexpr int NSB = E >= 32 ? E / 32 : 1;       // sub-blocks the lane touches
+    constexpr int NGE = E >= 32 ? 4 : E / 8;        // codebook entries per touched sub-block
+    const int lane = lane_id(), wave = __builtin_amdgcn_readfirstlane(tid_x() >> 6);
+    const int nb = s.in / 256, e0 = lane * E;
+    const int sbl = e0 / 256, sub0 = (e0 % 256) / 32, ge0 = E >= 32 ? 0 : (e0 % 32) / 8;
+    const int u0 = (blk * OH_MV_WAVES + wave) * s.upw;
+    const int u1 = u0 + s.upw < s.units ? u0 + s.upw : s.units;
+    const int sps = s.pair ? 2 : 1;
+    const int S = u1 > u0 ? (u1 - u0) * sps : 0;
+    const int64_t row_base = (int64_t)expert * s.rows;
+    float *y = s.y + (size_t)slot * s.ystride;
+    const WP wp = {s.A, s.B, s.C}, wp2 = {s.A2, s.B2, s.C2};
+    iq2_tables_load();
+    struct RW { uint32_t q[2 * NSB]; uint32_t d; };
+    auto load = [&](RW &r, int st) {
+        int sc = st < S ? st : S - 1;
+        sc = sc < 0 ? 0 : sc;
+        int row = u0 + sc / sps;
+        row = row < s.units ? row : s.units - 1;
+        const WP &p = (sc & (sps - 1)) ? wp2 : wp;
+        const int64_t bi = (row_base + row) * nb + sbl;
+        const uint32_t *q = (const uint32_t *)(p.A + bi * 64) + 2 * sub0;
+        if constexpr (NSB == 2) {
+            const uint4 v = ldg((const uint4 *)q);
+            r.q[0] = v.x; r.q[1] = v.y; r.q[2] = v.z; r.q[3] = v.w;
+        } else {
+            const uint2 v = ldg((const uint2 *)q);
+            r.q[0] = v.x; r.q[1] = v.y;
+        }
+        r.d = ldg((const uint16_t *)(p.C + bi * 2));
+    };
+    RW ra, rb;
+    load(ra, 0);
+    if (!w.wait()) return;
+    // this lane's slice of the f32 activation (from an earlier launch)
+    const size_t ao = (size_t)(s.adiv > 1 ? slot / s.adiv : slot) * s.astride;
+    float x[E];
+    const float4 *x4 = (const float4 *)(s.xf + ao + e0);
+#pragma unroll
+    for (int i = 0; i < E / 4; i++) {
+        const float4 v = ldc4(x4 + i);
+        x[4 * i] = v.x; x[4 * i + 1] = v.y; x[4 * i + 2] = v.z; x[4 * i + 3] = v.w;
+    }
+    lds_barrier();                                   // the tables
+    auto dot = [&](const RW &r) {
+        const float dd = h2f((uint16_t)r.d);
+        float acc = 0.0f;
+#pragma unroll
+        for (int b = 0; b < NSB; b++) {
+            const uint32_t w0 = r.q[2 * b], w1 = r.q[2 * b + 1];
+            const float db = dd * (0.5f + (float)(w1 >> 28)) * 0.25f;
+            float part = 0.0f;
+#pragma unroll
+            for (int e = 0; e < NGE; e++) {
+                const int ge = ge0 + e;
+                const uint64_t g = s_iq2_grid[(w0 >> (8 * ge)) & 0xffu];
+                const uint64_t m = s_iq2_sign[(w1 >> (7 * ge)) & 127u];
+                const uint32_t ml = (uint32_t)m, mh = (uint32_t)(m >> 32);
+                const uint32_t sl = ((uint32_t)g ^ ml) + (ml & 0x01010101u);
+                const uint32_t sh = ((uint32_t)(g >> 32) ^ mh) + (mh & 0x01010101u);
+                const int xo = b * 32 + e * 8;
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    part = fmaf((float)(int8_t)(sl >> (8 * j)), x[xo + j], part);
+                    part = fmaf((float)(int8_t)(sh >> (8 * j)), x[xo + 4 + j], part);
+                }
+            }
+            acc = fmaf(db, part, acc);
+        }
+        return wave_sum_f(acc);
+    };
+    float gsum = 0.0f;
+    auto comp = [&](const RW &r, int st) {
+        const float t = dot(r);
+        const int row = u0 + st / sps;
+        if (s.pair) {
+            if ((st & 1) == 0) gsum = t;
+            else if (lane == 0) emit(y, 0, row, ref_silu(gsum) * t);
+        } else if (lane == 0) {
+            emit(y, s.mode, row, t);
+        }
+    };
+    int st = 0;
+    for (; st + 2 < S; st += 2) {
+        load(rb, st + 1);
+        comp(ra, st);
+        load(ra, st + 2);
+        comp(rb, st + 1);
+    }
+    if (st + 1 < S) {
+        load(rb, st + 1);
+        comp(ra, st);
+        comp(rb, st + 1);
+    } else if (st < S) {
+        comp(ra, st);
+    }
+}
+
 // Launch body. TK >= 0: every segment is an integer-path segment of type TK;
 // TK < 0: any mix, including fallback segments (one lane per row, the f32
 // activation in LDS). With L.route every block first routes the MoE and
@@ -952,6 +1080,13 @@ OH_DEV void mv_body(const oh_mvlaunch &L, int vb, W &w) {
     const int expert = !s.eidx ? 0 : (L.route ? rsel[L.tslots > 0 ? slot % L.tslots : slot] : ldc(s.eidx + slot));
     if (TK >= 0) {
         mv_seg<TK < 0 ? OH_Q4_K : TK>(s, slot, blk, expert, smem, red, w);
+    } else if (s.type == OH_IQ2_XXS && s.iq2tree) {
+        switch (s.in / 64) {
+        case 64: iq2_tree<64>(s, slot, blk, expert, w); break;
+        case 32: iq2_tree<32>(s, slot, blk, expert, w); break;
+        case 16: iq2_tree<16>(s, slot, blk, expert, w); break;
+        default: iq2_tree<8>(s, slot, blk, expert, w); break;
+        }
     } else if (oh_qdot_can((uint32_t)s.type, s.in) && (s.xqs || s.pro != OH_PRO_Q8K)) {
         switch (s.type) {
         case OH_Q4_K: mv_seg<OH_Q4_K>(s, slot, blk, expert, smem, red, w); break;

@@ -107,6 +107,7 @@ typedef struct {
     const int32_t *eidx;           // stacked experts: slot k uses expert eidx[k]
     float eps;
     int pro, gdim, runs16;
+    int iq2tree;                   // IQ2_XXS rows summed as a tree (tolerance; else the f32 fallback's order)
     int type, nb, in, rows, mode;  // mode 0: y = dot, 1: y += dot
     int nsub, ystride, astride;
     int adiv;                      // slot k reads the activation of slot k / adiv (0, 1: its own)

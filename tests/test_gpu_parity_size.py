@@ -15,6 +15,15 @@
   the bench uses (matrix-core products; attention past 1024 positions on the
   tolerance paths), then 64 greedy steps: identical greedy tokens, logits
   within 1e-2 relative L2 (north_star's bar).
+* A C4-width slice (hidden 4096, 512 experts top-10 with IQ2_XXS routed
+  experts, vocab 248320, 3 delta-net + 1 GQA layer): a 32-token prompt and 64
+  greedy steps through the token step, (a) on the reference's f32 fallback
+  for IQ2_XXS: bit-identical logits and tokens. (b) With the IQ2_XXS rows
+  summed as a tree over lanes (ORNITH_HIP_IQ2_TREE=1: f32 arithmetic, exact
+  decoded weights, another summation order) the distance to the oracle is
+  printed, not asserted: the expert products move by ~1e-6 relative
+  (test_c2_iq2xxs_tree_matvec_within_tolerance), which is enough to change
+  near-tied top-10 picks among 512 experts of this random model.
 """
 import ctypes as C
 import os
@@ -32,6 +41,10 @@ C3 = dict(hidden=2048, n_layers=40, vocab=248320, full_interval=4, nh=16, nkv=2,
           nk=16, nv=32, dhead=128, conv_k=4, ne=256, top_k=8, moe_inter=512, shared_inter=512,
           t_default=Q4_K, t_attn_v=Q6_K, t_ffn_down=Q6_K, t_output=Q4_K, t_embd=Q4_K,
           seed=0, sigma=0.02)
+C4 = dict(hidden=4096, n_layers=60, vocab=248320, full_interval=4, nh=32, nkv=2, hd=256,
+          nk=16, nv=64, dhead=128, conv_k=4, ne=512, top_k=10, moe_inter=1024, shared_inter=1024,
+          t_default=Q4_K, t_attn_v=Q4_K, t_ffn_down=Q4_K, t_output=Q4_K, t_embd=Q4_K,
+          t_exps=IQ2_XXS, seed=0, sigma=0.02)
 THREADS = min(os.cpu_count() or 8, 16)
 
 
@@ -168,3 +181,54 @@ def test_c3_width_slice_long_prompt_matches_oracle(hip_ctx, orc, tmp_path, monke
           f"tokens equal {int((toks == rtoks).sum())}/64")
     assert rel_l2(lp, rp) < 1e-2 and rel_l2(lf, rf) < 1e-2
     assert np.array_equal(toks, rtoks)
+
+
+@pytest.mark.timeout(1200)
+def test_c4_width_slice_iq2xxs_experts_vs_oracle(hip_ctx, orc, tmp_path, monkeypatch):
+    cfg = dict(C4, n_layers=4, seed=9)
+    t0 = time.time()
+    m = hip_ctx.synth(**cfg)
+    print(f"[c4 slice] synthesised in {time.time() - t0:.1f} s", flush=True)
+    prompt = clibs.ids(5, "c4s.prompt", 32, cfg["vocab"])
+    monkeypatch.setenv("ORNITH_HIP_IQ2_TREE", "0")
+    lp0, toks0, lf0 = gpu_run(m, prompt, 64)
+    monkeypatch.setenv("ORNITH_HIP_IQ2_TREE", "1")
+    lp1, toks1, lf1 = gpu_run(m, prompt, 64)
+    monkeypatch.delenv("ORNITH_HIP_IQ2_TREE")
+    path = os.path.join(shm_dir(tmp_path), "c4_slice_parity.gguf")
+    try:
+        clibs.write_model_gguf(m, cfg, path)
+        m.free()
+        # the token recurrence for the prompt, as the engine's token step
+        rp, rtoks, rf = oracle_run(orc, path, prompt, 64, serial=1)
+        print(f"[c4 slice] oracle done at {time.time() - t0:.1f} s", flush=True)
+    finally:
+        if os.path.exists(path):
+            os.unlink(path)
+    print(f"[c4 slice] f32 fallback: prompt rel L2 {rel_l2(lp0, rp):.3e}, final {rel_l2(lf0, rf):.3e}, "
+          f"tokens equal {int((toks0 == rtoks).sum())}/64")
+    print(f"[c4 slice] IQ2_XXS rows summed as a tree: prompt rel L2 {rel_l2(lp1, rp):.3e}, final {rel_l2(lf1, rf):.3e}, "
+          f"tokens equal {int((toks1 == rtoks).sum())}/64")
+    assert np.array_equal(toks0, rtoks)
+    assert np.array_equal(u32(lp0), u32(rp)) and np.array_equal(u32(lf0), u32(rf))
+    assert np.isfinite(lp1).all() and np.isfinite(lf1).all()
+
+
+@pytest.mark.parametrize("shape", [(4096, 1024), (1024, 4096), (2048, 512), (512, 256)])
+def test_c2_iq2xxs_tree_matvec_within_tolerance(hip_ctx, monkeypatch, shape):
+    """The IQ2_XXS tree path (ORNITH_HIP_IQ2_TREE=1) against the exact
+    element-order path (itself bit-exact against the oracle above) on C4's
+    expert shapes: relative L2 <= 1e-5 (printed)."""
+    n, out = shape
+    w = clibs.gauss(2, f"c2.iq2t.{n}.{out}", n * out, 0.02)
+    enc = hip_ctx.quantize(IQ2_XXS, w)
+    W = hip_ctx.upload("c2.iq2t", IQ2_XXS, enc, (n, out))
+    x = clibs.gauss(1, f"c2.act.{n}", n, 1.0)
+    monkeypatch.setenv("ORNITH_HIP_IQ2_TREE", "0")
+    y0 = W.matvec(x)
+    monkeypatch.setenv("ORNITH_HIP_IQ2_TREE", "1")
+    y1 = W.matvec(x)
+    W.free()
+    r = rel_l2(y1, y0)
+    print(f"[{n} x {out}] IQ2_XXS tree vs element order: rel L2 {r:.3e}")
+    assert np.isfinite(y1).all() and r <= 1e-5
