@@ -440,6 +440,120 @@ def c5_bench(args) -> int:
     return 0
 
 
+def timeline(args) -> int:
+    """C3 at the bench's context: where one decode step's time goes, stage by
+    stage, printed as markdown. (1) The per-launch HIP-graph step: each
+    launch of one eager step timed with HIP events (launch order, first delta
+    and first full-attention layer shown, then the per-stage mean over all
+    layers), and every kernel kind replayed back to back as in the roofline
+    figure. (2) The persistent step kernel (ORNITH_HIP_STEP=1): each phase
+    between grid barriers. (3) The persistent tagged-word decode kernel
+    (ORNITH_HIP_DECODE=1): each operation's critical-path share (the last
+    block's completion after the previous operation's) and, for the first
+    matvec, delta and MoE-down operations, the median per-block sub-phases."""
+    ctx = oa.Context(0)
+    model = ctx.synth(**C3)
+    sess = model.session(args.ctx + 64)
+    sess.eval(np.random.default_rng(0).integers(0, C3["vocab"], args.ctx, dtype=np.int64).astype(np.int32))
+    ms = sess.time_decode(32)
+    print(f"# C3 decode stage timeline ({args.ctx}-token context)\n")
+    print(f"HIP-graph step: {ms / 32:.3f} ms/token ({32 / (ms / 1e3):.1f} tok/s), 32 steps.\n")
+    prof = sess.profile_step()
+    names = {"matvec": "Q4_K matvec", "matvec_mixed": "mixed matvec", "matvec_q6k": "Q6_K matvec"}
+    full = C3["full_interval"]
+    # launch sequence per layer (the head's launches at the end)
+    seq, i = [], 1                                     # launch 0: embedding
+    per_layer = []
+    for l in range(C3["n_layers"]):
+        n = 8 if l % full == full - 1 else 6
+        per_layer.append(prof[i:i + n])
+        i += n
+    head = prof[i:]
+    print("## 1. Per-launch step (eager, HIP events around every launch)\n")
+    for l in (0, full - 1):
+        kind = "full-attention" if l % full == full - 1 else "delta-net"
+        print(f"Layer {l} ({kind}):\n\n| # | kernel | us | MB |\n|---|---|---|---|")
+        for j, (k, b, t) in enumerate(per_layer[l]):
+            print(f"| {j} | {names.get(k, k)} | {t * 1e3:.2f} | {b / 1e6:.2f} |")
+        print()
+    for kind, pick in (("delta-net", lambda l: l % full != full - 1), ("full-attention", lambda l: l % full == full - 1)):
+        rows = [per_layer[l] for l in range(C3["n_layers"]) if pick(l)]
+        n = len(rows[0])
+        print(f"Mean over the {len(rows)} {kind} layers:\n\n| stage | kernel | us |\n|---|---|---|")
+        tot = 0.0
+        for j in range(n):
+            us = float(np.mean([r[j][2] for r in rows])) * 1e3
+            tot += us
+            print(f"| {j} | {names.get(rows[0][j][0], rows[0][j][0])} | {us:.2f} |")
+        print(f"| | layer total | {tot:.2f} |\n")
+    print(f"Head: {', '.join(f'{k} {t * 1e3:.2f} us' for k, _, t in head)}; embedding {prof[0][2] * 1e3:.2f} us.\n")
+    print("Kernel kinds replayed back to back (one step's launches of a kind, HIP graph):\n")
+    print("| kind | launches/step | us/launch | MB/launch | GB/s |\n|---|---|---|---|---|")
+    for k in sorted({k for k, _, _ in prof}):
+        if sum(1 for kk, _, _ in prof if kk == k) < 2:
+            continue                                   # a single launch: the replay times the graph launch
+        try:
+            us, bpl, nps = sess.time_kind(k, reps=3)
+        except oa.HipError:
+            continue
+        print(f"| {k} | {nps} | {us:.2f} | {bpl / 1e6:.2f} | {bpl / (us * 1e-6) / 1e9:.1f} |")
+    print()
+    try:
+        ph = sess.profile_phases()
+        agg = {}
+        for k, b, us in ph:
+            e = agg.setdefault(k or "barrier tail", [0, 0.0])
+            e[0] += 1
+            e[1] += us
+        total = sum(v[1] for v in agg.values())
+        print("## 2. Persistent step kernel (phases between grid barriers)\n")
+        print(f"One body launch: {total:.1f} us over {len(ph)} phases.\n\n| kind | phases | us total | us/phase |\n"
+              "|---|---|---|---|")
+        for k, (n, us) in sorted(agg.items(), key=lambda kv: -kv[1][1]):
+            print(f"| {k} | {n} | {us:.1f} | {us / n:.2f} |")
+        print()
+    except oa.HipError as e:
+        print(f"## 2. Persistent step kernel: unavailable ({e})\n")
+    try:
+        ops = sess.profile_decode()
+        print("## 3. Persistent tagged-word decode kernel\n")
+        crit = {}
+        prev = 0.0
+        for k, first, last in ops:
+            e = crit.setdefault(k, [0, 0.0])
+            e[0] += 1
+            e[1] += last - prev
+            prev = last
+        print(f"One launch: {ops[-1][2]:.1f} us over {len(ops)} operations (critical path: each operation's "
+              "last block done after the previous one's).\n\n| operation | count | us total | us/op |\n|---|---|---|---|")
+        for k, (n, us) in sorted(crit.items(), key=lambda kv: -kv[1][1]):
+            print(f"| {k} | {n} | {us:.1f} | {us / n:.2f} |")
+        print("\nPer-block sub-phases (median over blocks, us): start -> inputs in LDS (the front wave's "
+              "fetch) -> activation formed -> done (the delta operation stamps only its start and end).\n\n"
+              "| op | kind | inputs | activation | dot + store | block total |\n|---|---|---|---|---|---|")
+        want = {"matvec": None, "delta": None, "moe_down": None}
+        for i, (k, _, _) in enumerate(ops):
+            if k in want and want[k] is None:
+                want[k] = i
+        for k, i in want.items():
+            if i is None:
+                continue
+            g = sess.profile_decode_op(i)
+            tot = float(np.median(g[:, 5] - g[:, 0]))
+            if np.all(g[:, 2] == 0):
+                print(f"| {i} | {k} | | | | {tot:.2f} |")
+                continue
+            d = np.median(np.diff(g[:, [0, 2, 4, 5]], axis=1), axis=0)
+            print(f"| {i} | {k} | {d[0]:.2f} | {d[1]:.2f} | {d[2]:.2f} | {tot:.2f} |")
+        print()
+    except oa.HipError as e:
+        print(f"## 3. Persistent decode kernel: unavailable ({e})\n")
+    sess.free()
+    model.free()
+    ctx.close()
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -454,12 +568,17 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--batch", type=int, default=8, help="sessions of the batch-decode figure (0: skip)")
     ap.add_argument("--batch-steps", type=int, default=32)
+    ap.add_argument("--timeline", action="store_true",
+                    help="print where one C3 decode step's time goes, stage by stage (markdown), then exit")
     ap.add_argument("--traffic-probe", metavar="KIND", default=None,
                     help="run one device copy of known size and a replay of one step's KIND launches "
                          "(for rocprofv3 FETCH_SIZE / WRITE_SIZE passes), then exit")
     ap.add_argument("--traffic-summarize", nargs=3, metavar=("KIND", "FETCH_CSV", "WRITE_CSV"), default=None,
                     help="turn the two counter CSVs of --traffic-probe runs into profiles/traffic.json")
     args = ap.parse_args()
+    if args.timeline:
+        args.ctx = 4096 if args.ctx is None else args.ctx
+        return timeline(args)
     if args.traffic_probe:
         return traffic_probe(args.traffic_probe)
     if args.traffic_summarize:
