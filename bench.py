@@ -153,7 +153,8 @@ def traffic_summarize(kind: str, fetch_csv: str, write_csv: str) -> int:
     for counter, path in (("FETCH_SIZE", fetch_csv), ("WRITE_SIZE", write_csv)):
         rows = _counter_rows(path, counter)
         copy = [v for _, n, v in rows if "copy" in n.lower() or "elementwise" in n.lower()]
-        kern = [v for _, n, v in rows if n.split("(")[0].strip() == sym]
+        # plain and templated kernel names ("void oh_k_delta16<128, 4>(...)")
+        kern = [v for _, n, v in rows if n.split("(")[0].split("<")[0].split()[-1] == sym]
         if not copy or not kern:
             print(f"traffic: no {counter} rows for the copy or {sym}", file=sys.stderr)
             return 1
@@ -340,7 +341,7 @@ def batch_decode(model: oa.Model, n: int, ctx_len: int, steps: int) -> dict:
 
 # profile kind -> kernel symbol (as rocprofv3 names it)
 KERNEL_SYMBOL = {"matvec": "oh_k_mv_q4k", "matvec_q6k": "oh_k_mv_q6k", "matvec_q80": "oh_k_mv_q80",
-                 "matvec_mixed": "oh_k_mv_mixed", "moe_down": "oh_k_mv_down", "delta_step": "oh_k_delta_step",
+                 "matvec_mixed": "oh_k_mv_mixed", "moe_down": "oh_k_mv_down", "delta_step": "oh_k_delta16",
                  "attn_main": "oh_k_attn_main", "attn_combine": "oh_k_attn_combine", "attn_prep": "oh_k_attn_prep",
                  "step_body": "oh_k_step", "step_head": "oh_k_step"}
 
