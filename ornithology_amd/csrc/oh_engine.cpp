@@ -1189,6 +1189,7 @@ struct ornith_hip_session {
         int32_t *RIDX = nullptr, *CNT = nullptr, *LIST = nullptr;
         float *Hh = nullptr, *HSH = nullptr, *OD = nullptr, *ODSH = nullptr, *STAGE = nullptr, *GR = nullptr;
         float *GU = nullptr, *GSH = nullptr;      // [gate | up] rows of the matrix-core pairs
+        float *WY = nullptr;                      // WY factors of the matrix-core delta chunks (on first use)
         int32_t *ITEMS = nullptr;
         Q8Buf XQ, OQ, OAQ, HQ, HSQ;
     } pf;
@@ -2148,6 +2149,14 @@ static bool batch_fused() {
     return !(e && e[0] == '0');
 }
 
+// the prompt's chunked delta scan on the matrix cores in its WY form (a
+// tolerance path: the chunk sums re-associated; ORNITH_HIP_DELTA_MFMA=1)
+// instead of the reference-order vector-ALU scan
+static bool delta_mfma_enabled() {
+    const char *e = getenv("ORNITH_HIP_DELTA_MFMA");
+    return e && e[0] == '1';
+}
+
 static int pf_chunk_tokens() {
     const char *e = getenv("ORNITH_HIP_PREFILL_CHUNK");
     int c = e && *e ? atoi(e) : kPfChunk;
@@ -2221,6 +2230,7 @@ static int pf_alloc(ornith_hip_session *s, int tc) {
     CHK(salloc(s, &p.GU, T * K * 2 * I)); CHK(salloc(s, &p.GSH, T * 2 * sI));
     CHK(salloc(s, &p.ITEMS, (T * K + 63) / 64 + ne + 2));
     p.tc = tc;
+    p.WY = nullptr;                       // sized for tc tokens on its first use
     return ORNITH_HIP_OK;
 }
 
@@ -2339,12 +2349,16 @@ static int pf_chunk(ornith_hip_session *s, int base, int T, bool chunked, hipStr
             HCHK(oh_launch_conv_rows(p.CAT, (const float *)y.conv->A, z.conv, p.CONV, p.STAGE, T, base, cc, a.conv_k, st));
             HCHK(oh_launch_qk_gates_rows(a.dk, p.CONV, p.A, p.Bg, (const float *)y.ssm_a->A,
                                          (const float *)y.dt_bias->A, p.QN, p.KN, p.AL, p.BE, T, a.nk, a.nv, cc, st));
-            if (chunked)
-                HCHK(oh_launch_delta_chunked(a.dk, p.QN, p.KN, p.CONV, p.AL, p.BE, p.GR, z.S, p.O, T, a.nk, a.nv, cc,
+            if (chunked) {
+                if (delta_mfma_enabled() && !p.WY)
+                    CHK(salloc(s, &p.WY, (size_t)oh_delta_wy_floats(p.tc, a.nv, a.dk) + 64));
+                HCHK(oh_launch_delta_chunked(a.dk, p.QN, p.KN, p.CONV, p.AL, p.BE, p.GR,
+                                             delta_mfma_enabled() ? p.WY : nullptr, z.S, p.O, T, a.nk, a.nv, cc,
                                              1.0f / sqrtf((float)a.dk), st));
-            else
+            } else {
                 HCHK(oh_launch_delta_scan(a.dk, p.QN, p.KN, p.CONV, p.AL, p.BE, z.S, p.O, T, a.nk, a.nv, cc,
                                           1.0f / sqrtf((float)a.dk), st));
+            }
             HCHK(oh_launch_gnorm_q8k_rows(p.O, p.Z, (const float *)y.ssm_norm->A, a.eps, vd, a.dv, T, p.OQ.qs,
                                           p.OQ.d, p.OQ.bs, st, p.OQ.bp));
             CHK(pf_mm(y.ssm_out, p.OQ, p.X, H, T, 1, st));

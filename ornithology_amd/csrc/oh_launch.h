@@ -30,9 +30,11 @@ hipError_t oh_launch_delta_scan(int dk, const float *qn, const float *kn, const 
                                 float out_scale, hipStream_t st);
 // the reference's chunked delta scan (grams per key head and chunk, then the scan)
 int oh_delta_grams_floats(int T, int nk);
+// wy non-null: the matrix-core WY form over that scratch (oh_delta_wy_floats)
 hipError_t oh_launch_delta_chunked(int dk, const float *qn, const float *kn, const float *conv, const float *al,
-                                   const float *be, float *grams, float *S, float *out, int T, int nk, int nv,
-                                   int cc, float out_scale, hipStream_t st);
+                                   const float *be, float *grams, float *wy, float *S, float *out, int T, int nk,
+                                   int nv, int cc, float out_scale, hipStream_t st);
+int oh_delta_wy_floats(int T, int nv, int dk);
 // z: the raw attention gate (silu applied here)
 // gated per-head RMSNorm (sums of squares per 64-element run, as the decode
 // step forms them) + Q8_K of T vectors
