@@ -105,27 +105,20 @@ int oh_delta_wy_floats(int T, int nv, int dk) { return (T + kWyC - 1) / kWyC * n
 hipError_t oh_launch_delta_chunked(int dk, const float *qn, const float *kn, const float *conv, const float *al,
                                    const float *be, float *grams, float *wy, float *S, float *out, int T, int nk,
                                    int nv, int cc, float out_scale, hipStream_t st) {
+    if (T <= 0) return hipSuccess;                // no chunk (the scan kernels read row c0 + C - 1)
     const dim3 gg(nk, (T + kDeltaChunk - 1) / kDeltaChunk);
     if (wy) {
         // the matrix-core WY form: grams, the chunks' factors, then the scan
         if (dk != 128 && dk != 64) return hipErrorInvalidValue;
-        const void *kfn = dk == 128 ? (const void *)oh_k_delta_mfma<128> : (const void *)oh_k_delta_mfma<64>;
-        static bool lds_set[2] = {false, false};      // the slab + chunk operands exceed 64 KiB
-        const int li = dk == 128 ? 0 : 1, lds = dk == 128 ? delta_mfma_lds_bytes(128) : delta_mfma_lds_bytes(64);
-        if (!lds_set[li]) {
-            const hipError_t e = hipFuncSetAttribute(kfn, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
-            if (e != hipSuccess) return e;
-            lds_set[li] = true;
-        }
         if (dk == 128) {
             hipLaunchKernelGGL(oh_k_delta_grams<128>, gg, dim3(256), 0, st, qn, kn, T, nk, grams);
             hipLaunchKernelGGL(oh_k_delta_wy<128>, dim3(nv, gg.y), dim3(256), 0, st, kn, conv, al, be, grams, wy, T, nk, nv, cc);
-            hipLaunchKernelGGL(oh_k_delta_mfma<128>, dim3(nv * 8), dim3(256), (size_t)lds, st, qn, kn, wy, S, out, T, nk, nv,
+            hipLaunchKernelGGL(oh_k_delta_mfma<128>, dim3(nv * 8), dim3(256), 0, st, qn, kn, wy, S, out, T, nk, nv,
                                out_scale);
         } else {
             hipLaunchKernelGGL(oh_k_delta_grams<64>, gg, dim3(256), 0, st, qn, kn, T, nk, grams);
             hipLaunchKernelGGL(oh_k_delta_wy<64>, dim3(nv, gg.y), dim3(256), 0, st, kn, conv, al, be, grams, wy, T, nk, nv, cc);
-            hipLaunchKernelGGL(oh_k_delta_mfma<64>, dim3(nv * 4), dim3(256), (size_t)lds, st, qn, kn, wy, S, out, T, nk, nv,
+            hipLaunchKernelGGL(oh_k_delta_mfma<64>, dim3(nv * 4), dim3(256), 0, st, qn, kn, wy, S, out, T, nk, nv,
                                out_scale);
         }
         return hipGetLastError();

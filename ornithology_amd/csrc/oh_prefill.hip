@@ -240,7 +240,12 @@ oh_k_delta_chunked(const float *qn, const float *kn, const float *conv, const fl
     __shared__ int mz[CH];                               // row i of M holds a zero (j < i)
     __shared__ __align__(16) float xs[RB * XS];
     const int tid = tid_x();
-    const int vb = (int)blockIdx.x, hv = vb / (DK / RB), slab = vb % (DK / RB), kh = hv % nk;
+    // blocks go to the 8 XCDs round-robin (XCD = block % 8); with nv % 8 == 0
+    // the slabs of a head share one XCD and its L2 copy of the head's inputs
+    constexpr int NS = DK / RB;
+    const int vb = (int)blockIdx.x;
+    const int hv = (nv & 7) == 0 ? ((vb >> 3) / NS) * 8 + (vb & 7) : vb / NS;
+    const int slab = (nv & 7) == 0 ? (vb >> 3) % NS : vb % NS, kh = hv % nk;
     const int qd = nk * DK, vd = nv * DK, r0 = hv * DK + slab * RB;
     const int r = tid % RB, g = tid / RB;                // projections, outputs, reload
     const int ur = tid / RB, ucg = tid % RB;             // update: row, column group
