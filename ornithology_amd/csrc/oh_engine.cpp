@@ -1190,6 +1190,7 @@ struct ornith_hip_session {
         float *Hh = nullptr, *HSH = nullptr, *OD = nullptr, *ODSH = nullptr, *STAGE = nullptr, *GR = nullptr;
         float *GU = nullptr, *GSH = nullptr;      // [gate | up] rows of the matrix-core pairs
         float *WY = nullptr;                      // WY factors of the matrix-core delta chunks (on first use)
+        float *XN = nullptr;                      // f32 normalised rows for the per-token expert kernels
         int32_t *ITEMS = nullptr;
         Q8Buf XQ, OQ, OAQ, HQ, HSQ;
     } pf;
@@ -2168,6 +2169,20 @@ static bool pf_mvb_ok(const ornith_hip_tensor *W) {
     return W && oh_qdot_can(W->type, W->in) && W->in <= 8192 && W->in / 256 <= 64;
 }
 
+// routed experts the grouped batched products handle: integer-path types,
+// gate and up a pair
+static bool pf_moe_grouped(const OhLayer &y) {
+    return pf_mvb_ok(y.gate_exps) && pf_mvb_ok(y.up_exps) && pf_mvb_ok(y.down_exps) && pairable(y.gate_exps, y.up_exps);
+}
+
+// other expert types (IQ2_XXS) run the token step's expert kernels over the
+// chunk's (token, expert) slots
+static bool pf_moe_slots_ok(const OhLayer &y) {
+    for (const ornith_hip_tensor *W : {y.gate_exps, y.up_exps, y.down_exps})
+        if (!W || W->in % 256 || W->in > 8192 || W->nd != 3) return false;
+    return true;
+}
+
 static bool pf_supported(const ornith_hip_model *m) {
     const ornith_hip_arch &a = m->a;
     if (a.hidden > 8192 || a.nv * a.dv > 8192 || a.nh * a.hd > 8192) return false;
@@ -2182,9 +2197,8 @@ static bool pf_supported(const ornith_hip_model *m) {
             if (a.dk != 64 && a.dk != 128) return false;
         }
         if (a.ne > 0) {
-            if (!pf_mvb_ok(y.router) || !pf_mvb_ok(y.gate_exps) || !pf_mvb_ok(y.up_exps) || !pf_mvb_ok(y.down_exps))
-                return false;
-            if (!pairable(y.gate_exps, y.up_exps) || a.moe_inter > 8192 || a.ne > 1024 || a.top_k > 64) return false;
+            if (!pf_mvb_ok(y.router) || (!pf_moe_grouped(y) && !pf_moe_slots_ok(y))) return false;
+            if (a.moe_inter > 8192 || a.ne > 1024 || a.top_k > 64) return false;
             if (y.gate_sh && (!pf_mvb_ok(y.gate_sh) || !pf_mvb_ok(y.up_sh) || !pf_mvb_ok(y.down_sh) ||
                               !pairable(y.gate_sh, y.up_sh) || a.shared_inter > 8192))
                 return false;
@@ -2229,6 +2243,7 @@ static int pf_alloc(ornith_hip_session *s, int tc) {
     CHK(salloc(s, &p.OD, T * K * H)); CHK(salloc(s, &p.ODSH, T * H));
     CHK(salloc(s, &p.GU, T * K * 2 * I)); CHK(salloc(s, &p.GSH, T * 2 * sI));
     CHK(salloc(s, &p.ITEMS, (T * K + 63) / 64 + ne + 2));
+    CHK(salloc(s, &p.XN, T * H));
     p.tc = tc;
     p.WY = nullptr;                       // sized for tc tokens on its first use
     return ORNITH_HIP_OK;
@@ -2363,23 +2378,54 @@ static int pf_chunk(ornith_hip_session *s, int base, int T, bool chunked, hipStr
                                           p.OQ.d, p.OQ.bs, st, p.OQ.bp));
             CHK(pf_mm(y.ssm_out, p.OQ, p.X, H, T, 1, st));
         }
-        HCHK(oh_launch_norm_q8k_rows(p.X, (const float *)y.post_norm->A, a.eps, H, T, nullptr, p.XQ.qs, p.XQ.d,
-                                     p.XQ.bs, st, p.XQ.bp));
+        const bool slots = a.ne > 0 && !pf_moe_grouped(y);
+        HCHK(oh_launch_norm_q8k_rows(p.X, (const float *)y.post_norm->A, a.eps, H, T, slots ? p.XN : nullptr, p.XQ.qs,
+                                     p.XQ.d, p.XQ.bs, st, p.XQ.bp));
         if (a.ne > 0) {
             const int K = a.top_k, I = a.moe_inter, sI = a.shared_inter;
             CHK(pf_mm(y.router, p.XQ, p.RL, a.ne, T, 0, st));
             if (y.gate_inp_sh) CHK(pf_mm(y.gate_inp_sh, p.XQ, p.SHL, 1, T, 0, st));
             HCHK(oh_launch_route_rows(p.RL, a.ne, K, y.gate_inp_sh ? p.SHL : nullptr, p.RIDX, p.RW,
                                       y.gate_inp_sh ? p.SHG : nullptr, T, st));
-            HCHK(oh_launch_group_pairs(p.RIDX, T * K, p.CNT, a.ne, p.LIST, T, st));
-            const int max_items = (T * K + 63) / 64 + a.ne;
-            HCHK(oh_launch_mmq_items(p.CNT, a.ne, p.ITEMS, st));
-            CHK(pf_swiglu(y.gate_exps, y.up_exps, p.XQ, I, T * K, T, p.HQ, p.GU, p.Hh, st, p.CNT, p.LIST, T, K, a.ne,
-                          p.ITEMS, max_items));
-            if (pf_use_mmq(y.down_exps, true, T))
-                CHK(pf_mmq(y.down_exps, nullptr, p.HQ, p.OD, H, T, 0, st, p.CNT, p.LIST, T, 1, p.ITEMS, max_items));
-            else
-                CHK(pf_mvb(y.down_exps, nullptr, p.HQ, p.OD, H, T, 0, st, p.CNT, p.LIST, T, 1, a.ne));
+            if (slots) {
+                // experts without integer products (IQ2_XXS): the reference's
+                // prompt runs the MoE per token (ffn_moe, src/ornith_rforward.c:
+                // 672-673), so these are the token step's expert launches over
+                // the chunk's T * K (token, expert) slots: slot t K + j is
+                // token t's j-th routed expert and reads token t's normalised
+                // row (and Q8_K planes) or its own silu(gate) * up
+                const Act ax = act_of(p.XQ, p.XN);
+                MvBuild b2, b3;
+                if (pairable(y.gate_exps, y.up_exps)) {
+                    CHK(mv_add_pair(b2, y.gate_exps, y.up_exps, ax, p.Hh, p.RIDX, T * K, I));
+                    b2.L.s[b2.L.n - 1].astride = H;
+                    b2.L.s[b2.L.n - 1].adiv = K;
+                    CHK(mv_go(b2, st));
+                    Act ah;
+                    ah.pro = OH_PRO_F32;
+                    ah.xf = p.Hh;
+                    CHK(mv_add(b3, y.down_exps, ah, p.OD, 0, p.RIDX, T * K, H, I));
+                } else {
+                    float *G = p.GU, *U = p.GU + (size_t)T * K * I;
+                    CHK(mv_add(b2, y.gate_exps, ax, G, 0, p.RIDX, T * K, I, H));
+                    b2.L.s[b2.L.n - 1].adiv = K;
+                    CHK(mv_add(b2, y.up_exps, ax, U, 0, p.RIDX, T * K, I, H));
+                    b2.L.s[b2.L.n - 1].adiv = K;
+                    CHK(mv_go(b2, st));
+                    CHK(mv_add(b3, y.down_exps, act_swiglu(G, U), p.OD, 0, p.RIDX, T * K, H, I));
+                }
+                CHK(mv_go(b3, st));
+            } else {
+                HCHK(oh_launch_group_pairs(p.RIDX, T * K, p.CNT, a.ne, p.LIST, T, st));
+                const int max_items = (T * K + 63) / 64 + a.ne;
+                HCHK(oh_launch_mmq_items(p.CNT, a.ne, p.ITEMS, st));
+                CHK(pf_swiglu(y.gate_exps, y.up_exps, p.XQ, I, T * K, T, p.HQ, p.GU, p.Hh, st, p.CNT, p.LIST, T, K,
+                              a.ne, p.ITEMS, max_items));
+                if (pf_use_mmq(y.down_exps, true, T))
+                    CHK(pf_mmq(y.down_exps, nullptr, p.HQ, p.OD, H, T, 0, st, p.CNT, p.LIST, T, 1, p.ITEMS, max_items));
+                else
+                    CHK(pf_mvb(y.down_exps, nullptr, p.HQ, p.OD, H, T, 0, st, p.CNT, p.LIST, T, 1, a.ne));
+            }
             if (y.gate_sh) {
                 CHK(pf_swiglu(y.gate_sh, y.up_sh, p.XQ, sI, T, T, p.HSQ, p.GSH, p.HSH, st));
                 CHK(pf_mm(y.down_sh, p.HSQ, p.ODSH, H, T, 0, st));

@@ -3,7 +3,9 @@ batched projections, src/ornith_rforward.c:647-682) in both of the
 reference's prompt modes: ORNITH_PREFILL_SERIAL=1 (token recurrence) against
 the reference and against the token-by-token path (ORNITH_HIP_PREFILL=0), and
 the default chunked delta scan (src/ornith_attn.c:215-349) against the
-reference's golden fixture and the oracle.
+reference's golden fixture and the oracle. MoE models with IQ2_XXS routed
+experts take the same batched path with the experts per (token, expert) slot
+(the reference's prompt runs ffn_moe per token).
 
 Bar: bit-exact prompt logits and 64 greedy tokens on C1 against the
 reference's serial golden fixture; bit-identical logits, tokens and session
@@ -147,12 +149,18 @@ def same_state(m, a, b):
 
 
 HD256 = dict(MIX, hd=256, seed=9)     # head_dim 256: the four-token exact prompt walk
+# IQ2_XXS routed experts (C4's type): the prompt runs the token step's expert
+# kernels over its (token, expert) slots, in the f32 fallback's element order
+# or (ORNITH_HIP_IQ2_TREE=1) as tree-summed gate/up pairs
+IQ2X = dict(MIX, t_exps=clibs.IQ2_XXS, seed=13)
 
 
-@pytest.mark.parametrize("cfg", ["moe", "dense", "hd256"])
+@pytest.mark.parametrize("cfg", ["moe", "dense", "hd256", "iq2", "iq2-tree"])
 @pytest.mark.parametrize("exact_max", [None, 0], ids=["exact", "flash"])
 def test_prefill_equals_token_path(hip_ctx, monkeypatch, cfg, exact_max):
-    m = hip_ctx.synth(**{"moe": MIX, "dense": DENSE, "hd256": HD256}[cfg])
+    if cfg == "iq2-tree":
+        monkeypatch.setenv("ORNITH_HIP_IQ2_TREE", "1")
+    m = hip_ctx.synth(**{"moe": MIX, "dense": DENSE, "hd256": HD256, "iq2": IQ2X, "iq2-tree": IQ2X}[cfg])
     a = m.arch
     rng = np.random.default_rng(3)
     # 300 tokens span four engine chunks of 96; then evals starting at odd and
