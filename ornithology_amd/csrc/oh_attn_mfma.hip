@@ -12,6 +12,14 @@
 // softmax in fp32. Tolerance bar as for the flash chunks (logits within 1e-2
 // relative L2 of the reference order).
 //
+// fp16 range: each per-position scale s = m * 2^e (m in [1, 2)) enters the
+// fp16 operands only as its significand, code * m (|.| < 254, so every
+// operand is a normal fp16 or zero, whatever the scales are); the exponents
+// are applied in fp32, exactly: a score is multiplied by its key's 2^e after
+// the product, and the output accumulator is held in units of 2^E, E the
+// largest V exponent of the tiles seen so far (rescaled exactly when E
+// grows), so a probability enters P as p * 2^(e - E) <= 1.
+//
 // Work: a block of 4 waves takes one KV head g and TPB prompt tokens; wave w
 // owns 32 query rows = (32 / G) tokens x the G query heads of g. Per KV tile of
 // 64 positions the block converts the Q8 codes to fp16 in LDS once; each wave
@@ -30,7 +38,7 @@ constexpr int kFaPS = kFaT + 8;           // P^T and V^T row stride (fp16): 144 
 
 OH_HD inline int fa_ks(int hd) { return hd + 8; }     // K row stride (fp16)
 OH_HD inline int fa_lds_bytes(int hd) {
-    return (kFaT * fa_ks(hd) + hd * kFaPS + 4 * 32 * kFaPS) * 2 + 2 * kFaT * 4;
+    return (kFaT * fa_ks(hd) + hd * kFaPS + 4 * 32 * kFaPS) * 2 + 4 * kFaT * 4 + 16;
 }
 
 namespace {
@@ -45,8 +53,11 @@ oh_k_attn_mfma_rows(oh_op_attn a, int base, int tf0, int nt) {
     _Float16 *K16 = (_Float16 *)fsm;                    // [64 positions][KS]
     _Float16 *V16 = K16 + kFaT * KS;                    // [HD dims][kFaPS]
     _Float16 *P16 = V16 + HD * kFaPS;                   // [4 waves][32 queries][kFaPS]
-    float *sKs = (float *)(P16 + 4 * 32 * kFaPS);       // [64]
-    float *sVs = sKs + kFaT;                            // [64]
+    float *sKs = (float *)(P16 + 4 * 32 * kFaPS);       // [64] K scale significands
+    float *sVs = sKs + kFaT;                            // [64] V scale significands
+    int *sKe = (int *)(sVs + kFaT);                     // [64] K scale exponents
+    int *sVe = sKe + kFaT;                              // [64] V scale exponents
+    int *sVE = sVe + kFaT;                              // the tile's largest V exponent
     const int tid = tid_x(), lane = lane_id(), wave = tid >> 6;
     const int lq = lane & 31, hf = lane >> 5;           // query column, K half
     const int g = (int)blockIdx.y, nkv = a.nkv, cap = a.cap;
@@ -83,6 +94,7 @@ oh_k_attn_mfma_rows(oh_op_attn a, int base, int tf0, int nt) {
 #pragma unroll
         for (int v = 0; v < 16; v++) o[d][v] = 0.0f;
     float m = -INFINITY, l = 0.0f;
+    int E = -1000;                                      // o is held in units of 2^E
 
     // raw codes of a tile: K words [HD/4][64 positions] as uint4 of four
     // positions, V tiles [4][HD][16 positions] as uint4, and the scales
@@ -114,11 +126,19 @@ oh_k_attn_mfma_rows(oh_op_attn a, int base, int tf0, int nt) {
     fetch(0);
     for (int tile = 0; tile < ntiles; tile++) {
         const int t0 = tile * kFaT;
-        // scales, then the codes times their scale as fp16 (positions past the
-        // block's context are zero)
+        // scales as significand and exponent, then the codes times the
+        // significand as fp16 (positions past the block's context are zero)
         if (tid < 2 * kFaT) {
             const int p = t0 + (tid & (kFaT - 1));
-            (tid < kFaT ? sKs : sVs)[tid & (kFaT - 1)] = p < ctx ? scl : 0.0f;
+            const float sc = p < ctx ? scl : 0.0f;
+            const bool nz = sc != 0.0f && isfinite(sc);
+            const int ex = nz ? ilogbf(sc) : -1000;
+            (tid < kFaT ? sKs : sVs)[tid & (kFaT - 1)] = nz ? ldexpf(sc, -ex) : (isfinite(sc) ? 0.0f : sc);
+            (tid < kFaT ? sKe : sVe)[tid & (kFaT - 1)] = nz ? ex : 0;
+            if (tid >= kFaT) {
+                const int em = wave_max_i(ex);          // wave 1 holds the V scales
+                if (tid == kFaT) *sVE = em;
+            }
         }
         __syncthreads();
 #pragma unroll
@@ -163,20 +183,27 @@ oh_k_attn_mfma_rows(oh_op_attn a, int base, int tf0, int nt) {
                     sc[pt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qf[s], sc[pt], 0, 0, 0);
                 }
             }
-            // causal mask, online softmax of this lane's query (its 32
-            // positions here, the other 32 in lane ^ 32)
+            // each key's scale exponent, then the causal mask and the online
+            // softmax of this lane's query (its 32 positions here, the other
+            // 32 in lane ^ 32)
             float mx = -INFINITY;
 #pragma unroll
             for (int pt = 0; pt < 2; pt++)
 #pragma unroll
-                for (int v = 0; v < 16; v++) {
-                    const int p = t0 + 32 * pt + 8 * (v >> 2) + 4 * hf + (v & 3);
-                    if (p > qpos) sc[pt][v] = -INFINITY;
-                    mx = fmaxf(mx, sc[pt][v]);
+                for (int vg = 0; vg < 4; vg++) {
+                    const int4 ke = *(const int4 *)(sKe + 32 * pt + 8 * vg + 4 * hf);
+                    const int kes[4] = {ke.x, ke.y, ke.z, ke.w};
+#pragma unroll
+                    for (int k = 0; k < 4; k++) {
+                        const int v = 4 * vg + k, p = t0 + 32 * pt + 8 * vg + 4 * hf + k;
+                        sc[pt][v] = p > qpos ? -INFINITY : ldexpf(sc[pt][v], kes[k]);
+                        mx = fmaxf(mx, sc[pt][v]);
+                    }
                 }
             mx = fmaxf(mx, __shfl_xor(mx, 32));
             const float mn = fmaxf(m, mx);
             const float corr = mn == -INFINITY ? 1.0f : __expf(m - mn);
+            const int En = E > *sVE ? E : *sVE;         // the output's new unit 2^En
             float ls = 0.0f;
             _Float16 *pw = P16 + (wave * 32 + lq) * kFaPS;
 #pragma unroll
@@ -184,22 +211,26 @@ oh_k_attn_mfma_rows(oh_op_attn a, int base, int tf0, int nt) {
 #pragma unroll
                 for (int vg = 0; vg < 4; vg++) {
                     fa_h4 h;
+                    const int4 ve = *(const int4 *)(sVe + 32 * pt + 8 * vg + 4 * hf);
+                    const int ves[4] = {ve.x, ve.y, ve.z, ve.w};
 #pragma unroll
                     for (int k = 0; k < 4; k++) {
                         const float x = sc[pt][4 * vg + k];
                         const float e = x == -INFINITY ? 0.0f : __expf(x - mn);
                         ls += e;
-                        h[k] = (_Float16)e;
+                        h[k] = (_Float16)ldexpf(e, ves[k] - En);
                     }
                     *(fa_h4 *)(pw + 32 * pt + 8 * vg + 4 * hf) = h;
                 }
             ls += __shfl_xor(ls, 32);
             l = l * corr + ls;
             m = mn;
+            const float co = ldexpf(corr, E - En);
+            E = En;
 #pragma unroll
             for (int d = 0; d < NDT; d++)
 #pragma unroll
-                for (int v = 0; v < 16; v++) o[d][v] *= corr;
+                for (int v = 0; v < 16; v++) o[d][v] *= co;
             wave_lds_sync();
             // O^T += V^T P^T over the tile's 64 positions
 #pragma unroll
@@ -225,8 +256,10 @@ oh_k_attn_mfma_rows(oh_op_attn a, int base, int tf0, int nt) {
         for (int vg = 0; vg < 4; vg++) {
             const int dim = 32 * d + 8 * vg + 4 * hf;
             const float4 gt = ldg((const float4 *)(a.gate + ob + dim));
-            const float4 r = make_float4(o[d][4 * vg] * inv * ref_sigmoid(gt.x), o[d][4 * vg + 1] * inv * ref_sigmoid(gt.y),
-                                         o[d][4 * vg + 2] * inv * ref_sigmoid(gt.z), o[d][4 * vg + 3] * inv * ref_sigmoid(gt.w));
+            const float4 r = make_float4(ldexpf(o[d][4 * vg], E) * inv * ref_sigmoid(gt.x),
+                                         ldexpf(o[d][4 * vg + 1], E) * inv * ref_sigmoid(gt.y),
+                                         ldexpf(o[d][4 * vg + 2], E) * inv * ref_sigmoid(gt.z),
+                                         ldexpf(o[d][4 * vg + 3], E) * inv * ref_sigmoid(gt.w));
             stg((float4 *)(a.out + ob + dim), r);
         }
 }

@@ -235,6 +235,14 @@ OH_DEV int row16_sum_i(int v) {
 }
 // wave-wide max / min: DPP within each 16-lane row, then the four rows'
 // results read out as scalars (uniform in every lane)
+// integer max over the wave (every lane active)
+OH_DEV int wave_max_i(int v) {
+    v = max(v, dpp_i<0xB1>(v)); v = max(v, dpp_i<0x4E>(v));
+    v = max(v, dpp_i<0x141>(v)); v = max(v, dpp_i<0x140>(v));
+    const int r0 = __builtin_amdgcn_readlane(v, 0), r1 = __builtin_amdgcn_readlane(v, 16);
+    const int r2 = __builtin_amdgcn_readlane(v, 32), r3 = __builtin_amdgcn_readlane(v, 48);
+    return max(max(r0, r1), max(r2, r3));
+}
 OH_DEV float wave_max_fast(float v) {
     v = fmaxf(v, dpp_f<0xB1>(v)); v = fmaxf(v, dpp_f<0x4E>(v));
     v = fmaxf(v, dpp_f<0x141>(v)); v = fmaxf(v, dpp_f<0x140>(v));

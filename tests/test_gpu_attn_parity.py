@@ -13,7 +13,8 @@ everything upstream.
   on the vector ALUs (=0), and the matrix-core prompt attention
   (oh_k_attn_mfma_rows), re-associate the softmax and V sums. Bar: relative
   L2 of the whole output vector <= 1e-5 for the decode forms and <= 1e-3 for
-  the fp16-operand prompt kernel (the values are printed).
+  the fp16-operand prompt kernel (the values are printed), also with K and V
+  scales outside fp16's range.
 Head geometries: C3's (16 q / 2 kv heads, head_dim 256) and C4's (32 / 2).
 """
 import ctypes as C
@@ -114,6 +115,66 @@ def test_prompt_attention_output_vs_oracle(hip_ctx, orc, monkeypatch, cfg):
         r = rel_l2(o, ref)
         worst = max(worst, r)
         print(f"prompt row at pos {pos}: attention output rel L2 {r:.3e}")
+        assert np.isfinite(o).all()
+    assert worst <= 1e-3
+    s.free()
+    m.free()
+
+
+def scale_kv_scales(path, cfg, layer, kexp, vexp):
+    """multiply the cached K and V scales of a full-attention layer in an
+    ORNSESS v1 file by 2^kexp and 2^vexp (exact)"""
+    b = bytearray(open(path, "rb").read())
+    off = 8 + 4 + 13 * 4 + 4 + 4 + 8 + 4                   # magic .. have_logits
+    cc = 2 * cfg["nk"] * cfg["dhead"] + cfg["nv"] * cfg["dhead"]
+    for l in range(cfg["n_layers"]):
+        if (l + 1) % cfg["full_interval"]:
+            off += cfg["nv"] * cfg["dhead"] * cfg["dhead"] * 4 + 8 + (cfg["conv_k"] - 1) * cc * 4
+            continue
+        quant, n, nkv, hd = np.frombuffer(bytes(b[off:off + 16]), np.int32)
+        assert quant == 1 and nkv == cfg["nkv"] and hd == cfg["hd"]
+        off += 16 + 2 * n * nkv * hd
+        if l == layer:
+            for e in (kexp, vexp):
+                sc = np.frombuffer(bytes(b[off:off + 4 * n * nkv]), np.float32)
+                b[off:off + 4 * n * nkv] = np.ldexp(sc, e).astype(np.float32).tobytes()
+                off += 4 * n * nkv
+        else:
+            off += 8 * n * nkv
+    open(path, "wb").write(bytes(b))
+
+
+@pytest.mark.parametrize("cfg", [C3H, C4H], ids=["c3-heads", "c4-heads"])
+@pytest.mark.parametrize("exp", [30, -30], ids=["scales-x2^30", "scales-x2^-30"])
+def test_prompt_attention_fp16_range(hip_ctx, orc, monkeypatch, tmp_path, cfg, exp):
+    """K and V scales far outside fp16's range (the cached scales of 200
+    positions multiplied by 2^30 or 2^-30 through a session snapshot, codes
+    times scale far past fp16's largest and below its smallest normal): the
+    matrix-core prompt attention carries each scale's exponent in fp32, so a
+    following 64-token chunk's rows (all past the exact walk, limited to 64
+    positions here) stay within the same bar against the oracle over that
+    cache."""
+    monkeypatch.setenv("ORNITH_HIP_EXACT_ATTN_MAX", "64")
+    m = hip_ctx.synth(**cfg)
+    prompt = clibs.ids(33, "attn.prompt3", 264, cfg["vocab"])
+    s = m.session(300)
+    s.eval(prompt[:200])
+    path = str(tmp_path / "kv.ornsess")
+    s.save(path)
+    s.free()
+    layer = cfg["n_layers"] - 1
+    scale_kv_scales(path, cfg, layer, exp, exp)
+    s = m.load_session(path, 100)
+    ks = s.kv(layer)[1]
+    assert np.isfinite(ks).all()
+    s.eval(prompt[200:])
+    worst = 0.0
+    for row in (0, 31, 63):
+        o, ref, pos = check(orc, s, cfg, row)
+        r = rel_l2(o, ref)
+        worst = max(worst, r)
+        print(f"scales x2^{exp}, prompt row at pos {pos}: attention output rel L2 {r:.3e} "
+              f"(|o| max {float(np.max(np.abs(ref))):.3e})")
         assert np.isfinite(o).all()
     assert worst <= 1e-3
     s.free()
