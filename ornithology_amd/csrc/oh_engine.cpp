@@ -448,14 +448,21 @@ static void mv_plan(MvBuild &b, int waves = 4096) {
             s.bps = (s.units + OH_MV_WAVES * s.upw - 1) / (OH_MV_WAVES * s.upw);
         } else {
             s.upw = 1;
-            s.bps = s.type == OH_IQ2_XXS ? (s.rows + OH_IQ2_ROWS - 1) / OH_IQ2_ROWS : (s.rows + 255) / 256;
+            // IQ2_XXS fallback rows: the split form when the inputs are wide
+            // and one lane per row would leave most of the GPU idle
+            s.iq2split = s.type == OH_IQ2_XXS && s.in >= 2048 &&
+                         (int64_t)(s.rows + OH_IQ2_ROWS_LANE - 1) / OH_IQ2_ROWS_LANE * s.nsub < 256;
+            const int rpb = s.type != OH_IQ2_XXS ? 256 : s.iq2split ? OH_IQ2_ROWS : OH_IQ2_ROWS_LANE;
+            s.bps = (s.rows + rpb - 1) / rpb;
         }
         s.block0 = blocks;
         blocks += s.bps * s.nsub;
         const int nb = s.in / 256;
         const int voff = (nb * 272 + nb * 36 + 15) & ~15;
         int need = voff + ((!q8 || s.pro != OH_PRO_Q8K) ? s.in * 4 : 0) + (s.pro == OH_PRO_GNORM ? 512 : 0);
-        if (!q8 && s.type == OH_IQ2_XXS) need = ((voff + s.in * 4 + 15) & ~15) + 2048;   // + the grid
+        // + the grid (and the split form's two [OH_IQ2_ROWS][96 + 4] term tiles)
+        if (!q8 && s.type == OH_IQ2_XXS)
+            need = ((voff + s.in * 4 + 15) & ~15) + 2048 + (s.iq2split ? 2 * OH_IQ2_ROWS * 100 * 4 : 0);
         if (s.iq2tree) need = 0;                    // x in registers, the tables in static LDS
         if (need > b.lds) b.lds = need;
     }

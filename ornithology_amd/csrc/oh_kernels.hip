@@ -19,13 +19,15 @@ hipError_t oh_launch_matvec(const oh_mvlaunch *L, int tk, int lds_bytes, hipStre
     void (*k)(oh_mvlaunch) = tk == OH_Q4_K ? oh_k_mv_q4k : tk == OH_Q6_K ? oh_k_mv_q6k
                            : tk == OH_Q8_0 ? oh_k_mv_q80 : oh_k_mv_mixed;
     if (lds_bytes > 65536) {
-        // wide fallback rows (IQ2_XXS products, f32 activations past 8K)
-        static bool raised[4];
+        // wide fallback rows (IQ2_XXS term tiles, f32 activations past 8K):
+        // the kernel's dynamic LDS limit raised to what this launch needs
+        // (the limit plus the kernel's static LDS stays within the CU's)
+        static int raised[4];
         const int ki = tk == OH_Q4_K ? 0 : tk == OH_Q6_K ? 1 : tk == OH_Q8_0 ? 2 : 3;
-        if (!raised[ki]) {
-            const hipError_t e = hipFuncSetAttribute((const void *)k, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+        if (raised[ki] < lds_bytes) {
+            const hipError_t e = hipFuncSetAttribute((const void *)k, hipFuncAttributeMaxDynamicSharedMemorySize, lds_bytes);
             if (e != hipSuccess) return e;
-            raised[ki] = true;
+            raised[ki] = lds_bytes;
         }
     }
     hipLaunchKernelGGL(k, dim3(L->total_blocks), dim3(256), (size_t)lds_bytes, st, *L);

@@ -396,19 +396,32 @@ OH_HD inline int mv_lds_d_off(int nb) { return nb * kAS + nb * 32; }
 OH_HD inline int mv_lds_v_off(int nb) { return (nb * kAS + nb * 36 + 15) & ~15; }
 
 // IQ2_XXS rows (src/ornith_quant.c:660-680 decode, then ot_dot's strictly
-// sequential f32 accumulation, src/ornith_rforward.c:119-133): one lane per
-// row walks its row in element order, forming y_i * x_i and adding it at once.
-// y = (db * g) * (+-1), so y * x = +-((db * g) * x) exactly, and acc + (-t) is
-// acc - t. The f32 activation and the 256-entry grid sit in LDS (every lane
-// reads the same activation word); each row's next super-block (64 code bytes
-// and d) is in flight while the current one is reduced. LDS after v: the grid.
+// sequential f32 accumulation, src/ornith_rforward.c:119-133). A row's sum is
+// one chain of adds in element order; its terms are not: y_i * x_i with
+// y = (db * g) * (+-1) is +-((db * g) * x) exactly.
+//
+// iq2_rows_lane: one lane per row walks its row in element order, forming
+// each term and adding it at once (256 rows per block); each row's next
+// super-block (64 code bytes and d) is in flight while the current one is
+// reduced. Used when the launch has rows enough to fill the GPU this way.
+//
+// iq2_rows (few rows, wide inputs: the decode step's experts) takes 64 rows:
+// waves 1..3 form the terms of one 32-element sub-block each per chunk (lane =
+// row) into a double-buffered LDS tile [64 rows][96 + 4], and wave 0 adds a
+// chunk's terms in order while the next chunk is formed; the chunk barrier
+// hands a tile over. The f32 activation and the 256-entry grid sit in LDS
+// (every lane reads the same activation word); each producer's next
+// sub-block (two code words and d) is in flight while it forms the current.
+constexpr int kIq2P = 3, kIq2E = 32 * kIq2P, kIq2S = kIq2E + 4;   // producers, terms per chunk, tile row stride
+constexpr int kIq2D = 6;                                            // chunks of codes in flight per producer
 OH_HD inline int mv_lds_iq2_off(int nb, int in) { return (mv_lds_v_off(nb) + in * 4 + 15) & ~15; }
+OH_HD inline int mv_lds_iq2t_off(int nb, int in) { return mv_lds_iq2_off(nb, in) + 2048; }
 
-OH_DEV void iq2_rows(const oh_mvseg &s, int slot, int blk, int expert, uint8_t *smem) {
+OH_DEV void iq2_rows_lane(const oh_mvseg &s, int slot, int blk, int expert, uint8_t *smem) {
     const int in = s.in, nb = in / 256, tid = tid_x();
     const float *v = (const float *)(smem + mv_lds_v_off(nb));
     uint64_t *grid = (uint64_t *)(smem + mv_lds_iq2_off(nb, in));
-    const int row = blk * OH_IQ2_ROWS + tid;
+    const int row = blk * OH_IQ2_ROWS_LANE + tid;
     const int64_t bi0 = ((int64_t)expert * s.rows + (row < s.rows ? row : s.rows - 1)) * nb;
     uint4 qa[4], qn[4];
     uint16_t da, dn;
@@ -450,6 +463,84 @@ OH_DEV void iq2_rows(const oh_mvseg &s, int slot, int blk, int expert, uint8_t *
         da = dn;
     }
     if (row < s.rows) emit(s.y + (size_t)slot * s.ystride, s.mode, row, acc);
+}
+
+OH_DEV void iq2_rows(const oh_mvseg &s, int slot, int blk, int expert, uint8_t *smem) {
+    const int in = s.in, nb = in / 256, nsb = in / 32, tid = tid_x(), lane = tid & 63, wave = tid >> 6;
+    const float *v = (const float *)(smem + mv_lds_v_off(nb));
+    uint64_t *grid = (uint64_t *)(smem + mv_lds_iq2_off(nb, in));
+    float *tile = (float *)(smem + mv_lds_iq2t_off(nb, in));       // [2][OH_IQ2_ROWS][kIq2S]
+    const int row = blk * OH_IQ2_ROWS + lane;
+    const int64_t bi0 = ((int64_t)expert * s.rows + (row < s.rows ? row : s.rows - 1)) * nb;
+    const int nch = (nsb + kIq2P - 1) / kIq2P;
+    // a producer's code words and d for its next kIq2D chunks (a chunk's
+    // terms take well under one memory round trip)
+    uint2 wq[kIq2D];
+    uint16_t dq[kIq2D];
+    auto fetch = [&](int c, uint2 &w, uint16_t &d) {   // producer wave - 1: sub-block c * kIq2P + wave - 1
+        const int sb = c * kIq2P + wave - 1, sbc = sb < nsb ? sb : nsb - 1;
+        w = ldg((const uint2 *)(s.A + (bi0 + sbc / 8) * 64 + (sbc % 8) * 8));
+        d = ldg((const uint16_t *)(s.C + (bi0 + sbc / 8) * 2));
+    };
+    if (wave > 0) {
+#pragma unroll
+        for (int i = 0; i < kIq2D; i++) fetch(i < nch ? i : nch - 1, wq[i], dq[i]);
+    }
+    grid[tid] = k_iq2_grid[tid];
+    lds_barrier();
+    float acc = 0.0f;
+    for (int c = 0; c <= nch; c++) {
+        if (wave > 0 && c < nch) {
+            // terms of sub-block sb into tile c & 1, columns (wave - 1) * 32 ..
+            const int sb = c * kIq2P + wave - 1;
+            const uint2 w = wq[0];
+            const uint16_t d16 = dq[0];
+#pragma unroll
+            for (int i = 0; i + 1 < kIq2D; i++) {
+                wq[i] = wq[i + 1];
+                dq[i] = dq[i + 1];
+            }
+            const int cn = c + kIq2D < nch ? c + kIq2D : nch - 1;
+            fetch(cn, wq[kIq2D - 1], dq[kIq2D - 1]);
+            if (sb < nsb) {
+                const float dd = h2f(d16);
+                const uint32_t w0 = w.x, w1 = w.y;
+                const float db = dd * (0.5f + (float)(w1 >> 28)) * 0.25f;
+                const float4 *xb = (const float4 *)(v + sb * 32);
+                float *dst = tile + ((c & 1) * OH_IQ2_ROWS + lane) * kIq2S + (wave - 1) * 32;
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    const uint64_t gv = grid[(w0 >> (8 * k)) & 0xffu];
+                    const uint32_t s7 = (w1 >> (7 * k)) & 127u;
+                    const uint32_t sg = s7 | ((__popc(s7) & 1u) << 7);
+                    const float4 x0 = xb[2 * k], x1 = xb[2 * k + 1];
+                    const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+                    float ts[8];
+#pragma unroll
+                    for (int j = 0; j < 8; j++) {
+                        const float t = db * (float)((uint32_t)(gv >> (8 * j)) & 0xffu) * xs[j];
+                        ts[j] = (sg >> j) & 1u ? -t : t;
+                    }
+                    *(float4 *)(dst + 8 * k) = make_float4(ts[0], ts[1], ts[2], ts[3]);
+                    *(float4 *)(dst + 8 * k + 4) = make_float4(ts[4], ts[5], ts[6], ts[7]);
+                }
+            }
+        }
+        if (wave == 0 && c > 0) {
+            // the previous chunk's terms of this lane's row, in element order
+            const int e0 = (c - 1) * kIq2E, ne = in - e0 < kIq2E ? in - e0 : kIq2E;
+            const float *src = tile + (((c - 1) & 1) * OH_IQ2_ROWS + lane) * kIq2S;
+            for (int e = 0; e < ne; e += 4) {
+                const float4 q = *(const float4 *)(src + e);
+                acc += q.x;
+                acc += q.y;
+                acc += q.z;
+                acc += q.w;
+            }
+        }
+        lds_barrier();                              // the producers' next codes stay in flight
+    }
+    if (wave == 0 && row < s.rows) emit(s.y + (size_t)slot * s.ystride, s.mode, row, acc);
 }
 
 OH_DEV float4 f4_silu_mul(const float4 g, const float4 u) {
@@ -1097,7 +1188,8 @@ OH_DEV void mv_body(const oh_mvlaunch &L, int vb, W &w) {
         if (!w.wait()) return;
         mv_prologue(s, slot, blk, smem, red, false);
         if (s.type == OH_IQ2_XXS) {
-            iq2_rows(s, slot, blk, expert, smem);
+            if (s.iq2split) iq2_rows(s, slot, blk, expert, smem);
+            else iq2_rows_lane(s, slot, blk, expert, smem);
             return;
         }
         const float *v = (const float *)(smem + mv_lds_v_off(s.in / 256));

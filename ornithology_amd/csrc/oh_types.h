@@ -108,6 +108,7 @@ typedef struct {
     float eps;
     int pro, gdim, runs16;
     int iq2tree;                   // IQ2_XXS rows summed as a tree (tolerance; else the f32 fallback's order)
+    int iq2split;                  // IQ2_XXS fallback rows: adding wave + term-forming waves (else one lane per row)
     int type, nb, in, rows, mode;  // mode 0: y = dot, 1: y += dot
     int nsub, ystride, astride;
     int adiv;                      // slot k reads the activation of slot k / adiv (0, 1: its own)
@@ -120,8 +121,11 @@ typedef struct {
 #define OH_MAX_SEGS 8
 // blocks used by the argmax's first stage (the caller sizes its scratch)
 #define OH_ARGMAX_BLOCKS 256
-// IQ2_XXS rows of the f32 fallback per 256-thread block (one lane per row)
-#define OH_IQ2_ROWS 256
+// IQ2_XXS rows of the f32 fallback per 256-thread block: one lane per row,
+// or (segment flag iq2split) a lane of the adding wave per row with three
+// waves forming the terms
+#define OH_IQ2_ROWS_LANE 256
+#define OH_IQ2_ROWS 64
 #define OH_MV_WAVES 4              // waves per matvec block
 #define OH_MV_R 4                  // steps per prefetch batch of a wave
 // A launch with `route` set first routes the MoE in every block: top-k over
