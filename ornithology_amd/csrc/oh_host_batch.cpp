@@ -1,0 +1,558 @@
+// oh_host_batch.cpp - decode of several sessions at once (ornith_hip_batch_step).
+#include "oh_engine.h"
+
+
+// ---- decode of several sessions at once -------------------------------------------------
+// One token step (rforward_token, src/ornith_rforward.c:686-706) for each of n
+// sessions of one model: the projections batched over the sessions
+// (matmul_batch_q's Tn columns, src/ornith_rforward.c:91-196), the recurrent
+// state, KV cache and attention of each session by the decode step's own
+// kernels. Each column's arithmetic is its session's token step.
+int bw_alloc(ornith_hip_session *s, int n, size_t ops_bytes) {
+    auto &p = s->bw;
+    if (p.n >= n && p.ops_bytes >= ops_bytes) return ORNITH_HIP_OK;
+    const ornith_hip_arch &a = s->m->a;
+    const size_t N = (size_t)(n > p.n ? n : p.n), H = a.hidden, qd = (size_t)a.nk * a.dk, vd = (size_t)a.nv * a.dv;
+    const size_t cc = 2 * qd + vd, aq = (size_t)a.nh * a.hd, kvd = (size_t)a.nkv * a.hd;
+    const size_t K = a.top_k > 0 ? a.top_k : 1, I = a.moe_inter > 0 ? a.moe_inter : 1;
+    const size_t sI = a.shared_inter > 0 ? a.shared_inter : 1, ne = a.ne > 0 ? a.ne : 1;
+    CHK(salloc(s, &p.X, N * H)); CHK(q8alloc(s, p.XQ, N * H));
+    CHK(salloc(s, &p.CAT, N * cc + 1)); CHK(salloc(s, &p.Z, N * vd + 1)); CHK(salloc(s, &p.AB, N * 2 * a.nv + 1));
+    CHK(salloc(s, &p.O, N * vd + 1)); CHK(salloc(s, &p.OG, N * vd + 1)); CHK(salloc(s, &p.RUNS, N * (vd / 64) + 1));
+    CHK(q8alloc(s, p.OQ, N * vd + 256));
+    CHK(salloc(s, &p.QP, N * 2 * aq + 1)); CHK(salloc(s, &p.KB, N * kvd + 1)); CHK(salloc(s, &p.VB, N * kvd + 1));
+    CHK(salloc(s, &p.QR, N * aq + 1)); CHK(salloc(s, &p.AG, N * aq + 1)); CHK(salloc(s, &p.OA, N * aq + 1));
+    CHK(q8alloc(s, p.OAQ, N * aq + 256));
+    CHK(salloc(s, &p.RL, N * ne)); CHK(salloc(s, &p.SHL, N)); CHK(salloc(s, &p.SHG, N));
+    CHK(salloc(s, &p.RW, N * K)); CHK(salloc(s, &p.RIDX, N * K));
+    CHK(salloc(s, &p.CNT, ne)); CHK(salloc(s, &p.LIST, ne * N));
+    CHK(salloc(s, &p.ITEMS, (N * K + 63) / 64 + ne + 2));
+    CHK(salloc(s, &p.Hh, N * K * I)); CHK(q8alloc(s, p.HQ, N * K * I + 256));
+    CHK(salloc(s, &p.HSH, N * sI)); CHK(q8alloc(s, p.HSQ, N * sI + 256));
+    CHK(salloc(s, &p.GU, N * K * 2 * I)); CHK(salloc(s, &p.GSH, N * 2 * sI));
+    CHK(salloc(s, &p.OD, N * K * H)); CHK(salloc(s, &p.ODSH, N * H));
+    CHK(salloc(s, &p.LOGITS, N * (size_t)a.vocab)); CHK(salloc(s, &p.IDX, 3 * N + 1));
+    CHK(salloc(s, &p.AMV, N * OH_ARGMAX_BLOCKS)); CHK(salloc(s, &p.AMI, N * OH_ARGMAX_BLOCKS));
+    const size_t ob = ops_bytes > p.ops_bytes ? ops_bytes : p.ops_bytes;
+    CHK(salloc(s, &p.OPS, ob));
+    p.ops_bytes = ob;
+    p.n = (int)N;
+    p.gen++;
+    return ORNITH_HIP_OK;
+}
+
+// Host-side bounds check of a batch step's per-session descriptors (before
+// they are uploaded): every buffer a descriptor names, with the extent the
+// step's kernels reach through it at the session's position, lies inside one
+// allocation of the session that owns it (the batch buffers: the leading
+// session), and the attention grid and LDS cover every session's own.
+// Returns a description of the first violation, or an empty string.
+bool owns(const ornith_hip_session *s, const void *p, size_t bytes) {
+    const uintptr_t a = (uintptr_t)p;
+    for (size_t i = 0; i < s->allocs.size(); i++) {
+        const uintptr_t b = (uintptr_t)s->allocs[i];
+        if (a >= b && a + bytes >= a && a + bytes <= b + s->asz[i]) return true;
+    }
+    return false;
+}
+
+std::string batch_check(ornith_hip_session *const *ss, int n, const std::vector<size_t> &lofs,
+                               const uint8_t *host, int nvb_main, int lds_main) {
+    const ornith_hip_session *s0 = ss[0];
+    const ornith_hip_model *m = s0->m;
+    const ornith_hip_arch &a = m->a;
+    const size_t F = sizeof(float), qd = (size_t)a.nk * a.dk, vd = (size_t)a.nv * a.dv, cc = 2 * qd + vd;
+    const size_t aq = (size_t)a.nh * a.hd, kvd = (size_t)a.nkv * a.hd;
+    char msg[256];
+#define BC(own, ptr, bytes, what)                                                                           \
+    do {                                                                                                    \
+        if (!owns(own, ptr, bytes)) {                                                                       \
+            snprintf(msg, sizeof msg, "layer %d session %d: %s (%zu bytes) outside its allocations", l, b,  \
+                     what, (size_t)(bytes));                                                                \
+            return msg;                                                                                     \
+        }                                                                                                   \
+    } while (0)
+    for (int l = 0; l < a.n_layers; l++) {
+        const uint8_t *src = host + lofs[(size_t)l];
+        for (int b = 0; b < n; b++) {
+            const ornith_hip_session *sb = ss[b];
+            const int pos = sb->pos;
+            if (m->L[l].full) {
+                oh_op_prep pr;
+                oh_op_attn at;
+                memcpy(&pr, src + (size_t)b * sizeof(oh_op_prep), sizeof pr);
+                memcpy(&at, src + (size_t)n * sizeof(oh_op_prep) + (size_t)b * sizeof(oh_op_attn), sizeof at);
+                const size_t cap = (size_t)pr.cap, S = (size_t)oh_flash_slots(pr.cap);
+                if (pr.cap % 16 || pos >= pr.cap || at.cap != pr.cap) {
+                    snprintf(msg, sizeof msg, "layer %d session %d: position %d, KV capacity %d / %d", l, b, pos,
+                             pr.cap, at.cap);
+                    return msg;
+                }
+                BC(s0, pr.qproj, 2 * aq * F, "q projection");
+                BC(s0, pr.kin, kvd * F, "k projection");
+                BC(s0, pr.vin, kvd * F, "v projection");
+                BC(sb, pr.rope, ((size_t)pos + 1) * (a.hd / 2) * 2 * F, "RoPE table");
+                BC(s0, pr.qr, aq * F, "rotated queries");
+                BC(s0, pr.gate, aq * F, "output gate");
+                BC(sb, pr.Kt, kvd / 4 * cap * 4, "K codes");
+                BC(sb, pr.Ks, cap * a.nkv * F, "K scales");
+                BC(sb, pr.Vq, cap * kvd, "V codes");
+                BC(sb, pr.Vs, cap * a.nkv * F, "V scales");
+                if (at.qr != pr.qr || at.gate != pr.gate || at.Kt != pr.Kt || at.Ks != pr.Ks || at.Vq != pr.Vq ||
+                    at.Vs != pr.Vs) {
+                    snprintf(msg, sizeof msg, "layer %d session %d: attention and prep name different buffers", l, b);
+                    return msg;
+                }
+                BC(sb, at.scores, (size_t)a.nh * cap * F, "scores");
+                BC(sb, at.part_o, (size_t)a.nh * S * a.hd * F, "flash partial outputs");
+                BC(sb, at.part_ml, (size_t)a.nh * S * 2 * F, "flash partial max/sum");
+                BC(s0, at.out, aq * F, "attention output");
+                const int nv_ex = a.nh / (256 / a.hd), nv_fl = oh_flash_nvb(a.nh, a.nkv, at.cap, at.hb);
+                const int lds_ex = oh_exact_lds_bytes(a.hd, at.exact_max);
+                const int lds_fl = oh_flash_form_lds(a.nh, a.nkv, a.hd, at.hb);
+                if (nvb_main < nv_ex || nvb_main < nv_fl || lds_main < lds_ex || lds_main < lds_fl ||
+                    lds_main > 65536) {
+                    snprintf(msg, sizeof msg, "layer %d session %d: attention grid %d / LDS %d below %d, %d / %d, %d",
+                             l, b, nvb_main, lds_main, nv_ex, nv_fl, lds_ex, lds_fl);
+                    return msg;
+                }
+            } else {
+                oh_op_delta d;
+                memcpy(&d, src + (size_t)b * sizeof(oh_op_delta), sizeof d);
+                if (d.cc != (int)cc || d.nv != a.nv || d.dk != a.dk || d.K != a.conv_k) {
+                    snprintf(msg, sizeof msg, "layer %d session %d: delta shape", l, b);
+                    return msg;
+                }
+                BC(s0, d.cat, cc * F, "qkv mix");
+                BC(s0, d.ab, 2 * (size_t)a.nv * F, "alpha/beta");
+                BC(s0, d.gate, vd * F, "z gate");
+                BC(sb, d.conv_state, 2 * (size_t)(a.conv_k - 1) * cc * F, "conv window (two parities)");
+                BC(sb, d.S, vd * a.dk * F, "delta state");
+                BC(s0, d.out, vd * F, "delta output");
+                BC(s0, d.out_gate, vd * F, "delta output gate");
+                BC(s0, d.out_runs, vd / 64 * sizeof(double), "delta output runs");
+            }
+        }
+    }
+#undef BC
+    for (int b = 0; b < n; b++)
+        if (ss[b]->pos + 1 > ss[b]->cap || !owns(ss[b], ss[b]->toks, ((size_t)ss[b]->pos + 2) * 4)) {
+            snprintf(msg, sizeof msg, "session %d: token history at position %d of %d", b, ss[b]->pos, ss[b]->cap);
+            return msg;
+        }
+    return std::string();
+}
+
+int batch_enqueue(const BatchPlan &B, hipStream_t st) {
+    ornith_hip_session **ss = B.ss;
+    const int n = B.n;
+    ornith_hip_session *s0 = ss[0];
+    const ornith_hip_model *m = s0->m;
+    const ornith_hip_arch &a = m->a;
+    auto &p = s0->bw;
+    const int H = a.hidden, qd = a.nk * a.dk, vd = a.nv * a.dv, cc = 2 * qd + vd, aq = a.nh * a.hd;
+    const int kvd = a.nkv * a.hd;
+    const int32_t *dtok = (const int32_t *)(p.OPS + B.tok_ofs), *dpos = dtok + n;
+    int32_t *const *dtoks = (int32_t *const *)(p.OPS + B.tok_ofs + (((size_t)n * 8 + 15) & ~(size_t)15));
+    oh_op_embed emb = {m->embd->A, m->embd->B, m->embd->C, dtok, p.X, (int)m->embd->type, H};
+    HCHK(oh_launch_embed_rows(&emb, 0, n, st));
+    // below the matrix-core column count the dense projections run as the
+    // token step's fused multi-segment launches with one slot per session
+    // (the normalisation / gated norm / f32 activation formed in the launch's
+    // prologue, weights re-read per slot from the caches); the expert and
+    // head products keep the column-streaming batched kernels
+    const bool fused = n < kMmqMinTokens && batch_fused();
+    for (int l = 0; l < a.n_layers; l++) {
+        const OhLayer &y = m->L[l];
+        const uint8_t *dops = p.OPS + B.lofs[l];
+        const Act an = act_norm(p.X, (const float *)y.attn_norm->A, a.eps);
+        if (!fused)
+            HCHK(oh_launch_norm_q8k_rows(p.X, (const float *)y.attn_norm->A, a.eps, H, n, nullptr, p.XQ.qs, p.XQ.d,
+                                         p.XQ.bs, st, p.XQ.bp));
+        if (y.full) {
+            if (fused) {
+                MvBuild b;
+                CHK(mv_add(b, y.q, an, p.QP, 0, nullptr, n, 2 * aq, H));
+                CHK(mv_add(b, y.k, an, p.KB, 0, nullptr, n, kvd, H));
+                CHK(mv_add(b, y.v, an, p.VB, 0, nullptr, n, kvd, H));
+                CHK(mv_go(b, st));
+            } else {
+                CHK(pf_mm(y.q, p.XQ, p.QP, 2 * aq, n, 0, st));
+                CHK(pf_mm(y.k, p.XQ, p.KB, kvd, n, 0, st));
+                CHK(pf_mm(y.v, p.XQ, p.VB, kvd, n, 0, st));
+            }
+            const oh_op_prep *pops = (const oh_op_prep *)dops;
+            const oh_op_attn *aops = (const oh_op_attn *)(dops + (size_t)n * sizeof(oh_op_prep));
+            HCHK(oh_launch_prep_batch(pops, dpos, n, a.nh, a.nkv, st));
+            HCHK(oh_launch_attn_batch(aops, dpos, n, B.nvb_main, B.lds_main, a.nh, a.hd, st));
+            if (fused) {
+                MvBuild b;
+                Act af;
+                af.pro = OH_PRO_F32;
+                af.xf = p.OA;
+                CHK(mv_add(b, y.o, af, p.X, 1, nullptr, n, H, aq));
+                CHK(mv_go(b, st));
+            } else {
+                HCHK(oh_launch_norm_q8k_rows(p.OA, nullptr, 0.0f, aq, n, nullptr, p.OAQ.qs, p.OAQ.d, p.OAQ.bs, st,
+                                             p.OAQ.bp));
+                CHK(pf_mm(y.o, p.OAQ, p.X, H, n, 1, st));
+            }
+        } else {
+            if (fused) {
+                MvBuild b;
+                CHK(mv_add(b, y.qkv, an, p.CAT, 0, nullptr, n, cc, H));
+                CHK(mv_add(b, y.gate, an, p.Z, 0, nullptr, n, vd, H));
+                CHK(mv_add(b, y.alpha, an, p.AB, 0, nullptr, n, 2 * a.nv, H));
+                CHK(mv_add(b, y.beta, an, p.AB + a.nv, 0, nullptr, n, 2 * a.nv, H));
+                CHK(mv_go(b, st));
+            } else {
+                CHK(pf_mm(y.qkv, p.XQ, p.CAT, cc, n, 0, st));
+                CHK(pf_mm(y.gate, p.XQ, p.Z, vd, n, 0, st));
+                CHK(pf_mm(y.alpha, p.XQ, p.AB, 2 * a.nv, n, 0, st));
+                CHK(pf_mm(y.beta, p.XQ, p.AB + a.nv, 2 * a.nv, n, 0, st));
+            }
+            HCHK(oh_launch_delta_batch((const oh_op_delta *)dops, dpos, n, a.dk, a.conv_k, a.nv, st));
+            if (fused) {
+                MvBuild b;
+                CHK(mv_add(b, y.ssm_out, act_gnorm(p.O, p.OG, p.RUNS, (const float *)y.ssm_norm->A, a.eps, a.dv),
+                           p.X, 1, nullptr, n, H, vd));
+                CHK(mv_go(b, st));
+            } else {
+                HCHK(oh_launch_gnorm_q8k_rows(p.O, p.Z, (const float *)y.ssm_norm->A, a.eps, vd, a.dv, n, p.OQ.qs,
+                                              p.OQ.d, p.OQ.bs, st, p.OQ.bp));
+                CHK(pf_mm(y.ssm_out, p.OQ, p.X, H, n, 1, st));
+            }
+        }
+        const Act pn = act_norm(p.X, (const float *)y.post_norm->A, a.eps);
+        if (!fused || a.ne <= 0)
+            HCHK(oh_launch_norm_q8k_rows(p.X, (const float *)y.post_norm->A, a.eps, H, n, nullptr, p.XQ.qs, p.XQ.d,
+                                         p.XQ.bs, st, p.XQ.bp));
+        if (a.ne > 0) {
+            const int K = a.top_k, I = a.moe_inter, sI = a.shared_inter;
+            if (fused) {
+                // router + shared gate; each slot's first block stores its
+                // Q8_K activation (p.XQ) for the expert products
+                Act pst = pn;
+                pst.oqs = p.XQ.qs; pst.oqd = p.XQ.d; pst.oqb = p.XQ.bs;
+                MvBuild b;
+                CHK(mv_add(b, y.router, pst, p.RL, 0, nullptr, n, a.ne, H));
+                if (y.gate_inp_sh) CHK(mv_add(b, y.gate_inp_sh, pn, p.SHL, 0, nullptr, n, 1, H));
+                CHK(mv_go(b, st));
+            } else {
+                CHK(pf_mm(y.router, p.XQ, p.RL, a.ne, n, 0, st));
+                if (y.gate_inp_sh) CHK(pf_mm(y.gate_inp_sh, p.XQ, p.SHL, 1, n, 0, st));
+            }
+            // the token step's two MoE launches for all n tokens: the experts
+            // gate/up with each (token, expert) slot routing its own token,
+            // then the fused down projection + combine with a grid row per
+            // token (same conditions as the token step's fused down)
+            const bool paired = pairable(y.gate_exps, y.up_exps) && (!y.gate_sh || pairable(y.gate_sh, y.up_sh));
+            const uint32_t dt = y.down_exps->type;
+            const int nbd = I / 256, ns = K + (y.gate_sh ? 1 : 0);
+            const int rps = nbd >= 1 ? 64 / nbd : 1;
+            const int dlds = ns * ((nbd * 272 + nbd * 36 + 15) & ~15) + ns * I * 4 + ns * rps * 4;
+            if (fused && paired && oh_qdot_can(dt, I) && nbd >= 1 && nbd <= 64 && ns <= 10 && dlds <= 65536 &&
+                y.gate_exps->type == y.router->type && (!y.gate_sh || (y.down_sh->type == dt && sI == I))) {
+                MvBuild b2;
+                const Act ax = act_of(p.XQ, nullptr);
+                CHK(mv_add_pair(b2, y.gate_exps, y.up_exps, ax, p.Hh, p.RIDX, n * K, I));
+                b2.L.s[b2.L.n - 1].astride = H;
+                b2.L.s[b2.L.n - 1].adiv = K;
+                if (y.gate_sh) {
+                    CHK(mv_add_pair(b2, y.gate_sh, y.up_sh, ax, p.HSH, nullptr, n, sI));
+                    b2.L.s[b2.L.n - 1].astride = H;
+                }
+                b2.L.route = 1;
+                b2.L.tslots = K;
+                b2.L.rlog = p.RL;
+                b2.L.shl = y.gate_inp_sh ? p.SHL : nullptr;
+                b2.L.ne = a.ne;
+                b2.L.topk = K;
+                b2.L.ridx = p.RIDX;
+                b2.L.rw = p.RW;
+                b2.L.shg = p.SHG;
+                CHK(mv_go(b2, st));
+                oh_mvdown D;
+                memset(&D, 0, sizeof D);
+                D.A = y.down_exps->A; D.B = y.down_exps->B; D.C = y.down_exps->C;
+                if (y.gate_sh) { D.sA = y.down_sh->A; D.sB = y.down_sh->B; D.sC = y.down_sh->C; }
+                D.eidx = p.RIDX; D.w = p.RW; D.shg = y.gate_inp_sh ? p.SHG : nullptr;
+                D.h = p.Hh; D.hsh = p.HSH; D.x = p.X;
+                D.hts = (size_t)K * I; D.hsts = (size_t)sI; D.xts = (size_t)H;
+                D.type = (int)dt; D.nb = nbd; D.in = I; D.rows = H; D.k = K; D.stride = I;
+                HCHK(oh_launch_mv_down_rows(&D, (H + rps - 1) / rps, n, dlds, st));
+                continue;
+            }
+            HCHK(oh_launch_route_rows(p.RL, a.ne, K, y.gate_inp_sh ? p.SHL : nullptr, p.RIDX, p.RW,
+                                      y.gate_inp_sh ? p.SHG : nullptr, n, st));
+            HCHK(oh_launch_group_pairs(p.RIDX, n * K, p.CNT, a.ne, p.LIST, n, st));
+            const int max_items = (n * K + 63) / 64 + a.ne;
+            HCHK(oh_launch_mmq_items(p.CNT, a.ne, p.ITEMS, st));
+            CHK(pf_swiglu(y.gate_exps, y.up_exps, p.XQ, I, n * K, n, p.HQ, p.GU, p.Hh, st, p.CNT, p.LIST, n, K, a.ne,
+                          p.ITEMS, max_items));
+            if (pf_use_mmq(y.down_exps, true, n))
+                CHK(pf_mmq(y.down_exps, nullptr, p.HQ, p.OD, H, n, 0, st, p.CNT, p.LIST, n, 1, p.ITEMS, max_items));
+            else
+                CHK(pf_mvb(y.down_exps, nullptr, p.HQ, p.OD, H, n, 0, st, p.CNT, p.LIST, n, 1, a.ne));
+            if (y.gate_sh) {
+                CHK(pf_swiglu(y.gate_sh, y.up_sh, p.XQ, sI, n, n, p.HSQ, p.GSH, p.HSH, st));
+                CHK(pf_mm(y.down_sh, p.HSQ, p.ODSH, H, n, 0, st));
+            }
+            HCHK(oh_launch_moe_combine_rows(p.X, p.OD, p.RW, K, H, y.gate_sh ? p.ODSH : nullptr,
+                                            y.gate_inp_sh ? p.SHG : nullptr, n, st));
+        } else {
+            CHK(pf_swiglu(y.ffn_gate, y.ffn_up, p.XQ, a.shared_inter, n, n, p.HSQ, p.GSH, p.HSH, st));
+            CHK(pf_mm(y.ffn_down, p.HSQ, p.X, H, n, 1, st));
+        }
+    }
+    // head: output norm, lm_head over the n columns, each session's logits and
+    // greedy token; the token history of each session gets this step's token
+    // and, at the next position, the greedy one (where the token step's head
+    // leaves it for session_generate)
+    HCHK(oh_launch_norm_q8k_rows(p.X, (const float *)m->out_norm->A, a.eps, H, n, nullptr, p.XQ.qs, p.XQ.d,
+                                 p.XQ.bs, st, p.XQ.bp));
+    CHK(pf_mm(m->lm_head, p.XQ, p.LOGITS, a.vocab, n, 0, st));
+    HCHK(oh_launch_argmax_rows(p.LOGITS, a.vocab, n, p.IDX, st, p.AMV, p.AMI));
+    for (int b = 0; b < n; b++)
+        HCHK(hipMemcpyAsync(ss[b]->logits, p.LOGITS + (size_t)b * a.vocab, (size_t)a.vocab * 4,
+                            hipMemcpyDeviceToDevice, st));
+    HCHK(oh_launch_batch_tokens(dtoks, dpos, dtok, p.IDX, n, st));
+    return ORNITH_HIP_OK;
+}
+
+extern "C" int ornith_hip_batch_step(ornith_hip_session **ss, int n, const int32_t *tokens, int32_t *next) {
+    if (n <= 0) return ORNITH_HIP_OK;
+    if (!ss || !tokens) { seterr("batch_step: null sessions or tokens"); return ORNITH_HIP_ERR_FORMAT; }
+    ornith_hip_session *s0 = ss[0];
+    const ornith_hip_model *m = s0->m;
+    const ornith_hip_arch &a = m->a;
+    for (int b = 0; b < n; b++) {
+        if (!ss[b] || ss[b]->m != m) { seterr("batch_step: session %d is not of the first session's model", b); return ORNITH_HIP_ERR_FORMAT; }
+        for (int c = 0; c < b; c++)
+            if (ss[c] == ss[b]) { seterr("batch_step: session %d appears twice", b); return ORNITH_HIP_ERR_FORMAT; }
+        if (ss[b]->pos + 1 > ss[b]->cap) {
+            seterr("session capacity %d exceeded (pos %d + 1 token) in batch slot %d", ss[b]->cap, ss[b]->pos, b);
+            return ORNITH_HIP_ERR_UNSUPPORTED;
+        }
+        if (tokens[b] < 0 || tokens[b] >= a.vocab) {
+            seterr("token %d in batch slot %d outside the vocabulary (%d)", tokens[b], b, a.vocab);
+            return ORNITH_HIP_ERR_FORMAT;
+        }
+    }
+    // one KV capacity, exact_max and flash form across the batch, and every
+    // context on the same attention path (all within exact_max or all past
+    // it): the only mixes the batch step is run with; others are refused
+    for (int b = 1; b < n; b++) {
+        const ornith_hip_session *x = ss[b], *y = ss[0];
+        const int lim = oh_exact_limit(y->exact_max);
+        if (x->kvcap != y->kvcap || x->exact_max != y->exact_max || x->flash_mfma != y->flash_mfma ||
+            (x->pos + 1 <= lim) != (y->pos + 1 <= lim)) {
+            seterr("batch_step: session %d differs from session 0 in KV capacity (%d / %d), attention settings or "
+                   "attention path (position %d / %d); a batch takes sessions of one capacity on one path",
+                   b, x->kvcap, y->kvcap, x->pos, y->pos);
+            return ORNITH_HIP_ERR_UNSUPPORTED;
+        }
+    }
+    if (!pf_supported(m) || !oh_qdot_can(m->lm_head->type, m->lm_head->in) || m->lm_head->in > 8192) {
+        seterr("batch_step: the model is outside the batched projection path (widths <= 8192, integer dot types)");
+        return ORNITH_HIP_ERR_UNSUPPORTED;
+    }
+    if (!graphs_enabled()) {
+        // the batch step runs as one captured HIP graph; its eager form is
+        // switched off (a GPU fault in an eager batch run is not explained)
+        seterr("batch_step: needs HIP graphs (unset ORNITH_HIP_NO_GRAPH)");
+        return ORNITH_HIP_ERR_UNSUPPORTED;
+    }
+    HCHK(hipSetDevice(m->ctx->device));
+    hipStream_t st = m->ctx->st;
+    const int qd = a.nk * a.dk, vd = a.nv * a.dv, cc = 2 * qd + vd, aq = a.nh * a.hd;
+    const int kvd = a.nkv * a.hd;
+    // per-layer descriptors of every session: delta ops (linear layers) or
+    // prep + attention ops (full layers), n of each; then tokens, positions
+    // and the sessions' token histories
+    BatchPlan B;
+    B.ss = ss;
+    B.n = n;
+    B.lofs.resize((size_t)a.n_layers);
+    size_t ob = 0;
+    for (int l = 0; l < a.n_layers; l++) {
+        B.lofs[l] = ob;
+        ob += m->L[l].full ? (size_t)n * (sizeof(oh_op_prep) + sizeof(oh_op_attn)) : (size_t)n * sizeof(oh_op_delta);
+        ob = (ob + 15) & ~(size_t)15;
+    }
+    B.tok_ofs = ob;
+    ob += (((size_t)n * 8 + 15) & ~(size_t)15) + (size_t)n * sizeof(int32_t *) + 16;
+    CHK(bw_alloc(s0, n, ob));
+    auto &p = s0->bw;
+    std::vector<uint8_t> host(ob, 0);
+    B.nvb_main = 1;
+    B.lds_main = 0;
+    for (int l = 0; l < a.n_layers; l++) {
+        const OhLayer &y = m->L[l];
+        uint8_t *dst = host.data() + B.lofs[l];
+        for (int b = 0; b < n; b++) {
+            ornith_hip_session *sb = ss[b];
+            const LayerState &z = sb->ls[l];
+            if (y.full) {
+                oh_op_prep pr = {p.QP + (size_t)b * 2 * aq, p.KB + (size_t)b * kvd, p.VB + (size_t)b * kvd,
+                                 (const float *)y.q_norm->A, (const float *)y.k_norm->A, (const float *)sb->rope,
+                                 p.QR + (size_t)b * aq, p.AG + (size_t)b * aq, z.Kt, z.Ks, z.Vq, z.Vs,
+                                 a.nh, a.nkv, a.hd, a.rope_dim, sb->kvcap, a.eps};
+                memcpy(dst + (size_t)b * sizeof(oh_op_prep), &pr, sizeof pr);
+                oh_op_attn at;
+                memset(&at, 0, sizeof at);
+                at.qr = p.QR + (size_t)b * aq; at.gate = p.AG + (size_t)b * aq;
+                at.Kt = z.Kt; at.Ks = z.Ks; at.Vq = z.Vq; at.Vs = z.Vs;
+                at.scores = sb->scores; at.part_o = sb->fpo; at.part_ml = sb->fpml; at.out = p.OA + (size_t)b * aq;
+                at.nh = a.nh; at.nkv = a.nkv; at.hd = a.hd; at.cap = sb->kvcap; at.exact_max = sb->exact_max;
+                at.hb = oh_flash_form(a.nh, a.nkv, a.hd, sb->flash_mfma); at.scale = 1.0f / sqrtf((float)a.hd);
+                memcpy(dst + (size_t)n * sizeof(oh_op_prep) + (size_t)b * sizeof(oh_op_attn), &at, sizeof at);
+                const int nv_ex = a.nh / (256 / a.hd), nv_fl = oh_flash_nvb(a.nh, a.nkv, sb->kvcap, at.hb);
+                const int lds_ex = oh_exact_lds_bytes(a.hd, sb->exact_max), lds_fl = oh_flash_form_lds(a.nh, a.nkv, a.hd, at.hb);
+                B.nvb_main = std::max(B.nvb_main, std::max(nv_ex, nv_fl));
+                B.lds_main = std::max(B.lds_main, std::max(lds_ex, lds_fl));
+            } else {
+                oh_op_delta d = {p.CAT + (size_t)b * cc, p.AB + (size_t)b * 2 * a.nv, p.Z + (size_t)b * vd,
+                                 (const float *)y.conv->A, (const float *)y.ssm_a->A, (const float *)y.dt_bias->A,
+                                 z.conv, z.S, p.O + (size_t)b * vd, p.OG + (size_t)b * vd,
+                                 p.RUNS + (size_t)b * (vd / 64), a.dk, a.nk, a.nv, a.conv_k, cc,
+                                 1.0f / sqrtf((float)a.dk)};
+                memcpy(dst + (size_t)b * sizeof(oh_op_delta), &d, sizeof d);
+            }
+        }
+    }
+    // the full bounds check runs whenever a plan is captured (the descriptors
+    // of the same sessions do not change between replays; the positions are
+    // checked against the capacities above on every step)
+    auto check = [&]() -> int {
+        const std::string bad = batch_check(ss, n, B.lofs, host.data(), B.nvb_main, B.lds_main);
+        if (!bad.empty()) { seterr("batch_step plan: %s", bad.c_str()); return ORNITH_HIP_ERR_DEVICE; }
+        return ORNITH_HIP_OK;
+    };
+    int32_t *htp = (int32_t *)(host.data() + B.tok_ofs);
+    int32_t **htk = (int32_t **)(host.data() + B.tok_ofs + (((size_t)n * 8 + 15) & ~(size_t)15));
+    for (int b = 0; b < n; b++) { htp[b] = tokens[b]; htp[n + b] = ss[b]->pos; htk[b] = ss[b]->toks; }
+    HCHK(hipMemcpyAsync(p.OPS, host.data(), ob, hipMemcpyHostToDevice, st));
+    if (graphs_enabled()) {
+        // one captured step per set of sessions (ids, not addresses), buffer
+        // generation, product path, batch plan and attention grid
+        std::vector<uint64_t> key;
+        key.push_back((uint64_t)n);
+        key.push_back((uint64_t)p.gen);
+        key.push_back(mmq_enabled() ? 1u : 0u);
+        key.push_back(batch_fused() ? 1u : 0u);
+        key.push_back((uint64_t)B.nvb_main << 32 | (uint32_t)B.lds_main);
+        for (int b = 0; b < n; b++) key.push_back(ss[b]->sid);
+        if (!p.graph || p.key != key) {
+            CHK(check());
+            if (p.graph) { (void)hipGraphExecDestroy(p.graph); p.graph = nullptr; }
+            hipGraph_t g = nullptr;
+            HCHK(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+            const int r = batch_enqueue(B, st);
+            hipError_t e = hipStreamEndCapture(st, &g);
+            if (r != ORNITH_HIP_OK) { if (g) (void)hipGraphDestroy(g); return r; }
+            if (e != hipSuccess) { seterr("batch graph capture: %s", hipGetErrorString(e)); return ORNITH_HIP_ERR_DEVICE; }
+            e = hipGraphInstantiate(&p.graph, g, nullptr, nullptr, 0);
+            (void)hipGraphDestroy(g);
+            if (e != hipSuccess) { p.graph = nullptr; seterr("batch graph instantiate: %s", hipGetErrorString(e)); return ORNITH_HIP_ERR_DEVICE; }
+            p.key = key;
+        }
+        HCHK(hipGraphLaunch(p.graph, st));
+    } else {
+        CHK(check());
+        CHK(batch_enqueue(B, st));
+    }
+    std::vector<int32_t> hn((size_t)n);
+    HCHK(hipMemcpyAsync(hn.data(), p.IDX, (size_t)n * 4, hipMemcpyDeviceToHost, st));
+    HCHK(hipStreamSynchronize(st));
+    for (int b = 0; b < n; b++) {
+        ss[b]->pos += 1;
+        ss[b]->have_logits = true;
+        if (next) next[b] = hn[b];
+    }
+    return ORNITH_HIP_OK;
+}
+
+extern "C" int ornith_hip_session_eval(ornith_hip_session *s, const int32_t *tokens, int n) {
+    return session_eval(s, tokens, n, false);
+}
+
+// rforward_token whatever the prompt mode (a one-token evaluation in the
+// chunked mode is a one-token delta chunk, which rounds differently)
+extern "C" int ornith_hip_session_step(ornith_hip_session *s, int32_t token) {
+    return session_eval(s, &token, 1, true);
+}
+
+extern "C" int ornith_hip_session_logits(ornith_hip_session *s, float *out) {
+    if (!s->have_logits) { seterr("session has no logits; eval a prompt first"); return ORNITH_HIP_ERR_FORMAT; }
+    HCHK(hipSetDevice(s->m->ctx->device));
+    HCHK(hipMemcpyAsync(out, s->logits, (size_t)s->m->a.vocab * 4, hipMemcpyDeviceToHost, s->m->ctx->st));
+    HCHK(hipStreamSynchronize(s->m->ctx->st));
+    return ORNITH_HIP_OK;
+}
+
+extern "C" int ornith_hip_session_pos(const ornith_hip_session *s) { return s->pos; }
+
+extern "C" int ornith_hip_session_generate(ornith_hip_session *s, int n_predict, int32_t *out_tokens,
+                                           int *n_out) {
+    if (n_out) *n_out = 0;
+    if (!s->have_logits) { seterr("session has no logits; eval a prompt first"); return ORNITH_HIP_ERR_FORMAT; }
+    HCHK(hipSetDevice(s->m->ctx->device));
+    hipStream_t st = s->m->ctx->st;
+    int n = n_predict < 0 ? 0 : n_predict;
+    if (n > s->cap - s->pos) n = s->cap - s->pos;
+    CHK(sync_pos(s));
+    const int32_t eos = s->m->a.eos;
+    int emitted = 0;
+    if (eos < 0) {
+        // no stop token: the whole loop stays on the device
+        for (int i = 0; i < n; i++) CHK(run_step(s));
+        HCHK(hipMemcpyAsync(out_tokens, s->toks + s->pos, (size_t)n * 4, hipMemcpyDeviceToHost, st));
+        HCHK(hipStreamSynchronize(st));
+        CHK(step_check(s));
+        emitted = n;
+    } else {
+        for (int i = 0; i < n; i++) {
+            int32_t next;
+            HCHK(hipMemcpyAsync(&next, s->toks + s->pos + i, 4, hipMemcpyDeviceToHost, st));
+            HCHK(hipStreamSynchronize(st));
+            CHK(step_check(s));
+            if (next == eos) break;
+            out_tokens[emitted++] = next;
+            CHK(run_step(s));
+        }
+        HCHK(hipStreamSynchronize(st));
+    }
+    s->pos += emitted;
+    if (n_out) *n_out = emitted;
+    return ORNITH_HIP_OK;
+}
+
+extern "C" int ornith_hip_session_time_decode(ornith_hip_session *s, int n_steps, float *ms) {
+    if (!s->have_logits) { seterr("session has no logits; eval a prompt first"); return ORNITH_HIP_ERR_FORMAT; }
+    if (n_steps < 0 || s->pos + n_steps > s->cap) { seterr("time_decode: %d steps exceed capacity", n_steps); return ORNITH_HIP_ERR_UNSUPPORTED; }
+    HCHK(hipSetDevice(s->m->ctx->device));
+    hipStream_t st = s->m->ctx->st;
+    CHK(sync_pos(s));
+    if (step_enabled()) CHK(step_prepare(s));
+    if (dec_enabled() && !step_enabled()) CHK(dec_prepare(s));
+    if (!s->step_grid && !s->dec.grid && graphs_enabled()) {
+        if (!s->gbody) CHK(capture(s, enqueue_body, &s->gbody));
+        if (!s->ghead) CHK(capture(s, enqueue_head, &s->ghead));
+    }
+    hipEvent_t e0, e1;
+    HCHK(hipEventCreate(&e0));
+    HCHK(hipEventCreate(&e1));
+    HCHK(hipEventRecord(e0, st));
+    for (int i = 0; i < n_steps; i++) CHK(run_step(s));
+    HCHK(hipEventRecord(e1, st));
+    HCHK(hipEventSynchronize(e1));
+    float el = 0.0f;
+    HCHK(hipEventElapsedTime(&el, e0, e1));
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    CHK(step_check(s));
+    s->pos += n_steps;
+    *ms = el;
+    return ORNITH_HIP_OK;
+}
