@@ -181,7 +181,10 @@ bool oh_mmq_can(uint32_t type, int rows, int in) {
            in % 256 == 0 && in > 0;
 }
 hipError_t oh_launch_mmq(const oh_mmq *M, int max_items, int pair, hipStream_t st) {
-    const int ty = M->list ? max_items : (M->ncol + kMqCols - 1) / kMqCols;
+    // grouped: the item rows rounded up for the XCD runs of mq_block (rows past
+    // the item count exit)
+    const int ty = M->list ? (max_items + 8 * kMqRun - 1) / (8 * kMqRun) * (8 * kMqRun)
+                           : (M->ncol + kMqCols - 1) / kMqCols;
     if (ty <= 0) return hipSuccess;
     const dim3 grid(M->rows / kMqRows, ty, pair ? 2 : 1);
     if (M->type == OH_Q6_K) {

@@ -69,16 +69,37 @@ OH_DEV void mq_stage_load(const oh_mmq &M, const uint8_t *A, const uint8_t *Bh, 
 
 } // namespace
 
+// Expert-grouped launches: blocks go to the 8 XCDs round-robin (XCD = linear
+// block id % 8). Consecutive work items mostly belong to one expert (its
+// column tiles), so each XCD takes runs of kMqRun consecutive items, every
+// row tile of them, in turn: one expert's tiles then share an L2 and its
+// weights come from HBM about once. Dense launches keep the plain order
+// (a row tile's column tiles share an XCD when the row tiles are a multiple
+// of 8). The launcher rounds the item rows up to a multiple of 8 * kMqRun.
+constexpr int kMqRun = 8;
+OH_DEV void mq_block(const oh_mmq &M, int &bx, int &by) {
+    bx = (int)blockIdx.x;
+    by = (int)blockIdx.y;
+    const int gx = (int)gridDim.x, gy = (int)gridDim.y;
+    if (!M.list || gy % (8 * kMqRun)) return;
+    const int L = bx + gx * by, k = L & 7, j = L >> 3;
+    const int m = j / (kMqRun * gx), r = j - m * (kMqRun * gx);
+    by = (8 * m + k) * kMqRun + r / gx;
+    bx = r % gx;
+}
+
 extern "C" __global__ void __launch_bounds__(256, 2) oh_k_mmq_q4k(oh_mmq M) {
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ int sact[kMqCols], sout[kMqCols];
     const int tid = tid_x(), lane = lane_id();
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int zi = (int)blockIdx.z;
-    int g = 0, tile = (int)blockIdx.y, n;
+    int bx, by;
+    mq_block(M, bx, by);
+    int g = 0, tile = by, n;
     if (M.list) {
-        if ((int)blockIdx.y >= ldg(M.items)) return;
-        const int it = ldg(M.items + 1 + blockIdx.y);
+        if (by >= ldg(M.items)) return;
+        const int it = ldg(M.items + 1 + by);
         g = it >> 16;
         tile = it & 0xffff;
         n = ldg(M.cnt + g) - tile * kMqCols;
@@ -87,7 +108,7 @@ extern "C" __global__ void __launch_bounds__(256, 2) oh_k_mmq_q4k(oh_mmq M) {
     }
     n = n < kMqCols ? n : kMqCols;
     if (n <= 0) return;
-    const int R0 = (int)blockIdx.x * kMqRows;
+    const int R0 = bx * kMqRows;
     const uint8_t *A = zi ? M.A2 : M.A, *Bh = zi ? M.B2 : M.B;
     const int64_t rbase = M.list ? (int64_t)g * M.rows : 0;
     if (tid < kMqCols) {
@@ -286,10 +307,12 @@ extern "C" __global__ void __launch_bounds__(256, 1) oh_k_mmq_q6k(oh_mmq M) {
     const int tid = tid_x(), lane = lane_id();
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int zi = (int)blockIdx.z;
-    int g = 0, tile = (int)blockIdx.y, n;
+    int bx, by;
+    mq_block(M, bx, by);
+    int g = 0, tile = by, n;
     if (M.list) {
-        if ((int)blockIdx.y >= ldg(M.items)) return;
-        const int it = ldg(M.items + 1 + blockIdx.y);
+        if (by >= ldg(M.items)) return;
+        const int it = ldg(M.items + 1 + by);
         g = it >> 16;
         tile = it & 0xffff;
         n = ldg(M.cnt + g) - tile * kMqCols;
@@ -298,7 +321,7 @@ extern "C" __global__ void __launch_bounds__(256, 1) oh_k_mmq_q6k(oh_mmq M) {
     }
     n = n < kMqCols ? n : kMqCols;
     if (n <= 0) return;
-    const int R0 = (int)blockIdx.x * kMqRows;
+    const int R0 = bx * kMqRows;
     const uint8_t *A = zi ? M.A2 : M.A, *Bs = zi ? M.B2 : M.B, *Cd = zi ? M.C2 : M.C;
     const int64_t rbase = M.list ? (int64_t)g * M.rows : 0;
     const int nb = M.nb;
