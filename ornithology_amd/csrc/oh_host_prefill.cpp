@@ -213,9 +213,14 @@ int pf_chunk(ornith_hip_session *s, int base, int T, bool chunked, hipStream_t s
             const int lim = s->exact_max < 2048 ? s->exact_max : 2048;
             const int tsplit = attn_mfma_enabled() && oh_attn_mfma_supported(a.hd, a.nh, a.nkv)
                              ? (lim - base < 0 ? 0 : (lim - base > T ? T : lim - base)) : T;
-            for (int t0 = 0; t0 < tsplit; t0 += kPfAttnSub)
-                HCHK(oh_launch_attn_rows(&at, base, t0, tsplit - t0 < kPfAttnSub ? tsplit - t0 : kPfAttnSub, po, pml,
-                                         st));
+            if (tsplit < T || base + T <= lim) {
+                // every row before tsplit is inside the exact walk: one launch
+                HCHK(oh_launch_attn_exact_rows(&at, base, 0, tsplit, st));
+            } else {
+                for (int t0 = 0; t0 < tsplit; t0 += kPfAttnSub)
+                    HCHK(oh_launch_attn_rows(&at, base, t0, tsplit - t0 < kPfAttnSub ? tsplit - t0 : kPfAttnSub, po,
+                                             pml, st));
+            }
             if (tsplit < T) HCHK(oh_launch_attn_mfma_rows(&at, base, tsplit, T - tsplit, st));
             HCHK(oh_launch_norm_q8k_rows(p.OA, nullptr, 0.0f, aq, T, nullptr, p.OAQ.qs, p.OAQ.d, p.OAQ.bs, st,
                                          p.OAQ.bp));

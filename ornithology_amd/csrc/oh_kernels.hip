@@ -222,6 +222,14 @@ hipError_t oh_launch_prep_rows(const oh_op_prep *a, int base, int T, hipStream_t
     hipLaunchKernelGGL(oh_k_prep_rows, dim3(a->nh + a->nkv, T), dim3(256), 0, st, *a, base);
     return hipGetLastError();
 }
+hipError_t oh_launch_attn_exact_rows(const oh_op_attn *a, int base, int t0, int n, hipStream_t st) {
+    const int lim = a->exact_max < kExactMax ? a->exact_max : kExactMax;
+    if (n <= 0) return hipSuccess;
+    if (base + t0 + n > lim) return hipErrorInvalidValue;     // every row must be inside the exact walk
+    hipLaunchKernelGGL(oh_k_attn_exact_rows, dim3(a->nh / (256 / a->hd), n), dim3(256),
+                       (size_t)oh_exact_lds_bytes(a->hd, a->exact_max), st, *a, base, t0);
+    return hipGetLastError();
+}
 hipError_t oh_launch_attn_rows(const oh_op_attn *a, int base, int t0, int n, size_t po_stride, size_t pml_stride,
                                hipStream_t st) {
     const int lim = a->exact_max < kExactMax ? a->exact_max : kExactMax;

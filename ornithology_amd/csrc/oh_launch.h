@@ -61,6 +61,8 @@ hipError_t oh_launch_batch_tokens(int32_t *const *toks, const int32_t *pos, cons
 hipError_t oh_launch_prep_rows(const oh_op_prep *a, int base, int T, hipStream_t st);
 hipError_t oh_launch_attn_rows(const oh_op_attn *a, int base, int t0, int n, size_t po_stride, size_t pml_stride,
                                hipStream_t st);
+// the exact walk alone for n rows t0.. that are all inside it (one launch)
+hipError_t oh_launch_attn_exact_rows(const oh_op_attn *a, int base, int t0, int n, hipStream_t st);
 hipError_t oh_launch_route_rows(const float *logits, int ne, int k, const float *shl, int32_t *idx, float *w,
                                 float *shg, int T, hipStream_t st);
 hipError_t oh_launch_group_pairs(const int32_t *idx, int npairs, int32_t *cnt, int ne, int32_t *list, int lstride,

@@ -532,7 +532,9 @@ constexpr int kExactMax = 2048;
 // (src/ornith_tensor.c:108-115; tree-ordered double sum) and the output
 // o_i = sum_t (p_t*Vs_t)*code_t,i, sequential over t, skipping zero weights
 // (src/ornith_attn.c:132-140); then o *= sigmoid(gate).
-template <class W>
+// VT: tiles of 16 V positions in flight per thread (the decode step's single
+// row keeps 8; the prompt's many rows keep fewer, for occupancy)
+template <class W, int VT = 8>
 OH_DEV void exact_body(const oh_op_attn &a, int vb, int pos, int lim, W &w) {
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ float q[256];
@@ -607,16 +609,16 @@ OH_DEV void exact_body(const oh_op_attn &a, int vb, int pos, int lim, W &w) {
             }
         }
         __syncthreads();
-        // tiles of 16 positions, 8 tiles in flight, adds in position order
-        for (int k0 = 0; k0 < n; k0 += 128) {
-            uint4 cw[8];
+        // tiles of 16 positions, VT tiles in flight, adds in position order
+        for (int k0 = 0; k0 < n; k0 += 16 * VT) {
+            uint4 cw[VT];
 #pragma unroll
-            for (int u = 0; u < 8; u++) {
+            for (int u = 0; u < VT; u++) {
                 const int tile = k0 + 16 * u < n ? k0 + 16 * u : ((n - 1) & ~15);
                 cw[u] = ldg(vt + (size_t)((t0 + tile) / 16) * hd);
             }
 #pragma unroll
-            for (int u = 0; u < 8; u++) {
+            for (int u = 0; u < VT; u++) {
 #pragma unroll
                 for (int j = 0; j < 16; j++) {
                     const int k = k0 + 16 * u + j;

@@ -527,7 +527,10 @@ extern "C" __global__ void __launch_bounds__(256) oh_k_prep_rows(oh_op_prep a, i
 // tokens t0 + blockIdx.y; flash partials per token at part + (blockIdx.y) * pstride
 // exact walks of the sub-batch's tokens whose context is at most lim (the
 // others exit): token t0 + blockIdx.y at position base + t0 + blockIdx.y
-extern "C" __global__ void __launch_bounds__(256) oh_k_attn_exact_rows(oh_op_attn a, int base, int t0) {
+// the prompt's exact walks: many rows at once, so fewer V tiles in flight
+// per thread and more resident blocks (VGPRs for 6 blocks per CU)
+constexpr int kExactRowsVT = 2;
+extern "C" __global__ void __launch_bounds__(256, 6) oh_k_attn_exact_rows(oh_op_attn a, int base, int t0) {
     NoWait w;
     const int t = t0 + (int)blockIdx.y, qd = a.nh * a.hd;
     const int lim = a.exact_max < kExactMax ? a.exact_max : kExactMax;
@@ -535,7 +538,7 @@ extern "C" __global__ void __launch_bounds__(256) oh_k_attn_exact_rows(oh_op_att
     b.qr = a.qr + (size_t)t * qd;
     b.gate = a.gate + (size_t)t * qd;
     b.out = a.out + (size_t)t * qd;
-    exact_body(b, (int)blockIdx.x, base + t, lim, w);
+    exact_body<NoWait, kExactRowsVT>(b, (int)blockIdx.x, base + t, lim, w);
 }
 
 // flash chunks of the n tokens t0.. of a sub-batch: each block stages its KV
