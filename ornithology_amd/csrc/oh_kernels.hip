@@ -60,7 +60,8 @@ int oh_mvb_tcol(int nb) {
 hipError_t oh_launch_norm_q8k_rows(const float *x, const float *norm_w, float eps, int n, int rows, float *xn_out,
                                    int8_t *qs, float *d, int16_t *bs, hipStream_t st, int8_t *bp, int swiglu) {
     if (rows <= 0) return hipSuccess;
-    hipLaunchKernelGGL(oh_k_norm_q8k_rows, dim3(rows), dim3(256), 0, st, x, norm_w, eps, n, xn_out, qs, d, bs, bp,
+    if (n > 8192 || n % 256) return hipErrorInvalidValue;     // the kernel's register and LDS sizes
+    hipLaunchKernelGGL(oh_k_norm_q8k_rows, dim3(rows), dim3(256), (size_t)n * 4, st, x, norm_w, eps, n, xn_out, qs, d, bs, bp,
                        swiglu);
     return hipGetLastError();
 }

@@ -1604,13 +1604,23 @@ extern "C" __global__ void __launch_bounds__(256) oh_k_mvb_q80(oh_mvbatch B) { m
 // Q8_K (optionally after RMSNorm) of `rows` vectors of n elements, one block
 // per vector; the same arithmetic as oh_k_rmsnorm_q8k (and the matvec's
 // RMSNorm prologue). xn_out (optional) receives the normalised f32 vectors.
+// Dynamic LDS: n floats (the launcher's), so narrow rows keep more blocks
+// resident; the norm weights are requested with the row.
 extern "C" __global__ void __launch_bounds__(256)
 oh_k_norm_q8k_rows(const float *x, const float *norm_w, float eps, int n, float *xn_out, int8_t *qs, float *d,
                    int16_t *bs, int8_t *bp, int swiglu) {
-    __shared__ float v[8192];
+    extern __shared__ __align__(16) float v[];
     __shared__ double red[4];
     const size_t r = blockIdx.x;
     const int tid = tid_x(), wave = tid >> 6, nqb = n / 256;
+    float wn[32];                                   // this thread's norm weights (n <= 8192)
+    if (norm_w) {
+#pragma unroll
+        for (int k = 0; k < 32; k++) {
+            const int i = tid + 256 * k;
+            wn[k] = i < n ? ldg(norm_w + i) : 0.0f;
+        }
+    }
     if (swiglu) {
         // rows of [gate | up] (2n): v = silu(gate) * up, the paired matvec's h
         const float *xr = x + r * 2 * n;
@@ -1629,7 +1639,11 @@ oh_k_norm_q8k_rows(const float *x, const float *norm_w, float eps, int n, float 
         const double tot = (red[0] + red[1]) + (red[2] + red[3]);
         const float inv = (float)(1.0 / sqrt(tot / (double)n + (double)eps));
         __syncthreads();
-        for (int i = tid; i < n; i += 256) v[i] = v[i] * inv * ldg(norm_w + i);
+#pragma unroll
+        for (int k = 0; k < 32; k++) {
+            const int i = tid + 256 * k;
+            if (i < n) v[i] = v[i] * inv * wn[k];
+        }
         __syncthreads();
     }
     if (xn_out) for (int i = tid; i < n; i += 256) stg(xn_out + r * n + i, v[i]);
