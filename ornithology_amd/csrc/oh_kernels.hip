@@ -73,7 +73,8 @@ hipError_t oh_launch_embed_rows(const oh_op_embed *a, int base, int T, hipStream
 }
 hipError_t oh_launch_conv_rows(const float *cat, const float *conv_w, float *conv_state, float *out, float *stage,
                                int T, int base, int cc, int K, hipStream_t st) {
-    const dim3 g((cc + 255) / 256, T), gw((cc + 255) / 256, K - 1);
+    if (K < 2 || K > kConvKMax) return hipErrorInvalidValue;
+    const dim3 g((cc + 255) / 256, (T + kConvRun - 1) / kConvRun), gw((cc + 255) / 256, K - 1);
     hipLaunchKernelGGL(oh_k_conv_rows, g, dim3(256), 0, st, cat, conv_w, conv_state, out, T, base, cc, K);
     if (((base + T) & 1) != (base & 1)) {
         hipLaunchKernelGGL(oh_k_conv_window, gw, dim3(256), 0, st, cat, conv_state, T, base, cc, K);

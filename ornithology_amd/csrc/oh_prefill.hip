@@ -17,23 +17,43 @@ extern "C" __global__ void __launch_bounds__(256) oh_k_embed_rows(oh_op_embed a,
 }
 
 // ---- causal depthwise conv + SiLU over T tokens (src/ornith_attn.c:370-388) ------
-// Thread per (channel, token): the K-1 inputs before token t come from the
+// Thread per (channel, run of tokens): the K-1 inputs before token t come from the
 // chunk or, for the first tokens, from the window state (row j = position
 // base-(K-1)+j), summed as the decode step sums them. The window the next step
 // reads (parity (base+T)&1) receives the last K-1 inputs.
+constexpr int kConvRun = 16, kConvKMax = 8;      // tokens per thread, largest kernel width
 extern "C" __global__ void __launch_bounds__(256)
 oh_k_conv_rows(const float *cat, const float *conv_w, float *conv_state, float *out, int T, int base, int cc, int K) {
-    const int c = (int)(blockIdx.x * 256 + tid_x()), t = (int)blockIdx.y;
+    // a thread walks kConvRun tokens of one channel, the K - 1 earlier inputs
+    // in registers (K <= kConvKMax); per token the decode step's conv order
+    const int c = (int)(blockIdx.x * 256 + tid_x()), t0 = (int)blockIdx.y * kConvRun;
     if (c >= cc) return;
+    const int t1 = t0 + kConvRun < T ? t0 + kConvRun : T;
     const float *win = conv_state + (size_t)(base & 1) * (K - 1) * cc;
-    float acc = 0.0f;
-    for (int j = 0; j < K - 1; j++) {
-        const int tj = t - (K - 1) + j;
-        const float xv = tj >= 0 ? ldg(cat + (size_t)tj * cc + c) : ldg(win + (size_t)(t + j) * cc + c);
-        acc += ldg(conv_w + (size_t)c * K + j) * xv;
+    float w[kConvKMax], xw[kConvKMax];
+#pragma unroll
+    for (int j = 0; j < kConvKMax; j++) {
+        w[j] = j < K ? ldg(conv_w + (size_t)c * K + j) : 0.0f;
+        const int tj = t0 - (K - 1) + j;
+        xw[j] = j >= K - 1 ? 0.0f : tj >= 0 ? ldg(cat + (size_t)tj * cc + c) : ldg(win + (size_t)(t0 + j) * cc + c);
     }
-    acc += ldg(conv_w + (size_t)c * K + K - 1) * ldg(cat + (size_t)t * cc + c);
-    stg(out + (size_t)t * cc + c, ref_silu(acc));
+    for (int t = t0; t < t1; t++) {
+        const float xt = ldg(cat + (size_t)t * cc + c);
+        float acc = 0.0f, wl = 0.0f;
+#pragma unroll
+        for (int j = 0; j < kConvKMax; j++) {
+            if (j < K - 1) acc += w[j] * xw[j];
+            if (j == K - 1) wl = w[j];
+        }
+        acc += wl * xt;
+        stg(out + (size_t)t * cc + c, ref_silu(acc));
+#pragma unroll
+        for (int j = 0; j + 1 < kConvKMax; j++)
+            if (j + 1 < K - 1) xw[j] = xw[j + 1];
+#pragma unroll
+        for (int j = 0; j < kConvKMax; j++)
+            if (j == K - 2) xw[j] = xt;
+    }
 }
 
 // the window after the chunk (a separate launch: the conv above reads the old one)
