@@ -67,6 +67,14 @@ OH_DEV void mq_stage_load(const oh_mmq &M, const uint8_t *A, const uint8_t *Bh, 
     }
 }
 
+// packed nibbles (bytes <= 15) times a factor <= 7 held in both 16-bit
+// halves of f: bytes of at most 105 and halves below 2^16, so the two 16-bit
+// products (one full-rate instruction) equal the 32-bit product
+typedef unsigned short mq_u16x2 __attribute__((ext_vector_type(2)));
+OH_DEV int mq_mul_bytes(uint32_t n, uint32_t f) {
+    return __builtin_bit_cast(int, __builtin_bit_cast(mq_u16x2, n) * __builtin_bit_cast(mq_u16x2, f));
+}
+
 } // namespace
 
 // Expert-grouped launches: blocks go to the 8 XCDs round-robin (XCD = linear
@@ -165,12 +173,13 @@ extern "C" __global__ void __launch_bounds__(256, 2) oh_k_mmq_q4k(oh_mmq M) {
             for (int e = 0; e < 2; e++) {
                 const int s = 2 * m + e;
                 const uint32_t sc = ((s < 4 ? scl : sch) >> (8 * (s & 3))) & 0xffu;
-                const uint32_t lo = sc & 7u, hi = sc >> 3;
+                const uint32_t lo = (sc & 7u) * 0x10001u, hi = (sc >> 3) * 0x10001u;
                 const uint32_t n0 = (e ? wq.x >> 4 : wq.x) & NM, n1 = (e ? wq.y >> 4 : wq.y) & NM;
                 const uint32_t n2 = (e ? wq.z >> 4 : wq.z) & NM, n3 = (e ? wq.w >> 4 : wq.w) & NM;
-                // bytes of at most 15 * 7: no carry between the packed bytes
-                const mq_v4i alo = {(int)(n0 * lo), (int)(n1 * lo), (int)(n2 * lo), (int)(n3 * lo)};
-                const mq_v4i ahi = {(int)(n0 * hi), (int)(n1 * hi), (int)(n2 * hi), (int)(n3 * hi)};
+                const mq_v4i alo = {mq_mul_bytes(n0, lo), mq_mul_bytes(n1, lo), mq_mul_bytes(n2, lo),
+                                    mq_mul_bytes(n3, lo)};
+                const mq_v4i ahi = {mq_mul_bytes(n0, hi), mq_mul_bytes(n1, hi), mq_mul_bytes(n2, hi),
+                                    mq_mul_bytes(n3, hi)};
 #pragma unroll
                 for (int t = 0; t < 2; t++) {
                     const mq_v4i xb = *(const mq_v4i *)(S + kMqB + ((2 * s + h) * 64 + 32 * t + lr) * 16);
