@@ -18,8 +18,12 @@
 // Block: 256 threads, a tile of 128 rows x 64 columns; wave w owns rows
 // [32w, 32w + 32) and both 32-column halves. One super-block per stage; the
 // stage's operands go global -> LDS with global_load_lds (no registers), two
-// stages in flight. LDS layouts are piece-major so that the 32 lanes of an
-// MFMA operand read consecutive 16-byte chunks.
+// stages in flight. Weight codes are piece-major so that the 32 lanes of an
+// MFMA operand read consecutive 16-byte chunks. Activation codes are loaded
+// 4 columns per wave-load (16 lanes read a column's 256 bytes, whole cache
+// lines) and kept column-major with the piece index XOR-swizzled by the
+// column, so the operand reads (one piece of 16 consecutive columns) still
+// fall in distinct LDS banks.
 
 typedef int mq_v4i __attribute__((ext_vector_type(4)));
 typedef int mq_v16i __attribute__((ext_vector_type(16)));
@@ -27,12 +31,12 @@ typedef __attribute__((address_space(3))) void mq_lds_t;
 
 constexpr int kMqRows = 128, kMqCols = 64;
 constexpr int kMqA = 0;                         // codes [8 pieces][128 rows][16 B]
-constexpr int kMqB = kMqA + 8 * 128 * 16;       // activation codes [16 pieces][64 cols][16 B]
-constexpr int kMqH = kMqB + 16 * 64 * 16;       // weight headers [4 dwords][128 rows]
-constexpr int kMqP = kMqH + 4 * 128 * 4;        // pair-sum bytes [64 cols][16 B]
+constexpr int kMqB = kMqA + 8 * 128 * 16;       // activation codes [64 cols][16 slots][16 B]
+constexpr int kMqH = kMqB + 16 * 64 * 16;       // weight headers [128 rows][16 B]
+constexpr int kMqP = kMqH + 128 * 16;           // pair-sum bytes [64 cols][16 B]
 constexpr int kMqD = kMqP + 64 * 16;            // activation d [64 cols]
 constexpr int kMqStage = kMqD + 64 * 4;         // 36096 B
-constexpr int kMqLoads = 16 + 16 + 8 + 1 + 1;   // wave-loads per stage
+constexpr int kMqLoads = 16 + 16 + 2 + 1 + 1;   // wave-loads per stage (9 per wave)
 
 namespace {
 
@@ -43,26 +47,37 @@ OH_DEV void mq_load4(const void *g, uint8_t *lds) {
     __builtin_amdgcn_global_load_lds(g, (mq_lds_t *)lds, 4, 0, 0);
 }
 
-// wave-load L of super-block i into stage S; lane-dependent global address,
-// wave-uniform LDS base (lane k writes 16 B, or 4 B, at base + k * size)
+// LDS slot (16 B) of activation piece p of tile column c
+OH_DEV int mq_act_slot(int c, int p) { return c * 16 + (p ^ (c & 15)); }
+
+// The 9 wave-loads of super-block i that wave w issues into stage S (lane k
+// of a wave-load writes 16 B, or 4 B, at the wave-uniform base + k * size):
+// weight codes L = w + 4n (piece L / 2, rows 64 * (L & 1) + lane), activation
+// codes of columns 4j .. 4j + 3 for j = w + 4n (lane k: column 4j + k / 16,
+// slot k % 16), then the headers of rows 64w + lane (waves 0, 1), the pair-sum
+// bytes (wave 2) or the activation d (wave 3) of column lane. acs[n]: the
+// activation row of column 4(w + 4n) + lane / 16; acol: that of column lane.
 OH_DEV void mq_stage_load(const oh_mmq &M, const uint8_t *A, const uint8_t *Bh, int64_t rbase, int R0, int i,
-                          uint8_t *S, int L, int lane, int acol) {
+                          uint8_t *S, int w, int lane, const int (&acs)[4], int acol) {
     const int nb = M.nb;
-    if (L < 16) {                                   // codes: piece p, rows rh*64 + lane
-        const int p = L >> 1, rh = L & 1;
+#pragma unroll
+    for (int n = 0; n < 4; n++) {
+        const int L = w + 4 * n, p = L >> 1, rh = L & 1;
         const int64_t bi = (rbase + R0 + rh * 64 + lane) * nb + i;
         const uint4 *src = (const uint4 *)(A + (bi >> 6) * (int64_t)(64 * 128)) + (bi & 63) + p * 64;
         mq_load16(src, S + kMqA + (p * 128 + rh * 64) * 16);
-    } else if (L < 32) {                            // activation codes: piece q, column lane
-        const int q = L - 16;
-        mq_load16(M.xqs + (size_t)acol * M.in + (size_t)i * 256 + q * 16, S + kMqB + q * 64 * 16);
-    } else if (L < 40) {                            // header dword f of rows rh*64 + lane
-        const int f = (L - 32) >> 1, rh = (L - 32) & 1;
-        const int64_t bi = (rbase + R0 + rh * 64 + lane) * nb + i;
-        mq_load4(Bh + bi * 16 + f * 4, S + kMqH + (f * 128 + rh * 64) * 4);
-    } else if (L == 40) {                           // pair-sum bytes of column lane
+    }
+#pragma unroll
+    for (int n = 0; n < 4; n++) {
+        const int j = w + 4 * n, c = 4 * j + (lane >> 4), q = (lane & 15) ^ (c & 15);
+        mq_load16(M.xqs + (size_t)acs[n] * M.in + (size_t)i * 256 + q * 16, S + kMqB + j * 64 * 16);
+    }
+    if (w < 2) {
+        const int64_t bi = (rbase + R0 + w * 64 + lane) * nb + i;
+        mq_load16(Bh + bi * 16, S + kMqH + w * 64 * 16);
+    } else if (w == 2) {
         mq_load16(M.xbp + ((size_t)acol * nb + i) * 16, S + kMqP);
-    } else {                                        // activation d of column lane
+    } else {
         mq_load4(M.xd + (size_t)acol * nb + i, S + kMqD);
     }
 }
@@ -127,9 +142,11 @@ extern "C" __global__ void __launch_bounds__(256, 2) oh_k_mmq_q4k(oh_mmq M) {
     }
     __syncthreads();
     const int acol = sact[lane];                    // this lane's column in activation loads
+    int acs[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) acs[u] = sact[4 * (wave + 4 * u) + (lane >> 4)];
     auto stage = [&](int i, int buf) {
-        uint8_t *S = smem + buf * kMqStage;
-        for (int L = wave; L < kMqLoads; L += 4) mq_stage_load(M, A, Bh, rbase, R0, i, S, L, lane, acol);
+        mq_stage_load(M, A, Bh, rbase, R0, i, smem + buf * kMqStage, wave, lane, acs, acol);
     };
 
     const int h = lane >> 5, lr = lane & 31, arow = 32 * wave + lr;
@@ -147,8 +164,8 @@ extern "C" __global__ void __launch_bounds__(256, 2) oh_k_mmq_q4k(oh_mmq M) {
         if (i + 1 < nb) {
             stage(i + 1, buf ^ 1);
             // this wave's loads of stage i are the older ones; every wave
-            // issued at least 10 for stage i + 1
-            asm volatile("s_waitcnt vmcnt(10)" ::: "memory");
+            // issued 9 for stage i + 1
+            asm volatile("s_waitcnt vmcnt(9)" ::: "memory");
         } else {
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         }
@@ -156,7 +173,8 @@ extern "C" __global__ void __launch_bounds__(256, 2) oh_k_mmq_q4k(oh_mmq M) {
         const uint8_t *S = smem + buf * kMqStage;
         const uint32_t *H = (const uint32_t *)(S + kMqH);
         // scales and mins of this lane's A row (sb_term's unpacking of scales[12])
-        const uint32_t hy = H[128 + arow], hz = H[256 + arow], hw = H[384 + arow];
+        const uint4 hd = *(const uint4 *)(H + 4 * arow);
+        const uint32_t hy = hd.y, hz = hd.z, hw = hd.w;
         const uint32_t scl = hy & 0x3f3f3f3fu, sch = (hw & 0x0f0f0f0fu) | ((hy >> 2) & 0x30303030u);
         const uint32_t mnl = hz & 0x3f3f3f3fu, mnh = ((hw >> 4) & 0x0f0f0f0fu) | ((hz >> 2) & 0x30303030u);
         mq_v16i ihi[2], ilo[2];
@@ -182,7 +200,7 @@ extern "C" __global__ void __launch_bounds__(256, 2) oh_k_mmq_q4k(oh_mmq M) {
                                     mq_mul_bytes(n3, hi)};
 #pragma unroll
                 for (int t = 0; t < 2; t++) {
-                    const mq_v4i xb = *(const mq_v4i *)(S + kMqB + ((2 * s + h) * 64 + 32 * t + lr) * 16);
+                    const mq_v4i xb = *(const mq_v4i *)(S + kMqB + mq_act_slot(32 * t + lr, 2 * s + h) * 16);
                     ihi[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ahi, xb, ihi[t], 0, 0, 0);
                     ilo[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(alo, xb, ilo[t], 0, 0, 0);
                 }
@@ -210,8 +228,8 @@ extern "C" __global__ void __launch_bounds__(256, 2) oh_k_mmq_q4k(oh_mmq M) {
             const float yd = XD[32 * t + lr], nyd = -yd;
 #pragma unroll
             for (int vg = 0; vg < 4; vg++) {
-                const uint4 dd = *(const uint4 *)(H + 32 * wave + 8 * vg + 4 * h);
-                const uint32_t dw[4] = {dd.x, dd.y, dd.z, dd.w};
+                const uint32_t *hr = H + 4 * (32 * wave + 8 * vg + 4 * h);
+                const uint32_t dw[4] = {hr[0], hr[4], hr[8], hr[12]};
 #pragma unroll
                 for (int k = 0; k < 4; k++) {
                     const int v = 4 * vg + k;
@@ -256,33 +274,40 @@ extern "C" __global__ void __launch_bounds__(256, 2) oh_k_mmq_q4k(oh_mmq M) {
 // columns' activation codes and d; the rows' f16 d of every super-block sit in
 // LDS for the whole launch.
 constexpr int kM6A = 0;                          // codes [12 pieces][128 rows][16 B]
-constexpr int kM6B = kM6A + 12 * 128 * 16;       // activation codes [16 pieces][64 cols][16 B]
+constexpr int kM6B = kM6A + 12 * 128 * 16;       // activation codes [64 cols][16 slots][16 B]
 constexpr int kM6S = kM6B + 16 * 64 * 16;        // group scales [128 rows][16 B]
 constexpr int kM6X = kM6S + 128 * 16;            // activation d [64 cols]
 constexpr int kM6Stage = kM6X + 64 * 4;          // 43264 B
-constexpr int kM6Loads = 24 + 16 + 2 + 1;        // wave-loads per stage
+constexpr int kM6Loads = 24 + 16 + 2 + 1;        // wave-loads per stage (10 or 11 per wave)
 OH_HD inline int m6_lds_bytes(int nb) { return 2 * kM6Stage + 128 * nb * 2; }
 
 typedef short m6_s2 __attribute__((ext_vector_type(2)));
 
 namespace {
 
+// The wave-loads of super-block i that wave w issues into stage S: weight
+// codes L = w + 4n (piece L / 2, rows 64 * (L & 1) + lane), activation codes
+// as in mq_stage_load, then the group scales of rows 64w + lane (waves 0, 1)
+// or the activation d of column lane (wave 2): 11, 11, 11 and 10 loads.
 OH_DEV void m6_stage_load(const oh_mmq &M, const uint8_t *A, const uint8_t *Bs, int64_t rbase, int R0, int i,
-                          uint8_t *S, int L, int lane, int acol) {
+                          uint8_t *S, int w, int lane, const int (&acs)[4], int acol) {
     const int nb = M.nb;
-    if (L < 24) {                                   // codes: piece p, rows rh*64 + lane
-        const int p = L >> 1, rh = L & 1;
+#pragma unroll
+    for (int n = 0; n < 6; n++) {
+        const int L = w + 4 * n, p = L >> 1, rh = L & 1;
         const int64_t bi = (rbase + R0 + rh * 64 + lane) * nb + i;
         const uint4 *src = (const uint4 *)(A + (bi >> 6) * (int64_t)(64 * 192)) + (bi & 63) + p * 64;
         mq_load16(src, S + kM6A + (p * 128 + rh * 64) * 16);
-    } else if (L < 40) {                            // activation codes: piece q, column lane
-        const int q = L - 24;
-        mq_load16(M.xqs + (size_t)acol * M.in + (size_t)i * 256 + q * 16, S + kM6B + q * 64 * 16);
-    } else if (L < 42) {                            // group scales of rows rh*64 + lane
-        const int rh = L - 40;
-        const int64_t bi = (rbase + R0 + rh * 64 + lane) * nb + i;
-        mq_load16(Bs + bi * 16, S + kM6S + rh * 64 * 16);
-    } else {                                        // activation d of column lane
+    }
+#pragma unroll
+    for (int n = 0; n < 4; n++) {
+        const int j = w + 4 * n, c = 4 * j + (lane >> 4), q = (lane & 15) ^ (c & 15);
+        mq_load16(M.xqs + (size_t)acs[n] * M.in + (size_t)i * 256 + q * 16, S + kM6B + j * 64 * 16);
+    }
+    if (w < 2) {
+        const int64_t bi = (rbase + R0 + w * 64 + lane) * nb + i;
+        mq_load16(Bs + bi * 16, S + kM6S + w * 64 * 16);
+    } else if (w == 2) {
         mq_load4(M.xd + (size_t)acol * nb + i, S + kM6X);
     }
 }
@@ -347,9 +372,11 @@ extern "C" __global__ void __launch_bounds__(256, 1) oh_k_mmq_q6k(oh_mmq M) {
     }
     __syncthreads();
     const int acol = sact[lane];
+    int acs[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) acs[u] = sact[4 * (wave + 4 * u) + (lane >> 4)];
     auto stage = [&](int i, int buf) {
-        uint8_t *S = smem + buf * kM6Stage;
-        for (int L = wave; L < kM6Loads; L += 4) m6_stage_load(M, A, Bs, rbase, R0, i, S, L, lane, acol);
+        m6_stage_load(M, A, Bs, rbase, R0, i, smem + buf * kM6Stage, wave, lane, acs, acol);
     };
 
     const int h = lane >> 5, lr = lane & 31, arow = 32 * wave + lr;
@@ -397,7 +424,7 @@ extern "C" __global__ void __launch_bounds__(256, 1) oh_k_mmq_q6k(oh_mmq M) {
             m6_split(q6, (int)sc8[gq], alo, ahi);
 #pragma unroll
             for (int t = 0; t < 2; t++) {
-                const mq_v4i xb = *(const mq_v4i *)(S + kM6B + ((2 * ks + h) * 64 + 32 * t + lr) * 16);
+                const mq_v4i xb = *(const mq_v4i *)(S + kM6B + mq_act_slot(32 * t + lr, 2 * ks + h) * 16);
                 ihi[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ahi, xb, ihi[t], 0, 0, 0);
                 ilo[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(alo, xb, ilo[t], 0, 0, 0);
             }
