@@ -337,7 +337,7 @@ int mv_add_pair(MvBuild &b, const ornith_hip_tensor *W, const ornith_hip_tensor 
 // Lay the segments out over blocks: every wave gets a run of whole wave
 // steps sized so the launch spreads over about `waves` waves (4096, i.e. 16
 // per CU, for a standalone launch; the resident waves of the step kernel).
-void mv_plan(MvBuild &b, int waves) {
+void mv_plan(MvBuild &b, int waves, int small_waves) {
     int64_t steps = 0;
     int tk = -2;
     for (int i = 0; i < b.L.n; i++) {
@@ -350,6 +350,10 @@ void mv_plan(MvBuild &b, int waves) {
         }
     }
     b.tk = tk < 0 ? -1 : tk;
+    // launches of a few MB: fewer, longer waves (each block forms the
+    // activation once, so fewer blocks put less of that traffic ahead of the
+    // weights); large ones keep the full spread for bandwidth
+    if (small_waves > 0 && steps <= 4 * (int64_t)waves) waves = small_waves;
     const int64_t spw = (steps + waves - 1) / waves;
     int blocks = 0;
     b.lds = 0;

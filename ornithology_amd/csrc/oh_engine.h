@@ -338,7 +338,10 @@ int mv_add(MvBuild &b, const ornith_hip_tensor *W, const Act &act, float *y, int
 bool pairable(const ornith_hip_tensor *W, const ornith_hip_tensor *W2);
 int mv_add_pair(MvBuild &b, const ornith_hip_tensor *W, const ornith_hip_tensor *W2, const Act &act,
                        float *y, const int32_t *eidx = nullptr, int nsub = 1, int ystride = 0);
-void mv_plan(MvBuild &b, int waves = 4096);
+// Lay a launch's segments out over blocks for about `waves` waves; with
+// small_waves > 0, launches of at most 4 * waves wave steps are laid out for
+// small_waves instead.
+void mv_plan(MvBuild &b, int waves = 4096, int small_waves = 0);
 int mv_go(MvBuild &b, hipStream_t st);
 bool mmq_enabled();
 size_t matvec_col_bytes(int64_t in, int64_t out);

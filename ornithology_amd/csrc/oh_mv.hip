@@ -60,6 +60,16 @@ OH_DEV int group_isum(int v) {     // exact sum over the 8 lanes of a group
     return v;
 }
 
+// Smallest e = lane + 64k with a[k] == best over the wave (a[k]: lane's
+// element lane + 64k), from one ballot per quarter; 256 when none matches.
+// Wave-uniform.
+OH_DEV int first_hit(const float a[4], float best) {
+    const uint64_t m0 = __ballot(a[0] == best), m1 = __ballot(a[1] == best);
+    const uint64_t m2 = __ballot(a[2] == best), m3 = __ballot(a[3] == best);
+    return m0 ? (int)__builtin_ctzll(m0) : m1 ? 64 + (int)__builtin_ctzll(m1)
+         : m2 ? 128 + (int)__builtin_ctzll(m2) : m3 ? 192 + (int)__builtin_ctzll(m3) : 256;
+}
+
 // ---- Q8_K quantisation of one 256-element block held in LDS ------------------
 // One wave; exactly qdot_quantize_row_q8_K (src/ornith_qdot.c:32-62): the first
 // element of largest magnitude sets iscale = -127/x, codes = rint(iscale*x)
@@ -75,10 +85,7 @@ OH_DEV void q8k_block_from_lds(const float *v, int qb, int8_t *qs, float *d, int
     for (int k = 0; k < 4; k++) a[k] = fabsf(xb[lane + 64 * k]);
     // largest magnitude (NaN never wins), then its first index
     const float best = wave_max_fast(fmaxf(fmaxf(a[0], a[1]), fmaxf(a[2], a[3])));
-    int bi = 256;
-#pragma unroll
-    for (int k = 3; k >= 0; k--) if (a[k] == best) bi = lane + 64 * k;
-    bi = wave_min_fast(bi);
+    const int bi = first_hit(a, best);
     int8_t *q = qs + (int64_t)qb * qstride;
     int16_t *b = bs + (int64_t)qb * 16;
     auto put8 = [&](int8_t *p, int8_t x) { if (G) stc(p, x); else *p = x; };
@@ -133,14 +140,10 @@ OH_DEV void q8k_blocks(const float *v, int qb0, int qstep, int nb, int8_t *qs, f
     }
 #pragma unroll
     for (int n = 0; n < N; n++) best[n] = wave_max_fast(best[n]);
+    // first index of the largest magnitude: the lowest lane holding it in
+    // the first quarter (elements lane + 64k) that holds it at all
 #pragma unroll
-    for (int n = 0; n < N; n++) {
-        bi[n] = 256;
-#pragma unroll
-        for (int k = 3; k >= 0; k--) if (a[n][k] == best[n]) bi[n] = lane + 64 * k;
-    }
-#pragma unroll
-    for (int n = 0; n < N; n++) bi[n] = wave_min_fast(bi[n]);
+    for (int n = 0; n < N; n++) bi[n] = first_hit(a[n], best[n]);
 #pragma unroll
     for (int n = 0; n < N; n++) {
         const int qb = qb0 + n * qstep;
@@ -322,9 +325,18 @@ OH_DEV void iq2_tables_load() {
 }
 
 // outputs are read by later phases of the step kernel (device-scope accesses)
+// Output stores: device-scope (G) where a later phase of the same launch
+// reads them (the persistent step kernels), plain stores in a stand-alone
+// launch, whose end makes them visible to the next one.
+template <bool G = true>
+OH_DEV void put(float *p, float v) {
+    if (G) stc(p, v);
+    else stg(p, v);
+}
+template <bool G = true>
 OH_DEV void emit(float *y, int mode, int row, float v) {
-    if (mode == 1) stc(y + row, ldc(y + row) + v);
-    else stc(y + row, v);
+    if (mode == 1) put<G>(y + row, (G ? ldc(y + row) : ldg(y + row)) + v);
+    else put<G>(y + row, v);
 }
 
 // Fallback row of an F32 / F16 / BF16 tensor: convert on the fly and
@@ -723,13 +735,19 @@ OH_DEV void pro_load(PIn &p, const oh_mvseg &s, int slot) {
         const float4 *x = (const float4 *)(s.xf + ao);
         const bool wc = s.pro == OH_PRO_NORM;
         const float4 *w = (const float4 *)(wc ? s.nw : s.pro == OH_PRO_F32 ? s.xf + ao : s.xf2 + ao);
-        const int n4 = in / 4;
+        // nk float4 per thread cover the input (a uniform bound: no
+        // duplicate requests for the unused slots)
+        const int n4 = in / 4, nk = (n4 + 255) / 256;
 #pragma unroll
         for (int k = 0; k < 4; k++) {
-            const int i = tid + 256 * k < n4 ? tid + 256 * k : n4 - 1;
-            p.a[k] = ldc4(x + i);
-            p.b[k] = wc ? ldg(w + i) : ldc4(w + i);
-            if (s.pro == OH_PRO_GNORM) p.c[k] = ldg((const float4 *)s.nw + i % (s.gdim / 4));
+            if (k < nk) {
+                const int i = tid + 256 * k < n4 ? tid + 256 * k : n4 - 1;
+                p.a[k] = ldc4(x + i);
+                p.b[k] = wc ? ldg(w + i) : ldc4(w + i);
+                if (s.pro == OH_PRO_GNORM) p.c[k] = ldg((const float4 *)s.nw + i % (s.gdim / 4));
+            } else {
+                p.a[k] = p.b[k] = p.c[k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            }
         }
         if (s.pro == OH_PRO_GNORM) {
             if (s.runs16) {
@@ -749,46 +767,45 @@ OH_DEV void pro_load(PIn &p, const oh_mvseg &s, int slot) {
 
 // Q8_K of one 256-element block held in registers by a wave, four
 // consecutive elements x per lane (lane l: elements 4l..4l+3). Same result as
-// q8k_block_from_lds; codes are written as one packed word per lane. G: the
-// planes are global memory read by other workgroups (device-scope stores).
-template <bool G = false>
-OH_DEV void q8k_regs(const float4 x, int qb, int8_t *qs, float *d, int16_t *bs, int qstride) {
-    const int lane = lane_id();
+// q8k_block_from_lds: the scale comes from the first element of largest
+// magnitude, i.e. the first such element of the lowest lane holding one (a
+// ballot, then a read of that lane). q8k_pivot forms (largest magnitude,
+// signed element) and q8k_emit the codes, bsums and d, so that a wave can
+// run the reductions of several blocks back to back. G: the planes are
+// global memory read by other workgroups (device-scope stores).
+struct Q8kPiv { float best, piv; };
+OH_DEV Q8kPiv q8k_pivot(const float4 x) {
     const float a0 = fabsf(x.x), a1 = fabsf(x.y), a2 = fabsf(x.z), a3 = fabsf(x.w);
     const float best = wave_max_fast(fmaxf(fmaxf(a0, a1), fmaxf(a2, a3)));
-    int bi = 256;
-    if (a3 == best) bi = 4 * lane + 3;
-    if (a2 == best) bi = 4 * lane + 2;
-    if (a1 == best) bi = 4 * lane + 1;
-    if (a0 == best) bi = 4 * lane;
-    bi = wave_min_fast(bi);
+    const float v = a0 == best ? x.x : (a1 == best ? x.y : (a2 == best ? x.z : x.w));
+    const uint64_t m = __ballot(a0 == best || a1 == best || a2 == best || a3 == best);
+    const int l = m ? (int)__builtin_ctzll(m) : 0;
+    return {best, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l))};
+}
+template <bool G = false>
+OH_DEV void q8k_emit(const float4 x, const Q8kPiv p, int qb, int8_t *qs, float *d, int16_t *bs, int qstride) {
+    const int lane = lane_id();
     int *qw = (int *)(qs + (int64_t)qb * qstride) + lane;
     int16_t *b = bs + (int64_t)qb * 16;
     auto put32 = [&](int *p, int v) { if (G) stc(p, v); else *p = v; };
     auto put16 = [&](int16_t *p, int16_t v) { if (G) stc(p, v); else *p = v; };
     auto putf = [&](float *p, float v) { if (G) stc(p, v); else *p = v; };
-    if (best == 0.0f || !(best > 0.0f)) {
-        put32(qw, 0);
-        if (lane < 16) put16(b + lane, (int16_t)0);
-        if (lane == 0) putf(d + qb, 0.0f);
-        return;
-    }
-    const int sel = bi & 3;
-    const float mine = sel == 0 ? x.x : (sel == 1 ? x.y : (sel == 2 ? x.z : x.w));
-    const float iscale = -127.0f / shfl(mine, bi >> 2);
+    // an all-zero (or NaN-led) block has zero codes, bsums and d
+    const bool zero = p.best == 0.0f || !(p.best > 0.0f);
+    const float iscale = zero ? 0.0f : -127.0f / p.piv;
     int c[4];
     const float xs[4] = {x.x, x.y, x.z, x.w};
 #pragma unroll
     for (int j = 0; j < 4; j++) {
         const int v = (int)__builtin_rintf(iscale * xs[j]);
-        c[j] = v > 127 ? 127 : (v < -128 ? -128 : v);
+        c[j] = zero ? 0 : (v > 127 ? 127 : (v < -128 ? -128 : v));
     }
     put32(qw, (c[0] & 0xff) | ((c[1] & 0xff) << 8) | ((c[2] & 0xff) << 16) | ((c[3] & 0xff) << 24));
     int sv = c[0] + c[1] + c[2] + c[3];
     sv += dpp_i<0xB1>(sv);
     sv += dpp_i<0x4E>(sv);                         // codes 16*(lane/4) .. +15
     if ((lane & 3) == 0) put16(b + (lane >> 2), (int16_t)sv);
-    if (lane == 0) putf(d + qb, 1.0f / iscale);
+    if (lane == 0) putf(d + qb, zero ? 0.0f : 1.0f / iscale);
 }
 
 OH_DEV void pro_compute(const PIn &p, const oh_mvseg &s, int slot, int blk, uint8_t *smem, double *red) {
@@ -866,13 +883,19 @@ OH_DEV void pro_compute(const PIn &p, const oh_mvseg &s, int slot, int blk, uint
         }
     }
     const bool store = blk == 0 && s.oqs != nullptr;
+    // the pivots of the wave's blocks wave + 4k first (independent
+    // reductions back to back), then their codes
+    Q8kPiv pv[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+        if (wave + 4 * k < nb) pv[k] = q8k_pivot(fv[k]);
 #pragma unroll
     for (int k = 0; k < 4; k++) {
         const int qb = wave + 4 * k;
         if (qb < nb) {
             if (blk == 0 && s.oxf) stc4((float4 *)(s.oxf + ao) + tid + 256 * k, fv[k]);
-            q8k_regs(fv[k], qb, aqs, ad, abs, kAS);
-            if (store) q8k_regs<true>(fv[k], qb, s.oqs + ao, s.oqd + ao / 256, s.oqb + ao / 16, 256);
+            q8k_emit(fv[k], pv[k], qb, aqs, ad, abs, kAS);
+            if (store) q8k_emit<true>(fv[k], pv[k], qb, s.oqs + ao, s.oqd + ao / 256, s.oqb + ao / 16, 256);
         }
     }
     lds_barrier();
@@ -925,10 +948,10 @@ OH_DEV void mv_seg(const oh_mvseg &s, int slot, int blk, int expert, uint8_t *sm
         for (int i = 0; i < nb; i++) acc += shfl(t, rl * nb + i);
         if (s.pair) {
             if ((st & 1) == 0) gsum = acc;
-            else if (live && sb == 0) emit(y, 0, row, ref_silu(gsum) * acc);
+            else if (live && sb == 0) emit<W::kGrid>(y, 0, row, ref_silu(gsum) * acc);
         } else if (live && sb == 0) {
-            if (s.mode == 1 && st == 0) stc(y + row, ypre + acc);
-            else emit(y, s.mode, row, acc);
+            if (s.mode == 1 && st == 0) put<W::kGrid>(y + row, ypre + acc);
+            else emit<W::kGrid>(y, s.mode, row, acc);
         }
     };
     auto y_prefetch = [&]() {
