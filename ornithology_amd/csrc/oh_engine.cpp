@@ -354,7 +354,11 @@ void mv_plan(MvBuild &b, int waves, int small_waves) {
     // activation once, so fewer blocks put less of that traffic ahead of the
     // weights); large ones keep the full spread for bandwidth
     if (small_waves > 0 && steps <= 4 * (int64_t)waves) waves = small_waves;
-    const int64_t spw = (steps + waves - 1) / waves;
+    // and launches of hundreds of MB (lm_head): two steps per wave, many
+    // short blocks, so the last of them finish close together (measured
+    // 53.5 us for C3's 286 MB lm_head against 61.8 us at 8 steps per wave)
+    int64_t spw = (steps + waves - 1) / waves;
+    if (steps > 4 * (int64_t)waves && spw > 2) spw = 2;
     int blocks = 0;
     b.lds = 0;
     for (int i = 0; i < b.L.n; i++) {
@@ -362,6 +366,10 @@ void mv_plan(MvBuild &b, int waves, int small_waves) {
         const bool q8 = seg_q8(s);
         if (seg_steps(s)) {
             s.upw = (int)(spw / (s.pair ? 2 : 1) > 0 ? spw / (s.pair ? 2 : 1) : 1);
+            // a Q6_K step costs about twice a Q4_K one: half the run, so a
+            // Q6_K segment beside Q4_K ones (attn_v in the q/k/v launch)
+            // ends with them
+            if (s.type == OH_Q6_K && s.upw > 1) s.upw = (s.upw + 1) / 2;
             s.bps = (s.units + OH_MV_WAVES * s.upw - 1) / (OH_MV_WAVES * s.upw);
         } else {
             s.upw = 1;
