@@ -326,6 +326,15 @@ int build_body(ornith_hip_session *s, Prog &P) {
                 D.type = (int)dt; D.nb = nbd; D.in = I; D.rows = H; D.k = K; D.stride = IW;
                 const double db = (double)ns * ((double)H * gguf_nbytes(dt, (uint64_t)I) + 4.0 * I) + 8.0 * H + 4.0 * K;
                 oh_op o = op_new(OH_OP_MV_DOWN, (H + rps - 1) / rps, dlds);
+                if (!P.step && 16 % nbd == 0) {
+                    // narrow form: 16 / nb rows per block, four times the
+                    // blocks, each requesting only its rows' weights
+                    // (measured 9.3 -> 8.4 us per C3 launch, same bits)
+                    const int rn = 16 / nbd;
+                    D.narrow = 1;
+                    o.nvb = (H + rn - 1) / rn;
+                    o.lds = ns * sq + ns * I * 4 + ns * rn * 4;
+                }
                 if (P.step) {
                     // split form: (row group, 4-slot group) blocks, last one combines
                     D.dots = s->ddots;

@@ -307,7 +307,12 @@ hipError_t oh_launch_op(const oh_op *op, const int32_t *io, hipStream_t st) {
         return oh_launch_matvec(&op->u.mv, op->tk, op->lds, st);
     case OH_OP_MV_DOWN: {
         const int ns = op->u.down.k + (op->u.down.sA ? 1 : 0);
-        hipLaunchKernelGGL(oh_k_mv_down, g, dim3(64 * ns), (size_t)op->lds, st, op->u.down);
+        if (op->u.down.narrow) {
+            if (ns > 16 || 16 % op->u.down.nb) return hipErrorInvalidValue;
+            hipLaunchKernelGGL(oh_k_mv_down_narrow, g, dim3(64 * ((ns + 3) / 4)), (size_t)op->lds, st, op->u.down);
+        } else {
+            hipLaunchKernelGGL(oh_k_mv_down, g, dim3(64 * ns), (size_t)op->lds, st, op->u.down);
+        }
         break;
     }
     case OH_OP_EMBED: hipLaunchKernelGGL(oh_k_embed, g, b256, 0, st, op->u.embed, io); break;

@@ -1320,6 +1320,95 @@ OH_DEV void down_body(const oh_mvdown &D, int vb, W &wt) {
     }
 }
 
+// Fused down projection, narrow form: a block owns R = 64 / (4 nb) rows and
+// every slot; wave w reduces slots 4w .. 4w + 3 (lane: slot 4w + lane / (R nb),
+// row lane / nb % R, super-block lane % nb), so each block requests only its
+// rows' weights (4x the blocks of down_body at the same activation work per
+// block). Same arithmetic and orders as down_body.
+template <int T>
+OH_DEV void down_narrow(const oh_mvdown &D, int vb) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ float cw[17];
+    constexpr int HA = 8;                                 // h float4 per thread
+    const int lane = lane_id(), wave = __builtin_amdgcn_readfirstlane(tid_x() >> 6), tid = tid_x();
+    const int nw = (int)(blockDim.x >> 6), bd = (int)blockDim.x;
+    const int nb = D.nb, in = D.in, ns = D.k + (D.sA ? 1 : 0), R = 64 / (4 * nb);
+    const int js = lane / (R * nb), rl = (lane / nb) % R, sb = lane % nb;
+    const int j0 = 4 * wave + js, j = j0 < ns ? j0 : ns - 1;
+    const bool act = j0 < ns;
+    const int row0 = vb * R, row = row0 + rl;
+    const int rowc = row < D.rows ? row : D.rows - 1;
+    const int sq = (nb * kAS + nb * 36 + 15) & ~15;
+    float *v = (float *)(smem + ns * sq);
+    float *dots = v + ns * in;                            // [ns][R]
+    const bool sh = j >= D.k;
+    const int e = sh ? 0 : ldc(D.eidx + j);
+    const bool comb = wave == 0 && lane < R && row0 + lane < D.rows;
+    const float xrow = comb ? ldc(D.x + row0 + lane) : 0.0f;
+    const float cwv = tid < D.k ? ldc(D.w + tid) : (tid == 16 && D.shg ? ldc(D.shg) : 1.0f);
+    const int nf = ns * in / 4;
+    const bool hreg = nf <= HA * bd;
+    float4 ha[HA];
+    if (hreg) {
+#pragma unroll
+        for (int k = 0; k < HA; k++) {
+            const int f = tid + bd * k < nf ? tid + bd * k : nf - 1;
+            const int jj = 4 * f / in, el = 4 * f - jj * in;
+            ha[k] = ldc4((const float4 *)((jj < D.k ? D.h + (size_t)jj * D.stride : D.hsh) + el));
+        }
+    }
+    const WP wp = sh ? WP{D.sA, D.sB, D.sC} : WP{D.A, D.B, D.C};
+    SB<T> r;
+    sb_load(r, wp, (((int64_t)(sh ? 0 : e)) * D.rows + rowc) * nb + sb);
+    __builtin_amdgcn_sched_barrier(0);
+    if (tid <= 16) cw[tid] = cwv;
+    if (hreg) {
+#pragma unroll
+        for (int k = 0; k < HA; k++)
+            if (tid + bd * k < nf) ((float4 *)v)[tid + bd * k] = make_float4(ha[k].x, ha[k].y, ha[k].z, ha[k].w);
+    } else {
+        for (int i = tid; i < ns * in; i += bd) {
+            const int jj = i / in, el = i - jj * in;
+            v[i] = ldc((jj < D.k ? D.h + (size_t)jj * D.stride : D.hsh) + el);
+        }
+    }
+    lds_barrier();
+    for (int jj = wave; jj < ns; jj += nw) {              // wave jj % nw quantises slot jj
+        uint8_t *b = smem + (size_t)jj * sq;
+        if (nb == 2) {
+            q8k_blocks<2>(v + (size_t)jj * in, 0, 1, nb, (int8_t *)b, (float *)(b + mv_lds_d_off(nb)),
+                          (int16_t *)(b + mv_lds_bs_off(nb)), kAS);
+        } else {
+            for (int q0 = 0; q0 < nb; q0 += 4)
+                q8k_blocks<4>(v + (size_t)jj * in, q0, 1, nb, (int8_t *)b, (float *)(b + mv_lds_d_off(nb)),
+                              (int16_t *)(b + mv_lds_bs_off(nb)), kAS);
+        }
+    }
+    lds_barrier();
+    {
+        const uint8_t *b = smem + (size_t)j * sq;
+        const float tw = sb_term(r, (const int8_t *)b + sb * kAS, (const int16_t *)(b + mv_lds_bs_off(nb)) + sb * 16,
+                                 ((const float *)(b + mv_lds_d_off(nb)))[sb]);
+        const bool live = act && row < D.rows;
+        const float t = live ? tw : 0.0f;
+        const int base = lane - sb;
+        float acc = 0.0f;
+        for (int i = 0; i < nb; i++) acc += shfl(t, base + i);
+        if (act && sb == 0) dots[j * R + rl] = acc;
+    }
+    lds_barrier();
+    if (comb) {
+        float acc = 0.0f;
+        for (int jj = 0; jj < D.k; jj++) acc += cw[jj] * dots[jj * R + lane];
+        if (D.sA) {
+            const float so = dots[D.k * R + lane];
+            const float vv = D.shg ? so * cw[16] : so;
+            acc += vv;
+        }
+        stg(D.x + row0 + lane, xrow + acc);
+    }
+}
+
 // Split form of the fused down projection for the step kernel, where a block
 // has 4 waves: virtual block vb = (row group rg of 64/nb rows, slot group g);
 // wave w reduces slot j = 4g + w over the row group (its activation Q8_K(h_j)
@@ -1502,6 +1591,13 @@ extern "C" __global__ void __launch_bounds__(256) oh_k_mv_mixed(oh_mvlaunch L) {
 }
 
 // one wave per slot (blockDim = 64 * slots)
+extern "C" __global__ void __launch_bounds__(256) oh_k_mv_down_narrow(oh_mvdown D) {
+    switch (D.type) {
+    case OH_Q4_K: down_narrow<OH_Q4_K>(D, (int)blockIdx.x); break;
+    case OH_Q6_K: down_narrow<OH_Q6_K>(D, (int)blockIdx.x); break;
+    default: down_narrow<OH_Q8_0>(D, (int)blockIdx.x); break;
+    }
+}
 extern "C" __global__ void __launch_bounds__(640) oh_k_mv_down(oh_mvdown D0) {
     NoWait w;
     // token blockIdx.y of a batch (0: the only token)

@@ -167,6 +167,9 @@ typedef struct {
     float *dots;
     int *cnt;
     int type, nb, in, rows, k, stride;
+    // narrow form (stand-alone token-step launch): a block owns 16 / nb rows
+    // and every slot (oh_k_mv_down_narrow, 64 * ceil(slots / 4) threads)
+    int narrow;
 } oh_mvdown;
 
 // ---- operations of the token step -------------------------------------------
