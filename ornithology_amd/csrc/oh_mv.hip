@@ -995,7 +995,55 @@ OH_DEV void mv_seg(const oh_mvseg &s, int slot, int blk, int expert, uint8_t *sm
     }
 }
 
-// MoE routing of a block (src/ornith_moe.c:8-30): expert e's rank is the
+// Top-k routing of one token by wave 0 of a block (ne = 64 V logits, lane l
+// holding experts V l .. V l + V - 1): k rounds of a wave maximum, the
+// lowest index among equal maxima taken (the reference's ascending scan with
+// strict '>'), the pick removed from its lane. The softmax over the picks in
+// selection order: max = the first pick, e_s = expf(l_s - max), the sum in
+// order, w_s = e_s / sum. Returns false (nothing written) when a logit is NaN
+// or -inf: the sequential selection handles those.
+template <int V>
+OH_DEV bool route_fast(const float *rlog, int k, int *sel, float *rw) {
+    const int lane = lane_id();
+    float a[V];
+#pragma unroll
+    for (int q = 0; q < V / 4; q++) {
+        const float4 t = ldc4((const float4 *)rlog + V / 4 * lane + q);
+        a[4 * q] = t.x; a[4 * q + 1] = t.y; a[4 * q + 2] = t.z; a[4 * q + 3] = t.w;
+    }
+    bool fin = true;
+#pragma unroll
+    for (int j = 0; j < V; j++) fin = fin && a[j] > -INFINITY;
+    if (__ballot(!fin)) return false;
+    float mine = 0.0f, mx = 0.0f;
+    int pick = 0;
+    for (int s = 0; s < k; s++) {
+        float m = a[0];
+#pragma unroll
+        for (int j = 1; j < V; j++) m = fmaxf(m, a[j]);
+        const float M = wave_max_fast(m);
+        int jl = V;
+#pragma unroll
+        for (int j = V - 1; j >= 0; j--) if (a[j] == M) jl = j;
+        const uint64_t hm = __ballot(jl < V);
+        const int L = (int)__builtin_ctzll(hm);
+        const int J = __builtin_amdgcn_readlane(jl, L);
+        if (lane == L) {
+#pragma unroll
+            for (int j = 0; j < V; j++) if (j == J) a[j] = -INFINITY;
+        }
+        if (s == 0) mx = M;
+        if (lane == s) { mine = M; pick = V * L + J; }
+    }
+    const float e = lane < k ? ref_expf(mine - mx) : 0.0f;
+    float sum = 0.0f;
+    for (int s = 0; s < k; s++) sum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), s));
+    if (lane < k) { sel[lane] = pick; rw[lane] = e / sum; }
+    return true;
+}
+
+// MoE routing of a block (src/ornith_moe.c:8-30). With 256 or 512 experts
+// wave 0 selects them (route_fast). Otherwise expert e's rank is the
 // number of experts that precede it in the reference's selection order
 // (larger logit, or equal logit and lower index); the k experts of rank < k in
 // rank order are the reference's picks. Softmax over the selected logits in
@@ -1008,6 +1056,28 @@ OH_DEV void route_block(const oh_mvlaunch &L, int tok, bool store, float *lg, in
     const int ne4 = (ne + 3) & ~3;
     const bool has_sh = L.shl != nullptr;
     const float *rlog = L.rlog + (size_t)tok * ne;
+    if ((ne == 256 || ne == 512) && k <= 64) {
+        // wave 0 selects; the other waves wait at the barrier
+        int ok = 1;
+        if (tid < 64) {
+            ok = ne == 256 ? route_fast<4>(rlog, k, sel, rw) : route_fast<8>(rlog, k, sel, rw);
+            if (ok && tid == 0 && has_sh) *shg = ref_sigmoid(ldc(L.shl + tok));
+            if (tid == 0) *bad = !ok;
+        }
+        __syncthreads();
+        if (*bad) {
+            for (int e = tid; e < ne4; e += 256) lg[e] = e < ne ? ldc(rlog + e) : -INFINITY;
+            __syncthreads();
+            if (tid < 64) route_wave(lg, ne, k, nullptr, sel, rw, shg);
+            if (tid == 0 && has_sh) *shg = ref_sigmoid(ldc(L.shl + tok));
+            __syncthreads();
+        }
+        if (store) {
+            if (tid < k) { stc(L.ridx + (size_t)tok * k + tid, (int32_t)sel[tid]); stc(L.rw + (size_t)tok * k + tid, rw[tid]); }
+            if (tid == 0 && has_sh) stc(L.shg + tok, *shg);
+        }
+        return;
+    }
     if (tid == 0) *bad = 0;
     if (tid < 64) cnt[tid] = 0;
     for (int e = tid; e < ne4; e += 256) lg[e] = e < ne ? ldc(rlog + e) : -INFINITY;
