@@ -619,6 +619,16 @@ extern "C" __global__ void __launch_bounds__(64)
 oh_k_route_rows(const float *logits, int ne, int k, const float *shgate_logit, int32_t *idx, float *w,
                 float *shgate) {
     const size_t t = blockIdx.x;
+    // 256 / 512 experts: the expert launch's selection (route_fast), the
+    // sequential one when a logit is NaN or -inf
+    if ((ne == 256 || ne == 512) && k <= 64) {
+        const bool ok = ne == 256 ? route_fast<4>(logits + t * ne, k, idx + t * k, w + t * k)
+                                  : route_fast<8>(logits + t * ne, k, idx + t * k, w + t * k);
+        if (ok) {
+            if (lane_id() == 0 && shgate_logit) shgate[t] = ref_sigmoid(shgate_logit[t]);
+            return;
+        }
+    }
     route_wave(logits + t * ne, ne, k, shgate_logit ? shgate_logit + t : nullptr, idx + t * k, w + t * k,
                shgate ? shgate + t : nullptr);
 }
