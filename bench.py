@@ -427,8 +427,11 @@ def c5_bench(args) -> int:
     sess.free()
     bt = None
     if args.batch > 0:
-        bt = batch_decode(model, args.batch, T, args.batch_steps)
-        log(f"C5 batch {args.batch}: {bt['ms_per_step']:.2f} ms/step -> {bt['tok_s']:.1f} tok/s")
+        try:
+            bt = batch_decode(model, args.batch, T, args.batch_steps)
+            log(f"C5 batch {args.batch}: {bt['ms_per_step']:.2f} ms/step -> {bt['tok_s']:.1f} tok/s")
+        except oa.HipError as e:
+            log(f"C5 batch decode skipped: {e}")
     tok_s = steps / (ms / 1e3)
     print(json.dumps({"metric": "C5 long-context decode tok/s after a chunked 32K prefill", "value": round(tok_s, 2),
                       "unit": "tok/s", "n_gpus": 1, "steps": steps, "ms_per_step": round(ms / steps, 4),
@@ -570,7 +573,9 @@ def main() -> int:
     ap.add_argument("--profile-reps", type=int, default=3)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--batch", type=int, default=8, help="sessions of the batch-decode figure (0: skip)")
+    ap.add_argument("--batch", type=int, default=0,
+                    help="sessions of the batch-decode figure (0: skip; the batch step refuses contexts past the "
+                         "exact attention walk, so the figure is off by default)")
     ap.add_argument("--batch-steps", type=int, default=32)
     ap.add_argument("--timeline", action="store_true",
                     help="print where one C3 decode step's time goes, stage by stage (markdown), then exit")
@@ -675,9 +680,12 @@ def main() -> int:
 
     batch = None
     if args.batch > 0:
-        batch = batch_decode(model, args.batch, args.ctx, args.batch_steps)
-        log(f"batch decode: {args.batch} sessions at {args.ctx} context: {batch['ms_per_step']:.2f} ms/step "
-            f"-> {batch['tok_s']:.1f} tok/s")
+        try:
+            batch = batch_decode(model, args.batch, args.ctx, args.batch_steps)
+            log(f"batch decode: {args.batch} sessions at {args.ctx} context: {batch['ms_per_step']:.2f} ms/step "
+                f"-> {batch['tok_s']:.1f} tok/s")
+        except oa.HipError as e:
+            log(f"batch decode skipped: {e}")
 
     cpu = None
     if not args.no_cpu:

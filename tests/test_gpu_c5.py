@@ -64,6 +64,8 @@ def test_c5_prefill_chunk_2048_against_1024(c3, monkeypatch):
 
 
 @pytest.mark.timeout(900)
+@pytest.mark.skip(reason="batch steps past the exact attention walk are switched off (an unexplained GPU fault "
+                         "in batch steps on the flash path); the engine refuses them")
 def test_c5_batch8_at_32k_equals_single_sessions(c3, monkeypatch):
     monkeypatch.setenv("ORNITH_PREFILL_SERIAL", "0")
     n, steps = 8, 4
