@@ -15,8 +15,10 @@ Prints ONE JSON line (driver contract) with the roofline of the dominant
 kernel (per-launch HIP-event timing of one eager step) and the CPU baseline
 (the oracle port on a bounded sample on this host's cores). Also reported:
 the prompt rate (`prefill_tok_s`; `prefill_wy_tok_s` with the delta-net
-chunks on the matrix cores, ORNITH_HIP_DELTA_MFMA=1) and `batch_decode`, 8 sessions with their
-own 4096-token prompts stepped together (Model.batch_step).
+chunks on the matrix cores, ORNITH_HIP_DELTA_MFMA=1) and, with `--batch N`, `batch_decode`: N
+sessions with their own prompts stepped together (Model.batch_step; null by
+default, and null with the engine's refusal logged when the contexts are past
+the exact attention walk, where the batch step is switched off).
 """
 from __future__ import annotations
 
