@@ -26,7 +26,7 @@ OH_DEV float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
 // reduction r = x*N/ln2 - k and the polynomial are fused multiply-adds, which is
 // how the x86-64 FMA build of glibc evaluates them; that form matched glibc's
 // expf on every float input.
-__constant__ uint64_t k_exp2_tab[32] = {
+static __constant__ uint64_t k_exp2_tab[32] = {
     0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull,
     0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull,
     0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull,

@@ -1,14 +1,14 @@
-// oh_kernels.hip - the single device translation unit of the engine: the
-// kernels of oh_mv.hip and oh_layers.hip plus their host launchers.
+// oh_kernels.hip - the main device translation unit of the engine: the
+// per-operation kernels and their host launchers. The two persistent decode
+// kernels sit in translation units of their own (oh_kernels_step.hip,
+// oh_kernels_decode.hip) so that the three compile in parallel.
 #include "oh_mv.hip"
 #include "oh_layers.hip"
 #include "oh_synth.hip"
-#include "oh_step.hip"
 #include "oh_prefill.hip"
 #include "oh_mmq.hip"
 #include "oh_batch.hip"
 #include "oh_attn_mfma.hip"
-#include "oh_decode.hip"
 #include "oh_delta_mfma.hip"
 #include "oh_launch.h"
 
@@ -391,32 +391,6 @@ int oh_exact_lds_bytes(int hd, int exact_max) {
 // delta step LDS of the working wave (step kernel: dynamic LDS)
 int oh_delta_lds_bytes(int dk) { return (2 * dk + 64 * (dk + 4)) * 4; }
 int oh_delta16_lds_bytes(int dk) { return delta16_lds_floats(dk) * 4; }
-
-hipError_t oh_step_blocks_per_cu(int lds_bytes, int *blocks) {
-    hipError_t e = hipFuncSetAttribute((const void *)oh_k_step, hipFuncAttributeMaxDynamicSharedMemorySize, lds_bytes);
-    if (e != hipSuccess) return e;
-    return hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks, (const void *)oh_k_step, 256, (size_t)lds_bytes);
-}
-
-hipError_t oh_decode_blocks_per_cu(int lds_bytes, int *blocks) {
-    hipError_t e = hipFuncSetAttribute((const void *)oh_k_decode, hipFuncAttributeMaxDynamicSharedMemorySize, lds_bytes);
-    if (e != hipSuccess) return e;
-    return hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks, (const void *)oh_k_decode, 256, (size_t)lds_bytes);
-}
-
-hipError_t oh_launch_decode(const oh_dop *prog, int nops, int32_t *io, int advance, int grid, int lds_bytes,
-                            hipStream_t st, uint64_t *ts, int prof_op, uint64_t *ts2) {
-    void *args[] = {(void *)&prog, (void *)&nops, (void *)&io, (void *)&advance, (void *)&ts, (void *)&prof_op,
-                    (void *)&ts2};
-    return hipLaunchCooperativeKernel((const void *)oh_k_decode, dim3(grid), dim3(256), args, (size_t)lds_bytes, st);
-}
-
-hipError_t oh_launch_step(const oh_op *prog, int nops, int32_t *io, unsigned *ctrs, int epoch_slot, int advance,
-                          uint64_t *ts, int grid, int lds_bytes, hipStream_t st) {
-    void *args[] = {(void *)&prog, (void *)&nops, (void *)&io, (void *)&ctrs, (void *)&epoch_slot,
-                    (void *)&advance, (void *)&ts};
-    return hipLaunchCooperativeKernel((const void *)oh_k_step, dim3(grid), dim3(256), args, (size_t)lds_bytes, st);
-}
 
 hipError_t oh_launch_moe_route(const float *logits, int ne, int k, const float *shgate_logit,
                                int32_t *idx, float *w, float *shgate, hipStream_t st) {

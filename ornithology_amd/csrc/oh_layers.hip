@@ -1248,6 +1248,7 @@ OH_DEV void argmax2_body(const oh_op_argmax &a, int pos, W &w) {
     }
 }
 
+#ifndef OH_BODIES_ONLY
 // ---- standalone kernels (one launch per operation, captured into HIP graphs) -------
 extern "C" __global__ void __launch_bounds__(256) oh_k_embed(oh_op_embed a, const int32_t *io) {
     NoWait w;
@@ -1310,3 +1311,5 @@ oh_k_moe_route(const float *logits, int ne, int k, const float *shgate_logit,
 
 // advance the stream position after a token's layers (rforward_token s->pos++)
 extern "C" __global__ void oh_k_advance(int32_t *io_pos) { *io_pos = *io_pos + 1; }
+
+#endif // OH_BODIES_ONLY

@@ -24,7 +24,7 @@
 #include "oh_types.h"
 #include "../../include/ornith_iq2xxs_grid.h"
 
-__constant__ uint64_t k_iq2_grid[256] = { ORNITH_IQ2XXS_GRID_VALUES };
+static __constant__ uint64_t k_iq2_grid[256] = { ORNITH_IQ2XXS_GRID_VALUES };
 
 namespace {
 
@@ -1643,6 +1643,9 @@ OH_DEV void mvb_body(const oh_mvbatch &B) {
 
 } // namespace
 
+// The stand-alone kernels; a translation unit that only needs the bodies above
+// (the persistent kernels) defines OH_BODIES_ONLY.
+#ifndef OH_BODIES_ONLY
 extern "C" __global__ void __launch_bounds__(256) oh_k_mv_q4k(oh_mvlaunch L) {
     NoWait w;
     mv_body<OH_Q4_K>(L, (int)blockIdx.x, w);
@@ -1839,3 +1842,5 @@ oh_k_norm_q8k_rows(const float *x, const float *norm_w, float eps, int n, float 
     for (int qb = wave; qb < nqb; qb += 4)
         q8k_block_from_lds(v, qb, qs + r * n, d + r * nqb, bs + r * nqb * 16, 256, bp ? bp + r * nqb * 16 : nullptr);
 }
+
+#endif // OH_BODIES_ONLY
