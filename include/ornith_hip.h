@@ -151,7 +151,9 @@ const ornith_hip_tensor *ornith_hip_model_tensor(const ornith_hip_model *m, cons
 int  ornith_hip_session_new(ornith_hip_model *m, int cap, ornith_hip_session **out);
 void ornith_hip_session_free(ornith_hip_session *s);                             /* rmodel_session_free */
 /* rmodel_session_eval (src/ornith_rforward.c:838-849,933-944): the prompt runs
- * layer by layer over chunks of up to 2048 tokens (batched projections). As in
+ * layer by layer over engine chunks of up to 4096 tokens (ORNITH_HIP_PREFILL_CHUNK,
+ * a multiple of 32; the chunk length changes no result bit) with batched
+ * projections. As in
  * the reference, gated delta-net layers use the chunked scan of 32-token
  * chunks (src/ornith_attn.c:215-349) unless ORNITH_PREFILL_SERIAL=1 selects the
  * token recurrence; either way the results are the reference's bits for that

@@ -239,6 +239,18 @@ int orc_session_seed_context(orc_session *s, int n, uint64_t seed) {
     return 0;
 }
 
+int orc_session_adopt(orc_session *s, int n, const float *logits) {
+    const orc_arch *a = &s->m->a;
+    if (n < 0 || n >= s->cap || !logits) return -1;
+    for (int l = 0; l < a->n_layers; l++)
+        if (is_full(a, l)) s->kv[l].len = n;
+    memcpy(s->logits, logits, (size_t)a->vocab * sizeof(float));
+    s->pos = n;
+    s->nhist = n;
+    s->have_logits = 1;
+    return 0;
+}
+
 /* ---- layer math (src/ornith_rforward.c:282-503) ----------------------------- */
 static float decay_alpha(float a_in, float a_coef, float dt_bias) {
     return expf(a_coef * orc_softplus(a_in + dt_bias));

@@ -184,6 +184,13 @@ orc_kv *orc_session_kv(orc_session *s, int L);
  * token steps cost what they cost at that context. Returns 0, or -1 when the
  * session is not empty, n is out of range or the cache is not Q8. */
 int orc_session_seed_context(orc_session *s, int n, uint64_t seed);
+/* Test aid, not part of the reference's algorithm: take the state the caller
+ * wrote through orc_session_delta / _conv / _kv (a session's state computed
+ * elsewhere, e.g. by the GPU engine) as that of a session at position n whose
+ * last evaluation gave `logits`, so that token steps continue from it. Every
+ * full-attention layer's cache then holds n positions. Returns 0, or -1 when
+ * n is out of range. */
+int orc_session_adopt(orc_session *s, int n, const float *logits);
 
 /* ---- random-init GGUF generator --------------------------------------- */
 typedef struct {

@@ -285,7 +285,7 @@ int batch_enqueue(const BatchPlan &B, hipStream_t st) {
             }
             HCHK(oh_launch_route_rows(p.RL, a.ne, K, y.gate_inp_sh ? p.SHL : nullptr, p.RIDX, p.RW,
                                       y.gate_inp_sh ? p.SHG : nullptr, n, st));
-            HCHK(oh_launch_group_pairs(p.RIDX, n * K, p.CNT, a.ne, p.LIST, n, st));
+            HCHK(oh_launch_group_pairs(p.RIDX, n * K, p.CNT, a.ne, p.LIST, n, s0->io + OH_IO_ERR, st));
             const int max_items = (n * K + 63) / 64 + a.ne;
             HCHK(oh_launch_mmq_items(p.CNT, a.ne, p.ITEMS, st));
             CHK(pf_swiglu(y.gate_exps, y.up_exps, p.XQ, I, n * K, n, p.HQ, p.GU, p.Hh, st, p.CNT, p.LIST, n, K, a.ne,
@@ -473,6 +473,7 @@ extern "C" int ornith_hip_batch_step(ornith_hip_session **ss, int n, const int32
     std::vector<int32_t> hn((size_t)n);
     HCHK(hipMemcpyAsync(hn.data(), p.IDX, (size_t)n * 4, hipMemcpyDeviceToHost, st));
     HCHK(hipStreamSynchronize(st));
+    CHK(step_check(s0));
     for (int b = 0; b < n; b++) {
         ss[b]->pos += 1;
         ss[b]->have_logits = true;

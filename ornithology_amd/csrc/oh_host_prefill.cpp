@@ -2,7 +2,7 @@
 #include "oh_engine.h"
 
 
-// tokens per engine chunk (ORNITH_HIP_PREFILL_CHUNK, default 2048): a multiple
+// tokens per engine chunk (ORNITH_HIP_PREFILL_CHUNK, default kPfChunk = 4096): a multiple
 // of 32, because the chunked delta scan counts its 32-token chunks from the
 // start of the evaluation and an engine chunk must not split one
 // prompt attention past the exact walk on the matrix cores; on unless
@@ -285,7 +285,7 @@ int pf_chunk(ornith_hip_session *s, int base, int T, bool chunked, hipStream_t s
                 }
                 CHK(mv_go(b3, st));
             } else {
-                HCHK(oh_launch_group_pairs(p.RIDX, T * K, p.CNT, a.ne, p.LIST, T, st));
+                HCHK(oh_launch_group_pairs(p.RIDX, T * K, p.CNT, a.ne, p.LIST, T, s->io + OH_IO_ERR, st));
                 const int max_items = (T * K + 63) / 64 + a.ne;
                 HCHK(oh_launch_mmq_items(p.CNT, a.ne, p.ITEMS, st));
                 CHK(pf_swiglu(y.gate_exps, y.up_exps, p.XQ, I, T * K, T, p.HQ, p.GU, p.Hh, st, p.CNT, p.LIST, T, K,

@@ -489,12 +489,18 @@ int step_launch(ornith_hip_session *s, bool body, uint64_t *ts, bool advance) {
     return ORNITH_HIP_OK;
 }
 
-// a grid wait of the step kernel that gave up leaves io[OH_IO_ERR] set
+// io[OH_IO_ERR]: a grid wait of a persistent kernel that gave up, or an
+// expert pair list that would have overflowed (the list was left unwritten)
 int step_check(ornith_hip_session *s) {
     int32_t err = 0;
     HCHK(hipMemcpy(&err, s->io + OH_IO_ERR, 4, hipMemcpyDeviceToHost));
-    if (err) {
+    if (err & OH_ERR_WAIT) {
         seterr("decode step: a wait between workgroups timed out; the session state is undefined");
+        return ORNITH_HIP_ERR_DEVICE;
+    }
+    if (err) {
+        seterr("MoE: a token routed to one expert twice or outside the experts (router logits all NaN or -inf); "
+               "the session state is undefined");
         return ORNITH_HIP_ERR_DEVICE;
     }
     return ORNITH_HIP_OK;

@@ -258,9 +258,10 @@ hipError_t oh_launch_route_rows(const float *logits, int ne, int k, const float 
     return hipGetLastError();
 }
 hipError_t oh_launch_group_pairs(const int32_t *idx, int npairs, int32_t *cnt, int ne, int32_t *list, int lstride,
-                                 hipStream_t st) {
+                                 int32_t *err, hipStream_t st) {
     hipLaunchKernelGGL(oh_k_fill_i32, dim3((ne + 255) / 256), dim3(256), 0, st, cnt, ne, 0);
-    hipLaunchKernelGGL(oh_k_group_pairs, dim3((npairs + 255) / 256), dim3(256), 0, st, idx, npairs, cnt, list, lstride);
+    hipLaunchKernelGGL(oh_k_group_pairs, dim3((npairs + 255) / 256), dim3(256), 0, st, idx, npairs, cnt, ne, list,
+                       lstride, err);
     return hipGetLastError();
 }
 hipError_t oh_launch_moe_combine_rows(float *x, const float *o, const float *w, int k, int H, const float *so,

@@ -66,7 +66,7 @@ hipError_t oh_launch_attn_exact_rows(const oh_op_attn *a, int base, int t0, int 
 hipError_t oh_launch_route_rows(const float *logits, int ne, int k, const float *shl, int32_t *idx, float *w,
                                 float *shg, int T, hipStream_t st);
 hipError_t oh_launch_group_pairs(const int32_t *idx, int npairs, int32_t *cnt, int ne, int32_t *list, int lstride,
-                                 hipStream_t st);
+                                 int32_t *err, hipStream_t st);
 hipError_t oh_launch_moe_combine_rows(float *x, const float *o, const float *w, int k, int H, const float *so,
                                       const float *shgate, int T, hipStream_t st);
 hipError_t oh_launch_rmsnorm_q8k(const float *x, const float *norm_w, float eps, int n,

@@ -383,7 +383,8 @@ OH_DEV void route_wave(const float *logits, int ne, int k, const float *shgate_l
             const float ov = shfl_xor(bv, m); const int oi = shfl_xor(bi, m);
             if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
         }
-        if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
+        // (no candidate left, bi the sentinel: nothing to mark)
+        if (bi != 0x7fffffff && (bi & 63) == lane) taken |= 1u << (bi >> 6);
         if (lane == s) { mine = bv; sel = bi; }
     }
     // NaN/-inf logits can leave no candidate: never hand an out-of-range

@@ -636,11 +636,16 @@ oh_k_route_rows(const float *logits, int ne, int k, const float *shgate_logit, i
 // expert lists: pair p = t*k + s goes to list[e*lstride + j] of expert e = idx[p]
 // (the order inside a list does not matter: every pair is computed on its own)
 extern "C" __global__ void __launch_bounds__(256)
-oh_k_group_pairs(const int32_t *idx, int npairs, int32_t *cnt, int32_t *list, int lstride) {
+oh_k_group_pairs(const int32_t *idx, int npairs, int32_t *cnt, int ne, int32_t *list, int lstride, int32_t *err) {
     const int p = (int)(blockIdx.x * 256 + tid_x());
     if (p >= npairs) return;
     const int e = ldg(idx + p);
+    // an expert index outside [0, ne), or more pairs for one expert than the
+    // list holds (a token routed to one expert twice: the fallback pick of a
+    // router whose logits are all NaN or -inf), is reported, never written
+    if (e < 0 || e >= ne) { atomicOr(err, OH_ERR_EXPERT_LIST); return; }
     const int j = atomicAdd(cnt + e, 1);
+    if (j >= lstride) { atomicOr(err, OH_ERR_EXPERT_LIST); return; }
     stg(list + (size_t)e * lstride + j, (int32_t)p);
 }
 

@@ -268,6 +268,9 @@ typedef struct {
 #define OH_STEP_NCTR 32
 #define OH_STEP_CSTRIDE 16
 enum { OH_IO_POS = 0, OH_IO_BEST = 1, OH_IO_EPOCH_BODY = 2, OH_IO_EPOCH_HEAD = 3, OH_IO_ERR = 4 };
+// bits of io[OH_IO_ERR]: a bounded wait between workgroups gave up (the
+// persistent kernels); an expert pair list would have overflowed
+enum { OH_ERR_WAIT = 1, OH_ERR_EXPERT_LIST = 2 };
 
 // Batched matvec (prefill): Y[col] = W . X[col] for many activation columns,
 // the same integer dot per (row, column) as the matvec. Columns are dense

@@ -153,6 +153,7 @@ def oracle():
         "orc_session_conv": (fp, [vp, C.c_int]),
         "orc_session_kv": (C.POINTER(OrcKV), [vp, C.c_int]),
         "orc_session_seed_context": (C.c_int, [vp, C.c_int, C.c_uint64]),
+        "orc_session_adopt": (C.c_int, [vp, C.c_int, fp]),
         "orc_last_error": (C.c_char_p, []),
         "orc_gguf_load": (C.c_int, [C.c_char_p, C.POINTER(vp)]),
         "orc_gguf_free": (None, [vp]),
@@ -378,3 +379,37 @@ def write_model_gguf(model, cfg: dict, path, n_layers: int | None = None) -> Non
     L.orc_writer_free(w)
     if st:
         raise RuntimeError(L.orc_last_error().decode())
+
+
+def adopt_state(orc, dst, arch, pos, logits, delta_of, conv_of, kv_of):
+    """Copy a session's state into the empty oracle session `dst` (delta state
+    and conv window of every linear layer, the Q8 KV codes and scales of every
+    full-attention layer, in the reference's host layouts) and declare it at
+    position `pos` with last logits `logits` (orc_session_adopt), so that the
+    oracle's token steps continue from that state. delta_of(l), conv_of(l)
+    and kv_of(l) -> (Kq, Ks, Vq, Vs) read the source session."""
+    nv, dv, dk = arch["nv"], arch["dv"], arch["dk"]
+    cc = 2 * arch["nk"] * dk + nv * dv
+    kvn = pos * arch["nkv"] * arch["hd"]
+    for l in range(arch["n_layers"]):
+        kvp = orc.orc_session_kv(dst, l)
+        if kvp:
+            kv = kvp.contents
+            assert kv.quantized == 1 and kv.capacity > pos
+            kq, ks, vq, vs = kv_of(l)
+            np.ctypeslib.as_array(kv.Kq, (kvn,))[:] = np.asarray(kq, np.int8).reshape(-1)[:kvn]
+            np.ctypeslib.as_array(kv.Vq, (kvn,))[:] = np.asarray(vq, np.int8).reshape(-1)[:kvn]
+            ns = pos * arch["nkv"]
+            np.ctypeslib.as_array(kv.Ks, (ns,))[:] = np.asarray(ks, np.float32).reshape(-1)[:ns]
+            np.ctypeslib.as_array(kv.Vs, (ns,))[:] = np.asarray(vs, np.float32).reshape(-1)[:ns]
+        else:
+            np.ctypeslib.as_array(orc.orc_session_delta(dst, l), (nv * dv * dk,))[:] = delta_of(l)
+            np.ctypeslib.as_array(orc.orc_session_conv(dst, l), ((arch["conv_k"] - 1) * cc,))[:] = conv_of(l)
+    lg = np.ascontiguousarray(logits, np.float32)
+    assert orc.orc_session_adopt(dst, int(pos), f32p(lg)) == 0
+
+
+def orc_arch_dict(orc, model) -> dict:
+    a = orc.orc_model_arch(model).contents
+    return {k: getattr(a, k) for k in ("hidden", "n_layers", "vocab", "nh", "nkv", "hd", "nk", "nv", "dk", "dv",
+                                       "conv_k", "ne", "top_k")}

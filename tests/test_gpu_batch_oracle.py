@@ -14,7 +14,10 @@ that need fewer blocks:
   printed), and the same greedy token wherever the oracle's best two logits
   are further apart than 1e-2 of the best one's magnitude.
 Both batch plans: the slotted fused launches and the column-streaming batched
-kernels."""
+kernels. That mix of capacities and paths is refused by the engine (see the
+skip reason); the runnable form below keeps one capacity and the exact walk:
+three sessions of capacity 330 at 5, 40 and 300 prompt tokens step together,
+their logits bit-identical to the oracle's after every step."""
 import ctypes as C
 import os
 
@@ -106,6 +109,58 @@ def test_batch_step_matches_oracle_per_session(hip_ctx, orc, tmp_path, monkeypat
         toks = nxt
     assert worst <= 1e-2
     print(f"[{cfg} fused={fused}] worst rel L2 past the exact walk {worst:.3e}; near-tie argmax flips {flips}")
+    for s in sess:
+        s.free()
+    for o in osess:
+        orc.orc_session_free(o)
+    orc.orc_model_free(om)
+    m.free()
+
+
+@pytest.mark.timeout(300)
+@pytest.mark.parametrize("cfg", ["c1", "moe"])
+@pytest.mark.parametrize("fused", ["1", "0"], ids=["slotted-launches", "batched-kernels"])
+def test_batch_step_exact_walk_contexts_match_oracle(hip_ctx, orc, tmp_path, monkeypatch, cfg, fused):
+    """Sessions of one capacity at different contexts inside the exact walk:
+    the batch's attention grid and LDS (the maximum over the sessions) cover
+    sessions that need fewer positions; every logit bit-identical to the
+    oracle's token step of the same session, every greedy token the same."""
+    monkeypatch.setenv("ORNITH_PREFILL_SERIAL", "0")
+    monkeypatch.setenv("ORNITH_HIP_BATCH_FUSED", fused)
+    c = CFGS[cfg]
+    cap, lens = 330, PROMPTS[:EXACT]
+    m = hip_ctx.synth(**c)
+    V = m.arch["vocab"]
+    prompts = [clibs.ids(40 + b, "batch.oracle", lens[b], V) for b in range(len(lens))]
+    path = os.path.join(str(tmp_path), f"batch_exact_{cfg}.gguf")
+    clibs.write_model_gguf(m, c, path)
+    om = C.c_void_p()
+    assert orc.orc_model_load(path.encode(), C.byref(om)) == 0
+    orc.orc_model_set_threads(om, THREADS)
+    sess, osess = [], []
+    for p in prompts:
+        s = m.session(cap)
+        s.eval(p)
+        sess.append(s)
+        o = orc.orc_session_new(om, cap, 1)
+        assert orc.orc_session_eval(o, i32p(p), p.size, 0) == 0
+        osess.append(o)
+
+    def oracle_logits(b):
+        return np.ctypeslib.as_array(orc.orc_session_logits(osess[b]), (V,)).copy()
+
+    for b in range(len(sess)):
+        assert np.array_equal(u32(sess[b].logits()), u32(oracle_logits(b))), ("prompt", b)
+    toks = np.array([int(np.argmax(s.logits())) for s in sess], np.int32)
+    for step in range(STEPS):
+        nxt = m.batch_step(sess, toks)
+        for b in range(len(sess)):
+            assert orc.orc_session_step(osess[b], int(toks[b])) == 0
+            got, ref = sess[b].logits(), oracle_logits(b)
+            assert sess[b].pos == lens[b] + step + 1
+            assert np.array_equal(u32(got), u32(ref)), (cfg, fused, step, b)
+            assert int(nxt[b]) == int(np.argmax(ref))
+        toks = nxt
     for s in sess:
         s.free()
     for o in osess:

@@ -157,6 +157,64 @@ def test_c3_full_model_greedy_matches_oracle(hip_ctx, orc, tmp_path, monkeypatch
     assert np.array_equal(u32(lf), u32(rf))
 
 
+@pytest.mark.timeout(1100)
+def test_c3_full_model_4096_context_greedy_matches_oracle(hip_ctx, orc, tmp_path, monkeypatch):
+    """C3 at the benchmark's own context: the bench's 4096-token prompt
+    (default_rng(0) ids) through the GPU prefill in the reference's default
+    chunked mode, then the session's state (30 delta states and conv
+    windows, 10 Q8 KV caches of 4096 positions, the prompt logits) copied into
+    an oracle session (orc_session_adopt; an oracle prefill of 4096 tokens
+    would take minutes), and 64 greedy steps on both (rforward_token,
+    src/ornith_rforward.c:686-706): identical tokens, final logits within 1e-2
+    relative L2 (north_star's bar; every step's attention past 1024 positions
+    is the flash decode on the matrix cores, which re-associates the
+    reference's sums)."""
+    monkeypatch.setenv("ORNITH_PREFILL_SERIAL", "0")
+    T, steps = 4096, 64
+    t0 = time.time()
+    m = hip_ctx.synth(**C3)
+    prompt = np.random.default_rng(0).integers(0, C3["vocab"], T, dtype=np.int64).astype(np.int32)
+    s = m.session(T + steps + 8)
+    s.eval(prompt)
+    lp = s.logits().copy()
+    full = [(l + 1) % C3["full_interval"] == 0 for l in range(C3["n_layers"])]
+    delta = {l: s.delta_state(l) for l in range(C3["n_layers"]) if not full[l]}
+    conv = {l: s.conv_state(l) for l in range(C3["n_layers"]) if not full[l]}
+    kv = {l: s.kv(l) for l in range(C3["n_layers"]) if full[l]}
+    toks = s.generate(steps)
+    lf = s.logits().copy()
+    s.free()
+    path = os.path.join(shm_dir(tmp_path), "c3_ctx4096_parity.gguf")
+    try:
+        clibs.write_model_gguf(m, C3, path)
+        m.free()
+        print(f"[c3 4096] GPU prefill + {steps} steps + GGUF written in {time.time() - t0:.1f} s", flush=True)
+        om = C.c_void_p()
+        assert orc.orc_model_load(path.encode(), C.byref(om)) == 0, orc.orc_last_error()
+        orc.orc_model_set_threads(om, THREADS)
+        o = orc.orc_session_new(om, T + steps + 8, 1)
+        arch = clibs.orc_arch_dict(orc, om)
+        assert all(orc.orc_session_kv(o, l) is not None and bool(orc.orc_session_kv(o, l)) == full[l]
+                   for l in range(C3["n_layers"]))
+        clibs.adopt_state(orc, o, arch, T, lp, delta.__getitem__, conv.__getitem__, kv.__getitem__)
+        rtoks = np.zeros(steps, np.int32)
+        nout = C.c_int(0)
+        assert orc.orc_session_generate(o, steps, i32p(rtoks), C.byref(nout), None) == 0
+        assert nout.value == steps
+        rf = np.ctypeslib.as_array(orc.orc_session_logits(o), (C3["vocab"],)).copy()
+        orc.orc_session_free(o)
+        orc.orc_model_free(om)
+        print(f"[c3 4096] oracle ({THREADS} threads) {steps} steps done at {time.time() - t0:.1f} s", flush=True)
+    finally:
+        if os.path.exists(path):
+            os.unlink(path)
+    first = int(np.argmax(toks != rtoks)) if not np.array_equal(toks, rtoks) else steps
+    print(f"[c3 4096] final logits rel L2 {rel_l2(lf, rf):.3e}; tokens equal {int((toks == rtoks).sum())}/{steps} "
+          f"(first difference at step {first}); first tokens {toks[:8].tolist()}")
+    assert np.array_equal(toks, rtoks)
+    assert rel_l2(lf, rf) < 1e-2
+
+
 @pytest.mark.timeout(900)
 def test_c3_width_slice_long_prompt_matches_oracle(hip_ctx, orc, tmp_path, monkeypatch):
     """4 layers at C3 width with an 1100-token prompt: the prompt's positions

@@ -107,3 +107,63 @@ def test_generator_deterministic_streams(orc):
     part = np.zeros(10, np.float32)
     L.orc_fill_gauss(L.orc_stream_key(0, b"x"), 0.02, f32p(part), 10, 500)
     assert np.array_equal(part, a[500:510])
+
+
+def test_session_adopt_continues_bit_identically(orc, c1_path):
+    """orc_session_adopt (a test aid: a state copied in through the state
+    accessors, then declared at its position with its last logits) pinned
+    against the session it was copied from: after a 40-token chunked prompt,
+    the copy and the original give bit-identical logits over 12 greedy
+    steps. A copy missing one layer's state, or declared one position off,
+    parts from the original at once (checked below), so the aid cannot hide a
+    dropped layer or an off-by-one position."""
+    st, m = load(orc, c1_path)
+    assert st == 0
+    orc.orc_model_set_threads(m, 8)
+    arch = clibs.orc_arch_dict(orc, m)
+    V = arch["vocab"]
+    prompt = clibs.ids(9, "adopt", 40, V)
+    a = orc.orc_session_new(m, 64, 1)
+    assert orc.orc_session_eval(a, i32p(prompt), prompt.size, 0) == 0
+    nv, dv, dk = arch["nv"], arch["dv"], arch["dk"]
+    cc = 2 * arch["nk"] * dk + nv * dv
+    K = arch["conv_k"]
+
+    def delta_of(l):
+        return np.ctypeslib.as_array(orc.orc_session_delta(a, l), (nv * dv * dk,)).copy()
+
+    def conv_of(l):
+        return np.ctypeslib.as_array(orc.orc_session_conv(a, l), ((K - 1) * cc,)).copy()
+
+    def kv_of(l):
+        kv = orc.orc_session_kv(a, l).contents
+        n = kv.len * kv.n_kv_heads
+        return (np.ctypeslib.as_array(kv.Kq, (n * kv.head_dim,)).copy(), np.ctypeslib.as_array(kv.Ks, (n,)).copy(),
+                np.ctypeslib.as_array(kv.Vq, (n * kv.head_dim,)).copy(), np.ctypeslib.as_array(kv.Vs, (n,)).copy())
+
+    def logits(s):
+        return np.ctypeslib.as_array(orc.orc_session_logits(s), (V,)).copy()
+
+    def copy(skip_layer=None, pos=40):
+        b = orc.orc_session_new(m, 64, 1)
+        zero = lambda l, f, n: np.zeros(n, np.float32) if l == skip_layer else f(l)
+        clibs.adopt_state(orc, b, arch, pos, logits(a),
+                          lambda l: zero(l, delta_of, nv * dv * dk), lambda l: zero(l, conv_of, (K - 1) * cc), kv_of)
+        return b
+
+    b = copy()
+    assert orc.orc_session_pos(b) == 40
+    bad_layer, bad_pos = copy(skip_layer=0), copy(pos=39)
+    tok = int(np.argmax(logits(a)))
+    for step in range(12):
+        for s in (a, b, bad_layer, bad_pos):
+            assert orc.orc_session_step(s, tok) == 0
+        ref = logits(a)
+        assert np.array_equal(logits(b).view(np.uint32), ref.view(np.uint32)), step
+        if step == 0:
+            assert not np.array_equal(logits(bad_layer), ref)
+            assert not np.array_equal(logits(bad_pos), ref)
+        tok = int(np.argmax(ref))
+    for s in (a, b, bad_layer, bad_pos):
+        orc.orc_session_free(s)
+    orc.orc_model_free(m)
