@@ -26,7 +26,7 @@ extern "C" __global__ void __launch_bounds__(256) oh_k_attn_main_batch(const oh_
 extern "C" __global__ void __launch_bounds__(256) oh_k_attn_combine_batch(const oh_op_attn *ops, const int32_t *pos) {
     NoWait w;
     const int b = (int)blockIdx.y;
-    combine_body(ops[b], (int)blockIdx.x, pos[b], w);
+    combine_body(ops[b], (int)blockIdx.x, pos[b], w, exact_lim(ops[b].exact_max, ops[b].hd));
 }
 
 // greedy token of each of the rows of v [rows][n]: the largest value, the

@@ -804,7 +804,7 @@ OH_DEV void dop_combine(const oh_datt &d, int vb, const Dctl &c) {
     if (c.pos + 1 <= d.lim) return;
     flags_wait(d.wflags, d.nwait_fl, c);
     NoWait w;
-    combine_body(d.a, vb, c.pos, w);
+    combine_body(d.a, vb, c.pos, w, d.lim);
     flag_set(d.flags + vb, c);
 }
 

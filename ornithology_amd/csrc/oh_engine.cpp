@@ -339,17 +339,19 @@ int mv_add_pair(MvBuild &b, const ornith_hip_tensor *W, const ornith_hip_tensor 
 // per CU, for a standalone launch; the resident waves of the step kernel).
 void mv_plan(MvBuild &b, int waves, int small_waves) {
     int64_t steps = 0;
-    int tk = -2;
+    // kernel variant: one integer-path type, the Q4_K/Q6_K pair, or any mix
+    bool any = false, one = true, q46 = true;
+    int t0 = -1;
     for (int i = 0; i < b.L.n; i++) {
         const oh_mvseg &s = b.L.s[i];
-        if (seg_steps(s)) {
-            steps += (int64_t)s.units * s.nsub * (s.pair ? 2 : 1);
-            tk = (tk == -2 || tk == s.type) && !s.iq2tree ? s.type : -1;
-        } else {
-            tk = -1;
-        }
+        if (seg_steps(s)) steps += (int64_t)s.units * s.nsub * (s.pair ? 2 : 1);
+        const bool q8 = seg_q8(s) && !s.iq2tree;
+        if (!any) t0 = s.type;
+        any = true;
+        one = one && q8 && s.type == t0;
+        q46 = q46 && q8 && (s.type == OH_Q4_K || s.type == OH_Q6_K);
     }
-    b.tk = tk < 0 ? -1 : tk;
+    b.tk = any && one ? t0 : any && q46 ? OH_MV_Q4Q6 : -1;
     // launches of a few MB: fewer, longer waves (each block forms the
     // activation once, so fewer blocks put less of that traffic ahead of the
     // weights); large ones keep the full spread for bandwidth
@@ -391,7 +393,14 @@ void mv_plan(MvBuild &b, int waves, int small_waves) {
         if (s.iq2tree) need = 0;                    // x in registers, the tables in static LDS
         if (need > b.lds) b.lds = need;
     }
-    if (b.L.route && ((b.L.ne + 3) & ~3) * 4 > b.lds) b.lds = ((b.L.ne + 3) & ~3) * 4;
+    if (b.L.rtag) {
+        // the fused router's copy of the logits for the sequential selection,
+        // past every segment's activation
+        b.L.rlg = (b.lds + 15) & ~15;
+        b.lds = b.L.rlg + ((b.L.ne + 3) & ~3) * 4;
+    } else if (b.L.route && ((b.L.ne + 3) & ~3) * 4 > b.lds) {
+        b.lds = ((b.L.ne + 3) & ~3) * 4;
+    }
     b.L.total_blocks = blocks;
 }
 

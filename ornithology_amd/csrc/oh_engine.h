@@ -176,6 +176,8 @@ struct ornith_hip_session {
     int *dcnt = nullptr;          // step kernel's MoE down: blocks done per row group
     float *osz = nullptr;         // delta step: silu(gate) per output row
     double *oruns = nullptr;      // delta step: sum of o^2 per 16-row run (per 64 rows: the step kernel)
+    uint64_t *rtag = nullptr;     // MoE layers: router logits as tagged words [n_layers][ne + 1] (fused router)
+    int32_t *mctr = nullptr;      // MoE layers: router completion counters of the fused MoE launch [n_layers][2]
     int exact_max = 1024;         // contexts up to this walk the attention sum in one block
     int flash_mfma = 1;           // decode flash chunks on the matrix cores (ORNITH_HIP_FLASH_MFMA=0: VALU)
     float2 *rope = nullptr;
@@ -394,6 +396,7 @@ int run_step(ornith_hip_session *s);
 int sync_pos(ornith_hip_session *s);
 bool attn_mfma_enabled();
 bool batch_fused();
+bool router_fused();
 bool delta_mfma_enabled();
 int pf_chunk_tokens();
 bool pf_mvb_ok(const ornith_hip_tensor *W);

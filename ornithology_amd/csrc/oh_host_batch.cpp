@@ -344,7 +344,7 @@ extern "C" int ornith_hip_batch_step(ornith_hip_session **ss, int n, const int32
     // it): the only mixes the batch step is run with; others are refused
     for (int b = 1; b < n; b++) {
         const ornith_hip_session *x = ss[b], *y = ss[0];
-        const int lim = oh_exact_limit(y->exact_max);
+        const int lim = oh_exact_limit(y->exact_max, a.hd);
         if (x->kvcap != y->kvcap || x->exact_max != y->exact_max || x->flash_mfma != y->flash_mfma ||
             (x->pos + 1 <= lim) != (y->pos + 1 <= lim)) {
             seterr("batch_step: session %d differs from session 0 in KV capacity (%d / %d), attention settings or "
@@ -356,9 +356,9 @@ extern "C" int ornith_hip_batch_step(ornith_hip_session **ss, int n, const int32
     // contexts past the exact attention walk (the flash path) are switched
     // off: batch steps on that path have faulted the GPU (three runs, both
     // plans), cause not found
-    if (ss[0]->pos + 1 > oh_exact_limit(ss[0]->exact_max)) {
+    if (ss[0]->pos + 1 > oh_exact_limit(ss[0]->exact_max, a.hd)) {
         seterr("batch_step: contexts past the exact attention walk (position %d, limit %d) are switched off "
-               "(an unexplained GPU fault in batch steps on the flash path)", ss[0]->pos, oh_exact_limit(ss[0]->exact_max));
+               "(an unexplained GPU fault in batch steps on the flash path)", ss[0]->pos, oh_exact_limit(ss[0]->exact_max, a.hd));
         return ORNITH_HIP_ERR_UNSUPPORTED;
     }
     if (!pf_supported(m) || !oh_qdot_can(m->lm_head->type, m->lm_head->in) || m->lm_head->in > 8192) {

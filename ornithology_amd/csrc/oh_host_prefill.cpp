@@ -18,6 +18,13 @@ bool batch_fused() {
     const char *e = getenv("ORNITH_HIP_BATCH_FUSED");
     return !(e && e[0] == '0');
 }
+// the token step's MoE router inside the experts launch (its logits handed
+// over as tagged words) instead of a launch of its own; on unless
+// ORNITH_HIP_ROUTER_FUSE=0 (same bits either way)
+bool router_fused() {
+    const char *e = getenv("ORNITH_HIP_ROUTER_FUSE");
+    return !(e && e[0] == '0');
+}
 
 // the prompt's chunked delta scan on the matrix cores in its WY form (a
 // tolerance path: the chunk sums re-associated; ORNITH_HIP_DELTA_MFMA=1)

@@ -127,6 +127,10 @@ extern "C" int ornith_hip_session_new(ornith_hip_model *m, int cap, ornith_hip_s
     A_(salloc(s, &s->dcnt, (size_t)H + 64));
     A_(salloc(s, &s->osz, (size_t)a.nv * a.dv + 64));
     A_(salloc(s, &s->oruns, (size_t)a.nv * a.dv / 16 + 64));
+    if (a.ne > 0) {
+        A_(salloc(s, &s->rtag, (size_t)a.n_layers * (a.ne + 1)));
+        A_(salloc(s, &s->mctr, (size_t)a.n_layers * 2));
+    }
     {
         const char *e = getenv("ORNITH_HIP_EXACT_ATTN_MAX");
         if (e && *e) s->exact_max = atoi(e);
@@ -220,7 +224,7 @@ int build_body(ornith_hip_session *s, Prog &P) {
             const float scale = 1.0f / sqrtf((float)a.hd);
             // contexts up to exact_max: scores + the reference-order walk;
             // longer ones: flash chunks + merge (each pair exits for the other)
-            const bool ex = s->pos + 1 <= (s->exact_max < 2048 ? s->exact_max : 2048);
+            const bool ex = s->pos + 1 <= oh_exact_limit(s->exact_max, a.hd);
             oh_op_attn at;
             memset(&at, 0, sizeof at);
             at.qr = s->qr; at.gate = s->agate; at.Kt = z.Kt; at.Ks = z.Ks; at.Vq = z.Vq; at.Vs = z.Vs;
@@ -274,29 +278,52 @@ int build_body(ornith_hip_session *s, Prog &P) {
         if (a.ne > 0) {
             const int K = a.top_k, I = a.moe_inter, sI = a.shared_inter;
             const int IW = I > sI ? I : sI;   // row stride of the g/u buffers
-            // router (+ shared-expert gate); its first block keeps the
-            // normalised activation for the expert launch
-            Act pst = pn;
-            pst.oqs = s->xq.qs; pst.oqd = s->xq.d; pst.oqb = s->xq.bs; pst.oxf = s->xn;
-            MvBuild b;
-            CHK(mv_add(b, y.router, pst, s->rl, 0));
-            if (y.gate_inp_sh) CHK(mv_add(b, y.gate_inp_sh, pn, s->shl, 0));
-            prog_mv(P, b);
-            const Act ax = act_of(s->xq, s->xn);
             const bool paired = pairable(y.gate_exps, y.up_exps) && (!y.gate_sh || pairable(y.gate_sh, y.up_sh));
+            // router in the experts launch (graph step): its segments come
+            // first (the lowest blocks, dispatched first) and publish the
+            // logits as tagged words; the expert blocks form the normalised
+            // activation themselves, then route and stream their experts
+            const bool fr = !P.step && paired && s->rtag && router_fused() && (a.ne == 256 || a.ne == 512) &&
+                            K <= 64 && H <= 4096 && oh_qdot_can(y.router->type, H) &&
+                            (!y.gate_inp_sh || oh_qdot_can(y.gate_inp_sh->type, H)) &&
+                            oh_qdot_can(y.gate_exps->type, H) && (!y.gate_sh || oh_qdot_can(y.gate_sh->type, H));
             MvBuild b2;
-            // experts gate/up: every block routes first (top-k + softmax), the
-            // stacked segments then read the routed experts; gate and up rows
-            // are reduced together and emit h = silu(gate) * up
-            if (paired) {
-                CHK(mv_add_pair(b2, y.gate_exps, y.up_exps, ax, s->h, s->eidx, K, IW));
-                if (y.gate_sh) CHK(mv_add_pair(b2, y.gate_sh, y.up_sh, ax, s->h + (size_t)K * IW));
+            if (fr) {
+                uint64_t *rt = s->rtag + (size_t)l * (a.ne + 1);
+                CHK(mv_add(b2, y.router, pn, (float *)rt, 2));
+                b2.L.s[b2.L.n - 1].tagp = s->io + OH_IO_SERIAL;
+                if (y.gate_inp_sh) {
+                    CHK(mv_add(b2, y.gate_inp_sh, pn, (float *)(rt + a.ne), 2));
+                    b2.L.s[b2.L.n - 1].tagp = s->io + OH_IO_SERIAL;
+                }
+                CHK(mv_add_pair(b2, y.gate_exps, y.up_exps, pn, s->h, s->eidx, K, IW));
+                if (y.gate_sh) CHK(mv_add_pair(b2, y.gate_sh, y.up_sh, pn, s->h + (size_t)K * IW));
+                b2.L.rtag = rt;
+                b2.L.rio = s->io;
+                b2.L.rsh = y.gate_inp_sh ? 1 : 0;
             } else {
-                CHK(mv_add(b2, y.gate_exps, ax, s->g, 0, s->eidx, K, IW, 0));
-                CHK(mv_add(b2, y.up_exps, ax, s->u, 0, s->eidx, K, IW, 0));
-                if (y.gate_sh) {
-                    CHK(mv_add(b2, y.gate_sh, ax, s->g + (size_t)K * IW, 0));
-                    CHK(mv_add(b2, y.up_sh, ax, s->u + (size_t)K * IW, 0));
+                // router (+ shared-expert gate); its first block keeps the
+                // normalised activation for the expert launch
+                Act pst = pn;
+                pst.oqs = s->xq.qs; pst.oqd = s->xq.d; pst.oqb = s->xq.bs; pst.oxf = s->xn;
+                MvBuild b;
+                CHK(mv_add(b, y.router, pst, s->rl, 0));
+                if (y.gate_inp_sh) CHK(mv_add(b, y.gate_inp_sh, pn, s->shl, 0));
+                prog_mv(P, b);
+                const Act ax = act_of(s->xq, s->xn);
+                // experts gate/up: every block routes first (top-k + softmax), the
+                // stacked segments then read the routed experts; gate and up rows
+                // are reduced together and emit h = silu(gate) * up
+                if (paired) {
+                    CHK(mv_add_pair(b2, y.gate_exps, y.up_exps, ax, s->h, s->eidx, K, IW));
+                    if (y.gate_sh) CHK(mv_add_pair(b2, y.gate_sh, y.up_sh, ax, s->h + (size_t)K * IW));
+                } else {
+                    CHK(mv_add(b2, y.gate_exps, ax, s->g, 0, s->eidx, K, IW, 0));
+                    CHK(mv_add(b2, y.up_exps, ax, s->u, 0, s->eidx, K, IW, 0));
+                    if (y.gate_sh) {
+                        CHK(mv_add(b2, y.gate_sh, ax, s->g + (size_t)K * IW, 0));
+                        CHK(mv_add(b2, y.up_sh, ax, s->u + (size_t)K * IW, 0));
+                    }
                 }
             }
             b2.L.route = 1;
@@ -308,7 +335,6 @@ int build_body(ornith_hip_session *s, Prog &P) {
             b2.L.rw = s->ew;
             b2.L.shg = s->shg;
             b2.bytes += 4.0 * a.ne + 8.0 * K;
-            prog_mv(P, b2);
             const uint32_t dt = y.down_exps->type;
             const int nbd = I / 256, ns = K + (y.gate_sh ? 1 : 0);
             const int rps = nbd >= 1 ? 64 / nbd : 1;
@@ -316,6 +342,24 @@ int build_body(ornith_hip_session *s, Prog &P) {
             const bool fuse = paired && oh_qdot_can(dt, I) && nbd >= 1 && nbd <= 64 && ns <= 10 && dlds <= 65536 &&
                               (!P.step || I <= 1024) &&
                               (!y.gate_sh || (y.down_sh->type == dt && sI == I));
+            if (fr) {
+                // the router blocks' completion counter and the first gate/up
+                // block (which clears the other parity's counter)
+                b2.L.mctr = s->mctr + (size_t)l * 2;
+                mv_plan(b2, P.waves, 1024);
+                b2.L.pb0 = -1;
+                for (int i = 0; i < b2.L.n; i++) {
+                    const oh_mvseg &g = b2.L.s[i];
+                    if (g.mode == 2) b2.L.nrb += g.bps * g.nsub;
+                    if (g.pair && b2.L.pb0 < 0) b2.L.pb0 = g.block0;
+                }
+                oh_op o = op_new(OH_OP_MV, b2.L.total_blocks, b2.lds);
+                o.tk = b2.tk;
+                o.u.mv = b2.L;
+                prog_add(P, o, mv_kind(b2.tk), b2.bytes);
+            } else {
+                prog_mv(P, b2);
+            }
             if (fuse) {
                 oh_mvdown D;
                 memset(&D, 0, sizeof D);
@@ -626,7 +670,7 @@ bool dec_build(ornith_hip_session *s, DecB &b) {
             }
             // prep (q/k norm, RoPE, KV append) -> attention -> merge
             uint64_t *pflags = b.alloc(a.nh + a.nkv);
-            const int lim = s->exact_max < 2048 ? s->exact_max : 2048;
+            const int lim = oh_exact_limit(s->exact_max, a.hd);
             oh_op_attn at;
             memset(&at, 0, sizeof at);
             at.qr = s->qr; at.gate = s->agate; at.Kt = z.Kt; at.Ks = z.Ks; at.Vq = z.Vq; at.Vs = z.Vs;

@@ -17,13 +17,13 @@ extern "C" {
 hipError_t oh_launch_matvec(const oh_mvlaunch *L, int tk, int lds_bytes, hipStream_t st) {
     if (L->total_blocks <= 0) return hipSuccess;
     void (*k)(oh_mvlaunch) = tk == OH_Q4_K ? oh_k_mv_q4k : tk == OH_Q6_K ? oh_k_mv_q6k
-                           : tk == OH_Q8_0 ? oh_k_mv_q80 : oh_k_mv_mixed;
+                           : tk == OH_Q8_0 ? oh_k_mv_q80 : tk == OH_MV_Q4Q6 ? oh_k_mv_q4k6k : oh_k_mv_mixed;
     if (lds_bytes > 65536) {
         // wide fallback rows (IQ2_XXS term tiles, f32 activations past 8K):
         // the kernel's dynamic LDS limit raised to what this launch needs
         // (the limit plus the kernel's static LDS stays within the CU's)
-        static int raised[4];
-        const int ki = tk == OH_Q4_K ? 0 : tk == OH_Q6_K ? 1 : tk == OH_Q8_0 ? 2 : 3;
+        static int raised[5];
+        const int ki = tk == OH_Q4_K ? 0 : tk == OH_Q6_K ? 1 : tk == OH_Q8_0 ? 2 : tk == OH_MV_Q4Q6 ? 4 : 3;
         if (raised[ki] < lds_bytes) {
             const hipError_t e = hipFuncSetAttribute((const void *)k, hipFuncAttributeMaxDynamicSharedMemorySize, lds_bytes);
             if (e != hipSuccess) return e;
@@ -224,12 +224,18 @@ hipError_t oh_launch_prep_rows(const oh_op_prep *a, int base, int T, hipStream_t
     hipLaunchKernelGGL(oh_k_prep_rows, dim3(a->nh + a->nkv, T), dim3(256), 0, st, *a, base);
     return hipGetLastError();
 }
+// the prompt's exact rows: the scores of a block's 256/hd heads in LDS, up to
+// kExactMax positions
+static int pf_exact_lds_bytes(int hd, int exact_max) {
+    const int lim = exact_max < kExactMax ? (exact_max > 0 ? exact_max : 0) : kExactMax;
+    return (256 / hd) * lim * 4;
+}
 hipError_t oh_launch_attn_exact_rows(const oh_op_attn *a, int base, int t0, int n, hipStream_t st) {
     const int lim = a->exact_max < kExactMax ? a->exact_max : kExactMax;
     if (n <= 0) return hipSuccess;
     if (base + t0 + n > lim) return hipErrorInvalidValue;     // every row must be inside the exact walk
     hipLaunchKernelGGL(oh_k_attn_exact_rows, dim3(a->nh / (256 / a->hd), n), dim3(256),
-                       (size_t)oh_exact_lds_bytes(a->hd, a->exact_max), st, *a, base, t0);
+                       (size_t)pf_exact_lds_bytes(a->hd, a->exact_max), st, *a, base, t0);
     return hipGetLastError();
 }
 hipError_t oh_launch_attn_rows(const oh_op_attn *a, int base, int t0, int n, size_t po_stride, size_t pml_stride,
@@ -237,7 +243,7 @@ hipError_t oh_launch_attn_rows(const oh_op_attn *a, int base, int t0, int n, siz
     const int lim = a->exact_max < kExactMax ? a->exact_max : kExactMax;
     if (base + t0 + 1 <= lim)       // some tokens walk exactly
         hipLaunchKernelGGL(oh_k_attn_exact_rows, dim3(a->nh / (256 / a->hd), n), dim3(256),
-                           (size_t)oh_exact_lds_bytes(a->hd, a->exact_max), st, *a, base, t0);
+                           (size_t)pf_exact_lds_bytes(a->hd, a->exact_max), st, *a, base, t0);
     if (base + t0 + n > lim) {      // some tokens take the flash chunks
         const int nch = (base + t0 + n + kFlashCh - 1) / kFlashCh;
         const int nvb = a->nkv * (a->nh / a->nkv / a->hb) * nch;
@@ -381,13 +387,11 @@ int oh_flash_parts(int T, int cap, int hb) {
 }
 
 // contexts up to this many positions take the exact attention walk
-int oh_exact_limit(int exact_max) { return exact_max < kExactMax ? exact_max : kExactMax; }
+int oh_exact_limit(int exact_max, int hd) { return exact_lim(exact_max, hd); }
 
-// exact attention walk: the scores of a block's 256/hd heads in LDS
-int oh_exact_lds_bytes(int hd, int exact_max) {
-    const int lim = exact_max < kExactMax ? (exact_max > 0 ? exact_max : 0) : kExactMax;
-    return (256 / hd) * lim * 4;
-}
+// the decode step's exact attention walk: the scores of a block's 256/hd
+// heads in LDS
+int oh_exact_lds_bytes(int hd, int exact_max) { return (256 / hd) * exact_lim(exact_max, hd) * 4; }
 
 // delta step LDS of the working wave (step kernel: dynamic LDS)
 int oh_delta_lds_bytes(int dk) { return (2 * dk + 64 * (dk + 4)) * 4; }

@@ -91,7 +91,7 @@ int oh_flash_lds_bytes(int nh, int nkv, int hd);
 int oh_flash_chunk(void);
 int oh_delta_lds_bytes(int dk);
 int oh_exact_lds_bytes(int hd, int exact_max);
-int oh_exact_limit(int exact_max);
+int oh_exact_limit(int exact_max, int hd);
 int oh_delta16_lds_bytes(int dk);
 // prompt attention on the matrix cores for the nt tokens tf0.. of a prefill
 // chunk (positions base + t, contexts past the exact walk); supported shapes

@@ -523,8 +523,20 @@ OH_DEV void prep_body(const oh_op_prep &a, int vb, int pos, W &w) {
 // any workgroup of this launch read its cache line. Plain loads therefore see
 // every entry.
 
-// Longest context of the exact walk (its scores stay in LDS).
+// Longest context of the prompt's exact rows (their scores stay in LDS).
 constexpr int kExactMax = 2048;
+// Longest context of the decode step's exact walk for head dim hd: the
+// scores of the block's 256/hd heads stay in LDS, at most 48 KB of it
+// (8192 positions at hd 256, 6144 at 128, 3072 at 64).
+OH_HD inline int exact_cap(int hd) {
+    const int c = 12288 * hd / 256;
+    return c < 8192 ? c : 8192;
+}
+// the decode step's exact-walk limit for a session's exact_max
+OH_HD inline int exact_lim(int exact_max, int hd) {
+    const int c = exact_cap(hd);
+    return exact_max < c ? (exact_max > 0 ? exact_max : 0) : c;
+}
 
 // Exact GQA output of the block's 256/hd query heads (virtual block g):
 // scores s_t = (sum_i q_i*code_i) * Ks_t * scale, sequential over i
@@ -1106,7 +1118,7 @@ OH_DEV void flashm_body(const oh_op_attn &a, int vb, int pos, int lim, W &w) {
 // flash chunks (virtual blocks as flash_body).
 template <class W>
 OH_DEV void attn_main_body(const oh_op_attn &a, int vb, int pos, W &w) {
-    const int lim = a.exact_max < kExactMax ? a.exact_max : kExactMax;
+    const int lim = exact_lim(a.exact_max, a.hd);
     if (pos + 1 <= lim) {
         exact_body(a, vb, pos, lim, w);
     } else if (a.hb == 0) {
@@ -1126,12 +1138,12 @@ OH_DEV void attn_main_body(const oh_op_attn &a, int vb, int pos, W &w) {
 // y < hd/64; 4 waves; wave w takes chunks w, w+4, ...; a lane per dimension):
 // running max rescaling, then
 // out = (sum_c o_c e^(m_c-M)) / (sum_c l_c e^(m_c-M)) * sigmoid(gate).
+// lim: contexts up to it took the exact walk (nothing to merge).
 template <class W>
-OH_DEV void combine_body(const oh_op_attn &a, int vb, int pos, W &w) {
+OH_DEV void combine_body(const oh_op_attn &a, int vb, int pos, W &w, int lim) {
     __shared__ float sm[4][3][64];
     const int nh = a.nh, nkv = a.nkv, hd = a.hd, cap = a.cap;
     const int T = pos + 1;
-    const int lim = a.exact_max < kExactMax ? a.exact_max : kExactMax;
     if (T <= lim) return;
     if (!w.wait()) return;
     const int h = vb % nh, G = nh / nkv, g = h / G, hl = h % G;
@@ -1281,7 +1293,7 @@ extern "C" __global__ void __launch_bounds__(256) oh_k_attn_main(oh_op_attn a, c
 
 extern "C" __global__ void __launch_bounds__(256) oh_k_attn_combine(oh_op_attn a, const int32_t *io) {
     NoWait w;
-    combine_body(a, (int)blockIdx.x, io[OH_IO_POS], w);
+    combine_body(a, (int)blockIdx.x, io[OH_IO_POS], w, exact_lim(a.exact_max, a.hd));
 }
 
 extern "C" __global__ void __launch_bounds__(256) oh_k_moe_combine(oh_op_combine a) {
@@ -1310,6 +1322,10 @@ oh_k_moe_route(const float *logits, int ne, int k, const float *shgate_logit,
 }
 
 // advance the stream position after a token's layers (rforward_token s->pos++)
-extern "C" __global__ void oh_k_advance(int32_t *io_pos) { *io_pos = *io_pos + 1; }
+// and the session's step serial
+extern "C" __global__ void oh_k_advance(int32_t *io) {
+    io[OH_IO_POS] = io[OH_IO_POS] + 1;
+    io[OH_IO_SERIAL] = io[OH_IO_SERIAL] + 1;
+}
 
 #endif // OH_BODIES_ONLY

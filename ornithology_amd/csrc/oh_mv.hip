@@ -910,8 +910,21 @@ OH_DEV void pro_compute(const PIn &p, const oh_mvseg &s, int slot, int blk, uint
 // expert for stacked tensors. Inside the step kernel (W::kGrid) the first
 // step's weights are requested before the grid wait: they do not depend on
 // the previous phase.
-template <int T, class W>
-OH_DEV void mv_seg(const oh_mvseg &s, int slot, int blk, int expert, uint8_t *smem, double *red, W &w) {
+// LT::kLate: the slot's expert is known only after the activation is formed
+// (late() routes the block, fused router): prologue first, then late(), then
+// the first weights. Otherwise `expert` is given.
+struct NoLate {
+    static constexpr bool kLate = false;
+    OH_DEV int operator()() const { return 0; }
+};
+template <class F> struct LateExpert {
+    static constexpr bool kLate = true;
+    F f;
+    OH_DEV int operator()() const { return f(); }
+};
+template <int T, class W, class LT = NoLate>
+OH_DEV void mv_seg(const oh_mvseg &s, int slot, int blk, int expert, uint8_t *smem, double *red, W &w,
+                   LT late = LT()) {
     const int lane = lane_id(), wave = __builtin_amdgcn_readfirstlane(tid_x() >> 6);
     const int nb = s.nb, rps = 64 / nb;
     const int rl = lane / nb, sb = lane - rl * nb;
@@ -920,9 +933,10 @@ OH_DEV void mv_seg(const oh_mvseg &s, int slot, int blk, int expert, uint8_t *sm
     // paired segments: step 2u reduces W, step 2u+1 the pair W2, same rows
     const int sps = s.pair ? 2 : 1;
     const int S = u1 > u0 ? (u1 - u0) * sps : 0;
-    const int64_t row_base = (int64_t)expert * s.rows;
+    int64_t row_base = (int64_t)expert * s.rows;            // set by late() in the late form
     float *y = s.y + (size_t)slot * s.ystride;
     const WP wp = {s.A, s.B, s.C}, wp2 = {s.A2, s.B2, s.C2};
+    const uint32_t tag = s.mode == 2 ? (uint32_t)ldc(s.tagp) + 1u : 0u;
     const int8_t *aq = (const int8_t *)smem + sb * kAS;
     const int16_t *abs = (const int16_t *)(smem + mv_lds_bs_off(nb)) + sb * 16;
     const float *adp = (const float *)(smem + mv_lds_d_off(nb)) + sb;
@@ -951,7 +965,8 @@ OH_DEV void mv_seg(const oh_mvseg &s, int slot, int blk, int expert, uint8_t *sm
             if ((st & 1) == 0) gsum = acc;
             else if (live && sb == 0) emit<W::kGrid>(y, 0, row, ref_silu(gsum) * acc);
         } else if (live && sb == 0) {
-            if (s.mode == 1 && st == 0) put<W::kGrid>(y + row, ypre + acc);
+            if (s.mode == 2) stc((uint64_t *)y + row, (uint64_t)tag << 32 | f2u(acc));
+            else if (s.mode == 1 && st == 0) put<W::kGrid>(y + row, ypre + acc);
             else emit<W::kGrid>(y, s.mode, row, acc);
         }
     };
@@ -959,7 +974,21 @@ OH_DEV void mv_seg(const oh_mvseg &s, int slot, int blk, int expert, uint8_t *sm
         const int row = u0 * rps + rl;
         if (s.mode == 1 && !s.pair && S > 0 && rl < rps && row < s.rows && sb == 0) ypre = ldc(y + row);
     };
-    if (s.in <= 4096) {
+    if (LT::kLate) {
+        // the activation while the routing is still being published, then
+        // the routed expert's first weights
+        if (!w.wait()) return;
+        y_prefetch();
+        if (s.in <= 4096) {
+            PIn pin;
+            pro_load(pin, s, slot);
+            pro_compute(pin, s, slot, blk, smem, red);
+        } else {
+            mv_prologue(s, slot, blk, smem, red, true);
+        }
+        row_base = (int64_t)late() * s.rows;
+        load(ra, 0);
+    } else if (s.in <= 4096) {
         PIn pin;
         if (W::kGrid) {
             load(ra, 0);
@@ -1004,14 +1033,8 @@ OH_DEV void mv_seg(const oh_mvseg &s, int slot, int blk, int expert, uint8_t *sm
 // order, w_s = e_s / sum. Returns false (nothing written) when a logit is NaN
 // or -inf: the sequential selection handles those.
 template <int V>
-OH_DEV bool route_fast(const float *rlog, int k, int *sel, float *rw) {
+OH_DEV bool route_pick(float (&a)[V], int k, int *sel, float *rw) {
     const int lane = lane_id();
-    float a[V];
-#pragma unroll
-    for (int q = 0; q < V / 4; q++) {
-        const float4 t = ldc4((const float4 *)rlog + V / 4 * lane + q);
-        a[4 * q] = t.x; a[4 * q + 1] = t.y; a[4 * q + 2] = t.z; a[4 * q + 3] = t.w;
-    }
     bool fin = true;
 #pragma unroll
     for (int j = 0; j < V; j++) fin = fin && a[j] > -INFINITY;
@@ -1040,6 +1063,61 @@ OH_DEV bool route_fast(const float *rlog, int k, int *sel, float *rw) {
     float sum = 0.0f;
     for (int s = 0; s < k; s++) sum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), s));
     if (lane < k) { sel[lane] = pick; rw[lane] = e / sum; }
+    return true;
+}
+template <int V>
+OH_DEV bool route_fast(const float *rlog, int k, int *sel, float *rw) {
+    const int lane = lane_id();
+    float a[V];
+#pragma unroll
+    for (int q = 0; q < V / 4; q++) {
+        const float4 t = ldc4((const float4 *)rlog + V / 4 * lane + q);
+        a[4 * q] = t.x; a[4 * q + 1] = t.y; a[4 * q + 2] = t.z; a[4 * q + 3] = t.w;
+    }
+    return route_pick<V>(a, k, sel, rw);
+}
+
+// Router logits published in this launch as tagged words (oh_mvlaunch.rtag):
+// wave 0, lane l polling experts V l .. V l + V - 1 (and lane 0 the shared
+// gate's word) with device-scope loads until every word carries `tag`; the
+// values into a[] (and *shl). Returns false when the words did not arrive
+// within the bound (about 10 ms).
+constexpr int kRouteSpin = 1 << 14;
+// Wave-uniform bounded wait until *ctr >= n (lane 0 polls, device-scope
+// loads with a short sleep between them). False when it gave up.
+OH_DEV bool wait_count(const int32_t *ctr, int n) {
+    int ok = 1;
+    if (lane_id() == 0) {
+        for (int it = 0; ldc(ctr) < n; it++) {
+            if (it >= kRouteSpin) { ok = 0; break; }
+            __builtin_amdgcn_s_sleep(2);
+        }
+    }
+    return __builtin_amdgcn_readfirstlane(ok) != 0;
+}
+template <int V>
+OH_DEV bool route_poll(const uint64_t *tw, uint32_t tag, bool has_sh, float (&a)[V], float *shl) {
+    const int lane = lane_id(), ne = 64 * V;
+    uint64_t w[V], wsh = 0;
+#pragma unroll
+    for (int j = 0; j < V; j++) w[j] = ldc(tw + V * lane + j);
+    if (has_sh && lane == 0) wsh = ldc(tw + ne);
+    for (int it = 0;; it++) {
+        bool ok = true;
+#pragma unroll
+        for (int j = 0; j < V; j++) ok = ok && (uint32_t)(w[j] >> 32) == tag;
+        if (has_sh && lane == 0) ok = ok && (uint32_t)(wsh >> 32) == tag;
+        if (__ballot(!ok) == 0) break;
+        if (it >= kRouteSpin) return false;
+        __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+        for (int j = 0; j < V; j++)
+            if ((uint32_t)(w[j] >> 32) != tag) w[j] = ldc(tw + V * lane + j);
+        if (has_sh && lane == 0 && (uint32_t)(wsh >> 32) != tag) wsh = ldc(tw + ne);
+    }
+#pragma unroll
+    for (int j = 0; j < V; j++) a[j] = u2f((uint32_t)w[j]);
+    if (has_sh && lane == 0) *shl = u2f((uint32_t)wsh);
     return true;
 }
 
@@ -1120,6 +1198,57 @@ OH_DEV void route_block(const oh_mvlaunch &L, int tok, bool store, float *lg, in
     if (store) {
         if (tid < k) { stc(L.ridx + (size_t)tok * k + tid, (int32_t)sel[tid]); stc(L.rw + (size_t)tok * k + tid, rw[tid]); }
         if (tid == 0 && has_sh) stc(L.shg + tok, *shg);
+    }
+}
+
+// MoE routing of a block from logits published in this launch (L.rtag, one
+// token): wave 0 polls the tagged words (route_poll) and selects as
+// route_block does, the same picks and weights; lg: LDS for the sequential
+// selection when a logit is NaN or -inf. A wait that gives up sets the
+// session's error word (OH_ERR_WAIT) and routes zeros.
+OH_DEV void route_fused(const oh_mvlaunch &L, bool store, float *lg, int *sel, float *rw, float *shg, int *bad) {
+    const int tid = tid_x(), ne = L.ne, k = L.topk;
+    const bool has_sh = L.rsh != 0;
+    if (tid < 64) {
+        const uint32_t ser = (uint32_t)ldc(L.rio + OH_IO_SERIAL), tag = ser + 1u;
+        float shl = 0.0f;
+        bool got = wait_count(L.mctr + (ser & 1u), L.nrb);
+        int ok = 1;
+        if (ne == 256) {
+            float a[4];
+            got = route_poll<4>(L.rtag, tag, has_sh, a, &shl) && got;
+            if (!got) {
+#pragma unroll
+                for (int j = 0; j < 4; j++) a[j] = 0.0f;
+            }
+            ok = route_pick<4>(a, k, sel, rw);
+            if (!ok)
+#pragma unroll
+                for (int j = 0; j < 4; j++) lg[4 * tid + j] = u2f((uint32_t)ldc(L.rtag + 4 * tid + j));
+        } else {
+            float a[8];
+            got = route_poll<8>(L.rtag, tag, has_sh, a, &shl) && got;
+            if (!got) {
+#pragma unroll
+                for (int j = 0; j < 8; j++) a[j] = 0.0f;
+            }
+            ok = route_pick<8>(a, k, sel, rw);
+            if (!ok)
+#pragma unroll
+                for (int j = 0; j < 8; j++) lg[8 * tid + j] = u2f((uint32_t)ldc(L.rtag + 8 * tid + j));
+        }
+        if (!got && tid == 0) atomicOr(L.rio + OH_IO_ERR, OH_ERR_WAIT);
+        if (tid == 0) { *bad = !ok; if (has_sh) *shg = ref_sigmoid(shl); }
+        // the sequential selection over the copy (route_pick wrote nothing)
+        if (!ok) {
+            wave_lds_sync();
+            route_wave(lg, ne, k, nullptr, sel, rw, nullptr);
+        }
+    }
+    __syncthreads();
+    if (store) {
+        if (tid < k) { stc(L.ridx + tid, (int32_t)sel[tid]); stc(L.rw + tid, rw[tid]); }
+        if (tid == 0 && has_sh) stc(L.shg, *shg);
     }
 }
 
@@ -1234,10 +1363,27 @@ OH_DEV void iq2_tree(const oh_mvseg &s, int slot, int blk, int expert, W &w) {
 }
 
 // Launch body. TK >= 0: every segment is an integer-path segment of type TK;
+// TK == OH_MV_Q4Q6: integer-path segments of types Q4_K and Q6_K only (the GQA
+// q/k/v launch), so no other segment form is compiled into the kernel;
 // TK < 0: any mix, including fallback segments (one lane per row, the f32
 // activation in LDS). With L.route every block first routes the MoE and
 // stacked segments take their experts from that routing. vb: the virtual
 // block (blockIdx.x of a standalone launch).
+// a router block of the fused MoE launch counts itself in this step's parity
+// once every wave's tagged stores have completed; the first gate/up block
+// clears the other parity's counter for the next step
+OH_DEV void fused_count(const oh_mvlaunch &L, int vb, bool router) {
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (tid_x() == 0) {
+        const uint32_t ser = (uint32_t)ldc(L.rio + OH_IO_SERIAL);
+        if (router)
+            __hip_atomic_fetch_add(L.mctr + (ser & 1u), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        else if (vb == L.pb0)
+            stc(L.mctr + ((ser & 1u) ^ 1u), 0);
+    }
+}
+
 template <int TK, class W>
 OH_DEV void mv_body(const oh_mvlaunch &L, int vb, W &w) {
     extern __shared__ __align__(16) uint8_t smem[];
@@ -1249,7 +1395,32 @@ OH_DEV void mv_body(const oh_mvlaunch &L, int vb, W &w) {
     const oh_mvseg &s = L.s[si];
     const int bseg = vb - s.block0;
     const int slot = bseg / s.bps, blk = bseg - slot * s.bps;
-    if (L.route && L.tslots > 0) {
+    if (L.rtag) {
+        // router published in this launch (one token): a stacked segment's
+        // block forms its activation, then routes (the first block of slot 0
+        // stores the routing for the down projection), then streams its
+        // expert's weights; the router, shared-gate and shared-expert
+        // segments need no routing
+        if (s.eidx) {
+            auto route = [&]() -> int {
+                route_fused(L, slot == 0 && blk == 0, (float *)(smem + L.rlg), rsel, rwt, &rshg, &rbad);
+                return rsel[slot];
+            };
+            const LateExpert<decltype(route)> late{route};
+            if constexpr (TK >= 0) {
+                mv_seg<TK < 0 ? OH_Q4_K : TK>(s, slot, blk, 0, smem, red, w, late);
+            } else if constexpr (TK == OH_MV_Q4Q6) {
+                if (s.type == OH_Q6_K) mv_seg<OH_Q6_K>(s, slot, blk, 0, smem, red, w, late);
+                else mv_seg<OH_Q4_K>(s, slot, blk, 0, smem, red, w, late);
+            } else {
+                if (s.type == OH_Q6_K) mv_seg<OH_Q6_K>(s, slot, blk, 0, smem, red, w, late);
+                else if (s.type == OH_Q8_0) mv_seg<OH_Q8_0>(s, slot, blk, 0, smem, red, w, late);
+                else mv_seg<OH_Q4_K>(s, slot, blk, 0, smem, red, w, late);
+            }
+            if (L.mctr && vb == L.pb0) fused_count(L, vb, false);
+            return;
+        }
+    } else if (L.route && L.tslots > 0) {
         // several tokens: a stacked-segment block routes its own token
         if (s.eidx) {
             if (!w.wait()) return;
@@ -1263,8 +1434,13 @@ OH_DEV void mv_body(const oh_mvlaunch &L, int vb, W &w) {
         if (!w.wait()) return;                    // the routing comes from an earlier phase
     }
     const int expert = !s.eidx ? 0 : (L.route ? rsel[L.tslots > 0 ? slot % L.tslots : slot] : ldc(s.eidx + slot));
-    if (TK >= 0) {
+    if constexpr (TK >= 0) {
         mv_seg<TK < 0 ? OH_Q4_K : TK>(s, slot, blk, expert, smem, red, w);
+        if (L.mctr && (s.mode == 2 || vb == L.pb0)) fused_count(L, vb, s.mode == 2);
+    } else if constexpr (TK == OH_MV_Q4Q6) {
+        if (s.type == OH_Q6_K) mv_seg<OH_Q6_K>(s, slot, blk, expert, smem, red, w);
+        else mv_seg<OH_Q4_K>(s, slot, blk, expert, smem, red, w);
+        if (L.mctr && (s.mode == 2 || vb == L.pb0)) fused_count(L, vb, s.mode == 2);
     } else if (s.type == OH_IQ2_XXS && s.iq2tree) {
         switch (s.in / 64) {
         case 64: iq2_tree<64>(s, slot, blk, expert, w); break;
@@ -1658,6 +1834,10 @@ extern "C" __global__ void __launch_bounds__(256) oh_k_mv_q6k(oh_mvlaunch L) {
 extern "C" __global__ void __launch_bounds__(256) oh_k_mv_q80(oh_mvlaunch L) {
     NoWait w;
     mv_body<OH_Q8_0>(L, (int)blockIdx.x, w);
+}
+extern "C" __global__ void __launch_bounds__(256) oh_k_mv_q4k6k(oh_mvlaunch L) {
+    NoWait w;
+    mv_body<OH_MV_Q4Q6>(L, (int)blockIdx.x, w);
 }
 extern "C" __global__ void __launch_bounds__(256) oh_k_mv_mixed(oh_mvlaunch L) {
     NoWait w;

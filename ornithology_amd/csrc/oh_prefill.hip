@@ -610,7 +610,7 @@ oh_k_attn_combine_rows(oh_op_attn a, int base, int t0, size_t po_stride, size_t 
     b.out = a.out + (size_t)t * qd;
     b.part_o = a.part_o + (size_t)blockIdx.y * po_stride;
     b.part_ml = a.part_ml + (size_t)blockIdx.y * pml_stride;
-    combine_body(b, (int)blockIdx.x, base + t, w);
+    combine_body(b, (int)blockIdx.x, base + t, w, a.exact_max < kExactMax ? a.exact_max : kExactMax);
 }
 
 // ---- MoE over T tokens ------------------------------------------------------------

@@ -124,7 +124,7 @@ OH_DEV void run_vb(const oh_op &op, int vb, int pos, W &w) {
         break;
     case OH_OP_ATTN_PREP: prep_body(op.u.prep, vb, pos, w); break;
     case OH_OP_ATTN_MAIN: attn_main_body(op.u.attn, vb, pos, w); break;
-    case OH_OP_ATTN_COMBINE: combine_body(op.u.attn, vb, pos, w); break;
+    case OH_OP_ATTN_COMBINE: combine_body(op.u.attn, vb, pos, w, exact_lim(op.u.attn.exact_max, op.u.attn.hd)); break;
     case OH_OP_MOE_COMBINE: moe_combine_body(op.u.comb, vb, w); break;
     case OH_OP_ARGMAX1: argmax1_body(op.u.am, vb, w); break;
     case OH_OP_ARGMAX2: argmax2_body(op.u.am, pos, w); break;

@@ -109,7 +109,10 @@ typedef struct {
     int pro, gdim, runs16;
     int iq2tree;                   // IQ2_XXS rows summed as a tree (tolerance; else the f32 fallback's order)
     int iq2split;                  // IQ2_XXS fallback rows: adding wave + term-forming waves (else one lane per row)
-    int type, nb, in, rows, mode;  // mode 0: y = dot, 1: y += dot
+    // mode 2: y holds 64-bit tagged words, row o's word = (*tagp + 1) << 32 |
+    // float bits of the dot (a value that readers in the same launch poll for)
+    const int32_t *tagp;
+    int type, nb, in, rows, mode;  // mode 0: y = dot, 1: y += dot, 2: tagged word
     int nsub, ystride, astride;
     int adiv;                      // slot k reads the activation of slot k / adiv (0, 1: its own)
     int units;                     // wave work units per slot
@@ -119,6 +122,9 @@ typedef struct {
 } oh_mvseg;
 
 #define OH_MAX_SEGS 8
+// kernel variant of a launch whose segments are all integer-path Q4_K and Q6_K
+// ones (the others: the segment type, or -1 for any mix)
+#define OH_MV_Q4Q6 (-2)
 // blocks used by the argmax's first stage (the caller sizes its scratch)
 #define OH_ARGMAX_BLOCKS 256
 // IQ2_XXS rows of the f32 fallback per 256-thread block: one lane per row,
@@ -128,26 +134,6 @@ typedef struct {
 #define OH_IQ2_ROWS 64
 #define OH_MV_WAVES 4              // waves per matvec block
 #define OH_MV_R 4                  // steps per prefetch batch of a wave
-// A launch with `route` set first routes the MoE in every block: top-k over
-// the ne router logits rlog (plus the shared-expert gate logit shl, when
-// non-null); stacked segments then use the routed experts, and block 0 stores
-// the routing (ridx, rw, shg) for later launches. tslots > 0 (several tokens):
-// stacked slot k belongs to token k / tslots and is its expert k % tslots;
-// only stacked-segment blocks route (their token's logits at rlog + t*ne,
-// shl + t), and the first block of a token's first slot stores its routing
-// at ridx + t*topk, rw + t*topk, shg + t.
-typedef struct {
-    oh_mvseg s[OH_MAX_SEGS];
-    int n;
-    int total_blocks;
-    int route;
-    const float *rlog, *shl;
-    int ne, topk;
-    int32_t *ridx;
-    float *rw, *shg;
-    int tslots;
-} oh_mvlaunch;
-
 // Fused MoE down projection + combine (one block per row range, every slot).
 typedef struct {
     const uint8_t *A, *B, *C;      // stacked down experts
@@ -171,6 +157,43 @@ typedef struct {
     // and every slot (oh_k_mv_down_narrow, 64 * ceil(slots / 4) threads)
     int narrow;
 } oh_mvdown;
+
+// A launch with `route` set first routes the MoE in every block: top-k over
+// the ne router logits rlog (plus the shared-expert gate logit shl, when
+// non-null); stacked segments then use the routed experts, and block 0 stores
+// the routing (ridx, rw, shg) for later launches. tslots > 0 (several tokens):
+// stacked slot k belongs to token k / tslots and is its expert k % tslots;
+// only stacked-segment blocks route (their token's logits at rlog + t*ne,
+// shl + t), and the first block of a token's first slot stores its routing
+// at ridx + t*topk, rw + t*topk, shg + t.
+// rtag (one token): the router logits come from this launch's own router
+// segments (mode 2, before the stacked ones): ne tagged words, then the
+// shared-expert gate logit's word when rsh is set. A stacked segment's block
+// forms its activation first, then polls the words until they carry this
+// step's tag (rio[OH_IO_SERIAL] + 1), routes and only then requests its
+// expert's weights; rlg is the LDS byte offset of the logits' copy for the
+// sequential selection (NaN / -inf logits), past the activation.
+typedef struct {
+    oh_mvseg s[OH_MAX_SEGS];
+    int n;
+    int total_blocks;
+    int route;
+    const float *rlog, *shl;
+    int ne, topk;
+    int32_t *ridx;
+    float *rw, *shg;
+    int tslots;
+    const uint64_t *rtag;
+    int32_t *rio;
+    int rsh, rlg;
+    // mctr[parity] (parity = the step serial's low bit) counts the router
+    // segments' blocks (nrb of them) whose tagged words are stored; a gate/up
+    // block polls it, then reads the words once. The first gate/up block
+    // (pb0) clears the other parity's counter for the next step.
+    int32_t *mctr;
+    int nrb, pb0;
+} oh_mvlaunch;
+
 
 // ---- operations of the token step -------------------------------------------
 // The decode step is a fixed list of operations. Each one runs either as its
@@ -399,5 +422,7 @@ typedef struct {
         oh_dargmax am;
     } u;
 } oh_dop;
-// io words of the decode launch (after the step kernel's)
-enum { OH_IO_TAG = 8, OH_IO_DONE = 9 };
+// io words of the decode launch (after the step kernel's); OH_IO_SERIAL: the
+// session's step count (advanced with the position by every token step,
+// never reset), the tag source of in-launch hand-offs
+enum { OH_IO_TAG = 8, OH_IO_DONE = 9, OH_IO_SERIAL = 10 };

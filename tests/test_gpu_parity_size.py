@@ -161,15 +161,20 @@ def test_c3_full_model_greedy_matches_oracle(hip_ctx, orc, tmp_path, monkeypatch
 def test_c3_full_model_4096_context_greedy_matches_oracle(hip_ctx, orc, tmp_path, monkeypatch):
     """C3 at the benchmark's own context: the bench's 4096-token prompt
     (default_rng(0) ids) through the GPU prefill in the reference's default
-    chunked mode, then the session's state (30 delta states and conv
-    windows, 10 Q8 KV caches of 4096 positions, the prompt logits) copied into
-    an oracle session (orc_session_adopt; an oracle prefill of 4096 tokens
-    would take minutes), and 64 greedy steps on both (rforward_token,
-    src/ornith_rforward.c:686-706): identical tokens, final logits within 1e-2
-    relative L2 (north_star's bar; every step's attention past 1024 positions
-    is the flash decode on the matrix cores, which re-associates the
-    reference's sums)."""
+    chunked mode; the session's state (30 delta states and conv windows, 10
+    Q8 KV caches of 4096 positions, the prompt logits) is copied into an
+    oracle session (orc_session_adopt; an oracle prefill of 4096 tokens would
+    take minutes). Then 64 greedy steps on the GPU (rforward_token,
+    src/ornith_rforward.c:686-706) with the attention walked in the
+    reference's order at every context (ORNITH_HIP_EXACT_ATTN_MAX=8192), each
+    step's token fed to the oracle's token step as well: every step's logits
+    bit-identical to the oracle's, so the greedy tokens are identical too.
+    (With the default flash decode past 1024 positions, whose re-associated
+    sums move the attention output by ~1e-5 relative, this random model's
+    near-tied top-8 expert picks flip and the logits part by 3.8e-2 at the
+    first step.)"""
     monkeypatch.setenv("ORNITH_PREFILL_SERIAL", "0")
+    monkeypatch.setenv("ORNITH_HIP_EXACT_ATTN_MAX", "8192")
     T, steps = 4096, 64
     t0 = time.time()
     m = hip_ctx.synth(**C3)
@@ -181,10 +186,16 @@ def test_c3_full_model_4096_context_greedy_matches_oracle(hip_ctx, orc, tmp_path
     delta = {l: s.delta_state(l) for l in range(C3["n_layers"]) if not full[l]}
     conv = {l: s.conv_state(l) for l in range(C3["n_layers"]) if not full[l]}
     kv = {l: s.kv(l) for l in range(C3["n_layers"]) if full[l]}
-    toks = s.generate(steps)
-    lf = s.logits().copy()
+    toks, glog = np.zeros(steps, np.int32), []
+    tok = int(np.argmax(lp))
+    for i in range(steps):
+        toks[i] = tok
+        s.step(tok)
+        glog.append(s.logits().copy())
+        tok = int(np.argmax(glog[-1]))
     s.free()
     path = os.path.join(shm_dir(tmp_path), "c3_ctx4096_parity.gguf")
+    rows = []
     try:
         clibs.write_model_gguf(m, C3, path)
         m.free()
@@ -194,25 +205,29 @@ def test_c3_full_model_4096_context_greedy_matches_oracle(hip_ctx, orc, tmp_path
         orc.orc_model_set_threads(om, THREADS)
         o = orc.orc_session_new(om, T + steps + 8, 1)
         arch = clibs.orc_arch_dict(orc, om)
-        assert all(orc.orc_session_kv(o, l) is not None and bool(orc.orc_session_kv(o, l)) == full[l]
-                   for l in range(C3["n_layers"]))
+        assert [bool(orc.orc_session_kv(o, l)) for l in range(C3["n_layers"])] == full
         clibs.adopt_state(orc, o, arch, T, lp, delta.__getitem__, conv.__getitem__, kv.__getitem__)
-        rtoks = np.zeros(steps, np.int32)
-        nout = C.c_int(0)
-        assert orc.orc_session_generate(o, steps, i32p(rtoks), C.byref(nout), None) == 0
-        assert nout.value == steps
-        rf = np.ctypeslib.as_array(orc.orc_session_logits(o), (C3["vocab"],)).copy()
+        for i in range(steps):
+            assert orc.orc_session_step(o, int(toks[i])) == 0
+            ref = np.ctypeslib.as_array(orc.orc_session_logits(o), (C3["vocab"],)).copy()
+            top2 = np.sort(ref)[-2:]
+            rows.append((rel_l2(glog[i], ref), int(np.argmax(glog[i])) == int(np.argmax(ref)),
+                         float((top2[1] - top2[0]) / abs(top2[1])), np.array_equal(u32(glog[i]), u32(ref))))
         orc.orc_session_free(o)
         orc.orc_model_free(om)
         print(f"[c3 4096] oracle ({THREADS} threads) {steps} steps done at {time.time() - t0:.1f} s", flush=True)
     finally:
         if os.path.exists(path):
             os.unlink(path)
-    first = int(np.argmax(toks != rtoks)) if not np.array_equal(toks, rtoks) else steps
-    print(f"[c3 4096] final logits rel L2 {rel_l2(lf, rf):.3e}; tokens equal {int((toks == rtoks).sum())}/{steps} "
-          f"(first difference at step {first}); first tokens {toks[:8].tolist()}")
-    assert np.array_equal(toks, rtoks)
-    assert rel_l2(lf, rf) < 1e-2
+    for i, (r, same, gap, bits) in enumerate(rows):
+        if not bits:
+            print(f"[c3 4096] step {i:2d}: logits rel L2 {r:.3e}, argmax {'same' if same else 'DIFFERS'}, "
+                  f"oracle top-2 gap {gap:.2e}")
+    worst = max(r for r, _, _, _ in rows)
+    print(f"[c3 4096] {sum(1 for *_, bits in rows if bits)}/{steps} steps bit-identical; worst logits rel L2 "
+          f"{worst:.3e}; greedy tokens equal at {sum(1 for _, same, _, _ in rows if same)}/{steps} steps; "
+          f"first tokens {toks[:8].tolist()}")
+    assert all(bits for *_, bits in rows)
 
 
 @pytest.mark.timeout(900)
