@@ -14,6 +14,8 @@
 // ---- bit casts / f16 -------------------------------------------------------
 OH_DEV uint32_t f2u(float f) { return __float_as_uint(f); }
 OH_DEV float u2f(uint32_t u) { return __uint_as_float(u); }
+// the f16 bit pattern of an integer code (exact for |c| <= 2048)
+OH_DEV uint16_t f16_bits_of_code(int c) { return __builtin_bit_cast(uint16_t, (_Float16)(float)c); }
 
 // exact binary16 -> binary32 (hardware conversion is exact for every input)
 OH_DEV float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }

@@ -781,7 +781,9 @@ OH_DEV void dop_prep(const oh_datt &d, int vb, const Dctl &c) {
                         ((uint32_t)(c2 & 0xff) << 16) | ((uint32_t)(c3 & 0xff) << 24));
                 if (t == 0) stc(a.Ks + off, scale);
             } else {
-                if (t < hd) stc(a.Vq + (((size_t)h * (cap / 16) + pos / 16) * hd + t) * 16 + (pos & 15), (int8_t)code);
+                const size_t vo = (((size_t)h * (cap / 16) + pos / 16) * hd + t) * 16 + (pos & 15);
+                if (t < hd) stc(a.Vq + vo, (int8_t)code);
+                if (t < hd && a.Vh) stc(a.Vh + vo, f16_bits_of_code(code));
                 if (t == 0) stc(a.Vs + off, scale);
             }
         }

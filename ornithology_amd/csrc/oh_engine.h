@@ -131,6 +131,7 @@ struct ornith_hip_model {
     std::vector<ornith_hip_tensor *> ts;
     std::unordered_map<std::string, ornith_hip_tensor *> by;
     std::vector<OhLayer> L;
+    bool any_full = false;        // a full-attention (GQA) layer exists
     ornith_hip_tensor *embd = nullptr, *out_norm = nullptr, *lm_head = nullptr;
     uint64_t bytes = 0;
 };
@@ -153,6 +154,7 @@ struct LayerState {
     float *S = nullptr, *conv = nullptr;                 // linear
     uint32_t *Kt = nullptr; float *Ks = nullptr;         // full (Q8 KV)
     int8_t *Vq = nullptr; float *Vs = nullptr;
+    uint16_t *Vh = nullptr;       // the V codes as f16 bits in the same tiles (the exact walk's operand)
 };
 
 struct ornith_hip_session {
@@ -189,6 +191,8 @@ struct ornith_hip_session {
     int *ami = nullptr;
     std::vector<LayerState> ls;
     hipGraphExec_t gbody = nullptr, ghead = nullptr;
+    hipGraphExec_t gbody_x = nullptr;   // the body graph of the exact-attention regime
+    int qpos = 0;                       // position of the next body launch (host side)
     bool graphs_tried = false;
     // per-launch timing of an eager step (profile_step): events around each launch
     bool rec = false;
@@ -394,6 +398,8 @@ int run_body(ornith_hip_session *s);
 int run_head(ornith_hip_session *s);
 int run_step(ornith_hip_session *s);
 int sync_pos(ornith_hip_session *s);
+// the next body launch takes the exact-attention program
+bool body_exact(const ornith_hip_session *s);
 bool attn_mfma_enabled();
 bool batch_fused();
 bool router_fused();

@@ -97,6 +97,7 @@ std::string batch_check(ornith_hip_session *const *ss, int n, const std::vector<
                 BC(sb, pr.Kt, kvd / 4 * cap * 4, "K codes");
                 BC(sb, pr.Ks, cap * a.nkv * F, "K scales");
                 BC(sb, pr.Vq, cap * kvd, "V codes");
+                BC(sb, pr.Vh, cap * kvd * 2, "V codes (f16)");
                 BC(sb, pr.Vs, cap * a.nkv * F, "V scales");
                 if (at.qr != pr.qr || at.gate != pr.gate || at.Kt != pr.Kt || at.Ks != pr.Ks || at.Vq != pr.Vq ||
                     at.Vs != pr.Vs) {
@@ -323,6 +324,14 @@ int batch_enqueue(const BatchPlan &B, hipStream_t st) {
 extern "C" int ornith_hip_batch_step(ornith_hip_session **ss, int n, const int32_t *tokens, int32_t *next) {
     if (n <= 0) return ORNITH_HIP_OK;
     if (!ss || !tokens) { seterr("batch_step: null sessions or tokens"); return ORNITH_HIP_ERR_FORMAT; }
+    // switched off: batch runs have faulted the GPU four times (both plans,
+    // inside and past the exact walk; the last a case that had passed
+    // before), cause not found. The code below stays for the search.
+    seterr("batch_step: batch decode is switched off (unexplained GPU faults in batch runs)");
+    return ORNITH_HIP_ERR_UNSUPPORTED;
+}
+
+static int batch_step_off(ornith_hip_session **ss, int n, const int32_t *tokens, int32_t *next) {
     ornith_hip_session *s0 = ss[0];
     const ornith_hip_model *m = s0->m;
     const ornith_hip_arch &a = m->a;
@@ -405,7 +414,7 @@ extern "C" int ornith_hip_batch_step(ornith_hip_session **ss, int n, const int32
                 oh_op_prep pr = {p.QP + (size_t)b * 2 * aq, p.KB + (size_t)b * kvd, p.VB + (size_t)b * kvd,
                                  (const float *)y.q_norm->A, (const float *)y.k_norm->A, (const float *)sb->rope,
                                  p.QR + (size_t)b * aq, p.AG + (size_t)b * aq, z.Kt, z.Ks, z.Vq, z.Vs,
-                                 a.nh, a.nkv, a.hd, a.rope_dim, sb->kvcap, a.eps};
+                                 a.nh, a.nkv, a.hd, a.rope_dim, sb->kvcap, a.eps, z.Vh};
                 memcpy(dst + (size_t)b * sizeof(oh_op_prep), &pr, sizeof pr);
                 oh_op_attn at;
                 memset(&at, 0, sizeof at);
@@ -546,7 +555,11 @@ extern "C" int ornith_hip_session_time_decode(ornith_hip_session *s, int n_steps
     if (step_enabled()) CHK(step_prepare(s));
     if (dec_enabled() && !step_enabled()) CHK(dec_prepare(s));
     if (!s->step_grid && !s->dec.grid && graphs_enabled()) {
-        if (!s->gbody) CHK(capture(s, enqueue_body, &s->gbody));
+        // the first step's program captured outside the timed region (a run
+        // that crosses the exact-attention limit captures the other one at
+        // the crossing)
+        hipGraphExec_t &g = body_exact(s) ? s->gbody_x : s->gbody;
+        if (!g) CHK(capture(s, enqueue_body, &g));
         if (!s->ghead) CHK(capture(s, enqueue_head, &s->ghead));
     }
     hipEvent_t e0, e1;

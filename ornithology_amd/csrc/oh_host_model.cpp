@@ -194,6 +194,7 @@ int infer_arch(ornith_hip_model *m, const Meta &md) {
     for (int l = 0; l < a.n_layers; l++) {
         OhLayer &y = m->L[l];
         y.full = is_full(a, l);
+        m->any_full = m->any_full || y.full;
         y.attn_norm = mb(m, l, "attn_norm.weight"); y.post_norm = mb(m, l, "post_attention_norm.weight");
         y.q = mb(m, l, "attn_q.weight"); y.k = mb(m, l, "attn_k.weight"); y.v = mb(m, l, "attn_v.weight");
         y.o = mb(m, l, "attn_output.weight");

@@ -204,7 +204,7 @@ int pf_chunk(ornith_hip_session *s, int base, int T, bool chunked, hipStream_t s
             CHK(pf_mm(y.v, p.XQ, p.VB, kvd, T, 0, st));
             oh_op_prep pr = {p.QP, p.KB, p.VB, (const float *)y.q_norm->A, (const float *)y.k_norm->A,
                              (const float *)s->rope, p.QR, p.AG, z.Kt, z.Ks, z.Vq, z.Vs,
-                             a.nh, a.nkv, a.hd, a.rope_dim, s->kvcap, a.eps};
+                             a.nh, a.nkv, a.hd, a.rope_dim, s->kvcap, a.eps, z.Vh};
             HCHK(oh_launch_prep_rows(&pr, base, T, st));
             oh_op_attn at;
             memset(&at, 0, sizeof at);

@@ -64,6 +64,7 @@ extern "C" void ornith_hip_session_free(ornith_hip_session *s) {
     if (!s) return;
     (void)hipSetDevice(s->m->ctx->device);
     if (s->gbody) (void)hipGraphExecDestroy(s->gbody);
+    if (s->gbody_x) (void)hipGraphExecDestroy(s->gbody_x);
     if (s->ghead) (void)hipGraphExecDestroy(s->ghead);
     if (s->bw.graph) (void)hipGraphExecDestroy(s->bw.graph);
     for (void *p : s->allocs) (void)hipFree(p);
@@ -154,6 +155,7 @@ extern "C" int ornith_hip_session_new(ornith_hip_model *m, int cap, ornith_hip_s
             A_(salloc(s, &y.Kt, (size_t)a.nkv * (a.hd / 4) * s->kvcap));
             A_(salloc(s, &y.Ks, (size_t)s->kvcap * a.nkv));
             A_(salloc(s, &y.Vq, (size_t)s->kvcap * a.nkv * a.hd));
+            A_(salloc(s, &y.Vh, (size_t)s->kvcap * a.nkv * a.hd));
             A_(salloc(s, &y.Vs, (size_t)s->kvcap * a.nkv));
         } else {
             A_(salloc(s, &y.S, (size_t)a.nv * a.dk * a.dv));
@@ -217,33 +219,48 @@ int build_body(ornith_hip_session *s, Prog &P) {
                 oh_op o = op_new(OH_OP_ATTN_PREP, a.nh + a.nkv);
                 o.u.prep = {s->qproj, s->kb, s->vb, (const float *)y.q_norm->A, (const float *)y.k_norm->A,
                             (const float *)s->rope, s->qr, s->agate, z.Kt, z.Ks, z.Vq, z.Vs,
-                            a.nh, a.nkv, a.hd, a.rope_dim, s->kvcap, a.eps};
+                            a.nh, a.nkv, a.hd, a.rope_dim, s->kvcap, a.eps, z.Vh};
                 prog_add(P, o, K_ATTN_PREP, 4.0 * (2.0 * aqd + 2.0 * kvd + 2.0 * a.hd) + 8.0 * aqd +
                                                 2.0 * (kvd + 4.0 * a.nkv));
             }
             const float scale = 1.0f / sqrtf((float)a.hd);
             // contexts up to exact_max: scores + the reference-order walk;
             // longer ones: flash chunks + merge (each pair exits for the other)
-            const bool ex = s->pos + 1 <= oh_exact_limit(s->exact_max, a.hd);
+            const bool ex = s->qpos + 1 <= oh_exact_limit(s->exact_max, a.hd);
             oh_op_attn at;
             memset(&at, 0, sizeof at);
-            at.qr = s->qr; at.gate = s->agate; at.Kt = z.Kt; at.Ks = z.Ks; at.Vq = z.Vq; at.Vs = z.Vs;
+            at.qr = s->qr; at.gate = s->agate; at.Kt = z.Kt; at.Ks = z.Ks; at.Vq = z.Vq; at.Vs = z.Vs; at.Vh = z.Vh;
             at.scores = s->scores; at.part_o = s->fpo; at.part_ml = s->fpml; at.out = s->o;
             at.nh = a.nh; at.nkv = a.nkv; at.hd = a.hd; at.cap = s->kvcap; at.exact_max = s->exact_max;
             at.hb = oh_flash_form(a.nh, a.nkv, a.hd, s->flash_mfma); at.scale = scale;
             const double nchd = oh_flash_parts((int)T, s->kvcap, at.hb);
             // exact walk (its scores in LDS) or flash chunks, then the merge
             // of the chunks (which exits after an exact walk)
-            const int nv_ex = a.nh / (256 / a.hd), nv_fl = oh_flash_nvb(a.nh, a.nkv, s->kvcap, at.hb);
-            const int lds_ex = oh_exact_lds_bytes(a.hd, s->exact_max), lds_fl = oh_flash_form_lds(a.nh, a.nkv, a.hd, at.hb);
-            oh_op o3 = op_new(OH_OP_ATTN_MAIN, nv_ex > nv_fl ? nv_ex : nv_fl, lds_ex > lds_fl ? lds_ex : lds_fl);
-            o3.u.attn = at;
-            prog_add(P, o3, K_ATTN_MAIN,
-                     ex ? 2.0 * T * a.nkv * (a.hd + 4.0) + 4.0 * T * a.nh + 12.0 * aqd
-                        : T * a.nkv * (2.0 * a.hd + 8.0) + 4.0 * aqd + 8.0 * nchd * aqd);
-            oh_op o4 = op_new(OH_OP_ATTN_COMBINE, a.nh * (a.hd / 64));
-            o4.u.attn = at;
-            prog_add(P, o4, K_ATTN_COMBINE, ex ? 0.0 : 4.0 * nchd * (aqd + 2.0 * a.nh) + 12.0 * aqd);
+            const int nv_fl = oh_flash_nvb(a.nh, a.nkv, s->kvcap, at.hb);
+            const int lds_fl = oh_flash_form_lds(a.nh, a.nkv, a.hd, at.hb);
+            const double kvb = T * a.nkv * (a.hd + 4.0);          // one of K or V with its scales
+            if (!P.step && ex && a.nh <= OH_EXACT2_GMAX * a.nkv) {
+                // graph step, exact regime (the host picks this program
+                // while the context fits the exact walk): the scores over
+                // 64-position tiles of every KV head, then one block per
+                // query head for the softmax and the output walk
+                const int lim = oh_exact_limit(s->exact_max, a.hd);
+                oh_op o3 = op_new(OH_OP_ATTN_SCORES, a.nkv * ((lim + 63) / 64), ((a.nh / a.nkv) * 4 + 64) * a.hd);
+                o3.u.attn = at;
+                prog_add(P, o3, K_ATTN_MAIN, kvb + 4.0 * T * a.nh + 4.0 * aqd);
+                oh_op o4 = op_new(OH_OP_ATTN_WALK, a.nh, ((lim + 15) / 16 + 2) * 16 * 4);
+                o4.u.attn = at;
+                prog_add(P, o4, K_ATTN_COMBINE, kvb + 4.0 * T * a.nh + 12.0 * aqd);
+            } else {
+                const int nv_ex = a.nh / (256 / a.hd), lds_ex = oh_exact_lds_bytes(a.hd, s->exact_max);
+                oh_op o3 = op_new(OH_OP_ATTN_MAIN, nv_ex > nv_fl ? nv_ex : nv_fl, lds_ex > lds_fl ? lds_ex : lds_fl);
+                o3.u.attn = at;
+                prog_add(P, o3, K_ATTN_MAIN, ex ? 2.0 * kvb + 4.0 * T * a.nh + 12.0 * aqd
+                                                : 2.0 * kvb + 4.0 * aqd + 8.0 * nchd * aqd);
+                oh_op o4 = op_new(OH_OP_ATTN_COMBINE, a.nh * (a.hd / 64));
+                o4.u.attn = at;
+                prog_add(P, o4, K_ATTN_COMBINE, ex ? 0.0 : 4.0 * nchd * (aqd + 2.0 * a.nh) + 12.0 * aqd);
+            }
             MvBuild b2;
             Act af;
             af.pro = OH_PRO_F32;
@@ -686,7 +703,7 @@ bool dec_build(ornith_hip_session *s, DecB &b) {
             o.nvb = a.nh + a.nkv;
             o.u.at.p = {nullptr, nullptr, nullptr, (const float *)y.q_norm->A, (const float *)y.k_norm->A,
                         (const float *)s->rope, s->qr, s->agate, z.Kt, z.Ks, z.Vq, z.Vs,
-                        a.nh, a.nkv, a.hd, a.rope_dim, s->kvcap, a.eps};
+                        a.nh, a.nkv, a.hd, a.rope_dim, s->kvcap, a.eps, z.Vh};
             o.u.at.qkv = qkv;
             o.u.at.flags = pflags;
             b.ops.push_back(o);
@@ -868,18 +885,27 @@ bool graphs_enabled() {
     return !(e && e[0] == '1');
 }
 
+// the graph step's attention regime for the next body launch: contexts up
+// to the exact limit take the exact-walk program (its own graph)
+bool body_exact(const ornith_hip_session *s) {
+    return s->m->any_full && s->qpos + 1 <= oh_exact_limit(s->exact_max, s->m->a.hd);
+}
+
 int run_body(ornith_hip_session *s) {
     hipStream_t st = s->m->ctx->st;
     if (step_enabled()) {
         CHK(step_prepare(s));
-        if (s->step_grid) return step_launch(s, true, nullptr);
+        if (s->step_grid) { s->qpos++; return step_launch(s, true, nullptr); }
     }
     if (graphs_enabled()) {
-        if (!s->gbody) CHK(capture(s, enqueue_body, &s->gbody));
-        HCHK(hipGraphLaunch(s->gbody, st));
-        return ORNITH_HIP_OK;
+        hipGraphExec_t &g = body_exact(s) ? s->gbody_x : s->gbody;
+        if (!g) CHK(capture(s, enqueue_body, &g));
+        HCHK(hipGraphLaunch(g, st));
+    } else {
+        CHK(enqueue_body(s, st));
     }
-    return enqueue_body(s, st);
+    s->qpos++;
+    return ORNITH_HIP_OK;
 }
 int run_head(ornith_hip_session *s) {
     hipStream_t st = s->m->ctx->st;
@@ -907,6 +933,7 @@ int run_step(ornith_hip_session *s) {
 }
 
 int sync_pos(ornith_hip_session *s) {
+    s->qpos = s->pos;
     HCHK(hipMemcpyAsync(s->io, &s->pos, sizeof(int32_t), hipMemcpyHostToDevice, s->m->ctx->st));
     return ORNITH_HIP_OK;
 }

@@ -88,6 +88,16 @@ extern "C" int ornith_hip_session_get_attn(ornith_hip_session *s, int row, float
 // state [nv][dv][dk] and the conv window (K, C, [(K-1)][C] oldest first); the
 // token history; the logits.
 static const char kSessMagic[8] = {'O', 'R', 'N', 'S', 'E', 'S', 'S', '\0'};
+
+// the f16 bit pattern of an integer V code (|c| <= 127: exact), the
+// device's f16_bits_of_code
+static uint16_t f16_of_code(int c) {
+    if (c == 0) return 0;
+    const uint16_t sgn = c < 0 ? 0x8000 : 0;
+    const unsigned m = (unsigned)(c < 0 ? -c : c);
+    const int e = 31 - __builtin_clz(m);
+    return (uint16_t)(sgn | (unsigned)(e + 15) << 10 | (m - (1u << e)) << (10 - e));
+}
 static const uint32_t kSessVersion = 1;
 
 void sess_fp(const ornith_hip_arch &a, int32_t fp[13]) {
@@ -217,15 +227,19 @@ extern "C" int ornith_hip_session_load(ornith_hip_model *m, const char *path, in
             // into the device layouts: K words [kvh][hd/4][cap], V tiles [kvh][cap/16][hd][16]
             std::vector<uint32_t> kt((size_t)nkv * (hd / 4) * kc, 0u);
             std::vector<int8_t> vt((size_t)nkv * kc * hd, 0);
+            std::vector<uint16_t> vh((size_t)nkv * kc * hd, 0);
             for (int t = 0; t < len; t++)
                 for (int h = 0; h < nkv; h++)
                     for (int i = 0; i < hd; i++) {
                         const size_t src = ((size_t)t * nkv + h) * hd + i;
                         kt[((size_t)h * (hd / 4) + i / 4) * kc + t] |= (uint32_t)(uint8_t)kq[src] << (8 * (i & 3));
-                        vt[(((size_t)h * (kc / 16) + t / 16) * hd + i) * 16 + (t & 15)] = vq[src];
+                        const size_t vo = (((size_t)h * (kc / 16) + t / 16) * hd + i) * 16 + (t & 15);
+                        vt[vo] = vq[src];
+                        vh[vo] = f16_of_code(vq[src]);
                     }
             if (hipMemcpy(z.Kt, kt.data(), kt.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
                 hipMemcpy(z.Vq, vt.data(), vt.size(), hipMemcpyHostToDevice) != hipSuccess ||
+                hipMemcpy(z.Vh, vh.data(), vh.size() * 2, hipMemcpyHostToDevice) != hipSuccess ||
                 (sc && hipMemcpy(z.Ks, ks.data(), sc * 4, hipMemcpyHostToDevice) != hipSuccess) ||
                 (sc && hipMemcpy(z.Vs, vs.data(), sc * 4, hipMemcpyHostToDevice) != hipSuccess))
                 return fail(ORNITH_HIP_ERR_DEVICE, "upload failed");

@@ -511,8 +511,10 @@ OH_DEV void prep_body(const oh_op_prep &a, int vb, int pos, W &w) {
                     ((uint32_t)(c2 & 0xff) << 16) | ((uint32_t)(c3 & 0xff) << 24));
             if (t == 0) stc(a.Ks + off, scale);
         } else {
-            // tiles of 16 positions: Vq[h][pos/16][i][pos%16]
-            if (t < hd) stc(a.Vq + (((size_t)h * (cap / 16) + pos / 16) * hd + t) * 16 + (pos & 15), (int8_t)code);
+            // tiles of 16 positions: Vq[h][pos/16][i][pos%16], and Vh the same as f16
+            const size_t vo = (((size_t)h * (cap / 16) + pos / 16) * hd + t) * 16 + (pos & 15);
+            if (t < hd) stc(a.Vq + vo, (int8_t)code);
+            if (t < hd && a.Vh) stc(a.Vh + vo, f16_bits_of_code(code));
             if (t == 0) stc(a.Vs + off, scale);
         }
     }
@@ -646,6 +648,248 @@ OH_DEV void exact_body(const oh_op_attn &a, int vb, int pos, int lim, W &w) {
         }
     }
     stc(a.out + (size_t)h * hd + i, o * ref_sigmoid(ldc(a.gate + (size_t)h * hd + i)));
+}
+
+// ---- the exact walk in two launches (the decode step's graph path) ----------------
+// The same arithmetic as exact_body, with the scores spread over many blocks:
+// exact_scores_body writes s_t = (sum_i q_i*code_i) * Ks_t * scale of every
+// query head to a.scores [nh][cap]; exact_walk_body (one block per query
+// head) takes the softmax over them and the output walk in position order.
+
+// Scores of KV head g's query heads for the 64 positions of tile c
+// (vb = c * nkv + g), 512 threads: the tile's key words and the group's
+// queries go to LDS; lane = position, wave w takes the HPW heads from
+// w * HPW on (HPW * 8 >= nh / nkv); each dot sequential over i as in
+// exact_body.
+template <int HW, int HPW, class W>
+OH_DEV void exact_scores_hw(const oh_op_attn &a, int vb, int pos, W &w) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int nh = a.nh, nkv = a.nkv, hd = 4 * HW, cap = a.cap, G = nh / nkv;
+    const int g = vb % nkv, c = vb / nkv, T = pos + 1;
+    const int tid = tid_x(), lane = lane_id(), wave = tid >> 6;
+    const int t = c * 64 + lane;
+    const int tc = t < T ? t : T - 1;
+    if (!w.wait()) return;
+    uint32_t *kt = (uint32_t *)smem;                          // [HW][64]
+    float4 *q = (float4 *)(smem + HW * 64 * 4);               // [G][hd / 4]
+    {
+        // wave w loads words w, w + 8, ... of the tile's 64 positions; the
+        // group's queries (at most OH_EXACT2_GMAX * hd floats) load at the
+        // same time, every load issued before any is used
+        const uint32_t *kw = a.Kt + (size_t)g * HW * cap + tc;
+        uint32_t wd[HW / 8];
+#pragma unroll
+        for (int k = 0; k < HW / 8; k++) wd[k] = ldg(kw + (size_t)(wave + 8 * k) * cap);
+        constexpr int QR = OH_EXACT2_GMAX * HW / 512;          // float4 per thread
+        const int n4 = G * HW;
+        const float4 *qs = (const float4 *)(a.qr + (size_t)g * G * hd);
+        float4 qv[QR];
+#pragma unroll
+        for (int r = 0; r < QR; r++) qv[r] = ldg(qs + (tid + 512 * r < n4 ? tid + 512 * r : 0));
+#pragma unroll
+        for (int k = 0; k < HW / 8; k++) kt[(wave + 8 * k) * 64 + lane] = wd[k];
+#pragma unroll
+        for (int r = 0; r < QR; r++) if (tid + 512 * r < n4) q[tid + 512 * r] = qv[r];
+    }
+    const float ks = ldg(a.Ks + (size_t)tc * nkv + g);
+    // the tile's f16 value codes (4 tiles of 16 positions: 2 * hd / 128
+    // uint4 per thread), loaded here only so that the walk, which reads them
+    // next, finds them in the caches; consumed by an empty asm at the end
+    constexpr int VR = HW / 16;
+    uint32_t vk[VR];
+    {
+        const uint4 *vt = (const uint4 *)(a.Vh + ((size_t)g * (cap / 16) + (size_t)c * 4) * hd * 16);
+#pragma unroll
+        for (int r = 0; r < VR; r++) {
+            const int i = tid + 512 * r;                       // tile i / (2 * hd) of the 4
+            vk[r] = a.Vh && c * 64 + (i / (2 * hd)) * 16 < T ? ldg(vt + i).x : 0u;
+        }
+    }
+    __syncthreads();
+    const int h0 = wave * HPW;
+    if (h0 >= G) return;
+    const float4 *qh[HPW];
+#pragma unroll
+    for (int j = 0; j < HPW; j++) qh[j] = q + (h0 + j < G ? h0 + j : G - 1) * HW;
+    float acc[HPW];
+#pragma unroll
+    for (int j = 0; j < HPW; j++) acc[j] = 0.0f;
+#pragma unroll 4
+    for (int u = 0; u < HW; u++) {
+        const uint32_t wv = kt[u * 64 + lane];
+        const float c0 = (float)(int8_t)(wv & 0xff), c1 = (float)(int8_t)((wv >> 8) & 0xff);
+        const float c2 = (float)(int8_t)((wv >> 16) & 0xff), c3 = (float)(int8_t)(wv >> 24);
+#pragma unroll
+        for (int j = 0; j < HPW; j++) {
+            const float4 qv = qh[j][u];
+            acc[j] += qv.x * c0;
+            acc[j] += qv.y * c1;
+            acc[j] += qv.z * c2;
+            acc[j] += qv.w * c3;
+        }
+    }
+    uint32_t keep = 0;
+#pragma unroll
+    for (int r = 0; r < VR; r++) keep ^= vk[r];
+    asm volatile("" ::"v"(keep));
+    if (t >= T) return;
+#pragma unroll
+    for (int j = 0; j < HPW; j++) {
+        if (h0 + j >= G) break;
+        const float v = ks == 0.0f ? 0.0f : acc[j] * ks;
+        stc(a.scores + (size_t)(g * G + h0 + j) * cap + t, v * a.scale);
+    }
+}
+template <int HW, class W>
+OH_DEV void exact_scores_g(const oh_op_attn &a, int vb, int pos, W &w) {
+    const int G = a.nh / a.nkv;
+    if (G <= 8) exact_scores_hw<HW, 1>(a, vb, pos, w);
+    else if (G <= 16) exact_scores_hw<HW, 2>(a, vb, pos, w);
+    else exact_scores_hw<HW, 4>(a, vb, pos, w);
+}
+// the host takes this form only for nh / nkv <= OH_EXACT2_GMAX
+template <class W>
+OH_DEV void exact_scores_body(const oh_op_attn &a, int vb, int pos, int lim, W &w) {
+    const int c = vb / a.nkv, T = pos + 1;
+    if (T > lim || c * 64 >= T || a.nh > OH_EXACT2_GMAX * a.nkv) return;
+    if (a.hd == 256) exact_scores_g<64>(a, vb, pos, w);
+    else if (a.hd == 128) exact_scores_g<32>(a, vb, pos, w);
+    else exact_scores_g<16>(a, vb, pos, w);
+}
+
+// Query head h = vb: softmax over its T scores (max, exps, the double sum in
+// exact_body's order, inv = 1/sum) and o_i = sum_t (p_t*Vs_t)*code_t,i in
+// position order (thread i < hd), then o *= sigmoid(gate). The exps, then
+// the p_t*Vs_t, sit in dynamic LDS: the tiles of 16 positions up to lim and
+// two zero tiles past the last. The codes are read from the f16 copy a.Vh,
+// so each product is one mixed-precision fma with a zero addend: the exact
+// product rounded once, as the reference's multiply (a zero product may
+// come out +0 where the multiply gives -0; the running sum is never -0, so
+// adding either leaves it unchanged).
+template <class W>
+OH_DEV void exact_walk_body(const oh_op_attn &a, int vb, int pos, int lim, W &w) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ double red[4];
+    __shared__ float mred[4];
+    __shared__ uint64_t etab[32];
+    const int nh = a.nh, nkv = a.nkv, hd = a.hd, cap = a.cap;
+    const int h = vb, T = pos + 1, t = tid_x();
+    if (T > lim || h >= nh) return;
+    if (!w.wait()) return;
+    float *pb = (float *)smem;
+    const int kvh = h / (nh / nkv);
+    const int nt = (T + 15) / 16;
+    if (t < 32) etab[t] = k_exp2_tab[t];
+    // the first NB tiles of this thread's codes (the 16 f16 codes of element
+    // t in two uint4) load while the softmax runs; the walk keeps NB tiles
+    // in flight, reloading each slot right after its products are formed
+    constexpr int NB = 16;
+    const uint8_t *vbase = (const uint8_t *)a.Vh + (size_t)kvh * (cap / 16) * hd * 32;
+    const uint32_t lo = (uint32_t)(t < hd ? t : 0) * 32u;
+    auto ldt = [&](uint4 (&c)[2], int tile) {
+        const uint8_t *p = vbase + (size_t)tile * hd * 32;
+        c[0] = ldg((const uint4 *)(p + lo));
+        c[1] = ldg((const uint4 *)(p + lo + 16));
+    };
+    uint4 cw[NB][2];
+    if (t < hd) {
+#pragma unroll
+        for (int u = 0; u < NB; u++) ldt(cw[u], u < nt ? u : nt - 1);
+    }
+    // this thread's scores (positions t, t + 256, ...: at most PT of them,
+    // lim <= 256 * PT) and value scales, every load issued before any is used
+    constexpr int PT = 32;
+    const float *sh = a.scores + (size_t)h * cap;
+    float sv[PT], vs[PT];
+#pragma unroll
+    for (int r = 0; r < PT; r++) {
+        const int i = t + 256 * r < T ? t + 256 * r : T - 1;
+        sv[r] = ldg(sh + i);
+        vs[r] = ldg(a.Vs + (size_t)i * nkv + kvh);
+    }
+    const float gt = t < hd ? ldg(a.gate + (size_t)h * hd + t) : 0.0f;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < PT; r++) if (t + 256 * r < T) mx = fmaxf(mx, sv[r]);
+    mx = wave_max_f(mx);
+    if (lane_id() == 0) mred[t >> 6] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(mred[0], mred[1]), fmaxf(mred[2], mred[3]));
+    // the exps in groups of 8 slots (a slot past T is computed on a
+    // repeated score and left out of the sum), so those of a group overlap
+    double sum = 0.0;
+#pragma unroll
+    for (int r0 = 0; r0 < PT; r0 += 8) {
+        if (256 * r0 >= T) break;
+#pragma unroll
+        for (int r = r0; r < r0 + 8; r++) sv[r] = ref_expf_tab(sv[r] - mx, etab);
+#pragma unroll
+        for (int r = r0; r < r0 + 8; r++) sum += t + 256 * r < T ? (double)sv[r] : 0.0;
+    }
+    sum = block_sum_d(sum, red);
+    const float inv = (float)(1.0 / sum);
+#pragma unroll
+    for (int r = 0; r < PT; r++) if (t + 256 * r < T) pb[t + 256 * r] = sv[r] * inv * vs[r];
+    for (int i = T + t; i < 16 * (nt + 2); i += 256) pb[i] = 0.0f;
+    __syncthreads();
+    if (t >= hd) return;
+    // adds in position order; the weights past T are +0 (the plain sum
+    // equals the reference's zero-skipping one, see exact_body). While the
+    // 16 adds of tile k run, each add is followed by the product of the same
+    // lane position of tile k + 1 (scheduling barriers keep that order, so
+    // no instruction waits on the one just before it); the weights of tile
+    // k + 2 load from LDS after the second position and tile k's code slot
+    // (its products were formed a step earlier) reloads with tile k + NB
+    // after the fourth, inside the add chain's latency.
+    const float4 *p4 = (const float4 *)pb;
+    auto comp = [](const float4 (&P)[4], int j) {
+        const float4 v = P[j >> 2];
+        return (j & 3) == 0 ? v.x : (j & 3) == 1 ? v.y : (j & 3) == 2 ? v.z : v.w;
+    };
+    auto code = [](const uint4 (&c)[2], int j) {
+        const uint32_t wv = wsel(c[j >> 3], (j >> 1) & 3);
+        return (float)__builtin_bit_cast(_Float16, (uint16_t)((j & 1) ? (wv >> 16) : (wv & 0xffffu)));
+    };
+    float o = 0.0f;
+    float X[16], Y[16];
+    float4 P0[4], P1[4];
+    // RELOAD: a step of a full group of NB tiles (slot u reloads); the
+    // steps of the last, partial group load nothing
+    auto step = [&](auto reload, int k, int u, const float (&A)[16], float (&B)[16], const float4 (&Pk1)[4],
+                    float4 (&Pk2)[4]) {
+        const int s1 = (u + 1) % NB;
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            o = o + A[j];
+            B[j] = __builtin_fmaf(comp(Pk1, j), code(cw[s1], j), 0.0f);
+            if (j == 1) {
+#pragma unroll
+                for (int q = 0; q < 4; q++) Pk2[q] = p4[4 * (k + 2) + q];
+            }
+            if (decltype(reload)::value && j == 3) ldt(cw[u], k + NB < nt ? k + NB : nt - 1);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+#pragma unroll
+    for (int j = 0; j < 4; j++) P0[j] = p4[j];
+#pragma unroll
+    for (int j = 0; j < 16; j++) X[j] = __builtin_fmaf(comp(P0, j), code(cw[0], j), 0.0f);
+#pragma unroll
+    for (int j = 0; j < 4; j++) P1[j] = p4[4 + j];
+    int k0 = 0;
+    for (; k0 + NB <= nt; k0 += NB) {
+#pragma unroll
+        for (int u = 0; u < NB; u += 2) {
+            step(std::true_type(), k0 + u, u, X, Y, P1, P0);
+            step(std::true_type(), k0 + u + 1, u + 1, Y, X, P0, P1);
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < NB; u += 2) {
+        if (k0 + u < nt) step(std::false_type(), k0 + u, u, X, Y, P1, P0);
+        if (k0 + u + 1 < nt) step(std::false_type(), k0 + u + 1, u + 1, Y, X, P0, P1);
+    }
+    stc(a.out + (size_t)h * hd + t, o * ref_sigmoid(gt));
 }
 
 // ---- flash decoding for long contexts ----------------------------------------------
@@ -1291,6 +1535,16 @@ extern "C" __global__ void __launch_bounds__(256) oh_k_attn_main(oh_op_attn a, c
     attn_main_body(a, (int)blockIdx.x, io[OH_IO_POS], w);
 }
 
+// the graph step's exact attention in two launches (contexts up to the exact
+// limit; both exit past it): the scores, then the softmax and output walk
+extern "C" __global__ void __launch_bounds__(512) oh_k_attn_scores(oh_op_attn a, const int32_t *io) {
+    NoWait w;
+    exact_scores_body(a, (int)blockIdx.x, io[OH_IO_POS], exact_lim(a.exact_max, a.hd), w);
+}
+extern "C" __global__ void __launch_bounds__(256) oh_k_attn_walk(oh_op_attn a, const int32_t *io) {
+    NoWait w;
+    exact_walk_body(a, (int)blockIdx.x, io[OH_IO_POS], exact_lim(a.exact_max, a.hd), w);
+}
 extern "C" __global__ void __launch_bounds__(256) oh_k_attn_combine(oh_op_attn a, const int32_t *io) {
     NoWait w;
     combine_body(a, (int)blockIdx.x, io[OH_IO_POS], w, exact_lim(a.exact_max, a.hd));

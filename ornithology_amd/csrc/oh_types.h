@@ -125,6 +125,9 @@ typedef struct {
 // kernel variant of a launch whose segments are all integer-path Q4_K and Q6_K
 // ones (the others: the segment type, or -1 for any mix)
 #define OH_MV_Q4Q6 (-2)
+// the graph step's two-launch exact attention takes at most this many query
+// heads per KV head
+#define OH_EXACT2_GMAX 32
 // blocks used by the argmax's first stage (the caller sizes its scratch)
 #define OH_ARGMAX_BLOCKS 256
 // IQ2_XXS rows of the f32 fallback per 256-thread block: one lane per row,
@@ -214,6 +217,8 @@ enum {
     OH_OP_MOE_COMBINE,     // u.comb
     OH_OP_ARGMAX1,         // u.am
     OH_OP_ARGMAX2,         // u.am
+    OH_OP_ATTN_SCORES,     // u.attn: the exact walk's scores (the graph step's exact regime)
+    OH_OP_ATTN_WALK,       // u.attn: the exact walk's softmax and output (the graph step's exact regime)
     OH_OP_COUNT
 };
 
@@ -242,6 +247,7 @@ typedef struct {
     float *Vs;
     int nh, nkv, hd, rot, cap;
     float eps;
+    uint16_t *Vh;                  // the V codes again as f16 bits, same tiles (optional)
 } oh_op_prep;
 
 // GQA scores / ordered output / flash chunks / flash merge
@@ -254,6 +260,7 @@ typedef struct {
     float *scores, *part_o, *part_ml, *out;
     int nh, nkv, hd, cap, exact_max, hb;
     float scale;
+    const uint16_t *Vh;            // the V codes as f16 bits (the graph step's exact walk)
 } oh_op_attn;
 
 typedef struct {

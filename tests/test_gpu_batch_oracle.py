@@ -27,7 +27,10 @@ import pytest
 import clibs
 from clibs import i32p
 
-pytestmark = pytest.mark.gpu
+pytestmark = [pytest.mark.gpu,
+              pytest.mark.skip(reason="batch decode is switched off: a batch run faulted the GPU for the fourth time (slotted launches, C1, "
+                 "three sessions of capacity 330 inside the exact walk, a case that had passed before); cause not "
+                 "found; the engine refuses ornith_hip_batch_step")]
 
 MIX = dict(clibs.C1, hidden=768, n_layers=4, vocab=1000, nh=4, nkv=1, hd=128, nk=2, nv=4, dhead=128,
            ne=8, top_k=2, moe_inter=512, shared_inter=512, t_default=clibs.Q4_K, t_attn_v=clibs.Q6_K,
