@@ -182,7 +182,9 @@ int  ornith_hip_session_step(ornith_hip_session *s, int32_t token);
  * with every context on the same attention path (all within the exact walk
  * or all past it), and HIP graphs on; other batches return
  * ORNITH_HIP_ERR_UNSUPPORTED. Calls sharing a session or a first session must
- * not overlap (the first session holds the step's buffers). */
+ * not overlap (the first session holds the step's buffers).
+ * Currently switched off: every call returns ORNITH_HIP_ERR_UNSUPPORTED (batch
+ * runs have faulted the GPU with the cause not found). */
 int  ornith_hip_batch_step(ornith_hip_session **s, int n, const int32_t *tokens, int32_t *next);
 
 /* rmodel_session_save (src/ornith_rforward.c:1019-1075): the session as an

@@ -180,7 +180,11 @@ struct ornith_hip_session {
     double *oruns = nullptr;      // delta step: sum of o^2 per 16-row run (per 64 rows: the step kernel)
     uint64_t *rtag = nullptr;     // MoE layers: router logits as tagged words [n_layers][ne + 1] (fused router)
     int32_t *mctr = nullptr;      // MoE layers: router completion counters of the fused MoE launch [n_layers][2]
-    int exact_max = 1024;         // contexts up to this walk the attention sum in one block
+    // decode contexts up to this (at most the walk's cap for the head dim:
+    // 8192 positions at hd 256) take the attention sum in the reference's
+    // order; longer ones the flash chunks
+    int exact_max = 8192;
+    int pf_exact_max = 1024;      // prompt rows up to this context take the exact row walk
     int flash_mfma = 1;           // decode flash chunks on the matrix cores (ORNITH_HIP_FLASH_MFMA=0: VALU)
     float2 *rope = nullptr;
     float *rl = nullptr, *shl = nullptr, *shg = nullptr, *ew = nullptr;

@@ -210,14 +210,14 @@ int pf_chunk(ornith_hip_session *s, int base, int T, bool chunked, hipStream_t s
             memset(&at, 0, sizeof at);
             at.qr = p.QR; at.gate = p.AG; at.Kt = z.Kt; at.Ks = z.Ks; at.Vq = z.Vq; at.Vs = z.Vs;
             at.part_o = p.FPO; at.part_ml = p.FPML; at.out = p.OA;
-            at.nh = a.nh; at.nkv = a.nkv; at.hd = a.hd; at.cap = s->kvcap; at.exact_max = s->exact_max;
+            at.nh = a.nh; at.nkv = a.nkv; at.hd = a.hd; at.cap = s->kvcap; at.exact_max = s->pf_exact_max;
             at.hb = oh_flash_hb(a.nh, a.nkv); at.scale = 1.0f / sqrtf((float)a.hd);
             const int nch = (s->kvcap + oh_flash_chunk() - 1) / oh_flash_chunk();
             const size_t po = (size_t)a.nh * nch * a.hd, pml = (size_t)a.nh * nch * 2;
             // tokens whose context fits the exact walk take it (sub-batches of
             // kPfAttnSub); the rest go to the matrix-core kernel in one launch
             // (ORNITH_HIP_ATTN_MFMA=0: the flash chunks of the decode step)
-            const int lim = s->exact_max < 2048 ? s->exact_max : 2048;
+            const int lim = s->pf_exact_max < 2048 ? s->pf_exact_max : 2048;
             const int tsplit = attn_mfma_enabled() && oh_attn_mfma_supported(a.hd, a.nh, a.nkv)
                              ? (lim - base < 0 ? 0 : (lim - base > T ? T : lim - base)) : T;
             if (tsplit < T || base + T <= lim) {

@@ -134,7 +134,7 @@ extern "C" int ornith_hip_session_new(ornith_hip_model *m, int cap, ornith_hip_s
     }
     {
         const char *e = getenv("ORNITH_HIP_EXACT_ATTN_MAX");
-        if (e && *e) s->exact_max = atoi(e);
+        if (e && *e) s->exact_max = s->pf_exact_max = atoi(e);
         const char *f = getenv("ORNITH_HIP_FLASH_MFMA");
         if (f && *f) s->flash_mfma = atoi(f) != 0;
     }
