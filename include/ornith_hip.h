@@ -102,13 +102,15 @@ int  ornith_hip_matvec(ornith_hip_ctx *ctx, const ornith_hip_tensor *W,
                        const float *x, float *y, int Tn);
 
 /* No counterpart in the reference. ornith_hip_matvec for callers that cannot
- * allocate device memory (code under HIP graph capture, tight serving loops,
- * harnesses that forbid hipMalloc): the same results, computed one column at
- * a time in a fixed 4 MiB device array per GPU (resolved by ornith_hip_init)
- * instead of a buffer the library allocates. Limit: in*5 + (in/256)*40 +
- * out*4 + 4096 <= 4 MiB (e.g. out <= 1,040,000 rows at in = 2048); larger
- * tensors return ORNITH_HIP_ERR_UNSUPPORTED. Calls that overlap on one GPU
- * share the array and race: serialise them. */
+ * allocate device memory (tight serving loops, harnesses that forbid
+ * hipMalloc): the same results, computed one column at a time in a fixed
+ * 4 MiB device array per GPU (resolved by ornith_hip_init) instead of a buffer
+ * the library allocates. It still copies X and Y between host and device and
+ * synchronises the context's stream, so it must not be called while a stream
+ * capture is active. Limit: in*5 + (in/256)*40 + out*4 + 4096 <= 4 MiB (e.g.
+ * out <= 1,040,000 rows at in = 2048); larger tensors return
+ * ORNITH_HIP_ERR_UNSUPPORTED. Calls that overlap on one GPU share the array
+ * and race: serialise them. */
 int  ornith_hip_matvec_noalloc(ornith_hip_ctx *ctx, const ornith_hip_tensor *W,
                                const float *x, float *y, int Tn);
 

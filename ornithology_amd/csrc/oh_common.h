@@ -345,6 +345,27 @@ OH_DEV void stc4(float4 *p, const float4 v) {
     stc(q + 1, __longlong_as_double((long long)(((uint64_t)f2u(v.w) << 32) | f2u(v.z))));
 }
 
+// A load of another launch's (or phase's) output: device-scope inside the
+// persistent kernels (G: the phases of one launch), a plain load in a
+// stand-alone kernel, whose start is ordered after the earlier launches'
+// writes (a plain load may then hit in this XCD's L2, which a device-scope
+// one skips).
+template <bool G, typename T>
+OH_DEV T ldw(const T *p) {
+    if constexpr (G) return ldc(p);
+    else return ldg(p);
+}
+template <bool G>
+OH_DEV float4 ldw4(const float4 *p) {
+    if constexpr (G) return ldc4(p);
+    else return ldg(p);
+}
+template <bool G>
+OH_DEV int4 ldw4(const int4 *p) {
+    if constexpr (G) return ldc4(p);
+    else return ldg(p);
+}
+
 // LDS ordering between the lanes of one wave (no workgroup barrier): waits for
 // the wave's LDS operations and keeps the compiler from moving LDS accesses
 // across it.

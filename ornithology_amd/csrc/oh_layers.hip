@@ -143,9 +143,9 @@ OH_DEV void delta_body(const oh_op_delta &a, int vb, int pos, float *lds, W &w) 
     // then this step's inputs from the input projection
     float cx[NCH];
 #pragma unroll
-    for (int c = 0; c < NCH; c++) cx[c] = ldc(a.cat + ch[c]);
-    const float av = ldc(a.ab + hv), bv = ldc(a.ab + nv + hv);
-    const float gz = ldc(a.gate + (size_t)hv * DK + r);
+    for (int c = 0; c < NCH; c++) cx[c] = ldw<W::kGrid>(a.cat + ch[c]);
+    const float av = ldw<W::kGrid>(a.ab + hv), bv = ldw<W::kGrid>(a.ab + nv + hv);
+    const float gz = ldw<W::kGrid>(a.gate + (size_t)hv * DK + r);
     // slab -> LDS, row-padded (frees the slab's registers for the step)
 #pragma unroll
     for (int i = 0; i < DK / 4; i++) {
@@ -317,12 +317,12 @@ OH_DEV void delta16_body(const oh_op_delta &a, int vb, int pos, float *lds, W &w
     // this step's inputs from the input projection
     float cx[NQ];
 #pragma unroll
-    for (int i = 0; i < NQ; i++) cx[i] = (qk || (vl && i == 0)) ? ldc(a.cat + ch[i]) : 0.0f;
-    const float gz = vl ? ldc(a.gate + (size_t)hv * DK + r0 + lane) : 0.0f;
+    for (int i = 0; i < NQ; i++) cx[i] = (qk || (vl && i == 0)) ? ldw<W::kGrid>(a.cat + ch[i]) : 0.0f;
+    const float gz = vl ? ldw<W::kGrid>(a.gate + (size_t)hv * DK + r0 + lane) : 0.0f;
     float av = 0.0f, bv = 0.0f;
     if (wave == 3 && lane == 0) {
-        av = ldc(a.ab + hv);
-        bv = ldc(a.ab + nv + hv);
+        av = ldw<W::kGrid>(a.ab + hv);
+        bv = ldw<W::kGrid>(a.ab + nv + hv);
     }
     // causal depthwise conv (no bias) + SiLU, in delta_body's order
     float cv[NQ];
@@ -461,11 +461,12 @@ OH_DEV void prep_body(const oh_op_prep &a, int vb, int pos, W &w) {
     const float *src = isq ? a.qproj + (size_t)h * 2 * hd : a.kin + (size_t)h * hd;
     const float *nw = isq ? a.q_norm : a.k_norm;
     const float2 *rope = (const float2 *)a.rope;
-    const float x = t < hd ? ldc(src + t) : 0.0f;
+    const float x = t < hd ? ldw<W::kGrid>(src + t) : 0.0f;
     const float nwt = t < hd ? ldg(nw + t) : 0.0f;
     const int pi = t < half ? t : t - half;
     const float2 cs = t < 2 * half ? ldg(rope + (size_t)pos * (hd / 2) + pi) : make_float2(1.0f, 0.0f);
-    const float other = t < hd ? (isq ? ldc(a.qproj + (size_t)h * 2 * hd + hd + t) : ldc(a.vin + (size_t)h * hd + t))
+    const float other = t < hd ? (isq ? ldw<W::kGrid>(a.qproj + (size_t)h * 2 * hd + hd + t)
+                                      : ldw<W::kGrid>(a.vin + (size_t)h * hd + t))
                                : 0.0f;
     double ss = block_sum_d((double)x * x, red);
     const float inv = (float)(1.0 / sqrt(ss / (double)hd + (double)a.eps));
@@ -1405,9 +1406,9 @@ OH_DEV void combine_body(const oh_op_attn &a, int vb, int pos, W &w, int lim) {
         for (int u = 0; u < CB; u++) {
             const int c = c0 + 4 * u < nch ? c0 + 4 * u : c0;
             const size_t base = ((size_t)g * nchmax + c) * G + hl;
-            mb[u] = ldc(a.part_ml + base * 2);
-            lb[u] = ldc(a.part_ml + base * 2 + 1);
-            ob[u] = ldc(a.part_o + base * hd + i);
+            mb[u] = ldw<W::kGrid>(a.part_ml + base * 2);
+            lb[u] = ldw<W::kGrid>(a.part_ml + base * 2 + 1);
+            ob[u] = ldw<W::kGrid>(a.part_o + base * hd + i);
         }
 #pragma unroll
         for (int u = 0; u < CB; u++) {
@@ -1431,7 +1432,7 @@ OH_DEV void combine_body(const oh_op_attn &a, int vb, int pos, W &w, int lim) {
             Lt += sm[k][1][lane] * f;
             Ot += sm[k][2][lane] * f;
         }
-        stc(a.out + (size_t)h * hd + i, Ot / Lt * ref_sigmoid(ldc(a.gate + (size_t)h * hd + i)));
+        stc(a.out + (size_t)h * hd + i, Ot / Lt * ref_sigmoid(ldw<W::kGrid>(a.gate + (size_t)h * hd + i)));
     }
 }
 

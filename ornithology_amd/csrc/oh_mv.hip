@@ -566,6 +566,7 @@ OH_DEV float4 f4_silu_mul(const float4 g, const float4 u) {
 // in passes of up to 4 float4 per thread (4096 floats); every load of a pass
 // is issued before its first LDS store, so a pass costs one memory round trip.
 // Same values and summation orders as pro_compute.
+template <bool G>
 OH_DEV void mv_prologue(const oh_mvseg &s, int slot, int blk, uint8_t *smem, double *red, bool q8) {
     // activations come from earlier phases: device-scope loads
     const int in = s.in, nb = in / 256, tid = tid_x(), wave = tid >> 6;
@@ -583,21 +584,21 @@ OH_DEV void mv_prologue(const oh_mvseg &s, int slot, int blk, uint8_t *smem, dou
             for (int i0 = 0; i0 < n16; i0 += 256 * PW) {
                 int4 r[PW];
 #pragma unroll
-                for (int u = 0; u < PW; u++) r[u] = ldc4(gq + (i0 + tid + 256 * u < n16 ? i0 + tid + 256 * u : n16 - 1));
+                for (int u = 0; u < PW; u++) r[u] = ldw4<G>(gq + (i0 + tid + 256 * u < n16 ? i0 + tid + 256 * u : n16 - 1));
 #pragma unroll
                 for (int u = 0; u < PW; u++) {
                     const int i = i0 + tid + 256 * u;
                     if (i < n16) ((int4 *)aqs)[(i >> 4) * (kAS / 16) + (i & 15)] = r[u];
                 }
             }
-            for (int i = tid; i < nb * 16; i += 256) abs[i] = ldc(s.xbs + ao / 16 + i);
-            for (int i = tid; i < nb; i += 256) ad[i] = ldc(s.xd + ao / 256 + i);
+            for (int i = tid; i < nb * 16; i += 256) abs[i] = ldw<G>(s.xbs + ao / 16 + i);
+            for (int i = tid; i < nb; i += 256) ad[i] = ldw<G>(s.xd + ao / 256 + i);
         } else {
             // any width (fallback rows): scalar passes of 16 per thread
             for (int i0 = 0; i0 < in; i0 += 256 * 16) {
                 float r[16];
 #pragma unroll
-                for (int u = 0; u < 16; u++) r[u] = ldc(s.xf + ao + (i0 + tid + 256 * u < in ? i0 + tid + 256 * u : in - 1));
+                for (int u = 0; u < 16; u++) r[u] = ldw<G>(s.xf + ao + (i0 + tid + 256 * u < in ? i0 + tid + 256 * u : in - 1));
 #pragma unroll
                 for (int u = 0; u < 16; u++)
                     if (i0 + tid + 256 * u < in) v[i0 + tid + 256 * u] = r[u];
@@ -619,13 +620,13 @@ OH_DEV void mv_prologue(const oh_mvseg &s, int slot, int blk, uint8_t *smem, dou
             if (s.runs16) {
                 // 16-row partials: each 64-row run is (g0 + g1) + (g2 + g3)
                 const double *g = s.xruns + ao / 16 + (size_t)h * (gd / 16);
-                tot = (ldc(g) + ldc(g + 1)) + (ldc(g + 2) + ldc(g + 3));
+                tot = (ldw<G>(g) + ldw<G>(g + 1)) + (ldw<G>(g + 2) + ldw<G>(g + 3));
                 for (int k = 1; k < rpg; k++)
-                    tot += (ldc(g + 4 * k) + ldc(g + 4 * k + 1)) + (ldc(g + 4 * k + 2) + ldc(g + 4 * k + 3));
+                    tot += (ldw<G>(g + 4 * k) + ldw<G>(g + 4 * k + 1)) + (ldw<G>(g + 4 * k + 2) + ldw<G>(g + 4 * k + 3));
             } else {
                 const double *xr = s.xruns + ao / 64;  // the slot's run sums
-                tot = ldc(xr + h * rpg);
-                for (int k = 1; k < rpg; k++) tot += ldc(xr + h * rpg + k);
+                tot = ldw<G>(xr + h * rpg);
+                for (int k = 1; k < rpg; k++) tot += ldw<G>(xr + h * rpg + k);
             }
             hinv[h] = (float)(1.0 / sqrt(tot / (double)gd + (double)s.eps));
         }
@@ -636,8 +637,8 @@ OH_DEV void mv_prologue(const oh_mvseg &s, int slot, int blk, uint8_t *smem, dou
 #pragma unroll
             for (int u = 0; u < PW; u++) {
                 const int f = i0 + tid + 256 * u < n4 ? i0 + tid + 256 * u : n4 - 1;
-                xr[u] = ldc4(x4 + f);
-                zr[u] = ldc4(z4 + f);
+                xr[u] = ldw4<G>(x4 + f);
+                zr[u] = ldw4<G>(z4 + f);
                 wr[u] = ldg(w4 + f % (gd / 4));
             }
 #pragma unroll
@@ -659,8 +660,8 @@ OH_DEV void mv_prologue(const oh_mvseg &s, int slot, int blk, uint8_t *smem, dou
 #pragma unroll
             for (int u = 0; u < PW; u++) {
                 const int f = i0 + tid + 256 * u < n4 ? i0 + tid + 256 * u : n4 - 1;
-                gr[u] = ldc4(x4 + f);
-                ur[u] = ldc4(u4 + f);
+                gr[u] = ldw4<G>(x4 + f);
+                ur[u] = ldw4<G>(u4 + f);
             }
 #pragma unroll
             for (int u = 0; u < PW; u++)
@@ -671,7 +672,7 @@ OH_DEV void mv_prologue(const oh_mvseg &s, int slot, int blk, uint8_t *smem, dou
         for (int i0 = 0; i0 < n4; i0 += 256 * PW) {
             float4 xr[PW];
 #pragma unroll
-            for (int u = 0; u < PW; u++) xr[u] = ldc4(x4 + (i0 + tid + 256 * u < n4 ? i0 + tid + 256 * u : n4 - 1));
+            for (int u = 0; u < PW; u++) xr[u] = ldw4<G>(x4 + (i0 + tid + 256 * u < n4 ? i0 + tid + 256 * u : n4 - 1));
 #pragma unroll
             for (int u = 0; u < PW; u++)
                 if (i0 + tid + 256 * u < n4) v4[i0 + tid + 256 * u] = xr[u];
@@ -722,14 +723,15 @@ OH_DEV void mv_prologue(const oh_mvseg &s, int slot, int blk, uint8_t *smem, dou
 // weights would wait for them).
 struct PIn { float4 a[4], b[4], c[4]; int4 q, bsv; float d; double r0, r1; };
 
+template <bool G>
 OH_DEV void pro_load(PIn &p, const oh_mvseg &s, int slot) {
     const int tid = tid_x(), in = s.in, nb = in / 256;
     const size_t ao = (size_t)(s.adiv > 1 ? slot / s.adiv : slot) * s.astride;
     if (s.pro == OH_PRO_Q8K) {
         const int n16 = in / 16;
-        p.q = ldc4((const int4 *)(s.xqs + ao) + (tid < n16 ? tid : n16 - 1));
-        p.bsv = ldc4((const int4 *)(s.xbs + ao / 16) + (tid < 2 * nb ? tid : 2 * nb - 1));
-        p.d = ldc(s.xd + ao / 256 + (tid < nb ? tid : nb - 1));
+        p.q = ldw4<G>((const int4 *)(s.xqs + ao) + (tid < n16 ? tid : n16 - 1));
+        p.bsv = ldw4<G>((const int4 *)(s.xbs + ao / 16) + (tid < 2 * nb ? tid : 2 * nb - 1));
+        p.d = ldw<G>(s.xd + ao / 256 + (tid < nb ? tid : nb - 1));
     } else {
         // activations from earlier phases (device-scope loads); the RMSNorm
         // weights are constant
@@ -743,8 +745,8 @@ OH_DEV void pro_load(PIn &p, const oh_mvseg &s, int slot) {
         for (int k = 0; k < 4; k++) {
             if (k < nk) {
                 const int i = tid + 256 * k < n4 ? tid + 256 * k : n4 - 1;
-                p.a[k] = ldc4(x + i);
-                p.b[k] = wc ? ldg(w + i) : ldc4(w + i);
+                p.a[k] = ldw4<G>(x + i);
+                p.b[k] = wc ? ldg(w + i) : ldw4<G>(w + i);
                 if (s.pro == OH_PRO_GNORM) p.c[k] = ldg((const float4 *)s.nw + i % (s.gdim / 4));
             } else {
                 p.a[k] = p.b[k] = p.c[k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
@@ -754,13 +756,13 @@ OH_DEV void pro_load(PIn &p, const oh_mvseg &s, int slot) {
             if (s.runs16) {
                 // 16-row partials (in/16 <= 256): this thread's one
                 const int n16 = in / 16;
-                p.r0 = ldc(s.xruns + ao / 16 + (tid < n16 ? tid : n16 - 1));
+                p.r0 = ldw<G>(s.xruns + ao / 16 + (tid < n16 ? tid : n16 - 1));
             } else {
                 // this thread's head (tid < in/gdim): its first two run sums
                 const int rpg = s.gdim / 64, nh = in / s.gdim, h = tid < nh ? tid : nh - 1;
                 const double *xr = s.xruns + ao / 64;  // the slot's run sums
-                p.r0 = ldc(xr + h * rpg);
-                p.r1 = ldc(xr + h * rpg + (rpg > 1 ? 1 : 0));
+                p.r0 = ldw<G>(xr + h * rpg);
+                p.r1 = ldw<G>(xr + h * rpg + (rpg > 1 ? 1 : 0));
             }
         }
     }
@@ -936,7 +938,7 @@ OH_DEV void mv_seg(const oh_mvseg &s, int slot, int blk, int expert, uint8_t *sm
     int64_t row_base = (int64_t)expert * s.rows;            // set by late() in the late form
     float *y = s.y + (size_t)slot * s.ystride;
     const WP wp = {s.A, s.B, s.C}, wp2 = {s.A2, s.B2, s.C2};
-    const uint32_t tag = s.mode == 2 ? (uint32_t)ldc(s.tagp) + 1u : 0u;
+    const uint32_t tag = s.mode == 2 ? (uint32_t)ldw<W::kGrid>(s.tagp) + 1u : 0u;
     const int8_t *aq = (const int8_t *)smem + sb * kAS;
     const int16_t *abs = (const int16_t *)(smem + mv_lds_bs_off(nb)) + sb * 16;
     const float *adp = (const float *)(smem + mv_lds_d_off(nb)) + sb;
@@ -972,7 +974,7 @@ OH_DEV void mv_seg(const oh_mvseg &s, int slot, int blk, int expert, uint8_t *sm
     };
     auto y_prefetch = [&]() {
         const int row = u0 * rps + rl;
-        if (s.mode == 1 && !s.pair && S > 0 && rl < rps && row < s.rows && sb == 0) ypre = ldc(y + row);
+        if (s.mode == 1 && !s.pair && S > 0 && rl < rps && row < s.rows && sb == 0) ypre = ldw<W::kGrid>(y + row);
     };
     if (LT::kLate) {
         // the activation while the routing is still being published, then
@@ -981,10 +983,10 @@ OH_DEV void mv_seg(const oh_mvseg &s, int slot, int blk, int expert, uint8_t *sm
         y_prefetch();
         if (s.in <= 4096) {
             PIn pin;
-            pro_load(pin, s, slot);
+            pro_load<W::kGrid>(pin, s, slot);
             pro_compute(pin, s, slot, blk, smem, red);
         } else {
-            mv_prologue(s, slot, blk, smem, red, true);
+            mv_prologue<W::kGrid>(s, slot, blk, smem, red, true);
         }
         row_base = (int64_t)late() * s.rows;
         load(ra, 0);
@@ -993,10 +995,10 @@ OH_DEV void mv_seg(const oh_mvseg &s, int slot, int blk, int expert, uint8_t *sm
         if (W::kGrid) {
             load(ra, 0);
             if (!w.wait()) return;
-            pro_load(pin, s, slot);
+            pro_load<W::kGrid>(pin, s, slot);
             y_prefetch();
         } else {
-            pro_load(pin, s, slot);
+            pro_load<W::kGrid>(pin, s, slot);
             y_prefetch();
             load(ra, 0);
         }
@@ -1006,7 +1008,7 @@ OH_DEV void mv_seg(const oh_mvseg &s, int slot, int blk, int expert, uint8_t *sm
         load(ra, 0);
         if (!w.wait()) return;
         y_prefetch();
-        mv_prologue(s, slot, blk, smem, red, true);
+        mv_prologue<W::kGrid>(s, slot, blk, smem, red, true);
     }
     // ra holds step 0; a step's loads are only issued when it will be reduced
     int st = 0;
@@ -1384,15 +1386,26 @@ OH_DEV void fused_count(const oh_mvlaunch &L, int vb, bool router) {
     }
 }
 
+// The block's segment: every segment's first block is read at once (a
+// while loop over them is a chain of dependent kernel-argument reads).
+OH_DEV int seg_index(const oh_mvlaunch &L, int vb) {
+    const int n = L.n;
+    int b0[OH_MAX_SEGS];
+#pragma unroll
+    for (int i = 1; i < OH_MAX_SEGS; i++) b0[i] = L.s[i].block0;
+    int si = 0;
+#pragma unroll
+    for (int i = 1; i < OH_MAX_SEGS; i++) si += i < n && vb >= b0[i] ? 1 : 0;
+    return si;
+}
+
 template <int TK, class W>
 OH_DEV void mv_body(const oh_mvlaunch &L, int vb, W &w) {
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ double red[4];
     __shared__ int rsel[64], rbad, rcnt[64];
     __shared__ float rwt[64], rshg;
-    int si = 0;
-    while (si + 1 < L.n && vb >= L.s[si + 1].block0) si++;
-    const oh_mvseg &s = L.s[si];
+    const oh_mvseg &s = L.s[seg_index(L, vb)];
     const int bseg = vb - s.block0;
     const int slot = bseg / s.bps, blk = bseg - slot * s.bps;
     if (L.rtag) {
@@ -1433,7 +1446,7 @@ OH_DEV void mv_body(const oh_mvlaunch &L, int vb, W &w) {
     } else if (s.eidx) {
         if (!w.wait()) return;                    // the routing comes from an earlier phase
     }
-    const int expert = !s.eidx ? 0 : (L.route ? rsel[L.tslots > 0 ? slot % L.tslots : slot] : ldc(s.eidx + slot));
+    const int expert = !s.eidx ? 0 : (L.route ? rsel[L.tslots > 0 ? slot % L.tslots : slot] : ldw<W::kGrid>(s.eidx + slot));
     if constexpr (TK >= 0) {
         mv_seg<TK < 0 ? OH_Q4_K : TK>(s, slot, blk, expert, smem, red, w);
         if (L.mctr && (s.mode == 2 || vb == L.pb0)) fused_count(L, vb, s.mode == 2);
@@ -1456,7 +1469,7 @@ OH_DEV void mv_body(const oh_mvlaunch &L, int vb, W &w) {
         }
     } else {
         if (!w.wait()) return;
-        mv_prologue(s, slot, blk, smem, red, false);
+        mv_prologue<W::kGrid>(s, slot, blk, smem, red, false);
         if (s.type == OH_IQ2_XXS) {
             if (s.iq2split) iq2_rows(s, slot, blk, expert, smem);
             else iq2_rows_lane(s, slot, blk, expert, smem);
@@ -1589,10 +1602,10 @@ OH_DEV void down_narrow(const oh_mvdown &D, int vb) {
     float *v = (float *)(smem + ns * sq);
     float *dots = v + ns * in;                            // [ns][R]
     const bool sh = j >= D.k;
-    const int e = sh ? 0 : ldc(D.eidx + j);
+    const int e = sh ? 0 : ldg(D.eidx + j);
     const bool comb = wave == 0 && lane < R && row0 + lane < D.rows;
-    const float xrow = comb ? ldc(D.x + row0 + lane) : 0.0f;
-    const float cwv = tid < D.k ? ldc(D.w + tid) : (tid == 16 && D.shg ? ldc(D.shg) : 1.0f);
+    const float xrow = comb ? ldg(D.x + row0 + lane) : 0.0f;
+    const float cwv = tid < D.k ? ldg(D.w + tid) : (tid == 16 && D.shg ? ldg(D.shg) : 1.0f);
     const int nf = ns * in / 4;
     const bool hreg = nf <= HA * bd;
     float4 ha[HA];
@@ -1601,7 +1614,7 @@ OH_DEV void down_narrow(const oh_mvdown &D, int vb) {
         for (int k = 0; k < HA; k++) {
             const int f = tid + bd * k < nf ? tid + bd * k : nf - 1;
             const int jj = 4 * f / in, el = 4 * f - jj * in;
-            ha[k] = ldc4((const float4 *)((jj < D.k ? D.h + (size_t)jj * D.stride : D.hsh) + el));
+            ha[k] = ldg((const float4 *)((jj < D.k ? D.h + (size_t)jj * D.stride : D.hsh) + el));
         }
     }
     const WP wp = sh ? WP{D.sA, D.sB, D.sC} : WP{D.A, D.B, D.C};
@@ -1616,7 +1629,7 @@ OH_DEV void down_narrow(const oh_mvdown &D, int vb) {
     } else {
         for (int i = tid; i < ns * in; i += bd) {
             const int jj = i / in, el = i - jj * in;
-            v[i] = ldc((jj < D.k ? D.h + (size_t)jj * D.stride : D.hsh) + el);
+            v[i] = ldg((jj < D.k ? D.h + (size_t)jj * D.stride : D.hsh) + el);
         }
     }
     lds_barrier();
