@@ -344,8 +344,9 @@ def batch_decode(model: oa.Model, n: int, ctx_len: int, steps: int) -> dict:
 
 # profile kind -> kernel symbol (as rocprofv3 names it)
 KERNEL_SYMBOL = {"matvec": "oh_k_mv_q4k", "matvec_q6k": "oh_k_mv_q6k", "matvec_q80": "oh_k_mv_q80",
-                 "matvec_mixed": "oh_k_mv_mixed", "moe_down": "oh_k_mv_down", "delta_step": "oh_k_delta16",
-                 "attn_main": "oh_k_attn_main", "attn_combine": "oh_k_attn_combine", "attn_prep": "oh_k_attn_prep",
+                 "matvec_mixed": "oh_k_mv_mixed", "matvec_q4q6": "oh_k_mv_q4k6k", "moe_down": "oh_k_mv_down_narrow",
+                 "delta_step": "oh_k_delta16", "attn_main": "oh_k_attn_main", "attn_combine": "oh_k_attn_combine",
+                 "attn_prep": "oh_k_attn_prep", "attn_scores": "oh_k_attn_scores", "attn_walk": "oh_k_attn_walk",
                  "step_body": "oh_k_step", "step_head": "oh_k_step"}
 
 
@@ -468,16 +469,20 @@ def timeline(args) -> int:
     print(f"# C3 decode stage timeline ({args.ctx}-token context)\n")
     print(f"HIP-graph step: {ms / 32:.3f} ms/token ({32 / (ms / 1e3):.1f} tok/s), 32 steps.\n")
     prof = sess.profile_step()
-    names = {"matvec": "Q4_K matvec", "matvec_mixed": "mixed matvec", "matvec_q6k": "Q6_K matvec"}
+    names = {"matvec": "Q4_K matvec", "matvec_mixed": "mixed matvec", "matvec_q6k": "Q6_K matvec",
+             "matvec_q4q6": "Q4_K/Q6_K matvec", "attn_scores": "attn scores (exact)",
+             "attn_walk": "attn walk (exact)"}
     full = C3["full_interval"]
-    # launch sequence per layer (the head's launches at the end)
-    seq, i = [], 1                                     # launch 0: embedding
-    per_layer = []
-    for l in range(C3["n_layers"]):
-        n = 8 if l % full == full - 1 else 6
-        per_layer.append(prof[i:i + n])
-        i += n
-    head = prof[i:]
+    # launch sequence per layer: every C3 layer ends with its MoE down
+    # projection (launch 0 is the embedding, the head's launches come last)
+    per_layer, cur = [], []
+    for rec in prof[1:]:
+        cur.append(rec)
+        if rec[0] == "moe_down":
+            per_layer.append(cur)
+            cur = []
+    head = cur
+    assert len(per_layer) == C3["n_layers"], (len(per_layer), C3["n_layers"])
     print("## 1. Per-launch step (eager, HIP events around every launch)\n")
     for l in (0, full - 1):
         kind = "full-attention" if l % full == full - 1 else "delta-net"

@@ -265,8 +265,8 @@ struct ornith_hip_session {
 };
 
 enum { K_MATVEC = 0, K_NORM_Q8K, K_SWIGLU_Q8K, K_EMBED, K_DELTA, K_ATTN_PREP, K_ATTN_SCORES,
-       K_ATTN_OUT, K_ROUTE, K_COMBINE, K_ARGMAX, K_ADVANCE, K_MV_DOWN, K_ATTN_FLASH, K_ATTN_COMBINE,
-       K_MATVEC_Q6K, K_MATVEC_Q80, K_MATVEC_MIXED, K_STEP_BODY, K_STEP_HEAD, K_ATTN_MAIN };
+       K_ATTN_WALK, K_ROUTE, K_COMBINE, K_ARGMAX, K_ADVANCE, K_MV_DOWN, K_ATTN_FLASH, K_ATTN_COMBINE,
+       K_MATVEC_Q6K, K_MATVEC_Q80, K_MATVEC_MIXED, K_STEP_BODY, K_STEP_HEAD, K_ATTN_MAIN, K_MATVEC_Q4Q6 };
 
 // ---- the token step as a program of operations ----------------------------------------------
 // The same list of operations runs either launch by launch (captured into HIP

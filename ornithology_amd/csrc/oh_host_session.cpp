@@ -31,7 +31,8 @@ bool keep(ornith_hip_session *s, int kind, double bytes) {
 }
 // matvec launches are recorded by kernel variant (see oh_launch_matvec)
 int mv_kind(int tk) {
-    return tk == OH_Q4_K ? K_MATVEC : tk == OH_Q6_K ? K_MATVEC_Q6K : tk == OH_Q8_0 ? K_MATVEC_Q80 : K_MATVEC_MIXED;
+    return tk == OH_Q4_K ? K_MATVEC : tk == OH_Q6_K ? K_MATVEC_Q6K : tk == OH_Q8_0 ? K_MATVEC_Q80
+         : tk == OH_MV_Q4Q6 ? K_MATVEC_Q4Q6 : K_MATVEC_MIXED;
 }
 oh_op op_new(int kind, int nvb, int lds) {
     oh_op o;
@@ -247,10 +248,11 @@ int build_body(ornith_hip_session *s, Prog &P) {
                 const int lim = oh_exact_limit(s->exact_max, a.hd);
                 oh_op o3 = op_new(OH_OP_ATTN_SCORES, a.nkv * ((lim + 63) / 64), ((a.nh / a.nkv) * 4 + 64) * a.hd);
                 o3.u.attn = at;
-                prog_add(P, o3, K_ATTN_MAIN, kvb + 4.0 * T * a.nh + 4.0 * aqd);
+                prog_add(P, o3, K_ATTN_SCORES, kvb + 4.0 * T * a.nh + 4.0 * aqd);
                 oh_op o4 = op_new(OH_OP_ATTN_WALK, a.nh, ((lim + 15) / 16 + 2) * 16 * 4);
                 o4.u.attn = at;
-                prog_add(P, o4, K_ATTN_COMBINE, kvb + 4.0 * T * a.nh + 12.0 * aqd);
+                // the walk reads the f16 copy of the codes (2 bytes each) and the scales
+                prog_add(P, o4, K_ATTN_WALK, T * a.nkv * (2.0 * a.hd + 4.0) + 4.0 * T * a.nh + 12.0 * aqd);
             } else {
                 const int nv_ex = a.nh / (256 / a.hd), lds_ex = oh_exact_lds_bytes(a.hd, s->exact_max);
                 oh_op o3 = op_new(OH_OP_ATTN_MAIN, nv_ex > nv_fl ? nv_ex : nv_fl, lds_ex > lds_fl ? lds_ex : lds_fl);
