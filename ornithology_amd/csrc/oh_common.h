@@ -71,6 +71,43 @@ OH_DEV float ref_expf_tab(float x, const TabT *tab) {
     return (float)y;
 }
 OH_DEV float ref_expf(float x) { return ref_expf_tab(x, k_exp2_tab); }
+// The same function without branches: the table path runs for every input
+// and the special cases (|x| >= 88: -inf, NaN/+inf, overflow, underflow)
+// replace its value by selects, so that several of these in a row overlap
+// (the branches of ref_expf_tab keep each one in a block of its own).
+template <typename TabT>
+OH_DEV float ref_expf_sel(float x, const TabT *tab) {
+    const uint32_t ax = f2u(x) & 0x7fffffffu;
+    const double inv_ln2_n = 0x1.71547652b82fep+0 * 32.0;
+    const double shift = 0x1.8p+52;
+    const double c0 = 0x1.c6af84b912394p-5 / 32.0 / 32.0 / 32.0;
+    const double c1 = 0x1.ebfce50fac4f3p-3 / 32.0 / 32.0;
+    const double c2 = 0x1.62e42ff0c52d6p-1 / 32.0;
+    const double xd = (double)x;
+    const double z = inv_ln2_n * xd;
+    double kd = z + shift;
+    const uint64_t ki = (uint64_t)__double_as_longlong(kd);
+    kd -= shift;
+    const double r = fma(inv_ln2_n, xd, -kd);
+    uint64_t t = tab[ki % 32];
+    t += ki << 47;
+    const double s = __longlong_as_double((long long)t);
+    const double p = fma(c0, r, c1);
+    const double r2 = r * r;
+    double y = fma(c2, r, 1.0);
+    y = fma(p, r2, y);
+    y = y * s;
+    // every candidate formed first, then chosen by masks (a conditional
+    // operand would be turned back into a branch)
+    const uint32_t v = f2u((float)y), xx = f2u(x + x);
+    const uint32_t m_big = 0u - (uint32_t)(ax >= 0x42b00000u);
+    const uint32_t m_ninf = m_big & (0u - (uint32_t)(f2u(x) == 0xff800000u));
+    const uint32_t m_nan = m_big & ~m_ninf & (0u - (uint32_t)(ax >= 0x7f800000u));
+    const uint32_t m_over = m_big & ~m_ninf & ~m_nan & (0u - (uint32_t)(x > 0x1.62e42ep6f));
+    const uint32_t m_under = m_big & ~m_ninf & ~m_nan & ~m_over & (0u - (uint32_t)(x < -0x1.9fe368p6f));
+    const uint32_t m_keep = ~(m_ninf | m_nan | m_over | m_under);
+    return u2f((v & m_keep) | (xx & m_nan) | (0x7f800000u & m_over));
+}
 
 // ---- glibc-compatible log1pf ------------------------------------------------
 // fdlibm s_log1pf.c (Sun Microsystems, freely redistributable), the

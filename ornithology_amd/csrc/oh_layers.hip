@@ -792,26 +792,36 @@ OH_DEV void exact_walk_body(const oh_op_attn &a, int vb, int pos, int lim, W &w)
         c[0] = ldg((const uint4 *)(p + lo));
         c[1] = ldg((const uint4 *)(p + lo + 16));
     };
+    // this thread's scores (positions t, t + 256, ...: at most PT of them,
+    // lim <= 256 * PT, requested in groups of 8 up to T) and value scales,
+    // then the gate and the code ring: every load issued before any is used,
+    // the softmax's first (they return in order)
+    constexpr int PT = 32;
+    const float *sh = a.scores + (size_t)h * cap;
+    float sv[PT], vs[PT];
+#pragma unroll
+    for (int r0 = 0; r0 < PT; r0 += 8) {
+        if (256 * r0 >= T) break;
+#pragma unroll
+        for (int r = r0; r < r0 + 8; r++) {
+            const int i = t + 256 * r < T ? t + 256 * r : T - 1;
+            sv[r] = ldg(sh + i);
+            vs[r] = ldg(a.Vs + (size_t)i * nkv + kvh);
+        }
+    }
+    const float gt = t < hd ? ldg(a.gate + (size_t)h * hd + t) : 0.0f;
     uint4 cw[NB][2];
     if (t < hd) {
 #pragma unroll
         for (int u = 0; u < NB; u++) ldt(cw[u], u < nt ? u : nt - 1);
     }
-    // this thread's scores (positions t, t + 256, ...: at most PT of them,
-    // lim <= 256 * PT) and value scales, every load issued before any is used
-    constexpr int PT = 32;
-    const float *sh = a.scores + (size_t)h * cap;
-    float sv[PT], vs[PT];
-#pragma unroll
-    for (int r = 0; r < PT; r++) {
-        const int i = t + 256 * r < T ? t + 256 * r : T - 1;
-        sv[r] = ldg(sh + i);
-        vs[r] = ldg(a.Vs + (size_t)i * nkv + kvh);
-    }
-    const float gt = t < hd ? ldg(a.gate + (size_t)h * hd + t) : 0.0f;
     float mx = -INFINITY;
 #pragma unroll
-    for (int r = 0; r < PT; r++) if (t + 256 * r < T) mx = fmaxf(mx, sv[r]);
+    for (int r0 = 0; r0 < PT; r0 += 8) {
+        if (256 * r0 >= T) break;
+#pragma unroll
+        for (int r = r0; r < r0 + 8; r++) if (t + 256 * r < T) mx = fmaxf(mx, sv[r]);
+    }
     mx = wave_max_f(mx);
     if (lane_id() == 0) mred[t >> 6] = mx;
     __syncthreads();
@@ -823,14 +833,18 @@ OH_DEV void exact_walk_body(const oh_op_attn &a, int vb, int pos, int lim, W &w)
     for (int r0 = 0; r0 < PT; r0 += 8) {
         if (256 * r0 >= T) break;
 #pragma unroll
-        for (int r = r0; r < r0 + 8; r++) sv[r] = ref_expf_tab(sv[r] - mx, etab);
+        for (int r = r0; r < r0 + 8; r++) sv[r] = ref_expf_sel(sv[r] - mx, etab);
 #pragma unroll
         for (int r = r0; r < r0 + 8; r++) sum += t + 256 * r < T ? (double)sv[r] : 0.0;
     }
     sum = block_sum_d(sum, red);
     const float inv = (float)(1.0 / sum);
 #pragma unroll
-    for (int r = 0; r < PT; r++) if (t + 256 * r < T) pb[t + 256 * r] = sv[r] * inv * vs[r];
+    for (int r0 = 0; r0 < PT; r0 += 8) {
+        if (256 * r0 >= T) break;
+#pragma unroll
+        for (int r = r0; r < r0 + 8; r++) if (t + 256 * r < T) pb[t + 256 * r] = sv[r] * inv * vs[r];
+    }
     for (int i = T + t; i < 16 * (nt + 2); i += 256) pb[i] = 0.0f;
     __syncthreads();
     if (t >= hd) return;
