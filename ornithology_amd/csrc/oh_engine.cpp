@@ -377,7 +377,9 @@ void mv_plan(MvBuild &b, int waves, int small_waves) {
             s.upw = 1;
             // IQ2_XXS fallback rows: the split form when the inputs are wide
             // and one lane per row would leave most of the GPU idle
-            s.iq2split = s.type == OH_IQ2_XXS && s.in >= 2048 &&
+            // (its scale table in LDS takes an even number of super-blocks
+            // per row, at most 32)
+            s.iq2split = s.type == OH_IQ2_XXS && s.in >= 2048 && s.in <= 8192 && (s.in / 256) % 2 == 0 &&
                          (int64_t)(s.rows + OH_IQ2_ROWS_LANE - 1) / OH_IQ2_ROWS_LANE * s.nsub < 256;
             const int rpb = s.type != OH_IQ2_XXS ? 256 : s.iq2split ? OH_IQ2_ROWS : OH_IQ2_ROWS_LANE;
             s.bps = (s.rows + rpb - 1) / rpb;
@@ -387,9 +389,12 @@ void mv_plan(MvBuild &b, int waves, int small_waves) {
         const int nb = s.in / 256;
         const int voff = (nb * 272 + nb * 36 + 15) & ~15;
         int need = voff + ((!q8 || s.pro != OH_PRO_Q8K) ? s.in * 4 : 0) + (s.pro == OH_PRO_GNORM ? 512 : 0);
-        // + the grid (and the split form's two [OH_IQ2_ROWS][96 + 4] term tiles)
+        // + the grid, then the split form's two [OH_IQ2_ROWS][96 + 4] term
+        // tiles and its [OH_IQ2_ROWS][nb] half scales (its sign masks sit in
+        // the Q8_K planes' place), or the lane form's 2 KB of sign masks
         if (!q8 && s.type == OH_IQ2_XXS)
-            need = ((voff + s.in * 4 + 15) & ~15) + 2048 + (s.iq2split ? 2 * OH_IQ2_ROWS * 100 * 4 : 0);
+            need = ((voff + s.in * 4 + 15) & ~15) + 2048 +
+                   (s.iq2split ? 2 * OH_IQ2_ROWS * 100 * 4 + OH_IQ2_ROWS * nb * 2 : 2048);
         if (s.iq2tree) need = 0;                    // x in registers, the tables in static LDS
         if (need > b.lds) b.lds = need;
     }

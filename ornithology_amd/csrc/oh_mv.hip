@@ -427,54 +427,90 @@ OH_HD inline int mv_lds_v_off(int nb) { return (nb * kAS + nb * 36 + 15) & ~15; 
 // sub-block (two code words and d) is in flight while it forms the current.
 constexpr int kIq2P = 3, kIq2E = 32 * kIq2P, kIq2S = kIq2E + 4;   // producers, terms per chunk, tile row stride
 constexpr int kIq2D = 6;                                            // chunks of codes in flight per producer
+static_assert(kIq2S == 100, "the host's LDS plan takes term-tile rows of 100 floats");
 OH_HD inline int mv_lds_iq2_off(int nb, int in) { return (mv_lds_v_off(nb) + in * 4 + 15) & ~15; }
 OH_HD inline int mv_lds_iq2t_off(int nb, int in) { return mv_lds_iq2_off(nb, in) + 2048; }
+// the split form's scales d: [OH_IQ2_ROWS][nb] halves after the two term tiles
+OH_HD inline int mv_lds_iq2d_off(int nb, int in) { return mv_lds_iq2t_off(nb, in) + 2 * OH_IQ2_ROWS * kIq2S * 4; }
+
+// The 128 sign patterns of IQ2_XXS as byte masks (the eighth sign is the
+// parity of the seven stored ones): entry s7 = {m_lo, m_hi, m_lo & 0x01..,
+// m_hi & 0x01..}, m byte j = 0xff where sign j is negative, so that
+// (g ^ m) + (m & 0x01..) negates exactly those bytes of a grid entry g.
+OH_DEV void iq2_sign_table(uint4 *stab) {
+    const int tid = tid_x();
+    if (tid < 128) {
+        const uint32_t sg = (uint32_t)tid | ((__popc((uint32_t)tid) & 1u) << 7);
+        uint32_t m0 = 0, m1 = 0;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            m0 |= ((sg >> j) & 1u) * (0xffu << (8 * j));
+            m1 |= ((sg >> (j + 4)) & 1u) * (0xffu << (8 * j));
+        }
+        stab[tid] = make_uint4(m0, m1, m0 & 0x01010101u, m1 & 0x01010101u);
+    }
+}
+// Eight terms of one codebook entry: (db * +-g_j) * x_j, the grid bytes of
+// entry gv carrying their signs (sm: the entry's sign masks); (db * -g) * x
+// is -((db * g) * x) exactly.
+OH_DEV void iq2_terms8(uint64_t gv, const uint4 sm, float db, const float4 x0, const float4 x1, float (&ts)[8]) {
+    const uint32_t gs[2] = {((uint32_t)gv ^ sm.x) + sm.z, ((uint32_t)(gv >> 32) ^ sm.y) + sm.w};
+    const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+    for (int j = 0; j < 8; j++) ts[j] = db * (float)(int8_t)(gs[j / 4] >> (8 * (j % 4))) * xs[j];
+}
 
 OH_DEV void iq2_rows_lane(const oh_mvseg &s, int slot, int blk, int expert, uint8_t *smem) {
     const int in = s.in, nb = in / 256, tid = tid_x();
     const float *v = (const float *)(smem + mv_lds_v_off(nb));
     uint64_t *grid = (uint64_t *)(smem + mv_lds_iq2_off(nb, in));
+    uint4 *stab = (uint4 *)(smem + mv_lds_iq2t_off(nb, in));      // the sign masks, after the grid
     const int row = blk * OH_IQ2_ROWS_LANE + tid;
     const int64_t bi0 = ((int64_t)expert * s.rows + (row < s.rows ? row : s.rows - 1)) * nb;
-    uint4 qa[4], qn[4];
-    uint16_t da, dn;
-    auto fetch = [&](uint4 *q, uint16_t &d, int b) {
+    // two super-blocks' codes and d, used in turn: a slot is refilled only
+    // after its super-block was reduced, so the load lands in the slot's own
+    // registers (a copy between slots would wait for the load in flight)
+    uint4 qa[4], qb[4];
+    uint32_t da, dbb;
+    auto fetch = [&](uint4 (&q)[4], uint32_t &d, int b) {
         const int bc = b < nb ? b : nb - 1;
         const uint4 *src = (const uint4 *)(s.A + (bi0 + bc) * 64);
 #pragma unroll
         for (int k = 0; k < 4; k++) q[k] = ldg(src + k);
         d = ldg((const uint16_t *)(s.C + (bi0 + bc) * 2));
     };
+    const uint64_t g = k_iq2_grid[tid];
     fetch(qa, da, 0);
-    grid[tid] = k_iq2_grid[tid];
+    grid[tid] = g;
+    iq2_sign_table(stab);
     lds_barrier();
     float acc = 0.0f;
-    for (int b = 0; b < nb; b++) {
-        fetch(qn, dn, b + 1);
-        const float dd = h2f(da);
+    // super-block b: each term added at once, in element order
+    auto reduce = [&](int b, const uint4 (&q)[4], uint32_t d) {
+        const float dd = h2f((uint16_t)d);
         const float4 *xb = (const float4 *)(v + b * 256);
 #pragma unroll
         for (int g32 = 0; g32 < 8; g32++) {
-            const uint32_t w0 = wsel(qa[g32 >> 1], 2 * (g32 & 1)), w1 = wsel(qa[g32 >> 1], 2 * (g32 & 1) + 1);
+            const uint32_t w0 = wsel(q[g32 >> 1], 2 * (g32 & 1)), w1 = wsel(q[g32 >> 1], 2 * (g32 & 1) + 1);
             const float db = dd * (0.5f + (float)(w1 >> 28)) * 0.25f;
 #pragma unroll
             for (int k = 0; k < 4; k++) {
-                const uint64_t gv = grid[(w0 >> (8 * k)) & 0xffu];
-                const uint32_t s7 = (w1 >> (7 * k)) & 127u;
-                const uint32_t sg = s7 | ((__popc(s7) & 1u) << 7);
-                const float4 x0 = xb[g32 * 8 + 2 * k], x1 = xb[g32 * 8 + 2 * k + 1];
-                const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+                float ts[8];
+                iq2_terms8(grid[(w0 >> (8 * k)) & 0xffu], stab[(w1 >> (7 * k)) & 127u], db,
+                           xb[g32 * 8 + 2 * k], xb[g32 * 8 + 2 * k + 1], ts);
 #pragma unroll
-                for (int j = 0; j < 8; j++) {
-                    const float t = db * (float)((uint32_t)(gv >> (8 * j)) & 0xffu) * xs[j];
-                    acc += (sg >> j) & 1u ? -t : t;
-                }
+                for (int j = 0; j < 8; j++) acc += ts[j];
             }
         }
-#pragma unroll
-        for (int k = 0; k < 4; k++) qa[k] = qn[k];
-        da = dn;
+    };
+    int b = 0;
+    for (; b + 2 <= nb; b += 2) {
+        fetch(qb, dbb, b + 1);
+        reduce(b, qa, da);
+        fetch(qa, da, b + 2);
+        reduce(b + 1, qb, dbb);
     }
+    if (b < nb) reduce(b, qa, da);
     if (row < s.rows) emit(s.y + (size_t)slot * s.ystride, s.mode, row, acc);
 }
 
@@ -486,54 +522,65 @@ OH_DEV void iq2_rows(const oh_mvseg &s, int slot, int blk, int expert, uint8_t *
     const int row = blk * OH_IQ2_ROWS + lane;
     const int64_t bi0 = ((int64_t)expert * s.rows + (row < s.rows ? row : s.rows - 1)) * nb;
     const int nch = (nsb + kIq2P - 1) / kIq2P;
-    // a producer's code words and d for its next kIq2D chunks (a chunk's
-    // terms take well under one memory round trip)
-    uint2 wq[kIq2D];
-    uint16_t dq[kIq2D];
-    auto fetch = [&](int c, uint2 &w, uint16_t &d) {   // producer wave - 1: sub-block c * kIq2P + wave - 1
-        const int sb = c * kIq2P + wave - 1, sbc = sb < nsb ? sb : nsb - 1;
-        w = ldg((const uint2 *)(s.A + (bi0 + sbc / 8) * 64 + (sbc % 8) * 8));
-        d = ldg((const uint16_t *)(s.C + (bi0 + sbc / 8) * 2));
-    };
-    if (wave > 0) {
+    // the super-block scales d of the block's rows, [OH_IQ2_ROWS][nb] halves
+    // in LDS (64 * nb * 2 contiguous bytes of the C plane; nb is even)
+    uint32_t *dl = (uint32_t *)(smem + mv_lds_iq2d_off(nb, in));
+    const int nh = nb / 2;
+    uint32_t dv[OH_IQ2_ROWS * 32 / 2 / 256];        // up to nb = 32
+    const uint32_t *dsrc = (const uint32_t *)s.C;
 #pragma unroll
-        for (int i = 0; i < kIq2D; i++) fetch(i < nch ? i : nch - 1, wq[i], dq[i]);
+    for (int u = 0; u < OH_IQ2_ROWS * 32 / 2 / 256; u++) {
+        const int i = tid + 256 * u, r = i / nh, rr = blk * OH_IQ2_ROWS + r;
+        if (i < OH_IQ2_ROWS * nh)
+            dv[u] = ldg(dsrc + ((int64_t)expert * s.rows + (rr < s.rows ? rr : s.rows - 1)) * nh + (i - r * nh));
     }
-    grid[tid] = k_iq2_grid[tid];
+    // a producer's code words for its next kIq2D chunks (a chunk's terms
+    // take well under one memory round trip). Every wave issues the same
+    // loads (the adding wave those of producer 0, the same lines) so that
+    // each wave's wait for a slot leaves the later slots in flight.
+    uint2 wq[kIq2D];
+    const int pw = wave > 0 ? wave - 1 : 0;          // producer index: sub-block pw of each chunk
+    auto fetch = [&](int c, uint2 &w) {
+        const int sb = c * kIq2P + pw, sbc = sb < nsb ? sb : nsb - 1;
+        w = ldg((const uint2 *)(s.A + (bi0 + sbc / 8) * 64 + (sbc % 8) * 8));
+    };
+    const uint64_t g = k_iq2_grid[tid];            // requested before the codes: its wait leaves them in flight
+    // the sign masks in LDS below the f32 activation (the Q8_K planes'
+    // place, which this form does not use: at least 2464 bytes for inputs of
+    // 2048 and more)
+    uint4 *stab = (uint4 *)smem;
+    iq2_sign_table(stab);
+#pragma unroll
+    for (int i = 0; i + 1 < kIq2D; i++) fetch(i < nch ? i : nch - 1, wq[i]);
+    grid[tid] = g;
+#pragma unroll
+    for (int u = 0; u < OH_IQ2_ROWS * 32 / 2 / 256; u++)
+        if (tid + 256 * u < OH_IQ2_ROWS * nh) dl[tid + 256 * u] = dv[u];
     lds_barrier();
+    const uint16_t *dh = (const uint16_t *)dl + lane * nb;
     float acc = 0.0f;
-    for (int c = 0; c <= nch; c++) {
-        if (wave > 0 && c < nch) {
+    // chunk c: every wave refills the slot that chunk c - 1 emptied (wn)
+    // with chunk c + kIq2D - 1 and takes its own slot's words (wr); the
+    // producers form chunk c from them, the adding wave adds chunk c - 1. A
+    // slot is refilled only after its words were taken, so the refill lands
+    // in the slot's own registers (no copy, which would wait for every load
+    // in flight).
+    auto chunk = [&](auto inner, int c, uint2 &wr, uint2 &wn) {
+        fetch(c + kIq2D - 1 < nch ? c + kIq2D - 1 : nch - 1, wn);
+        const uint32_t w0 = wr.x, w1 = wr.y;
+        if (wave > 0 && (decltype(inner)::value || c < nch)) {
             // terms of sub-block sb into tile c & 1, columns (wave - 1) * 32 ..
             const int sb = c * kIq2P + wave - 1;
-            const uint2 w = wq[0];
-            const uint16_t d16 = dq[0];
-#pragma unroll
-            for (int i = 0; i + 1 < kIq2D; i++) {
-                wq[i] = wq[i + 1];
-                dq[i] = dq[i + 1];
-            }
-            const int cn = c + kIq2D < nch ? c + kIq2D : nch - 1;
-            fetch(cn, wq[kIq2D - 1], dq[kIq2D - 1]);
             if (sb < nsb) {
-                const float dd = h2f(d16);
-                const uint32_t w0 = w.x, w1 = w.y;
+                const float dd = h2f(dh[sb / 8]);
                 const float db = dd * (0.5f + (float)(w1 >> 28)) * 0.25f;
                 const float4 *xb = (const float4 *)(v + sb * 32);
                 float *dst = tile + ((c & 1) * OH_IQ2_ROWS + lane) * kIq2S + (wave - 1) * 32;
 #pragma unroll
                 for (int k = 0; k < 4; k++) {
-                    const uint64_t gv = grid[(w0 >> (8 * k)) & 0xffu];
-                    const uint32_t s7 = (w1 >> (7 * k)) & 127u;
-                    const uint32_t sg = s7 | ((__popc(s7) & 1u) << 7);
-                    const float4 x0 = xb[2 * k], x1 = xb[2 * k + 1];
-                    const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
                     float ts[8];
-#pragma unroll
-                    for (int j = 0; j < 8; j++) {
-                        const float t = db * (float)((uint32_t)(gv >> (8 * j)) & 0xffu) * xs[j];
-                        ts[j] = (sg >> j) & 1u ? -t : t;
-                    }
+                    iq2_terms8(grid[(w0 >> (8 * k)) & 0xffu], stab[(w1 >> (7 * k)) & 127u], db, xb[2 * k],
+                               xb[2 * k + 1], ts);
                     *(float4 *)(dst + 8 * k) = make_float4(ts[0], ts[1], ts[2], ts[3]);
                     *(float4 *)(dst + 8 * k + 4) = make_float4(ts[4], ts[5], ts[6], ts[7]);
                 }
@@ -543,15 +590,45 @@ OH_DEV void iq2_rows(const oh_mvseg &s, int slot, int blk, int expert, uint8_t *
             // the previous chunk's terms of this lane's row, in element order
             const int e0 = (c - 1) * kIq2E, ne = in - e0 < kIq2E ? in - e0 : kIq2E;
             const float *src = tile + (((c - 1) & 1) * OH_IQ2_ROWS + lane) * kIq2S;
-            for (int e = 0; e < ne; e += 4) {
-                const float4 q = *(const float4 *)(src + e);
-                acc += q.x;
-                acc += q.y;
-                acc += q.z;
-                acc += q.w;
+            if (ne == kIq2E) {
+                // every read of the chunk issued before the first add: the
+                // adds then wait on no LDS round trip
+                float4 q[kIq2E / 4];
+#pragma unroll
+                for (int i = 0; i < kIq2E / 4; i++) q[i] = *(const float4 *)(src + 4 * i);
+#pragma unroll
+                for (int i = 0; i < kIq2E / 4; i++) {
+                    acc += q[i].x;
+                    acc += q[i].y;
+                    acc += q[i].z;
+                    acc += q[i].w;
+                }
+            } else {
+                for (int e = 0; e < ne; e += 4) {
+                    const float4 q = *(const float4 *)(src + e);
+                    acc += q.x;
+                    acc += q.y;
+                    acc += q.z;
+                    acc += q.w;
+                }
             }
         }
         lds_barrier();                              // the producers' next codes stay in flight
+    };
+    // the ring indexed statically, and whole groups of kIq2D chunks before
+    // c = nch without any test between them (a register shift of the slots,
+    // or a chunk that may be skipped, makes each use wait for every load in
+    // flight)
+    int c0 = 0;
+    for (; c0 + kIq2D <= nch; c0 += kIq2D) {
+#pragma unroll
+        for (int r = 0; r < kIq2D; r++) {
+            chunk(std::true_type(), c0 + r, wq[r], wq[(r + kIq2D - 1) % kIq2D]);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < kIq2D; r++) {
+        if (c0 + r <= nch) chunk(std::false_type(), c0 + r, wq[r], wq[(r + kIq2D - 1) % kIq2D]);
     }
     if (wave == 0 && row < s.rows) emit(s.y + (size_t)slot * s.ystride, s.mode, row, acc);
 }
