@@ -399,10 +399,27 @@ void mv_plan(MvBuild &b, int waves, int small_waves) {
         if (need > b.lds) b.lds = need;
     }
     if (b.L.rtag) {
-        // the fused router's copy of the logits for the sequential selection,
-        // past every segment's activation
-        b.L.rlg = (b.lds + 15) & ~15;
-        b.lds = b.L.rlg + ((b.L.ne + 3) & ~3) * 4;
+        // the fused router's copy of the logits for the sequential selection:
+        // past every segment's activation, or, when the routed segments are
+        // IQ2_XXS fallback rows (of one width), in their term tiles / sign
+        // masks, which are written only once the routing is done (the
+        // launch's LDS, two blocks per CU, does not grow)
+        int iq2 = -1;
+        bool other = false;
+        for (int i = 0; i < b.L.n; i++) {
+            const oh_mvseg &g = b.L.s[i];
+            if (!g.eidx) continue;
+            const int gnb = g.in / 256, gv = (gnb * 272 + gnb * 36 + 15) & ~15;
+            const int off = ((gv + g.in * 4 + 15) & ~15) + 2048;
+            if (g.type == OH_IQ2_XXS && !g.iq2tree && (iq2 < 0 || iq2 == off)) iq2 = off;
+            else other = true;
+        }
+        if (iq2 >= 0 && !other && b.L.ne <= 512) {
+            b.L.rlg = iq2;
+        } else {
+            b.L.rlg = (b.lds + 15) & ~15;
+            b.lds = b.L.rlg + ((b.L.ne + 3) & ~3) * 4;
+        }
     } else if (b.L.route && ((b.L.ne + 3) & ~3) * 4 > b.lds) {
         b.lds = ((b.L.ne + 3) & ~3) * 4;
     }

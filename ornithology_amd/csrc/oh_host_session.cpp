@@ -306,8 +306,16 @@ int build_body(ornith_hip_session *s, Prog &P) {
                             K <= 64 && H <= 4096 && oh_qdot_can(y.router->type, H) &&
                             (!y.gate_inp_sh || oh_qdot_can(y.gate_inp_sh->type, H)) &&
                             oh_qdot_can(y.gate_exps->type, H) && (!y.gate_sh || oh_qdot_can(y.gate_sh->type, H));
+            // the same with IQ2_XXS routed experts (their fallback rows, gate
+            // and up as separate segments): each expert block forms the
+            // normalised f32 activation, then routes from the tagged logits
+            const bool fr2 = !fr && !P.step && s->rtag && router_fused() && (a.ne == 256 || a.ne == 512) &&
+                             K <= 64 && H <= 4096 && oh_qdot_can(y.router->type, H) &&
+                             (!y.gate_inp_sh || oh_qdot_can(y.gate_inp_sh->type, H)) &&
+                             y.gate_exps->type == OH_IQ2_XXS && y.up_exps->type == OH_IQ2_XXS && !iq2_tree_on() &&
+                             (!y.gate_sh || (oh_qdot_can(y.gate_sh->type, H) && oh_qdot_can(y.up_sh->type, H)));
             MvBuild b2;
-            if (fr) {
+            if (fr || fr2) {
                 uint64_t *rt = s->rtag + (size_t)l * (a.ne + 1);
                 CHK(mv_add(b2, y.router, pn, (float *)rt, 2));
                 b2.L.s[b2.L.n - 1].tagp = s->io + OH_IO_SERIAL;
@@ -315,8 +323,20 @@ int build_body(ornith_hip_session *s, Prog &P) {
                     CHK(mv_add(b2, y.gate_inp_sh, pn, (float *)(rt + a.ne), 2));
                     b2.L.s[b2.L.n - 1].tagp = s->io + OH_IO_SERIAL;
                 }
-                CHK(mv_add_pair(b2, y.gate_exps, y.up_exps, pn, s->h, s->eidx, K, IW));
-                if (y.gate_sh) CHK(mv_add_pair(b2, y.gate_sh, y.up_sh, pn, s->h + (size_t)K * IW));
+                if (fr) {
+                    CHK(mv_add_pair(b2, y.gate_exps, y.up_exps, pn, s->h, s->eidx, K, IW));
+                    if (y.gate_sh) CHK(mv_add_pair(b2, y.gate_sh, y.up_sh, pn, s->h + (size_t)K * IW));
+                } else {
+                    // the layout of the unfused launch: g and u, the shared
+                    // expert's after the K routed slots (the down projection
+                    // forms silu(g) * u)
+                    CHK(mv_add(b2, y.gate_exps, pn, s->g, 0, s->eidx, K, IW, 0));
+                    CHK(mv_add(b2, y.up_exps, pn, s->u, 0, s->eidx, K, IW, 0));
+                    if (y.gate_sh) {
+                        CHK(mv_add(b2, y.gate_sh, pn, s->g + (size_t)K * IW, 0));
+                        CHK(mv_add(b2, y.up_sh, pn, s->u + (size_t)K * IW, 0));
+                    }
+                }
                 b2.L.rtag = rt;
                 b2.L.rio = s->io;
                 b2.L.rsh = y.gate_inp_sh ? 1 : 0;
@@ -361,7 +381,7 @@ int build_body(ornith_hip_session *s, Prog &P) {
             const bool fuse = paired && oh_qdot_can(dt, I) && nbd >= 1 && nbd <= 64 && ns <= 10 && dlds <= 65536 &&
                               (!P.step || I <= 1024) &&
                               (!y.gate_sh || (y.down_sh->type == dt && sI == I));
-            if (fr) {
+            if (fr || fr2) {
                 // the router blocks' completion counter and the first gate/up
                 // block (which clears the other parity's counter)
                 b2.L.mctr = s->mctr + (size_t)l * 2;
@@ -370,7 +390,7 @@ int build_body(ornith_hip_session *s, Prog &P) {
                 for (int i = 0; i < b2.L.n; i++) {
                     const oh_mvseg &g = b2.L.s[i];
                     if (g.mode == 2) b2.L.nrb += g.bps * g.nsub;
-                    if (g.pair && b2.L.pb0 < 0) b2.L.pb0 = g.block0;
+                    if ((fr ? g.pair != 0 : g.eidx != nullptr) && b2.L.pb0 < 0) b2.L.pb0 = g.block0;
                 }
                 oh_op o = op_new(OH_OP_MV, b2.L.total_blocks, b2.lds);
                 o.tk = b2.tk;

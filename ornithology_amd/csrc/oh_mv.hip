@@ -1492,6 +1492,19 @@ OH_DEV void mv_body(const oh_mvlaunch &L, int vb, W &w) {
         // expert's weights; the router, shared-gate and shared-expert
         // segments need no routing
         if (s.eidx) {
+            if constexpr (TK == -1) {
+                if (s.type == OH_IQ2_XXS && !s.iq2tree) {
+                    // IQ2_XXS fallback rows: the normalised f32 activation
+                    // first (while the router blocks run), then the routing,
+                    // then the routed expert's rows
+                    mv_prologue<W::kGrid>(s, slot, blk, smem, red, false);
+                    route_fused(L, slot == 0 && blk == 0, (float *)(smem + L.rlg), rsel, rwt, &rshg, &rbad);
+                    if (s.iq2split) iq2_rows(s, slot, blk, rsel[slot], smem);
+                    else iq2_rows_lane(s, slot, blk, rsel[slot], smem);
+                    if (L.mctr && vb == L.pb0) fused_count(L, vb, false);
+                    return;
+                }
+            }
             auto route = [&]() -> int {
                 route_fused(L, slot == 0 && blk == 0, (float *)(smem + L.rlg), rsel, rwt, &rshg, &rbad);
                 return rsel[slot];
@@ -1544,6 +1557,8 @@ OH_DEV void mv_body(const oh_mvlaunch &L, int vb, W &w) {
         case OH_Q6_K: mv_seg<OH_Q6_K>(s, slot, blk, expert, smem, red, w); break;
         default: mv_seg<OH_Q8_0>(s, slot, blk, expert, smem, red, w); break;
         }
+        // the router segments of a fused-router launch count themselves
+        if (L.mctr && (s.mode == 2 || vb == L.pb0)) fused_count(L, vb, s.mode == 2);
     } else {
         if (!w.wait()) return;
         mv_prologue<W::kGrid>(s, slot, blk, smem, red, false);
