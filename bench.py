@@ -345,8 +345,9 @@ def batch_decode(model: oa.Model, n: int, ctx_len: int, steps: int) -> dict:
 # profile kind -> kernel symbol (as rocprofv3 names it)
 KERNEL_SYMBOL = {"matvec": "oh_k_mv_q4k", "matvec_q6k": "oh_k_mv_q6k", "matvec_q80": "oh_k_mv_q80",
                  "matvec_mixed": "oh_k_mv_mixed", "matvec_q4q6": "oh_k_mv_q4k6k", "moe_down": "oh_k_mv_down_narrow",
-                 "delta_step": "oh_k_delta16", "attn_main": "oh_k_attn_main", "attn_combine": "oh_k_attn_combine",
-                 "attn_prep": "oh_k_attn_prep", "attn_scores": "oh_k_attn_scores", "attn_walk": "oh_k_attn_walk",
+                 "delta_step": "oh_k_delta16", "delta_mv": "oh_k_delta_mv", "attn_main": "oh_k_attn_main",
+                 "attn_combine": "oh_k_attn_combine", "attn_prep": "oh_k_attn_prep", "attn_scores": "oh_k_attn_scores",
+                 "attn_walk": "oh_k_attn_walk",
                  "step_body": "oh_k_step", "step_head": "oh_k_step"}
 
 
@@ -471,7 +472,7 @@ def timeline(args) -> int:
     prof = sess.profile_step()
     names = {"matvec": "Q4_K matvec", "matvec_mixed": "mixed matvec", "matvec_q6k": "Q6_K matvec",
              "matvec_q4q6": "Q4_K/Q6_K matvec", "attn_scores": "attn scores (exact)",
-             "attn_walk": "attn walk (exact)"}
+             "attn_walk": "attn walk (exact)", "delta_mv": "delta step + Q4_K matvec"}
     full = C3["full_interval"]
     # launch sequence per layer: every C3 layer ends with its MoE down
     # projection (launch 0 is the embedding, the head's launches come last)

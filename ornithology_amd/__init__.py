@@ -373,7 +373,7 @@ class Session:
     KERNEL_KINDS = ("matvec", "rmsnorm_q8k", "swiglu_q8k", "embed", "delta_step", "attn_prep",
                     "attn_scores", "attn_walk", "moe_route", "moe_combine", "argmax", "advance",
                     "moe_down", "attn_flash", "attn_combine", "matvec_q6k", "matvec_q80", "matvec_mixed",
-                    "step_body", "step_head", "attn_main", "matvec_q4q6")
+                    "step_body", "step_head", "attn_main", "matvec_q4q6", "delta_mv")
 
     def time_kind(self, kind: str, reps: int = 5):
         """Back-to-back replay of one step's launches of `kind`: returns

@@ -180,6 +180,7 @@ struct ornith_hip_session {
     double *oruns = nullptr;      // delta step: sum of o^2 per 16-row run (per 64 rows: the step kernel)
     uint64_t *rtag = nullptr;     // MoE layers: router logits as tagged words [n_layers][ne + 1] (fused router)
     int32_t *mctr = nullptr;      // MoE layers: router completion counters of the fused MoE launch [n_layers][2]
+    int32_t *dmctr = nullptr;     // delta-net layers: arrival and departure counters of the delta-step launch [n_layers][2]
     // decode contexts up to this (at most the walk's cap for the head dim:
     // 8192 positions at hd 256) take the attention sum in the reference's
     // order; longer ones the flash chunks
@@ -266,7 +267,8 @@ struct ornith_hip_session {
 
 enum { K_MATVEC = 0, K_NORM_Q8K, K_SWIGLU_Q8K, K_EMBED, K_DELTA, K_ATTN_PREP, K_ATTN_SCORES,
        K_ATTN_WALK, K_ROUTE, K_COMBINE, K_ARGMAX, K_ADVANCE, K_MV_DOWN, K_ATTN_FLASH, K_ATTN_COMBINE,
-       K_MATVEC_Q6K, K_MATVEC_Q80, K_MATVEC_MIXED, K_STEP_BODY, K_STEP_HEAD, K_ATTN_MAIN, K_MATVEC_Q4Q6 };
+       K_MATVEC_Q6K, K_MATVEC_Q80, K_MATVEC_MIXED, K_STEP_BODY, K_STEP_HEAD, K_ATTN_MAIN, K_MATVEC_Q4Q6,
+       K_DELTA_MV };
 
 // ---- the token step as a program of operations ----------------------------------------------
 // The same list of operations runs either launch by launch (captured into HIP
@@ -407,6 +409,7 @@ bool body_exact(const ornith_hip_session *s);
 bool attn_mfma_enabled();
 bool batch_fused();
 bool router_fused();
+bool delta_fused();
 bool delta_mfma_enabled();
 int pf_chunk_tokens();
 bool pf_mvb_ok(const ornith_hip_tensor *W);

@@ -132,6 +132,7 @@ extern "C" int ornith_hip_session_new(ornith_hip_model *m, int cap, ornith_hip_s
     if (a.ne > 0) {
         A_(salloc(s, &s->rtag, (size_t)a.n_layers * (a.ne + 1)));
         A_(salloc(s, &s->mctr, (size_t)a.n_layers * 2));
+        A_(salloc(s, &s->dmctr, (size_t)a.n_layers * 2));
     }
     {
         const char *e = getenv("ORNITH_HIP_EXACT_ATTN_MAX");
@@ -284,12 +285,36 @@ int build_body(ornith_hip_session *s, Prog &P) {
             o.u.delta = {s->cat, s->ab, s->gate, (const float *)y.conv->A, (const float *)y.ssm_a->A,
                          (const float *)y.dt_bias->A, z.conv, z.S, s->o, s->osz, s->oruns,
                          a.dk, a.nk, a.nv, a.conv_k, cc, out_scale};
-            prog_add(P, o, K_DELTA, sb);
             // per-head gated RMSNorm of the delta output inside the projection
             MvBuild b2;
             CHK(mv_add(b2, y.ssm_out,
                        act_gnorm(s->o, s->osz, s->oruns, (const float *)y.ssm_norm->A, a.eps, a.dv, 1), s->x, 1));
-            prog_mv(P, b2);
+            if (!P.step && delta_fused() && a.dk == 128 && a.conv_k <= 8 && s->dmctr &&
+                (y.ssm_out->type == OH_Q4_K || y.ssm_out->type == OH_Q6_K)) {
+                // one launch: the delta step's blocks, then the projection's
+                // blocks (first weights requested, then the arrival wait)
+                mv_plan(b2, P.waves, 1024);
+                if (b2.tk == (int)y.ssm_out->type && b2.lds <= 65536) {
+                    oh_op f = op_new(OH_OP_DELTA_MV, o.nvb + b2.L.total_blocks, b2.lds);
+                    f.tk = b2.tk;
+                    f.u.dmv.mv = b2.L;
+                    f.u.dmv.mv.rio = s->io;
+                    f.u.dmv.d = o.u.delta;
+                    f.u.dmv.arr = s->dmctr + (size_t)l * 2;
+                    f.u.dmv.dep = s->dmctr + (size_t)l * 2 + 1;
+                    f.u.dmv.nd = o.nvb;
+                    prog_add(P, f, K_DELTA_MV, sb + b2.bytes);
+                } else {
+                    prog_add(P, o, K_DELTA, sb);
+                    oh_op m = op_new(OH_OP_MV, b2.L.total_blocks, b2.lds);
+                    m.tk = b2.tk;
+                    m.u.mv = b2.L;
+                    prog_add(P, m, mv_kind(b2.tk), b2.bytes);
+                }
+            } else {
+                prog_add(P, o, K_DELTA, sb);
+                prog_mv(P, b2);
+            }
         }
         // FFN: post_attention_norm (formed inside the first FFN launch), then
         // MoE (or dense SwiGLU)

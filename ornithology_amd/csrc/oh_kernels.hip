@@ -12,7 +12,43 @@
 #include "oh_delta_mfma.hip"
 #include "oh_launch.h"
 
+// The graph step's delta step and the projection of its output in one launch
+// (oh_op_dmv): workgroups [0, nd) run the delta step and count their
+// arrival once their outputs (device-scope stores) are complete; the others
+// are the projection's matvec workgroups behind the arrival wait.
+template <int DK, int KMAX, int TK>
+__global__ void __launch_bounds__(256) oh_k_delta_mv(oh_op_dmv a, const int32_t *io) {
+    const int vb = (int)blockIdx.x;
+    if (vb < a.nd) {
+        __shared__ __align__(16) float lds[delta16_lds_floats(DK)];
+        NoWait w;
+        delta16_body<DK, KMAX>(a.d, vb, io[OH_IO_POS], lds, w);
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (tid_x() == 0) __hip_atomic_fetch_add(a.arr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
+    CtrWait w{a.arr, a.dep, a.nd, a.mv.total_blocks, a.mv.rio + OH_IO_ERR, false, true};
+    mv_body<TK>(a.mv, vb - a.nd, w);
+}
+
 extern "C" {
+
+// delta step + projection: head dim 128, conv kernels up to 8, a Q4_K or
+// Q6_K projection (the host builds the fused op only for these)
+hipError_t oh_launch_delta_mv(const oh_op_dmv *a, int tk, int lds_bytes, const int32_t *io, hipStream_t st) {
+    if (a->d.dk != 128 || a->d.K > 8 || (tk != OH_Q4_K && tk != OH_Q6_K) || a->mv.rio == nullptr || lds_bytes > 65536)
+        return hipErrorInvalidValue;
+    const dim3 g(a->nd + a->mv.total_blocks), b(256);
+    if (tk == OH_Q4_K) {
+        if (a->d.K <= 4) hipLaunchKernelGGL((oh_k_delta_mv<128, 4, OH_Q4_K>), g, b, (size_t)lds_bytes, st, *a, io);
+        else hipLaunchKernelGGL((oh_k_delta_mv<128, 8, OH_Q4_K>), g, b, (size_t)lds_bytes, st, *a, io);
+    } else {
+        if (a->d.K <= 4) hipLaunchKernelGGL((oh_k_delta_mv<128, 4, OH_Q6_K>), g, b, (size_t)lds_bytes, st, *a, io);
+        else hipLaunchKernelGGL((oh_k_delta_mv<128, 8, OH_Q6_K>), g, b, (size_t)lds_bytes, st, *a, io);
+    }
+    return hipGetLastError();
+}
 
 hipError_t oh_launch_matvec(const oh_mvlaunch *L, int tk, int lds_bytes, hipStream_t st) {
     if (L->total_blocks <= 0) return hipSuccess;
@@ -312,6 +348,8 @@ hipError_t oh_launch_op(const oh_op *op, const int32_t *io, hipStream_t st) {
     switch (op->kind) {
     case OH_OP_MV:
         return oh_launch_matvec(&op->u.mv, op->tk, op->lds, st);
+    case OH_OP_DELTA_MV:
+        return oh_launch_delta_mv(&op->u.dmv, op->tk, op->lds, io, st);
     case OH_OP_MV_DOWN: {
         const int ns = op->u.down.k + (op->u.down.sA ? 1 : 0);
         if (op->u.down.narrow) {

@@ -9,6 +9,7 @@ extern "C" {
 // tk: the integer-path type every segment has (OH_Q4_K/OH_Q6_K/OH_Q8_0), or -1
 // for a launch that mixes types or has fallback segments
 hipError_t oh_launch_matvec(const oh_mvlaunch *L, int tk, int lds_bytes, hipStream_t st);
+hipError_t oh_launch_delta_mv(const oh_op_dmv *a, int tk, int lds_bytes, const int32_t *io, hipStream_t st);
 // batched matvec (grid: row blocks x groups) and its LDS column tile
 hipError_t oh_launch_mvb(const oh_mvbatch *B, int groups, hipStream_t st);
 int oh_mvb_tcol(int nb);

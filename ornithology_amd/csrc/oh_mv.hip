@@ -1174,6 +1174,44 @@ OH_DEV bool wait_count(const int32_t *ctr, int n) {
     }
     return __builtin_amdgcn_readfirstlane(ok) != 0;
 }
+// The wait of a workgroup whose inputs other workgroups of the same launch
+// produce (the projection part of the delta-step launch): one thread polls
+// the arrival counter until it reaches n (bounded),
+// the block takes one decision, then counts its departure; the last of the
+// ndep departing workgroups sets both counters back to 0 (every producer has
+// arrived and every consumer has passed by then). A wait that gives up sets
+// the error flag. kGrid: the inputs are read with device-scope loads.
+struct CtrWait {
+    static constexpr bool kGrid = true;
+    int32_t *arr, *dep;
+    int n, ndep;
+    int32_t *err;
+    bool done, ok;
+    OH_DEV bool wait() {
+        if (done) return ok;
+        done = true;
+        __shared__ int s_ok;
+        if (tid_x() == 0) {
+            // polled about every 0.4 us: every projection block polls the
+            // one counter the delta blocks add to
+            bool got = true;
+            for (int it = 0; ldc(arr) < n; it++) {
+                if (it >= kRouteSpin / 4) { got = false; break; }
+                __builtin_amdgcn_s_sleep(16);
+            }
+            s_ok = got ? 1 : 0;
+            if (!got) atomicOr(err, OH_ERR_WAIT);
+            if (__hip_atomic_fetch_add(dep, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == ndep - 1) {
+                stc(arr, 0);
+                stc(dep, 0);
+            }
+        }
+        __syncthreads();
+        ok = s_ok != 0;
+        return ok;
+    }
+};
+
 template <int V>
 OH_DEV bool route_poll(const uint64_t *tw, uint32_t tag, bool has_sh, float (&a)[V], float *shl) {
     const int lane = lane_id(), ne = 64 * V;

@@ -219,6 +219,7 @@ enum {
     OH_OP_ARGMAX2,         // u.am
     OH_OP_ATTN_SCORES,     // u.attn: the exact walk's scores (the graph step's exact regime)
     OH_OP_ATTN_WALK,       // u.attn: the exact walk's softmax and output (the graph step's exact regime)
+    OH_OP_DELTA_MV,        // u.dmv: the delta step and the projection of its output in one launch
     OH_OP_COUNT
 };
 
@@ -277,6 +278,21 @@ typedef struct {
     int32_t *toks, *best;
 } oh_op_argmax;
 
+// The graph step's delta step and its output projection in one launch:
+// workgroups [0, nd) run the delta step (16 state rows each) and add 1 to
+// *arr once their outputs are stored; the projection's workgroups (the rest)
+// request their first weights, wait (bounded) until *arr reaches nd, add 1
+// to *dep, then form the gated RMSNorm of the delta output and reduce. The
+// last workgroup past the wait (*dep reaching the projection's workgroup
+// count) sets both counters back to 0, so every launch (replays for timing
+// included) starts from zero.
+typedef struct {
+    oh_mvlaunch mv;
+    oh_op_delta d;
+    int32_t *arr, *dep;
+    int nd;
+} oh_op_dmv;
+
 typedef struct {
     int kind, nvb;
     int tk;                // OH_OP_MV: OH_Q4_K / OH_Q6_K / OH_Q8_0, or -1 (mixed)
@@ -290,6 +306,7 @@ typedef struct {
         oh_op_attn attn;
         oh_op_combine comb;
         oh_op_argmax am;
+        oh_op_dmv dmv;
     } u;
 } oh_op;
 

@@ -364,3 +364,26 @@ def test_c2_iq2xxs_tree_matvec_within_tolerance(hip_ctx, monkeypatch, shape):
     r = rel_l2(y1, y0)
     print(f"[{n} x {out}] IQ2_XXS tree vs element order: rel L2 {r:.3e}")
     assert np.isfinite(y1).all() and r <= 1e-5
+
+
+@pytest.mark.timeout(300)
+def test_c3_width_slice_fused_delta_launch_bitexact(hip_ctx, monkeypatch):
+    """The opt-in one-launch delta step + output projection
+    (ORNITH_HIP_DELTA_FUSE=1: the projection's blocks wait in the launch for
+    the delta step's blocks) gives the bits of the two separate launches,
+    which the full-model tests pin to the oracle."""
+    monkeypatch.setenv("ORNITH_PREFILL_SERIAL", "0")
+    cfg = dict(C3, n_layers=4, seed=11)
+    m = hip_ctx.synth(**cfg)
+    prompt = clibs.ids(5, "c3f.prompt", 48, cfg["vocab"])
+    runs = {}
+    for fuse in ("0", "1"):
+        monkeypatch.setenv("ORNITH_HIP_DELTA_FUSE", fuse)
+        runs[fuse] = gpu_run(m, prompt, 24)
+    m.free()
+    (lp0, t0, lf0), (lp1, t1, lf1) = runs["0"], runs["1"]
+    print(f"[c3 fused delta] tokens equal {int((t0 == t1).sum())}/24, final logits identical "
+          f"{bool(np.array_equal(lf0, lf1))}")
+    assert np.array_equal(lp0, lp1)
+    assert np.array_equal(t0, t1)
+    assert np.array_equal(lf0, lf1)
