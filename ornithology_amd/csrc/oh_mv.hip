@@ -1329,7 +1329,13 @@ OH_DEV void route_fused(const oh_mvlaunch &L, bool store, float *lg, int *sel, f
     if (tid < 64) {
         const uint32_t ser = (uint32_t)ldc(L.rio + OH_IO_SERIAL), tag = ser + 1u;
         float shl = 0.0f;
-        bool got = wait_count(L.mctr + (ser & 1u), L.nrb);
+        bool got = wait_count(L.mctr, L.nrb);
+        // the departure; the last routed block resets the counters
+        if (tid == 0 &&
+            __hip_atomic_fetch_add(L.mctr + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == L.ncons - 1) {
+            stc(L.mctr, 0);
+            stc(L.mctr + 1, 0);
+        }
         int ok = 1;
         if (ne == 256) {
             float a[4];
@@ -1486,19 +1492,12 @@ OH_DEV void iq2_tree(const oh_mvseg &s, int slot, int blk, int expert, W &w) {
 // activation in LDS). With L.route every block first routes the MoE and
 // stacked segments take their experts from that routing. vb: the virtual
 // block (blockIdx.x of a standalone launch).
-// a router block of the fused MoE launch counts itself in this step's parity
-// once every wave's tagged stores have completed; the first gate/up block
-// clears the other parity's counter for the next step
-OH_DEV void fused_count(const oh_mvlaunch &L, int vb, bool router) {
+// a router block of the fused MoE launch counts its arrival once every
+// wave's tagged stores have completed
+OH_DEV void fused_count(const oh_mvlaunch &L) {
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    if (tid_x() == 0) {
-        const uint32_t ser = (uint32_t)ldc(L.rio + OH_IO_SERIAL);
-        if (router)
-            __hip_atomic_fetch_add(L.mctr + (ser & 1u), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        else if (vb == L.pb0)
-            stc(L.mctr + ((ser & 1u) ^ 1u), 0);
-    }
+    if (tid_x() == 0) __hip_atomic_fetch_add(L.mctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // The block's segment: every segment's first block is read at once (a
@@ -1539,7 +1538,6 @@ OH_DEV void mv_body(const oh_mvlaunch &L, int vb, W &w) {
                     route_fused(L, slot == 0 && blk == 0, (float *)(smem + L.rlg), rsel, rwt, &rshg, &rbad);
                     if (s.iq2split) iq2_rows(s, slot, blk, rsel[slot], smem);
                     else iq2_rows_lane(s, slot, blk, rsel[slot], smem);
-                    if (L.mctr && vb == L.pb0) fused_count(L, vb, false);
                     return;
                 }
             }
@@ -1558,7 +1556,6 @@ OH_DEV void mv_body(const oh_mvlaunch &L, int vb, W &w) {
                 else if (s.type == OH_Q8_0) mv_seg<OH_Q8_0>(s, slot, blk, 0, smem, red, w, late);
                 else mv_seg<OH_Q4_K>(s, slot, blk, 0, smem, red, w, late);
             }
-            if (L.mctr && vb == L.pb0) fused_count(L, vb, false);
             return;
         }
     } else if (L.route && L.tslots > 0) {
@@ -1577,11 +1574,11 @@ OH_DEV void mv_body(const oh_mvlaunch &L, int vb, W &w) {
     const int expert = !s.eidx ? 0 : (L.route ? rsel[L.tslots > 0 ? slot % L.tslots : slot] : ldw<W::kGrid>(s.eidx + slot));
     if constexpr (TK >= 0) {
         mv_seg<TK < 0 ? OH_Q4_K : TK>(s, slot, blk, expert, smem, red, w);
-        if (L.mctr && (s.mode == 2 || vb == L.pb0)) fused_count(L, vb, s.mode == 2);
+        if (L.mctr && s.mode == 2) fused_count(L);
     } else if constexpr (TK == OH_MV_Q4Q6) {
         if (s.type == OH_Q6_K) mv_seg<OH_Q6_K>(s, slot, blk, expert, smem, red, w);
         else mv_seg<OH_Q4_K>(s, slot, blk, expert, smem, red, w);
-        if (L.mctr && (s.mode == 2 || vb == L.pb0)) fused_count(L, vb, s.mode == 2);
+        if (L.mctr && s.mode == 2) fused_count(L);
     } else if (s.type == OH_IQ2_XXS && s.iq2tree) {
         switch (s.in / 64) {
         case 64: iq2_tree<64>(s, slot, blk, expert, w); break;
@@ -1596,7 +1593,7 @@ OH_DEV void mv_body(const oh_mvlaunch &L, int vb, W &w) {
         default: mv_seg<OH_Q8_0>(s, slot, blk, expert, smem, red, w); break;
         }
         // the router segments of a fused-router launch count themselves
-        if (L.mctr && (s.mode == 2 || vb == L.pb0)) fused_count(L, vb, s.mode == 2);
+        if (L.mctr && s.mode == 2) fused_count(L);
     } else {
         if (!w.wait()) return;
         mv_prologue<W::kGrid>(s, slot, blk, smem, red, false);

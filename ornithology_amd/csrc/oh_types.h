@@ -189,12 +189,13 @@ typedef struct {
     const uint64_t *rtag;
     int32_t *rio;
     int rsh, rlg;
-    // mctr[parity] (parity = the step serial's low bit) counts the router
-    // segments' blocks (nrb of them) whose tagged words are stored; a gate/up
-    // block polls it, then reads the words once. The first gate/up block
-    // (pb0) clears the other parity's counter for the next step.
+    // mctr[0] counts the router segments' blocks (nrb of them) whose tagged
+    // words are stored; a routed block (ncons of them: the blocks of the
+    // segments with eidx) polls it, then reads the words once, and counts
+    // itself in mctr[1]; the last routed block past the wait sets both back
+    // to 0, so every launch (replays for timing included) starts from zero.
     int32_t *mctr;
-    int nrb, pb0;
+    int nrb, ncons;
 } oh_mvlaunch;
 
 
