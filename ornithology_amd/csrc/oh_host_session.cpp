@@ -407,14 +407,15 @@ int build_body(ornith_hip_session *s, Prog &P) {
                               (!P.step || I <= 1024) &&
                               (!y.gate_sh || (y.down_sh->type == dt && sI == I));
             if (fr || fr2) {
-                // the router blocks' arrival counter and the routed blocks'
-                // departure counter (the last routed block resets both)
+                // the router blocks' completion counter and the first gate/up
+                // block (which clears the other parity's counter)
                 b2.L.mctr = s->mctr + (size_t)l * 2;
                 mv_plan(b2, P.waves, 1024);
+                b2.L.pb0 = -1;
                 for (int i = 0; i < b2.L.n; i++) {
                     const oh_mvseg &g = b2.L.s[i];
                     if (g.mode == 2) b2.L.nrb += g.bps * g.nsub;
-                    if (g.eidx) b2.L.ncons += g.bps * g.nsub;
+                    if ((fr ? g.pair != 0 : g.eidx != nullptr) && b2.L.pb0 < 0) b2.L.pb0 = g.block0;
                 }
                 oh_op o = op_new(OH_OP_MV, b2.L.total_blocks, b2.lds);
                 o.tk = b2.tk;

@@ -50,17 +50,28 @@ extern "C" int ornith_hip_session_time_kind(ornith_hip_session *s, int kind, int
     s->only = kind;
     s->only_n = 0;
     s->only_bytes = 0.0;
-    int r = enqueue_body(s, st);                   // warm-up pass: counts launches and bytes
+    // the fused MoE launch's router counters are cleared step by step by the
+    // launch itself, keyed on the step serial, which replays do not advance:
+    // zero them before every pass (eager, not captured) so that its routed
+    // blocks wait for the router blocks as in a decode step
+    const size_t mb = (size_t)s->m->a.n_layers * 2 * sizeof(int32_t);
+    hipError_t e = s->mctr ? hipMemsetAsync(s->mctr, 0, mb, st) : hipSuccess;
+    int r = e == hipSuccess ? enqueue_body(s, st) : ORNITH_HIP_ERR_DEVICE;   // warm-up pass: counts launches and bytes
     if (r == ORNITH_HIP_OK) r = enqueue_head(s, st);
     const int n = s->only_n;
     const double by = s->only_bytes;
-    hipError_t e = hipEventRecord(e0, st);
+    if (e == hipSuccess) e = hipEventRecord(e0, st);
     for (int i = 0; i < reps && r == ORNITH_HIP_OK && e == hipSuccess; i++) {
-        r = enqueue_body(s, st);
-        if (r == ORNITH_HIP_OK) r = enqueue_head(s, st);
+        if (s->mctr) e = hipMemsetAsync(s->mctr, 0, mb, st);
+        if (e == hipSuccess) r = enqueue_body(s, st);
+        if (r == ORNITH_HIP_OK && e == hipSuccess) r = enqueue_head(s, st);
     }
     if (e == hipSuccess) e = hipEventRecord(e1, st);
+    // and after the last pass, for the next decode step (its parity's counter
+    // holds the replay's arrivals)
+    if (e == hipSuccess && s->mctr) e = hipMemsetAsync(s->mctr, 0, mb, st);
     if (e == hipSuccess) e = hipEventSynchronize(e1);
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
     s->only = -1;
     float el = 0.0f;
     if (r == ORNITH_HIP_OK && e == hipSuccess) e = hipEventElapsedTime(&el, e0, e1);

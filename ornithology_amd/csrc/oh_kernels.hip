@@ -28,8 +28,9 @@ __global__ void __launch_bounds__(256) oh_k_delta_mv(oh_op_dmv a, const int32_t 
         if (tid_x() == 0) __hip_atomic_fetch_add(a.arr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         return;
     }
-    CtrWait w{a.arr, a.dep, a.nd, a.mv.total_blocks, a.mv.rio + OH_IO_ERR, false, true};
+    CtrWait w{a.arr, a.nd, a.mv.rio + OH_IO_ERR, false, true};
     mv_body<TK>(a.mv, vb - a.nd, w);
+    fused_depart(a.arr, a.dep, a.mv.total_blocks);
 }
 
 extern "C" {

@@ -1176,15 +1176,14 @@ OH_DEV bool wait_count(const int32_t *ctr, int n) {
 }
 // The wait of a workgroup whose inputs other workgroups of the same launch
 // produce (the projection part of the delta-step launch): one thread polls
-// the arrival counter until it reaches n (bounded),
-// the block takes one decision, then counts its departure; the last of the
-// ndep departing workgroups sets both counters back to 0 (every producer has
-// arrived and every consumer has passed by then). A wait that gives up sets
-// the error flag. kGrid: the inputs are read with device-scope loads.
+// the arrival counter until it reaches n (bounded), the block takes one
+// decision (the departure is counted at the end of the workgroup's work,
+// fused_depart). A wait that gives up sets the error flag. kGrid: the inputs
+// are read with device-scope loads.
 struct CtrWait {
     static constexpr bool kGrid = true;
-    int32_t *arr, *dep;
-    int n, ndep;
+    int32_t *arr;
+    int n;
     int32_t *err;
     bool done, ok;
     OH_DEV bool wait() {
@@ -1201,10 +1200,6 @@ struct CtrWait {
             }
             s_ok = got ? 1 : 0;
             if (!got) atomicOr(err, OH_ERR_WAIT);
-            if (__hip_atomic_fetch_add(dep, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == ndep - 1) {
-                stc(arr, 0);
-                stc(dep, 0);
-            }
         }
         __syncthreads();
         ok = s_ok != 0;
@@ -1329,13 +1324,7 @@ OH_DEV void route_fused(const oh_mvlaunch &L, bool store, float *lg, int *sel, f
     if (tid < 64) {
         const uint32_t ser = (uint32_t)ldc(L.rio + OH_IO_SERIAL), tag = ser + 1u;
         float shl = 0.0f;
-        bool got = wait_count(L.mctr, L.nrb);
-        // the departure; the last routed block resets the counters
-        if (tid == 0 &&
-            __hip_atomic_fetch_add(L.mctr + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == L.ncons - 1) {
-            stc(L.mctr, 0);
-            stc(L.mctr + 1, 0);
-        }
+        bool got = wait_count(L.mctr + (ser & 1u), L.nrb);
         int ok = 1;
         if (ne == 256) {
             float a[4];
@@ -1492,12 +1481,28 @@ OH_DEV void iq2_tree(const oh_mvseg &s, int slot, int blk, int expert, W &w) {
 // activation in LDS). With L.route every block first routes the MoE and
 // stacked segments take their experts from that routing. vb: the virtual
 // block (blockIdx.x of a standalone launch).
-// a router block of the fused MoE launch counts its arrival once every
-// wave's tagged stores have completed
-OH_DEV void fused_count(const oh_mvlaunch &L) {
+// a router block of the fused MoE launch counts itself in this step's parity
+// once every wave's tagged stores have completed; the first gate/up block
+// clears the other parity's counter for the next step
+OH_DEV void fused_count(const oh_mvlaunch &L, int vb, bool router) {
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    if (tid_x() == 0) __hip_atomic_fetch_add(L.mctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid_x() == 0) {
+        const uint32_t ser = (uint32_t)ldc(L.rio + OH_IO_SERIAL);
+        if (router)
+            __hip_atomic_fetch_add(L.mctr + (ser & 1u), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        else if (vb == L.pb0)
+            stc(L.mctr + ((ser & 1u) ^ 1u), 0);
+    }
+}
+// the delta-step launch's consumer departure at the end of its work: the last
+// of ncons consumers, every one of them past its wait and so every producer
+// arrived, sets both counters back to 0
+OH_DEV void fused_depart(int32_t *arr, int32_t *dep, int ncons) {
+    if (tid_x() == 0 && __hip_atomic_fetch_add(dep, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == ncons - 1) {
+        stc(arr, 0);
+        stc(dep, 0);
+    }
 }
 
 // The block's segment: every segment's first block is read at once (a
@@ -1538,6 +1543,7 @@ OH_DEV void mv_body(const oh_mvlaunch &L, int vb, W &w) {
                     route_fused(L, slot == 0 && blk == 0, (float *)(smem + L.rlg), rsel, rwt, &rshg, &rbad);
                     if (s.iq2split) iq2_rows(s, slot, blk, rsel[slot], smem);
                     else iq2_rows_lane(s, slot, blk, rsel[slot], smem);
+                    if (L.mctr && vb == L.pb0) fused_count(L, vb, false);
                     return;
                 }
             }
@@ -1556,6 +1562,7 @@ OH_DEV void mv_body(const oh_mvlaunch &L, int vb, W &w) {
                 else if (s.type == OH_Q8_0) mv_seg<OH_Q8_0>(s, slot, blk, 0, smem, red, w, late);
                 else mv_seg<OH_Q4_K>(s, slot, blk, 0, smem, red, w, late);
             }
+            if (L.mctr && vb == L.pb0) fused_count(L, vb, false);
             return;
         }
     } else if (L.route && L.tslots > 0) {
@@ -1574,11 +1581,11 @@ OH_DEV void mv_body(const oh_mvlaunch &L, int vb, W &w) {
     const int expert = !s.eidx ? 0 : (L.route ? rsel[L.tslots > 0 ? slot % L.tslots : slot] : ldw<W::kGrid>(s.eidx + slot));
     if constexpr (TK >= 0) {
         mv_seg<TK < 0 ? OH_Q4_K : TK>(s, slot, blk, expert, smem, red, w);
-        if (L.mctr && s.mode == 2) fused_count(L);
+        if (L.mctr && (s.mode == 2 || vb == L.pb0)) fused_count(L, vb, s.mode == 2);
     } else if constexpr (TK == OH_MV_Q4Q6) {
         if (s.type == OH_Q6_K) mv_seg<OH_Q6_K>(s, slot, blk, expert, smem, red, w);
         else mv_seg<OH_Q4_K>(s, slot, blk, expert, smem, red, w);
-        if (L.mctr && s.mode == 2) fused_count(L);
+        if (L.mctr && (s.mode == 2 || vb == L.pb0)) fused_count(L, vb, s.mode == 2);
     } else if (s.type == OH_IQ2_XXS && s.iq2tree) {
         switch (s.in / 64) {
         case 64: iq2_tree<64>(s, slot, blk, expert, w); break;
@@ -1593,7 +1600,7 @@ OH_DEV void mv_body(const oh_mvlaunch &L, int vb, W &w) {
         default: mv_seg<OH_Q8_0>(s, slot, blk, expert, smem, red, w); break;
         }
         // the router segments of a fused-router launch count themselves
-        if (L.mctr && s.mode == 2) fused_count(L);
+        if (L.mctr && (s.mode == 2 || vb == L.pb0)) fused_count(L, vb, s.mode == 2);
     } else {
         if (!w.wait()) return;
         mv_prologue<W::kGrid>(s, slot, blk, smem, red, false);

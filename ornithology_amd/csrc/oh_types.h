@@ -189,13 +189,14 @@ typedef struct {
     const uint64_t *rtag;
     int32_t *rio;
     int rsh, rlg;
-    // mctr[0] counts the router segments' blocks (nrb of them) whose tagged
-    // words are stored; a routed block (ncons of them: the blocks of the
-    // segments with eidx) polls it, then reads the words once, and counts
-    // itself in mctr[1]; the last routed block past the wait sets both back
-    // to 0, so every launch (replays for timing included) starts from zero.
+    // mctr[parity] (parity = the step serial's low bit) counts the router
+    // segments' blocks (nrb of them) whose tagged words are stored; a gate/up
+    // block polls it, then reads the words once. The first gate/up block
+    // (pb0) clears the other parity's counter for the next step. (A replay
+    // of one kind's launches for timing zeroes both counters before each
+    // pass, so its blocks wait as in a decode step.)
     int32_t *mctr;
-    int nrb, ncons;
+    int nrb, pb0;
 } oh_mvlaunch;
 
 
@@ -282,10 +283,10 @@ typedef struct {
 // The graph step's delta step and its output projection in one launch:
 // workgroups [0, nd) run the delta step (16 state rows each) and add 1 to
 // *arr once their outputs are stored; the projection's workgroups (the rest)
-// request their first weights, wait (bounded) until *arr reaches nd, add 1
-// to *dep, then form the gated RMSNorm of the delta output and reduce. The
-// last workgroup past the wait (*dep reaching the projection's workgroup
-// count) sets both counters back to 0, so every launch (replays for timing
+// request their first weights, wait (bounded) until *arr reaches nd, form
+// the gated RMSNorm of the delta output, reduce, and at the end add 1 to
+// *dep. The last of them (*dep reaching the projection's workgroup count)
+// sets both counters back to 0, so every launch (replays for timing
 // included) starts from zero.
 typedef struct {
     oh_mvlaunch mv;
