@@ -540,9 +540,12 @@ OH_DEV void iq2_rows(const oh_mvseg &s, int slot, int blk, int expert, uint8_t *
     // each wave's wait for a slot leaves the later slots in flight.
     uint2 wq[kIq2D];
     const int pw = wave > 0 ? wave - 1 : 0;          // producer index: sub-block pw of each chunk
+    // sub-block sb of the row: byte (sb / 8) * 64 + (sb % 8) * 8 = 8 sb of
+    // the row's 64-byte super-blocks, so one 8-byte word per sub-block
+    const uint2 *arow = (const uint2 *)(s.A + bi0 * 64);
     auto fetch = [&](int c, uint2 &w) {
-        const int sb = c * kIq2P + pw, sbc = sb < nsb ? sb : nsb - 1;
-        w = ldg((const uint2 *)(s.A + (bi0 + sbc / 8) * 64 + (sbc % 8) * 8));
+        const int sb = c * kIq2P + pw;
+        w = ldg(arow + (sb < nsb ? sb : nsb - 1));
     };
     const uint64_t g = k_iq2_grid[tid];            // requested before the codes: its wait leaves them in flight
     // the sign masks in LDS below the f32 activation (the Q8_K planes'
