@@ -228,11 +228,13 @@ int  ornith_hip_session_get_attn(ornith_hip_session *s, int row, float *q, float
 int  ornith_hip_session_time_decode(ornith_hip_session *s, int n_steps, float *ms);
 /* Run one greedy decode step eagerly with HIP events around every kernel
  * launch: kinds[i] (0 matvec with Q4_K weights, 1 rmsnorm+Q8_K, 2 SwiGLU+Q8_K,
- * 3 embed, 4 delta step, 5 attn prep, 6 attn scores, 7 attn out, 8 router,
- * 9 MoE combine, 10 argmax, 11 advance, 12 fused MoE down + combine, 13 flash
- * attention chunks, 14 flash merge, 15 matvec Q6_K, 16 matvec Q8_0, 17 matvec
- * of mixed types), algorithmic HBM bytes[i] and ms[i]. Advances the session by
- * one position. */
+ * 3 embed, 4 delta step, 5 attn prep, 6 attn scores (exact regime), 7 attn
+ * walk (exact regime), 8 router, 9 MoE combine, 10 argmax, 11 advance, 12
+ * fused MoE down + combine, 13 flash attention chunks, 14 flash merge, 15
+ * matvec Q6_K, 16 matvec Q8_0, 17 matvec of mixed types, 20 attention of the
+ * one-launch form, 21 matvec of Q4_K and Q6_K segments, 22 delta step and its
+ * output projection in one launch), algorithmic HBM bytes[i] and ms[i].
+ * Advances the session by one position. */
 int  ornith_hip_session_profile_step(ornith_hip_session *s, int max_launches, int32_t *kinds,
                                      double *bytes, float *ms, int *n_launches);
 /* Replay, back to back, the launches of one kind (numbering as above) that a
