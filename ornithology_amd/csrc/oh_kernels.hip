@@ -390,7 +390,7 @@ hipError_t oh_launch_op(const oh_op *op, const int32_t *io, hipStream_t st) {
     case OH_OP_ATTN_MAIN: hipLaunchKernelGGL(oh_k_attn_main, g, b256, (size_t)op->lds, st, op->u.attn, io); break;
     case OH_OP_ATTN_COMBINE: hipLaunchKernelGGL(oh_k_attn_combine, g, b256, 0, st, op->u.attn, io); break;
     case OH_OP_ATTN_SCORES: hipLaunchKernelGGL(oh_k_attn_scores, g, dim3(512), (size_t)op->lds, st, op->u.attn, io); break;
-    case OH_OP_ATTN_WALK: hipLaunchKernelGGL(oh_k_attn_walk, g, b256, (size_t)op->lds, st, op->u.attn, io); break;
+    case OH_OP_ATTN_WALK: hipLaunchKernelGGL(oh_k_attn_walk, g, dim3(512), (size_t)op->lds, st, op->u.attn, io); break;
     case OH_OP_MOE_COMBINE: hipLaunchKernelGGL(oh_k_moe_combine, g, b256, 0, st, op->u.comb); break;
     case OH_OP_ARGMAX1: hipLaunchKernelGGL(oh_k_argmax1, g, b256, 0, st, op->u.am); break;
     case OH_OP_ARGMAX2: hipLaunchKernelGGL(oh_k_argmax2, dim3(1), dim3(64), 0, st, op->u.am, io); break;

@@ -770,8 +770,10 @@ OH_DEV void exact_scores_body(const oh_op_attn &a, int vb, int pos, int lim, W &
 template <class W>
 OH_DEV void exact_walk_body(const oh_op_attn &a, int vb, int pos, int lim, W &w) {
     extern __shared__ __align__(16) uint8_t smem[];
-    __shared__ double red[4];
-    __shared__ float mred[4];
+    constexpr int NT = 512;                     // threads: the softmax on all, the walk on the first hd
+    static_assert(NT == 512, "the block sum below adds eight wave sums");
+    __shared__ double red[NT / 64];
+    __shared__ float mred[NT / 64];
     __shared__ uint64_t etab[32];
     const int nh = a.nh, nkv = a.nkv, hd = a.hd, cap = a.cap;
     const int h = vb, T = pos + 1, t = tid_x();
@@ -792,19 +794,19 @@ OH_DEV void exact_walk_body(const oh_op_attn &a, int vb, int pos, int lim, W &w)
         c[0] = ldg((const uint4 *)(p + lo));
         c[1] = ldg((const uint4 *)(p + lo + 16));
     };
-    // this thread's scores (positions t, t + 256, ...: at most PT of them,
-    // lim <= 256 * PT, requested in groups of 8 up to T) and value scales,
+    // this thread's scores (positions t, t + NT, ...: at most PT of them,
+    // lim <= NT * PT, requested in groups of 8 up to T) and value scales,
     // then the gate and the code ring: every load issued before any is used,
     // the softmax's first (they return in order)
-    constexpr int PT = 32;
+    constexpr int PT = 16;
     const float *sh = a.scores + (size_t)h * cap;
     float sv[PT], vs[PT];
 #pragma unroll
     for (int r0 = 0; r0 < PT; r0 += 8) {
-        if (256 * r0 >= T) break;
+        if (NT * r0 >= T) break;
 #pragma unroll
         for (int r = r0; r < r0 + 8; r++) {
-            const int i = t + 256 * r < T ? t + 256 * r : T - 1;
+            const int i = t + NT * r < T ? t + NT * r : T - 1;
             sv[r] = ldg(sh + i);
             vs[r] = ldg(a.Vs + (size_t)i * nkv + kvh);
         }
@@ -818,34 +820,41 @@ OH_DEV void exact_walk_body(const oh_op_attn &a, int vb, int pos, int lim, W &w)
     float mx = -INFINITY;
 #pragma unroll
     for (int r0 = 0; r0 < PT; r0 += 8) {
-        if (256 * r0 >= T) break;
+        if (NT * r0 >= T) break;
 #pragma unroll
-        for (int r = r0; r < r0 + 8; r++) if (t + 256 * r < T) mx = fmaxf(mx, sv[r]);
+        for (int r = r0; r < r0 + 8; r++) if (t + NT * r < T) mx = fmaxf(mx, sv[r]);
     }
     mx = wave_max_f(mx);
     if (lane_id() == 0) mred[t >> 6] = mx;
     __syncthreads();
-    mx = fmaxf(fmaxf(mred[0], mred[1]), fmaxf(mred[2], mred[3]));
+#pragma unroll
+    for (int k = 0; k < NT / 64; k++) mx = fmaxf(mx, mred[k]);
     // the exps in groups of 8 slots (a slot past T is computed on a
     // repeated score and left out of the sum), so those of a group overlap
     double sum = 0.0;
 #pragma unroll
     for (int r0 = 0; r0 < PT; r0 += 8) {
-        if (256 * r0 >= T) break;
+        if (NT * r0 >= T) break;
 #pragma unroll
         for (int r = r0; r < r0 + 8; r++) sv[r] = ref_expf_sel(sv[r] - mx, etab);
 #pragma unroll
-        for (int r = r0; r < r0 + 8; r++) sum += t + 256 * r < T ? (double)sv[r] : 0.0;
+        for (int r = r0; r < r0 + 8; r++) sum += t + NT * r < T ? (double)sv[r] : 0.0;
     }
-    sum = block_sum_d(sum, red);
+    // the double sum over the block (tree-ordered, as the walk's other
+    // forms; the exps are at most 1, so the order moves only the last
+    // bits of a double)
+    sum = wave_sum_d(sum);
+    if (lane_id() == 0) red[t >> 6] = sum;
+    __syncthreads();
+    sum = ((red[0] + red[1]) + (red[2] + red[3])) + ((red[4] + red[5]) + (red[6] + red[7]));
     const float inv = (float)(1.0 / sum);
 #pragma unroll
     for (int r0 = 0; r0 < PT; r0 += 8) {
-        if (256 * r0 >= T) break;
+        if (NT * r0 >= T) break;
 #pragma unroll
-        for (int r = r0; r < r0 + 8; r++) if (t + 256 * r < T) pb[t + 256 * r] = sv[r] * inv * vs[r];
+        for (int r = r0; r < r0 + 8; r++) if (t + NT * r < T) pb[t + NT * r] = sv[r] * inv * vs[r];
     }
-    for (int i = T + t; i < 16 * (nt + 2); i += 256) pb[i] = 0.0f;
+    for (int i = T + t; i < 16 * (nt + 2); i += NT) pb[i] = 0.0f;
     __syncthreads();
     if (t >= hd) return;
     // adds in position order; the weights past T are +0 (the plain sum
@@ -1556,7 +1565,7 @@ extern "C" __global__ void __launch_bounds__(512) oh_k_attn_scores(oh_op_attn a,
     NoWait w;
     exact_scores_body(a, (int)blockIdx.x, io[OH_IO_POS], exact_lim(a.exact_max, a.hd), w);
 }
-extern "C" __global__ void __launch_bounds__(256) oh_k_attn_walk(oh_op_attn a, const int32_t *io) {
+extern "C" __global__ void __launch_bounds__(512) oh_k_attn_walk(oh_op_attn a, const int32_t *io) {
     NoWait w;
     exact_walk_body(a, (int)blockIdx.x, io[OH_IO_POS], exact_lim(a.exact_max, a.hd), w);
 }
