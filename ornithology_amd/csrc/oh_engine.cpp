@@ -203,6 +203,7 @@ int tensor_alloc(ornith_hip_ctx *ctx, const char *name, uint32_t type, uint32_t 
 extern "C" void ornith_hip_tensor_free(ornith_hip_tensor *t) {
     if (!t) return;
     if (t->mem) (void)hipFree(t->mem);
+    if (t->pmem) (void)hipFree(t->pmem);
     delete t;
 }
 

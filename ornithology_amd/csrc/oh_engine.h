@@ -84,6 +84,9 @@ struct ornith_hip_tensor {
     uint64_t gguf_bytes = 0;
     uint8_t *mem = nullptr;
     uint8_t *A = nullptr, *B = nullptr, *C = nullptr;
+    // Q4_K / Q6_K prompt tiles (the matrix-core prompt kernels' copy of A and
+    // B, in 64-row tiles), built on the tensor's first such launch
+    mutable uint8_t *pmem = nullptr, *PA = nullptr, *PB = nullptr;
 };
 
 // ---- matvec launch builder ------------------------------------------------------------
@@ -356,6 +359,9 @@ int mv_add_pair(MvBuild &b, const ornith_hip_tensor *W, const ornith_hip_tensor 
 void mv_plan(MvBuild &b, int waves = 4096, int small_waves = 0);
 int mv_go(MvBuild &b, hipStream_t st);
 bool mmq_enabled();
+// The prompt tiles of a Q4_K / Q6_K tensor (PA, PB), built once on stream st
+// and waited for; a no-op when they exist
+int mmq_tiles(const ornith_hip_tensor *W, hipStream_t st);
 size_t matvec_col_bytes(int64_t in, int64_t out);
 int matvec_cols(ornith_hip_ctx *ctx, const ornith_hip_tensor *W, const float *x, float *y, int Tn,
                        void *sp);
@@ -421,6 +427,7 @@ int pf_mvb(const ornith_hip_tensor *W, const ornith_hip_tensor *W2, const Q8Buf 
                   int T, int mode, hipStream_t st, const int32_t *cnt = nullptr, const int32_t *list = nullptr,
                   int lstride = 0, int adiv = 1, int groups = 1);
 bool pf_use_mmq(const ornith_hip_tensor *W, bool grouped, int T);
+int pf_tiles(const ornith_hip_model *m, hipStream_t st);
 int pf_mmq(const ornith_hip_tensor *W, const ornith_hip_tensor *W2, const Q8Buf &x, float *y, int ystride,
                   int T, int mode, hipStream_t st, const int32_t *cnt = nullptr, const int32_t *list = nullptr,
                   int lstride = 0, int adiv = 1, const int32_t *items = nullptr, int max_items = 0);

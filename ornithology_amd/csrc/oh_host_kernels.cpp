@@ -41,6 +41,35 @@ bool mmq_enabled() {
     return !(e && e[0] == '0');
 }
 
+int mmq_tiles(const ornith_hip_tensor *W, hipStream_t st) {
+    if (W->PA) return ORNITH_HIP_OK;
+    const int P = W->type == OH_Q4_K ? 8 : W->type == OH_Q6_K ? 12 : 0;
+    if (!P || W->rows % 64 || W->in % 256) {
+        seterr("tensor '%s': no prompt tiles for type %u with %lld rows", W->name.c_str(), W->type,
+               (long long)W->rows);
+        return ORNITH_HIP_ERR_UNSUPPORTED;
+    }
+    const size_t nblk = (size_t)W->rows * (size_t)(W->in / 256), a = nblk * 16 * P, b = nblk * 16;
+    uint8_t *mem = nullptr;
+    hipError_t e = hipMalloc(&mem, up256(a) + b);
+    if (e != hipSuccess) {
+        seterr("tensor '%s': prompt tiles, hipMalloc(%zu): %s", W->name.c_str(), up256(a) + b,
+               hipGetErrorString(e));
+        return ORNITH_HIP_ERR_OOM;
+    }
+    e = oh_launch_mmq_tiles(W->A, W->B, mem, mem + up256(a), W->rows, (int)(W->in / 256), P, st);
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    if (e != hipSuccess) {
+        (void)hipFree(mem);
+        seterr("tensor '%s': prompt tiles: %s", W->name.c_str(), hipGetErrorString(e));
+        return ORNITH_HIP_ERR_DEVICE;
+    }
+    W->pmem = mem;
+    W->PA = mem;
+    W->PB = mem + up256(a);
+    return ORNITH_HIP_OK;
+}
+
 // device bytes of matvec_cols' buffer: input, output, Q8_K planes (256-aligned)
 size_t matvec_col_bytes(int64_t in, int64_t out) {
     return (size_t)in * 5 + (size_t)(in / 256) * 40 + (size_t)out * 4 + 4096;
@@ -65,9 +94,10 @@ extern "C" int ornith_hip_matvec(ornith_hip_ctx *ctx, const ornith_hip_tensor *W
         HCHK(hipMemcpyAsync(dx, x, T * in * 4, hipMemcpyHostToDevice, ctx->st));
         HCHK(oh_launch_norm_q8k_rows(dx, nullptr, 0.0f, (int)in, Tn, nullptr, qs, dd, bs, ctx->st, bp));
         if (mmq_enabled() && oh_mmq_can(W->type, (int)out, (int)in)) {
+            CHK(mmq_tiles(W, ctx->st));
             oh_mmq M;
             memset(&M, 0, sizeof M);
-            M.A = W->A; M.B = W->B; M.C = W->C; M.type = (int)W->type;
+            M.A = W->PA; M.B = W->PB; M.C = W->C; M.type = (int)W->type;
             M.xqs = qs; M.xd = dd; M.xbp = bp; M.y = dy;
             M.nb = (int)nb; M.in = (int)in; M.rows = (int)out; M.ncol = Tn; M.adiv = 1; M.ystride = (int)out;
             HCHK(oh_launch_mmq(&M, 0, 0, ctx->st));

@@ -153,13 +153,40 @@ bool pf_use_mmq(const ornith_hip_tensor *W, bool grouped, int T) {
     return mmq_enabled() && T >= kMmqMinTokens && oh_mmq_can(W->type, rows, (int)W->in);
 }
 
+// The prompt tiles of every tensor that pf_chunk runs on the matrix cores
+// (the pairs of pf_swiglu only when both qualify)
+int pf_tiles(const ornith_hip_model *m, hipStream_t st) {
+    if (!mmq_enabled()) return ORNITH_HIP_OK;
+    const int T = kMmqMinTokens;
+    for (const OhLayer &y : m->L) {
+        const ornith_hip_tensor *dense[] = {y.q, y.k, y.v, y.o, y.qkv, y.gate, y.alpha, y.beta, y.ssm_out,
+                                            y.router, y.gate_inp_sh, y.down_sh, y.ffn_down};
+        for (const ornith_hip_tensor *W : dense)
+            if (W && pf_use_mmq(W, false, T)) CHK(mmq_tiles(W, st));
+        const ornith_hip_tensor *pairs[][2] = {{y.gate_sh, y.up_sh}, {y.ffn_gate, y.ffn_up}};
+        for (auto &pr : pairs)
+            if (pr[0] && pr[1] && pf_use_mmq(pr[0], false, T) && pf_use_mmq(pr[1], false, T)) {
+                CHK(mmq_tiles(pr[0], st));
+                CHK(mmq_tiles(pr[1], st));
+            }
+        if (y.gate_exps && y.up_exps && pf_use_mmq(y.gate_exps, true, T) && pf_use_mmq(y.up_exps, true, T)) {
+            CHK(mmq_tiles(y.gate_exps, st));
+            CHK(mmq_tiles(y.up_exps, st));
+        }
+        if (y.down_exps && pf_use_mmq(y.down_exps, true, T)) CHK(mmq_tiles(y.down_exps, st));
+    }
+    return ORNITH_HIP_OK;
+}
+
 int pf_mmq(const ornith_hip_tensor *W, const ornith_hip_tensor *W2, const Q8Buf &x, float *y, int ystride,
                   int T, int mode, hipStream_t st, const int32_t *cnt, const int32_t *list,
                   int lstride, int adiv, const int32_t *items, int max_items) {
+    CHK(mmq_tiles(W, st));
+    if (W2) CHK(mmq_tiles(W2, st));
     oh_mmq M;
     memset(&M, 0, sizeof M);
-    M.A = W->A; M.B = W->B; M.C = W->C; M.type = (int)W->type;
-    if (W2) { M.A2 = W2->A; M.B2 = W2->B; M.C2 = W2->C; }
+    M.A = W->PA; M.B = W->PB; M.C = W->C; M.type = (int)W->type;
+    if (W2) { M.A2 = W2->PA; M.B2 = W2->PB; M.C2 = W2->C; }
     M.xqs = x.qs; M.xd = x.d; M.xbp = x.bp; M.y = y;
     M.cnt = cnt; M.list = list; M.items = items;
     M.nb = (int)(W->in / 256); M.in = (int)W->in; M.rows = list ? (int)W->dims[1] : (int)W->rows;

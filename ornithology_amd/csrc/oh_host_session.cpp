@@ -187,6 +187,9 @@ extern "C" int ornith_hip_session_new(ornith_hip_model *m, int cap, ornith_hip_s
         hipError_t e = hipMemcpy(s->rope, tab.data(), tab.size() * sizeof(float2), hipMemcpyHostToDevice);
         if (e != hipSuccess) { ornith_hip_session_free(s); seterr("rope upload: %s", hipGetErrorString(e)); return ORNITH_HIP_ERR_DEVICE; }
     }
+    // a session long enough for matrix-core prompt chunks has the model's
+    // prompt tiles built here, once per model, outside its prompts
+    if (cap >= kMmqMinTokens) A_(pf_tiles(m, m->ctx->st));
 #undef A_
     *out = s;
     return ORNITH_HIP_OK;

@@ -219,6 +219,15 @@ bool oh_mmq_can(uint32_t type, int rows, int in) {
     return (type == OH_Q4_K || (type == OH_Q6_K && in <= 8192)) && rows > 0 && rows % kMqRows == 0 &&
            in % 256 == 0 && in > 0;
 }
+hipError_t oh_launch_mmq_tiles(const uint8_t *A, const uint8_t *B, uint8_t *PA, uint8_t *PB, int64_t rows,
+                               int nb, int P, hipStream_t st) {
+    if (rows <= 0 || rows % 64 || nb <= 0 || (P != 8 && P != 12)) return hipErrorInvalidValue;
+    const int64_t n = rows * nb * (P + 1);
+    const int64_t nbk = (n + 255) / 256;
+    hipLaunchKernelGGL(oh_k_mmq_tiles, dim3((unsigned)(nbk < 16384 ? nbk : 16384)), dim3(256), 0, st,
+                       (const uint4 *)A, (const uint4 *)B, (uint4 *)PA, (uint4 *)PB, rows, nb, P);
+    return hipGetLastError();
+}
 hipError_t oh_launch_mmq(const oh_mmq *M, int max_items, int pair, hipStream_t st) {
     // grouped: the item rows rounded up for the XCD runs of mq_block (rows past
     // the item count exit)
@@ -229,12 +238,18 @@ hipError_t oh_launch_mmq(const oh_mmq *M, int max_items, int pair, hipStream_t s
     if (M->type == OH_Q6_K) {
         static bool lds6 = false;      // stages + the rows' d exceed the default dynamic LDS limit
         if (!lds6) {
-            const hipError_t e = hipFuncSetAttribute((const void *)oh_k_mmq_q6k,
-                                                     hipFuncAttributeMaxDynamicSharedMemorySize, m6_lds_bytes(32));
+            hipError_t e = hipFuncSetAttribute((const void *)oh_k_mmq_q6k,
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, m6_lds_bytes(32, 2));
+            if (e == hipSuccess)
+                e = hipFuncSetAttribute((const void *)oh_k_mmq_q6k_s1, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                        m6_lds_bytes(kM6OneBuf, 1));
             if (e != hipSuccess) return e;
             lds6 = true;
         }
-        hipLaunchKernelGGL(oh_k_mmq_q6k, grid, dim3(256), (size_t)m6_lds_bytes(M->nb), st, *M);
+        if (M->nb <= kM6OneBuf)
+            hipLaunchKernelGGL(oh_k_mmq_q6k_s1, grid, dim3(256), (size_t)m6_lds_bytes(M->nb, 1), st, *M);
+        else
+            hipLaunchKernelGGL(oh_k_mmq_q6k, grid, dim3(256), (size_t)m6_lds_bytes(M->nb, 2), st, *M);
         return hipGetLastError();
     }
     static bool lds_set = false;   // two stages exceed the default dynamic LDS limit

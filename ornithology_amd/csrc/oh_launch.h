@@ -47,6 +47,10 @@ hipError_t oh_launch_gnorm_q8k_rows(const float *x, const float *z, const float 
 hipError_t oh_launch_mmq(const oh_mmq *M, int max_items, int pair, hipStream_t st);
 hipError_t oh_launch_mmq_items(const int32_t *cnt, int ne, int32_t *items, hipStream_t st);
 bool oh_mmq_can(uint32_t type, int rows, int in);
+// the prompt tiles of a Q4_K (P = 8 code pieces) or Q6_K (P = 12) tensor of
+// `rows` rows (a multiple of 64) from its A and B planes
+hipError_t oh_launch_mmq_tiles(const uint8_t *A, const uint8_t *B, uint8_t *PA, uint8_t *PB, int64_t rows,
+                               int nb, int P, hipStream_t st);
 // decode of n sessions at once: the decode bodies, one grid row per session,
 // descriptors and positions in device arrays of n
 hipError_t oh_launch_delta_batch(const oh_op_delta *ops, const int32_t *pos, int n, int dk, int K, int nv,

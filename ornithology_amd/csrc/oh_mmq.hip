@@ -18,8 +18,10 @@
 // Block: 256 threads, a tile of 128 rows x 64 columns; wave w owns rows
 // [32w, 32w + 32) and both 32-column halves. One super-block per stage; the
 // stage's operands go global -> LDS with global_load_lds (no registers), two
-// stages in flight. Weight codes are piece-major so that the 32 lanes of an
-// MFMA operand read consecutive 16-byte chunks. Activation codes are loaded
+// stages in flight. The weights come from the tensor's prompt tiles (below):
+// one wave-load of a code piece, or of the headers, for 64 rows of one
+// super-block reads 1 KB contiguously, and in LDS the 32 lanes of an MFMA
+// operand read consecutive 16-byte chunks. Activation codes are loaded
 // 4 columns per wave-load (16 lanes read a column's 256 bytes, whole cache
 // lines) and kept column-major with the piece index XOR-swizzled by the
 // column, so the operand reads (one piece of 16 consecutive columns) still
@@ -37,6 +39,28 @@ constexpr int kMqP = kMqH + 128 * 16;           // pair-sum bytes [64 cols][16 B
 constexpr int kMqD = kMqP + 64 * 16;            // activation d [64 cols]
 constexpr int kMqStage = kMqD + 64 * 4;         // 36096 B
 constexpr int kMqLoads = 16 + 16 + 2 + 1 + 1;   // wave-loads per stage (9 per wave)
+
+// Prompt tiles: a copy of a Q4_K / Q6_K tensor's code plane A (P = 8 or 12
+// pieces of 16 B per super-block) and header plane B (16 B per super-block)
+// for these kernels. Row r, super-block i, piece p sits at 16-byte index
+// ((r / 64 * nb + i) * P + p) * 64 + r % 64 of PA, its header at
+// (r / 64 * nb + i) * 64 + r % 64 of PB. The decode planes group 64
+// consecutive super-blocks of a row instead, which leaves the 64 rows of one
+// stage load in 64 different cache lines. One thread per 16-byte destination.
+extern "C" __global__ void __launch_bounds__(256) oh_k_mmq_tiles(const uint4 *A, const uint4 *B, uint4 *PA,
+                                                                 uint4 *PB, int64_t rows, int nb, int P) {
+    const int64_t na = rows * nb * P, n = na + rows * nb;
+    for (int64_t d = (int64_t)blockIdx.x * 256 + threadIdx.x; d < n; d += (int64_t)gridDim.x * 256) {
+        const bool code = d < na;
+        const int64_t e = code ? d : d - na, q = e >> 6;
+        const int p = code ? (int)(q % P) : 0;
+        const int64_t ti = code ? q / P : q;
+        const int i = (int)(ti % nb);
+        const int64_t r = ti / nb * 64 + (e & 63), bi = r * nb + i;
+        if (code) PA[e] = A[(bi >> 6) * 64 * P + p * 64 + (bi & 63)];
+        else PB[e] = B[bi];
+    }
+}
 
 namespace {
 
@@ -60,11 +84,11 @@ OH_DEV int mq_act_slot(int c, int p) { return c * 16 + (p ^ (c & 15)); }
 OH_DEV void mq_stage_load(const oh_mmq &M, const uint8_t *A, const uint8_t *Bh, int64_t rbase, int R0, int i,
                           uint8_t *S, int w, int lane, const int (&acs)[4], int acol) {
     const int nb = M.nb;
+    const int64_t rt = (rbase + R0) >> 6;          // first 64-row tile of the block
 #pragma unroll
     for (int n = 0; n < 4; n++) {
         const int L = w + 4 * n, p = L >> 1, rh = L & 1;
-        const int64_t bi = (rbase + R0 + rh * 64 + lane) * nb + i;
-        const uint4 *src = (const uint4 *)(A + (bi >> 6) * (int64_t)(64 * 128)) + (bi & 63) + p * 64;
+        const uint4 *src = (const uint4 *)A + ((rt + rh) * nb + i) * (8 * 64) + p * 64 + lane;
         mq_load16(src, S + kMqA + (p * 128 + rh * 64) * 16);
     }
 #pragma unroll
@@ -73,8 +97,7 @@ OH_DEV void mq_stage_load(const oh_mmq &M, const uint8_t *A, const uint8_t *Bh, 
         mq_load16(M.xqs + (size_t)acs[n] * M.in + (size_t)i * 256 + q * 16, S + kMqB + j * 64 * 16);
     }
     if (w < 2) {
-        const int64_t bi = (rbase + R0 + w * 64 + lane) * nb + i;
-        mq_load16(Bh + bi * 16, S + kMqH + w * 64 * 16);
+        mq_load16((const uint4 *)Bh + ((rt + w) * nb + i) * 64 + lane, S + kMqH + w * 64 * 16);
     } else if (w == 2) {
         mq_load16(M.xbp + ((size_t)acol * nb + i) * 16, S + kMqP);
     } else {
@@ -279,7 +302,11 @@ constexpr int kM6S = kM6B + 16 * 64 * 16;        // group scales [128 rows][16 B
 constexpr int kM6X = kM6S + 128 * 16;            // activation d [64 cols]
 constexpr int kM6Stage = kM6X + 64 * 4;          // 43264 B
 constexpr int kM6Loads = 24 + 16 + 2 + 1;        // wave-loads per stage (10 or 11 per wave)
-OH_HD inline int m6_lds_bytes(int nb) { return 2 * kM6Stage + 128 * nb * 2; }
+OH_HD inline int m6_lds_bytes(int nb, int nbuf) { return nbuf * kM6Stage + 128 * nb * 2; }
+// Products of at most kM6OneBuf super-blocks (K <= 512: the expert down
+// projections) are a short latency chain per block; one stage buffer (44 KB of
+// LDS instead of 87 KB) lets two blocks share a CU and overlap their chains.
+constexpr int kM6OneBuf = 2;
 
 typedef short m6_s2 __attribute__((ext_vector_type(2)));
 
@@ -292,11 +319,11 @@ namespace {
 OH_DEV void m6_stage_load(const oh_mmq &M, const uint8_t *A, const uint8_t *Bs, int64_t rbase, int R0, int i,
                           uint8_t *S, int w, int lane, const int (&acs)[4], int acol) {
     const int nb = M.nb;
+    const int64_t rt = (rbase + R0) >> 6;
 #pragma unroll
     for (int n = 0; n < 6; n++) {
         const int L = w + 4 * n, p = L >> 1, rh = L & 1;
-        const int64_t bi = (rbase + R0 + rh * 64 + lane) * nb + i;
-        const uint4 *src = (const uint4 *)(A + (bi >> 6) * (int64_t)(64 * 192)) + (bi & 63) + p * 64;
+        const uint4 *src = (const uint4 *)A + ((rt + rh) * nb + i) * (12 * 64) + p * 64 + lane;
         mq_load16(src, S + kM6A + (p * 128 + rh * 64) * 16);
     }
 #pragma unroll
@@ -305,8 +332,7 @@ OH_DEV void m6_stage_load(const oh_mmq &M, const uint8_t *A, const uint8_t *Bs, 
         mq_load16(M.xqs + (size_t)acs[n] * M.in + (size_t)i * 256 + q * 16, S + kM6B + j * 64 * 16);
     }
     if (w < 2) {
-        const int64_t bi = (rbase + R0 + w * 64 + lane) * nb + i;
-        mq_load16(Bs + bi * 16, S + kM6S + w * 64 * 16);
+        mq_load16((const uint4 *)Bs + ((rt + w) * nb + i) * 64 + lane, S + kM6S + w * 64 * 16);
     } else if (w == 2) {
         mq_load4(M.xd + (size_t)acol * nb + i, S + kM6X);
     }
@@ -333,11 +359,10 @@ OH_DEV void m6_split(const uint32_t q6[4], int sc, mq_v4i &lo, mq_v4i &hi) {
     }
 }
 
-} // namespace
-
-extern "C" __global__ void __launch_bounds__(256, 1) oh_k_mmq_q6k(oh_mmq M) {
-    extern __shared__ __align__(16) uint8_t smem[];
-    __shared__ int sact[kMqCols], sout[kMqCols];
+// NBUF stage buffers: 2 overlaps the loads of super-block i + 1 with the
+// products of i; 1 loads super-block i + 1 after the products of i.
+template <int NBUF>
+OH_DEV void m6_body(const oh_mmq &M, uint8_t *smem, int *sact, int *sout) {
     const int tid = tid_x(), lane = lane_id();
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int zi = (int)blockIdx.z;
@@ -359,7 +384,7 @@ extern "C" __global__ void __launch_bounds__(256, 1) oh_k_mmq_q6k(oh_mmq M) {
     const uint8_t *A = zi ? M.A2 : M.A, *Bs = zi ? M.B2 : M.B, *Cd = zi ? M.C2 : M.C;
     const int64_t rbase = M.list ? (int64_t)g * M.rows : 0;
     const int nb = M.nb;
-    uint16_t *Dr = (uint16_t *)(smem + 2 * kM6Stage);      // [128 rows][nb] f16 d
+    uint16_t *Dr = (uint16_t *)(smem + NBUF * kM6Stage);   // [128 rows][nb] f16 d
     for (int k = tid; k < 128 * nb; k += 256) {
         const int r = k / nb, i = k - r * nb;
         Dr[k] = ldg((const uint16_t *)(Cd + ((rbase + R0 + r) * nb + i) * 2));
@@ -389,8 +414,8 @@ extern "C" __global__ void __launch_bounds__(256, 1) oh_k_mmq_q6k(oh_mmq M) {
 
     stage(0, 0);
     for (int i = 0; i < nb; i++) {
-        const int buf = i & 1;
-        if (i + 1 < nb) {
+        const int buf = NBUF == 2 ? i & 1 : 0;
+        if (NBUF == 2 && i + 1 < nb) {
             stage(i + 1, buf ^ 1);
             // this wave's loads of stage i are the older ones; every wave
             // issued at least 10 for stage i + 1
@@ -443,7 +468,8 @@ extern "C" __global__ void __launch_bounds__(256, 1) oh_k_mmq_q6k(oh_mmq M) {
                 acc[t][v] += d * (float)isum;
             }
         }
-        __syncthreads();                            // stage buf is refilled next iteration
+        __syncthreads();                            // stage buf is refilled next
+        if (NBUF == 1 && i + 1 < nb) stage(i + 1, 0);
     }
     const size_t zoff = (size_t)zi * M.rows;
 #pragma unroll
@@ -458,6 +484,19 @@ extern "C" __global__ void __launch_bounds__(256, 1) oh_k_mmq_q6k(oh_mmq M) {
             else stg(yp, acc[t][v]);
         }
     }
+}
+
+} // namespace
+
+extern "C" __global__ void __launch_bounds__(256, 1) oh_k_mmq_q6k(oh_mmq M) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ int sact[kMqCols], sout[kMqCols];
+    m6_body<2>(M, smem, sact, sout);
+}
+extern "C" __global__ void __launch_bounds__(256, 2) oh_k_mmq_q6k_s1(oh_mmq M) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ int sact[kMqCols], sout[kMqCols];
+    m6_body<1>(M, smem, sact, sout);
 }
 
 // Work items of a grouped product: (group, 64-column tile) pairs, packed as

@@ -84,12 +84,14 @@ def test_matvec_vs_oracle(hip_ctx, orc, t, shape):
 
 
 @pytest.mark.parametrize("t", [Q4_K, Q6_K], ids=["Q4_K", "Q6_K"])
-@pytest.mark.parametrize("shape,ncol", [((2048, 1024), 70), ((512, 384), 1), ((4096, 256), 130), ((1024, 200), 65)])
+@pytest.mark.parametrize("shape,ncol", [((2048, 1024), 70), ((512, 384), 1), ((4096, 256), 130), ((1024, 200), 65),
+                                         ((512, 256), 70), ((256, 128), 65)])
 def test_batched_q4k_distinct_columns(hip_ctx, orc, monkeypatch, shape, ncol, t):
     """Batched Q4_K / Q6_K products (matmul_batch_q Tn semantics) on
     independent columns: the matrix-core path (rows a multiple of 128) and the
     vector-ALU path (ORNITH_HIP_MMQ=0, and 200 rows) both equal the oracle's
-    per-column qdot bit for bit; partial 64-column tiles included."""
+    per-column qdot bit for bit; partial 64-column tiles included. K = 512 and
+    256 take the one-stage Q6_K kernel, the longer rows the two-stage one."""
     n, out = shape
     w = clibs.gauss(11, f"bq.{n}.{out}", n * out, 0.02)
     if t == Q6_K:
