@@ -149,7 +149,10 @@ int  ornith_hip_model_tensor_info(const ornith_hip_model *m, const char *name,
 const ornith_hip_tensor *ornith_hip_model_tensor(const ornith_hip_model *m, const char *name);
 
 /* rmodel_session_new: capacity `cap` positions, Q8 KV cache (ORNITH_KV_Q8=1
- * semantics, src/ornith_attn.h:39-68). */
+ * semantics, src/ornith_attn.h:39-68). With cap >= 64 the first such session
+ * of a model also builds the model's prompt tiles (a second copy of the Q4_K /
+ * Q6_K tensors the prompt runs on the matrix cores, about their GGUF size;
+ * none with ORNITH_HIP_MMQ=0); they are freed with the model. */
 int  ornith_hip_session_new(ornith_hip_model *m, int cap, ornith_hip_session **out);
 void ornith_hip_session_free(ornith_hip_session *s);                             /* rmodel_session_free */
 /* rmodel_session_eval (src/ornith_rforward.c:838-849,933-944): the prompt runs
