@@ -97,7 +97,9 @@ int  ornith_hip_quantize_q8K(ornith_hip_ctx *ctx, const float *x, int64_t k,
 
 /* matmul_batch_q (src/ornith_rforward.c:138-196): Y[t*out+o] = W[o,:].X[t,:]
  * for Tn columns; Q8_K integer path for Q4_K/Q6_K/Q8_0 (qdot_can), ordered
- * f32 fallback otherwise. Host X [Tn*in], Y [Tn*out]. */
+ * f32 fallback otherwise. Host X [Tn*in], Y [Tn*out]. The first call with
+ * Tn > 1 that runs a Q4_K / Q6_K tensor on the matrix cores builds that
+ * tensor's prompt tiles (see ornith_hip_session_new). */
 int  ornith_hip_matvec(ornith_hip_ctx *ctx, const ornith_hip_tensor *W,
                        const float *x, float *y, int Tn);
 
