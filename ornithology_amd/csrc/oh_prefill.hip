@@ -346,28 +346,56 @@ oh_k_delta_chunked(const float *qn, const float *kn, const float *conv, const fl
         // decay products: thread i owns row i of the coefficient tables, which
         // turn in place into M[i][j] = beta_i (p_i/p_j) k_j.k_i and
         // W[i][j] = (p_i/p_j) k_j.q_i
+        // (the gates and row i are read into registers first, so the
+        // product chains wait on no LDS read; the same products in the same
+        // order as a loop over LDS)
         if (tid < C) {
             const int i = tid;
-            float pi = alpha[0];
-            for (int l = 1; l <= i; l++) pi = pi * alpha[l];
+            float ag[CH], mr[CH], wr[CH];
+#pragma unroll
+            for (int l = 0; l < CH; l++) ag[l] = alpha[l];
+#pragma unroll
+            for (int q = 0; q < CH / 4; q++) {
+                const float4 vm = *(const float4 *)&M[i][4 * q], vw = *(const float4 *)&W[i][4 * q];
+                mr[4 * q] = vm.x; mr[4 * q + 1] = vm.y; mr[4 * q + 2] = vm.z; mr[4 * q + 3] = vm.w;
+                wr[4 * q] = vw.x; wr[4 * q + 1] = vw.y; wr[4 * q + 2] = vw.z; wr[4 * q + 3] = vw.w;
+            }
+            float pi = ag[0];
+#pragma unroll
+            for (int l = 1; l < CH; l++)
+                if (l <= i) pi = pi * ag[l];
             p[i] = pi;
             const float bi = beta[i];
             float ratio = 1.0f;
             int z = 0;
-            for (int j = i - 1; j >= 0; j--) {
-                ratio *= alpha[j + 1];
-                const float mij = bi * ratio * M[i][j];
-                M[i][j] = mij;
-                z |= mij == 0.0f;
-                W[i][j] = ratio * W[i][j];
+#pragma unroll
+            for (int j = CH - 2; j >= 0; j--) {
+                if (j < i) {
+                    ratio *= ag[j + 1];
+                    const float mij = bi * ratio * mr[j];
+                    mr[j] = mij;
+                    z |= mij == 0.0f;
+                    wr[j] = ratio * wr[j];
+                }
+            }
+#pragma unroll
+            for (int q = 0; q < CH / 4; q++) {
+                *(float4 *)&M[i][4 * q] = float4{mr[4 * q], mr[4 * q + 1], mr[4 * q + 2], mr[4 * q + 3]};
+                *(float4 *)&W[i][4 * q] = float4{wr[4 * q], wr[4 * q + 1], wr[4 * q + 2], wr[4 * q + 3]};
             }
             mz[i] = z;
         }
         if (tid == 64) {
+            float ag[CH];
+#pragma unroll
+            for (int l = 0; l < CH; l++) ag[l] = alpha[l];
             float ratio = 1.0f;
-            for (int j = C - 1; j >= 0; j--) {
-                wend[j] = ratio;
-                ratio *= alpha[j];
+#pragma unroll
+            for (int j = CH - 1; j >= 0; j--) {
+                if (j < C) {
+                    wend[j] = ratio;
+                    ratio *= ag[j];
+                }
             }
         }
         __syncthreads();
