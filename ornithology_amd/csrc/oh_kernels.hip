@@ -269,7 +269,9 @@ hipError_t oh_launch_mmq_items(const int32_t *cnt, int ne, int32_t *items, hipSt
 }
 hipError_t oh_launch_gnorm_q8k_rows(const float *x, const float *z, const float *w, float eps, int n, int gdim,
                                     int T, int8_t *qs, float *d, int16_t *bs, hipStream_t st, int8_t *bp) {
-    hipLaunchKernelGGL(oh_k_gnorm_q8k_rows, dim3(T), dim3(256), 0, st, x, z, w, eps, n, gdim, qs, d, bs, bp);
+    if (n <= 0 || n > 8192 || gdim <= 0 || n % gdim || n / gdim > 128) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(oh_k_gnorm_q8k_rows, dim3(T), dim3(256), (size_t)n * 4, st, x, z, w, eps, n, gdim, qs, d, bs,
+                       bp);
     return hipGetLastError();
 }
 hipError_t oh_launch_prep_rows(const oh_op_prep *a, int base, int T, hipStream_t st) {

@@ -530,10 +530,11 @@ oh_k_delta_chunked(const float *qn, const float *kn, const float *conv, const fl
 // ---- gated per-head RMSNorm + Q8_K of T vectors (src/ornith_rforward.c:300-319) ---
 // one block per token: per head of gdim elements the runs' sums of squares in
 // order, inv = 1/sqrt(ss/gdim + eps), v = x * inv * w * silu(z); then Q8_K.
+// Dynamic LDS: n floats (n <= 8192), so narrower rows keep more blocks resident.
 extern "C" __global__ void __launch_bounds__(256)
 oh_k_gnorm_q8k_rows(const float *x, const float *z, const float *w, float eps, int n, int gdim, int8_t *qs,
                     float *d, int16_t *bs, int8_t *bp) {
-    __shared__ float v[8192];
+    extern __shared__ __align__(16) float v[];
     __shared__ float hinv[128];
     __shared__ double runs[128];
     const size_t t = blockIdx.x;
