@@ -37,8 +37,15 @@ oh_k_conv_rows(const float *cat, const float *conv_w, float *conv_state, float *
         const int tj = t0 - (K - 1) + j;
         xw[j] = j >= K - 1 ? 0.0f : tj >= 0 ? ldg(cat + (size_t)tj * cc + c) : ldg(win + (size_t)(t0 + j) * cc + c);
     }
-    for (int t = t0; t < t1; t++) {
-        const float xt = ldg(cat + (size_t)t * cc + c);
+    // the run's inputs are requested together (one memory latency per run)
+    float xr[kConvRun];
+#pragma unroll
+    for (int u = 0; u < kConvRun; u++) xr[u] = t0 + u < t1 ? ldg(cat + (size_t)(t0 + u) * cc + c) : 0.0f;
+#pragma unroll
+    for (int u = 0; u < kConvRun; u++) {
+        const int t = t0 + u;
+        if (t >= t1) break;
+        const float xt = xr[u];
         float acc = 0.0f, wl = 0.0f;
 #pragma unroll
         for (int j = 0; j < kConvKMax; j++) {
@@ -684,13 +691,27 @@ extern "C" __global__ void __launch_bounds__(256) oh_k_fill_i32(int32_t *p, int 
 }
 
 // x_t += sum_s w_ts * o_ts (s in routing order) + shared * gate_t; grid (H/256, T)
+constexpr int kCombineK = 16;                    // slots whose loads are issued together
 extern "C" __global__ void __launch_bounds__(256)
 oh_k_moe_combine_rows(float *x, const float *o, const float *w, int k, int H, const float *so, const float *shgate) {
     const int i = (int)(blockIdx.x * 256 + tid_x());
     const size_t t = blockIdx.y;
     if (i >= H) return;
     float acc = 0.0f;
-    for (int s = 0; s < k; s++) acc += ldg(w + t * k + s) * ldg(o + (t * k + s) * H + i);
+    if (k <= kCombineK) {
+        // every slot's weight and output requested before the ordered sum
+        float ws[kCombineK], os[kCombineK];
+#pragma unroll
+        for (int s = 0; s < kCombineK; s++) {
+            ws[s] = s < k ? ldg(w + t * k + s) : 0.0f;
+            os[s] = s < k ? ldg(o + (t * k + s) * H + i) : 0.0f;
+        }
+#pragma unroll
+        for (int s = 0; s < kCombineK; s++)
+            if (s < k) acc += ws[s] * os[s];
+    } else {
+        for (int s = 0; s < k; s++) acc += ldg(w + t * k + s) * ldg(o + (t * k + s) * H + i);
+    }
     if (so) {
         const float sv = ldg(so + t * H + i);
         const float v = shgate ? sv * ldg(shgate + t) : sv;
