@@ -2150,12 +2150,15 @@ oh_k_norm_q8k_rows(const float *x, const float *norm_w, float eps, int n, float 
             wn[k] = i < n ? ldg(norm_w + i) : 0.0f;
         }
     }
+    // (unrolled, so that a thread's row loads are requested together)
     if (swiglu) {
         // rows of [gate | up] (2n): v = silu(gate) * up, the paired matvec's h
         const float *xr = x + r * 2 * n;
+#pragma unroll 8
         for (int i = tid; i < n; i += 256) v[i] = ref_silu(ldg(xr + i)) * ldg(xr + n + i);
     } else {
         const float *xr = x + r * n;
+#pragma unroll 8
         for (int i = tid; i < n; i += 256) v[i] = ldg(xr + i);
     }
     __syncthreads();
